@@ -1,0 +1,80 @@
+"""ctypes binding of libllmy.so (the C ABI declared in include/llmy.h).
+
+Mirrors the reference binding style (llmy_cuda/python/sample.py:104-175:
+``ctypes.CDLL`` + explicit argtypes/restype).  The library is looked up in
+``$LLMY_LIBRARY`` or next to this file; a missing library raises — there is
+no fallback path.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from pathlib import Path
+
+_P = C.c_void_p
+_I = C.c_int32
+_F = C.c_float
+_I64 = C.c_int64
+_U64P = C.POINTER(C.c_uint64)
+
+# name -> (restype, argtypes); one entry per declaration in include/llmy.h.
+SIGNATURES: dict[str, tuple[object, list[object]]] = {
+    "llmy_abi_version": (_I, []),
+    "llmy_router_topk_bf16": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _P]),
+    "llmy_router_topk_logits_f32": (_I, [_P, _P, _P, _I, _I, _I, _P]),
+    "llmy_moe_permute": (_I, [_P, _I, _I, _P, _P, _P, _P, _P]),
+    "llmy_sample_argmax_f32": (_I, [_P, _I, _I, _P, _P]),
+    "llmy_linear_bf16": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _P]),
+    "llmy_moe_experts_bf16": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),
+    "llmy_moe_combine": (_I, [_P, _P, _P, _I, _I, _I, _I, _P]),
+    "llmy_banded_attn_decode_bf16": (_I, [_P, _P, _P, _I64, _I64, _P, _P, _P, _P, _I, _I, _I,
+                                          _I, _F, _P]),
+    "llmy_gdn_step_bf16": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P]),
+    "llmy_gdn_step_fused_f32": (_I, [_P, _I64, _P, _P, _P, _P, _I, _I, _I, _I, _P]),
+    "llmy_gdn_conv_gate": (_I, [_P, _P, _P, _P, _I, _I, _I, _P]),
+    "llmy_rmsnorm_f32_bf16": (_I, [_P, _P, _P, _I, _I, _F, _P]),
+    "llmy_embed_bf16": (_I, [_P, _P, _P, _I, _I, _I, _P]),
+}
+
+_LIB: C.CDLL | None = None
+
+
+def library_path() -> Path:
+    env = os.environ.get("LLMY_LIBRARY")
+    if env:
+        return Path(env)
+    return Path(__file__).resolve().parent / "libllmy.so"
+
+
+def load() -> C.CDLL:
+    """Load libllmy.so once and bind every exported signature."""
+    global _LIB
+    if _LIB is not None:
+        return _LIB
+    path = library_path()
+    if not path.exists():
+        raise RuntimeError(
+            f"libllmy.so not found at {path}; build it with `python -m hybrid_llm_amd._build` "
+            "(or __graft_entry__.build()). There is no CPU fallback.")
+    lib = C.CDLL(str(path))
+    for name, (restype, argtypes) in SIGNATURES.items():
+        fn = getattr(lib, name)  # AttributeError = library/ABI mismatch
+        fn.restype = restype
+        fn.argtypes = argtypes
+    _LIB = lib
+    return lib
+
+
+class LlmyError(RuntimeError):
+    def __init__(self, fn: str, code: int):
+        super().__init__(f"{fn} failed with hipError {code}"
+                         + (" (invalid argument)" if code == 1 else ""))
+        self.code = code
+
+
+def call(name: str, *args) -> None:
+    """Call an entry point and raise LlmyError on a nonzero status
+    (the reference caller's rule, sample_standalone.py:3059-3063)."""
+    code = int(getattr(load(), name)(*args))
+    if code != 0:
+        raise LlmyError(name, code)

@@ -1,0 +1,129 @@
+"""Configuration and deterministic synthetic weights for the hybrid block stack.
+
+The block stack is the reference's looped recurrent core with mHC disabled
+(model/model.py:119-126: ``_read`` = identity for one stream, ``_write`` =
+residual add), i.e. a pre-norm residual block
+
+    x <- x + Mixer(RMSNorm(x));  x <- x + MoE(RMSNorm(x))
+
+with mixers alternating banded attention and GDN, looped ``num_loops`` times
+with weights shared across loops and one KV cache / GDN state per
+(loop, layer) (model/model.py:618-687, state namespace ``loop{i}`` at :645).
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+
+import torch
+
+
+@dataclass(frozen=True)
+class HybridConfig:
+    d_model: int
+    layer_kinds: tuple[str, ...]
+    attn_heads: int
+    attn_head_dim: int
+    window: int
+    gdn_heads: int
+    gdn_dk: int
+    gdn_dv: int
+    n_experts: int
+    top_k: int
+    expert_hidden: int
+    vocab: int
+    num_loops: int
+    conv_kernel: int = 4
+    eps: float = 1e-6
+    init_std: float = 0.02
+    decay_logit_init: float = 2.0  # model/layers/gated_deltanet.py:113
+
+    @property
+    def n_layers(self) -> int:
+        return len(self.layer_kinds)
+
+    @property
+    def attn_scale(self) -> float:
+        return 1.0 / math.sqrt(self.attn_head_dim)
+
+    def attn_layers(self) -> list[int]:
+        return [i for i, k in enumerate(self.layer_kinds) if k == "attn"]
+
+    def gdn_layers(self) -> list[int]:
+        return [i for i, k in enumerate(self.layer_kinds) if k == "gdn"]
+
+
+def alternating(n: int) -> tuple[str, ...]:
+    return tuple("attn" if i % 2 == 0 else "gdn" for i in range(n))
+
+
+# random-init small LLMY (CPU reference, fp32).
+C1 = HybridConfig(d_model=256, layer_kinds=alternating(4), attn_heads=4, attn_head_dim=64,
+                  window=128, gdn_heads=4, gdn_dk=64, gdn_dv=64, n_experts=8, top_k=2,
+                  expert_hidden=512, vocab=32000, num_loops=2)
+
+# the bs=64 hybrid-MoE decode step.
+C5 = HybridConfig(d_model=1024, layer_kinds=alternating(12), attn_heads=16, attn_head_dim=64,
+                  window=2048, gdn_heads=16, gdn_dk=64, gdn_dv=64, n_experts=24, top_k=2,
+                  expert_hidden=2048, vocab=32000, num_loops=2)
+
+
+def weight_shapes(cfg: HybridConfig) -> list[tuple[str, tuple[int, ...], str]]:
+    """(name, shape, kind) in generation order; kind in {normal, ones, zeros, decay}."""
+    D, E, Hf = cfg.d_model, cfg.n_experts, cfg.expert_hidden
+    out: list[tuple[str, tuple[int, ...], str]] = [("embed", (cfg.vocab, D), "normal")]
+    for l, kind in enumerate(cfg.layer_kinds):
+        p = f"L{l}."
+        out.append((p + "mix_norm", (D,), "ones"))
+        if kind == "attn":
+            w = cfg.attn_heads * cfg.attn_head_dim
+            out += [(p + "wq", (w, D), "normal"), (p + "wk", (w, D), "normal"),
+                    (p + "wv", (w, D), "normal"), (p + "wo", (D, w), "normal")]
+        else:
+            Hg, dk, dv = cfg.gdn_heads, cfg.gdn_dk, cfg.gdn_dv
+            out += [(p + "wq", (Hg * dk, D), "normal"), (p + "wk", (Hg * dk, D), "normal"),
+                    (p + "wv", (Hg * dv, D), "normal"), (p + "wg", (Hg * dv, D), "normal"),
+                    (p + "wb", (Hg, D), "normal"), (p + "bb", (Hg,), "zeros"),
+                    (p + "wout", (D, Hg * dv), "normal"),
+                    (p + "conv", (D, cfg.conv_kernel), "normal"),
+                    (p + "decay", (Hg,), "decay")]
+        out += [(p + "ffn_norm", (D,), "ones"), (p + "router_norm", (D,), "ones"),
+                (p + "w_router", (E, D), "normal"),
+                (p + "w_gate", (E, Hf, D), "normal"), (p + "w_up", (E, Hf, D), "normal"),
+                (p + "w_down", (E, D, Hf), "normal")]
+    out.append(("final_norm", (D,), "ones"))
+    return out
+
+
+# Parameters kept in fp32 on the device; every other matrix is stored bf16.
+FP32_PARAMS = ("mix_norm", "ffn_norm", "router_norm", "final_norm", "w_router", "bb", "conv",
+               "decay")
+
+
+def is_fp32_param(name: str) -> bool:
+    return name.split(".")[-1] in FP32_PARAMS
+
+
+def init_weights(cfg: HybridConfig, seed: int = 0, device: str | torch.device = "cpu"
+                 ) -> dict[str, torch.Tensor]:
+    """Random-init weights: every matrix N(0, init_std) drawn in ``weight_shapes``
+    order from one generator seeded ``seed`` on ``device``; RMSNorm weights 1,
+    biases 0, GDN decay logits 2.0.  Matrices are rounded to bf16 except the
+    fp32 parameters listed in FP32_PARAMS (the router is fp32 end to end).
+    CPU and GPU generators give different streams: parity tests generate on
+    the CPU and copy to the GPU.
+    """
+    gen = torch.Generator(device=device).manual_seed(seed)
+    weights: dict[str, torch.Tensor] = {}
+    for name, shape, kind in weight_shapes(cfg):
+        if kind == "normal":
+            t = torch.empty(shape, dtype=torch.float32, device=device)
+            t.normal_(0.0, cfg.init_std, generator=gen)
+        elif kind == "ones":
+            t = torch.ones(shape, dtype=torch.float32, device=device)
+        elif kind == "zeros":
+            t = torch.zeros(shape, dtype=torch.float32, device=device)
+        else:
+            t = torch.full(shape, cfg.decay_logit_init, dtype=torch.float32, device=device)
+        weights[name] = t if is_fp32_param(name) else t.to(torch.bfloat16)
+    return weights

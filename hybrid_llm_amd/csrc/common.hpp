@@ -1,0 +1,101 @@
+// Shared device helpers for the gfx950 (CDNA4) kernels of libllmy.
+//
+// Storage conventions used by every kernel in this library:
+//   * bf16 tensors are passed as raw 16-bit words (uint16_t); conversion to
+//     fp32 is a 16-bit shift, conversion back is round-to-nearest-even with
+//     NaN kept quiet (the same rounding torch uses for .to(torch.bfloat16)).
+//   * every buffer is a plain contiguous device allocation owned by the
+//     caller; kernels never allocate.
+//   * wavefronts are 64 lanes wide.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace llmy {
+
+constexpr int kWave = 64;
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ float bf2f(uint16_t v) {
+  return __uint_as_float(static_cast<uint32_t>(v) << 16);
+}
+
+__device__ __forceinline__ uint16_t f2bf(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+__device__ __forceinline__ uint32_t pack_bf2(float a, float b) {
+  return static_cast<uint32_t>(f2bf(a)) | (static_cast<uint32_t>(f2bf(b)) << 16);
+}
+
+// Unpack 8 bf16 held in a 16-byte vector into fp32.
+__device__ __forceinline__ void unpack8(const uint4& v, float* out) {
+  out[0] = __uint_as_float(v.x << 16);
+  out[1] = __uint_as_float(v.x & 0xffff0000u);
+  out[2] = __uint_as_float(v.y << 16);
+  out[3] = __uint_as_float(v.y & 0xffff0000u);
+  out[4] = __uint_as_float(v.z << 16);
+  out[5] = __uint_as_float(v.z & 0xffff0000u);
+  out[6] = __uint_as_float(v.w << 16);
+  out[7] = __uint_as_float(v.w & 0xffff0000u);
+}
+
+__device__ __forceinline__ bf16x8 as_bf16x8(const uint4& v) {
+  return __builtin_bit_cast(bf16x8, v);
+}
+
+// Butterfly reductions across one 64-lane wavefront.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
+  return v;
+}
+
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    uint64_t o = __shfl_xor(v, off, kWave);
+    v = o > v ? o : v;
+  }
+  return v;
+}
+
+// Total-order key for an fp32 value: larger value -> larger key.  NaN (any
+// sign) sorts above +inf, and -0.0 equals +0.0, matching torch's topk/argmax
+// comparison rules.
+__device__ __forceinline__ uint32_t order_key(float f) {
+  if (f != f) return 0xffffffffu;
+  if (f == 0.0f) f = 0.0f;
+  uint32_t u = __float_as_uint(f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// (value, index) packed so that an unsigned max picks the largest value and,
+// among equal values, the lowest index.
+__device__ __forceinline__ uint64_t value_index_key(float f, uint32_t idx) {
+  return (static_cast<uint64_t>(order_key(f)) << 32) | static_cast<uint64_t>(~idx);
+}
+
+__device__ __forceinline__ uint32_t key_index(uint64_t key) {
+  return ~static_cast<uint32_t>(key & 0xffffffffu);
+}
+
+__device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+__device__ __forceinline__ float siluf_(float x) { return x / (1.0f + expf(-x)); }
+
+}  // namespace llmy

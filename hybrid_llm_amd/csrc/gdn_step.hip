@@ -1,0 +1,205 @@
+// Gated delta-rule decode step: one token per (batch, head), fp32 state
+// S [DK, DV] updated in place (model/layers/gated_deltanet.py:140-149):
+//
+//   pred = k^T S;  S <- g S + beta k (v - pred)^T;  o = (q^T S) * gate
+//
+// One 256-thread workgroup per (b, h).  Thread t owns columns
+// [4*(t % (DV/4)), +4) of rows t / (DV/4) + i * RPP (RPP = 1024/DV rows per
+// pass): every state row is read and written as contiguous float4 runs, the
+// state lives in registers between the two reductions (k^T S, then q^T S'),
+// and the reductions over rows go through LDS in a fixed order, so results
+// are deterministic.  The state is read and written exactly once: the kernel
+// is HBM-bound on 2 * DK * DV * 4 bytes per (b, h).
+//
+// Two input layouts:
+//   op:    q, k [B,H,DK] / v, gate [B,H,DV] bf16, beta, g [B,H] fp32 (q, k
+//          already L2-normalised; gate optional);
+//   model: the fused fp32 projection row [q | k | v | gate logits | beta
+//          logits] of the GDN block, from which the kernel applies the
+//          per-head L2 norm of q and k (clamp 1e-12, gated_deltanet.py:128-129),
+//          beta = sigmoid(logit + bias) (:130), gate = sigmoid(logit) (:131) and
+//          g = sigmoid(decay_logit[h]) (:132).
+#include "common.hpp"
+#include "abi_util.hpp"
+
+namespace llmy {
+
+struct GdnStepArgs {
+  const uint16_t *q, *k, *v, *gate;
+  const float *beta, *g;
+  const float* proj;
+  long long proj_ld;
+  const float* beta_bias;
+  const float* decay_logit;
+  float* state;
+  uint16_t* out;
+  int H;
+};
+
+template <int DK, int DV, bool MODEL>
+__global__ __launch_bounds__(256) void gdn_step_kernel(GdnStepArgs a) {
+  constexpr int CPT = DV / 4;        // threads per state row
+  constexpr int RPP = 256 / CPT;     // rows per pass
+  constexpr int NR = DK / RPP;       // rows per thread
+  __shared__ float qs[DK], ks[DK], vs[DV], gs[DV];
+  __shared__ float red[RPP][DV];
+  __shared__ float bg[2];
+
+  const int bh = blockIdx.x;
+  const int b = bh / a.H;
+  const int h = bh - b * a.H;
+  const int t = threadIdx.x;
+  const int c4 = (t % CPT) * 4;
+  const int rg = t / CPT;
+
+  float* S = a.state + static_cast<long long>(bh) * DK * DV;
+  float4 st[NR];
+#pragma unroll
+  for (int i = 0; i < NR; ++i)
+    st[i] = *reinterpret_cast<const float4*>(S + (rg + i * RPP) * DV + c4);
+
+  const int lane = t & 63;
+  const int wave = t >> 6;
+  if (MODEL) {
+    const float* row = a.proj + static_cast<long long>(b) * a.proj_ld;
+    const int HK = a.H * DK, HV = a.H * DV;
+    if (wave < 2) {  // wave 0: q, wave 1: k -> L2 normalised
+      const float* src = row + (wave == 0 ? 0 : HK) + h * DK;
+      float vals[(DK + 63) / 64];
+      float ss = 0.f;
+#pragma unroll
+      for (int i = 0; i < (DK + 63) / 64; ++i) {
+        const int d = lane + 64 * i;
+        vals[i] = d < DK ? src[d] : 0.f;
+        ss += vals[i] * vals[i];
+      }
+      const float r = rsqrtf(fmaxf(wave_sum(ss), 1e-12f));
+      float* dst = wave == 0 ? qs : ks;
+#pragma unroll
+      for (int i = 0; i < (DK + 63) / 64; ++i) {
+        const int d = lane + 64 * i;
+        if (d < DK) dst[d] = vals[i] * r;
+      }
+    } else if (wave == 2) {
+      for (int d = lane; d < DV; d += 64) {
+        vs[d] = row[2 * HK + h * DV + d];
+        gs[d] = sigmoidf_(row[2 * HK + HV + h * DV + d]);
+      }
+    } else if (lane == 0) {
+      bg[0] = sigmoidf_(row[2 * HK + 2 * HV + h] + a.beta_bias[h]);
+      bg[1] = sigmoidf_(a.decay_logit[h]);
+    }
+  } else {
+    const long long qk = static_cast<long long>(bh) * DK;
+    const long long vv = static_cast<long long>(bh) * DV;
+    for (int d = t; d < DK; d += 256) {
+      qs[d] = bf2f(a.q[qk + d]);
+      ks[d] = bf2f(a.k[qk + d]);
+    }
+    for (int d = t; d < DV; d += 256) {
+      vs[d] = bf2f(a.v[vv + d]);
+      gs[d] = a.gate ? bf2f(a.gate[vv + d]) : 1.f;
+    }
+    if (t == 0) {
+      bg[0] = a.beta[bh];
+      bg[1] = a.g[bh];
+    }
+  }
+  __syncthreads();
+
+  // pred = k^T S (partial over this thread's rows, then a fixed-order LDS sum)
+  float4 pp = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+  for (int i = 0; i < NR; ++i) {
+    const float kr = ks[rg + i * RPP];
+    pp.x = fmaf(kr, st[i].x, pp.x);
+    pp.y = fmaf(kr, st[i].y, pp.y);
+    pp.z = fmaf(kr, st[i].z, pp.z);
+    pp.w = fmaf(kr, st[i].w, pp.w);
+  }
+  *reinterpret_cast<float4*>(&red[rg][c4]) = pp;
+  __syncthreads();
+  __shared__ float delta[DV];
+  if (t < DV) {
+    float pred = 0.f;
+#pragma unroll 8
+    for (int r = 0; r < RPP; ++r) pred += red[r][t];
+    delta[t] = vs[t] - pred;
+  }
+  __syncthreads();
+
+  const float beta = bg[0];
+  const float g = bg[1];
+  const float4 dl = *reinterpret_cast<const float4*>(&delta[c4]);
+  float4 op = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+  for (int i = 0; i < NR; ++i) {
+    const int r = rg + i * RPP;
+    const float bk = beta * ks[r];
+    float4 sn;
+    sn.x = fmaf(g, st[i].x, bk * dl.x);
+    sn.y = fmaf(g, st[i].y, bk * dl.y);
+    sn.z = fmaf(g, st[i].z, bk * dl.z);
+    sn.w = fmaf(g, st[i].w, bk * dl.w);
+    *reinterpret_cast<float4*>(S + r * DV + c4) = sn;
+    const float qr = qs[r];
+    op.x = fmaf(qr, sn.x, op.x);
+    op.y = fmaf(qr, sn.y, op.y);
+    op.z = fmaf(qr, sn.z, op.z);
+    op.w = fmaf(qr, sn.w, op.w);
+  }
+  *reinterpret_cast<float4*>(&red[rg][c4]) = op;
+  __syncthreads();
+  if (t < DV) {
+    float o = 0.f;
+#pragma unroll 8
+    for (int r = 0; r < RPP; ++r) o += red[r][t];
+    a.out[static_cast<long long>(bh) * DV + t] = f2bf(o * gs[t]);
+  }
+}
+
+template <bool MODEL>
+static int32_t launch_gdn_step(const GdnStepArgs& a, int B, int dk, int dv, hipStream_t s) {
+  const dim3 grid(B * a.H), block(256);
+  if (dk == 64 && dv == 64) {
+    hipLaunchKernelGGL((gdn_step_kernel<64, 64, MODEL>), grid, block, 0, s, a);
+  } else if (dk == 128 && dv == 128) {
+    hipLaunchKernelGGL((gdn_step_kernel<128, 128, MODEL>), grid, block, 0, s, a);
+  } else {
+    return static_cast<int32_t>(hipErrorInvalidValue);
+  }
+  return launch_status();
+}
+
+}  // namespace llmy
+
+using namespace llmy;
+
+extern "C" int32_t llmy_gdn_step_bf16(const llmy_bf16* q, const llmy_bf16* k, const llmy_bf16* v,
+                                      const float* beta, const float* g, const llmy_bf16* gate,
+                                      float* state, llmy_bf16* out, int32_t B, int32_t H,
+                                      int32_t dk, int32_t dv, void* stream) {
+  LLMY_REQUIRE(B >= 0 && H > 0 && ((dk == 64 && dv == 64) || (dk == 128 && dv == 128)));
+  if (B == 0) return 0;
+  LLMY_REQUIRE(q && k && v && beta && g && state && out);
+  LLMY_REQUIRE(aligned(state, 16));
+  GdnStepArgs a{};
+  a.q = q; a.k = k; a.v = v; a.gate = gate; a.beta = beta; a.g = g;
+  a.state = state; a.out = out; a.H = H;
+  return launch_gdn_step<false>(a, B, dk, dv, as_stream(stream));
+}
+
+extern "C" int32_t llmy_gdn_step_fused_f32(const float* proj, int64_t proj_ld,
+                                           const float* beta_bias, const float* decay_logit,
+                                           float* state, llmy_bf16* out, int32_t B, int32_t H,
+                                           int32_t dk, int32_t dv, void* stream) {
+  LLMY_REQUIRE(B >= 0 && H > 0 && ((dk == 64 && dv == 64) || (dk == 128 && dv == 128)));
+  LLMY_REQUIRE(proj_ld >= static_cast<int64_t>(H) * (2 * dk + 2 * dv + 1));
+  if (B == 0) return 0;
+  LLMY_REQUIRE(proj && beta_bias && decay_logit && state && out);
+  LLMY_REQUIRE(aligned(state, 16));
+  GdnStepArgs a{};
+  a.proj = proj; a.proj_ld = proj_ld; a.beta_bias = beta_bias; a.decay_logit = decay_logit;
+  a.state = state; a.out = out; a.H = H;
+  return launch_gdn_step<true>(a, B, dk, dv, as_stream(stream));
+}

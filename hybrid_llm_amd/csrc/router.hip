@@ -1,0 +1,283 @@
+// MoE router (fp32 logits -> top-k -> softmax over the k values) and the
+// expert-major token permutation (stable counting sort of the routes).
+//
+// Router semantics follow model/layers/context_router.py:62,71-74 with the
+// context-aware branch off: logits = RMSNorm(x) . W_r^T in fp32, top-k by
+// value, gates = softmax of the k selected values.  Ties resolve to the lower
+// expert index (the reference's torch.topk leaves this unspecified).
+//
+// Permutation semantics follow model/layers/moe.py:39-66 (flat route id
+// r = t*k + j, grouped by expert, counts = bincount, offsets = exclusive
+// cumsum) with the order inside an expert pinned to ascending r, i.e. the
+// order of a stable sort of the expert ids.
+#include "common.hpp"
+#include "abi_util.hpp"
+
+namespace llmy {
+
+// One wavefront per token, four tokens per 256-thread block.  The normalised
+// row is staged in LDS (D floats per wave) so every expert's dot product reads
+// it from LDS while the fp32 router matrix streams through L2.
+__global__ __launch_bounds__(256) void router_topk_bf16_kernel(
+    const uint16_t* __restrict__ x, const float* __restrict__ norm_w,
+    const float* __restrict__ w, float* __restrict__ logits_out,
+    int32_t* __restrict__ idx_out, float* __restrict__ gates_out,
+    int T, int D, int E, int k, float eps) {
+  extern __shared__ float lds[];
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * 4 + wave;
+  if (t >= T) return;
+  float* h = lds + static_cast<size_t>(wave) * D;
+  const uint16_t* xr = x + static_cast<size_t>(t) * D;
+
+  // Stage the row and accumulate sum of squares (fp32, as norms.py:14).
+  float ss = 0.0f;
+  for (int d = lane * 4; d < D; d += 256) {
+    const uint2 raw = *reinterpret_cast<const uint2*>(xr + d);
+    const float v0 = __uint_as_float(raw.x << 16);
+    const float v1 = __uint_as_float(raw.x & 0xffff0000u);
+    const float v2 = __uint_as_float(raw.y << 16);
+    const float v3 = __uint_as_float(raw.y & 0xffff0000u);
+    h[d] = v0; h[d + 1] = v1; h[d + 2] = v2; h[d + 3] = v3;
+    ss += v0 * v0 + v1 * v1 + v2 * v2 + v3 * v3;
+  }
+  if (norm_w != nullptr) {
+    const float r = rsqrtf(wave_sum(ss) / static_cast<float>(D) + eps);
+    for (int d = lane * 4; d < D; d += 256) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) h[d + j] = (h[d + j] * r) * norm_w[d + j];
+    }
+  }
+  __builtin_amdgcn_wave_barrier();
+
+  // Logits: lane (e mod 64) ends up holding logit e for its slot e / 64.
+  float mine[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int e = 0; e < E; ++e) {
+    const float* wr = w + static_cast<size_t>(e) * D;
+    float acc = 0.0f;
+    for (int d = lane * 4; d < D; d += 256) {
+      const float4 wv = *reinterpret_cast<const float4*>(wr + d);
+      acc = fmaf(h[d], wv.x, acc);
+      acc = fmaf(h[d + 1], wv.y, acc);
+      acc = fmaf(h[d + 2], wv.z, acc);
+      acc = fmaf(h[d + 3], wv.w, acc);
+    }
+    acc = wave_sum(acc);
+    if ((e & 63) == lane) mine[e >> 6] = acc;
+  }
+  if (logits_out != nullptr) {
+    for (int s = 0; s < 4; ++s) {
+      const int e = lane + 64 * s;
+      if (e < E) logits_out[static_cast<size_t>(t) * E + e] = mine[s];
+    }
+  }
+
+  // k rounds of (value, lowest index) argmax over the remaining experts.
+  uint64_t keys[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    const int e = lane + 64 * s;
+    keys[s] = (e < E) ? value_index_key(mine[s], static_cast<uint32_t>(e)) : 0ull;
+  }
+  float top_val[32];
+  int top_idx[32];
+  for (int j = 0; j < k; ++j) {
+    uint64_t best = keys[0];
+#pragma unroll
+    for (int s = 1; s < 4; ++s) best = keys[s] > best ? keys[s] : best;
+    best = wave_max_u64(best);
+    const int e = static_cast<int>(key_index(best));
+    top_idx[j] = e;
+    top_val[j] = __shfl(mine[e >> 6], e & 63, kWave);
+    if ((e & 63) == lane) keys[e >> 6] = 0ull;
+  }
+  if (lane == 0) {
+    const float m = top_val[0];
+    float ex[32];
+    float sum = 0.0f;
+    for (int j = 0; j < k; ++j) {
+      ex[j] = expf(top_val[j] - m);
+      sum += ex[j];
+    }
+    const float inv = 1.0f / sum;
+    for (int j = 0; j < k; ++j) {
+      idx_out[static_cast<size_t>(t) * k + j] = top_idx[j];
+      gates_out[static_cast<size_t>(t) * k + j] = ex[j] * inv;
+    }
+  }
+}
+
+// Top-k + softmax from precomputed fp32 logits [T, E]; one wavefront per token.
+__global__ __launch_bounds__(256) void router_topk_from_logits_kernel(
+    const float* __restrict__ logits, int32_t* __restrict__ idx_out,
+    float* __restrict__ gates_out, int T, int E, int k) {
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * 4 + wave;
+  if (t >= T) return;
+  float mine[4];
+  uint64_t keys[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    const int e = lane + 64 * s;
+    mine[s] = (e < E) ? logits[static_cast<size_t>(t) * E + e] : 0.0f;
+    keys[s] = (e < E) ? value_index_key(mine[s], static_cast<uint32_t>(e)) : 0ull;
+  }
+  float top_val[32];
+  int top_idx[32];
+  for (int j = 0; j < k; ++j) {
+    uint64_t best = keys[0];
+#pragma unroll
+    for (int s = 1; s < 4; ++s) best = keys[s] > best ? keys[s] : best;
+    best = wave_max_u64(best);
+    const int e = static_cast<int>(key_index(best));
+    top_idx[j] = e;
+    top_val[j] = __shfl(mine[e >> 6], e & 63, kWave);
+    if ((e & 63) == lane) keys[e >> 6] = 0ull;
+  }
+  if (lane == 0) {
+    const float m = top_val[0];
+    float ex[32];
+    float sum = 0.0f;
+    for (int j = 0; j < k; ++j) {
+      ex[j] = expf(top_val[j] - m);
+      sum += ex[j];
+    }
+    const float inv = 1.0f / sum;
+    for (int j = 0; j < k; ++j) {
+      idx_out[static_cast<size_t>(t) * k + j] = top_idx[j];
+      gates_out[static_cast<size_t>(t) * k + j] = ex[j] * inv;
+    }
+  }
+}
+
+// Stable counting sort of n = T*k expert ids in [0, E) with one 1024-thread
+// workgroup.  Wave w owns a contiguous run of 64-route chunks, so walking the
+// waves in order and the chunks in order visits routes in ascending r.
+//   pass 1: per-wave expert histograms (LDS integer atomics: order-free);
+//   scan:   expert offsets and per-wave bases;
+//   pass 2: each chunk ranks its lanes per expert with ballots and places
+//           route r at offsets[e] + (routes of e before r).
+// Routes with an id outside [0, E) are not placed (callers pass router
+// output, which is always in range).
+constexpr int kPermuteWaves = 16;
+
+__global__ __launch_bounds__(1024) void moe_permute_kernel(
+    const int32_t* __restrict__ expert_ids, int n, int E,
+    int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
+    int32_t* __restrict__ sorted_routes, int32_t* __restrict__ route_pos) {
+  extern __shared__ int32_t cnt[];  // [kPermuteWaves][E], then offsets[E+1]
+  int32_t* offs = cnt + kPermuteWaves * E;
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  for (int i = threadIdx.x; i < kPermuteWaves * E; i += blockDim.x) cnt[i] = 0;
+  __syncthreads();
+
+  const int nchunks = (n + 63) / 64;
+  const int per_wave = (nchunks + kPermuteWaves - 1) / kPermuteWaves;
+  const int c0 = wave * per_wave;
+  const int c1 = min(nchunks, c0 + per_wave);
+  for (int c = c0; c < c1; ++c) {
+    const int r = c * 64 + lane;
+    if (r < n) {
+      const int e = expert_ids[r];
+      if (e >= 0 && e < E) atomicAdd(&cnt[wave * E + e], 1);
+    }
+  }
+  __syncthreads();
+
+  // Per-expert totals and per-wave exclusive bases (serial over 16 waves).
+  for (int e = threadIdx.x; e < E; e += blockDim.x) {
+    int run = 0;
+    for (int w = 0; w < kPermuteWaves; ++w) {
+      const int c = cnt[w * E + e];
+      cnt[w * E + e] = run;
+      run += c;
+    }
+    offs[e] = run;  // total for now
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int run = 0;
+    for (int e = 0; e < E; ++e) {
+      const int c = offs[e];
+      counts[e] = c;
+      offs[e] = run;
+      offsets[e] = run;
+      run += c;
+    }
+    offs[E] = run;
+    offsets[E] = run;
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < kPermuteWaves * E; i += blockDim.x) cnt[i] += offs[i % E];
+  __syncthreads();
+
+  int32_t* running = cnt + wave * E;
+  for (int c = c0; c < c1; ++c) {
+    const int r = c * 64 + lane;
+    int e = -1;
+    if (r < n) {
+      e = expert_ids[r];
+      if (e < 0 || e >= E) e = -1;
+    }
+    uint64_t pending = __ballot(e >= 0);
+    while (pending) {
+      const int leader = __builtin_ctzll(pending);
+      const int le = __shfl(e, leader, kWave);
+      const uint64_t same = __ballot(e == le);
+      if (e == le) {
+        const uint64_t below = same & ((1ull << lane) - 1ull);
+        const int pos = running[le] + __popcll(below);
+        sorted_routes[pos] = r;
+        route_pos[r] = pos;
+      }
+      __builtin_amdgcn_wave_barrier();
+      if (lane == leader) running[le] += __popcll(same);
+      __builtin_amdgcn_wave_barrier();
+      pending &= ~same;
+    }
+  }
+}
+
+}  // namespace llmy
+
+using namespace llmy;
+
+extern "C" int32_t llmy_router_topk_bf16(const uint16_t* x, const float* norm_w,
+                                         const float* w_router, float* logits_out, int32_t* idx,
+                                         float* gates, int32_t T, int32_t D, int32_t E, int32_t k,
+                                         float eps, void* stream) {
+  LLMY_REQUIRE(T >= 0 && D > 0 && D % 4 == 0 && D <= 8192);
+  LLMY_REQUIRE(E > 0 && E <= 256 && k > 0 && k <= 32 && k <= E);
+  if (T == 0) return 0;
+  LLMY_REQUIRE(x && w_router && idx && gates);
+  LLMY_REQUIRE(aligned(x, 8) && aligned(w_router, 16) && (norm_w == nullptr || aligned(norm_w, 4)));
+  const size_t lds = 4 * static_cast<size_t>(D) * sizeof(float);
+  hipLaunchKernelGGL(router_topk_bf16_kernel, dim3((T + 3) / 4), dim3(256), lds,
+                     as_stream(stream), x, norm_w, w_router, logits_out, idx, gates, T, D, E, k,
+                     eps);
+  return launch_status();
+}
+
+extern "C" int32_t llmy_router_topk_logits_f32(const float* logits, int32_t* idx, float* gates,
+                                               int32_t T, int32_t E, int32_t k, void* stream) {
+  LLMY_REQUIRE(T >= 0 && E > 0 && E <= 256 && k > 0 && k <= 32 && k <= E);
+  if (T == 0) return 0;
+  LLMY_REQUIRE(logits && idx && gates);
+  hipLaunchKernelGGL(router_topk_from_logits_kernel, dim3((T + 3) / 4), dim3(256), 0,
+                     as_stream(stream), logits, idx, gates, T, E, k);
+  return launch_status();
+}
+
+extern "C" int32_t llmy_moe_permute(const int32_t* expert_ids, int32_t n_routes, int32_t E,
+                                    int32_t* counts, int32_t* offsets, int32_t* sorted_routes,
+                                    int32_t* route_pos, void* stream) {
+  LLMY_REQUIRE(counts && offsets && n_routes >= 0 && E > 0 && E <= 1024);
+  LLMY_REQUIRE(n_routes == 0 || (expert_ids && sorted_routes && route_pos));
+  const size_t lds = (static_cast<size_t>(kPermuteWaves) * E + E + 1) * sizeof(int32_t);
+  hipLaunchKernelGGL(moe_permute_kernel, dim3(1), dim3(1024), lds, as_stream(stream), expert_ids,
+                     n_routes, E, counts, offsets, sorted_routes, route_pos);
+  return launch_status();
+}

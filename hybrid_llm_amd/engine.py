@@ -1,0 +1,205 @@
+"""Batched decode engine for the looped hybrid block stack on one MI355X.
+
+Host orchestration in Python over the libllmy kernels (the reference's native
+per-token step is llmy_cuda/src/model.cpp:1774-1935, batch 1 only; this one
+decodes B sequences per step).  All device buffers — packed weights, per
+(loop, layer) KV caches and GDN states, and every activation/scratch buffer —
+are allocated once at construction, so ``step()`` enqueues kernels only and
+the whole step can be captured into one HIP graph (``capture()``/``replay()``).
+
+Packed weight layouts (built from the per-matrix weights of
+``hybrid_llm_amd.config.init_weights``):
+  * attention: wqkv [3*H*hd, D] = cat(wq, wk, wv); wo [D, H*hd];
+  * GDN: wproj [N16, D] = cat(wq, wk, wv, wg, wb) padded with zero rows to a
+    multiple of 16; the step kernel reads the fp32 projection row in place;
+  * MoE: w_gate_up [E, 2H, D] = cat(w_gate, w_up, dim=1) (the reference's
+    packing, llmy_cuda/include/llmy.h:80-82); w_down [E, D, H].
+State layouts: KV caches [B, H, W, hd] bf16 (ring buffer, head-major);
+GDN states [B, H, dk, dv] fp32; conv histories [B, K-1, D] bf16.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import ops
+from .config import HybridConfig
+
+
+def _pad_rows(w: torch.Tensor, mult: int) -> torch.Tensor:
+    n = w.shape[0]
+    pad = (-n) % mult
+    if pad == 0:
+        return w
+    return torch.cat([w, torch.zeros(pad, *w.shape[1:], dtype=w.dtype, device=w.device)], 0)
+
+
+class HybridDecoder:
+    def __init__(self, cfg: HybridConfig, weights: dict[str, torch.Tensor], batch: int,
+                 device: str | torch.device = "cuda"):
+        self.cfg = cfg
+        self.B = batch
+        self.dev = torch.device(device)
+        dev = self.dev
+        D, B = cfg.d_model, batch
+
+        def up(name, dtype=None):
+            t = weights[name]
+            return t.to(device=dev, dtype=dtype or t.dtype).contiguous()
+
+        self.w: dict[str, torch.Tensor] = {"embed": up("embed"), "final_norm": up("final_norm")}
+        for l, kind in enumerate(cfg.layer_kinds):
+            p = f"L{l}."
+            self.w[p + "mix_norm"] = up(p + "mix_norm")
+            if kind == "attn":
+                self.w[p + "wqkv"] = torch.cat([up(p + "wq"), up(p + "wk"), up(p + "wv")], 0)
+                self.w[p + "wo"] = up(p + "wo")
+            else:
+                wproj = torch.cat([up(p + n) for n in ("wq", "wk", "wv", "wg", "wb")], 0)
+                self.w[p + "wproj"] = _pad_rows(wproj, 16).contiguous()
+                self.w[p + "wout"] = up(p + "wout")
+                self.w[p + "bb"] = up(p + "bb")
+                self.w[p + "conv"] = up(p + "conv")
+                self.w[p + "decay"] = up(p + "decay")
+            self.w[p + "ffn_norm"] = up(p + "ffn_norm")
+            self.w[p + "router_norm"] = up(p + "router_norm")
+            self.w[p + "w_router"] = up(p + "w_router")
+            self.w[p + "w_gate_up"] = torch.cat([up(p + "w_gate"), up(p + "w_up")], 1).contiguous()
+            self.w[p + "w_down"] = up(p + "w_down")
+
+        # ---- state
+        self.pos = torch.zeros(B, dtype=torch.int32, device=dev)
+        self.state: dict = {}
+        for loop in range(cfg.num_loops):
+            for l, kind in enumerate(cfg.layer_kinds):
+                if kind == "attn":
+                    shape = (B, cfg.attn_heads, cfg.window, cfg.attn_head_dim)
+                    self.state[(loop, l)] = {
+                        "k": torch.zeros(shape, dtype=torch.bfloat16, device=dev),
+                        "v": torch.zeros(shape, dtype=torch.bfloat16, device=dev)}
+                else:
+                    self.state[(loop, l)] = {
+                        "S": torch.zeros(B, cfg.gdn_heads, cfg.gdn_dk, cfg.gdn_dv,
+                                         dtype=torch.float32, device=dev),
+                        "hist": torch.zeros(B, cfg.conv_kernel - 1, D, dtype=torch.bfloat16,
+                                            device=dev)}
+
+        # ---- activations / scratch (allocated once)
+        f32, bf = torch.float32, torch.bfloat16
+        Ha, hd = cfg.attn_heads, cfg.attn_head_dim
+        Hg, dk, dv = cfg.gdn_heads, cfg.gdn_dk, cfg.gdn_dv
+        k, E, Hf = cfg.top_k, cfg.n_experts, cfg.expert_hidden
+        nproj = self.w[f"L{cfg.gdn_layers()[0]}.wproj"].shape[0] if cfg.gdn_layers() else 16
+        self.buf = {
+            "tokens": torch.zeros(B, dtype=torch.int32, device=dev),
+            "x": torch.zeros(B, D, dtype=f32, device=dev),
+            "h": torch.zeros(B, D, dtype=bf, device=dev),
+            "qkv": torch.zeros(B, 3 * Ha * hd, dtype=bf, device=dev),
+            "ao": torch.zeros(B, Ha, hd, dtype=bf, device=dev),
+            "proj": torch.zeros(B, nproj, dtype=f32, device=dev),
+            "go": torch.zeros(B, Hg * dv, dtype=bf, device=dev),
+            "cg": torch.zeros(B, D, dtype=f32, device=dev),
+            "idx": torch.zeros(B, k, dtype=torch.int32, device=dev),
+            "gates": torch.zeros(B, k, dtype=f32, device=dev),
+            "counts": torch.zeros(E, dtype=torch.int32, device=dev),
+            "offsets": torch.zeros(E + 1, dtype=torch.int32, device=dev),
+            "sorted_routes": torch.zeros(B * k, dtype=torch.int32, device=dev),
+            "route_pos": torch.zeros(B * k, dtype=torch.int32, device=dev),
+            "act": torch.zeros(B * k, Hf, dtype=bf, device=dev),
+            "y": torch.zeros(B * k, D, dtype=f32, device=dev),
+            "logits": torch.zeros(B, cfg.vocab, dtype=f32, device=dev),
+            "next": torch.zeros(B, dtype=torch.int32, device=dev),
+        }
+        self.graph: torch.cuda.CUDAGraph | None = None
+
+    # ------------------------------------------------------------------ blocks
+    def _attn(self, l: int, st: dict) -> None:
+        cfg, w, b = self.cfg, self.w, self.buf
+        p = f"L{l}."
+        Hhd = cfg.attn_heads * cfg.attn_head_dim
+        B, H, hd = self.B, cfg.attn_heads, cfg.attn_head_dim
+        ops.linear(b["h"], w[p + "wqkv"], out=b["qkv"])
+        qkv = b["qkv"]
+        q = qkv[:, :Hhd].view(B, H, hd)
+        kn = qkv[:, Hhd:2 * Hhd].view(B, H, hd)
+        vn = qkv[:, 2 * Hhd:].view(B, H, hd)
+        ops.banded_attn_decode(q, kn, vn, st["k"], st["v"], self.pos, cfg.attn_scale,
+                               out=b["ao"])
+        ops.linear(b["ao"].view(B, Hhd), w[p + "wo"], out=b["x"], epilogue=ops.EPI_RESID_ADD)
+
+    def _gdn(self, l: int, st: dict) -> None:
+        w, b = self.w, self.buf
+        p = f"L{l}."
+        ops.linear(b["h"], w[p + "wproj"], out=b["proj"], epilogue=ops.EPI_STORE_F32)
+        ops.gdn_step_fused(b["proj"], w[p + "bb"], w[p + "decay"], st["S"], out=b["go"])
+        ops.gdn_conv_gate(b["h"], st["hist"], w[p + "conv"], out=b["cg"])
+        ops.linear(b["go"], w[p + "wout"], out=b["x"], epilogue=ops.EPI_RESID_GATED, aux=b["cg"])
+
+    def _moe(self, l: int) -> None:
+        cfg, w, b = self.cfg, self.w, self.buf
+        p = f"L{l}."
+        ops.rmsnorm(b["x"], w[p + "ffn_norm"], cfg.eps, out=b["h"])
+        from . import _lib
+        s = torch.cuda.current_stream().cuda_stream
+        _lib.call("llmy_router_topk_bf16", b["h"].data_ptr(), w[p + "router_norm"].data_ptr(),
+                  w[p + "w_router"].data_ptr(), None, b["idx"].data_ptr(), b["gates"].data_ptr(),
+                  self.B, cfg.d_model, cfg.n_experts, cfg.top_k, cfg.eps, s)
+        _lib.call("llmy_moe_permute", b["idx"].data_ptr(), self.B * cfg.top_k, cfg.n_experts,
+                  b["counts"].data_ptr(), b["offsets"].data_ptr(), b["sorted_routes"].data_ptr(),
+                  b["route_pos"].data_ptr(), s)
+        perm = {"offsets": b["offsets"], "sorted_routes": b["sorted_routes"]}
+        ops.moe_experts(b["h"], perm, b["gates"], w[p + "w_gate_up"], w[p + "w_down"],
+                        act=b["act"], y=b["y"])
+        ops.moe_combine(b["y"], b["route_pos"], self.B, cfg.top_k, out=b["x"],
+                        mode=ops.MOE_OUT_RESID)
+
+    # ------------------------------------------------------------------ step
+    def _step_body(self) -> None:
+        cfg, w, b = self.cfg, self.w, self.buf
+        ops.embed(b["tokens"], w["embed"], out=b["x"])
+        for loop in range(cfg.num_loops):
+            for l, kind in enumerate(cfg.layer_kinds):
+                ops.rmsnorm(b["x"], w[f"L{l}.mix_norm"], cfg.eps, out=b["h"])
+                if kind == "attn":
+                    self._attn(l, self.state[(loop, l)])
+                else:
+                    self._gdn(l, self.state[(loop, l)])
+                self._moe(l)
+        ops.rmsnorm(b["x"], w["final_norm"], cfg.eps, out=b["h"])
+        ops.linear(b["h"], w["embed"], out=b["logits"], epilogue=ops.EPI_STORE_F32)
+        from . import _lib
+        _lib.call("llmy_sample_argmax_f32", b["logits"].data_ptr(), self.B, cfg.vocab,
+                  b["next"].data_ptr(), torch.cuda.current_stream().cuda_stream)
+        self.pos.add_(1)
+
+    def step(self, tokens: torch.Tensor | None = None) -> torch.Tensor:
+        """Decode one token for every sequence.  ``tokens`` [B] int32 (device or
+        host) is copied into the static input buffer; returns the logits buffer."""
+        if tokens is not None:
+            self.buf["tokens"].copy_(tokens.to(torch.int32).view(-1))
+        if self.graph is not None:
+            self.graph.replay()
+        else:
+            self._step_body()
+        return self.buf["logits"]
+
+    def capture(self) -> None:
+        """Capture one step (embedding .. argmax, pos += 1) into a HIP graph.
+        Capturing runs nothing, so the state is unchanged."""
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            with torch.cuda.graph(g, stream=s):
+                self._step_body()
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        self.graph = g
+
+    # ------------------------------------------------------------------ state io
+    def load_state(self, pos: torch.Tensor, state: dict) -> None:
+        """Copy a host state (the oracle's layout) into the device buffers."""
+        self.pos.copy_(pos.to(torch.int32))
+        for key, st in self.state.items():
+            for name, t in st.items():
+                t.copy_(state[key][name].to(t.dtype))

@@ -1,0 +1,259 @@
+"""Torch-facing wrappers over the libllmy C ABI.
+
+Each op checks device, dtype, contiguity and shape on the host, allocates its
+outputs with torch (device memory is plumbing; kernels never allocate), and
+launches on torch's current HIP stream.  A failed launch raises; there is no
+eager/CPU fallback.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _check(t: torch.Tensor, dtype: torch.dtype, name: str, shape: tuple | None = None) -> None:
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be a GPU tensor")
+    if t.dtype != dtype:
+        raise ValueError(f"{name} must be {dtype}, got {t.dtype}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    if shape is not None and tuple(t.shape) != tuple(shape):
+        raise ValueError(f"{name} shape {tuple(t.shape)} != expected {tuple(shape)}")
+
+
+# --------------------------------------------------------------------------- router
+def router_topk(x: torch.Tensor, w_router: torch.Tensor, k: int,
+                norm_w: torch.Tensor | None = None, eps: float = 1e-6,
+                return_logits: bool = False):
+    """(idx [T,k] int32, gates [T,k] fp32[, logits [T,E] fp32]) for bf16 x [T,D]."""
+    T, D = x.shape
+    E = w_router.shape[0]
+    _check(x, torch.bfloat16, "x")
+    _check(w_router, torch.float32, "w_router", (E, D))
+    if norm_w is not None:
+        _check(norm_w, torch.float32, "norm_w", (D,))
+    idx = torch.empty(T, k, dtype=torch.int32, device=x.device)
+    gates = torch.empty(T, k, dtype=torch.float32, device=x.device)
+    logits = torch.empty(T, E, dtype=torch.float32, device=x.device) if return_logits else None
+    _lib.call("llmy_router_topk_bf16", _ptr(x), _ptr(norm_w), _ptr(w_router), _ptr(logits),
+              _ptr(idx), _ptr(gates), T, D, E, k, eps, _stream())
+    return (idx, gates, logits) if return_logits else (idx, gates)
+
+
+def router_topk_from_logits(logits: torch.Tensor, k: int):
+    T, E = logits.shape
+    _check(logits, torch.float32, "logits")
+    idx = torch.empty(T, k, dtype=torch.int32, device=logits.device)
+    gates = torch.empty(T, k, dtype=torch.float32, device=logits.device)
+    _lib.call("llmy_router_topk_logits_f32", _ptr(logits), _ptr(idx), _ptr(gates), T, E, k,
+              _stream())
+    return idx, gates
+
+
+def moe_permute(expert_ids: torch.Tensor, num_experts: int):
+    """Stable expert-major permutation of flat routes; returns a dict of int32
+    tensors: counts [E], offsets [E+1], sorted_routes [n], route_pos [n]."""
+    _check(expert_ids, torch.int32, "expert_ids")
+    n = expert_ids.numel()
+    dev = expert_ids.device
+    out = {
+        "counts": torch.empty(num_experts, dtype=torch.int32, device=dev),
+        "offsets": torch.empty(num_experts + 1, dtype=torch.int32, device=dev),
+        "sorted_routes": torch.empty(n, dtype=torch.int32, device=dev),
+        "route_pos": torch.empty(n, dtype=torch.int32, device=dev),
+    }
+    _lib.call("llmy_moe_permute", _ptr(expert_ids), n, num_experts, _ptr(out["counts"]),
+              _ptr(out["offsets"]), _ptr(out["sorted_routes"]), _ptr(out["route_pos"]),
+              _stream())
+    return out
+
+
+# --------------------------------------------------------------------------- sampling
+def argmax(logits: torch.Tensor) -> torch.Tensor:
+    R, V = logits.shape
+    _check(logits, torch.float32, "logits")
+    out = torch.empty(R, dtype=torch.int32, device=logits.device)
+    _lib.call("llmy_sample_argmax_f32", _ptr(logits), R, V, _ptr(out), _stream())
+    return out
+
+
+# --------------------------------------------------------------------------- projections
+EPI_STORE_BF16, EPI_STORE_F32, EPI_RESID_ADD, EPI_RESID_GATED = 0, 1, 2, 3
+
+
+def linear(x: torch.Tensor, w: torch.Tensor, out: torch.Tensor | None = None,
+           epilogue: int = EPI_STORE_BF16, aux: torch.Tensor | None = None) -> torch.Tensor:
+    """x [M,K] bf16 . w [N,K]^T with a fused epilogue (see llmy_linear_bf16)."""
+    M, K = x.shape
+    N = w.shape[0]
+    _check(x, torch.bfloat16, "x")
+    _check(w, torch.bfloat16, "w", (N, K))
+    if out is None:
+        if epilogue not in (EPI_STORE_BF16, EPI_STORE_F32):
+            raise ValueError("residual epilogues need an explicit out tensor")
+        dt = torch.bfloat16 if epilogue == EPI_STORE_BF16 else torch.float32
+        out = torch.empty(M, N, dtype=dt, device=x.device)
+    else:
+        _check(out, torch.bfloat16 if epilogue == EPI_STORE_BF16 else torch.float32, "out", (M, N))
+    if aux is not None:
+        _check(aux, torch.float32, "aux", (M, N))
+    _lib.call("llmy_linear_bf16", _ptr(x), _ptr(w), _ptr(out), _ptr(aux), M, N, K, epilogue,
+              _stream())
+    return out
+
+
+# --------------------------------------------------------------------------- MoE
+def moe_experts(x: torch.Tensor, perm: dict, gates: torch.Tensor, w_gate_up: torch.Tensor,
+                w_down: torch.Tensor, act: torch.Tensor | None = None,
+                y: torch.Tensor | None = None):
+    """Routed SwiGLU experts over the permuted routes; returns (act, y)."""
+    T, D = x.shape
+    E, H2, D2 = w_gate_up.shape
+    H = H2 // 2
+    k = gates.shape[-1]
+    _check(x, torch.bfloat16, "x")
+    _check(w_gate_up, torch.bfloat16, "w_gate_up", (E, 2 * H, D))
+    _check(w_down, torch.bfloat16, "w_down", (E, D, H))
+    _check(gates, torch.float32, "gates", (T, k))
+    n = T * k
+    if act is None:
+        act = torch.empty(n, H, dtype=torch.bfloat16, device=x.device)
+    if y is None:
+        y = torch.empty(n, D, dtype=torch.float32, device=x.device)
+    _check(act, torch.bfloat16, "act", (n, H))
+    _check(y, torch.float32, "y", (n, D))
+    _lib.call("llmy_moe_experts_bf16", _ptr(x), _ptr(perm["offsets"]), _ptr(perm["sorted_routes"]),
+              _ptr(gates), _ptr(w_gate_up), _ptr(w_down), _ptr(act), _ptr(y), T, D, H, E, k,
+              _stream())
+    return act, y
+
+
+MOE_OUT_BF16, MOE_OUT_F32, MOE_OUT_RESID = 0, 1, 2
+
+
+def moe_combine(y: torch.Tensor, route_pos: torch.Tensor, T: int, k: int,
+                out: torch.Tensor | None = None, mode: int = MOE_OUT_BF16) -> torch.Tensor:
+    D = y.shape[1]
+    _check(y, torch.float32, "y", (T * k, D))
+    if out is None:
+        out = torch.empty(T, D, dtype=torch.bfloat16 if mode == MOE_OUT_BF16 else torch.float32,
+                          device=y.device)
+    _lib.call("llmy_moe_combine", _ptr(y), _ptr(route_pos), _ptr(out), T, D, k, mode, _stream())
+    return out
+
+
+def moe_forward(x: torch.Tensor, w_router: torch.Tensor, w_gate_up: torch.Tensor,
+                w_down: torch.Tensor, k: int, router_norm: torch.Tensor | None = None,
+                eps: float = 1e-6) -> dict:
+    """Full routed MoE layer op: router -> permute -> experts ->
+    combine.  Returns a dict with idx, gates, perm, out (bf16 [T,D])."""
+    T, D = x.shape
+    E = w_router.shape[0]
+    idx, gates = router_topk(x, w_router, k, router_norm, eps)
+    perm = moe_permute(idx.view(-1), E)
+    act, y = moe_experts(x, perm, gates, w_gate_up, w_down)
+    out = moe_combine(y, perm["route_pos"], T, k)
+    return {"idx": idx, "gates": gates, "perm": perm, "out": out}
+
+
+# --------------------------------------------------------------------------- attention
+def banded_attn_decode(q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor,
+                       k_cache: torch.Tensor, v_cache: torch.Tensor, pos: torch.Tensor,
+                       scale: float | None = None, out: torch.Tensor | None = None
+                       ) -> torch.Tensor:
+    """q/k_new/v_new [B,H,hd] (or row-strided views of a fused projection),
+    caches [B,H,W,hd] bf16 updated in place, pos [B] int32 -> out [B,H,hd] bf16."""
+    B, H, W, hd = k_cache.shape
+    for t, nm in ((q, "q"), (k_new, "k_new"), (v_new, "v_new")):
+        if t.dtype != torch.bfloat16 or not t.is_cuda or tuple(t.shape) != (B, H, hd):
+            raise ValueError(f"{nm} must be bf16 [B,H,hd] on the GPU")
+        if t.stride(2) != 1 or t.stride(1) != hd:
+            raise ValueError(f"{nm} must have contiguous heads")
+    if k_new.stride(0) != v_new.stride(0):
+        raise ValueError("k_new and v_new must share a batch stride")
+    _check(k_cache, torch.bfloat16, "k_cache")
+    _check(v_cache, torch.bfloat16, "v_cache", (B, H, W, hd))
+    _check(pos, torch.int32, "pos", (B,))
+    if out is None:
+        out = torch.empty(B, H, hd, dtype=torch.bfloat16, device=q.device)
+    scale = hd ** -0.5 if scale is None else scale
+    _lib.call("llmy_banded_attn_decode_bf16", _ptr(q), _ptr(k_new), _ptr(v_new), q.stride(0),
+              k_new.stride(0), _ptr(k_cache), _ptr(v_cache), _ptr(pos), _ptr(out), B, H, hd, W,
+              scale, _stream())
+    return out
+
+
+# --------------------------------------------------------------------------- GDN
+def gdn_step(q, k, v, beta, g, state, gate=None, out=None) -> torch.Tensor:
+    """In-place state update; q,k [B,H,dk], v/gate [B,H,dv] bf16, beta/g [B,H] fp32,
+    state [B,H,dk,dv] fp32.  Returns out [B,H,dv] bf16."""
+    B, H, dk = q.shape
+    dv = v.shape[-1]
+    _check(q, torch.bfloat16, "q")
+    _check(k, torch.bfloat16, "k", (B, H, dk))
+    _check(v, torch.bfloat16, "v", (B, H, dv))
+    _check(beta, torch.float32, "beta", (B, H))
+    _check(g, torch.float32, "g", (B, H))
+    _check(state, torch.float32, "state", (B, H, dk, dv))
+    if gate is not None:
+        _check(gate, torch.bfloat16, "gate", (B, H, dv))
+    if out is None:
+        out = torch.empty(B, H, dv, dtype=torch.bfloat16, device=q.device)
+    _lib.call("llmy_gdn_step_bf16", _ptr(q), _ptr(k), _ptr(v), _ptr(beta), _ptr(g), _ptr(gate),
+              _ptr(state), _ptr(out), B, H, dk, dv, _stream())
+    return out
+
+
+def gdn_step_fused(proj, beta_bias, decay_logit, state, out=None) -> torch.Tensor:
+    B, H, dk, dv = state.shape
+    _check(proj, torch.float32, "proj")
+    _check(state, torch.float32, "state")
+    if out is None:
+        out = torch.empty(B, H * dv, dtype=torch.bfloat16, device=proj.device)
+    _lib.call("llmy_gdn_step_fused_f32", _ptr(proj), proj.shape[1], _ptr(beta_bias),
+              _ptr(decay_logit), _ptr(state), _ptr(out), B, H, dk, dv, _stream())
+    return out
+
+
+def gdn_conv_gate(h, hist, w, out=None) -> torch.Tensor:
+    B, D = h.shape
+    _check(h, torch.bfloat16, "h")
+    _check(hist, torch.bfloat16, "hist", (B, w.shape[1] - 1, D))
+    _check(w, torch.float32, "w", (D, w.shape[1]))
+    if out is None:
+        out = torch.empty(B, D, dtype=torch.float32, device=h.device)
+    _lib.call("llmy_gdn_conv_gate", _ptr(h), _ptr(hist), _ptr(w), _ptr(out), B, D, w.shape[1],
+              _stream())
+    return out
+
+
+# --------------------------------------------------------------------------- glue
+def rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float = 1e-6, out=None) -> torch.Tensor:
+    M, D = x.shape
+    _check(x, torch.float32, "x")
+    _check(w, torch.float32, "w", (D,))
+    if out is None:
+        out = torch.empty(M, D, dtype=torch.bfloat16, device=x.device)
+    _lib.call("llmy_rmsnorm_f32_bf16", _ptr(x), _ptr(w), _ptr(out), M, D, eps, _stream())
+    return out
+
+
+def embed(tokens: torch.Tensor, table: torch.Tensor, out=None) -> torch.Tensor:
+    V, D = table.shape
+    _check(tokens, torch.int32, "tokens")
+    _check(table, torch.bfloat16, "table")
+    B = tokens.numel()
+    if out is None:
+        out = torch.empty(B, D, dtype=torch.float32, device=table.device)
+    _lib.call("llmy_embed_bf16", _ptr(tokens), _ptr(table), _ptr(out), B, D, V, _stream())
+    return out

@@ -1,0 +1,169 @@
+/*
+ * libllmy — MI355X (gfx950) kernels for the LLMY hybrid-block inference hot
+ * path, exported as a plain C ABI so ctypes (or any FFI) can bind them.
+ *
+ * Conventions shared by every entry point below:
+ *   - All tensor pointers are device pointers to contiguous, caller-owned
+ *     buffers.  bf16 tensors are passed as llmy_bf16 (the raw 16-bit word).
+ *     No entry point allocates or frees device memory.
+ *   - `stream` is a hipStream_t (NULL = the legacy default stream); work is
+ *     enqueued on it and the call returns without synchronising.
+ *   - The return value is a hipError_t: 0 on success; hipErrorInvalidValue
+ *     (1) when an argument fails validation, returned before anything is
+ *     launched; otherwise the launch status (hipGetLastError).
+ *   - A size of 0 along the token/batch axis is a valid no-op.
+ *   Conventions follow the reference op hooks: llmy_cuda/include/llmy.h:74-88
+ *   and their validation in llmy_cuda/src/llmy.cpp:213-240.
+ */
+#ifndef LLMY_H
+#define LLMY_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef uint16_t llmy_bf16;
+
+/* --- Library identity ---------------------------------------------------- */
+
+/* Version of this ABI; bumped when a signature changes.  No counterpart in
+ * the reference (a probe for bindings). */
+int32_t llmy_abi_version(void);
+
+/* --- Router (model/layers/context_router.py:62,71-74) --------------------- */
+
+/* logits[t,e] = (RMSNorm(x[t]) * norm_w) . w_router[e] in fp32 (norm skipped
+ * when norm_w == NULL), then the k largest logits per token (descending,
+ * ties -> lower expert index) and gates = softmax over those k values.
+ * x [T,D] bf16, norm_w [D] fp32 or NULL, w_router [E,D] fp32,
+ * logits_out [T,E] fp32 or NULL, idx [T,k] int32, gates [T,k] fp32.
+ * Limits: D % 4 == 0, D <= 8192, E <= 256, k <= min(E, 32).
+ * Replaces the router of SparseMoE.forward (model/layers/moe.py:180) and the
+ * native router_topk_kernel (llmy_cuda/src/kernels/router.cu:14-132). */
+int32_t llmy_router_topk_bf16(const llmy_bf16* x, const float* norm_w,
+                              const float* w_router, float* logits_out,
+                              int32_t* idx, float* gates, int32_t T, int32_t D,
+                              int32_t E, int32_t k, float eps, void* stream);
+
+/* Top-k + softmax of precomputed fp32 logits [T,E] (same tie rule).
+ * Replaces torch.topk(...).softmax (context_router.py:73-74). */
+int32_t llmy_router_topk_logits_f32(const float* logits, int32_t* idx,
+                                    float* gates, int32_t T, int32_t E,
+                                    int32_t k, void* stream);
+
+/* --- MoE token permutation (model/layers/moe.py:39-66) -------------------- */
+
+/* Stable counting sort of n_routes expert ids (flat route r = t*k + j):
+ * counts [E], offsets [E+1] (exclusive cumsum, offsets[E] = n_routes),
+ * sorted_routes [n_routes] (route ids grouped by expert, ascending r inside an
+ * expert), route_pos [n_routes] (inverse: sorted position of route r).
+ * Ids outside [0,E) are not placed.  E <= 1024. */
+int32_t llmy_moe_permute(const int32_t* expert_ids, int32_t n_routes,
+                         int32_t E, int32_t* counts, int32_t* offsets,
+                         int32_t* sorted_routes, int32_t* route_pos,
+                         void* stream);
+
+/* --- Dense projections (weight-streaming GEMM, decode path) --------------- */
+
+/* Y[M,N] = X[M,K] . W[N,K]^T, bf16 operands, fp32 accumulation, with a fused
+ * epilogue: 0 = store bf16 into out [M,N]; 1 = store fp32; 2 = out (fp32)
+ * += Y (residual add); 3 = out (fp32) += Y * aux[M,N] (gated residual).
+ * Limits: N % 16 == 0, K % 256 == 0.  Replaces linear_forward / k_linear_gemv
+ * (llmy_cuda/src/model.cpp:1467-1515) and nn.Linear on the decode path. */
+int32_t llmy_linear_bf16(const llmy_bf16* x, const llmy_bf16* w, void* out,
+                         const float* aux, int32_t M, int32_t N, int32_t K,
+                         int32_t epilogue, void* stream);
+
+/* --- SwiGLU MoE experts (model/layers/moe.py:72-81, expert.py:14-15) ------ */
+
+/* For every route p (sorted by expert, from llmy_moe_permute):
+ *   act[p] = bf16(silu(Wg[e] x[t]) * (Wu[e] x[t])),  t = sorted_routes[p] / k
+ *   y[p]   = gates[sorted_routes[p]] * (Wd[e] act[p])           (fp32)
+ * x [T,D] bf16; w_gate_up [E,2H,D] bf16 (gate rows then up rows, the packing
+ * of llmy.h:80-82 in the reference); w_down [E,D,H] bf16; gates [T*k] fp32;
+ * act [T*k,H] bf16 and y [T*k,D] fp32 are caller-provided scratch.  Experts
+ * with no routes read no weights.  Limits: D % 256 == 0, H % 256 == 0. */
+int32_t llmy_moe_experts_bf16(const llmy_bf16* x, const int32_t* offsets,
+                              const int32_t* sorted_routes, const float* gates,
+                              const llmy_bf16* w_gate_up, const llmy_bf16* w_down,
+                              llmy_bf16* act, float* y, int32_t T, int32_t D,
+                              int32_t H, int32_t E, int32_t k, void* stream);
+
+/* out[t] = sum_j y[route_pos[t*k + j]] (j ascending) — the un-permute /
+ * combine of moe.py:78-81 without atomics.  mode 0: store bf16 out [T,D];
+ * 1: store fp32; 2: fp32 out += sum (residual add).  D % 4 == 0. */
+int32_t llmy_moe_combine(const float* y, const int32_t* route_pos, void* out,
+                         int32_t T, int32_t D, int32_t k, int32_t mode,
+                         void* stream);
+
+/* --- Banded attention, decode (model/layers/hca.py:119-128) --------------- */
+
+/* One query per (b, h) against a ring-buffer cache k_cache/v_cache
+ * [B,H,W,head_dim] bf16.  The new key/value are written to slot pos[b] % W,
+ * then o = softmax(scale * q.K^T) V over the last min(pos[b] + 1, W) tokens
+ * (the new one included).  q, k_new, v_new: head h of batch row b starts at
+ * b*stride + h*head_dim (q_bstride / kv_bstride elements per batch row, so
+ * a fused [B, 3*H*hd] projection can be passed directly).  out [B,H,hd] bf16.
+ * head_dim in {64, 128}.  Replaces local_attn_decode_kernel
+ * (llmy_cuda/src/kernels/attn.cu:135-229). */
+int32_t llmy_banded_attn_decode_bf16(const llmy_bf16* q, const llmy_bf16* k_new,
+                                     const llmy_bf16* v_new, int64_t q_bstride,
+                                     int64_t kv_bstride, llmy_bf16* k_cache,
+                                     llmy_bf16* v_cache, const int32_t* pos,
+                                     llmy_bf16* out, int32_t B, int32_t H,
+                                     int32_t head_dim, int32_t W, float scale,
+                                     void* stream);
+
+/* --- Gated delta rule, decode (model/layers/gated_deltanet.py:140-149) ---- */
+
+/* pred = k^T S; S <- g S + beta k (v - pred)^T (in place); out = (q^T S) * gate.
+ * q, k [B,H,dk], v [B,H,dv], gate [B,H,dv] or NULL (bf16); beta, g [B,H] fp32;
+ * state [B,H,dk,dv] fp32; out [B,H,dv] bf16.  (dk,dv) in {(64,64),(128,128)}.
+ * Replaces gdn_step_kernel (llmy_cuda/src/kernels/gdn.cu:22-87). */
+int32_t llmy_gdn_step_bf16(const llmy_bf16* q, const llmy_bf16* k,
+                           const llmy_bf16* v, const float* beta, const float* g,
+                           const llmy_bf16* gate, float* state, llmy_bf16* out,
+                           int32_t B, int32_t H, int32_t dk, int32_t dv,
+                           void* stream);
+
+/* The GDN block's step from its fused fp32 projection row
+ * proj[b] = [q (H*dk) | k (H*dk) | v (H*dv) | gate logits (H*dv) | beta logits (H)]:
+ * q, k L2-normalised per head (clamp 1e-12), beta = sigmoid(logit + beta_bias),
+ * gate = sigmoid(logit), g = sigmoid(decay_logit[h]) (gated_deltanet.py:125-132),
+ * then the step above.  out [B, H*dv] bf16. */
+int32_t llmy_gdn_step_fused_f32(const float* proj, int64_t proj_ld,
+                                const float* beta_bias, const float* decay_logit,
+                                float* state, llmy_bf16* out, int32_t B, int32_t H,
+                                int32_t dk, int32_t dv, void* stream);
+
+/* Causal depthwise conv gate for one new token (gated_deltanet.py:257-268):
+ * out[b,d] = sigmoid(sum_j w[d,j] * [hist[b,0..K-2,d], h[b,d]]_j), then the
+ * history [B,K-1,D] bf16 shifts by one.  kernel == 4. */
+int32_t llmy_gdn_conv_gate(const llmy_bf16* h, llmy_bf16* hist, const float* w,
+                           float* out, int32_t B, int32_t D, int32_t kernel,
+                           void* stream);
+
+/* --- Glue (model/layers/norms.py:13-16, model/model.py:386) --------------- */
+
+/* out[m] = bf16(x[m] * rsqrt(mean(x[m]^2) + eps) * w); x [M,D] fp32. */
+int32_t llmy_rmsnorm_f32_bf16(const float* x, const float* w, llmy_bf16* out,
+                              int32_t M, int32_t D, float eps, void* stream);
+
+/* x[b] = float(table[tokens[b]]) (ids clamped to [0,V)); table [V,D] bf16. */
+int32_t llmy_embed_bf16(const int32_t* tokens, const llmy_bf16* table, float* x,
+                        int32_t B, int32_t D, int32_t V, void* stream);
+
+/* --- Sampling (sample_standalone.py:5609-5636) ---------------------------- */
+
+/* out[r] = first index of the maximum of logits[r, :V] (NaN counts as the
+ * maximum), i.e. torch.argmax.  logits [rows,V] fp32, out [rows] int32. */
+int32_t llmy_sample_argmax_f32(const float* logits, int32_t rows, int32_t V,
+                               int32_t* out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* LLMY_H */

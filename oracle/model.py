@@ -1,0 +1,132 @@
+"""Looped hybrid-block stack oracle (test infrastructure only).
+
+Composes the pinned ops into the block of model/model.py:162-264 with mHC
+disabled (model.py:119-126), looping the core ``num_loops`` times with one
+state per (loop, layer) (model.py:618-687, :645), tied LM head (model.py:705).
+
+Mixers:
+  * attention: q/k/v projections, banded attention over a ring KV cache
+    (decode window of model/layers/hca.py:119-128), output projection;
+  * GDN: gated_deltanet.py:125-149,254-275 — q/k/v/gate/beta projections,
+    per-head L2 norm of q and k (clamp 1e-12), beta = sigmoid(.+bias),
+    gate = sigmoid(.), decay = sigmoid(decay_logit) per head, the delta-rule
+    step, o = (q^T S) * gate, out_proj, times sigmoid(causal depthwise conv)
+    over the last ``conv_kernel`` normalised inputs.
+MoE: router (own RMSNorm + fp32 logits + top-k + softmax), routed SwiGLU
+experts (model/layers/moe.py:172-199, no shared experts in these configs).
+
+``act_bf16=True`` rounds activations to bf16 exactly where the HIP path
+stores them in bf16 (GEMM inputs, the KV cache, the MoE activation), so the
+comparison isolates accumulation-order differences; ``False`` is the plain
+fp32 reference of BASELINE config 1.
+"""
+from __future__ import annotations
+
+import numpy as np
+import torch
+import torch.nn.functional as F
+
+from hybrid_llm_amd.config import HybridConfig
+
+from .attention import banded_attention_decode
+from .gdn import gdn_step
+from .moe import moe_grouped
+from .router import rmsnorm, router_logits, router_topk
+
+
+def _bf16(t: torch.Tensor) -> torch.Tensor:
+    return t.to(torch.bfloat16).float()
+
+
+class HybridOracle:
+    def __init__(self, cfg: HybridConfig, weights: dict[str, torch.Tensor], act_bf16: bool = False):
+        self.cfg = cfg
+        self.w = {k: v.float() for k, v in weights.items()}
+        self.rnd = _bf16 if act_bf16 else (lambda t: t)
+
+    # ---- state -----------------------------------------------------------
+    def new_state(self, batch: int) -> dict:
+        cfg = self.cfg
+        st: dict = {"pos": torch.zeros(batch, dtype=torch.long)}
+        for loop in range(cfg.num_loops):
+            for l, kind in enumerate(cfg.layer_kinds):
+                if kind == "attn":
+                    shape = (batch, cfg.attn_heads, cfg.window, cfg.attn_head_dim)
+                    st[(loop, l)] = {"k": torch.zeros(shape), "v": torch.zeros(shape)}
+                else:
+                    st[(loop, l)] = {
+                        "S": torch.zeros(batch, cfg.gdn_heads, cfg.gdn_dk, cfg.gdn_dv),
+                        "hist": torch.zeros(batch, cfg.conv_kernel - 1, cfg.d_model),
+                    }
+        return st
+
+    # ---- blocks ----------------------------------------------------------
+    def _attn(self, l: int, h: torch.Tensor, st: dict, pos: torch.Tensor) -> torch.Tensor:
+        cfg, w, rnd = self.cfg, self.w, self.rnd
+        B = h.shape[0]
+        H, hd = cfg.attn_heads, cfg.attn_head_dim
+        p = f"L{l}."
+        q = rnd(h @ w[p + "wq"].t()).view(B, H, hd)
+        k = rnd(h @ w[p + "wk"].t()).view(B, H, hd)
+        v = rnd(h @ w[p + "wv"].t()).view(B, H, hd)
+        o, st["k"], st["v"] = banded_attention_decode(q, k, v, st["k"], st["v"], pos,
+                                                      cfg.attn_scale)
+        return rnd(o).reshape(B, H * hd) @ w[p + "wo"].t()
+
+    def _gdn(self, l: int, h: torch.Tensor, st: dict) -> torch.Tensor:
+        cfg, w, rnd = self.cfg, self.w, self.rnd
+        B = h.shape[0]
+        H, dk, dv = cfg.gdn_heads, cfg.gdn_dk, cfg.gdn_dv
+        p = f"L{l}."
+        q = (h @ w[p + "wq"].t()).view(B, H, dk)
+        k = (h @ w[p + "wk"].t()).view(B, H, dk)
+        v = (h @ w[p + "wv"].t()).view(B, H, dv)
+        gate = torch.sigmoid(h @ w[p + "wg"].t()).view(B, H, dv)
+        beta = torch.sigmoid(h @ w[p + "wb"].t() + w[p + "bb"])
+        q = q * torch.rsqrt((q * q).sum(-1, keepdim=True).clamp_min(1e-12))
+        k = k * torch.rsqrt((k * k).sum(-1, keepdim=True).clamp_min(1e-12))
+        g = torch.sigmoid(w[p + "decay"]).expand(B, H)
+        o, st["S"] = gdn_step(q, k, v, beta, g, st["S"], gate=gate)
+        o = rnd(o.reshape(B, H * dv))
+        window = torch.cat([st["hist"], h[:, None]], dim=1)  # [B, K, D]
+        conv = (window * w[p + "conv"].t()[None]).sum(1)      # tap j -> position t-(K-1)+j
+        st["hist"] = window[:, 1:].clone()
+        return (o @ w[p + "wout"].t()) * torch.sigmoid(conv)
+
+    def _moe(self, l: int, h2: torch.Tensor) -> torch.Tensor:
+        cfg, w = self.cfg, self.w
+        p = f"L{l}."
+        logits = router_logits(h2, w[p + "w_router"], w[p + "router_norm"], cfg.eps)
+        idx, gates = router_topk(logits, cfg.top_k)
+        return moe_grouped(h2, idx, gates, w[p + "w_gate"], w[p + "w_up"], w[p + "w_down"],
+                           act_round=self.rnd)
+
+    # ---- step ------------------------------------------------------------
+    def step(self, tokens, st: dict, num_loops: int | None = None) -> torch.Tensor:
+        """Decode one token per sequence; returns fp32 logits [B, V]."""
+        cfg, w, rnd = self.cfg, self.w, self.rnd
+        tokens = torch.as_tensor(np.asarray(tokens), dtype=torch.long).view(-1)
+        pos = st["pos"].clone()
+        x = w["embed"][tokens].clone()
+        loops = cfg.num_loops if not num_loops else num_loops
+        for loop in range(loops):
+            for l, kind in enumerate(cfg.layer_kinds):
+                s = st[(loop, l)]
+                h = rnd(rmsnorm(x, w[f"L{l}.mix_norm"], cfg.eps))
+                if kind == "attn":
+                    x = x + self._attn(l, h, s, pos)
+                else:
+                    x = x + self._gdn(l, h, s)
+                h2 = rnd(rmsnorm(x, w[f"L{l}.ffn_norm"], cfg.eps))
+                x = x + self._moe(l, h2)
+        st["pos"] = pos + 1
+        hf = rnd(rmsnorm(x, w["final_norm"], cfg.eps))
+        return hf @ w["embed"].t()
+
+    def prefill(self, tokens, st: dict) -> torch.Tensor:
+        """Token-by-token prefill of a [B, T] prompt; returns logits [B, T, V]."""
+        tokens = torch.as_tensor(np.asarray(tokens), dtype=torch.long)
+        if tokens.dim() == 1:
+            tokens = tokens[None]
+        outs = [self.step(tokens[:, t], st) for t in range(tokens.shape[1])]
+        return torch.stack(outs, dim=1)

@@ -1,0 +1,82 @@
+"""Router and token permutation oracle (test infrastructure only)."""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+
+def rmsnorm(x: torch.Tensor, weight: torch.Tensor | None, eps: float = 1e-6) -> torch.Tensor:
+    """RMSNorm in fp32: ``x * rsqrt(mean(x^2) + eps) * w``.
+
+    Restates model/layers/norms.py:13-16 (fp32 variance, eps 1e-6).
+    """
+    xf = x.float()
+    var = xf.pow(2).mean(dim=-1, keepdim=True)
+    out = xf * torch.rsqrt(var + eps)
+    if weight is not None:
+        out = out * weight.float()
+    return out
+
+
+def router_logits(x: torch.Tensor, w_router: torch.Tensor, norm_w: torch.Tensor | None = None,
+                  eps: float = 1e-6) -> torch.Tensor:
+    """fp32 router logits ``RMSNorm(x) @ W_r^T``.
+
+    Restates model/layers/context_router.py:62,71-72 with context_aware=False.
+    ``norm_w=None`` skips the router's own RMSNorm (the bare logits op).
+    """
+    h = rmsnorm(x, norm_w, eps) if norm_w is not None else x.float()
+    return h @ w_router.float().t()
+
+
+def topk_lower_index(logits: torch.Tensor, k: int) -> tuple[np.ndarray, np.ndarray]:
+    """Indices and values of the k largest entries per row.
+
+    Order: descending value; equal values -> lower index first; NaN above
+    everything (torch.topk's comparison).  The reference uses torch.topk
+    (context_router.py:73), whose tie order is unspecified; this pins it.
+    Implemented as a lexicographic sort so it is independent of torch.topk.
+    """
+    v = logits.detach().float().cpu().numpy()
+    rows, n = v.shape
+    idx = np.empty((rows, k), dtype=np.int64)
+    vals = np.empty((rows, k), dtype=np.float32)
+    cols = np.arange(n)
+    for r in range(rows):
+        row = v[r]
+        nan = np.isnan(row)
+        clean = np.where(nan, 0.0, row)
+        clean = np.where(clean == 0.0, 0.0, clean)  # -0.0 == +0.0
+        order = np.lexsort((cols, -clean, ~nan))
+        idx[r] = order[:k]
+        vals[r] = row[order[:k]]
+    return idx, vals
+
+
+def router_topk(logits: torch.Tensor, k: int) -> tuple[np.ndarray, torch.Tensor]:
+    """(expert ids [T,k] int64, gates [T,k] fp32 = softmax of the k values).
+
+    Restates context_router.py:73-74 with the tie rule of topk_lower_index.
+    """
+    idx, vals = topk_lower_index(logits, k)
+    gates = torch.from_numpy(vals).softmax(dim=-1)
+    return idx, gates
+
+
+def moe_permute(expert_ids: np.ndarray, num_experts: int) -> dict[str, np.ndarray]:
+    """Stable counting sort of flat route ids ``r = t*k + j`` by expert.
+
+    Restates model/layers/moe.py:42-60 (flat routes, sort by expert, bincount,
+    exclusive-cumsum offsets) with the sort made stable (moe.py:46 uses an
+    unstable torch.sort; the combined output does not depend on the order).
+    Returns counts [E], offsets [E+1], sorted_routes [n], route_pos [n].
+    """
+    ids = np.asarray(expert_ids, dtype=np.int64).reshape(-1)
+    counts = np.bincount(ids, minlength=num_experts).astype(np.int64)
+    offsets = np.zeros(num_experts + 1, dtype=np.int64)
+    offsets[1:] = np.cumsum(counts)
+    sorted_routes = np.argsort(ids, kind="stable").astype(np.int64)
+    route_pos = np.empty_like(sorted_routes)
+    route_pos[sorted_routes] = np.arange(ids.size)
+    return {"counts": counts, "offsets": offsets, "sorted_routes": sorted_routes,
+            "route_pos": route_pos}

@@ -1,0 +1,77 @@
+"""C-ABI checks that run without a GPU: the library loads, exports every
+symbol include/llmy.h declares, and rejects bad arguments before launching
+(the reference convention, llmy_cuda/src/llmy.cpp:216-217,230-233)."""
+import ctypes as C
+import re
+from pathlib import Path
+
+import pytest
+
+from hybrid_llm_amd import _lib
+
+ROOT = Path(__file__).resolve().parents[1]
+INVALID = 1  # hipErrorInvalidValue
+
+
+def declared_symbols() -> list[str]:
+    text = (ROOT / "include" / "llmy.h").read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(llmy_\w+)\s*\(", text)))
+
+
+def test_header_declares_entry_points():
+    syms = declared_symbols()
+    assert "llmy_router_topk_bf16" in syms and len(syms) >= 5
+
+
+def test_library_exports_every_declared_symbol(lib):
+    for name in declared_symbols():
+        assert hasattr(lib, name), f"{name} declared in llmy.h but not exported"
+
+
+def test_binding_covers_every_declared_symbol():
+    assert sorted(_lib.SIGNATURES) == declared_symbols()
+
+
+def test_abi_version(lib):
+    assert lib.llmy_abi_version() >= 1
+
+
+FAKE = 0x10000  # non-null, 256-byte aligned; never dereferenced (validation fails first)
+
+
+@pytest.mark.parametrize("args", [
+    # null x
+    (None, None, FAKE, None, FAKE, FAKE, 4, 64, 8, 2, 1e-6, None),
+    # D not a multiple of 4
+    (FAKE, None, FAKE, None, FAKE, FAKE, 4, 62, 8, 2, 1e-6, None),
+    # k > E
+    (FAKE, None, FAKE, None, FAKE, FAKE, 4, 64, 8, 9, 1e-6, None),
+    # E too large
+    (FAKE, None, FAKE, None, FAKE, FAKE, 4, 64, 300, 2, 1e-6, None),
+    # negative T
+    (FAKE, None, FAKE, None, FAKE, FAKE, -1, 64, 8, 2, 1e-6, None),
+    # misaligned router weights
+    (FAKE, None, FAKE + 4, None, FAKE, FAKE, 4, 64, 8, 2, 1e-6, None),
+])
+def test_router_rejects_bad_arguments(lib, args):
+    assert lib.llmy_router_topk_bf16(*args) == INVALID
+
+
+def test_empty_token_axis_is_noop(lib):
+    assert lib.llmy_router_topk_bf16(FAKE, None, FAKE, None, FAKE, FAKE, 0, 64, 8, 2, 1e-6,
+                                     None) == 0
+    assert lib.llmy_sample_argmax_f32(FAKE, 0, 10, FAKE, None) == 0
+
+
+def test_permute_and_argmax_reject_bad_arguments(lib):
+    assert lib.llmy_moe_permute(None, 8, 4, FAKE, FAKE, FAKE, FAKE, None) == INVALID
+    assert lib.llmy_moe_permute(FAKE, 8, 0, FAKE, FAKE, FAKE, FAKE, None) == INVALID
+    assert lib.llmy_sample_argmax_f32(FAKE, 4, 0, FAKE, None) == INVALID
+    assert lib.llmy_sample_argmax_f32(None, 4, 10, FAKE, None) == INVALID
+    assert lib.llmy_router_topk_logits_f32(FAKE, FAKE, FAKE, 4, 8, 0, None) == INVALID
+
+
+def test_call_raises_on_status():
+    with pytest.raises(_lib.LlmyError):
+        _lib.call("llmy_sample_argmax_f32", None, 4, 10, FAKE, None)

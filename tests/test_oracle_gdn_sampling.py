@@ -1,0 +1,117 @@
+"""Pins the GDN and sampling oracles (CPU only)."""
+import numpy as np
+import torch
+import torch.nn.functional as F
+
+from oracle.gdn import gdn_chunked, gdn_sequential, gdn_step
+from oracle.sampling import argmax, top_p_sample
+
+
+def _gdn_inputs(B, T, H, dk, dv, seed, s0_std=0.1):
+    g = torch.Generator().manual_seed(seed)
+    q = F.normalize(torch.randn(B, T, H, dk, generator=g), dim=-1)
+    k = F.normalize(torch.randn(B, T, H, dk, generator=g), dim=-1)
+    v = torch.randn(B, T, H, dv, generator=g)
+    beta = torch.sigmoid(torch.randn(B, T, H, generator=g))
+    gd = torch.exp(-F.softplus(torch.randn(B, T, H, generator=g)))
+    S0 = torch.randn(B, H, dk, dv, generator=g) * s0_std
+    return q, k, v, beta, gd, S0
+
+
+def test_beta_zero_is_pure_decay():
+    q, k, v, beta, g, S0 = _gdn_inputs(2, 30, 2, 8, 4, 0)
+    o, S = gdn_sequential(q, k, v, torch.zeros_like(beta), g, S0, dtype=torch.float64)
+    expect = torch.prod(g.double(), dim=1)[..., None, None] * S0.double()
+    assert torch.allclose(S, expect, atol=1e-12)
+    # o_t = q_t^T (Gamma_t S0)
+    gam = torch.cumprod(g.double(), dim=1)
+    ref = torch.einsum("bthk,bhkv->bthv", q.double(), S0.double()) * gam[..., None]
+    assert torch.allclose(o, ref, atol=1e-12)
+
+
+def test_orthonormal_keys_overwrite_exactly():
+    # g = 1, beta = 1, keys orthonormal: S = sum_i k_i v_i^T, reading q = k_i gives v_i.
+    dk, dv, T = 8, 5, 8
+    basis = torch.linalg.qr(torch.randn(dk, dk, generator=torch.Generator().manual_seed(1)))[0]
+    k = basis.t()[None, :, None, :]                      # [1, T, 1, dk]
+    v = torch.randn(1, T, 1, dv, generator=torch.Generator().manual_seed(2))
+    ones = torch.ones(1, T, 1)
+    _, S = gdn_sequential(k, k, v, ones, ones, torch.zeros(1, 1, dk, dv), dtype=torch.float64)
+    read = torch.einsum("tk,kv->tv", k[0, :, 0].double(), S[0, 0])
+    assert torch.allclose(read, v[0, :, 0].double(), atol=1e-12)
+    # writing the same key again replaces (not adds) its value
+    v2 = torch.randn(1, 1, 1, dv, generator=torch.Generator().manual_seed(3))
+    _, S2 = gdn_sequential(k[:, :1], k[:, :1], v2, ones[:, :1], ones[:, :1], S,
+                           dtype=torch.float64)
+    assert torch.allclose(k[0, 0, 0].double() @ S2[0, 0], v2[0, 0, 0].double(), atol=1e-12)
+
+
+def test_prediction_uses_undecayed_state():
+    # Distinguishes the reference transition g*S + beta*k(v - k^T S) from
+    # the textbook g*(S + beta*k(v - k^T S)): one step, hand computed.
+    dk, dv = 2, 1
+    S0 = torch.tensor([[[[1.0], [0.0]]]])
+    k = torch.tensor([[[[1.0, 0.0]]]])
+    v = torch.tensor([[[[3.0]]]])
+    beta = torch.tensor([[[0.5]]])
+    g = torch.tensor([[[0.25]]])
+    _, S = gdn_sequential(k, k, v, beta, g, S0, dtype=torch.float64)
+    # 0.25*1 + 0.5*1*(3 - 1) = 1.25
+    assert abs(float(S[0, 0, 0, 0]) - 1.25) < 1e-12
+
+
+def test_chunked_matches_sequential():
+    for (T, C) in [(130, 64), (64, 64), (50, 16), (7, 64)]:
+        q, k, v, beta, g, S0 = _gdn_inputs(2, T, 3, 16, 8, T)
+        o1, S1 = gdn_sequential(q, k, v, beta, g, S0, dtype=torch.float64)
+        o2, S2 = gdn_chunked(q, k, v, beta, g, S0, chunk=C)
+        assert torch.allclose(o1, o2, atol=1e-10), (T, C)
+        assert torch.allclose(S1, S2, atol=1e-10), (T, C)
+
+
+def test_step_equals_one_token_scan():
+    q, k, v, beta, g, S0 = _gdn_inputs(3, 1, 2, 8, 8, 5)
+    o1, S1 = gdn_sequential(q, k, v, beta, g, S0)
+    o2, S2 = gdn_step(q[:, 0], k[:, 0], v[:, 0], beta[:, 0], g[:, 0], S0)
+    assert torch.equal(o1[:, 0], o2) and torch.equal(S1, S2)
+
+
+def test_argmax_first_occurrence_and_nan():
+    x = torch.tensor([[1.0, 5.0, 5.0, 2.0], [float("nan"), 1.0, float("nan"), 9.0],
+                      [-1.0, -1.0, -3.0, -2.0]])
+    assert list(argmax(x)) == [1, 0, 0]
+    r = torch.randn(64, 1000, generator=torch.Generator().manual_seed(0))
+    assert np.array_equal(argmax(r), torch.argmax(r, -1).numpy())
+
+
+def test_top_p_closed_forms():
+    g = torch.Generator().manual_seed(7)
+    logits = torch.randn(16, 500, generator=g) * 2
+    greedy = torch.argmax(logits, -1).numpy()
+    zeros = torch.zeros(16)
+    # u = 0 picks the most probable token
+    assert np.array_equal(top_p_sample(logits, 0.8, 0.9, zeros), greedy)
+    # p -> 0 keeps only the top token, whatever u is
+    u = torch.rand(16, generator=g)
+    assert np.array_equal(top_p_sample(logits, 0.8, 1e-9, u), greedy)
+    # p = 1 (disabled): plain inverse CDF over the full sorted distribution
+    out = top_p_sample(logits, 0.8, 1.0, u)
+    for r in range(16):
+        order = np.lexsort((np.arange(500), -logits[r].double().numpy()))
+        p = torch.softmax(logits[r].double() / 0.8, -1).numpy()[order]
+        expect = order[np.searchsorted(np.cumsum(p), float(u[r]), side="right")]
+        assert out[r] == expect
+
+
+def test_top_p_nucleus_matches_torch_sampler_rule():
+    # The kept set is the smallest prefix reaching p; u just below the kept
+    # mass boundary picks the last kept token, never one outside it.
+    g = torch.Generator().manual_seed(9)
+    logits = torch.randn(8, 50, generator=g)
+    for r in range(8):
+        sv, order = torch.sort(logits[r].double() / 0.8, descending=True, stable=True)
+        p = torch.softmax(sv, -1)
+        c = torch.cumsum(p, -1)
+        cut = int(torch.nonzero(c >= 0.9)[0]) + 1
+        got = top_p_sample(logits[r:r + 1], 0.8, 0.9, torch.tensor([0.999999]))
+        assert got[0] == int(order[cut - 1])

@@ -1,0 +1,92 @@
+"""Pins the MoE and banded-attention oracles (CPU only)."""
+import numpy as np
+import torch
+import torch.nn.functional as F
+
+from oracle.attention import banded_attention, banded_attention_decode
+from oracle.moe import moe_grouped, moe_per_token, swiglu
+from oracle.router import router_topk
+
+
+def _experts(E, H, D, seed):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(E, H, D, generator=g) * 0.2, torch.randn(E, H, D, generator=g) * 0.2,
+            torch.randn(E, D, H, generator=g) * 0.2)
+
+
+def test_grouped_moe_matches_per_token_brute_force():
+    T, D, H, E, k = 13, 16, 24, 5, 2
+    wg, wu, wd = _experts(E, H, D, 0)
+    g = torch.Generator().manual_seed(1)
+    x = torch.randn(T, D, generator=g)
+    idx, gates = router_topk(torch.randn(T, E, generator=g), k)
+    a = moe_grouped(x, idx, gates, wg, wu, wd)
+    b = moe_per_token(x, idx, gates, wg, wu, wd)
+    assert torch.allclose(a, b, atol=1e-5, rtol=1e-5)
+
+
+def test_moe_single_expert_is_dense_swiglu():
+    T, D, H, E = 9, 16, 32, 4
+    wg, wu, wd = _experts(E, H, D, 2)
+    x = torch.randn(T, D, generator=torch.Generator().manual_seed(3))
+    idx = np.full((T, 1), 2)
+    out = moe_grouped(x, idx, torch.ones(T, 1), wg, wu, wd)
+    assert torch.allclose(out, swiglu(x, wg[2], wu[2], wd[2]), atol=1e-6)
+    # swiglu itself against the closed form silu(a)*b
+    a = x @ wg[2].t()
+    assert torch.allclose(swiglu(x, wg[2], wu[2], wd[2]),
+                          (a * torch.sigmoid(a) * (x @ wu[2].t())) @ wd[2].t(), atol=1e-6)
+
+
+def test_moe_is_token_order_invariant():
+    T, D, H, E, k = 20, 8, 12, 6, 2
+    wg, wu, wd = _experts(E, H, D, 4)
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(T, D, generator=g)
+    idx, gates = router_topk(torch.randn(T, E, generator=g), k)
+    perm = torch.randperm(T, generator=g)
+    a = moe_grouped(x, idx, gates, wg, wu, wd)[perm]
+    b = moe_grouped(x[perm], idx[perm.numpy()], gates[perm], wg, wu, wd)
+    assert torch.allclose(a, b, atol=1e-6)
+
+
+def _qkv(B, T, H, hd, seed):
+    g = torch.Generator().manual_seed(seed)
+    return [torch.randn(B, T, H, hd, generator=g) for _ in range(3)]
+
+
+def test_banded_equals_causal_sdpa_when_window_covers_sequence():
+    q, k, v = _qkv(2, 37, 3, 16, 0)
+    out = banded_attention(q, k, v, window=64, block=8)
+    ref = F.scaled_dot_product_attention(q.transpose(1, 2), k.transpose(1, 2),
+                                         v.transpose(1, 2), is_causal=True).transpose(1, 2)
+    assert torch.allclose(out, ref, atol=1e-5)
+
+
+def test_window_one_returns_values():
+    q, k, v = _qkv(1, 20, 2, 8, 1)
+    assert torch.allclose(banded_attention(q, k, v, window=1, block=7), v, atol=1e-6)
+
+
+def test_banded_brute_force():
+    B, T, H, hd, W = 1, 12, 2, 4, 5
+    q, k, v = _qkv(B, T, H, hd, 2)
+    out = banded_attention(q, k, v, window=W, block=5)
+    for i in range(T):
+        for h in range(H):
+            js = [j for j in range(T) if 0 <= i - j < W]
+            s = torch.stack([q[0, i, h] @ k[0, j, h] for j in js]) / hd ** 0.5
+            ref = (torch.softmax(s, 0)[:, None] * v[0, js, h]).sum(0)
+            assert torch.allclose(out[0, i, h], ref, atol=1e-5)
+
+
+def test_decode_equals_last_row_of_prefill():
+    B, T, H, hd, W = 2, 40, 3, 8, 16
+    q, k, v = _qkv(B, T, H, hd, 3)
+    full = banded_attention(q, k, v, window=W, block=16)
+    kc = torch.zeros(B, H, W, hd)
+    vc = torch.zeros(B, H, W, hd)
+    for t in range(T):
+        o, kc, vc = banded_attention_decode(q[:, t], k[:, t], v[:, t], kc, vc,
+                                            torch.full((B,), t))
+        assert torch.allclose(o, full[:, t], atol=1e-5), t
