@@ -110,6 +110,15 @@ class HybridDecoder:
             "next": torch.zeros(B, dtype=torch.int32, device=dev),
         }
         self.graph: torch.cuda.CUDAGraph | None = None
+        # Optional record of every MoE application's expert ids (verification
+        # aid: lets a checker replay the kernel's discrete routing decisions).
+        self.route_log: torch.Tensor | None = None
+
+    def enable_route_log(self) -> None:
+        n_apps = self.cfg.num_loops * self.cfg.n_layers
+        self.route_log = torch.zeros(n_apps, self.B, self.cfg.top_k, dtype=torch.int32,
+                                     device=self.dev)
+        self._app = 0
 
     # ------------------------------------------------------------------ blocks
     def _attn(self, l: int, st: dict) -> None:
@@ -146,6 +155,9 @@ class HybridDecoder:
         _lib.call("llmy_moe_permute", b["idx"].data_ptr(), self.B * cfg.top_k, cfg.n_experts,
                   b["counts"].data_ptr(), b["offsets"].data_ptr(), b["sorted_routes"].data_ptr(),
                   b["route_pos"].data_ptr(), s)
+        if self.route_log is not None:
+            self.route_log[self._app].copy_(b["idx"])
+            self._app = (self._app + 1) % self.route_log.shape[0]
         perm = {"offsets": b["offsets"], "sorted_routes": b["sorted_routes"]}
         ops.moe_experts(b["h"], perm, b["gates"], w[p + "w_gate_up"], w[p + "w_down"],
                         act=b["act"], y=b["y"])

@@ -43,6 +43,14 @@ class HybridOracle:
         self.cfg = cfg
         self.w = {k: v.float() for k, v in weights.items()}
         self.rnd = _bf16 if act_bf16 else (lambda t: t)
+        # Discrete-decision forcing: when set to a list of [B, k] expert-id
+        # arrays (one per MoE application, in execution order), the oracle
+        # routes with those ids instead of its own top-k, and records in
+        # route_gaps the logit gap of every token whose choice differed.
+        self.forced_routes: list | None = None
+        self.routes: list[np.ndarray] = []
+        self.route_gaps: list[float] = []
+        self.route_total = 0
 
     # ---- state -----------------------------------------------------------
     def new_state(self, batch: int) -> dict:
@@ -98,8 +106,25 @@ class HybridOracle:
         p = f"L{l}."
         logits = router_logits(h2, w[p + "w_router"], w[p + "router_norm"], cfg.eps)
         idx, gates = router_topk(logits, cfg.top_k)
+        if self.forced_routes is not None:
+            forced = np.asarray(self.forced_routes.pop(0)).reshape(idx.shape).astype(np.int64)
+            self._check_forced(logits, idx, forced)
+            idx = forced
+            gates = torch.gather(logits, 1, torch.from_numpy(idx)).softmax(-1)
+        self.routes.append(idx.copy())
         return moe_grouped(h2, idx, gates, w[p + "w_gate"], w[p + "w_up"], w[p + "w_down"],
                            act_round=self.rnd)
+
+    def _check_forced(self, logits: torch.Tensor, own: np.ndarray, forced: np.ndarray) -> None:
+        """Record how far a forced routing is from the oracle's own choice: for
+        every token whose forced expert set differs, the logit gap between the
+        oracle's weakest own pick and the forced set's weakest pick (0 for a tie)."""
+        for t in range(own.shape[0]):
+            if sorted(own[t]) != sorted(forced[t]):
+                lo_own = float(logits[t, own[t]].min())
+                lo_forced = float(logits[t, forced[t]].min())
+                self.route_gaps.append(lo_own - lo_forced)
+            self.route_total += 1
 
     # ---- step ------------------------------------------------------------
     def step(self, tokens, st: dict, num_loops: int | None = None) -> torch.Tensor:
