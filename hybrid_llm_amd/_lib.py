@@ -24,13 +24,19 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "llmy_router_topk_logits_f32": (_I, [_P, _P, _P, _I, _I, _I, _P]),
     "llmy_moe_permute": (_I, [_P, _I, _I, _P, _P, _P, _P, _P]),
     "llmy_sample_argmax_f32": (_I, [_P, _I, _I, _P, _P]),
-    "llmy_linear_bf16": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _P]),
-    "llmy_moe_experts_bf16": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),
+    "llmy_linear_bf16": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),
+    "llmy_pack_weights_bf16": (_I, [_P, _P, _I64, _I, _I, _P]),
+    "llmy_moe_experts_bf16": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P]),
     "llmy_moe_combine": (_I, [_P, _P, _P, _I, _I, _I, _I, _P]),
     "llmy_banded_attn_decode_bf16": (_I, [_P, _P, _P, _I64, _I64, _P, _P, _P, _P, _I, _I, _I,
                                           _I, _F, _P]),
     "llmy_gdn_step_bf16": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P]),
-    "llmy_gdn_step_fused_f32": (_I, [_P, _I64, _P, _P, _P, _P, _I, _I, _I, _I, _P]),
+    "llmy_gdn_step_fused_f32": (_I, [_P, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I,
+                                     _I, _I, _P]),
+    "llmy_embed_norm_bf16": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _F, _P]),
+    "llmy_moe_combine_norm": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _F, _P]),
+    "llmy_moe_route_decode": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I,
+                                   _F, _P]),
     "llmy_gdn_conv_gate": (_I, [_P, _P, _P, _P, _I, _I, _I, _P]),
     "llmy_rmsnorm_f32_bf16": (_I, [_P, _P, _P, _I, _I, _F, _P]),
     "llmy_embed_bf16": (_I, [_P, _P, _P, _I, _I, _I, _P]),

@@ -34,6 +34,12 @@ struct GdnStepArgs {
   float* state;
   uint16_t* out;
   int H;
+  // optional causal conv gate fused into the model variant
+  const uint16_t* conv_h;  // [B, D] mixer input (bf16)
+  uint16_t* conv_hist;     // [B, K-1, D]
+  const float* conv_w;     // [D, K]
+  float* conv_out;         // [B, D] sigmoid(conv)
+  int D;
 };
 
 template <int DK, int DV, bool MODEL>
@@ -60,6 +66,27 @@ __global__ __launch_bounds__(256) void gdn_step_kernel(GdnStepArgs a) {
 
   const int lane = t & 63;
   const int wave = t >> 6;
+  if (MODEL && a.conv_h != nullptr) {
+    // Causal depthwise conv gate (gated_deltanet.py:257-268) for this head's
+    // D/H channels of row b: window = [hist[0..2], h]; out = sigmoid(w . window);
+    // the history shifts by one.  Each thread owns one channel.
+    const int per = a.D / a.H;
+    for (int c = t; c < per; c += 256) {
+      const int d = h * per + c;
+      uint16_t* hb = a.conv_hist + static_cast<long long>(b) * 3 * a.D + d;
+      const uint16_t w0 = hb[0], w1 = hb[a.D], w2 = hb[2 * a.D];
+      const uint16_t w3 = a.conv_h[static_cast<long long>(b) * a.D + d];
+      const float4 cw = *reinterpret_cast<const float4*>(a.conv_w + 4 * d);
+      float acc = cw.x * bf2f(w0);
+      acc = fmaf(cw.y, bf2f(w1), acc);
+      acc = fmaf(cw.z, bf2f(w2), acc);
+      acc = fmaf(cw.w, bf2f(w3), acc);
+      a.conv_out[static_cast<long long>(b) * a.D + d] = sigmoidf_(acc);
+      hb[0] = w1;
+      hb[a.D] = w2;
+      hb[2 * a.D] = w3;
+    }
+  }
   if (MODEL) {
     const float* row = a.proj + static_cast<long long>(b) * a.proj_ld;
     const int HK = a.H * DK, HV = a.H * DV;
@@ -191,15 +218,23 @@ extern "C" int32_t llmy_gdn_step_bf16(const llmy_bf16* q, const llmy_bf16* k, co
 
 extern "C" int32_t llmy_gdn_step_fused_f32(const float* proj, int64_t proj_ld,
                                            const float* beta_bias, const float* decay_logit,
-                                           float* state, llmy_bf16* out, int32_t B, int32_t H,
-                                           int32_t dk, int32_t dv, void* stream) {
+                                           float* state, llmy_bf16* out, const llmy_bf16* conv_h,
+                                           llmy_bf16* conv_hist, const float* conv_w,
+                                           float* conv_out, int32_t D, int32_t conv_kernel,
+                                           int32_t B, int32_t H, int32_t dk, int32_t dv,
+                                           void* stream) {
   LLMY_REQUIRE(B >= 0 && H > 0 && ((dk == 64 && dv == 64) || (dk == 128 && dv == 128)));
   LLMY_REQUIRE(proj_ld >= static_cast<int64_t>(H) * (2 * dk + 2 * dv + 1));
   if (B == 0) return 0;
   LLMY_REQUIRE(proj && beta_bias && decay_logit && state && out);
   LLMY_REQUIRE(aligned(state, 16));
+  if (conv_h != nullptr) {
+    LLMY_REQUIRE(conv_hist && conv_w && conv_out && conv_kernel == 4 && D > 0 && D % H == 0);
+    LLMY_REQUIRE(aligned(conv_w, 16));
+  }
   GdnStepArgs a{};
   a.proj = proj; a.proj_ld = proj_ld; a.beta_bias = beta_bias; a.decay_logit = decay_logit;
   a.state = state; a.out = out; a.H = H;
+  a.conv_h = conv_h; a.conv_hist = conv_hist; a.conv_w = conv_w; a.conv_out = conv_out; a.D = D;
   return launch_gdn_step<true>(a, B, dk, dv, as_stream(stream));
 }

@@ -69,6 +69,87 @@ __global__ __launch_bounds__(256) void gdn_conv_kernel(const uint16_t* __restric
   for (int j = 0; j < KC - 1; ++j) hb[static_cast<long long>(j) * D] = win[j + 1];
 }
 
+// Row-wise RMSNorm of an fp32 row held by one wavefront as NCH float4 chunks
+// (element 4*lane + 256*c + j), written as bf16.
+template <int NCH>
+__device__ __forceinline__ void norm_row_store(const float4* v, const float* __restrict__ w,
+                                               uint16_t* __restrict__ out, int lane, float eps) {
+  constexpr int D = NCH * 256;
+  float ss = 0.f;
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) ss += v[c].x * v[c].x + v[c].y * v[c].y + v[c].z * v[c].z + v[c].w * v[c].w;
+  const float r = rsqrtf(wave_sum(ss) / static_cast<float>(D) + eps);
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    const int d = 4 * lane + 256 * c;
+    const float4 wv = *reinterpret_cast<const float4*>(w + d);
+    *reinterpret_cast<uint2*>(out + d) =
+        make_uint2(pack_bf2(v[c].x * r * wv.x, v[c].y * r * wv.y),
+                   pack_bf2(v[c].z * r * wv.z, v[c].w * r * wv.w));
+  }
+}
+
+// x[b] = float(table[tok[b]]); h[b] = bf16(RMSNorm(x[b]) * w).  One wave per row.
+template <int NCH>
+__global__ __launch_bounds__(256) void embed_norm_kernel(const int32_t* __restrict__ tokens,
+                                                         const uint16_t* __restrict__ table,
+                                                         const float* __restrict__ w,
+                                                         float* __restrict__ x,
+                                                         uint16_t* __restrict__ h, int B, int V,
+                                                         float eps) {
+  constexpr int D = NCH * 256;
+  const int b = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (b >= B) return;
+  int tok = tokens[b];
+  tok = tok < 0 ? 0 : (tok >= V ? V - 1 : tok);
+  const uint16_t* src = table + static_cast<long long>(tok) * D;
+  float* xr = x + static_cast<long long>(b) * D;
+  float4 v[NCH];
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    const int d = 4 * lane + 256 * c;
+    const uint2 raw = *reinterpret_cast<const uint2*>(src + d);
+    v[c] = make_float4(__uint_as_float(raw.x << 16), __uint_as_float(raw.x & 0xffff0000u),
+                       __uint_as_float(raw.y << 16), __uint_as_float(raw.y & 0xffff0000u));
+    *reinterpret_cast<float4*>(xr + d) = v[c];
+  }
+  norm_row_store<NCH>(v, w, h + static_cast<long long>(b) * D, lane, eps);
+}
+
+// MoE combine fused with the next RMSNorm: x[t] += sum_j y[route_pos[t*k+j]]
+// (j ascending), then h[t] = bf16(RMSNorm(x[t]) * w) (skipped when w is null).
+// One wave per row.
+template <int NCH>
+__global__ __launch_bounds__(256) void combine_norm_kernel(const float* __restrict__ y,
+                                                           const int32_t* __restrict__ route_pos,
+                                                           const float* __restrict__ w,
+                                                           float* __restrict__ x,
+                                                           uint16_t* __restrict__ h, int T, int k,
+                                                           float eps) {
+  constexpr int D = NCH * 256;
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (t >= T) return;
+  float* xr = x + static_cast<long long>(t) * D;
+  float4 v[NCH];
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    const int d = 4 * lane + 256 * c;
+    float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int j = 0; j < k; ++j) {
+      const int p = min(max(route_pos[t * k + j], 0), T * k - 1);
+      const float4 yv = *reinterpret_cast<const float4*>(y + static_cast<long long>(p) * D + d);
+      s.x += yv.x; s.y += yv.y; s.z += yv.z; s.w += yv.w;
+    }
+    float4 xv = *reinterpret_cast<const float4*>(xr + d);
+    xv.x += s.x; xv.y += s.y; xv.z += s.z; xv.w += s.w;
+    *reinterpret_cast<float4*>(xr + d) = xv;
+    v[c] = xv;
+  }
+  if (w != nullptr) norm_row_store<NCH>(v, w, h + static_cast<long long>(t) * D, lane, eps);
+}
+
 }  // namespace llmy
 
 using namespace llmy;
@@ -103,5 +184,45 @@ extern "C" int32_t llmy_gdn_conv_gate(const llmy_bf16* h, llmy_bf16* hist, const
   const long long n = static_cast<long long>(B) * D;
   hipLaunchKernelGGL(gdn_conv_kernel<4>, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256),
                      0, as_stream(stream), h, hist, w, out, B, D);
+  return launch_status();
+}
+
+#define LLMY_NCH_SWITCH(D, MACRO)      \
+  switch (D) {                         \
+    case 256: MACRO(1); break;         \
+    case 512: MACRO(2); break;         \
+    case 1024: MACRO(4); break;        \
+    default: MACRO(8); break;          \
+  }
+
+extern "C" int32_t llmy_embed_norm_bf16(const int32_t* tokens, const llmy_bf16* table,
+                                        const float* w, float* x, llmy_bf16* h, int32_t B,
+                                        int32_t D, int32_t V, float eps, void* stream) {
+  LLMY_REQUIRE(B >= 0 && V > 0 && (D == 256 || D == 512 || D == 1024 || D == 2048));
+  if (B == 0) return 0;
+  LLMY_REQUIRE(tokens && table && w && x && h);
+  LLMY_REQUIRE(aligned(table, 8) && aligned(w, 16) && aligned(x, 16) && aligned(h, 8));
+  const hipStream_t s = as_stream(stream);
+#define LLMY_EMBED(N)                                                                        \
+  hipLaunchKernelGGL(embed_norm_kernel<N>, dim3((B + 3) / 4), dim3(256), 0, s, tokens, table, \
+                     w, x, h, B, V, eps)
+  LLMY_NCH_SWITCH(D, LLMY_EMBED)
+#undef LLMY_EMBED
+  return launch_status();
+}
+
+extern "C" int32_t llmy_moe_combine_norm(const float* y, const int32_t* route_pos,
+                                         const float* w, float* x, llmy_bf16* h, int32_t T,
+                                         int32_t D, int32_t k, float eps, void* stream) {
+  LLMY_REQUIRE(T >= 0 && k > 0 && (D == 256 || D == 512 || D == 1024 || D == 2048));
+  if (T == 0) return 0;
+  LLMY_REQUIRE(y && route_pos && x && (w == nullptr || h != nullptr));
+  LLMY_REQUIRE(aligned(y, 16) && aligned(x, 16) && (w == nullptr || (aligned(w, 16) && aligned(h, 8))));
+  const hipStream_t s = as_stream(stream);
+#define LLMY_COMBINE(N)                                                                        \
+  hipLaunchKernelGGL(combine_norm_kernel<N>, dim3((T + 3) / 4), dim3(256), 0, s, y, route_pos, \
+                     w, x, h, T, k, eps)
+  LLMY_NCH_SWITCH(D, LLMY_COMBINE)
+#undef LLMY_COMBINE
   return launch_status();
 }

@@ -1,20 +1,25 @@
 // Weight-streaming GEMM for the decode path: Y[M, N] = X[M, K] . W[N, K]^T
-// with few rows M (decode batch, or the tokens routed to one expert) and the
-// weights read from HBM exactly once per 64-row chunk of M.
+// with few rows M (the decode batch, or the tokens routed to one expert); the
+// weights are read from HBM once per chunk of M and the kernel is HBM-bound.
 //
 // Mapping onto v_mfma_f32_16x16x32_bf16 (wave64):
-//   * tokens are the MFMA rows (A), weight rows the MFMA columns (B), so one
-//     wave owns 16 weight rows and up to 64 tokens (4 row blocks);
-//   * a K block of 256 is 8 MFMAs.  Lane l (row/col r = l%16, group g = l/16)
-//     loads 128 contiguous bytes, elements [kb + 64g, kb + 64g + 64), of its
-//     weight row and of its token row.  MFMA j consumes the j-th 16 bytes, so
-//     A and B agree on which k each (lane, slot) holds; over the 8 MFMAs every
-//     k of the block is used once.  Per weight row a wave reads 512
-//     contiguous bytes per K block, no LDS staging is needed, and the next K
-//     block's weights are prefetched into registers during the MFMAs;
+//   * tokens are the MFMA rows (A), weight rows the MFMA columns (B); one
+//     workgroup owns 16 weight rows and splits K over its S waves (wave w
+//     takes the 256-wide K blocks w, w + S, ...), so all of a tile's weight
+//     bytes are requested at once; partial sums meet in LDS in wave order
+//     (deterministic) and wave 0 runs the fused epilogue;
+//   * a 256-wide K block is 8 MFMAs.  Lane l (row r = l%16, group g = l/16)
+//     supplies for MFMA j the elements k = kb + 32j + 8g .. +8 of its token
+//     row and of its weight row (the instruction's native k order), so the 4
+//     lanes of a row read 64 contiguous bytes per load instruction;
+//   * weights can be stored in that operand order ("packed": for each 16-row
+//     block and 256-wide K block, 8 tiles of 64 lanes x 16 bytes), so one
+//     wave's 16-byte-per-lane load of a B operand reads 1 KiB contiguous.
+//     The row-major [N, K] layout is also accepted (16-byte pieces of 16
+//     different rows per load instruction);
 //   * D layout: lane l holds D[4*(l/16) + i][l % 16], i = 0..3.
-// Epilogues are fused: bf16/fp32 store, residual add, gated residual add,
-// SwiGLU over a (gate, up) row pair, and the gate-weighted MoE down store.
+// Epilogues: bf16/fp32 store, residual add, gated residual add, SwiGLU over
+// a (gate, up) row pair, and the gate-weighted MoE down store.
 #include "common.hpp"
 #include "abi_util.hpp"
 
@@ -51,19 +56,26 @@ struct WsArgs {
   int x_rows;      // MoE: rows of x (bounds for the gathered token index)
 };
 
-__device__ __forceinline__ void load128(const uint16_t* p, uint4* v) {
-  const uint4* q = reinterpret_cast<const uint4*>(p);
-#pragma unroll
-  for (int j = 0; j < 8; ++j) v[j] = q[j];
+// Packed index of W[n][k] (N % 16 == 0, K % 256 == 0): block (n/16, k/256)
+// holds 8 tiles j; tile j lane l element e is W[16*nb + l%16][256*kb + 32*j + 8*(l/16) + e].
+__host__ __device__ __forceinline__ long long packed_index(int n, int k, int K) {
+  const int nb = n >> 4, r = n & 15;
+  const int kb = k >> 8, kk = k & 255;
+  const int j = kk >> 5, g = (kk >> 3) & 3, e = kk & 7;
+  const int lane = g * 16 + r;
+  return ((((static_cast<long long>(nb) * (K >> 8) + kb) * 8 + j) * 64 + lane) << 3) + e;
 }
 
-template <int EPI, int MODE>
-__global__ __launch_bounds__(256) void wsgemm_kernel(WsArgs a) {
+template <int EPI, int MODE, bool PACKED, int MB>
+__global__ __launch_bounds__(512) void wsgemm_kernel(WsArgs a) {
   constexpr bool kPair = (EPI == kSwiGLU);
+  constexpr int kSlots = (kPair ? 2 : 1) * MB * 4;
+  constexpr int kRows = 16 * MB;  // token rows per chunk
+  extern __shared__ float red[];  // [S][kSlots][64]
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int n0 = (blockIdx.x * 4 + wave) * 16;
-  if (n0 >= a.N) return;  // no block-level synchronisation below
+  const int S = blockDim.x >> 6;
+  const int n0 = blockIdx.x * 16;
   int row_begin = 0;
   int M = a.M;
   if (MODE != kDense) {
@@ -72,74 +84,102 @@ __global__ __launch_bounds__(256) void wsgemm_kernel(WsArgs a) {
     row_begin = min(max(a.offsets[blockIdx.y], 0), a.rows_total);
     M = min(max(a.offsets[blockIdx.y + 1], row_begin), a.rows_total) - row_begin;
   }
-  if (M <= 0) return;  // an expert with no routes reads no weights
+  if (M <= 0) return;  // uniform over the workgroup: an idle expert reads no weights
 
   const int r = lane & 15;
   const int g = lane >> 4;
-  const uint16_t* wrow = a.w + static_cast<long long>(blockIdx.y) * a.w_expert_stride +
-                         static_cast<long long>(n0 + r) * a.K + 64 * g;
   const int K = a.K;
+  const uint16_t* wbase = a.w + static_cast<long long>(blockIdx.y) * a.w_expert_stride;
+  // B operand address of (K block kb, MFMA j) for this lane: packed -> tile
+  // (kb*8 + j) of the 16-row block; row-major -> row n0 + r, k = kb + 32j + 8g.
+  const uint16_t* wlane =
+      PACKED ? wbase + (static_cast<long long>(blockIdx.x) * (K >> 8) * 8 * 64 + lane) * 8
+             : wbase + static_cast<long long>(n0 + r) * K + 8 * g;
 
-  for (int m0 = 0; m0 < M; m0 += 64) {
-    const int nmb = min(4, (M - m0 + 15) >> 4);
-    const uint16_t* xrow[4];
-    bool valid[4];
+  for (int m0 = 0; m0 < M; m0 += kRows) {
+    const int nmb = min(MB, (M - m0 + 15) >> 4);
+    const uint16_t* xrow[MB];
+    bool valid[MB];
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb) {
+    for (int mb = 0; mb < MB; ++mb) {
       const int m = m0 + 16 * mb + r;
       valid[mb] = m < M;
       int src = valid[mb] ? row_begin + m : row_begin;
       if (MODE == kMoeGather) src = min(max(a.sorted_routes[src] / a.route_k, 0), a.x_rows - 1);
-      xrow[mb] = a.x + static_cast<long long>(src) * a.ldx + 64 * g;
+      xrow[mb] = a.x + static_cast<long long>(src) * a.ldx + 8 * g;
     }
-    f32x4 acc[4], accu[4];
+    f32x4 acc[MB], accu[MB];
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb) {
+    for (int mb = 0; mb < MB; ++mb) {
       acc[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
       accu[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
-    uint4 bw[8], bu[8], nw[8], nu[8];
-    load128(wrow, bw);
-    if (kPair) load128(wrow + a.pair_offset, bu);
-    for (int kb = 0; kb < K; kb += 256) {
-      const bool more = kb + 256 < K;
-      if (more) {
-        load128(wrow + kb + 256, nw);
-        if (kPair) load128(wrow + a.pair_offset + kb + 256, nu);
+    for (int kb = wave * 256; kb < K; kb += S * 256) {
+      // Issue every load of this K block before the first MFMA.
+      uint4 bw[8], bu[8], av[MB][8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const long long off = PACKED ? (static_cast<long long>(kb >> 8) * 8 + j) * 512 : kb + 32 * j;
+        bw[j] = *reinterpret_cast<const uint4*>(wlane + off);
+        if (kPair) bu[j] = *reinterpret_cast<const uint4*>(wlane + a.pair_offset + off);
       }
 #pragma unroll
-      for (int mb = 0; mb < 4; ++mb) {
-        if (mb < nmb) {
-          uint4 av[8];
-          if (valid[mb]) {
-            load128(xrow[mb] + kb, av);
-          } else {
+      for (int mb = 0; mb < MB; ++mb) {
 #pragma unroll
-            for (int j = 0; j < 8; ++j) av[j] = uint4{0u, 0u, 0u, 0u};
-          }
+        for (int j = 0; j < 8; ++j)
+          av[mb][j] = (mb < nmb && valid[mb])
+                          ? *reinterpret_cast<const uint4*>(xrow[mb] + kb + 32 * j)
+                          : uint4{0u, 0u, 0u, 0u};
+      }
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
+        if (mb < nmb) {
 #pragma unroll
           for (int j = 0; j < 8; ++j) {
-            acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(av[j]), as_bf16x8(bw[j]),
-                                                              acc[mb], 0, 0, 0);
+            acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(av[mb][j]),
+                                                              as_bf16x8(bw[j]), acc[mb], 0, 0, 0);
             if (kPair)
               accu[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                  as_bf16x8(av[j]), as_bf16x8(bu[j]), accu[mb], 0, 0, 0);
+                  as_bf16x8(av[mb][j]), as_bf16x8(bu[j]), accu[mb], 0, 0, 0);
           }
-        }
-      }
-      if (more) {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          bw[j] = nw[j];
-          if (kPair) bu[j] = nu[j];
         }
       }
     }
 
+    if (S > 1) {
+      __syncthreads();  // the previous chunk's reduction has finished reading
+      if (wave > 0) {
+        float* dst = red + (static_cast<size_t>(wave) * kSlots) * 64 + lane;
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            dst[(mb * 4 + i) * 64] = acc[mb][i];
+            if (kPair) dst[(MB * 4 + mb * 4 + i) * 64] = accu[mb][i];
+          }
+        }
+      }
+      __syncthreads();
+      if (wave == 0) {
+        for (int w = 1; w < S; ++w) {
+          const float* src = red + (static_cast<size_t>(w) * kSlots) * 64 + lane;
+#pragma unroll
+          for (int mb = 0; mb < MB; ++mb) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              acc[mb][i] += src[(mb * 4 + i) * 64];
+              if (kPair) accu[mb][i] += src[(MB * 4 + mb * 4 + i) * 64];
+            }
+          }
+        }
+      }
+    }
+    if (wave != 0) continue;
+
     // Epilogue: lane holds rows m0 + 16mb + 4g + i, column n0 + r.
     const int n = n0 + r;
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb) {
+    for (int mb = 0; mb < MB; ++mb) {
       if (mb < nmb) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -169,11 +209,32 @@ __global__ __launch_bounds__(256) void wsgemm_kernel(WsArgs a) {
   }
 }
 
-template <int EPI, int MODE>
-static int32_t launch_ws(const WsArgs& a, int grid_y, hipStream_t s) {
-  const int tiles = (a.N + 63) / 64;
-  hipLaunchKernelGGL((wsgemm_kernel<EPI, MODE>), dim3(tiles, grid_y), dim3(256), 0, s, a);
+template <int EPI, int MODE, int MB>
+static int32_t launch_ws(const WsArgs& a, int grid_y, bool packed, hipStream_t s) {
+  const int waves = std::max(1, std::min(8, a.K / 256));
+  const size_t lds = waves > 1 ? static_cast<size_t>(waves) * (EPI == kSwiGLU ? 2 : 1) * MB * 4 *
+                                     64 * sizeof(float)
+                               : 0;
+  const dim3 grid(a.N / 16, grid_y), block(64 * waves);
+  if (packed)
+    hipLaunchKernelGGL((wsgemm_kernel<EPI, MODE, true, MB>), grid, block, lds, s, a);
+  else
+    hipLaunchKernelGGL((wsgemm_kernel<EPI, MODE, false, MB>), grid, block, lds, s, a);
   return launch_status();
+}
+
+// Row-major [batch][N][K] -> packed tiles (same element count).
+__global__ __launch_bounds__(256) void pack_kernel(const uint16_t* __restrict__ w,
+                                                   uint16_t* __restrict__ out, int N, int K,
+                                                   long long total) {
+  for (long long i = blockIdx.x * 256ll + threadIdx.x; i < total; i += 256ll * gridDim.x) {
+    const long long per = static_cast<long long>(N) * K;
+    const long long b = i / per;
+    const long long rem = i - b * per;
+    const int n = static_cast<int>(rem / K);
+    const int k = static_cast<int>(rem - static_cast<long long>(n) * K);
+    out[b * per + packed_index(n, k, K)] = w[i];
+  }
 }
 
 // out[t] (+)= sum_j y[route_pos[t*k + j]] in j order; y [T*k, D] fp32.
@@ -211,11 +272,24 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restric
 
 using namespace llmy;
 
+extern "C" int32_t llmy_pack_weights_bf16(const llmy_bf16* w, llmy_bf16* out, int64_t batch,
+                                          int32_t N, int32_t K, void* stream) {
+  LLMY_REQUIRE(batch >= 0 && N > 0 && N % 16 == 0 && K > 0 && K % 256 == 0);
+  if (batch == 0) return 0;
+  LLMY_REQUIRE(w && out && w != out);
+  const long long total = batch * N * static_cast<long long>(K);
+  const int blocks = static_cast<int>(std::min<long long>((total + 255) / 256, 65536));
+  hipLaunchKernelGGL(pack_kernel, dim3(blocks), dim3(256), 0, as_stream(stream), w, out, N, K,
+                     total);
+  return launch_status();
+}
+
 extern "C" int32_t llmy_linear_bf16(const llmy_bf16* x, const llmy_bf16* w, void* out,
                                     const float* aux, int32_t M, int32_t N, int32_t K,
-                                    int32_t epilogue, void* stream) {
+                                    int32_t epilogue, int32_t weight_layout, void* stream) {
   LLMY_REQUIRE(M >= 0 && N > 0 && N % 16 == 0 && K > 0 && K % 256 == 0);
   LLMY_REQUIRE(epilogue >= kStoreBf16 && epilogue <= kResidGated);
+  LLMY_REQUIRE(weight_layout == 0 || weight_layout == 1);
   if (M == 0) return 0;
   LLMY_REQUIRE(x && w && out);
   LLMY_REQUIRE(epilogue != kResidGated || aux != nullptr);
@@ -224,11 +298,12 @@ extern "C" int32_t llmy_linear_bf16(const llmy_bf16* x, const llmy_bf16* w, void
   a.x = x; a.w = w; a.out = out; a.aux = aux;
   a.M = M; a.N = N; a.K = K; a.ldx = K; a.ldo = N; a.route_k = 1;
   const hipStream_t s = as_stream(stream);
+  const bool packed = weight_layout == 1;
   switch (epilogue) {
-    case kStoreBf16: return launch_ws<kStoreBf16, kDense>(a, 1, s);
-    case kStoreF32: return launch_ws<kStoreF32, kDense>(a, 1, s);
-    case kResidAdd: return launch_ws<kResidAdd, kDense>(a, 1, s);
-    default: return launch_ws<kResidGated, kDense>(a, 1, s);
+    case kStoreBf16: return launch_ws<kStoreBf16, kDense, 4>(a, 1, packed, s);
+    case kStoreF32: return launch_ws<kStoreF32, kDense, 4>(a, 1, packed, s);
+    case kResidAdd: return launch_ws<kResidAdd, kDense, 4>(a, 1, packed, s);
+    default: return launch_ws<kResidGated, kDense, 4>(a, 1, packed, s);
   }
 }
 
@@ -236,27 +311,36 @@ extern "C" int32_t llmy_moe_experts_bf16(const llmy_bf16* x, const int32_t* offs
                                          const int32_t* sorted_routes, const float* gates,
                                          const llmy_bf16* w_gate_up, const llmy_bf16* w_down,
                                          llmy_bf16* act, float* y, int32_t T, int32_t D,
-                                         int32_t H, int32_t E, int32_t k, void* stream) {
+                                         int32_t H, int32_t E, int32_t k, int32_t weight_layout,
+                                         void* stream) {
   LLMY_REQUIRE(T >= 0 && D > 0 && D % 256 == 0 && H > 0 && H % 256 == 0);
-  LLMY_REQUIRE(E > 0 && k > 0 && k <= E);
+  LLMY_REQUIRE(E > 0 && k > 0 && k <= E && (weight_layout == 0 || weight_layout == 1));
   if (T == 0) return 0;
   LLMY_REQUIRE(x && offsets && sorted_routes && gates && w_gate_up && w_down && act && y);
   LLMY_REQUIRE(aligned(x, 16) && aligned(w_gate_up, 16) && aligned(w_down, 16) &&
                aligned(act, 16) && aligned(y, 16));
   const hipStream_t s = as_stream(stream);
+  const bool packed = weight_layout == 1;
   WsArgs a{};
   a.x = x; a.w = w_gate_up; a.out = act; a.offsets = offsets; a.sorted_routes = sorted_routes;
   a.w_expert_stride = 2ll * H * D; a.pair_offset = static_cast<long long>(H) * D;
   a.N = H; a.K = D; a.ldx = D; a.ldo = H; a.route_k = k;
   a.rows_total = T * k; a.x_rows = T;
-  int32_t st = launch_ws<kSwiGLU, kMoeGather>(a, E, s);
-  if (st != 0) return st;
   WsArgs b{};
   b.x = act; b.w = w_down; b.out = y; b.aux = gates; b.offsets = offsets;
   b.sorted_routes = sorted_routes; b.w_expert_stride = static_cast<long long>(D) * H;
   b.N = D; b.K = H; b.ldx = H; b.ldo = D; b.route_k = k;
   b.rows_total = T * k; b.x_rows = T * k;
-  return launch_ws<kMoeDown, kMoeDirect>(b, E, s);
+  // Few routes per expert (decode): 16-row chunks; otherwise 64-row chunks.
+  int32_t st;
+  if (T * k <= 16 * E) {
+    st = launch_ws<kSwiGLU, kMoeGather, 1>(a, E, packed, s);
+    if (st != 0) return st;
+    return launch_ws<kMoeDown, kMoeDirect, 1>(b, E, packed, s);
+  }
+  st = launch_ws<kSwiGLU, kMoeGather, 4>(a, E, packed, s);
+  if (st != 0) return st;
+  return launch_ws<kMoeDown, kMoeDirect, 4>(b, E, packed, s);
 }
 
 extern "C" int32_t llmy_moe_combine(const float* y, const int32_t* route_pos, void* out,

@@ -15,6 +15,50 @@
 
 namespace llmy {
 
+// Top-k over the logits held as mine[s] = logit(lane + 64 s) (E <= 256) and
+// softmax over the k picks, written to idx_row[0..k) / gates_row[0..k).  Rank
+// j is kept by lane j, so no per-lane arrays are indexed dynamically.
+__device__ __forceinline__ void topk_softmax_store(const float (&mine)[4], int E, int k,
+                                                   int lane, int32_t* __restrict__ idx_row,
+                                                   float* __restrict__ gates_row) {
+  uint64_t keys[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    const int e = lane + 64 * s;
+    keys[s] = (e < E) ? value_index_key(mine[s], static_cast<uint32_t>(e)) : 0ull;
+  }
+  int my_idx = 0;
+  float my_val = 0.f;
+  for (int j = 0; j < k; ++j) {
+    uint64_t best = keys[0];
+#pragma unroll
+    for (int s = 1; s < 4; ++s) best = keys[s] > best ? keys[s] : best;
+    best = wave_max_u64(best);
+    const int e = static_cast<int>(key_index(best));
+    float val = mine[0];
+#pragma unroll
+    for (int s = 1; s < 4; ++s) val = (e >> 6) == s ? mine[s] : val;
+    val = __shfl(val, e & 63, kWave);
+    if (lane == j) {
+      my_idx = e;
+      my_val = val;
+    }
+    if ((e & 63) == lane) {
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+        if ((e >> 6) == s) keys[s] = 0ull;
+    }
+  }
+  const float m = __shfl(my_val, 0, kWave);
+  const float ex = lane < k ? expf(my_val - m) : 0.f;
+  const float inv = 1.0f / wave_sum(ex);
+  if (lane < k) {
+    idx_row[lane] = my_idx;
+    gates_row[lane] = ex * inv;
+  }
+}
+
+
 // One wavefront per token, four tokens per 256-thread block.  The normalised
 // row is staged in LDS (D floats per wave) so every expert's dot product reads
 // it from LDS while the fp32 router matrix streams through L2.
@@ -73,39 +117,8 @@ __global__ __launch_bounds__(256) void router_topk_bf16_kernel(
     }
   }
 
-  // k rounds of (value, lowest index) argmax over the remaining experts.
-  uint64_t keys[4];
-#pragma unroll
-  for (int s = 0; s < 4; ++s) {
-    const int e = lane + 64 * s;
-    keys[s] = (e < E) ? value_index_key(mine[s], static_cast<uint32_t>(e)) : 0ull;
-  }
-  float top_val[32];
-  int top_idx[32];
-  for (int j = 0; j < k; ++j) {
-    uint64_t best = keys[0];
-#pragma unroll
-    for (int s = 1; s < 4; ++s) best = keys[s] > best ? keys[s] : best;
-    best = wave_max_u64(best);
-    const int e = static_cast<int>(key_index(best));
-    top_idx[j] = e;
-    top_val[j] = __shfl(mine[e >> 6], e & 63, kWave);
-    if ((e & 63) == lane) keys[e >> 6] = 0ull;
-  }
-  if (lane == 0) {
-    const float m = top_val[0];
-    float ex[32];
-    float sum = 0.0f;
-    for (int j = 0; j < k; ++j) {
-      ex[j] = expf(top_val[j] - m);
-      sum += ex[j];
-    }
-    const float inv = 1.0f / sum;
-    for (int j = 0; j < k; ++j) {
-      idx_out[static_cast<size_t>(t) * k + j] = top_idx[j];
-      gates_out[static_cast<size_t>(t) * k + j] = ex[j] * inv;
-    }
-  }
+  topk_softmax_store(mine, E, k, lane, idx_out + static_cast<size_t>(t) * k, gates_out + static_cast<size_t>(t) * k);
+
 }
 
 // Top-k + softmax from precomputed fp32 logits [T, E]; one wavefront per token.
@@ -117,39 +130,13 @@ __global__ __launch_bounds__(256) void router_topk_from_logits_kernel(
   const int t = blockIdx.x * 4 + wave;
   if (t >= T) return;
   float mine[4];
-  uint64_t keys[4];
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
     const int e = lane + 64 * s;
     mine[s] = (e < E) ? logits[static_cast<size_t>(t) * E + e] : 0.0f;
-    keys[s] = (e < E) ? value_index_key(mine[s], static_cast<uint32_t>(e)) : 0ull;
   }
-  float top_val[32];
-  int top_idx[32];
-  for (int j = 0; j < k; ++j) {
-    uint64_t best = keys[0];
-#pragma unroll
-    for (int s = 1; s < 4; ++s) best = keys[s] > best ? keys[s] : best;
-    best = wave_max_u64(best);
-    const int e = static_cast<int>(key_index(best));
-    top_idx[j] = e;
-    top_val[j] = __shfl(mine[e >> 6], e & 63, kWave);
-    if ((e & 63) == lane) keys[e >> 6] = 0ull;
-  }
-  if (lane == 0) {
-    const float m = top_val[0];
-    float ex[32];
-    float sum = 0.0f;
-    for (int j = 0; j < k; ++j) {
-      ex[j] = expf(top_val[j] - m);
-      sum += ex[j];
-    }
-    const float inv = 1.0f / sum;
-    for (int j = 0; j < k; ++j) {
-      idx_out[static_cast<size_t>(t) * k + j] = top_idx[j];
-      gates_out[static_cast<size_t>(t) * k + j] = ex[j] * inv;
-    }
-  }
+  topk_softmax_store(mine, E, k, lane, idx_out + static_cast<size_t>(t) * k, gates_out + static_cast<size_t>(t) * k);
+
 }
 
 // Stable counting sort of n = T*k expert ids in [0, E) with one 1024-thread
@@ -163,11 +150,20 @@ __global__ __launch_bounds__(256) void router_topk_from_logits_kernel(
 // output, which is always in range).
 constexpr int kPermuteWaves = 16;
 
-__global__ __launch_bounds__(1024) void moe_permute_kernel(
-    const int32_t* __restrict__ expert_ids, int n, int E,
-    int32_t* __restrict__ counts, int32_t* __restrict__ offsets,
-    int32_t* __restrict__ sorted_routes, int32_t* __restrict__ route_pos) {
-  extern __shared__ int32_t cnt[];  // [kPermuteWaves][E], then offsets[E+1]
+// Stable counting sort of n expert ids (read through `get(r)`) by one
+// 1024-thread workgroup.  Wave w owns a contiguous run of 64-route chunks, so
+// walking the waves in order and the chunks in order visits routes in
+// ascending r.
+//   pass 1: per-wave expert histograms (LDS integer atomics: order-free);
+//   scan:   expert offsets and per-wave bases;
+//   pass 2: each chunk ranks its lanes per expert with ballots and places
+//           route r at offsets[e] + (routes of e before r).
+// `cnt` is LDS scratch of kPermuteWaves * E + E + 1 ints.  Ids outside
+// [0, E) are not placed.
+template <typename Get>
+__device__ void permute_block(Get get, int n, int E, int32_t* __restrict__ counts,
+                              int32_t* __restrict__ offsets, int32_t* __restrict__ sorted_routes,
+                              int32_t* __restrict__ route_pos, int32_t* cnt) {
   int32_t* offs = cnt + kPermuteWaves * E;
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
@@ -181,7 +177,7 @@ __global__ __launch_bounds__(1024) void moe_permute_kernel(
   for (int c = c0; c < c1; ++c) {
     const int r = c * 64 + lane;
     if (r < n) {
-      const int e = expert_ids[r];
+      const int e = get(r);
       if (e >= 0 && e < E) atomicAdd(&cnt[wave * E + e], 1);
     }
   }
@@ -219,7 +215,7 @@ __global__ __launch_bounds__(1024) void moe_permute_kernel(
     const int r = c * 64 + lane;
     int e = -1;
     if (r < n) {
-      e = expert_ids[r];
+      e = get(r);
       if (e < 0 || e >= E) e = -1;
     }
     uint64_t pending = __ballot(e >= 0);
@@ -239,6 +235,109 @@ __global__ __launch_bounds__(1024) void moe_permute_kernel(
       pending &= ~same;
     }
   }
+}
+
+__global__ __launch_bounds__(1024) void moe_permute_kernel(
+    const int32_t* __restrict__ expert_ids, int n, int E, int32_t* __restrict__ counts,
+    int32_t* __restrict__ offsets, int32_t* __restrict__ sorted_routes,
+    int32_t* __restrict__ route_pos) {
+  extern __shared__ int32_t cnt[];
+  permute_block([&](int r) { return expert_ids[r]; }, n, E, counts, offsets, sorted_routes,
+                route_pos, cnt);
+}
+
+// Decode-time MoE front end, router part: one wavefront per token, four
+// tokens per 256-thread workgroup, W_r [E, D] staged in LDS per workgroup:
+//   h2[t]    = bf16(RMSNorm(x[t]) * ffn_w)                 (norms.py:13-16)
+//   logits   = (RMSNorm(h2[t]) * router_w) . W_r^T, fp32   (context_router.py:62,71-72)
+//   idx, gates: top-k (ties -> lower index) + softmax      (context_router.py:73-74)
+// The token rows are requested before the W_r staging loads so both are in
+// flight together; each lane holds NCH float4 chunks of its row.
+template <int NCH>
+__global__ __launch_bounds__(256) void moe_route_norm_kernel(
+    const float* __restrict__ x, const float* __restrict__ ffn_w,
+    const float* __restrict__ router_w, const float* __restrict__ w_router,
+    uint16_t* __restrict__ h2, int32_t* __restrict__ idx_out, float* __restrict__ gates_out,
+    int T, int E, int k, float eps) {
+  constexpr int D = NCH * 256;
+  extern __shared__ float wr[];  // [E][D]
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * 4 + wave;
+  const bool active = t < T;
+  float4 v[NCH];
+#pragma unroll
+  for (int c = 0; c < NCH; ++c)
+    v[c] = active ? *reinterpret_cast<const float4*>(x + static_cast<long long>(t) * D +
+                                                       4 * lane + 256 * c)
+                  : make_float4(0.f, 0.f, 0.f, 0.f);
+  {
+    // E*D <= 24576 floats = at most 24 float4 per thread, in 3 batches of 8.
+    const int n4 = (E * D) >> 2;
+#pragma unroll
+    for (int b8 = 0; b8 < 3; ++b8) {
+      float4 st[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const int i = min(static_cast<int>(threadIdx.x) + (b8 * 8 + q) * 256, n4 - 1);
+        st[q] = reinterpret_cast<const float4*>(w_router)[i];
+      }
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const int i = threadIdx.x + (b8 * 8 + q) * 256;
+        if (i < n4) reinterpret_cast<float4*>(wr)[i] = st[q];
+      }
+    }
+  }
+  __syncthreads();
+  if (!active) return;
+
+  float ss = 0.f;
+#pragma unroll
+  for (int c = 0; c < NCH; ++c)
+    ss += v[c].x * v[c].x + v[c].y * v[c].y + v[c].z * v[c].z + v[c].w * v[c].w;
+  const float r1 = rsqrtf(wave_sum(ss) / static_cast<float>(D) + eps);
+  float ss2 = 0.f;
+  uint16_t* hrow = h2 + static_cast<long long>(t) * D;
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    const int d = 4 * lane + 256 * c;
+    const float4 fw = *reinterpret_cast<const float4*>(ffn_w + d);
+    const uint32_t lo = pack_bf2(v[c].x * r1 * fw.x, v[c].y * r1 * fw.y);
+    const uint32_t hi = pack_bf2(v[c].z * r1 * fw.z, v[c].w * r1 * fw.w);
+    *reinterpret_cast<uint2*>(hrow + d) = make_uint2(lo, hi);
+    v[c].x = __uint_as_float(lo << 16);
+    v[c].y = __uint_as_float(lo & 0xffff0000u);
+    v[c].z = __uint_as_float(hi << 16);
+    v[c].w = __uint_as_float(hi & 0xffff0000u);
+    ss2 += v[c].x * v[c].x + v[c].y * v[c].y + v[c].z * v[c].z + v[c].w * v[c].w;
+  }
+  const float r2 = rsqrtf(wave_sum(ss2) / static_cast<float>(D) + eps);
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    const float4 rw = *reinterpret_cast<const float4*>(router_w + 4 * lane + 256 * c);
+    v[c].x = (v[c].x * r2) * rw.x;
+    v[c].y = (v[c].y * r2) * rw.y;
+    v[c].z = (v[c].z * r2) * rw.z;
+    v[c].w = (v[c].w * r2) * rw.w;
+  }
+  float mine[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int e = 0; e < E; ++e) {
+    const float* we = wr + e * D + 4 * lane;
+    float acc = 0.f;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      const float4 w4 = *reinterpret_cast<const float4*>(we + 256 * c);
+      acc = fmaf(v[c].x, w4.x, acc);
+      acc = fmaf(v[c].y, w4.y, acc);
+      acc = fmaf(v[c].z, w4.z, acc);
+      acc = fmaf(v[c].w, w4.w, acc);
+    }
+    acc = wave_sum(acc);
+    if ((e & 63) == lane) mine[e >> 6] = acc;
+  }
+  topk_softmax_store(mine, E, k, lane, idx_out + t * k, gates_out + t * k);
+
 }
 
 }  // namespace llmy
@@ -279,5 +378,40 @@ extern "C" int32_t llmy_moe_permute(const int32_t* expert_ids, int32_t n_routes,
   const size_t lds = (static_cast<size_t>(kPermuteWaves) * E + E + 1) * sizeof(int32_t);
   hipLaunchKernelGGL(moe_permute_kernel, dim3(1), dim3(1024), lds, as_stream(stream), expert_ids,
                      n_routes, E, counts, offsets, sorted_routes, route_pos);
+  return launch_status();
+}
+
+extern "C" int32_t llmy_moe_route_decode(const float* x, const float* ffn_w, const float* router_w,
+                                         const float* w_router, llmy_bf16* h2, int32_t* idx,
+                                         float* gates, int32_t* counts, int32_t* offsets,
+                                         int32_t* sorted_routes, int32_t* route_pos, int32_t T,
+                                         int32_t D, int32_t E, int32_t k, float eps,
+                                         void* stream) {
+  LLMY_REQUIRE(T >= 0 && (D == 256 || D == 512 || D == 1024));
+  LLMY_REQUIRE(E > 0 && E <= 256 && k > 0 && k <= 8 && k <= E);
+  LLMY_REQUIRE(static_cast<long long>(E) * D <= 24576);
+  LLMY_REQUIRE(counts && offsets);
+  const hipStream_t s = as_stream(stream);
+  const size_t perm_lds = (static_cast<size_t>(kPermuteWaves) * E + E + 1) * sizeof(int32_t);
+  if (T > 0) {
+    LLMY_REQUIRE(x && ffn_w && router_w && w_router && h2 && idx && gates && sorted_routes &&
+                 route_pos);
+    LLMY_REQUIRE(aligned(x, 16) && aligned(ffn_w, 16) && aligned(router_w, 16) &&
+                 aligned(w_router, 16) && aligned(h2, 8));
+    const size_t lds = static_cast<size_t>(E) * D * sizeof(float);
+#define LLMY_ROUTE(NCH)                                                                       \
+  hipLaunchKernelGGL(moe_route_norm_kernel<NCH>, dim3((T + 3) / 4), dim3(256), lds, s, x,      \
+                     ffn_w, router_w, w_router, h2, idx, gates, T, E, k, eps)
+    switch (D) {
+      case 256: LLMY_ROUTE(1); break;
+      case 512: LLMY_ROUTE(2); break;
+      default: LLMY_ROUTE(4); break;
+    }
+#undef LLMY_ROUTE
+    const int32_t st = launch_status();
+    if (st != 0) return st;
+  }
+  hipLaunchKernelGGL(moe_permute_kernel, dim3(1), dim3(1024), perm_lds, s, idx, T * k, E, counts,
+                     offsets, sorted_routes, route_pos);
   return launch_status();
 }

@@ -66,6 +66,15 @@ class HybridDecoder:
             self.w[p + "w_gate_up"] = torch.cat([up(p + "w_gate"), up(p + "w_up")], 1).contiguous()
             self.w[p + "w_down"] = up(p + "w_down")
 
+        # Decode GEMM weights are re-laid once into the packed operand order
+        # (llmy_pack_weights_bf16), so every weight byte streams as contiguous
+        # 1 KiB wavefront loads; the embedding keeps a row-major copy for the
+        # token lookup and a packed copy for the tied LM head.
+        for name in list(self.w):
+            if name.split(".")[-1] in ("wqkv", "wo", "wproj", "wout", "w_gate_up", "w_down"):
+                self.w[name] = ops.pack_weights(self.w[name])
+        self.w["lm_head"] = ops.pack_weights(self.w["embed"])
+
         # ---- state
         self.pos = torch.zeros(B, dtype=torch.int32, device=dev)
         self.state: dict = {}
@@ -110,6 +119,9 @@ class HybridDecoder:
             "next": torch.zeros(B, dtype=torch.int32, device=dev),
         }
         self.graph: torch.cuda.CUDAGraph | None = None
+        # Fused MoE front end (norm + router with W_r in LDS, then the
+        # permutation) when W_r fits in LDS; else three separate kernels.
+        self.fused_route = E * D <= 24576 and D in (256, 512, 1024) and k <= 8
         # Optional record of every MoE application's expert ids (verification
         # aid: lets a checker replay the kernel's discrete routing decisions).
         self.route_log: torch.Tensor | None = None
@@ -126,58 +138,67 @@ class HybridDecoder:
         p = f"L{l}."
         Hhd = cfg.attn_heads * cfg.attn_head_dim
         B, H, hd = self.B, cfg.attn_heads, cfg.attn_head_dim
-        ops.linear(b["h"], w[p + "wqkv"], out=b["qkv"])
+        ops.linear(b["h"], w[p + "wqkv"], out=b["qkv"], layout=ops.LAYOUT_PACKED)
         qkv = b["qkv"]
         q = qkv[:, :Hhd].view(B, H, hd)
         kn = qkv[:, Hhd:2 * Hhd].view(B, H, hd)
         vn = qkv[:, 2 * Hhd:].view(B, H, hd)
         ops.banded_attn_decode(q, kn, vn, st["k"], st["v"], self.pos, cfg.attn_scale,
                                out=b["ao"])
-        ops.linear(b["ao"].view(B, Hhd), w[p + "wo"], out=b["x"], epilogue=ops.EPI_RESID_ADD)
+        ops.linear(b["ao"].view(B, Hhd), w[p + "wo"], out=b["x"], epilogue=ops.EPI_RESID_ADD,
+                   layout=ops.LAYOUT_PACKED)
 
     def _gdn(self, l: int, st: dict) -> None:
         w, b = self.w, self.buf
         p = f"L{l}."
-        ops.linear(b["h"], w[p + "wproj"], out=b["proj"], epilogue=ops.EPI_STORE_F32)
-        ops.gdn_step_fused(b["proj"], w[p + "bb"], w[p + "decay"], st["S"], out=b["go"])
-        ops.gdn_conv_gate(b["h"], st["hist"], w[p + "conv"], out=b["cg"])
-        ops.linear(b["go"], w[p + "wout"], out=b["x"], epilogue=ops.EPI_RESID_GATED, aux=b["cg"])
+        ops.linear(b["h"], w[p + "wproj"], out=b["proj"], epilogue=ops.EPI_STORE_F32,
+                   layout=ops.LAYOUT_PACKED)
+        ops.gdn_step_fused(b["proj"], w[p + "bb"], w[p + "decay"], st["S"], out=b["go"],
+                           conv=(b["h"], st["hist"], w[p + "conv"], b["cg"]))
+        ops.linear(b["go"], w[p + "wout"], out=b["x"], epilogue=ops.EPI_RESID_GATED, aux=b["cg"],
+                   layout=ops.LAYOUT_PACKED)
 
-    def _moe(self, l: int) -> None:
+    def _moe(self, l: int, next_norm: torch.Tensor | None) -> None:
+        """Pre-MoE norm + router + permutation, experts, then the combine fused
+        with the next block's pre-norm (``next_norm``) into ``h``."""
         cfg, w, b = self.cfg, self.w, self.buf
         p = f"L{l}."
-        ops.rmsnorm(b["x"], w[p + "ffn_norm"], cfg.eps, out=b["h"])
-        from . import _lib
-        s = torch.cuda.current_stream().cuda_stream
-        _lib.call("llmy_router_topk_bf16", b["h"].data_ptr(), w[p + "router_norm"].data_ptr(),
-                  w[p + "w_router"].data_ptr(), None, b["idx"].data_ptr(), b["gates"].data_ptr(),
-                  self.B, cfg.d_model, cfg.n_experts, cfg.top_k, cfg.eps, s)
-        _lib.call("llmy_moe_permute", b["idx"].data_ptr(), self.B * cfg.top_k, cfg.n_experts,
-                  b["counts"].data_ptr(), b["offsets"].data_ptr(), b["sorted_routes"].data_ptr(),
-                  b["route_pos"].data_ptr(), s)
+        if self.fused_route:
+            ops.moe_route_decode(b["x"], w[p + "ffn_norm"], w[p + "router_norm"],
+                                 w[p + "w_router"], cfg.top_k, cfg.eps, bufs=b)
+        else:
+            ops.rmsnorm(b["x"], w[p + "ffn_norm"], cfg.eps, out=b["h"])
+            from . import _lib
+            s = torch.cuda.current_stream().cuda_stream
+            _lib.call("llmy_router_topk_bf16", b["h"].data_ptr(),
+                      w[p + "router_norm"].data_ptr(), w[p + "w_router"].data_ptr(), None,
+                      b["idx"].data_ptr(), b["gates"].data_ptr(), self.B, cfg.d_model,
+                      cfg.n_experts, cfg.top_k, cfg.eps, s)
+            _lib.call("llmy_moe_permute", b["idx"].data_ptr(), self.B * cfg.top_k,
+                      cfg.n_experts, b["counts"].data_ptr(), b["offsets"].data_ptr(),
+                      b["sorted_routes"].data_ptr(), b["route_pos"].data_ptr(), s)
         if self.route_log is not None:
             self.route_log[self._app].copy_(b["idx"])
             self._app = (self._app + 1) % self.route_log.shape[0]
-        perm = {"offsets": b["offsets"], "sorted_routes": b["sorted_routes"]}
-        ops.moe_experts(b["h"], perm, b["gates"], w[p + "w_gate_up"], w[p + "w_down"],
-                        act=b["act"], y=b["y"])
-        ops.moe_combine(b["y"], b["route_pos"], self.B, cfg.top_k, out=b["x"],
-                        mode=ops.MOE_OUT_RESID)
+        ops.moe_experts(b["h"], b, b["gates"], w[p + "w_gate_up"], w[p + "w_down"],
+                        act=b["act"], y=b["y"], layout=ops.LAYOUT_PACKED)
+        ops.moe_combine_norm(b["y"], b["route_pos"], b["x"], b["h"], next_norm, cfg.top_k,
+                             cfg.eps)
 
     # ------------------------------------------------------------------ step
     def _step_body(self) -> None:
         cfg, w, b = self.cfg, self.w, self.buf
-        ops.embed(b["tokens"], w["embed"], out=b["x"])
-        for loop in range(cfg.num_loops):
-            for l, kind in enumerate(cfg.layer_kinds):
-                ops.rmsnorm(b["x"], w[f"L{l}.mix_norm"], cfg.eps, out=b["h"])
-                if kind == "attn":
-                    self._attn(l, self.state[(loop, l)])
-                else:
-                    self._gdn(l, self.state[(loop, l)])
-                self._moe(l)
-        ops.rmsnorm(b["x"], w["final_norm"], cfg.eps, out=b["h"])
-        ops.linear(b["h"], w["embed"], out=b["logits"], epilogue=ops.EPI_STORE_F32)
+        ops.embed_norm(b["tokens"], w["embed"], w["L0.mix_norm"], b["x"], b["h"], cfg.eps)
+        apps = [(loop, l) for loop in range(cfg.num_loops) for l in range(cfg.n_layers)]
+        for i, (loop, l) in enumerate(apps):
+            if cfg.layer_kinds[l] == "attn":
+                self._attn(l, self.state[(loop, l)])
+            else:
+                self._gdn(l, self.state[(loop, l)])
+            nxt = w[f"L{apps[i + 1][1]}.mix_norm"] if i + 1 < len(apps) else w["final_norm"]
+            self._moe(l, nxt)
+        ops.linear(b["h"], w["lm_head"], out=b["logits"], epilogue=ops.EPI_STORE_F32,
+                   layout=ops.LAYOUT_PACKED)
         from . import _lib
         _lib.call("llmy_sample_argmax_f32", b["logits"].data_ptr(), self.B, cfg.vocab,
                   b["next"].data_ptr(), torch.cuda.current_stream().cuda_stream)

@@ -91,9 +91,24 @@ def argmax(logits: torch.Tensor) -> torch.Tensor:
 EPI_STORE_BF16, EPI_STORE_F32, EPI_RESID_ADD, EPI_RESID_GATED = 0, 1, 2, 3
 
 
+LAYOUT_ROWMAJOR, LAYOUT_PACKED = 0, 1
+
+
+def pack_weights(w: torch.Tensor) -> torch.Tensor:
+    """Row-major [..., N, K] bf16 -> the packed operand order (same shape/size)."""
+    _check(w, torch.bfloat16, "w")
+    N, K = w.shape[-2:]
+    batch = w.numel() // (N * K)
+    out = torch.empty_like(w)
+    _lib.call("llmy_pack_weights_bf16", _ptr(w), _ptr(out), batch, N, K, _stream())
+    return out
+
+
 def linear(x: torch.Tensor, w: torch.Tensor, out: torch.Tensor | None = None,
-           epilogue: int = EPI_STORE_BF16, aux: torch.Tensor | None = None) -> torch.Tensor:
-    """x [M,K] bf16 . w [N,K]^T with a fused epilogue (see llmy_linear_bf16)."""
+           epilogue: int = EPI_STORE_BF16, aux: torch.Tensor | None = None,
+           layout: int = LAYOUT_ROWMAJOR) -> torch.Tensor:
+    """x [M,K] bf16 . w [N,K]^T with a fused epilogue (see llmy_linear_bf16).
+    ``layout=LAYOUT_PACKED`` when w came from pack_weights."""
     M, K = x.shape
     N = w.shape[0]
     _check(x, torch.bfloat16, "x")
@@ -108,14 +123,14 @@ def linear(x: torch.Tensor, w: torch.Tensor, out: torch.Tensor | None = None,
     if aux is not None:
         _check(aux, torch.float32, "aux", (M, N))
     _lib.call("llmy_linear_bf16", _ptr(x), _ptr(w), _ptr(out), _ptr(aux), M, N, K, epilogue,
-              _stream())
+              layout, _stream())
     return out
 
 
 # --------------------------------------------------------------------------- MoE
 def moe_experts(x: torch.Tensor, perm: dict, gates: torch.Tensor, w_gate_up: torch.Tensor,
                 w_down: torch.Tensor, act: torch.Tensor | None = None,
-                y: torch.Tensor | None = None):
+                y: torch.Tensor | None = None, layout: int = LAYOUT_ROWMAJOR):
     """Routed SwiGLU experts over the permuted routes; returns (act, y)."""
     T, D = x.shape
     E, H2, D2 = w_gate_up.shape
@@ -134,7 +149,7 @@ def moe_experts(x: torch.Tensor, perm: dict, gates: torch.Tensor, w_gate_up: tor
     _check(y, torch.float32, "y", (n, D))
     _lib.call("llmy_moe_experts_bf16", _ptr(x), _ptr(perm["offsets"]), _ptr(perm["sorted_routes"]),
               _ptr(gates), _ptr(w_gate_up), _ptr(w_down), _ptr(act), _ptr(y), T, D, H, E, k,
-              _stream())
+              layout, _stream())
     return act, y
 
 
@@ -154,14 +169,14 @@ def moe_combine(y: torch.Tensor, route_pos: torch.Tensor, T: int, k: int,
 
 def moe_forward(x: torch.Tensor, w_router: torch.Tensor, w_gate_up: torch.Tensor,
                 w_down: torch.Tensor, k: int, router_norm: torch.Tensor | None = None,
-                eps: float = 1e-6) -> dict:
+                eps: float = 1e-6, layout: int = LAYOUT_ROWMAJOR) -> dict:
     """Full routed MoE layer op: router -> permute -> experts ->
     combine.  Returns a dict with idx, gates, perm, out (bf16 [T,D])."""
     T, D = x.shape
     E = w_router.shape[0]
     idx, gates = router_topk(x, w_router, k, router_norm, eps)
     perm = moe_permute(idx.view(-1), E)
-    act, y = moe_experts(x, perm, gates, w_gate_up, w_down)
+    act, y = moe_experts(x, perm, gates, w_gate_up, w_down, layout=layout)
     out = moe_combine(y, perm["route_pos"], T, k)
     return {"idx": idx, "gates": gates, "perm": perm, "out": out}
 
@@ -214,15 +229,69 @@ def gdn_step(q, k, v, beta, g, state, gate=None, out=None) -> torch.Tensor:
     return out
 
 
-def gdn_step_fused(proj, beta_bias, decay_logit, state, out=None) -> torch.Tensor:
+def gdn_step_fused(proj, beta_bias, decay_logit, state, out=None, conv=None) -> torch.Tensor:
+    """GDN step from the fused fp32 projection; ``conv=(h, hist, w, cg_out)``
+    also computes the causal conv gate in the same launch."""
     B, H, dk, dv = state.shape
     _check(proj, torch.float32, "proj")
     _check(state, torch.float32, "state")
     if out is None:
         out = torch.empty(B, H * dv, dtype=torch.bfloat16, device=proj.device)
+    ch = hist = cw = cg = None
+    D = 0
+    if conv is not None:
+        ch, hist, cw, cg = conv
+        D = ch.shape[1]
+        _check(ch, torch.bfloat16, "conv_h", (B, D))
+        _check(hist, torch.bfloat16, "conv_hist", (B, 3, D))
+        _check(cw, torch.float32, "conv_w", (D, 4))
+        _check(cg, torch.float32, "conv_out", (B, D))
     _lib.call("llmy_gdn_step_fused_f32", _ptr(proj), proj.shape[1], _ptr(beta_bias),
-              _ptr(decay_logit), _ptr(state), _ptr(out), B, H, dk, dv, _stream())
+              _ptr(decay_logit), _ptr(state), _ptr(out), _ptr(ch), _ptr(hist), _ptr(cw), _ptr(cg),
+              D, 4, B, H, dk, dv, _stream())
     return out
+
+
+def moe_route_decode(x, ffn_w, router_w, w_router, k, eps=1e-6, bufs=None) -> dict:
+    """Fused pre-MoE norm + router + permutation for small T (one launch)."""
+    T, D = x.shape
+    E = w_router.shape[0]
+    _check(x, torch.float32, "x")
+    _check(w_router, torch.float32, "w_router", (E, D))
+    dev = x.device
+    if bufs is None:
+        bufs = {"h": torch.empty(T, D, dtype=torch.bfloat16, device=dev),
+                "idx": torch.empty(T, k, dtype=torch.int32, device=dev),
+                "gates": torch.empty(T, k, dtype=torch.float32, device=dev),
+                "counts": torch.empty(E, dtype=torch.int32, device=dev),
+                "offsets": torch.empty(E + 1, dtype=torch.int32, device=dev),
+                "sorted_routes": torch.empty(T * k, dtype=torch.int32, device=dev),
+                "route_pos": torch.empty(T * k, dtype=torch.int32, device=dev)}
+    b = bufs
+    _lib.call("llmy_moe_route_decode", _ptr(x), _ptr(ffn_w), _ptr(router_w), _ptr(w_router),
+              _ptr(b["h"]), _ptr(b["idx"]), _ptr(b["gates"]), _ptr(b["counts"]),
+              _ptr(b["offsets"]), _ptr(b["sorted_routes"]), _ptr(b["route_pos"]), T, D, E, k,
+              eps, _stream())
+    return b
+
+
+def embed_norm(tokens, table, w, x, h, eps=1e-6) -> None:
+    V, D = table.shape
+    _check(tokens, torch.int32, "tokens")
+    _check(table, torch.bfloat16, "table")
+    B = tokens.numel()
+    _check(x, torch.float32, "x", (B, D))
+    _check(h, torch.bfloat16, "h", (B, D))
+    _lib.call("llmy_embed_norm_bf16", _ptr(tokens), _ptr(table), _ptr(w), _ptr(x), _ptr(h), B, D,
+              V, eps, _stream())
+
+
+def moe_combine_norm(y, route_pos, x, h=None, w=None, k=2, eps=1e-6) -> None:
+    T, D = x.shape
+    _check(y, torch.float32, "y", (T * k, D))
+    _check(x, torch.float32, "x")
+    _lib.call("llmy_moe_combine_norm", _ptr(y), _ptr(route_pos), _ptr(w), _ptr(x), _ptr(h), T, D,
+              k, eps, _stream())
 
 
 def gdn_conv_gate(h, hist, w, out=None) -> torch.Tensor:

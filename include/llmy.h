@@ -71,11 +71,22 @@ int32_t llmy_moe_permute(const int32_t* expert_ids, int32_t n_routes,
 /* Y[M,N] = X[M,K] . W[N,K]^T, bf16 operands, fp32 accumulation, with a fused
  * epilogue: 0 = store bf16 into out [M,N]; 1 = store fp32; 2 = out (fp32)
  * += Y (residual add); 3 = out (fp32) += Y * aux[M,N] (gated residual).
- * Limits: N % 16 == 0, K % 256 == 0.  Replaces linear_forward / k_linear_gemv
- * (llmy_cuda/src/model.cpp:1467-1515) and nn.Linear on the decode path. */
+ * weight_layout 0: W row-major [N,K] (nn.Linear); 1: W in the packed tile
+ * order of llmy_pack_weights_bf16.  Limits: N % 16 == 0, K % 256 == 0.
+ * Replaces linear_forward / k_linear_gemv (llmy_cuda/src/model.cpp:1467-1515)
+ * and nn.Linear on the decode path. */
 int32_t llmy_linear_bf16(const llmy_bf16* x, const llmy_bf16* w, void* out,
                          const float* aux, int32_t M, int32_t N, int32_t K,
-                         int32_t epilogue, void* stream);
+                         int32_t epilogue, int32_t weight_layout, void* stream);
+
+/* Re-lay batch row-major [N,K] bf16 matrices into the operand order the
+ * weight-streaming kernels read (for each 16-row block and 256-wide K
+ * block, 8 tiles of 64 lanes x 8 elements; tile j lane l element e =
+ * W[16*nb + l%16][256*kb + 32*j + 8*(l/16) + e]), so a wavefront's operand
+ * load is one contiguous KiB.  Same element count; out must not alias w.
+ * No counterpart in the reference (a load-time layout transform). */
+int32_t llmy_pack_weights_bf16(const llmy_bf16* w, llmy_bf16* out, int64_t batch,
+                               int32_t N, int32_t K, void* stream);
 
 /* --- SwiGLU MoE experts (model/layers/moe.py:72-81, expert.py:14-15) ------ */
 
@@ -85,12 +96,15 @@ int32_t llmy_linear_bf16(const llmy_bf16* x, const llmy_bf16* w, void* out,
  * x [T,D] bf16; w_gate_up [E,2H,D] bf16 (gate rows then up rows, the packing
  * of llmy.h:80-82 in the reference); w_down [E,D,H] bf16; gates [T*k] fp32;
  * act [T*k,H] bf16 and y [T*k,D] fp32 are caller-provided scratch.  Experts
- * with no routes read no weights.  Limits: D % 256 == 0, H % 256 == 0. */
+ * with no routes read no weights.  weight_layout as in llmy_linear_bf16
+ * (packed: each expert's [2H,D] and [D,H] packed separately).
+ * Limits: D % 256 == 0, H % 256 == 0. */
 int32_t llmy_moe_experts_bf16(const llmy_bf16* x, const int32_t* offsets,
                               const int32_t* sorted_routes, const float* gates,
                               const llmy_bf16* w_gate_up, const llmy_bf16* w_down,
                               llmy_bf16* act, float* y, int32_t T, int32_t D,
-                              int32_t H, int32_t E, int32_t k, void* stream);
+                              int32_t H, int32_t E, int32_t k, int32_t weight_layout,
+                              void* stream);
 
 /* out[t] = sum_j y[route_pos[t*k + j]] (j ascending) — the un-permute /
  * combine of moe.py:78-81 without atomics.  mode 0: store bf16 out [T,D];
@@ -133,11 +147,17 @@ int32_t llmy_gdn_step_bf16(const llmy_bf16* q, const llmy_bf16* k,
  * proj[b] = [q (H*dk) | k (H*dk) | v (H*dv) | gate logits (H*dv) | beta logits (H)]:
  * q, k L2-normalised per head (clamp 1e-12), beta = sigmoid(logit + beta_bias),
  * gate = sigmoid(logit), g = sigmoid(decay_logit[h]) (gated_deltanet.py:125-132),
- * then the step above.  out [B, H*dv] bf16. */
+ * then the step above; out [B, H*dv] bf16.  When conv_h != NULL the causal
+ * conv gate of llmy_gdn_conv_gate is computed in the same launch
+ * (conv_h [B,D] bf16 mixer input, conv_hist [B,3,D], conv_w [D,4],
+ * conv_out [B,D] fp32; D % H == 0, conv_kernel == 4). */
 int32_t llmy_gdn_step_fused_f32(const float* proj, int64_t proj_ld,
                                 const float* beta_bias, const float* decay_logit,
-                                float* state, llmy_bf16* out, int32_t B, int32_t H,
-                                int32_t dk, int32_t dv, void* stream);
+                                float* state, llmy_bf16* out, const llmy_bf16* conv_h,
+                                llmy_bf16* conv_hist, const float* conv_w,
+                                float* conv_out, int32_t D, int32_t conv_kernel,
+                                int32_t B, int32_t H, int32_t dk, int32_t dv,
+                                void* stream);
 
 /* Causal depthwise conv gate for one new token (gated_deltanet.py:257-268):
  * out[b,d] = sigmoid(sum_j w[d,j] * [hist[b,0..K-2,d], h[b,d]]_j), then the
@@ -155,6 +175,34 @@ int32_t llmy_rmsnorm_f32_bf16(const float* x, const float* w, llmy_bf16* out,
 /* x[b] = float(table[tokens[b]]) (ids clamped to [0,V)); table [V,D] bf16. */
 int32_t llmy_embed_bf16(const int32_t* tokens, const llmy_bf16* table, float* x,
                         int32_t B, int32_t D, int32_t V, void* stream);
+
+/* x[b] = float(table[tokens[b]]); h[b] = bf16(RMSNorm(x[b]) * w) — embedding
+ * gather fused with the first block's pre-norm.  D in {256,512,1024,2048}. */
+int32_t llmy_embed_norm_bf16(const int32_t* tokens, const llmy_bf16* table,
+                             const float* w, float* x, llmy_bf16* h, int32_t B,
+                             int32_t D, int32_t V, float eps, void* stream);
+
+/* MoE combine fused with the next pre-norm: x[t] += sum_j y[route_pos[t*k+j]]
+ * (j ascending), then h[t] = bf16(RMSNorm(x[t]) * w) unless w == NULL.
+ * D in {256,512,1024,2048}. */
+int32_t llmy_moe_combine_norm(const float* y, const int32_t* route_pos,
+                              const float* w, float* x, llmy_bf16* h, int32_t T,
+                              int32_t D, int32_t k, float eps, void* stream);
+
+/* Decode-time MoE front end (E*D <= 24576, D in {256,512,1024}, k <= 8):
+ *   h2[t] = bf16(RMSNorm(x[t]) * ffn_w)   (the block's pre-MoE norm),
+ *   logits = (RMSNorm(h2[t]) * router_w) . w_router^T in fp32, top-k (ties ->
+ *   lower index) + softmax -> idx [T,k], gates [T,k],
+ *   and the stable permutation of llmy_moe_permute — two launches (router with
+ *   W_r staged in LDS, one wave per token; then the permutation).
+ * Equivalent to llmy_rmsnorm_f32_bf16 + llmy_router_topk_bf16 +
+ * llmy_moe_permute (context_router.py:62,71-74; moe.py:42-66). */
+int32_t llmy_moe_route_decode(const float* x, const float* ffn_w,
+                              const float* router_w, const float* w_router,
+                              llmy_bf16* h2, int32_t* idx, float* gates,
+                              int32_t* counts, int32_t* offsets,
+                              int32_t* sorted_routes, int32_t* route_pos, int32_t T,
+                              int32_t D, int32_t E, int32_t k, float eps, void* stream);
 
 /* --- Sampling (sample_standalone.py:5609-5636) ---------------------------- */
 

@@ -136,12 +136,27 @@ def test_c5_slice_decode_step():
     assert float((lg.cpu() - lr).abs().max()) <= 2e-2 * float(lr.abs().max())
     for key, s in eng.state.items():
         if "S" in s:
-            assert rel_l2(s["S"], st[key]["S"]) <= 1e-4
+            # the state update's inputs (k, v, beta) are projections of the
+            # bf16-rounded activations, so the composed state agrees at bf16
+            # level; the kernel-level 1e-4 bound is test_gdn_step's
+            assert rel_l2(s["S"], st[key]["S"]) <= 5e-3
         else:
-            assert torch.equal(s["k"].float().cpu(), st[key]["k"])
+            # untouched slots are copied bit for bit; the new token's slot holds
+            # a GEMM output (one bf16 rounding of an fp32 sum) -> bf16 tolerance
+            slot = cfg.window % cfg.window
+            for name in ("k", "v"):
+                got, want = s[name].float().cpu(), st[key][name]
+                keep = torch.ones(cfg.window, dtype=torch.bool)
+                keep[slot] = False
+                assert torch.equal(got[:, :, keep], want[:, :, keep])
+                assert float((got[:, :, slot] - want[:, :, slot]).abs().max()) <= 2e-2
+    # greedy ids: exact wherever the oracle's top-2 gap exceeds twice the
+    # largest logit difference (only there is the argmax determined by both)
     gpu_next = eng.buf["next"].cpu().numpy()
     top2 = torch.topk(lr, 2).values
-    safe = ((top2[:, 0] - top2[:, 1]) > 1e-3).numpy()
+    eps = float((lg.cpu() - lr).abs().max())
+    safe = ((top2[:, 0] - top2[:, 1]) > 2 * eps).numpy()
+    assert safe.mean() > 0.5
     assert np.array_equal(gpu_next[safe], lr.argmax(-1).numpy()[safe])
 
 
