@@ -27,6 +27,8 @@ COMMON_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-I", str(INCLUDE), "-I", str(CSRC),
+    # streamed operands (weights, KV windows) use non-temporal loads
+    "-DLLMY_NT=1",
 ]
 
 _NOISE = "is not a recognized feature for this target"

@@ -28,6 +28,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "llmy_pack_weights_bf16": (_I, [_P, _P, _I64, _I, _I, _P]),
     "llmy_moe_experts_bf16": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P]),
     "llmy_moe_combine": (_I, [_P, _P, _P, _I, _I, _I, _I, _P]),
+    "llmy_moe_experts_routed_bf16": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I,
+                                          _P]),
     "llmy_banded_attn_decode_bf16": (_I, [_P, _P, _P, _I64, _I64, _P, _P, _P, _P, _I, _I, _I,
                                           _I, _F, _P]),
     "llmy_gdn_step_bf16": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P]),

@@ -84,8 +84,8 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
       const int key = c * 64 + i * KPG + kk;
       const int kl = min(key, W - 1);
       const long long off = slab + static_cast<long long>(kl) * HD + 8 * dc;
-      const uint4 kr = *reinterpret_cast<const uint4*>(k_cache + off);
-      vr[i] = *reinterpret_cast<const uint4*>(v_cache + off);
+      const uint4 kr = ld_stream(k_cache + off);
+      vr[i] = ld_stream(v_cache + off);
       float kf[8];
       unpack8(kr, kf);
       float d = 0.f;

@@ -48,6 +48,20 @@ __device__ __forceinline__ void unpack8(const uint4& v, float* out) {
   out[7] = __uint_as_float(v.w & 0xffff0000u);
 }
 
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+// 16-byte load of data that is streamed once per kernel (weights, the KV
+// window): with LLMY_NT the load carries the non-temporal hint so it does not
+// displace reusable lines in L2 / the Infinity Cache.
+__device__ __forceinline__ uint4 ld_stream(const void* p) {
+#if defined(LLMY_NT) && LLMY_NT
+  const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  return uint4{v.x, v.y, v.z, v.w};
+#else
+  return *reinterpret_cast<const uint4*>(p);
+#endif
+}
+
 __device__ __forceinline__ bf16x8 as_bf16x8(const uint4& v) {
   return __builtin_bit_cast(bf16x8, v);
 }

@@ -138,7 +138,7 @@ __global__ __launch_bounds__(256) void combine_norm_kernel(const float* __restri
     const int d = 4 * lane + 256 * c;
     float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
     for (int j = 0; j < k; ++j) {
-      const int p = min(max(route_pos[t * k + j], 0), T * k - 1);
+      const int p = route_pos ? min(max(route_pos[t * k + j], 0), T * k - 1) : t * k + j;
       const float4 yv = *reinterpret_cast<const float4*>(y + static_cast<long long>(p) * D + d);
       s.x += yv.x; s.y += yv.y; s.z += yv.z; s.w += yv.w;
     }
@@ -216,7 +216,7 @@ extern "C" int32_t llmy_moe_combine_norm(const float* y, const int32_t* route_po
                                          int32_t D, int32_t k, float eps, void* stream) {
   LLMY_REQUIRE(T >= 0 && k > 0 && (D == 256 || D == 512 || D == 1024 || D == 2048));
   if (T == 0) return 0;
-  LLMY_REQUIRE(y && route_pos && x && (w == nullptr || h != nullptr));
+  LLMY_REQUIRE(y && x && (w == nullptr || h != nullptr));
   LLMY_REQUIRE(aligned(y, 16) && aligned(x, 16) && (w == nullptr || (aligned(w, 16) && aligned(h, 8))));
   const hipStream_t s = as_stream(stream);
 #define LLMY_COMBINE(N)                                                                        \

@@ -40,7 +40,14 @@ enum RowMode : int {
   kDense = 0,         // x row m, out row m
   kMoeGather = 1,     // x row sorted_routes[p] / route_k, out row p (p = offsets[e] + m)
   kMoeDirect = 2,     // x row p, out row p
+  // Route-indexed (decode): the workgroup of expert e derives its route list
+  // {r : ids[r] == e} (ascending) from the router's ids with wavefront ballots;
+  // rows are route ids, so no permutation is materialised.
+  kRouteGather = 3,   // x row r / route_k, out row r
+  kRouteDirect = 4,   // x row r, out row r, gate aux[r]
 };
+
+constexpr int kMaxRouteList = 2048;
 
 struct WsArgs {
   const uint16_t* x;
@@ -51,6 +58,7 @@ struct WsArgs {
   const float* aux;
   const int32_t* offsets;
   const int32_t* sorted_routes;
+  const int32_t* ids;  // route-indexed modes: expert id per route [rows_total]
   int M, N, K, ldx, ldo, route_k;
   int rows_total;  // MoE: number of routes (bounds for offsets / sorted_routes)
   int x_rows;      // MoE: rows of x (bounds for the gathered token index)
@@ -78,11 +86,30 @@ __global__ __launch_bounds__(512) void wsgemm_kernel(WsArgs a) {
   const int n0 = blockIdx.x * 16;
   int row_begin = 0;
   int M = a.M;
-  if (MODE != kDense) {
+  constexpr bool kRouted = (MODE == kRouteGather || MODE == kRouteDirect);
+  __shared__ int32_t rlist[kRouted ? kMaxRouteList : 1];
+  __shared__ int32_t rcount;
+  if (MODE == kMoeGather || MODE == kMoeDirect) {
     // Clamp the (device-resident) offsets so a corrupt permutation cannot
     // move any access out of bounds.
     row_begin = min(max(a.offsets[blockIdx.y], 0), a.rows_total);
     M = min(max(a.offsets[blockIdx.y + 1], row_begin), a.rows_total) - row_begin;
+  }
+  if (kRouted) {
+    if (wave == 0) {
+      const int e = blockIdx.y;
+      int cnt = 0;
+      for (int c0 = 0; c0 < a.rows_total; c0 += 64) {
+        const int rr = c0 + lane;
+        const int id = rr < a.rows_total ? a.ids[rr] : -1;
+        const uint64_t m = __ballot(id == e);
+        if (id == e) rlist[cnt + __popcll(m & ((1ull << lane) - 1ull))] = rr;
+        cnt += __popcll(m);
+      }
+      if (lane == 0) rcount = cnt;
+    }
+    __syncthreads();
+    M = rcount;
   }
   if (M <= 0) return;  // uniform over the workgroup: an idle expert reads no weights
 
@@ -106,6 +133,8 @@ __global__ __launch_bounds__(512) void wsgemm_kernel(WsArgs a) {
       valid[mb] = m < M;
       int src = valid[mb] ? row_begin + m : row_begin;
       if (MODE == kMoeGather) src = min(max(a.sorted_routes[src] / a.route_k, 0), a.x_rows - 1);
+      if (MODE == kRouteGather) src = rlist[valid[mb] ? m : 0] / a.route_k;
+      if (MODE == kRouteDirect) src = rlist[valid[mb] ? m : 0];
       xrow[mb] = a.x + static_cast<long long>(src) * a.ldx + 8 * g;
     }
     f32x4 acc[MB], accu[MB];
@@ -120,8 +149,8 @@ __global__ __launch_bounds__(512) void wsgemm_kernel(WsArgs a) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const long long off = PACKED ? (static_cast<long long>(kb >> 8) * 8 + j) * 512 : kb + 32 * j;
-        bw[j] = *reinterpret_cast<const uint4*>(wlane + off);
-        if (kPair) bu[j] = *reinterpret_cast<const uint4*>(wlane + a.pair_offset + off);
+        bw[j] = ld_stream(wlane + off);
+        if (kPair) bu[j] = ld_stream(wlane + a.pair_offset + off);
       }
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb) {
@@ -185,7 +214,7 @@ __global__ __launch_bounds__(512) void wsgemm_kernel(WsArgs a) {
         for (int i = 0; i < 4; ++i) {
           const int m = m0 + 16 * mb + 4 * g + i;
           if (m < M) {
-            const long long row = row_begin + m;
+            const long long row = kRouted ? rlist[m] : row_begin + m;
             const long long o = row * a.ldo + n;
             const float v = acc[mb][i];
             if (EPI == kStoreBf16) {
@@ -199,7 +228,8 @@ __global__ __launch_bounds__(512) void wsgemm_kernel(WsArgs a) {
             } else if (EPI == kSwiGLU) {
               static_cast<uint16_t*>(a.out)[o] = f2bf(siluf_(v) * accu[mb][i]);
             } else if (EPI == kMoeDown) {
-              const int route = min(max(a.sorted_routes[row], 0), a.rows_total - 1);
+              const int route = kRouted ? static_cast<int>(row)
+                                        : min(max(a.sorted_routes[row], 0), a.rows_total - 1);
               static_cast<float*>(a.out)[o] = v * a.aux[route];
             }
           }
@@ -220,6 +250,92 @@ static int32_t launch_ws(const WsArgs& a, int grid_y, bool packed, hipStream_t s
     hipLaunchKernelGGL((wsgemm_kernel<EPI, MODE, true, MB>), grid, block, lds, s, a);
   else
     hipLaunchKernelGGL((wsgemm_kernel<EPI, MODE, false, MB>), grid, block, lds, s, a);
+  return launch_status();
+}
+
+// Dense GEMM for large N (the tied LM head): one workgroup owns 64 weight rows
+// (4 waves x 16) for up to 64 tokens over the whole K.  Per 256-wide K block
+// the token tile [64 x 256] is staged once into LDS with coalesced 16-byte
+// loads (rows padded by 16 bytes so the MFMA fragment reads are conflict
+// free) and shared by the 4 waves; each wave streams its own packed weight
+// tiles from HBM.  Activation traffic is 1/4 of the 16-row split-K kernel's.
+constexpr int kLdsRow = 256 + 8;  // bf16 elements per staged token row (16-byte pad)
+
+template <int EPI>
+__global__ __launch_bounds__(256) void dense_lds_kernel(WsArgs a) {
+  __shared__ __align__(16) uint16_t As[64 * kLdsRow];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int r = lane & 15;
+  const int g = lane >> 4;
+  const int K = a.K;
+  const int M = a.M;
+  const int nblk = blockIdx.x * 4 + wave;  // this wave's 16-row block
+  const bool wave_active = nblk * 16 < a.N;
+  const uint16_t* wlane = a.w + (static_cast<long long>(nblk) * (K >> 8) * 8 * 64 + lane) * 8;
+  f32x4 acc[4];
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb) acc[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  for (int kb = 0; kb < K; kb += 256) {
+    uint4 bw[8];
+    if (wave_active) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) bw[j] = ld_stream(wlane + (static_cast<long long>(kb >> 8) * 8 + j) * 512);
+    }
+    // stage the [64 x 256] token tile: flat 16-byte index f = i*256 + tid
+    uint4 av[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int f = i * 256 + threadIdx.x;
+      const int row = f >> 5, c16 = f & 31;
+      av[i] = row < M ? *reinterpret_cast<const uint4*>(a.x + static_cast<long long>(row) * a.ldx +
+                                                         kb + 8 * c16)
+                      : uint4{0u, 0u, 0u, 0u};
+    }
+    __syncthreads();  // previous block's fragment reads are done
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int f = i * 256 + threadIdx.x;
+      const int row = f >> 5, c16 = f & 31;
+      *reinterpret_cast<uint4*>(As + row * kLdsRow + 8 * c16) = av[i];
+    }
+    __syncthreads();
+    if (wave_active) {
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const uint4 af =
+              *reinterpret_cast<const uint4*>(As + (16 * mb + r) * kLdsRow + 32 * j + 8 * g);
+          acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(af), as_bf16x8(bw[j]),
+                                                            acc[mb], 0, 0, 0);
+        }
+      }
+    }
+  }
+  if (!wave_active) return;
+  const int n = nblk * 16 + r;
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int m = 16 * mb + 4 * g + i;
+      if (m < M) {
+        const long long o = static_cast<long long>(m) * a.ldo + n;
+        const float v = acc[mb][i];
+        if (EPI == kStoreBf16) static_cast<uint16_t*>(a.out)[o] = f2bf(v);
+        else if (EPI == kStoreF32) static_cast<float*>(a.out)[o] = v;
+        else if (EPI == kResidAdd) static_cast<float*>(a.out)[o] += v;
+        else static_cast<float*>(a.out)[o] += v * a.aux[o];
+      }
+    }
+  }
+}
+
+template <int EPI>
+static int32_t launch_dense_lds(const WsArgs& a, hipStream_t s) {
+  hipLaunchKernelGGL((dense_lds_kernel<EPI>), dim3((a.N + 63) / 64), dim3(256), 0, s, a);
   return launch_status();
 }
 
@@ -299,6 +415,16 @@ extern "C" int32_t llmy_linear_bf16(const llmy_bf16* x, const llmy_bf16* w, void
   a.M = M; a.N = N; a.K = K; a.ldx = K; a.ldo = N; a.route_k = 1;
   const hipStream_t s = as_stream(stream);
   const bool packed = weight_layout == 1;
+  // Large N with packed weights: the LDS-tiled kernel (enough workgroups
+  // without splitting K, and 4x less activation traffic).
+  if (packed && M <= 64 && N >= 8192) {
+    switch (epilogue) {
+      case kStoreBf16: return launch_dense_lds<kStoreBf16>(a, s);
+      case kStoreF32: return launch_dense_lds<kStoreF32>(a, s);
+      case kResidAdd: return launch_dense_lds<kResidAdd>(a, s);
+      default: return launch_dense_lds<kResidGated>(a, s);
+    }
+  }
   switch (epilogue) {
     case kStoreBf16: return launch_ws<kStoreBf16, kDense, 4>(a, 1, packed, s);
     case kStoreF32: return launch_ws<kStoreF32, kDense, 4>(a, 1, packed, s);
@@ -355,4 +481,39 @@ extern "C" int32_t llmy_moe_combine(const float* y, const int32_t* route_pos, vo
   hipLaunchKernelGGL(moe_combine_kernel, dim3(blocks), dim3(256), 0, as_stream(stream), y,
                      route_pos, out, T, D, k, mode);
   return launch_status();
+}
+
+extern "C" int32_t llmy_moe_experts_routed_bf16(const llmy_bf16* x, const int32_t* ids,
+                                                const float* gates, const llmy_bf16* w_gate_up,
+                                                const llmy_bf16* w_down, llmy_bf16* act, float* y,
+                                                int32_t T, int32_t D, int32_t H, int32_t E,
+                                                int32_t k, int32_t weight_layout, void* stream) {
+  LLMY_REQUIRE(T >= 0 && D > 0 && D % 256 == 0 && H > 0 && H % 256 == 0);
+  LLMY_REQUIRE(E > 0 && k > 0 && k <= E && (weight_layout == 0 || weight_layout == 1));
+  LLMY_REQUIRE(static_cast<long long>(T) * k <= kMaxRouteList);
+  if (T == 0) return 0;
+  LLMY_REQUIRE(x && ids && gates && w_gate_up && w_down && act && y);
+  LLMY_REQUIRE(aligned(x, 16) && aligned(w_gate_up, 16) && aligned(w_down, 16) &&
+               aligned(act, 16) && aligned(y, 16));
+  const hipStream_t s = as_stream(stream);
+  const bool packed = weight_layout == 1;
+  WsArgs a{};
+  a.x = x; a.w = w_gate_up; a.out = act; a.ids = ids;
+  a.w_expert_stride = 2ll * H * D; a.pair_offset = static_cast<long long>(H) * D;
+  a.N = H; a.K = D; a.ldx = D; a.ldo = H; a.route_k = k;
+  a.rows_total = T * k; a.x_rows = T;
+  WsArgs b{};
+  b.x = act; b.w = w_down; b.out = y; b.aux = gates; b.ids = ids;
+  b.w_expert_stride = static_cast<long long>(D) * H;
+  b.N = D; b.K = H; b.ldx = H; b.ldo = D; b.route_k = k;
+  b.rows_total = T * k; b.x_rows = T * k;
+  int32_t st;
+  if (T * k <= 16 * E) {
+    st = launch_ws<kSwiGLU, kRouteGather, 1>(a, E, packed, s);
+    if (st != 0) return st;
+    return launch_ws<kMoeDown, kRouteDirect, 1>(b, E, packed, s);
+  }
+  st = launch_ws<kSwiGLU, kRouteGather, 4>(a, E, packed, s);
+  if (st != 0) return st;
+  return launch_ws<kMoeDown, kRouteDirect, 4>(b, E, packed, s);
 }

@@ -164,14 +164,15 @@ template <typename Get>
 __device__ void permute_block(Get get, int n, int E, int32_t* __restrict__ counts,
                               int32_t* __restrict__ offsets, int32_t* __restrict__ sorted_routes,
                               int32_t* __restrict__ route_pos, int32_t* cnt) {
-  int32_t* offs = cnt + kPermuteWaves * E;
+  const int nw = blockDim.x >> 6;  // waves in the workgroup (<= kPermuteWaves)
+  int32_t* offs = cnt + nw * E;
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
-  for (int i = threadIdx.x; i < kPermuteWaves * E; i += blockDim.x) cnt[i] = 0;
+  for (int i = threadIdx.x; i < nw * E; i += blockDim.x) cnt[i] = 0;
   __syncthreads();
 
   const int nchunks = (n + 63) / 64;
-  const int per_wave = (nchunks + kPermuteWaves - 1) / kPermuteWaves;
+  const int per_wave = (nchunks + nw - 1) / nw;
   const int c0 = wave * per_wave;
   const int c1 = min(nchunks, c0 + per_wave);
   for (int c = c0; c < c1; ++c) {
@@ -186,7 +187,7 @@ __device__ void permute_block(Get get, int n, int E, int32_t* __restrict__ count
   // Per-expert totals and per-wave exclusive bases (serial over 16 waves).
   for (int e = threadIdx.x; e < E; e += blockDim.x) {
     int run = 0;
-    for (int w = 0; w < kPermuteWaves; ++w) {
+    for (int w = 0; w < nw; ++w) {
       const int c = cnt[w * E + e];
       cnt[w * E + e] = run;
       run += c;
@@ -207,7 +208,7 @@ __device__ void permute_block(Get get, int n, int E, int32_t* __restrict__ count
     offsets[E] = run;
   }
   __syncthreads();
-  for (int i = threadIdx.x; i < kPermuteWaves * E; i += blockDim.x) cnt[i] += offs[i % E];
+  for (int i = threadIdx.x; i < nw * E; i += blockDim.x) cnt[i] += offs[i % E];
   __syncthreads();
 
   int32_t* running = cnt + wave * E;
@@ -237,6 +238,9 @@ __device__ void permute_block(Get get, int n, int E, int32_t* __restrict__ count
   }
 }
 
+// Few routes: one wavefront does the whole sort (no cross-wave barriers).
+static inline int permute_threads(int n) { return n <= 2048 ? 64 : 1024; }
+
 __global__ __launch_bounds__(1024) void moe_permute_kernel(
     const int32_t* __restrict__ expert_ids, int n, int E, int32_t* __restrict__ counts,
     int32_t* __restrict__ offsets, int32_t* __restrict__ sorted_routes,
@@ -260,7 +264,8 @@ __global__ __launch_bounds__(256) void moe_route_norm_kernel(
     uint16_t* __restrict__ h2, int32_t* __restrict__ idx_out, float* __restrict__ gates_out,
     int T, int E, int k, float eps) {
   constexpr int D = NCH * 256;
-  extern __shared__ float wr[];  // [E][D]
+  extern __shared__ float wr[];  // [E][D + 4] padded rows, then [4][D] normalised token rows
+  float* hs = wr + E * (D + 4);
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int t = blockIdx.x * 4 + wave;
@@ -272,20 +277,21 @@ __global__ __launch_bounds__(256) void moe_route_norm_kernel(
                                                        4 * lane + 256 * c)
                   : make_float4(0.f, 0.f, 0.f, 0.f);
   {
-    // E*D <= 24576 floats = at most 24 float4 per thread, in 3 batches of 8.
+    // E*D <= 24576 floats = at most 24 float4 per thread: all loads in flight at once.
     const int n4 = (E * D) >> 2;
+    const int row4 = D >> 2;
+    float4 st[24];
 #pragma unroll
-    for (int b8 = 0; b8 < 3; ++b8) {
-      float4 st[8];
+    for (int q = 0; q < 24; ++q) {
+      const int i = min(static_cast<int>(threadIdx.x) + q * 256, n4 - 1);
+      st[q] = reinterpret_cast<const float4*>(w_router)[i];
+    }
 #pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        const int i = min(static_cast<int>(threadIdx.x) + (b8 * 8 + q) * 256, n4 - 1);
-        st[q] = reinterpret_cast<const float4*>(w_router)[i];
-      }
-#pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        const int i = threadIdx.x + (b8 * 8 + q) * 256;
-        if (i < n4) reinterpret_cast<float4*>(wr)[i] = st[q];
+    for (int q = 0; q < 24; ++q) {
+      const int i = threadIdx.x + q * 256;
+      if (i < n4) {
+        const int e = i / row4;
+        reinterpret_cast<float4*>(wr + e * (D + 4))[i - e * row4] = st[q];
       }
     }
   }
@@ -321,20 +327,56 @@ __global__ __launch_bounds__(256) void moe_route_norm_kernel(
     v[c].z = (v[c].z * r2) * rw.z;
     v[c].w = (v[c].w * r2) * rw.w;
   }
-  float mine[4] = {0.f, 0.f, 0.f, 0.f};
-  for (int e = 0; e < E; ++e) {
-    const float* we = wr + e * D + 4 * lane;
-    float acc = 0.f;
+  // Logits: stage the normalised row in this wave's LDS slot, then lane
+  // (e, part) accumulates the dot product of expert e over D-part `part`
+  // (P = 64 / E parts, up to 4) straight from LDS — the W_r rows are padded by
+  // 4 floats so the lanes' 16-byte reads fall in distinct banks — and the
+  // parts meet in P - 1 shuffles.
+  float* hrow_l = hs + wave * D;
 #pragma unroll
-    for (int c = 0; c < NCH; ++c) {
-      const float4 w4 = *reinterpret_cast<const float4*>(we + 256 * c);
-      acc = fmaf(v[c].x, w4.x, acc);
-      acc = fmaf(v[c].y, w4.y, acc);
-      acc = fmaf(v[c].z, w4.z, acc);
-      acc = fmaf(v[c].w, w4.w, acc);
+  for (int c = 0; c < NCH; ++c) *reinterpret_cast<float4*>(hrow_l + 4 * lane + 256 * c) = v[c];
+  __builtin_amdgcn_wave_barrier();
+  const int P = E <= 16 ? 4 : (E <= 32 ? 2 : 1);
+  const int e_l = lane / P;
+  const int part = lane - e_l * P;
+  const int span = D / P;
+  float acc = 0.f;
+  if (e_l < E) {
+    const float* we = wr + e_l * (D + 4) + part * span;
+    const float* hh = hrow_l + part * span;
+    for (int d = 0; d < span; d += 4) {
+      const float4 w4 = *reinterpret_cast<const float4*>(we + d);
+      const float4 h4 = *reinterpret_cast<const float4*>(hh + d);
+      acc = fmaf(h4.x, w4.x, acc);
+      acc = fmaf(h4.y, w4.y, acc);
+      acc = fmaf(h4.z, w4.z, acc);
+      acc = fmaf(h4.w, w4.w, acc);
     }
-    acc = wave_sum(acc);
-    if ((e & 63) == lane) mine[e >> 6] = acc;
+  }
+  for (int off = 1; off < P; off <<= 1) acc += __shfl_xor(acc, off, kWave);
+  // logit e now sits in lane e*P; gather into the mine[] layout (lane e % 64, slot e / 64)
+  float mine[4] = {0.f, 0.f, 0.f, 0.f};
+  if (E <= 64) {
+    mine[0] = __shfl(acc, min(lane, E - 1) * P, kWave);
+  } else {
+    // E > 64: P == 1, lane e < 64 holds logit e; recompute slots 1..3 sequentially
+    mine[0] = acc;
+    for (int s2 = 1; s2 < 4; ++s2) {
+      const int e = lane + 64 * s2;
+      float a2 = 0.f;
+      if (e < E) {
+        const float* we = wr + e * (D + 4);
+        for (int d = 0; d < D; d += 4) {
+          const float4 w4 = *reinterpret_cast<const float4*>(we + d);
+          const float4 h4 = *reinterpret_cast<const float4*>(hrow_l + d);
+          a2 = fmaf(h4.x, w4.x, a2);
+          a2 = fmaf(h4.y, w4.y, a2);
+          a2 = fmaf(h4.z, w4.z, a2);
+          a2 = fmaf(h4.w, w4.w, a2);
+        }
+      }
+      mine[s2] = a2;
+    }
   }
   topk_softmax_store(mine, E, k, lane, idx_out + t * k, gates_out + t * k);
 
@@ -376,8 +418,9 @@ extern "C" int32_t llmy_moe_permute(const int32_t* expert_ids, int32_t n_routes,
   LLMY_REQUIRE(counts && offsets && n_routes >= 0 && E > 0 && E <= 1024);
   LLMY_REQUIRE(n_routes == 0 || (expert_ids && sorted_routes && route_pos));
   const size_t lds = (static_cast<size_t>(kPermuteWaves) * E + E + 1) * sizeof(int32_t);
-  hipLaunchKernelGGL(moe_permute_kernel, dim3(1), dim3(1024), lds, as_stream(stream), expert_ids,
-                     n_routes, E, counts, offsets, sorted_routes, route_pos);
+  hipLaunchKernelGGL(moe_permute_kernel, dim3(1), dim3(permute_threads(n_routes)), lds,
+                     as_stream(stream), expert_ids, n_routes, E, counts, offsets, sorted_routes,
+                     route_pos);
   return launch_status();
 }
 
@@ -390,15 +433,16 @@ extern "C" int32_t llmy_moe_route_decode(const float* x, const float* ffn_w, con
   LLMY_REQUIRE(T >= 0 && (D == 256 || D == 512 || D == 1024));
   LLMY_REQUIRE(E > 0 && E <= 256 && k > 0 && k <= 8 && k <= E);
   LLMY_REQUIRE(static_cast<long long>(E) * D <= 24576);
-  LLMY_REQUIRE(counts && offsets);
+  const bool permute = counts != nullptr;
+  LLMY_REQUIRE(!permute || offsets);
   const hipStream_t s = as_stream(stream);
   const size_t perm_lds = (static_cast<size_t>(kPermuteWaves) * E + E + 1) * sizeof(int32_t);
   if (T > 0) {
-    LLMY_REQUIRE(x && ffn_w && router_w && w_router && h2 && idx && gates && sorted_routes &&
-                 route_pos);
+    LLMY_REQUIRE(x && ffn_w && router_w && w_router && h2 && idx && gates);
+    LLMY_REQUIRE(!permute || (sorted_routes && route_pos));
     LLMY_REQUIRE(aligned(x, 16) && aligned(ffn_w, 16) && aligned(router_w, 16) &&
                  aligned(w_router, 16) && aligned(h2, 8));
-    const size_t lds = static_cast<size_t>(E) * D * sizeof(float);
+    const size_t lds = (static_cast<size_t>(E) * (D + 4) + 4 * static_cast<size_t>(D)) * sizeof(float);
 #define LLMY_ROUTE(NCH)                                                                       \
   hipLaunchKernelGGL(moe_route_norm_kernel<NCH>, dim3((T + 3) / 4), dim3(256), lds, s, x,      \
                      ffn_w, router_w, w_router, h2, idx, gates, T, E, k, eps)
@@ -411,7 +455,8 @@ extern "C" int32_t llmy_moe_route_decode(const float* x, const float* ffn_w, con
     const int32_t st = launch_status();
     if (st != 0) return st;
   }
-  hipLaunchKernelGGL(moe_permute_kernel, dim3(1), dim3(1024), perm_lds, s, idx, T * k, E, counts,
-                     offsets, sorted_routes, route_pos);
+  if (!permute) return 0;
+  hipLaunchKernelGGL(moe_permute_kernel, dim3(1), dim3(permute_threads(T * k)), perm_lds, s, idx,
+                     T * k, E, counts, offsets, sorted_routes, route_pos);
   return launch_status();
 }

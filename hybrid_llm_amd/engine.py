@@ -119,9 +119,11 @@ class HybridDecoder:
             "next": torch.zeros(B, dtype=torch.int32, device=dev),
         }
         self.graph: torch.cuda.CUDAGraph | None = None
-        # Fused MoE front end (norm + router with W_r in LDS, then the
-        # permutation) when W_r fits in LDS; else three separate kernels.
-        self.fused_route = E * D <= 24576 and D in (256, 512, 1024) and k <= 8
+        # Decode MoE: fused norm + router (W_r in LDS) and route-indexed experts
+        # that derive their routes from the ids (no permutation pass) when the
+        # sizes allow; else norm, router, permutation and sorted experts.
+        self.fused_route = (E * D <= 24576 and D in (256, 512, 1024) and k <= 8
+                            and B * k <= 2048)
         # Optional record of every MoE application's expert ids (verification
         # aid: lets a checker replay the kernel's discrete routing decisions).
         self.route_log: torch.Tensor | None = None
@@ -164,8 +166,9 @@ class HybridDecoder:
         cfg, w, b = self.cfg, self.w, self.buf
         p = f"L{l}."
         if self.fused_route:
+            # decode: router only; the experts derive their routes from the ids
             ops.moe_route_decode(b["x"], w[p + "ffn_norm"], w[p + "router_norm"],
-                                 w[p + "w_router"], cfg.top_k, cfg.eps, bufs=b)
+                                 w[p + "w_router"], cfg.top_k, cfg.eps, bufs=b, permute=False)
         else:
             ops.rmsnorm(b["x"], w[p + "ffn_norm"], cfg.eps, out=b["h"])
             from . import _lib
@@ -180,10 +183,16 @@ class HybridDecoder:
         if self.route_log is not None:
             self.route_log[self._app].copy_(b["idx"])
             self._app = (self._app + 1) % self.route_log.shape[0]
-        ops.moe_experts(b["h"], b, b["gates"], w[p + "w_gate_up"], w[p + "w_down"],
-                        act=b["act"], y=b["y"], layout=ops.LAYOUT_PACKED)
-        ops.moe_combine_norm(b["y"], b["route_pos"], b["x"], b["h"], next_norm, cfg.top_k,
-                             cfg.eps)
+        if self.fused_route:
+            ops.moe_experts_routed(b["h"], b["idx"], b["gates"], w[p + "w_gate_up"],
+                                   w[p + "w_down"], act=b["act"], y=b["y"],
+                                   layout=ops.LAYOUT_PACKED)
+            route_pos = None
+        else:
+            ops.moe_experts(b["h"], b, b["gates"], w[p + "w_gate_up"], w[p + "w_down"],
+                            act=b["act"], y=b["y"], layout=ops.LAYOUT_PACKED)
+            route_pos = b["route_pos"]
+        ops.moe_combine_norm(b["y"], route_pos, b["x"], b["h"], next_norm, cfg.top_k, cfg.eps)
 
     # ------------------------------------------------------------------ step
     def _step_body(self) -> None:

@@ -153,6 +153,29 @@ def moe_experts(x: torch.Tensor, perm: dict, gates: torch.Tensor, w_gate_up: tor
     return act, y
 
 
+def moe_experts_routed(x: torch.Tensor, ids: torch.Tensor, gates: torch.Tensor,
+                       w_gate_up: torch.Tensor, w_down: torch.Tensor,
+                       act: torch.Tensor | None = None, y: torch.Tensor | None = None,
+                       layout: int = LAYOUT_ROWMAJOR):
+    """Route-indexed experts (no permutation): act/y rows are route ids t*k+j."""
+    T, D = x.shape
+    E, H2, _ = w_gate_up.shape
+    H = H2 // 2
+    k = gates.shape[-1]
+    _check(x, torch.bfloat16, "x")
+    _check(ids, torch.int32, "ids", (T, k))
+    _check(gates, torch.float32, "gates", (T, k))
+    _check(w_gate_up, torch.bfloat16, "w_gate_up", (E, 2 * H, D))
+    _check(w_down, torch.bfloat16, "w_down", (E, D, H))
+    if act is None:
+        act = torch.empty(T * k, H, dtype=torch.bfloat16, device=x.device)
+    if y is None:
+        y = torch.empty(T * k, D, dtype=torch.float32, device=x.device)
+    _lib.call("llmy_moe_experts_routed_bf16", _ptr(x), _ptr(ids), _ptr(gates), _ptr(w_gate_up),
+              _ptr(w_down), _ptr(act), _ptr(y), T, D, H, E, k, layout, _stream())
+    return act, y
+
+
 MOE_OUT_BF16, MOE_OUT_F32, MOE_OUT_RESID = 0, 1, 2
 
 
@@ -252,8 +275,9 @@ def gdn_step_fused(proj, beta_bias, decay_logit, state, out=None, conv=None) -> 
     return out
 
 
-def moe_route_decode(x, ffn_w, router_w, w_router, k, eps=1e-6, bufs=None) -> dict:
-    """Fused pre-MoE norm + router + permutation for small T (one launch)."""
+def moe_route_decode(x, ffn_w, router_w, w_router, k, eps=1e-6, bufs=None,
+                     permute: bool = True) -> dict:
+    """Fused pre-MoE norm + router (+ the permutation unless permute=False)."""
     T, D = x.shape
     E = w_router.shape[0]
     _check(x, torch.float32, "x")
@@ -268,10 +292,10 @@ def moe_route_decode(x, ffn_w, router_w, w_router, k, eps=1e-6, bufs=None) -> di
                 "sorted_routes": torch.empty(T * k, dtype=torch.int32, device=dev),
                 "route_pos": torch.empty(T * k, dtype=torch.int32, device=dev)}
     b = bufs
+    P = (lambda n: _ptr(b[n])) if permute else (lambda n: None)
     _lib.call("llmy_moe_route_decode", _ptr(x), _ptr(ffn_w), _ptr(router_w), _ptr(w_router),
-              _ptr(b["h"]), _ptr(b["idx"]), _ptr(b["gates"]), _ptr(b["counts"]),
-              _ptr(b["offsets"]), _ptr(b["sorted_routes"]), _ptr(b["route_pos"]), T, D, E, k,
-              eps, _stream())
+              _ptr(b["h"]), _ptr(b["idx"]), _ptr(b["gates"]), P("counts"), P("offsets"),
+              P("sorted_routes"), P("route_pos"), T, D, E, k, eps, _stream())
     return b
 
 
@@ -287,6 +311,8 @@ def embed_norm(tokens, table, w, x, h, eps=1e-6) -> None:
 
 
 def moe_combine_norm(y, route_pos, x, h=None, w=None, k=2, eps=1e-6) -> None:
+    """x += sum_j y[route_pos[t*k+j]] (route_pos None: route-indexed y), then
+    h = bf16(RMSNorm(x) * w) when w is given."""
     T, D = x.shape
     _check(y, torch.float32, "y", (T * k, D))
     _check(x, torch.float32, "x")

@@ -106,6 +106,18 @@ int32_t llmy_moe_experts_bf16(const llmy_bf16* x, const int32_t* offsets,
                               int32_t H, int32_t E, int32_t k, int32_t weight_layout,
                               void* stream);
 
+/* Route-indexed variant for small T*k (<= 2048, the decode path): no
+ * permutation is materialised.  The workgroups of expert e derive the routes
+ * {r : ids[r] == e} themselves (wavefront ballots over ids [T*k], ascending r)
+ * and read x[r / k]; act [T*k,H] and y [T*k,D] are indexed by route id:
+ *   act[r] = bf16(silu(Wg[e] x[r/k]) * (Wu[e] x[r/k])),  y[r] = gates[r] * (Wd[e] act[r]).
+ * Same arithmetic as llmy_moe_experts_bf16. */
+int32_t llmy_moe_experts_routed_bf16(const llmy_bf16* x, const int32_t* ids,
+                                     const float* gates, const llmy_bf16* w_gate_up,
+                                     const llmy_bf16* w_down, llmy_bf16* act, float* y,
+                                     int32_t T, int32_t D, int32_t H, int32_t E,
+                                     int32_t k, int32_t weight_layout, void* stream);
+
 /* out[t] = sum_j y[route_pos[t*k + j]] (j ascending) — the un-permute /
  * combine of moe.py:78-81 without atomics.  mode 0: store bf16 out [T,D];
  * 1: store fp32; 2: fp32 out += sum (residual add).  D % 4 == 0. */
@@ -183,7 +195,8 @@ int32_t llmy_embed_norm_bf16(const int32_t* tokens, const llmy_bf16* table,
                              int32_t D, int32_t V, float eps, void* stream);
 
 /* MoE combine fused with the next pre-norm: x[t] += sum_j y[route_pos[t*k+j]]
- * (j ascending), then h[t] = bf16(RMSNorm(x[t]) * w) unless w == NULL.
+ * (j ascending; route_pos == NULL means y is route-indexed, y[t*k+j]), then
+ * h[t] = bf16(RMSNorm(x[t]) * w) unless w == NULL.
  * D in {256,512,1024,2048}. */
 int32_t llmy_moe_combine_norm(const float* y, const int32_t* route_pos,
                               const float* w, float* x, llmy_bf16* h, int32_t T,
@@ -193,8 +206,8 @@ int32_t llmy_moe_combine_norm(const float* y, const int32_t* route_pos,
  *   h2[t] = bf16(RMSNorm(x[t]) * ffn_w)   (the block's pre-MoE norm),
  *   logits = (RMSNorm(h2[t]) * router_w) . w_router^T in fp32, top-k (ties ->
  *   lower index) + softmax -> idx [T,k], gates [T,k],
- *   and the stable permutation of llmy_moe_permute — two launches (router with
- *   W_r staged in LDS, one wave per token; then the permutation).
+ *   and (unless counts == NULL) the stable permutation of llmy_moe_permute —
+ *   router with W_r staged in LDS, one wave per token, then the permutation.
  * Equivalent to llmy_rmsnorm_f32_bf16 + llmy_router_topk_bf16 +
  * llmy_moe_permute (context_router.py:62,71-74; moe.py:42-66). */
 int32_t llmy_moe_route_decode(const float* x, const float* ffn_w,
