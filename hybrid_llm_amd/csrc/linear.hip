@@ -74,7 +74,7 @@ __host__ __device__ __forceinline__ long long packed_index(int n, int k, int K) 
   return ((((static_cast<long long>(nb) * (K >> 8) + kb) * 8 + j) * 64 + lane) << 3) + e;
 }
 
-template <int EPI, int MODE, bool PACKED, int MB>
+template <int EPI, int MODE, bool PACKED, int MB, int KB>
 __global__ __launch_bounds__(512) void wsgemm_kernel(WsArgs a) {
   constexpr bool kPair = (EPI == kSwiGLU);
   constexpr int kSlots = (kPair ? 2 : 1) * MB * 4;
@@ -143,33 +143,46 @@ __global__ __launch_bounds__(512) void wsgemm_kernel(WsArgs a) {
       acc[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
       accu[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
-    for (int kb = wave * 256; kb < K; kb += S * 256) {
-      // Issue every load of this K block before the first MFMA.
-      uint4 bw[8], bu[8], av[MB][8];
+    // Each wave takes KB consecutive 256-wide K blocks per step (KB blocks of
+    // weights in flight at once); K % (256 * KB) == 0.
+    for (int kb0 = wave * 256 * KB; kb0 < K; kb0 += S * 256 * KB) {
+      // Issue every load of these K blocks before the first MFMA.
+      uint4 bw[KB][8], bu[KB][8], av[KB][MB][8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const long long off = PACKED ? (static_cast<long long>(kb >> 8) * 8 + j) * 512 : kb + 32 * j;
-        bw[j] = ld_stream(wlane + off);
-        if (kPair) bu[j] = ld_stream(wlane + a.pair_offset + off);
+      for (int q = 0; q < KB; ++q) {
+        const int kb = kb0 + 256 * q;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const long long off =
+              PACKED ? (static_cast<long long>(kb >> 8) * 8 + j) * 512 : kb + 32 * j;
+          bw[q][j] = ld_stream(wlane + off);
+          if (kPair) bu[q][j] = ld_stream(wlane + a.pair_offset + off);
+        }
       }
 #pragma unroll
-      for (int mb = 0; mb < MB; ++mb) {
+      for (int q = 0; q < KB; ++q) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j)
-          av[mb][j] = (mb < nmb && valid[mb])
-                          ? *reinterpret_cast<const uint4*>(xrow[mb] + kb + 32 * j)
-                          : uint4{0u, 0u, 0u, 0u};
+        for (int mb = 0; mb < MB; ++mb) {
+#pragma unroll
+          for (int j = 0; j < 8; ++j)
+            av[q][mb][j] = (mb < nmb && valid[mb])
+                               ? *reinterpret_cast<const uint4*>(xrow[mb] + kb0 + 256 * q + 32 * j)
+                               : uint4{0u, 0u, 0u, 0u};
+        }
       }
 #pragma unroll
-      for (int mb = 0; mb < MB; ++mb) {
-        if (mb < nmb) {
+      for (int q = 0; q < KB; ++q) {
 #pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(av[mb][j]),
-                                                              as_bf16x8(bw[j]), acc[mb], 0, 0, 0);
-            if (kPair)
-              accu[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                  as_bf16x8(av[mb][j]), as_bf16x8(bu[j]), accu[mb], 0, 0, 0);
+        for (int mb = 0; mb < MB; ++mb) {
+          if (mb < nmb) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+              acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                  as_bf16x8(av[q][mb][j]), as_bf16x8(bw[q][j]), acc[mb], 0, 0, 0);
+              if (kPair)
+                accu[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                    as_bf16x8(av[q][mb][j]), as_bf16x8(bu[q][j]), accu[mb], 0, 0, 0);
+            }
           }
         }
       }
@@ -239,17 +252,18 @@ __global__ __launch_bounds__(512) void wsgemm_kernel(WsArgs a) {
   }
 }
 
-template <int EPI, int MODE, int MB>
+template <int EPI, int MODE, int MB, int KB = 1>
 static int32_t launch_ws(const WsArgs& a, int grid_y, bool packed, hipStream_t s) {
-  const int waves = std::max(1, std::min(8, a.K / 256));
+  if (a.K % (256 * KB) != 0) return launch_ws<EPI, MODE, MB, 1>(a, grid_y, packed, s);
+  const int waves = std::max(1, std::min(8, a.K / (256 * KB)));
   const size_t lds = waves > 1 ? static_cast<size_t>(waves) * (EPI == kSwiGLU ? 2 : 1) * MB * 4 *
                                      64 * sizeof(float)
                                : 0;
   const dim3 grid(a.N / 16, grid_y), block(64 * waves);
   if (packed)
-    hipLaunchKernelGGL((wsgemm_kernel<EPI, MODE, true, MB>), grid, block, lds, s, a);
+    hipLaunchKernelGGL((wsgemm_kernel<EPI, MODE, true, MB, KB>), grid, block, lds, s, a);
   else
-    hipLaunchKernelGGL((wsgemm_kernel<EPI, MODE, false, MB>), grid, block, lds, s, a);
+    hipLaunchKernelGGL((wsgemm_kernel<EPI, MODE, false, MB, KB>), grid, block, lds, s, a);
   return launch_status();
 }
 
@@ -457,12 +471,14 @@ extern "C" int32_t llmy_moe_experts_bf16(const llmy_bf16* x, const int32_t* offs
   b.sorted_routes = sorted_routes; b.w_expert_stride = static_cast<long long>(D) * H;
   b.N = D; b.K = H; b.ldx = H; b.ldo = D; b.route_k = k;
   b.rows_total = T * k; b.x_rows = T * k;
-  // Few routes per expert (decode): 16-row chunks; otherwise 64-row chunks.
+  // Few routes per expert (decode): 16-row chunks, two K blocks per wave for
+  // the down projection; otherwise 64-row chunks.  (The route-indexed entry
+  // point uses the same configurations, so the two agree bit for bit.)
   int32_t st;
   if (T * k <= 16 * E) {
     st = launch_ws<kSwiGLU, kMoeGather, 1>(a, E, packed, s);
     if (st != 0) return st;
-    return launch_ws<kMoeDown, kMoeDirect, 1>(b, E, packed, s);
+    return launch_ws<kMoeDown, kMoeDirect, 1, 2>(b, E, packed, s);
   }
   st = launch_ws<kSwiGLU, kMoeGather, 4>(a, E, packed, s);
   if (st != 0) return st;
@@ -511,7 +527,7 @@ extern "C" int32_t llmy_moe_experts_routed_bf16(const llmy_bf16* x, const int32_
   if (T * k <= 16 * E) {
     st = launch_ws<kSwiGLU, kRouteGather, 1>(a, E, packed, s);
     if (st != 0) return st;
-    return launch_ws<kMoeDown, kRouteDirect, 1>(b, E, packed, s);
+    return launch_ws<kMoeDown, kRouteDirect, 1, 2>(b, E, packed, s);
   }
   st = launch_ws<kSwiGLU, kRouteGather, 4>(a, E, packed, s);
   if (st != 0) return st;

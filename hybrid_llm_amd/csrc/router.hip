@@ -270,12 +270,17 @@ __global__ __launch_bounds__(256) void moe_route_norm_kernel(
   const int lane = threadIdx.x & 63;
   const int t = blockIdx.x * 4 + wave;
   const bool active = t < T;
-  float4 v[NCH];
+  // Every global operand of the wave is requested up front: the token row,
+  // both RMSNorm weight slices and (below) the W_r staging loads.
+  float4 v[NCH], fw[NCH], rw[NCH];
 #pragma unroll
-  for (int c = 0; c < NCH; ++c)
-    v[c] = active ? *reinterpret_cast<const float4*>(x + static_cast<long long>(t) * D +
-                                                       4 * lane + 256 * c)
+  for (int c = 0; c < NCH; ++c) {
+    const int d = 4 * lane + 256 * c;
+    v[c] = active ? *reinterpret_cast<const float4*>(x + static_cast<long long>(t) * D + d)
                   : make_float4(0.f, 0.f, 0.f, 0.f);
+    fw[c] = *reinterpret_cast<const float4*>(ffn_w + d);
+    rw[c] = *reinterpret_cast<const float4*>(router_w + d);
+  }
   {
     // E*D <= 24576 floats = at most 24 float4 per thread: all loads in flight at once.
     const int n4 = (E * D) >> 2;
@@ -308,9 +313,8 @@ __global__ __launch_bounds__(256) void moe_route_norm_kernel(
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
     const int d = 4 * lane + 256 * c;
-    const float4 fw = *reinterpret_cast<const float4*>(ffn_w + d);
-    const uint32_t lo = pack_bf2(v[c].x * r1 * fw.x, v[c].y * r1 * fw.y);
-    const uint32_t hi = pack_bf2(v[c].z * r1 * fw.z, v[c].w * r1 * fw.w);
+    const uint32_t lo = pack_bf2(v[c].x * r1 * fw[c].x, v[c].y * r1 * fw[c].y);
+    const uint32_t hi = pack_bf2(v[c].z * r1 * fw[c].z, v[c].w * r1 * fw[c].w);
     *reinterpret_cast<uint2*>(hrow + d) = make_uint2(lo, hi);
     v[c].x = __uint_as_float(lo << 16);
     v[c].y = __uint_as_float(lo & 0xffff0000u);
@@ -321,11 +325,10 @@ __global__ __launch_bounds__(256) void moe_route_norm_kernel(
   const float r2 = rsqrtf(wave_sum(ss2) / static_cast<float>(D) + eps);
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
-    const float4 rw = *reinterpret_cast<const float4*>(router_w + 4 * lane + 256 * c);
-    v[c].x = (v[c].x * r2) * rw.x;
-    v[c].y = (v[c].y * r2) * rw.y;
-    v[c].z = (v[c].z * r2) * rw.z;
-    v[c].w = (v[c].w * r2) * rw.w;
+    v[c].x = (v[c].x * r2) * rw[c].x;
+    v[c].y = (v[c].y * r2) * rw[c].y;
+    v[c].z = (v[c].z * r2) * rw[c].z;
+    v[c].w = (v[c].w * r2) * rw[c].w;
   }
   // Logits: stage the normalised row in this wave's LDS slot, then lane
   // (e, part) accumulates the dot product of expert e over D-part `part`
@@ -342,16 +345,27 @@ __global__ __launch_bounds__(256) void moe_route_norm_kernel(
   const int span = D / P;
   float acc = 0.f;
   if (e_l < E) {
+    // span is a multiple of 64 (D >= 256, P <= 4): 8 float4 reads per step
+    // with four independent accumulators, so LDS reads and FMAs pipeline.
     const float* we = wr + e_l * (D + 4) + part * span;
     const float* hh = hrow_l + part * span;
-    for (int d = 0; d < span; d += 4) {
-      const float4 w4 = *reinterpret_cast<const float4*>(we + d);
-      const float4 h4 = *reinterpret_cast<const float4*>(hh + d);
-      acc = fmaf(h4.x, w4.x, acc);
-      acc = fmaf(h4.y, w4.y, acc);
-      acc = fmaf(h4.z, w4.z, acc);
-      acc = fmaf(h4.w, w4.w, acc);
+    float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+    for (int d = 0; d < span; d += 32) {
+      float4 w4[8], h4[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        w4[u] = *reinterpret_cast<const float4*>(we + d + 4 * u);
+        h4[u] = *reinterpret_cast<const float4*>(hh + d + 4 * u);
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        a0 = fmaf(h4[u].x, w4[u].x, a0);
+        a1 = fmaf(h4[u].y, w4[u].y, a1);
+        a2 = fmaf(h4[u].z, w4[u].z, a2);
+        a3 = fmaf(h4[u].w, w4[u].w, a3);
+      }
     }
+    acc = (a0 + a1) + (a2 + a3);
   }
   for (int off = 1; off < P; off <<= 1) acc += __shfl_xor(acc, off, kWave);
   // logit e now sits in lane e*P; gather into the mine[] layout (lane e % 64, slot e / 64)
