@@ -30,8 +30,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "llmy_moe_combine": (_I, [_P, _P, _P, _I, _I, _I, _I, _P]),
     "llmy_moe_experts_routed_bf16": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I,
                                           _P]),
+    "llmy_banded_attn_prefill_bf16": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _P]),
     "llmy_banded_attn_decode_bf16": (_I, [_P, _P, _P, _I64, _I64, _P, _P, _P, _P, _I, _I, _I,
                                           _I, _F, _P]),
+    "llmy_gdn_prefill_workspace_bytes": (C.c_int64, [_I, _I, _I, _I, _I]),
+    "llmy_gdn_prefill_bf16": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I, _I, _I, _I, _I, _P]),
     "llmy_gdn_step_bf16": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P]),
     "llmy_gdn_step_fused_f32": (_I, [_P, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I,
                                      _I, _I, _P]),

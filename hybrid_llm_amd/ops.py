@@ -205,6 +205,22 @@ def moe_forward(x: torch.Tensor, w_router: torch.Tensor, w_gate_up: torch.Tensor
 
 
 # --------------------------------------------------------------------------- attention
+def banded_attn_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, window: int,
+                        scale: float | None = None, out: torch.Tensor | None = None
+                        ) -> torch.Tensor:
+    """q, k, v [B,T,H,hd] bf16 -> o [B,T,H,hd] bf16 (banded causal attention)."""
+    B, T, H, hd = q.shape
+    _check(q, torch.bfloat16, "q")
+    _check(k, torch.bfloat16, "k", (B, T, H, hd))
+    _check(v, torch.bfloat16, "v", (B, T, H, hd))
+    if out is None:
+        out = torch.empty_like(q)
+    scale = hd ** -0.5 if scale is None else scale
+    _lib.call("llmy_banded_attn_prefill_bf16", _ptr(q), _ptr(k), _ptr(v), _ptr(out), B, T, H, hd,
+              window, scale, _stream())
+    return out
+
+
 def banded_attn_decode(q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor,
                        k_cache: torch.Tensor, v_cache: torch.Tensor, pos: torch.Tensor,
                        scale: float | None = None, out: torch.Tensor | None = None
@@ -232,6 +248,27 @@ def banded_attn_decode(q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor
 
 
 # --------------------------------------------------------------------------- GDN
+def gdn_prefill(q, k, v, beta, g, state, out=None, workspace=None) -> torch.Tensor:
+    """Chunked delta-rule scan; q,k [B,T,H,dk], v [B,T,H,dv] bf16, beta/g [B,T,H]
+    fp32, state [B,H,dk,dv] fp32 updated in place.  Returns out [B,T,H,dv] bf16."""
+    B, T, H, dk = q.shape
+    dv = v.shape[-1]
+    _check(q, torch.bfloat16, "q")
+    _check(k, torch.bfloat16, "k", (B, T, H, dk))
+    _check(v, torch.bfloat16, "v", (B, T, H, dv))
+    _check(beta, torch.float32, "beta", (B, T, H))
+    _check(g, torch.float32, "g", (B, T, H))
+    _check(state, torch.float32, "state", (B, H, dk, dv))
+    nbytes = int(_lib.load().llmy_gdn_prefill_workspace_bytes(B, T, H, dk, dv))
+    if workspace is None or workspace.numel() * workspace.element_size() < nbytes:
+        workspace = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=q.device)
+    if out is None:
+        out = torch.empty(B, T, H, dv, dtype=torch.bfloat16, device=q.device)
+    _lib.call("llmy_gdn_prefill_bf16", _ptr(q), _ptr(k), _ptr(v), _ptr(beta), _ptr(g),
+              _ptr(state), _ptr(out), _ptr(workspace), nbytes, B, T, H, dk, dv, _stream())
+    return out
+
+
 def gdn_step(q, k, v, beta, g, state, gate=None, out=None) -> torch.Tensor:
     """In-place state update; q,k [B,H,dk], v/gate [B,H,dv] bf16, beta/g [B,H] fp32,
     state [B,H,dk,dv] fp32.  Returns out [B,H,dv] bf16."""

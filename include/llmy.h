@@ -125,6 +125,19 @@ int32_t llmy_moe_combine(const float* y, const int32_t* route_pos, void* out,
                          int32_t T, int32_t D, int32_t k, int32_t mode,
                          void* stream);
 
+/* --- Banded attention, prefill (runpod/kernels/fused_attention.py:6-41) --- */
+
+/* o_i = sum_{j: 0 <= i-j < W} softmax_j(scale * q_i . k_j) v_j per (b, h), fp32
+ * scores/accumulation.  q, k, v, o [B,T,H,head_dim] bf16; head_dim in {64,128}.
+ * Replaces the Triton _banded_attn_fwd_kernel
+ * (runpod/kernels/triton_banded_attention.py:23-90) and banded_attn_kernel
+ * (llmy_cuda/src/kernels/attn.cu:17-126); rows whose window holds no valid
+ * key cannot occur (every query sees itself). */
+int32_t llmy_banded_attn_prefill_bf16(const llmy_bf16* q, const llmy_bf16* k,
+                                      const llmy_bf16* v, llmy_bf16* o, int32_t B,
+                                      int32_t T, int32_t H, int32_t head_dim, int32_t W,
+                                      float scale, void* stream);
+
 /* --- Banded attention, decode (model/layers/hca.py:119-128) --------------- */
 
 /* One query per (b, h) against a ring-buffer cache k_cache/v_cache
@@ -142,6 +155,27 @@ int32_t llmy_banded_attn_decode_bf16(const llmy_bf16* q, const llmy_bf16* k_new,
                                      llmy_bf16* out, int32_t B, int32_t H,
                                      int32_t head_dim, int32_t W, float scale,
                                      void* stream);
+
+/* --- Gated delta rule, prefill (chunked; model/layers/gated_deltanet.py:140-149) */
+
+/* Workspace (bytes) that llmy_gdn_prefill_bf16 needs for (B, T, H, dk, dv):
+ * per 64-token chunk W [64,dk], U0 [64,dv], A [64,64] and 64 cumulative
+ * log-decays, fp32.  No counterpart in the reference. */
+int64_t llmy_gdn_prefill_workspace_bytes(int32_t B, int32_t T, int32_t H, int32_t dk,
+                                         int32_t dv);
+
+/* The recurrence over T tokens, chunked (C = 64) with the exact transition
+ * A_t = g_t I - beta_t k_t k_t^T of the reference:
+ *   S_t = g_t S_{t-1} + beta_t k_t (v_t - S_{t-1}^T k_t)^T,  out_t = S_t^T q_t.
+ * q, k [B,T,H,dk], v [B,T,H,dv] bf16; beta, g [B,T,H] fp32 (g in (0,1]);
+ * state [B,H,dk,dv] fp32 in/out (initial -> final); out [B,T,H,dv] bf16.
+ * (dk,dv) in {(64,64),(128,128)}.  Replaces the sequential scans of
+ * gated_deltanet.py:42-53,236-252 and runpod/kernels/triton_gdn.py:57-118. */
+int32_t llmy_gdn_prefill_bf16(const llmy_bf16* q, const llmy_bf16* k, const llmy_bf16* v,
+                              const float* beta, const float* g, float* state,
+                              llmy_bf16* out, void* workspace, int64_t workspace_bytes,
+                              int32_t B, int32_t T, int32_t H, int32_t dk, int32_t dv,
+                              void* stream);
 
 /* --- Gated delta rule, decode (model/layers/gated_deltanet.py:140-149) ---- */
 
