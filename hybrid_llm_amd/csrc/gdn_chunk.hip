@@ -76,7 +76,7 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(
   __shared__ float Gm[kC * PG];   // K K^T, then L
   __shared__ float Qk[kC * PG];   // Q K^T
   __shared__ float Ti[kC * PG];   // (I + L)^{-1}
-  __shared__ float cum[kC], prv[kC], bet[kC];
+  __shared__ float cum[kC], prv[kC], bet[kC], wsc[kC];  // wsc = beta * Gamma_prev
 
   const int cid = blockIdx.x;
   const int bh = cid / NC;
@@ -121,6 +121,7 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(
     cum[lane] = sc;
     prv[lane] = sc - lg;
     bet[lane] = bt;
+    wsc[lane] = bt * expf(sc - lg);
   }
   __syncthreads();
 
@@ -188,7 +189,7 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(
 #pragma unroll
         for (int jj = 0; jj < 8; ++jj) {
           const int i = 32 * s + 8 * g4 + jj;
-          const float sc = isW ? bet[i] * expf(prv[i]) : bet[i];
+          const float sc = isW ? wsc[i] : bet[i];
           av[jj] = Ti[row * PG + i] * sc;
         }
         uint4 ahi, alo;
@@ -226,7 +227,7 @@ __global__ __launch_bounds__(256) void gdn_chunk_scan_kernel(
   __shared__ __align__(16) uint16_t Qs[kC * PK];
   __shared__ __align__(16) uint16_t Ks[kC * PK];
   __shared__ float As[kC * PG];
-  __shared__ float cum[kC];
+  __shared__ float cum[kC], ecum[kC], dec[kC];  // cum, Gamma_t, Gamma_C / Gamma_t
 
   const int bh = blockIdx.x / NSL;
   const int sl = blockIdx.x - bh * NSL;
@@ -264,7 +265,13 @@ __global__ __launch_bounds__(256) void gdn_chunk_scan_kernel(
     }
     for (int e = threadIdx.x; e < kC * kC; e += 256)
       As[(e >> 6) * PG + (e & 63)] = Ag[cid * kC * kC + e];
-    if (threadIdx.x < kC) cum[threadIdx.x] = cumg[cid * kC + threadIdx.x];
+    if (threadIdx.x < kC) {
+      const float cv = cumg[cid * kC + threadIdx.x];
+      const float cl_ = cumg[cid * kC + kC - 1];
+      cum[threadIdx.x] = cv;
+      ecum[threadIdx.x] = expf(cv);
+      dec[threadIdx.x] = expf(cl_ - cv);
+    }
     __syncthreads();
 
     // ---- U = U0 - W S   [64 x DVS]: 8 tiles of 16x16, 2 per wave
@@ -330,7 +337,7 @@ __global__ __launch_bounds__(256) void gdn_chunk_scan_kernel(
       for (int i = 0; i < 4; ++i) {
         const int t = 16 * tm + 4 * g4 + i;
         if (t < Tc) {
-          const float o = expf(cum[t]) * qs[i] + au[i];
+          const float o = ecum[t] * qs[i] + au[i];
           out[(static_cast<long long>(b) * T + t0 + t) * rv + static_cast<long long>(h) * DV +
               DVS * sl + 16 * tn + r16] = f2bf(o);
         }
@@ -351,7 +358,7 @@ __global__ __launch_bounds__(256) void gdn_chunk_scan_kernel(
 #pragma unroll
         for (int jj = 0; jj < 8; ++jj) {
           const int t = 32 * s + 8 * g4 + jj;
-          bv[jj] = expf(cl - cum[t]) * Us[t * PS + 16 * tn + r16];
+          bv[jj] = dec[t] * Us[t * PS + 16 * tn + r16];
         }
         uint4 bhi, blo;
         split8(bv, bhi, blo);

@@ -87,6 +87,33 @@ def argmax(logits: torch.Tensor) -> torch.Tensor:
     return out
 
 
+def sample_top_p(logits: torch.Tensor, temperature: float, top_p: float, u: torch.Tensor,
+                 top_k: int = 0, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Temperature + top-k + nucleus draw per row with the supplied uniforms u [R]
+    (sample_standalone.py:5611-5636; llmy.cpp:132-202).  temperature <= 0 is greedy."""
+    R, V = logits.shape
+    _check(logits, torch.float32, "logits")
+    _check(u, torch.float32, "u", (R,))
+    if out is None:
+        out = torch.empty(R, dtype=torch.int32, device=logits.device)
+    _lib.call("llmy_sample_top_p_f32", _ptr(logits), R, V, float(temperature), int(top_k),
+              float(top_p), _ptr(u), _ptr(out), _stream())
+    return out
+
+
+def repetition_penalty_(logits: torch.Tensor, recent: torch.Tensor, penalty: float) -> torch.Tensor:
+    """In place: penalise each distinct id of recent[r] (int32 [R, n], -1 = none) in logits[r]
+    (sample_standalone.py:5601-5605)."""
+    R, V = logits.shape
+    _check(logits, torch.float32, "logits")
+    _check(recent, torch.int32, "recent")
+    if recent.dim() != 2 or recent.shape[0] != R:
+        raise ValueError("recent must be [rows, n]")
+    _lib.call("llmy_repetition_penalty_f32", _ptr(logits), R, V, _ptr(recent), recent.shape[1],
+              float(penalty), _stream())
+    return logits
+
+
 # --------------------------------------------------------------------------- projections
 EPI_STORE_BF16, EPI_STORE_F32, EPI_RESID_ADD, EPI_RESID_GATED = 0, 1, 2, 3
 

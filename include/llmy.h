@@ -258,6 +258,32 @@ int32_t llmy_moe_route_decode(const float* x, const float* ffn_w,
 int32_t llmy_sample_argmax_f32(const float* logits, int32_t rows, int32_t V,
                                int32_t* out, void* stream);
 
+/* Temperature + top-k + nucleus sampling with a caller-supplied uniform draw
+ * per row; replaces the CPU sampler llmy_sample (llmy_cuda/include/llmy.h:64-67,
+ * llmy_cuda/src/llmy.cpp:132-202), whose xorshift draw the caller makes and
+ * passes as u[r] in [0, 1).  Per row: order ids by descending logit (equal
+ * logits by ascending id); keep the first top_k (top_k <= 0 or >= V: all);
+ * p = softmax(logit / temperature) over the kept ids; keep the shortest prefix
+ * whose probability reaches top_p (top_p outside (0, 1): all); out[r] = the
+ * first kept id whose cumulative renormalised probability exceeds u[r].
+ * temperature <= 0 (or NaN) gives the greedy id of llmy_sample_argmax_f32.
+ * logits [rows,V] fp32 with V <= 32768, u [rows] fp32, out [rows] int32.
+ * Deterministic: probabilities are summed as exact 2^-47 fixed point. */
+int32_t llmy_sample_top_p_f32(const float* logits, int32_t rows, int32_t V,
+                              float temperature, int32_t top_k, float top_p,
+                              const float* u, int32_t* out, void* stream);
+
+/* In-place repetition penalty (sample_standalone.py:5601-5605; the C twin is
+ * the penalty loop of llmy_sample, llmy_cuda/src/llmy.cpp:145-156): for each
+ * distinct id in recent[r, :n_recent] inside [0, V), logits[r, id] is divided
+ * by penalty if positive, else multiplied by it.  An id listed more than once
+ * is penalised once (the Python sampler's set; the C twin would apply it per
+ * listing).  Ids outside [0, V) (e.g. -1 padding) are ignored.  V <= 262144,
+ * penalty > 0; penalty == 1 is a no-op. */
+int32_t llmy_repetition_penalty_f32(float* logits, int32_t rows, int32_t V,
+                                    const int32_t* recent, int32_t n_recent,
+                                    float penalty, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

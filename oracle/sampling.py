@@ -16,7 +16,7 @@ def argmax(logits: torch.Tensor) -> np.ndarray:
 
 
 def top_p_sample(logits: torch.Tensor, temperature: float, top_p: float, u: torch.Tensor,
-                 top_k: int = 0) -> np.ndarray:
+                 top_k: int = 0, return_margin: bool = False):
     """Temperature + nucleus sampling with a caller-supplied uniform per row.
 
     Restates sample_standalone.py:5611-5636 and the C twin
@@ -27,12 +27,18 @@ def top_p_sample(logits: torch.Tensor, temperature: float, top_p: float, u: torc
         reaches top_p (first element always kept; llmy.cpp:179-185);
       * renormalise; return the first kept token i with u < cumsum_i
         (inverse CDF, llmy.cpp:195-200), the last kept one if none.
-    Arithmetic in fp64.
+    Arithmetic in fp64.  With return_margin, also returns per row the distance
+    of the two decisions from a flip: for the nucleus, how far the cumulative
+    probabilities either side of the cut are from top_p; for the draw, how far
+    u is from the two CDF steps that bound the picked token.  An implementation
+    whose cumulative probabilities are off by less than that margin must pick
+    the same id.
     """
     x = logits.detach().double().cpu().numpy() / float(temperature)
     rows, V = x.shape
     uu = u.detach().double().cpu().numpy().reshape(-1)
     out = np.empty(rows, dtype=np.int64)
+    margin = np.full(rows, np.inf)
     ids = np.arange(V)
     for r in range(rows):
         order = np.lexsort((ids, -x[r]))
@@ -47,8 +53,30 @@ def top_p_sample(logits: torch.Tensor, temperature: float, top_p: float, u: torc
             hit = np.nonzero(c >= top_p)[0]
             if hit.size:
                 cut = int(hit[0]) + 1
+            margin[r] = abs(c[cut - 1] - top_p)
+            if cut >= 2:
+                margin[r] = min(margin[r], abs(top_p - c[cut - 2]))
         kept = p[:cut] / p[:cut].sum()
         cdf = np.cumsum(kept)
         pick = np.nonzero(uu[r] < cdf)[0]
-        out[r] = order[int(pick[0])] if pick.size else order[cut - 1]
-    return out
+        i = int(pick[0]) if pick.size else cut - 1
+        out[r] = order[i]
+        lo = cdf[i - 1] if i > 0 else -np.inf
+        margin[r] = min(margin[r], abs(cdf[i] - uu[r]), abs(uu[r] - lo))
+    return (out, margin) if return_margin else out
+
+
+def repetition_penalty(logits: torch.Tensor, recent, penalty: float) -> torch.Tensor:
+    """sample_standalone.py:5601-5605: each distinct id of recent[r] (ids outside
+    [0, V) ignored) has its logit divided by penalty if > 0, else multiplied.
+    The arithmetic is one IEEE fp32 operation with the penalty rounded to fp32,
+    as it is on fp32 logits."""
+    x = logits.detach().float().cpu().numpy().copy()
+    V = x.shape[1]
+    pen = np.float32(penalty)
+    rec = np.asarray(recent)
+    for r in range(x.shape[0]):
+        for t in sorted(set(int(i) for i in rec[r] if 0 <= int(i) < V)):
+            v = x[r, t]
+            x[r, t] = v / pen if v > 0 else v * pen
+    return torch.from_numpy(x)

@@ -75,3 +75,19 @@ def test_permute_and_argmax_reject_bad_arguments(lib):
 def test_call_raises_on_status():
     with pytest.raises(_lib.LlmyError):
         _lib.call("llmy_sample_argmax_f32", None, 4, 10, FAKE, None)
+
+
+def test_sampling_entries_reject_bad_arguments(lib):
+    top_p = lib.llmy_sample_top_p_f32
+    assert top_p(FAKE, 4, 32769, 0.8, 0, 0.9, FAKE, FAKE, None) == INVALID   # V > 32768
+    assert top_p(FAKE, 4, 0, 0.8, 0, 0.9, FAKE, FAKE, None) == INVALID       # empty vocab
+    assert top_p(FAKE, -1, 10, 0.8, 0, 0.9, FAKE, FAKE, None) == INVALID
+    assert top_p(FAKE, 4, 10, 0.8, 0, 0.9, None, FAKE, None) == INVALID      # u missing
+    assert top_p(None, 4, 10, 0.8, 0, 0.9, FAKE, FAKE, None) == INVALID
+    assert top_p(FAKE, 0, 10, 0.8, 0, 0.9, None, None, None) == 0            # no rows: no-op
+    pen = lib.llmy_repetition_penalty_f32
+    assert pen(FAKE, 4, 10, FAKE, 3, 0.0, None) == INVALID                   # penalty <= 0
+    assert pen(FAKE, 4, 10, FAKE, -1, 1.3, None) == INVALID
+    assert pen(FAKE, 4, (1 << 18) + 1, FAKE, 3, 1.3, None) == INVALID
+    assert pen(None, 4, 10, None, 0, 1.3, None) == 0                          # nothing listed
+    assert pen(None, 4, 10, None, 3, 1.0, None) == 0                          # penalty 1: no-op

@@ -1,0 +1,143 @@
+"""GPU parity: temperature + top-k + nucleus sampling and the repetition penalty.
+
+The kernel sums probabilities exactly (integer fixed point) but computes each
+one in fp32, so its cumulative probabilities differ from the fp64 oracle's by
+a few 1e-7.  Rows whose oracle decision margin exceeds EPS must pick exactly
+the oracle's id; the rest must pick a neighbour (one position away in the
+sorted order) of it.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle.sampling import repetition_penalty, top_p_sample
+
+pytestmark = pytest.mark.gpu
+
+EPS = 4e-6  # bound on the kernel's cumulative-probability error (fp32 exp of |arg| <= ~20)
+P90 = float(np.float32(0.9))  # the value the fp32 ABI argument carries
+
+
+def ops():
+    from hybrid_llm_amd import ops as o
+    return o
+
+
+def _order_pos(logits_row: np.ndarray, ids: np.ndarray) -> np.ndarray:
+    order = np.lexsort((np.arange(logits_row.size), -logits_row.astype(np.float64)))
+    pos = np.empty_like(order)
+    pos[order] = np.arange(order.size)
+    return pos[ids]
+
+
+def _check(logits, T, p, u, top_k, min_exact=0.6):
+    got = ops().sample_top_p(logits.cuda(), T, p, u.cuda(), top_k=top_k).cpu().numpy()
+    ref, margin = top_p_sample(logits, T, p, u, top_k=top_k, return_margin=True)
+    safe = margin > EPS
+    assert safe.mean() >= min_exact, safe.mean()
+    bad = np.nonzero(safe & (got != ref))[0]
+    assert bad.size == 0, (bad[:8], got[bad[:8]], ref[bad[:8]], margin[bad[:8]])
+    x = logits.numpy()
+    for r in np.nonzero(~safe)[0]:
+        pg, pr = _order_pos(x[r], np.array([got[r], ref[r]]))
+        assert abs(int(pg) - int(pr)) <= 1, (r, got[r], ref[r])
+    return got
+
+
+@pytest.mark.parametrize("scale", [0.6, 2.0, 8.0])
+@pytest.mark.parametrize("top_k", [0, 50])
+def test_top_p_c5(scale, top_k):
+    """C5 sampling shape: logits [64, 32000] fp32, T=0.8, p=0.9, one uniform per row.
+    With near-flat logits each token holds ~3e-5 of the mass, so u or p often
+    lands within EPS of a step and fewer rows qualify for the exact check."""
+    g = torch.Generator().manual_seed(int(scale * 10) + top_k)
+    logits = torch.randn(64, 32000, generator=g) * scale
+    u = torch.rand(64, generator=g)
+    _check(logits, 0.8, P90, u, top_k, min_exact=0.25 if (scale < 1 and top_k == 0) else 0.6)
+
+
+def test_top_p_ties_resolve_by_id():
+    # quantised logits: long runs of exactly equal values, ordered by id
+    g = torch.Generator().manual_seed(5)
+    logits = torch.round(torch.randn(32, 32000, generator=g) * 2) / 4
+    u = torch.rand(32, generator=g)
+    for k in (0, 7, 1000):
+        _check(logits, 0.8, P90, u, k, min_exact=0.6 if k == 7 else 0.3)
+    # every logit equal: the draw is uniform over ids, floor(u * V)
+    flat = torch.zeros(4, 1000)
+    uu = torch.tensor([0.0, 0.25, 0.5004, 0.9995])
+    got = ops().sample_top_p(flat.cuda(), 1.0, 1.0, uu.cuda()).cpu().numpy()
+    assert list(got) == [0, 250, 500, 999]
+
+
+@pytest.mark.parametrize("V", [1, 3, 7, 100, 4097, 32768])
+def test_top_p_shapes(V):
+    g = torch.Generator().manual_seed(V)
+    logits = torch.randn(5, V, generator=g) * 3
+    u = torch.rand(5, generator=g)
+    for k in (0, 1, 2, V - 1, V, V + 5):
+        for p in (P90, 0.5, 1.0):
+            _check(logits, 0.7, p, u, k, min_exact=0.0)
+
+
+def test_top_p_closed_forms():
+    g = torch.Generator().manual_seed(3)
+    logits = torch.randn(16, 2000, generator=g) * 2
+    L = logits.cuda()
+    greedy = torch.argmax(logits, -1).numpy()
+    s = ops().sample_top_p
+    assert np.array_equal(s(L, 0.8, P90, torch.zeros(16, device="cuda")).cpu().numpy(), greedy)
+    u = torch.rand(16, generator=g).cuda()
+    assert np.array_equal(s(L, 0.8, 1e-9, u).cpu().numpy(), greedy)        # p -> 0
+    assert np.array_equal(s(L, 0.8, P90, u, top_k=1).cpu().numpy(), greedy)  # k = 1
+    assert np.array_equal(s(L, 0.0, P90, u).cpu().numpy(), greedy)         # T <= 0: greedy
+    assert np.array_equal(s(L, -1.0, P90, u).cpu().numpy(), greedy)
+    # u -> 1 picks the last token of the nucleus
+    ref = top_p_sample(logits, 0.8, P90, torch.full((16,), 0.9999999))
+    got = s(L, 0.8, P90, torch.full((16,), 0.9999999, device="cuda")).cpu().numpy()
+    assert np.array_equal(got, ref)
+
+
+def test_top_p_masked_tokens_never_drawn():
+    g = torch.Generator().manual_seed(8)
+    logits = torch.randn(64, 5000, generator=g)
+    banned = torch.rand(64, 5000, generator=g) < 0.5
+    logits[banned] = -float("inf")
+    u = torch.rand(64, generator=g)
+    got = _check(logits, 1.0, 1.0, u, 0)
+    assert not banned[torch.arange(64), torch.from_numpy(got).long()].any()
+    # a row of -inf only: every token weighs the same
+    row = torch.full((1, 64), -float("inf"), device="cuda")
+    assert ops().sample_top_p(row, 1.0, 1.0, torch.tensor([0.51], device="cuda")).item() == 32
+
+
+def test_top_p_deterministic():
+    g = torch.Generator().manual_seed(4)
+    logits = (torch.randn(64, 32000, generator=g) * 0.6).cuda()
+    u = torch.rand(64, generator=g).cuda()
+    a = ops().sample_top_p(logits, 0.8, P90, u, top_k=50)
+    for _ in range(3):
+        assert torch.equal(ops().sample_top_p(logits, 0.8, P90, u, top_k=50), a)
+
+
+def test_top_p_distribution():
+    """Over a grid of u the draw reproduces the nucleus distribution exactly
+    (each token's share of the grid equals its renormalised probability)."""
+    logits = torch.log(torch.tensor([[0.1, 0.4, 0.2, 0.05, 0.25]]))
+    n = 4000
+    u = (torch.arange(n, dtype=torch.float64) + 0.5) / n
+    got = ops().sample_top_p(logits.expand(n, 5).contiguous().cuda(), 1.0, 0.8,
+                             u.float().cuda()).cpu().numpy()
+    # nucleus of p=0.8: 0.4, 0.25, 0.2 (cumulative 0.85 >= 0.8); renormalised
+    share = np.bincount(got, minlength=5) / n
+    assert np.allclose(share, [0, 0.4 / 0.85, 0.2 / 0.85, 0, 0.25 / 0.85], atol=2.0 / n)
+
+
+@pytest.mark.parametrize("n", [1, 40, 3000])
+def test_repetition_penalty(n):
+    g = torch.Generator().manual_seed(n)
+    logits = torch.randn(64, 32000, generator=g) * 3
+    recent = torch.randint(-3, 32000, (64, n), generator=g, dtype=torch.int32)
+    recent[:, n // 2:] = recent[:, : n - n // 2]  # repeated ids are penalised once
+    got = ops().repetition_penalty_(logits.clone().cuda(), recent.cuda(), 1.3).cpu()
+    assert torch.equal(got, repetition_penalty(logits, recent.numpy(), 1.3))

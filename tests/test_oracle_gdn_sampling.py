@@ -115,3 +115,37 @@ def test_top_p_nucleus_matches_torch_sampler_rule():
         cut = int(torch.nonzero(c >= 0.9)[0]) + 1
         got = top_p_sample(logits[r:r + 1], 0.8, 0.9, torch.tensor([0.999999]))
         assert got[0] == int(order[cut - 1])
+
+
+def test_top_k_rules():
+    g = torch.Generator().manual_seed(11)
+    logits = torch.randn(12, 300, generator=g) * 3
+    u = torch.rand(12, generator=g)
+    greedy = torch.argmax(logits, -1).numpy()
+    # top_k = 1 keeps only the most probable token
+    assert np.array_equal(top_p_sample(logits, 0.7, 1.0, u, top_k=1), greedy)
+    # top-k with the nucleus off: inverse CDF of the renormalised top-k softmax,
+    # taken here through torch.topk (distinct values, so its order is unique)
+    out = top_p_sample(logits, 0.7, 1.0, u, top_k=20)
+    for r in range(12):
+        v, i = torch.topk(logits[r].double(), 20)
+        p = torch.softmax(v / 0.7, -1).numpy()
+        assert out[r] == int(i[np.searchsorted(np.cumsum(p), float(u[r]), side="right")])
+    # the margin is the distance of u from the CDF steps around the pick
+    _, m = top_p_sample(logits[:1], 0.7, 1.0, torch.tensor([0.5]), top_k=2, return_margin=True)
+    v, _ = torch.topk(logits[0].double(), 2)
+    p0 = float(torch.softmax(v / 0.7, -1)[0])
+    assert abs(m[0] - (abs(p0 - 0.5) if p0 > 0.5 else min(0.5 - p0, 0.5))) < 1e-12
+    # ... and, with the nucleus on, from top_p around the cut: three tokens of
+    # probabilities (0.5, 0.3, 0.2), p = 0.85 cuts after the second (0.8 < 0.85 <= 1.0)
+    x = torch.log(torch.tensor([[0.5, 0.3, 0.2]], dtype=torch.float64))
+    got, m = top_p_sample(x, 1.0, 0.85, torch.tensor([0.3]), return_margin=True)
+    assert got[0] == 0 and abs(m[0] - min(0.05, 0.15, 0.5 / 0.8 - 0.3, 0.3)) < 1e-12
+
+
+def test_repetition_penalty_rule():
+    from oracle.sampling import repetition_penalty
+    x = torch.tensor([[2.0, -2.0, 0.0, 4.0, 1.0]])
+    got = repetition_penalty(x, [[0, 1, 1, 2, 7, -1, 3, 3, 3]], 2.0)
+    # positive logits halve, non-positive ones double, each id once
+    assert torch.equal(got, torch.tensor([[1.0, -4.0, 0.0, 2.0, 1.0]]))
