@@ -2,25 +2,37 @@
 
 A step is one decode token for all 64 sequences through the full stack —
 embedding, 12 layers (6 banded-attention + 6 GDN, each with a 24-expert
-SwiGLU MoE) looped twice, final norm, tied LM head and greedy argmax — with
-the KV caches pre-filled to the 2048-token window and random fp32 GDN states,
+SwiGLU MoE) looped twice, final norm, tied LM head, greedy argmax and a
+temperature-0.8 / top-p-0.9 draw from a fixed per-row uniform — with the KV
+caches pre-filled to the 2048-token window and random fp32 GDN states,
 captured once into a HIP graph and replayed.  Inputs and state are resident
 in HBM before the timed region.  Weights are random N(0, 0.02) drawn on the
 GPU from seed 0 (synthetic; no checkpoint).
 
 Also reported on the same JSON line:
-  roofline      the dominant kernel of the step, timed alone with HIP events
-                on its own stream over rotated state buffers, against the
-                HBM peak (8 TB/s);
+  roofline      the dominant kernel of the step (banded attention decode),
+                timed alone with HIP events on its launch stream over rotated
+                cache sets, against the HBM peak (8 TB/s); ``traffic`` is its
+                HBM bytes per launch from two rocprofv3 --pmc runs (FETCH_SIZE,
+                WRITE_SIZE) of this script's --pmc-child mode, each scaled by
+                the counter's reading for a plain copy of known size;
+  kernels       the other hot-path kernels the metric names (MoE, attention,
+                GDN; decode and prefill), each timed the same way against the
+                HBM or bf16-MFMA peak;
   cpu_baseline  the oracle (fp32 PyTorch restatement of the reference math)
                 on the host cores, on a bounded sample of the same workload.
 """
 from __future__ import annotations
 
 import argparse
+import csv
+import glob
 import json
 import os
+import shutil
+import subprocess
 import sys
+import tempfile
 import time
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
@@ -28,6 +40,10 @@ if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0   # dense bf16 MFMA
+METRIC = "decode tok/s @bs64 + per-kernel % of HBM/MFMA roofline (MoE, attn, GDN)"
+SAMPLING = (0.8, 0.9, 0)         # temperature, top_p, top_k (0 = off)
+COPY_BYTES = 1 << 29             # calibration copy: 512 MiB read + 512 MiB written
 
 
 def parse():
@@ -36,7 +52,11 @@ def parse():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-traffic", action="store_true",
+                    help="skip the rocprofv3 --pmc runs (e.g. when already under a profiler)")
+    ap.add_argument("--no-kernels", action="store_true", help="skip the per-kernel table")
     ap.add_argument("--kernel-iters", type=int, default=50)
+    ap.add_argument("--pmc-child", action="store_true", help=argparse.SUPPRESS)
     return ap.parse_args()
 
 
@@ -54,12 +74,29 @@ def fill_state(eng, gen):
     torch.cuda.synchronize()
 
 
-def time_attn_decode(cfg, B, iters, gen):
-    """Average duration of llmy_banded_attn_decode_bf16 at the C5 shape, HIP
-    events on the launch stream, rotating 3 cache sets (1.6 GB) so the
-    256 MB Infinity Cache cannot serve the window."""
+def event_time(launch, iters, warm=3):
+    """Average duration (us) of ``launch(i)`` on a stream of its own, bracketed
+    by HIP events recorded on that stream."""
     import torch
-    from hybrid_llm_amd import _lib
+    stream = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        for i in range(warm):
+            launch(i)
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for i in range(iters):
+            launch(warm + i)
+        end.record(stream)
+    end.synchronize()
+    return start.elapsed_time(end) * 1e3 / iters
+
+
+def attn_decode_sets(cfg, B, gen):
+    """3 rotated cache sets (1.6 GB) so the 256 MB Infinity Cache cannot serve
+    the window between launches."""
+    import torch
     H, hd, W = cfg.attn_heads, cfg.attn_head_dim, cfg.window
     sets = []
     for _ in range(3):
@@ -67,10 +104,15 @@ def time_attn_decode(cfg, B, iters, gen):
         vc = torch.empty_like(kc).normal_(generator=gen)
         qkv = torch.empty(B, 3 * H * hd, dtype=torch.bfloat16, device="cuda").normal_(generator=gen)
         sets.append((kc, vc, qkv))
+    return sets
+
+
+def attn_decode_launcher(cfg, B, sets):
+    import torch
+    from hybrid_llm_amd import _lib
+    H, hd, W = cfg.attn_heads, cfg.attn_head_dim, cfg.window
     pos = torch.full((B,), W, dtype=torch.int32, device="cuda")
     out = torch.empty(B, H, hd, dtype=torch.bfloat16, device="cuda")
-    stream = torch.cuda.Stream()
-    sp = stream.cuda_stream
 
     def launch(i):
         kc, vc, qkv = sets[i % 3]
@@ -78,36 +120,197 @@ def time_attn_decode(cfg, B, iters, gen):
         p = qkv.data_ptr()
         _lib.call("llmy_banded_attn_decode_bf16", p, p + 2 * Hhd, p + 4 * Hhd, 3 * Hhd, 3 * Hhd,
                   kc.data_ptr(), vc.data_ptr(), pos.data_ptr(), out.data_ptr(), B, H, hd, W,
-                  cfg.attn_scale, sp)
+                  cfg.attn_scale, torch.cuda.current_stream().cuda_stream)
+    return launch
 
-    torch.cuda.synchronize()
-    with torch.cuda.stream(stream):
-        for i in range(5):
-            launch(i)
-        start = torch.cuda.Event(enable_timing=True)
-        end = torch.cuda.Event(enable_timing=True)
-        start.record(stream)
-        for i in range(iters):
-            launch(i)
-        end.record(stream)
-    end.synchronize()
-    us = start.elapsed_time(end) * 1e3 / iters
-    # algorithmic bytes: K and V windows read, new K/V written, q/k/v/out rows
-    bytes_ = 2 * B * H * W * hd * 2 + 2 * B * H * hd * 2 + 4 * B * H * hd * 2
+
+def attn_decode_bytes(cfg, B):
+    """Algorithmic bytes of one decode launch: the K and V windows read, the new
+    K/V rows written, the q/k/v rows read and the output written (bf16)."""
+    H, hd, W = cfg.attn_heads, cfg.attn_head_dim, cfg.window
+    return 2 * B * H * W * hd * 2 + 2 * B * H * hd * 2 + 4 * B * H * hd * 2
+
+
+def time_attn_decode(cfg, B, iters, gen):
+    import torch
+    sets = attn_decode_sets(cfg, B, gen)
+    us = event_time(attn_decode_launcher(cfg, B, sets), iters, warm=5)
     del sets
     torch.cuda.empty_cache()
-    return us, bytes_
+    return us, attn_decode_bytes(cfg, B)
 
 
-def cpu_baseline(B, seconds_budget=30.0):
-    """Oracle (fp32 torch on the host) on a bounded sample: one decode step of
-    a C5-shaped slice — one attention + one GDN layer with their MoEs, one
-    loop, batch 64, 2048-token window — scaled to the full step (12 such
-    layer pairs plus the LM head, which is timed separately)."""
+# --------------------------------------------------------------------------- HBM traffic
+def pmc_child():
+    """Run under ``rocprofv3 --pmc``: a plain device copy of COPY_BYTES (the
+    calibration), then the dominant kernel at the bench shape."""
+    import torch
+    from hybrid_llm_amd.config import C5
+    torch.cuda.set_device(0)
+    gen = torch.Generator(device="cuda").manual_seed(0)
+    src = torch.empty(COPY_BYTES // 4, dtype=torch.float32, device="cuda").normal_(generator=gen)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+    torch.cuda.empty_cache()
+    sets = attn_decode_sets(C5, 64, gen)
+    launch = attn_decode_launcher(C5, 64, sets)
+    for i in range(9):
+        launch(i)
+    torch.cuda.synchronize()
+    print("[pmc-child] done", flush=True)
+
+
+def _pmc_run(counter, outdir):
+    """One rocprofv3 pass collecting ``counter``; returns {kernel name: [values]}."""
+    cmd = ["rocprofv3", "--pmc", counter, "--output-format", "csv", "-d", outdir, "-o", "pmc",
+           "--", sys.executable, os.path.abspath(__file__), "--pmc-child"]
+    subprocess.run(cmd, check=True, timeout=240, stdout=subprocess.DEVNULL,
+                   stderr=subprocess.DEVNULL, cwd=ROOT)
+    per: dict[str, dict[int, float]] = {}
+    for path in glob.glob(os.path.join(outdir, "**", "*counter_collection.csv"), recursive=True):
+        with open(path, newline="") as f:
+            for row in csv.DictReader(f):
+                if row.get("Counter_Name") != counter:
+                    continue
+                d = per.setdefault(row["Kernel_Name"], {})
+                key = int(row["Dispatch_Id"])
+                d[key] = d.get(key, 0.0) + float(row["Counter_Value"])
+    return {k: [v[i] for i in sorted(v)] for k, v in per.items()}
+
+
+def measure_traffic():
+    """HBM bytes per launch of the decode attention kernel: FETCH_SIZE and
+    WRITE_SIZE (KiB per dispatch) each divided by the same counter's reading
+    per byte of a plain 512 MiB device copy.  Runs before this process touches
+    the GPU; any failure yields None."""
+    if shutil.which("rocprofv3") is None:
+        return None
+    out = {}
+    try:
+        for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+            with tempfile.TemporaryDirectory(prefix="llmy_pmc_") as d:
+                per = _pmc_run(counter, d)
+            copy = [v for k, vals in per.items() if "copy" in k.lower() for v in vals]
+            attn = [v for k, vals in per.items() if "attn_decode_kernel" in k for v in vals]
+            if not copy or len(attn) < 4:
+                return None
+            factor = (sum(copy) / len(copy)) * 1024.0 / COPY_BYTES
+            attn = attn[3:]  # the first launches warm the caches' tags
+            out[counter] = {"kib_per_launch": sum(attn) / len(attn), "copy_factor": factor}
+    except (subprocess.SubprocessError, OSError, ValueError, KeyError):
+        return None
+    fetch = out["FETCH_SIZE"]["kib_per_launch"] * 1024.0 / out["FETCH_SIZE"]["copy_factor"]
+    write = out["WRITE_SIZE"]["kib_per_launch"] * 1024.0 / out["WRITE_SIZE"]["copy_factor"]
+    return {"bytes": fetch + write, "fetch_bytes": fetch, "write_bytes": write,
+            "fetch_copy_factor": out["FETCH_SIZE"]["copy_factor"],
+            "write_copy_factor": out["WRITE_SIZE"]["copy_factor"]}
+
+
+# --------------------------------------------------------------------------- kernel table
+def kernel_table(cfg, B, gen, iters):
+    """Per-kernel roofline fractions for the kernels the metric names."""
+    import torch
+    import torch.nn.functional as F
+    from hybrid_llm_amd import _lib, ops
+    rows = {}
+
+    def hbm(name, us, bytes_, workload):
+        gbs = bytes_ / (us * 1e-6) / 1e9
+        rows[name] = {"workload": workload, "bound": "hbm", "avg_us": round(us, 2),
+                      "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                      "frac": round(gbs / HBM_PEAK_GBS, 4)}
+
+    def mfma(name, us, flops, workload):
+        tf = flops / (us * 1e-6) / 1e12
+        rows[name] = {"workload": workload, "bound": "mfma", "avg_us": round(us, 2),
+                      "achieved": round(tf, 1), "peak": MFMA_BF16_PEAK_TFLOPS,
+                      "unit": "TFLOP/s", "frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4)}
+
+    D, E, Hf, k = cfg.d_model, cfg.n_experts, cfg.expert_hidden, cfg.top_k
+    # MoE decode (C2 decode variant / one C5 MoE application): packed expert
+    # weights, 3 rotated sets; bytes = weights of the experts the routes touch
+    wsets = [(ops.pack_weights((torch.randn(E, 2 * Hf, D, device="cuda", generator=gen) * 0.02)
+                               .bfloat16()),
+              ops.pack_weights((torch.randn(E, D, Hf, device="cuda", generator=gen) * 0.02)
+                               .bfloat16())) for _ in range(3)]
+    x = torch.randn(B, D, device="cuda", generator=gen)
+    wr = torch.randn(E, D, device="cuda", generator=gen) * 0.02
+    ones = torch.ones(D, device="cuda")
+    bufs = ops.moe_route_decode(x, ones, ones, wr, k)
+    act = torch.empty(B * k, Hf, dtype=torch.bfloat16, device="cuda")
+    y = torch.empty(B * k, D, device="cuda")
+    n_active = int((bufs["counts"] > 0).sum())
+    us = event_time(lambda i: ops.moe_experts_routed(bufs["h"], bufs["idx"], bufs["gates"],
+                                                     *wsets[i % 3], act=act, y=y,
+                                                     layout=ops.LAYOUT_PACKED), iters)
+    hbm("moe_decode_experts", us, n_active * 3 * Hf * D * 2 + B * D * 2 + B * k * D * 4,
+        f"T={B}, D={D}, E={E}, top-{k}, H={Hf}; {n_active} experts active")
+    del wsets
+    # GDN decode step (C4 decode variant at C5 head shape): fp32 state read + written
+    Hg, dk, dv = cfg.gdn_heads, cfg.gdn_dk, cfg.gdn_dv
+    nproj = 2 * Hg * dk + Hg * dv + D + Hg
+    Ss = [torch.randn(B, Hg, dk, dv, device="cuda", generator=gen) * 0.1 for _ in range(3)]
+    proj = torch.randn(B, nproj, device="cuda", generator=gen)
+    go = torch.empty(B, Hg * dv, dtype=torch.bfloat16, device="cuda")
+    zb, dec = torch.zeros(Hg, device="cuda"), torch.full((Hg,), 2.0, device="cuda")
+    us = event_time(lambda i: ops.gdn_step_fused(proj, zb, dec, Ss[i % 3], out=go), iters)
+    hbm("gdn_decode_step", us, 2 * B * Hg * dk * dv * 4 + B * nproj * 4 + B * Hg * dv * 2,
+        f"B={B}, H={Hg}, dk=dv={dk}, fp32 state")
+    del Ss
+    # MoE prefill (C2): router -> permute -> grouped experts -> combine
+    T2 = 4096
+    x2 = torch.randn(T2, D, device="cuda", generator=gen).bfloat16()
+    wr2 = torch.randn(E, D, device="cuda", generator=gen) * 0.02
+    wgu = (torch.randn(E, 2 * Hf, D, device="cuda", generator=gen) * 0.02).bfloat16()
+    wd = (torch.randn(E, D, Hf, device="cuda", generator=gen) * 0.02).bfloat16()
+    us = event_time(lambda i: ops.moe_forward(x2, wr2, wgu, wd, k), max(3, iters // 10))
+    mfma("moe_prefill_layer", us, 2 * T2 * k * (D * 2 * Hf + Hf * D),
+         f"C2: T={T2}, D={D}, E={E}, top-{k}, H={Hf} (router+permute+experts+combine)")
+    del x2, wgu, wd
+    # attention prefill (C3)
+    Bq, Tq, Hq, hq, Wq = 4, 8192, 16, 64, 512
+    qkv = [torch.randn(Bq, Tq, Hq, hq, device="cuda", generator=gen).bfloat16() for _ in range(3)]
+    ao = torch.empty_like(qkv[0])
+    us = event_time(lambda i: ops.banded_attn_prefill(*qkv, Wq, out=ao), max(3, iters // 5))
+    pairs = sum(min(t + 1, Wq) for t in range(Tq))
+    mfma("attn_prefill", us, 4 * Bq * Hq * hq * pairs,
+         f"C3: B={Bq}, T={Tq}, H={Hq}, hd={hq}, window={Wq}")
+    del qkv, ao
+    # GDN prefill (C4): chunked gated delta rule
+    Bg, Tg, Hg4, d4 = 8, 4096, 16, 128
+    gq = F.normalize(torch.randn(Bg, Tg, Hg4, d4, device="cuda", generator=gen), dim=-1).bfloat16()
+    gk = F.normalize(torch.randn(Bg, Tg, Hg4, d4, device="cuda", generator=gen), dim=-1).bfloat16()
+    gv = torch.randn(Bg, Tg, Hg4, d4, device="cuda", generator=gen).bfloat16()
+    gb = torch.sigmoid(torch.randn(Bg, Tg, Hg4, device="cuda", generator=gen))
+    gg = torch.exp(-F.softplus(torch.randn(Bg, Tg, Hg4, device="cuda", generator=gen)))
+    gS = torch.zeros(Bg, Hg4, d4, d4, device="cuda")
+    go4 = torch.empty(Bg, Tg, Hg4, d4, dtype=torch.bfloat16, device="cuda")
+    nb = int(_lib.load().llmy_gdn_prefill_workspace_bytes(Bg, Tg, Hg4, d4, d4))
+    ws = torch.empty(nb, dtype=torch.uint8, device="cuda")
+    us = event_time(lambda i: ops.gdn_prefill(gq, gk, gv, gb, gg, gS, out=go4, workspace=ws), 3,
+                    warm=1)
+    bytes4 = 4 * Bg * Tg * Hg4 * d4 * 2 + 2 * Bg * Tg * Hg4 * 4 + 2 * Bg * Hg4 * d4 * d4 * 4
+    hbm("gdn_prefill", us, bytes4, f"C4: B={Bg}, T={Tg}, H={Hg4}, dk=dv={d4}, chunk 64")
+    del gq, gk, gv, go4, ws
+    torch.cuda.empty_cache()
+    return rows
+
+
+def cpu_baseline(B, seconds_budget=10.0):
+    """Oracle (fp32 torch on the host) on a bounded sample: decode steps of a
+    C5-shaped slice — one attention + one GDN layer with their MoEs, one loop,
+    batch 64, 2048-token window — repeated for about ``seconds_budget`` and
+    scaled to the full step (12 such layer pairs plus one LM head and the
+    sampling, which the sample's own step includes once)."""
     import torch
     from dataclasses import replace
     from hybrid_llm_amd.config import C5, alternating, init_weights
     from oracle.model import HybridOracle
+    from oracle.sampling import top_p_sample
 
     threads = len(os.sched_getaffinity(0))
     torch.set_num_threads(threads)
@@ -123,26 +326,48 @@ def cpu_baseline(B, seconds_budget=30.0):
         for name, t in s.items():
             t.normal_(0.0, 0.1 if name == "S" else 1.0, generator=g)
     tokens = torch.randint(0, cfg.vocab, (B,), generator=g)
-    ora.step(tokens, st)  # warmup
-    t0 = time.perf_counter()
-    ora.step(tokens, st)
-    t_pair = time.perf_counter() - t0
+    u = torch.rand(B, generator=g)
+
+    def step():
+        logits = ora.step(tokens, st)
+        top_p_sample(logits, SAMPLING[0], SAMPLING[1], u, top_k=SAMPLING[2])
+
+    step()  # warmup
+    n, t0 = 0, time.perf_counter()
+    while True:
+        step()
+        n += 1
+        t_pair = (time.perf_counter() - t0) / n
+        if time.perf_counter() - t0 >= seconds_budget:
+            break
     # the sample's step includes one LM head; the full step has 12 pairs + 1 head
     hf = torch.randn(B, cfg.d_model, generator=g)
-    t0 = time.perf_counter()
-    _ = hf @ ora.w["embed"].t()
-    t_head = time.perf_counter() - t0
+    m, t0 = 5, time.perf_counter()
+    for _ in range(m):
+        _ = hf @ ora.w["embed"].t()
+    t_head = (time.perf_counter() - t0) / m
     t_full = 12 * (t_pair - t_head) + t_head
     return {"value": B / t_full, "unit": "tok/s", "cores": threads, "kind": "port",
-            "sample": (f"oracle fp32 decode step of 1 attention + 1 GDN layer (+MoE) at batch {B},"
-                       f" window 2048, timed {t_pair:.2f}s; scaled x12 layer pairs + LM head")}
+            "sample": (f"oracle fp32 decode steps of a C5 slice (1 attention + 1 GDN layer, each"
+                       f" with its 24-expert MoE, batch {B}, window 2048, LM head, top-p draw):"
+                       f" {n} steps in {n * t_pair:.1f}s, {t_pair * 1e3:.0f} ms/step; scaled to"
+                       f" 12 layer pairs + one LM head")}
 
 
 def main():
     args = parse()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1"}))
+        print(json.dumps({"error": "this build runs on one GPU (one MI355X per box); "
+                                   "--gpus must be 1"}))
         sys.exit(2)
+    if args.pmc_child:
+        pmc_child()
+        return
+    # the counter passes run as child processes before this process touches the GPU
+    traffic = None if args.no_traffic else measure_traffic()
+    if traffic is not None:
+        print(f"[bench] attn decode traffic {traffic['bytes'] / 1e6:.1f} MB/launch",
+              file=sys.stderr, flush=True)
     import torch
     from hybrid_llm_amd.config import C5, init_weights
     from hybrid_llm_amd.engine import HybridDecoder
@@ -154,12 +379,13 @@ def main():
     gen = torch.Generator(device=dev).manual_seed(0)
     t0 = time.time()
     weights = init_weights(cfg, seed=0, device=dev)
-    eng = HybridDecoder(cfg, weights, B, device=dev)
+    eng = HybridDecoder(cfg, weights, B, device=dev, sampling=SAMPLING)
     del weights
     torch.cuda.empty_cache()
     fill_state(eng, gen)
     tokens = torch.randint(0, cfg.vocab, (B,), device=dev, generator=gen, dtype=torch.int64)
     eng.buf["tokens"].copy_(tokens.to(torch.int32))
+    eng.set_uniforms(torch.rand(B, device=dev, generator=gen))
     eng.capture()
     print(f"[bench] setup {time.time() - t0:.1f}s", file=sys.stderr, flush=True)
 
@@ -181,23 +407,36 @@ def main():
     achieved = bytes_ / (us * 1e-6) / 1e9
     roofline = {"kernel": "attn_decode_kernel<64>", "bound": "hbm", "achieved": round(achieved, 1),
                 "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                "traffic": None, "avg_us": round(us, 2), "bytes_per_launch": bytes_}
+                "traffic": None if traffic is None else round(traffic["bytes"]),
+                "avg_us": round(us, 2), "bytes_per_launch": bytes_}
+    if traffic is not None:
+        roofline["traffic_detail"] = {k: (round(v, 4) if "factor" in k else round(v))
+                                      for k, v in traffic.items() if k != "bytes"}
     print(f"[bench] attn decode {us:.1f} us, {achieved:.0f} GB/s", file=sys.stderr, flush=True)
+
+    kernels = None
+    if not args.no_kernels:
+        kernels = kernel_table(cfg, B, gen, args.kernel_iters)
+        for name, r in kernels.items():
+            print(f"[bench] {name}: {r['avg_us']} us, {r['achieved']} {r['unit']} "
+                  f"({100 * r['frac']:.1f}%)", file=sys.stderr, flush=True)
 
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(B)
         print(f"[bench] cpu baseline {cpu['value']:.2f} tok/s", file=sys.stderr, flush=True)
 
-    line = {"metric": "decode tok/s @bs64 (hybrid-MoE decode step, BASELINE config 5)",
+    line = {"metric": METRIC,
             "value": round(value, 1), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
             "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True,
             "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
-            "config": {"workload": "C5 full hybrid-MoE decode step, bs64",
+            "config": {"workload": "C5 full hybrid-MoE decode step, bs64 (greedy + top-p draw)",
                        "d_model": cfg.d_model, "layers": cfg.n_layers, "loops": cfg.num_loops,
                        "experts": cfg.n_experts, "top_k": cfg.top_k, "window": cfg.window,
+                       "vocab": cfg.vocab, "sampling": {"temperature": SAMPLING[0],
+                                                        "top_p": SAMPLING[1]},
                        "global_batch": B, "parallelism": "single GPU"},
-            "roofline": roofline, "cpu_baseline": cpu}
+            "roofline": roofline, "kernels": kernels, "cpu_baseline": cpu}
     print(json.dumps(line))
 
 

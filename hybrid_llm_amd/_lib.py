@@ -24,6 +24,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "llmy_router_topk_logits_f32": (_I, [_P, _P, _P, _I, _I, _I, _P]),
     "llmy_moe_permute": (_I, [_P, _I, _I, _P, _P, _P, _P, _P]),
     "llmy_sample_argmax_f32": (_I, [_P, _I, _I, _P, _P]),
+    "llmy_moe_selected_fp32": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P]),
+    "llmy_mhc_sinkhorn4": (_I, [_P, _P, _I, _I, _P]),
     "llmy_sample_top_p_f32": (_I, [_P, _I, _I, _F, _I, _F, _P, _P, _P]),
     "llmy_repetition_penalty_f32": (_I, [_P, _I, _I, _P, _I, _F, _P]),
     "llmy_linear_bf16": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),

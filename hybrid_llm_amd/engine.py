@@ -35,8 +35,14 @@ def _pad_rows(w: torch.Tensor, mult: int) -> torch.Tensor:
 
 class HybridDecoder:
     def __init__(self, cfg: HybridConfig, weights: dict[str, torch.Tensor], batch: int,
-                 device: str | torch.device = "cuda"):
+                 device: str | torch.device = "cuda",
+                 sampling: tuple[float, float, int] | None = None):
+        """``sampling`` = (temperature, top_p, top_k): each step then also draws
+        ``buf["sampled"]`` with llmy_sample_top_p_f32 from the per-row uniforms
+        in ``buf["u"]`` (set with ``set_uniforms``), beside the greedy
+        ``buf["next"]``."""
         self.cfg = cfg
+        self.sampling = sampling
         self.B = batch
         self.dev = torch.device(device)
         dev = self.dev
@@ -117,6 +123,8 @@ class HybridDecoder:
             "y": torch.zeros(B * k, D, dtype=f32, device=dev),
             "logits": torch.zeros(B, cfg.vocab, dtype=f32, device=dev),
             "next": torch.zeros(B, dtype=torch.int32, device=dev),
+            "u": torch.zeros(B, dtype=f32, device=dev),
+            "sampled": torch.zeros(B, dtype=torch.int32, device=dev),
         }
         self.graph: torch.cuda.CUDAGraph | None = None
         # Decode MoE: fused norm + router (W_r in LDS) and route-indexed experts
@@ -209,9 +217,19 @@ class HybridDecoder:
         ops.linear(b["h"], w["lm_head"], out=b["logits"], epilogue=ops.EPI_STORE_F32,
                    layout=ops.LAYOUT_PACKED)
         from . import _lib
+        stream = torch.cuda.current_stream().cuda_stream
         _lib.call("llmy_sample_argmax_f32", b["logits"].data_ptr(), self.B, cfg.vocab,
-                  b["next"].data_ptr(), torch.cuda.current_stream().cuda_stream)
+                  b["next"].data_ptr(), stream)
+        if self.sampling is not None:
+            T, p, k = self.sampling
+            _lib.call("llmy_sample_top_p_f32", b["logits"].data_ptr(), self.B, cfg.vocab,
+                      float(T), int(k), float(p), b["u"].data_ptr(), b["sampled"].data_ptr(),
+                      stream)
         self.pos.add_(1)
+
+    def set_uniforms(self, u: torch.Tensor) -> None:
+        """Per-row uniform draws in [0, 1) for the next steps' top-p sampling."""
+        self.buf["u"].copy_(u.to(torch.float32).view(-1))
 
     def step(self, tokens: torch.Tensor | None = None) -> torch.Tensor:
         """Decode one token for every sequence.  ``tokens`` [B] int32 (device or
@@ -225,7 +243,7 @@ class HybridDecoder:
         return self.buf["logits"]
 
     def capture(self) -> None:
-        """Capture one step (embedding .. argmax, pos += 1) into a HIP graph.
+        """Capture one step (embedding .. argmax [, top-p draw], pos += 1) into a HIP graph.
         Capturing runs nothing, so the state is unchanged."""
         torch.cuda.synchronize()
         g = torch.cuda.CUDAGraph()

@@ -251,6 +251,31 @@ int32_t llmy_moe_route_decode(const float* x, const float* ffn_w,
                               int32_t* sorted_routes, int32_t* route_pos, int32_t T,
                               int32_t D, int32_t E, int32_t k, float eps, void* stream);
 
+/* --- The reference ABI's fp32 operator hooks (same signatures) ------------ */
+
+/* One-token sparse MoE over the k selected experts, fp32 throughout; replaces
+ * llmy_moe_selected_fp32 (llmy_cuda/include/llmy.h:80-88), called by
+ * sample_standalone.py:3001-3075.  x [D], idx [k] int64, prob [k],
+ * gate_up [E,2H,D] (gate rows then up rows), down [E,D,H]; scratch
+ * activation [k,H] and route_output [k,D]; out [D]:
+ *   activation[j] = silu(W_gate[e_j] x) * (W_up[e_j] x),
+ *   route_output[j] = prob[j] * W_down[e_j] activation[j],
+ *   out = sum over j (ascending) of route_output[j].
+ * A route id outside [0, E) contributes zeros.  Returns 1 before any launch
+ * for a null pointer or a non-positive size. */
+int32_t llmy_moe_selected_fp32(const float* x, const int64_t* idx, const float* prob,
+                               const float* gate_up, const float* down, float* activation,
+                               float* route_output, float* out, int32_t D, int32_t H,
+                               int32_t E, int32_t k, void* stream);
+
+/* Out-of-place Sinkhorn on [matrices,4,4] fp32 in the log domain; replaces
+ * llmy_mhc_sinkhorn4 (llmy_cuda/include/llmy.h:74-78), called by
+ * sample_standalone.py:2544-2587: `iterations` rounds of subtracting each row's
+ * logsumexp and then each column's, then output = exp.  matrices > 0,
+ * iterations >= 0. */
+int32_t llmy_mhc_sinkhorn4(const float* input, float* output, int32_t matrices,
+                           int32_t iterations, void* stream);
+
 /* --- Sampling (sample_standalone.py:5609-5636) ---------------------------- */
 
 /* out[r] = first index of the maximum of logits[r, :V] (NaN counts as the

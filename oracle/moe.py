@@ -69,3 +69,31 @@ def moe_per_token(x: torch.Tensor, idx: np.ndarray, gates: torch.Tensor, w_gate:
             a = g / (1.0 + torch.exp(-g)) * u
             out[t] += float(gates[t, j]) * (w_down[e].double() @ a)
     return out.float()
+
+
+def moe_selected_fp32(x: np.ndarray, idx: np.ndarray, prob: np.ndarray, gate_up: np.ndarray,
+                      down: np.ndarray):
+    """One-token selected-expert MoE with the packed gate_up [E, 2H, D] layout.
+
+    Restates the PyTorch path of sample_standalone.py:3065-3075 (index_select
+    the k experts, gate_up GEMV, silu(g) * u, down GEMV, prob-weighted sum)
+    and the scratch contents of llmy_cuda/src/kernels/moe.cu:174-267
+    (activation [k, H], route_output [k, D] = prob * expert output).  Routes
+    with an id outside [0, E) contribute zeros.  fp64; returns
+    (activation, route_output, out).
+    """
+    x = np.asarray(x, dtype=np.float64).reshape(-1)
+    E, H2, D = gate_up.shape
+    H = H2 // 2
+    k = idx.size
+    act = np.zeros((k, H))
+    ro = np.zeros((k, D))
+    for j in range(k):
+        e = int(idx.reshape(-1)[j])
+        if not 0 <= e < E:
+            continue
+        gu = gate_up[e].astype(np.float64) @ x
+        g, u = gu[:H], gu[H:]
+        act[j] = g / (1.0 + np.exp(-g)) * u
+        ro[j] = float(prob.reshape(-1)[j]) * (down[e].astype(np.float64) @ act[j])
+    return act, ro, ro.sum(0)

@@ -91,3 +91,15 @@ def test_sampling_entries_reject_bad_arguments(lib):
     assert pen(FAKE, 4, (1 << 18) + 1, FAKE, 3, 1.3, None) == INVALID
     assert pen(None, 4, 10, None, 0, 1.3, None) == 0                          # nothing listed
     assert pen(None, 4, 10, None, 3, 1.0, None) == 0                          # penalty 1: no-op
+
+
+def test_reference_op_hooks_reject_bad_arguments(lib):
+    moe = lib.llmy_moe_selected_fp32
+    ptrs = [FAKE] * 8
+    assert moe(None, *ptrs[1:], 16, 8, 2, 1, None) == INVALID
+    for bad in ((0, 8, 2, 1), (16, 0, 2, 1), (16, 8, 0, 1), (16, 8, 2, 0)):
+        assert moe(*ptrs, *bad, None) == INVALID
+    sk = lib.llmy_mhc_sinkhorn4
+    assert sk(None, FAKE, 4, 20, None) == INVALID
+    assert sk(FAKE, FAKE, 0, 20, None) == INVALID
+    assert sk(FAKE, FAKE, 4, -1, None) == INVALID

@@ -90,3 +90,43 @@ def test_decode_equals_last_row_of_prefill():
         o, kc, vc = banded_attention_decode(q[:, t], k[:, t], v[:, t], kc, vc,
                                             torch.full((B,), t))
         assert torch.allclose(o, full[:, t], atol=1e-5), t
+
+
+def test_moe_selected_matches_per_token_brute_force():
+    from oracle.moe import moe_per_token, moe_selected_fp32
+    g = torch.Generator().manual_seed(21)
+    E, H, D, k = 5, 12, 16, 3
+    wg = torch.randn(E, H, D, generator=g)
+    wu = torch.randn(E, H, D, generator=g)
+    wd = torch.randn(E, D, H, generator=g)
+    x = torch.randn(1, D, generator=g)
+    idx = np.array([[4, 0, 2]])
+    prob = torch.tensor([[0.5, 0.3, 0.2]])
+    _, ro, out = moe_selected_fp32(x.numpy(), idx, prob.numpy(),
+                                   torch.cat([wg, wu], 1).numpy(), wd.numpy())
+    ref = moe_per_token(x, idx, prob, wg, wu, wd)
+    assert np.allclose(out, ref.numpy()[0], rtol=1e-5, atol=1e-5)
+    # route_output rows are the prob-weighted expert outputs
+    assert np.allclose(ro[1], 0.3 * moe_per_token(x, idx[:, 1:2], torch.ones(1, 1), wg, wu,
+                                                  wd).numpy()[0], rtol=1e-5, atol=1e-5)
+    # an out-of-range id contributes nothing
+    _, _, out2 = moe_selected_fp32(x.numpy(), np.array([[4, 7, 2]]), prob.numpy(),
+                                   torch.cat([wg, wu], 1).numpy(), wd.numpy())
+    ref2 = moe_per_token(x, idx[:, [0, 2]], prob[:, [0, 2]], wg, wu, wd)
+    assert np.allclose(out2, ref2.numpy()[0], rtol=1e-5, atol=1e-5)
+
+
+def test_sinkhorn4_closed_forms():
+    from oracle.mhc import sinkhorn4
+    rng = np.random.default_rng(0)
+    x = rng.normal(size=(50, 4, 4))
+    assert np.allclose(sinkhorn4(x, 0), np.exp(x))                    # no iteration: exp
+    assert np.allclose(sinkhorn4(np.full((1, 4, 4), 3.0), 5), 0.25)  # constant -> uniform
+    d = sinkhorn4(x, 200)                                              # converged: doubly stochastic
+    assert np.allclose(d.sum(-1), 1, atol=1e-9) and np.allclose(d.sum(-2), 1, atol=1e-9)
+    # one iteration by hand: row softmax, then column normalisation of that
+    r = np.exp(x[0]) / np.exp(x[0]).sum(-1, keepdims=True)
+    assert np.allclose(sinkhorn4(x[:1], 1)[0], r / r.sum(0, keepdims=True))
+    # permuting rows and columns permutes the result
+    p, q = rng.permutation(4), rng.permutation(4)
+    assert np.allclose(sinkhorn4(x[:, p][:, :, q], 7), sinkhorn4(x, 7)[:, p][:, :, q])
