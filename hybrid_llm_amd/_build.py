@@ -74,8 +74,9 @@ def build(force: bool = True, jobs: int | None = None, verbose: bool = False) ->
         if warn.strip() and verbose:
             print(warn, file=sys.stderr)
     tmp = LIB.with_suffix(".so.tmp")
-    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *[str(o) for o, _ in results],
-           "-o", str(tmp)]
+    # -z defs: an unresolved symbol fails the link instead of the first dlopen
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,-z,defs",
+           *[str(o) for o, _ in results], "-o", str(tmp)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"link failed:\n{_filter(proc.stderr)}")

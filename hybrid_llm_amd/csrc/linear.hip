@@ -398,6 +398,12 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restric
   }
 }
 
+// Tiled MFMA grouped GEMMs for MoE prefill (moe_gemm.hip).
+int32_t moe_gemm_prefill(const uint16_t* x, const int32_t* offsets, const int32_t* sorted_routes,
+                         const float* gates, const uint16_t* w_gate_up, const uint16_t* w_down,
+                         uint16_t* act, float* y, int T, int D, int H, int E, int k, bool packed,
+                         hipStream_t s);
+
 }  // namespace llmy
 
 using namespace llmy;
@@ -473,16 +479,17 @@ extern "C" int32_t llmy_moe_experts_bf16(const llmy_bf16* x, const int32_t* offs
   b.rows_total = T * k; b.x_rows = T * k;
   // Few routes per expert (decode): 16-row chunks, two K blocks per wave for
   // the down projection; otherwise 64-row chunks.  (The route-indexed entry
-  // point uses the same configurations, so the two agree bit for bit.)
+  // point uses the same configurations, so at these sizes the two agree bit
+  // for bit.)
   int32_t st;
   if (T * k <= 16 * E) {
     st = launch_ws<kSwiGLU, kMoeGather, 1>(a, E, packed, s);
     if (st != 0) return st;
     return launch_ws<kMoeDown, kMoeDirect, 1, 2>(b, E, packed, s);
   }
-  st = launch_ws<kSwiGLU, kMoeGather, 4>(a, E, packed, s);
-  if (st != 0) return st;
-  return launch_ws<kMoeDown, kMoeDirect, 4>(b, E, packed, s);
+  // Prefill: tiled MFMA grouped GEMMs (moe_gemm.hip).
+  return moe_gemm_prefill(x, offsets, sorted_routes, gates, w_gate_up, w_down, act, y, T, D, H,
+                          E, k, packed, s);
 }
 
 extern "C" int32_t llmy_moe_combine(const float* y, const int32_t* route_pos, void* out,

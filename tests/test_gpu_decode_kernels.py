@@ -328,8 +328,11 @@ def test_gdn_step_with_fused_conv_gate():
 
 @pytest.mark.parametrize("T,E", [(64, 24), (1, 8), (300, 24)])
 def test_moe_routed_equals_sorted(T, E):
-    """Route-indexed experts (no permutation) give bit-identical rows to the
-    sorted path: y_routed[r] == y_sorted[route_pos[r]]."""
+    """Route-indexed experts (no permutation) match the sorted path row for
+    row: y_routed[r] vs y_sorted[route_pos[r]].  At decode sizes (T*k <= 16*E)
+    both run the same weight-streaming configuration and agree bit for bit;
+    above that the sorted path runs the tiled MFMA GEMMs (another summation
+    order), so the rows agree to bf16/fp32 rounding."""
     wg, wu, wd, wr = _c2_weights(E=E, D=512, H=512, seed=T)
     x = _bf(torch.randn(T, 512, generator=torch.Generator().manual_seed(T))).cuda()
     wgu = ops().pack_weights(torch.cat([wg, wu], 1).cuda())
@@ -339,10 +342,15 @@ def test_moe_routed_equals_sorted(T, E):
     act_s, y_s = ops().moe_experts(x, perm, gates, wgu, wdn, layout=1)
     act_r, y_r = ops().moe_experts_routed(x, idx, gates, wgu, wdn, layout=1)
     rp = perm["route_pos"].long()
-    assert torch.equal(y_r, y_s[rp])
-    assert torch.equal(act_r, act_s[rp])
     xs = torch.randn(T, 512, device="cuda")
     xr = xs.clone()
     ops().moe_combine_norm(y_s, perm["route_pos"], xs, None, None, 2)
     ops().moe_combine_norm(y_r, None, xr, None, None, 2)
-    assert torch.equal(xs, xr)
+    if T * 2 <= 16 * E:
+        assert torch.equal(y_r, y_s[rp])
+        assert torch.equal(act_r, act_s[rp])
+        assert torch.equal(xs, xr)
+    else:
+        assert (act_r.float() - act_s[rp].float()).abs().max() <= 2e-2 * act_s.float().abs().max()
+        assert rel_l2(y_r, y_s[rp]) <= 1e-2
+        assert rel_l2(xr, xs) <= 1e-3
