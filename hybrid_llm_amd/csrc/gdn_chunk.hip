@@ -15,13 +15,15 @@
 //
 // Kernel 1 (gdn_chunk_prep) runs once per (b, h, chunk), all chunks in
 // parallel: K K^T and Q K^T on bf16 MFMA (exact: the inputs are bf16 and the
-// accumulation fp32), the unit lower-triangular inverse by per-column forward
-// substitution in fp32, then W, U0 (written as fp32), A and the cumulative
-// log-decays.  Kernel 2 (gdn_chunk_scan) runs once per (b, h, 32-column slice
-// of the state), sequentially over the chunks with the state slice in LDS.
-// Every product with an fp32 operand uses split-bf16 MFMA: x = hi + lo with
-// hi = bf16(x), lo = bf16(x - hi), keeping hi*hi + hi*lo + lo*hi (relative
-// error about 2^-16); products of two bf16 tensors are exact.
+// accumulation fp32), the unit lower-triangular inverse blocked by 16 (four
+// diagonal forward substitutions, then three levels of 16 x 16 block
+// products), then W, U0, A and the cumulative log-decays.  W and A are
+// written as (hi, lo) bf16 planes, U0 and the log-decays as fp32.  Kernel 2
+// (gdn_chunk_scan) runs once per (b, h, 32-column slice of the state),
+// sequentially over the chunks.  Every product with an fp32 operand uses
+// split-bf16 MFMA: x = hi + lo with hi = bf16(x), lo = bf16(x - hi), keeping
+// hi*hi + hi*lo + lo*hi (relative error about 2^-16); products of two bf16
+// tensors are exact.  Each fp32 operand is split once, where it is made.
 //
 // MFMA v_mfma_f32_16x16x32_bf16 fragments: A lane l holds A[l%16][8(l/16)+j],
 // B lane l holds B[8(l/16)+j][l%16], D lane l holds D[4(l/16)+i][l%16].
@@ -67,15 +69,19 @@ template <int DK, int DV>
 __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, const float* __restrict__ beta,
-    const float* __restrict__ g, float* __restrict__ Wg, float* __restrict__ U0g,
-    float* __restrict__ Ag, float* __restrict__ cumg, int T, int H, int NC) {
-  constexpr int PK = DK + 8, PV = DV + 8, PG = kC + 1;
+    const float* __restrict__ g, uint16_t* __restrict__ Wg, float* __restrict__ U0g,
+    uint16_t* __restrict__ Ag, float* __restrict__ cumg, int T, int H, int NC) {
+  constexpr int PK = DK + 8, PG = kC + 1, PT = kC + 8;
   __shared__ __align__(16) uint16_t Ks[kC * PK];
   __shared__ __align__(16) uint16_t Qs[kC * PK];
-  __shared__ __align__(16) uint16_t Vs[kC * PV];
+  __shared__ __align__(16) uint16_t KsT[DK * PT];  // K^T [DK][64]: B operand over t
+  __shared__ __align__(16) uint16_t VsT[DV * PT];  // V^T [DV][64]
   __shared__ float Gm[kC * PG];   // K K^T, then L
-  __shared__ float Qk[kC * PG];   // Q K^T
   __shared__ float Ti[kC * PG];   // (I + L)^{-1}
+  __shared__ float Pm[kC * 17];   // per-wave 16 x 16 block products
+  // Ti diag(beta Gamma_prev) and Ti diag(beta) as (hi, lo) bf16 pairs: the A
+  // operands of W and U0, split once
+  __shared__ __align__(16) uint16_t TWh[kC * PT], TWl[kC * PT], TUh[kC * PT], TUl[kC * PT];
   __shared__ float cum[kC], prv[kC], bet[kC], wsc[kC];  // wsc = beta * Gamma_prev
 
   const int cid = blockIdx.x;
@@ -90,7 +96,7 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(
   const long long kbase = (static_cast<long long>(b) * T + t0) * rk + static_cast<long long>(h) * DK;
   const long long vbase = (static_cast<long long>(b) * T + t0) * rv + static_cast<long long>(h) * DV;
 
-  // ---- stage K, Q (DK) and V (DV) rows; padded rows are zero
+  // ---- stage K and Q rows, and K, V transposed; padded rows are zero
   for (int f = threadIdx.x; f < kC * (DK / 8); f += 256) {
     const int t = f / (DK / 8), cc = f - t * (DK / 8);
     uint4 kv = uint4{0u, 0u, 0u, 0u}, qv = uint4{0u, 0u, 0u, 0u};
@@ -101,11 +107,25 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(
     *reinterpret_cast<uint4*>(Ks + t * PK + 8 * cc) = kv;
     *reinterpret_cast<uint4*>(Qs + t * PK + 8 * cc) = qv;
   }
+  // transposed copies: token fastest across lanes, so the 2-byte LDS stores of
+  // a wave land in consecutive addresses
+  for (int f = threadIdx.x; f < kC * (DK / 8); f += 256) {
+    const int t = f % kC, cc = f / kC;
+    uint4 kv = uint4{0u, 0u, 0u, 0u};
+    if (t < Tc) kv = *reinterpret_cast<const uint4*>(k + kbase + t * rk + 8 * cc);
+    const uint32_t w[4] = {kv.x, kv.y, kv.z, kv.w};
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj)
+      KsT[(8 * cc + jj) * PT + t] = static_cast<uint16_t>(w[jj >> 1] >> (16 * (jj & 1)));
+  }
   for (int f = threadIdx.x; f < kC * (DV / 8); f += 256) {
-    const int t = f / (DV / 8), cc = f - t * (DV / 8);
+    const int t = f % kC, cc = f / kC;
     uint4 vv = uint4{0u, 0u, 0u, 0u};
     if (t < Tc) vv = *reinterpret_cast<const uint4*>(v + vbase + t * rv + 8 * cc);
-    *reinterpret_cast<uint4*>(Vs + t * PV + 8 * cc) = vv;
+    const uint32_t w[4] = {vv.x, vv.y, vv.z, vv.w};
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj)
+      VsT[(8 * cc + jj) * PT + t] = static_cast<uint16_t>(w[jj >> 1] >> (16 * (jj & 1)));
   }
   if (wave == 0) {
     // inclusive prefix sum of log g over the chunk (padded tokens: g = 1, beta = 0)
@@ -125,7 +145,10 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(
   }
   __syncthreads();
 
-  // ---- K K^T and Q K^T (exact): wave w owns output row block w, 4 column blocks
+  // ---- K K^T and Q K^T (exact): wave w owns output row block w, 4 column
+  // blocks.  K K^T goes to LDS (for L); A = (Gamma_t / Gamma_i) q_t . k_i
+  // (i <= t) is formed in registers and written as (hi, lo) bf16 planes.
+  const long long wo = static_cast<long long>(cid) * kC;
 #pragma unroll
   for (int tj = 0; tj < 4; ++tj) {
     f32x4 a1 = f32x4{0.f, 0.f, 0.f, 0.f}, a2 = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -141,42 +164,103 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(
     for (int i = 0; i < 4; ++i) {
       const int t = 16 * wave + 4 * g4 + i, j = 16 * tj + r16;
       Gm[t * PG + j] = a1[i];
-      Qk[t * PG + j] = a2[i];
+      const float am = j <= t ? expf(cum[t] - cum[j]) * a2[i] : 0.f;
+      const uint16_t hv = f2bf(am);
+      Ag[wo * kC * 2 + t * kC + j] = hv;
+      Ag[wo * kC * 2 + kC * kC + t * kC + j] = f2bf(am - bf2f(hv));
     }
   }
   __syncthreads();
-  // ---- L (strictly lower) and A = M o Q K^T (lower incl. diagonal)
+  // ---- L (strictly lower)
   for (int e = threadIdx.x; e < kC * kC; e += 256) {
     const int t = e >> 6, i = e & 63;
-    const float l = i < t ? bet[t] * expf(prv[t] - cum[i]) * Gm[t * PG + i] : 0.f;
-    Gm[t * PG + i] = l;
-    const float am = i <= t ? expf(cum[t] - cum[i]) * Qk[t * PG + i] : 0.f;
-    Qk[t * PG + i] = am;
+    Gm[t * PG + i] = i < t ? bet[t] * expf(prv[t] - cum[i]) * Gm[t * PG + i] : 0.f;
   }
   __syncthreads();
-  // ---- (I + L)^{-1} by forward substitution; lane j of wave 0 owns column j
-  if (wave == 0) {
-    const int j = lane;
-    for (int t = 0; t < kC; ++t) {
-      float a0 = (t == j) ? 1.f : 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
-      int i = j;
-      for (; i + 3 < t; i += 4) {
-        a0 -= Gm[t * PG + i] * Ti[i * PG + j];
-        a1 -= Gm[t * PG + i + 1] * Ti[(i + 1) * PG + j];
-        a2 -= Gm[t * PG + i + 2] * Ti[(i + 2) * PG + j];
-        a3 -= Gm[t * PG + i + 3] * Ti[(i + 3) * PG + j];
+  // ---- (I + L)^{-1}, blocked by 16: N = I + L is unit lower triangular with
+  // 16 x 16 blocks N_ij; T = N^{-1} has T_ii = N_ii^{-1} and, for i > j,
+  // T_ij = -T_ii * sum_{m=j}^{i-1} N_im T_mj.  Wave w inverts diagonal block w
+  // by forward substitution (lanes 0..15 own its columns), then the three
+  // off-diagonal levels i - j = 1, 2, 3 are 16 x 16 products, one block per
+  // wave and level.
+  {
+    const int d0 = 16 * wave;
+    if (lane < 16) {
+      const int j = lane;
+      float x[16];
+#pragma unroll
+      for (int t = 0; t < 16; ++t) {
+        float a = (t == j) ? 1.f : 0.f;
+#pragma unroll
+        for (int i = 0; i < t; ++i) a -= Gm[(d0 + t) * PG + d0 + i] * x[i];
+        x[t] = t < j ? 0.f : a;
+        Ti[(d0 + t) * PG + d0 + j] = x[t];
       }
-      for (; i < t; ++i) a0 -= Gm[t * PG + i] * Ti[i * PG + j];
-      Ti[t * PG + j] = t < j ? 0.f : (a0 + a1) + (a2 + a3);
+    }
+    // upper blocks of T are zero
+    for (int e = threadIdx.x; e < kC * kC; e += 256) {
+      const int t = e >> 6, i = e & 63;
+      if ((i >> 4) > (t >> 4)) Ti[t * PG + i] = 0.f;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int lvl = 1; lvl < 4; ++lvl) {
+      const int bi = wave, bj = wave - lvl;  // block (bi, bj), bi - bj = lvl
+      float p[4];
+      if (bj >= 0) {
+        // lane l: rows r = 4 (l / 16) + 0..3 of P = sum_m N_{bi,m} T_{m,bj}, column c = l % 16
+        const int c = lane & 15, r0 = 4 * (lane >> 4);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) p[u] = 0.f;
+        for (int m = bj; m < bi; ++m) {
+#pragma unroll
+          for (int kk = 0; kk < 16; ++kk) {
+            const float tv = Ti[(16 * m + kk) * PG + 16 * bj + c];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) p[u] += Gm[(16 * bi + r0 + u) * PG + 16 * m + kk] * tv;
+          }
+        }
+      }
+      __syncthreads();
+      if (bj >= 0) {
+        const int c = lane & 15, r0 = 4 * (lane >> 4);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) Pm[(16 * wave + r0 + u) * 17 + c] = p[u];
+      }
+      __syncthreads();
+      if (bj >= 0) {
+        // T_{bi,bj} = -T_{bi,bi} P
+        const int c = lane & 15, r0 = 4 * (lane >> 4);
+        float o[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kk = 0; kk < 16; ++kk) {
+          const float pv = Pm[(16 * wave + kk) * 17 + c];
+#pragma unroll
+          for (int u = 0; u < 4; ++u) o[u] += Ti[(16 * bi + r0 + u) * PG + 16 * bi + kk] * pv;
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) Ti[(16 * bi + r0 + u) * PG + 16 * bj + c] = -o[u];
+      }
+      __syncthreads();
     }
   }
-  __syncthreads();
 
-  // ---- W = Ti diag(beta Gamma_prev) K  [64 x DK],  U0 = Ti diag(beta) V  [64 x DV]
-  const long long wo = static_cast<long long>(cid) * kC;
+  // ---- split the A operands once: TW = Ti diag(beta Gamma_prev), TU = Ti diag(beta)
+  for (int e = threadIdx.x; e < kC * kC; e += 256) {
+    const int t = e >> 6, i = e & 63;
+    const float tv = Ti[t * PG + i];
+    const float w = tv * wsc[i], u = tv * bet[i];
+    const uint16_t wh = f2bf(w), uh = f2bf(u);
+    TWh[t * PT + i] = wh;
+    TWl[t * PT + i] = f2bf(w - bf2f(wh));
+    TUh[t * PT + i] = uh;
+    TUl[t * PT + i] = f2bf(u - bf2f(uh));
+  }
+  __syncthreads();
+  // ---- W = TW K  [64 x DK] (stored as (hi, lo) bf16 planes),  U0 = TU V  [64 x DV] (fp32)
   {
-    constexpr int NT = 4 * (DK / 16) + 4 * (DV / 16);  // output tiles of both products
-    for (int tile = wave; tile < NT; tile += 4) {
+    constexpr int NTL = 4 * (DK / 16) + 4 * (DV / 16);  // output tiles of both products
+    for (int tile = wave; tile < NTL; tile += 4) {
       const bool isW = tile < 4 * (DK / 16);
       const int tt = isW ? tile : tile - 4 * (DK / 16);
       const int nd = isW ? DK / 16 : DV / 16;
@@ -184,154 +268,249 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(
       f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int s = 0; s < kC / 32; ++s) {
-        float av[8];
-        const int row = 16 * tm + r16;
-#pragma unroll
-        for (int jj = 0; jj < 8; ++jj) {
-          const int i = 32 * s + 8 * g4 + jj;
-          const float sc = isW ? wsc[i] : bet[i];
-          av[jj] = Ti[row * PG + i] * sc;
-        }
-        uint4 ahi, alo;
-        split8(av, ahi, alo);
-        const uint4 bb = isW ? gather8_bf16(Ks + (32 * s + 8 * g4) * PK + 16 * tn + r16, PK)
-                             : gather8_bf16(Vs + (32 * s + 8 * g4) * PV + 16 * tn + r16, PV);
+        const int ao = (16 * tm + r16) * PT + 32 * s + 8 * g4;
+        const uint4 ahi = *reinterpret_cast<const uint4*>((isW ? TWh : TUh) + ao);
+        const uint4 alo = *reinterpret_cast<const uint4*>((isW ? TWl : TUl) + ao);
+        const uint4 bb = *reinterpret_cast<const uint4*>(
+            (isW ? KsT : VsT) + (16 * tn + r16) * PT + 32 * s + 8 * g4);
         acc = mfma16(ahi, bb, acc);
         acc = mfma16(alo, bb, acc);
       }
-      float* dst = isW ? Wg + wo * DK : U0g + wo * DV;
-      const int ld = isW ? DK : DV;
+      if (isW) {
+        // W as a (hi, lo) pair of bf16 planes [2][64][DK]: W = hi + lo to ~2^-16
+        uint16_t* whi = Wg + wo * DK * 2;
+        uint16_t* wlo = whi + kC * DK;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) dst[(16 * tm + 4 * g4 + i) * ld + 16 * tn + r16] = acc[i];
+        for (int i = 0; i < 4; ++i) {
+          const int idx = (16 * tm + 4 * g4 + i) * DK + 16 * tn + r16;
+          const uint16_t hv = f2bf(acc[i]);
+          whi[idx] = hv;
+          wlo[idx] = f2bf(acc[i] - bf2f(hv));
+        }
+      } else {
+        float* dst = U0g + wo * DV;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dst[(16 * tm + 4 * g4 + i) * DV + 16 * tn + r16] = acc[i];
+      }
     }
   }
-  for (int e = threadIdx.x; e < kC * kC; e += 256)
-    Ag[wo * kC + e] = Qk[(e >> 6) * PG + (e & 63)];
   if (threadIdx.x < kC) cumg[wo + threadIdx.x] = cum[threadIdx.x];
 }
 
 // ---------------------------------------------------------------------------
-// Kernel 2: sequential scan over chunks for one (b, h, 32-column state slice).
-template <int DK, int DV>
-__global__ __launch_bounds__(256) void gdn_chunk_scan_kernel(
-    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
-    const float* __restrict__ Wg, const float* __restrict__ U0g, const float* __restrict__ Ag,
-    const float* __restrict__ cumg, float* __restrict__ state, uint16_t* __restrict__ out, int T,
-    int H, int NC) {
-  constexpr int DVS = 32;                 // state columns per workgroup
-  constexpr int NSL = DV / DVS;
-  constexpr int PK = DK + 8, PW = DK + 4, PS = DVS + 4, PG = kC + 1;
-  __shared__ __align__(16) float Ss[DK * PS];     // state slice [DK][DVS]
-  __shared__ __align__(16) float Us[kC * PS];     // U [64][DVS]
-  __shared__ __align__(16) float Ws[kC * PW];     // W [64][DK]
-  __shared__ __align__(16) uint16_t Qs[kC * PK];
-  __shared__ __align__(16) uint16_t Ks[kC * PK];
-  __shared__ float As[kC * PG];
-  __shared__ float cum[kC], ecum[kC], dec[kC];  // cum, Gamma_t, Gamma_C / Gamma_t
+// Kernel 2: sequential scan over chunks for one (b, h, DVS-column state
+// slice), 8 wavefronts.  Every fp32 operand enters the MFMA as a (hi, lo)
+// bf16 pair made once: W and A arrive split from kernel 1; the state slice
+// lives in the registers of the wave that owns each 16 x 16 tile and is
+// split into a transposed LDS copy after every update; U and Gamma_C/Gamma o U
+// are split once into transposed LDS tiles.  Per chunk:
+//   U = U0 - W S                       (one tile per wave)
+//   O = Gamma Q S + A U                (one tile per wave, bf16 out)
+//   S = Gamma_C S + K^T diag(Gamma_C / Gamma) U   (owner waves, registers)
+// The next chunk's operands (K, Q, W, A, U0, cumulative log-decays) are
+// fetched into registers at the start of a chunk and stored to LDS after it.
+// Workgroups are placed so the slices of one (b, h) share an XCD (block id
+// mod 8) and read the chunk operands through one L2.
+constexpr int kScanThreads = 512;
 
-  const int bh = blockIdx.x / NSL;
-  const int sl = blockIdx.x - bh * NSL;
+__device__ __forceinline__ uint32_t pack_bf2u(uint16_t a, uint16_t b) {
+  return static_cast<uint32_t>(a) | (static_cast<uint32_t>(b) << 16);
+}
+
+template <int DK, int DV, int DVS>
+__global__ __launch_bounds__(kScanThreads) void gdn_chunk_scan_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
+    const uint16_t* __restrict__ Wg, const float* __restrict__ U0g, const uint16_t* __restrict__ Ag,
+    const float* __restrict__ cumg, float* __restrict__ state, uint16_t* __restrict__ out, int T,
+    int H, int NC, int n_units) {
+  constexpr int NSL = DV / DVS;
+  constexpr int NTN = DVS / 16;                  // column tiles of U, O and S
+  constexpr int OT = (kC / 16) * NTN / 8;        // U / O tiles per wave
+  constexpr int SU = (DK / 16) * NTN / 8;        // state tiles per wave
+  constexpr int PB = DK + 8;                     // bf16 pitch of [*][DK] tiles
+  constexpr int PT = kC + 8;                     // bf16 pitch of [*][64] tiles
+  constexpr int NT = kScanThreads;
+  constexpr int KQ_N = kC * DK / 8 / NT;         // uint4 of K (and of Q) per thread
+  constexpr int W_N = 2 * kC * DK / 8 / NT;      // uint4 of W (hi and lo planes) per thread
+  constexpr int A_N = 2 * kC * kC / 8 / NT;      // uint4 of A (hi and lo planes) per thread
+  static_assert(OT >= 1 && SU >= 1 && KQ_N >= 1 && W_N >= 1 && A_N >= 1, "tile split");
+  __shared__ __align__(16) uint16_t Whi[kC * PB], Wlo[kC * PB], Qs[kC * PB];
+  __shared__ __align__(16) uint16_t Ahi[kC * PT], Alo[kC * PT];
+  __shared__ __align__(16) uint16_t KsT[DK * PT];                  // K^T [DK][64]
+  __shared__ __align__(16) uint16_t SThi[DVS * PB], STlo[DVS * PB];  // S^T [DVS][DK]
+  __shared__ __align__(16) uint16_t UThi[DVS * PT], UTlo[DVS * PT];  // U^T [DVS][64]
+  __shared__ __align__(16) uint16_t DThi[DVS * PT], DTlo[DVS * PT];  // (dec o U)^T
+  __shared__ float cum[kC], ecum[kC], dec[kC];
+
+  const int per_xcd = (gridDim.x + 7) / 8;
+  const int unit = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+  if (unit >= n_units) return;
+  const int bh = unit / NSL;
+  const int sl = unit - bh * NSL;
   const int b = bh / H, h = bh - (bh / H) * H;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r16 = lane & 15, g4 = lane >> 4;
   const long long rk = static_cast<long long>(H) * DK, rv = static_cast<long long>(H) * DV;
   float* Sg = state + (static_cast<long long>(bh) * DK) * DV + DVS * sl;
 
-  for (int e = threadIdx.x; e < DK * DVS; e += 256) {
-    const int d = e / DVS, cc = e - (e / DVS) * DVS;
-    Ss[d * PS + cc] = Sg[static_cast<long long>(d) * DV + cc];
+  // ---- the wave's state tiles in registers (D layout: row d = 16 tm + 4 g4 + i, col 16 tn + r16)
+  float sreg[SU][4];
+#pragma unroll
+  for (int u = 0; u < SU; ++u) {
+    const int st = SU * wave + u, tm = st / NTN, tn = st % NTN;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      sreg[u][i] = Sg[static_cast<long long>(16 * tm + 4 * g4 + i) * DV + 16 * tn + r16];
   }
+  // transposed (hi, lo) copy of the wave's state tiles: S^T[v][d], 4 consecutive d per lane
+#define GDN_SPLIT_STATE()                                                                      \
+  do {                                                                                         \
+    _Pragma("unroll") for (int u = 0; u < SU; ++u) {                                           \
+      const int st = SU * wave + u, tm = st / NTN, tn = st % NTN;                              \
+      uint16_t hh[4], ll[4];                                                                   \
+      _Pragma("unroll") for (int i = 0; i < 4; ++i) {                                          \
+        hh[i] = f2bf(sreg[u][i]);                                                              \
+        ll[i] = f2bf(sreg[u][i] - bf2f(hh[i]));                                                \
+      }                                                                                        \
+      const int off = (16 * tn + r16) * PB + 16 * tm + 4 * g4;                                 \
+      *reinterpret_cast<uint2*>(SThi + off) = uint2{pack_bf2u(hh[0], hh[1]), pack_bf2u(hh[2], hh[3])}; \
+      *reinterpret_cast<uint2*>(STlo + off) = uint2{pack_bf2u(ll[0], ll[1]), pack_bf2u(ll[2], ll[3])}; \
+    }                                                                                          \
+  } while (0)
+  GDN_SPLIT_STATE();
 
+  // ---- prefetch registers (native vectors, so they stay in VGPRs)
+  u32x4 pk[KQ_N], pq[KQ_N], pw[W_N], pa[A_N];
+  float pu_nxt[OT][4], pu[OT][4], pc;
+#define GDN_FETCH(c_)                                                                          \
+  do {                                                                                         \
+    const int ft0 = (c_) * kC;                                                                 \
+    const int fTc = min(kC, T - ft0);                                                          \
+    const long long fcid = static_cast<long long>(bh) * NC + (c_);                             \
+    const long long fkb = (static_cast<long long>(b) * T + ft0) * rk + static_cast<long long>(h) * DK; \
+    _Pragma("unroll") for (int i = 0; i < KQ_N; ++i) {                                         \
+      const int f = tid + NT * i;                                                              \
+      /* K: token fastest (conflict-free transposed stores); Q: row-major */                   \
+      const int tk = f % kC, ck = f / kC;                                                      \
+      const int tq = f / (DK / 8), cq = f % (DK / 8);                                          \
+      pk[i] = tk < fTc ? *reinterpret_cast<const u32x4*>(k + fkb + tk * rk + 8 * ck)           \
+                       : u32x4{0u, 0u, 0u, 0u};                                                \
+      pq[i] = tq < fTc ? *reinterpret_cast<const u32x4*>(q + fkb + tq * rk + 8 * cq)           \
+                       : u32x4{0u, 0u, 0u, 0u};                                                \
+    }                                                                                          \
+    _Pragma("unroll") for (int i = 0; i < W_N; ++i)                                            \
+      pw[i] = *reinterpret_cast<const u32x4*>(Wg + fcid * kC * DK * 2 + 8 * (tid + NT * i));   \
+    _Pragma("unroll") for (int i = 0; i < A_N; ++i)                                            \
+      pa[i] = *reinterpret_cast<const u32x4*>(Ag + fcid * kC * kC * 2 + 8 * (tid + NT * i));   \
+    _Pragma("unroll") for (int ot = 0; ot < OT; ++ot) {                                        \
+      const int tt = OT * wave + ot, tm = tt / NTN, tn = tt % NTN;                             \
+      _Pragma("unroll") for (int i = 0; i < 4; ++i)                                            \
+        pu_nxt[ot][i] = U0g[(fcid * kC + 16 * tm + 4 * g4 + i) * DV + DVS * sl + 16 * tn + r16]; \
+    }                                                                                          \
+    pc = tid < kC ? cumg[fcid * kC + tid] : 0.f;                                               \
+  } while (0)
+#define GDN_STASH()                                                                            \
+  do {                                                                                         \
+    _Pragma("unroll") for (int i = 0; i < KQ_N; ++i) {                                         \
+      const int f = tid + NT * i;                                                              \
+      const int tk = f % kC, ck = f / kC;                                                      \
+      const int tq = f / (DK / 8), cq = f % (DK / 8);                                          \
+      *reinterpret_cast<u32x4*>(Qs + tq * PB + 8 * cq) = pq[i];                                \
+      _Pragma("unroll") for (int jj = 0; jj < 8; ++jj)                                         \
+        KsT[(8 * ck + jj) * PT + tk] = static_cast<uint16_t>(pk[i][jj >> 1] >> (16 * (jj & 1))); \
+    }                                                                                          \
+    _Pragma("unroll") for (int i = 0; i < W_N; ++i) {                                          \
+      const int f = 8 * (tid + NT * i);                                                        \
+      const int pl = f / (kC * DK), rem = f % (kC * DK);                                       \
+      const int t = rem / DK, cc = rem % DK;                                                   \
+      *reinterpret_cast<u32x4*>((pl ? Wlo : Whi) + t * PB + cc) = pw[i];                       \
+    }                                                                                          \
+    _Pragma("unroll") for (int i = 0; i < A_N; ++i) {                                          \
+      const int f = 8 * (tid + NT * i);                                                        \
+      const int pl = f / (kC * kC), rem = f % (kC * kC);                                       \
+      const int t = rem / kC, cc = rem % kC;                                                   \
+      *reinterpret_cast<u32x4*>((pl ? Alo : Ahi) + t * PT + cc) = pa[i];                       \
+    }                                                                                          \
+    if (tid < kC) cum[tid] = pc;                                                               \
+  } while (0)
+
+  GDN_FETCH(0);
+  GDN_STASH();
+#pragma unroll
+  for (int ot = 0; ot < OT; ++ot)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) pu[ot][i] = pu_nxt[ot][i];
+  __syncthreads();
   for (int c = 0; c < NC; ++c) {
     const int t0 = c * kC;
     const int Tc = min(kC, T - t0);
-    const long long cid = static_cast<long long>(bh) * NC + c;
-    const long long kbase = (static_cast<long long>(b) * T + t0) * rk + static_cast<long long>(h) * DK;
-    __syncthreads();  // previous chunk finished with every LDS buffer
-    for (int f = threadIdx.x; f < kC * (DK / 8); f += 256) {
-      const int t = f / (DK / 8), cc = f - t * (DK / 8);
-      uint4 kv = uint4{0u, 0u, 0u, 0u}, qv = uint4{0u, 0u, 0u, 0u};
-      if (t < Tc) {
-        kv = *reinterpret_cast<const uint4*>(k + kbase + t * rk + 8 * cc);
-        qv = *reinterpret_cast<const uint4*>(q + kbase + t * rk + 8 * cc);
-      }
-      *reinterpret_cast<uint4*>(Ks + t * PK + 8 * cc) = kv;
-      *reinterpret_cast<uint4*>(Qs + t * PK + 8 * cc) = qv;
+    if (tid < kC) {
+      const float cv = cum[tid], cl_ = cum[kC - 1];
+      ecum[tid] = expf(cv);
+      dec[tid] = expf(cl_ - cv);
     }
-    for (int f = threadIdx.x; f < kC * (DK / 4); f += 256) {
-      const int t = f / (DK / 4), cc = f - t * (DK / 4);
-      *reinterpret_cast<float4*>(Ws + t * PW + 4 * cc) =
-          *reinterpret_cast<const float4*>(Wg + (cid * kC + t) * DK + 4 * cc);
-    }
-    for (int e = threadIdx.x; e < kC * kC; e += 256)
-      As[(e >> 6) * PG + (e & 63)] = Ag[cid * kC * kC + e];
-    if (threadIdx.x < kC) {
-      const float cv = cumg[cid * kC + threadIdx.x];
-      const float cl_ = cumg[cid * kC + kC - 1];
-      cum[threadIdx.x] = cv;
-      ecum[threadIdx.x] = expf(cv);
-      dec[threadIdx.x] = expf(cl_ - cv);
-    }
-    __syncthreads();
+    const float gc = expf(cum[kC - 1]);
+    if (c + 1 < NC) GDN_FETCH(c + 1);
+    __syncthreads();  // dec visible
 
-    // ---- U = U0 - W S   [64 x DVS]: 8 tiles of 16x16, 2 per wave
+    // ---- U = U0 - W S, split once into U^T and (dec o U)^T
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int tile = 2 * wave + u;
-      const int tm = tile >> 1, tn = tile & 1;
+    for (int ot = 0; ot < OT; ++ot) {
+      const int tt = OT * wave + ot, tm = tt / NTN, tn = tt % NTN;
       f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int s = 0; s < DK / 32; ++s) {
-        uint4 ahi, alo, bhi, blo;
-        split8(Ws + (16 * tm + r16) * PW + 32 * s + 8 * g4, ahi, alo);
-        float bv[8];
-#pragma unroll
-        for (int jj = 0; jj < 8; ++jj) bv[jj] = Ss[(32 * s + 8 * g4 + jj) * PS + 16 * tn + r16];
-        split8(bv, bhi, blo);
-        acc = mfma16(ahi, bhi, acc);
-        acc = mfma16(ahi, blo, acc);
-        acc = mfma16(alo, bhi, acc);
+        const int ao = (16 * tm + r16) * PB + 32 * s + 8 * g4;
+        const int bo = (16 * tn + r16) * PB + 32 * s + 8 * g4;
+        const uint4 ah = *reinterpret_cast<const uint4*>(Whi + ao);
+        const uint4 al = *reinterpret_cast<const uint4*>(Wlo + ao);
+        const uint4 bhv = *reinterpret_cast<const uint4*>(SThi + bo);
+        const uint4 blv = *reinterpret_cast<const uint4*>(STlo + bo);
+        acc = mfma16(ah, bhv, acc);
+        acc = mfma16(ah, blv, acc);
+        acc = mfma16(al, bhv, acc);
       }
+      uint16_t uh[4], ul[4], dh[4], dl[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int t = 16 * tm + 4 * g4 + i, cc = 16 * tn + r16;
-        Us[t * PS + cc] = U0g[(cid * kC + t) * DV + DVS * sl + cc] - acc[i];
+        const int t = 16 * tm + 4 * g4 + i;
+        const float uval = pu[ot][i] - acc[i];
+        uh[i] = f2bf(uval);
+        ul[i] = f2bf(uval - bf2f(uh[i]));
+        const float dv = dec[t] * uval;
+        dh[i] = f2bf(dv);
+        dl[i] = f2bf(dv - bf2f(dh[i]));
       }
+      const int off = (16 * tn + r16) * PT + 16 * tm + 4 * g4;
+      *reinterpret_cast<uint2*>(UThi + off) = uint2{pack_bf2u(uh[0], uh[1]), pack_bf2u(uh[2], uh[3])};
+      *reinterpret_cast<uint2*>(UTlo + off) = uint2{pack_bf2u(ul[0], ul[1]), pack_bf2u(ul[2], ul[3])};
+      *reinterpret_cast<uint2*>(DThi + off) = uint2{pack_bf2u(dh[0], dh[1]), pack_bf2u(dh[2], dh[3])};
+      *reinterpret_cast<uint2*>(DTlo + off) = uint2{pack_bf2u(dl[0], dl[1]), pack_bf2u(dl[2], dl[3])};
     }
-    __syncthreads();
+    __syncthreads();  // U^T, (dec o U)^T complete
 
-    // ---- O = Gamma (Q S) + A U  [64 x DVS]; and S' = Gamma_C S + K^T diag(Gamma_C/Gamma) U
-    const float cl = cum[kC - 1];
+    // ---- O = Gamma (Q S) + A U
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int tile = 2 * wave + u;
-      const int tm = tile >> 1, tn = tile & 1;
+    for (int ot = 0; ot < OT; ++ot) {
+      const int tt = OT * wave + ot, tm = tt / NTN, tn = tt % NTN;
       f32x4 qs = f32x4{0.f, 0.f, 0.f, 0.f}, au = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int s = 0; s < DK / 32; ++s) {
-        const uint4 qa = *reinterpret_cast<const uint4*>(Qs + (16 * tm + r16) * PK + 32 * s + 8 * g4);
-        float bv[8];
-#pragma unroll
-        for (int jj = 0; jj < 8; ++jj) bv[jj] = Ss[(32 * s + 8 * g4 + jj) * PS + 16 * tn + r16];
-        uint4 bhi, blo;
-        split8(bv, bhi, blo);
-        qs = mfma16(qa, bhi, qs);
-        qs = mfma16(qa, blo, qs);
+        const uint4 qa = *reinterpret_cast<const uint4*>(Qs + (16 * tm + r16) * PB + 32 * s + 8 * g4);
+        const int bo = (16 * tn + r16) * PB + 32 * s + 8 * g4;
+        qs = mfma16(qa, *reinterpret_cast<const uint4*>(SThi + bo), qs);
+        qs = mfma16(qa, *reinterpret_cast<const uint4*>(STlo + bo), qs);
       }
 #pragma unroll
       for (int s = 0; s < kC / 32; ++s) {
-        uint4 ahi, alo, bhi, blo;
-        float av[8], bv[8];
-#pragma unroll
-        for (int jj = 0; jj < 8; ++jj) {
-          av[jj] = As[(16 * tm + r16) * PG + 32 * s + 8 * g4 + jj];
-          bv[jj] = Us[(32 * s + 8 * g4 + jj) * PS + 16 * tn + r16];
-        }
-        split8(av, ahi, alo);
-        split8(bv, bhi, blo);
-        au = mfma16(ahi, bhi, au);
-        au = mfma16(ahi, blo, au);
-        au = mfma16(alo, bhi, au);
+        const int ao = (16 * tm + r16) * PT + 32 * s + 8 * g4;
+        const int bo = (16 * tn + r16) * PT + 32 * s + 8 * g4;
+        const uint4 ah = *reinterpret_cast<const uint4*>(Ahi + ao);
+        const uint4 al = *reinterpret_cast<const uint4*>(Alo + ao);
+        const uint4 bhv = *reinterpret_cast<const uint4*>(UThi + bo);
+        au = mfma16(ah, bhv, au);
+        au = mfma16(ah, *reinterpret_cast<const uint4*>(UTlo + bo), au);
+        au = mfma16(al, bhv, au);
       }
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -343,49 +522,42 @@ __global__ __launch_bounds__(256) void gdn_chunk_scan_kernel(
         }
       }
     }
-    // state update: [DK x DVS] = 16 tiles, 4 per wave; A = K^T (exact), B = diag(.) U (split)
-    f32x4 sacc[4];
-    float sold[4][4];
+    // ---- S = Gamma_C S + K^T (dec o U): the owner wave updates its tiles in registers
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int tile = 4 * wave + u;
-      const int tm = tile >> 1, tn = tile & 1;
+    for (int u = 0; u < SU; ++u) {
+      const int st = SU * wave + u, tm = st / NTN, tn = st % NTN;
       f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int s = 0; s < kC / 32; ++s) {
-        const uint4 ka = gather8_bf16(Ks + (32 * s + 8 * g4) * PK + 16 * tm + r16, PK);
-        float bv[8];
-#pragma unroll
-        for (int jj = 0; jj < 8; ++jj) {
-          const int t = 32 * s + 8 * g4 + jj;
-          bv[jj] = dec[t] * Us[t * PS + 16 * tn + r16];
-        }
-        uint4 bhi, blo;
-        split8(bv, bhi, blo);
-        acc = mfma16(ka, bhi, acc);
-        acc = mfma16(ka, blo, acc);
+        const uint4 ka = *reinterpret_cast<const uint4*>(KsT + (16 * tm + r16) * PT + 32 * s + 8 * g4);
+        const int bo = (16 * tn + r16) * PT + 32 * s + 8 * g4;
+        acc = mfma16(ka, *reinterpret_cast<const uint4*>(DThi + bo), acc);
+        acc = mfma16(ka, *reinterpret_cast<const uint4*>(DTlo + bo), acc);
       }
-      sacc[u] = acc;
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        sold[u][i] = Ss[(16 * tm + 4 * g4 + i) * PS + 16 * tn + r16];
+      for (int i = 0; i < 4; ++i) sreg[u][i] = gc * sreg[u][i] + acc[i];
     }
-    __syncthreads();  // every wave has read S for this chunk
-    const float gc = expf(cl);
+    __syncthreads();  // every wave is done with this chunk's LDS operands and S^T
+    GDN_SPLIT_STATE();
+    if (c + 1 < NC) {
+      GDN_STASH();
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int tile = 4 * wave + u;
-      const int tm = tile >> 1, tn = tile & 1;
+      for (int ot = 0; ot < OT; ++ot)
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        Ss[(16 * tm + 4 * g4 + i) * PS + 16 * tn + r16] = gc * sold[u][i] + sacc[u][i];
+        for (int i = 0; i < 4; ++i) pu[ot][i] = pu_nxt[ot][i];
     }
+    __syncthreads();
   }
-  __syncthreads();
-  for (int e = threadIdx.x; e < DK * DVS; e += 256) {
-    const int d = e / DVS, cc = e - (e / DVS) * DVS;
-    Sg[static_cast<long long>(d) * DV + cc] = Ss[d * PS + cc];
+#pragma unroll
+  for (int u = 0; u < SU; ++u) {
+    const int st = SU * wave + u, tm = st / NTN, tn = st % NTN;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      Sg[static_cast<long long>(16 * tm + 4 * g4 + i) * DV + 16 * tn + r16] = sreg[u][i];
   }
+#undef GDN_SPLIT_STATE
+#undef GDN_FETCH
+#undef GDN_STASH
 }
 
 }  // namespace llmy
@@ -415,25 +587,28 @@ extern "C" int32_t llmy_gdn_prefill_bf16(const llmy_bf16* q, const llmy_bf16* k,
   const int NC = (T + kC - 1) / kC;
   const long long chunks = static_cast<long long>(B) * H * NC;
   LLMY_REQUIRE(chunks < (1ll << 31));
-  float* W = static_cast<float*>(workspace);
-  float* U0 = W + chunks * kC * dk;
-  float* A = U0 + chunks * kC * dv;
-  float* cum = A + chunks * kC * kC;
+  // workspace: W as (hi, lo) bf16 planes, U0 fp32, A as (hi, lo) bf16 planes, cum fp32
+  uint16_t* W = static_cast<uint16_t*>(workspace);
+  float* U0 = reinterpret_cast<float*>(W + chunks * kC * dk * 2);
+  uint16_t* A = reinterpret_cast<uint16_t*>(U0 + chunks * kC * dv);
+  float* cum = reinterpret_cast<float*>(A + chunks * kC * kC * 2);
   const hipStream_t s = as_stream(stream);
   if (dk == 64) {
     hipLaunchKernelGGL((gdn_chunk_prep_kernel<64, 64>), dim3(static_cast<unsigned>(chunks)),
                        dim3(256), 0, s, q, k, v, beta, g, W, U0, A, cum, T, H, NC);
     int32_t st = launch_status();
     if (st != 0) return st;
-    hipLaunchKernelGGL((gdn_chunk_scan_kernel<64, 64>), dim3(B * H * (64 / 32)), dim3(256), 0, s,
-                       q, k, W, U0, A, cum, state, out, T, H, NC);
+    const int units = B * H * (64 / 32);
+    hipLaunchKernelGGL((gdn_chunk_scan_kernel<64, 64, 32>), dim3((units + 7) / 8 * 8),
+                       dim3(kScanThreads), 0, s, q, k, W, U0, A, cum, state, out, T, H, NC, units);
   } else {
     hipLaunchKernelGGL((gdn_chunk_prep_kernel<128, 128>), dim3(static_cast<unsigned>(chunks)),
                        dim3(256), 0, s, q, k, v, beta, g, W, U0, A, cum, T, H, NC);
     int32_t st = launch_status();
     if (st != 0) return st;
-    hipLaunchKernelGGL((gdn_chunk_scan_kernel<128, 128>), dim3(B * H * (128 / 32)), dim3(256), 0,
-                       s, q, k, W, U0, A, cum, state, out, T, H, NC);
+    const int units = B * H * (128 / 32);
+    hipLaunchKernelGGL((gdn_chunk_scan_kernel<128, 128, 32>), dim3((units + 7) / 8 * 8),
+                       dim3(kScanThreads), 0, s, q, k, W, U0, A, cum, state, out, T, H, NC, units);
   }
   return launch_status();
 }
