@@ -250,13 +250,15 @@ __global__ __launch_bounds__(1024) void moe_permute_kernel(
                 route_pos, cnt);
 }
 
-// Decode-time MoE front end, router part: one wavefront per token, four
-// tokens per 256-thread workgroup, W_r [E, D] staged in LDS per workgroup:
-//   h2[t]    = bf16(RMSNorm(x[t]) * ffn_w)                 (norms.py:13-16)
-//   logits   = (RMSNorm(h2[t]) * router_w) . W_r^T, fp32   (context_router.py:62,71-72)
-//   idx, gates: top-k (ties -> lower index) + softmax      (context_router.py:73-74)
-// The token rows are requested before the W_r staging loads so both are in
-// flight together; each lane holds NCH float4 chunks of its row.
+// Fused pre-MoE RMSNorm + router for decode (context_router.py:62,71-74;
+// moe.py:42-66): one workgroup per token, 4 wavefronts.  Every wave
+// normalises the token row itself with the arithmetic of rmsnorm_kernel (so
+// h2 equals llmy_rmsnorm_f32_bf16's output bit for bit; wave 0 stores it),
+// then wave w computes the logits of experts w, w+4, ... straight from W_r in
+// global memory: the W_r loads are issued before the norm, so their latency
+// overlaps it, and the lanes split D and meet in one wave reduction per
+// expert.  Wave 0 takes the top-k and the softmax from the logits in LDS.
+// E * D <= 24576 (at most 24 float4 of W_r per lane).
 template <int NCH>
 __global__ __launch_bounds__(256) void moe_route_norm_kernel(
     const float* __restrict__ x, const float* __restrict__ ffn_w,
@@ -264,44 +266,28 @@ __global__ __launch_bounds__(256) void moe_route_norm_kernel(
     uint16_t* __restrict__ h2, int32_t* __restrict__ idx_out, float* __restrict__ gates_out,
     int T, int E, int k, float eps) {
   constexpr int D = NCH * 256;
-  extern __shared__ float wr[];  // [E][D + 4] padded rows, then [4][D] normalised token rows
-  float* hs = wr + E * (D + 4);
+  constexpr int MAXE = 24 / NCH;  // experts per wave: E <= 4 * MAXE
+  __shared__ float lg[4 * MAXE];
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
-  const int t = blockIdx.x * 4 + wave;
-  const bool active = t < T;
-  // Every global operand of the wave is requested up front: the token row,
-  // both RMSNorm weight slices and (below) the W_r staging loads.
+  const int t = blockIdx.x;
   float4 v[NCH], fw[NCH], rw[NCH];
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
     const int d = 4 * lane + 256 * c;
-    v[c] = active ? *reinterpret_cast<const float4*>(x + static_cast<long long>(t) * D + d)
-                  : make_float4(0.f, 0.f, 0.f, 0.f);
+    v[c] = *reinterpret_cast<const float4*>(x + static_cast<long long>(t) * D + d);
     fw[c] = *reinterpret_cast<const float4*>(ffn_w + d);
     rw[c] = *reinterpret_cast<const float4*>(router_w + d);
   }
-  {
-    // E*D <= 24576 floats = at most 24 float4 per thread: all loads in flight at once.
-    const int n4 = (E * D) >> 2;
-    const int row4 = D >> 2;
-    float4 st[24];
+  float4 wq[MAXE][NCH];
 #pragma unroll
-    for (int q = 0; q < 24; ++q) {
-      const int i = min(static_cast<int>(threadIdx.x) + q * 256, n4 - 1);
-      st[q] = reinterpret_cast<const float4*>(w_router)[i];
-    }
+  for (int j = 0; j < MAXE; ++j) {
+    const int e = min(wave + 4 * j, E - 1);  // clamped: rows past E are loaded but unused
 #pragma unroll
-    for (int q = 0; q < 24; ++q) {
-      const int i = threadIdx.x + q * 256;
-      if (i < n4) {
-        const int e = i / row4;
-        reinterpret_cast<float4*>(wr + e * (D + 4))[i - e * row4] = st[q];
-      }
-    }
+    for (int c = 0; c < NCH; ++c)
+      wq[j][c] = *reinterpret_cast<const float4*>(w_router + static_cast<long long>(e) * D +
+                                                  4 * lane + 256 * c);
   }
-  __syncthreads();
-  if (!active) return;
 
   float ss = 0.f;
 #pragma unroll
@@ -315,7 +301,7 @@ __global__ __launch_bounds__(256) void moe_route_norm_kernel(
     const int d = 4 * lane + 256 * c;
     const uint32_t lo = pack_bf2(v[c].x * r1 * fw[c].x, v[c].y * r1 * fw[c].y);
     const uint32_t hi = pack_bf2(v[c].z * r1 * fw[c].z, v[c].w * r1 * fw[c].w);
-    *reinterpret_cast<uint2*>(hrow + d) = make_uint2(lo, hi);
+    if (wave == 0) *reinterpret_cast<uint2*>(hrow + d) = make_uint2(lo, hi);
     v[c].x = __uint_as_float(lo << 16);
     v[c].y = __uint_as_float(lo & 0xffff0000u);
     v[c].z = __uint_as_float(hi << 16);
@@ -330,70 +316,27 @@ __global__ __launch_bounds__(256) void moe_route_norm_kernel(
     v[c].z = (v[c].z * r2) * rw[c].z;
     v[c].w = (v[c].w * r2) * rw[c].w;
   }
-  // Logits: stage the normalised row in this wave's LDS slot, then lane
-  // (e, part) accumulates the dot product of expert e over D-part `part`
-  // (P = 64 / E parts, up to 4) straight from LDS — the W_r rows are padded by
-  // 4 floats so the lanes' 16-byte reads fall in distinct banks — and the
-  // parts meet in P - 1 shuffles.
-  float* hrow_l = hs + wave * D;
 #pragma unroll
-  for (int c = 0; c < NCH; ++c) *reinterpret_cast<float4*>(hrow_l + 4 * lane + 256 * c) = v[c];
-  __builtin_amdgcn_wave_barrier();
-  const int P = E <= 16 ? 4 : (E <= 32 ? 2 : 1);
-  const int e_l = lane / P;
-  const int part = lane - e_l * P;
-  const int span = D / P;
-  float acc = 0.f;
-  if (e_l < E) {
-    // span is a multiple of 64 (D >= 256, P <= 4): 8 float4 reads per step
-    // with four independent accumulators, so LDS reads and FMAs pipeline.
-    const float* we = wr + e_l * (D + 4) + part * span;
-    const float* hh = hrow_l + part * span;
-    float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
-    for (int d = 0; d < span; d += 32) {
-      float4 w4[8], h4[8];
+  for (int j = 0; j < MAXE; ++j) {
+    const int e = wave + 4 * j;
+    if (e < E) {
+      float a = 0.f;
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        w4[u] = *reinterpret_cast<const float4*>(we + d + 4 * u);
-        h4[u] = *reinterpret_cast<const float4*>(hh + d + 4 * u);
-      }
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        a0 = fmaf(h4[u].x, w4[u].x, a0);
-        a1 = fmaf(h4[u].y, w4[u].y, a1);
-        a2 = fmaf(h4[u].z, w4[u].z, a2);
-        a3 = fmaf(h4[u].w, w4[u].w, a3);
-      }
+      for (int c = 0; c < NCH; ++c)
+        a += (v[c].x * wq[j][c].x + v[c].y * wq[j][c].y) + (v[c].z * wq[j][c].z + v[c].w * wq[j][c].w);
+      a = wave_sum(a);
+      if (lane == 0) lg[e] = a;
     }
-    acc = (a0 + a1) + (a2 + a3);
   }
-  for (int off = 1; off < P; off <<= 1) acc += __shfl_xor(acc, off, kWave);
-  // logit e now sits in lane e*P; gather into the mine[] layout (lane e % 64, slot e / 64)
+  __syncthreads();
+  if (wave != 0) return;
   float mine[4] = {0.f, 0.f, 0.f, 0.f};
-  if (E <= 64) {
-    mine[0] = __shfl(acc, min(lane, E - 1) * P, kWave);
-  } else {
-    // E > 64: P == 1, lane e < 64 holds logit e; recompute slots 1..3 sequentially
-    mine[0] = acc;
-    for (int s2 = 1; s2 < 4; ++s2) {
-      const int e = lane + 64 * s2;
-      float a2 = 0.f;
-      if (e < E) {
-        const float* we = wr + e * (D + 4);
-        for (int d = 0; d < D; d += 4) {
-          const float4 w4 = *reinterpret_cast<const float4*>(we + d);
-          const float4 h4 = *reinterpret_cast<const float4*>(hrow_l + d);
-          a2 = fmaf(h4.x, w4.x, a2);
-          a2 = fmaf(h4.y, w4.y, a2);
-          a2 = fmaf(h4.z, w4.z, a2);
-          a2 = fmaf(h4.w, w4.w, a2);
-        }
-      }
-      mine[s2] = a2;
-    }
+#pragma unroll
+  for (int s2 = 0; s2 < 2; ++s2) {
+    const int e = lane + 64 * s2;
+    if (e < E) mine[s2] = lg[e];
   }
   topk_softmax_store(mine, E, k, lane, idx_out + t * k, gates_out + t * k);
-
 }
 
 }  // namespace llmy
@@ -456,9 +399,8 @@ extern "C" int32_t llmy_moe_route_decode(const float* x, const float* ffn_w, con
     LLMY_REQUIRE(!permute || (sorted_routes && route_pos));
     LLMY_REQUIRE(aligned(x, 16) && aligned(ffn_w, 16) && aligned(router_w, 16) &&
                  aligned(w_router, 16) && aligned(h2, 8));
-    const size_t lds = (static_cast<size_t>(E) * (D + 4) + 4 * static_cast<size_t>(D)) * sizeof(float);
 #define LLMY_ROUTE(NCH)                                                                       \
-  hipLaunchKernelGGL(moe_route_norm_kernel<NCH>, dim3((T + 3) / 4), dim3(256), lds, s, x,      \
+  hipLaunchKernelGGL(moe_route_norm_kernel<NCH>, dim3(T), dim3(256), 0, s, x,                    \
                      ffn_w, router_w, w_router, h2, idx, gates, T, E, k, eps)
     switch (D) {
       case 256: LLMY_ROUTE(1); break;
