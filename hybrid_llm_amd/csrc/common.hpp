@@ -2,8 +2,8 @@
 //
 // Storage conventions used by every kernel in this library:
 //   * bf16 tensors are passed as raw 16-bit words (uint16_t); conversion to
-//     fp32 is a 16-bit shift, conversion back is round-to-nearest-even with
-//     NaN kept quiet (the same rounding torch uses for .to(torch.bfloat16)).
+//     fp32 is a 16-bit shift, conversion back is round-to-nearest-even (the
+//     same rounding torch uses for .to(torch.bfloat16)).
 //   * every buffer is a plain contiguous device allocation owned by the
 //     caller; kernels never allocate.
 //   * wavefronts are 64 lanes wide.
@@ -25,15 +25,17 @@ __device__ __forceinline__ float bf2f(uint16_t v) {
   return __uint_as_float(static_cast<uint32_t>(v) << 16);
 }
 
+// fp32 -> bf16 with round-to-nearest-even (NaN stays NaN): one
+// v_cvt_pk_bf16_f32 on gfx950, the rounding torch applies in .to(bfloat16).
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
 __device__ __forceinline__ uint16_t f2bf(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return static_cast<uint16_t>(u >> 16);
+  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
 }
 
 __device__ __forceinline__ uint32_t pack_bf2(float a, float b) {
-  return static_cast<uint32_t>(f2bf(a)) | (static_cast<uint32_t>(f2bf(b)) << 16);
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, bf16x2_t));
 }
 
 // Unpack 8 bf16 held in a 16-byte vector into fp32.
