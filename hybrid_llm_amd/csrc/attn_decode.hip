@@ -107,13 +107,13 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
     for (int off = LPK; off < 64; off <<= 1) mloc = fmaxf(mloc, __shfl_xor(mloc, off, kWave));
     const float m_new = fmaxf(m_run, mloc);
     if (m_new == -INFINITY) continue;  // nothing valid yet in this wave (uniform)
-    const float alpha = exp2f(m_run - m_new);
+    const float alpha = exp2_fast(m_run - m_new);
     l_run *= alpha;
 #pragma unroll
     for (int j = 0; j < 8; ++j) o[j] *= alpha;
 #pragma unroll
     for (int i = 0; i < NIT; ++i) {
-      const float pi = exp2f(s[i] - m_new);  // 0 for masked keys
+      const float pi = exp2_fast(s[i] - m_new);  // 0 for masked keys
       l_run += pi;
       if (s[i] != -INFINITY) {
         float vf[8];
@@ -149,7 +149,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
     float num = 0.f, den = 0.f;
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
-      const float sc = exp2f(sm_m[w] - mstar);
+      const float sc = exp2_fast(sm_m[w] - mstar);
       num = fmaf(sm_o[w][d], sc, num);
       den = fmaf(sm_l[w], sc, den);
     }

@@ -93,6 +93,9 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const uint16_t* __res
   constexpr int CH = HD / 8;                     // 16-byte chunks per row
   constexpr int NCHK = (kBN * CH + 255) / 256;   // chunks per thread per tile
   uint4 kreg[NCHK], vreg[NCHK];
+  // K is fetched row-major (8 lanes per 128-byte row, 16-byte LDS stores);
+  // V is fetched key-fastest across lanes, so its transposed 2-byte LDS
+  // stores from one wave land at consecutive addresses.
   auto fetch = [&](int tile) {
     const int kt = tile * kBN;
 #pragma unroll
@@ -103,8 +106,10 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const uint16_t* __res
       const bool ok = f < kBN * CH && kk < T;
       kreg[u] = ok ? *reinterpret_cast<const uint4*>(k + base + kk * rs + 8 * c)
                    : uint4{0u, 0u, 0u, 0u};
-      vreg[u] = ok ? *reinterpret_cast<const uint4*>(v + base + kk * rs + 8 * c)
-                   : uint4{0u, 0u, 0u, 0u};
+      const int vkey = f % kBN, vc = f / kBN;
+      const bool vok = f < kBN * CH && kt + vkey < T;
+      vreg[u] = vok ? *reinterpret_cast<const uint4*>(v + base + (kt + vkey) * rs + 8 * vc)
+                    : uint4{0u, 0u, 0u, 0u};
     }
   };
   fetch(t_lo);
@@ -118,9 +123,11 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const uint16_t* __res
       if (f < kBN * CH) {
         const int key = f / CH, c = f - (f / CH) * CH;
         *reinterpret_cast<uint4*>(Ks + key * (HD + kKPad) + 8 * c) = kreg[u];
-        const uint16_t* ve = reinterpret_cast<const uint16_t*>(&vreg[u]);
+        const int vkey = f % kBN, vc = f / kBN;
+        const uint32_t w4[4] = {vreg[u].x, vreg[u].y, vreg[u].z, vreg[u].w};
 #pragma unroll
-        for (int e = 0; e < 8; ++e) Vt[(8 * c + e) * (kBN + kVPad) + key] = ve[e];
+        for (int e = 0; e < 8; ++e)
+          Vt[(8 * vc + e) * (kBN + kVPad) + vkey] = static_cast<uint16_t>(w4[e >> 1] >> (16 * (e & 1)));
       }
     }
     __syncthreads();
@@ -142,25 +149,32 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const uint16_t* __res
         s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(kf), as_bf16x8(qf[t]), s, 0, 0, 0);
       }
       // ---- mask + online softmax (log2 domain); register r holds key
-      //      ks + (r & 3) + 8 (r >> 2) + 4 half for query qi
+      //      kk = ks + (r & 3) + 8 (r >> 2) + 4 half for query qi, kept when
+      //      0 <= qi - kk < W: one unsigned compare of dq - c_r against W
+      //      (dq < 0 marks a query past T, which fails every compare).
+      const int dq = q_ok ? qi - ks - 4 * half : -(1 << 30);
+      // a sub-tile inside every window of the wave's 32 queries (all keys at
+      // or before the first query, within W of the last) needs no mask
+      const bool interior = ks + 31 <= qw && qw + 31 - ks < W && qw + 31 < T;
       float mloc = -INFINITY;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int kk = ks + (r & 3) + 8 * (r >> 2) + 4 * half;
-        const bool ok = q_ok && kk <= qi && qi - kk < W;
-        s[r] = ok ? s[r] * scale_log2 : -INFINITY;
+        const int cr = (r & 3) + 8 * (r >> 2);
+        const bool ok = interior || static_cast<unsigned>(dq - cr) < static_cast<unsigned>(W);
+        s[r] = ok ? s[r] : -INFINITY;
         mloc = fmaxf(mloc, s[r]);
       }
+      // scores stay unscaled; scale_log2 > 0 is applied inside the exponent
       mloc = fmaxf(mloc, __shfl_xor(mloc, 32, kWave));
       const float m_new = fmaxf(m_run, mloc);
-      const float m_use = m_new == -INFINITY ? 0.f : m_new;
-      const float alpha = exp2f(m_run - m_use);
+      const float m_sc = m_new == -INFINITY ? 0.f : m_new * scale_log2;
+      const float alpha = exp2_fast(fmaf(m_run, scale_log2, -m_sc));  // 0 while m_run = -inf
       m_run = m_new;
       float p[16];
       float psum = 0.f;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        p[r] = exp2f(s[r] - m_use);
+        p[r] = exp2_fast(fmaf(s[r], scale_log2, -m_sc));
         psum += p[r];
       }
       l_run = l_run * alpha + psum;

@@ -148,6 +148,12 @@ __device__ __forceinline__ uint32_t key_index(uint64_t key) {
   return ~static_cast<uint32_t>(key & 0xffffffffu);
 }
 
+// 2^x as the single v_exp_f32 instruction (exp2f adds a range rescale
+// around it for results below 2^-126).  Used for softmax weights, whose
+// exponents are <= 0: results under 2^-126 flush to zero, all others are
+// within about 1 ulp.  exp2(-inf) = 0.
+__device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }
 
 __device__ __forceinline__ float siluf_(float x) { return x / (1.0f + expf(-x)); }

@@ -102,7 +102,7 @@ struct NucRow {
 // Mass of a logit: trunc(2^47 * exp((x - max) / T)); the maximum itself (also
 // in a row of infinities) weighs exactly 2^47, NaN weighs 0.
 __device__ __forceinline__ u64 nuc_mass(float x, NucRow r) {
-  const float e = x == r.m ? 1.f : exp2f((x - r.m) * r.c);
+  const float e = x == r.m ? 1.f : exp2_fast((x - r.m) * r.c);
   return e > 0.f ? static_cast<u64>(e * kMassScale) : 0ull;
 }
 
