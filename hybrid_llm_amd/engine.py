@@ -135,6 +135,8 @@ class HybridDecoder:
         # Optional record of every MoE application's expert ids (verification
         # aid: lets a checker replay the kernel's discrete routing decisions).
         self.route_log: torch.Tensor | None = None
+        # The same for prefill: one [B*T, k] id tensor per MoE application.
+        self.route_log_seq: list | None = None
 
     def enable_route_log(self) -> None:
         n_apps = self.cfg.num_loops * self.cfg.n_layers
@@ -216,16 +218,22 @@ class HybridDecoder:
             self._moe(l, nxt)
         ops.linear(b["h"], w["lm_head"], out=b["logits"], epilogue=ops.EPI_STORE_F32,
                    layout=ops.LAYOUT_PACKED)
+        self._sample()
+        self.pos.add_(1)
+
+    def _sample(self) -> None:
+        """Greedy argmax into buf["next"], and the top-p draw into buf["sampled"]
+        when sampling is configured."""
         from . import _lib
+        b, V = self.buf, self.cfg.vocab
         stream = torch.cuda.current_stream().cuda_stream
-        _lib.call("llmy_sample_argmax_f32", b["logits"].data_ptr(), self.B, cfg.vocab,
+        _lib.call("llmy_sample_argmax_f32", b["logits"].data_ptr(), self.B, V,
                   b["next"].data_ptr(), stream)
         if self.sampling is not None:
             T, p, k = self.sampling
-            _lib.call("llmy_sample_top_p_f32", b["logits"].data_ptr(), self.B, cfg.vocab,
+            _lib.call("llmy_sample_top_p_f32", b["logits"].data_ptr(), self.B, V,
                       float(T), int(k), float(p), b["u"].data_ptr(), b["sampled"].data_ptr(),
                       stream)
-        self.pos.add_(1)
 
     def set_uniforms(self, u: torch.Tensor) -> None:
         """Per-row uniform draws in [0, 1) for the next steps' top-p sampling."""
@@ -255,6 +263,111 @@ class HybridDecoder:
         torch.cuda.current_stream().wait_stream(s)
         torch.cuda.synchronize()
         self.graph = g
+
+    # ------------------------------------------------------------------ prefill
+    def reset(self) -> None:
+        """Fresh sequences: zero every KV cache, GDN state and conv history, pos = 0
+        (llmy_state_reset, llmy_cuda/src/llmy.cpp:99-114)."""
+        for st in self.state.values():
+            for t in st.values():
+                t.zero_()
+        self.pos.zero_()
+
+    def prefill(self, tokens: torch.Tensor) -> torch.Tensor:
+        """Prefill B fresh sequences with a [B, T] prompt through the sequence
+        kernels and return the logits buffer [B, V] of the last position.
+
+        The reference prefills token by token through its decode step
+        (model_prefill, llmy_cuda/src/model.cpp:1955-1966); this runs every
+        block once over all B*T tokens: projections as GEMMs over B*T rows,
+        banded attention prefill (then the last min(T, W) K/V rows into the
+        ring caches), the chunked GDN scan from the zero state with the
+        sequence conv gate, and the MoE through router -> permutation ->
+        grouped expert GEMMs -> combine.  Afterwards the state is the one T
+        decode steps would leave, pos = T, ``buf["next"]`` holds the greedy
+        next token (and ``buf["sampled"]`` the draw when sampling is set), and
+        decoding continues with ``step``.  Intermediate buffers scale with
+        B*T and are allocated per call."""
+        cfg, w = self.cfg, self.w
+        tokens = tokens.to(device=self.dev, dtype=torch.int32)
+        if tokens.dim() != 2 or tokens.shape[0] != self.B or tokens.shape[1] < 1:
+            raise ValueError(f"tokens must be [B={self.B}, T>=1], got {tuple(tokens.shape)}")
+        B, T = tokens.shape
+        R, D = B * T, cfg.d_model
+        self.reset()
+        x = torch.empty(R, D, dtype=torch.float32, device=self.dev)
+        h = torch.empty(R, D, dtype=torch.bfloat16, device=self.dev)
+        ops.embed_norm(tokens.contiguous().view(-1), w["embed"], w["L0.mix_norm"], x, h, cfg.eps)
+        apps = [(loop, l) for loop in range(cfg.num_loops) for l in range(cfg.n_layers)]
+        for i, (loop, l) in enumerate(apps):
+            st = self.state[(loop, l)]
+            if cfg.layer_kinds[l] == "attn":
+                self._attn_seq(l, st, x, h, B, T)
+            else:
+                self._gdn_seq(l, st, x, h, B, T)
+            nxt = w[f"L{apps[i + 1][1]}.mix_norm"] if i + 1 < len(apps) else w["final_norm"]
+            self._moe_seq(l, x, h, nxt)
+        b = self.buf
+        b["h"].copy_(h.view(B, T, D)[:, -1])
+        ops.linear(b["h"], w["lm_head"], out=b["logits"], epilogue=ops.EPI_STORE_F32,
+                   layout=ops.LAYOUT_PACKED)
+        self._sample()
+        self.pos.fill_(T)
+        return b["logits"]
+
+    def _attn_seq(self, l: int, st: dict, x, h, B: int, T: int) -> None:
+        cfg, w = self.cfg, self.w
+        p = f"L{l}."
+        H, hd = cfg.attn_heads, cfg.attn_head_dim
+        Hhd, R = H * hd, B * T
+        # Rows [a, b) (multiples of 16) of a packed weight are themselves the
+        # packed [b - a, K] matrix, so q, k, v come from slices of wqkv.
+        wqkv = w[p + "wqkv"]
+        q, k, v = (ops.linear(h, wqkv[j * Hhd:(j + 1) * Hhd], layout=ops.LAYOUT_PACKED)
+                   for j in range(3))
+        o = ops.banded_attn_prefill(q.view(B, T, H, hd), k.view(B, T, H, hd),
+                                    v.view(B, T, H, hd), cfg.window, cfg.attn_scale)
+        ops.kv_cache_fill(k.view(B, T, Hhd), v.view(B, T, Hhd), st["k"], st["v"])
+        ops.linear(o.view(R, Hhd), w[p + "wo"], out=x, epilogue=ops.EPI_RESID_ADD,
+                   layout=ops.LAYOUT_PACKED)
+
+    def _gdn_seq(self, l: int, st: dict, x, h, B: int, T: int) -> None:
+        cfg, w = self.cfg, self.w
+        p = f"L{l}."
+        H, dk, dv = cfg.gdn_heads, cfg.gdn_dk, cfg.gdn_dv
+        R, HV = B * T, H * dv
+        proj = ops.linear(h, w[p + "wproj"], epilogue=ops.EPI_STORE_F32,
+                          layout=ops.LAYOUT_PACKED)
+        pp = ops.gdn_prefill_prep(proj, w[p + "bb"], w[p + "decay"], H, dk, dv)
+        o = ops.gdn_prefill(pp["q"].view(B, T, H, dk), pp["k"].view(B, T, H, dk),
+                            pp["v"].view(B, T, H, dv), pp["beta"].view(B, T, H),
+                            pp["g"].view(B, T, H), st["S"])
+        go = o.view(R, HV)
+        ops.gdn_gate(go, proj, 2 * H * dk + HV, out=go)
+        cg = ops.gdn_conv_gate_prefill(h.view(B, T, cfg.d_model), st["hist"], w[p + "conv"])
+        ops.linear(go, w[p + "wout"], out=x, epilogue=ops.EPI_RESID_GATED,
+                   aux=cg.view(R, cfg.d_model), layout=ops.LAYOUT_PACKED)
+
+    def _moe_seq(self, l: int, x, h, next_norm) -> None:
+        """Pre-MoE norm, router + top-k, stable permutation, grouped expert
+        GEMMs, then the combine fused with the next block's pre-norm into h."""
+        from . import _lib
+        cfg, w = self.cfg, self.w
+        p = f"L{l}."
+        R, D, E, k = x.shape[0], cfg.d_model, cfg.n_experts, cfg.top_k
+        dev, s = self.dev, torch.cuda.current_stream().cuda_stream
+        ops.rmsnorm(x, w[p + "ffn_norm"], cfg.eps, out=h)
+        idx = torch.empty(R, k, dtype=torch.int32, device=dev)
+        gates = torch.empty(R, k, dtype=torch.float32, device=dev)
+        _lib.call("llmy_router_topk_bf16", h.data_ptr(), w[p + "router_norm"].data_ptr(),
+                  w[p + "w_router"].data_ptr(), None, idx.data_ptr(), gates.data_ptr(), R, D, E,
+                  k, cfg.eps, s)
+        if self.route_log_seq is not None:
+            self.route_log_seq.append(idx.clone())
+        perm = ops.moe_permute(idx.view(-1), E)
+        _, y = ops.moe_experts(h, perm, gates, w[p + "w_gate_up"], w[p + "w_down"],
+                               layout=ops.LAYOUT_PACKED)
+        ops.moe_combine_norm(y, perm["route_pos"], x, h, next_norm, k, cfg.eps)
 
     # ------------------------------------------------------------------ state io
     def load_state(self, pos: torch.Tensor, state: dict) -> None:

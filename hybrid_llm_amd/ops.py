@@ -396,6 +396,68 @@ def gdn_conv_gate(h, hist, w, out=None) -> torch.Tensor:
     return out
 
 
+# --------------------------------------------------------------------------- prefill glue
+def kv_cache_fill(k, v, k_cache, v_cache) -> None:
+    """K/V rows [B, T, ld] bf16 (head h at columns h*hd..; rows may be strided
+    views of a fused qkv row) into ring caches [B, H, W, hd]: the last
+    min(T, W) positions, position t at slot t % W."""
+    B, H, W, hd = k_cache.shape
+    T = k.shape[1]
+    _check(k_cache, torch.bfloat16, "k_cache")
+    _check(v_cache, torch.bfloat16, "v_cache", (B, H, W, hd))
+    for name, t in (("k", k), ("v", v)):
+        if t.dtype != torch.bfloat16 or t.shape[:2] != (B, T) or t.shape[2] < H * hd \
+                or t.stride(-1) != 1 or t.stride(0) != T * t.stride(1) or not t.is_cuda:
+            raise ValueError(f"{name}: expected bf16 rows [B, T, >=H*hd] with a common row stride")
+    if k.stride(1) != v.stride(1):
+        raise ValueError("k and v must share a row stride")
+    _lib.call("llmy_kv_cache_fill_bf16", _ptr(k), _ptr(v), k.stride(1), _ptr(k_cache),
+              _ptr(v_cache), B, T, H, hd, W, _stream())
+
+
+def gdn_prefill_prep(proj, beta_bias, decay_logit, H, dk, dv, out=None):
+    """q, k (L2-normalised), v bf16 [R, H, d] and beta, g fp32 [R, H] from the
+    fused fp32 projection rows proj [R, ld]."""
+    R = proj.shape[0]
+    _check(proj, torch.float32, "proj")
+    dev = proj.device
+    if out is None:
+        out = {"q": torch.empty(R, H, dk, dtype=torch.bfloat16, device=dev),
+               "k": torch.empty(R, H, dk, dtype=torch.bfloat16, device=dev),
+               "v": torch.empty(R, H, dv, dtype=torch.bfloat16, device=dev),
+               "beta": torch.empty(R, H, dtype=torch.float32, device=dev),
+               "g": torch.empty(R, H, dtype=torch.float32, device=dev)}
+    _lib.call("llmy_gdn_prefill_prep_f32", _ptr(proj), proj.shape[1], _ptr(beta_bias),
+              _ptr(decay_logit), _ptr(out["q"]), _ptr(out["k"]), _ptr(out["v"]),
+              _ptr(out["beta"]), _ptr(out["g"]), R, H, dk, dv, _stream())
+    return out
+
+
+def gdn_gate(o, proj, gate_off, out=None) -> torch.Tensor:
+    """bf16(o * sigmoid(proj[:, gate_off : gate_off + HV])); o [R, HV] bf16."""
+    R, HV = o.shape
+    _check(o, torch.bfloat16, "o")
+    _check(proj, torch.float32, "proj")
+    if out is None:
+        out = torch.empty_like(o)
+    _lib.call("llmy_gdn_gate_bf16", _ptr(o), _ptr(proj), proj.shape[1], gate_off, _ptr(out), R,
+              HV, _stream())
+    return out
+
+
+def gdn_conv_gate_prefill(h, hist, w, out=None) -> torch.Tensor:
+    """Conv gate over a sequence: h [B, T, D] bf16, hist [B, K-1, D] updated."""
+    B, T, D = h.shape
+    _check(h, torch.bfloat16, "h")
+    _check(hist, torch.bfloat16, "hist", (B, w.shape[1] - 1, D))
+    _check(w, torch.float32, "w", (D, w.shape[1]))
+    if out is None:
+        out = torch.empty(B, T, D, dtype=torch.float32, device=h.device)
+    _lib.call("llmy_gdn_conv_gate_prefill", _ptr(h), _ptr(hist), _ptr(w), _ptr(out), B, T, D,
+              w.shape[1], _stream())
+    return out
+
+
 # --------------------------------------------------------------------------- glue
 def rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float = 1e-6, out=None) -> torch.Tensor:
     M, D = x.shape

@@ -212,6 +212,48 @@ int32_t llmy_gdn_conv_gate(const llmy_bf16* h, llmy_bf16* hist, const float* w,
                            float* out, int32_t B, int32_t D, int32_t kernel,
                            void* stream);
 
+/* --- Sequence prefill glue ------------------------------------------------
+ * The reference prefills token by token through its decode step
+ * (model_prefill, llmy_cuda/src/model.cpp:1955-1966, behind llmy_prefill,
+ * llmy_cuda/include/llmy.h:51-53).  These entries let a caller prefill a
+ * whole [B, T] prompt with the sequence kernels above instead. */
+
+/* K/V rows of a prompt (k, v [B*T rows, ld] bf16, head h at columns
+ * h*head_dim..) into the ring caches [B, H, W, head_dim] of
+ * llmy_banded_attn_decode_bf16: position t in [max(0, T-W), T) goes to slot
+ * t % W (the decode window of model/layers/hca.py:119-128). */
+int32_t llmy_kv_cache_fill_bf16(const llmy_bf16* k, const llmy_bf16* v, int64_t ld,
+                                llmy_bf16* k_cache, llmy_bf16* v_cache, int32_t B,
+                                int32_t T, int32_t H, int32_t head_dim, int32_t W,
+                                void* stream);
+
+/* Per-token GDN inputs for llmy_gdn_prefill_bf16 from the fused fp32
+ * projection rows of llmy_gdn_step_fused_f32 (proj [rows, ld]): q, k
+ * [rows, H, dk] bf16 L2-normalised (clamp 1e-12), v [rows, H, dv] bf16,
+ * beta = sigmoid(logit + beta_bias) and g = sigmoid(decay_logit[h]) as
+ * [rows, H] fp32 (gated_deltanet.py:124-132).  dk in {64, 128, 256}. */
+int32_t llmy_gdn_prefill_prep_f32(const float* proj, int64_t ld,
+                                  const float* beta_bias, const float* decay_logit,
+                                  llmy_bf16* q, llmy_bf16* k, llmy_bf16* v,
+                                  float* beta, float* g, int32_t rows, int32_t H,
+                                  int32_t dk, int32_t dv, void* stream);
+
+/* Output gate of a GDN scan (gated_deltanet.py:176,247):
+ * out[r, j] = bf16(o[r, j] * sigmoid(proj[r, gate_off + j])) for o
+ * [rows, HV] bf16 (may alias out) and fp32 gate logits read in place from
+ * proj [rows, ld].  HV % 8 == 0, ld and gate_off multiples of 4. */
+int32_t llmy_gdn_gate_bf16(const llmy_bf16* o, const float* proj, int64_t ld,
+                           int32_t gate_off, llmy_bf16* out, int32_t rows, int32_t HV,
+                           void* stream);
+
+/* Causal depthwise conv gate over a sequence with carried history
+ * (gated_deltanet.py:254-269): h [B,T,D] bf16, hist [B,K-1,D] bf16 (read,
+ * then set to the last K-1 entries of [hist, h]), w [D,K] fp32, out [B,T,D]
+ * fp32 = sigmoid(conv).  Equal to T calls of llmy_gdn_conv_gate.  kernel == 4. */
+int32_t llmy_gdn_conv_gate_prefill(const llmy_bf16* h, llmy_bf16* hist, const float* w,
+                                   float* out, int32_t B, int32_t T, int32_t D,
+                                   int32_t kernel, void* stream);
+
 /* --- Glue (model/layers/norms.py:13-16, model/model.py:386) --------------- */
 
 /* out[m] = bf16(x[m] * rsqrt(mean(x[m]^2) + eps) * w); x [M,D] fp32. */

@@ -103,3 +103,26 @@ def test_reference_op_hooks_reject_bad_arguments(lib):
     assert sk(None, FAKE, 4, 20, None) == INVALID
     assert sk(FAKE, FAKE, 0, 20, None) == INVALID
     assert sk(FAKE, FAKE, 4, -1, None) == INVALID
+
+
+def test_prefill_glue_rejects_bad_arguments(lib):
+    fill = lib.llmy_kv_cache_fill_bf16
+    assert fill(FAKE, FAKE, 256, FAKE, FAKE, 2, 10, 4, 64, 0, None) == INVALID     # W = 0
+    assert fill(FAKE, FAKE, 255, FAKE, FAKE, 2, 10, 4, 64, 8, None) == INVALID     # ld < H*hd
+    assert fill(FAKE, FAKE, 256, FAKE, FAKE, 2, 10, 4, 60, 8, None) == INVALID     # hd % 8
+    assert fill(None, FAKE, 256, FAKE, FAKE, 2, 10, 4, 64, 8, None) == INVALID
+    assert fill(None, None, 256, None, None, 2, 0, 4, 64, 8, None) == 0            # T = 0
+    prep = lib.llmy_gdn_prefill_prep_f32
+    ptrs = [FAKE] * 7
+    assert prep(FAKE, 800, *ptrs, 4, 2, 96, 64, None) == INVALID                   # dk
+    assert prep(FAKE, 100, *ptrs, 4, 2, 64, 64, None) == INVALID                   # ld too small
+    assert prep(None, 800, *ptrs, 4, 2, 64, 64, None) == INVALID
+    assert prep(None, 800, *([None] * 7), 0, 2, 64, 64, None) == 0
+    gate = lib.llmy_gdn_gate_bf16
+    assert gate(FAKE, FAKE, 512, 256, FAKE, 4, 100, None) == INVALID              # HV % 8
+    assert gate(FAKE, FAKE, 300, 256, FAKE, 4, 128, None) == INVALID              # ld < off+HV
+    assert gate(FAKE, FAKE, 512, 2, FAKE, 4, 128, None) == INVALID                # off % 4
+    conv = lib.llmy_gdn_conv_gate_prefill
+    assert conv(FAKE, FAKE, FAKE, FAKE, 2, 10, 256, 3, None) == INVALID           # kernel != 4
+    assert conv(None, FAKE, FAKE, FAKE, 2, 10, 256, 4, None) == INVALID
+    assert conv(None, None, None, None, 2, 0, 256, 4, None) == 0
