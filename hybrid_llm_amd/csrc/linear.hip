@@ -403,6 +403,14 @@ int32_t moe_gemm_prefill(const uint16_t* x, const int32_t* offsets, const int32_
                          const float* gates, const uint16_t* w_gate_up, const uint16_t* w_down,
                          uint16_t* act, float* y, int T, int D, int H, int E, int k, bool packed,
                          hipStream_t s);
+// The same tiles as a dense GEMM with the epilogues above (moe_gemm.hip).
+int32_t dense_gemm_mfma(const uint16_t* x, const uint16_t* w, void* out, const float* aux,
+                        int M, int N, int K, int epi, bool packed, hipStream_t s);
+
+// Rows from which the dense projections switch from the weight-streaming
+// kernel (every weight byte read once per 64 rows, HBM-bound) to the MFMA
+// tiles (compute-bound); decode batches stay below it.
+constexpr int kDenseMfmaMinRows = 256;
 
 }  // namespace llmy
 
@@ -435,6 +443,8 @@ extern "C" int32_t llmy_linear_bf16(const llmy_bf16* x, const llmy_bf16* w, void
   a.M = M; a.N = N; a.K = K; a.ldx = K; a.ldo = N; a.route_k = 1;
   const hipStream_t s = as_stream(stream);
   const bool packed = weight_layout == 1;
+  if (M >= kDenseMfmaMinRows && aligned(out, 16))
+    return dense_gemm_mfma(x, w, out, aux, M, N, K, epilogue, packed, s);
   // Large N with packed weights: the LDS-tiled kernel (enough workgroups
   // without splitting K, and 4x less activation traffic).
   if (packed && M <= 64 && N >= 8192) {

@@ -28,6 +28,12 @@
 // m fastest, and each XCD (block id mod 8) takes a contiguous range of them,
 // so the m-tiles that share a weight tile, and the n-tiles that share an
 // expert's token rows, run back to back in the same XCD's L2.
+//
+// The same tiles serve the dense projections of a sequence prefill
+// (llmy_linear_bf16 with many rows): MODE 2 is one "expert" owning all M
+// rows, BN = 128, an N tail (rows past N re-read row N-1, their columns are
+// not stored) and the linear epilogues (bf16 / fp32 store, fp32 residual
+// add, gated residual add).
 #include "common.hpp"
 #include "abi_util.hpp"
 
@@ -55,6 +61,10 @@ struct MoeGemmArgs {
   int K, ldo, E, route_k, rows_total, x_rows;
   int n_tiles;  // output column tiles per expert
   int packed;
+  // dense (MODE 2) only
+  const float* aux;  // gated residual: out += acc * aux[m * ldo + n]
+  int N;             // output columns (the last n-tile may be partial)
+  int m_tiles;
 };
 
 // Packed operand order of llmy_pack_weights_bf16 (see linear.hip): the 8
@@ -107,8 +117,12 @@ __device__ __forceinline__ f32x16 mfma32(const u32x4& a, const u32x4& b, const f
 
 }  // namespace
 
-// MODE 0: gate_up + SwiGLU (BN = 256); MODE 1: down + gate scale (BN = 128).
-template <int MODE>
+// Dense epilogues (values of the linear entry's epilogue argument).
+enum DenseEpi : int { kDenseBf16 = 0, kDenseF32 = 1, kDenseResid = 2, kDenseGated = 3 };
+
+// MODE 0: gate_up + SwiGLU (BN = 256); MODE 1: down + gate scale (BN = 128);
+// MODE 2: dense with epilogue EPI (BN = 128).
+template <int MODE, int EPI = 0>
 __global__ __launch_bounds__(kGemmThreads) void moe_gemm_kernel(MoeGemmArgs a) {
   constexpr int BN = MODE == 0 ? 256 : 128;
   constexpr int CT = BN / 128;       // 32-column MFMA blocks per wavefront (2 x 4 wave grid)
@@ -117,8 +131,19 @@ __global__ __launch_bounds__(kGemmThreads) void moe_gemm_kernel(MoeGemmArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave & 1, wn = wave >> 1;  // rows 64 wm .., columns (BN/4) wn ..
 
-  // ---- which tile: wave 0 scans the experts' m-tile counts
-  if (wave == 0) {
+  // ---- which tile.  Dense: work item w = (n-tile, m-tile), m fastest.
+  // Grouped: wave 0 scans the experts' m-tile counts.
+  if (MODE == 2) {
+    if (tid == 0) {
+      const int nblk = gridDim.x;
+      const int per_xcd = (nblk + kNumXcd - 1) / kNumXcd;
+      const int w = (blockIdx.x % kNumXcd) * per_xcd + blockIdx.x / kNumXcd;
+      const bool ok = w < a.m_tiles * a.n_tiles;
+      s_work[0] = ok ? 0 : -1;
+      s_work[1] = ok ? (w % a.m_tiles) * kBM : 0;
+      s_work[2] = ok ? w / a.m_tiles : 0;
+    }
+  } else if (wave == 0) {
     const int nblk = gridDim.x;
     const int per_xcd = (nblk + kNumXcd - 1) / kNumXcd;
     const int w = (blockIdx.x % kNumXcd) * per_xcd + blockIdx.x / kNumXcd;
@@ -163,8 +188,9 @@ __global__ __launch_bounds__(kGemmThreads) void moe_gemm_kernel(MoeGemmArgs a) {
   const int e = s_work[0];
   if (e < 0) return;
   const int m0 = s_work[1], ntile = s_work[2];
-  const int row_lo = min(max(a.offsets[e], 0), a.rows_total);
-  const int rows_e = min(max(a.offsets[e + 1], row_lo), a.rows_total) - row_lo;
+  const int row_lo = MODE == 2 ? 0 : min(max(a.offsets[e], 0), a.rows_total);
+  const int rows_e =
+      MODE == 2 ? a.rows_total : min(max(a.offsets[e + 1], row_lo), a.rows_total) - row_lo;
   const int K = a.K;
   const int nk = K / kBK;
 
@@ -212,8 +238,10 @@ __global__ __launch_bounds__(kGemmThreads) void moe_gemm_kernel(MoeGemmArgs a) {
       // wavefront column quarter wn gets 32 gate rows and their 32 up rows
       n = 128 * ntile + 32 * (r >> 6) + (r & 31);
       if ((r >> 5) & 1) off = a.up_offset;
-    } else {
+    } else if (MODE == 1) {
       n = BN * ntile + r;
+    } else {
+      n = min(BN * ntile + r, a.N - 1);  // N tail: repeat the last row
     }
     const int ch = dma_chunk(B_INS * wave + q);
     b_src[q] = off + (packed ? packed_at(n, 8 * ch, K) : static_cast<long long>(n) * K + 8 * ch);
@@ -308,6 +336,20 @@ __global__ __launch_bounds__(kGemmThreads) void moe_gemm_kernel(MoeGemmArgs a) {
         uint16_t* act = static_cast<uint16_t*>(a.out) + p * a.ldo;
         const float g = acc[i][0][r], u = acc[i][1][r];
         act[128 * ntile + 32 * wn + (lane & 31)] = f2bf(siluf_(g) * u);
+      } else if (MODE == 2) {
+        const int n = BN * ntile + 32 * wn + (lane & 31);
+        if (n >= a.N) continue;
+        const long long o = p * a.ldo + n;
+        const float v = acc[i][0][r];
+        if (EPI == kDenseBf16) {
+          static_cast<uint16_t*>(a.out)[o] = f2bf(v);
+        } else if (EPI == kDenseF32) {
+          static_cast<float*>(a.out)[o] = v;
+        } else if (EPI == kDenseResid) {
+          static_cast<float*>(a.out)[o] += v;
+        } else {
+          static_cast<float*>(a.out)[o] += v * a.aux[o];
+        }
       } else {
         const int route = min(max(a.sorted_routes[p], 0), a.rows_total - 1);
         const float gs = a.gates[route];
@@ -364,6 +406,39 @@ int32_t moe_gemm_prefill(const uint16_t* x, const int32_t* offsets, const int32_
   blocks = (blocks + kNumXcd - 1) / kNumXcd * kNumXcd;
   hipLaunchKernelGGL(moe_gemm_kernel<1>, dim3(static_cast<unsigned>(blocks)), dim3(kGemmThreads),
                      0, s, d);
+  return launch_status();
+}
+
+// Dense out[M, N] (epilogue epi) = x[M, K] . w[N, K]^T on the same tiles.
+// Validated by the caller: M >= 1, N >= 1, K % 256 == 0, 16-byte aligned
+// x and w, aux given for the gated epilogue.
+int32_t dense_gemm_mfma(const uint16_t* x, const uint16_t* w, void* out, const float* aux,
+                        int M, int N, int K, int epi, bool packed, hipStream_t s) {
+  MoeGemmArgs g{};
+  g.x = x;
+  g.w = w;
+  g.out = out;
+  g.aux = aux;
+  g.K = K;
+  g.ldo = N;
+  g.E = 1;
+  g.route_k = 1;
+  g.rows_total = M;
+  g.x_rows = M;
+  g.N = N;
+  g.n_tiles = (N + 127) / 128;
+  g.m_tiles = (M + kBM - 1) / kBM;
+  g.packed = packed;
+  long long blocks = static_cast<long long>(g.m_tiles) * g.n_tiles;
+  if (blocks >= (1ll << 31) - kNumXcd) return static_cast<int32_t>(hipErrorInvalidValue);
+  blocks = (blocks + kNumXcd - 1) / kNumXcd * kNumXcd;
+  const dim3 grid(static_cast<unsigned>(blocks)), block(kGemmThreads);
+  switch (epi) {
+    case kDenseBf16: hipLaunchKernelGGL((moe_gemm_kernel<2, kDenseBf16>), grid, block, 0, s, g); break;
+    case kDenseF32: hipLaunchKernelGGL((moe_gemm_kernel<2, kDenseF32>), grid, block, 0, s, g); break;
+    case kDenseResid: hipLaunchKernelGGL((moe_gemm_kernel<2, kDenseResid>), grid, block, 0, s, g); break;
+    default: hipLaunchKernelGGL((moe_gemm_kernel<2, kDenseGated>), grid, block, 0, s, g); break;
+  }
   return launch_status();
 }
 

@@ -66,15 +66,17 @@ int32_t llmy_moe_permute(const int32_t* expert_ids, int32_t n_routes,
                          int32_t* sorted_routes, int32_t* route_pos,
                          void* stream);
 
-/* --- Dense projections (weight-streaming GEMM, decode path) --------------- */
+/* --- Dense projections ---------------------------------------------------- */
 
 /* Y[M,N] = X[M,K] . W[N,K]^T, bf16 operands, fp32 accumulation, with a fused
  * epilogue: 0 = store bf16 into out [M,N]; 1 = store fp32; 2 = out (fp32)
  * += Y (residual add); 3 = out (fp32) += Y * aux[M,N] (gated residual).
  * weight_layout 0: W row-major [N,K] (nn.Linear); 1: W in the packed tile
  * order of llmy_pack_weights_bf16.  Limits: N % 16 == 0, K % 256 == 0.
+ * M < 256 (decode batches): weight-streaming kernels; M >= 256 (prefill
+ * sequences) with a 16-byte aligned out: MFMA tiles (128 x 128 per workgroup).
  * Replaces linear_forward / k_linear_gemv (llmy_cuda/src/model.cpp:1467-1515)
- * and nn.Linear on the decode path. */
+ * and nn.Linear on the decode and prefill paths. */
 int32_t llmy_linear_bf16(const llmy_bf16* x, const llmy_bf16* w, void* out,
                          const float* aux, int32_t M, int32_t N, int32_t K,
                          int32_t epilogue, int32_t weight_layout, void* stream);

@@ -41,7 +41,10 @@ def _bf(t):
 # ---------------------------------------------------------------- linear
 @pytest.mark.parametrize("M,N,K", [(64, 3072, 1024), (64, 1024, 1024), (1, 4112, 1024),
                                    (5, 32000, 1024), (64, 1040, 256), (130, 512, 512),
-                                   (17, 16, 2048)])
+                                   (17, 16, 2048),
+                                   # M >= 256: MFMA tiles, incl. partial m/n tiles
+                                   (256, 1024, 1024), (300, 4112, 1024), (1000, 1040, 256),
+                                   (257, 16, 512), (4096, 1024, 1024)])
 @pytest.mark.parametrize("epi", [0, 1, 2, 3])
 @pytest.mark.parametrize("layout", [0, 1])
 def test_linear_epilogues(M, N, K, epi, layout):
