@@ -443,7 +443,8 @@ extern "C" int32_t llmy_linear_bf16(const llmy_bf16* x, const llmy_bf16* w, void
   a.M = M; a.N = N; a.K = K; a.ldx = K; a.ldo = N; a.route_k = 1;
   const hipStream_t s = as_stream(stream);
   const bool packed = weight_layout == 1;
-  if (M >= kDenseMfmaMinRows && aligned(out, 16))
+  if (M >= kDenseMfmaMinRows && aligned(out, 16) && (aux == nullptr || aligned(aux, 16)) &&
+      2ll * M * K < (1ll << 31) && 2ll * N * K < (1ll << 31))
     return dense_gemm_mfma(x, w, out, aux, M, N, K, epilogue, packed, s);
   // Large N with packed weights: the LDS-tiled kernel (enough workgroups
   // without splitting K, and 4x less activation traffic).
@@ -492,7 +493,10 @@ extern "C" int32_t llmy_moe_experts_bf16(const llmy_bf16* x, const int32_t* offs
   // point uses the same configurations, so at these sizes the two agree bit
   // for bit.)
   int32_t st;
-  if (T * k <= 16 * E) {
+  // The tiled path addresses each operand block with 32-bit byte offsets.
+  const bool tiled_fits = 2ll * T * D < (1ll << 31) && 2ll * T * k * H < (1ll << 31) &&
+                          4ll * H * D < (1ll << 31);
+  if (T * k <= 16 * E || !tiled_fits) {
     st = launch_ws<kSwiGLU, kMoeGather, 1>(a, E, packed, s);
     if (st != 0) return st;
     return launch_ws<kMoeDown, kMoeDirect, 1, 2>(b, E, packed, s);
@@ -541,7 +545,10 @@ extern "C" int32_t llmy_moe_experts_routed_bf16(const llmy_bf16* x, const int32_
   b.N = D; b.K = H; b.ldx = H; b.ldo = D; b.route_k = k;
   b.rows_total = T * k; b.x_rows = T * k;
   int32_t st;
-  if (T * k <= 16 * E) {
+  // The tiled path addresses each operand block with 32-bit byte offsets.
+  const bool tiled_fits = 2ll * T * D < (1ll << 31) && 2ll * T * k * H < (1ll << 31) &&
+                          4ll * H * D < (1ll << 31);
+  if (T * k <= 16 * E || !tiled_fits) {
     st = launch_ws<kSwiGLU, kRouteGather, 1>(a, E, packed, s);
     if (st != 0) return st;
     return launch_ws<kMoeDown, kRouteDirect, 1, 2>(b, E, packed, s);

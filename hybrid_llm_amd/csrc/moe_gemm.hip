@@ -1,71 +1,77 @@
-// Grouped expert GEMMs for MoE prefill on bf16 MFMA (gfx950).
+// Tiled bf16 MFMA GEMMs on gfx950: the grouped expert GEMMs of MoE prefill
+// and the dense projections of a sequence prefill.
 //
-// Math (model/layers/moe.py:72-76, expert.py:14-15), per expert e over its
-// routes in permuted order p = offsets[e] .. offsets[e+1]-1:
+// Math of the grouped GEMMs (model/layers/moe.py:72-76, expert.py:14-15), per
+// expert e over its routes in permuted order p = offsets[e] .. offsets[e+1]-1:
 //   act[p, :] = silu(x[t_p] . W_gate[e]^T) * (x[t_p] . W_up[e]^T)   (bf16 out)
 //   y[p, :]   = gate[r_p] * (act[p] . W_down[e]^T)                  (fp32 out)
 // with r_p = sorted_routes[p] and t_p = r_p / k: the same contract, layouts
 // and rounding points as the weight-streaming path of llmy_moe_experts_bf16.
+// The dense mode (llmy_linear_bf16 with many rows) is one "expert" owning
+// all M rows, with an N tail (rows past N re-read row N-1, their columns are
+// not stored) and the linear epilogues.
 //
-// Tiling: a workgroup of 8 wavefronts (2 per SIMD) computes a BM x BN tile
-// (BM = 128 routes of one expert; BN = 256 for gate_up, BN = 128 for down).
-// The gate_up tile's weight rows are [32 gate | 32 up] per wavefront column,
-// so every gate accumulator sits in the same lanes as its up partner and
-// SwiGLU is applied in registers.  Wavefront (wm, wn) of the 2 x 4 grid owns
-// rows 64 wm .. 64 wm + 63 and columns (BN/4) wn .. as 2 x (BN/128) blocks of
-// v_mfma_f32_32x32x16_bf16.
+// Tiling: a workgroup of 4 wavefronts computes a BM x BN tile of the A rows
+// times the B (weight) rows; wavefront (wm, wn) of the 2 x 2 grid owns a
+// (BM/2) x (BN/2) sub-tile as (BM/64) x (BN/64) blocks of
+// v_mfma_f32_32x32x16_bf16, so LDS traffic is (BM/64 + BN/64) fragment reads
+// per (BM/64)(BN/64) MFMAs.  256 x 256 tiles run one workgroup per CU (the
+// accumulators fill the AGPR half of the register file); 128-row tiles run
+// two per CU, one wavefront of each per SIMD, so one workgroup's barrier and
+// load waits are covered by the other's MFMAs.  The MFMA takes the weight
+// fragment as its first operand, so each lane ends with four consecutive
+// output columns per register group and stores them as one vector.  The
+// gate_up tile's B rows are [gate | up] halves per wavefront column, so every
+// gate accumulator sits in the same lanes as its up partner and SwiGLU is
+// applied in registers.
 //
-// K advances 64 at a time through two LDS stages filled by
-// global_load_lds_dwordx4 (global memory straight into LDS, no staging
-// registers): while one K tile is multiplied, the next is in flight.  Tile
-// rows are 128 bytes with an XOR swizzle of their 16-byte chunks, so each DMA
-// instruction reads 8 whole global rows and each MFMA fragment read (inline
-// asm ds_read_b128, see lds_frag) is conflict-free.  Per K tile a wavefront
-// waits for its own loads (s_waitcnt vmcnt), the workgroup meets at one
-// barrier, the next tile is issued, then the tile is multiplied.
+// K advances BK (32 or 64) at a time through a ring of NS LDS stages filled
+// by global_load_lds_dwordx4 (global memory straight into LDS) from scalar
+// base addresses plus 32-bit lane offsets: while one K tile is multiplied,
+// the next NS-1 are in flight.  Tile rows hold BK k with an XOR swizzle of
+// their 16-byte chunks, so each DMA instruction reads whole global row
+// segments and each fragment read (inline-asm ds_read_b128, see lds_frag) is
+// conflict-free.  The loop is a software pipeline with scheduling fences:
+// the fragment reads of k-step s+1 are in flight during the MFMAs of step s,
+// and the first reads of tile kt+1 during the last MFMAs of tile kt.
 //
 // Work order: work items (expert, n-tile, m-tile) are numbered expert-major,
 // m fastest, and each XCD (block id mod 8) takes a contiguous range of them,
 // so the m-tiles that share a weight tile, and the n-tiles that share an
-// expert's token rows, run back to back in the same XCD's L2.
-//
-// The same tiles serve the dense projections of a sequence prefill
-// (llmy_linear_bf16 with many rows): MODE 2 is one "expert" owning all M
-// rows, BN = 128, an N tail (rows past N re-read row N-1, their columns are
-// not stored) and the linear epilogues (bf16 / fp32 store, fp32 residual
-// add, gated residual add).
+// expert's token rows, run back to back in the same XCD's L2.  Dense work is
+// grouped 4 m-tiles x all n-tiles, so the tiles an XCD runs together share
+// few A and B tiles.
 #include "common.hpp"
 #include "abi_util.hpp"
 
 namespace llmy {
 
-namespace {
+enum Mode : int { kGateUp = 0, kDown = 1, kDense = 2 };
+// Dense epilogues (values of the linear entry's epilogue argument).
+enum DenseEpi : int { kDenseBf16 = 0, kDenseF32 = 1, kDenseResid = 2, kDenseGated = 3 };
 
-constexpr int kGemmThreads = 512;  // 8 wavefronts: 2 per SIMD
-constexpr int kBM = 128;
-constexpr int kBK = 64;   // K per pipeline stage (four 16-k MFMA steps)
-constexpr int kSteps = kBK / 16;
-constexpr int kRowB = kBK * 2;  // bytes of one tile row in a stage (8 chunks of 16)
-constexpr int kBlock = 1024;            // one 32 x 16 bf16 MFMA operand block
-constexpr int kNumXcd = 8;
-
-struct MoeGemmArgs {
-  const uint16_t* x;       // gate_up: token rows [x_rows, K]; down: act [rows_total, K]
-  const uint16_t* w;       // expert weights, row-major [E, N_w, K] or packed
-  void* out;               // gate_up: act bf16 [rows_total, ldo]; down: y f32 [rows_total, ldo]
+struct TileArgs {
+  const uint16_t* x;       // gate_up: token rows [x_rows, K]; down: act; dense: [M, K]
+  const uint16_t* w;       // weights, row-major [E, N_w, K] or packed
+  void* out;               // act bf16 / y f32 / dense out, row stride ldo
   const float* gates;      // down: gate per route id
-  const int32_t* offsets;  // [E + 1]
+  const float* aux;        // dense gated residual: out += acc * aux[m * ldo + n]
+  const int32_t* offsets;  // grouped: [E + 1]
   const int32_t* sorted_routes;
   long long w_expert_stride;  // elements per expert block of w
   long long up_offset;        // gate_up: elements from gate row n to up row n (H * K)
   int K, ldo, E, route_k, rows_total, x_rows;
+  int N;        // dense: output columns (last n-tile may be partial)
   int n_tiles;  // output column tiles per expert
+  int m_tiles;  // dense: row tiles
+  int group_m;  // dense: m-tiles per work group (0: m fastest over all rows)
   int packed;
-  // dense (MODE 2) only
-  const float* aux;  // gated residual: out += acc * aux[m * ldo + n]
-  int N;             // output columns (the last n-tile may be partial)
-  int m_tiles;
 };
+
+namespace {
+
+constexpr int kThreads = 256;  // 4 wavefronts: one per SIMD
+constexpr int kNumXcd = 8;
 
 // Packed operand order of llmy_pack_weights_bf16 (see linear.hip): the 8
 // elements W[n][k .. k+7] (k % 8 == 0) are contiguous at this index.
@@ -82,17 +88,23 @@ typedef __attribute__((address_space(3))) void lds_void;
 // global_load_lds).
 __device__ __forceinline__ lds_void* as_lds(void* p) { return (lds_void*)p; }
 
+// One global_load_lds_dwordx4: 16 bytes per lane from src into LDS at dst
+// (+16 bytes per lane).  Kept in a device function: the builtin inside a
+// kernel template body stops the host pass from emitting the launch stub.
+__device__ __forceinline__ void dma16(const void* src, void* dst) {
+  __builtin_amdgcn_global_load_lds(src, as_lds(dst), 16, 0, 0);
+}
+
 // s_waitcnt immediate (gfx9 encoding) that waits until at most n vector
-// memory operations of this wavefront are outstanding (vmcnt bits [3:0] and
-// [15:14]; expcnt [6:4] = 7 and lgkmcnt [11:8] = 15 wait for nothing) ...
-constexpr int waitcnt_vm(int n) { return 0x0F70 | (n & 15) | ((n >> 4) << 14); }
-// ... and also for all of this wavefront's LDS operations (lgkmcnt = 0).
+// memory operations of this wavefront are outstanding and for all of its LDS
+// operations (vmcnt bits [3:0] and [15:14]; expcnt [6:4] = 7; lgkmcnt
+// [11:8] = 0).
 constexpr int waitcnt_vm_lgkm0(int n) { return 0x0070 | (n & 15) | ((n >> 4) << 14); }
 
 // 16-byte LDS read at byte address addr + OFF, as inline asm: the compiler's
-// LDS-DMA tracking cannot separate the stage being read from the stages
-// being filled and would make every read wait for all loads in flight.  The
-// result is valid only after lds_settle().
+// LDS-DMA tracking cannot separate the stage being read from the stage being
+// filled and would make every read wait for all loads in flight.  The result
+// is valid only after a settle below.
 template <int OFF>
 __device__ __forceinline__ u32x4 lds_frag(uint32_t addr) {
   u32x4 v;
@@ -100,10 +112,17 @@ __device__ __forceinline__ u32x4 lds_frag(uint32_t addr) {
   return v;
 }
 
-// Wait for this wavefront's LDS reads; the "+v" operand makes every later use
-// of v follow the wait.
-__device__ __forceinline__ void lds_settle(u32x4& v) {
-  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(v) :: "memory");
+// Wait until at most N of this wavefront's LDS operations are outstanding
+// (LDS operations complete in order, so every read issued before the last N
+// is done) and tie the registers those reads filled to the wait, so every
+// later use of them follows it.
+template <int N>
+__device__ __forceinline__ void settle4(u32x4& a, u32x4& b, u32x4& c, u32x4& d) {
+  asm volatile("s_waitcnt lgkmcnt(%4)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d) : "i"(N) : "memory");
+}
+template <int N>
+__device__ __forceinline__ void settle2(u32x4& a, u32x4& b) {
+  asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(a), "+v"(b) : "i"(N) : "memory");
 }
 
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
@@ -117,36 +136,54 @@ __device__ __forceinline__ f32x16 mfma32(const u32x4& a, const u32x4& b, const f
 
 }  // namespace
 
-// Dense epilogues (values of the linear entry's epilogue argument).
-enum DenseEpi : int { kDenseBf16 = 0, kDenseF32 = 1, kDenseResid = 2, kDenseGated = 3 };
-
-// MODE 0: gate_up + SwiGLU (BN = 256); MODE 1: down + gate scale (BN = 128);
-// MODE 2: dense with epilogue EPI (BN = 128).
-template <int MODE, int EPI = 0>
-__global__ __launch_bounds__(kGemmThreads) void moe_gemm_kernel(MoeGemmArgs a) {
-  constexpr int BN = MODE == 0 ? 256 : 128;
-  constexpr int CT = BN / 128;       // 32-column MFMA blocks per wavefront (2 x 4 wave grid)
-  __shared__ int s_work[3];          // expert, m0, n-tile (or -1: no work)
+template <int MODE, int BM, int BN, int BK, int NS, int EPI, int OCC = 1>
+__global__ __launch_bounds__(kThreads, OCC) void tile_gemm_kernel(TileArgs a) {
+  constexpr int WM = BM / 2, WN = BN / 2;  // wavefront sub-tile
+  constexpr int FA = WM / 32, FB = WN / 32;  // 32-row / 32-column MFMA blocks per wavefront
+  constexpr int ROWB = BK * 2;      // bytes of one tile row in a stage
+  constexpr int CPR = BK / 8;       // 16-byte chunks per row
+  constexpr int RPI = 64 / CPR;     // tile rows per DMA instruction
+  constexpr int SWZ = 16 / CPR;     // rows sharing one swizzle value
+  constexpr int KS = BK / 16;       // MFMA k-steps per stage
+  constexpr int A_INS = BM / RPI / 4;  // DMA instructions per wavefront per stage
+  constexpr int B_INS = BN / RPI / 4;
+  constexpr int DPT = A_INS + B_INS;   // DMA instructions per wavefront per K tile
+  constexpr int A_BYTES = BM * ROWB;
+  constexpr int STAGE_BYTES = (BM + BN) * ROWB;
+  constexpr int NF = FA + FB;  // fragment reads per k-step
+  static_assert(FA == 2 || FA == 4, "wavefront rows");
+  static_assert(FB == 2 || FB == 4, "wavefront columns");
+  static_assert(MODE != kGateUp || FB % 2 == 0, "gate/up halves");
+  static_assert(BK == 32 || BK == 64, "K tile");
+  static_assert(NS >= 2 && DPT * (NS - 2) <= 63, "vmcnt range");
+  __shared__ int s_work[3];  // expert, m0, n-tile (or -1: no work)
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave & 1, wn = wave >> 1;  // rows 64 wm .., columns (BN/4) wn ..
+  const int wm = wave & 1, wn = wave >> 1;
 
   // ---- which tile.  Dense: work item w = (n-tile, m-tile), m fastest.
   // Grouped: wave 0 scans the experts' m-tile counts.
-  if (MODE == 2) {
+  const int nblk = gridDim.x;
+  const int per_xcd = (nblk + kNumXcd - 1) / kNumXcd;
+  const int w_item = (blockIdx.x % kNumXcd) * per_xcd + blockIdx.x / kNumXcd;
+  if (MODE == kDense) {
     if (tid == 0) {
-      const int nblk = gridDim.x;
-      const int per_xcd = (nblk + kNumXcd - 1) / kNumXcd;
-      const int w = (blockIdx.x % kNumXcd) * per_xcd + blockIdx.x / kNumXcd;
-      const bool ok = w < a.m_tiles * a.n_tiles;
+      const bool ok = w_item < a.m_tiles * a.n_tiles;
+      int mt = w_item % a.m_tiles, nt = w_item / a.m_tiles;
+      if (a.group_m > 0) {
+        // groups of group_m m-tiles x all n-tiles, m fastest inside a group,
+        // so the tiles an XCD runs together share few A and B tiles
+        const int per_group = a.group_m * a.n_tiles;
+        const int grp = w_item / per_group, in = w_item % per_group;
+        const int gm = min(a.group_m, a.m_tiles - grp * a.group_m);
+        mt = grp * a.group_m + in % gm;
+        nt = in / gm;
+      }
       s_work[0] = ok ? 0 : -1;
-      s_work[1] = ok ? (w % a.m_tiles) * kBM : 0;
-      s_work[2] = ok ? w / a.m_tiles : 0;
+      s_work[1] = ok ? mt * BM : 0;
+      s_work[2] = ok ? nt : 0;
     }
   } else if (wave == 0) {
-    const int nblk = gridDim.x;
-    const int per_xcd = (nblk + kNumXcd - 1) / kNumXcd;
-    const int w = (blockIdx.x % kNumXcd) * per_xcd + blockIdx.x / kNumXcd;
     int found = -1, m0 = 0, nt = 0;
     int base = 0;  // m-tiles of the experts before this chunk of 64
     for (int e0 = 0; e0 < a.E; e0 += kWave) {
@@ -155,7 +192,7 @@ __global__ __launch_bounds__(kGemmThreads) void moe_gemm_kernel(MoeGemmArgs a) {
       if (e < a.E) {
         const int lo = min(max(a.offsets[e], 0), a.rows_total);
         const int hi = min(max(a.offsets[e + 1], lo), a.rows_total);
-        tiles = (hi - lo + kBM - 1) / kBM;
+        tiles = (hi - lo + BM - 1) / BM;
       }
       int inc = tiles;  // inclusive scan over the wave
 #pragma unroll
@@ -165,15 +202,15 @@ __global__ __launch_bounds__(kGemmThreads) void moe_gemm_kernel(MoeGemmArgs a) {
       }
       const int first = (base + inc - tiles) * a.n_tiles;  // first work item of expert e
       const int last = (base + inc) * a.n_tiles;
-      const unsigned long long hit = __ballot(e < a.E && w >= first && w < last);
+      const unsigned long long hit = __ballot(e < a.E && w_item >= first && w_item < last);
       if (hit) {
         const int src = __ffsll(static_cast<long long>(hit)) - 1;
         const int f = __shfl(first, src, kWave);
         const int t = __shfl(tiles, src, kWave);
         found = e0 + src;
-        const int local = w - f;
+        const int local = w_item - f;
         nt = local / t;
-        m0 = (local - nt * t) * kBM;
+        m0 = (local - nt * t) * BM;
         break;
       }
       base += __shfl(inc, kWave - 1, kWave);
@@ -188,188 +225,297 @@ __global__ __launch_bounds__(kGemmThreads) void moe_gemm_kernel(MoeGemmArgs a) {
   const int e = s_work[0];
   if (e < 0) return;
   const int m0 = s_work[1], ntile = s_work[2];
-  const int row_lo = MODE == 2 ? 0 : min(max(a.offsets[e], 0), a.rows_total);
+  const int row_lo = MODE == kDense ? 0 : min(max(a.offsets[e], 0), a.rows_total);
   const int rows_e =
-      MODE == 2 ? a.rows_total : min(max(a.offsets[e + 1], row_lo), a.rows_total) - row_lo;
+      MODE == kDense ? a.rows_total : min(max(a.offsets[e + 1], row_lo), a.rows_total) - row_lo;
   const int K = a.K;
-  const int nk = K / kBK;
+  const int nk = K / BK;
 
-  // ---- global sources.  A stage holds the A tile (128 rows) then the B tile
-  // (BN rows), each row 128 bytes = 8 chunks of 8 k, chunk c of row r stored
-  // in slot c ^ ((r >> 1) & 7).  A ds_read_b128 is served 16 lanes at a time
-  // from 256 bytes of banks; the 16 lanes of a fragment read take 16
-  // consecutive rows at one chunk index, which this swizzle spreads over all
-  // 16 bank groups (two rows per 256 bytes, 8 slots each).  Each
-  // global_load_lds instruction fills 8 consecutive tile rows, lane l taking
-  // row 8q + l/8 and slot l%8, i.e. a whole 128-byte global row per 8 lanes.
-  constexpr int A_INS = kBM / 8 / 8;  // per wave per stage
-  constexpr int B_INS = BN / 8 / 8;
-  constexpr int LOADS = A_INS + B_INS;
-  constexpr int A_BYTES = kBM * kRowB;
-  constexpr int STAGE_BYTES = (kBM + BN) * kRowB;
-  const int dma_row = lane >> 3;  // row within the instruction's 8
-  // global chunk fetched by this lane for an instruction starting at tile row 8q
-  auto dma_chunk = [&](int q) { return (lane & 7) ^ (((8 * q + dma_row) >> 1) & 7); };
-  long long a_src[A_INS];
+  // ---- global sources.  A stage holds the A tile (BM rows) then the B tile
+  // (BN rows), each row BK k = CPR chunks of 16 bytes, chunk c of row r
+  // stored in slot c ^ ((r / SWZ) % CPR).  A ds_read_b128 is served 16 lanes
+  // at a time from 256 bytes of banks; the 16 lanes of a fragment read take
+  // 16 consecutive rows at one chunk index, which this swizzle spreads over
+  // all 16 bank groups.  Each global_load_lds instruction fills RPI
+  // consecutive tile rows, lane l taking row l / CPR and slot l % CPR, i.e.
+  // one whole row segment per CPR lanes.
+  const int dma_row = lane / CPR;
+  // Byte offsets (32-bit; the host bounds each operand block below 2 GiB)
+  // of the 16 bytes this lane fetches, relative to the operand base: for
+  // tile row r the lane takes global chunk (lane % CPR) ^ ((r / SWZ) % CPR).
+#define DMA_CH(r) ((lane % CPR) ^ (((r) / SWZ) % CPR))
+  uint32_t a_off[A_INS];
 #pragma unroll
   for (int q = 0; q < A_INS; ++q) {
-    const int r = 8 * (A_INS * wave + q) + dma_row;  // tile row
-    const int m = min(m0 + r, rows_e - 1);            // past the expert: repeat its last row
+    const int r = RPI * (A_INS * wave + q) + dma_row;  // tile row
+    const int m = min(m0 + r, rows_e - 1);              // past the rows: repeat the last
     const int p = row_lo + m;
     long long src;
-    if (MODE == 0) {
+    if (MODE == kGateUp) {
       src = min(max(a.sorted_routes[p], 0), a.rows_total - 1) / a.route_k;
       src = min(src, static_cast<long long>(a.x_rows - 1));
     } else {
       src = p;
     }
-    a_src[q] = src * K + 8 * dma_chunk(A_INS * wave + q);
+    a_off[q] = static_cast<uint32_t>((src * K + 8 * DMA_CH(r)) * 2);
   }
-  const uint16_t* wexp = a.w + static_cast<long long>(e) * a.w_expert_stride;
   const bool packed = a.packed != 0;
-  long long b_src[B_INS];
+  uint32_t b_off[B_INS];
 #pragma unroll
   for (int q = 0; q < B_INS; ++q) {
-    const int r = 8 * (B_INS * wave + q) + dma_row;  // tile row
+    const int r = RPI * (B_INS * wave + q) + dma_row;  // tile row
     long long off = 0;
     int n;
-    if (MODE == 0) {
-      // [gate n0..+31 | up n0..+31 | gate n0+32..+63 | up ...], n0 = 128 * ntile:
-      // wavefront column quarter wn gets 32 gate rows and their 32 up rows
-      n = 128 * ntile + 32 * (r >> 6) + (r & 31);
-      if ((r >> 5) & 1) off = a.up_offset;
-    } else if (MODE == 1) {
+    if (MODE == kGateUp) {
+      // wavefront column c = r / WN holds [gate cols | up cols] of output
+      // columns (BN/2) ntile + (WN/2) c + 0 .. WN/2 - 1
+      const int c = r / WN, rr = r % WN;
+      n = (BN / 2) * ntile + (WN / 2) * c + rr % (WN / 2);
+      if (rr >= WN / 2) off = a.up_offset;
+    } else if (MODE == kDown) {
       n = BN * ntile + r;
     } else {
       n = min(BN * ntile + r, a.N - 1);  // N tail: repeat the last row
     }
-    const int ch = dma_chunk(B_INS * wave + q);
-    b_src[q] = off + (packed ? packed_at(n, 8 * ch, K) : static_cast<long long>(n) * K + 8 * ch);
+    const int ch = DMA_CH(r);
+    b_off[q] = static_cast<uint32_t>(
+        (off + (packed ? packed_at(n, 8 * ch, K) : static_cast<long long>(n) * K + 8 * ch)) * 2);
   }
+#undef DMA_CH
+  const char* a_base = reinterpret_cast<const char*>(a.x);
+  const char* b_base =
+      reinterpret_cast<const char*>(a.w + static_cast<long long>(e) * a.w_expert_stride);
+  // The wavefront index as a scalar, so LDS destinations (M0) are scalar arithmetic.
+  const int wv = __builtin_amdgcn_readfirstlane(wave);
 
-  // Two named LDS stages: K tile kt+1 is in flight while tile kt is
-  // multiplied (named objects let the compiler's LDS-DMA tracking keep them
-  // apart).
-  __shared__ __align__(1024) unsigned char st0[STAGE_BYTES];
-  __shared__ __align__(1024) unsigned char st1[STAGE_BYTES];
+  // NS LDS stages in a ring: K tiles kt+1 .. kt+NS-1 are in flight while
+  // tile kt is multiplied.
+  __shared__ __align__(1024) unsigned char smem[NS * STAGE_BYTES];
+  const uint32_t smem_base = lds_addr(smem);
 
-  // Element offset of K tile kt within a B row: row-major 64 kt; packed:
-  // 256-k blocks are 4096 elements apart, 64-k tiles 1024.
-  auto issue = [&](int kt, unsigned char* st) {
-    const long long ka = static_cast<long long>(kt) * kBK;
-    const long long kb = packed ? static_cast<long long>(kt >> 2) * 4096 + (kt & 3) * 1024 : ka;
-#pragma unroll
-    for (int q = 0; q < A_INS; ++q)
-      __builtin_amdgcn_global_load_lds(static_cast<const void*>(a.x + a_src[q] + ka),
-                                       as_lds(st + (8 * (A_INS * wave + q)) * kRowB), 16, 0, 0);
-#pragma unroll
-    for (int q = 0; q < B_INS; ++q)
-      __builtin_amdgcn_global_load_lds(static_cast<const void*>(wexp + b_src[q] + kb),
-                                       as_lds(st + A_BYTES + (8 * (B_INS * wave + q)) * kRowB), 16,
-                                       0, 0);
-  };
+  // K tile kt of both operands into stage `stage`.  Byte offset of K tile kt
+  // within a B row: row-major 2 BK kt; packed: 256-k blocks are 8 KiB apart,
+  // 32-k pieces 1 KiB.
+#define TILE_ISSUE(kt, stage)                                                               \
+  do {                                                                                      \
+    const long long ka_ = static_cast<long long>(kt) * BK;                                  \
+    const long long kb_ = packed ? (ka_ >> 8) * 4096 + ((ka_ & 255) >> 5) * 512 : ka_;      \
+    const char* ab_ = a_base + 2 * ka_;                                                     \
+    const char* bb_ = b_base + 2 * kb_;                                                     \
+    unsigned char* st_ = smem + (stage) * STAGE_BYTES;                                      \
+    _Pragma("unroll") for (int q = 0; q < A_INS; ++q)                                       \
+        dma16(ab_ + a_off[q], st_ + (RPI * (A_INS * wv + q)) * ROWB);                       \
+    _Pragma("unroll") for (int q = 0; q < B_INS; ++q)                                       \
+        dma16(bb_ + b_off[q], st_ + A_BYTES + (RPI * (B_INS * wv + q)) * ROWB);             \
+  } while (0)
 
-  f32x16 acc[2][CT];
+  f32x16 acc[FA][FB];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < FA; ++i)
 #pragma unroll
-    for (int c = 0; c < CT; ++c)
+    for (int j = 0; j < FB; ++j)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][c][r] = 0.f;
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-  // Fragment addresses: lane l reads tile row (32-row block base) + l%32,
-  // chunk 2s + l/32 of k step s, stored in slot (2s + l/32) ^ ((l%32 >> 1) & 7).
-  uint32_t frag_off[kSteps];
+  // Fragment address of k-step s: lane l reads tile row (32-row block base) +
+  // l%32, chunk 2s + l/32, stored in slot (2s + l/32) ^ ((l%32 / SWZ) % CPR).
+  uint32_t frag_off[KS];
 #pragma unroll
-  for (int s = 0; s < kSteps; ++s)
-    frag_off[s] = (lane & 31) * kRowB + (((2 * s + (lane >> 5)) ^ ((lane >> 1) & 7)) << 4);
-  const uint32_t fa_base = (64 * wm) * kRowB;
-  const uint32_t fb_base = A_BYTES + ((BN / 4) * wn) * kRowB;
+  for (int s = 0; s < KS; ++s)
+    frag_off[s] = (lane & 31) * ROWB + (((2 * s + (lane >> 5)) ^ (((lane & 31) / SWZ) % CPR)) << 4);
+  const uint32_t fa_base = (WM * wm) * ROWB;
+  const uint32_t fb_base = A_BYTES + (WN * wn) * ROWB;
+  constexpr int BLK = 32 * ROWB;  // bytes between 32-row blocks
 
-  // One K tile: wait for this wave's loads of tile kt and its fragment reads
-  // of the previous tile, meet the workgroup at the barrier (then all of tile
-  // kt is in LDS and the other buffer is free), fetch tile kt+1 into it,
-  // multiply tile kt.
-  auto step = [&](int kt, const unsigned char* cur, unsigned char* refill) {
-    __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));
+  // Fragment reads of k-step S of the tile in stage STG into (FA_, FB_).
+#define TILE_READ(FA_, FB_, STG, S)                                                        \
+  do {                                                                                     \
+    const uint32_t xa_ = smem_base + (STG) * STAGE_BYTES + fa_base + frag_off[S];          \
+    const uint32_t xb_ = smem_base + (STG) * STAGE_BYTES + fb_base + frag_off[S];          \
+    FA_[0] = lds_frag<0>(xa_);                                                             \
+    FA_[1] = lds_frag<BLK>(xa_);                                                           \
+    if (FA == 4) {                                                                         \
+      FA_[FA - 2] = lds_frag<2 * BLK>(xa_);                                                \
+      FA_[FA - 1] = lds_frag<3 * BLK>(xa_);                                                \
+    }                                                                                      \
+    FB_[0] = lds_frag<0>(xb_);                                                             \
+    FB_[1] = lds_frag<BLK>(xb_);                                                           \
+    if (FB == 4) {                                                                         \
+      FB_[FB - 2] = lds_frag<2 * BLK>(xb_);                                                \
+      FB_[FB - 1] = lds_frag<3 * BLK>(xb_);                                                \
+    }                                                                                      \
+  } while (0)
+
+  // Wait until only the N most recent reads are outstanding, tying (FA_, FB_).
+#define TILE_SETTLE(FA_, FB_, N)                                       \
+  do {                                                                 \
+    if (FA == 4) settle4<N>(FA_[0], FA_[1], FA_[FA - 2], FA_[FA - 1]); \
+    else settle2<N>(FA_[0], FA_[1]);                                   \
+    if (FB == 4) settle4<N>(FB_[0], FB_[1], FB_[FB - 2], FB_[FB - 1]); \
+    else settle2<N>(FB_[0], FB_[1]);                                   \
+  } while (0)
+
+#define TILE_MMA(FA_, FB_)                                 \
+  do {                                                     \
+    _Pragma("unroll") for (int i = 0; i < FA; ++i)         \
+        _Pragma("unroll") for (int j = 0; j < FB; ++j)     \
+            acc[i][j] = mfma32(FB_[j], FA_[i], acc[i][j]); \
+  } while (0)
+
+  // Scheduling fence: the compiler keeps every instruction on its side.
+#define FENCE() __builtin_amdgcn_sched_barrier(0)
+
+  // Software pipeline.  Before iteration kt: tile kt is in LDS for every
+  // wavefront (barrier passed), its step-0 fragment reads are in flight, and
+  // tiles kt+1 .. kt+NS-2 are being fetched.  Iteration kt: fetch tile
+  // kt+NS-1 into the stage of tile kt-1 (free since the last barrier); for
+  // each k-step s, issue the reads of step s+1, wait for those of step s,
+  // multiply step s; before the last step's MFMAs, wait for tile kt+1, meet
+  // the workgroup, and issue the step-0 reads of tile kt+1, whose latency
+  // the last step's MFMAs cover.
+#pragma unroll
+  for (int t = 0; t < NS - 1; ++t)
+    if (t < nk) TILE_ISSUE(t, t);
+  if (NS > 2 && nk > NS - 2) __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(DPT * (NS - 2)));
+  else __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+  u32x4 pa[FA], pb[FB], qa[FA], qb[FB];
+  TILE_READ(pa, pb, 0, 0);
+  int stage = 0;
+  for (int kt = 0; kt < nk; ++kt) {
+    const int nxt = stage == NS - 1 ? 0 : stage + 1;
+    FENCE();
+    if (kt + NS - 1 < nk) TILE_ISSUE(kt + NS - 1, stage == 0 ? NS - 1 : stage - 1);
+    FENCE();
+    TILE_READ(qa, qb, stage, 1);
+    FENCE();
+    TILE_SETTLE(pa, pb, NF);
+    TILE_MMA(pa, pb);
+    FENCE();
+    if (KS == 4) {
+      TILE_READ(pa, pb, stage, KS - 2);
+      FENCE();
+      TILE_SETTLE(qa, qb, NF);
+      TILE_MMA(qa, qb);
+      FENCE();
+      TILE_READ(qa, qb, stage, KS - 1);
+      FENCE();
+      TILE_SETTLE(pa, pb, NF);
+      TILE_MMA(pa, pb);
+      FENCE();
+    }
+    TILE_SETTLE(qa, qb, 0);
+    FENCE();
+    // tile kt+1 landed: the tiles issued after it (up to kt+NS-1) may stay in flight
+    if (kt + NS - 1 < nk) __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(DPT * (NS - 2)));
+    else __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
-    if (kt + 1 < nk) issue(kt + 1, refill);
-    const uint32_t ca = lds_addr(cur) + fa_base, cb = lds_addr(cur) + fb_base;
-#pragma unroll
-    for (int s = 0; s < kSteps; ++s) {
-      u32x4 fa[2], fb[CT];
-      const uint32_t xa = ca + frag_off[s], xb = cb + frag_off[s];
-      fa[0] = lds_frag<0>(xa);
-      fa[1] = lds_frag<32 * kRowB>(xa);
-      fb[0] = lds_frag<0>(xb);
-      if (CT == 2) fb[CT - 1] = lds_frag<32 * kRowB>(xb);
-#pragma unroll
-      for (int i = 0; i < 2; ++i) lds_settle(fa[i]);
-#pragma unroll
-      for (int c = 0; c < CT; ++c) lds_settle(fb[c]);
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int c = 0; c < CT; ++c) acc[i][c] = mfma32(fa[i], fb[c], acc[i][c]);
-    }
-  };
-
-  // nk is even (K % 256 == 0, checked by the host)
-  issue(0, st0);
-  for (int kt = 0; kt < nk; kt += 2) {
-    step(kt, st0, st1);
-    step(kt + 1, st1, st0);
+    if (kt + 1 < nk) TILE_READ(pa, pb, nxt, 0);
+    FENCE();
+    TILE_MMA(qa, qb);
+    stage = nxt;
   }
+#undef FENCE
+#undef TILE_MMA
+#undef TILE_SETTLE
+#undef TILE_READ
+#undef TILE_ISSUE
 
-  // ---- epilogue: D layout of 32x32 blocks: lane l, reg r -> row (r&3) + 8(r>>2) + 4(l>>5), col l&31
+  // ---- epilogue.  acc[i][j] = (weight block j) . (row block i)^T, so in the
+  // 32x32 D layout lane l holds row m = 32 i + (l & 31) of the tile and, in
+  // registers 4g .. 4g+3, the four consecutive columns 32 j + 8g + 4(l >> 5)
+  // .. +3: every store is a 4-column vector.
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
+  for (int i = 0; i < FA; ++i) {
+    const int m = m0 + WM * wm + 32 * i + (lane & 31);
+    if (m >= rows_e) continue;
+    const long long p = row_lo + m;
+    if (MODE == kGateUp) {
+      uint16_t* act = static_cast<uint16_t*>(a.out) + p * a.ldo;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int row = 64 * wm + 32 * i + (r & 3) + 8 * (r >> 2) + 4 * (lane >> 5);
-      const int m = m0 + row;
-      if (m >= rows_e) continue;
-      const long long p = row_lo + m;
-      if (MODE == 0) {
-        uint16_t* act = static_cast<uint16_t*>(a.out) + p * a.ldo;
-        const float g = acc[i][0][r], u = acc[i][1][r];
-        act[128 * ntile + 32 * wn + (lane & 31)] = f2bf(siluf_(g) * u);
-      } else if (MODE == 2) {
-        const int n = BN * ntile + 32 * wn + (lane & 31);
-        if (n >= a.N) continue;
-        const long long o = p * a.ldo + n;
-        const float v = acc[i][0][r];
-        if (EPI == kDenseBf16) {
-          static_cast<uint16_t*>(a.out)[o] = f2bf(v);
-        } else if (EPI == kDenseF32) {
-          static_cast<float*>(a.out)[o] = v;
-        } else if (EPI == kDenseResid) {
-          static_cast<float*>(a.out)[o] += v;
-        } else {
-          static_cast<float*>(a.out)[o] += v * a.aux[o];
+      for (int j = 0; j < FB / 2; ++j)
+#pragma unroll
+        for (int g4 = 0; g4 < 4; ++g4) {
+          const int c = (BN / 2) * ntile + (WN / 2) * wn + 32 * j + 8 * g4 + 4 * (lane >> 5);
+          float v[4];
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            const float g = acc[i][j][4 * g4 + t], u = acc[i][j + FB / 2][4 * g4 + t];
+            v[t] = siluf_(g) * u;
+          }
+          *reinterpret_cast<uint2*>(act + c) = make_uint2(pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3]));
         }
-      } else {
-        const int route = min(max(a.sorted_routes[p], 0), a.rows_total - 1);
-        const float gs = a.gates[route];
-        float* y = static_cast<float*>(a.out) + p * a.ldo;
+    } else if (MODE == kDown) {
+      const int route = min(max(a.sorted_routes[p], 0), a.rows_total - 1);
+      const float gs = a.gates[route];
+      float* y = static_cast<float*>(a.out) + p * a.ldo;
 #pragma unroll
-        for (int c = 0; c < CT; ++c) y[BN * ntile + 32 * wn + 32 * c + (lane & 31)] = acc[i][c][r] * gs;
-      }
+      for (int j = 0; j < FB; ++j)
+#pragma unroll
+        for (int g4 = 0; g4 < 4; ++g4) {
+          const int c = BN * ntile + WN * wn + 32 * j + 8 * g4 + 4 * (lane >> 5);
+          *reinterpret_cast<float4*>(y + c) =
+              make_float4(acc[i][j][4 * g4] * gs, acc[i][j][4 * g4 + 1] * gs,
+                          acc[i][j][4 * g4 + 2] * gs, acc[i][j][4 * g4 + 3] * gs);
+        }
+    } else {
+#pragma unroll
+      for (int j = 0; j < FB; ++j)
+#pragma unroll
+        for (int g4 = 0; g4 < 4; ++g4) {
+          const int n = BN * ntile + WN * wn + 32 * j + 8 * g4 + 4 * (lane >> 5);
+          if (n >= a.N) continue;  // N % 16 == 0: a 4-column group is all in or all out
+          const long long o = p * a.ldo + n;
+          const float v0 = acc[i][j][4 * g4], v1 = acc[i][j][4 * g4 + 1];
+          const float v2 = acc[i][j][4 * g4 + 2], v3 = acc[i][j][4 * g4 + 3];
+          if (EPI == kDenseBf16) {
+            *reinterpret_cast<uint2*>(static_cast<uint16_t*>(a.out) + o) =
+                make_uint2(pack_bf2(v0, v1), pack_bf2(v2, v3));
+          } else if (EPI == kDenseF32) {
+            *reinterpret_cast<float4*>(static_cast<float*>(a.out) + o) = make_float4(v0, v1, v2, v3);
+          } else if (EPI == kDenseResid) {
+            float4* op = reinterpret_cast<float4*>(static_cast<float*>(a.out) + o);
+            float4 r = *op;
+            r.x += v0; r.y += v1; r.z += v2; r.w += v3;
+            *op = r;
+          } else {
+            float4* op = reinterpret_cast<float4*>(static_cast<float*>(a.out) + o);
+            const float4 g = *reinterpret_cast<const float4*>(a.aux + o);
+            float4 r = *op;
+            r.x += v0 * g.x; r.y += v1 * g.y; r.z += v2 * g.z; r.w += v3 * g.w;
+            *op = r;
+          }
+        }
     }
   }
 }
 
-// Launch both GEMMs; returns the launch status.  Shapes were validated by the
-// caller: D % 256 == 0, H % 256 == 0, rows_total = T * k >= 1.
+template <int MODE, int BM, int BN, int BK, int NS, int EPI, int OCC = 1>
+int32_t launch_tiles(const TileArgs& g, long long items, hipStream_t s) {
+  const unsigned grid = static_cast<unsigned>((items + kNumXcd - 1) / kNumXcd * kNumXcd);
+  hipLaunchKernelGGL((tile_gemm_kernel<MODE, BM, BN, BK, NS, EPI, OCC>), dim3(grid), dim3(kThreads),
+                     0, s, g);
+  return launch_status();
+}
+
+// Launch both grouped GEMMs; returns the launch status.  Shapes were validated
+// by the caller: D % 256 == 0, H % 256 == 0, rows_total = T * k >= 1.
 int32_t moe_gemm_prefill(const uint16_t* x, const int32_t* offsets, const int32_t* sorted_routes,
                          const float* gates, const uint16_t* w_gate_up, const uint16_t* w_down,
                          uint16_t* act, float* y, int T, int D, int H, int E, int k, bool packed,
                          hipStream_t s) {
+  constexpr int BM = 128;
   const int rows_total = T * k;
-  const int max_mtiles = (rows_total + kBM - 1) / kBM + E;  // sum over experts of ceil(n_e/BM)
-  MoeGemmArgs g{};
+  // operand blocks addressed with 32-bit byte offsets
+  constexpr long long kMaxBytes = 1ll << 31;
+  if (2ll * T * D >= kMaxBytes || 2ll * rows_total * H >= kMaxBytes || 4ll * H * D >= kMaxBytes)
+    return static_cast<int32_t>(hipErrorInvalidValue);
+  const long long max_mtiles = (rows_total + BM - 1) / BM + E;  // >= sum_e ceil(n_e / BM)
+  TileArgs g{};
   g.x = x;
   g.w = w_gate_up;
   g.out = act;
@@ -383,15 +529,13 @@ int32_t moe_gemm_prefill(const uint16_t* x, const int32_t* offsets, const int32_
   g.route_k = k;
   g.rows_total = rows_total;
   g.x_rows = T;
-  g.n_tiles = H / 128;
+  g.n_tiles = H / 128;  // BN = 256 B rows -> 128 output columns
   g.packed = packed;
-  long long blocks = static_cast<long long>(max_mtiles) * g.n_tiles;
-  blocks = (blocks + kNumXcd - 1) / kNumXcd * kNumXcd;
-  hipLaunchKernelGGL(moe_gemm_kernel<0>, dim3(static_cast<unsigned>(blocks)), dim3(kGemmThreads),
-                     0, s, g);
-  const int32_t st = launch_status();
+  // Two workgroups per CU (one wavefront of each per SIMD): one's barrier and
+  // load waits are covered by the other's MFMAs.  gate_up: 3 stages of K 32.
+  int32_t st = launch_tiles<kGateUp, BM, 256, 32, 3, 0, 2>(g, max_mtiles * g.n_tiles, s);
   if (st != 0) return st;
-  MoeGemmArgs d = g;
+  TileArgs d = g;
   d.x = act;
   d.w = w_down;
   d.out = y;
@@ -402,19 +546,18 @@ int32_t moe_gemm_prefill(const uint16_t* x, const int32_t* offsets, const int32_
   d.ldo = D;
   d.x_rows = rows_total;
   d.n_tiles = D / 128;
-  blocks = static_cast<long long>(max_mtiles) * d.n_tiles;
-  blocks = (blocks + kNumXcd - 1) / kNumXcd * kNumXcd;
-  hipLaunchKernelGGL(moe_gemm_kernel<1>, dim3(static_cast<unsigned>(blocks)), dim3(kGemmThreads),
-                     0, s, d);
-  return launch_status();
+  return launch_tiles<kDown, BM, 128, 64, 2, 0, 2>(d, max_mtiles * d.n_tiles, s);
 }
 
-// Dense out[M, N] (epilogue epi) = x[M, K] . w[N, K]^T on the same tiles.
-// Validated by the caller: M >= 1, N >= 1, K % 256 == 0, 16-byte aligned
-// x and w, aux given for the gated epilogue.
+// Dense out[M, N] (epilogue epi) = x[M, K] . w[N, K]^T.  Validated by the
+// caller: M >= 1, N >= 1, K % 256 == 0, 16-byte aligned x and w, aux given
+// for the gated epilogue.
 int32_t dense_gemm_mfma(const uint16_t* x, const uint16_t* w, void* out, const float* aux,
                         int M, int N, int K, int epi, bool packed, hipStream_t s) {
-  MoeGemmArgs g{};
+  // operand blocks addressed with 32-bit byte offsets
+  if (2ll * M * K >= (1ll << 31) || 2ll * N * K >= (1ll << 31))
+    return static_cast<int32_t>(hipErrorInvalidValue);
+  TileArgs g{};
   g.x = x;
   g.w = w;
   g.out = out;
@@ -426,20 +569,27 @@ int32_t dense_gemm_mfma(const uint16_t* x, const uint16_t* w, void* out, const f
   g.rows_total = M;
   g.x_rows = M;
   g.N = N;
-  g.n_tiles = (N + 127) / 128;
-  g.m_tiles = (M + kBM - 1) / kBM;
   g.packed = packed;
-  long long blocks = static_cast<long long>(g.m_tiles) * g.n_tiles;
-  if (blocks >= (1ll << 31) - kNumXcd) return static_cast<int32_t>(hipErrorInvalidValue);
-  blocks = (blocks + kNumXcd - 1) / kNumXcd * kNumXcd;
-  const dim3 grid(static_cast<unsigned>(blocks)), block(kGemmThreads);
-  switch (epi) {
-    case kDenseBf16: hipLaunchKernelGGL((moe_gemm_kernel<2, kDenseBf16>), grid, block, 0, s, g); break;
-    case kDenseF32: hipLaunchKernelGGL((moe_gemm_kernel<2, kDenseF32>), grid, block, 0, s, g); break;
-    case kDenseResid: hipLaunchKernelGGL((moe_gemm_kernel<2, kDenseResid>), grid, block, 0, s, g); break;
-    default: hipLaunchKernelGGL((moe_gemm_kernel<2, kDenseGated>), grid, block, 0, s, g); break;
+  // 256 x 256 tiles (one workgroup per CU) when there is one per CU, else
+  // 128 x 128 (two workgroups per CU); both 2 stages of K 64, in groups of 4
+  // m-tiles.
+  const bool wide = static_cast<long long>((M + 255) / 256) * ((N + 255) / 256) >= 256;
+  const int bt = wide ? 256 : 128;
+  g.m_tiles = (M + bt - 1) / bt;
+  g.n_tiles = (N + bt - 1) / bt;
+  g.group_m = 4;
+  const long long items = static_cast<long long>(g.m_tiles) * g.n_tiles;
+  if (items >= (1ll << 31) - kNumXcd) return static_cast<int32_t>(hipErrorInvalidValue);
+#define LLMY_DENSE(T_, OCC_)                                                                 \
+  switch (epi) {                                                                             \
+    case kDenseBf16: return launch_tiles<kDense, T_, T_, 64, 2, kDenseBf16, OCC_>(g, items, s); \
+    case kDenseF32: return launch_tiles<kDense, T_, T_, 64, 2, kDenseF32, OCC_>(g, items, s);   \
+    case kDenseResid: return launch_tiles<kDense, T_, T_, 64, 2, kDenseResid, OCC_>(g, items, s); \
+    default: return launch_tiles<kDense, T_, T_, 64, 2, kDenseGated, OCC_>(g, items, s);        \
   }
-  return launch_status();
+  if (wide) LLMY_DENSE(256, 1)
+  LLMY_DENSE(128, 2)
+#undef LLMY_DENSE
 }
 
 }  // namespace llmy
