@@ -271,6 +271,32 @@ def kernel_table(cfg, B, gen, iters):
     mfma("moe_prefill_layer", us, 2 * T2 * k * (D * 2 * Hf + Hf * D),
          f"C2: T={T2}, D={D}, E={E}, top-{k}, H={Hf} (router+permute+experts+combine)")
     del x2, wgu, wd
+    # the grouped expert GEMMs alone (C2 shape, routes from the router above)
+    x2 = torch.randn(T2, D, device="cuda", generator=gen).bfloat16()
+    idx2, gates2 = ops.router_topk(x2, wr2, k)
+    perm2 = ops.moe_permute(idx2.view(-1), E)
+    esets = [((torch.randn(E, 2 * Hf, D, device="cuda", generator=gen) * 0.02).bfloat16(),
+              (torch.randn(E, D, Hf, device="cuda", generator=gen) * 0.02).bfloat16())
+             for _ in range(2)]
+    act2 = torch.empty(T2 * k, Hf, dtype=torch.bfloat16, device="cuda")
+    y2 = torch.empty(T2 * k, D, device="cuda")
+    us = event_time(lambda i: ops.moe_experts(x2, perm2, gates2, *esets[i % 2], act=act2, y=y2),
+                    max(3, iters // 10))
+    mfma("moe_prefill_experts", us, 2 * T2 * k * (D * 2 * Hf + Hf * D),
+         f"C2 grouped GEMMs only: {T2 * k} routes, gate_up+SwiGLU then down, 2 weight sets")
+    del x2, esets, act2, y2
+    # dense prefill projection: the C5 GDN input projection over 4096 tokens
+    nprj = 2 * Hg * dk + 2 * Hg * dv + Hg
+    nprj += (-nprj) % 16
+    xs = torch.randn(4096, D, device="cuda", generator=gen).bfloat16()
+    wps = [ops.pack_weights((torch.randn(nprj, D, device="cuda", generator=gen) * 0.02).bfloat16())
+           for _ in range(2)]
+    po = torch.empty(4096, nprj, device="cuda")
+    us = event_time(lambda i: ops.linear(xs, wps[i % 2], out=po, epilogue=ops.EPI_STORE_F32,
+                                         layout=ops.LAYOUT_PACKED), max(3, iters // 5))
+    mfma("dense_prefill_gemm", us, 2 * 4096 * nprj * D,
+         f"C5 GDN projection over 4096 tokens: M=4096, N={nprj}, K={D}, packed weights")
+    del xs, wps, po
     # attention prefill (C3)
     Bq, Tq, Hq, hq, Wq = 4, 8192, 16, 64, 512
     qkv = [torch.randn(Bq, Tq, Hq, hq, device="cuda", generator=gen).bfloat16() for _ in range(3)]
@@ -298,6 +324,51 @@ def kernel_table(cfg, B, gen, iters):
     del gq, gk, gv, go4, ws
     torch.cuda.empty_cache()
     return rows
+
+
+def model_flops_per_token(cfg, T):
+    """Dense-equivalent FLOPs per prompt token of a [B, T] prefill: every
+    projection, banded attention over the average window of a T-token
+    prompt, the GDN recurrence (6 dk dv per head), router and top-k
+    experts; the LM head of the last position is left out."""
+    D, Hhd = cfg.d_model, cfg.attn_heads * cfg.attn_head_dim
+    Hg, dk, dv = cfg.gdn_heads, cfg.gdn_dk, cfg.gdn_dv
+    keys = sum(min(t + 1, cfg.window) for t in range(T)) / T
+    attn = 2 * 4 * D * Hhd + 4 * Hhd * keys
+    nproj = 2 * Hg * dk + 2 * Hg * dv + Hg
+    gdn = 2 * (D * nproj + Hg * dv * D) + 6 * Hg * dk * dv
+    moe = 2 * D * cfg.n_experts + 2 * cfg.top_k * 3 * D * cfg.expert_hidden
+    per_loop = sum((attn if kind == "attn" else gdn) + moe for kind in cfg.layer_kinds)
+    return per_loop * cfg.num_loops
+
+
+def engine_prefill(cfg, gen, Bp=8, Tp=512, iters=5):
+    """Whole-model prefill of Bp fresh sequences of Tp prompt tokens through
+    HybridDecoder.prefill (embedding to the last position's logits and
+    greedy token)."""
+    import torch
+    from hybrid_llm_amd.config import init_weights
+    from hybrid_llm_amd.engine import HybridDecoder
+    weights = init_weights(cfg, seed=1, device="cuda")
+    eng = HybridDecoder(cfg, weights, Bp, device="cuda")
+    del weights
+    toks = torch.randint(0, cfg.vocab, (Bp, Tp), device="cuda", generator=gen)
+    eng.prefill(toks)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(iters):
+        eng.prefill(toks)
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / iters
+    del eng
+    torch.cuda.empty_cache()
+    tok_s = Bp * Tp / (ms / 1e3)
+    tf = model_flops_per_token(cfg, Tp) * tok_s / 1e12
+    return {"workload": f"C5 model prefill, {Bp} fresh sequences x {Tp} tokens (to last logits)",
+            "bound": "mfma", "ms": round(ms, 3), "tok_s": round(tok_s, 1),
+            "achieved": round(tf, 1), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4),
+            "flops_per_token": round(model_flops_per_token(cfg, Tp))}
 
 
 def cpu_baseline(B, seconds_budget=10.0):
@@ -420,6 +491,10 @@ def main():
         for name, r in kernels.items():
             print(f"[bench] {name}: {r['avg_us']} us, {r['achieved']} {r['unit']} "
                   f"({100 * r['frac']:.1f}%)", file=sys.stderr, flush=True)
+        kernels["engine_prefill"] = engine_prefill(cfg, gen)
+        r = kernels["engine_prefill"]
+        print(f"[bench] engine_prefill: {r['ms']} ms, {r['tok_s']:.0f} tok/s, "
+              f"{r['achieved']} TFLOP/s ({100 * r['frac']:.1f}%)", file=sys.stderr, flush=True)
 
     cpu = None
     if not args.no_cpu_baseline:
