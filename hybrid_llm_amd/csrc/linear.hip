@@ -74,7 +74,7 @@ __host__ __device__ __forceinline__ long long packed_index(int n, int k, int K) 
   return ((((static_cast<long long>(nb) * (K >> 8) + kb) * 8 + j) * 64 + lane) << 3) + e;
 }
 
-template <int EPI, int MODE, bool PACKED, int MB, int KB>
+template <int EPI, int MODE, bool PACKED, int MB, int KB, int JT = 8>
 __global__ __launch_bounds__(512) void wsgemm_kernel(WsArgs a) {
   constexpr bool kPair = (EPI == kSwiGLU);
   constexpr int kSlots = (kPair ? 2 : 1) * MB * 4;
@@ -143,18 +143,21 @@ __global__ __launch_bounds__(512) void wsgemm_kernel(WsArgs a) {
       acc[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
       accu[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
-    // Each wave takes KB consecutive 256-wide K blocks per step (KB blocks of
-    // weights in flight at once); K % (256 * KB) == 0.
-    for (int kb0 = wave * 256 * KB; kb0 < K; kb0 += S * 256 * KB) {
-      // Issue every load of these K blocks before the first MFMA.
-      uint4 bw[KB][8], bu[KB][8], av[KB][MB][8];
+    // Each wave takes KB consecutive pieces of 32*JT k per step (JT = 8: whole
+    // 256-wide K blocks; 4: half blocks, twice the waves for a given K);
+    // K % (32 * JT * KB) == 0.
+    constexpr int KP = 32 * JT;
+    for (int kb0 = wave * KP * KB; kb0 < K; kb0 += S * KP * KB) {
+      // Issue every load of these K pieces before the first MFMA.
+      uint4 bw[KB][JT], bu[KB][JT], av[KB][MB][JT];
 #pragma unroll
       for (int q = 0; q < KB; ++q) {
-        const int kb = kb0 + 256 * q;
+        const int kb = kb0 + KP * q;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
+        for (int j = 0; j < JT; ++j) {
           const long long off =
-              PACKED ? (static_cast<long long>(kb >> 8) * 8 + j) * 512 : kb + 32 * j;
+              PACKED ? (static_cast<long long>(kb >> 8) * 8 + ((kb & 255) >> 5) + j) * 512
+                     : kb + 32 * j;
           bw[q][j] = ld_stream(wlane + off);
           if (kPair) bu[q][j] = ld_stream(wlane + a.pair_offset + off);
         }
@@ -164,9 +167,9 @@ __global__ __launch_bounds__(512) void wsgemm_kernel(WsArgs a) {
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb) {
 #pragma unroll
-          for (int j = 0; j < 8; ++j)
+          for (int j = 0; j < JT; ++j)
             av[q][mb][j] = (mb < nmb && valid[mb])
-                               ? *reinterpret_cast<const uint4*>(xrow[mb] + kb0 + 256 * q + 32 * j)
+                               ? *reinterpret_cast<const uint4*>(xrow[mb] + kb0 + KP * q + 32 * j)
                                : uint4{0u, 0u, 0u, 0u};
         }
       }
@@ -176,7 +179,7 @@ __global__ __launch_bounds__(512) void wsgemm_kernel(WsArgs a) {
         for (int mb = 0; mb < MB; ++mb) {
           if (mb < nmb) {
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
+            for (int j = 0; j < JT; ++j) {
               acc[mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
                   as_bf16x8(av[q][mb][j]), as_bf16x8(bw[q][j]), acc[mb], 0, 0, 0);
               if (kPair)
@@ -218,52 +221,73 @@ __global__ __launch_bounds__(512) void wsgemm_kernel(WsArgs a) {
     }
     if (wave != 0) continue;
 
-    // Epilogue: lane holds rows m0 + 16mb + 4g + i, column n0 + r.
+    // Epilogue: lane holds rows m0 + 16mb + 4g + i, column n0 + r.  Every
+    // value the epilogue reads (residual, gate) is loaded before the first
+    // store: the compiler cannot prove a store and a later load of another
+    // row apart, and would otherwise wait out one memory round trip per value.
     const int n = n0 + r;
+    long long orow[MB][4];
+    float in0[MB][4], in1[MB][4];
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) {
-      if (mb < nmb) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int m = m0 + 16 * mb + 4 * g + i;
-          if (m < M) {
-            const long long row = kRouted ? rlist[m] : row_begin + m;
-            const long long o = row * a.ldo + n;
-            const float v = acc[mb][i];
-            if (EPI == kStoreBf16) {
-              static_cast<uint16_t*>(a.out)[o] = f2bf(v);
-            } else if (EPI == kStoreF32) {
-              static_cast<float*>(a.out)[o] = v;
-            } else if (EPI == kResidAdd) {
-              static_cast<float*>(a.out)[o] += v;
-            } else if (EPI == kResidGated) {
-              static_cast<float*>(a.out)[o] += v * a.aux[o];
-            } else if (EPI == kSwiGLU) {
-              static_cast<uint16_t*>(a.out)[o] = f2bf(siluf_(v) * accu[mb][i]);
-            } else if (EPI == kMoeDown) {
-              const int route = kRouted ? static_cast<int>(row)
-                                        : min(max(a.sorted_routes[row], 0), a.rows_total - 1);
-              static_cast<float*>(a.out)[o] = v * a.aux[route];
-            }
+      for (int i = 0; i < 4; ++i) {
+        const int m = m0 + 16 * mb + 4 * g + i;
+        const bool ok = mb < nmb && m < M;
+        const long long row = ok ? (kRouted ? rlist[m] : row_begin + m) : -1;
+        orow[mb][i] = row;
+        const long long o = row * a.ldo + n;
+        in0[mb][i] = 0.f;
+        in1[mb][i] = 1.f;
+        if (ok) {
+          if (EPI == kResidAdd || EPI == kResidGated) in0[mb][i] = static_cast<const float*>(a.out)[o];
+          if (EPI == kResidGated) in1[mb][i] = a.aux[o];
+          if (EPI == kMoeDown) {
+            const int route = kRouted ? static_cast<int>(row)
+                                      : min(max(a.sorted_routes[row], 0), a.rows_total - 1);
+            in1[mb][i] = a.aux[route];
           }
+        }
+      }
+    }
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const long long row = orow[mb][i];
+        if (row < 0) continue;
+        const long long o = row * a.ldo + n;
+        const float v = acc[mb][i];
+        if (EPI == kStoreBf16) {
+          static_cast<uint16_t*>(a.out)[o] = f2bf(v);
+        } else if (EPI == kStoreF32) {
+          static_cast<float*>(a.out)[o] = v;
+        } else if (EPI == kResidAdd) {
+          static_cast<float*>(a.out)[o] = in0[mb][i] + v;
+        } else if (EPI == kResidGated) {
+          static_cast<float*>(a.out)[o] = in0[mb][i] + v * in1[mb][i];
+        } else if (EPI == kSwiGLU) {
+          static_cast<uint16_t*>(a.out)[o] = f2bf(siluf_(v) * accu[mb][i]);
+        } else if (EPI == kMoeDown) {
+          static_cast<float*>(a.out)[o] = v * in1[mb][i];
         }
       }
     }
   }
 }
 
-template <int EPI, int MODE, int MB, int KB = 1>
+template <int EPI, int MODE, int MB, int KB = 1, int JT = 8>
 static int32_t launch_ws(const WsArgs& a, int grid_y, bool packed, hipStream_t s) {
-  if (a.K % (256 * KB) != 0) return launch_ws<EPI, MODE, MB, 1>(a, grid_y, packed, s);
-  const int waves = std::max(1, std::min(8, a.K / (256 * KB)));
+  if (a.K % (32 * JT * KB) != 0) return launch_ws<EPI, MODE, MB, 1, 8>(a, grid_y, packed, s);
+  const int waves = std::max(1, std::min(8, a.K / (32 * JT * KB)));
   const size_t lds = waves > 1 ? static_cast<size_t>(waves) * (EPI == kSwiGLU ? 2 : 1) * MB * 4 *
                                      64 * sizeof(float)
                                : 0;
   const dim3 grid(a.N / 16, grid_y), block(64 * waves);
   if (packed)
-    hipLaunchKernelGGL((wsgemm_kernel<EPI, MODE, true, MB, KB>), grid, block, lds, s, a);
+    hipLaunchKernelGGL((wsgemm_kernel<EPI, MODE, true, MB, KB, JT>), grid, block, lds, s, a);
   else
-    hipLaunchKernelGGL((wsgemm_kernel<EPI, MODE, false, MB, KB>), grid, block, lds, s, a);
+    hipLaunchKernelGGL((wsgemm_kernel<EPI, MODE, false, MB, KB, JT>), grid, block, lds, s, a);
   return launch_status();
 }
 
@@ -488,8 +512,8 @@ extern "C" int32_t llmy_moe_experts_bf16(const llmy_bf16* x, const int32_t* offs
   b.sorted_routes = sorted_routes; b.w_expert_stride = static_cast<long long>(D) * H;
   b.N = D; b.K = H; b.ldx = H; b.ldo = D; b.route_k = k;
   b.rows_total = T * k; b.x_rows = T * k;
-  // Few routes per expert (decode): 16-row chunks, two K blocks per wave for
-  // the down projection; otherwise 64-row chunks.  (The route-indexed entry
+  // Few routes per expert (decode): 16-row chunks, half K blocks per wave
+  // (8 waves) for the down projection; otherwise 64-row chunks.  (The route-indexed entry
   // point uses the same configurations, so at these sizes the two agree bit
   // for bit.)
   int32_t st;
@@ -499,7 +523,7 @@ extern "C" int32_t llmy_moe_experts_bf16(const llmy_bf16* x, const int32_t* offs
   if (T * k <= 16 * E || !tiled_fits) {
     st = launch_ws<kSwiGLU, kMoeGather, 1>(a, E, packed, s);
     if (st != 0) return st;
-    return launch_ws<kMoeDown, kMoeDirect, 1, 2>(b, E, packed, s);
+    return launch_ws<kMoeDown, kMoeDirect, 1, 1, 4>(b, E, packed, s);
   }
   // Prefill: tiled MFMA grouped GEMMs (moe_gemm.hip).
   return moe_gemm_prefill(x, offsets, sorted_routes, gates, w_gate_up, w_down, act, y, T, D, H,
@@ -545,13 +569,10 @@ extern "C" int32_t llmy_moe_experts_routed_bf16(const llmy_bf16* x, const int32_
   b.N = D; b.K = H; b.ldx = H; b.ldo = D; b.route_k = k;
   b.rows_total = T * k; b.x_rows = T * k;
   int32_t st;
-  // The tiled path addresses each operand block with 32-bit byte offsets.
-  const bool tiled_fits = 2ll * T * D < (1ll << 31) && 2ll * T * k * H < (1ll << 31) &&
-                          4ll * H * D < (1ll << 31);
-  if (T * k <= 16 * E || !tiled_fits) {
+  if (T * k <= 16 * E) {
     st = launch_ws<kSwiGLU, kRouteGather, 1>(a, E, packed, s);
     if (st != 0) return st;
-    return launch_ws<kMoeDown, kRouteDirect, 1, 2>(b, E, packed, s);
+    return launch_ws<kMoeDown, kRouteDirect, 1, 1, 4>(b, E, packed, s);
   }
   st = launch_ws<kSwiGLU, kRouteGather, 4>(a, E, packed, s);
   if (st != 0) return st;

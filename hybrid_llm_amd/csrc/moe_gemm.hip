@@ -46,7 +46,7 @@
 
 namespace llmy {
 
-enum Mode : int { kGateUp = 0, kDown = 1, kDense = 2 };
+enum Mode : int { kTileGateUp = 0, kTileDown = 1, kTileDense = 2 };
 // Dense epilogues (values of the linear entry's epilogue argument).
 enum DenseEpi : int { kDenseBf16 = 0, kDenseF32 = 1, kDenseResid = 2, kDenseGated = 3 };
 
@@ -153,7 +153,7 @@ __global__ __launch_bounds__(kThreads, OCC) void tile_gemm_kernel(TileArgs a) {
   constexpr int NF = FA + FB;  // fragment reads per k-step
   static_assert(FA == 2 || FA == 4, "wavefront rows");
   static_assert(FB == 2 || FB == 4, "wavefront columns");
-  static_assert(MODE != kGateUp || FB % 2 == 0, "gate/up halves");
+  static_assert(MODE != kTileGateUp || FB % 2 == 0, "gate/up halves");
   static_assert(BK == 32 || BK == 64, "K tile");
   static_assert(NS >= 2 && DPT * (NS - 2) <= 63, "vmcnt range");
   __shared__ int s_work[3];  // expert, m0, n-tile (or -1: no work)
@@ -166,7 +166,7 @@ __global__ __launch_bounds__(kThreads, OCC) void tile_gemm_kernel(TileArgs a) {
   const int nblk = gridDim.x;
   const int per_xcd = (nblk + kNumXcd - 1) / kNumXcd;
   const int w_item = (blockIdx.x % kNumXcd) * per_xcd + blockIdx.x / kNumXcd;
-  if (MODE == kDense) {
+  if (MODE == kTileDense) {
     if (tid == 0) {
       const bool ok = w_item < a.m_tiles * a.n_tiles;
       int mt = w_item % a.m_tiles, nt = w_item / a.m_tiles;
@@ -225,9 +225,9 @@ __global__ __launch_bounds__(kThreads, OCC) void tile_gemm_kernel(TileArgs a) {
   const int e = s_work[0];
   if (e < 0) return;
   const int m0 = s_work[1], ntile = s_work[2];
-  const int row_lo = MODE == kDense ? 0 : min(max(a.offsets[e], 0), a.rows_total);
+  const int row_lo = MODE == kTileDense ? 0 : min(max(a.offsets[e], 0), a.rows_total);
   const int rows_e =
-      MODE == kDense ? a.rows_total : min(max(a.offsets[e + 1], row_lo), a.rows_total) - row_lo;
+      MODE == kTileDense ? a.rows_total : min(max(a.offsets[e + 1], row_lo), a.rows_total) - row_lo;
   const int K = a.K;
   const int nk = K / BK;
 
@@ -251,7 +251,7 @@ __global__ __launch_bounds__(kThreads, OCC) void tile_gemm_kernel(TileArgs a) {
     const int m = min(m0 + r, rows_e - 1);              // past the rows: repeat the last
     const int p = row_lo + m;
     long long src;
-    if (MODE == kGateUp) {
+    if (MODE == kTileGateUp) {
       src = min(max(a.sorted_routes[p], 0), a.rows_total - 1) / a.route_k;
       src = min(src, static_cast<long long>(a.x_rows - 1));
     } else {
@@ -266,13 +266,13 @@ __global__ __launch_bounds__(kThreads, OCC) void tile_gemm_kernel(TileArgs a) {
     const int r = RPI * (B_INS * wave + q) + dma_row;  // tile row
     long long off = 0;
     int n;
-    if (MODE == kGateUp) {
+    if (MODE == kTileGateUp) {
       // wavefront column c = r / WN holds [gate cols | up cols] of output
       // columns (BN/2) ntile + (WN/2) c + 0 .. WN/2 - 1
       const int c = r / WN, rr = r % WN;
       n = (BN / 2) * ntile + (WN / 2) * c + rr % (WN / 2);
       if (rr >= WN / 2) off = a.up_offset;
-    } else if (MODE == kDown) {
+    } else if (MODE == kTileDown) {
       n = BN * ntile + r;
     } else {
       n = min(BN * ntile + r, a.N - 1);  // N tail: repeat the last row
@@ -434,7 +434,7 @@ __global__ __launch_bounds__(kThreads, OCC) void tile_gemm_kernel(TileArgs a) {
     const int m = m0 + WM * wm + 32 * i + (lane & 31);
     if (m >= rows_e) continue;
     const long long p = row_lo + m;
-    if (MODE == kGateUp) {
+    if (MODE == kTileGateUp) {
       uint16_t* act = static_cast<uint16_t*>(a.out) + p * a.ldo;
 #pragma unroll
       for (int j = 0; j < FB / 2; ++j)
@@ -449,7 +449,7 @@ __global__ __launch_bounds__(kThreads, OCC) void tile_gemm_kernel(TileArgs a) {
           }
           *reinterpret_cast<uint2*>(act + c) = make_uint2(pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3]));
         }
-    } else if (MODE == kDown) {
+    } else if (MODE == kTileDown) {
       const int route = min(max(a.sorted_routes[p], 0), a.rows_total - 1);
       const float gs = a.gates[route];
       float* y = static_cast<float*>(a.out) + p * a.ldo;
@@ -463,8 +463,24 @@ __global__ __launch_bounds__(kThreads, OCC) void tile_gemm_kernel(TileArgs a) {
                           acc[i][j][4 * g4 + 2] * gs, acc[i][j][4 * g4 + 3] * gs);
         }
     } else {
+      // Residual epilogues load a column block's residual (and gate) groups
+      // before its first store: a store and a later load of another group
+      // cannot be proved apart, so interleaving them would serialise one
+      // memory round trip per group.
 #pragma unroll
-      for (int j = 0; j < FB; ++j)
+      for (int j = 0; j < FB; ++j) {
+        float4 res[4], gat[4];
+#pragma unroll
+        for (int g4 = 0; g4 < 4; ++g4) {
+          const int n = BN * ntile + WN * wn + 32 * j + 8 * g4 + 4 * (lane >> 5);
+          const long long o = p * a.ldo + n;
+          res[g4] = make_float4(0.f, 0.f, 0.f, 0.f);
+          gat[g4] = make_float4(1.f, 1.f, 1.f, 1.f);
+          if (n < a.N && (EPI == kDenseResid || EPI == kDenseGated))
+            res[g4] = *reinterpret_cast<const float4*>(static_cast<const float*>(a.out) + o);
+          if (n < a.N && EPI == kDenseGated)
+            gat[g4] = *reinterpret_cast<const float4*>(a.aux + o);
+        }
 #pragma unroll
         for (int g4 = 0; g4 < 4; ++g4) {
           const int n = BN * ntile + WN * wn + 32 * j + 8 * g4 + 4 * (lane >> 5);
@@ -478,18 +494,16 @@ __global__ __launch_bounds__(kThreads, OCC) void tile_gemm_kernel(TileArgs a) {
           } else if (EPI == kDenseF32) {
             *reinterpret_cast<float4*>(static_cast<float*>(a.out) + o) = make_float4(v0, v1, v2, v3);
           } else if (EPI == kDenseResid) {
-            float4* op = reinterpret_cast<float4*>(static_cast<float*>(a.out) + o);
-            float4 r = *op;
-            r.x += v0; r.y += v1; r.z += v2; r.w += v3;
-            *op = r;
+            const float4 r = res[g4];
+            *reinterpret_cast<float4*>(static_cast<float*>(a.out) + o) =
+                make_float4(r.x + v0, r.y + v1, r.z + v2, r.w + v3);
           } else {
-            float4* op = reinterpret_cast<float4*>(static_cast<float*>(a.out) + o);
-            const float4 g = *reinterpret_cast<const float4*>(a.aux + o);
-            float4 r = *op;
-            r.x += v0 * g.x; r.y += v1 * g.y; r.z += v2 * g.z; r.w += v3 * g.w;
-            *op = r;
+            const float4 r = res[g4], g = gat[g4];
+            *reinterpret_cast<float4*>(static_cast<float*>(a.out) + o) =
+                make_float4(r.x + v0 * g.x, r.y + v1 * g.y, r.z + v2 * g.z, r.w + v3 * g.w);
           }
         }
+      }
     }
   }
 }
@@ -533,7 +547,7 @@ int32_t moe_gemm_prefill(const uint16_t* x, const int32_t* offsets, const int32_
   g.packed = packed;
   // Two workgroups per CU (one wavefront of each per SIMD): one's barrier and
   // load waits are covered by the other's MFMAs.  gate_up: 3 stages of K 32.
-  int32_t st = launch_tiles<kGateUp, BM, 256, 32, 3, 0, 2>(g, max_mtiles * g.n_tiles, s);
+  int32_t st = launch_tiles<kTileGateUp, BM, 256, 32, 3, 0, 2>(g, max_mtiles * g.n_tiles, s);
   if (st != 0) return st;
   TileArgs d = g;
   d.x = act;
@@ -546,7 +560,7 @@ int32_t moe_gemm_prefill(const uint16_t* x, const int32_t* offsets, const int32_
   d.ldo = D;
   d.x_rows = rows_total;
   d.n_tiles = D / 128;
-  return launch_tiles<kDown, BM, 128, 64, 2, 0, 2>(d, max_mtiles * d.n_tiles, s);
+  return launch_tiles<kTileDown, BM, 128, 64, 2, 0, 2>(d, max_mtiles * d.n_tiles, s);
 }
 
 // Dense out[M, N] (epilogue epi) = x[M, K] . w[N, K]^T.  Validated by the
@@ -582,10 +596,10 @@ int32_t dense_gemm_mfma(const uint16_t* x, const uint16_t* w, void* out, const f
   if (items >= (1ll << 31) - kNumXcd) return static_cast<int32_t>(hipErrorInvalidValue);
 #define LLMY_DENSE(T_, OCC_)                                                                 \
   switch (epi) {                                                                             \
-    case kDenseBf16: return launch_tiles<kDense, T_, T_, 64, 2, kDenseBf16, OCC_>(g, items, s); \
-    case kDenseF32: return launch_tiles<kDense, T_, T_, 64, 2, kDenseF32, OCC_>(g, items, s);   \
-    case kDenseResid: return launch_tiles<kDense, T_, T_, 64, 2, kDenseResid, OCC_>(g, items, s); \
-    default: return launch_tiles<kDense, T_, T_, 64, 2, kDenseGated, OCC_>(g, items, s);        \
+    case kDenseBf16: return launch_tiles<kTileDense, T_, T_, 64, 2, kDenseBf16, OCC_>(g, items, s); \
+    case kDenseF32: return launch_tiles<kTileDense, T_, T_, 64, 2, kDenseF32, OCC_>(g, items, s);   \
+    case kDenseResid: return launch_tiles<kTileDense, T_, T_, 64, 2, kDenseResid, OCC_>(g, items, s); \
+    default: return launch_tiles<kTileDense, T_, T_, 64, 2, kDenseGated, OCC_>(g, items, s);        \
   }
   if (wide) LLMY_DENSE(256, 1)
   LLMY_DENSE(128, 2)

@@ -220,8 +220,18 @@ def test_prefill_with_sampling_and_validation():
     want, margin = top_p_sample(lg.cpu(), 0.8, torch.tensor(0.9).item(),
                                 torch.tensor([0.1, 0.5, 0.9]), return_margin=True)
     got = eng.buf["sampled"].cpu().numpy()
-    sure = margin > 4e-6       # decisions further than the kernel's mass error from a flip
-    assert sure.any() and np.array_equal(got[sure], want[sure])
+    # Decisions further than the kernel's cumulative-mass error (4e-6) from a
+    # flip must match exactly; near-uniform random-init logits put most draws
+    # within that of a step, and those may land on the neighbouring id in order.
+    x = lg.cpu().double().numpy()
+    for r in range(B):
+        if margin[r] > 4e-6:
+            assert got[r] == want[r], (r, got[r], want[r])
+        else:
+            order = np.lexsort((np.arange(x.shape[1]), -x[r]))
+            pos = np.empty_like(order)
+            pos[order] = np.arange(order.size)
+            assert abs(int(pos[got[r]]) - int(pos[want[r]])) <= 1, (r, got[r], want[r])
     with pytest.raises(ValueError):
         eng.prefill(tokens[:2].cuda())
     with pytest.raises(ValueError):
