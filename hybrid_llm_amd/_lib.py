@@ -52,6 +52,32 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
                                        _P]),
     "llmy_gdn_gate_bf16": (_I, [_P, _P, _I64, _I, _P, _I, _I, _P]),
     "llmy_gdn_conv_gate_prefill": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _P]),
+    # engine handles (the reference binding's argtypes, llmy_cuda/python/sample.py:110-170)
+    "llmy_load": (_P, [C.c_char_p]),
+    "llmy_free": (None, [_P]),
+    "llmy_vocab_size": (_I, [_P]),
+    "llmy_d_model": (_I, [_P]),
+    "llmy_num_loops": (_I, [_P]),
+    "llmy_max_loops": (_I, [_P]),
+    "llmy_mhc_streams": (_I, [_P]),
+    "llmy_set_num_loops": (None, [_P, _I]),
+    "llmy_set_fixed_loops": (None, [_P, _I]),
+    "llmy_state_new": (_P, [_P]),
+    "llmy_state_free": (None, [_P]),
+    "llmy_state_reset": (None, [_P]),
+    "llmy_prefill": (None, [_P, _P, C.POINTER(C.c_int32), _I, C.POINTER(C.c_float)]),
+    "llmy_decode": (None, [_P, _P, _I, _I, _I, C.POINTER(C.c_float)]),
+    "llmy_sample": (_I, [C.POINTER(C.c_float), _I, _F, _I, _F, _F, C.POINTER(C.c_int32), _I,
+                         C.POINTER(C.c_uint64)]),
+    "llmy_last_executed_loops": (_I, [_P]),
+    "llmy_sync": (None, []),
+    "llmy_state_new_batch": (_P, [_P, _I]),
+    "llmy_prefill_batch": (_I, [_P, _P, _P, _I, _P]),
+    "llmy_decode_batch": (_I, [_P, _P, _P, _P, _I, _P]),
+    "llmy_greedy_tokens": (_I, [_P, _P]),
+    "llmy_last_status": (_I, []),
+    "llmy_last_error": (C.c_char_p, []),
+    "llmy_checkpoint_describe": (_I, [C.c_char_p, C.c_char_p, _I64]),
     "llmy_rmsnorm_f32_bf16": (_I, [_P, _P, _P, _I, _I, _F, _P]),
     "llmy_embed_bf16": (_I, [_P, _P, _P, _I, _I, _I, _P]),
 }

@@ -1,0 +1,188 @@
+"""`.llmy` v1 checkpoint files for the hybrid block stack: writer and reader.
+
+The container is the reference engine's flat format
+(llmy_cuda/tools/convert_checkpoint.py:1-31,42-47,205-236 writes it,
+llmy_cuda/src/checkpoint.cpp:103-170 parses it):
+
+    offset 0   magic "LLMY"
+    4          u32 version = 1
+    8          u32 cfg_len, then cfg_len bytes of UTF-8 `key=value` lines
+    ...        u32 n_tensors, then n_tensors index entries of 108 bytes:
+               <I 64s I I 4I Q Q> = name_len, name (NUL padded), dtype
+               (0 f32, 1 f16, 2 bf16), ndim, shape[4], offset, nbytes
+    data_start the first multiple of 4096 after the index; each entry's
+               offset is relative to it
+
+Tensor names and config keys follow the reference model's where the concept
+is the same (`embed_tokens.weight`, `recurrent_core.<i>.mixer_norm.weight`,
+GDN `q_proj/k_proj/v_proj/gate_proj/beta_proj/out_proj/conv/decay_logit`,
+MoE `router.norm/router.logits` and expert stacks `[E, H, D]`; `gdn.*` and
+`moe.*` keys).  The banded attention mixer of this block stack has no
+reference counterpart with the same weights, so its layout entry is `attn`
+and its keys are `attn.heads`, `attn.head_dim`, `attn.window`.
+
+The native loader `llmy_load` (hybrid_llm_amd/csrc/engine.cpp) reads the same
+files; this module writes them from `config.init_weights`-style dicts and
+reads them back for tests.
+"""
+from __future__ import annotations
+
+import struct
+from pathlib import Path
+
+import numpy as np
+import torch
+
+from .config import HybridConfig
+
+MAGIC = b"LLMY"
+VERSION = 1
+INDEX_ENTRY = struct.Struct("<I64sII4IQQ")
+assert INDEX_ENTRY.size == 108
+DATA_ALIGN = 4096
+DTYPES = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
+DTYPE_OF = {v: k for k, v in DTYPES.items()}
+ITEMSIZE = {0: 4, 1: 2, 2: 2}
+
+_GDN = {"wq": "q_proj.weight", "wk": "k_proj.weight", "wv": "v_proj.weight",
+        "wg": "gate_proj.weight", "wb": "beta_proj.weight", "bb": "beta_proj.bias",
+        "wout": "out_proj.weight", "conv": "conv.weight", "decay": "decay_logit"}
+_ATTN = {"wq": "q.weight", "wk": "k.weight", "wv": "v.weight", "wo": "o.weight"}
+_BLOCK = {"mix_norm": "mixer_norm.weight", "ffn_norm": "ffn_norm.weight",
+          "router_norm": "moe.router.norm.weight", "w_router": "moe.router.logits.weight",
+          "w_gate": "moe.experts.gate_proj.weight", "w_up": "moe.experts.up_proj.weight",
+          "w_down": "moe.experts.down_proj.weight"}
+
+
+def file_name(cfg: HybridConfig, key: str) -> str:
+    """The `.llmy` tensor name of a `config.weight_shapes` key."""
+    if key == "embed":
+        return "embed_tokens.weight"
+    if key == "final_norm":
+        return "final_norm.weight"
+    layer, short = key.split(".", 1)
+    l = int(layer[1:])
+    p = f"recurrent_core.{l}."
+    if short in _BLOCK:
+        return p + _BLOCK[short]
+    table = _ATTN if cfg.layer_kinds[l] == "attn" else _GDN
+    return p + "mixer." + table[short]
+
+
+def config_text(cfg: HybridConfig) -> str:
+    keys = {
+        "vocab_size": cfg.vocab, "d_model": cfg.d_model, "num_loops": cfg.num_loops,
+        "stem_blocks": 0, "tail_blocks": 0, "recurrent_blocks": cfg.n_layers,
+        "recurrent_layout": ",".join(cfg.layer_kinds), "mhc.enabled": 0,
+        "attn.heads": cfg.attn_heads, "attn.head_dim": cfg.attn_head_dim,
+        "attn.window": cfg.window,
+        "gdn.qk_heads": cfg.gdn_heads, "gdn.value_heads": cfg.gdn_heads,
+        "gdn.qk_head_dim": cfg.gdn_dk, "gdn.value_head_dim": cfg.gdn_dv,
+        "gdn.conv_kernel": cfg.conv_kernel,
+        "moe.routed_experts": cfg.n_experts, "moe.routed_top_k": cfg.top_k,
+        "moe.expert_hidden": cfg.expert_hidden, "moe.shared_experts": 0,
+        "rms_norm_eps": repr(float(cfg.eps)),
+    }
+    return "".join(f"{k}={keys[k]}\n" for k in sorted(keys))
+
+
+def config_from_text(text: str) -> HybridConfig:
+    kv = dict(line.split("=", 1) for line in text.splitlines() if "=" in line)
+    kinds = tuple(kv["recurrent_layout"].split(","))
+    if int(kv.get("stem_blocks", 0)) or int(kv.get("tail_blocks", 0)):
+        raise ValueError("stem/tail blocks are not part of this block stack")
+    if int(kv.get("moe.shared_experts", 0)):
+        raise ValueError("shared experts are not part of this block stack")
+    if kv.get("gdn.qk_heads") != kv.get("gdn.value_heads"):
+        raise ValueError("GDN q/k and value head counts must match")
+    return HybridConfig(
+        d_model=int(kv["d_model"]), layer_kinds=kinds, attn_heads=int(kv["attn.heads"]),
+        attn_head_dim=int(kv["attn.head_dim"]), window=int(kv["attn.window"]),
+        gdn_heads=int(kv["gdn.qk_heads"]), gdn_dk=int(kv["gdn.qk_head_dim"]),
+        gdn_dv=int(kv["gdn.value_head_dim"]), n_experts=int(kv["moe.routed_experts"]),
+        top_k=int(kv["moe.routed_top_k"]), expert_hidden=int(kv["moe.expert_hidden"]),
+        vocab=int(kv["vocab_size"]), num_loops=int(kv["num_loops"]),
+        conv_kernel=int(kv.get("gdn.conv_kernel", 4)), eps=float(kv.get("rms_norm_eps", 1e-6)))
+
+
+def save_llmy(path: str | Path, cfg: HybridConfig, weights: dict[str, torch.Tensor]) -> None:
+    """Write ``weights`` (keys of `config.weight_shapes`) as a `.llmy` v1 file.
+    The depthwise conv is stored as nn.Conv1d's [D, 1, K]."""
+    from .config import weight_shapes
+    entries = []
+    for key, shape, _ in weight_shapes(cfg):
+        t = weights[key].detach().to("cpu").contiguous()
+        if tuple(t.shape) != tuple(shape):
+            raise ValueError(f"{key}: shape {tuple(t.shape)} != {shape}")
+        if key.endswith(".conv"):
+            t = t.view(shape[0], 1, shape[1])
+        entries.append((file_name(cfg, key), t))
+    entries.sort(key=lambda e: e[0])
+    cfg_b = config_text(cfg).encode()
+    head = MAGIC + struct.pack("<II", VERSION, len(cfg_b)) + cfg_b + struct.pack("<I", len(entries))
+    index_end = len(head) + INDEX_ENTRY.size * len(entries)
+    data_start = (index_end + DATA_ALIGN - 1) // DATA_ALIGN * DATA_ALIGN
+    index, blobs, off = [], [], 0
+    for name, t in entries:
+        if t.dtype not in DTYPES:
+            raise ValueError(f"{name}: unsupported dtype {t.dtype}")
+        blob = t.view(torch.uint8).numpy().tobytes() if t.dtype == torch.bfloat16 else t.numpy().tobytes()
+        nb = name.encode()
+        if len(nb) > 63 or t.dim() > 4:
+            raise ValueError(f"{name}: name longer than 63 bytes or more than 4 dims")
+        shape4 = list(t.shape) + [0] * (4 - t.dim())
+        index.append(INDEX_ENTRY.pack(len(nb), nb.ljust(64, b"\0"), DTYPES[t.dtype], t.dim(),
+                                      *shape4, off, len(blob)))
+        blobs.append(blob)
+        off += len(blob)
+    with open(path, "wb") as f:
+        f.write(head)
+        f.write(b"".join(index))
+        f.write(b"\0" * (data_start - index_end))
+        for blob in blobs:
+            f.write(blob)
+
+
+def read_llmy(path: str | Path) -> tuple[str, dict[str, torch.Tensor]]:
+    """(config text, {name: tensor}) of a `.llmy` v1 file, with the bounds
+    checks of the native reader."""
+    data = Path(path).read_bytes()
+    if data[:4] != MAGIC:
+        raise ValueError("not an .llmy file (bad magic)")
+    version, cfg_len = struct.unpack_from("<II", data, 4)
+    if version != VERSION:
+        raise ValueError(f"unsupported .llmy version {version}")
+    p = 12 + cfg_len
+    text = data[12:p].decode()
+    (n,) = struct.unpack_from("<I", data, p)
+    p += 4
+    index_end = p + n * INDEX_ENTRY.size
+    if index_end > len(data):
+        raise ValueError("truncated index")
+    data_start = (index_end + DATA_ALIGN - 1) // DATA_ALIGN * DATA_ALIGN
+    out = {}
+    for i in range(n):
+        nl, name, dt, nd, s0, s1, s2, s3, off, nbytes = INDEX_ENTRY.unpack_from(data, p + i * 108)
+        if nl > 63 or nd > 4:
+            raise ValueError("bad index entry (name length or rank)")
+        name = name[:nl].decode()
+        shape = (s0, s1, s2, s3)[:nd]
+        if dt not in DTYPE_OF or nbytes != int(np.prod(shape, dtype=np.int64)) * ITEMSIZE[dt]:
+            raise ValueError(f"{name}: bad dtype or size")
+        if data_start + off + nbytes > len(data):
+            raise ValueError(f"{name}: payload out of the file")
+        raw = torch.frombuffer(bytearray(data[data_start + off:data_start + off + nbytes]),
+                               dtype=torch.uint8)
+        out[name] = raw.view(DTYPE_OF[dt]).view(shape)
+    return text, out
+
+
+def load_weights(path: str | Path) -> tuple[HybridConfig, dict[str, torch.Tensor]]:
+    """Config and `config.weight_shapes`-keyed weights of a `.llmy` file."""
+    from .config import weight_shapes
+    text, tensors = read_llmy(path)
+    cfg = config_from_text(text)
+    w = {}
+    for key, shape, _ in weight_shapes(cfg):
+        w[key] = tensors[file_name(cfg, key)].reshape(shape)
+    return cfg, w

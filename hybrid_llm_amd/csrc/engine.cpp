@@ -1,0 +1,972 @@
+// Native engine behind the reference's engine C API (llmy_cuda/include/llmy.h:31-72):
+// llmy_load / llmy_free, introspection, state handles, llmy_prefill,
+// llmy_decode, llmy_sample, llmy_last_executed_loops, llmy_sync, plus batched
+// forms of prefill/decode and a status query.
+//
+// The model handle owns the device weights, the state handle the per
+// (loop, layer) KV caches, GDN states and conv histories and every
+// activation buffer, as the reference's Model and State do
+// (llmy_cuda/include/model.h:143-267).  The reference engine is batch-1 and
+// fp32 (llmy_cuda/src/model.cpp:627); this one runs B sequences per state in
+// bf16 through the same kernels as hybrid_llm_amd/engine.py:
+//   decode  = embedding + pre-norm, then per (loop, layer) the attention or GDN
+//             mixer and the MoE (fused router, route-indexed experts, combine
+//             fused with the next pre-norm), the tied LM head;
+//   prefill = the same blocks over all B*T prompt tokens with the sequence
+//             kernels (banded attention prefill + KV ring fill, GDN input
+//             preparation + chunked scan + output gate + sequence conv gate,
+//             router + permutation + grouped expert GEMMs), from position 0.
+// Weights come from a `.llmy` v1 file (format of
+// llmy_cuda/tools/convert_checkpoint.py:1-31; parsed here with bounds checks
+// on every index entry) through mmap.
+//
+// No C++ exception leaves the C ABI: each entry point catches, records the
+// message (llmy_last_status / llmy_last_error) and returns NULL or a nonzero
+// status, where the reference would have let a throw escape
+// (llmy_cuda/src/llmy.cpp:116-131).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <memory>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include <fcntl.h>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
+#include "llmy.h"
+
+namespace {
+
+thread_local int32_t g_status = 0;
+thread_local char g_error[512] = "";
+
+void set_error(int32_t st, const char* msg) {
+  g_status = st;
+  std::snprintf(g_error, sizeof(g_error), "%s", msg);
+}
+
+void check_hip(hipError_t e, const char* what) {
+  if (e != hipSuccess)
+    throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(e));
+}
+
+void check_call(int32_t st, const char* what) {
+  if (st != 0) throw std::runtime_error(std::string(what) + " returned status " + std::to_string(st));
+}
+
+// ------------------------------------------------------------------ .llmy reader
+constexpr uint32_t kVersion = 1;
+constexpr size_t kEntry = 108;
+constexpr size_t kAlign = 4096;
+
+struct TensorRef {
+  uint32_t dtype = 0;  // 0 f32, 1 f16, 2 bf16
+  std::vector<int64_t> shape;
+  const unsigned char* data = nullptr;
+  uint64_t nbytes = 0;
+  int64_t numel() const {
+    int64_t n = 1;
+    for (int64_t s : shape) n *= s;
+    return n;
+  }
+};
+
+struct MappedFile {
+  void* base = MAP_FAILED;
+  size_t size = 0;
+  ~MappedFile() {
+    if (base != MAP_FAILED) munmap(base, size);
+  }
+};
+
+struct Checkpoint {
+  MappedFile file;
+  std::string config;
+  std::map<std::string, TensorRef> tensors;
+
+  const TensorRef& get(const std::string& name) const {
+    auto it = tensors.find(name);
+    if (it == tensors.end()) throw std::runtime_error("checkpoint has no tensor " + name);
+    return it->second;
+  }
+};
+
+template <typename T>
+T read_le(const unsigned char* p) {
+  T v;
+  std::memcpy(&v, p, sizeof(T));
+  return v;
+}
+
+void parse_checkpoint(const char* path, Checkpoint& ck) {
+  const int fd = open(path, O_RDONLY);
+  if (fd < 0) throw std::runtime_error(std::string("cannot open ") + path);
+  struct stat st {};
+  if (fstat(fd, &st) != 0) {
+    close(fd);
+    throw std::runtime_error("cannot stat checkpoint");
+  }
+  ck.file.size = static_cast<size_t>(st.st_size);
+  ck.file.base = ck.file.size ? mmap(nullptr, ck.file.size, PROT_READ, MAP_PRIVATE, fd, 0) : MAP_FAILED;
+  close(fd);
+  if (ck.file.base == MAP_FAILED) throw std::runtime_error("cannot map checkpoint");
+  const auto* b = static_cast<const unsigned char*>(ck.file.base);
+  const size_t n = ck.file.size;
+  if (n < 16 || std::memcmp(b, "LLMY", 4) != 0) throw std::runtime_error("bad magic");
+  if (read_le<uint32_t>(b + 4) != kVersion) throw std::runtime_error("unsupported version");
+  const uint64_t cfg_len = read_le<uint32_t>(b + 8);
+  if (12 + cfg_len + 4 > n) throw std::runtime_error("truncated config");
+  ck.config.assign(reinterpret_cast<const char*>(b + 12), cfg_len);
+  const uint64_t count = read_le<uint32_t>(b + 12 + cfg_len);
+  const uint64_t index = 16 + cfg_len;
+  const uint64_t index_end = index + count * kEntry;
+  if (index_end > n) throw std::runtime_error("truncated index");
+  const uint64_t data_start = (index_end + kAlign - 1) / kAlign * kAlign;
+  for (uint64_t i = 0; i < count; ++i) {
+    const unsigned char* e = b + index + i * kEntry;
+    const uint32_t name_len = read_le<uint32_t>(e);
+    if (name_len > 63) throw std::runtime_error("bad tensor name length");
+    TensorRef t;
+    std::string name(reinterpret_cast<const char*>(e + 4), name_len);
+    t.dtype = read_le<uint32_t>(e + 68);
+    const uint32_t ndim = read_le<uint32_t>(e + 72);
+    if (t.dtype > 2 || ndim > 4) throw std::runtime_error("bad dtype or rank for " + name);
+    for (uint32_t d = 0; d < ndim; ++d) t.shape.push_back(read_le<uint32_t>(e + 76 + 4 * d));
+    const uint64_t off = read_le<uint64_t>(e + 92);
+    t.nbytes = read_le<uint64_t>(e + 100);
+    const uint64_t item = t.dtype == 0 ? 4 : 2;
+    if (t.nbytes != static_cast<uint64_t>(t.numel()) * item)
+      throw std::runtime_error("size does not match shape for " + name);
+    if (data_start > n || off > n - data_start || t.nbytes > n - data_start - off)
+      throw std::runtime_error("payload outside the file for " + name);
+    t.data = b + data_start + off;
+    ck.tensors[name] = t;
+  }
+}
+
+std::map<std::string, std::string> parse_config(const std::string& text) {
+  std::map<std::string, std::string> kv;
+  size_t p = 0;
+  while (p < text.size()) {
+    size_t e = text.find('\n', p);
+    if (e == std::string::npos) e = text.size();
+    const std::string line = text.substr(p, e - p);
+    const size_t eq = line.find('=');
+    if (eq != std::string::npos) kv[line.substr(0, eq)] = line.substr(eq + 1);
+    p = e + 1;
+  }
+  return kv;
+}
+
+// ------------------------------------------------------------------ model
+enum Kind { kAttn = 0, kGdn = 1 };
+
+struct Config {
+  int vocab = 0, d_model = 0, num_loops = 0;
+  std::vector<int> kinds;
+  int attn_heads = 0, attn_head_dim = 0, window = 0;
+  int gdn_heads = 0, dk = 0, dv = 0, conv_kernel = 4;
+  int experts = 0, top_k = 0, hidden = 0;
+  float eps = 1e-6f;
+  int nproj16() const {
+    const int n = 2 * gdn_heads * dk + 2 * gdn_heads * dv + gdn_heads;
+    return (n + 15) / 16 * 16;
+  }
+};
+
+int cfg_int(const std::map<std::string, std::string>& kv, const char* key, int dflt, bool need) {
+  auto it = kv.find(key);
+  if (it == kv.end()) {
+    if (need) throw std::runtime_error(std::string("config lacks ") + key);
+    return dflt;
+  }
+  return std::stoi(it->second);
+}
+
+Config config_from(const std::string& text) {
+  const auto kv = parse_config(text);
+  Config c;
+  c.vocab = cfg_int(kv, "vocab_size", 0, true);
+  c.d_model = cfg_int(kv, "d_model", 0, true);
+  c.num_loops = cfg_int(kv, "num_loops", 1, true);
+  if (cfg_int(kv, "stem_blocks", 0, false) || cfg_int(kv, "tail_blocks", 0, false) ||
+      cfg_int(kv, "moe.shared_experts", 0, false) || cfg_int(kv, "mhc.enabled", 0, false))
+    throw std::runtime_error("stem/tail blocks, shared experts and mHC are not part of this engine");
+  auto lay = kv.find("recurrent_layout");
+  if (lay == kv.end()) throw std::runtime_error("config lacks recurrent_layout");
+  size_t p = 0;
+  const std::string& s = lay->second;
+  while (p <= s.size()) {
+    size_t e = s.find(',', p);
+    if (e == std::string::npos) e = s.size();
+    const std::string k = s.substr(p, e - p);
+    if (k == "attn") c.kinds.push_back(kAttn);
+    else if (k == "gdn") c.kinds.push_back(kGdn);
+    else throw std::runtime_error("unsupported block kind " + k);
+    p = e + 1;
+  }
+  const bool any_attn = std::count(c.kinds.begin(), c.kinds.end(), kAttn) > 0;
+  const bool any_gdn = std::count(c.kinds.begin(), c.kinds.end(), kGdn) > 0;
+  c.attn_heads = cfg_int(kv, "attn.heads", 0, any_attn);
+  c.attn_head_dim = cfg_int(kv, "attn.head_dim", 0, any_attn);
+  c.window = cfg_int(kv, "attn.window", 0, any_attn);
+  c.gdn_heads = cfg_int(kv, "gdn.qk_heads", 0, any_gdn);
+  if (any_gdn && cfg_int(kv, "gdn.value_heads", c.gdn_heads, false) != c.gdn_heads)
+    throw std::runtime_error("GDN q/k and value head counts must match");
+  c.dk = cfg_int(kv, "gdn.qk_head_dim", 0, any_gdn);
+  c.dv = cfg_int(kv, "gdn.value_head_dim", 0, any_gdn);
+  c.conv_kernel = cfg_int(kv, "gdn.conv_kernel", 4, false);
+  c.experts = cfg_int(kv, "moe.routed_experts", 0, true);
+  c.top_k = cfg_int(kv, "moe.routed_top_k", 0, true);
+  c.hidden = cfg_int(kv, "moe.expert_hidden", 0, true);
+  auto eps = kv.find("rms_norm_eps");
+  if (eps != kv.end()) c.eps = std::stof(eps->second);
+  if (c.kinds.empty() || c.num_loops < 1 || c.vocab < 1 || c.d_model % 256 != 0 ||
+      c.hidden % 256 != 0 || c.top_k < 1 || c.top_k > c.experts || c.conv_kernel != 4)
+    throw std::runtime_error("unsupported model shape");
+  return c;
+}
+
+float bf16_to_f32(uint16_t v) {
+  uint32_t u = static_cast<uint32_t>(v) << 16;
+  float f;
+  std::memcpy(&f, &u, 4);
+  return f;
+}
+
+uint16_t f32_to_bf16(float f) {  // round to nearest even, NaN kept quiet
+  uint32_t u;
+  std::memcpy(&u, &f, 4);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+float f16_to_f32(uint16_t h) {
+  const uint32_t s = (h >> 15) & 1u, e = (h >> 10) & 0x1fu, m = h & 0x3ffu;
+  float v;
+  if (e == 0) v = std::ldexp(static_cast<float>(m), -24);
+  else if (e == 31) v = m ? NAN : INFINITY;
+  else v = std::ldexp(static_cast<float>(m | 0x400u), static_cast<int>(e) - 25);
+  return s ? -v : v;
+}
+
+std::vector<float> as_f32(const TensorRef& t) {
+  std::vector<float> out(static_cast<size_t>(t.numel()));
+  for (size_t i = 0; i < out.size(); ++i) {
+    if (t.dtype == 0) std::memcpy(&out[i], t.data + 4 * i, 4);
+    else {
+      uint16_t v;
+      std::memcpy(&v, t.data + 2 * i, 2);
+      out[i] = t.dtype == 2 ? bf16_to_f32(v) : f16_to_f32(v);
+    }
+  }
+  return out;
+}
+
+std::vector<uint16_t> as_bf16(const TensorRef& t) {
+  std::vector<uint16_t> out(static_cast<size_t>(t.numel()));
+  if (t.dtype == 2) {
+    std::memcpy(out.data(), t.data, out.size() * 2);
+    return out;
+  }
+  const std::vector<float> f = as_f32(t);
+  for (size_t i = 0; i < out.size(); ++i) out[i] = f32_to_bf16(f[i]);
+  return out;
+}
+
+void expect_shape(const TensorRef& t, std::vector<int64_t> want, const std::string& name) {
+  if (t.shape != want) throw std::runtime_error("unexpected shape for " + name);
+}
+
+struct Layer {
+  int kind = kAttn;
+  float* mix_norm = nullptr;
+  float* ffn_norm = nullptr;
+  float* router_norm = nullptr;
+  float* w_router = nullptr;
+  uint16_t* wqkv = nullptr;  // packed [3 H hd, D]
+  uint16_t* wo = nullptr;    // packed [D, H hd]
+  uint16_t* wproj = nullptr; // packed [N16, D]
+  uint16_t* wout = nullptr;  // packed [D, H dv]
+  float* bb = nullptr;
+  float* conv = nullptr;     // [D, 4]
+  float* decay = nullptr;
+  uint16_t* w_gate_up = nullptr;  // packed per expert [E, 2H, D]
+  uint16_t* w_down = nullptr;     // packed per expert [E, D, H]
+};
+
+struct Model {
+  Config cfg;
+  int loops = 0;  // loops a forward runs by default (llmy_set_num_loops)
+  uint16_t* embed = nullptr;    // row-major [V, D] (token lookup)
+  uint16_t* lm_head = nullptr;  // packed copy (tied LM head)
+  float* final_norm = nullptr;
+  std::vector<Layer> layers;
+  std::vector<void*> allocs;
+
+  ~Model() {
+    for (void* p : allocs) (void)hipFree(p);
+  }
+  template <typename T>
+  T* alloc(size_t count) {
+    void* p = nullptr;
+    check_hip(hipMalloc(&p, std::max<size_t>(count, 1) * sizeof(T)), "hipMalloc (weights)");
+    allocs.push_back(p);
+    return static_cast<T*>(p);
+  }
+  template <typename T>
+  T* upload(const std::vector<T>& host) {
+    T* d = alloc<T>(host.size());
+    check_hip(hipMemcpy(d, host.data(), host.size() * sizeof(T), hipMemcpyHostToDevice),
+              "hipMemcpy (weights)");
+    return d;
+  }
+  // [batch, N, K] row-major bf16 -> device, re-laid in the packed operand order.
+  uint16_t* upload_packed(const std::vector<uint16_t>& host, int64_t batch, int N, int K) {
+    void* tmp = nullptr;
+    check_hip(hipMalloc(&tmp, host.size() * 2), "hipMalloc (staging)");
+    std::unique_ptr<void, void (*)(void*)> guard(tmp, [](void* p) { (void)hipFree(p); });
+    check_hip(hipMemcpy(tmp, host.data(), host.size() * 2, hipMemcpyHostToDevice), "hipMemcpy");
+    uint16_t* out = alloc<uint16_t>(host.size());
+    check_call(llmy_pack_weights_bf16(static_cast<const llmy_bf16*>(tmp), out, batch, N, K,
+                                      nullptr),
+               "llmy_pack_weights_bf16");
+    check_hip(hipDeviceSynchronize(), "pack");
+    return out;
+  }
+};
+
+std::vector<uint16_t> concat_rows(std::initializer_list<std::vector<uint16_t>> parts, size_t pad_to) {
+  std::vector<uint16_t> out;
+  for (const auto& p : parts) out.insert(out.end(), p.begin(), p.end());
+  out.resize(std::max(out.size(), pad_to), 0);
+  return out;
+}
+
+std::unique_ptr<Model> load_model(const char* path) {
+  Checkpoint ck;
+  parse_checkpoint(path, ck);
+  auto m = std::make_unique<Model>();
+  Config& c = m->cfg;
+  c = config_from(ck.config);
+  m->loops = c.num_loops;
+  const int D = c.d_model, V = c.vocab, E = c.experts, Hf = c.hidden;
+  const auto& emb = ck.get("embed_tokens.weight");
+  expect_shape(emb, {V, D}, "embed_tokens.weight");
+  const std::vector<uint16_t> embed = as_bf16(emb);
+  m->embed = m->upload(embed);
+  m->lm_head = m->upload_packed(embed, 1, V, D);
+  const auto& fn = ck.get("final_norm.weight");
+  expect_shape(fn, {D}, "final_norm.weight");
+  m->final_norm = m->upload(as_f32(fn));
+  for (size_t l = 0; l < c.kinds.size(); ++l) {
+    Layer L;
+    L.kind = c.kinds[l];
+    const std::string p = "recurrent_core." + std::to_string(l) + ".";
+    auto vec_f32 = [&](const std::string& n, std::vector<int64_t> shape) {
+      const auto& t = ck.get(p + n);
+      expect_shape(t, shape, p + n);
+      return m->upload(as_f32(t));
+    };
+    auto mat_bf16 = [&](const std::string& n, std::vector<int64_t> shape) {
+      const auto& t = ck.get(p + n);
+      expect_shape(t, shape, p + n);
+      return as_bf16(t);
+    };
+    L.mix_norm = vec_f32("mixer_norm.weight", {D});
+    L.ffn_norm = vec_f32("ffn_norm.weight", {D});
+    L.router_norm = vec_f32("moe.router.norm.weight", {D});
+    L.w_router = vec_f32("moe.router.logits.weight", {E, D});
+    if (L.kind == kAttn) {
+      const int W = c.attn_heads * c.attn_head_dim;
+      if (W % 16 != 0 || W % 256 != 0 || (c.attn_head_dim != 64 && c.attn_head_dim != 128))
+        throw std::runtime_error("unsupported attention shape");
+      const auto wqkv = concat_rows({mat_bf16("mixer.q.weight", {W, D}),
+                                     mat_bf16("mixer.k.weight", {W, D}),
+                                     mat_bf16("mixer.v.weight", {W, D})}, 0);
+      L.wqkv = m->upload_packed(wqkv, 1, 3 * W, D);
+      L.wo = m->upload_packed(mat_bf16("mixer.o.weight", {D, W}), 1, D, W);
+    } else {
+      const int H = c.gdn_heads, HK = H * c.dk, HV = H * c.dv;
+      if (HV % 256 != 0 || (c.dk != 64 && c.dk != 128) || c.dk != c.dv)
+        throw std::runtime_error("unsupported GDN shape");
+      const auto wproj = concat_rows({mat_bf16("mixer.q_proj.weight", {HK, D}),
+                                      mat_bf16("mixer.k_proj.weight", {HK, D}),
+                                      mat_bf16("mixer.v_proj.weight", {HV, D}),
+                                      mat_bf16("mixer.gate_proj.weight", {HV, D}),
+                                      mat_bf16("mixer.beta_proj.weight", {H, D})},
+                                     static_cast<size_t>(c.nproj16()) * D);
+      L.wproj = m->upload_packed(wproj, 1, c.nproj16(), D);
+      L.wout = m->upload_packed(mat_bf16("mixer.out_proj.weight", {D, HV}), 1, D, HV);
+      L.bb = vec_f32("mixer.beta_proj.bias", {H});
+      L.decay = vec_f32("mixer.decay_logit", {H});
+      const auto& cv = ck.get(p + "mixer.conv.weight");
+      if (cv.shape != std::vector<int64_t>{D, 1, 4} && cv.shape != std::vector<int64_t>{D, 4})
+        throw std::runtime_error("unexpected conv shape");
+      L.conv = m->upload(as_f32(cv));
+    }
+    const auto g = mat_bf16("moe.experts.gate_proj.weight", {E, Hf, D});
+    const auto u = mat_bf16("moe.experts.up_proj.weight", {E, Hf, D});
+    std::vector<uint16_t> gu(static_cast<size_t>(E) * 2 * Hf * D);
+    const size_t blk = static_cast<size_t>(Hf) * D;
+    for (int e = 0; e < E; ++e) {  // [E, 2H, D]: gate rows, then up rows
+      std::memcpy(gu.data() + 2 * e * blk, g.data() + e * blk, blk * 2);
+      std::memcpy(gu.data() + (2 * e + 1) * blk, u.data() + e * blk, blk * 2);
+    }
+    L.w_gate_up = m->upload_packed(gu, E, 2 * Hf, D);
+    L.w_down = m->upload_packed(mat_bf16("moe.experts.down_proj.weight", {E, D, Hf}), E, D, Hf);
+    m->layers.push_back(L);
+  }
+  return m;
+}
+
+// ------------------------------------------------------------------ state
+struct DeviceArena {
+  std::vector<void*> ptrs;
+  ~DeviceArena() { release(); }
+  void release() {
+    for (void* p : ptrs) (void)hipFree(p);
+    ptrs.clear();
+  }
+  template <typename T>
+  T* zeros(size_t count) {
+    void* p = nullptr;
+    const size_t bytes = std::max<size_t>(count, 1) * sizeof(T);
+    check_hip(hipMalloc(&p, bytes), "hipMalloc (state)");
+    ptrs.push_back(p);
+    check_hip(hipMemset(p, 0, bytes), "hipMemset (state)");
+    return static_cast<T*>(p);
+  }
+};
+
+struct LayerState {
+  uint16_t* k = nullptr;  // [B, H, W, hd]
+  uint16_t* v = nullptr;
+  float* S = nullptr;       // [B, H, dk, dv]
+  uint16_t* hist = nullptr; // [B, 3, D]
+  size_t k_bytes = 0, s_bytes = 0, hist_bytes = 0;
+};
+
+struct Buffers {  // activations for `rows` token rows
+  int rows = 0;
+  float *x = nullptr, *proj = nullptr, *cg = nullptr, *gates = nullptr, *y = nullptr;
+  float *beta = nullptr, *g = nullptr;
+  uint16_t *h = nullptr, *qkv = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *ao = nullptr,
+           *go = nullptr, *act = nullptr, *gq = nullptr, *gk = nullptr, *gv = nullptr;
+  int32_t *tokens = nullptr, *idx = nullptr, *counts = nullptr, *offsets = nullptr,
+          *sorted = nullptr, *route_pos = nullptr;
+  void* ws = nullptr;
+  int64_t ws_bytes = 0;
+  DeviceArena arena;
+};
+
+struct State {
+  Model* model = nullptr;
+  int B = 1;
+  int last_loops = 0;
+  std::vector<LayerState> layers;  // index loop * n_layers + layer
+  DeviceArena arena;
+  int32_t* pos = nullptr;    // [B] device: absolute position of the next token
+  float* logits = nullptr;   // [B, V]
+  int32_t* next = nullptr;   // [B]
+  Buffers step;              // decode: B rows
+  std::unique_ptr<Buffers> seq;  // prefill: B*T rows, grown on demand
+};
+
+void alloc_buffers(const Config& c, int rows, int B, int T, Buffers& b) {
+  const int D = c.d_model, k = c.top_k, E = c.experts;
+  b.rows = rows;
+  b.x = b.arena.zeros<float>(static_cast<size_t>(rows) * D);
+  b.h = b.arena.zeros<uint16_t>(static_cast<size_t>(rows) * D);
+  const int Hhd = c.attn_heads * c.attn_head_dim;
+  b.qkv = b.arena.zeros<uint16_t>(static_cast<size_t>(rows) * 3 * std::max(Hhd, 1));
+  b.q = b.qkv;
+  b.k = b.qkv + static_cast<size_t>(rows) * std::max(Hhd, 1);
+  b.v = b.qkv + 2 * static_cast<size_t>(rows) * std::max(Hhd, 1);
+  b.ao = b.arena.zeros<uint16_t>(static_cast<size_t>(rows) * std::max(Hhd, 1));
+  const int HK = c.gdn_heads * c.dk, HV = c.gdn_heads * c.dv;
+  b.proj = b.arena.zeros<float>(static_cast<size_t>(rows) * c.nproj16());
+  b.go = b.arena.zeros<uint16_t>(static_cast<size_t>(rows) * std::max(HV, 1));
+  b.cg = b.arena.zeros<float>(static_cast<size_t>(rows) * D);
+  b.gq = b.arena.zeros<uint16_t>(static_cast<size_t>(rows) * std::max(HK, 1));
+  b.gk = b.arena.zeros<uint16_t>(static_cast<size_t>(rows) * std::max(HK, 1));
+  b.gv = b.arena.zeros<uint16_t>(static_cast<size_t>(rows) * std::max(HV, 1));
+  b.beta = b.arena.zeros<float>(static_cast<size_t>(rows) * std::max(c.gdn_heads, 1));
+  b.g = b.arena.zeros<float>(static_cast<size_t>(rows) * std::max(c.gdn_heads, 1));
+  b.tokens = b.arena.zeros<int32_t>(rows);
+  b.idx = b.arena.zeros<int32_t>(static_cast<size_t>(rows) * k);
+  b.gates = b.arena.zeros<float>(static_cast<size_t>(rows) * k);
+  b.counts = b.arena.zeros<int32_t>(E);
+  b.offsets = b.arena.zeros<int32_t>(E + 1);
+  b.sorted = b.arena.zeros<int32_t>(static_cast<size_t>(rows) * k);
+  b.route_pos = b.arena.zeros<int32_t>(static_cast<size_t>(rows) * k);
+  b.act = b.arena.zeros<uint16_t>(static_cast<size_t>(rows) * k * c.hidden);
+  b.y = b.arena.zeros<float>(static_cast<size_t>(rows) * k * D);
+  if (T > 1 && c.gdn_heads > 0) {
+    b.ws_bytes = llmy_gdn_prefill_workspace_bytes(B, T, c.gdn_heads, c.dk, c.dv);
+    if (b.ws_bytes < 0) throw std::runtime_error("GDN prefill workspace size");
+    b.ws = b.arena.zeros<unsigned char>(static_cast<size_t>(b.ws_bytes));
+  }
+}
+
+std::unique_ptr<State> new_state(Model* m, int B) {
+  if (B < 1) throw std::runtime_error("batch must be >= 1");
+  const Config& c = m->cfg;
+  auto s = std::make_unique<State>();
+  s->model = m;
+  s->B = B;
+  const int D = c.d_model;
+  for (int loop = 0; loop < c.num_loops; ++loop) {
+    for (int kind : c.kinds) {
+      LayerState L;
+      if (kind == kAttn) {
+        const size_t n = static_cast<size_t>(B) * c.attn_heads * c.window * c.attn_head_dim;
+        L.k = s->arena.zeros<uint16_t>(n);
+        L.v = s->arena.zeros<uint16_t>(n);
+        L.k_bytes = n * 2;
+      } else {
+        const size_t n = static_cast<size_t>(B) * c.gdn_heads * c.dk * c.dv;
+        L.S = s->arena.zeros<float>(n);
+        L.s_bytes = n * 4;
+        L.hist = s->arena.zeros<uint16_t>(static_cast<size_t>(B) * 3 * D);
+        L.hist_bytes = static_cast<size_t>(B) * 3 * D * 2;
+      }
+      s->layers.push_back(L);
+    }
+  }
+  s->pos = s->arena.zeros<int32_t>(B);
+  s->logits = s->arena.zeros<float>(static_cast<size_t>(B) * c.vocab);
+  s->next = s->arena.zeros<int32_t>(B);
+  alloc_buffers(c, B, B, 1, s->step);
+  return s;
+}
+
+void reset_state(State& s) {
+  for (auto& L : s.layers) {
+    if (L.k) {
+      check_hip(hipMemset(L.k, 0, L.k_bytes), "reset");
+      check_hip(hipMemset(L.v, 0, L.k_bytes), "reset");
+    }
+    if (L.S) {
+      check_hip(hipMemset(L.S, 0, L.s_bytes), "reset");
+      check_hip(hipMemset(L.hist, 0, L.hist_bytes), "reset");
+    }
+  }
+  check_hip(hipMemset(s.pos, 0, sizeof(int32_t) * s.B), "reset");
+  s.last_loops = 0;
+}
+
+// ------------------------------------------------------------------ forward
+constexpr int kStoreBf16 = 0, kStoreF32 = 1, kResidAdd = 2, kResidGated = 3, kPacked = 1;
+
+void linear(const uint16_t* x, const uint16_t* w, void* out, const float* aux, int M, int N, int K,
+            int epi) {
+  check_call(llmy_linear_bf16(x, w, out, aux, M, N, K, epi, kPacked, nullptr), "llmy_linear_bf16");
+}
+
+// MoE of layer l over `rows` rows (x updated, h = next pre-norm of x).
+// Decode uses the fused router and route-indexed experts where the sizes
+// allow; a prefill always takes router -> permutation -> grouped experts.
+void moe_block(const Model& m, const Layer& L, Buffers& b, int rows, const float* next_norm,
+               bool sequence) {
+  const Config& c = m.cfg;
+  const int D = c.d_model, E = c.experts, k = c.top_k, Hf = c.hidden;
+  const bool fused = !sequence && static_cast<long long>(E) * D <= 24576 &&
+                     (D == 256 || D == 512 || D == 1024) && k <= 8 && rows * k <= 2048;
+  if (fused) {
+    check_call(llmy_moe_route_decode(b.x, L.ffn_norm, L.router_norm, L.w_router, b.h, b.idx,
+                                     b.gates, nullptr, nullptr, nullptr, nullptr, rows, D, E, k,
+                                     c.eps, nullptr),
+               "llmy_moe_route_decode");
+    check_call(llmy_moe_experts_routed_bf16(b.h, b.idx, b.gates, L.w_gate_up, L.w_down, b.act, b.y,
+                                            rows, D, Hf, E, k, kPacked, nullptr),
+               "llmy_moe_experts_routed_bf16");
+    check_call(llmy_moe_combine_norm(b.y, nullptr, next_norm, b.x, b.h, rows, D, k, c.eps, nullptr),
+               "llmy_moe_combine_norm");
+    return;
+  }
+  check_call(llmy_rmsnorm_f32_bf16(b.x, L.ffn_norm, b.h, rows, D, c.eps, nullptr), "rmsnorm");
+  check_call(llmy_router_topk_bf16(b.h, L.router_norm, L.w_router, nullptr, b.idx, b.gates, rows,
+                                   D, E, k, c.eps, nullptr),
+             "llmy_router_topk_bf16");
+  check_call(llmy_moe_permute(b.idx, rows * k, E, b.counts, b.offsets, b.sorted, b.route_pos,
+                              nullptr),
+             "llmy_moe_permute");
+  check_call(llmy_moe_experts_bf16(b.h, b.offsets, b.sorted, b.gates, L.w_gate_up, L.w_down, b.act,
+                                   b.y, rows, D, Hf, E, k, kPacked, nullptr),
+             "llmy_moe_experts_bf16");
+  check_call(llmy_moe_combine_norm(b.y, b.route_pos, next_norm, b.x, b.h, rows, D, k, c.eps,
+                                   nullptr),
+             "llmy_moe_combine_norm");
+}
+
+const float* next_norm_of(const Model& m, int loop, int l, int loops) {
+  const int n = static_cast<int>(m.layers.size());
+  if (l + 1 < n) return m.layers[l + 1].mix_norm;
+  return loop + 1 < loops ? m.layers[0].mix_norm : m.final_norm;
+}
+
+// One decode step for all B rows; tokens already in s.step.tokens, s.pos set.
+void decode_step(Model& m, State& s, int loops) {
+  const Config& c = m.cfg;
+  Buffers& b = s.step;
+  const int B = s.B, D = c.d_model, n = static_cast<int>(m.layers.size());
+  check_call(llmy_embed_norm_bf16(b.tokens, m.embed, m.layers[0].mix_norm, b.x, b.h, B, D, c.vocab,
+                                  c.eps, nullptr),
+             "llmy_embed_norm_bf16");
+  const int Hhd = c.attn_heads * c.attn_head_dim;
+  for (int loop = 0; loop < loops; ++loop) {
+    for (int l = 0; l < n; ++l) {
+      const Layer& L = m.layers[l];
+      LayerState& st = s.layers[static_cast<size_t>(loop) * n + l];
+      if (L.kind == kAttn) {
+        linear(b.h, L.wqkv, b.qkv, nullptr, B, 3 * Hhd, D, kStoreBf16);
+        check_call(llmy_banded_attn_decode_bf16(b.qkv, b.qkv + Hhd, b.qkv + 2 * Hhd, 3 * Hhd,
+                                                3 * Hhd, st.k, st.v, s.pos, b.ao, B, c.attn_heads,
+                                                c.attn_head_dim, c.window,
+                                                1.0f / std::sqrt(static_cast<float>(c.attn_head_dim)),
+                                                nullptr),
+                   "llmy_banded_attn_decode_bf16");
+        linear(b.ao, L.wo, b.x, nullptr, B, D, Hhd, kResidAdd);
+      } else {
+        const int HV = c.gdn_heads * c.dv;
+        linear(b.h, L.wproj, b.proj, nullptr, B, c.nproj16(), D, kStoreF32);
+        check_call(llmy_gdn_step_fused_f32(b.proj, c.nproj16(), L.bb, L.decay, st.S, b.go, b.h,
+                                           st.hist, L.conv, b.cg, D, 4, B, c.gdn_heads, c.dk,
+                                           c.dv, nullptr),
+                   "llmy_gdn_step_fused_f32");
+        linear(b.go, L.wout, b.x, b.cg, B, D, HV, kResidGated);
+      }
+      moe_block(m, L, b, B, next_norm_of(m, loop, l, loops), false);
+    }
+  }
+  linear(b.h, m.lm_head, s.logits, nullptr, B, c.vocab, D, kStoreF32);
+  check_call(llmy_sample_argmax_f32(s.logits, B, c.vocab, s.next, nullptr), "argmax");
+  s.last_loops = loops;
+}
+
+// Prefill of B fresh sequences of T tokens each (tokens on the host, [B, T]).
+void prefill(Model& m, State& s, const int32_t* tokens, int T, bool tokens_on_device) {
+  const Config& c = m.cfg;
+  const int B = s.B, R = B * T, D = c.d_model, n = static_cast<int>(m.layers.size());
+  reset_state(s);
+  if (!s.seq || s.seq->rows < R || (c.gdn_heads > 0 && s.seq->ws_bytes <
+                                    llmy_gdn_prefill_workspace_bytes(B, T, c.gdn_heads, c.dk, c.dv))) {
+    s.seq.reset();
+    auto nb = std::make_unique<Buffers>();
+    alloc_buffers(c, R, B, std::max(T, 2), *nb);
+    s.seq = std::move(nb);
+  }
+  Buffers& b = *s.seq;
+  check_hip(hipMemcpy(b.tokens, tokens, sizeof(int32_t) * R,
+                      tokens_on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice),
+            "tokens");
+  check_call(llmy_embed_norm_bf16(b.tokens, m.embed, m.layers[0].mix_norm, b.x, b.h, R, D, c.vocab,
+                                  c.eps, nullptr),
+             "llmy_embed_norm_bf16");
+  const int loops = c.num_loops;
+  const int Hhd = c.attn_heads * c.attn_head_dim;
+  for (int loop = 0; loop < loops; ++loop) {
+    for (int l = 0; l < n; ++l) {
+      const Layer& L = m.layers[l];
+      LayerState& st = s.layers[static_cast<size_t>(loop) * n + l];
+      if (L.kind == kAttn) {
+        // q, k, v from row slices of the packed wqkv (each a packed [Hhd, D] matrix)
+        const size_t slice = static_cast<size_t>(Hhd) * D;
+        linear(b.h, L.wqkv, b.q, nullptr, R, Hhd, D, kStoreBf16);
+        linear(b.h, L.wqkv + slice, b.k, nullptr, R, Hhd, D, kStoreBf16);
+        linear(b.h, L.wqkv + 2 * slice, b.v, nullptr, R, Hhd, D, kStoreBf16);
+        check_call(llmy_banded_attn_prefill_bf16(b.q, b.k, b.v, b.ao, B, T, c.attn_heads,
+                                                 c.attn_head_dim, c.window,
+                                                 1.0f / std::sqrt(static_cast<float>(c.attn_head_dim)),
+                                                 nullptr),
+                   "llmy_banded_attn_prefill_bf16");
+        check_call(llmy_kv_cache_fill_bf16(b.k, b.v, Hhd, st.k, st.v, B, T, c.attn_heads,
+                                           c.attn_head_dim, c.window, nullptr),
+                   "llmy_kv_cache_fill_bf16");
+        linear(b.ao, L.wo, b.x, nullptr, R, D, Hhd, kResidAdd);
+      } else {
+        const int H = c.gdn_heads, HV = H * c.dv;
+        linear(b.h, L.wproj, b.proj, nullptr, R, c.nproj16(), D, kStoreF32);
+        check_call(llmy_gdn_prefill_prep_f32(b.proj, c.nproj16(), L.bb, L.decay, b.gq, b.gk, b.gv,
+                                             b.beta, b.g, R, H, c.dk, c.dv, nullptr),
+                   "llmy_gdn_prefill_prep_f32");
+        check_call(llmy_gdn_prefill_bf16(b.gq, b.gk, b.gv, b.beta, b.g, st.S, b.go, b.ws, b.ws_bytes,
+                                         B, T, H, c.dk, c.dv, nullptr),
+                   "llmy_gdn_prefill_bf16");
+        check_call(llmy_gdn_gate_bf16(b.go, b.proj, c.nproj16(), 2 * H * c.dk + HV, b.go, R, HV,
+                                      nullptr),
+                   "llmy_gdn_gate_bf16");
+        check_call(llmy_gdn_conv_gate_prefill(b.h, st.hist, L.conv, b.cg, B, T, D, 4, nullptr),
+                   "llmy_gdn_conv_gate_prefill");
+        linear(b.go, L.wout, b.x, b.cg, R, D, HV, kResidGated);
+      }
+      moe_block(m, L, b, R, next_norm_of(m, loop, l, loops), true);
+    }
+  }
+  // last position of each sequence -> the decode buffer, then the LM head
+  check_hip(hipMemcpy2D(s.step.h, static_cast<size_t>(D) * 2,
+                        b.h + static_cast<size_t>(T - 1) * D, static_cast<size_t>(T) * D * 2,
+                        static_cast<size_t>(D) * 2, B, hipMemcpyDeviceToDevice),
+            "last rows");
+  linear(s.step.h, m.lm_head, s.logits, nullptr, B, c.vocab, D, kStoreF32);
+  check_call(llmy_sample_argmax_f32(s.logits, B, c.vocab, s.next, nullptr), "argmax");
+  std::vector<int32_t> pos(B, T);
+  check_hip(hipMemcpy(s.pos, pos.data(), sizeof(int32_t) * B, hipMemcpyHostToDevice), "pos");
+  s.last_loops = loops;
+}
+
+void copy_logits_out(const State& s, float* out) {
+  const size_t bytes = sizeof(float) * s.B * s.model->cfg.vocab;
+  check_hip(hipMemcpy(out, s.logits, bytes, hipMemcpyDefault), "logits");
+}
+
+Model* as_model(llmy_model* p) { return reinterpret_cast<Model*>(p); }
+State* as_state(llmy_state* p) { return reinterpret_cast<State*>(p); }
+
+template <typename F>
+int32_t guarded(F&& f) {
+  try {
+    f();
+    g_status = 0;
+    g_error[0] = '\0';
+    return 0;
+  } catch (const std::exception& e) {
+    set_error(1, e.what());
+    std::fprintf(stderr, "[llmy] %s\n", e.what());
+    return 1;
+  }
+}
+
+}  // namespace
+
+// ================================================================== C ABI
+extern "C" {
+
+llmy_model* llmy_load(const char* path) {
+  if (!path) {
+    set_error(1, "null path");
+    return nullptr;
+  }
+  Model* out = nullptr;
+  guarded([&] { out = load_model(path).release(); });
+  return reinterpret_cast<llmy_model*>(out);
+}
+
+void llmy_free(llmy_model* m) { delete as_model(m); }
+
+int32_t llmy_vocab_size(const llmy_model* m) {
+  return m ? reinterpret_cast<const Model*>(m)->cfg.vocab : 0;
+}
+int32_t llmy_d_model(const llmy_model* m) {
+  return m ? reinterpret_cast<const Model*>(m)->cfg.d_model : 0;
+}
+int32_t llmy_num_loops(const llmy_model* m) {
+  return m ? reinterpret_cast<const Model*>(m)->loops : 0;
+}
+int32_t llmy_max_loops(const llmy_model* m) {
+  return m ? reinterpret_cast<const Model*>(m)->cfg.num_loops : 0;
+}
+int32_t llmy_mhc_streams(const llmy_model* m) { return m ? 1 : 0; }
+
+void llmy_set_num_loops(llmy_model* m, int32_t n) {
+  if (!m) return;
+  Model* mm = as_model(m);
+  mm->loops = std::max(1, std::min<int32_t>(n, mm->cfg.num_loops));
+}
+void llmy_set_fixed_loops(llmy_model* m, int32_t n) {
+  if (n >= 1) llmy_set_num_loops(m, n);
+}
+
+llmy_state* llmy_state_new(llmy_model* m) { return llmy_state_new_batch(m, 1); }
+
+llmy_state* llmy_state_new_batch(llmy_model* m, int32_t batch) {
+  if (!m || batch < 1) {
+    set_error(1, "null model or batch < 1");
+    return nullptr;
+  }
+  State* out = nullptr;
+  guarded([&] { out = new_state(as_model(m), batch).release(); });
+  return reinterpret_cast<llmy_state*>(out);
+}
+
+void llmy_state_free(llmy_state* s) { delete as_state(s); }
+
+void llmy_state_reset(llmy_state* s) {
+  if (s) guarded([&] { reset_state(*as_state(s)); });
+}
+
+void llmy_prefill(llmy_model* m, llmy_state* s, const int32_t* tokens, int32_t n_tokens,
+                  float* logits_out) {
+  (void)llmy_prefill_batch(m, s, tokens, n_tokens, logits_out);
+}
+
+int32_t llmy_prefill_batch(llmy_model* m, llmy_state* s, const int32_t* tokens, int32_t n_tokens,
+                           float* logits_out) {
+  if (!m || !s || !tokens || n_tokens < 1 || as_state(s)->model != as_model(m)) {
+    set_error(1, "invalid prefill arguments");
+    return 1;
+  }
+  return guarded([&] {
+    hipPointerAttribute_t attr{};
+    const bool on_device = hipPointerGetAttributes(&attr, tokens) == hipSuccess &&
+                           attr.type == hipMemoryTypeDevice;
+    (void)hipGetLastError();
+    prefill(*as_model(m), *as_state(s), tokens, n_tokens, on_device);
+    if (logits_out) copy_logits_out(*as_state(s), logits_out);
+    check_hip(hipDeviceSynchronize(), "prefill");
+  });
+}
+
+void llmy_decode(llmy_model* m, llmy_state* s, int32_t token, int32_t position, int32_t num_loops,
+                 float* logits_out) {
+  if (!s || as_state(s)->B != 1) {
+    set_error(1, "llmy_decode needs a batch-1 state");
+    return;
+  }
+  (void)llmy_decode_batch(m, s, &token, &position, num_loops, logits_out);
+}
+
+int32_t llmy_decode_batch(llmy_model* m, llmy_state* s, const int32_t* tokens,
+                          const int32_t* positions, int32_t num_loops, float* logits_out) {
+  if (!m || !s || !tokens || as_state(s)->model != as_model(m)) {
+    set_error(1, "invalid decode arguments");
+    return 1;
+  }
+  return guarded([&] {
+    Model& mm = *as_model(m);
+    State& st = *as_state(s);
+    const int loops = num_loops <= 0 ? mm.loops : std::min<int32_t>(num_loops, mm.cfg.num_loops);
+    check_hip(hipMemcpy(st.step.tokens, tokens, sizeof(int32_t) * st.B, hipMemcpyDefault), "tokens");
+    if (positions)
+      check_hip(hipMemcpy(st.pos, positions, sizeof(int32_t) * st.B, hipMemcpyDefault), "positions");
+    decode_step(mm, st, loops);
+    // the next token's position: one past this one
+    std::vector<int32_t> pos(st.B);
+    check_hip(hipMemcpy(pos.data(), st.pos, sizeof(int32_t) * st.B, hipMemcpyDeviceToHost), "pos");
+    for (int32_t& p : pos) ++p;
+    check_hip(hipMemcpy(st.pos, pos.data(), sizeof(int32_t) * st.B, hipMemcpyHostToDevice), "pos");
+    if (logits_out) copy_logits_out(st, logits_out);
+    check_hip(hipDeviceSynchronize(), "decode");
+  });
+}
+
+int32_t llmy_greedy_tokens(const llmy_state* s, int32_t* out) {
+  if (!s || !out) return 1;
+  const State* st = reinterpret_cast<const State*>(s);
+  return static_cast<int32_t>(
+      hipMemcpy(out, st->next, sizeof(int32_t) * st->B, hipMemcpyDefault));
+}
+
+int32_t llmy_sample(const float* logits, int32_t vocab_size, float temperature, int32_t top_k,
+                    float top_p, float repetition_penalty, const int32_t* recent_tokens,
+                    int32_t n_recent, uint64_t* rng_state) {
+  // The CPU sampler of the reference ABI (llmy_cuda/src/llmy.cpp:132-202):
+  // penalty per listed id, top-k (capped at 256) by descending logit, greedy
+  // for temperature <= 0, softmax / temperature in fp32, the first prefix
+  // whose cumulative probability reaches top_p, renormalise, one xorshift64
+  // draw u = (r >> 11) / 2^53, the first id whose running sum exceeds u.
+  // Equal logits are ordered by ascending id (the twin's partial_sort leaves
+  // them unordered).
+  if (vocab_size <= 0 || !logits) return 0;
+  if (top_k <= 0 || top_k > vocab_size) top_k = vocab_size;
+  top_k = std::min(top_k, 256);
+  std::vector<float> work(logits, logits + vocab_size);
+  if (repetition_penalty != 1.0f && n_recent > 0 && recent_tokens) {
+    for (int r = 0; r < n_recent; ++r) {
+      const int id = recent_tokens[r];
+      if (id < 0 || id >= vocab_size) continue;
+      work[id] = work[id] > 0.0f ? work[id] / repetition_penalty : work[id] * repetition_penalty;
+    }
+  }
+  std::vector<int> order(vocab_size);
+  for (int i = 0; i < vocab_size; ++i) order[i] = i;
+  std::partial_sort(order.begin(), order.begin() + top_k, order.end(), [&](int a, int b) {
+    return work[a] > work[b] || (work[a] == work[b] && a < b);
+  });
+  if (!(temperature > 0.0f)) return order[0];
+  const float maxv = work[order[0]];
+  std::vector<float> probs(top_k);
+  float sum = 0.0f;
+  for (int i = 0; i < top_k; ++i) {
+    probs[i] = std::exp((work[order[i]] - maxv) / temperature);
+    sum += probs[i];
+  }
+  for (float& p : probs) p /= sum;
+  int cutoff = top_k;
+  if (top_p > 0.0f && top_p < 1.0f) {
+    float cdf = 0.0f;
+    for (int i = 0; i < top_k; ++i) {
+      cdf += probs[i];
+      if (cdf >= top_p) {
+        cutoff = i + 1;
+        break;
+      }
+    }
+  }
+  float renorm = 0.0f;
+  for (int i = 0; i < cutoff; ++i) renorm += probs[i];
+  for (int i = 0; i < cutoff; ++i) probs[i] /= renorm;
+  uint64_t r = rng_state ? *rng_state : 0x9E3779B97F4A7C15ull;
+  r ^= r << 13;
+  r ^= r >> 7;
+  r ^= r << 17;
+  if (rng_state) *rng_state = r;
+  const double u = static_cast<double>(r >> 11) / static_cast<double>(1ull << 53);
+  float acc = 0.0f;
+  for (int i = 0; i < cutoff; ++i) {
+    acc += probs[i];
+    if (u < acc) return order[i];
+  }
+  return order[cutoff - 1];
+}
+
+int32_t llmy_last_executed_loops(const llmy_state* s) {
+  return s ? reinterpret_cast<const State*>(s)->last_loops : 0;
+}
+
+void llmy_sync(void) { (void)hipDeviceSynchronize(); }
+
+int32_t llmy_last_status(void) { return g_status; }
+
+const char* llmy_last_error(void) { return g_error; }
+
+int32_t llmy_checkpoint_describe(const char* path, char* buf, int64_t buf_len) {
+  // Parse only (no device work): config text, then one line per tensor
+  // "name dtype ndim d0 d1 d2 d3 nbytes", for hosts without a GPU.
+  if (!path || !buf || buf_len < 1) return 1;
+  return guarded([&] {
+    Checkpoint ck;
+    parse_checkpoint(path, ck);
+    (void)config_from(ck.config);
+    std::string out = ck.config;
+    if (!out.empty() && out.back() != '\n') out += '\n';
+    out += "--\n";
+    for (const auto& kv : ck.tensors) {
+      const TensorRef& t = kv.second;
+      int64_t d[4] = {0, 0, 0, 0};
+      for (size_t i = 0; i < t.shape.size(); ++i) d[i] = t.shape[i];
+      char line[160];
+      std::snprintf(line, sizeof(line), "%s %u %zu %lld %lld %lld %lld %llu\n", kv.first.c_str(),
+                    t.dtype, t.shape.size(), static_cast<long long>(d[0]),
+                    static_cast<long long>(d[1]), static_cast<long long>(d[2]),
+                    static_cast<long long>(d[3]), static_cast<unsigned long long>(t.nbytes));
+      out += line;
+    }
+    if (static_cast<int64_t>(out.size()) + 1 > buf_len)
+      throw std::runtime_error("description buffer too small");
+    std::memcpy(buf, out.c_str(), out.size() + 1);
+  });
+}
+
+}  // extern "C"

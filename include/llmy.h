@@ -353,6 +353,74 @@ int32_t llmy_repetition_penalty_f32(float* logits, int32_t rows, int32_t V,
                                     const int32_t* recent, int32_t n_recent,
                                     float penalty, void* stream);
 
+/* --- Engine handles (llmy_cuda/include/llmy.h:27-72) ----------------------
+ * The reference engine API with the same signatures and meaning; the model
+ * comes from a `.llmy` v1 file of this block stack (hybrid_llm_amd/checkpoint.py
+ * writes one).  Replaces llmy_cuda/src/llmy.cpp:21-210 over model.cpp:1774-1972.
+ * The model handle owns the device weights, the state handle the caches and
+ * buffers; these entry points allocate device memory, the kernel entries
+ * above never do.  No exception crosses the ABI: a failure returns NULL (load,
+ * state_new) or is recorded for llmy_last_status / llmy_last_error. */
+typedef struct llmy_model llmy_model;
+typedef struct llmy_state llmy_state;
+
+llmy_model* llmy_load(const char* path);                 /* llmy.h:31 */
+void        llmy_free(llmy_model* m);                    /* llmy.h:32 */
+int32_t llmy_vocab_size(const llmy_model* m);            /* llmy.h:35 */
+int32_t llmy_d_model(const llmy_model* m);               /* llmy.h:36 */
+/* loops a forward runs by default (set_num_loops, clamped to the built ones) */
+int32_t llmy_num_loops(const llmy_model* m);             /* llmy.h:37 */
+int32_t llmy_max_loops(const llmy_model* m);             /* llmy.h:38 */
+/* 1: this block stack has no mHC stream mixing */
+int32_t llmy_mhc_streams(const llmy_model* m);           /* llmy.h:39 */
+void    llmy_set_num_loops(llmy_model* m, int32_t n);    /* llmy.h:40 */
+void    llmy_set_fixed_loops(llmy_model* m, int32_t n);  /* llmy.h:41 */
+/* batch-1 state, as the reference */
+llmy_state* llmy_state_new(llmy_model* m);               /* llmy.h:44 */
+void        llmy_state_free(llmy_state* s);              /* llmy.h:45 */
+/* zero every cache and state, position 0 (llmy.cpp:99-114) */
+void        llmy_state_reset(llmy_state* s);             /* llmy.h:46 */
+/* A fresh conversation of n_tokens from position 0 (the reference's
+ * model_prefill runs it token by token, model.cpp:1955-1966; here it is one
+ * sequence pass); logits of the last position into logits_out [vocab] on the
+ * host or the device (llmy.h:49-53). */
+void llmy_prefill(llmy_model* m, llmy_state* s, const int32_t* tokens,
+                  int32_t n_tokens, float* logits_out);
+/* One token at absolute position `position`; num_loops 0 = the model's
+ * default (llmy.h:55-59). */
+void llmy_decode(llmy_model* m, llmy_state* s, int32_t token, int32_t position,
+                 int32_t num_loops, float* logits_out);
+/* The CPU sampler (llmy.h:61-68, llmy.cpp:132-202): host logits, xorshift64
+ * state; equal logits order by ascending id. */
+int32_t llmy_sample(const float* logits, int32_t vocab_size, float temperature,
+                    int32_t top_k, float top_p, float repetition_penalty,
+                    const int32_t* recent_tokens, int32_t n_recent,
+                    uint64_t* rng_state);
+int32_t llmy_last_executed_loops(const llmy_state* s);   /* llmy.h:71 */
+void    llmy_sync(void);                                 /* llmy.h:72 */
+
+/* Batched forms — no counterpart in the reference, whose engine throws for
+ * B > 1 (model.cpp:627,678): a state of `batch` sequences; prefill of
+ * tokens [batch, n_tokens] (host or device) from position 0 and decode of
+ * tokens [batch] at positions [batch] (NULL: one past the previous token),
+ * logits_out [batch, vocab] (NULL: not copied).  Return 0 or 1 (see
+ * llmy_last_error). */
+llmy_state* llmy_state_new_batch(llmy_model* m, int32_t batch);
+int32_t llmy_prefill_batch(llmy_model* m, llmy_state* s, const int32_t* tokens,
+                           int32_t n_tokens, float* logits_out);
+int32_t llmy_decode_batch(llmy_model* m, llmy_state* s, const int32_t* tokens,
+                          const int32_t* positions, int32_t num_loops,
+                          float* logits_out);
+/* greedy (argmax) token of each row after the last forward into out [batch] */
+int32_t llmy_greedy_tokens(const llmy_state* s, int32_t* out);
+/* Status of the last engine call on this thread (0 ok) and its message — the
+ * status query the reference lacks for prefill/decode (llmy.cpp:116-131). */
+int32_t     llmy_last_status(void);
+const char* llmy_last_error(void);
+/* Parse a `.llmy` file without touching the GPU: config text, "--", then one
+ * line per tensor "name dtype ndim d0 d1 d2 d3 nbytes" into buf. */
+int32_t llmy_checkpoint_describe(const char* path, char* buf, int64_t buf_len);
+
 #ifdef __cplusplus
 }
 #endif

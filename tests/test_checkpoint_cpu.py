@@ -1,0 +1,194 @@
+"""`.llmy` v1 files and the engine API pieces that need no GPU.
+
+* The writer's byte layout against the format of
+  llmy_cuda/tools/convert_checkpoint.py:1-31 (magic, version, config,
+  108-byte `<I 64s I I 4I Q Q>` index entries, 4 KiB-aligned data start).
+* The native parser (llmy_checkpoint_describe) agrees with the writer on the
+  config and every tensor, and rejects corrupt files.
+* llmy_sample (the reference's CPU sampler) against hand-computed cases and
+  the oracle's sampling rule.
+* llmy_load without a GPU fails with NULL and a message, never a crash.
+"""
+import ctypes as C
+import struct
+
+import numpy as np
+import pytest
+import torch
+
+from hybrid_llm_amd import _lib
+from hybrid_llm_amd.checkpoint import (INDEX_ENTRY, config_from_text, config_text, file_name,
+                                       load_weights, read_llmy, save_llmy)
+from hybrid_llm_amd.config import C1, HybridConfig, alternating, init_weights, weight_shapes
+
+TINY = HybridConfig(d_model=256, layer_kinds=alternating(2), attn_heads=4, attn_head_dim=64,
+                    window=16, gdn_heads=4, gdn_dk=64, gdn_dv=64, n_experts=4, top_k=2,
+                    expert_hidden=256, vocab=512, num_loops=2)
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return _lib.load()
+
+
+@pytest.fixture(scope="module")
+def tiny_file(tmp_path_factory):
+    path = tmp_path_factory.mktemp("ck") / "tiny.llmy"
+    w = init_weights(TINY, seed=3)
+    save_llmy(path, TINY, w)
+    return path, w
+
+
+def test_byte_layout(tiny_file):
+    path, w = tiny_file
+    data = path.read_bytes()
+    assert data[:4] == b"LLMY"
+    version, cfg_len = struct.unpack_from("<II", data, 4)
+    assert version == 1
+    text = data[12:12 + cfg_len].decode()
+    assert text == config_text(TINY)
+    (n,) = struct.unpack_from("<I", data, 12 + cfg_len)
+    assert n == len(weight_shapes(TINY))
+    index = 16 + cfg_len
+    data_start = -(-(index + 108 * n) // 4096) * 4096
+    names, expect_off = [], 0
+    for i in range(n):
+        nl, name, dt, nd, *rest = INDEX_ENTRY.unpack_from(data, index + 108 * i)
+        shape, off, nbytes = rest[:4], rest[4], rest[5]
+        assert 0 < nl <= 63 and name[nl:] == b"\0" * (64 - nl)
+        assert off == expect_off and data_start + off + nbytes <= len(data)
+        expect_off += nbytes
+        names.append(name[:nl].decode())
+    assert names == sorted(names)
+    # one payload checked byte for byte: the first GDN beta bias (fp32 zeros)
+    # and the embedding (bf16 words)
+    _, tensors = read_llmy(path)
+    assert torch.equal(tensors["embed_tokens.weight"], w["embed"])
+    assert tensors["recurrent_core.1.mixer.conv.weight"].shape == (256, 1, 4)
+
+
+def test_roundtrip_and_names(tiny_file):
+    path, w = tiny_file
+    cfg, back = load_weights(path)
+    assert cfg == TINY
+    for key, t in w.items():
+        assert torch.equal(back[key], t), key
+    assert file_name(C1, "L0.wq") == "recurrent_core.0.mixer.q.weight"
+    assert file_name(C1, "L1.wq") == "recurrent_core.1.mixer.q_proj.weight"
+    assert file_name(C1, "L1.bb") == "recurrent_core.1.mixer.beta_proj.bias"
+    assert file_name(C1, "L3.w_down") == "recurrent_core.3.moe.experts.down_proj.weight"
+    assert config_from_text(config_text(C1)) == C1
+
+
+def _describe(lib, path):
+    buf = C.create_string_buffer(1 << 20)
+    st = lib.llmy_checkpoint_describe(str(path).encode(), buf, len(buf))
+    return st, buf.value.decode()
+
+
+def test_native_parser_agrees(lib, tiny_file):
+    path, _ = tiny_file
+    st, text = _describe(lib, path)
+    assert st == 0, lib.llmy_last_error()
+    cfg_part, tensor_part = text.split("--\n")
+    assert cfg_part == config_text(TINY)
+    _, tensors = read_llmy(path)
+    lines = [l.split() for l in tensor_part.strip().splitlines()]
+    assert [l[0] for l in lines] == sorted(tensors)
+    for name, dt, nd, d0, d1, d2, d3, nb in lines:
+        t = tensors[name]
+        assert int(nd) == t.dim() and [int(x) for x in (d0, d1, d2, d3)][:t.dim()] == list(t.shape)
+        assert int(nb) == t.numel() * t.element_size()
+        assert int(dt) == {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}[t.dtype]
+
+
+@pytest.mark.parametrize("damage", ["magic", "version", "truncate_index", "payload", "name_len",
+                                    "shape"])
+def test_native_parser_rejects_corrupt_files(lib, tiny_file, tmp_path, damage):
+    path, _ = tiny_file
+    data = bytearray(path.read_bytes())
+    cfg_len = struct.unpack_from("<I", data, 8)[0]
+    first = 16 + cfg_len
+    if damage == "magic":
+        data[:4] = b"LLMZ"
+    elif damage == "version":
+        struct.pack_into("<I", data, 4, 2)
+    elif damage == "truncate_index":
+        data = data[:first + 50]
+    elif damage == "payload":
+        struct.pack_into("<Q", data, first + 92, len(data))  # offset past the end
+    elif damage == "name_len":
+        struct.pack_into("<I", data, first, 64)
+    elif damage == "shape":
+        struct.pack_into("<I", data, first + 76, 7)  # shape no longer matches nbytes
+    bad = tmp_path / "bad.llmy"
+    bad.write_bytes(bytes(data))
+    st, _ = _describe(lib, bad)
+    assert st != 0
+    assert lib.llmy_last_status() != 0 and lib.llmy_last_error()
+    with pytest.raises(ValueError):
+        read_llmy(bad)
+
+
+def test_load_without_gpu_fails_cleanly(lib, tiny_file):
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present; the GPU tests cover llmy_load")
+    path, _ = tiny_file
+    assert lib.llmy_load(str(path).encode()) is None
+    assert lib.llmy_last_status() != 0 and lib.llmy_last_error()
+    assert lib.llmy_load(b"/nonexistent.llmy") is None
+
+
+def _sample(lib, logits, T, k, p, rep=1.0, recent=(), seed=1337):
+    x = np.ascontiguousarray(np.asarray(logits, dtype=np.float32))
+    rec = (C.c_int32 * max(len(recent), 1))(*recent)
+    rng = C.c_uint64(seed)
+    tok = lib.llmy_sample(x.ctypes.data_as(C.POINTER(C.c_float)), x.size, T, k, p, rep, rec,
+                          len(recent), C.byref(rng))
+    return tok, rng.value
+
+
+def _xorshift(r):
+    m = (1 << 64) - 1
+    r ^= (r << 13) & m
+    r ^= r >> 7
+    r ^= (r << 17) & m
+    return r
+
+
+def test_sampler_rules(lib):
+    x = np.array([0.5, 3.0, 3.0, -1.0, 2.0], np.float32)
+    # greedy: ties to the lower id
+    assert _sample(lib, x, 0.0, 0, 0.9)[0] == 1
+    # top_k = 1 returns the top id for any temperature
+    assert _sample(lib, x, 0.7, 1, 1.0)[0] == 1
+    # the generator advances exactly one xorshift64 step per draw
+    assert _sample(lib, x, 0.7, 0, 0.9, seed=99)[1] == _xorshift(99)
+    # the draw: first id in order whose running probability exceeds u
+    r = _xorshift(1337)
+    u = (r >> 11) / 2.0 ** 53
+    order = [1, 2, 4, 0, 3]
+    e = np.exp((x[order] - x.max()) / np.float32(0.7)).astype(np.float64)
+    cdf = np.cumsum(e / e.sum())
+    want = order[int(np.searchsorted(cdf, u, side="right"))]
+    assert _sample(lib, x, 0.7, 0, 1.0)[0] == want
+    # repetition penalty divides positive logits, multiplies negative ones
+    assert _sample(lib, x, 0.0, 0, 1.0, rep=2.0, recent=(1, 2))[0] == 4
+
+
+def test_sampler_matches_oracle_rule(lib):
+    from oracle.sampling import top_p_sample
+    g = np.random.default_rng(0)
+    agree = 0
+    for trial in range(40):
+        x = g.standard_normal(300).astype(np.float32) * 2
+        seed = 1000 + trial
+        tok, _ = _sample(lib, x, 0.8, 0, 0.9, seed=seed)
+        u = (_xorshift(seed) >> 11) / 2.0 ** 53
+        # the C sampler caps top-k at 256 (llmy.cpp:139)
+        ref, margin = top_p_sample(torch.from_numpy(x[None]), 0.8, float(np.float32(0.9)),
+                                   torch.tensor([u]), top_k=256, return_margin=True)
+        if margin[0] > 1e-5:
+            assert tok == int(ref[0]), trial
+            agree += 1
+    assert agree >= 30

@@ -1,0 +1,172 @@
+"""The native engine behind the reference's engine API (llmy_load, state
+handles, llmy_prefill, llmy_decode, llmy_sample), bound exactly as
+llmy_cuda/python/sample.py:104-175 binds it.
+
+The engine runs the same kernels in the same order as
+hybrid_llm_amd.engine.HybridDecoder, so its logits must equal the Python
+engine's bit for bit; the Python engine is pinned against the oracle in
+test_gpu_engine.py and test_gpu_prefill.py.  Loop control is checked against
+the oracle directly.
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+import torch
+
+from hybrid_llm_amd.checkpoint import save_llmy
+from hybrid_llm_amd.config import C1, init_weights
+
+pytestmark = pytest.mark.gpu
+
+
+def _bind(lib):
+    """The reference binding's signatures (llmy_cuda/python/sample.py:110-170)."""
+    lib.llmy_load.argtypes = [C.c_char_p]
+    lib.llmy_load.restype = C.c_void_p
+    lib.llmy_free.argtypes = [C.c_void_p]
+    lib.llmy_vocab_size.argtypes = [C.c_void_p]
+    lib.llmy_vocab_size.restype = C.c_int32
+    lib.llmy_num_loops.argtypes = [C.c_void_p]
+    lib.llmy_num_loops.restype = C.c_int32
+    lib.llmy_max_loops.argtypes = [C.c_void_p]
+    lib.llmy_max_loops.restype = C.c_int32
+    lib.llmy_set_num_loops.argtypes = [C.c_void_p, C.c_int32]
+    lib.llmy_state_new.argtypes = [C.c_void_p]
+    lib.llmy_state_new.restype = C.c_void_p
+    lib.llmy_state_free.argtypes = [C.c_void_p]
+    lib.llmy_prefill.argtypes = [C.c_void_p, C.c_void_p, C.POINTER(C.c_int32), C.c_int32,
+                                 C.POINTER(C.c_float)]
+    lib.llmy_prefill.restype = None
+    lib.llmy_decode.argtypes = [C.c_void_p, C.c_void_p, C.c_int32, C.c_int32, C.c_int32,
+                                C.POINTER(C.c_float)]
+    lib.llmy_decode.restype = None
+    lib.llmy_last_executed_loops.argtypes = [C.c_void_p]
+    lib.llmy_last_executed_loops.restype = C.c_int32
+    return lib
+
+
+@pytest.fixture(scope="module")
+def c1_file(tmp_path_factory):
+    w = init_weights(C1, seed=0)
+    path = tmp_path_factory.mktemp("engine") / "c1.llmy"
+    save_llmy(path, C1, w)
+    return path, w
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from hybrid_llm_amd import _lib
+    return _bind(_lib.load())
+
+
+def test_prefill_and_decode_match_python_engine(lib, c1_file):
+    from hybrid_llm_amd.engine import HybridDecoder
+    path, w = c1_file
+    prompt = torch.randint(0, C1.vocab, (40,), generator=torch.Generator().manual_seed(7))
+    print("[engine-api] C1 prefill 40 + decode 6", flush=True)
+    m = lib.llmy_load(str(path).encode())
+    assert m, lib.llmy_last_error()
+    try:
+        assert lib.llmy_vocab_size(m) == C1.vocab
+        assert lib.llmy_num_loops(m) == C1.num_loops == lib.llmy_max_loops(m)
+        s = lib.llmy_state_new(m)
+        assert s
+        V = C1.vocab
+        out = (C.c_float * V)()
+        toks = (C.c_int32 * 40)(*prompt.tolist())
+        lib.llmy_prefill(m, s, toks, 40, out)
+        assert lib.llmy_last_status() == 0, lib.llmy_last_error()
+        native = [np.frombuffer(out, dtype=np.float32).copy()]
+        py = HybridDecoder(C1, w, 1)
+        ref = [py.prefill(prompt.view(1, -1).cuda())[0].cpu().numpy().copy()]
+        tok = int(np.argmax(native[0]))
+        for step in range(6):
+            lib.llmy_decode(m, s, tok, 40 + step, 0, out)
+            assert lib.llmy_last_status() == 0, lib.llmy_last_error()
+            native.append(np.frombuffer(out, dtype=np.float32).copy())
+            ref.append(py.step(torch.tensor([tok], dtype=torch.int32).cuda())[0].cpu().numpy().copy())
+            tok = int(np.argmax(native[-1]))
+        for a, b in zip(native, ref):
+            assert np.array_equal(a, b)
+        assert lib.llmy_last_executed_loops(s) == C1.num_loops
+        lib.llmy_state_free(s)
+    finally:
+        lib.llmy_free(m)
+
+
+def test_batched_api_and_device_logits(lib, c1_file):
+    from hybrid_llm_amd.engine import HybridDecoder
+    path, w = c1_file
+    B, T = 3, 24
+    prompt = torch.randint(0, C1.vocab, (B, T), generator=torch.Generator().manual_seed(8),
+                           dtype=torch.int32)
+    m = lib.llmy_load(str(path).encode())
+    assert m
+    try:
+        s = lib.llmy_state_new_batch(m, B)
+        assert s
+        out = torch.zeros(B, C1.vocab, device="cuda")    # device-resident logits
+        toks = prompt.cuda()                              # device-resident tokens
+        assert lib.llmy_prefill_batch(m, s, toks.data_ptr(), T, out.data_ptr()) == 0
+        py = HybridDecoder(C1, w, B)
+        assert torch.equal(out, py.prefill(prompt.cuda()))
+        nxt = torch.zeros(B, dtype=torch.int32)
+        assert lib.llmy_greedy_tokens(s, nxt.data_ptr()) == 0
+        assert torch.equal(nxt, py.buf["next"].cpu())
+        for _ in range(3):
+            assert lib.llmy_decode_batch(m, s, nxt.data_ptr(), None, 0, out.data_ptr()) == 0
+            assert torch.equal(out, py.step(nxt.cuda()))
+            assert lib.llmy_greedy_tokens(s, nxt.data_ptr()) == 0
+        # reset, then a decode from position 0 equals a fresh engine's first step
+        lib.llmy_state_reset(s)
+        first = torch.tensor([5, 6, 7], dtype=torch.int32)
+        pos = torch.zeros(B, dtype=torch.int32)
+        assert lib.llmy_decode_batch(m, s, first.data_ptr(), pos.data_ptr(), 0, out.data_ptr()) == 0
+        py2 = HybridDecoder(C1, w, B)
+        assert torch.equal(out, py2.step(first.cuda()))
+        lib.llmy_state_free(s)
+    finally:
+        lib.llmy_free(m)
+
+
+def test_loop_control(lib, c1_file):
+    """num_loops = 1 runs the first loop only: bitwise the Python engine of
+    the one-loop model (loops share weights), and close to the oracle's
+    one-loop step (median over tokens: an unforced router near-tie may flip)."""
+    from dataclasses import replace
+    from hybrid_llm_amd.engine import HybridDecoder
+    from oracle.model import HybridOracle
+    path, w = c1_file
+    m = lib.llmy_load(str(path).encode())
+    assert m
+    try:
+        s = lib.llmy_state_new(m)
+        out = (C.c_float * C1.vocab)()
+        one = HybridDecoder(replace(C1, num_loops=1), w, 1)
+        ref = HybridOracle(C1, w, act_bf16=True)
+        st = ref.new_state(1)
+        errs = []
+        for i, tok in enumerate([11, 22, 33, 44]):
+            lib.llmy_decode(m, s, tok, i, 1, out)            # one loop of two
+            assert lib.llmy_last_executed_loops(s) == 1
+            got = torch.from_numpy(np.frombuffer(out, dtype=np.float32).copy())
+            assert torch.equal(got, one.step(torch.tensor([tok], dtype=torch.int32).cuda())[0].cpu())
+            want = ref.step([tok], st, num_loops=1)[0]
+            errs.append(float(torch.linalg.norm(got - want) / torch.linalg.norm(want)))
+        assert np.median(errs) < 2e-2, errs
+        lib.llmy_set_num_loops(m, 1)
+        assert lib.llmy_num_loops(m) == 1
+        lib.llmy_decode(m, s, 55, 4, 0, out)                # default is now one loop
+        assert lib.llmy_last_executed_loops(s) == 1
+        lib.llmy_state_free(s)
+    finally:
+        lib.llmy_free(m)
+
+
+def test_errors_are_reported_not_thrown(lib, tmp_path):
+    bad = tmp_path / "x.llmy"
+    bad.write_bytes(b"LLMY" + b"\0" * 8)
+    assert lib.llmy_load(str(bad).encode()) is None
+    assert lib.llmy_last_status() != 0 and lib.llmy_last_error()
+    assert lib.llmy_state_new_batch(None, 2) is None
