@@ -474,6 +474,9 @@ struct State {
   Model* model = nullptr;
   int B = 1;
   int last_loops = 0;
+  hipStream_t stream = nullptr;         // every launch of this state (default priority)
+  std::map<int, hipGraphExec_t> graphs; // decode step per loop count, captured on first use
+  std::vector<int32_t> hpos;            // host copy of pos
   std::vector<LayerState> layers;  // index loop * n_layers + layer
   DeviceArena arena;
   int32_t* pos = nullptr;    // [B] device: absolute position of the next token
@@ -481,6 +484,12 @@ struct State {
   int32_t* next = nullptr;   // [B]
   Buffers step;              // decode: B rows
   std::unique_ptr<Buffers> seq;  // prefill: B*T rows, grown on demand
+
+  ~State() {
+    if (stream) (void)hipStreamSynchronize(stream);
+    for (auto& kv : graphs) (void)hipGraphExecDestroy(kv.second);
+    if (stream) (void)hipStreamDestroy(stream);
+  }
 };
 
 void alloc_buffers(const Config& c, int rows, int B, int T, Buffers& b) {
@@ -544,6 +553,8 @@ std::unique_ptr<State> new_state(Model* m, int B) {
       s->layers.push_back(L);
     }
   }
+  check_hip(hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking), "hipStreamCreate");
+  s->hpos.assign(B, 0);
   s->pos = s->arena.zeros<int32_t>(B);
   s->logits = s->arena.zeros<float>(static_cast<size_t>(B) * c.vocab);
   s->next = s->arena.zeros<int32_t>(B);
@@ -554,15 +565,17 @@ std::unique_ptr<State> new_state(Model* m, int B) {
 void reset_state(State& s) {
   for (auto& L : s.layers) {
     if (L.k) {
-      check_hip(hipMemset(L.k, 0, L.k_bytes), "reset");
-      check_hip(hipMemset(L.v, 0, L.k_bytes), "reset");
+      check_hip(hipMemsetAsync(L.k, 0, L.k_bytes, s.stream), "reset");
+      check_hip(hipMemsetAsync(L.v, 0, L.k_bytes, s.stream), "reset");
     }
     if (L.S) {
-      check_hip(hipMemset(L.S, 0, L.s_bytes), "reset");
-      check_hip(hipMemset(L.hist, 0, L.hist_bytes), "reset");
+      check_hip(hipMemsetAsync(L.S, 0, L.s_bytes, s.stream), "reset");
+      check_hip(hipMemsetAsync(L.hist, 0, L.hist_bytes, s.stream), "reset");
     }
   }
-  check_hip(hipMemset(s.pos, 0, sizeof(int32_t) * s.B), "reset");
+  check_hip(hipMemsetAsync(s.pos, 0, sizeof(int32_t) * s.B, s.stream), "reset");
+  check_hip(hipStreamSynchronize(s.stream), "reset");
+  s.hpos.assign(s.B, 0);
   s.last_loops = 0;
 }
 
@@ -570,15 +583,15 @@ void reset_state(State& s) {
 constexpr int kStoreBf16 = 0, kStoreF32 = 1, kResidAdd = 2, kResidGated = 3, kPacked = 1;
 
 void linear(const uint16_t* x, const uint16_t* w, void* out, const float* aux, int M, int N, int K,
-            int epi) {
-  check_call(llmy_linear_bf16(x, w, out, aux, M, N, K, epi, kPacked, nullptr), "llmy_linear_bf16");
+            int epi, hipStream_t st) {
+  check_call(llmy_linear_bf16(x, w, out, aux, M, N, K, epi, kPacked, st), "llmy_linear_bf16");
 }
 
 // MoE of layer l over `rows` rows (x updated, h = next pre-norm of x).
 // Decode uses the fused router and route-indexed experts where the sizes
 // allow; a prefill always takes router -> permutation -> grouped experts.
 void moe_block(const Model& m, const Layer& L, Buffers& b, int rows, const float* next_norm,
-               bool sequence) {
+               bool sequence, hipStream_t st) {
   const Config& c = m.cfg;
   const int D = c.d_model, E = c.experts, k = c.top_k, Hf = c.hidden;
   const bool fused = !sequence && static_cast<long long>(E) * D <= 24576 &&
@@ -586,27 +599,27 @@ void moe_block(const Model& m, const Layer& L, Buffers& b, int rows, const float
   if (fused) {
     check_call(llmy_moe_route_decode(b.x, L.ffn_norm, L.router_norm, L.w_router, b.h, b.idx,
                                      b.gates, nullptr, nullptr, nullptr, nullptr, rows, D, E, k,
-                                     c.eps, nullptr),
+                                     c.eps, st),
                "llmy_moe_route_decode");
     check_call(llmy_moe_experts_routed_bf16(b.h, b.idx, b.gates, L.w_gate_up, L.w_down, b.act, b.y,
-                                            rows, D, Hf, E, k, kPacked, nullptr),
+                                            rows, D, Hf, E, k, kPacked, st),
                "llmy_moe_experts_routed_bf16");
-    check_call(llmy_moe_combine_norm(b.y, nullptr, next_norm, b.x, b.h, rows, D, k, c.eps, nullptr),
+    check_call(llmy_moe_combine_norm(b.y, nullptr, next_norm, b.x, b.h, rows, D, k, c.eps, st),
                "llmy_moe_combine_norm");
     return;
   }
-  check_call(llmy_rmsnorm_f32_bf16(b.x, L.ffn_norm, b.h, rows, D, c.eps, nullptr), "rmsnorm");
+  check_call(llmy_rmsnorm_f32_bf16(b.x, L.ffn_norm, b.h, rows, D, c.eps, st), "rmsnorm");
   check_call(llmy_router_topk_bf16(b.h, L.router_norm, L.w_router, nullptr, b.idx, b.gates, rows,
-                                   D, E, k, c.eps, nullptr),
+                                   D, E, k, c.eps, st),
              "llmy_router_topk_bf16");
   check_call(llmy_moe_permute(b.idx, rows * k, E, b.counts, b.offsets, b.sorted, b.route_pos,
-                              nullptr),
+                              st),
              "llmy_moe_permute");
   check_call(llmy_moe_experts_bf16(b.h, b.offsets, b.sorted, b.gates, L.w_gate_up, L.w_down, b.act,
-                                   b.y, rows, D, Hf, E, k, kPacked, nullptr),
+                                   b.y, rows, D, Hf, E, k, kPacked, st),
              "llmy_moe_experts_bf16");
   check_call(llmy_moe_combine_norm(b.y, b.route_pos, next_norm, b.x, b.h, rows, D, k, c.eps,
-                                   nullptr),
+                                   st),
              "llmy_moe_combine_norm");
 }
 
@@ -618,11 +631,12 @@ const float* next_norm_of(const Model& m, int loop, int l, int loops) {
 
 // One decode step for all B rows; tokens already in s.step.tokens, s.pos set.
 void decode_step(Model& m, State& s, int loops) {
+  hipStream_t st_ = s.stream;
   const Config& c = m.cfg;
   Buffers& b = s.step;
   const int B = s.B, D = c.d_model, n = static_cast<int>(m.layers.size());
   check_call(llmy_embed_norm_bf16(b.tokens, m.embed, m.layers[0].mix_norm, b.x, b.h, B, D, c.vocab,
-                                  c.eps, nullptr),
+                                  c.eps, st_),
              "llmy_embed_norm_bf16");
   const int Hhd = c.attn_heads * c.attn_head_dim;
   for (int loop = 0; loop < loops; ++loop) {
@@ -630,33 +644,34 @@ void decode_step(Model& m, State& s, int loops) {
       const Layer& L = m.layers[l];
       LayerState& st = s.layers[static_cast<size_t>(loop) * n + l];
       if (L.kind == kAttn) {
-        linear(b.h, L.wqkv, b.qkv, nullptr, B, 3 * Hhd, D, kStoreBf16);
+        linear(b.h, L.wqkv, b.qkv, nullptr, B, 3 * Hhd, D, kStoreBf16, st_);
         check_call(llmy_banded_attn_decode_bf16(b.qkv, b.qkv + Hhd, b.qkv + 2 * Hhd, 3 * Hhd,
                                                 3 * Hhd, st.k, st.v, s.pos, b.ao, B, c.attn_heads,
                                                 c.attn_head_dim, c.window,
                                                 1.0f / std::sqrt(static_cast<float>(c.attn_head_dim)),
-                                                nullptr),
+                                                st_),
                    "llmy_banded_attn_decode_bf16");
-        linear(b.ao, L.wo, b.x, nullptr, B, D, Hhd, kResidAdd);
+        linear(b.ao, L.wo, b.x, nullptr, B, D, Hhd, kResidAdd, st_);
       } else {
         const int HV = c.gdn_heads * c.dv;
-        linear(b.h, L.wproj, b.proj, nullptr, B, c.nproj16(), D, kStoreF32);
+        linear(b.h, L.wproj, b.proj, nullptr, B, c.nproj16(), D, kStoreF32, st_);
         check_call(llmy_gdn_step_fused_f32(b.proj, c.nproj16(), L.bb, L.decay, st.S, b.go, b.h,
                                            st.hist, L.conv, b.cg, D, 4, B, c.gdn_heads, c.dk,
-                                           c.dv, nullptr),
+                                           c.dv, st_),
                    "llmy_gdn_step_fused_f32");
-        linear(b.go, L.wout, b.x, b.cg, B, D, HV, kResidGated);
+        linear(b.go, L.wout, b.x, b.cg, B, D, HV, kResidGated, st_);
       }
-      moe_block(m, L, b, B, next_norm_of(m, loop, l, loops), false);
+      moe_block(m, L, b, B, next_norm_of(m, loop, l, loops), false, st_);
     }
   }
-  linear(b.h, m.lm_head, s.logits, nullptr, B, c.vocab, D, kStoreF32);
-  check_call(llmy_sample_argmax_f32(s.logits, B, c.vocab, s.next, nullptr), "argmax");
+  linear(b.h, m.lm_head, s.logits, nullptr, B, c.vocab, D, kStoreF32, st_);
+  check_call(llmy_sample_argmax_f32(s.logits, B, c.vocab, s.next, st_), "argmax");
   s.last_loops = loops;
 }
 
 // Prefill of B fresh sequences of T tokens each (tokens on the host, [B, T]).
 void prefill(Model& m, State& s, const int32_t* tokens, int T, bool tokens_on_device) {
+  hipStream_t st_ = s.stream;
   const Config& c = m.cfg;
   const int B = s.B, R = B * T, D = c.d_model, n = static_cast<int>(m.layers.size());
   reset_state(s);
@@ -668,11 +683,11 @@ void prefill(Model& m, State& s, const int32_t* tokens, int T, bool tokens_on_de
     s.seq = std::move(nb);
   }
   Buffers& b = *s.seq;
-  check_hip(hipMemcpy(b.tokens, tokens, sizeof(int32_t) * R,
-                      tokens_on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice),
+  check_hip(hipMemcpyAsync(b.tokens, tokens, sizeof(int32_t) * R,
+                           tokens_on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice, st_),
             "tokens");
   check_call(llmy_embed_norm_bf16(b.tokens, m.embed, m.layers[0].mix_norm, b.x, b.h, R, D, c.vocab,
-                                  c.eps, nullptr),
+                                  c.eps, st_),
              "llmy_embed_norm_bf16");
   const int loops = c.num_loops;
   const int Hhd = c.attn_heads * c.attn_head_dim;
@@ -683,52 +698,81 @@ void prefill(Model& m, State& s, const int32_t* tokens, int T, bool tokens_on_de
       if (L.kind == kAttn) {
         // q, k, v from row slices of the packed wqkv (each a packed [Hhd, D] matrix)
         const size_t slice = static_cast<size_t>(Hhd) * D;
-        linear(b.h, L.wqkv, b.q, nullptr, R, Hhd, D, kStoreBf16);
-        linear(b.h, L.wqkv + slice, b.k, nullptr, R, Hhd, D, kStoreBf16);
-        linear(b.h, L.wqkv + 2 * slice, b.v, nullptr, R, Hhd, D, kStoreBf16);
+        linear(b.h, L.wqkv, b.q, nullptr, R, Hhd, D, kStoreBf16, st_);
+        linear(b.h, L.wqkv + slice, b.k, nullptr, R, Hhd, D, kStoreBf16, st_);
+        linear(b.h, L.wqkv + 2 * slice, b.v, nullptr, R, Hhd, D, kStoreBf16, st_);
         check_call(llmy_banded_attn_prefill_bf16(b.q, b.k, b.v, b.ao, B, T, c.attn_heads,
                                                  c.attn_head_dim, c.window,
                                                  1.0f / std::sqrt(static_cast<float>(c.attn_head_dim)),
-                                                 nullptr),
+                                                 st_),
                    "llmy_banded_attn_prefill_bf16");
         check_call(llmy_kv_cache_fill_bf16(b.k, b.v, Hhd, st.k, st.v, B, T, c.attn_heads,
-                                           c.attn_head_dim, c.window, nullptr),
+                                           c.attn_head_dim, c.window, st_),
                    "llmy_kv_cache_fill_bf16");
-        linear(b.ao, L.wo, b.x, nullptr, R, D, Hhd, kResidAdd);
+        linear(b.ao, L.wo, b.x, nullptr, R, D, Hhd, kResidAdd, st_);
       } else {
         const int H = c.gdn_heads, HV = H * c.dv;
-        linear(b.h, L.wproj, b.proj, nullptr, R, c.nproj16(), D, kStoreF32);
+        linear(b.h, L.wproj, b.proj, nullptr, R, c.nproj16(), D, kStoreF32, st_);
         check_call(llmy_gdn_prefill_prep_f32(b.proj, c.nproj16(), L.bb, L.decay, b.gq, b.gk, b.gv,
-                                             b.beta, b.g, R, H, c.dk, c.dv, nullptr),
+                                             b.beta, b.g, R, H, c.dk, c.dv, st_),
                    "llmy_gdn_prefill_prep_f32");
         check_call(llmy_gdn_prefill_bf16(b.gq, b.gk, b.gv, b.beta, b.g, st.S, b.go, b.ws, b.ws_bytes,
-                                         B, T, H, c.dk, c.dv, nullptr),
+                                         B, T, H, c.dk, c.dv, st_),
                    "llmy_gdn_prefill_bf16");
         check_call(llmy_gdn_gate_bf16(b.go, b.proj, c.nproj16(), 2 * H * c.dk + HV, b.go, R, HV,
-                                      nullptr),
+                                      st_),
                    "llmy_gdn_gate_bf16");
-        check_call(llmy_gdn_conv_gate_prefill(b.h, st.hist, L.conv, b.cg, B, T, D, 4, nullptr),
+        check_call(llmy_gdn_conv_gate_prefill(b.h, st.hist, L.conv, b.cg, B, T, D, 4, st_),
                    "llmy_gdn_conv_gate_prefill");
-        linear(b.go, L.wout, b.x, b.cg, R, D, HV, kResidGated);
+        linear(b.go, L.wout, b.x, b.cg, R, D, HV, kResidGated, st_);
       }
-      moe_block(m, L, b, R, next_norm_of(m, loop, l, loops), true);
+      moe_block(m, L, b, R, next_norm_of(m, loop, l, loops), true, st_);
     }
   }
   // last position of each sequence -> the decode buffer, then the LM head
-  check_hip(hipMemcpy2D(s.step.h, static_cast<size_t>(D) * 2,
-                        b.h + static_cast<size_t>(T - 1) * D, static_cast<size_t>(T) * D * 2,
-                        static_cast<size_t>(D) * 2, B, hipMemcpyDeviceToDevice),
+  check_hip(hipMemcpy2DAsync(s.step.h, static_cast<size_t>(D) * 2,
+                             b.h + static_cast<size_t>(T - 1) * D, static_cast<size_t>(T) * D * 2,
+                             static_cast<size_t>(D) * 2, B, hipMemcpyDeviceToDevice, st_),
             "last rows");
-  linear(s.step.h, m.lm_head, s.logits, nullptr, B, c.vocab, D, kStoreF32);
-  check_call(llmy_sample_argmax_f32(s.logits, B, c.vocab, s.next, nullptr), "argmax");
-  std::vector<int32_t> pos(B, T);
-  check_hip(hipMemcpy(s.pos, pos.data(), sizeof(int32_t) * B, hipMemcpyHostToDevice), "pos");
+  linear(s.step.h, m.lm_head, s.logits, nullptr, B, c.vocab, D, kStoreF32, st_);
+  check_call(llmy_sample_argmax_f32(s.logits, B, c.vocab, s.next, st_), "argmax");
+  s.hpos.assign(B, T);
+  check_hip(hipMemcpyAsync(s.pos, s.hpos.data(), sizeof(int32_t) * B, hipMemcpyHostToDevice, st_),
+            "pos");
+  check_hip(hipStreamSynchronize(st_), "prefill");
   s.last_loops = loops;
 }
 
 void copy_logits_out(const State& s, float* out) {
   const size_t bytes = sizeof(float) * s.B * s.model->cfg.vocab;
-  check_hip(hipMemcpy(out, s.logits, bytes, hipMemcpyDefault), "logits");
+  check_hip(hipMemcpyAsync(out, s.logits, bytes, hipMemcpyDefault, s.stream), "logits");
+  check_hip(hipStreamSynchronize(s.stream), "logits");
+}
+
+// The decode step for `loops` loops as one graph launch: captured on the
+// state's stream the first time (kernels only, no memory set or copy), then
+// replayed.  Token ids and positions live in device buffers the graph reads.
+void run_decode(Model& m, State& s, int loops) {
+  auto it = s.graphs.find(loops);
+  if (it == s.graphs.end()) {
+    hipGraph_t g = nullptr;
+    check_hip(hipStreamBeginCapture(s.stream, hipStreamCaptureModeRelaxed), "begin capture");
+    try {
+      decode_step(m, s, loops);
+    } catch (...) {
+      (void)hipStreamEndCapture(s.stream, &g);
+      if (g) (void)hipGraphDestroy(g);
+      throw;
+    }
+    check_hip(hipStreamEndCapture(s.stream, &g), "end capture");
+    hipGraphExec_t exec = nullptr;
+    const hipError_t e = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    check_hip(e, "graph instantiate");
+    it = s.graphs.emplace(loops, exec).first;
+  }
+  check_hip(hipGraphLaunch(it->second, s.stream), "graph launch");
+  s.last_loops = loops;
 }
 
 Model* as_model(llmy_model* p) { return reinterpret_cast<Model*>(p); }
@@ -824,7 +868,6 @@ int32_t llmy_prefill_batch(llmy_model* m, llmy_state* s, const int32_t* tokens, 
     (void)hipGetLastError();
     prefill(*as_model(m), *as_state(s), tokens, n_tokens, on_device);
     if (logits_out) copy_logits_out(*as_state(s), logits_out);
-    check_hip(hipDeviceSynchronize(), "prefill");
   });
 }
 
@@ -847,25 +890,29 @@ int32_t llmy_decode_batch(llmy_model* m, llmy_state* s, const int32_t* tokens,
     Model& mm = *as_model(m);
     State& st = *as_state(s);
     const int loops = num_loops <= 0 ? mm.loops : std::min<int32_t>(num_loops, mm.cfg.num_loops);
-    check_hip(hipMemcpy(st.step.tokens, tokens, sizeof(int32_t) * st.B, hipMemcpyDefault), "tokens");
     if (positions)
-      check_hip(hipMemcpy(st.pos, positions, sizeof(int32_t) * st.B, hipMemcpyDefault), "positions");
-    decode_step(mm, st, loops);
-    // the next token's position: one past this one
-    std::vector<int32_t> pos(st.B);
-    check_hip(hipMemcpy(pos.data(), st.pos, sizeof(int32_t) * st.B, hipMemcpyDeviceToHost), "pos");
-    for (int32_t& p : pos) ++p;
-    check_hip(hipMemcpy(st.pos, pos.data(), sizeof(int32_t) * st.B, hipMemcpyHostToDevice), "pos");
+      check_hip(hipMemcpy(st.hpos.data(), positions, sizeof(int32_t) * st.B, hipMemcpyDefault),
+                "positions");
+    check_hip(hipMemcpyAsync(st.step.tokens, tokens, sizeof(int32_t) * st.B, hipMemcpyDefault,
+                             st.stream),
+              "tokens");
+    check_hip(hipMemcpyAsync(st.pos, st.hpos.data(), sizeof(int32_t) * st.B,
+                             hipMemcpyHostToDevice, st.stream),
+              "positions");
+    run_decode(mm, st, loops);
+    for (int32_t& p : st.hpos) ++p;  // the next token's position: one past this one
     if (logits_out) copy_logits_out(st, logits_out);
-    check_hip(hipDeviceSynchronize(), "decode");
+    check_hip(hipStreamSynchronize(st.stream), "decode");
   });
 }
 
 int32_t llmy_greedy_tokens(const llmy_state* s, int32_t* out) {
   if (!s || !out) return 1;
   const State* st = reinterpret_cast<const State*>(s);
-  return static_cast<int32_t>(
-      hipMemcpy(out, st->next, sizeof(int32_t) * st->B, hipMemcpyDefault));
+  hipError_t e = hipMemcpyAsync(out, st->next, sizeof(int32_t) * st->B, hipMemcpyDefault,
+                                st->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(st->stream);
+  return static_cast<int32_t>(e);
 }
 
 int32_t llmy_sample(const float* logits, int32_t vocab_size, float temperature, int32_t top_k,
