@@ -461,6 +461,8 @@ struct Buffers {  // activations for `rows` token rows
   int rows = 0;
   float *x = nullptr, *proj = nullptr, *cg = nullptr, *gates = nullptr, *y = nullptr;
   float *beta = nullptr, *g = nullptr;
+  float* parts = nullptr;  // decode: mixer output projection partials [n, rows, D]
+  int max_parts = 0;
   uint16_t *h = nullptr, *qkv = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *ao = nullptr,
            *go = nullptr, *act = nullptr, *gq = nullptr, *gk = nullptr, *gv = nullptr;
   int32_t *tokens = nullptr, *idx = nullptr, *counts = nullptr, *offsets = nullptr,
@@ -521,6 +523,11 @@ void alloc_buffers(const Config& c, int rows, int B, int T, Buffers& b) {
   b.route_pos = b.arena.zeros<int32_t>(static_cast<size_t>(rows) * k);
   b.act = b.arena.zeros<uint16_t>(static_cast<size_t>(rows) * k * c.hidden);
   b.y = b.arena.zeros<float>(static_cast<size_t>(rows) * k * D);
+  if (T == 1 && rows <= 64 && Hhd % 256 == 0 && HV % 256 == 0 &&
+      std::max(Hhd, HV) / 256 <= 8) {
+    b.max_parts = std::max(Hhd, HV) / 256;
+    b.parts = b.arena.zeros<float>(static_cast<size_t>(b.max_parts) * rows * D);
+  }
   if (T > 1 && c.gdn_heads > 0) {
     b.ws_bytes = llmy_gdn_prefill_workspace_bytes(B, T, c.gdn_heads, c.dk, c.dv);
     if (b.ws_bytes < 0) throw std::runtime_error("GDN prefill workspace size");
@@ -580,26 +587,38 @@ void reset_state(State& s) {
 }
 
 // ------------------------------------------------------------------ forward
-constexpr int kStoreBf16 = 0, kStoreF32 = 1, kResidAdd = 2, kResidGated = 3, kPacked = 1;
+constexpr int kStoreBf16 = 0, kStoreF32 = 1, kResidAdd = 2, kResidGated = 3, kPartialF32 = 4,
+              kPacked = 1;
 
 void linear(const uint16_t* x, const uint16_t* w, void* out, const float* aux, int M, int N, int K,
             int epi, hipStream_t st) {
   check_call(llmy_linear_bf16(x, w, out, aux, M, N, K, epi, kPacked, st), "llmy_linear_bf16");
 }
 
+// Decode sizes for which the MoE front end is the fused router
+// (llmy_moe_route_decode) with route-indexed experts.
+bool fused_route(const Config& c, int rows) {
+  const int D = c.d_model;
+  return static_cast<long long>(c.experts) * D <= 24576 && (D == 256 || D == 512 || D == 1024) &&
+         c.top_k <= 8 && rows * c.top_k <= 2048;
+}
+
 // MoE of layer l over `rows` rows (x updated, h = next pre-norm of x).
 // Decode uses the fused router and route-indexed experts where the sizes
 // allow; a prefill always takes router -> permutation -> grouped experts.
+// `parts` (decode, fused router only): nparts partial products of the mixer's
+// output projection that the router folds into x first (times `gate` if set).
 void moe_block(const Model& m, const Layer& L, Buffers& b, int rows, const float* next_norm,
-               bool sequence, hipStream_t st) {
+               bool sequence, hipStream_t st, const float* parts = nullptr, int nparts = 0,
+               const float* gate = nullptr) {
   const Config& c = m.cfg;
   const int D = c.d_model, E = c.experts, k = c.top_k, Hf = c.hidden;
-  const bool fused = !sequence && static_cast<long long>(E) * D <= 24576 &&
-                     (D == 256 || D == 512 || D == 1024) && k <= 8 && rows * k <= 2048;
+  const bool fused = !sequence && fused_route(c, rows);
+  if (nparts > 0 && !fused) throw std::logic_error("partial products need the fused router");
   if (fused) {
-    check_call(llmy_moe_route_decode(b.x, L.ffn_norm, L.router_norm, L.w_router, b.h, b.idx,
-                                     b.gates, nullptr, nullptr, nullptr, nullptr, rows, D, E, k,
-                                     c.eps, st),
+    check_call(llmy_moe_route_decode(b.x, parts, nparts, gate, L.ffn_norm, L.router_norm,
+                                     L.w_router, b.h, b.idx, b.gates, nullptr, nullptr, nullptr,
+                                     nullptr, rows, D, E, k, c.eps, st),
                "llmy_moe_route_decode");
     check_call(llmy_moe_experts_routed_bf16(b.h, b.idx, b.gates, L.w_gate_up, L.w_down, b.act, b.y,
                                             rows, D, Hf, E, k, kPacked, st),
@@ -639,10 +658,14 @@ void decode_step(Model& m, State& s, int loops) {
                                   c.eps, st_),
              "llmy_embed_norm_bf16");
   const int Hhd = c.attn_heads * c.attn_head_dim;
+  // mixer output projections as partial products folded by the router
+  const bool defer = b.parts != nullptr && fused_route(c, B);
   for (int loop = 0; loop < loops; ++loop) {
     for (int l = 0; l < n; ++l) {
       const Layer& L = m.layers[l];
       LayerState& st = s.layers[static_cast<size_t>(loop) * n + l];
+      int nparts = 0;
+      const float* gate = nullptr;
       if (L.kind == kAttn) {
         linear(b.h, L.wqkv, b.qkv, nullptr, B, 3 * Hhd, D, kStoreBf16, st_);
         check_call(llmy_banded_attn_decode_bf16(b.qkv, b.qkv + Hhd, b.qkv + 2 * Hhd, 3 * Hhd,
@@ -651,7 +674,12 @@ void decode_step(Model& m, State& s, int loops) {
                                                 1.0f / std::sqrt(static_cast<float>(c.attn_head_dim)),
                                                 st_),
                    "llmy_banded_attn_decode_bf16");
-        linear(b.ao, L.wo, b.x, nullptr, B, D, Hhd, kResidAdd, st_);
+        if (defer) {
+          linear(b.ao, L.wo, b.parts, nullptr, B, D, Hhd, kPartialF32, st_);
+          nparts = Hhd / 256;
+        } else {
+          linear(b.ao, L.wo, b.x, nullptr, B, D, Hhd, kResidAdd, st_);
+        }
       } else {
         const int HV = c.gdn_heads * c.dv;
         linear(b.h, L.wproj, b.proj, nullptr, B, c.nproj16(), D, kStoreF32, st_);
@@ -659,9 +687,15 @@ void decode_step(Model& m, State& s, int loops) {
                                            st.hist, L.conv, b.cg, D, 4, B, c.gdn_heads, c.dk,
                                            c.dv, st_),
                    "llmy_gdn_step_fused_f32");
-        linear(b.go, L.wout, b.x, b.cg, B, D, HV, kResidGated, st_);
+        if (defer) {
+          linear(b.go, L.wout, b.parts, nullptr, B, D, HV, kPartialF32, st_);
+          nparts = HV / 256;
+          gate = b.cg;
+        } else {
+          linear(b.go, L.wout, b.x, b.cg, B, D, HV, kResidGated, st_);
+        }
       }
-      moe_block(m, L, b, B, next_norm_of(m, loop, l, loops), false, st_);
+      moe_block(m, L, b, B, next_norm_of(m, loop, l, loops), false, st_, b.parts, nparts, gate);
     }
   }
   linear(b.h, m.lm_head, s.logits, nullptr, B, c.vocab, D, kStoreF32, st_);

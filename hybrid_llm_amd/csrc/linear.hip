@@ -18,8 +18,16 @@
 //     The row-major [N, K] layout is also accepted (16-byte pieces of 16
 //     different rows per load instruction);
 //   * D layout: lane l holds D[4*(l/16) + i][l % 16], i = 0..3.
-// Epilogues: bf16/fp32 store, residual add, gated residual add, SwiGLU over
-// a (gate, up) row pair, and the gate-weighted MoE down store.
+// Epilogues: bf16/fp32 store, residual add, gated residual add, per-K-block
+// partial products, SwiGLU over a (gate, up) row pair, and the gate-weighted
+// MoE down store.
+//
+// Partial products (decode batches): one single-wave workgroup per (16-row
+// weight block, 256-wide K block) writes its fp32 product to its own slice;
+// the kernel that next reads the rows folds the slices in K order.  A
+// workgroup then pulls 32 KiB of activations into its CU instead of the
+// whole [M, K] tile, which is what bounds the 4-wave split-K kernel at small
+// N, and no residual is read back before the store.
 #include "common.hpp"
 #include "abi_util.hpp"
 
@@ -32,8 +40,9 @@ enum Epilogue : int {
   kStoreF32 = 1,      // out f32 [rows, ldo] = acc
   kResidAdd = 2,      // out f32 [rows, ldo] += acc
   kResidGated = 3,    // out f32 [rows, ldo] += acc * aux[row * ldo + n]
-  kSwiGLU = 4,        // out bf16 [rows, ldo] = silu(acc_gate) * acc_up  (paired rows)
-  kMoeDown = 5,       // out f32 [rows, ldo] = acc * aux[sorted_routes[row]]
+  kPartialF32 = 4,    // out f32 [K/256, rows, ldo]: slice s = the product over k in [256s, 256s+256)
+  kSwiGLU = 5,        // out bf16 [rows, ldo] = silu(acc_gate) * acc_up  (paired rows)
+  kMoeDown = 6,       // out f32 [rows, ldo] = acc * aux[sorted_routes[row]]
 };
 
 enum RowMode : int {
@@ -77,6 +86,7 @@ __host__ __device__ __forceinline__ long long packed_index(int n, int k, int K) 
 template <int EPI, int MODE, bool PACKED, int MB, int KB, int JT = 8>
 __global__ __launch_bounds__(512) void wsgemm_kernel(WsArgs a) {
   constexpr bool kPair = (EPI == kSwiGLU);
+  constexpr bool kSplit = (EPI == kPartialF32);  // blockIdx.y = K block, one wave
   constexpr int kSlots = (kPair ? 2 : 1) * MB * 4;
   constexpr int kRows = 16 * MB;  // token rows per chunk
   extern __shared__ float red[];  // [S][kSlots][64]
@@ -116,7 +126,7 @@ __global__ __launch_bounds__(512) void wsgemm_kernel(WsArgs a) {
   const int r = lane & 15;
   const int g = lane >> 4;
   const int K = a.K;
-  const uint16_t* wbase = a.w + static_cast<long long>(blockIdx.y) * a.w_expert_stride;
+  const uint16_t* wbase = a.w + (kSplit ? 0ll : static_cast<long long>(blockIdx.y) * a.w_expert_stride);
   // B operand address of (K block kb, MFMA j) for this lane: packed -> tile
   // (kb*8 + j) of the 16-row block; row-major -> row n0 + r, k = kb + 32j + 8g.
   const uint16_t* wlane =
@@ -147,7 +157,9 @@ __global__ __launch_bounds__(512) void wsgemm_kernel(WsArgs a) {
     // 256-wide K blocks; 4: half blocks, twice the waves for a given K);
     // K % (32 * JT * KB) == 0.
     constexpr int KP = 32 * JT;
-    for (int kb0 = wave * KP * KB; kb0 < K; kb0 += S * KP * KB) {
+    const int k_first = kSplit ? static_cast<int>(blockIdx.y) * KP * KB : wave * KP * KB;
+    const int k_end = kSplit ? k_first + KP * KB : K;
+    for (int kb0 = k_first; kb0 < k_end; kb0 += S * KP * KB) {
       // Issue every load of these K pieces before the first MFMA.
       uint4 bw[KB][JT], bu[KB][JT], av[KB][MB][JT];
 #pragma unroll
@@ -226,6 +238,8 @@ __global__ __launch_bounds__(512) void wsgemm_kernel(WsArgs a) {
     // store: the compiler cannot prove a store and a later load of another
     // row apart, and would otherwise wait out one memory round trip per value.
     const int n = n0 + r;
+    float* const outf = static_cast<float*>(a.out) +
+                        (kSplit ? static_cast<long long>(blockIdx.y) * a.M * a.ldo : 0ll);
     long long orow[MB][4];
     float in0[MB][4], in1[MB][4];
 #pragma unroll
@@ -260,8 +274,8 @@ __global__ __launch_bounds__(512) void wsgemm_kernel(WsArgs a) {
         const float v = acc[mb][i];
         if (EPI == kStoreBf16) {
           static_cast<uint16_t*>(a.out)[o] = f2bf(v);
-        } else if (EPI == kStoreF32) {
-          static_cast<float*>(a.out)[o] = v;
+        } else if (EPI == kStoreF32 || EPI == kPartialF32) {
+          outf[o] = v;
         } else if (EPI == kResidAdd) {
           static_cast<float*>(a.out)[o] = in0[mb][i] + v;
         } else if (EPI == kResidGated) {
@@ -456,7 +470,9 @@ extern "C" int32_t llmy_linear_bf16(const llmy_bf16* x, const llmy_bf16* w, void
                                     const float* aux, int32_t M, int32_t N, int32_t K,
                                     int32_t epilogue, int32_t weight_layout, void* stream) {
   LLMY_REQUIRE(M >= 0 && N > 0 && N % 16 == 0 && K > 0 && K % 256 == 0);
-  LLMY_REQUIRE(epilogue >= kStoreBf16 && epilogue <= kResidGated);
+  LLMY_REQUIRE(epilogue >= kStoreBf16 && epilogue <= kPartialF32);
+  // partial products: decode batches only (one row chunk per workgroup)
+  LLMY_REQUIRE(epilogue != kPartialF32 || M <= 64);
   LLMY_REQUIRE(weight_layout == 0 || weight_layout == 1);
   if (M == 0) return 0;
   LLMY_REQUIRE(x && w && out);
@@ -467,6 +483,15 @@ extern "C" int32_t llmy_linear_bf16(const llmy_bf16* x, const llmy_bf16* w, void
   a.M = M; a.N = N; a.K = K; a.ldx = K; a.ldo = N; a.route_k = 1;
   const hipStream_t s = as_stream(stream);
   const bool packed = weight_layout == 1;
+  if (epilogue == kPartialF32) {
+    LLMY_REQUIRE(static_cast<long long>(K / 256) * M * N < (1ll << 31));
+    const dim3 grid(N / 16, K / 256), block(64);
+    if (packed)
+      hipLaunchKernelGGL((wsgemm_kernel<kPartialF32, kDense, true, 4, 1, 8>), grid, block, 0, s, a);
+    else
+      hipLaunchKernelGGL((wsgemm_kernel<kPartialF32, kDense, false, 4, 1, 8>), grid, block, 0, s, a);
+    return launch_status();
+  }
   if (M >= kDenseMfmaMinRows && aligned(out, 16) && (aux == nullptr || aligned(aux, 16)) &&
       2ll * M * K < (1ll << 31) && 2ll * N * K < (1ll << 31))
     return dense_gemm_mfma(x, w, out, aux, M, N, K, epilogue, packed, s);

@@ -259,9 +259,17 @@ __global__ __launch_bounds__(1024) void moe_permute_kernel(
 // overlaps it, and the lanes split D and meet in one wave reduction per
 // expert.  Wave 0 takes the top-k and the softmax from the logits in LDS.
 // E * D <= 24576 (at most 24 float4 of W_r per lane).
+//
+// With nparts > 0 the residual row is first completed from the preceding
+// projection's per-K-block partial products: x[t] += sum_p parts[p][t]
+// (p ascending), or x[t] += gate[t] * sum_p parts[p][t] for a gated residual
+// (one fma per element), and the completed row is written back to x.  Every
+// wave reads x[t] before the workgroup barrier; wave 0 writes it after it.
+constexpr int kMaxParts = 8;
 template <int NCH>
 __global__ __launch_bounds__(256) void moe_route_norm_kernel(
-    const float* __restrict__ x, const float* __restrict__ ffn_w,
+    float* __restrict__ x, const float* __restrict__ parts, int nparts,
+    const float* __restrict__ gate, const float* __restrict__ ffn_w,
     const float* __restrict__ router_w, const float* __restrict__ w_router,
     uint16_t* __restrict__ h2, int32_t* __restrict__ idx_out, float* __restrict__ gates_out,
     int T, int E, int k, float eps) {
@@ -279,6 +287,51 @@ __global__ __launch_bounds__(256) void moe_route_norm_kernel(
     fw[c] = *reinterpret_cast<const float4*>(ffn_w + d);
     rw[c] = *reinterpret_cast<const float4*>(router_w + d);
   }
+  if (nparts > 0) {
+    float4 pv[kMaxParts][NCH], gv[NCH];
+#pragma unroll
+    for (int p = 0; p < kMaxParts; ++p) {
+      if (p < nparts) {
+#pragma unroll
+        for (int c = 0; c < NCH; ++c)
+          pv[p][c] = *reinterpret_cast<const float4*>(
+              parts + (static_cast<long long>(p) * T + t) * D + 4 * lane + 256 * c);
+      }
+    }
+    if (gate) {
+#pragma unroll
+      for (int c = 0; c < NCH; ++c)
+        gv[c] = *reinterpret_cast<const float4*>(gate + static_cast<long long>(t) * D +
+                                                 4 * lane + 256 * c);
+    }
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      float4 acc = pv[0][c];
+#pragma unroll
+      for (int p = 1; p < kMaxParts; ++p) {
+        if (p < nparts) {
+          acc.x += pv[p][c].x;
+          acc.y += pv[p][c].y;
+          acc.z += pv[p][c].z;
+          acc.w += pv[p][c].w;
+        }
+      }
+      if (gate) {
+        v[c].x = fmaf(acc.x, gv[c].x, v[c].x);
+        v[c].y = fmaf(acc.y, gv[c].y, v[c].y);
+        v[c].z = fmaf(acc.z, gv[c].z, v[c].z);
+        v[c].w = fmaf(acc.w, gv[c].w, v[c].w);
+      } else {
+        v[c].x += acc.x;
+        v[c].y += acc.y;
+        v[c].z += acc.z;
+        v[c].w += acc.w;
+      }
+    }
+  }
+  float4 xnew[NCH];
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) xnew[c] = v[c];
   float4 wq[MAXE][NCH];
 #pragma unroll
   for (int j = 0; j < MAXE; ++j) {
@@ -330,6 +383,11 @@ __global__ __launch_bounds__(256) void moe_route_norm_kernel(
   }
   __syncthreads();
   if (wave != 0) return;
+  if (nparts > 0) {
+#pragma unroll
+    for (int c = 0; c < NCH; ++c)
+      *reinterpret_cast<float4*>(x + static_cast<long long>(t) * D + 4 * lane + 256 * c) = xnew[c];
+  }
   float mine[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int s2 = 0; s2 < 2; ++s2) {
@@ -381,7 +439,9 @@ extern "C" int32_t llmy_moe_permute(const int32_t* expert_ids, int32_t n_routes,
   return launch_status();
 }
 
-extern "C" int32_t llmy_moe_route_decode(const float* x, const float* ffn_w, const float* router_w,
+extern "C" int32_t llmy_moe_route_decode(float* x, const float* parts, int32_t nparts,
+                                         const float* gate, const float* ffn_w,
+                                         const float* router_w,
                                          const float* w_router, llmy_bf16* h2, int32_t* idx,
                                          float* gates, int32_t* counts, int32_t* offsets,
                                          int32_t* sorted_routes, int32_t* route_pos, int32_t T,
@@ -390,6 +450,7 @@ extern "C" int32_t llmy_moe_route_decode(const float* x, const float* ffn_w, con
   LLMY_REQUIRE(T >= 0 && (D == 256 || D == 512 || D == 1024));
   LLMY_REQUIRE(E > 0 && E <= 256 && k > 0 && k <= 8 && k <= E);
   LLMY_REQUIRE(static_cast<long long>(E) * D <= 24576);
+  LLMY_REQUIRE(nparts >= 0 && nparts <= kMaxParts && (nparts > 0 || gate == nullptr));
   const bool permute = counts != nullptr;
   LLMY_REQUIRE(!permute || offsets);
   const hipStream_t s = as_stream(stream);
@@ -399,9 +460,10 @@ extern "C" int32_t llmy_moe_route_decode(const float* x, const float* ffn_w, con
     LLMY_REQUIRE(!permute || (sorted_routes && route_pos));
     LLMY_REQUIRE(aligned(x, 16) && aligned(ffn_w, 16) && aligned(router_w, 16) &&
                  aligned(w_router, 16) && aligned(h2, 8));
+    LLMY_REQUIRE(nparts == 0 || (parts && aligned(parts, 16) && (!gate || aligned(gate, 16))));
 #define LLMY_ROUTE(NCH)                                                                       \
-  hipLaunchKernelGGL(moe_route_norm_kernel<NCH>, dim3(T), dim3(256), 0, s, x,                    \
-                     ffn_w, router_w, w_router, h2, idx, gates, T, E, k, eps)
+  hipLaunchKernelGGL(moe_route_norm_kernel<NCH>, dim3(T), dim3(256), 0, s, x, parts, nparts,      \
+                     gate, ffn_w, router_w, w_router, h2, idx, gates, T, E, k, eps)
     switch (D) {
       case 256: LLMY_ROUTE(1); break;
       case 512: LLMY_ROUTE(2); break;

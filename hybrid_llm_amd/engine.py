@@ -132,6 +132,16 @@ class HybridDecoder:
         # sizes allow; else norm, router, permutation and sorted experts.
         self.fused_route = (E * D <= 24576 and D in (256, 512, 1024) and k <= 8
                             and B * k <= 2048)
+        # Mixer output projections (attention o, GDN out) as per-K-block
+        # partial products that the fused router folds into the residual: a
+        # workgroup then reads a 256-wide slice of the activations instead of
+        # all of them, and no residual round trip precedes the store.
+        n_parts = max(Ha * hd, Hg * dv) // 256
+        self.defer_resid = (self.fused_route and B <= 64 and (Ha * hd) % 256 == 0
+                            and (Hg * dv) % 256 == 0 and n_parts <= 8)
+        if self.defer_resid:
+            self.buf["parts"] = torch.zeros(n_parts, B, D, dtype=f32, device=dev)
+        self._pending: tuple | None = None
         # Optional record of every MoE application's expert ids (verification
         # aid: lets a checker replay the kernel's discrete routing decisions).
         self.route_log: torch.Tensor | None = None
@@ -157,8 +167,14 @@ class HybridDecoder:
         vn = qkv[:, 2 * Hhd:].view(B, H, hd)
         ops.banded_attn_decode(q, kn, vn, st["k"], st["v"], self.pos, cfg.attn_scale,
                                out=b["ao"])
-        ops.linear(b["ao"].view(B, Hhd), w[p + "wo"], out=b["x"], epilogue=ops.EPI_RESID_ADD,
-                   layout=ops.LAYOUT_PACKED)
+        if self.defer_resid:
+            parts = b["parts"][:Hhd // 256]
+            ops.linear(b["ao"].view(B, Hhd), w[p + "wo"], out=parts,
+                       epilogue=ops.EPI_PARTIAL_F32, layout=ops.LAYOUT_PACKED)
+            self._pending = (parts, None)
+        else:
+            ops.linear(b["ao"].view(B, Hhd), w[p + "wo"], out=b["x"],
+                       epilogue=ops.EPI_RESID_ADD, layout=ops.LAYOUT_PACKED)
 
     def _gdn(self, l: int, st: dict) -> None:
         w, b = self.w, self.buf
@@ -167,8 +183,14 @@ class HybridDecoder:
                    layout=ops.LAYOUT_PACKED)
         ops.gdn_step_fused(b["proj"], w[p + "bb"], w[p + "decay"], st["S"], out=b["go"],
                            conv=(b["h"], st["hist"], w[p + "conv"], b["cg"]))
-        ops.linear(b["go"], w[p + "wout"], out=b["x"], epilogue=ops.EPI_RESID_GATED, aux=b["cg"],
-                   layout=ops.LAYOUT_PACKED)
+        if self.defer_resid:
+            parts = b["parts"][:b["go"].shape[1] // 256]
+            ops.linear(b["go"], w[p + "wout"], out=parts, epilogue=ops.EPI_PARTIAL_F32,
+                       layout=ops.LAYOUT_PACKED)
+            self._pending = (parts, b["cg"])
+        else:
+            ops.linear(b["go"], w[p + "wout"], out=b["x"], epilogue=ops.EPI_RESID_GATED,
+                       aux=b["cg"], layout=ops.LAYOUT_PACKED)
 
     def _moe(self, l: int, next_norm: torch.Tensor | None) -> None:
         """Pre-MoE norm + router + permutation, experts, then the combine fused
@@ -177,8 +199,11 @@ class HybridDecoder:
         p = f"L{l}."
         if self.fused_route:
             # decode: router only; the experts derive their routes from the ids
+            parts, gate = self._pending if self._pending is not None else (None, None)
+            self._pending = None
             ops.moe_route_decode(b["x"], w[p + "ffn_norm"], w[p + "router_norm"],
-                                 w[p + "w_router"], cfg.top_k, cfg.eps, bufs=b, permute=False)
+                                 w[p + "w_router"], cfg.top_k, cfg.eps, bufs=b, permute=False,
+                                 parts=parts, gate=gate)
         else:
             ops.rmsnorm(b["x"], w[p + "ffn_norm"], cfg.eps, out=b["h"])
             from . import _lib

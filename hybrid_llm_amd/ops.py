@@ -116,6 +116,9 @@ def repetition_penalty_(logits: torch.Tensor, recent: torch.Tensor, penalty: flo
 
 # --------------------------------------------------------------------------- projections
 EPI_STORE_BF16, EPI_STORE_F32, EPI_RESID_ADD, EPI_RESID_GATED = 0, 1, 2, 3
+# per-256-wide-K-block partial products [K/256, M, N] fp32 (M <= 64), folded by
+# moe_route_decode(parts=...)
+EPI_PARTIAL_F32 = 4
 
 
 LAYOUT_ROWMAJOR, LAYOUT_PACKED = 0, 1
@@ -135,12 +138,17 @@ def linear(x: torch.Tensor, w: torch.Tensor, out: torch.Tensor | None = None,
            epilogue: int = EPI_STORE_BF16, aux: torch.Tensor | None = None,
            layout: int = LAYOUT_ROWMAJOR) -> torch.Tensor:
     """x [M,K] bf16 . w [N,K]^T with a fused epilogue (see llmy_linear_bf16).
-    ``layout=LAYOUT_PACKED`` when w came from pack_weights."""
+    ``layout=LAYOUT_PACKED`` when w came from pack_weights.  EPI_PARTIAL_F32
+    returns the per-K-block products [K/256, M, N]."""
     M, K = x.shape
     N = w.shape[0]
     _check(x, torch.bfloat16, "x")
     _check(w, torch.bfloat16, "w", (N, K))
-    if out is None:
+    if epilogue == EPI_PARTIAL_F32:
+        if out is None:
+            out = torch.empty(K // 256, M, N, dtype=torch.float32, device=x.device)
+        _check(out, torch.float32, "out", (K // 256, M, N))
+    elif out is None:
         if epilogue not in (EPI_STORE_BF16, EPI_STORE_F32):
             raise ValueError("residual epilogues need an explicit out tensor")
         dt = torch.bfloat16 if epilogue == EPI_STORE_BF16 else torch.float32
@@ -340,12 +348,23 @@ def gdn_step_fused(proj, beta_bias, decay_logit, state, out=None, conv=None) -> 
 
 
 def moe_route_decode(x, ffn_w, router_w, w_router, k, eps=1e-6, bufs=None,
-                     permute: bool = True) -> dict:
-    """Fused pre-MoE norm + router (+ the permutation unless permute=False)."""
+                     permute: bool = True, parts: torch.Tensor | None = None,
+                     gate: torch.Tensor | None = None) -> dict:
+    """Fused pre-MoE norm + router (+ the permutation unless permute=False).
+    ``parts`` [P, T, D]: partial products of the preceding projection
+    (EPI_PARTIAL_F32), folded into x first (x += sum, or x += gate * sum)."""
     T, D = x.shape
     E = w_router.shape[0]
     _check(x, torch.float32, "x")
     _check(w_router, torch.float32, "w_router", (E, D))
+    nparts = 0
+    if parts is not None:
+        nparts = parts.shape[0]
+        _check(parts, torch.float32, "parts", (nparts, T, D))
+        if gate is not None:
+            _check(gate, torch.float32, "gate", (T, D))
+    elif gate is not None:
+        raise ValueError("gate needs parts")
     dev = x.device
     if bufs is None:
         bufs = {"h": torch.empty(T, D, dtype=torch.bfloat16, device=dev),
@@ -357,7 +376,8 @@ def moe_route_decode(x, ffn_w, router_w, w_router, k, eps=1e-6, bufs=None,
                 "route_pos": torch.empty(T * k, dtype=torch.int32, device=dev)}
     b = bufs
     P = (lambda n: _ptr(b[n])) if permute else (lambda n: None)
-    _lib.call("llmy_moe_route_decode", _ptr(x), _ptr(ffn_w), _ptr(router_w), _ptr(w_router),
+    _lib.call("llmy_moe_route_decode", _ptr(x), _ptr(parts), nparts, _ptr(gate), _ptr(ffn_w),
+              _ptr(router_w), _ptr(w_router),
               _ptr(b["h"]), _ptr(b["idx"]), _ptr(b["gates"]), P("counts"), P("offsets"),
               P("sorted_routes"), P("route_pos"), T, D, E, k, eps, _stream())
     return b

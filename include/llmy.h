@@ -70,7 +70,10 @@ int32_t llmy_moe_permute(const int32_t* expert_ids, int32_t n_routes,
 
 /* Y[M,N] = X[M,K] . W[N,K]^T, bf16 operands, fp32 accumulation, with a fused
  * epilogue: 0 = store bf16 into out [M,N]; 1 = store fp32; 2 = out (fp32)
- * += Y (residual add); 3 = out (fp32) += Y * aux[M,N] (gated residual).
+ * += Y (residual add); 3 = out (fp32) += Y * aux[M,N] (gated residual);
+ * 4 = per-K-block partial products, M <= 64: out (fp32) [K/256, M, N], slice
+ * s = X[:, 256s:256s+256] . W[:, 256s:256s+256]^T, for a consumer that folds
+ * the slices in order (llmy_moe_route_decode).
  * weight_layout 0: W row-major [N,K] (nn.Linear); 1: W in the packed tile
  * order of llmy_pack_weights_bf16.  Limits: N % 16 == 0, K % 256 == 0.
  * M < 256 (decode batches): weight-streaming kernels; M >= 256 (prefill
@@ -287,8 +290,13 @@ int32_t llmy_moe_combine_norm(const float* y, const int32_t* route_pos,
  *   and (unless counts == NULL) the stable permutation of llmy_moe_permute —
  *   router with W_r staged in LDS, one wave per token, then the permutation.
  * Equivalent to llmy_rmsnorm_f32_bf16 + llmy_router_topk_bf16 +
- * llmy_moe_permute (context_router.py:62,71-74; moe.py:42-66). */
-int32_t llmy_moe_route_decode(const float* x, const float* ffn_w,
+ * llmy_moe_permute (context_router.py:62,71-74; moe.py:42-66).
+ * nparts in [0, 8]: first complete the residual from the preceding
+ * projection's partial products (llmy_linear_bf16 epilogue 4), parts
+ * [nparts, T, D]: x[t] += sum_p parts[p][t] (p ascending), or, with gate
+ * [T, D] non-NULL, x[t] += gate[t] * sum_p parts[p][t]; x is written back. */
+int32_t llmy_moe_route_decode(float* x, const float* parts, int32_t nparts,
+                              const float* gate, const float* ffn_w,
                               const float* router_w, const float* w_router,
                               llmy_bf16* h2, int32_t* idx, float* gates,
                               int32_t* counts, int32_t* offsets,

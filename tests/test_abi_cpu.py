@@ -126,3 +126,14 @@ def test_prefill_glue_rejects_bad_arguments(lib):
     assert conv(FAKE, FAKE, FAKE, FAKE, 2, 10, 256, 3, None) == INVALID           # kernel != 4
     assert conv(None, FAKE, FAKE, FAKE, 2, 10, 256, 4, None) == INVALID
     assert conv(None, None, None, None, 2, 0, 256, 4, None) == 0
+
+
+def test_partial_products_and_fold_reject_bad_arguments(lib):
+    lin = lib.llmy_linear_bf16
+    assert lin(FAKE, FAKE, FAKE, None, 65, 1024, 1024, 4, 1, None) == INVALID    # M > 64
+    assert lin(FAKE, FAKE, FAKE, None, 64, 1024, 1024, 5, 1, None) == INVALID    # epilogue
+    route = lib.llmy_moe_route_decode
+    rest = [FAKE] * 6 + [None] * 4  # ffn_w .. gates, then no permutation
+    assert route(FAKE, FAKE, 9, None, *rest, 64, 1024, 24, 2, 1e-6, None) == INVALID  # nparts
+    assert route(FAKE, None, 0, FAKE, *rest, 64, 1024, 24, 2, 1e-6, None) == INVALID  # gate alone
+    assert route(FAKE, None, 4, None, *rest, 64, 1024, 24, 2, 1e-6, None) == INVALID  # parts NULL

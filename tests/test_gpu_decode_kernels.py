@@ -70,6 +70,31 @@ def test_linear_epilogues(M, N, K, epi, layout):
     assert torch.allclose(out.cpu(), expect, atol=1e-4, rtol=1e-4)
 
 
+@pytest.mark.parametrize("M,N,K", [(64, 1024, 1024), (64, 1024, 2048), (1, 4112, 256),
+                                   (37, 1040, 512)])
+@pytest.mark.parametrize("layout", [0, 1])
+def test_linear_partial_products(M, N, K, layout):
+    """Epilogue 4: slice s is the product over the K block [256s, 256s+256),
+    and folding the slices in order is the residual-add epilogue bit for bit
+    (both sum the same 256-wide block products in K order)."""
+    g = torch.Generator().manual_seed(M + N + K)
+    x = _bf(torch.randn(M, K, generator=g))
+    w = _bf(torch.randn(N, K, generator=g) * 0.02)
+    wg = w.cuda() if layout == 0 else ops().pack_weights(w.cuda())
+    parts = ops().linear(x.cuda(), wg, epilogue=ops().EPI_PARTIAL_F32, layout=layout)
+    assert parts.shape == (K // 256, M, N)
+    for s in range(K // 256):
+        ref = x[:, 256 * s:256 * s + 256].float() @ w[:, 256 * s:256 * s + 256].float().t()
+        assert torch.allclose(parts[s].cpu(), ref, atol=1e-4, rtol=1e-4), s
+    base = torch.randn(M, N, generator=g).cuda()
+    want = base.clone()
+    ops().linear(x.cuda(), wg, out=want, epilogue=ops().EPI_RESID_ADD, layout=layout)
+    folded = parts[0].clone()
+    for s in range(1, K // 256):
+        folded += parts[s]
+    assert torch.equal(base + folded, want)
+
+
 def test_pack_layout_closed_form():
     # tile j, lane l, element e of block (nb, kb) = W[16nb + l%16][256kb + 32j + 8(l//16) + e]
     N, K = 32, 512
@@ -283,6 +308,37 @@ def test_moe_route_decode_equals_unfused(T, D, E, k):
     assert np.array_equal(fused["idx"].cpu().numpy()[safe], ref_idx[safe])
 
 
+@pytest.mark.parametrize("nparts,gated", [(4, False), (4, True), (1, False), (8, True)])
+def test_moe_route_decode_folds_partials(nparts, gated):
+    """x += sum_p parts[p] (p ascending; gated: one fma per element with the
+    gate), written back to x, then the same norm/router as on the folded x."""
+    T, D, E, k = 64, 1024, 24, 2
+    g = torch.Generator().manual_seed(nparts * 2 + gated)
+    x0 = (torch.randn(T, D, generator=g) * 2).cuda()
+    parts = (torch.randn(nparts, T, D, generator=g) * 0.5).cuda()
+    gate = torch.rand(T, D, generator=g).cuda() if gated else None
+    fw = (torch.rand(D, generator=g) + 0.5).cuda()
+    rw = (torch.rand(D, generator=g) + 0.5).cuda()
+    wr = (torch.randn(E, D, generator=g) * 0.02).cuda()
+    acc = parts[0].clone()
+    for p in range(1, nparts):
+        acc += parts[p]
+    if gated:
+        want = (acc.double() * gate.double() + x0.double()).float().cpu()
+    else:
+        want = (x0 + acc).cpu()
+    x = x0.clone()
+    got = ops().moe_route_decode(x, fw, rw, wr, k, parts=parts, gate=gate)
+    if gated:
+        # fma rounds once: within one fp32 ulp of the exactly rounded value
+        assert torch.allclose(x.cpu(), want, rtol=2 ** -23, atol=1e-30)
+    else:
+        assert torch.equal(x.cpu(), want)
+    ref = ops().moe_route_decode(x.clone(), fw, rw, wr, k)
+    for key in ("h", "idx", "gates", "counts", "offsets", "sorted_routes", "route_pos"):
+        assert torch.equal(got[key], ref[key]), key
+
+
 @pytest.mark.parametrize("D", [256, 1024])
 def test_embed_norm_and_combine_norm(D):
     g = torch.Generator().manual_seed(D)
@@ -329,15 +385,19 @@ def test_gdn_step_with_fused_conv_gate():
     assert torch.allclose(cg, cg2, atol=1e-6)
 
 
-@pytest.mark.parametrize("T,E", [(64, 24), (1, 8), (300, 24)])
-def test_moe_routed_equals_sorted(T, E):
+@pytest.mark.parametrize("T,E,D,H", [(64, 24, 512, 512), (1, 8, 512, 512), (300, 24, 512, 512),
+                                     # C5 decode shape: down K = 2048 is two pieces per wave
+                                     (64, 24, 1024, 2048),
+                                     # about 16 routes per expert: several 16-route chunks
+                                     (64, 8, 512, 512), (20, 24, 256, 512)])
+def test_moe_routed_equals_sorted(T, E, D, H):
     """Route-indexed experts (no permutation) match the sorted path row for
     row: y_routed[r] vs y_sorted[route_pos[r]].  At decode sizes (T*k <= 16*E)
     both run the same weight-streaming configuration and agree bit for bit;
     above that the sorted path runs the tiled MFMA GEMMs (another summation
     order), so the rows agree to bf16/fp32 rounding."""
-    wg, wu, wd, wr = _c2_weights(E=E, D=512, H=512, seed=T)
-    x = _bf(torch.randn(T, 512, generator=torch.Generator().manual_seed(T))).cuda()
+    wg, wu, wd, wr = _c2_weights(E=E, D=D, H=H, seed=T)
+    x = _bf(torch.randn(T, D, generator=torch.Generator().manual_seed(T))).cuda()
     wgu = ops().pack_weights(torch.cat([wg, wu], 1).cuda())
     wdn = ops().pack_weights(wd.cuda())
     idx, gates = ops().router_topk(x, wr.cuda(), 2)
@@ -345,7 +405,7 @@ def test_moe_routed_equals_sorted(T, E):
     act_s, y_s = ops().moe_experts(x, perm, gates, wgu, wdn, layout=1)
     act_r, y_r = ops().moe_experts_routed(x, idx, gates, wgu, wdn, layout=1)
     rp = perm["route_pos"].long()
-    xs = torch.randn(T, 512, device="cuda")
+    xs = torch.randn(T, D, device="cuda")
     xr = xs.clone()
     ops().moe_combine_norm(y_s, perm["route_pos"], xs, None, None, 2)
     ops().moe_combine_norm(y_r, None, xr, None, None, 2)
