@@ -91,12 +91,14 @@ struct NucLds {
   uint32_t pick_digit;
   int32_t pick_id;
   float red[kNucWaves];
+  float red_min[kNucWaves];
 };
 
 // Per-row weighting: x_max and log2(e) / T.
 struct NucRow {
   float m;
   float c;
+  float b;  // bucket path: buckets per log2 unit below the maximum
 };
 
 // Mass of a logit: trunc(2^47 * exp((x - max) / T)); the maximum itself (also
@@ -127,7 +129,7 @@ __device__ __forceinline__ u64 nuc_weight(float xj, uint32_t live, int j, NucRow
 }
 
 // Exclusive prefix sum over the block in thread order; *total = block sum.
-__device__ u64 nuc_excl_scan(u64 v, NucLds& sh, u64* total) {
+__device__ u64 nuc_excl_scan(u64 v, u64* wave_tot, u64* total) {
   const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
   u64 inc = v;
 #pragma unroll
@@ -135,12 +137,12 @@ __device__ u64 nuc_excl_scan(u64 v, NucLds& sh, u64* total) {
     const u64 o = __shfl_up(inc, off, kWave);
     if (lane >= off) inc += o;
   }
-  if (lane == kWave - 1) sh.wave_tot[wave] = inc;
+  if (lane == kWave - 1) wave_tot[wave] = inc;
   __syncthreads();
   u64 before = 0, all = 0;
   for (int w = 0; w < kNucWaves; ++w) {
-    if (w < wave) before += sh.wave_tot[w];
-    all += sh.wave_tot[w];
+    if (w < wave) before += wave_tot[w];
+    all += wave_tot[w];
   }
   __syncthreads();
   *total = all;
@@ -157,7 +159,7 @@ __device__ void nuc_scan(const u64* hist, int nb, u64 rem, NucLds& sh, uint32_t*
   u64 s = 0;
   for (int i = 0; i < per; ++i) s += hist[nb - 1 - (t * per + i)];
   u64 total;
-  u64 run = nuc_excl_scan(s, sh, &total);
+  u64 run = nuc_excl_scan(s, sh.wave_tot, &total);
   if (run < rem && rem <= run + s) {  // true for exactly one thread
     for (int i = 0; i < per; ++i) {
       const int d = nb - 1 - (t * per + i);
@@ -189,7 +191,7 @@ __device__ u64 nuc_top_hist(const float* x, uint32_t live, NucRow r, NucLds& sh)
     mine += w;
   }
   u64 total;
-  nuc_excl_scan(mine, sh, &total);  // also orders the histogram writes before any read
+  nuc_excl_scan(mine, sh.wave_tot, &total);  // also orders the histogram writes before any read
   return total;
 }
 
@@ -242,7 +244,7 @@ __device__ int nuc_select(const float* x, uint32_t live, NucRow r, int base, u64
     }
   }
   u64 ties;
-  const u64 before = nuc_excl_scan(static_cast<u64>(mine), sh, &ties);
+  const u64 before = nuc_excl_scan(static_cast<u64>(mine), sh.wave_tot, &ties);
   if (mine > 0 && before == 0) sh.tie_weight = wt;  // the first holder
   __syncthreads();
   const u64 w_tie = sh.tie_weight;
@@ -266,6 +268,154 @@ __device__ int nuc_select(const float* x, uint32_t live, NucRow r, int base, u64
   return id;
 }
 
+// ---------------------------------------------------------------------------
+// Nucleus + draw without top-k, by buckets (the order, masses and thresholds
+// of the radix select above, hence the same ids).
+//
+// An element's bucket is its log2 distance below the row maximum,
+// floor((max - x) * log2(e) / T * kFastBins / range), capped at the last
+// bucket; the maximum itself is bucket 0.  range is the row's own spread in
+// log2 units, (max - min) * log2(e) / T, capped at kFastRange = 48 octaves: a
+// mass below 1 (2^-47 of the maximum's) truncates to 0 and never holds a
+// threshold, so the capped range still spans every element that can be
+// picked, and a narrow row spreads over all the buckets (few members each:
+// little LDS atomic contention, small resolves).  The map is monotone (x1 > x2
+// gives bucket(x1) <= bucket(x2): a correctly rounded subtraction and products
+// with positive constants keep the order), so every element of a lower bucket
+// precedes every element of a higher one, and the running mass at a bucket's
+// start is the exact sum over the buckets before it.
+//
+// One scan of the bucket masses places both thresholds (the nucleus size and
+// the draw); inside the bucket holding a threshold its members (at most
+// kFastCap, else the caller falls back to the radix select) are gathered to
+// LDS and each computes its running mass in the exact order (key, then id).
+constexpr int kFastBins = 2 * kNucThreads;  // two per thread
+constexpr int kFastCap = kNucThreads;
+constexpr float kFastRange = 48.f;
+
+struct FastLds {
+  u64 mass[kFastBins];
+  u64 cand_mass[kFastCap];
+  uint32_t cand_key[kFastCap];
+  int32_t cand_id[kFastCap];
+  u64 wave_tot[kNucWaves];
+  u64 above;
+  u64 run;
+  int32_t ncand;
+  int32_t bin;
+  int32_t id;
+};
+
+__device__ __forceinline__ int fast_bin(float x, NucRow r) {
+  if (x == r.m) return 0;
+  const float d = ((r.m - x) * r.c) * r.b;
+  return d < static_cast<float>(kFastBins - 1) ? static_cast<int>(d) : kFastBins - 1;
+}
+
+// Bucket holding running mass thr (1 <= thr <= total), from the scan state of
+// thread t (bins 2t, 2t+1: masses h0, h1, exclusive prefix P): sets fs.bin and
+// fs.above (the mass of the buckets before it).
+__device__ void fast_find(u64 thr, u64 P, u64 h0, u64 h1, FastLds& fs) {
+  if (P < thr && thr <= P + h0 + h1) {  // exactly one thread
+    const int t = threadIdx.x;
+    if (thr <= P + h0) {
+      fs.bin = 2 * t;
+      fs.above = P;
+    } else {
+      fs.bin = 2 * t + 1;
+      fs.above = P + h0;
+    }
+  }
+  if (threadIdx.x == 0) fs.ncand = 0;
+  __syncthreads();
+}
+
+// The member of bucket fs.bin at which the running mass inside the bucket
+// reaches rem; false (uniformly) when the bucket has more than kFastCap
+// members.  *id = that member, *run = the bucket-local running mass through it.
+__device__ bool fast_resolve(const float* x, uint32_t live, NucRow r, int base, u64 rem,
+                             FastLds& fs, int* id, u64* run) {
+  const int bin = fs.bin;
+#pragma unroll
+  for (int j = 0; j < kNucPer; ++j) {
+    const float xj = nuc_x(x, j);
+    if (fast_bin(xj, r) != bin) continue;  // the mass only for the bucket's members
+    const u64 w = nuc_weight<false>(xj, live, j, r);
+    if (w != 0ull) {
+      const int slot = atomicAdd(&fs.ncand, 1);
+      if (slot < kFastCap) {
+        fs.cand_key[slot] = order_key(xj);
+        fs.cand_id[slot] = base + j;
+        fs.cand_mass[slot] = w;
+      }
+    }
+  }
+  __syncthreads();
+  const int n = fs.ncand;
+  if (n > kFastCap) return false;
+  const int t = threadIdx.x;
+  if (t < n) {
+    const uint32_t k = fs.cand_key[t];
+    const int my = fs.cand_id[t];
+    const u64 w = fs.cand_mass[t];
+    u64 before = 0ull;
+#pragma unroll 8
+    for (int i = 0; i < n; ++i) {
+      const uint32_t ki = fs.cand_key[i];
+      if (ki > k || (ki == k && fs.cand_id[i] < my)) before += fs.cand_mass[i];
+    }
+    if (before < rem && rem <= before + w) {  // exactly one member
+      fs.id = my;
+      fs.run = before + w;
+    }
+  }
+  __syncthreads();
+  *id = fs.id;
+  *run = fs.run;
+  __syncthreads();
+  return true;
+}
+
+// The whole draw without top-k; false (uniformly) when a bucket overflows or
+// the row has no mass, for the caller's radix path.
+__device__ bool fast_top_p(const float* x, uint32_t live, NucRow r, int base, float top_p,
+                           float u, FastLds& fs, int* out_id) {
+  const int t = threadIdx.x;
+  for (int i = t; i < kFastBins; i += kNucThreads) fs.mass[i] = 0ull;
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < kNucPer; ++j) {
+    const float xj = nuc_x(x, j);
+    const u64 w = nuc_weight<false>(xj, live, j, r);
+    if (w != 0ull) atomicAdd(&fs.mass[fast_bin(xj, r)], w);
+  }
+  __syncthreads();
+  const u64 h0 = fs.mass[2 * t], h1 = fs.mass[2 * t + 1];
+  u64 total;
+  const u64 P = nuc_excl_scan(h0 + h1, fs.wave_tot, &total);
+  if (total == 0ull) return false;
+  u64 kept = total;
+  int id;
+  u64 run;
+  if (top_p > 0.f && top_p < 1.f) {
+    u64 thr = static_cast<u64>(ceil(static_cast<double>(top_p) * static_cast<double>(total)));
+    thr = thr < 1ull ? 1ull : (thr > total ? total : thr);
+    fast_find(thr, P, h0, h1, fs);
+    const u64 above = fs.above;
+    if (!fast_resolve(x, live, r, base, thr - above, fs, &id, &run)) return false;
+    kept = above + run;
+  }
+  const double ud = static_cast<double>(u);
+  u64 y = 1ull;
+  if (ud > 0.0) y = static_cast<u64>(floor(ud * static_cast<double>(kept))) + 1ull;
+  if (y > kept) y = kept;
+  fast_find(y, P, h0, h1, fs);
+  const u64 above = fs.above;
+  if (!fast_resolve(x, live, r, base, y - above, fs, &id, &run)) return false;
+  *out_id = id;
+  return true;
+}
+
 template <bool kVec4>
 __global__ __launch_bounds__(kNucThreads) void top_p_kernel(const float* __restrict__ logits,
                                                             int V, float temperature, int top_k,
@@ -273,6 +423,7 @@ __global__ __launch_bounds__(kNucThreads) void top_p_kernel(const float* __restr
                                                             const float* __restrict__ u,
                                                             int32_t* __restrict__ out) {
   __shared__ NucLds sh;
+  __shared__ FastLds fs;
   const int t = threadIdx.x;
   const int lane = t & (kWave - 1), wave = t / kWave;
   const int base = t * kNucPer;
@@ -294,20 +445,44 @@ __global__ __launch_bounds__(kNucThreads) void top_p_kernel(const float* __restr
 #pragma unroll
     for (int j = 0; j < kNucPer; ++j) x[j] = base + j < V ? row[base + j] : 0.f;
   }
-  float m = -INFINITY;
+  float m = -INFINITY, mn = INFINITY;
 #pragma unroll
   for (int j = 0; j < kNucPer; ++j) {
     const bool ok = base + j < V;
     live |= static_cast<uint32_t>(ok) << j;
-    if (ok) m = fmaxf(m, x[j]);
+    if (ok) {
+      m = fmaxf(m, x[j]);
+      mn = fminf(mn, x[j]);
+    }
   }
   m = wave_max(m);
-  if (lane == 0) sh.red[wave] = m;
+  mn = -wave_max(-mn);
+  if (lane == 0) {
+    sh.red[wave] = m;
+    sh.red_min[wave] = mn;
+  }
   __syncthreads();
   m = sh.red[0];
-  for (int w = 1; w < kNucWaves; ++w) m = fmaxf(m, sh.red[w]);
-  const NucRow r{m, 1.4426950408889634f / temperature};  // log2(e) / T
+  mn = sh.red_min[0];
+  for (int w = 1; w < kNucWaves; ++w) {
+    m = fmaxf(m, sh.red[w]);
+    mn = fminf(mn, sh.red_min[w]);
+  }
+  const float c = 1.4426950408889634f / temperature;  // log2(e) / T
+  float range = (m - mn) * c;                          // NaN for a row of one infinity
+  if (!(range > 1e-6f)) range = 1e-6f;
+  if (range > kFastRange) range = kFastRange;
+  const NucRow r{m, c, static_cast<float>(kFastBins) / range};
 
+  // top_k <= 0: the bucket path (top_k >= V, the same id set, stays on the
+  // radix path below)
+  if (top_k <= 0) {
+    int id;
+    if (fast_top_p(x, live, r, base, top_p, u[blockIdx.x], fs, &id)) {
+      if (t == 0) out[blockIdx.x] = id;
+      return;
+    }
+  }
   u64 cum;
   uint32_t kkey;
   if (top_k > 0 && top_k < V) {

@@ -141,3 +141,33 @@ def test_repetition_penalty(n):
     recent[:, n // 2:] = recent[:, : n - n // 2]  # repeated ids are penalised once
     got = ops().repetition_penalty_(logits.clone().cuda(), recent.cuda(), 1.3).cpu()
     assert torch.equal(got, repetition_penalty(logits, recent.numpy(), 1.3))
+
+
+@pytest.mark.parametrize("kind", ["c5_0.6", "c5_2", "c5_8", "ties", "masked", "flat", "spiky"])
+def test_top_p_bucket_path_equals_radix_path(kind):
+    """Without top-k the kernel places the thresholds by log2-distance buckets;
+    top_k = V (the same id set) keeps the radix select.  Both sum the same
+    integer masses in the same order, so every row must pick the same id."""
+    g = torch.Generator().manual_seed(len(kind))
+    V = 32000
+    if kind.startswith("c5"):
+        logits = torch.randn(64, V, generator=g) * float(kind.split("_")[1])
+    elif kind == "ties":
+        logits = torch.round(torch.randn(64, V, generator=g) * 2) / 4
+    elif kind == "masked":
+        logits = torch.randn(64, V, generator=g)
+        logits[torch.rand(64, V, generator=g) < 0.7] = -float("inf")
+    elif kind == "flat":   # one bucket holds the row: the bucket path falls back
+        logits = torch.zeros(64, V)
+        logits[:, ::7] = 1e-3
+    else:                  # a few dominant ids
+        logits = torch.randn(64, V, generator=g)
+        logits[:, :5] += 30
+    L = logits.cuda()
+    for p in (P90, 0.5, 1.0, 1e-6):
+        u = torch.rand(64, generator=g)
+        u[0], u[1] = 0.0, 0.9999999
+        uc = u.cuda()
+        a = ops().sample_top_p(L, 0.8, p, uc, top_k=0)
+        b = ops().sample_top_p(L, 0.8, p, uc, top_k=V)
+        assert torch.equal(a, b), (kind, p, torch.nonzero(a != b)[:5])
