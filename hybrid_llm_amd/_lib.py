@@ -40,8 +40,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "llmy_gdn_prefill_workspace_bytes": (C.c_int64, [_I, _I, _I, _I, _I]),
     "llmy_gdn_prefill_bf16": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I, _I, _I, _I, _I, _P]),
     "llmy_gdn_step_bf16": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P]),
-    "llmy_gdn_step_fused_f32": (_I, [_P, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I,
-                                     _I, _I, _P]),
+    "llmy_gdn_step_fused_f32": (_I, [_P, _I64, _I, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I,
+                                     _I, _I, _I, _P]),
     "llmy_embed_norm_bf16": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _F, _P]),
     "llmy_moe_combine_norm": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _F, _P]),
     "llmy_moe_route_decode": (_I, [_P, _P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I,

@@ -463,6 +463,7 @@ struct Buffers {  // activations for `rows` token rows
   float *beta = nullptr, *g = nullptr;
   float* parts = nullptr;  // decode: mixer output projection partials [n, rows, D]
   int max_parts = 0;
+  float* proj_parts = nullptr;  // decode: GDN input projection partials [D/256, rows, nproj16]
   uint16_t *h = nullptr, *qkv = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *ao = nullptr,
            *go = nullptr, *act = nullptr, *gq = nullptr, *gk = nullptr, *gv = nullptr;
   int32_t *tokens = nullptr, *idx = nullptr, *counts = nullptr, *offsets = nullptr,
@@ -528,6 +529,8 @@ void alloc_buffers(const Config& c, int rows, int B, int T, Buffers& b) {
     b.max_parts = std::max(Hhd, HV) / 256;
     b.parts = b.arena.zeros<float>(static_cast<size_t>(b.max_parts) * rows * D);
   }
+  if (T == 1 && rows <= 64 && D % 256 == 0 && D / 256 <= 8 && c.gdn_heads > 0)
+    b.proj_parts = b.arena.zeros<float>(static_cast<size_t>(D / 256) * rows * c.nproj16());
   if (T > 1 && c.gdn_heads > 0) {
     b.ws_bytes = llmy_gdn_prefill_workspace_bytes(B, T, c.gdn_heads, c.dk, c.dv);
     if (b.ws_bytes < 0) throw std::runtime_error("GDN prefill workspace size");
@@ -682,8 +685,12 @@ void decode_step(Model& m, State& s, int loops) {
         }
       } else {
         const int HV = c.gdn_heads * c.dv;
-        linear(b.h, L.wproj, b.proj, nullptr, B, c.nproj16(), D, kStoreF32, st_);
-        check_call(llmy_gdn_step_fused_f32(b.proj, c.nproj16(), L.bb, L.decay, st.S, b.go, b.h,
+        // the input projection as partial products, summed by the step kernel
+        const bool pp = b.proj_parts != nullptr;
+        float* proj = pp ? b.proj_parts : b.proj;
+        linear(b.h, L.wproj, proj, nullptr, B, c.nproj16(), D, pp ? kPartialF32 : kStoreF32, st_);
+        check_call(llmy_gdn_step_fused_f32(proj, c.nproj16(), pp ? D / 256 : 1, L.bb, L.decay, st.S,
+                                           b.go, b.h,
                                            st.hist, L.conv, b.cg, D, 4, B, c.gdn_heads, c.dk,
                                            c.dv, st_),
                    "llmy_gdn_step_fused_f32");

@@ -15,7 +15,8 @@
 //   op:    q, k [B,H,DK] / v, gate [B,H,DV] bf16, beta, g [B,H] fp32 (q, k
 //          already L2-normalised; gate optional);
 //   model: the fused fp32 projection row [q | k | v | gate logits | beta
-//          logits] of the GDN block, from which the kernel applies the
+//          logits] of the GDN block (or nparts per-K-block partial products
+//          of it, summed here in slice order), from which the kernel applies the
 //          per-head L2 norm of q and k (clamp 1e-12, gated_deltanet.py:128-129),
 //          beta = sigmoid(logit + bias) (:130), gate = sigmoid(logit) (:131) and
 //          g = sigmoid(decay_logit[h]) (:132).
@@ -29,6 +30,8 @@ struct GdnStepArgs {
   const float *beta, *g;
   const float* proj;
   long long proj_ld;
+  int nparts;             // model variant: slices of proj, [nparts, B, proj_ld]
+  long long part_stride;  // floats between slices
   const float* beta_bias;
   const float* decay_logit;
   float* state;
@@ -89,6 +92,14 @@ __global__ __launch_bounds__(256) void gdn_step_kernel(GdnStepArgs a) {
   }
   if (MODEL) {
     const float* row = a.proj + static_cast<long long>(b) * a.proj_ld;
+    const int np = a.nparts;
+    const long long ps = a.part_stride;
+    // projection value at offset i of the row: the slices summed in order
+    auto pv = [&](int i) {
+      float v = row[i];
+      for (int sl = 1; sl < np; ++sl) v += row[sl * ps + i];
+      return v;
+    };
     const int HK = a.H * DK, HV = a.H * DV;
     if (wave < 2) {  // wave 0: q, wave 1: k -> L2 normalised
       const float* src = row + (wave == 0 ? 0 : HK) + h * DK;
@@ -97,7 +108,7 @@ __global__ __launch_bounds__(256) void gdn_step_kernel(GdnStepArgs a) {
 #pragma unroll
       for (int i = 0; i < (DK + 63) / 64; ++i) {
         const int d = lane + 64 * i;
-        vals[i] = d < DK ? src[d] : 0.f;
+        vals[i] = d < DK ? pv(static_cast<int>(src - row) + d) : 0.f;
         ss += vals[i] * vals[i];
       }
       const float r = rsqrtf(fmaxf(wave_sum(ss), 1e-12f));
@@ -109,11 +120,11 @@ __global__ __launch_bounds__(256) void gdn_step_kernel(GdnStepArgs a) {
       }
     } else if (wave == 2) {
       for (int d = lane; d < DV; d += 64) {
-        vs[d] = row[2 * HK + h * DV + d];
-        gs[d] = sigmoidf_(row[2 * HK + HV + h * DV + d]);
+        vs[d] = pv(2 * HK + h * DV + d);
+        gs[d] = sigmoidf_(pv(2 * HK + HV + h * DV + d));
       }
     } else if (lane == 0) {
-      bg[0] = sigmoidf_(row[2 * HK + 2 * HV + h] + a.beta_bias[h]);
+      bg[0] = sigmoidf_(pv(2 * HK + 2 * HV + h) + a.beta_bias[h]);
       bg[1] = sigmoidf_(a.decay_logit[h]);
     }
   } else {
@@ -216,7 +227,7 @@ extern "C" int32_t llmy_gdn_step_bf16(const llmy_bf16* q, const llmy_bf16* k, co
   return launch_gdn_step<false>(a, B, dk, dv, as_stream(stream));
 }
 
-extern "C" int32_t llmy_gdn_step_fused_f32(const float* proj, int64_t proj_ld,
+extern "C" int32_t llmy_gdn_step_fused_f32(const float* proj, int64_t proj_ld, int32_t nparts,
                                            const float* beta_bias, const float* decay_logit,
                                            float* state, llmy_bf16* out, const llmy_bf16* conv_h,
                                            llmy_bf16* conv_hist, const float* conv_w,
@@ -225,6 +236,8 @@ extern "C" int32_t llmy_gdn_step_fused_f32(const float* proj, int64_t proj_ld,
                                            void* stream) {
   LLMY_REQUIRE(B >= 0 && H > 0 && ((dk == 64 && dv == 64) || (dk == 128 && dv == 128)));
   LLMY_REQUIRE(proj_ld >= static_cast<int64_t>(H) * (2 * dk + 2 * dv + 1));
+  LLMY_REQUIRE(nparts >= 1 && nparts <= 8);
+  LLMY_REQUIRE(static_cast<long long>(nparts) * B * proj_ld < (1ll << 31));
   if (B == 0) return 0;
   LLMY_REQUIRE(proj && beta_bias && decay_logit && state && out);
   LLMY_REQUIRE(aligned(state, 16));
@@ -234,6 +247,7 @@ extern "C" int32_t llmy_gdn_step_fused_f32(const float* proj, int64_t proj_ld,
   }
   GdnStepArgs a{};
   a.proj = proj; a.proj_ld = proj_ld; a.beta_bias = beta_bias; a.decay_logit = decay_logit;
+  a.nparts = nparts; a.part_stride = static_cast<long long>(B) * proj_ld;
   a.state = state; a.out = out; a.H = H;
   a.conv_h = conv_h; a.conv_hist = conv_hist; a.conv_w = conv_w; a.conv_out = conv_out; a.D = D;
   return launch_gdn_step<true>(a, B, dk, dv, as_stream(stream));

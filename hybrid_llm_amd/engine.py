@@ -141,6 +141,11 @@ class HybridDecoder:
                             and (Hg * dv) % 256 == 0 and n_parts <= 8)
         if self.defer_resid:
             self.buf["parts"] = torch.zeros(n_parts, B, D, dtype=f32, device=dev)
+        # The GDN input projection the same way: its partials are summed by
+        # the GDN step kernel as it reads the row.
+        self.proj_parts = B <= 64 and D % 256 == 0 and D // 256 <= 8 and bool(cfg.gdn_layers())
+        if self.proj_parts:
+            self.buf["proj_parts"] = torch.zeros(D // 256, B, nproj, dtype=f32, device=dev)
         self._pending: tuple | None = None
         # Optional record of every MoE application's expert ids (verification
         # aid: lets a checker replay the kernel's discrete routing decisions).
@@ -179,9 +184,15 @@ class HybridDecoder:
     def _gdn(self, l: int, st: dict) -> None:
         w, b = self.w, self.buf
         p = f"L{l}."
-        ops.linear(b["h"], w[p + "wproj"], out=b["proj"], epilogue=ops.EPI_STORE_F32,
-                   layout=ops.LAYOUT_PACKED)
-        ops.gdn_step_fused(b["proj"], w[p + "bb"], w[p + "decay"], st["S"], out=b["go"],
+        if self.proj_parts:
+            proj = b["proj_parts"]
+            ops.linear(b["h"], w[p + "wproj"], out=proj, epilogue=ops.EPI_PARTIAL_F32,
+                       layout=ops.LAYOUT_PACKED)
+        else:
+            proj = b["proj"]
+            ops.linear(b["h"], w[p + "wproj"], out=proj, epilogue=ops.EPI_STORE_F32,
+                       layout=ops.LAYOUT_PACKED)
+        ops.gdn_step_fused(proj, w[p + "bb"], w[p + "decay"], st["S"], out=b["go"],
                            conv=(b["h"], st["hist"], w[p + "conv"], b["cg"]))
         if self.defer_resid:
             parts = b["parts"][:b["go"].shape[1] // 256]

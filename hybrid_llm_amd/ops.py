@@ -325,10 +325,14 @@ def gdn_step(q, k, v, beta, g, state, gate=None, out=None) -> torch.Tensor:
 
 
 def gdn_step_fused(proj, beta_bias, decay_logit, state, out=None, conv=None) -> torch.Tensor:
-    """GDN step from the fused fp32 projection; ``conv=(h, hist, w, cg_out)``
+    """GDN step from the fused fp32 projection [B, ld] (or its per-K-block
+    partial products [P, B, ld], summed in order); ``conv=(h, hist, w, cg_out)``
     also computes the causal conv gate in the same launch."""
     B, H, dk, dv = state.shape
     _check(proj, torch.float32, "proj")
+    nparts = proj.shape[0] if proj.dim() == 3 else 1
+    if proj.dim() == 3 and proj.shape[1] != B:
+        raise ValueError(f"proj: {tuple(proj.shape)} has {proj.shape[1]} rows, state {B}")
     _check(state, torch.float32, "state")
     if out is None:
         out = torch.empty(B, H * dv, dtype=torch.bfloat16, device=proj.device)
@@ -341,7 +345,7 @@ def gdn_step_fused(proj, beta_bias, decay_logit, state, out=None, conv=None) -> 
         _check(hist, torch.bfloat16, "conv_hist", (B, 3, D))
         _check(cw, torch.float32, "conv_w", (D, 4))
         _check(cg, torch.float32, "conv_out", (B, D))
-    _lib.call("llmy_gdn_step_fused_f32", _ptr(proj), proj.shape[1], _ptr(beta_bias),
+    _lib.call("llmy_gdn_step_fused_f32", _ptr(proj), proj.shape[-1], nparts, _ptr(beta_bias),
               _ptr(decay_logit), _ptr(state), _ptr(out), _ptr(ch), _ptr(hist), _ptr(cw), _ptr(cg),
               D, 4, B, H, dk, dv, _stream())
     return out

@@ -201,8 +201,10 @@ int32_t llmy_gdn_step_bf16(const llmy_bf16* q, const llmy_bf16* k,
  * then the step above; out [B, H*dv] bf16.  When conv_h != NULL the causal
  * conv gate of llmy_gdn_conv_gate is computed in the same launch
  * (conv_h [B,D] bf16 mixer input, conv_hist [B,3,D], conv_w [D,4],
- * conv_out [B,D] fp32; D % H == 0, conv_kernel == 4). */
-int32_t llmy_gdn_step_fused_f32(const float* proj, int64_t proj_ld,
+ * conv_out [B,D] fp32; D % H == 0, conv_kernel == 4).  nparts in [1, 8]: proj
+ * holds nparts slices [nparts, B, proj_ld] (the per-K-block partial products
+ * of llmy_linear_bf16 epilogue 4), summed in slice order; 1 = the row itself. */
+int32_t llmy_gdn_step_fused_f32(const float* proj, int64_t proj_ld, int32_t nparts,
                                 const float* beta_bias, const float* decay_logit,
                                 float* state, llmy_bf16* out, const llmy_bf16* conv_h,
                                 llmy_bf16* conv_hist, const float* conv_w,

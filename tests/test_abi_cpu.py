@@ -137,3 +137,11 @@ def test_partial_products_and_fold_reject_bad_arguments(lib):
     assert route(FAKE, FAKE, 9, None, *rest, 64, 1024, 24, 2, 1e-6, None) == INVALID  # nparts
     assert route(FAKE, None, 0, FAKE, *rest, 64, 1024, 24, 2, 1e-6, None) == INVALID  # gate alone
     assert route(FAKE, None, 4, None, *rest, 64, 1024, 24, 2, 1e-6, None) == INVALID  # parts NULL
+
+
+def test_gdn_step_partial_slices_reject_bad_arguments(lib):
+    f = lib.llmy_gdn_step_fused_f32
+    tail = [FAKE, FAKE, FAKE, FAKE, None, None, None, None, 0, 4, 64, 16, 64, 64, None]
+    assert f(FAKE, 4112, 0, *tail) == INVALID     # nparts < 1
+    assert f(FAKE, 4112, 9, *tail) == INVALID     # nparts > 8
+    assert f(FAKE, 4000, 4, *tail) == INVALID     # ld below the row

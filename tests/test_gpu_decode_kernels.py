@@ -256,6 +256,26 @@ def test_gdn_step_fused_projection():
     close_bf16(out.view(B, H, d), o_ref)
 
 
+@pytest.mark.parametrize("nparts", [2, 4, 8])
+def test_gdn_step_fused_partial_products(nparts):
+    """Projection slices [P, B, ld] are summed in slice order by the step:
+    the same outputs and state as the step on the summed row, bit for bit."""
+    B, H, d = 64, 16, 64
+    g = torch.Generator().manual_seed(nparts)
+    ld = 4 * H * d + H + 16
+    parts = (torch.randn(nparts, B, ld, generator=g) * 0.5).cuda()
+    bb = (torch.randn(H, generator=g) * 0.1).cuda()
+    decay = torch.randn(H, generator=g).cuda()
+    S0 = (torch.randn(B, H, d, d, generator=g) * 0.1).cuda()
+    summed = parts[0].clone()
+    for p in range(1, nparts):
+        summed += parts[p]
+    S1, S2 = S0.clone(), S0.clone()
+    o1 = ops().gdn_step_fused(parts, bb, decay, S1)
+    o2 = ops().gdn_step_fused(summed, bb, decay, S2)
+    assert torch.equal(o1, o2) and torch.equal(S1, S2)
+
+
 # ---------------------------------------------------------------- glue
 def test_rmsnorm_embed_conv():
     g = torch.Generator().manual_seed(8)
