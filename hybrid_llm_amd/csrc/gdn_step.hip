@@ -45,7 +45,9 @@ struct GdnStepArgs {
   int D;
 };
 
-template <int DK, int DV, bool MODEL>
+// NP: compile-time bound on the projection slices (1, 4 or 8), so that every
+// slice load of a value is issued before the first add.
+template <int DK, int DV, bool MODEL, int NP = 1>
 __global__ __launch_bounds__(256) void gdn_step_kernel(GdnStepArgs a) {
   constexpr int CPT = DV / 4;        // threads per state row
   constexpr int RPP = 256 / CPT;     // rows per pass
@@ -69,35 +71,19 @@ __global__ __launch_bounds__(256) void gdn_step_kernel(GdnStepArgs a) {
 
   const int lane = t & 63;
   const int wave = t >> 6;
-  if (MODEL && a.conv_h != nullptr) {
-    // Causal depthwise conv gate (gated_deltanet.py:257-268) for this head's
-    // D/H channels of row b: window = [hist[0..2], h]; out = sigmoid(w . window);
-    // the history shifts by one.  Each thread owns one channel.
-    const int per = a.D / a.H;
-    for (int c = t; c < per; c += 256) {
-      const int d = h * per + c;
-      uint16_t* hb = a.conv_hist + static_cast<long long>(b) * 3 * a.D + d;
-      const uint16_t w0 = hb[0], w1 = hb[a.D], w2 = hb[2 * a.D];
-      const uint16_t w3 = a.conv_h[static_cast<long long>(b) * a.D + d];
-      const float4 cw = *reinterpret_cast<const float4*>(a.conv_w + 4 * d);
-      float acc = cw.x * bf2f(w0);
-      acc = fmaf(cw.y, bf2f(w1), acc);
-      acc = fmaf(cw.z, bf2f(w2), acc);
-      acc = fmaf(cw.w, bf2f(w3), acc);
-      a.conv_out[static_cast<long long>(b) * a.D + d] = sigmoidf_(acc);
-      hb[0] = w1;
-      hb[a.D] = w2;
-      hb[2 * a.D] = w3;
-    }
-  }
   if (MODEL) {
     const float* row = a.proj + static_cast<long long>(b) * a.proj_ld;
     const int np = a.nparts;
     const long long ps = a.part_stride;
     // projection value at offset i of the row: the slices summed in order
+    // (slices past np repeat the last one and are not added)
     auto pv = [&](int i) {
-      float v = row[i];
-      for (int sl = 1; sl < np; ++sl) v += row[sl * ps + i];
+      float t[NP];
+#pragma unroll
+      for (int sl = 0; sl < NP; ++sl) t[sl] = row[min(sl, np - 1) * ps + i];
+      float v = t[0];
+#pragma unroll
+      for (int sl = 1; sl < NP; ++sl) v = sl < np ? v + t[sl] : v;
       return v;
     };
     const int HK = a.H * DK, HV = a.H * DV;
@@ -141,6 +127,29 @@ __global__ __launch_bounds__(256) void gdn_step_kernel(GdnStepArgs a) {
     if (t == 0) {
       bg[0] = a.beta[bh];
       bg[1] = a.g[bh];
+    }
+  }
+  // After the projection reads: its global stores would otherwise hold them
+  // back (the compiler cannot tell the buffers apart).
+  if (MODEL && a.conv_h != nullptr) {
+    // Causal depthwise conv gate (gated_deltanet.py:257-268) for this head's
+    // D/H channels of row b: window = [hist[0..2], h]; out = sigmoid(w . window);
+    // the history shifts by one.  Each thread owns one channel.
+    const int per = a.D / a.H;
+    for (int c = t; c < per; c += 256) {
+      const int d = h * per + c;
+      uint16_t* hb = a.conv_hist + static_cast<long long>(b) * 3 * a.D + d;
+      const uint16_t w0 = hb[0], w1 = hb[a.D], w2 = hb[2 * a.D];
+      const uint16_t w3 = a.conv_h[static_cast<long long>(b) * a.D + d];
+      const float4 cw = *reinterpret_cast<const float4*>(a.conv_w + 4 * d);
+      float acc = cw.x * bf2f(w0);
+      acc = fmaf(cw.y, bf2f(w1), acc);
+      acc = fmaf(cw.z, bf2f(w2), acc);
+      acc = fmaf(cw.w, bf2f(w3), acc);
+      a.conv_out[static_cast<long long>(b) * a.D + d] = sigmoidf_(acc);
+      hb[0] = w1;
+      hb[a.D] = w2;
+      hb[2 * a.D] = w3;
     }
   }
   __syncthreads();
@@ -196,17 +205,28 @@ __global__ __launch_bounds__(256) void gdn_step_kernel(GdnStepArgs a) {
   }
 }
 
-template <bool MODEL>
-static int32_t launch_gdn_step(const GdnStepArgs& a, int B, int dk, int dv, hipStream_t s) {
+template <bool MODEL, int NP>
+static int32_t launch_gdn_step_np(const GdnStepArgs& a, int B, int dk, int dv, hipStream_t s) {
   const dim3 grid(B * a.H), block(256);
   if (dk == 64 && dv == 64) {
-    hipLaunchKernelGGL((gdn_step_kernel<64, 64, MODEL>), grid, block, 0, s, a);
+    hipLaunchKernelGGL((gdn_step_kernel<64, 64, MODEL, NP>), grid, block, 0, s, a);
   } else if (dk == 128 && dv == 128) {
-    hipLaunchKernelGGL((gdn_step_kernel<128, 128, MODEL>), grid, block, 0, s, a);
+    hipLaunchKernelGGL((gdn_step_kernel<128, 128, MODEL, NP>), grid, block, 0, s, a);
   } else {
     return static_cast<int32_t>(hipErrorInvalidValue);
   }
   return launch_status();
+}
+
+template <bool MODEL>
+static int32_t launch_gdn_step(const GdnStepArgs& a, int B, int dk, int dv, hipStream_t s) {
+  if constexpr (!MODEL) {
+    return launch_gdn_step_np<false, 1>(a, B, dk, dv, s);
+  } else {
+    if (a.nparts <= 1) return launch_gdn_step_np<true, 1>(a, B, dk, dv, s);
+    if (a.nparts <= 4) return launch_gdn_step_np<true, 4>(a, B, dk, dv, s);
+    return launch_gdn_step_np<true, 8>(a, B, dk, dv, s);
+  }
 }
 
 }  // namespace llmy
