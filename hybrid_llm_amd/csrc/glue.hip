@@ -119,7 +119,10 @@ __global__ __launch_bounds__(256) void embed_norm_kernel(const int32_t* __restri
 
 // MoE combine fused with the next RMSNorm: x[t] += sum_j y[route_pos[t*k+j]]
 // (j ascending), then h[t] = bf16(RMSNorm(x[t]) * w) (skipped when w is null).
-// One wave per row.
+// One wave per row.  Routes are taken in groups of KG, and each group's route
+// indices, y rows (with x and the norm weight in the first group) are
+// requested together: a runtime loop over k waits on each load in turn.
+constexpr int kCombineGroup = 2;
 template <int NCH>
 __global__ __launch_bounds__(256) void combine_norm_kernel(const float* __restrict__ y,
                                                            const int32_t* __restrict__ route_pos,
@@ -128,26 +131,61 @@ __global__ __launch_bounds__(256) void combine_norm_kernel(const float* __restri
                                                            uint16_t* __restrict__ h, int T, int k,
                                                            float eps) {
   constexpr int D = NCH * 256;
+  constexpr int KG = kCombineGroup;
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (t >= T) return;
   float* xr = x + static_cast<long long>(t) * D;
-  float4 v[NCH];
+  float4 v[NCH], wv[NCH], s[NCH];
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) s[c] = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int j0 = 0; j0 < k; j0 += KG) {
+    int p[KG];
+#pragma unroll
+    for (int j = 0; j < KG; ++j) {
+      const int jj = min(j0 + j, k - 1);  // past k: repeats the last route, not added
+      p[j] = route_pos ? min(max(route_pos[t * k + jj], 0), T * k - 1) : t * k + jj;
+    }
+    float4 yv[KG][NCH];
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      const int d = 4 * lane + 256 * c;
+#pragma unroll
+      for (int j = 0; j < KG; ++j)
+        yv[j][c] = *reinterpret_cast<const float4*>(y + static_cast<long long>(p[j]) * D + d);
+      if (j0 == 0) {
+        v[c] = *reinterpret_cast<const float4*>(xr + d);
+        if (w != nullptr) wv[c] = *reinterpret_cast<const float4*>(w + d);
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+#pragma unroll
+      for (int j = 0; j < KG; ++j) {
+        if (j0 + j < k) {
+          s[c].x += yv[j][c].x; s[c].y += yv[j][c].y; s[c].z += yv[j][c].z; s[c].w += yv[j][c].w;
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    v[c].x += s[c].x; v[c].y += s[c].y; v[c].z += s[c].z; v[c].w += s[c].w;
+    *reinterpret_cast<float4*>(xr + 4 * lane + 256 * c) = v[c];
+  }
+  if (w == nullptr) return;
+  float ss = 0.f;
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) ss += v[c].x * v[c].x + v[c].y * v[c].y + v[c].z * v[c].z + v[c].w * v[c].w;
+  const float r = rsqrtf(wave_sum(ss) / static_cast<float>(D) + eps);
+  uint16_t* out = h + static_cast<long long>(t) * D;
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
     const int d = 4 * lane + 256 * c;
-    float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int j = 0; j < k; ++j) {
-      const int p = route_pos ? min(max(route_pos[t * k + j], 0), T * k - 1) : t * k + j;
-      const float4 yv = *reinterpret_cast<const float4*>(y + static_cast<long long>(p) * D + d);
-      s.x += yv.x; s.y += yv.y; s.z += yv.z; s.w += yv.w;
-    }
-    float4 xv = *reinterpret_cast<const float4*>(xr + d);
-    xv.x += s.x; xv.y += s.y; xv.z += s.z; xv.w += s.w;
-    *reinterpret_cast<float4*>(xr + d) = xv;
-    v[c] = xv;
+    *reinterpret_cast<uint2*>(out + d) =
+        make_uint2(pack_bf2(v[c].x * r * wv[c].x, v[c].y * r * wv[c].y),
+                   pack_bf2(v[c].z * r * wv[c].z, v[c].w * r * wv[c].w));
   }
-  if (w != nullptr) norm_row_store<NCH>(v, w, h + static_cast<long long>(t) * D, lane, eps);
 }
 
 }  // namespace llmy

@@ -319,9 +319,15 @@ constexpr int kLdsRow = 256 + 8;  // bf16 elements per staged token row (16-byte
 // wsgemm_kernel): four waves then share one staged 32 KiB activation slice
 // for 64 weight rows, 2.5x less traffic into each CU than four single-wave
 // workgroups of 16 rows.
-template <int EPI>
-__global__ __launch_bounds__(256) void dense_lds_kernel(WsArgs a) {
+//
+// WV waves per workgroup (16 weight rows each) share the staged tile; with PF
+// each wave requests the next K block's weights before the current block's
+// MFMAs.
+template <int EPI, int WV = 4, bool PF = false>
+__global__ __launch_bounds__(64 * WV) void dense_lds_kernel(WsArgs a) {
   constexpr bool kSplit = (EPI == kPartialF32);
+  constexpr int kThreads = 64 * WV;
+  constexpr int kStage = 2048 / kThreads;  // 16-byte pieces per thread of a [64 x 256] tile
   __shared__ __align__(16) uint16_t As[64 * kLdsRow];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -329,7 +335,7 @@ __global__ __launch_bounds__(256) void dense_lds_kernel(WsArgs a) {
   const int g = lane >> 4;
   const int K = a.K;
   const int M = a.M;
-  const int nblk = blockIdx.x * 4 + wave;  // this wave's 16-row block
+  const int nblk = blockIdx.x * WV + wave;  // this wave's 16-row block
   const bool wave_active = nblk * 16 < a.N;
   const uint16_t* wlane = a.w + (static_cast<long long>(nblk) * (K >> 8) * 8 * 64 + lane) * 8;
   f32x4 acc[4];
@@ -338,17 +344,20 @@ __global__ __launch_bounds__(256) void dense_lds_kernel(WsArgs a) {
 
   const int k_first = kSplit ? static_cast<int>(blockIdx.y) * 256 : 0;
   const int k_end = kSplit ? k_first + 256 : K;
+  auto load_w = [&](uint4* dst, int kb) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      dst[j] = ld_stream(wlane + (static_cast<long long>(kb >> 8) * 8 + j) * 512);
+  };
+  uint4 bw[8];
+  if (PF && wave_active) load_w(bw, k_first);
   for (int kb = k_first; kb < k_end; kb += 256) {
-    uint4 bw[8];
-    if (wave_active) {
+    if (!PF && wave_active) load_w(bw, kb);
+    // stage the [64 x 256] token tile: flat 16-byte index f = i*kThreads + tid
+    uint4 av[kStage];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) bw[j] = ld_stream(wlane + (static_cast<long long>(kb >> 8) * 8 + j) * 512);
-    }
-    // stage the [64 x 256] token tile: flat 16-byte index f = i*256 + tid
-    uint4 av[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int f = i * 256 + threadIdx.x;
+    for (int i = 0; i < kStage; ++i) {
+      const int f = i * kThreads + threadIdx.x;
       const int row = f >> 5, c16 = f & 31;
       av[i] = row < M ? *reinterpret_cast<const uint4*>(a.x + static_cast<long long>(row) * a.ldx +
                                                          kb + 8 * c16)
@@ -356,12 +365,15 @@ __global__ __launch_bounds__(256) void dense_lds_kernel(WsArgs a) {
     }
     __syncthreads();  // previous block's fragment reads are done
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int f = i * 256 + threadIdx.x;
+    for (int i = 0; i < kStage; ++i) {
+      const int f = i * kThreads + threadIdx.x;
       const int row = f >> 5, c16 = f & 31;
       *reinterpret_cast<uint4*>(As + row * kLdsRow + 8 * c16) = av[i];
     }
     __syncthreads();
+    uint4 bn[8];
+    const bool more = PF && kb + 256 < k_end;
+    if (more && wave_active) load_w(bn, kb + 256);
     if (wave_active) {
 #pragma unroll
       for (int mb = 0; mb < 4; ++mb) {
@@ -373,6 +385,10 @@ __global__ __launch_bounds__(256) void dense_lds_kernel(WsArgs a) {
                                                             acc[mb], 0, 0, 0);
         }
       }
+    }
+    if (more) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) bw[j] = bn[j];
     }
   }
   if (!wave_active) return;
@@ -398,8 +414,15 @@ __global__ __launch_bounds__(256) void dense_lds_kernel(WsArgs a) {
 
 template <int EPI>
 static int32_t launch_dense_lds(const WsArgs& a, hipStream_t s) {
-  const dim3 grid((a.N + 63) / 64, EPI == kPartialF32 ? a.K / 256 : 1);
-  hipLaunchKernelGGL((dense_lds_kernel<EPI>), grid, dim3(256), 0, s, a);
+  if (EPI == kPartialF32) {
+    const dim3 grid((a.N + 63) / 64, a.K / 256);
+    hipLaunchKernelGGL((dense_lds_kernel<EPI>), grid, dim3(256), 0, s, a);
+    return launch_status();
+  }
+  // full K per workgroup: next-block weight prefetch (LM head 17.9 -> 16.2 us);
+  // 8 waves per workgroup measured no faster than 4
+  const dim3 grid((a.N + 63) / 64);
+  hipLaunchKernelGGL((dense_lds_kernel<EPI, 4, true>), grid, dim3(256), 0, s, a);
   return launch_status();
 }
 
@@ -497,15 +520,12 @@ extern "C" int32_t llmy_linear_bf16(const llmy_bf16* x, const llmy_bf16* w, void
   const bool packed = weight_layout == 1;
   if (epilogue == kPartialF32) {
     LLMY_REQUIRE(static_cast<long long>(K / 256) * M * N < (1ll << 31));
-#ifndef LLMY_PARTIAL_LDS_MIN_N
-#define LLMY_PARTIAL_LDS_MIN_N 0
-#endif
-    if (packed && N >= LLMY_PARTIAL_LDS_MIN_N) return launch_dense_lds<kPartialF32>(a, s);
-    const dim3 grid(N / 16, K / 256), block(64);
-    if (packed)
-      hipLaunchKernelGGL((wsgemm_kernel<kPartialF32, kDense, true, 4, 1, 8>), grid, block, 0, s, a);
-    else
-      hipLaunchKernelGGL((wsgemm_kernel<kPartialF32, kDense, false, 4, 1, 8>), grid, block, 0, s, a);
+    // packed weights: four waves share a staged activation slice (faster than
+    // the single-wave kernel below at every decode shape measured, N = 1024..4112)
+    if (packed) return launch_dense_lds<kPartialF32>(a, s);
+    // row-major weights: one single-wave workgroup per (16 rows, K block)
+    hipLaunchKernelGGL((wsgemm_kernel<kPartialF32, kDense, false, 4, 1, 8>),
+                       dim3(N / 16, K / 256), dim3(64), 0, s, a);
     return launch_status();
   }
   if (M >= kDenseMfmaMinRows && aligned(out, 16) && (aux == nullptr || aligned(aux, 16)) &&

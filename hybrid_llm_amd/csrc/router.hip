@@ -266,7 +266,8 @@ __global__ __launch_bounds__(1024) void moe_permute_kernel(
 // (one fma per element), and the completed row is written back to x.  Every
 // wave reads x[t] before the workgroup barrier; wave 0 writes it after it.
 constexpr int kMaxParts = 8;
-template <int NCH>
+// NPM: compile-time bound on nparts (0, 4 or 8) that sizes the slice registers.
+template <int NCH, int NPM>
 __global__ __launch_bounds__(256) void moe_route_norm_kernel(
     float* __restrict__ x, const float* __restrict__ parts, int nparts,
     const float* __restrict__ gate, const float* __restrict__ ffn_w,
@@ -287,10 +288,21 @@ __global__ __launch_bounds__(256) void moe_route_norm_kernel(
     fw[c] = *reinterpret_cast<const float4*>(ffn_w + d);
     rw[c] = *reinterpret_cast<const float4*>(router_w + d);
   }
-  if (nparts > 0) {
-    float4 pv[kMaxParts][NCH], gv[NCH];
+  // W_r rows are requested with the row and the partial slices (one round trip)
+  float4 wq[MAXE][NCH];
 #pragma unroll
-    for (int p = 0; p < kMaxParts; ++p) {
+  for (int j = 0; j < MAXE; ++j) {
+    const int e = min(wave + 4 * j, E - 1);  // clamped: rows past E are loaded but unused
+#pragma unroll
+    for (int c = 0; c < NCH; ++c)
+      wq[j][c] = *reinterpret_cast<const float4*>(w_router + static_cast<long long>(e) * D +
+                                                  4 * lane + 256 * c);
+  }
+  if (NPM > 0 && nparts > 0) {
+    constexpr int NPA = NPM > 0 ? NPM : 1;
+    float4 pv[NPA][NCH], gv[NCH];
+#pragma unroll
+    for (int p = 0; p < NPA; ++p) {
       if (p < nparts) {
 #pragma unroll
         for (int c = 0; c < NCH; ++c)
@@ -308,7 +320,7 @@ __global__ __launch_bounds__(256) void moe_route_norm_kernel(
     for (int c = 0; c < NCH; ++c) {
       float4 acc = pv[0][c];
 #pragma unroll
-      for (int p = 1; p < kMaxParts; ++p) {
+      for (int p = 1; p < NPA; ++p) {
         if (p < nparts) {
           acc.x += pv[p][c].x;
           acc.y += pv[p][c].y;
@@ -332,15 +344,6 @@ __global__ __launch_bounds__(256) void moe_route_norm_kernel(
   float4 xnew[NCH];
 #pragma unroll
   for (int c = 0; c < NCH; ++c) xnew[c] = v[c];
-  float4 wq[MAXE][NCH];
-#pragma unroll
-  for (int j = 0; j < MAXE; ++j) {
-    const int e = min(wave + 4 * j, E - 1);  // clamped: rows past E are loaded but unused
-#pragma unroll
-    for (int c = 0; c < NCH; ++c)
-      wq[j][c] = *reinterpret_cast<const float4*>(w_router + static_cast<long long>(e) * D +
-                                                  4 * lane + 256 * c);
-  }
 
   float ss = 0.f;
 #pragma unroll
@@ -461,15 +464,24 @@ extern "C" int32_t llmy_moe_route_decode(float* x, const float* parts, int32_t n
     LLMY_REQUIRE(aligned(x, 16) && aligned(ffn_w, 16) && aligned(router_w, 16) &&
                  aligned(w_router, 16) && aligned(h2, 8));
     LLMY_REQUIRE(nparts == 0 || (parts && aligned(parts, 16) && (!gate || aligned(gate, 16))));
-#define LLMY_ROUTE(NCH)                                                                       \
-  hipLaunchKernelGGL(moe_route_norm_kernel<NCH>, dim3(T), dim3(256), 0, s, x, parts, nparts,      \
-                     gate, ffn_w, router_w, w_router, h2, idx, gates, T, E, k, eps)
+#define LLMY_ROUTE_NP(NCH, NPM)                                                               \
+  hipLaunchKernelGGL((moe_route_norm_kernel<NCH, NPM>), dim3(T), dim3(256), 0, s, x, parts,        \
+                     nparts, gate, ffn_w, router_w, w_router, h2, idx, gates, T, E, k, eps)
+#define LLMY_ROUTE(NCH)                \
+  if (nparts == 0) {                   \
+    LLMY_ROUTE_NP(NCH, 0);             \
+  } else if (nparts <= 4) {            \
+    LLMY_ROUTE_NP(NCH, 4);             \
+  } else {                             \
+    LLMY_ROUTE_NP(NCH, 8);             \
+  }
     switch (D) {
       case 256: LLMY_ROUTE(1); break;
       case 512: LLMY_ROUTE(2); break;
       default: LLMY_ROUTE(4); break;
     }
 #undef LLMY_ROUTE
+#undef LLMY_ROUTE_NP
     const int32_t st = launch_status();
     if (st != 0) return st;
   }
