@@ -131,6 +131,32 @@ def attn_decode_bytes(cfg, B):
     return 2 * B * H * W * hd * 2 + 2 * B * H * hd * 2 + 4 * B * H * hd * 2
 
 
+def step_bytes(cfg, B: int) -> dict:
+    """Algorithmic HBM bytes of one decode step (every weight, cache and state
+    byte the step must move once), by component; experts count the expected
+    number of distinct experts hit by B*top_k routes drawn over E."""
+    E, k, D, H = cfg.n_experts, cfg.top_k, cfg.d_model, cfg.expert_hidden
+    apps = cfg.num_loops * cfg.n_layers
+    n_attn = cfg.num_loops * sum(1 for kd in cfg.layer_kinds if kd == "attn")
+    n_gdn = apps - n_attn
+    Ha, hd, W = cfg.attn_heads, cfg.attn_head_dim, cfg.window
+    Hg, dk, dv = cfg.gdn_heads, cfg.gdn_dk, cfg.gdn_dv
+    distinct = E * (1.0 - (1.0 - k / E) ** B)
+    parts = {
+        "experts": apps * distinct * 3 * H * D * 2,
+        "attn_projections": n_attn * 4 * D * Ha * hd * 2,
+        "gdn_projections": n_gdn * ((2 * Hg * dk + 2 * Hg * dv + Hg) * D + D * Hg * dv) * 2,
+        "kv_reads": n_attn * 2 * B * Ha * W * hd * 2,
+        "kv_writes": n_attn * 2 * B * Ha * hd * 2,
+        "gdn_state": n_gdn * 2 * B * Hg * dk * dv * 4,
+        "router": apps * E * D * 4,
+        "lm_head": cfg.vocab * D * 2,
+        "logits": 2 * B * cfg.vocab * 4,
+    }
+    parts["total"] = sum(parts.values())
+    return parts
+
+
 def time_attn_decode(cfg, B, iters, gen):
     import torch
     sets = attn_decode_sets(cfg, B, gen)
@@ -496,6 +522,14 @@ def main():
         print(f"[bench] engine_prefill: {r['ms']} ms, {r['tok_s']:.0f} tok/s, "
               f"{r['achieved']} TFLOP/s ({100 * r['frac']:.1f}%)", file=sys.stderr, flush=True)
 
+    sb = step_bytes(cfg, B)
+    step_gbs = sb["total"] / (ms * 1e-3) / 1e9
+    step_rf = {"bound": "hbm", "bytes_per_step": round(sb["total"]), "achieved": round(step_gbs, 1),
+               "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(step_gbs / HBM_PEAK_GBS, 4),
+               "ms_at_peak": round(sb["total"] / (HBM_PEAK_GBS * 1e9) * 1e3, 4)}
+    print(f"[bench] step {sb['total'] / 1e9:.2f} GB: {step_gbs:.0f} GB/s "
+          f"({100 * step_rf['frac']:.1f}% of peak)", file=sys.stderr, flush=True)
+
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(B)
@@ -511,7 +545,8 @@ def main():
                        "vocab": cfg.vocab, "sampling": {"temperature": SAMPLING[0],
                                                         "top_p": SAMPLING[1]},
                        "global_batch": B, "parallelism": "single GPU"},
-            "roofline": roofline, "kernels": kernels, "cpu_baseline": cpu}
+            "roofline": roofline, "step_roofline": step_rf, "kernels": kernels,
+            "cpu_baseline": cpu}
     print(json.dumps(line))
 
 
