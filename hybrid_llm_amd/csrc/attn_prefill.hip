@@ -93,9 +93,14 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const uint16_t* __res
   constexpr int CH = HD / 8;                     // 16-byte chunks per row
   constexpr int NCHK = (kBN * CH + 255) / 256;   // chunks per thread per tile
   uint4 kreg[NCHK], vreg[NCHK];
-  // K is fetched row-major (8 lanes per 128-byte row, 16-byte LDS stores);
-  // V is fetched key-fastest across lanes, so its transposed 2-byte LDS
-  // stores from one wave land at consecutive addresses.
+  // K is fetched row-major (8 lanes per 128-byte row, 16-byte LDS stores).
+  // V is fetched as key pairs: entry f = (pair f % 32, chunk f / 32) holds
+  // keys 2p and 2p+1 of one 8-dim chunk in vreg[2w], vreg[2w+1], so each of
+  // the chunk's 8 dims is stored to V^T as one dword (the two keys' values),
+  // lanes of a wave writing consecutive dwords of a row: no bank conflicts
+  // (2-byte stores put two lanes on one dword).
+  constexpr int NPW = (kBN / 2) * CH / 256;      // key-pair entries per thread
+  static_assert(2 * NPW == NCHK, "V pair staging covers the tile");
   auto fetch = [&](int tile) {
     const int kt = tile * kBN;
 #pragma unroll
@@ -106,10 +111,16 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const uint16_t* __res
       const bool ok = f < kBN * CH && kk < T;
       kreg[u] = ok ? *reinterpret_cast<const uint4*>(k + base + kk * rs + 8 * c)
                    : uint4{0u, 0u, 0u, 0u};
-      const int vkey = f % kBN, vc = f / kBN;
-      const bool vok = f < kBN * CH && kt + vkey < T;
-      vreg[u] = vok ? *reinterpret_cast<const uint4*>(v + base + (kt + vkey) * rs + 8 * vc)
-                    : uint4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int w = 0; w < NPW; ++w) {
+      const int f = threadIdx.x + 256 * w;
+      const int vk = kt + 2 * (f % (kBN / 2)), vc = f / (kBN / 2);
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+        vreg[2 * w + i] = vk + i < T
+                              ? *reinterpret_cast<const uint4*>(v + base + (vk + i) * rs + 8 * vc)
+                              : uint4{0u, 0u, 0u, 0u};
     }
   };
   fetch(t_lo);
@@ -123,11 +134,21 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const uint16_t* __res
       if (f < kBN * CH) {
         const int key = f / CH, c = f - (f / CH) * CH;
         *reinterpret_cast<uint4*>(Ks + key * (HD + kKPad) + 8 * c) = kreg[u];
-        const int vkey = f % kBN, vc = f / kBN;
-        const uint32_t w4[4] = {vreg[u].x, vreg[u].y, vreg[u].z, vreg[u].w};
+      }
+    }
 #pragma unroll
-        for (int e = 0; e < 8; ++e)
-          Vt[(8 * vc + e) * (kBN + kVPad) + vkey] = static_cast<uint16_t>(w4[e >> 1] >> (16 * (e & 1)));
+    for (int w = 0; w < NPW; ++w) {
+      const int f = threadIdx.x + 256 * w;
+      const int p2 = 2 * (f % (kBN / 2)), vc = f / (kBN / 2);
+      const uint32_t a4[4] = {vreg[2 * w].x, vreg[2 * w].y, vreg[2 * w].z, vreg[2 * w].w};
+      const uint32_t b4[4] = {vreg[2 * w + 1].x, vreg[2 * w + 1].y, vreg[2 * w + 1].z,
+                              vreg[2 * w + 1].w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        // dim 8vc + e: key 2p in the low half, key 2p+1 in the high half
+        const uint32_t lo = (a4[e >> 1] >> (16 * (e & 1))) & 0xffffu;
+        const uint32_t hi = (b4[e >> 1] >> (16 * (e & 1))) & 0xffffu;
+        *reinterpret_cast<uint32_t*>(Vt + (8 * vc + e) * (kBN + kVPad) + p2) = lo | (hi << 16);
       }
     }
     __syncthreads();
