@@ -175,7 +175,21 @@ __device__ void permute_block(Get get, int n, int E, int32_t* __restrict__ count
   const int per_wave = (nchunks + nw - 1) / nw;
   const int c0 = wave * per_wave;
   const int c1 = min(nchunks, c0 + per_wave);
-  for (int c = c0; c < c1; ++c) {
+  // The wave's ids are read once, all at once, and kept for pass 2 (up to
+  // kHeld chunks per wave; beyond that pass 2 reads them again).
+  constexpr int kHeld = 16;
+  int held[kHeld];
+#pragma unroll
+  for (int i = 0; i < kHeld; ++i) {
+    const int r = (c0 + i) * 64 + lane;
+    held[i] = (c0 + i < c1 && r < n) ? get(r) : -1;
+  }
+#pragma unroll
+  for (int i = 0; i < kHeld; ++i) {
+    const int e = held[i];
+    if (e >= 0 && e < E) atomicAdd(&cnt[wave * E + e], 1);
+  }
+  for (int c = c0 + kHeld; c < c1; ++c) {
     const int r = c * 64 + lane;
     if (r < n) {
       const int e = get(r);
@@ -212,11 +226,52 @@ __device__ void permute_block(Get get, int n, int E, int32_t* __restrict__ count
   __syncthreads();
 
   int32_t* running = cnt + wave * E;
+  if (E <= kWave) {
+    // Lane e keeps expert e's next position for this wave; per chunk, one
+    // ballot per expert ranks the routes of that expert (ascending r) and one
+    // shuffle hands each route its expert's base.  Same placement as below.
+    int next = lane < E ? running[lane] : 0;
+    for (int c = c0; c < c1; ++c) {
+      const int r = c * 64 + lane;
+      int e = -1;
+      if (r < n) {
+        if (c - c0 < kHeld) {
+#pragma unroll
+          for (int i = 0; i < kHeld; ++i)
+            if (c - c0 == i) e = held[i];
+        } else {
+          e = get(r);
+        }
+        if (e < 0 || e >= E) e = -1;
+      }
+      uint64_t mine = 0ull;
+      int add = 0;
+      for (int ee = 0; ee < E; ++ee) {
+        const uint64_t m = __ballot(e == ee);
+        if (e == ee) mine = m;
+        if (lane == ee) add = __popcll(m);
+      }
+      const int base = __shfl(next, e < 0 ? 0 : e, kWave);
+      if (e >= 0) {
+        const int pos = base + __popcll(mine & ((1ull << lane) - 1ull));
+        sorted_routes[pos] = r;
+        route_pos[r] = pos;
+      }
+      next += add;
+    }
+    return;
+  }
   for (int c = c0; c < c1; ++c) {
     const int r = c * 64 + lane;
     int e = -1;
     if (r < n) {
-      e = get(r);
+      if (c - c0 < kHeld) {
+#pragma unroll
+        for (int i = 0; i < kHeld; ++i)
+          if (c - c0 == i) e = held[i];
+      } else {
+        e = get(r);
+      }
       if (e < 0 || e >= E) e = -1;
     }
     uint64_t pending = __ballot(e >= 0);
