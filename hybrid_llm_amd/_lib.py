@@ -47,6 +47,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "llmy_moe_route_decode": (_I, [_P, _P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I,
                                    _I, _I, _I, _F, _P]),
     "llmy_gdn_conv_gate": (_I, [_P, _P, _P, _P, _I, _I, _I, _P]),
+    "llmy_moe_append_shared": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _P]),
     "llmy_kv_cache_fill_bf16": (_I, [_P, _P, _I64, _P, _P, _I, _I, _I, _I, _I, _P]),
     "llmy_gdn_prefill_prep_f32": (_I, [_P, _I64, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I,
                                        _P]),

@@ -51,7 +51,10 @@ _ATTN = {"wq": "q.weight", "wk": "k.weight", "wv": "v.weight", "wo": "o.weight"}
 _BLOCK = {"mix_norm": "mixer_norm.weight", "ffn_norm": "ffn_norm.weight",
           "router_norm": "moe.router.norm.weight", "w_router": "moe.router.logits.weight",
           "w_gate": "moe.experts.gate_proj.weight", "w_up": "moe.experts.up_proj.weight",
-          "w_down": "moe.experts.down_proj.weight"}
+          "w_down": "moe.experts.down_proj.weight",
+          "w_shared_gate": "moe.shared.gate_proj.weight",
+          "w_shared_up": "moe.shared.up_proj.weight",
+          "w_shared_down": "moe.shared.down_proj.weight"}
 
 
 def file_name(cfg: HybridConfig, key: str) -> str:
@@ -80,7 +83,7 @@ def config_text(cfg: HybridConfig) -> str:
         "gdn.qk_head_dim": cfg.gdn_dk, "gdn.value_head_dim": cfg.gdn_dv,
         "gdn.conv_kernel": cfg.conv_kernel,
         "moe.routed_experts": cfg.n_experts, "moe.routed_top_k": cfg.top_k,
-        "moe.expert_hidden": cfg.expert_hidden, "moe.shared_experts": 0,
+        "moe.expert_hidden": cfg.expert_hidden, "moe.shared_experts": cfg.shared_experts,
         "rms_norm_eps": repr(float(cfg.eps)),
     }
     return "".join(f"{k}={keys[k]}\n" for k in sorted(keys))
@@ -91,8 +94,6 @@ def config_from_text(text: str) -> HybridConfig:
     kinds = tuple(kv["recurrent_layout"].split(","))
     if int(kv.get("stem_blocks", 0)) or int(kv.get("tail_blocks", 0)):
         raise ValueError("stem/tail blocks are not part of this block stack")
-    if int(kv.get("moe.shared_experts", 0)):
-        raise ValueError("shared experts are not part of this block stack")
     if kv.get("gdn.qk_heads") != kv.get("gdn.value_heads"):
         raise ValueError("GDN q/k and value head counts must match")
     return HybridConfig(
@@ -102,7 +103,8 @@ def config_from_text(text: str) -> HybridConfig:
         gdn_dv=int(kv["gdn.value_head_dim"]), n_experts=int(kv["moe.routed_experts"]),
         top_k=int(kv["moe.routed_top_k"]), expert_hidden=int(kv["moe.expert_hidden"]),
         vocab=int(kv["vocab_size"]), num_loops=int(kv["num_loops"]),
-        conv_kernel=int(kv.get("gdn.conv_kernel", 4)), eps=float(kv.get("rms_norm_eps", 1e-6)))
+        conv_kernel=int(kv.get("gdn.conv_kernel", 4)), eps=float(kv.get("rms_norm_eps", 1e-6)),
+        shared_experts=int(kv.get("moe.shared_experts", 0)))
 
 
 def save_llmy(path: str | Path, cfg: HybridConfig, weights: dict[str, torch.Tensor]) -> None:

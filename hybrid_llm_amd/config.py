@@ -34,6 +34,10 @@ class HybridConfig:
     vocab: int
     num_loops: int
     conv_kernel: int = 4
+    # shared experts per MoE (model/layers/moe.py:110,185-199): dense SwiGLU
+    # experts of size expert_hidden on every token, summed and scaled by
+    # 1/sqrt(shared_experts), added to the routed output
+    shared_experts: int = 0
     eps: float = 1e-6
     init_std: float = 0.02
     decay_logit_init: float = 2.0  # model/layers/gated_deltanet.py:113
@@ -91,6 +95,11 @@ def weight_shapes(cfg: HybridConfig) -> list[tuple[str, tuple[int, ...], str]]:
                 (p + "w_router", (E, D), "normal"),
                 (p + "w_gate", (E, Hf, D), "normal"), (p + "w_up", (E, Hf, D), "normal"),
                 (p + "w_down", (E, D, Hf), "normal")]
+        if cfg.shared_experts > 0:
+            S = cfg.shared_experts
+            out += [(p + "w_shared_gate", (S, Hf, D), "normal"),
+                    (p + "w_shared_up", (S, Hf, D), "normal"),
+                    (p + "w_shared_down", (S, D, Hf), "normal")]
     out.append(("final_norm", (D,), "ones"))
     return out
 

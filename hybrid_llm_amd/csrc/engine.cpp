@@ -176,7 +176,10 @@ struct Config {
   int attn_heads = 0, attn_head_dim = 0, window = 0;
   int gdn_heads = 0, dk = 0, dv = 0, conv_kernel = 4;
   int experts = 0, top_k = 0, hidden = 0;
+  int shared = 0;  // shared experts, stacked after the routed ones (experts .. experts+shared-1)
   float eps = 1e-6f;
+  int routes() const { return top_k + shared; }      // routes per token, shared included
+  int all_experts() const { return experts + shared; }
   int nproj16() const {
     const int n = 2 * gdn_heads * dk + 2 * gdn_heads * dv + gdn_heads;
     return (n + 15) / 16 * 16;
@@ -199,8 +202,8 @@ Config config_from(const std::string& text) {
   c.d_model = cfg_int(kv, "d_model", 0, true);
   c.num_loops = cfg_int(kv, "num_loops", 1, true);
   if (cfg_int(kv, "stem_blocks", 0, false) || cfg_int(kv, "tail_blocks", 0, false) ||
-      cfg_int(kv, "moe.shared_experts", 0, false) || cfg_int(kv, "mhc.enabled", 0, false))
-    throw std::runtime_error("stem/tail blocks, shared experts and mHC are not part of this engine");
+      cfg_int(kv, "mhc.enabled", 0, false))
+    throw std::runtime_error("stem/tail blocks and mHC are not part of this engine");
   auto lay = kv.find("recurrent_layout");
   if (lay == kv.end()) throw std::runtime_error("config lacks recurrent_layout");
   size_t p = 0;
@@ -228,10 +231,12 @@ Config config_from(const std::string& text) {
   c.experts = cfg_int(kv, "moe.routed_experts", 0, true);
   c.top_k = cfg_int(kv, "moe.routed_top_k", 0, true);
   c.hidden = cfg_int(kv, "moe.expert_hidden", 0, true);
+  c.shared = cfg_int(kv, "moe.shared_experts", 0, false);
   auto eps = kv.find("rms_norm_eps");
   if (eps != kv.end()) c.eps = std::stof(eps->second);
   if (c.kinds.empty() || c.num_loops < 1 || c.vocab < 1 || c.d_model % 256 != 0 ||
-      c.hidden % 256 != 0 || c.top_k < 1 || c.top_k > c.experts || c.conv_kernel != 4)
+      c.hidden % 256 != 0 || c.top_k < 1 || c.top_k > c.experts || c.conv_kernel != 4 ||
+      c.shared < 0 || c.shared > 64)
     throw std::runtime_error("unsupported model shape");
   return c;
 }
@@ -415,16 +420,29 @@ std::unique_ptr<Model> load_model(const char* path) {
         throw std::runtime_error("unexpected conv shape");
       L.conv = m->upload(as_f32(cv));
     }
+    // Routed experts, then the S shared experts (moe.shared.*, stacked
+    // [S, H, D] / [S, D, H] by the converter) as experts E .. E+S-1.
+    const int S = c.shared, EX = E + S;
     const auto g = mat_bf16("moe.experts.gate_proj.weight", {E, Hf, D});
     const auto u = mat_bf16("moe.experts.up_proj.weight", {E, Hf, D});
-    std::vector<uint16_t> gu(static_cast<size_t>(E) * 2 * Hf * D);
-    const size_t blk = static_cast<size_t>(Hf) * D;
-    for (int e = 0; e < E; ++e) {  // [E, 2H, D]: gate rows, then up rows
-      std::memcpy(gu.data() + 2 * e * blk, g.data() + e * blk, blk * 2);
-      std::memcpy(gu.data() + (2 * e + 1) * blk, u.data() + e * blk, blk * 2);
+    auto dn = mat_bf16("moe.experts.down_proj.weight", {E, D, Hf});
+    std::vector<uint16_t> sg, su;
+    if (S > 0) {
+      sg = mat_bf16("moe.shared.gate_proj.weight", {S, Hf, D});
+      su = mat_bf16("moe.shared.up_proj.weight", {S, Hf, D});
+      const auto sd = mat_bf16("moe.shared.down_proj.weight", {S, D, Hf});
+      dn.insert(dn.end(), sd.begin(), sd.end());
     }
-    L.w_gate_up = m->upload_packed(gu, E, 2 * Hf, D);
-    L.w_down = m->upload_packed(mat_bf16("moe.experts.down_proj.weight", {E, D, Hf}), E, D, Hf);
+    std::vector<uint16_t> gu(static_cast<size_t>(EX) * 2 * Hf * D);
+    const size_t blk = static_cast<size_t>(Hf) * D;
+    for (int e = 0; e < EX; ++e) {  // [E+S, 2H, D]: gate rows, then up rows
+      const uint16_t* ge = e < E ? g.data() + e * blk : sg.data() + (e - E) * blk;
+      const uint16_t* ue = e < E ? u.data() + e * blk : su.data() + (e - E) * blk;
+      std::memcpy(gu.data() + 2 * e * blk, ge, blk * 2);
+      std::memcpy(gu.data() + (2 * e + 1) * blk, ue, blk * 2);
+    }
+    L.w_gate_up = m->upload_packed(gu, EX, 2 * Hf, D);
+    L.w_down = m->upload_packed(dn, EX, D, Hf);
     m->layers.push_back(L);
   }
   return m;
@@ -468,6 +486,8 @@ struct Buffers {  // activations for `rows` token rows
            *go = nullptr, *act = nullptr, *gq = nullptr, *gk = nullptr, *gv = nullptr;
   int32_t *tokens = nullptr, *idx = nullptr, *counts = nullptr, *offsets = nullptr,
           *sorted = nullptr, *route_pos = nullptr;
+  int32_t* idx_all = nullptr;  // shared experts: [rows, k + S] routes
+  float* gates_all = nullptr;
   void* ws = nullptr;
   int64_t ws_bytes = 0;
   DeviceArena arena;
@@ -496,7 +516,7 @@ struct State {
 };
 
 void alloc_buffers(const Config& c, int rows, int B, int T, Buffers& b) {
-  const int D = c.d_model, k = c.top_k, E = c.experts;
+  const int D = c.d_model, k = c.top_k, kx = c.routes(), EX = c.all_experts();
   b.rows = rows;
   b.x = b.arena.zeros<float>(static_cast<size_t>(rows) * D);
   b.h = b.arena.zeros<uint16_t>(static_cast<size_t>(rows) * D);
@@ -518,12 +538,16 @@ void alloc_buffers(const Config& c, int rows, int B, int T, Buffers& b) {
   b.tokens = b.arena.zeros<int32_t>(rows);
   b.idx = b.arena.zeros<int32_t>(static_cast<size_t>(rows) * k);
   b.gates = b.arena.zeros<float>(static_cast<size_t>(rows) * k);
-  b.counts = b.arena.zeros<int32_t>(E);
-  b.offsets = b.arena.zeros<int32_t>(E + 1);
-  b.sorted = b.arena.zeros<int32_t>(static_cast<size_t>(rows) * k);
-  b.route_pos = b.arena.zeros<int32_t>(static_cast<size_t>(rows) * k);
-  b.act = b.arena.zeros<uint16_t>(static_cast<size_t>(rows) * k * c.hidden);
-  b.y = b.arena.zeros<float>(static_cast<size_t>(rows) * k * D);
+  if (c.shared > 0) {  // the router's routes plus the always-on shared ones
+    b.idx_all = b.arena.zeros<int32_t>(static_cast<size_t>(rows) * kx);
+    b.gates_all = b.arena.zeros<float>(static_cast<size_t>(rows) * kx);
+  }
+  b.counts = b.arena.zeros<int32_t>(EX);
+  b.offsets = b.arena.zeros<int32_t>(EX + 1);
+  b.sorted = b.arena.zeros<int32_t>(static_cast<size_t>(rows) * kx);
+  b.route_pos = b.arena.zeros<int32_t>(static_cast<size_t>(rows) * kx);
+  b.act = b.arena.zeros<uint16_t>(static_cast<size_t>(rows) * kx * c.hidden);
+  b.y = b.arena.zeros<float>(static_cast<size_t>(rows) * kx * D);
   if (T == 1 && rows <= 64 && Hhd % 256 == 0 && HV % 256 == 0 &&
       std::max(Hhd, HV) / 256 <= 8) {
     b.max_parts = std::max(Hhd, HV) / 256;
@@ -603,7 +627,7 @@ void linear(const uint16_t* x, const uint16_t* w, void* out, const float* aux, i
 bool fused_route(const Config& c, int rows) {
   const int D = c.d_model;
   return static_cast<long long>(c.experts) * D <= 24576 && (D == 256 || D == 512 || D == 1024) &&
-         c.top_k <= 8 && rows * c.top_k <= 2048;
+         c.top_k <= 8 && rows * c.routes() <= 2048;
 }
 
 // MoE of layer l over `rows` rows (x updated, h = next pre-norm of x).
@@ -616,17 +640,32 @@ void moe_block(const Model& m, const Layer& L, Buffers& b, int rows, const float
                const float* gate = nullptr) {
   const Config& c = m.cfg;
   const int D = c.d_model, E = c.experts, k = c.top_k, Hf = c.hidden;
+  const int kx = c.routes(), EX = c.all_experts();
   const bool fused = !sequence && fused_route(c, rows);
   if (nparts > 0 && !fused) throw std::logic_error("partial products need the fused router");
+  // the router's [rows, k] routes, extended by the always-on shared experts
+  auto with_shared = [&](const int32_t*& ids, const float*& gts) {
+    ids = b.idx;
+    gts = b.gates;
+    if (c.shared == 0) return;
+    check_call(llmy_moe_append_shared(b.idx, b.gates, b.idx_all, b.gates_all, rows, k, E, c.shared,
+                                      st),
+               "llmy_moe_append_shared");
+    ids = b.idx_all;
+    gts = b.gates_all;
+  };
+  const int32_t* ids = nullptr;
+  const float* gts = nullptr;
   if (fused) {
     check_call(llmy_moe_route_decode(b.x, parts, nparts, gate, L.ffn_norm, L.router_norm,
                                      L.w_router, b.h, b.idx, b.gates, nullptr, nullptr, nullptr,
                                      nullptr, rows, D, E, k, c.eps, st),
                "llmy_moe_route_decode");
-    check_call(llmy_moe_experts_routed_bf16(b.h, b.idx, b.gates, L.w_gate_up, L.w_down, b.act, b.y,
-                                            rows, D, Hf, E, k, kPacked, st),
+    with_shared(ids, gts);
+    check_call(llmy_moe_experts_routed_bf16(b.h, ids, gts, L.w_gate_up, L.w_down, b.act, b.y,
+                                            rows, D, Hf, EX, kx, kPacked, st),
                "llmy_moe_experts_routed_bf16");
-    check_call(llmy_moe_combine_norm(b.y, nullptr, next_norm, b.x, b.h, rows, D, k, c.eps, st),
+    check_call(llmy_moe_combine_norm(b.y, nullptr, next_norm, b.x, b.h, rows, D, kx, c.eps, st),
                "llmy_moe_combine_norm");
     return;
   }
@@ -634,13 +673,14 @@ void moe_block(const Model& m, const Layer& L, Buffers& b, int rows, const float
   check_call(llmy_router_topk_bf16(b.h, L.router_norm, L.w_router, nullptr, b.idx, b.gates, rows,
                                    D, E, k, c.eps, st),
              "llmy_router_topk_bf16");
-  check_call(llmy_moe_permute(b.idx, rows * k, E, b.counts, b.offsets, b.sorted, b.route_pos,
+  with_shared(ids, gts);
+  check_call(llmy_moe_permute(ids, rows * kx, EX, b.counts, b.offsets, b.sorted, b.route_pos,
                               st),
              "llmy_moe_permute");
-  check_call(llmy_moe_experts_bf16(b.h, b.offsets, b.sorted, b.gates, L.w_gate_up, L.w_down, b.act,
-                                   b.y, rows, D, Hf, E, k, kPacked, st),
+  check_call(llmy_moe_experts_bf16(b.h, b.offsets, b.sorted, gts, L.w_gate_up, L.w_down, b.act,
+                                   b.y, rows, D, Hf, EX, kx, kPacked, st),
              "llmy_moe_experts_bf16");
-  check_call(llmy_moe_combine_norm(b.y, b.route_pos, next_norm, b.x, b.h, rows, D, k, c.eps,
+  check_call(llmy_moe_combine_norm(b.y, b.route_pos, next_norm, b.x, b.h, rows, D, kx, c.eps,
                                    st),
              "llmy_moe_combine_norm");
 }

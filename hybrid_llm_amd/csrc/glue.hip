@@ -3,6 +3,8 @@
 #include "common.hpp"
 #include "abi_util.hpp"
 
+#include <cmath>
+
 namespace llmy {
 
 // out[m] = bf16(x[m] * rsqrt(mean(x[m]^2) + eps) * w)  (model/layers/norms.py:13-16,
@@ -188,6 +190,23 @@ __global__ __launch_bounds__(256) void combine_norm_kernel(const float* __restri
   }
 }
 
+// Shared experts as always-on routes: ids/gates [T, k] of the router become
+// [T, k + S] with routes k .. k+S-1 of every token going to experts
+// E .. E+S-1 (the shared experts, stacked after the routed ones) with gate
+// g = 1/sqrt(S) (model/layers/moe.py:185-199).
+__global__ __launch_bounds__(256) void append_shared_kernel(const int32_t* __restrict__ idx,
+                                                            const float* __restrict__ gates,
+                                                            int32_t* __restrict__ idx_out,
+                                                            float* __restrict__ gates_out, int T,
+                                                            int k, int E, int S, float g) {
+  const int kx = k + S;
+  const long long i = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= static_cast<long long>(T) * kx) return;
+  const int t = static_cast<int>(i / kx), j = static_cast<int>(i - static_cast<long long>(t) * kx);
+  idx_out[i] = j < k ? idx[t * k + j] : E + (j - k);
+  gates_out[i] = j < k ? gates[t * k + j] : g;
+}
+
 }  // namespace llmy
 
 using namespace llmy;
@@ -262,5 +281,18 @@ extern "C" int32_t llmy_moe_combine_norm(const float* y, const int32_t* route_po
                      w, x, h, T, k, eps)
   LLMY_NCH_SWITCH(D, LLMY_COMBINE)
 #undef LLMY_COMBINE
+  return launch_status();
+}
+
+extern "C" int32_t llmy_moe_append_shared(const int32_t* idx, const float* gates, int32_t* idx_out,
+                                          float* gates_out, int32_t T, int32_t k, int32_t E,
+                                          int32_t S, void* stream) {
+  LLMY_REQUIRE(T >= 0 && k > 0 && E > 0 && S > 0 && static_cast<long long>(T) * (k + S) < (1ll << 31));
+  if (T == 0) return 0;
+  LLMY_REQUIRE(idx && gates && idx_out && gates_out);
+  const long long n = static_cast<long long>(T) * (k + S);
+  hipLaunchKernelGGL(append_shared_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256),
+                     0, as_stream(stream), idx, gates, idx_out, gates_out, T, k, E, S,
+                     1.0f / std::sqrt(static_cast<float>(S)));
   return launch_status();
 }

@@ -69,8 +69,16 @@ class HybridDecoder:
             self.w[p + "ffn_norm"] = up(p + "ffn_norm")
             self.w[p + "router_norm"] = up(p + "router_norm")
             self.w[p + "w_router"] = up(p + "w_router")
-            self.w[p + "w_gate_up"] = torch.cat([up(p + "w_gate"), up(p + "w_up")], 1).contiguous()
-            self.w[p + "w_down"] = up(p + "w_down")
+            gate_up = torch.cat([up(p + "w_gate"), up(p + "w_up")], 1)
+            down = up(p + "w_down")
+            if cfg.shared_experts > 0:
+                # shared experts stacked after the routed ones: experts E .. E+S-1,
+                # reached by the always-on routes of llmy_moe_append_shared
+                gate_up = torch.cat(
+                    [gate_up, torch.cat([up(p + "w_shared_gate"), up(p + "w_shared_up")], 1)], 0)
+                down = torch.cat([down, up(p + "w_shared_down")], 0)
+            self.w[p + "w_gate_up"] = gate_up.contiguous()
+            self.w[p + "w_down"] = down.contiguous()
 
         # Decode GEMM weights are re-laid once into the packed operand order
         # (llmy_pack_weights_bf16), so every weight byte streams as contiguous
@@ -103,6 +111,8 @@ class HybridDecoder:
         Ha, hd = cfg.attn_heads, cfg.attn_head_dim
         Hg, dk, dv = cfg.gdn_heads, cfg.gdn_dk, cfg.gdn_dv
         k, E, Hf = cfg.top_k, cfg.n_experts, cfg.expert_hidden
+        S = cfg.shared_experts
+        kx, Ex = k + S, E + S  # routes per token and experts, shared ones included
         nproj = self.w[f"L{cfg.gdn_layers()[0]}.wproj"].shape[0] if cfg.gdn_layers() else 16
         self.buf = {
             "tokens": torch.zeros(B, dtype=torch.int32, device=dev),
@@ -115,12 +125,12 @@ class HybridDecoder:
             "cg": torch.zeros(B, D, dtype=f32, device=dev),
             "idx": torch.zeros(B, k, dtype=torch.int32, device=dev),
             "gates": torch.zeros(B, k, dtype=f32, device=dev),
-            "counts": torch.zeros(E, dtype=torch.int32, device=dev),
-            "offsets": torch.zeros(E + 1, dtype=torch.int32, device=dev),
-            "sorted_routes": torch.zeros(B * k, dtype=torch.int32, device=dev),
-            "route_pos": torch.zeros(B * k, dtype=torch.int32, device=dev),
-            "act": torch.zeros(B * k, Hf, dtype=bf, device=dev),
-            "y": torch.zeros(B * k, D, dtype=f32, device=dev),
+            "counts": torch.zeros(Ex, dtype=torch.int32, device=dev),
+            "offsets": torch.zeros(Ex + 1, dtype=torch.int32, device=dev),
+            "sorted_routes": torch.zeros(B * kx, dtype=torch.int32, device=dev),
+            "route_pos": torch.zeros(B * kx, dtype=torch.int32, device=dev),
+            "act": torch.zeros(B * kx, Hf, dtype=bf, device=dev),
+            "y": torch.zeros(B * kx, D, dtype=f32, device=dev),
             "logits": torch.zeros(B, cfg.vocab, dtype=f32, device=dev),
             "next": torch.zeros(B, dtype=torch.int32, device=dev),
             "u": torch.zeros(B, dtype=f32, device=dev),
@@ -131,7 +141,10 @@ class HybridDecoder:
         # that derive their routes from the ids (no permutation pass) when the
         # sizes allow; else norm, router, permutation and sorted experts.
         self.fused_route = (E * D <= 24576 and D in (256, 512, 1024) and k <= 8
-                            and B * k <= 2048)
+                            and B * kx <= 2048)
+        if S > 0:
+            self.buf["idx_all"] = torch.zeros(B, kx, dtype=torch.int32, device=dev)
+            self.buf["gates_all"] = torch.zeros(B, kx, dtype=f32, device=dev)
         # Mixer output projections (attention o, GDN out) as per-K-block
         # partial products that the fused router folds into the residual: a
         # workgroup then reads a 256-wide slice of the activations instead of
@@ -223,22 +236,29 @@ class HybridDecoder:
                       w[p + "router_norm"].data_ptr(), w[p + "w_router"].data_ptr(), None,
                       b["idx"].data_ptr(), b["gates"].data_ptr(), self.B, cfg.d_model,
                       cfg.n_experts, cfg.top_k, cfg.eps, s)
-            _lib.call("llmy_moe_permute", b["idx"].data_ptr(), self.B * cfg.top_k,
-                      cfg.n_experts, b["counts"].data_ptr(), b["offsets"].data_ptr(),
+        S = cfg.shared_experts
+        idx, gates = b["idx"], b["gates"]
+        if S > 0:
+            idx, gates = ops.moe_append_shared(idx, gates, cfg.n_experts, S,
+                                               idx_out=b["idx_all"], gates_out=b["gates_all"])
+        kx = cfg.top_k + S
+        if not self.fused_route:
+            _lib.call("llmy_moe_permute", idx.data_ptr(), self.B * kx, cfg.n_experts + S,
+                      b["counts"].data_ptr(), b["offsets"].data_ptr(),
                       b["sorted_routes"].data_ptr(), b["route_pos"].data_ptr(), s)
         if self.route_log is not None:
             self.route_log[self._app].copy_(b["idx"])
             self._app = (self._app + 1) % self.route_log.shape[0]
         if self.fused_route:
-            ops.moe_experts_routed(b["h"], b["idx"], b["gates"], w[p + "w_gate_up"],
+            ops.moe_experts_routed(b["h"], idx, gates, w[p + "w_gate_up"],
                                    w[p + "w_down"], act=b["act"], y=b["y"],
                                    layout=ops.LAYOUT_PACKED)
             route_pos = None
         else:
-            ops.moe_experts(b["h"], b, b["gates"], w[p + "w_gate_up"], w[p + "w_down"],
+            ops.moe_experts(b["h"], b, gates, w[p + "w_gate_up"], w[p + "w_down"],
                             act=b["act"], y=b["y"], layout=ops.LAYOUT_PACKED)
             route_pos = b["route_pos"]
-        ops.moe_combine_norm(b["y"], route_pos, b["x"], b["h"], next_norm, cfg.top_k, cfg.eps)
+        ops.moe_combine_norm(b["y"], route_pos, b["x"], b["h"], next_norm, kx, cfg.eps)
 
     # ------------------------------------------------------------------ step
     def _step_body(self) -> None:
@@ -400,6 +420,9 @@ class HybridDecoder:
                   k, cfg.eps, s)
         if self.route_log_seq is not None:
             self.route_log_seq.append(idx.clone())
+        if cfg.shared_experts > 0:
+            idx, gates = ops.moe_append_shared(idx, gates, E, cfg.shared_experts)
+            E, k = E + cfg.shared_experts, k + cfg.shared_experts
         perm = ops.moe_permute(idx.view(-1), E)
         _, y = ops.moe_experts(h, perm, gates, w[p + "w_gate_up"], w[p + "w_down"],
                                layout=ops.LAYOUT_PACKED)

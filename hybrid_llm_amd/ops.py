@@ -387,6 +387,24 @@ def moe_route_decode(x, ffn_w, router_w, w_router, k, eps=1e-6, bufs=None,
     return b
 
 
+def moe_append_shared(idx, gates, n_experts: int, n_shared: int, idx_out=None, gates_out=None):
+    """[T, k] router output -> [T, k + S] with every token also routed to the
+    shared experts E .. E+S-1 at gate 1/sqrt(S)."""
+    T, k = idx.shape
+    _check(idx, torch.int32, "idx")
+    _check(gates, torch.float32, "gates", (T, k))
+    kx = k + n_shared
+    if idx_out is None:
+        idx_out = torch.empty(T, kx, dtype=torch.int32, device=idx.device)
+    if gates_out is None:
+        gates_out = torch.empty(T, kx, dtype=torch.float32, device=idx.device)
+    _check(idx_out, torch.int32, "idx_out", (T, kx))
+    _check(gates_out, torch.float32, "gates_out", (T, kx))
+    _lib.call("llmy_moe_append_shared", _ptr(idx), _ptr(gates), _ptr(idx_out), _ptr(gates_out),
+              T, k, n_experts, n_shared, _stream())
+    return idx_out, gates_out
+
+
 def embed_norm(tokens, table, w, x, h, eps=1e-6) -> None:
     V, D = table.shape
     _check(tokens, torch.int32, "tokens")

@@ -285,6 +285,16 @@ int32_t llmy_moe_combine_norm(const float* y, const int32_t* route_pos,
                               const float* w, float* x, llmy_bf16* h, int32_t T,
                               int32_t D, int32_t k, float eps, void* stream);
 
+/* Shared experts (model/layers/moe.py:185-199; llmy_cuda/src/model.cpp:
+ * 1205-1225 computes them in a loop after the routed ones) as always-on
+ * routes: idx_out/gates_out [T, k+S] = the router's [T, k], then experts
+ * E .. E+S-1 (the shared experts stacked after the routed ones in the expert
+ * weights) with gate 1/sqrt(S) for every token.  The expert and combine
+ * entries then run with k+S routes per token over E+S experts. */
+int32_t llmy_moe_append_shared(const int32_t* idx, const float* gates, int32_t* idx_out,
+                               float* gates_out, int32_t T, int32_t k, int32_t E,
+                               int32_t S, void* stream);
+
 /* Decode-time MoE front end (E*D <= 24576, D in {256,512,1024}, k <= 8):
  *   h2[t] = bf16(RMSNorm(x[t]) * ffn_w)   (the block's pre-MoE norm),
  *   logits = (RMSNorm(h2[t]) * router_w) . w_router^T in fp32, top-k (ties ->

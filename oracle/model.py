@@ -13,7 +13,8 @@ Mixers:
     step, o = (q^T S) * gate, out_proj, times sigmoid(causal depthwise conv)
     over the last ``conv_kernel`` normalised inputs.
 MoE: router (own RMSNorm + fp32 logits + top-k + softmax), routed SwiGLU
-experts (model/layers/moe.py:172-199, no shared experts in these configs).
+experts (model/layers/moe.py:172-199) plus the shared experts when the config has
+them (moe.py:185-199: their sum scaled by 1/sqrt(S), added to the routed output).
 
 ``act_bf16=True`` rounds activations to bf16 exactly where the HIP path
 stores them in bf16 (GEMM inputs, the KV cache, the MoE activation), so the
@@ -30,7 +31,7 @@ from hybrid_llm_amd.config import HybridConfig
 
 from .attention import banded_attention_decode
 from .gdn import gdn_step
-from .moe import moe_grouped
+from .moe import moe_grouped, shared_experts
 from .router import rmsnorm, router_logits, router_topk
 
 
@@ -112,8 +113,12 @@ class HybridOracle:
             idx = forced
             gates = torch.gather(logits, 1, torch.from_numpy(idx)).softmax(-1)
         self.routes.append(idx.copy())
-        return moe_grouped(h2, idx, gates, w[p + "w_gate"], w[p + "w_up"], w[p + "w_down"],
-                           act_round=self.rnd)
+        out = moe_grouped(h2, idx, gates, w[p + "w_gate"], w[p + "w_up"], w[p + "w_down"],
+                          act_round=self.rnd)
+        if cfg.shared_experts > 0:
+            out = out + shared_experts(h2, w[p + "w_shared_gate"], w[p + "w_shared_up"],
+                                       w[p + "w_shared_down"], act_round=self.rnd)
+        return out
 
     def _check_forced(self, logits: torch.Tensor, own: np.ndarray, forced: np.ndarray) -> None:
         """Record how far a forced routing is from the oracle's own choice: for

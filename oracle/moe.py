@@ -50,6 +50,24 @@ def moe_grouped(x: torch.Tensor, idx: np.ndarray, gates: torch.Tensor, w_gate: t
     return out
 
 
+def shared_experts(x: torch.Tensor, w_gate: torch.Tensor, w_up: torch.Tensor,
+                   w_down: torch.Tensor, act_round=None) -> torch.Tensor:
+    """Shared experts: every token through each of the S dense SwiGLU experts,
+    summed, then scaled by 1/sqrt(S); fp32.  Restates model/layers/moe.py:
+    185-199 (``sum(expert(flat) for expert in self.shared) / sqrt(S)``) and
+    llmy_cuda/src/model.cpp:1205-1225 (sum, then scale by 1/sqrt(S)).
+    w_gate, w_up [S,H,D], w_down [S,D,H]; ``act_round`` as in moe_grouped."""
+    S = w_gate.shape[0]
+    xf = x.float()
+    out = torch.zeros(x.shape[0], w_down.shape[1], dtype=torch.float32)
+    for s in range(S):
+        act = F.silu(xf @ w_gate[s].float().t()) * (xf @ w_up[s].float().t())
+        if act_round is not None:
+            act = act_round(act)
+        out += act @ w_down[s].float().t()
+    return out / np.float32(np.sqrt(S))
+
+
 def moe_per_token(x: torch.Tensor, idx: np.ndarray, gates: torch.Tensor, w_gate: torch.Tensor,
                   w_up: torch.Tensor, w_down: torch.Tensor) -> torch.Tensor:
     """Brute-force routed MoE, one token and one route at a time (tiny sizes).

@@ -102,6 +102,27 @@ def test_native_parser_agrees(lib, tiny_file):
         assert int(dt) == {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}[t.dtype]
 
 
+def test_shared_experts_roundtrip(lib, tmp_path):
+    """Shared experts travel as moe.shared.{gate,up,down}_proj.weight, stacked
+    [S, H, D] / [S, D, H] (model/layers/moe.py:110), with moe.shared_experts=S
+    in the config; both parsers read them back unchanged."""
+    from dataclasses import replace
+    cfg = replace(TINY, shared_experts=2)
+    w = init_weights(cfg, seed=4)
+    path = tmp_path / "shared.llmy"
+    save_llmy(path, cfg, w)
+    back_cfg, back = load_weights(path)
+    assert back_cfg == cfg and "moe.shared_experts=2\n" in config_text(cfg)
+    for key, t in w.items():
+        assert torch.equal(back[key], t), key
+    assert file_name(cfg, "L0.w_shared_down") == "recurrent_core.0.moe.shared.down_proj.weight"
+    assert back["L1.w_shared_gate"].shape == (2, 256, 256)
+    st, text = _describe(lib, path)
+    assert st == 0, lib.llmy_last_error()
+    names = [l.split()[0] for l in text.split("--\n")[1].strip().splitlines()]
+    assert sum(".moe.shared." in n for n in names) == 3 * cfg.n_layers
+
+
 @pytest.mark.parametrize("damage", ["magic", "version", "truncate_index", "payload", "name_len",
                                     "shape"])
 def test_native_parser_rejects_corrupt_files(lib, tiny_file, tmp_path, damage):

@@ -170,3 +170,37 @@ def test_errors_are_reported_not_thrown(lib, tmp_path):
     assert lib.llmy_load(str(bad).encode()) is None
     assert lib.llmy_last_status() != 0 and lib.llmy_last_error()
     assert lib.llmy_state_new_batch(None, 2) is None
+
+
+def test_shared_experts_match_python_engine(lib, tmp_path):
+    """A checkpoint with shared experts (moe.shared_experts=2): the native
+    engine stacks them after the routed experts exactly as the Python engine
+    does, so prefill and decode logits agree bit for bit, on the fused decode
+    router (B=2) and the sorted prefill path."""
+    from dataclasses import replace
+    from hybrid_llm_amd.engine import HybridDecoder
+    cfg = replace(C1, shared_experts=2)
+    w = init_weights(cfg, seed=1)
+    path = tmp_path / "shared.llmy"
+    save_llmy(path, cfg, w)
+    B, T = 2, 20
+    prompt = torch.randint(0, cfg.vocab, (B, T), generator=torch.Generator().manual_seed(9),
+                           dtype=torch.int32)
+    print("[engine-api] shared experts: prefill 20 + decode 3, B=2", flush=True)
+    m = lib.llmy_load(str(path).encode())
+    assert m, lib.llmy_last_error()
+    try:
+        s = lib.llmy_state_new_batch(m, B)
+        assert s
+        out = torch.zeros(B, cfg.vocab, device="cuda")
+        assert lib.llmy_prefill_batch(m, s, prompt.cuda().data_ptr(), T, out.data_ptr()) == 0
+        py = HybridDecoder(cfg, w, B)
+        assert torch.equal(out, py.prefill(prompt.cuda()))
+        nxt = torch.zeros(B, dtype=torch.int32)
+        for _ in range(3):
+            assert lib.llmy_greedy_tokens(s, nxt.data_ptr()) == 0
+            assert lib.llmy_decode_batch(m, s, nxt.data_ptr(), None, 0, out.data_ptr()) == 0
+            assert torch.equal(out, py.step(nxt.cuda()))
+        lib.llmy_state_free(s)
+    finally:
+        lib.llmy_free(m)

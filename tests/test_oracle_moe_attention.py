@@ -4,7 +4,7 @@ import torch
 import torch.nn.functional as F
 
 from oracle.attention import banded_attention, banded_attention_decode
-from oracle.moe import moe_grouped, moe_per_token, swiglu
+from oracle.moe import moe_grouped, moe_per_token, shared_experts, swiglu
 from oracle.router import router_topk
 
 
@@ -53,6 +53,34 @@ def test_moe_is_token_order_invariant():
 def _qkv(B, T, H, hd, seed):
     g = torch.Generator().manual_seed(seed)
     return [torch.randn(B, T, H, hd, generator=g) for _ in range(3)]
+
+
+def test_shared_expert_closed_forms():
+    """Shared experts (moe.py:185-199): one shared expert equal to routed
+    expert e, on tokens routed to e alone (k = 1, gate 1), doubles that
+    expert's output; S copies of one expert give sqrt(S) times it (sum of S,
+    scaled by 1/sqrt(S)); and the sum is taken before the scale, over the
+    experts in any order."""
+    g = torch.Generator().manual_seed(11)
+    T, D, H, E = 6, 32, 48, 3
+    x = torch.randn(T, D, generator=g)
+    wg, wu = torch.randn(E, H, D, generator=g) * 0.2, torch.randn(E, H, D, generator=g) * 0.2
+    wd = torch.randn(E, D, H, generator=g) * 0.2
+    e = 1
+    idx = np.full((T, 1), e)
+    routed = moe_grouped(x, idx, torch.ones(T, 1), wg, wu, wd)
+    one = shared_experts(x, wg[e:e + 1], wu[e:e + 1], wd[e:e + 1])
+    assert torch.allclose(routed + one, 2 * swiglu(x, wg[e], wu[e], wd[e]), atol=1e-5)
+    S = 4
+    rep = shared_experts(x, wg[e:e + 1].repeat(S, 1, 1), wu[e:e + 1].repeat(S, 1, 1),
+                         wd[e:e + 1].repeat(S, 1, 1))
+    assert torch.allclose(rep, np.sqrt(S) * swiglu(x, wg[e], wu[e], wd[e]), atol=1e-5)
+    perm = [2, 0, 1]
+    a = shared_experts(x, wg, wu, wd)
+    b = shared_experts(x, wg[perm], wu[perm], wd[perm])
+    brute = sum(swiglu(x, wg[s], wu[s], wd[s]).double() for s in range(E)) / np.sqrt(E)
+    assert torch.allclose(a, b, atol=1e-5)
+    assert torch.allclose(a.double(), brute, atol=1e-5)
 
 
 def test_banded_equals_causal_sdpa_when_window_covers_sequence():
