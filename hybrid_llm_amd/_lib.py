@@ -48,6 +48,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
                                    _I, _I, _I, _F, _P]),
     "llmy_gdn_conv_gate": (_I, [_P, _P, _P, _P, _I, _I, _I, _P]),
     "llmy_moe_append_shared": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _P]),
+    "llmy_router_context_latent_f32": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _F, _F,
+                                            _P]),
+    "llmy_router_context_window": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _P]),
+    "llmy_router_context_logits_f32": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _P]),
     "llmy_kv_cache_fill_bf16": (_I, [_P, _P, _I64, _P, _P, _I, _I, _I, _I, _I, _P]),
     "llmy_gdn_prefill_prep_f32": (_I, [_P, _I64, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I,
                                        _P]),

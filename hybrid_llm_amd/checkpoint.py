@@ -54,7 +54,13 @@ _BLOCK = {"mix_norm": "mixer_norm.weight", "ffn_norm": "ffn_norm.weight",
           "w_down": "moe.experts.down_proj.weight",
           "w_shared_gate": "moe.shared.gate_proj.weight",
           "w_shared_up": "moe.shared.up_proj.weight",
-          "w_shared_down": "moe.shared.down_proj.weight"}
+          "w_shared_down": "moe.shared.down_proj.weight",
+          "ctx_down": "moe.router.latent_memory.down.weight",
+          "ctx_ln_w": "moe.router.latent_memory.norm.weight",
+          "ctx_ln_b": "moe.router.latent_memory.norm.bias",
+          "ctx_local_out": "moe.router.local_context_out.weight",
+          "ctx_out": "moe.router.context_out.weight",
+          "ctx_gate": "moe.router.route_gate"}
 
 
 def file_name(cfg: HybridConfig, key: str) -> str:
@@ -84,6 +90,8 @@ def config_text(cfg: HybridConfig) -> str:
         "gdn.conv_kernel": cfg.conv_kernel,
         "moe.routed_experts": cfg.n_experts, "moe.routed_top_k": cfg.top_k,
         "moe.expert_hidden": cfg.expert_hidden, "moe.shared_experts": cfg.shared_experts,
+        "router.context_aware": int(cfg.context_router),
+        "router.local_context": cfg.router_context, "mla.latent_dim": cfg.latent_dim,
         "rms_norm_eps": repr(float(cfg.eps)),
     }
     return "".join(f"{k}={keys[k]}\n" for k in sorted(keys))
@@ -104,7 +112,20 @@ def config_from_text(text: str) -> HybridConfig:
         top_k=int(kv["moe.routed_top_k"]), expert_hidden=int(kv["moe.expert_hidden"]),
         vocab=int(kv["vocab_size"]), num_loops=int(kv["num_loops"]),
         conv_kernel=int(kv.get("gdn.conv_kernel", 4)), eps=float(kv.get("rms_norm_eps", 1e-6)),
-        shared_experts=int(kv.get("moe.shared_experts", 0)))
+        shared_experts=int(kv.get("moe.shared_experts", 0)),
+        # absent keys take the reference defaults (llmy_cuda/include/config.h:60-66)
+        context_router=_parse_bool(kv.get("router.context_aware", "1")),
+        router_context=int(kv.get("router.local_context", 128)),
+        latent_dim=int(kv.get("mla.latent_dim", 256)))
+
+
+def _parse_bool(s: str) -> bool:
+    """The reference's boolean config values (llmy_cuda/src/config.cpp:18-22)."""
+    if s in ("1", "true", "True", "yes"):
+        return True
+    if s in ("0", "false", "False", "no"):
+        return False
+    raise ValueError(f"expected bool, got: {s}")
 
 
 def save_llmy(path: str | Path, cfg: HybridConfig, weights: dict[str, torch.Tensor]) -> None:

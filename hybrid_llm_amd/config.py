@@ -38,6 +38,14 @@ class HybridConfig:
     # experts of size expert_hidden on every token, summed and scaled by
     # 1/sqrt(shared_experts), added to the routed output
     shared_experts: int = 0
+    # context-aware router, local-context branch (model/layers/context_router.py:
+    # 13-27,59-76; mla_memory.py:18-24): a latent channel of width latent_dim
+    # averaged over the last router_context tokens, added to the router input
+    # through context_out at weight sigmoid(route_gate)
+    context_router: bool = False
+    latent_dim: int = 256
+    router_context: int = 128
+    route_gate_init: float = -4.59512  # context_router.py:25
     eps: float = 1e-6
     init_std: float = 0.02
     decay_logit_init: float = 2.0  # model/layers/gated_deltanet.py:113
@@ -73,7 +81,7 @@ C5 = HybridConfig(d_model=1024, layer_kinds=alternating(12), attn_heads=16, attn
 
 
 def weight_shapes(cfg: HybridConfig) -> list[tuple[str, tuple[int, ...], str]]:
-    """(name, shape, kind) in generation order; kind in {normal, ones, zeros, decay}."""
+    """(name, shape, kind) in generation order; kind in {normal, ones, zeros, decay, gate}."""
     D, E, Hf = cfg.d_model, cfg.n_experts, cfg.expert_hidden
     out: list[tuple[str, tuple[int, ...], str]] = [("embed", (cfg.vocab, D), "normal")]
     for l, kind in enumerate(cfg.layer_kinds):
@@ -95,6 +103,11 @@ def weight_shapes(cfg: HybridConfig) -> list[tuple[str, tuple[int, ...], str]]:
                 (p + "w_router", (E, D), "normal"),
                 (p + "w_gate", (E, Hf, D), "normal"), (p + "w_up", (E, Hf, D), "normal"),
                 (p + "w_down", (E, D, Hf), "normal")]
+        if cfg.context_router:
+            L = cfg.latent_dim
+            out += [(p + "ctx_down", (L, D), "normal"), (p + "ctx_ln_w", (L,), "ones"),
+                    (p + "ctx_ln_b", (L,), "zeros"), (p + "ctx_local_out", (D, L), "normal"),
+                    (p + "ctx_out", (D, D), "normal"), (p + "ctx_gate", (), "gate")]
         if cfg.shared_experts > 0:
             S = cfg.shared_experts
             out += [(p + "w_shared_gate", (S, Hf, D), "normal"),
@@ -106,7 +119,7 @@ def weight_shapes(cfg: HybridConfig) -> list[tuple[str, tuple[int, ...], str]]:
 
 # Parameters kept in fp32 on the device; every other matrix is stored bf16.
 FP32_PARAMS = ("mix_norm", "ffn_norm", "router_norm", "final_norm", "w_router", "bb", "conv",
-               "decay")
+               "decay", "ctx_down", "ctx_ln_w", "ctx_ln_b", "ctx_gate")
 
 
 def is_fp32_param(name: str) -> bool:
@@ -117,7 +130,7 @@ def init_weights(cfg: HybridConfig, seed: int = 0, device: str | torch.device = 
                  ) -> dict[str, torch.Tensor]:
     """Random-init weights: every matrix N(0, init_std) drawn in ``weight_shapes``
     order from one generator seeded ``seed`` on ``device``; RMSNorm weights 1,
-    biases 0, GDN decay logits 2.0.  Matrices are rounded to bf16 except the
+    biases 0, GDN decay logits 2.0, the context router's gate route_gate_init.  Matrices are rounded to bf16 except the
     fp32 parameters listed in FP32_PARAMS (the router is fp32 end to end).
     CPU and GPU generators give different streams: parity tests generate on
     the CPU and copy to the GPU.
@@ -132,6 +145,8 @@ def init_weights(cfg: HybridConfig, seed: int = 0, device: str | torch.device = 
             t = torch.ones(shape, dtype=torch.float32, device=device)
         elif kind == "zeros":
             t = torch.zeros(shape, dtype=torch.float32, device=device)
+        elif kind == "gate":
+            t = torch.full(shape, cfg.route_gate_init, dtype=torch.float32, device=device)
         else:
             t = torch.full(shape, cfg.decay_logit_init, dtype=torch.float32, device=device)
         weights[name] = t if is_fp32_param(name) else t.to(torch.bfloat16)

@@ -69,6 +69,12 @@ class HybridDecoder:
             self.w[p + "ffn_norm"] = up(p + "ffn_norm")
             self.w[p + "router_norm"] = up(p + "router_norm")
             self.w[p + "w_router"] = up(p + "w_router")
+            if cfg.context_router:
+                # latent encoder and gate fp32; the two wide projections bf16,
+                # packed below like the other GEMM weights
+                for n in ("ctx_down", "ctx_ln_w", "ctx_ln_b", "ctx_gate", "ctx_local_out",
+                          "ctx_out"):
+                    self.w[p + n] = up(p + n)
             gate_up = torch.cat([up(p + "w_gate"), up(p + "w_up")], 1)
             down = up(p + "w_down")
             if cfg.shared_experts > 0:
@@ -85,7 +91,8 @@ class HybridDecoder:
         # 1 KiB wavefront loads; the embedding keeps a row-major copy for the
         # token lookup and a packed copy for the tied LM head.
         for name in list(self.w):
-            if name.split(".")[-1] in ("wqkv", "wo", "wproj", "wout", "w_gate_up", "w_down"):
+            if name.split(".")[-1] in ("wqkv", "wo", "wproj", "wout", "w_gate_up", "w_down",
+                                       "ctx_local_out", "ctx_out"):
                 self.w[name] = ops.pack_weights(self.w[name])
         self.w["lm_head"] = ops.pack_weights(self.w["embed"])
 
@@ -105,6 +112,10 @@ class HybridDecoder:
                                          dtype=torch.float32, device=dev),
                         "hist": torch.zeros(B, cfg.conv_kernel - 1, D, dtype=torch.bfloat16,
                                             device=dev)}
+                if cfg.context_router:
+                    # the router's last router_context latents per sequence (slot pos % W)
+                    self.state[(loop, l)]["ctx_ring"] = torch.zeros(
+                        B, cfg.router_context, cfg.latent_dim, dtype=torch.float32, device=dev)
 
         # ---- activations / scratch (allocated once)
         f32, bf = torch.float32, torch.bfloat16
@@ -145,6 +156,17 @@ class HybridDecoder:
         if S > 0:
             self.buf["idx_all"] = torch.zeros(B, kx, dtype=torch.int32, device=dev)
             self.buf["gates_all"] = torch.zeros(B, kx, dtype=f32, device=dev)
+        if cfg.context_router:
+            if cfg.latent_dim % 256 or cfg.latent_dim > 512 or D > 1024:
+                raise ValueError("the context router needs latent_dim in {256, 512}, d_model <= 1024")
+            Lc = cfg.latent_dim
+            self.ctx_buf = {"local": torch.zeros(B, D, dtype=f32, device=dev),
+                            "lat": torch.zeros(B, Lc, dtype=f32, device=dev),
+                            "ctx": torch.zeros(B, Lc, dtype=bf, device=dev),
+                            "ctx_d": torch.zeros(B, D, dtype=bf, device=dev),
+                            "ctx_c": torch.zeros(B, D, dtype=f32, device=dev),
+                            "logits": torch.zeros(B, E, dtype=f32, device=dev),
+                            "idx": self.buf["idx"], "gates": self.buf["gates"]}
         # Mixer output projections (attention o, GDN out) as per-K-block
         # partial products that the fused router folds into the residual: a
         # workgroup then reads a 256-wide slice of the activations instead of
@@ -216,7 +238,12 @@ class HybridDecoder:
             ops.linear(b["go"], w[p + "wout"], out=b["x"], epilogue=ops.EPI_RESID_GATED,
                        aux=b["cg"], layout=ops.LAYOUT_PACKED)
 
-    def _moe(self, l: int, next_norm: torch.Tensor | None) -> None:
+    def _ctx_weights(self, p: str) -> dict:
+        w = self.w
+        return {n: w[p + n] for n in ("router_norm", "ctx_down", "ctx_ln_w", "ctx_ln_b",
+                                       "ctx_local_out", "ctx_out", "ctx_gate", "w_router")}
+
+    def _moe(self, l: int, next_norm: torch.Tensor | None, st: dict) -> None:
         """Pre-MoE norm + router + permutation, experts, then the combine fused
         with the next block's pre-norm (``next_norm``) into ``h``."""
         cfg, w, b = self.cfg, self.w, self.buf
@@ -236,6 +263,11 @@ class HybridDecoder:
                       w[p + "router_norm"].data_ptr(), w[p + "w_router"].data_ptr(), None,
                       b["idx"].data_ptr(), b["gates"].data_ptr(), self.B, cfg.d_model,
                       cfg.n_experts, cfg.top_k, cfg.eps, s)
+        if cfg.context_router:
+            # the context-aware ids replace the plain router's (same buffers)
+            ops.router_context(b["h"], self._ctx_weights(p), st["ctx_ring"], cfg.top_k,
+                               pos=self.pos, eps=cfg.eps, layout=ops.LAYOUT_PACKED,
+                               bufs=self.ctx_buf)
         S = cfg.shared_experts
         idx, gates = b["idx"], b["gates"]
         if S > 0:
@@ -271,7 +303,7 @@ class HybridDecoder:
             else:
                 self._gdn(l, self.state[(loop, l)])
             nxt = w[f"L{apps[i + 1][1]}.mix_norm"] if i + 1 < len(apps) else w["final_norm"]
-            self._moe(l, nxt)
+            self._moe(l, nxt, self.state[(loop, l)])
         ops.linear(b["h"], w["lm_head"], out=b["logits"], epilogue=ops.EPI_STORE_F32,
                    layout=ops.LAYOUT_PACKED)
         self._sample()
@@ -362,7 +394,7 @@ class HybridDecoder:
             else:
                 self._gdn_seq(l, st, x, h, B, T)
             nxt = w[f"L{apps[i + 1][1]}.mix_norm"] if i + 1 < len(apps) else w["final_norm"]
-            self._moe_seq(l, x, h, nxt)
+            self._moe_seq(l, x, h, nxt, st, B)
         b = self.buf
         b["h"].copy_(h.view(B, T, D)[:, -1])
         ops.linear(b["h"], w["lm_head"], out=b["logits"], epilogue=ops.EPI_STORE_F32,
@@ -404,7 +436,7 @@ class HybridDecoder:
         ops.linear(go, w[p + "wout"], out=x, epilogue=ops.EPI_RESID_GATED,
                    aux=cg.view(R, cfg.d_model), layout=ops.LAYOUT_PACKED)
 
-    def _moe_seq(self, l: int, x, h, next_norm) -> None:
+    def _moe_seq(self, l: int, x, h, next_norm, st: dict, B: int) -> None:
         """Pre-MoE norm, router + top-k, stable permutation, grouped expert
         GEMMs, then the combine fused with the next block's pre-norm into h."""
         from . import _lib
@@ -415,9 +447,15 @@ class HybridDecoder:
         ops.rmsnorm(x, w[p + "ffn_norm"], cfg.eps, out=h)
         idx = torch.empty(R, k, dtype=torch.int32, device=dev)
         gates = torch.empty(R, k, dtype=torch.float32, device=dev)
-        _lib.call("llmy_router_topk_bf16", h.data_ptr(), w[p + "router_norm"].data_ptr(),
-                  w[p + "w_router"].data_ptr(), None, idx.data_ptr(), gates.data_ptr(), R, D, E,
-                  k, cfg.eps, s)
+        if cfg.context_router:
+            # rows are B sequences of T tokens from position 0 (fresh state)
+            idx, gates, _ = ops.router_context(h, self._ctx_weights(p), st["ctx_ring"], k,
+                                               eps=cfg.eps, layout=ops.LAYOUT_PACKED,
+                                               bufs={"idx": idx, "gates": gates})
+        else:
+            _lib.call("llmy_router_topk_bf16", h.data_ptr(), w[p + "router_norm"].data_ptr(),
+                      w[p + "w_router"].data_ptr(), None, idx.data_ptr(), gates.data_ptr(), R, D,
+                      E, k, cfg.eps, s)
         if self.route_log_seq is not None:
             self.route_log_seq.append(idx.clone())
         if cfg.shared_experts > 0:
@@ -434,4 +472,13 @@ class HybridDecoder:
         self.pos.copy_(pos.to(torch.int32))
         for key, st in self.state.items():
             for name, t in st.items():
+                if name == "ctx_ring":
+                    # the oracle keeps the last n latents in order: slot (pos - n + i) % W
+                    hist = state[key]["lat"]
+                    n, W = hist.shape[1], t.shape[1]
+                    for bi in range(t.shape[0]):
+                        p0 = int(pos[bi])
+                        for i in range(n):
+                            t[bi, (p0 - n + i) % W].copy_(hist[bi, i].to(t.dtype))
+                    continue
                 t.copy_(state[key][name].to(t.dtype))

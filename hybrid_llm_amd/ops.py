@@ -50,11 +50,15 @@ def router_topk(x: torch.Tensor, w_router: torch.Tensor, k: int,
     return (idx, gates, logits) if return_logits else (idx, gates)
 
 
-def router_topk_from_logits(logits: torch.Tensor, k: int):
+def router_topk_from_logits(logits: torch.Tensor, k: int, idx=None, gates=None):
     T, E = logits.shape
     _check(logits, torch.float32, "logits")
-    idx = torch.empty(T, k, dtype=torch.int32, device=logits.device)
-    gates = torch.empty(T, k, dtype=torch.float32, device=logits.device)
+    if idx is None:
+        idx = torch.empty(T, k, dtype=torch.int32, device=logits.device)
+    if gates is None:
+        gates = torch.empty(T, k, dtype=torch.float32, device=logits.device)
+    _check(idx, torch.int32, "idx", (T, k))
+    _check(gates, torch.float32, "gates", (T, k))
     _lib.call("llmy_router_topk_logits_f32", _ptr(logits), _ptr(idx), _ptr(gates), T, E, k,
               _stream())
     return idx, gates
@@ -403,6 +407,84 @@ def moe_append_shared(idx, gates, n_experts: int, n_shared: int, idx_out=None, g
     _lib.call("llmy_moe_append_shared", _ptr(idx), _ptr(gates), _ptr(idx_out), _ptr(gates_out),
               T, k, n_experts, n_shared, _stream())
     return idx_out, gates_out
+
+
+# ------------------------------------------------------------- context router
+def router_context_latent(h, norm_w, w_down, ln_w, ln_b, eps: float = 1e-6,
+                          ln_eps: float = 1e-5, local=None, lat=None):
+    """h [rows, D] bf16 -> (local = RMSNorm(h) * norm_w fp32 [rows, D],
+    lat = LayerNorm(local . w_down^T) fp32 [rows, L])."""
+    rows, D = h.shape
+    L = w_down.shape[0]
+    _check(h, torch.bfloat16, "h")
+    _check(w_down, torch.float32, "w_down", (L, D))
+    for n, t in (("norm_w", norm_w), ("ln_w", ln_w), ("ln_b", ln_b)):
+        _check(t, torch.float32, n)
+    if local is None:
+        local = torch.empty(rows, D, dtype=torch.float32, device=h.device)
+    if lat is None:
+        lat = torch.empty(rows, L, dtype=torch.float32, device=h.device)
+    _check(local, torch.float32, "local", (rows, D))
+    _check(lat, torch.float32, "lat", (rows, L))
+    _lib.call("llmy_router_context_latent_f32", _ptr(h), _ptr(norm_w), _ptr(w_down), _ptr(ln_w),
+              _ptr(ln_b), _ptr(local), _ptr(lat), rows, D, L, eps, ln_eps, _stream())
+    return local, lat
+
+
+def router_context_window(lat, ring, pos=None, ctx=None):
+    """lat [B*T, L] (B sequences of T tokens) -> ctx bf16 [B*T, L], the mean of
+    each token's window of W latents; ring [B, W, L] updated."""
+    B, W, L = ring.shape
+    rows = lat.shape[0]
+    if rows % max(B, 1):
+        raise ValueError("lat rows must be B * T")
+    T = rows // B if B else 0
+    _check(lat, torch.float32, "lat", (rows, L))
+    _check(ring, torch.float32, "ring", (B, W, L))
+    if pos is not None:
+        _check(pos, torch.int32, "pos", (B,))
+    if ctx is None:
+        ctx = torch.empty(rows, L, dtype=torch.bfloat16, device=lat.device)
+    _check(ctx, torch.bfloat16, "ctx", (rows, L))
+    _lib.call("llmy_router_context_window", _ptr(lat), _ptr(ring), _ptr(pos), _ptr(ctx), B, T, W,
+              L, _stream())
+    return ctx
+
+
+def router_context_logits(local, c, route_gate, w_router, logits=None):
+    """logits = (local + sigmoid(route_gate) * c) . w_router^T, fp32 [rows, E]."""
+    rows, D = local.shape
+    E = w_router.shape[0]
+    _check(local, torch.float32, "local")
+    _check(c, torch.float32, "c", (rows, D))
+    _check(route_gate, torch.float32, "route_gate")
+    _check(w_router, torch.float32, "w_router", (E, D))
+    if logits is None:
+        logits = torch.empty(rows, E, dtype=torch.float32, device=local.device)
+    _check(logits, torch.float32, "logits", (rows, E))
+    _lib.call("llmy_router_context_logits_f32", _ptr(local), _ptr(c), _ptr(route_gate),
+              _ptr(w_router), _ptr(logits), rows, D, E, _stream())
+    return logits
+
+
+def router_context(h, w: dict, ring, k: int, pos=None, eps: float = 1e-6,
+                   layout: int = LAYOUT_ROWMAJOR, bufs: dict | None = None):
+    """The whole context-aware routing of rows h [B*T, D] (bf16): returns
+    (idx [rows, k] int32, gates [rows, k] fp32, logits [rows, E] fp32).
+    ``w`` holds router_norm, ctx_down, ctx_ln_w, ctx_ln_b, ctx_local_out (bf16
+    [D, L]), ctx_out (bf16 [D, D]), ctx_gate and w_router (fp32); ``layout``
+    is that of the two bf16 matrices."""
+    b = bufs if bufs is not None else {}
+    local, lat = router_context_latent(h, w["router_norm"], w["ctx_down"], w["ctx_ln_w"],
+                                       w["ctx_ln_b"], eps, local=b.get("local"), lat=b.get("lat"))
+    ctx = router_context_window(lat, ring, pos, ctx=b.get("ctx"))
+    cl = linear(ctx, w["ctx_local_out"], out=b.get("ctx_d"), epilogue=EPI_STORE_BF16,
+                layout=layout)
+    c = linear(cl, w["ctx_out"], out=b.get("ctx_c"), epilogue=EPI_STORE_F32, layout=layout)
+    logits = router_context_logits(local, c, w["ctx_gate"], w["w_router"],
+                                   logits=b.get("logits"))
+    idx, gates = router_topk_from_logits(logits, k, idx=b.get("idx"), gates=b.get("gates"))
+    return idx, gates, logits
 
 
 def embed_norm(tokens, table, w, x, h, eps=1e-6) -> None:

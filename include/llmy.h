@@ -295,6 +295,36 @@ int32_t llmy_moe_append_shared(const int32_t* idx, const float* gates, int32_t* 
                                float* gates_out, int32_t T, int32_t k, int32_t E,
                                int32_t S, void* stream);
 
+/* Context-aware router, local-context branch (model/layers/context_router.py:
+ * 59-76 for a prompt, :94-137 for a decode token; replaces the router half of
+ * llmy_cuda/src/model.cpp:1110-1147 with its router_history_update_mean
+ * :1253-1290).  Five launches route rows of h (the block's bf16 pre-MoE norm):
+ *   1. llmy_router_context_latent_f32: local = RMSNorm(h) * norm_w (fp32
+ *      [rows, D]); lat = LayerNorm(local . w_down^T) * ln_w + ln_b (fp32
+ *      [rows, L], LayerNorm eps ln_eps = 1e-5, mla_memory.py:23-24).
+ *      D in {256,512,768,1024}; L % 64 == 0, L <= 512.
+ *   2. llmy_router_context_window: rows are B sequences of T tokens at
+ *      absolute positions pos[b] + t (pos NULL: 0).  ring [B, W, L] fp32 holds
+ *      each sequence's last W latents (slot p % W); ctx[b, t] = bf16(mean of
+ *      the min(p+1, W) latents up to position p) (mla_memory.py:29-48), and
+ *      the ring is updated.
+ *   3. llmy_linear_bf16(ctx, W_lco [D, L]) -> bf16 [rows, D] (epilogue 0).
+ *   4. llmy_linear_bf16(that, W_co [D, D]) -> c fp32 [rows, D] (epilogue 1).
+ *   5. llmy_router_context_logits_f32: logits = (local + sigmoid(route_gate[0])
+ *      * c) . w_router^T, fp32 [rows, E]; then llmy_router_topk_logits_f32. */
+int32_t llmy_router_context_latent_f32(const llmy_bf16* h, const float* norm_w,
+                                       const float* w_down, const float* ln_w,
+                                       const float* ln_b, float* local, float* lat,
+                                       int32_t rows, int32_t D, int32_t L, float eps,
+                                       float ln_eps, void* stream);
+int32_t llmy_router_context_window(const float* lat, float* ring, const int32_t* pos,
+                                   llmy_bf16* ctx, int32_t B, int32_t T, int32_t W,
+                                   int32_t L, void* stream);
+int32_t llmy_router_context_logits_f32(const float* local, const float* c,
+                                       const float* route_gate, const float* w_router,
+                                       float* logits, int32_t rows, int32_t D, int32_t E,
+                                       void* stream);
+
 /* Decode-time MoE front end (E*D <= 24576, D in {256,512,1024}, k <= 8):
  *   h2[t] = bf16(RMSNorm(x[t]) * ffn_w)   (the block's pre-MoE norm),
  *   logits = (RMSNorm(h2[t]) * router_w) . w_router^T in fp32, top-k (ties ->

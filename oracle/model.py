@@ -12,7 +12,9 @@ Mixers:
     gate = sigmoid(.), decay = sigmoid(decay_logit) per head, the delta-rule
     step, o = (q^T S) * gate, out_proj, times sigmoid(causal depthwise conv)
     over the last ``conv_kernel`` normalised inputs.
-MoE: router (own RMSNorm + fp32 logits + top-k + softmax), routed SwiGLU
+MoE: router (own RMSNorm + fp32 logits + top-k + softmax; with the context-aware
+router, the logits of context_router.py:94-137 from a per-(loop, layer)
+history of the last router_context latents), routed SwiGLU
 experts (model/layers/moe.py:172-199) plus the shared experts when the config has
 them (moe.py:185-199: their sum scaled by 1/sqrt(S), added to the routed output).
 
@@ -32,7 +34,8 @@ from hybrid_llm_amd.config import HybridConfig
 from .attention import banded_attention_decode
 from .gdn import gdn_step
 from .moe import moe_grouped, shared_experts
-from .router import rmsnorm, router_logits, router_topk
+from .router import (context_latents, context_route_logits, rmsnorm, router_logits,
+                     router_topk)
 
 
 def _bf16(t: torch.Tensor) -> torch.Tensor:
@@ -67,6 +70,8 @@ class HybridOracle:
                         "S": torch.zeros(batch, cfg.gdn_heads, cfg.gdn_dk, cfg.gdn_dv),
                         "hist": torch.zeros(batch, cfg.conv_kernel - 1, cfg.d_model),
                     }
+                # the router's latent history (context_router.py:108-121)
+                st[(loop, l)]["lat"] = torch.zeros(batch, 0, cfg.latent_dim)
         return st
 
     # ---- blocks ----------------------------------------------------------
@@ -102,10 +107,20 @@ class HybridOracle:
         st["hist"] = window[:, 1:].clone()
         return (o @ w[p + "wout"].t()) * torch.sigmoid(conv)
 
-    def _moe(self, l: int, h2: torch.Tensor) -> torch.Tensor:
+    def _moe(self, l: int, h2: torch.Tensor, s: dict | None = None) -> torch.Tensor:
         cfg, w = self.cfg, self.w
         p = f"L{l}."
-        logits = router_logits(h2, w[p + "w_router"], w[p + "router_norm"], cfg.eps)
+        if cfg.context_router:
+            # forward_step: mean of the last W latents (history + current)
+            local, lat = context_latents(h2, w[p + "router_norm"], w[p + "ctx_down"],
+                                         w[p + "ctx_ln_w"], w[p + "ctx_ln_b"], cfg.eps)
+            hist = torch.cat([s["lat"], lat[:, None]], dim=1)[:, -cfg.router_context:]
+            s["lat"] = hist
+            ctx = hist.double().mean(1).float()
+            logits = context_route_logits(local, ctx, w[p + "ctx_local_out"], w[p + "ctx_out"],
+                                          w[p + "ctx_gate"], w[p + "w_router"], self.rnd)
+        else:
+            logits = router_logits(h2, w[p + "w_router"], w[p + "router_norm"], cfg.eps)
         idx, gates = router_topk(logits, cfg.top_k)
         if self.forced_routes is not None:
             forced = np.asarray(self.forced_routes.pop(0)).reshape(idx.shape).astype(np.int64)
@@ -148,7 +163,7 @@ class HybridOracle:
                 else:
                     x = x + self._gdn(l, h, s)
                 h2 = rnd(rmsnorm(x, w[f"L{l}.ffn_norm"], cfg.eps))
-                x = x + self._moe(l, h2)
+                x = x + self._moe(l, h2, s)
         st["pos"] = pos + 1
         hf = rnd(rmsnorm(x, w["final_norm"], cfg.eps))
         return hf @ w["embed"].t()

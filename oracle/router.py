@@ -29,6 +29,59 @@ def router_logits(x: torch.Tensor, w_router: torch.Tensor, norm_w: torch.Tensor 
     return h @ w_router.float().t()
 
 
+def layernorm(x: torch.Tensor, w: torch.Tensor, b: torch.Tensor, eps: float = 1e-5
+              ) -> torch.Tensor:
+    """``(x - mean) / sqrt(var + eps) * w + b`` over the last dim, biased
+    variance, in fp64 then fp32.  Restates torch.nn.LayerNorm with its default
+    eps 1e-5, the latent norm of model/layers/mla_memory.py:21,23-24."""
+    xd = x.double()
+    mu = xd.mean(-1, keepdim=True)
+    var = (xd - mu).pow(2).mean(-1, keepdim=True)
+    return ((xd - mu) / torch.sqrt(var + eps) * w.double() + b.double()).float()
+
+
+def context_latents(h: torch.Tensor, norm_w: torch.Tensor, w_down: torch.Tensor,
+                    ln_w: torch.Tensor, ln_b: torch.Tensor, eps: float = 1e-6
+                    ) -> tuple[torch.Tensor, torch.Tensor]:
+    """(local, lat): local = RMSNorm(h) * norm_w (context_router.py:61), lat =
+    LayerNorm(local . W_down^T) (MLALatentMemory.encode, mla_memory.py:23-24)."""
+    local = rmsnorm(h, norm_w, eps)
+    lat = layernorm((local.double() @ w_down.double().t()).float(), ln_w, ln_b)
+    return local, lat
+
+
+def context_window_mean(lat: torch.Tensor, window: int) -> torch.Tensor:
+    """Causal box mean over the last ``window`` latents of a sequence starting at
+    position 0: ctx[t] = mean(lat[max(0, t-W+1) .. t]) along dim -2 (fp64 sums).
+
+    Restates MLALatentMemory.forward (mla_memory.py:29-48: a width-W box filter
+    with the first positions divided by t+1 instead of W) and, token by token,
+    ContextAwareRouter.forward_step (context_router.py:108-128: the mean of the
+    rolling history plus the current latent, its last W entries)."""
+    x = lat.double()
+    T = x.shape[-2]
+    c = torch.cumsum(x, dim=-2)
+    out = torch.empty_like(x)
+    for t in range(T):
+        lo = t - window
+        s = c[..., t, :] - (c[..., lo, :] if lo >= 0 else 0.0)
+        out[..., t, :] = s / min(t + 1, window)
+    return out.float()
+
+
+def context_route_logits(local: torch.Tensor, ctx: torch.Tensor, w_local_out: torch.Tensor,
+                         w_ctx_out: torch.Tensor, route_gate: torch.Tensor,
+                         w_router: torch.Tensor, act_round=lambda t: t) -> torch.Tensor:
+    """route = local + sigmoid(g) * context_out(local_context_out(ctx)); logits =
+    route . W_r^T (context_router.py:65-72 without the HCA global branch).
+    ``act_round`` rounds the inputs of the two projections where the HIP path
+    stores them in bf16."""
+    cl = act_round(act_round(ctx) @ w_local_out.float().t())
+    c = cl @ w_ctx_out.float().t()
+    route = local + torch.sigmoid(route_gate.float()) * c
+    return route @ w_router.float().t()
+
+
 def topk_lower_index(logits: torch.Tensor, k: int) -> tuple[np.ndarray, np.ndarray]:
     """Indices and values of the k largest entries per row.
 

@@ -59,7 +59,7 @@ def test_block_parity(kind):
     if kind == "moe":
         h2 = rmsnorm(x, ora.w["L0.ffn_norm"]).to(torch.bfloat16).float()
         ref = x + ora._moe(0, h2)
-        eng._moe(0, None)
+        eng._moe(0, None, eng.state[(0, 0)])
     else:
         l = 0 if kind == "attn" else 1
         h = rmsnorm(x, ora.w[f"L{l}.mix_norm"]).to(torch.bfloat16).float()
