@@ -177,6 +177,10 @@ struct Config {
   int gdn_heads = 0, dk = 0, dv = 0, conv_kernel = 4;
   int experts = 0, top_k = 0, hidden = 0;
   int shared = 0;  // shared experts, stacked after the routed ones (experts .. experts+shared-1)
+  // context-aware router (local latent window): router.context_aware,
+  // router.local_context, mla.latent_dim (llmy_cuda/include/config.h:60-66)
+  bool ctx = false;
+  int ctx_window = 128, latent = 256;
   float eps = 1e-6f;
   int routes() const { return top_k + shared; }      // routes per token, shared included
   int all_experts() const { return experts + shared; }
@@ -193,6 +197,16 @@ int cfg_int(const std::map<std::string, std::string>& kv, const char* key, int d
     return dflt;
   }
   return std::stoi(it->second);
+}
+
+// Boolean config values as the reference reads them (llmy_cuda/src/config.cpp:18-22).
+bool cfg_bool(const std::map<std::string, std::string>& kv, const char* key, bool dflt) {
+  auto it = kv.find(key);
+  if (it == kv.end()) return dflt;
+  const std::string& v = it->second;
+  if (v == "1" || v == "true" || v == "True" || v == "yes") return true;
+  if (v == "0" || v == "false" || v == "False" || v == "no") return false;
+  throw std::runtime_error(std::string("expected bool for ") + key);
 }
 
 Config config_from(const std::string& text) {
@@ -232,12 +246,18 @@ Config config_from(const std::string& text) {
   c.top_k = cfg_int(kv, "moe.routed_top_k", 0, true);
   c.hidden = cfg_int(kv, "moe.expert_hidden", 0, true);
   c.shared = cfg_int(kv, "moe.shared_experts", 0, false);
+  c.ctx = cfg_bool(kv, "router.context_aware", true);
+  c.ctx_window = cfg_int(kv, "router.local_context", 128, false);
+  c.latent = cfg_int(kv, "mla.latent_dim", 256, false);
   auto eps = kv.find("rms_norm_eps");
   if (eps != kv.end()) c.eps = std::stof(eps->second);
   if (c.kinds.empty() || c.num_loops < 1 || c.vocab < 1 || c.d_model % 256 != 0 ||
       c.hidden % 256 != 0 || c.top_k < 1 || c.top_k > c.experts || c.conv_kernel != 4 ||
       c.shared < 0 || c.shared > 64)
     throw std::runtime_error("unsupported model shape");
+  if (c.ctx && (c.latent % 256 != 0 || c.latent > 512 || c.d_model > 1024 || c.ctx_window < 1))
+    throw std::runtime_error("context-aware router needs mla.latent_dim in {256, 512}, "
+                             "d_model <= 1024, router.local_context >= 1");
   return c;
 }
 
@@ -308,6 +328,10 @@ struct Layer {
   float* decay = nullptr;
   uint16_t* w_gate_up = nullptr;  // packed per expert [E, 2H, D]
   uint16_t* w_down = nullptr;     // packed per expert [E, D, H]
+  // context-aware router: latent encoder [L, D] + LayerNorm, gate (fp32);
+  // local_context_out [D, L] and context_out [D, D] packed bf16
+  float *ctx_down = nullptr, *ctx_ln_w = nullptr, *ctx_ln_b = nullptr, *ctx_gate = nullptr;
+  uint16_t *ctx_local_out = nullptr, *ctx_out = nullptr;
 };
 
 struct Model {
@@ -392,6 +416,19 @@ std::unique_ptr<Model> load_model(const char* path) {
     L.ffn_norm = vec_f32("ffn_norm.weight", {D});
     L.router_norm = vec_f32("moe.router.norm.weight", {D});
     L.w_router = vec_f32("moe.router.logits.weight", {E, D});
+    if (c.ctx) {
+      const int Lc = c.latent;
+      L.ctx_down = vec_f32("moe.router.latent_memory.down.weight", {Lc, D});
+      L.ctx_ln_w = vec_f32("moe.router.latent_memory.norm.weight", {Lc});
+      L.ctx_ln_b = vec_f32("moe.router.latent_memory.norm.bias", {Lc});
+      const auto& gt = ck.get(p + "moe.router.route_gate");  // a 0-d parameter
+      if (!(gt.shape.empty() || gt.shape == std::vector<int64_t>{1}))
+        throw std::runtime_error("unexpected shape for moe.router.route_gate");
+      L.ctx_gate = m->upload(as_f32(gt));
+      L.ctx_local_out = m->upload_packed(mat_bf16("moe.router.local_context_out.weight", {D, Lc}),
+                                         1, D, Lc);
+      L.ctx_out = m->upload_packed(mat_bf16("moe.router.context_out.weight", {D, D}), 1, D, D);
+    }
     if (L.kind == kAttn) {
       const int W = c.attn_heads * c.attn_head_dim;
       if (W % 16 != 0 || W % 256 != 0 || (c.attn_head_dim != 64 && c.attn_head_dim != 128))
@@ -472,7 +509,8 @@ struct LayerState {
   uint16_t* v = nullptr;
   float* S = nullptr;       // [B, H, dk, dv]
   uint16_t* hist = nullptr; // [B, 3, D]
-  size_t k_bytes = 0, s_bytes = 0, hist_bytes = 0;
+  float* ring = nullptr;    // context router: [B, W, L], the last W latents (slot pos % W)
+  size_t k_bytes = 0, s_bytes = 0, hist_bytes = 0, ring_bytes = 0;
 };
 
 struct Buffers {  // activations for `rows` token rows
@@ -488,6 +526,10 @@ struct Buffers {  // activations for `rows` token rows
           *sorted = nullptr, *route_pos = nullptr;
   int32_t* idx_all = nullptr;  // shared experts: [rows, k + S] routes
   float* gates_all = nullptr;
+  // context router: local [rows, D], lat [rows, L], c [rows, D], logits [rows, E] fp32;
+  // window means [rows, L] and local_context_out [rows, D] bf16
+  float *c_local = nullptr, *c_lat = nullptr, *c_c = nullptr, *c_logits = nullptr;
+  uint16_t *c_ctx = nullptr, *c_d = nullptr;
   void* ws = nullptr;
   int64_t ws_bytes = 0;
   DeviceArena arena;
@@ -542,6 +584,14 @@ void alloc_buffers(const Config& c, int rows, int B, int T, Buffers& b) {
     b.idx_all = b.arena.zeros<int32_t>(static_cast<size_t>(rows) * kx);
     b.gates_all = b.arena.zeros<float>(static_cast<size_t>(rows) * kx);
   }
+  if (c.ctx) {
+    b.c_local = b.arena.zeros<float>(static_cast<size_t>(rows) * D);
+    b.c_lat = b.arena.zeros<float>(static_cast<size_t>(rows) * c.latent);
+    b.c_c = b.arena.zeros<float>(static_cast<size_t>(rows) * D);
+    b.c_logits = b.arena.zeros<float>(static_cast<size_t>(rows) * c.experts);
+    b.c_ctx = b.arena.zeros<uint16_t>(static_cast<size_t>(rows) * c.latent);
+    b.c_d = b.arena.zeros<uint16_t>(static_cast<size_t>(rows) * D);
+  }
   b.counts = b.arena.zeros<int32_t>(EX);
   b.offsets = b.arena.zeros<int32_t>(EX + 1);
   b.sorted = b.arena.zeros<int32_t>(static_cast<size_t>(rows) * kx);
@@ -584,6 +634,11 @@ std::unique_ptr<State> new_state(Model* m, int B) {
         L.hist = s->arena.zeros<uint16_t>(static_cast<size_t>(B) * 3 * D);
         L.hist_bytes = static_cast<size_t>(B) * 3 * D * 2;
       }
+      if (c.ctx) {
+        const size_t n = static_cast<size_t>(B) * c.ctx_window * c.latent;
+        L.ring = s->arena.zeros<float>(n);
+        L.ring_bytes = n * 4;
+      }
       s->layers.push_back(L);
     }
   }
@@ -606,6 +661,7 @@ void reset_state(State& s) {
       check_hip(hipMemsetAsync(L.S, 0, L.s_bytes, s.stream), "reset");
       check_hip(hipMemsetAsync(L.hist, 0, L.hist_bytes, s.stream), "reset");
     }
+    if (L.ring) check_hip(hipMemsetAsync(L.ring, 0, L.ring_bytes, s.stream), "reset");
   }
   check_hip(hipMemsetAsync(s.pos, 0, sizeof(int32_t) * s.B, s.stream), "reset");
   check_hip(hipStreamSynchronize(s.stream), "reset");
@@ -635,9 +691,14 @@ bool fused_route(const Config& c, int rows) {
 // allow; a prefill always takes router -> permutation -> grouped experts.
 // `parts` (decode, fused router only): nparts partial products of the mixer's
 // output projection that the router folds into x first (times `gate` if set).
+//
+// With the context-aware router the ids and gates of b.idx / b.gates come from
+// the context path (llmy_router_context_*): rows are nseq sequences of
+// rows / nseq tokens at positions pos[b] + t (pos NULL: a prompt from 0), and
+// `ring` is the layer's latent window state.
 void moe_block(const Model& m, const Layer& L, Buffers& b, int rows, const float* next_norm,
-               bool sequence, hipStream_t st, const float* parts = nullptr, int nparts = 0,
-               const float* gate = nullptr) {
+               bool sequence, hipStream_t st, float* ring, const int32_t* pos, int nseq,
+               const float* parts = nullptr, int nparts = 0, const float* gate = nullptr) {
   const Config& c = m.cfg;
   const int D = c.d_model, E = c.experts, k = c.top_k, Hf = c.hidden;
   const int kx = c.routes(), EX = c.all_experts();
@@ -654,6 +715,24 @@ void moe_block(const Model& m, const Layer& L, Buffers& b, int rows, const float
     ids = b.idx_all;
     gts = b.gates_all;
   };
+  auto context_route = [&] {
+    if (!c.ctx) return;
+    const int Lc = c.latent;
+    check_call(llmy_router_context_latent_f32(b.h, L.router_norm, L.ctx_down, L.ctx_ln_w,
+                                              L.ctx_ln_b, b.c_local, b.c_lat, rows, D, Lc, c.eps,
+                                              1e-5f, st),
+               "llmy_router_context_latent_f32");
+    check_call(llmy_router_context_window(b.c_lat, ring, pos, b.c_ctx, nseq, rows / nseq,
+                                          c.ctx_window, Lc, st),
+               "llmy_router_context_window");
+    linear(b.c_ctx, L.ctx_local_out, b.c_d, nullptr, rows, D, Lc, kStoreBf16, st);
+    linear(b.c_d, L.ctx_out, b.c_c, nullptr, rows, D, D, kStoreF32, st);
+    check_call(llmy_router_context_logits_f32(b.c_local, b.c_c, L.ctx_gate, L.w_router,
+                                              b.c_logits, rows, D, E, st),
+               "llmy_router_context_logits_f32");
+    check_call(llmy_router_topk_logits_f32(b.c_logits, b.idx, b.gates, rows, E, k, st),
+               "llmy_router_topk_logits_f32");
+  };
   const int32_t* ids = nullptr;
   const float* gts = nullptr;
   if (fused) {
@@ -661,6 +740,7 @@ void moe_block(const Model& m, const Layer& L, Buffers& b, int rows, const float
                                      L.w_router, b.h, b.idx, b.gates, nullptr, nullptr, nullptr,
                                      nullptr, rows, D, E, k, c.eps, st),
                "llmy_moe_route_decode");
+    context_route();
     with_shared(ids, gts);
     check_call(llmy_moe_experts_routed_bf16(b.h, ids, gts, L.w_gate_up, L.w_down, b.act, b.y,
                                             rows, D, Hf, EX, kx, kPacked, st),
@@ -673,6 +753,7 @@ void moe_block(const Model& m, const Layer& L, Buffers& b, int rows, const float
   check_call(llmy_router_topk_bf16(b.h, L.router_norm, L.w_router, nullptr, b.idx, b.gates, rows,
                                    D, E, k, c.eps, st),
              "llmy_router_topk_bf16");
+  context_route();
   with_shared(ids, gts);
   check_call(llmy_moe_permute(ids, rows * kx, EX, b.counts, b.offsets, b.sorted, b.route_pos,
                               st),
@@ -742,7 +823,8 @@ void decode_step(Model& m, State& s, int loops) {
           linear(b.go, L.wout, b.x, b.cg, B, D, HV, kResidGated, st_);
         }
       }
-      moe_block(m, L, b, B, next_norm_of(m, loop, l, loops), false, st_, b.parts, nparts, gate);
+      moe_block(m, L, b, B, next_norm_of(m, loop, l, loops), false, st_, st.ring, s.pos, B,
+                b.parts, nparts, gate);
     }
   }
   linear(b.h, m.lm_head, s.logits, nullptr, B, c.vocab, D, kStoreF32, st_);
@@ -807,7 +889,7 @@ void prefill(Model& m, State& s, const int32_t* tokens, int T, bool tokens_on_de
                    "llmy_gdn_conv_gate_prefill");
         linear(b.go, L.wout, b.x, b.cg, R, D, HV, kResidGated, st_);
       }
-      moe_block(m, L, b, R, next_norm_of(m, loop, l, loops), true, st_);
+      moe_block(m, L, b, R, next_norm_of(m, loop, l, loops), true, st_, st.ring, nullptr, B);
     }
   }
   // last position of each sequence -> the decode buffer, then the LM head

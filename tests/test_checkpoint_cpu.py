@@ -123,6 +123,39 @@ def test_shared_experts_roundtrip(lib, tmp_path):
     assert sum(".moe.shared." in n for n in names) == 3 * cfg.n_layers
 
 
+def test_context_router_roundtrip(lib, tmp_path):
+    """Context-aware router weights under the reference's names
+    (llmy_cuda/src/model.cpp:89-116), the route gate as a 0-d tensor, and the
+    three config keys; an absent router.context_aware reads as true, the
+    reference default (llmy_cuda/include/config.h:63)."""
+    from dataclasses import replace
+    cfg = replace(TINY, context_router=True, router_context=32)
+    w = init_weights(cfg, seed=5)
+    assert w["L0.ctx_gate"].shape == () and float(w["L0.ctx_gate"]) == pytest.approx(-4.59512)
+    path = tmp_path / "ctx.llmy"
+    save_llmy(path, cfg, w)
+    back_cfg, back = load_weights(path)
+    assert back_cfg == cfg
+    for key, t in w.items():
+        assert torch.equal(back[key], t), key
+    text = config_text(cfg)
+    assert "router.context_aware=1\n" in text and "router.local_context=32\n" in text
+    assert "mla.latent_dim=256\n" in text
+    assert file_name(cfg, "L1.ctx_gate") == "recurrent_core.1.moe.router.route_gate"
+    assert file_name(cfg, "L0.ctx_down") == "recurrent_core.0.moe.router.latent_memory.down.weight"
+    st, desc = _describe(lib, path)
+    assert st == 0, lib.llmy_last_error()
+    gate_lines = [l for l in desc.split("--\n")[1].splitlines() if l.endswith("route_gate 0 0 0 0 0 4")
+                  or ".route_gate " in l]
+    assert len(gate_lines) == cfg.n_layers and all(l.split()[2] == "0" for l in gate_lines)
+    plain = "".join(l + "\n" for l in config_text(TINY).splitlines()
+                    if not l.startswith("router.context_aware"))
+    assert config_from_text(plain).context_router
+    assert not config_from_text(config_text(TINY)).context_router
+    with pytest.raises(ValueError):
+        config_from_text(config_text(TINY).replace("router.context_aware=0", "router.context_aware=2"))
+
+
 @pytest.mark.parametrize("damage", ["magic", "version", "truncate_index", "payload", "name_len",
                                     "shape"])
 def test_native_parser_rejects_corrupt_files(lib, tiny_file, tmp_path, damage):

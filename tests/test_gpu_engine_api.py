@@ -204,3 +204,36 @@ def test_shared_experts_match_python_engine(lib, tmp_path):
         lib.llmy_state_free(s)
     finally:
         lib.llmy_free(m)
+
+
+def test_context_router_matches_python_engine(lib, tmp_path):
+    """router.context_aware=1 (local latent window of 8 tokens, latent 256):
+    the native engine's prefill and decode logits equal the Python engine's
+    bit for bit; the prompt is longer than the window, so the ring wraps."""
+    from dataclasses import replace
+    from hybrid_llm_amd.engine import HybridDecoder
+    cfg = replace(C1, context_router=True, router_context=8, route_gate_init=0.0)
+    w = init_weights(cfg, seed=2)
+    path = tmp_path / "ctx.llmy"
+    save_llmy(path, cfg, w)
+    B, T = 2, 20
+    prompt = torch.randint(0, cfg.vocab, (B, T), generator=torch.Generator().manual_seed(10),
+                           dtype=torch.int32)
+    print("[engine-api] context router: prefill 20 + decode 3, B=2", flush=True)
+    m = lib.llmy_load(str(path).encode())
+    assert m, lib.llmy_last_error()
+    try:
+        s = lib.llmy_state_new_batch(m, B)
+        assert s
+        out = torch.zeros(B, cfg.vocab, device="cuda")
+        assert lib.llmy_prefill_batch(m, s, prompt.cuda().data_ptr(), T, out.data_ptr()) == 0
+        py = HybridDecoder(cfg, w, B)
+        assert torch.equal(out, py.prefill(prompt.cuda()))
+        nxt = torch.zeros(B, dtype=torch.int32)
+        for _ in range(3):
+            assert lib.llmy_greedy_tokens(s, nxt.data_ptr()) == 0
+            assert lib.llmy_decode_batch(m, s, nxt.data_ptr(), None, 0, out.data_ptr()) == 0
+            assert torch.equal(out, py.step(nxt.cuda()))
+        lib.llmy_state_free(s)
+    finally:
+        lib.llmy_free(m)
