@@ -72,16 +72,19 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(
     const float* __restrict__ g, uint16_t* __restrict__ Wg, float* __restrict__ U0g,
     uint16_t* __restrict__ Ag, float* __restrict__ cumg, int T, int H, int NC) {
   constexpr int PK = DK + 8, PG = kC + 1, PT = kC + 8;
-  __shared__ __align__(16) uint16_t Ks[kC * PK];
-  __shared__ __align__(16) uint16_t Qs[kC * PK];
-  __shared__ __align__(16) uint16_t KsT[DK * PT];  // K^T [DK][64]: B operand over t
-  __shared__ __align__(16) uint16_t VsT[DV * PT];  // V^T [DV][64]
+  // LDS by lifetime, so that two workgroups fit on a CU: region R0 holds K
+  // and Q rows (products), then the per-wave block products of the inverse,
+  // then K^T and V^T (the B operands of W and U0, staged after the inverse).
+  constexpr int R0_KQ = 2 * kC * PK * 2, R0_T = (DK + DV) * PT * 2, R0_P = kC * 17 * 4;
+  constexpr int R0 = (R0_KQ > R0_T ? (R0_KQ > R0_P ? R0_KQ : R0_P) : (R0_T > R0_P ? R0_T : R0_P));
+  __shared__ __align__(16) unsigned char r0buf[R0];
+  uint16_t* const Ks = reinterpret_cast<uint16_t*>(r0buf);
+  uint16_t* const Qs = Ks + kC * PK;
+  float* const Pm = reinterpret_cast<float*>(r0buf);  // per-wave 16 x 16 block products
+  uint16_t* const KsT = reinterpret_cast<uint16_t*>(r0buf);  // K^T [DK][64]: B operand over t
+  uint16_t* const VsT = KsT + DK * PT;                      // V^T [DV][64]
   __shared__ float Gm[kC * PG];   // K K^T, then L
   __shared__ float Ti[kC * PG];   // (I + L)^{-1}
-  __shared__ float Pm[kC * 17];   // per-wave 16 x 16 block products
-  // Ti diag(beta Gamma_prev) and Ti diag(beta) as (hi, lo) bf16 pairs: the A
-  // operands of W and U0, split once
-  __shared__ __align__(16) uint16_t TWh[kC * PT], TWl[kC * PT], TUh[kC * PT], TUl[kC * PT];
   __shared__ float cum[kC], prv[kC], bet[kC], wsc[kC];  // wsc = beta * Gamma_prev
 
   const int cid = blockIdx.x;
@@ -106,26 +109,6 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(
     }
     *reinterpret_cast<uint4*>(Ks + t * PK + 8 * cc) = kv;
     *reinterpret_cast<uint4*>(Qs + t * PK + 8 * cc) = qv;
-  }
-  // transposed copies: token fastest across lanes, so the 2-byte LDS stores of
-  // a wave land in consecutive addresses
-  for (int f = threadIdx.x; f < kC * (DK / 8); f += 256) {
-    const int t = f % kC, cc = f / kC;
-    uint4 kv = uint4{0u, 0u, 0u, 0u};
-    if (t < Tc) kv = *reinterpret_cast<const uint4*>(k + kbase + t * rk + 8 * cc);
-    const uint32_t w[4] = {kv.x, kv.y, kv.z, kv.w};
-#pragma unroll
-    for (int jj = 0; jj < 8; ++jj)
-      KsT[(8 * cc + jj) * PT + t] = static_cast<uint16_t>(w[jj >> 1] >> (16 * (jj & 1)));
-  }
-  for (int f = threadIdx.x; f < kC * (DV / 8); f += 256) {
-    const int t = f % kC, cc = f / kC;
-    uint4 vv = uint4{0u, 0u, 0u, 0u};
-    if (t < Tc) vv = *reinterpret_cast<const uint4*>(v + vbase + t * rv + 8 * cc);
-    const uint32_t w[4] = {vv.x, vv.y, vv.z, vv.w};
-#pragma unroll
-    for (int jj = 0; jj < 8; ++jj)
-      VsT[(8 * cc + jj) * PT + t] = static_cast<uint16_t>(w[jj >> 1] >> (16 * (jj & 1)));
   }
   if (wave == 0) {
     // inclusive prefix sum of log g over the chunk (padded tokens: g = 1, beta = 0)
@@ -245,16 +228,26 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(
     }
   }
 
-  // ---- split the A operands once: TW = Ti diag(beta Gamma_prev), TU = Ti diag(beta)
-  for (int e = threadIdx.x; e < kC * kC; e += 256) {
-    const int t = e >> 6, i = e & 63;
-    const float tv = Ti[t * PG + i];
-    const float w = tv * wsc[i], u = tv * bet[i];
-    const uint16_t wh = f2bf(w), uh = f2bf(u);
-    TWh[t * PT + i] = wh;
-    TWl[t * PT + i] = f2bf(w - bf2f(wh));
-    TUh[t * PT + i] = uh;
-    TUl[t * PT + i] = f2bf(u - bf2f(uh));
+  // ---- K^T and V^T into R0 (the block products above are done): token
+  // fastest across lanes, so the 2-byte LDS stores of a wave land in
+  // consecutive addresses
+  for (int f = threadIdx.x; f < kC * (DK / 8); f += 256) {
+    const int t = f % kC, cc = f / kC;
+    uint4 kv = uint4{0u, 0u, 0u, 0u};
+    if (t < Tc) kv = *reinterpret_cast<const uint4*>(k + kbase + t * rk + 8 * cc);
+    const uint32_t w[4] = {kv.x, kv.y, kv.z, kv.w};
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj)
+      KsT[(8 * cc + jj) * PT + t] = static_cast<uint16_t>(w[jj >> 1] >> (16 * (jj & 1)));
+  }
+  for (int f = threadIdx.x; f < kC * (DV / 8); f += 256) {
+    const int t = f % kC, cc = f / kC;
+    uint4 vv = uint4{0u, 0u, 0u, 0u};
+    if (t < Tc) vv = *reinterpret_cast<const uint4*>(v + vbase + t * rv + 8 * cc);
+    const uint32_t w[4] = {vv.x, vv.y, vv.z, vv.w};
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj)
+      VsT[(8 * cc + jj) * PT + t] = static_cast<uint16_t>(w[jj >> 1] >> (16 * (jj & 1)));
   }
   __syncthreads();
   // ---- W = TW K  [64 x DK] (stored as (hi, lo) bf16 planes),  U0 = TU V  [64 x DV] (fp32)
@@ -268,9 +261,15 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(
       f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int s = 0; s < kC / 32; ++s) {
-        const int ao = (16 * tm + r16) * PT + 32 * s + 8 * g4;
-        const uint4 ahi = *reinterpret_cast<const uint4*>((isW ? TWh : TUh) + ao);
-        const uint4 alo = *reinterpret_cast<const uint4*>((isW ? TWl : TUl) + ao);
+        // A operand: Ti diag(beta Gamma_prev) (W) or Ti diag(beta) (U0), split
+        // into (hi, lo) bf16 in registers
+        const int col = 32 * s + 8 * g4;
+        const float* sc = isW ? wsc : bet;
+        float av[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) av[j] = Ti[(16 * tm + r16) * PG + col + j] * sc[col + j];
+        uint4 ahi, alo;
+        split8(av, ahi, alo);
         const uint4 bb = *reinterpret_cast<const uint4*>(
             (isW ? KsT : VsT) + (16 * tn + r16) * PT + 32 * s + 8 * g4);
         acc = mfma16(ahi, bb, acc);
