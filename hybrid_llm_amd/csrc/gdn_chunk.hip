@@ -58,6 +58,10 @@ __device__ __forceinline__ uint4 gather8_bf16(const uint16_t* p, int stride) {
                static_cast<uint32_t>(p[6 * stride]) | (static_cast<uint32_t>(p[7 * stride]) << 16)};
 }
 
+__device__ __forceinline__ uint32_t pack_bf2u(uint16_t a, uint16_t b) {
+  return static_cast<uint32_t>(a) | (static_cast<uint32_t>(b) << 16);
+}
+
 __device__ __forceinline__ f32x4 mfma16(const uint4& a, const uint4& b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a), as_bf16x8(b), c, 0, 0, 0);
 }
@@ -141,16 +145,27 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(
       const uint4 qa = *reinterpret_cast<const uint4*>(Qs + (16 * wave + r16) * PK + 32 * s + 8 * g4);
       const uint4 kb = *reinterpret_cast<const uint4*>(Ks + (16 * tj + r16) * PK + 32 * s + 8 * g4);
       a1 = mfma16(ka, kb, a1);
-      a2 = mfma16(qa, kb, a2);
+      a2 = mfma16(kb, qa, a2);  // (K Q^T) block: lane holds 4 consecutive j of row t
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int t = 16 * wave + 4 * g4 + i, j = 16 * tj + r16;
       Gm[t * PG + j] = a1[i];
-      const float am = j <= t ? expf(cum[t] - cum[j]) * a2[i] : 0.f;
-      const uint16_t hv = f2bf(am);
-      Ag[wo * kC * 2 + t * kC + j] = hv;
-      Ag[wo * kC * 2 + kC * kC + t * kC + j] = f2bf(am - bf2f(hv));
+    }
+    {
+      const int t = 16 * wave + r16, j0 = 16 * tj + 4 * g4;
+      uint16_t hv[4], lv[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int j = j0 + i;
+        const float am = j <= t ? expf(cum[t] - cum[j]) * a2[i] : 0.f;
+        hv[i] = f2bf(am);
+        lv[i] = f2bf(am - bf2f(hv[i]));
+      }
+      uint16_t* arow = Ag + wo * kC * 2 + t * kC + j0;
+      *reinterpret_cast<uint2*>(arow) = make_uint2(pack_bf2u(hv[0], hv[1]), pack_bf2u(hv[2], hv[3]));
+      *reinterpret_cast<uint2*>(arow + kC * kC) =
+          make_uint2(pack_bf2u(lv[0], lv[1]), pack_bf2u(lv[2], lv[3]));
     }
   }
   __syncthreads();
@@ -252,44 +267,54 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(
   __syncthreads();
   // ---- W = TW K  [64 x DK] (stored as (hi, lo) bf16 planes),  U0 = TU V  [64 x DV] (fp32)
   {
-    constexpr int NTL = 4 * (DK / 16) + 4 * (DV / 16);  // output tiles of both products
-    for (int tile = wave; tile < NTL; tile += 4) {
-      const bool isW = tile < 4 * (DK / 16);
-      const int tt = isW ? tile : tile - 4 * (DK / 16);
+    // wave w takes row blocks (product, tm) = w and w + 4 of the 8 (W: tm 0..3,
+    // U0: tm 0..3); their A fragments are scaled and split once, then reused
+    // across the column tiles
+    for (int pr = wave; pr < 8; pr += 4) {
+      const bool isW = pr < 4;
+      const int tm = pr & 3;
       const int nd = isW ? DK / 16 : DV / 16;
-      const int tm = tt / nd, tn = tt - (tt / nd) * nd;
-      f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+      const float* sc = isW ? wsc : bet;
+      uint4 ahi[kC / 32], alo[kC / 32];
 #pragma unroll
       for (int s = 0; s < kC / 32; ++s) {
-        // A operand: Ti diag(beta Gamma_prev) (W) or Ti diag(beta) (U0), split
-        // into (hi, lo) bf16 in registers
+        // A operand: Ti diag(beta Gamma_prev) (W) or Ti diag(beta) (U0)
         const int col = 32 * s + 8 * g4;
-        const float* sc = isW ? wsc : bet;
         float av[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) av[j] = Ti[(16 * tm + r16) * PG + col + j] * sc[col + j];
-        uint4 ahi, alo;
-        split8(av, ahi, alo);
-        const uint4 bb = *reinterpret_cast<const uint4*>(
-            (isW ? KsT : VsT) + (16 * tn + r16) * PT + 32 * s + 8 * g4);
-        acc = mfma16(ahi, bb, acc);
-        acc = mfma16(alo, bb, acc);
+        split8(av, ahi[s], alo[s]);
       }
-      if (isW) {
-        // W as a (hi, lo) pair of bf16 planes [2][64][DK]: W = hi + lo to ~2^-16
-        uint16_t* whi = Wg + wo * DK * 2;
-        uint16_t* wlo = whi + kC * DK;
+      const int row = 16 * tm + r16;
+      for (int tn = 0; tn < nd; ++tn) {
+        f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int idx = (16 * tm + 4 * g4 + i) * DK + 16 * tn + r16;
-          const uint16_t hv = f2bf(acc[i]);
-          whi[idx] = hv;
-          wlo[idx] = f2bf(acc[i] - bf2f(hv));
+        for (int s = 0; s < kC / 32; ++s) {
+          const uint4 bb = *reinterpret_cast<const uint4*>(
+              (isW ? KsT : VsT) + (16 * tn + r16) * PT + 32 * s + 8 * g4);
+          // transposed product (B^T A^T): lane l ends with row 16 tm + l % 16
+          // and the 4 consecutive columns 16 tn + 4 (l / 16) .. +3
+          acc = mfma16(bb, ahi[s], acc);
+          acc = mfma16(bb, alo[s], acc);
         }
-      } else {
-        float* dst = U0g + wo * DV;
+        const int col0 = 16 * tn + 4 * g4;
+        if (isW) {
+          // W as a (hi, lo) pair of bf16 planes [2][64][DK]: W = hi + lo to ~2^-16
+          uint16_t* whi = Wg + wo * DK * 2 + row * DK + col0;
+          uint16_t hv[4], lv[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) dst[(16 * tm + 4 * g4 + i) * DV + 16 * tn + r16] = acc[i];
+          for (int i = 0; i < 4; ++i) {
+            hv[i] = f2bf(acc[i]);
+            lv[i] = f2bf(acc[i] - bf2f(hv[i]));
+          }
+          *reinterpret_cast<uint2*>(whi) =
+              make_uint2(pack_bf2u(hv[0], hv[1]), pack_bf2u(hv[2], hv[3]));
+          *reinterpret_cast<uint2*>(whi + kC * DK) =
+              make_uint2(pack_bf2u(lv[0], lv[1]), pack_bf2u(lv[2], lv[3]));
+        } else {
+          *reinterpret_cast<float4*>(U0g + wo * DV + row * DV + col0) =
+              make_float4(acc[0], acc[1], acc[2], acc[3]);
+        }
       }
     }
   }
@@ -312,9 +337,6 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(
 // mod 8) and read the chunk operands through one L2.
 constexpr int kScanThreads = 512;
 
-__device__ __forceinline__ uint32_t pack_bf2u(uint16_t a, uint16_t b) {
-  return static_cast<uint32_t>(a) | (static_cast<uint32_t>(b) << 16);
-}
 
 template <int DK, int DV, int DVS>
 __global__ __launch_bounds__(kScanThreads) void gdn_chunk_scan_kernel(
