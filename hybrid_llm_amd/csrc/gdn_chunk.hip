@@ -323,13 +323,17 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(
 
 // ---------------------------------------------------------------------------
 // Kernel 2: sequential scan over chunks for one (b, h, DVS-column state
-// slice), 8 wavefronts.  Every fp32 operand enters the MFMA as a (hi, lo)
-// bf16 pair made once: W and A arrive split from kernel 1; the state slice
-// lives in the registers of the wave that owns each 16 x 16 tile and is
-// split into a transposed LDS copy after every update; U and Gamma_C/Gamma o U
-// are split once into transposed LDS tiles.  Per chunk:
-//   U = U0 - W S                       (one tile per wave)
-//   O = Gamma Q S + A U                (one tile per wave, bf16 out)
+// slice), 8 wavefronts.  Every slice reads the chunk's K, Q, W and A, so wider
+// slices cut that stream: dk = dv = 128 runs 64-column slices (one round of
+// workgroups), dk = dv = 64 runs 32-column ones (two workgroups per CU).
+// Every fp32 operand enters the MFMA as a (hi, lo) bf16 pair made once: W and
+// A arrive split from kernel 1; the state slice lives in the registers of the
+// wave that owns each 16 x 16 tile and is split into a transposed LDS copy
+// after every update; U is split once into a transposed LDS tile, and
+// (Gamma_C/Gamma) o U is formed from that split where the state update reads
+// it.  Per chunk (tiles spread evenly over the waves):
+//   U = U0 - W S
+//   O = Gamma Q S + A U                (bf16 out)
 //   S = Gamma_C S + K^T diag(Gamma_C / Gamma) U   (owner waves, registers)
 // The next chunk's operands (K, Q, W, A, U0, cumulative log-decays) are
 // fetched into registers at the start of a chunk and stored to LDS after it.
@@ -360,7 +364,6 @@ __global__ __launch_bounds__(kScanThreads) void gdn_chunk_scan_kernel(
   __shared__ __align__(16) uint16_t KsT[DK * PT];                  // K^T [DK][64]
   __shared__ __align__(16) uint16_t SThi[DVS * PB], STlo[DVS * PB];  // S^T [DVS][DK]
   __shared__ __align__(16) uint16_t UThi[DVS * PT], UTlo[DVS * PT];  // U^T [DVS][64]
-  __shared__ __align__(16) uint16_t DThi[DVS * PT], DTlo[DVS * PT];  // (dec o U)^T
   __shared__ float cum[kC], ecum[kC], dec[kC];
 
   const int per_xcd = (gridDim.x + 7) / 8;
@@ -491,22 +494,16 @@ __global__ __launch_bounds__(kScanThreads) void gdn_chunk_scan_kernel(
         acc = mfma16(ah, blv, acc);
         acc = mfma16(al, bhv, acc);
       }
-      uint16_t uh[4], ul[4], dh[4], dl[4];
+      uint16_t uh[4], ul[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int t = 16 * tm + 4 * g4 + i;
         const float uval = pu[ot][i] - acc[i];
         uh[i] = f2bf(uval);
         ul[i] = f2bf(uval - bf2f(uh[i]));
-        const float dv = dec[t] * uval;
-        dh[i] = f2bf(dv);
-        dl[i] = f2bf(dv - bf2f(dh[i]));
       }
       const int off = (16 * tn + r16) * PT + 16 * tm + 4 * g4;
       *reinterpret_cast<uint2*>(UThi + off) = uint2{pack_bf2u(uh[0], uh[1]), pack_bf2u(uh[2], uh[3])};
       *reinterpret_cast<uint2*>(UTlo + off) = uint2{pack_bf2u(ul[0], ul[1]), pack_bf2u(ul[2], ul[3])};
-      *reinterpret_cast<uint2*>(DThi + off) = uint2{pack_bf2u(dh[0], dh[1]), pack_bf2u(dh[2], dh[3])};
-      *reinterpret_cast<uint2*>(DTlo + off) = uint2{pack_bf2u(dl[0], dl[1]), pack_bf2u(dl[2], dl[3])};
     }
     __syncthreads();  // U^T, (dec o U)^T complete
 
@@ -552,8 +549,19 @@ __global__ __launch_bounds__(kScanThreads) void gdn_chunk_scan_kernel(
       for (int s = 0; s < kC / 32; ++s) {
         const uint4 ka = *reinterpret_cast<const uint4*>(KsT + (16 * tm + r16) * PT + 32 * s + 8 * g4);
         const int bo = (16 * tn + r16) * PT + 32 * s + 8 * g4;
-        acc = mfma16(ka, *reinterpret_cast<const uint4*>(DThi + bo), acc);
-        acc = mfma16(ka, *reinterpret_cast<const uint4*>(DTlo + bo), acc);
+        // B operand (dec o U)^T: dec[t] (U_hi + U_lo) for the 8 tokens of the
+        // fragment, split again into (hi, lo) bf16
+        const uint4 uhv = *reinterpret_cast<const uint4*>(UThi + bo);
+        const uint4 ulv = *reinterpret_cast<const uint4*>(UTlo + bo);
+        float hf[8], lf[8], dv[8];
+        unpack8(uhv, hf);
+        unpack8(ulv, lf);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) dv[j] = dec[32 * s + 8 * g4 + j] * (hf[j] + lf[j]);
+        uint4 dhv, dlv;
+        split8(dv, dhv, dlv);
+        acc = mfma16(ka, dhv, acc);
+        acc = mfma16(ka, dlv, acc);
       }
 #pragma unroll
       for (int i = 0; i < 4; ++i) sreg[u][i] = gc * sreg[u][i] + acc[i];
@@ -627,8 +635,8 @@ extern "C" int32_t llmy_gdn_prefill_bf16(const llmy_bf16* q, const llmy_bf16* k,
                        dim3(256), 0, s, q, k, v, beta, g, W, U0, A, cum, T, H, NC);
     int32_t st = launch_status();
     if (st != 0) return st;
-    const int units = B * H * (128 / 32);
-    hipLaunchKernelGGL((gdn_chunk_scan_kernel<128, 128, 32>), dim3((units + 7) / 8 * 8),
+    const int units = B * H * (128 / 64);
+    hipLaunchKernelGGL((gdn_chunk_scan_kernel<128, 128, 64>), dim3((units + 7) / 8 * 8),
                        dim3(kScanThreads), 0, s, q, k, W, U0, A, cum, state, out, T, H, NC, units);
   }
   return launch_status();
