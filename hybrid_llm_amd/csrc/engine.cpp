@@ -680,11 +680,15 @@ void linear(const uint16_t* x, const uint16_t* w, void* out, const float* aux, i
 
 // Decode sizes for which the MoE front end is the fused router
 // (llmy_moe_route_decode) with route-indexed experts.
-bool fused_route(const Config& c, int rows) {
+// The fused norm + router kernel (llmy_moe_route_decode) takes any number of
+// rows at these sizes; the route-indexed decode experts also need few routes.
+bool router_fusable(const Config& c) {
   const int D = c.d_model;
   return static_cast<long long>(c.experts) * D <= 24576 && (D == 256 || D == 512 || D == 1024) &&
-         c.top_k <= 8 && rows * c.routes() <= 2048;
+         c.top_k <= 8;
 }
+
+bool fused_route(const Config& c, int rows) { return router_fusable(c) && rows * c.routes() <= 2048; }
 
 // MoE of layer l over `rows` rows (x updated, h = next pre-norm of x).
 // Decode uses the fused router and route-indexed experts where the sizes
@@ -749,10 +753,17 @@ void moe_block(const Model& m, const Layer& L, Buffers& b, int rows, const float
                "llmy_moe_combine_norm");
     return;
   }
-  check_call(llmy_rmsnorm_f32_bf16(b.x, L.ffn_norm, b.h, rows, D, c.eps, st), "rmsnorm");
-  check_call(llmy_router_topk_bf16(b.h, L.router_norm, L.w_router, nullptr, b.idx, b.gates, rows,
-                                   D, E, k, c.eps, st),
-             "llmy_router_topk_bf16");
+  if (router_fusable(c)) {  // one launch per token: pre-MoE norm + router + top-k
+    check_call(llmy_moe_route_decode(b.x, nullptr, 0, nullptr, L.ffn_norm, L.router_norm,
+                                     L.w_router, b.h, b.idx, b.gates, nullptr, nullptr, nullptr,
+                                     nullptr, rows, D, E, k, c.eps, st),
+               "llmy_moe_route_decode");
+  } else {
+    check_call(llmy_rmsnorm_f32_bf16(b.x, L.ffn_norm, b.h, rows, D, c.eps, st), "rmsnorm");
+    check_call(llmy_router_topk_bf16(b.h, L.router_norm, L.w_router, nullptr, b.idx, b.gates,
+                                     rows, D, E, k, c.eps, st),
+               "llmy_router_topk_bf16");
+  }
   context_route();
   with_shared(ids, gts);
   check_call(llmy_moe_permute(ids, rows * kx, EX, b.counts, b.offsets, b.sorted, b.route_pos,

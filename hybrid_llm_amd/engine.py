@@ -151,8 +151,9 @@ class HybridDecoder:
         # Decode MoE: fused norm + router (W_r in LDS) and route-indexed experts
         # that derive their routes from the ids (no permutation pass) when the
         # sizes allow; else norm, router, permutation and sorted experts.
-        self.fused_route = (E * D <= 24576 and D in (256, 512, 1024) and k <= 8
-                            and B * kx <= 2048)
+        # the fused norm + router kernel (any number of rows)
+        self.fused_router_ok = E * D <= 24576 and D in (256, 512, 1024) and k <= 8
+        self.fused_route = self.fused_router_ok and B * kx <= 2048
         if S > 0:
             self.buf["idx_all"] = torch.zeros(B, kx, dtype=torch.int32, device=dev)
             self.buf["gates_all"] = torch.zeros(B, kx, dtype=f32, device=dev)
@@ -444,15 +445,21 @@ class HybridDecoder:
         p = f"L{l}."
         R, D, E, k = x.shape[0], cfg.d_model, cfg.n_experts, cfg.top_k
         dev, s = self.dev, torch.cuda.current_stream().cuda_stream
-        ops.rmsnorm(x, w[p + "ffn_norm"], cfg.eps, out=h)
         idx = torch.empty(R, k, dtype=torch.int32, device=dev)
         gates = torch.empty(R, k, dtype=torch.float32, device=dev)
+        if self.fused_router_ok:
+            # one launch per token: pre-MoE norm (h) + router + top-k
+            ops.moe_route_decode(x, w[p + "ffn_norm"], w[p + "router_norm"], w[p + "w_router"],
+                                 k, cfg.eps, bufs={"h": h, "idx": idx, "gates": gates},
+                                 permute=False)
+        else:
+            ops.rmsnorm(x, w[p + "ffn_norm"], cfg.eps, out=h)
         if cfg.context_router:
             # rows are B sequences of T tokens from position 0 (fresh state)
             idx, gates, _ = ops.router_context(h, self._ctx_weights(p), st["ctx_ring"], k,
                                                eps=cfg.eps, layout=ops.LAYOUT_PACKED,
                                                bufs={"idx": idx, "gates": gates})
-        else:
+        elif not self.fused_router_ok:
             _lib.call("llmy_router_topk_bf16", h.data_ptr(), w[p + "router_norm"].data_ptr(),
                       w[p + "w_router"].data_ptr(), None, idx.data_ptr(), gates.data_ptr(), R, D,
                       E, k, cfg.eps, s)
