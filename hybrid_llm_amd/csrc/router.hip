@@ -121,6 +121,78 @@ __global__ __launch_bounds__(256) void router_topk_bf16_kernel(
 
 }
 
+// The same arithmetic for D = 256 NCH (NCH = 1, 2, 4): the normalised row stays
+// in registers and the W_r rows of four experts are requested before their
+// dot products, so a token waits on one memory round trip per four experts
+// instead of one per expert.  Every product, sum and reduction is taken in the
+// order of router_topk_bf16_kernel, so logits, ids and gates are identical.
+template <int NCH>
+__global__ __launch_bounds__(256) void router_topk_bf16_nch_kernel(
+    const uint16_t* __restrict__ x, const float* __restrict__ norm_w,
+    const float* __restrict__ w, float* __restrict__ logits_out,
+    int32_t* __restrict__ idx_out, float* __restrict__ gates_out,
+    int T, int E, int k, float eps) {
+  constexpr int D = 256 * NCH;
+  constexpr int G = 4;  // experts per batch of W_r loads
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * 4 + wave;
+  if (t >= T) return;
+  const uint16_t* xr = x + static_cast<size_t>(t) * D;
+  float h[NCH][4];
+  float ss = 0.0f;
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    const uint2 raw = *reinterpret_cast<const uint2*>(xr + 4 * lane + 256 * c);
+    h[c][0] = __uint_as_float(raw.x << 16);
+    h[c][1] = __uint_as_float(raw.x & 0xffff0000u);
+    h[c][2] = __uint_as_float(raw.y << 16);
+    h[c][3] = __uint_as_float(raw.y & 0xffff0000u);
+    ss += h[c][0] * h[c][0] + h[c][1] * h[c][1] + h[c][2] * h[c][2] + h[c][3] * h[c][3];
+  }
+  if (norm_w != nullptr) {
+    const float r = rsqrtf(wave_sum(ss) / static_cast<float>(D) + eps);
+#pragma unroll
+    for (int c = 0; c < NCH; ++c)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) h[c][j] = (h[c][j] * r) * norm_w[4 * lane + 256 * c + j];
+  }
+  float mine[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int e0 = 0; e0 < E; e0 += G) {
+    float4 wv[G][NCH];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const int e = min(e0 + g, E - 1);  // rows past E are loaded but unused
+#pragma unroll
+      for (int c = 0; c < NCH; ++c)
+        wv[g][c] = *reinterpret_cast<const float4*>(w + static_cast<size_t>(e) * D + 4 * lane +
+                                                    256 * c);
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      float acc = 0.0f;
+#pragma unroll
+      for (int c = 0; c < NCH; ++c) {
+        acc = fmaf(h[c][0], wv[g][c].x, acc);
+        acc = fmaf(h[c][1], wv[g][c].y, acc);
+        acc = fmaf(h[c][2], wv[g][c].z, acc);
+        acc = fmaf(h[c][3], wv[g][c].w, acc);
+      }
+      acc = wave_sum(acc);
+      const int e = e0 + g;
+      if (e < E && (e & 63) == lane) mine[e >> 6] = acc;
+    }
+  }
+  if (logits_out != nullptr) {
+    for (int s = 0; s < 4; ++s) {
+      const int e = lane + 64 * s;
+      if (e < E) logits_out[static_cast<size_t>(t) * E + e] = mine[s];
+    }
+  }
+  topk_softmax_store(mine, E, k, lane, idx_out + static_cast<size_t>(t) * k,
+                     gates_out + static_cast<size_t>(t) * k);
+}
+
 // Top-k + softmax from precomputed fp32 logits [T, E]; one wavefront per token.
 __global__ __launch_bounds__(256) void router_topk_from_logits_kernel(
     const float* __restrict__ logits, int32_t* __restrict__ idx_out,
@@ -468,6 +540,14 @@ extern "C" int32_t llmy_router_topk_bf16(const uint16_t* x, const float* norm_w,
   if (T == 0) return 0;
   LLMY_REQUIRE(x && w_router && idx && gates);
   LLMY_REQUIRE(aligned(x, 8) && aligned(w_router, 16) && (norm_w == nullptr || aligned(norm_w, 4)));
+  const hipStream_t s = as_stream(stream);
+  const dim3 grid((T + 3) / 4);
+  switch (D) {
+    case 256: hipLaunchKernelGGL(router_topk_bf16_nch_kernel<1>, grid, dim3(256), 0, s, x, norm_w, w_router, logits_out, idx, gates, T, E, k, eps); return launch_status();
+    case 512: hipLaunchKernelGGL(router_topk_bf16_nch_kernel<2>, grid, dim3(256), 0, s, x, norm_w, w_router, logits_out, idx, gates, T, E, k, eps); return launch_status();
+    case 1024: hipLaunchKernelGGL(router_topk_bf16_nch_kernel<4>, grid, dim3(256), 0, s, x, norm_w, w_router, logits_out, idx, gates, T, E, k, eps); return launch_status();
+    default: break;
+  }
   const size_t lds = 4 * static_cast<size_t>(D) * sizeof(float);
   hipLaunchKernelGGL(router_topk_bf16_kernel, dim3((T + 3) / 4), dim3(256), lds,
                      as_stream(stream), x, norm_w, w_router, logits_out, idx, gates, T, D, E, k,
