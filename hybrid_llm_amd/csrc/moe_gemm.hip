@@ -589,6 +589,45 @@ int32_t dense_gemm_mfma(const uint16_t* x, const uint16_t* w, void* out, const f
   // m-tiles.
   const bool wide = static_cast<long long>((M + 255) / 256) * ((N + 255) / 256) >= 256;
   const int bt = wide ? 256 : 128;
+  // A narrow column tail (N = 256 n + 16 .. 64, e.g. a 4096-row projection
+  // plus its 16 gate rows) would cost a whole 256-wide tile per m-tile, often
+  // a second round of workgroups: the whole 256-column tiles run first, and
+  // the tail columns follow as a 128-tile launch of their own (the same
+  // output rows, column offset and stride N).
+  const int tail = wide && N > 256 ? N % 256 : 0;
+  if (tail > 0 && tail <= 64) {
+    const int n_main = N - tail;
+    TileArgs t = g;
+    t.N = n_main;
+    t.m_tiles = (M + 255) / 256;
+    t.n_tiles = n_main / 256;
+    t.group_m = 4;
+    const long long main_items = static_cast<long long>(t.m_tiles) * t.n_tiles;
+    if (main_items >= (1ll << 31) - kNumXcd) return static_cast<int32_t>(hipErrorInvalidValue);
+    int32_t st = 0;
+#define LLMY_DENSE_T(T_, OCC_, ARGS_, ITEMS_)                                                      \
+  switch (epi) {                                                                                   \
+    case kDenseBf16: st = launch_tiles<kTileDense, T_, T_, 64, 2, kDenseBf16, OCC_>(ARGS_, ITEMS_, s); break; \
+    case kDenseF32: st = launch_tiles<kTileDense, T_, T_, 64, 2, kDenseF32, OCC_>(ARGS_, ITEMS_, s); break;   \
+    case kDenseResid: st = launch_tiles<kTileDense, T_, T_, 64, 2, kDenseResid, OCC_>(ARGS_, ITEMS_, s); break; \
+    default: st = launch_tiles<kTileDense, T_, T_, 64, 2, kDenseGated, OCC_>(ARGS_, ITEMS_, s); break;        \
+  }
+    LLMY_DENSE_T(256, 1, t, main_items)
+    if (st != 0) return st;
+    // the tail: rows n_main .. N-1 of w (for the packed order too: 16-row
+    // groups are contiguous), output columns n_main .. N-1
+    TileArgs u = g;
+    u.w = w + static_cast<long long>(n_main) * K;
+    u.out = static_cast<char*>(out) + static_cast<long long>(n_main) * (epi == kDenseBf16 ? 2 : 4);
+    u.aux = aux ? aux + n_main : nullptr;
+    u.N = tail;
+    u.m_tiles = (M + 127) / 128;
+    u.n_tiles = 1;
+    u.group_m = 4;
+    LLMY_DENSE_T(128, 2, u, static_cast<long long>(u.m_tiles))
+#undef LLMY_DENSE_T
+    return st;
+  }
   g.m_tiles = (M + bt - 1) / bt;
   g.n_tiles = (N + bt - 1) / bt;
   g.group_m = 4;

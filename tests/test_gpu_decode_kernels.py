@@ -44,7 +44,10 @@ def _bf(t):
                                    (17, 16, 2048),
                                    # M >= 256: MFMA tiles, incl. partial m/n tiles
                                    (256, 1024, 1024), (300, 4112, 1024), (1000, 1040, 256),
-                                   (257, 16, 512), (4096, 1024, 1024)])
+                                   (257, 16, 512), (4096, 1024, 1024),
+                                   # wide tiles with a narrow column tail (16 / 64 columns)
+                                   # run as two launches; an 80-column tail stays in one
+                                   (4096, 4112, 1024), (4000, 4160, 256), (4096, 4176, 256)])
 @pytest.mark.parametrize("epi", [0, 1, 2, 3])
 @pytest.mark.parametrize("layout", [0, 1])
 def test_linear_epilogues(M, N, K, epi, layout):
