@@ -168,6 +168,29 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(
           make_uint2(pack_bf2u(lv[0], lv[1]), pack_bf2u(lv[2], lv[3]));
     }
   }
+  // K and V rows for the transposed staging after the inverse, fetched now so
+  // their latency hides behind the inverse: item i = (token pair, 8-dim chunk)
+  // f = threadIdx.x + 256 i.  Rows past the chunk are clamped (valid
+  // addresses) here and zeroed at the store, so no load is waited on early.
+  constexpr int KPI = (kC / 2) * (DK / 8) / 256, VPI = (kC / 2) * (DV / 8) / 256;
+  static_assert(KPI * 256 == (kC / 2) * (DK / 8) && VPI * 256 == (kC / 2) * (DV / 8), "pairs");
+  uint4 kp[KPI][2], vp[VPI][2];
+#pragma unroll
+  for (int i = 0; i < KPI; ++i) {
+    const int f = threadIdx.x + 256 * i;
+    const int t2 = 2 * (f % (kC / 2)), cc = f / (kC / 2);
+#pragma unroll
+    for (int e = 0; e < 2; ++e)
+      kp[i][e] = *reinterpret_cast<const uint4*>(k + kbase + min(t2 + e, Tc - 1) * rk + 8 * cc);
+  }
+#pragma unroll
+  for (int i = 0; i < VPI; ++i) {
+    const int f = threadIdx.x + 256 * i;
+    const int t2 = 2 * (f % (kC / 2)), cc = f / (kC / 2);
+#pragma unroll
+    for (int e = 0; e < 2; ++e)
+      vp[i][e] = *reinterpret_cast<const uint4*>(v + vbase + min(t2 + e, Tc - 1) * rv + 8 * cc);
+  }
   __syncthreads();
   // ---- L (strictly lower)
   for (int e = threadIdx.x; e < kC * kC; e += 256) {
@@ -243,26 +266,37 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(
     }
   }
 
-  // ---- K^T and V^T into R0 (the block products above are done): token
-  // fastest across lanes, so the 2-byte LDS stores of a wave land in
-  // consecutive addresses
-  for (int f = threadIdx.x; f < kC * (DK / 8); f += 256) {
-    const int t = f % kC, cc = f / kC;
-    uint4 kv = uint4{0u, 0u, 0u, 0u};
-    if (t < Tc) kv = *reinterpret_cast<const uint4*>(k + kbase + t * rk + 8 * cc);
-    const uint32_t w[4] = {kv.x, kv.y, kv.z, kv.w};
+  // ---- K^T and V^T into R0 (the block products above are done), from the
+  // rows fetched before the inverse: each of a pair's 8 dims is stored as one
+  // dword holding both tokens (zero past the chunk), the lanes of a wave
+  // writing consecutive dwords of a row.
 #pragma unroll
-    for (int jj = 0; jj < 8; ++jj)
-      KsT[(8 * cc + jj) * PT + t] = static_cast<uint16_t>(w[jj >> 1] >> (16 * (jj & 1)));
+  for (int i = 0; i < KPI; ++i) {
+    const int f = threadIdx.x + 256 * i;
+    const int t2 = 2 * (f % (kC / 2)), cc = f / (kC / 2);
+    const uint4 z = uint4{0u, 0u, 0u, 0u};
+    const uint4 a0 = t2 < Tc ? kp[i][0] : z, a1 = t2 + 1 < Tc ? kp[i][1] : z;
+    const uint32_t w0[4] = {a0.x, a0.y, a0.z, a0.w}, w1[4] = {a1.x, a1.y, a1.z, a1.w};
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj) {
+      const uint32_t lo = (w0[jj >> 1] >> (16 * (jj & 1))) & 0xffffu;
+      const uint32_t hi = (w1[jj >> 1] >> (16 * (jj & 1))) & 0xffffu;
+      *reinterpret_cast<uint32_t*>(KsT + (8 * cc + jj) * PT + t2) = lo | (hi << 16);
+    }
   }
-  for (int f = threadIdx.x; f < kC * (DV / 8); f += 256) {
-    const int t = f % kC, cc = f / kC;
-    uint4 vv = uint4{0u, 0u, 0u, 0u};
-    if (t < Tc) vv = *reinterpret_cast<const uint4*>(v + vbase + t * rv + 8 * cc);
-    const uint32_t w[4] = {vv.x, vv.y, vv.z, vv.w};
 #pragma unroll
-    for (int jj = 0; jj < 8; ++jj)
-      VsT[(8 * cc + jj) * PT + t] = static_cast<uint16_t>(w[jj >> 1] >> (16 * (jj & 1)));
+  for (int i = 0; i < VPI; ++i) {
+    const int f = threadIdx.x + 256 * i;
+    const int t2 = 2 * (f % (kC / 2)), cc = f / (kC / 2);
+    const uint4 z = uint4{0u, 0u, 0u, 0u};
+    const uint4 a0 = t2 < Tc ? vp[i][0] : z, a1 = t2 + 1 < Tc ? vp[i][1] : z;
+    const uint32_t w0[4] = {a0.x, a0.y, a0.z, a0.w}, w1[4] = {a1.x, a1.y, a1.z, a1.w};
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj) {
+      const uint32_t lo = (w0[jj >> 1] >> (16 * (jj & 1))) & 0xffffu;
+      const uint32_t hi = (w1[jj >> 1] >> (16 * (jj & 1))) & 0xffffu;
+      *reinterpret_cast<uint32_t*>(VsT + (8 * cc + jj) * PT + t2) = lo | (hi << 16);
+    }
   }
   __syncthreads();
   // ---- W = TW K  [64 x DK] (stored as (hi, lo) bf16 planes),  U0 = TU V  [64 x DV] (fp32)
