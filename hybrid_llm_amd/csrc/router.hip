@@ -303,19 +303,9 @@ __device__ void permute_block(Get get, int n, int E, int32_t* __restrict__ count
     // ballot per expert ranks the routes of that expert (ascending r) and one
     // shuffle hands each route its expert's base.  Same placement as below.
     int next = lane < E ? running[lane] : 0;
-    for (int c = c0; c < c1; ++c) {
+    auto place = [&](int c, int e) {
       const int r = c * 64 + lane;
-      int e = -1;
-      if (r < n) {
-        if (c - c0 < kHeld) {
-#pragma unroll
-          for (int i = 0; i < kHeld; ++i)
-            if (c - c0 == i) e = held[i];
-        } else {
-          e = get(r);
-        }
-        if (e < 0 || e >= E) e = -1;
-      }
+      if (r >= n || e < 0 || e >= E) e = -1;
       uint64_t mine = 0ull;
       int add = 0;
       for (int ee = 0; ee < E; ++ee) {
@@ -330,7 +320,17 @@ __device__ void permute_block(Get get, int n, int E, int32_t* __restrict__ count
         route_pos[r] = pos;
       }
       next += add;
+    };
+    // The held chunks first, from registers: no load sits in this loop, so
+    // the scattered stores of successive chunks stay in flight together (a
+    // load here would make each chunk wait for the previous chunk's stores,
+    // which share the vector memory counter).
+#pragma unroll
+    for (int i = 0; i < kHeld; ++i) {
+      if (c0 + i >= c1) break;
+      place(c0 + i, held[i]);
     }
+    for (int c = c0 + kHeld; c < c1; ++c) place(c, c * 64 + lane < n ? get(c * 64 + lane) : -1);
     return;
   }
   for (int c = c0; c < c1; ++c) {
