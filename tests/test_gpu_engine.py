@@ -174,3 +174,31 @@ def test_graph_replay_matches_eager():
         torch.cuda.synchronize()
         assert torch.equal(out, eager[i]), i
     assert torch.equal(a.pos, b.pos)
+
+
+def test_graph_replay_with_sampling_matches_eager():
+    """The captured step with a top-p draw configured: every replay, with eager
+    work and synchronisations between replays, equals the eager step bit for
+    bit (logits, greedy ids and drawn ids)."""
+    from hybrid_llm_amd.engine import HybridDecoder
+    cfg = replace(C1, layer_kinds=alternating(2))
+    w = init_weights(cfg, seed=7)
+    B = 4
+    u = torch.tensor([0.05, 0.4, 0.7, 0.95])
+    toks = torch.randint(0, cfg.vocab, (5, B), generator=torch.Generator().manual_seed(8))
+    a = HybridDecoder(cfg, w, B, sampling=(0.8, 0.9, 0))
+    a.set_uniforms(u)
+    eager = []
+    for i in range(5):
+        lg = a.step(toks[i].to(torch.int32).cuda()).clone()
+        eager.append((lg, a.buf["next"].clone(), a.buf["sampled"].clone()))
+    b = HybridDecoder(cfg, w, B, sampling=(0.8, 0.9, 0))
+    b.set_uniforms(u)
+    b.capture()
+    for i in range(5):
+        lg = b.step(toks[i].to(torch.int32).cuda()).clone()
+        torch.cuda.synchronize()
+        _ = (lg * 2).sum().item()  # eager work between replays
+        assert torch.equal(lg, eager[i][0]), i
+        assert torch.equal(b.buf["next"], eager[i][1]), i
+        assert torch.equal(b.buf["sampled"], eager[i][2]), i
