@@ -145,3 +145,32 @@ def test_gdn_step_partial_slices_reject_bad_arguments(lib):
     assert f(FAKE, 4112, 0, *tail) == INVALID     # nparts < 1
     assert f(FAKE, 4112, 9, *tail) == INVALID     # nparts > 8
     assert f(FAKE, 4000, 4, *tail) == INVALID     # ld below the row
+
+
+def test_context_router_entries_reject_bad_arguments(lib):
+    """Checked before any launch (no GPU needed): shapes outside the kernels'
+    range, missing pointers, misaligned rows; an empty token axis is a no-op."""
+    lat = lib.llmy_router_context_latent_f32
+    ok = (FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE)
+    assert lat(*ok, 0, 1024, 256, 1e-6, 1e-5, None) == 0                    # no rows
+    assert lat(*ok, 4, 300, 256, 1e-6, 1e-5, None) == INVALID               # D not 256 n (n <= 4)
+    assert lat(*ok, 4, 2048, 256, 1e-6, 1e-5, None) == INVALID
+    assert lat(*ok, 4, 1024, 100, 1e-6, 1e-5, None) == INVALID              # L % 64
+    assert lat(*ok, 4, 1024, 1024, 1e-6, 1e-5, None) == INVALID             # L > 512
+    assert lat(None, *ok[1:], 4, 1024, 256, 1e-6, 1e-5, None) == INVALID
+    assert lat(*ok[:6], None, 4, 1024, 256, 1e-6, 1e-5, None) == INVALID
+    assert lat(FAKE, FAKE, FAKE + 4, *ok[3:], 4, 1024, 256, 1e-6, 1e-5, None) == INVALID
+    win = lib.llmy_router_context_window
+    assert win(FAKE, FAKE, None, FAKE, 0, 5, 8, 256, None) == 0               # no sequences
+    assert win(FAKE, FAKE, None, FAKE, 2, 0, 8, 256, None) == 0               # no tokens
+    assert win(FAKE, FAKE, None, FAKE, 2, 5, 0, 256, None) == INVALID         # window < 1
+    assert win(None, FAKE, None, FAKE, 2, 5, 8, 256, None) == INVALID
+    assert win(FAKE, FAKE, None, FAKE, 70000, 5, 8, 256, None) == INVALID     # grid y limit
+    lg = lib.llmy_router_context_logits_f32
+    assert lg(FAKE, FAKE, FAKE, FAKE, FAKE, 0, 1024, 24, None) == 0
+    assert lg(FAKE, FAKE, FAKE, FAKE, FAKE, 4, 1000, 24, None) == INVALID
+    assert lg(FAKE, FAKE, None, FAKE, FAKE, 4, 1024, 24, None) == INVALID     # no gate
+    assert lg(FAKE, FAKE, FAKE, FAKE, FAKE, 4, 1024, 0, None) == INVALID
+    shared = lib.llmy_moe_append_shared
+    assert shared(FAKE, FAKE, FAKE, FAKE, 4, 2, 8, 0, None) == INVALID         # S = 0
+    assert shared(FAKE, FAKE, FAKE, FAKE, 4, 0, 8, 2, None) == INVALID         # k = 0
