@@ -20,7 +20,8 @@ Also reported on the same JSON line:
                 GDN; decode and prefill), each timed the same way against the
                 HBM or bf16-MFMA peak;
   cpu_baseline  the oracle (fp32 PyTorch restatement of the reference math)
-                on the host cores, on a bounded sample of the same workload.
+                on the host cores, on the same workload (the full C5 step at
+                batch 64): 1 warmup + median of 3 steps.
 """
 from __future__ import annotations
 
@@ -49,13 +50,13 @@ COPY_BYTES = 1 << 29             # calibration copy: 512 MiB read + 512 MiB writ
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-traffic", action="store_true",
                     help="skip the rocprofv3 --pmc runs (e.g. when already under a profiler)")
     ap.add_argument("--no-kernels", action="store_true", help="skip the per-kernel table")
-    ap.add_argument("--kernel-iters", type=int, default=50)
+    ap.add_argument("--kernel-iters", type=int, default=100)
     ap.add_argument("--pmc-child", action="store_true", help=argparse.SUPPRESS)
     return ap.parse_args()
 
@@ -74,23 +75,27 @@ def fill_state(eng, gen):
     torch.cuda.synchronize()
 
 
-def event_time(launch, iters, warm=3):
-    """Average duration (us) of ``launch(i)`` on a stream of its own, bracketed
-    by HIP events recorded on that stream."""
+def event_time(launch, iters, warm=10):
+    """Duration (us) of ``launch(i)`` on a stream of its own: each of ``iters``
+    launches (after ``warm`` untimed ones) is bracketed by its own pair of HIP
+    events recorded on that stream.  Returns (mean, median) over the launches."""
     import torch
     stream = torch.cuda.Stream()
     torch.cuda.synchronize()
     with torch.cuda.stream(stream):
         for i in range(warm):
             launch(i)
-        start = torch.cuda.Event(enable_timing=True)
-        end = torch.cuda.Event(enable_timing=True)
-        start.record(stream)
-        for i in range(iters):
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in range(iters)]
+        for i, (a, b) in enumerate(ev):
+            a.record(stream)
             launch(warm + i)
-        end.record(stream)
-    end.synchronize()
-    return start.elapsed_time(end) * 1e3 / iters
+            b.record(stream)
+    ev[-1][1].synchronize()
+    us = sorted(a.elapsed_time(b) * 1e3 for a, b in ev)
+    mid = len(us) // 2
+    median = us[mid] if len(us) % 2 else 0.5 * (us[mid - 1] + us[mid])
+    return sum(us) / len(us), median
 
 
 def attn_decode_sets(cfg, B, gen):
@@ -160,10 +165,10 @@ def step_bytes(cfg, B: int) -> dict:
 def time_attn_decode(cfg, B, iters, gen):
     import torch
     sets = attn_decode_sets(cfg, B, gen)
-    us = event_time(attn_decode_launcher(cfg, B, sets), iters, warm=5)
+    t = event_time(attn_decode_launcher(cfg, B, sets), iters)
     del sets
     torch.cuda.empty_cache()
-    return us, attn_decode_bytes(cfg, B)
+    return t, attn_decode_bytes(cfg, B)
 
 
 # --------------------------------------------------------------------------- HBM traffic
@@ -237,28 +242,49 @@ def measure_traffic():
 
 
 # --------------------------------------------------------------------------- kernel table
+MALL_BYTES = 256 << 20   # Infinity Cache: rotated input sets must exceed it
+
+
+def n_sets(bytes_per_set: float, minimum: int = 3) -> int:
+    """Number of rotated input sets whose total exceeds the Infinity Cache."""
+    return max(minimum, int(MALL_BYTES // max(bytes_per_set, 1)) + 1)
+
+
 def kernel_table(cfg, B, gen, iters):
-    """Per-kernel roofline fractions for the kernels the metric names."""
+    """Per-kernel roofline fractions for the kernels the metric names.  Every
+    row: HIP events around each launch on the launch stream, 10 warmup
+    launches, mean and median over ``iters``; bandwidth-bound rows rotate
+    input sets totalling more than the 256 MB Infinity Cache."""
     import torch
     import torch.nn.functional as F
     from hybrid_llm_amd import _lib, ops
     rows = {}
 
-    def hbm(name, us, bytes_, workload):
+    def hbm(name, t, bytes_, workload):
+        us, med = t
         gbs = bytes_ / (us * 1e-6) / 1e9
         rows[name] = {"workload": workload, "bound": "hbm", "avg_us": round(us, 2),
+                      "median_us": round(med, 2), "bytes": round(bytes_),
                       "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                       "frac": round(gbs / HBM_PEAK_GBS, 4)}
 
-    def mfma(name, us, flops, workload):
+    def mfma(name, t, flops, workload):
+        us, med = t
         tf = flops / (us * 1e-6) / 1e12
         rows[name] = {"workload": workload, "bound": "mfma", "avg_us": round(us, 2),
+                      "median_us": round(med, 2), "flops": round(flops),
                       "achieved": round(tf, 1), "peak": MFMA_BF16_PEAK_TFLOPS,
                       "unit": "TFLOP/s", "frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4)}
 
+    def latency(name, t, workload):
+        us, med = t
+        rows[name] = {"workload": workload, "bound": "latency", "avg_us": round(us, 2),
+                      "median_us": round(med, 2)}
+
     D, E, Hf, k = cfg.d_model, cfg.n_experts, cfg.expert_hidden, cfg.top_k
     # MoE decode (C2 decode variant / one C5 MoE application): packed expert
-    # weights, 3 rotated sets; bytes = weights of the experts the routes touch
+    # weights (302 MB per set, 3 rotated sets); bytes = weights of the experts
+    # the routes touch
     wsets = [(ops.pack_weights((torch.randn(E, 2 * Hf, D, device="cuda", generator=gen) * 0.02)
                                .bfloat16()),
               ops.pack_weights((torch.randn(E, D, Hf, device="cuda", generator=gen) * 0.02)
@@ -270,45 +296,81 @@ def kernel_table(cfg, B, gen, iters):
     act = torch.empty(B * k, Hf, dtype=torch.bfloat16, device="cuda")
     y = torch.empty(B * k, D, device="cuda")
     n_active = int((bufs["counts"] > 0).sum())
-    us = event_time(lambda i: ops.moe_experts_routed(bufs["h"], bufs["idx"], bufs["gates"],
-                                                     *wsets[i % 3], act=act, y=y,
-                                                     layout=ops.LAYOUT_PACKED), iters)
-    hbm("moe_decode_experts", us, n_active * 3 * Hf * D * 2 + B * D * 2 + B * k * D * 4,
-        f"T={B}, D={D}, E={E}, top-{k}, H={Hf}; {n_active} experts active")
+    t = event_time(lambda i: ops.moe_experts_routed(bufs["h"], bufs["idx"], bufs["gates"],
+                                                    *wsets[i % 3], act=act, y=y,
+                                                    layout=ops.LAYOUT_PACKED), iters)
+    hbm("moe_decode_experts", t, n_active * 3 * Hf * D * 2 + B * D * 2 + B * k * D * 4,
+        f"T={B}, D={D}, E={E}, top-{k}, H={Hf}; {n_active} experts active, 3 weight sets")
     del wsets
-    # GDN decode step (C4 decode variant at C5 head shape): fp32 state read + written
+    # GDN decode step at the C5 head shape (dk = dv = 64): the fused step of
+    # the engine (projection row in, conv gate, state in place)
     Hg, dk, dv = cfg.gdn_heads, cfg.gdn_dk, cfg.gdn_dv
     nproj = 2 * Hg * dk + Hg * dv + D + Hg
-    Ss = [torch.randn(B, Hg, dk, dv, device="cuda", generator=gen) * 0.1 for _ in range(3)]
+    sb = B * Hg * dk * dv * 4
+    ns = n_sets(sb)
+    Ss = [torch.randn(B, Hg, dk, dv, device="cuda", generator=gen) * 0.1 for _ in range(ns)]
     proj = torch.randn(B, nproj, device="cuda", generator=gen)
     go = torch.empty(B, Hg * dv, dtype=torch.bfloat16, device="cuda")
     zb, dec = torch.zeros(Hg, device="cuda"), torch.full((Hg,), 2.0, device="cuda")
-    us = event_time(lambda i: ops.gdn_step_fused(proj, zb, dec, Ss[i % 3], out=go), iters)
-    hbm("gdn_decode_step", us, 2 * B * Hg * dk * dv * 4 + B * nproj * 4 + B * Hg * dv * 2,
-        f"B={B}, H={Hg}, dk=dv={dk}, fp32 state")
+    t = event_time(lambda i: ops.gdn_step_fused(proj, zb, dec, Ss[i % ns], out=go), iters)
+    hbm("gdn_decode_step", t, 2 * sb + B * nproj * 4 + B * Hg * dv * 2,
+        f"C5 shape: B={B}, H={Hg}, dk=dv={dk}, fp32 state, {ns} rotated states "
+        f"({ns * sb / 1e6:.0f} MB)")
     del Ss
+    # GDN decode step, BASELINE config 4's decode variant: B=64, H=16,
+    # dk = dv = 128 (134 MB of state read + written)
+    B4, H4, d4 = 64, 16, 128
+    sb = B4 * H4 * d4 * d4 * 4
+    ns = n_sets(sb)
+    Ss = [torch.randn(B4, H4, d4, d4, device="cuda", generator=gen) * 0.1 for _ in range(ns)]
+    q4 = F.normalize(torch.randn(B4, H4, d4, device="cuda", generator=gen), dim=-1).bfloat16()
+    k4 = F.normalize(torch.randn(B4, H4, d4, device="cuda", generator=gen), dim=-1).bfloat16()
+    v4 = torch.randn(B4, H4, d4, device="cuda", generator=gen).bfloat16()
+    b4 = torch.sigmoid(torch.randn(B4, H4, device="cuda", generator=gen))
+    g4 = torch.exp(-F.softplus(torch.randn(B4, H4, device="cuda", generator=gen)))
+    o4 = torch.empty(B4, H4, d4, dtype=torch.bfloat16, device="cuda")
+    t = event_time(lambda i: ops.gdn_step(q4, k4, v4, b4, g4, Ss[i % ns], out=o4), iters)
+    hbm("gdn_decode_step_c4", t, 2 * sb + 4 * B4 * H4 * d4 * 2 + 2 * B4 * H4 * 4,
+        f"C4 decode: B={B4}, H={H4}, dk=dv={d4}, fp32 state, {ns} rotated states "
+        f"({ns * sb / 1e6:.0f} MB)")
+    del Ss
+    # sampling over [64, 32000] fp32 logits (8.2 MB per set, rotated)
+    V = cfg.vocab
+    lb = B * V * 4
+    ns = n_sets(lb)
+    lsets = [torch.randn(B, V, device="cuda", generator=gen) * 0.6 for _ in range(ns)]
+    us_ = torch.rand(B, device="cuda", generator=gen)
+    so = torch.empty(B, dtype=torch.int32, device="cuda")
+    strm = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
+    t = event_time(lambda i: _lib.call("llmy_sample_argmax_f32", lsets[i % ns].data_ptr(), B, V,
+                                       so.data_ptr(), strm()), iters)
+    latency("sample_argmax", t, f"greedy argmax over [{B}, {V}] fp32, {ns} rotated logit sets")
+    t = event_time(lambda i: _lib.call("llmy_sample_top_p_f32", lsets[i % ns].data_ptr(), B, V,
+                                       SAMPLING[0], SAMPLING[2], SAMPLING[1], us_.data_ptr(),
+                                       so.data_ptr(), strm()), iters)
+    latency("sample_top_p", t, f"T={SAMPLING[0]}, top-p={SAMPLING[1]} draw over [{B}, {V}] fp32, "
+                               f"{ns} rotated logit sets")
+    del lsets
     # MoE prefill (C2): router -> permute -> grouped experts -> combine
+    it_mfma = max(10, iters // 5)
     T2 = 4096
     x2 = torch.randn(T2, D, device="cuda", generator=gen).bfloat16()
     wr2 = torch.randn(E, D, device="cuda", generator=gen) * 0.02
-    wgu = (torch.randn(E, 2 * Hf, D, device="cuda", generator=gen) * 0.02).bfloat16()
-    wd = (torch.randn(E, D, Hf, device="cuda", generator=gen) * 0.02).bfloat16()
-    us = event_time(lambda i: ops.moe_forward(x2, wr2, wgu, wd, k), max(3, iters // 10))
-    mfma("moe_prefill_layer", us, 2 * T2 * k * (D * 2 * Hf + Hf * D),
-         f"C2: T={T2}, D={D}, E={E}, top-{k}, H={Hf} (router+permute+experts+combine)")
-    del x2, wgu, wd
-    # the grouped expert GEMMs alone (C2 shape, routes from the router above)
-    x2 = torch.randn(T2, D, device="cuda", generator=gen).bfloat16()
-    idx2, gates2 = ops.router_topk(x2, wr2, k)
-    perm2 = ops.moe_permute(idx2.view(-1), E)
     esets = [((torch.randn(E, 2 * Hf, D, device="cuda", generator=gen) * 0.02).bfloat16(),
               (torch.randn(E, D, Hf, device="cuda", generator=gen) * 0.02).bfloat16())
              for _ in range(2)]
+    t = event_time(lambda i: ops.moe_forward(x2, wr2, *esets[i % 2], k), it_mfma)
+    mfma("moe_prefill_layer", t, 2 * T2 * k * (D * 2 * Hf + Hf * D),
+         f"C2: T={T2}, D={D}, E={E}, top-{k}, H={Hf} (router+permute+experts+combine), "
+         f"2 weight sets")
+    # the grouped expert GEMMs alone (C2 shape, routes from the router above)
+    idx2, gates2 = ops.router_topk(x2, wr2, k)
+    perm2 = ops.moe_permute(idx2.view(-1), E)
     act2 = torch.empty(T2 * k, Hf, dtype=torch.bfloat16, device="cuda")
     y2 = torch.empty(T2 * k, D, device="cuda")
-    us = event_time(lambda i: ops.moe_experts(x2, perm2, gates2, *esets[i % 2], act=act2, y=y2),
-                    max(3, iters // 10))
-    mfma("moe_prefill_experts", us, 2 * T2 * k * (D * 2 * Hf + Hf * D),
+    t = event_time(lambda i: ops.moe_experts(x2, perm2, gates2, *esets[i % 2], act=act2, y=y2),
+                   it_mfma)
+    mfma("moe_prefill_experts", t, 2 * T2 * k * (D * 2 * Hf + Hf * D),
          f"C2 grouped GEMMs only: {T2 * k} routes, gate_up+SwiGLU then down, 2 weight sets")
     del x2, esets, act2, y2
     # dense prefill projection: the C5 GDN input projection over 4096 tokens
@@ -318,18 +380,18 @@ def kernel_table(cfg, B, gen, iters):
     wps = [ops.pack_weights((torch.randn(nprj, D, device="cuda", generator=gen) * 0.02).bfloat16())
            for _ in range(2)]
     po = torch.empty(4096, nprj, device="cuda")
-    us = event_time(lambda i: ops.linear(xs, wps[i % 2], out=po, epilogue=ops.EPI_STORE_F32,
-                                         layout=ops.LAYOUT_PACKED), max(3, iters // 5))
-    mfma("dense_prefill_gemm", us, 2 * 4096 * nprj * D,
+    t = event_time(lambda i: ops.linear(xs, wps[i % 2], out=po, epilogue=ops.EPI_STORE_F32,
+                                        layout=ops.LAYOUT_PACKED), it_mfma)
+    mfma("dense_prefill_gemm", t, 2 * 4096 * nprj * D,
          f"C5 GDN projection over 4096 tokens: M=4096, N={nprj}, K={D}, packed weights")
     del xs, wps, po
     # attention prefill (C3)
     Bq, Tq, Hq, hq, Wq = 4, 8192, 16, 64, 512
     qkv = [torch.randn(Bq, Tq, Hq, hq, device="cuda", generator=gen).bfloat16() for _ in range(3)]
     ao = torch.empty_like(qkv[0])
-    us = event_time(lambda i: ops.banded_attn_prefill(*qkv, Wq, out=ao), max(3, iters // 5))
-    pairs = sum(min(t + 1, Wq) for t in range(Tq))
-    mfma("attn_prefill", us, 4 * Bq * Hq * hq * pairs,
+    t = event_time(lambda i: ops.banded_attn_prefill(*qkv, Wq, out=ao), it_mfma)
+    pairs = sum(min(t_ + 1, Wq) for t_ in range(Tq))
+    mfma("attn_prefill", t, 4 * Bq * Hq * hq * pairs,
          f"C3: B={Bq}, T={Tq}, H={Hq}, hd={hq}, window={Wq}")
     del qkv, ao
     # GDN prefill (C4): chunked gated delta rule
@@ -342,11 +404,11 @@ def kernel_table(cfg, B, gen, iters):
     gS = torch.zeros(Bg, Hg4, d4, d4, device="cuda")
     go4 = torch.empty(Bg, Tg, Hg4, d4, dtype=torch.bfloat16, device="cuda")
     nb = int(_lib.load().llmy_gdn_prefill_workspace_bytes(Bg, Tg, Hg4, d4, d4))
-    ws = torch.empty(nb, dtype=torch.uint8, device="cuda")
-    us = event_time(lambda i: ops.gdn_prefill(gq, gk, gv, gb, gg, gS, out=go4, workspace=ws), 3,
-                    warm=1)
+    ws = torch.empty(max(nb, 1), dtype=torch.uint8, device="cuda")
+    t = event_time(lambda i: ops.gdn_prefill(gq, gk, gv, gb, gg, gS, out=go4, workspace=ws), 10,
+                   warm=2)
     bytes4 = 4 * Bg * Tg * Hg4 * d4 * 2 + 2 * Bg * Tg * Hg4 * 4 + 2 * Bg * Hg4 * d4 * d4 * 4
-    hbm("gdn_prefill", us, bytes4, f"C4: B={Bg}, T={Tg}, H={Hg4}, dk=dv={d4}, chunk 64")
+    hbm("gdn_prefill", t, bytes4, f"C4: B={Bg}, T={Tg}, H={Hg4}, dk=dv={d4}, chunk 64")
     del gq, gk, gv, go4, ws
     torch.cuda.empty_cache()
     return rows
@@ -397,23 +459,37 @@ def engine_prefill(cfg, gen, Bp=8, Tp=512, iters=5):
             "flops_per_token": round(model_flops_per_token(cfg, Tp))}
 
 
-def cpu_baseline(B, seconds_budget=10.0):
-    """Oracle (fp32 torch on the host) on a bounded sample: decode steps of a
-    C5-shaped slice — one attention + one GDN layer with their MoEs, one loop,
-    batch 64, 2048-token window — repeated for about ``seconds_budget`` and
-    scaled to the full step (12 such layer pairs plus one LM head and the
-    sampling, which the sample's own step includes once)."""
+def _cpu_model_name() -> str:
+    """The host CPU's model name, as ``lscpu`` prints it (from /proc/cpuinfo)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.lower().startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+    return platform.processor() or "unknown"
+
+
+def cpu_baseline(B):
+    """The oracle (fp32 PyTorch restatement of the reference math) on the host
+    cores, on the full C5 decode step at batch B: all 12 layers looped twice,
+    2048-token windows pre-filled, the LM head and the top-p draw.  One warmup
+    step, then the median of three timed steps (wall clock).  Needs about
+    22 GB of host memory (fp32 weights 7.6 GB, KV caches 12.9 GB)."""
     import torch
-    from dataclasses import replace
-    from hybrid_llm_amd.config import C5, alternating, init_weights
+    from hybrid_llm_amd.config import C5, init_weights
     from oracle.model import HybridOracle
     from oracle.sampling import top_p_sample
 
     threads = len(os.sched_getaffinity(0))
     torch.set_num_threads(threads)
-    cfg = replace(C5, layer_kinds=alternating(2), num_loops=1)
+    cfg = C5
+    t_setup = time.perf_counter()
     w = init_weights(cfg, seed=0)
     ora = HybridOracle(cfg, w, act_bf16=False)
+    del w
     st = ora.new_state(B)
     g = torch.Generator().manual_seed(2)
     st["pos"].fill_(cfg.window)
@@ -421,34 +497,29 @@ def cpu_baseline(B, seconds_budget=10.0):
         if key == "pos":
             continue
         for name, t in s.items():
-            t.normal_(0.0, 0.1 if name == "S" else 1.0, generator=g)
+            if t.numel():
+                t.normal_(0.0, 0.1 if name == "S" else 1.0, generator=g)
     tokens = torch.randint(0, cfg.vocab, (B,), generator=g)
     u = torch.rand(B, generator=g)
+    t_setup = time.perf_counter() - t_setup
 
     def step():
+        t0 = time.perf_counter()
         logits = ora.step(tokens, st)
         top_p_sample(logits, SAMPLING[0], SAMPLING[1], u, top_k=SAMPLING[2])
+        return time.perf_counter() - t0
 
     step()  # warmup
-    n, t0 = 0, time.perf_counter()
-    while True:
-        step()
-        n += 1
-        t_pair = (time.perf_counter() - t0) / n
-        if time.perf_counter() - t0 >= seconds_budget:
-            break
-    # the sample's step includes one LM head; the full step has 12 pairs + 1 head
-    hf = torch.randn(B, cfg.d_model, generator=g)
-    m, t0 = 5, time.perf_counter()
-    for _ in range(m):
-        _ = hf @ ora.w["embed"].t()
-    t_head = (time.perf_counter() - t0) / m
-    t_full = 12 * (t_pair - t_head) + t_head
-    return {"value": B / t_full, "unit": "tok/s", "cores": threads, "kind": "port",
-            "sample": (f"oracle fp32 decode steps of a C5 slice (1 attention + 1 GDN layer, each"
-                       f" with its 24-expert MoE, batch {B}, window 2048, LM head, top-p draw):"
-                       f" {n} steps in {n * t_pair:.1f}s, {t_pair * 1e3:.0f} ms/step; scaled to"
-                       f" 12 layer pairs + one LM head")}
+    times = sorted(step() for _ in range(3))
+    t_step = times[1]
+    del ora, st
+    return {"value": B / t_step, "unit": "tok/s", "cores": threads, "kind": "port",
+            "cpu_model": _cpu_model_name(), "torch": torch.__version__,
+            "step_s": [round(x, 3) for x in times],
+            "sample": (f"oracle fp32 decode step of the full C5 model (12 layers x 2 loops, "
+                       f"24-expert MoEs, batch {B}, 2048-token windows, LM head, top-p draw): "
+                       f"1 warmup + median of 3 steps = {t_step:.2f} s/step on {threads} threads "
+                       f"(setup {t_setup:.0f} s untimed)")}
 
 
 def main():
@@ -488,24 +559,36 @@ def main():
 
     for _ in range(args.warmup):
         eng.graph.replay()
+    # the timed region: exactly `steps` replays between two synchronisations;
+    # a pair of HIP events on the replay stream brackets each one as well
+    stream = torch.cuda.current_stream()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(args.steps)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for _ in range(args.steps):
+    for a, b in ev:
+        a.record(stream)
         eng.graph.replay()
+        b.record(stream)
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
     ms = dt * 1e3 / args.steps
     value = B / (ms / 1e3)
-    print(f"[bench] {ms:.3f} ms/step, {value:.0f} tok/s", file=sys.stderr, flush=True)
+    ev_ms = sorted(a.elapsed_time(b) for a, b in ev)
+    mid = len(ev_ms) // 2
+    ev_median = ev_ms[mid] if len(ev_ms) % 2 else 0.5 * (ev_ms[mid - 1] + ev_ms[mid])
+    print(f"[bench] {ms:.3f} ms/step, {value:.0f} tok/s (event median {ev_median:.3f} ms)",
+          file=sys.stderr, flush=True)
 
     del eng
     torch.cuda.empty_cache()
-    us, bytes_ = time_attn_decode(cfg, B, args.kernel_iters, gen)
+    (us, us_med), bytes_ = time_attn_decode(cfg, B, args.kernel_iters, gen)
     achieved = bytes_ / (us * 1e-6) / 1e9
     roofline = {"kernel": "attn_decode_kernel<64>", "bound": "hbm", "achieved": round(achieved, 1),
                 "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                 "traffic": None if traffic is None else round(traffic["bytes"]),
-                "avg_us": round(us, 2), "bytes_per_launch": bytes_}
+                "avg_us": round(us, 2), "median_us": round(us_med, 2),
+                "bytes_per_launch": bytes_}
     if traffic is not None:
         roofline["traffic_detail"] = {k: (round(v, 4) if "factor" in k else round(v))
                                       for k, v in traffic.items() if k != "bytes"}
@@ -515,8 +598,11 @@ def main():
     if not args.no_kernels:
         kernels = kernel_table(cfg, B, gen, args.kernel_iters)
         for name, r in kernels.items():
-            print(f"[bench] {name}: {r['avg_us']} us, {r['achieved']} {r['unit']} "
-                  f"({100 * r['frac']:.1f}%)", file=sys.stderr, flush=True)
+            if "frac" in r:
+                print(f"[bench] {name}: {r['avg_us']} us, {r['achieved']} {r['unit']} "
+                      f"({100 * r['frac']:.1f}%)", file=sys.stderr, flush=True)
+            else:
+                print(f"[bench] {name}: {r['avg_us']} us", file=sys.stderr, flush=True)
         kernels["engine_prefill"] = engine_prefill(cfg, gen)
         r = kernels["engine_prefill"]
         print(f"[bench] engine_prefill: {r['ms']} ms, {r['tok_s']:.0f} tok/s, "
@@ -537,7 +623,8 @@ def main():
 
     line = {"metric": METRIC,
             "value": round(value, 1), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
-            "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True,
+            "warmup": args.warmup, "ms_per_step": round(ms, 4),
+            "ms_per_step_event_median": round(ev_median, 4), "higher_is_better": True,
             "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
             "config": {"workload": "C5 full hybrid-MoE decode step, bs64 (greedy + top-p draw)",
                        "d_model": cfg.d_model, "layers": cfg.n_layers, "loops": cfg.num_loops,

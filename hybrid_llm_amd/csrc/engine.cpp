@@ -863,7 +863,9 @@ void prefill(Model& m, State& s, const int32_t* tokens, int T, bool tokens_on_de
   check_call(llmy_embed_norm_bf16(b.tokens, m.embed, m.layers[0].mix_norm, b.x, b.h, R, D, c.vocab,
                                   c.eps, st_),
              "llmy_embed_norm_bf16");
-  const int loops = c.num_loops;
+  // the loop count set by llmy_set_num_loops (model_prefill runs cfg.num_loops,
+  // which llmy_set_num_loops overwrites: llmy_cuda/src/model.cpp:1964, llmy.cpp:66-69)
+  const int loops = m.loops;
   const int Hhd = c.attn_heads * c.attn_head_dim;
   for (int loop = 0; loop < loops; ++loop) {
     for (int l = 0; l < n; ++l) {
@@ -1063,7 +1065,9 @@ int32_t llmy_decode_batch(llmy_model* m, llmy_state* s, const int32_t* tokens,
   return guarded([&] {
     Model& mm = *as_model(m);
     State& st = *as_state(s);
-    const int loops = num_loops <= 0 ? mm.loops : std::min<int32_t>(num_loops, mm.cfg.num_loops);
+    // an explicit count is capped at the set one (model.cpp:1824-1825 caps at
+    // cfg.num_loops, which llmy_set_num_loops overwrites)
+    const int loops = num_loops <= 0 ? mm.loops : std::min<int32_t>(num_loops, mm.loops);
     if (positions)
       check_hip(hipMemcpy(st.hpos.data(), positions, sizeof(int32_t) * st.B, hipMemcpyDefault),
                 "positions");
@@ -1074,9 +1078,11 @@ int32_t llmy_decode_batch(llmy_model* m, llmy_state* s, const int32_t* tokens,
                              hipMemcpyHostToDevice, st.stream),
               "positions");
     run_decode(mm, st, loops);
-    for (int32_t& p : st.hpos) ++p;  // the next token's position: one past this one
     if (logits_out) copy_logits_out(st, logits_out);
     check_hip(hipStreamSynchronize(st.stream), "decode");
+    // the next token's position: one past this one (changed only after the
+    // stream has drained, so the pageable source of the copy above is stable)
+    for (int32_t& p : st.hpos) ++p;
   });
 }
 

@@ -66,6 +66,38 @@ def top_p_sample(logits: torch.Tensor, temperature: float, top_p: float, u: torc
     return (out, margin) if return_margin else out
 
 
+def top_p_error_bound(logits: torch.Tensor, temperature: float, top_k: int = 0) -> np.ndarray:
+    """Per row, a bound on how far the cumulative probabilities of an fp32
+    implementation of top_p_sample can lie from its fp64 ones.
+
+    An fp32 implementation forms each exponent a_i = (x_i - max) / T with a
+    few roundings (the reciprocal temperature, the difference and the
+    product: relative error <= 4 * 2^-24 of |a_i|, in part common to every
+    term) and exponentiates it with <= 1 ulp error (2^-23), so each
+    unnormalised probability carries a
+    relative error delta_i <= 2^-23 (1 + 2 |a_i|).  With the sums taken
+    exactly (fixed point) or in fp64, a ratio of two partial sums of such
+    terms (a cumulative probability of the kept set) then moves by at most
+    2 sum_i p_i |delta_i| = 2^-22 (1 + 2 E_p|a|), p the fp64 softmax over
+    the top-k set; one more 2^-22 covers the fp32 products that place the
+    thresholds (top_p and u times a total).  This follows the fp32 arithmetic
+    the reference itself does (logits / temperature and the softmax in fp32:
+    sample_standalone.py:5611-5636).
+    """
+    x = logits.detach().double().cpu().numpy() / float(temperature)
+    rows, V = x.shape
+    out = np.empty(rows)
+    for r in range(rows):
+        v = np.sort(x[r])[::-1]
+        if top_k > 0:
+            v = v[:top_k]
+        a = v - v[0]
+        p = np.exp(a)
+        p /= p.sum()
+        out[r] = 2.0 ** -22 * (2.0 + 2.0 * float(np.sum(p * np.abs(a))))
+    return out
+
+
 def repetition_penalty(logits: torch.Tensor, recent, penalty: float) -> torch.Tensor:
     """sample_standalone.py:5601-5605: each distinct id of recent[r] (ids outside
     [0, V) ignored) has its logit divided by penalty if > 0, else multiplied.

@@ -77,8 +77,15 @@ def test_c1_prompt_and_greedy_decode():
 
 
 def test_c1_unforced_fp32_reference_agreement():
-    """Against the plain fp32 reference (no bf16 emulation, own routing):
-    report teacher-forced logits agreement and greedy agreement."""
+    """Against the plain fp32 reference (no bf16 emulation, its own routing):
+    teacher-forced logits over the 64-token prompt, then 32 greedy tokens
+    where the engine's token must be the reference's argmax at every step
+    whose reference top-2 gap exceeds twice the step's largest logit
+    difference.  The logits differ by the bf16 rounding of the activations
+    (the engine's, and the reference's own bf16 run's, storage precision),
+    so the rel-L2 bound here is that of a bf16 model against fp32, 5e-2;
+    the stated 1e-2 tolerance is checked against the bf16-emulating oracle
+    in test_c1_prompt_and_greedy_decode."""
     w = init_weights(C1, seed=0)
     prompt = torch.randint(0, C1.vocab, (64,), generator=torch.Generator().manual_seed(1))
     ref = HybridOracle(C1, w, act_bf16=False)
@@ -89,10 +96,22 @@ def test_c1_unforced_fp32_reference_agreement():
         lr = ref.step([int(prompt[t])], st)
         lg = eng.step(prompt[t:t + 1].to(torch.int32).cuda())
         errs.append(rel_l2(lg, lr))
-    agree = int(eng.buf["next"][0]) == int(lr[0].argmax())
+    agree = checked = 0
+    for _ in range(32):                      # free-running greedy, the engine's tokens
+        nxt = int(eng.buf["next"][0])
+        diff = float((lg.cpu()[0] - lr[0]).abs().max())
+        top2 = torch.topk(lr[0], 2).values
+        if float(top2[0] - top2[1]) > 2 * diff:
+            checked += 1
+            assert nxt == int(lr[0].argmax()), (checked, nxt, int(lr[0].argmax()))
+        agree += int(nxt == int(lr[0].argmax()))
+        lr = ref.step([nxt], st)
+        lg = eng.step(torch.tensor([nxt], dtype=torch.int32).cuda())
+        errs.append(rel_l2(lg, lr))
     print(f"C1 vs fp32 reference: median rel-L2 {np.median(errs):.2e}, max {max(errs):.2e}, "
-          f"last-token greedy agree {agree}")
-    assert np.median(errs) < 0.1
+          f"greedy agree {agree}/32 ({checked} determined)")
+    assert np.median(errs) < 5e-2
+    assert checked >= 8
 
 
 def _c5_slice():

@@ -2,19 +2,19 @@
 
 The kernel sums probabilities exactly (integer fixed point) but computes each
 one in fp32, so its cumulative probabilities differ from the fp64 oracle's by
-a few 1e-7.  Rows whose oracle decision margin exceeds EPS must pick exactly
-the oracle's id; the rest must pick a neighbour (one position away in the
-sorted order) of it.
+at most oracle.sampling.top_p_error_bound (a per-row fp32 rounding bound,
+about 1e-6).  Rows whose oracle decision margin exceeds that bound must pick
+exactly the oracle's id; the rest must pick a neighbour (one position away in
+the sorted order) of it.
 """
 import numpy as np
 import pytest
 import torch
 
-from oracle.sampling import repetition_penalty, top_p_sample
+from oracle.sampling import repetition_penalty, top_p_error_bound, top_p_sample
 
 pytestmark = pytest.mark.gpu
 
-EPS = 4e-6  # bound on the kernel's cumulative-probability error (fp32 exp of |arg| <= ~20)
 P90 = float(np.float32(0.9))  # the value the fp32 ABI argument carries
 
 
@@ -33,7 +33,7 @@ def _order_pos(logits_row: np.ndarray, ids: np.ndarray) -> np.ndarray:
 def _check(logits, T, p, u, top_k, min_exact=0.6):
     got = ops().sample_top_p(logits.cuda(), T, p, u.cuda(), top_k=top_k).cpu().numpy()
     ref, margin = top_p_sample(logits, T, p, u, top_k=top_k, return_margin=True)
-    safe = margin > EPS
+    safe = margin > top_p_error_bound(logits, T, top_k)
     assert safe.mean() >= min_exact, safe.mean()
     bad = np.nonzero(safe & (got != ref))[0]
     assert bad.size == 0, (bad[:8], got[bad[:8]], ref[bad[:8]], margin[bad[:8]])
@@ -48,12 +48,13 @@ def _check(logits, T, p, u, top_k, min_exact=0.6):
 @pytest.mark.parametrize("top_k", [0, 50])
 def test_top_p_c5(scale, top_k):
     """C5 sampling shape: logits [64, 32000] fp32, T=0.8, p=0.9, one uniform per row.
-    With near-flat logits each token holds ~3e-5 of the mass, so u or p often
-    lands within EPS of a step and fewer rows qualify for the exact check."""
+    With near-flat logits each token holds ~3e-5 of the mass, so u or p
+    lands within the error bound of a step more often and fewer rows qualify
+    for the exact check (about 70% here)."""
     g = torch.Generator().manual_seed(int(scale * 10) + top_k)
     logits = torch.randn(64, 32000, generator=g) * scale
     u = torch.rand(64, generator=g)
-    _check(logits, 0.8, P90, u, top_k, min_exact=0.25 if (scale < 1 and top_k == 0) else 0.6)
+    _check(logits, 0.8, P90, u, top_k, min_exact=0.6 if (scale < 1 and top_k == 0) else 0.75)
 
 
 def test_top_p_ties_resolve_by_id():
