@@ -476,6 +476,10 @@ int32_t moe_gemm_prefill(const uint16_t* x, const int32_t* offsets, const int32_
                          const float* gates, const uint16_t* w_gate_up, const uint16_t* w_down,
                          uint16_t* act, float* y, int T, int D, int H, int E, int k, bool packed,
                          hipStream_t s);
+int32_t moe_grouped_prefill(const uint16_t* x, const int32_t* offsets, const int32_t* sorted_routes,
+                            const float* gates, const uint16_t* w_gate_up, const uint16_t* w_down,
+                            uint16_t* act, float* y, int T, int D, int H, int E, int k, bool packed,
+                            hipStream_t s);
 // The same tiles as a dense GEMM with the epilogues above (moe_gemm.hip).
 int32_t dense_gemm_mfma(const uint16_t* x, const uint16_t* w, void* out, const float* aux,
                         int M, int N, int K, int epi, bool packed, hipStream_t s);
@@ -586,9 +590,14 @@ extern "C" int32_t llmy_moe_experts_bf16(const llmy_bf16* x, const int32_t* offs
     if (st != 0) return st;
     return launch_ws<kMoeDown, kMoeDirect, 1, 1, 4>(b, E, packed, s);
   }
-  // Prefill: tiled MFMA grouped GEMMs (moe_gemm.hip).
+  // Prefill: grouped MFMA GEMMs (moe_grouped.hip).
+#ifdef LLMY_OLD_GROUPED
   return moe_gemm_prefill(x, offsets, sorted_routes, gates, w_gate_up, w_down, act, y, T, D, H,
                           E, k, packed, s);
+#else
+  return moe_grouped_prefill(x, offsets, sorted_routes, gates, w_gate_up, w_down, act, y, T, D,
+                             H, E, k, packed, s);
+#endif
 }
 
 extern "C" int32_t llmy_moe_combine(const float* y, const int32_t* route_pos, void* out,

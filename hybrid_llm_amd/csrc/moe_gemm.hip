@@ -417,6 +417,10 @@ __global__ __launch_bounds__(kThreads, OCC) void tile_gemm_kernel(TileArgs a) {
     if (kt + 1 < nk) TILE_READ(pa, pb, nxt, 0);
     FENCE();
     TILE_MMA(qa, qb);
+    FENCE();
+    // the next tile's first reads land before the loop edge: the compiler
+    // knows nothing of asm reads in flight and may move their registers
+    TILE_SETTLE(pa, pb, 0);
     stage = nxt;
   }
 #undef FENCE

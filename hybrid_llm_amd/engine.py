@@ -184,15 +184,23 @@ class HybridDecoder:
             self.buf["proj_parts"] = torch.zeros(D // 256, B, nproj, dtype=f32, device=dev)
         self._pending: tuple | None = None
         # Optional record of every MoE application's expert ids (verification
-        # aid: lets a checker replay the kernel's discrete routing decisions).
+        # aid: lets a checker replay the kernel's discrete routing decisions),
+        # and of the residual stream after each application.
         self.route_log: torch.Tensor | None = None
+        self.x_log: torch.Tensor | None = None
         # The same for prefill: one [B*T, k] id tensor per MoE application.
         self.route_log_seq: list | None = None
 
-    def enable_route_log(self) -> None:
+    def enable_route_log(self, residuals: bool = False) -> None:
+        """Record every MoE application's expert ids in ``route_log`` [apps, B, k]
+        and, with ``residuals``, the residual stream after each application in
+        ``x_log`` [apps, B, D] (verification aids: a checker can replay the
+        discrete routing and check each application from the same input)."""
         n_apps = self.cfg.num_loops * self.cfg.n_layers
         self.route_log = torch.zeros(n_apps, self.B, self.cfg.top_k, dtype=torch.int32,
                                      device=self.dev)
+        self.x_log = (torch.zeros(n_apps, self.B, self.cfg.d_model, dtype=torch.float32,
+                                  device=self.dev) if residuals else None)
         self._app = 0
 
     # ------------------------------------------------------------------ blocks
@@ -281,7 +289,6 @@ class HybridDecoder:
                       b["sorted_routes"].data_ptr(), b["route_pos"].data_ptr(), s)
         if self.route_log is not None:
             self.route_log[self._app].copy_(b["idx"])
-            self._app = (self._app + 1) % self.route_log.shape[0]
         if self.fused_route:
             ops.moe_experts_routed(b["h"], idx, gates, w[p + "w_gate_up"],
                                    w[p + "w_down"], act=b["act"], y=b["y"],
@@ -292,6 +299,10 @@ class HybridDecoder:
                             act=b["act"], y=b["y"], layout=ops.LAYOUT_PACKED)
             route_pos = b["route_pos"]
         ops.moe_combine_norm(b["y"], route_pos, b["x"], b["h"], next_norm, kx, cfg.eps)
+        if self.route_log is not None:
+            if self.x_log is not None:
+                self.x_log[self._app].copy_(b["x"])
+            self._app = (self._app + 1) % self.route_log.shape[0]
 
     # ------------------------------------------------------------------ step
     def _step_body(self) -> None:

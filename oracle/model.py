@@ -147,26 +147,40 @@ class HybridOracle:
             self.route_total += 1
 
     # ---- step ------------------------------------------------------------
+    def embed(self, tokens) -> torch.Tensor:
+        """The residual stream's start: embedding rows (model.py:386)."""
+        tokens = torch.as_tensor(np.asarray(tokens), dtype=torch.long).view(-1)
+        return self.w["embed"][tokens].clone()
+
+    def apply(self, l: int, x: torch.Tensor, s: dict, pos: torch.Tensor) -> torch.Tensor:
+        """One application of layer l (mixer block then MoE block, each a
+        pre-norm residual branch: model.py:119-126,162-264) to the residual x,
+        updating that (loop, layer)'s state s in place; returns the new x."""
+        cfg, w, rnd = self.cfg, self.w, self.rnd
+        h = rnd(rmsnorm(x, w[f"L{l}.mix_norm"], cfg.eps))
+        if cfg.layer_kinds[l] == "attn":
+            x = x + self._attn(l, h, s, pos)
+        else:
+            x = x + self._gdn(l, h, s)
+        h2 = rnd(rmsnorm(x, w[f"L{l}.ffn_norm"], cfg.eps))
+        return x + self._moe(l, h2, s)
+
+    def head(self, x: torch.Tensor) -> torch.Tensor:
+        """Final RMSNorm and the tied LM head (model.py:705): fp32 logits."""
+        hf = self.rnd(rmsnorm(x, self.w["final_norm"], self.cfg.eps))
+        return hf @ self.w["embed"].t()
+
     def step(self, tokens, st: dict, num_loops: int | None = None) -> torch.Tensor:
         """Decode one token per sequence; returns fp32 logits [B, V]."""
-        cfg, w, rnd = self.cfg, self.w, self.rnd
-        tokens = torch.as_tensor(np.asarray(tokens), dtype=torch.long).view(-1)
+        cfg = self.cfg
         pos = st["pos"].clone()
-        x = w["embed"][tokens].clone()
+        x = self.embed(tokens)
         loops = cfg.num_loops if not num_loops else num_loops
         for loop in range(loops):
-            for l, kind in enumerate(cfg.layer_kinds):
-                s = st[(loop, l)]
-                h = rnd(rmsnorm(x, w[f"L{l}.mix_norm"], cfg.eps))
-                if kind == "attn":
-                    x = x + self._attn(l, h, s, pos)
-                else:
-                    x = x + self._gdn(l, h, s)
-                h2 = rnd(rmsnorm(x, w[f"L{l}.ffn_norm"], cfg.eps))
-                x = x + self._moe(l, h2, s)
+            for l in range(cfg.n_layers):
+                x = self.apply(l, x, st[(loop, l)], pos)
         st["pos"] = pos + 1
-        hf = rnd(rmsnorm(x, w["final_norm"], cfg.eps))
-        return hf @ w["embed"].t()
+        return self.head(x)
 
     def prefill(self, tokens, st: dict) -> torch.Tensor:
         """Token-by-token prefill of a [B, T] prompt; returns logits [B, T, V]."""

@@ -91,6 +91,10 @@ def top_p_error_bound(logits: torch.Tensor, temperature: float, top_k: int = 0) 
         v = np.sort(x[r])[::-1]
         if top_k > 0:
             v = v[:top_k]
+        v = v[np.isfinite(v)]          # -inf (masked) ids carry no mass
+        if v.size == 0:
+            out[r] = 2.0 ** -21
+            continue
         a = v - v[0]
         p = np.exp(a)
         p /= p.sum()
