@@ -39,6 +39,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
                                           _I, _F, _P]),
     "llmy_gdn_prefill_workspace_bytes": (C.c_int64, [_I, _I, _I, _I, _I]),
     "llmy_gdn_prefill_bf16": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I, _I, _I, _I, _I, _P]),
+    "llmy_gdn_prefill_bf16_noalloc": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),
     "llmy_gdn_step_bf16": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P]),
     "llmy_gdn_step_fused_f32": (_I, [_P, _I64, _I, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I,
                                      _I, _I, _I, _P]),

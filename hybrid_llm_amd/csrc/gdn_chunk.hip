@@ -27,6 +27,8 @@
 //
 // MFMA v_mfma_f32_16x16x32_bf16 fragments: A lane l holds A[l%16][8(l/16)+j],
 // B lane l holds B[8(l/16)+j][l%16], D lane l holds D[4(l/16)+i][l%16].
+#include <mutex>
+
 #include "common.hpp"
 #include "abi_util.hpp"
 
@@ -635,27 +637,21 @@ extern "C" int64_t llmy_gdn_prefill_workspace_bytes(int32_t B, int32_t T, int32_
   return chunks * kC * (static_cast<long long>(dk) + dv + kC + 1) * static_cast<long long>(sizeof(float));
 }
 
-extern "C" int32_t llmy_gdn_prefill_bf16(const llmy_bf16* q, const llmy_bf16* k,
-                                         const llmy_bf16* v, const float* beta, const float* g,
-                                         float* state, llmy_bf16* out, void* workspace,
-                                         int64_t workspace_bytes, int32_t B, int32_t T,
-                                         int32_t H, int32_t dk, int32_t dv, void* stream) {
-  LLMY_REQUIRE(B >= 0 && T >= 0 && H > 0);
-  LLMY_REQUIRE((dk == 64 && dv == 64) || (dk == 128 && dv == 128));
-  if (B == 0 || T == 0) return 0;
-  LLMY_REQUIRE(q && k && v && beta && g && state && out && workspace);
-  LLMY_REQUIRE(workspace_bytes >= llmy_gdn_prefill_workspace_bytes(B, T, H, dk, dv));
-  LLMY_REQUIRE(aligned(q, 16) && aligned(k, 16) && aligned(v, 16) && aligned(state, 16) &&
-               aligned(workspace, 16));
+namespace {
+
+// The prep + scan launches over a caller-sized workspace (validated by the
+// entry points below).
+int32_t gdn_prefill_launch(const llmy_bf16* q, const llmy_bf16* k, const llmy_bf16* v,
+                           const float* beta, const float* g, float* state, llmy_bf16* out,
+                           void* workspace, int B, int T, int H, int dk, hipStream_t s) {
   const int NC = (T + kC - 1) / kC;
   const long long chunks = static_cast<long long>(B) * H * NC;
-  LLMY_REQUIRE(chunks < (1ll << 31));
+  const int dv = dk;
   // workspace: W as (hi, lo) bf16 planes, U0 fp32, A as (hi, lo) bf16 planes, cum fp32
   uint16_t* W = static_cast<uint16_t*>(workspace);
   float* U0 = reinterpret_cast<float*>(W + chunks * kC * dk * 2);
   uint16_t* A = reinterpret_cast<uint16_t*>(U0 + chunks * kC * dv);
   float* cum = reinterpret_cast<float*>(A + chunks * kC * kC * 2);
-  const hipStream_t s = as_stream(stream);
   if (dk == 64) {
     hipLaunchKernelGGL((gdn_chunk_prep_kernel<64, 64>), dim3(static_cast<unsigned>(chunks)),
                        dim3(256), 0, s, q, k, v, beta, g, W, U0, A, cum, T, H, NC);
@@ -674,4 +670,72 @@ extern "C" int32_t llmy_gdn_prefill_bf16(const llmy_bf16* q, const llmy_bf16* k,
                        dim3(kScanThreads), 0, s, q, k, W, U0, A, cum, state, out, T, H, NC, units);
   }
   return launch_status();
+}
+
+// Workspace of the no-allocation entry point: a fixed device array, one copy
+// per GPU (each device holds it from module load until the process ends).
+// Host code never passes `scratch` itself (in host code the name is a
+// stand-in, not a device address): the per-device address comes from
+// hipGetSymbolAddress, once per device, with that device current.
+constexpr long long kStaticWorkspaceBytes = 64ll << 20;
+__device__ __align__(256) unsigned char scratch[kStaticWorkspaceBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The current device's copy of `scratch` (null on failure).
+void* static_workspace() {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) {
+      (void)hipGetLastError();
+      return nullptr;
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  return g_scratch_ptr[dev];
+}
+
+}  // namespace
+
+extern "C" int32_t llmy_gdn_prefill_bf16(const llmy_bf16* q, const llmy_bf16* k,
+                                         const llmy_bf16* v, const float* beta, const float* g,
+                                         float* state, llmy_bf16* out, void* workspace,
+                                         int64_t workspace_bytes, int32_t B, int32_t T,
+                                         int32_t H, int32_t dk, int32_t dv, void* stream) {
+  LLMY_REQUIRE(B >= 0 && T >= 0 && H > 0);
+  LLMY_REQUIRE((dk == 64 && dv == 64) || (dk == 128 && dv == 128));
+  if (B == 0 || T == 0) return 0;
+  LLMY_REQUIRE(q && k && v && beta && g && state && out && workspace);
+  LLMY_REQUIRE(workspace_bytes >= llmy_gdn_prefill_workspace_bytes(B, T, H, dk, dv));
+  LLMY_REQUIRE(aligned(q, 16) && aligned(k, 16) && aligned(v, 16) && aligned(state, 16) &&
+               aligned(workspace, 16));
+  const long long chunks = static_cast<long long>(B) * H * ((T + kC - 1) / kC);
+  LLMY_REQUIRE(chunks < (1ll << 31));
+  return gdn_prefill_launch(q, k, v, beta, g, state, out, workspace, B, T, H, dk,
+                            as_stream(stream));
+}
+
+extern "C" int32_t llmy_gdn_prefill_bf16_noalloc(const llmy_bf16* q, const llmy_bf16* k,
+                                                 const llmy_bf16* v, const float* beta,
+                                                 const float* g, float* state, llmy_bf16* out,
+                                                 int32_t B, int32_t T, int32_t H, int32_t dk,
+                                                 int32_t dv, void* stream) {
+  LLMY_REQUIRE(B >= 0 && T >= 0 && H > 0);
+  LLMY_REQUIRE((dk == 64 && dv == 64) || (dk == 128 && dv == 128));
+  if (B == 0 || T == 0) return 0;
+  LLMY_REQUIRE(q && k && v && beta && g && state && out);
+  LLMY_REQUIRE(aligned(q, 16) && aligned(k, 16) && aligned(v, 16) && aligned(state, 16));
+  // beyond the fixed workspace: a distinct status, before anything runs
+  if (llmy_gdn_prefill_workspace_bytes(B, T, H, dk, dv) > kStaticWorkspaceBytes)
+    return static_cast<int32_t>(hipErrorOutOfMemory);
+  void* ws = static_workspace();
+  if (!ws) return static_cast<int32_t>(hipErrorInvalidDevicePointer);
+  // every workspace byte the scan reads is written by this call's prep kernel
+  // first, so what an earlier call left there does not matter
+  return gdn_prefill_launch(q, k, v, beta, g, state, out, ws, B, T, H, dk, as_stream(stream));
 }

@@ -182,6 +182,21 @@ int32_t llmy_gdn_prefill_bf16(const llmy_bf16* q, const llmy_bf16* k, const llmy
                               int32_t B, int32_t T, int32_t H, int32_t dk, int32_t dv,
                               void* stream);
 
+/* No counterpart in the reference: llmy_gdn_prefill_bf16 for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  Same arguments, arithmetic and
+ * results, without the workspace pair: the library keeps a fixed 64 MiB
+ * workspace per GPU (a static device array, held from module load to process
+ * end), enough for llmy_gdn_prefill_workspace_bytes(B, T, H, dk, dv) <= 64 MiB
+ * (e.g. 1024 chunks of 64 tokens x heads at dk = dv = 64, 816 at 128).
+ * Larger sizes return hipErrorOutOfMemory (2) before anything runs.  Calls
+ * that overlap on one GPU (other streams, other threads) share that
+ * workspace and race; each call fully rewrites the part it reads. */
+int32_t llmy_gdn_prefill_bf16_noalloc(const llmy_bf16* q, const llmy_bf16* k,
+                                      const llmy_bf16* v, const float* beta, const float* g,
+                                      float* state, llmy_bf16* out, int32_t B, int32_t T,
+                                      int32_t H, int32_t dk, int32_t dv, void* stream);
+
 /* --- Gated delta rule, decode (model/layers/gated_deltanet.py:140-149) ---- */
 
 /* pred = k^T S; S <- g S + beta k (v - pred)^T (in place); out = (q^T S) * gate.

@@ -174,3 +174,16 @@ def test_context_router_entries_reject_bad_arguments(lib):
     shared = lib.llmy_moe_append_shared
     assert shared(FAKE, FAKE, FAKE, FAKE, 4, 2, 8, 0, None) == INVALID         # S = 0
     assert shared(FAKE, FAKE, FAKE, FAKE, 4, 0, 8, 2, None) == INVALID         # k = 0
+
+
+def test_gdn_prefill_noalloc_rejects_before_any_device_call(lib):
+    """Argument checks and the fixed-workspace limit run before the library
+    touches a device (so they answer here, without a GPU)."""
+    f = lib.llmy_gdn_prefill_bf16_noalloc
+    ptrs = [FAKE] * 7
+    assert f(*ptrs, 1, 64, 2, 96, 96, None) == INVALID                            # head size
+    assert f(None, *ptrs[1:], 1, 64, 2, 64, 64, None) == INVALID
+    assert f(*([None] * 7), 0, 64, 2, 64, 64, None) == 0                          # B = 0
+    # 832 chunks x 82 KB at dk = dv = 128: beyond the 64 MiB workspace
+    assert f(*ptrs, 1, 64 * 52, 16, 128, 128, None) == 2                         # hipErrorOutOfMemory
+    assert lib.llmy_gdn_prefill_workspace_bytes(1, 64 * 51, 16, 128, 128) <= 64 << 20
