@@ -58,6 +58,13 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
                                        _P]),
     "llmy_gdn_gate_bf16": (_I, [_P, _P, _I64, _I, _P, _I, _I, _P]),
     "llmy_gdn_conv_gate_prefill": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _P]),
+    "llmy_gdn_prefill_reset_bf16": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I, _I, _I,
+                                         _I, _I, _P]),
+    "llmy_gdn_step_reset_bf16": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P]),
+    "llmy_gdn_step_fused_reset_f32": (_I, [_P, _I64, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P,
+                                           _I, _I, _I, _I, _I, _I, _P]),
+    "llmy_gdn_conv_gate_prefill_reset": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _P]),
+    "llmy_zero_rows": (_I, [_P, _I64, _I, _P, _P]),
     # engine handles (the reference binding's argtypes, llmy_cuda/python/sample.py:110-170)
     "llmy_load": (_P, [C.c_char_p]),
     "llmy_free": (None, [_P]),
@@ -81,6 +88,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "llmy_prefill_batch": (_I, [_P, _P, _P, _I, _P]),
     "llmy_decode_batch": (_I, [_P, _P, _P, _P, _I, _P]),
     "llmy_greedy_tokens": (_I, [_P, _P]),
+    "llmy_state_reset_rows": (_I, [_P, _P]),
     "llmy_last_status": (_I, []),
     "llmy_last_error": (C.c_char_p, []),
     "llmy_checkpoint_describe": (_I, [C.c_char_p, C.c_char_p, _I64]),

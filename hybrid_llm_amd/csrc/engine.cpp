@@ -545,6 +545,7 @@ struct State {
   std::vector<LayerState> layers;  // index loop * n_layers + layer
   DeviceArena arena;
   int32_t* pos = nullptr;    // [B] device: absolute position of the next token
+  int32_t* reset_mask = nullptr;  // [B] device: rows of the last llmy_state_reset_rows
   float* logits = nullptr;   // [B, V]
   int32_t* next = nullptr;   // [B]
   Buffers step;              // decode: B rows
@@ -645,6 +646,7 @@ std::unique_ptr<State> new_state(Model* m, int B) {
   check_hip(hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking), "hipStreamCreate");
   s->hpos.assign(B, 0);
   s->pos = s->arena.zeros<int32_t>(B);
+  s->reset_mask = s->arena.zeros<int32_t>(B);
   s->logits = s->arena.zeros<float>(static_cast<size_t>(B) * c.vocab);
   s->next = s->arena.zeros<int32_t>(B);
   alloc_buffers(c, B, B, 1, s->step);
@@ -667,6 +669,34 @@ void reset_state(State& s) {
   check_hip(hipStreamSynchronize(s.stream), "reset");
   s.hpos.assign(s.B, 0);
   s.last_loops = 0;
+}
+
+// Rows b with mask[b] != 0 (host or device int32 [B]) start over: every
+// per-row state buffer is zeroed by a kernel (no memory set) and the next
+// position is 0 (recurrent_state.py:213-225, model.py:814-822).
+void reset_rows(State& s, const int32_t* mask) {
+  check_hip(hipMemcpyAsync(s.reset_mask, mask, sizeof(int32_t) * s.B, hipMemcpyDefault, s.stream),
+            "reset mask");
+  auto zero = [&](void* p, size_t bytes) {
+    if (p)
+      check_call(llmy_zero_rows(p, static_cast<int64_t>(bytes / s.B), s.B, s.reset_mask, s.stream),
+                 "llmy_zero_rows");
+  };
+  for (auto& L : s.layers) {
+    zero(L.k, L.k_bytes);
+    zero(L.v, L.k_bytes);
+    zero(L.S, L.s_bytes);
+    zero(L.hist, L.hist_bytes);
+    zero(L.ring, L.ring_bytes);
+  }
+  zero(s.pos, sizeof(int32_t) * s.B);
+  std::vector<int32_t> host(s.B);
+  check_hip(hipMemcpyAsync(host.data(), s.reset_mask, sizeof(int32_t) * s.B, hipMemcpyDeviceToHost,
+                           s.stream),
+            "reset mask");
+  check_hip(hipStreamSynchronize(s.stream), "reset rows");
+  for (int b = 0; b < s.B; ++b)
+    if (host[b] != 0) s.hpos[b] = 0;
 }
 
 // ------------------------------------------------------------------ forward
@@ -1084,6 +1114,14 @@ int32_t llmy_decode_batch(llmy_model* m, llmy_state* s, const int32_t* tokens,
     // stream has drained, so the pageable source of the copy above is stable)
     for (int32_t& p : st.hpos) ++p;
   });
+}
+
+int32_t llmy_state_reset_rows(llmy_state* s, const int32_t* mask) {
+  if (!s || !mask) {
+    set_error(1, "null state or mask");
+    return 1;
+  }
+  return guarded([&] { reset_rows(*as_state(s), mask); });
 }
 
 int32_t llmy_greedy_tokens(const llmy_state* s, int32_t* out) {

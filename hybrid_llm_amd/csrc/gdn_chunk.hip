@@ -25,6 +25,17 @@
 // hi*hi + hi*lo + lo*hi (relative error about 2^-16); products of two bf16
 // tensors are exact.  Each fp32 operand is split once, where it is made.
 //
+// Resets (gated_deltanet.py:138-142: the state is zeroed before token t's
+// update where reset[b, t]): a reset starts a new segment of the chunk.
+// Log-decays are cumulated per segment, the couplings L and A vanish between
+// tokens of different segments, S0 reaches only the segment before the first
+// reset (Gamma masked to 0 after it), and S' takes only the last segment's
+// tokens (Gamma_C / Gamma_t masked to 0 before it, Gamma_C to 0 when the
+// chunk resets).  Kernel 1 therefore stores, per token, the two decay factors
+// the scan applies (e_t = Gamma_t, d_t = Gamma_C / Gamma_t, masked) instead
+// of the log-decays; without resets they are the same expf values the scan
+// formed from the log-decays.
+//
 // MFMA v_mfma_f32_16x16x32_bf16 fragments: A lane l holds A[l%16][8(l/16)+j],
 // B lane l holds B[8(l/16)+j][l%16], D lane l holds D[4(l/16)+i][l%16].
 #include <mutex>
@@ -70,13 +81,15 @@ __device__ __forceinline__ f32x4 mfma16(const uint4& a, const uint4& b, f32x4 c)
 
 // ---------------------------------------------------------------------------
 // Kernel 1: per-chunk preparation.  Scratch layout per chunk id
-// cid = (b*H + h) * NC + c:  W [64][DK], U0 [64][DV], A [64][64], cum [64] (fp32).
+// cid = (b*H + h) * NC + c:  W [64][DK], U0 [64][DV], A [64][64], decay
+// factors [2][64] (e_t then d_t, fp32).  reset [B, T] or null.
 template <int DK, int DV>
 __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, const float* __restrict__ beta,
-    const float* __restrict__ g, uint16_t* __restrict__ Wg, float* __restrict__ U0g,
-    uint16_t* __restrict__ Ag, float* __restrict__ cumg, int T, int H, int NC) {
+    const float* __restrict__ g, const int32_t* __restrict__ reset, uint16_t* __restrict__ Wg,
+    float* __restrict__ U0g, uint16_t* __restrict__ Ag, float* __restrict__ edg, int T, int H,
+    int NC) {
   constexpr int PK = DK + 8, PG = kC + 1, PT = kC + 8;
   // LDS by lifetime, so that two workgroups fit on a CU: region R0 holds K
   // and Q rows (products), then the per-wave block products of the inverse,
@@ -92,6 +105,7 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(
   __shared__ float Gm[kC * PG];   // K K^T, then L
   __shared__ float Ti[kC * PG];   // (I + L)^{-1}
   __shared__ float cum[kC], prv[kC], bet[kC], wsc[kC];  // wsc = beta * Gamma_prev
+  __shared__ int seg[kC];  // segment of each token (resets seen up to it in the chunk)
 
   const int cid = blockIdx.x;
   const int bh = cid / NC;
@@ -127,10 +141,26 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(
       const float o = __shfl_up(sc, off, kWave);
       if (lane >= off) sc += o;
     }
+    // segments: a reset at token r starts a new one; cumulative log-decays
+    // restart there (minus the prefix before r)
+    const bool rs = reset != nullptr && lane < Tc &&
+                    reset[static_cast<long long>(b) * T + t0 + lane] != 0;
+    const unsigned long long rm = __ballot(rs);
+    const unsigned long long upto = lane == 63 ? ~0ull : ((2ull << lane) - 1);
+    const int sg = __popcll(rm & upto);
+    float base = 0.f;
+    if (rm != 0) {
+      const unsigned long long before = rm & upto;
+      const int r0 = before ? 63 - __clzll(static_cast<long long>(before)) : lane;
+      const float pre = __shfl(sc - lg, r0, kWave);  // cumulative log-decay before token r0
+      if (before) base = pre;
+    }
+    sc -= base;
     cum[lane] = sc;
     prv[lane] = sc - lg;
     bet[lane] = bt;
-    wsc[lane] = bt * expf(sc - lg);
+    seg[lane] = sg;
+    wsc[lane] = sg == 0 ? bt * expf(sc - lg) : 0.f;
   }
   __syncthreads();
 
@@ -160,7 +190,7 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int j = j0 + i;
-        const float am = j <= t ? expf(cum[t] - cum[j]) * a2[i] : 0.f;
+        const float am = j <= t && seg[j] == seg[t] ? expf(cum[t] - cum[j]) * a2[i] : 0.f;
         hv[i] = f2bf(am);
         lv[i] = f2bf(am - bf2f(hv[i]));
       }
@@ -197,7 +227,8 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(
   // ---- L (strictly lower)
   for (int e = threadIdx.x; e < kC * kC; e += 256) {
     const int t = e >> 6, i = e & 63;
-    Gm[t * PG + i] = i < t ? bet[t] * expf(prv[t] - cum[i]) * Gm[t * PG + i] : 0.f;
+    Gm[t * PG + i] = i < t && seg[i] == seg[t] ? bet[t] * expf(prv[t] - cum[i]) * Gm[t * PG + i]
+                                               : 0.f;
   }
   __syncthreads();
   // ---- (I + L)^{-1}, blocked by 16: N = I + L is unit lower triangular with
@@ -354,7 +385,14 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(
       }
     }
   }
-  if (threadIdx.x < kC) cumg[wo + threadIdx.x] = cum[threadIdx.x];
+  if (threadIdx.x < kC) {
+    // e_t = Gamma_t (the S0 term of O), d_t = Gamma_C / Gamma_t (the S' update),
+    // masked to the segments that see S0 and reach the chunk's end
+    const int t = threadIdx.x;
+    const float ct = cum[t], cl = cum[kC - 1];
+    edg[2 * wo + t] = seg[t] == 0 ? expf(ct) : 0.f;
+    edg[2 * wo + kC + t] = seg[t] == seg[kC - 1] ? expf(cl - ct) : 0.f;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -382,7 +420,7 @@ template <int DK, int DV, int DVS>
 __global__ __launch_bounds__(kScanThreads) void gdn_chunk_scan_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ Wg, const float* __restrict__ U0g, const uint16_t* __restrict__ Ag,
-    const float* __restrict__ cumg, float* __restrict__ state, uint16_t* __restrict__ out, int T,
+    const float* __restrict__ edg, float* __restrict__ state, uint16_t* __restrict__ out, int T,
     int H, int NC, int n_units) {
   constexpr int NSL = DV / DVS;
   constexpr int NTN = DVS / 16;                  // column tiles of U, O and S
@@ -400,7 +438,7 @@ __global__ __launch_bounds__(kScanThreads) void gdn_chunk_scan_kernel(
   __shared__ __align__(16) uint16_t KsT[DK * PT];                  // K^T [DK][64]
   __shared__ __align__(16) uint16_t SThi[DVS * PB], STlo[DVS * PB];  // S^T [DVS][DK]
   __shared__ __align__(16) uint16_t UThi[DVS * PT], UTlo[DVS * PT];  // U^T [DVS][64]
-  __shared__ float cum[kC], ecum[kC], dec[kC];
+  __shared__ float ecum[kC], dec[kC];  // per token: Gamma_t, Gamma_C / Gamma_t (kernel 1)
 
   const int per_xcd = (gridDim.x + 7) / 8;
   const int unit = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
@@ -467,7 +505,7 @@ __global__ __launch_bounds__(kScanThreads) void gdn_chunk_scan_kernel(
       _Pragma("unroll") for (int i = 0; i < 4; ++i)                                            \
         pu_nxt[ot][i] = U0g[(fcid * kC + 16 * tm + 4 * g4 + i) * DV + DVS * sl + 16 * tn + r16]; \
     }                                                                                          \
-    pc = tid < kC ? cumg[fcid * kC + tid] : 0.f;                                               \
+    pc = tid < 2 * kC ? edg[fcid * 2 * kC + tid] : 0.f;                                        \
   } while (0)
 #define GDN_STASH()                                                                            \
   do {                                                                                         \
@@ -491,7 +529,8 @@ __global__ __launch_bounds__(kScanThreads) void gdn_chunk_scan_kernel(
       const int t = rem / kC, cc = rem % kC;                                                   \
       *reinterpret_cast<u32x4*>((pl ? Alo : Ahi) + t * PT + cc) = pa[i];                       \
     }                                                                                          \
-    if (tid < kC) cum[tid] = pc;                                                               \
+    if (tid < kC) ecum[tid] = pc;                                                              \
+    else if (tid < 2 * kC) dec[tid - kC] = pc;                                                 \
   } while (0)
 
   GDN_FETCH(0);
@@ -504,14 +543,9 @@ __global__ __launch_bounds__(kScanThreads) void gdn_chunk_scan_kernel(
   for (int c = 0; c < NC; ++c) {
     const int t0 = c * kC;
     const int Tc = min(kC, T - t0);
-    if (tid < kC) {
-      const float cv = cum[tid], cl_ = cum[kC - 1];
-      ecum[tid] = expf(cv);
-      dec[tid] = expf(cl_ - cv);
-    }
-    const float gc = expf(cum[kC - 1]);
+    const float gc = ecum[kC - 1];  // Gamma_C (0 when the chunk resets)
     if (c + 1 < NC) GDN_FETCH(c + 1);
-    __syncthreads();  // dec visible
+    __syncthreads();
 
     // ---- U = U0 - W S, split once into U^T and (dec o U)^T
 #pragma unroll
@@ -634,7 +668,7 @@ extern "C" int64_t llmy_gdn_prefill_workspace_bytes(int32_t B, int32_t T, int32_
   if (B <= 0 || T <= 0 || H <= 0 || dk <= 0 || dv <= 0) return 0;
   const long long nc = (T + kC - 1) / kC;
   const long long chunks = static_cast<long long>(B) * H * nc;
-  return chunks * kC * (static_cast<long long>(dk) + dv + kC + 1) * static_cast<long long>(sizeof(float));
+  return chunks * kC * (static_cast<long long>(dk) + dv + kC + 2) * static_cast<long long>(sizeof(float));
 }
 
 namespace {
@@ -642,32 +676,34 @@ namespace {
 // The prep + scan launches over a caller-sized workspace (validated by the
 // entry points below).
 int32_t gdn_prefill_launch(const llmy_bf16* q, const llmy_bf16* k, const llmy_bf16* v,
-                           const float* beta, const float* g, float* state, llmy_bf16* out,
-                           void* workspace, int B, int T, int H, int dk, hipStream_t s) {
+                           const float* beta, const float* g, const int32_t* reset, float* state,
+                           llmy_bf16* out, void* workspace, int B, int T, int H, int dk,
+                           hipStream_t s) {
   const int NC = (T + kC - 1) / kC;
   const long long chunks = static_cast<long long>(B) * H * NC;
   const int dv = dk;
-  // workspace: W as (hi, lo) bf16 planes, U0 fp32, A as (hi, lo) bf16 planes, cum fp32
+  // workspace: W as (hi, lo) bf16 planes, U0 fp32, A as (hi, lo) bf16 planes,
+  // decay factors [2][64] fp32
   uint16_t* W = static_cast<uint16_t*>(workspace);
   float* U0 = reinterpret_cast<float*>(W + chunks * kC * dk * 2);
   uint16_t* A = reinterpret_cast<uint16_t*>(U0 + chunks * kC * dv);
-  float* cum = reinterpret_cast<float*>(A + chunks * kC * kC * 2);
+  float* ed = reinterpret_cast<float*>(A + chunks * kC * kC * 2);
   if (dk == 64) {
     hipLaunchKernelGGL((gdn_chunk_prep_kernel<64, 64>), dim3(static_cast<unsigned>(chunks)),
-                       dim3(256), 0, s, q, k, v, beta, g, W, U0, A, cum, T, H, NC);
+                       dim3(256), 0, s, q, k, v, beta, g, reset, W, U0, A, ed, T, H, NC);
     int32_t st = launch_status();
     if (st != 0) return st;
     const int units = B * H * (64 / 32);
     hipLaunchKernelGGL((gdn_chunk_scan_kernel<64, 64, 32>), dim3((units + 7) / 8 * 8),
-                       dim3(kScanThreads), 0, s, q, k, W, U0, A, cum, state, out, T, H, NC, units);
+                       dim3(kScanThreads), 0, s, q, k, W, U0, A, ed, state, out, T, H, NC, units);
   } else {
     hipLaunchKernelGGL((gdn_chunk_prep_kernel<128, 128>), dim3(static_cast<unsigned>(chunks)),
-                       dim3(256), 0, s, q, k, v, beta, g, W, U0, A, cum, T, H, NC);
+                       dim3(256), 0, s, q, k, v, beta, g, reset, W, U0, A, ed, T, H, NC);
     int32_t st = launch_status();
     if (st != 0) return st;
     const int units = B * H * (128 / 64);
     hipLaunchKernelGGL((gdn_chunk_scan_kernel<128, 128, 64>), dim3((units + 7) / 8 * 8),
-                       dim3(kScanThreads), 0, s, q, k, W, U0, A, cum, state, out, T, H, NC, units);
+                       dim3(kScanThreads), 0, s, q, k, W, U0, A, ed, state, out, T, H, NC, units);
   }
   return launch_status();
 }
@@ -716,7 +752,26 @@ extern "C" int32_t llmy_gdn_prefill_bf16(const llmy_bf16* q, const llmy_bf16* k,
                aligned(workspace, 16));
   const long long chunks = static_cast<long long>(B) * H * ((T + kC - 1) / kC);
   LLMY_REQUIRE(chunks < (1ll << 31));
-  return gdn_prefill_launch(q, k, v, beta, g, state, out, workspace, B, T, H, dk,
+  return gdn_prefill_launch(q, k, v, beta, g, nullptr, state, out, workspace, B, T, H, dk,
+                            as_stream(stream));
+}
+
+extern "C" int32_t llmy_gdn_prefill_reset_bf16(const llmy_bf16* q, const llmy_bf16* k,
+                                               const llmy_bf16* v, const float* beta,
+                                               const float* g, const int32_t* reset, float* state,
+                                               llmy_bf16* out, void* workspace,
+                                               int64_t workspace_bytes, int32_t B, int32_t T,
+                                               int32_t H, int32_t dk, int32_t dv, void* stream) {
+  LLMY_REQUIRE(B >= 0 && T >= 0 && H > 0);
+  LLMY_REQUIRE((dk == 64 && dv == 64) || (dk == 128 && dv == 128));
+  if (B == 0 || T == 0) return 0;
+  LLMY_REQUIRE(q && k && v && beta && g && reset && state && out && workspace);
+  LLMY_REQUIRE(workspace_bytes >= llmy_gdn_prefill_workspace_bytes(B, T, H, dk, dv));
+  LLMY_REQUIRE(aligned(q, 16) && aligned(k, 16) && aligned(v, 16) && aligned(state, 16) &&
+               aligned(workspace, 16));
+  const long long chunks = static_cast<long long>(B) * H * ((T + kC - 1) / kC);
+  LLMY_REQUIRE(chunks < (1ll << 31));
+  return gdn_prefill_launch(q, k, v, beta, g, reset, state, out, workspace, B, T, H, dk,
                             as_stream(stream));
 }
 
@@ -737,5 +792,6 @@ extern "C" int32_t llmy_gdn_prefill_bf16_noalloc(const llmy_bf16* q, const llmy_
   if (!ws) return static_cast<int32_t>(hipErrorInvalidDevicePointer);
   // every workspace byte the scan reads is written by this call's prep kernel
   // first, so what an earlier call left there does not matter
-  return gdn_prefill_launch(q, k, v, beta, g, state, out, ws, B, T, H, dk, as_stream(stream));
+  return gdn_prefill_launch(q, k, v, beta, g, nullptr, state, out, ws, B, T, H, dk,
+                            as_stream(stream));
 }

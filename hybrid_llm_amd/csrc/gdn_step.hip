@@ -20,6 +20,12 @@
 //          per-head L2 norm of q and k (clamp 1e-12, gated_deltanet.py:128-129),
 //          beta = sigmoid(logit + bias) (:130), gate = sigmoid(logit) (:131) and
 //          g = sigmoid(decay_logit[h]) (:132).
+//
+// Optional per-row reset (gated_deltanet.py:138-142,165-166; the reference's
+// native step takes a per-head mask, llmy_cuda/src/kernels/gdn.cu:28,36-40):
+// where reset[b] != 0 the row's state and conv history count as zero before
+// the update (the state is still read, so the loads start at once; its values
+// are dropped).
 #include "common.hpp"
 #include "abi_util.hpp"
 
@@ -43,6 +49,7 @@ struct GdnStepArgs {
   const float* conv_w;     // [D, K]
   float* conv_out;         // [B, D] sigmoid(conv)
   int D;
+  const int32_t* reset;    // [B] or null: nonzero = the row starts from zero
 };
 
 // NP: compile-time bound on the projection slices (1, 4 or 8), so that every
@@ -64,10 +71,15 @@ __global__ __launch_bounds__(256) void gdn_step_kernel(GdnStepArgs a) {
   const int rg = t / CPT;
 
   float* S = a.state + static_cast<long long>(bh) * DK * DV;
+  const bool fresh = a.reset != nullptr && a.reset[b] != 0;
   float4 st[NR];
 #pragma unroll
   for (int i = 0; i < NR; ++i)
     st[i] = *reinterpret_cast<const float4*>(S + (rg + i * RPP) * DV + c4);
+  if (fresh) {
+#pragma unroll
+    for (int i = 0; i < NR; ++i) st[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+  }
 
   const int lane = t & 63;
   const int wave = t >> 6;
@@ -139,7 +151,8 @@ __global__ __launch_bounds__(256) void gdn_step_kernel(GdnStepArgs a) {
     for (int c = t; c < per; c += 256) {
       const int d = h * per + c;
       uint16_t* hb = a.conv_hist + static_cast<long long>(b) * 3 * a.D + d;
-      const uint16_t w0 = hb[0], w1 = hb[a.D], w2 = hb[2 * a.D];
+      uint16_t w0 = hb[0], w1 = hb[a.D], w2 = hb[2 * a.D];
+      if (fresh) w0 = w1 = w2 = 0;
       const uint16_t w3 = a.conv_h[static_cast<long long>(b) * a.D + d];
       const float4 cw = *reinterpret_cast<const float4*>(a.conv_w + 4 * d);
       float acc = cw.x * bf2f(w0);
@@ -269,6 +282,48 @@ extern "C" int32_t llmy_gdn_step_fused_f32(const float* proj, int64_t proj_ld, i
   a.proj = proj; a.proj_ld = proj_ld; a.beta_bias = beta_bias; a.decay_logit = decay_logit;
   a.nparts = nparts; a.part_stride = static_cast<long long>(B) * proj_ld;
   a.state = state; a.out = out; a.H = H;
+  a.conv_h = conv_h; a.conv_hist = conv_hist; a.conv_w = conv_w; a.conv_out = conv_out; a.D = D;
+  return launch_gdn_step<true>(a, B, dk, dv, as_stream(stream));
+}
+
+extern "C" int32_t llmy_gdn_step_reset_bf16(const llmy_bf16* q, const llmy_bf16* k,
+                                            const llmy_bf16* v, const float* beta, const float* g,
+                                            const llmy_bf16* gate, const int32_t* reset,
+                                            float* state, llmy_bf16* out, int32_t B, int32_t H,
+                                            int32_t dk, int32_t dv, void* stream) {
+  LLMY_REQUIRE(B >= 0 && H > 0 && ((dk == 64 && dv == 64) || (dk == 128 && dv == 128)));
+  if (B == 0) return 0;
+  LLMY_REQUIRE(q && k && v && beta && g && reset && state && out);
+  LLMY_REQUIRE(aligned(state, 16));
+  GdnStepArgs a{};
+  a.q = q; a.k = k; a.v = v; a.gate = gate; a.beta = beta; a.g = g;
+  a.state = state; a.out = out; a.H = H; a.reset = reset;
+  return launch_gdn_step<false>(a, B, dk, dv, as_stream(stream));
+}
+
+extern "C" int32_t llmy_gdn_step_fused_reset_f32(const float* proj, int64_t proj_ld,
+                                                 int32_t nparts, const float* beta_bias,
+                                                 const float* decay_logit, const int32_t* reset,
+                                                 float* state, llmy_bf16* out,
+                                                 const llmy_bf16* conv_h, llmy_bf16* conv_hist,
+                                                 const float* conv_w, float* conv_out, int32_t D,
+                                                 int32_t conv_kernel, int32_t B, int32_t H,
+                                                 int32_t dk, int32_t dv, void* stream) {
+  LLMY_REQUIRE(B >= 0 && H > 0 && ((dk == 64 && dv == 64) || (dk == 128 && dv == 128)));
+  LLMY_REQUIRE(proj_ld >= static_cast<int64_t>(H) * (2 * dk + 2 * dv + 1));
+  LLMY_REQUIRE(nparts >= 1 && nparts <= 8);
+  LLMY_REQUIRE(static_cast<long long>(nparts) * B * proj_ld < (1ll << 31));
+  if (B == 0) return 0;
+  LLMY_REQUIRE(proj && beta_bias && decay_logit && reset && state && out);
+  LLMY_REQUIRE(aligned(state, 16));
+  if (conv_h != nullptr) {
+    LLMY_REQUIRE(conv_hist && conv_w && conv_out && conv_kernel == 4 && D > 0 && D % H == 0);
+    LLMY_REQUIRE(aligned(conv_w, 16));
+  }
+  GdnStepArgs a{};
+  a.proj = proj; a.proj_ld = proj_ld; a.beta_bias = beta_bias; a.decay_logit = decay_logit;
+  a.nparts = nparts; a.part_stride = static_cast<long long>(B) * proj_ld;
+  a.state = state; a.out = out; a.H = H; a.reset = reset;
   a.conv_h = conv_h; a.conv_hist = conv_hist; a.conv_w = conv_w; a.conv_out = conv_out; a.D = D;
   return launch_gdn_step<true>(a, B, dk, dv, as_stream(stream));
 }

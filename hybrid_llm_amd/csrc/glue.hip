@@ -3,6 +3,7 @@
 #include "common.hpp"
 #include "abi_util.hpp"
 
+#include <algorithm>
 #include <cmath>
 
 namespace llmy {
@@ -207,6 +208,21 @@ __global__ __launch_bounds__(256) void append_shared_kernel(const int32_t* __res
   gates_out[i] = j < k ? gates[t * k + j] : g;
 }
 
+// Zero row b of a [rows, row_bytes] buffer where mask[b] != 0 (the per-row
+// state reset of model/recurrent_state.py:213-225).  A kernel rather than a
+// memory set, so a captured graph may hold it.  V = 16-byte or 4-byte words.
+template <typename V>
+__global__ __launch_bounds__(256) void zero_rows_kernel(V* __restrict__ base, long long words,
+                                                        const int32_t* __restrict__ mask) {
+  const int b = blockIdx.y;
+  if (mask[b] == 0) return;
+  V* row = base + static_cast<long long>(b) * words;
+  const V z{};
+  for (long long i = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x; i < words;
+       i += static_cast<long long>(gridDim.x) * 256)
+    row[i] = z;
+}
+
 }  // namespace llmy
 
 using namespace llmy;
@@ -294,5 +310,22 @@ extern "C" int32_t llmy_moe_append_shared(const int32_t* idx, const float* gates
   hipLaunchKernelGGL(append_shared_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256),
                      0, as_stream(stream), idx, gates, idx_out, gates_out, T, k, E, S,
                      1.0f / std::sqrt(static_cast<float>(S)));
+  return launch_status();
+}
+
+extern "C" int32_t llmy_zero_rows(void* base, int64_t row_bytes, int32_t rows,
+                                  const int32_t* mask, void* stream) {
+  LLMY_REQUIRE(rows >= 0 && row_bytes >= 0 && row_bytes % 4 == 0 && rows <= 65535);
+  if (rows == 0 || row_bytes == 0) return 0;
+  LLMY_REQUIRE(base && mask);
+  const bool wide = row_bytes % 16 == 0 && aligned(base, 16);
+  const long long words = wide ? row_bytes / 16 : row_bytes / 4;
+  const unsigned gx = static_cast<unsigned>(std::min<long long>((words + 255) / 256, 64));
+  if (wide)
+    hipLaunchKernelGGL(zero_rows_kernel<uint4>, dim3(gx, rows), dim3(256), 0, as_stream(stream),
+                       static_cast<uint4*>(base), words, mask);
+  else
+    hipLaunchKernelGGL(zero_rows_kernel<uint32_t>, dim3(gx, rows), dim3(256), 0,
+                       as_stream(stream), static_cast<uint32_t*>(base), words, mask);
   return launch_status();
 }

@@ -120,12 +120,18 @@ __global__ __launch_bounds__(256) void gdn_gate_kernel(const uint16_t* __restric
 // of the last KC inputs; the window of the first block starts from the
 // carried history.  Only the first block's thread rewrites the history of
 // (b, d) — after reading it — so no thread reads a history another writes.
+// With resets [B, T] (gated_deltanet.py:56-78: taps do not cross a reset),
+// a tap at position p counts for token t only if no reset lies in (p, t];
+// history taps only if none lies in [0, t].  The new history is then what a
+// token-by-token pass would leave: the last KC - 1 inputs, zero where they
+// precede the last reset.
 constexpr int kConvSpan = 16;
 
 template <int KC>
 __global__ __launch_bounds__(256) void gdn_conv_prefill_kernel(const uint16_t* __restrict__ h,
                                                                uint16_t* __restrict__ hist,
                                                                const float* __restrict__ w,
+                                                               const int32_t* __restrict__ reset,
                                                                float* __restrict__ out, int B,
                                                                int T, int D) {
   const int nblk = (T + kConvSpan - 1) / kConvSpan;
@@ -149,13 +155,22 @@ __global__ __launch_bounds__(256) void gdn_conv_prefill_kernel(const uint16_t* _
     win[j + 1] = p >= 0 ? hb[static_cast<long long>(p) * D] : hs[static_cast<long long>(j) * D];
   }
   const int t1 = min(t0 + kConvSpan, T);
+  // first position a tap may read (the last reset so far; -KC: none, history valid)
+  const int32_t* rb = reset ? reset + static_cast<long long>(b) * T : nullptr;
+  int vstart = -KC;
+  if (rb) {
+    for (int p = max(0, t0 - (KC - 1)); p < t0; ++p)
+      if (rb[p] != 0) vstart = p;
+  }
   for (int t = t0; t < t1; ++t) {
 #pragma unroll
     for (int j = 0; j < KC - 1; ++j) win[j] = win[j + 1];
     win[KC - 1] = hb[static_cast<long long>(t) * D];
+    if (rb && rb[t] != 0) vstart = t;
     float acc = 0.f;
 #pragma unroll
-    for (int j = 0; j < KC; ++j) acc = fmaf(wt[j], bf2f(win[j]), acc);
+    for (int j = 0; j < KC; ++j)
+      acc = t - (KC - 1) + j >= vstart ? fmaf(wt[j], bf2f(win[j]), acc) : acc;
     out[(static_cast<long long>(b) * T + t) * D + d] = sigmoidf_(acc);
   }
   if (tb == 0) {
@@ -163,10 +178,16 @@ __global__ __launch_bounds__(256) void gdn_conv_prefill_kernel(const uint16_t* _
     // When this block reached T its window already holds them (including
     // old history entries for T < KC - 1); otherwise T > kConvSpan > KC - 1
     // and they are all inputs.
+    int last = -KC;  // the last reset of the sequence (inputs before it are not kept)
+    if (rb) {
+      for (int p = max(0, T - (KC - 1)); p < T; ++p)
+        if (rb[p] != 0) last = p;
+    }
 #pragma unroll
-    for (int j = 0; j < KC - 1; ++j)
-      hs[static_cast<long long>(j) * D] =
-          t1 == T ? win[j + 1] : hb[static_cast<long long>(T - (KC - 1) + j) * D];
+    for (int j = 0; j < KC - 1; ++j) {
+      const uint16_t hv = t1 == T ? win[j + 1] : hb[static_cast<long long>(T - (KC - 1) + j) * D];
+      hs[static_cast<long long>(j) * D] = T - (KC - 1) + j >= last ? hv : 0;
+    }
   }
 }
 
@@ -246,6 +267,21 @@ extern "C" int32_t llmy_gdn_conv_gate_prefill(const llmy_bf16* h, llmy_bf16* his
       static_cast<long long>(B) * ((T + kConvSpan - 1) / kConvSpan) * static_cast<long long>(D);
   LLMY_REQUIRE((n + 255) / 256 < (1ll << 31));
   hipLaunchKernelGGL(gdn_conv_prefill_kernel<4>, dim3(static_cast<unsigned>((n + 255) / 256)),
-                     dim3(256), 0, as_stream(stream), h, hist, w, out, B, T, D);
+                     dim3(256), 0, as_stream(stream), h, hist, w, nullptr, out, B, T, D);
+  return launch_status();
+}
+
+extern "C" int32_t llmy_gdn_conv_gate_prefill_reset(const llmy_bf16* h, llmy_bf16* hist,
+                                                    const float* w, const int32_t* reset,
+                                                    float* out, int32_t B, int32_t T, int32_t D,
+                                                    int32_t kernel, void* stream) {
+  LLMY_REQUIRE(B >= 0 && T >= 0 && D > 0 && kernel == 4);
+  if (B == 0 || T == 0) return 0;
+  LLMY_REQUIRE(h && hist && w && reset && out);
+  const long long n =
+      static_cast<long long>(B) * ((T + kConvSpan - 1) / kConvSpan) * static_cast<long long>(D);
+  LLMY_REQUIRE((n + 255) / 256 < (1ll << 31));
+  hipLaunchKernelGGL(gdn_conv_prefill_kernel<4>, dim3(static_cast<unsigned>((n + 255) / 256)),
+                     dim3(256), 0, as_stream(stream), h, hist, w, reset, out, B, T, D);
   return launch_status();
 }

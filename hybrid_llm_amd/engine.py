@@ -127,6 +127,7 @@ class HybridDecoder:
         nproj = self.w[f"L{cfg.gdn_layers()[0]}.wproj"].shape[0] if cfg.gdn_layers() else 16
         self.buf = {
             "tokens": torch.zeros(B, dtype=torch.int32, device=dev),
+            "reset": torch.zeros(B, dtype=torch.int32, device=dev),
             "x": torch.zeros(B, D, dtype=f32, device=dev),
             "h": torch.zeros(B, D, dtype=bf, device=dev),
             "qkv": torch.zeros(B, 3 * Ha * hd, dtype=bf, device=dev),
@@ -339,9 +340,26 @@ class HybridDecoder:
         """Per-row uniform draws in [0, 1) for the next steps' top-p sampling."""
         self.buf["u"].copy_(u.to(torch.float32).view(-1))
 
-    def step(self, tokens: torch.Tensor | None = None) -> torch.Tensor:
+    def reset_rows(self, mask: torch.Tensor) -> None:
+        """Rows b with mask[b] != 0 start a new sequence: their KV caches, GDN
+        states, conv histories and router latent rings are zeroed and their
+        next position is 0 (RecurrentState.reset_rows,
+        model/recurrent_state.py:213-225, as decode_step applies it,
+        model/model.py:814-822).  Kernels only, no memory set."""
+        m = self.buf["reset"]
+        m.copy_(torch.as_tensor(mask).to(torch.int32).view(-1))
+        for st in self.state.values():
+            for t in st.values():
+                ops.zero_rows(t, m)
+        ops.zero_rows(self.pos, m)
+
+    def step(self, tokens: torch.Tensor | None = None, reset=None) -> torch.Tensor:
         """Decode one token for every sequence.  ``tokens`` [B] int32 (device or
-        host) is copied into the static input buffer; returns the logits buffer."""
+        host) is copied into the static input buffer; ``reset`` [B] (optional):
+        those rows start a new sequence at position 0 first (``reset_rows``).
+        Returns the logits buffer."""
+        if reset is not None:
+            self.reset_rows(reset)
         if tokens is not None:
             self.buf["tokens"].copy_(tokens.to(torch.int32).view(-1))
         if self.graph is not None:

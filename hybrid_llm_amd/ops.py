@@ -287,9 +287,21 @@ def banded_attn_decode(q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor
 
 
 # --------------------------------------------------------------------------- GDN
-def gdn_prefill(q, k, v, beta, g, state, out=None, workspace=None) -> torch.Tensor:
+def _reset_arg(reset, shape, dev):
+    """A reset mask as the device int32 array the kernels read (nonzero = reset)."""
+    if reset is None:
+        return None
+    r = torch.as_tensor(reset, device=dev).to(torch.int32).contiguous()
+    if tuple(r.shape) != tuple(shape):
+        raise ValueError(f"reset: expected shape {tuple(shape)}, got {tuple(r.shape)}")
+    return r
+
+
+def gdn_prefill(q, k, v, beta, g, state, out=None, workspace=None, reset=None) -> torch.Tensor:
     """Chunked delta-rule scan; q,k [B,T,H,dk], v [B,T,H,dv] bf16, beta/g [B,T,H]
-    fp32, state [B,H,dk,dv] fp32 updated in place.  Returns out [B,T,H,dv] bf16."""
+    fp32, state [B,H,dk,dv] fp32 updated in place.  Returns out [B,T,H,dv] bf16.
+    ``reset`` [B, T] (bool/int): the state entering token t is zero where set
+    (gated_deltanet.py:138-142)."""
     B, T, H, dk = q.shape
     dv = v.shape[-1]
     _check(q, torch.bfloat16, "q")
@@ -303,14 +315,21 @@ def gdn_prefill(q, k, v, beta, g, state, out=None, workspace=None) -> torch.Tens
         workspace = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=q.device)
     if out is None:
         out = torch.empty(B, T, H, dv, dtype=torch.bfloat16, device=q.device)
-    _lib.call("llmy_gdn_prefill_bf16", _ptr(q), _ptr(k), _ptr(v), _ptr(beta), _ptr(g),
-              _ptr(state), _ptr(out), _ptr(workspace), nbytes, B, T, H, dk, dv, _stream())
+    rs = _reset_arg(reset, (B, T), q.device)
+    if rs is None:
+        _lib.call("llmy_gdn_prefill_bf16", _ptr(q), _ptr(k), _ptr(v), _ptr(beta), _ptr(g),
+                  _ptr(state), _ptr(out), _ptr(workspace), nbytes, B, T, H, dk, dv, _stream())
+    else:
+        _lib.call("llmy_gdn_prefill_reset_bf16", _ptr(q), _ptr(k), _ptr(v), _ptr(beta), _ptr(g),
+                  _ptr(rs), _ptr(state), _ptr(out), _ptr(workspace), nbytes, B, T, H, dk, dv,
+                  _stream())
     return out
 
 
-def gdn_step(q, k, v, beta, g, state, gate=None, out=None) -> torch.Tensor:
+def gdn_step(q, k, v, beta, g, state, gate=None, out=None, reset=None) -> torch.Tensor:
     """In-place state update; q,k [B,H,dk], v/gate [B,H,dv] bf16, beta/g [B,H] fp32,
-    state [B,H,dk,dv] fp32.  Returns out [B,H,dv] bf16."""
+    state [B,H,dk,dv] fp32.  Returns out [B,H,dv] bf16.  ``reset`` [B]: those
+    rows start from a zero state."""
     B, H, dk = q.shape
     dv = v.shape[-1]
     _check(q, torch.bfloat16, "q")
@@ -323,15 +342,22 @@ def gdn_step(q, k, v, beta, g, state, gate=None, out=None) -> torch.Tensor:
         _check(gate, torch.bfloat16, "gate", (B, H, dv))
     if out is None:
         out = torch.empty(B, H, dv, dtype=torch.bfloat16, device=q.device)
-    _lib.call("llmy_gdn_step_bf16", _ptr(q), _ptr(k), _ptr(v), _ptr(beta), _ptr(g), _ptr(gate),
-              _ptr(state), _ptr(out), B, H, dk, dv, _stream())
+    rs = _reset_arg(reset, (B,), q.device)
+    if rs is None:
+        _lib.call("llmy_gdn_step_bf16", _ptr(q), _ptr(k), _ptr(v), _ptr(beta), _ptr(g),
+                  _ptr(gate), _ptr(state), _ptr(out), B, H, dk, dv, _stream())
+    else:
+        _lib.call("llmy_gdn_step_reset_bf16", _ptr(q), _ptr(k), _ptr(v), _ptr(beta), _ptr(g),
+                  _ptr(gate), _ptr(rs), _ptr(state), _ptr(out), B, H, dk, dv, _stream())
     return out
 
 
-def gdn_step_fused(proj, beta_bias, decay_logit, state, out=None, conv=None) -> torch.Tensor:
+def gdn_step_fused(proj, beta_bias, decay_logit, state, out=None, conv=None,
+                   reset=None) -> torch.Tensor:
     """GDN step from the fused fp32 projection [B, ld] (or its per-K-block
     partial products [P, B, ld], summed in order); ``conv=(h, hist, w, cg_out)``
-    also computes the causal conv gate in the same launch."""
+    also computes the causal conv gate in the same launch.  ``reset``: a device
+    int32 [B] array (nonzero: the row starts from a zero state and history)."""
     B, H, dk, dv = state.shape
     _check(proj, torch.float32, "proj")
     nparts = proj.shape[0] if proj.dim() == 3 else 1
@@ -349,9 +375,15 @@ def gdn_step_fused(proj, beta_bias, decay_logit, state, out=None, conv=None) -> 
         _check(hist, torch.bfloat16, "conv_hist", (B, 3, D))
         _check(cw, torch.float32, "conv_w", (D, 4))
         _check(cg, torch.float32, "conv_out", (B, D))
-    _lib.call("llmy_gdn_step_fused_f32", _ptr(proj), proj.shape[-1], nparts, _ptr(beta_bias),
-              _ptr(decay_logit), _ptr(state), _ptr(out), _ptr(ch), _ptr(hist), _ptr(cw), _ptr(cg),
-              D, 4, B, H, dk, dv, _stream())
+    if reset is None:
+        _lib.call("llmy_gdn_step_fused_f32", _ptr(proj), proj.shape[-1], nparts,
+                  _ptr(beta_bias), _ptr(decay_logit), _ptr(state), _ptr(out), _ptr(ch),
+                  _ptr(hist), _ptr(cw), _ptr(cg), D, 4, B, H, dk, dv, _stream())
+    else:
+        _check(reset, torch.int32, "reset", (B,))
+        _lib.call("llmy_gdn_step_fused_reset_f32", _ptr(proj), proj.shape[-1], nparts,
+                  _ptr(beta_bias), _ptr(decay_logit), _ptr(reset), _ptr(state), _ptr(out),
+                  _ptr(ch), _ptr(hist), _ptr(cw), _ptr(cg), D, 4, B, H, dk, dv, _stream())
     return out
 
 
@@ -520,6 +552,16 @@ def gdn_conv_gate(h, hist, w, out=None) -> torch.Tensor:
     return out
 
 
+def zero_rows(t: torch.Tensor, mask: torch.Tensor) -> None:
+    """Zero t[b] wherever mask[b] != 0; t contiguous [rows, ...] on the device,
+    mask device int32 [rows] (a kernel, so it may sit in a captured graph)."""
+    if not t.is_contiguous() or t.dim() < 1:
+        raise ValueError("zero_rows: contiguous tensor with a row dimension expected")
+    _check(mask, torch.int32, "mask", (t.shape[0],))
+    row_bytes = t[0].numel() * t.element_size() if t.shape[0] else 0
+    _lib.call("llmy_zero_rows", _ptr(t), row_bytes, t.shape[0], _ptr(mask), _stream())
+
+
 # --------------------------------------------------------------------------- prefill glue
 def kv_cache_fill(k, v, k_cache, v_cache) -> None:
     """K/V rows [B, T, ld] bf16 (head h at columns h*hd..; rows may be strided
@@ -569,16 +611,22 @@ def gdn_gate(o, proj, gate_off, out=None) -> torch.Tensor:
     return out
 
 
-def gdn_conv_gate_prefill(h, hist, w, out=None) -> torch.Tensor:
-    """Conv gate over a sequence: h [B, T, D] bf16, hist [B, K-1, D] updated."""
+def gdn_conv_gate_prefill(h, hist, w, out=None, reset=None) -> torch.Tensor:
+    """Conv gate over a sequence: h [B, T, D] bf16, hist [B, K-1, D] updated.
+    ``reset`` [B, T]: taps do not cross a reset (gated_deltanet.py:56-78)."""
     B, T, D = h.shape
     _check(h, torch.bfloat16, "h")
     _check(hist, torch.bfloat16, "hist", (B, w.shape[1] - 1, D))
     _check(w, torch.float32, "w", (D, w.shape[1]))
     if out is None:
         out = torch.empty(B, T, D, dtype=torch.float32, device=h.device)
-    _lib.call("llmy_gdn_conv_gate_prefill", _ptr(h), _ptr(hist), _ptr(w), _ptr(out), B, T, D,
-              w.shape[1], _stream())
+    rs = _reset_arg(reset, (B, T), h.device)
+    if rs is None:
+        _lib.call("llmy_gdn_conv_gate_prefill", _ptr(h), _ptr(hist), _ptr(w), _ptr(out), B, T, D,
+                  w.shape[1], _stream())
+    else:
+        _lib.call("llmy_gdn_conv_gate_prefill_reset", _ptr(h), _ptr(hist), _ptr(w), _ptr(rs),
+                  _ptr(out), B, T, D, w.shape[1], _stream())
     return out
 
 

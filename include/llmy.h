@@ -164,8 +164,8 @@ int32_t llmy_banded_attn_decode_bf16(const llmy_bf16* q, const llmy_bf16* k_new,
 /* --- Gated delta rule, prefill (chunked; model/layers/gated_deltanet.py:140-149) */
 
 /* Workspace (bytes) that llmy_gdn_prefill_bf16 needs for (B, T, H, dk, dv):
- * per 64-token chunk W [64,dk], U0 [64,dv], A [64,64] and 64 cumulative
- * log-decays, fp32.  No counterpart in the reference. */
+ * per 64-token chunk W [64,dk], U0 [64,dv], A [64,64] and 2 x 64 decay
+ * factors, fp32.  No counterpart in the reference. */
 int64_t llmy_gdn_prefill_workspace_bytes(int32_t B, int32_t T, int32_t H, int32_t dk,
                                          int32_t dv);
 
@@ -275,6 +275,55 @@ int32_t llmy_gdn_gate_bf16(const llmy_bf16* o, const float* proj, int64_t ld,
 int32_t llmy_gdn_conv_gate_prefill(const llmy_bf16* h, llmy_bf16* hist, const float* w,
                                    float* out, int32_t B, int32_t T, int32_t D,
                                    int32_t kernel, void* stream);
+
+/* --- Per-row resets of the GDN recurrence (gated_deltanet.py:138-142,165-166:
+ * the state is zeroed before token t's update where reset[b, t]; :56-78: conv
+ * taps do not cross a reset, and :262-266: a reset clears the conv history).
+ * reset arrays are device int32, nonzero = reset.  The reference's native
+ * step takes a per-head mask for its one sequence (llmy_cuda/src/kernels/
+ * gdn.cu:28,36-40); these take one flag per batch row (all heads).  Each is
+ * the entry of the same name without "_reset" plus the mask, with the same
+ * arithmetic where no reset is set. */
+
+/* llmy_gdn_prefill_bf16 with reset [B, T]: a reset at token t starts a new
+ * segment (the state entering token t is zero). */
+int32_t llmy_gdn_prefill_reset_bf16(const llmy_bf16* q, const llmy_bf16* k, const llmy_bf16* v,
+                                    const float* beta, const float* g, const int32_t* reset,
+                                    float* state, llmy_bf16* out, void* workspace,
+                                    int64_t workspace_bytes, int32_t B, int32_t T, int32_t H,
+                                    int32_t dk, int32_t dv, void* stream);
+
+/* llmy_gdn_step_bf16 with reset [B]: row b starts from a zero state. */
+int32_t llmy_gdn_step_reset_bf16(const llmy_bf16* q, const llmy_bf16* k, const llmy_bf16* v,
+                                 const float* beta, const float* g, const llmy_bf16* gate,
+                                 const int32_t* reset, float* state, llmy_bf16* out, int32_t B,
+                                 int32_t H, int32_t dk, int32_t dv, void* stream);
+
+/* llmy_gdn_step_fused_f32 with reset [B]: row b starts from a zero state and
+ * a zero conv history. */
+int32_t llmy_gdn_step_fused_reset_f32(const float* proj, int64_t proj_ld, int32_t nparts,
+                                      const float* beta_bias, const float* decay_logit,
+                                      const int32_t* reset, float* state, llmy_bf16* out,
+                                      const llmy_bf16* conv_h, llmy_bf16* conv_hist,
+                                      const float* conv_w, float* conv_out, int32_t D,
+                                      int32_t conv_kernel, int32_t B, int32_t H, int32_t dk,
+                                      int32_t dv, void* stream);
+
+/* llmy_gdn_conv_gate_prefill with reset [B, T]: the tap at position p counts
+ * for token t only if no reset lies in (p, t] (history taps: none in [0, t]);
+ * the new history is the last 3 inputs, zero where they precede the last
+ * reset (what a token-by-token pass leaves). */
+int32_t llmy_gdn_conv_gate_prefill_reset(const llmy_bf16* h, llmy_bf16* hist, const float* w,
+                                         const int32_t* reset, float* out, int32_t B, int32_t T,
+                                         int32_t D, int32_t kernel, void* stream);
+
+/* Zero row b of a [rows, row_bytes] buffer wherever mask[b] != 0 (device int32
+ * [rows]): the per-row state reset of model/recurrent_state.py:213-225 applied
+ * to one state buffer (GDN states, conv histories, KV rings, router latent
+ * rings, positions).  A kernel, so a captured graph may hold it; row_bytes a
+ * multiple of 4. */
+int32_t llmy_zero_rows(void* base, int64_t row_bytes, int32_t rows, const int32_t* mask,
+                       void* stream);
 
 /* --- Glue (model/layers/norms.py:13-16, model/model.py:386) --------------- */
 
@@ -476,6 +525,13 @@ int32_t llmy_prefill_batch(llmy_model* m, llmy_state* s, const int32_t* tokens,
 int32_t llmy_decode_batch(llmy_model* m, llmy_state* s, const int32_t* tokens,
                           const int32_t* positions, int32_t num_loops,
                           float* logits_out);
+/* Reset the rows of a batched state where mask[b] != 0 (host or device int32
+ * [batch]): their GDN states, conv histories, KV caches and router latent
+ * rings are zeroed and their next position is 0, the reset_rows of
+ * model/recurrent_state.py:213-225 that decode_step applies before a token
+ * whose reset_mask is set (model/model.py:814-822).  Other rows keep their
+ * state.  Returns 0 or 1 (see llmy_last_error). */
+int32_t llmy_state_reset_rows(llmy_state* s, const int32_t* mask);
 /* greedy (argmax) token of each row after the last forward into out [batch] */
 int32_t llmy_greedy_tokens(const llmy_state* s, int32_t* out);
 /* Status of the last engine call on this thread (0 ok) and its message — the

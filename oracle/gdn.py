@@ -15,12 +15,14 @@ from __future__ import annotations
 import torch
 
 
-def gdn_sequential(q, k, v, beta, g, state, gate=None, dtype=torch.float32):
+def gdn_sequential(q, k, v, beta, g, state, gate=None, dtype=torch.float32, reset=None):
     """Sequential recurrence over T, restating gated_deltanet.py:140-149.
 
     q, k [B,T,H,dk]; v [B,T,H,dv]; beta, g [B,T,H]; state [B,H,dk,dv];
     gate [B,T,H,dv] or None.  Arithmetic in ``dtype`` (fp32 as the reference;
-    fp64 for pinning).  Returns (o [B,T,H,dv], final state [B,H,dk,dv]).
+    fp64 for pinning).  ``reset`` [B,T] bool or None: where set, the state is
+    zeroed before token t's update (the carry reset of gated_deltanet.py:138-142).
+    Returns (o [B,T,H,dv], final state [B,H,dk,dv]).
     """
     B, T, H, dk = q.shape
     dv = v.shape[-1]
@@ -28,7 +30,10 @@ def gdn_sequential(q, k, v, beta, g, state, gate=None, dtype=torch.float32):
     qd, kd, vd = q.to(dtype), k.to(dtype), v.to(dtype)
     bd, gd = beta.to(dtype), g.to(dtype)
     out = torch.empty(B, T, H, dv, dtype=dtype)
+    rs = None if reset is None else torch.as_tensor(reset).to(torch.bool).view(B, T)
     for t in range(T):
+        if rs is not None:
+            S = torch.where(rs[:, t, None, None, None], torch.zeros_like(S), S)
         kt = kd[:, t]
         pred = torch.einsum("bhk,bhkv->bhv", kt, S)
         delta = vd[:, t] - pred
@@ -40,11 +45,32 @@ def gdn_sequential(q, k, v, beta, g, state, gate=None, dtype=torch.float32):
     return out, S
 
 
-def gdn_step(q, k, v, beta, g, state, gate=None, dtype=torch.float32):
-    """One-token update (T = 1) of ``gdn_sequential``; q,k,v [B,H,d], beta,g [B,H]."""
+def gdn_step(q, k, v, beta, g, state, gate=None, dtype=torch.float32, reset=None):
+    """One-token update (T = 1) of ``gdn_sequential``; q,k,v [B,H,d], beta,g [B,H];
+    reset [B] or None."""
     o, S = gdn_sequential(q[:, None], k[:, None], v[:, None], beta[:, None], g[:, None],
-                          state, None if gate is None else gate[:, None], dtype)
+                          state, None if gate is None else gate[:, None], dtype,
+                          None if reset is None else torch.as_tensor(reset).view(-1, 1))
     return o[:, 0], S
+
+
+def causal_conv_reset(h, hist, w, reset=None):
+    """Causal depthwise conv over a sequence with a carried history, restating
+    gated_deltanet.py:56-78 (taps do not cross a reset) token by token, the
+    decode rule of :257-270 (window = [history, h_t]; a reset clears the
+    history first).  h [B,T,D], hist [B,K-1,D], w [D,K]; reset [B,T] or None.
+    Returns (pre-sigmoid conv [B,T,D], new history [B,K-1,D])."""
+    B, T, D = h.shape
+    hist = hist.clone()
+    out = torch.empty(B, T, D, dtype=h.dtype)
+    rs = None if reset is None else torch.as_tensor(reset).to(torch.bool).view(B, T)
+    for t in range(T):
+        if rs is not None:
+            hist = torch.where(rs[:, t, None, None], torch.zeros_like(hist), hist)
+        window = torch.cat([hist, h[:, t:t + 1]], dim=1)      # [B, K, D]
+        out[:, t] = (window * w.t()[None]).sum(1)
+        hist = window[:, 1:]
+    return out, hist
 
 
 def gdn_chunked(q, k, v, beta, g, state, chunk=64, dtype=torch.float64):

@@ -116,7 +116,15 @@ class HybridOracle:
                                          w[p + "ctx_ln_w"], w[p + "ctx_ln_b"], cfg.eps)
             hist = torch.cat([s["lat"], lat[:, None]], dim=1)[:, -cfg.router_context:]
             s["lat"] = hist
-            ctx = hist.double().mean(1).float()
+            if "lat_n" in s:
+                # rows reset earlier hold fewer valid latents (the last n of the window)
+                n = (s["lat_n"] + 1).clamp(max=cfg.router_context)
+                s["lat_n"] = n
+                W = hist.shape[1]
+                ctx = torch.stack([hist[b, W - int(n[b]):].double().mean(0)
+                                   for b in range(hist.shape[0])]).float()
+            else:
+                ctx = hist.double().mean(1).float()
             logits = context_route_logits(local, ctx, w[p + "ctx_local_out"], w[p + "ctx_out"],
                                           w[p + "ctx_gate"], w[p + "w_router"], self.rnd)
         else:
@@ -170,9 +178,34 @@ class HybridOracle:
         hf = self.rnd(rmsnorm(x, self.w["final_norm"], self.cfg.eps))
         return hf @ self.w["embed"].t()
 
-    def step(self, tokens, st: dict, num_loops: int | None = None) -> torch.Tensor:
-        """Decode one token per sequence; returns fp32 logits [B, V]."""
+    def reset_rows(self, st: dict, mask) -> None:
+        """Rows b with mask[b] start a new sequence: their GDN states, conv
+        histories, KV caches and router latent histories are zeroed and their
+        position is 0 (RecurrentState.reset_rows, model/recurrent_state.py:213-225,
+        applied by decode_step before a token whose reset_mask is set,
+        model/model.py:814-822)."""
+        rows = torch.as_tensor(np.asarray(mask)).to(torch.bool).view(-1)
+        st["pos"] = torch.where(rows, torch.zeros_like(st["pos"]), st["pos"])
+        for key, s in st.items():
+            if key == "pos":
+                continue
+            for name in ("S", "hist", "k", "v"):
+                if name in s:
+                    s[name] = s[name].clone()
+                    s[name][rows] = 0
+            if self.cfg.context_router:
+                n = s.get("lat_n", torch.full((rows.numel(),), s["lat"].shape[1],
+                                              dtype=torch.long))
+                s["lat_n"] = torch.where(rows, torch.zeros_like(n), n)
+                s["lat"] = s["lat"].clone()
+                s["lat"][rows] = 0
+
+    def step(self, tokens, st: dict, num_loops: int | None = None, reset=None) -> torch.Tensor:
+        """Decode one token per sequence; returns fp32 logits [B, V].  ``reset``
+        [B]: those rows start a new sequence first (``reset_rows``)."""
         cfg = self.cfg
+        if reset is not None:
+            self.reset_rows(st, reset)
         pos = st["pos"].clone()
         x = self.embed(tokens)
         loops = cfg.num_loops if not num_loops else num_loops

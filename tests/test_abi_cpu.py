@@ -184,6 +184,7 @@ def test_gdn_prefill_noalloc_rejects_before_any_device_call(lib):
     assert f(*ptrs, 1, 64, 2, 96, 96, None) == INVALID                            # head size
     assert f(None, *ptrs[1:], 1, 64, 2, 64, 64, None) == INVALID
     assert f(*([None] * 7), 0, 64, 2, 64, 64, None) == 0                          # B = 0
-    # 832 chunks x 82 KB at dk = dv = 128: beyond the 64 MiB workspace
-    assert f(*ptrs, 1, 64 * 52, 16, 128, 128, None) == 2                         # hipErrorOutOfMemory
-    assert lib.llmy_gdn_prefill_workspace_bytes(1, 64 * 51, 16, 128, 128) <= 64 << 20
+    # 816 chunks x 82 KB at dk = dv = 128: beyond the 64 MiB workspace; 800 fit
+    assert f(*ptrs, 1, 64 * 51, 16, 128, 128, None) == 2                         # hipErrorOutOfMemory
+    assert lib.llmy_gdn_prefill_workspace_bytes(1, 64 * 51, 16, 128, 128) > 64 << 20
+    assert lib.llmy_gdn_prefill_workspace_bytes(1, 64 * 50, 16, 128, 128) <= 64 << 20

@@ -221,3 +221,47 @@ def test_graph_replay_with_sampling_matches_eager():
         assert torch.equal(lg, eager[i][0]), i
         assert torch.equal(b.buf["next"], eager[i][1]), i
         assert torch.equal(b.buf["sampled"], eager[i][2]), i
+
+
+def test_reset_rows_matches_oracle_and_graph():
+    """decode_step with a reset_mask (model/model.py:814-822): the reset rows'
+    GDN states, conv histories, KV caches and positions start over, the other
+    rows continue.  Engine vs the oracle's reset_rows with the engine's routing
+    replayed; the reset row also matches a fresh engine's row; a captured step
+    after an eager reset equals the eager engine bit for bit."""
+    cfg = replace(C1, layer_kinds=alternating(2))
+    w = init_weights(cfg, seed=11)
+    B = 3
+    toks = torch.randint(0, cfg.vocab, (9, B), generator=torch.Generator().manual_seed(12),
+                         dtype=torch.int32)
+    reset = torch.tensor([0, 1, 0], dtype=torch.int32)
+    ref = HybridOracle(cfg, w, act_bf16=True)
+    st = ref.new_state(B)
+    eng = engine(cfg, w, B)
+    eng.enable_route_log()
+    worst = 0.0
+    outs = []
+    for i in range(9):
+        r = reset if i == 6 else None
+        lg = eng.step(toks[i].cuda(), reset=None if r is None else r.cuda()).clone()
+        ref.forced_routes = [x for x in eng.route_log.cpu().numpy()]
+        lr = ref.step(toks[i].numpy(), st, reset=None if r is None else r.numpy())
+        worst = max(worst, rel_l2(lg, lr))
+        outs.append(lg)
+    _check_routes(ref)
+    assert eng.pos.cpu().tolist() == [9, 3, 9]
+    print(f"reset rows: worst step rel-L2 {worst:.2e}", flush=True)
+    assert worst <= REL_L2, worst
+    # row 1 after the reset = row 1 of a fresh engine fed the same tokens
+    fresh = engine(cfg, w, B)
+    for i in range(6, 9):
+        lf = fresh.step(toks[i].cuda())
+        d = float((lf[1] - outs[i][1]).abs().max())
+        assert d <= 1e-4 * float(lf[1].abs().max()), (i, d)
+    # graph: the reset runs eagerly between replays
+    g = engine(cfg, w, B)
+    g.capture()
+    for i in range(9):
+        out = g.step(toks[i].cuda(), reset=reset.cuda() if i == 6 else None).clone()
+        torch.cuda.synchronize()
+        assert torch.equal(out, outs[i]), i

@@ -225,6 +225,50 @@ def test_shared_experts_match_python_engine(lib, tmp_path):
         lib.llmy_free(m)
 
 
+def test_state_reset_rows_matches_python_engine(lib, tmp_path):
+    """llmy_state_reset_rows (RecurrentState.reset_rows before decode_step,
+    model/model.py:814-822) with the context router on, so the latent ring is
+    reset too: the next decodes (positions NULL: the reset row restarts at 0)
+    equal the Python engine's reset_rows + step bit for bit."""
+    from dataclasses import replace
+    from hybrid_llm_amd.engine import HybridDecoder
+    cfg = replace(C1, context_router=True, router_context=8, route_gate_init=0.0)
+    w = init_weights(cfg, seed=3)
+    path = tmp_path / "ctx_reset.llmy"
+    save_llmy(path, cfg, w)
+    B, T = 3, 12
+    prompt = torch.randint(0, cfg.vocab, (B, T), generator=torch.Generator().manual_seed(13),
+                           dtype=torch.int32)
+    print("[engine-api] reset rows: prefill 12 + decode 4 with a reset, B=3", flush=True)
+    m = lib.llmy_load(str(path).encode())
+    assert m, lib.llmy_last_error()
+    try:
+        s = lib.llmy_state_new_batch(m, B)
+        assert s
+        out = torch.zeros(B, cfg.vocab, device="cuda")
+        assert lib.llmy_prefill_batch(m, s, prompt.cuda().data_ptr(), T, out.data_ptr()) == 0
+        py = HybridDecoder(cfg, w, B)
+        assert torch.equal(out, py.prefill(prompt.cuda()))
+        mask = torch.tensor([0, 1, 1], dtype=torch.int32)
+        nxt = torch.zeros(B, dtype=torch.int32)
+        for i in range(4):
+            assert lib.llmy_greedy_tokens(s, nxt.data_ptr()) == 0
+            if i == 1:
+                assert lib.llmy_state_reset_rows(s, mask.data_ptr()) == 0       # host mask
+                py.reset_rows(mask.cuda())
+            if i == 3:
+                dmask = torch.tensor([1, 0, 0], dtype=torch.int32, device="cuda")
+                assert lib.llmy_state_reset_rows(s, dmask.data_ptr()) == 0      # device mask
+                py.reset_rows(dmask)
+            assert lib.llmy_decode_batch(m, s, nxt.data_ptr(), None, 0, out.data_ptr()) == 0
+            assert torch.equal(out, py.step(nxt.cuda())), i
+        assert py.pos.cpu().tolist() == [1, 3, 3]
+        assert lib.llmy_state_reset_rows(None, mask.data_ptr()) == 1
+        lib.llmy_state_free(s)
+    finally:
+        lib.llmy_free(m)
+
+
 def test_context_router_matches_python_engine(lib, tmp_path):
     """router.context_aware=1 (local latent window of 8 tokens, latent 256):
     the native engine's prefill and decode logits equal the Python engine's

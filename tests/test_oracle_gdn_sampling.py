@@ -3,7 +3,7 @@ import numpy as np
 import torch
 import torch.nn.functional as F
 
-from oracle.gdn import gdn_chunked, gdn_sequential, gdn_step
+from oracle.gdn import causal_conv_reset, gdn_chunked, gdn_sequential, gdn_step
 from oracle.sampling import argmax, top_p_error_bound, top_p_sample
 
 
@@ -74,6 +74,70 @@ def test_step_equals_one_token_scan():
     o1, S1 = gdn_sequential(q, k, v, beta, g, S0)
     o2, S2 = gdn_step(q[:, 0], k[:, 0], v[:, 0], beta[:, 0], g[:, 0], S0)
     assert torch.equal(o1[:, 0], o2) and torch.equal(S1, S2)
+
+
+def test_reset_restarts_from_zero_state():
+    # A reset before token t: tokens < t are unaffected, tokens >= t equal a
+    # fresh run of the suffix from S = 0 (gated_deltanet.py:138-142).
+    B, T = 3, 40
+    q, k, v, beta, g, S0 = _gdn_inputs(B, T, 2, 8, 6, 11, s0_std=1.0)
+    reset = torch.zeros(B, T, dtype=torch.bool)
+    reset[0, 17] = True
+    reset[1, 0] = True
+    reset[1, 25] = True                     # two resets in one row
+    o, S = gdn_sequential(q, k, v, beta, g, S0, dtype=torch.float64, reset=reset)
+    o_plain, S_plain = gdn_sequential(q, k, v, beta, g, S0, dtype=torch.float64)
+    assert torch.allclose(o[0, :17], o_plain[0, :17], atol=1e-12)
+    assert torch.equal(o[2], o_plain[2]) and torch.equal(S[2], S_plain[2])
+    for b, t in [(0, 17), (1, 25)]:
+        sl = slice(t, T)
+        o_s, S_s = gdn_sequential(q[b:b + 1, sl], k[b:b + 1, sl], v[b:b + 1, sl],
+                                  beta[b:b + 1, sl], g[b:b + 1, sl],
+                                  torch.zeros_like(S0[:1]), dtype=torch.float64)
+        assert torch.allclose(o[b:b + 1, sl], o_s, atol=1e-12)
+        assert torch.allclose(S[b:b + 1], S_s, atol=1e-12)
+    # a reset at t = 0 discards the given state for that row only
+    o_z, _ = gdn_sequential(q[1:2, :25], k[1:2, :25], v[1:2, :25], beta[1:2, :25],
+                            g[1:2, :25], torch.zeros_like(S0[:1]), dtype=torch.float64)
+    assert torch.allclose(o[1:2, :25], o_z, atol=1e-12)
+    # the step form with a per-row reset equals the one-token scan
+    o1, S1 = gdn_step(q[:, 0], k[:, 0], v[:, 0], beta[:, 0], g[:, 0], S0,
+                      reset=torch.tensor([True, False, True]))
+    o2, S2 = gdn_sequential(q[:, :1], k[:, :1], v[:, :1], beta[:, :1], g[:, :1], S0,
+                            reset=torch.tensor([[True], [False], [True]]))
+    assert torch.equal(o1, o2[:, 0]) and torch.equal(S1, S2)
+    assert torch.allclose(S1[0], torch.einsum("hk,hv->hkv", k[0, 0], beta[0, 0, :, None]
+                                              * v[0, 0]), atol=1e-6)
+
+
+def test_causal_conv_matches_library_conv_and_resets():
+    B, T, D, K = 2, 23, 5, 4
+    gen = torch.Generator().manual_seed(4)
+    h = torch.randn(B, T, D, generator=gen, dtype=torch.float64)
+    w = torch.randn(D, K, generator=gen, dtype=torch.float64)
+    hist0 = torch.zeros(B, K - 1, D, dtype=torch.float64)
+    out, hist = causal_conv_reset(h, hist0, w)
+    # zero history = the reference's left-padded depthwise Conv1d (gated_deltanet.py:65-66)
+    lib = F.conv1d(F.pad(h.transpose(1, 2), (K - 1, 0)), w[:, None, :], groups=D)
+    assert torch.allclose(out, lib.transpose(1, 2), atol=1e-12)
+    assert torch.equal(hist, h[:, -(K - 1):])
+    # the carried history makes a split run equal the whole run
+    o_a, h_a = causal_conv_reset(h[:, :9], hist0, w)
+    o_b, h_b = causal_conv_reset(h[:, 9:], h_a, w)
+    assert torch.allclose(torch.cat([o_a, o_b], 1), out, atol=1e-12) and torch.equal(h_b, hist)
+    # a reset at t: taps never reach before t (the masked taps of :67-78)
+    reset = torch.zeros(B, T, dtype=torch.bool)
+    reset[0, 10] = True
+    reset[1, 21] = True
+    o_r, h_r = causal_conv_reset(h, torch.randn(B, K - 1, D, dtype=torch.float64,
+                                                generator=gen), w, reset)
+    for b, t in [(0, 10), (1, 21)]:
+        o_s, h_s = causal_conv_reset(h[b:b + 1, t:], hist0[:1], w)
+        assert torch.allclose(o_r[b:b + 1, t:], o_s, atol=1e-12)
+        assert torch.equal(h_r[b:b + 1], h_s)
+    assert torch.allclose(o_r[0, 3:10], out[0, 3:10], atol=1e-12)   # beyond the old history
+    # a reset near the end leaves fewer than K-1 new tokens: the rest of the history is 0
+    assert torch.equal(h_r[1, 0], torch.zeros(D, dtype=torch.float64))
 
 
 def test_argmax_first_occurrence_and_nan():
