@@ -290,6 +290,111 @@ __global__ __launch_bounds__(512) void wsgemm_kernel(WsArgs a) {
   }
 }
 
+// Route-indexed MoE gate/up projection for decode (kRouteGather, packed
+// weights, a few 16-route chunks per expert): the arithmetic of
+// wsgemm_kernel<kSwiGLU, kRouteGather, packed, 1, 1, 8> (S waves, wave w takes
+// the 256-wide K blocks w, w + S, ...; partial sums meet in wave order), so the
+// two agree bit for bit, but every weight load of the workgroup is requested
+// first, before the route scan: the scan's round trip to the router's ids then
+// hides behind the weight stream instead of delaying it, and the weights stay
+// in registers for every 16-route chunk.  NP K blocks per wave.
+template <int NP>
+__global__ __launch_bounds__(512) void routed_gate_up_kernel(WsArgs a) {
+  extern __shared__ float red[];  // [S][8][64]: gate then up partial sums
+  __shared__ int32_t rlist[kMaxRouteList];
+  __shared__ int32_t rcount;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int S = blockDim.x >> 6;
+  const int e = blockIdx.y;
+  const int r = lane & 15;
+  const int g = lane >> 4;
+  const int K = a.K;
+  const uint16_t* wl = a.w + static_cast<long long>(e) * a.w_expert_stride +
+                       (static_cast<long long>(blockIdx.x) * (K >> 8) * 8 * 64 + lane) * 8;
+  uint4 bw[NP][8], bu[NP][8];
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    const long long kb = wave + p * S;  // 256-wide K block
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      bw[p][j] = ld_stream(wl + (kb * 8 + j) * 512);
+      bu[p][j] = ld_stream(wl + a.pair_offset + (kb * 8 + j) * 512);
+    }
+  }
+  if (wave == 0) {
+    int cnt = 0;
+    for (int c0 = 0; c0 < a.rows_total; c0 += 64) {
+      const int rr = c0 + lane;
+      const int id = rr < a.rows_total ? a.ids[rr] : -1;
+      const uint64_t m = __ballot(id == e);
+      if (id == e) rlist[cnt + __popcll(m & ((1ull << lane) - 1ull))] = rr;
+      cnt += __popcll(m);
+    }
+    if (lane == 0) rcount = cnt;
+  }
+  __syncthreads();
+  const int M = rcount;
+
+  for (int m0 = 0; m0 < M; m0 += 16) {
+    const bool valid = m0 + r < M;
+    const int src = rlist[valid ? m0 + r : m0] / a.route_k;
+    const uint16_t* xrow = a.x + static_cast<long long>(src) * a.ldx + 8 * g;
+    uint4 av[NP][8];
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      const int kb = (wave + p * S) * 256;
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        av[p][j] = valid ? *reinterpret_cast<const uint4*>(xrow + kb + 32 * j)
+                         : uint4{0u, 0u, 0u, 0u};
+    }
+    f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f}, accu = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(av[p][j]), as_bf16x8(bw[p][j]),
+                                                      acc, 0, 0, 0);
+        accu = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(av[p][j]), as_bf16x8(bu[p][j]),
+                                                       accu, 0, 0, 0);
+      }
+    }
+    if (S > 1) {
+      __syncthreads();  // the previous chunk's reduction has finished reading
+      if (wave > 0) {
+        float* dst = red + static_cast<size_t>(wave) * 8 * 64 + lane;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          dst[i * 64] = acc[i];
+          dst[(4 + i) * 64] = accu[i];
+        }
+      }
+      __syncthreads();
+      if (wave == 0) {
+        for (int w = 1; w < S; ++w) {
+          const float* sp = red + static_cast<size_t>(w) * 8 * 64 + lane;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            acc[i] += sp[i * 64];
+            accu[i] += sp[(4 + i) * 64];
+          }
+        }
+      }
+    }
+    if (wave != 0) continue;
+    // lane holds routes m0 + 4g + i, column 16 * blockIdx.x + r
+    const int n = 16 * blockIdx.x + r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int mm = m0 + 4 * g + i;
+      if (mm < M)
+        static_cast<uint16_t*>(a.out)[static_cast<long long>(rlist[mm]) * a.ldo + n] =
+            f2bf(siluf_(acc[i]) * accu[i]);
+    }
+  }
+}
+
 template <int EPI, int MODE, int MB, int KB = 1, int JT = 8>
 static int32_t launch_ws(const WsArgs& a, int grid_y, bool packed, hipStream_t s) {
   if (a.K % (32 * JT * KB) != 0) return launch_ws<EPI, MODE, MB, 1, 8>(a, grid_y, packed, s);
@@ -639,6 +744,24 @@ extern "C" int32_t llmy_moe_experts_routed_bf16(const llmy_bf16* x, const int32_
   b.N = D; b.K = H; b.ldx = H; b.ldo = D; b.route_k = k;
   b.rows_total = T * k; b.x_rows = T * k;
   int32_t st;
+  // Gate/up through routed_gate_up_kernel where its shape fits (packed
+  // weights, D in at most 8 waves of whole 256-wide blocks, 1, 2 or 4 per
+  // wave); the same arithmetic as the wsgemm configuration below.
+  const int kblk = D / 256, gu_waves = std::min(8, kblk), gu_np = kblk / gu_waves;
+  if (T * k <= 16 * E && packed && kblk % gu_waves == 0 &&
+      (gu_np == 1 || gu_np == 2 || gu_np == 4)) {
+    const size_t lds = static_cast<size_t>(gu_waves) * 8 * 64 * sizeof(float);
+    const dim3 grid(H / 16, E), block(64 * gu_waves);
+    if (gu_np == 1)
+      hipLaunchKernelGGL(routed_gate_up_kernel<1>, grid, block, lds, s, a);
+    else if (gu_np == 2)
+      hipLaunchKernelGGL(routed_gate_up_kernel<2>, grid, block, lds, s, a);
+    else
+      hipLaunchKernelGGL(routed_gate_up_kernel<4>, grid, block, lds, s, a);
+    st = launch_status();
+    if (st != 0) return st;
+    return launch_ws<kMoeDown, kRouteDirect, 1, 1, 4>(b, E, packed, s);
+  }
   if (T * k <= 16 * E) {
     st = launch_ws<kSwiGLU, kRouteGather, 1>(a, E, packed, s);
     if (st != 0) return st;
