@@ -58,6 +58,10 @@ def parse():
     ap.add_argument("--no-kernels", action="store_true", help="skip the per-kernel table")
     ap.add_argument("--kernel-iters", type=int, default=100)
     ap.add_argument("--pmc-child", action="store_true", help=argparse.SUPPRESS)
+    ap.add_argument("--only", default=None,
+                    help="comma-separated kernel-table rows to run alone (after a 512 MiB "
+                         "device copy that calibrates HBM counters), e.g. attn_prefill; "
+                         "prints those rows as JSON and exits")
     return ap.parse_args()
 
 
@@ -172,6 +176,21 @@ def time_attn_decode(cfg, B, iters, gen):
 
 
 # --------------------------------------------------------------------------- HBM traffic
+def copy_calibration():
+    """Three plain device copies of COPY_BYTES: a counter run divides a kernel's
+    FETCH_SIZE / WRITE_SIZE by these launches' reading per byte copied."""
+    import torch
+    gen = torch.Generator(device="cuda").manual_seed(1)
+    src = torch.empty(COPY_BYTES // 4, dtype=torch.float32, device="cuda").normal_(generator=gen)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+    torch.cuda.empty_cache()
+
+
 def pmc_child():
     """Run under ``rocprofv3 --pmc``: a plain device copy of COPY_BYTES (the
     calibration), then the dominant kernel at the bench shape."""
@@ -250,11 +269,17 @@ def n_sets(bytes_per_set: float, minimum: int = 3) -> int:
     return max(minimum, int(MALL_BYTES // max(bytes_per_set, 1)) + 1)
 
 
-def kernel_table(cfg, B, gen, iters):
+KERNEL_ROWS = ("moe_decode_experts", "lm_head", "gdn_decode_step", "gdn_decode_step_c4",
+               "sample_argmax", "sample_top_p", "moe_prefill_layer", "moe_prefill_experts",
+               "dense_prefill_gemm", "attn_prefill", "gdn_prefill")
+
+
+def kernel_table(cfg, B, gen, iters, only=None):
     """Per-kernel roofline fractions for the kernels the metric names.  Every
     row: HIP events around each launch on the launch stream, 10 warmup
     launches, mean and median over ``iters``; bandwidth-bound rows rotate
-    input sets totalling more than the 256 MB Infinity Cache."""
+    input sets totalling more than the 256 MB Infinity Cache.  ``only``: the
+    row names to run (each row sets up its own inputs)."""
     import torch
     import torch.nn.functional as F
     from hybrid_llm_amd import _lib, ops
@@ -282,135 +307,182 @@ def kernel_table(cfg, B, gen, iters):
                       "median_us": round(med, 2)}
 
     D, E, Hf, k = cfg.d_model, cfg.n_experts, cfg.expert_hidden, cfg.top_k
-    # MoE decode (C2 decode variant / one C5 MoE application): packed expert
-    # weights (302 MB per set, 3 rotated sets); bytes = weights of the experts
-    # the routes touch
-    wsets = [(ops.pack_weights((torch.randn(E, 2 * Hf, D, device="cuda", generator=gen) * 0.02)
-                               .bfloat16()),
-              ops.pack_weights((torch.randn(E, D, Hf, device="cuda", generator=gen) * 0.02)
-                               .bfloat16())) for _ in range(3)]
-    x = torch.randn(B, D, device="cuda", generator=gen)
-    wr = torch.randn(E, D, device="cuda", generator=gen) * 0.02
-    ones = torch.ones(D, device="cuda")
-    bufs = ops.moe_route_decode(x, ones, ones, wr, k)
-    act = torch.empty(B * k, Hf, dtype=torch.bfloat16, device="cuda")
-    y = torch.empty(B * k, D, device="cuda")
-    n_active = int((bufs["counts"] > 0).sum())
-    t = event_time(lambda i: ops.moe_experts_routed(bufs["h"], bufs["idx"], bufs["gates"],
-                                                    *wsets[i % 3], act=act, y=y,
-                                                    layout=ops.LAYOUT_PACKED), iters)
-    hbm("moe_decode_experts", t, n_active * 3 * Hf * D * 2 + B * D * 2 + B * k * D * 4,
-        f"T={B}, D={D}, E={E}, top-{k}, H={Hf}; {n_active} experts active, 3 weight sets")
-    del wsets
-    # GDN decode step at the C5 head shape (dk = dv = 64): the fused step of
-    # the engine (projection row in, conv gate, state in place)
     Hg, dk, dv = cfg.gdn_heads, cfg.gdn_dk, cfg.gdn_dv
-    nproj = 2 * Hg * dk + Hg * dv + D + Hg
-    sb = B * Hg * dk * dv * 4
-    ns = n_sets(sb)
-    Ss = [torch.randn(B, Hg, dk, dv, device="cuda", generator=gen) * 0.1 for _ in range(ns)]
-    proj = torch.randn(B, nproj, device="cuda", generator=gen)
-    go = torch.empty(B, Hg * dv, dtype=torch.bfloat16, device="cuda")
-    zb, dec = torch.zeros(Hg, device="cuda"), torch.full((Hg,), 2.0, device="cuda")
-    t = event_time(lambda i: ops.gdn_step_fused(proj, zb, dec, Ss[i % ns], out=go), iters)
-    hbm("gdn_decode_step", t, 2 * sb + B * nproj * 4 + B * Hg * dv * 2,
-        f"C5 shape: B={B}, H={Hg}, dk=dv={dk}, fp32 state, {ns} rotated states "
-        f"({ns * sb / 1e6:.0f} MB)")
-    del Ss
-    # GDN decode step, BASELINE config 4's decode variant: B=64, H=16,
-    # dk = dv = 128 (134 MB of state read + written)
-    B4, H4, d4 = 64, 16, 128
-    sb = B4 * H4 * d4 * d4 * 4
-    ns = n_sets(sb)
-    Ss = [torch.randn(B4, H4, d4, d4, device="cuda", generator=gen) * 0.1 for _ in range(ns)]
-    q4 = F.normalize(torch.randn(B4, H4, d4, device="cuda", generator=gen), dim=-1).bfloat16()
-    k4 = F.normalize(torch.randn(B4, H4, d4, device="cuda", generator=gen), dim=-1).bfloat16()
-    v4 = torch.randn(B4, H4, d4, device="cuda", generator=gen).bfloat16()
-    b4 = torch.sigmoid(torch.randn(B4, H4, device="cuda", generator=gen))
-    g4 = torch.exp(-F.softplus(torch.randn(B4, H4, device="cuda", generator=gen)))
-    o4 = torch.empty(B4, H4, d4, dtype=torch.bfloat16, device="cuda")
-    t = event_time(lambda i: ops.gdn_step(q4, k4, v4, b4, g4, Ss[i % ns], out=o4), iters)
-    hbm("gdn_decode_step_c4", t, 2 * sb + 4 * B4 * H4 * d4 * 2 + 2 * B4 * H4 * 4,
-        f"C4 decode: B={B4}, H={H4}, dk=dv={d4}, fp32 state, {ns} rotated states "
-        f"({ns * sb / 1e6:.0f} MB)")
-    del Ss
-    # sampling over [64, 32000] fp32 logits (8.2 MB per set, rotated)
     V = cfg.vocab
-    lb = B * V * 4
-    ns = n_sets(lb)
-    lsets = [torch.randn(B, V, device="cuda", generator=gen) * 0.6 for _ in range(ns)]
-    us_ = torch.rand(B, device="cuda", generator=gen)
-    so = torch.empty(B, dtype=torch.int32, device="cuda")
-    strm = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
-    t = event_time(lambda i: _lib.call("llmy_sample_argmax_f32", lsets[i % ns].data_ptr(), B, V,
-                                       so.data_ptr(), strm()), iters)
-    latency("sample_argmax", t, f"greedy argmax over [{B}, {V}] fp32, {ns} rotated logit sets")
-    t = event_time(lambda i: _lib.call("llmy_sample_top_p_f32", lsets[i % ns].data_ptr(), B, V,
-                                       SAMPLING[0], SAMPLING[2], SAMPLING[1], us_.data_ptr(),
-                                       so.data_ptr(), strm()), iters)
-    latency("sample_top_p", t, f"T={SAMPLING[0]}, top-p={SAMPLING[1]} draw over [{B}, {V}] fp32, "
-                               f"{ns} rotated logit sets")
-    del lsets
-    # MoE prefill (C2): router -> permute -> grouped experts -> combine
     it_mfma = max(10, iters // 5)
+    strm = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
+
+    def moe_decode_experts():
+        # one C5 MoE application at decode: packed expert weights (302 MB per
+        # set, 3 rotated sets); bytes = weights of the experts the routes touch
+        wsets = [(ops.pack_weights((torch.randn(E, 2 * Hf, D, device="cuda", generator=gen)
+                                    * 0.02).bfloat16()),
+                  ops.pack_weights((torch.randn(E, D, Hf, device="cuda", generator=gen)
+                                    * 0.02).bfloat16())) for _ in range(3)]
+        x = torch.randn(B, D, device="cuda", generator=gen)
+        wr = torch.randn(E, D, device="cuda", generator=gen) * 0.02
+        ones = torch.ones(D, device="cuda")
+        bufs = ops.moe_route_decode(x, ones, ones, wr, k)
+        act = torch.empty(B * k, Hf, dtype=torch.bfloat16, device="cuda")
+        y = torch.empty(B * k, D, device="cuda")
+        n_active = int((bufs["counts"] > 0).sum())
+        t = event_time(lambda i: ops.moe_experts_routed(bufs["h"], bufs["idx"], bufs["gates"],
+                                                        *wsets[i % 3], act=act, y=y,
+                                                        layout=ops.LAYOUT_PACKED), iters)
+        hbm("moe_decode_experts", t, n_active * 3 * Hf * D * 2 + B * D * 2 + B * k * D * 4,
+            f"T={B}, D={D}, E={E}, top-{k}, H={Hf}; {n_active} experts active, 3 weight sets")
+
+    def lm_head():
+        # the tied LM head of the decode step: [B, D] bf16 x packed [V, D] -> fp32 logits
+        wb = V * D * 2
+        ns = n_sets(wb)
+        heads = [ops.pack_weights((torch.randn(V, D, device="cuda", generator=gen) * 0.02)
+                                  .bfloat16()) for _ in range(ns)]
+        hx = torch.randn(B, D, device="cuda", generator=gen).bfloat16()
+        lo = torch.empty(B, V, device="cuda")
+        t = event_time(lambda i: ops.linear(hx, heads[i % ns], out=lo, epilogue=ops.EPI_STORE_F32,
+                                            layout=ops.LAYOUT_PACKED), iters)
+        hbm("lm_head", t, wb + B * D * 2 + B * V * 4,
+            f"B={B} rows x [{V}, {D}] packed bf16 weights -> fp32 logits, {ns} rotated weight sets")
+
+    def gdn_decode_step():
+        # the fused step of the engine at the C5 head shape (dk = dv = 64):
+        # projection row in, conv gate, state in place
+        nproj = 2 * Hg * dk + Hg * dv + D + Hg
+        sb = B * Hg * dk * dv * 4
+        ns = n_sets(sb)
+        Ss = [torch.randn(B, Hg, dk, dv, device="cuda", generator=gen) * 0.1 for _ in range(ns)]
+        proj = torch.randn(B, nproj, device="cuda", generator=gen)
+        go = torch.empty(B, Hg * dv, dtype=torch.bfloat16, device="cuda")
+        zb, dec = torch.zeros(Hg, device="cuda"), torch.full((Hg,), 2.0, device="cuda")
+        t = event_time(lambda i: ops.gdn_step_fused(proj, zb, dec, Ss[i % ns], out=go), iters)
+        hbm("gdn_decode_step", t, 2 * sb + B * nproj * 4 + B * Hg * dv * 2,
+            f"C5 shape: B={B}, H={Hg}, dk=dv={dk}, fp32 state, {ns} rotated states "
+            f"({ns * sb / 1e6:.0f} MB)")
+
+    def gdn_decode_step_c4():
+        # BASELINE config 4's decode variant: B=64, H=16, dk = dv = 128
+        # (134 MB of state read + written)
+        B4, H4, d4 = 64, 16, 128
+        sb = B4 * H4 * d4 * d4 * 4
+        ns = n_sets(sb)
+        Ss = [torch.randn(B4, H4, d4, d4, device="cuda", generator=gen) * 0.1 for _ in range(ns)]
+        q4 = F.normalize(torch.randn(B4, H4, d4, device="cuda", generator=gen), dim=-1).bfloat16()
+        k4 = F.normalize(torch.randn(B4, H4, d4, device="cuda", generator=gen), dim=-1).bfloat16()
+        v4 = torch.randn(B4, H4, d4, device="cuda", generator=gen).bfloat16()
+        b4 = torch.sigmoid(torch.randn(B4, H4, device="cuda", generator=gen))
+        g4 = torch.exp(-F.softplus(torch.randn(B4, H4, device="cuda", generator=gen)))
+        o4 = torch.empty(B4, H4, d4, dtype=torch.bfloat16, device="cuda")
+        t = event_time(lambda i: ops.gdn_step(q4, k4, v4, b4, g4, Ss[i % ns], out=o4), iters)
+        hbm("gdn_decode_step_c4", t, 2 * sb + 4 * B4 * H4 * d4 * 2 + 2 * B4 * H4 * 4,
+            f"C4 decode: B={B4}, H={H4}, dk=dv={d4}, fp32 state, {ns} rotated states "
+            f"({ns * sb / 1e6:.0f} MB)")
+
+    def _logit_sets():
+        ns = n_sets(B * V * 4)
+        return ns, [torch.randn(B, V, device="cuda", generator=gen) * 0.6 for _ in range(ns)]
+
+    def sample_argmax():
+        ns, lsets = _logit_sets()
+        so = torch.empty(B, dtype=torch.int32, device="cuda")
+        t = event_time(lambda i: _lib.call("llmy_sample_argmax_f32", lsets[i % ns].data_ptr(), B,
+                                           V, so.data_ptr(), strm()), iters)
+        latency("sample_argmax", t, f"greedy argmax over [{B}, {V}] fp32, {ns} rotated logit sets")
+
+    def sample_top_p():
+        ns, lsets = _logit_sets()
+        us_ = torch.rand(B, device="cuda", generator=gen)
+        so = torch.empty(B, dtype=torch.int32, device="cuda")
+        t = event_time(lambda i: _lib.call("llmy_sample_top_p_f32", lsets[i % ns].data_ptr(), B,
+                                           V, SAMPLING[0], SAMPLING[2], SAMPLING[1],
+                                           us_.data_ptr(), so.data_ptr(), strm()), iters)
+        latency("sample_top_p", t, f"T={SAMPLING[0]}, top-p={SAMPLING[1]} draw over [{B}, {V}] "
+                                   f"fp32, {ns} rotated logit sets")
+
     T2 = 4096
-    x2 = torch.randn(T2, D, device="cuda", generator=gen).bfloat16()
-    wr2 = torch.randn(E, D, device="cuda", generator=gen) * 0.02
-    esets = [((torch.randn(E, 2 * Hf, D, device="cuda", generator=gen) * 0.02).bfloat16(),
-              (torch.randn(E, D, Hf, device="cuda", generator=gen) * 0.02).bfloat16())
-             for _ in range(2)]
-    t = event_time(lambda i: ops.moe_forward(x2, wr2, *esets[i % 2], k), it_mfma)
-    mfma("moe_prefill_layer", t, 2 * T2 * k * (D * 2 * Hf + Hf * D),
-         f"C2: T={T2}, D={D}, E={E}, top-{k}, H={Hf} (router+permute+experts+combine), "
-         f"2 weight sets")
-    # the grouped expert GEMMs alone (C2 shape, routes from the router above)
-    idx2, gates2 = ops.router_topk(x2, wr2, k)
-    perm2 = ops.moe_permute(idx2.view(-1), E)
-    act2 = torch.empty(T2 * k, Hf, dtype=torch.bfloat16, device="cuda")
-    y2 = torch.empty(T2 * k, D, device="cuda")
-    t = event_time(lambda i: ops.moe_experts(x2, perm2, gates2, *esets[i % 2], act=act2, y=y2),
-                   it_mfma)
-    mfma("moe_prefill_experts", t, 2 * T2 * k * (D * 2 * Hf + Hf * D),
-         f"C2 grouped GEMMs only: {T2 * k} routes, gate_up+SwiGLU then down, 2 weight sets")
-    del x2, esets, act2, y2
-    # dense prefill projection: the C5 GDN input projection over 4096 tokens
-    nprj = 2 * Hg * dk + 2 * Hg * dv + Hg
-    nprj += (-nprj) % 16
-    xs = torch.randn(4096, D, device="cuda", generator=gen).bfloat16()
-    wps = [ops.pack_weights((torch.randn(nprj, D, device="cuda", generator=gen) * 0.02).bfloat16())
-           for _ in range(2)]
-    po = torch.empty(4096, nprj, device="cuda")
-    t = event_time(lambda i: ops.linear(xs, wps[i % 2], out=po, epilogue=ops.EPI_STORE_F32,
-                                        layout=ops.LAYOUT_PACKED), it_mfma)
-    mfma("dense_prefill_gemm", t, 2 * 4096 * nprj * D,
-         f"C5 GDN projection over 4096 tokens: M=4096, N={nprj}, K={D}, packed weights")
-    del xs, wps, po
-    # attention prefill (C3)
-    Bq, Tq, Hq, hq, Wq = 4, 8192, 16, 64, 512
-    qkv = [torch.randn(Bq, Tq, Hq, hq, device="cuda", generator=gen).bfloat16() for _ in range(3)]
-    ao = torch.empty_like(qkv[0])
-    t = event_time(lambda i: ops.banded_attn_prefill(*qkv, Wq, out=ao), it_mfma)
-    pairs = sum(min(t_ + 1, Wq) for t_ in range(Tq))
-    mfma("attn_prefill", t, 4 * Bq * Hq * hq * pairs,
-         f"C3: B={Bq}, T={Tq}, H={Hq}, hd={hq}, window={Wq}")
-    del qkv, ao
-    # GDN prefill (C4): chunked gated delta rule
-    Bg, Tg, Hg4, d4 = 8, 4096, 16, 128
-    gq = F.normalize(torch.randn(Bg, Tg, Hg4, d4, device="cuda", generator=gen), dim=-1).bfloat16()
-    gk = F.normalize(torch.randn(Bg, Tg, Hg4, d4, device="cuda", generator=gen), dim=-1).bfloat16()
-    gv = torch.randn(Bg, Tg, Hg4, d4, device="cuda", generator=gen).bfloat16()
-    gb = torch.sigmoid(torch.randn(Bg, Tg, Hg4, device="cuda", generator=gen))
-    gg = torch.exp(-F.softplus(torch.randn(Bg, Tg, Hg4, device="cuda", generator=gen)))
-    gS = torch.zeros(Bg, Hg4, d4, d4, device="cuda")
-    go4 = torch.empty(Bg, Tg, Hg4, d4, dtype=torch.bfloat16, device="cuda")
-    nb = int(_lib.load().llmy_gdn_prefill_workspace_bytes(Bg, Tg, Hg4, d4, d4))
-    ws = torch.empty(max(nb, 1), dtype=torch.uint8, device="cuda")
-    t = event_time(lambda i: ops.gdn_prefill(gq, gk, gv, gb, gg, gS, out=go4, workspace=ws), 10,
-                   warm=2)
-    bytes4 = 4 * Bg * Tg * Hg4 * d4 * 2 + 2 * Bg * Tg * Hg4 * 4 + 2 * Bg * Hg4 * d4 * d4 * 4
-    hbm("gdn_prefill", t, bytes4, f"C4: B={Bg}, T={Tg}, H={Hg4}, dk=dv={d4}, chunk 64")
-    del gq, gk, gv, go4, ws
-    torch.cuda.empty_cache()
+
+    def _moe_prefill_inputs():
+        # C2 (T=4096) with the engine's packed expert weights, 2 rotated sets
+        x2 = torch.randn(T2, D, device="cuda", generator=gen).bfloat16()
+        wr2 = torch.randn(E, D, device="cuda", generator=gen) * 0.02
+        esets = [(ops.pack_weights((torch.randn(E, 2 * Hf, D, device="cuda", generator=gen)
+                                    * 0.02).bfloat16()),
+                  ops.pack_weights((torch.randn(E, D, Hf, device="cuda", generator=gen)
+                                    * 0.02).bfloat16())) for _ in range(2)]
+        return x2, wr2, esets
+
+    def moe_prefill_layer():
+        x2, wr2, esets = _moe_prefill_inputs()
+        t = event_time(lambda i: ops.moe_forward(x2, wr2, *esets[i % 2], k,
+                                                 layout=ops.LAYOUT_PACKED), it_mfma)
+        mfma("moe_prefill_layer", t, 2 * T2 * k * (D * 2 * Hf + Hf * D),
+             f"C2: T={T2}, D={D}, E={E}, top-{k}, H={Hf} (router+permute+experts+combine), "
+             f"packed weights, 2 weight sets")
+
+    def moe_prefill_experts():
+        x2, wr2, esets = _moe_prefill_inputs()
+        idx2, gates2 = ops.router_topk(x2, wr2, k)
+        perm2 = ops.moe_permute(idx2.view(-1), E)
+        act2 = torch.empty(T2 * k, Hf, dtype=torch.bfloat16, device="cuda")
+        y2 = torch.empty(T2 * k, D, device="cuda")
+        t = event_time(lambda i: ops.moe_experts(x2, perm2, gates2, *esets[i % 2], act=act2, y=y2,
+                                                 layout=ops.LAYOUT_PACKED), it_mfma)
+        mfma("moe_prefill_experts", t, 2 * T2 * k * (D * 2 * Hf + Hf * D),
+             f"C2 grouped GEMMs only: {T2 * k} routes, gate_up+SwiGLU then down, packed "
+             f"weights, 2 weight sets")
+
+    def dense_prefill_gemm():
+        # the C5 GDN input projection over 4096 tokens
+        nprj = 2 * Hg * dk + 2 * Hg * dv + Hg
+        nprj += (-nprj) % 16
+        xs = torch.randn(4096, D, device="cuda", generator=gen).bfloat16()
+        wps = [ops.pack_weights((torch.randn(nprj, D, device="cuda", generator=gen) * 0.02)
+                                .bfloat16()) for _ in range(2)]
+        po = torch.empty(4096, nprj, device="cuda")
+        t = event_time(lambda i: ops.linear(xs, wps[i % 2], out=po, epilogue=ops.EPI_STORE_F32,
+                                            layout=ops.LAYOUT_PACKED), it_mfma)
+        mfma("dense_prefill_gemm", t, 2 * 4096 * nprj * D,
+             f"C5 GDN projection over 4096 tokens: M=4096, N={nprj}, K={D}, packed weights")
+
+    def attn_prefill():
+        Bq, Tq, Hq, hq, Wq = 4, 8192, 16, 64, 512
+        qkv = [torch.randn(Bq, Tq, Hq, hq, device="cuda", generator=gen).bfloat16()
+               for _ in range(3)]
+        ao = torch.empty_like(qkv[0])
+        t = event_time(lambda i: ops.banded_attn_prefill(*qkv, Wq, out=ao), it_mfma)
+        pairs = sum(min(t_ + 1, Wq) for t_ in range(Tq))
+        mfma("attn_prefill", t, 4 * Bq * Hq * hq * pairs,
+             f"C3: B={Bq}, T={Tq}, H={Hq}, hd={hq}, window={Wq}")
+
+    def gdn_prefill():
+        # C4: chunked gated delta rule
+        Bg, Tg, Hg4, d4 = 8, 4096, 16, 128
+        gq = F.normalize(torch.randn(Bg, Tg, Hg4, d4, device="cuda", generator=gen),
+                         dim=-1).bfloat16()
+        gk = F.normalize(torch.randn(Bg, Tg, Hg4, d4, device="cuda", generator=gen),
+                         dim=-1).bfloat16()
+        gv = torch.randn(Bg, Tg, Hg4, d4, device="cuda", generator=gen).bfloat16()
+        gb = torch.sigmoid(torch.randn(Bg, Tg, Hg4, device="cuda", generator=gen))
+        gg = torch.exp(-F.softplus(torch.randn(Bg, Tg, Hg4, device="cuda", generator=gen)))
+        gS = torch.zeros(Bg, Hg4, d4, d4, device="cuda")
+        go4 = torch.empty(Bg, Tg, Hg4, d4, dtype=torch.bfloat16, device="cuda")
+        nb = int(_lib.load().llmy_gdn_prefill_workspace_bytes(Bg, Tg, Hg4, d4, d4))
+        ws = torch.empty(max(nb, 1), dtype=torch.uint8, device="cuda")
+        t = event_time(lambda i: ops.gdn_prefill(gq, gk, gv, gb, gg, gS, out=go4, workspace=ws),
+                       10, warm=2)
+        bytes4 = 4 * Bg * Tg * Hg4 * d4 * 2 + 2 * Bg * Tg * Hg4 * 4 + 2 * Bg * Hg4 * d4 * d4 * 4
+        hbm("gdn_prefill", t, bytes4, f"C4: B={Bg}, T={Tg}, H={Hg4}, dk=dv={d4}, chunk 64")
+
+    fns = {"moe_decode_experts": moe_decode_experts, "lm_head": lm_head,
+           "gdn_decode_step": gdn_decode_step,
+           "gdn_decode_step_c4": gdn_decode_step_c4, "sample_argmax": sample_argmax,
+           "sample_top_p": sample_top_p, "moe_prefill_layer": moe_prefill_layer,
+           "moe_prefill_experts": moe_prefill_experts, "dense_prefill_gemm": dense_prefill_gemm,
+           "attn_prefill": attn_prefill, "gdn_prefill": gdn_prefill}
+    for name in KERNEL_ROWS:
+        if only is None or name in only:
+            fns[name]()
+            torch.cuda.empty_cache()
     return rows
 
 
@@ -530,6 +602,20 @@ def main():
         sys.exit(2)
     if args.pmc_child:
         pmc_child()
+        return
+    if args.only:
+        only = [r.strip() for r in args.only.split(",") if r.strip()]
+        unknown = [r for r in only if r not in KERNEL_ROWS]
+        if unknown:
+            print(json.dumps({"error": f"unknown rows {unknown}; rows: {list(KERNEL_ROWS)}"}))
+            sys.exit(2)
+        import torch
+        from hybrid_llm_amd.config import C5
+        torch.cuda.set_device(0)
+        gen = torch.Generator(device="cuda").manual_seed(0)
+        copy_calibration()
+        rows = kernel_table(C5, 64, gen, args.kernel_iters, only=only)
+        print(json.dumps(rows))
         return
     # the counter passes run as child processes before this process touches the GPU
     traffic = None if args.no_traffic else measure_traffic()

@@ -99,6 +99,11 @@ __global__ __launch_bounds__(512) void wsgemm_kernel(WsArgs a) {
   constexpr bool kRouted = (MODE == kRouteGather || MODE == kRouteDirect);
   __shared__ int32_t rlist[kRouted ? kMaxRouteList : 1];
   __shared__ int32_t rcount;
+  if (MODE == kDense && !kSplit && gridDim.y > 1) {
+    // dense rows split over the grid's y dimension, kRows per workgroup
+    row_begin = static_cast<int>(blockIdx.y) * kRows;
+    M = min(kRows, a.M - row_begin);
+  }
   if (MODE == kMoeGather || MODE == kMoeDirect) {
     // Clamp the (device-resident) offsets so a corrupt permutation cannot
     // move any access out of bounds.
@@ -290,6 +295,13 @@ __global__ __launch_bounds__(512) void wsgemm_kernel(WsArgs a) {
   }
 }
 
+// Dense out[M, N] = x[M, K] . w[N, K]^T for a narrow N (a few 16-row weight
+// blocks) and many rows: the weight-streaming kernel with its rows split over
+// the grid (16 per workgroup), out row stride ldo.  epi uses the Epilogue
+// numbering (store bf16 / fp32, residual add, gated residual add).
+int32_t dense_narrow_ws(const uint16_t* x, const uint16_t* w, void* out, const float* aux, int M,
+                        int N, int K, int ldo, int epi, bool packed, hipStream_t s);
+
 // Route-indexed MoE gate/up projection for decode (kRouteGather, packed
 // weights, a few 16-route chunks per expert): the arithmetic of
 // wsgemm_kernel<kSwiGLU, kRouteGather, packed, 1, 1, 8> (S waves, wave w takes
@@ -408,6 +420,30 @@ static int32_t launch_ws(const WsArgs& a, int grid_y, bool packed, hipStream_t s
   else
     hipLaunchKernelGGL((wsgemm_kernel<EPI, MODE, false, MB, KB, JT>), grid, block, lds, s, a);
   return launch_status();
+}
+
+int32_t dense_narrow_ws(const uint16_t* x, const uint16_t* w, void* out, const float* aux, int M,
+                        int N, int K, int ldo, int epi, bool packed, hipStream_t s) {
+  WsArgs a{};
+  a.x = x; a.w = w; a.out = out; a.aux = aux;
+  a.M = M; a.N = N; a.K = K; a.ldx = K; a.ldo = ldo;
+  if ((M + 15) / 16 > 65535) {  // more rows than the grid's y dimension takes: 64 per workgroup
+    const int gy = (M + 63) / 64;
+    if (gy > 65535) return static_cast<int32_t>(hipErrorInvalidValue);
+    switch (epi) {
+      case kStoreBf16: return launch_ws<kStoreBf16, kDense, 4>(a, gy, packed, s);
+      case kStoreF32: return launch_ws<kStoreF32, kDense, 4>(a, gy, packed, s);
+      case kResidAdd: return launch_ws<kResidAdd, kDense, 4>(a, gy, packed, s);
+      default: return launch_ws<kResidGated, kDense, 4>(a, gy, packed, s);
+    }
+  }
+  const int grid_y = (M + 15) / 16;
+  switch (epi) {
+    case kStoreBf16: return launch_ws<kStoreBf16, kDense, 1>(a, grid_y, packed, s);
+    case kStoreF32: return launch_ws<kStoreF32, kDense, 1>(a, grid_y, packed, s);
+    case kResidAdd: return launch_ws<kResidAdd, kDense, 1>(a, grid_y, packed, s);
+    default: return launch_ws<kResidGated, kDense, 1>(a, grid_y, packed, s);
+  }
 }
 
 // Dense GEMM for large N (the tied LM head): one workgroup owns 64 weight rows

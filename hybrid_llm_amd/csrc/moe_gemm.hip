@@ -567,6 +567,9 @@ int32_t moe_gemm_prefill(const uint16_t* x, const int32_t* offsets, const int32_
   return launch_tiles<kTileDown, BM, 128, 64, 2, 0, 2>(d, max_mtiles * d.n_tiles, s);
 }
 
+int32_t dense_narrow_ws(const uint16_t* x, const uint16_t* w, void* out, const float* aux, int M,
+                        int N, int K, int ldo, int epi, bool packed, hipStream_t s);
+
 // Dense out[M, N] (epilogue epi) = x[M, K] . w[N, K]^T.  Validated by the
 // caller: M >= 1, N >= 1, K % 256 == 0, 16-byte aligned x and w, aux given
 // for the gated epilogue.
@@ -618,19 +621,15 @@ int32_t dense_gemm_mfma(const uint16_t* x, const uint16_t* w, void* out, const f
   }
     LLMY_DENSE_T(256, 1, t, main_items)
     if (st != 0) return st;
-    // the tail: rows n_main .. N-1 of w (for the packed order too: 16-row
-    // groups are contiguous), output columns n_main .. N-1
-    TileArgs u = g;
-    u.w = w + static_cast<long long>(n_main) * K;
-    u.out = static_cast<char*>(out) + static_cast<long long>(n_main) * (epi == kDenseBf16 ? 2 : 4);
-    u.aux = aux ? aux + n_main : nullptr;
-    u.N = tail;
-    u.m_tiles = (M + 127) / 128;
-    u.n_tiles = 1;
-    u.group_m = 4;
-    LLMY_DENSE_T(128, 2, u, static_cast<long long>(u.m_tiles))
 #undef LLMY_DENSE_T
-    return st;
+    // the tail: rows n_main .. N-1 of w (for the packed order too: 16-row
+    // groups are contiguous), output columns n_main .. N-1, through the
+    // weight-streaming kernel with the rows split 16 per workgroup (a tile
+    // launch would spend a 128-wide tile per 16 columns)
+    return dense_narrow_ws(x, w + static_cast<long long>(n_main) * K,
+                           static_cast<char*>(out) +
+                               static_cast<long long>(n_main) * (epi == kDenseBf16 ? 2 : 4),
+                           aux ? aux + n_main : nullptr, M, tail, K, N, epi, packed, s);
   }
   g.m_tiles = (M + bt - 1) / bt;
   g.n_tiles = (N + bt - 1) / bt;
