@@ -269,7 +269,7 @@ def n_sets(bytes_per_set: float, minimum: int = 3) -> int:
     return max(minimum, int(MALL_BYTES // max(bytes_per_set, 1)) + 1)
 
 
-KERNEL_ROWS = ("moe_decode_experts", "lm_head", "gdn_decode_step", "gdn_decode_step_c4",
+KERNEL_ROWS = ("hbm_copy", "moe_decode_experts", "lm_head", "gdn_decode_step", "gdn_decode_step_c4",
                "sample_argmax", "sample_top_p", "moe_prefill_layer", "moe_prefill_experts",
                "dense_prefill_gemm", "attn_prefill", "gdn_prefill")
 
@@ -311,6 +311,15 @@ def kernel_table(cfg, B, gen, iters, only=None):
     V = cfg.vocab
     it_mfma = max(10, iters // 5)
     strm = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
+
+    def hbm_copy():
+        # the practical ceiling of a read + write stream: a plain 512 MiB device
+        # copy (torch), bytes = read + written; 2 rotated source buffers
+        n = COPY_BYTES // 4
+        srcs = [torch.empty(n, device="cuda").normal_(generator=gen) for _ in range(2)]
+        dst = torch.empty(n, device="cuda")
+        t = event_time(lambda i: dst.copy_(srcs[i % 2]), max(10, iters // 5))
+        hbm("hbm_copy", t, 2 * COPY_BYTES, "torch device copy of 512 MiB (read + write)")
 
     def moe_decode_experts():
         # one C5 MoE application at decode: packed expert weights (302 MB per
@@ -473,7 +482,7 @@ def kernel_table(cfg, B, gen, iters, only=None):
         bytes4 = 4 * Bg * Tg * Hg4 * d4 * 2 + 2 * Bg * Tg * Hg4 * 4 + 2 * Bg * Hg4 * d4 * d4 * 4
         hbm("gdn_prefill", t, bytes4, f"C4: B={Bg}, T={Tg}, H={Hg4}, dk=dv={d4}, chunk 64")
 
-    fns = {"moe_decode_experts": moe_decode_experts, "lm_head": lm_head,
+    fns = {"hbm_copy": hbm_copy, "moe_decode_experts": moe_decode_experts, "lm_head": lm_head,
            "gdn_decode_step": gdn_decode_step,
            "gdn_decode_step_c4": gdn_decode_step_c4, "sample_argmax": sample_argmax,
            "sample_top_p": sample_top_p, "moe_prefill_layer": moe_prefill_layer,
