@@ -65,6 +65,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
                                            _I, _I, _I, _I, _I, _I, _P]),
     "llmy_gdn_conv_gate_prefill_reset": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _P]),
     "llmy_zero_rows": (_I, [_P, _I64, _I, _P, _P]),
+    "llmy_mhc_embed": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _P]),
+    "llmy_mhc_read": (_I, [_P, _P, _I64, _P, _P, _P, _P, _I, _P, _P, _F, _P, _F, _P, _P,
+                           _I, _I, _I, _P]),
+    "llmy_mhc_write": (_I, [_P, _P, _I64, _P, _P, _P, _I, _I, _I, _P]),
+    "llmy_f32_to_bf16": (_I, [_P, _P, _I64, _P]),
     # engine handles (the reference binding's argtypes, llmy_cuda/python/sample.py:110-170)
     "llmy_load": (_P, [C.c_char_p]),
     "llmy_free": (None, [_P]),

@@ -132,6 +132,9 @@ def save_llmy(path: str | Path, cfg: HybridConfig, weights: dict[str, torch.Tens
     """Write ``weights`` (keys of `config.weight_shapes`) as a `.llmy` v1 file.
     The depthwise conv is stored as nn.Conv1d's [D, 1, K]."""
     from .config import weight_shapes
+    if cfg.mhc_streams > 1:
+        raise ValueError("the .llmy writer and the native engine cover the single-stream "
+                         "block (mhc_streams = 1); mHC models run in HybridDecoder")
     entries = []
     for key, shape, _ in weight_shapes(cfg):
         t = weights[key].detach().to("cpu").contiguous()

@@ -46,6 +46,16 @@ class HybridConfig:
     latent_dim: int = 256
     router_context: int = 128
     route_gate_init: float = -4.59512  # context_router.py:25
+    # multi-stream hyper-connections (model/layers/mhc.py:156-231; model.py:84-86,
+    # 119-126,389-421,442-444,699-700): mhc_streams residual streams per token,
+    # read before and written after every mixer and MoE sublayer through
+    # input-dependent maps (pre / post weights, a Sinkhorn-normalised stream
+    # mixing matrix), seeded from the embedding plus a per-stream vector and
+    # collapsed by a linear map before the final norm; 1 = the single residual
+    # stream of the schematic block (no mHC)
+    mhc_streams: int = 1
+    mhc_sinkhorn_iters: int = 10   # model/config.py:12
+    mhc_gating_init: float = 0.01  # model/config.py:13
     eps: float = 1e-6
     init_std: float = 0.02
     decay_logit_init: float = 2.0  # model/layers/gated_deltanet.py:113
@@ -84,8 +94,18 @@ def weight_shapes(cfg: HybridConfig) -> list[tuple[str, tuple[int, ...], str]]:
     """(name, shape, kind) in generation order; kind in {normal, ones, zeros, decay, gate}."""
     D, E, Hf = cfg.d_model, cfg.n_experts, cfg.expert_hidden
     out: list[tuple[str, tuple[int, ...], str]] = [("embed", (cfg.vocab, D), "normal")]
+    Sm = cfg.mhc_streams
+    if Sm > 1:
+        out.append(("stream_seed", (Sm, D), "seed"))
     for l, kind in enumerate(cfg.layer_kinds):
         p = f"L{l}."
+        if Sm > 1:
+            out += [(p + "mhc_map_norm", (Sm * D,), "ones"),
+                    (p + "mhc_theta", (2 * Sm + Sm * Sm, Sm * D), "normal"),
+                    (p + "mhc_pre_bias", (Sm,), "mhc_pre"), (p + "mhc_post_bias", (Sm,), "zeros"),
+                    (p + "mhc_res_bias", (Sm, Sm), "eye4"), (p + "mhc_alpha", (3,), "alpha"),
+                    (p + "mhc_gating", (1,), "mhc_gate"), (p + "mhc_scale", (Sm, D), "ones"),
+                    (p + "mhc_ln_w", (D,), "ones"), (p + "mhc_ln_b", (D,), "zeros")]
         out.append((p + "mix_norm", (D,), "ones"))
         if kind == "attn":
             w = cfg.attn_heads * cfg.attn_head_dim
@@ -113,13 +133,17 @@ def weight_shapes(cfg: HybridConfig) -> list[tuple[str, tuple[int, ...], str]]:
             out += [(p + "w_shared_gate", (S, Hf, D), "normal"),
                     (p + "w_shared_up", (S, Hf, D), "normal"),
                     (p + "w_shared_down", (S, D, Hf), "normal")]
+    if Sm > 1:
+        out.append(("mhc_collapse", (D, Sm * D), "collapse"))
     out.append(("final_norm", (D,), "ones"))
     return out
 
 
 # Parameters kept in fp32 on the device; every other matrix is stored bf16.
 FP32_PARAMS = ("mix_norm", "ffn_norm", "router_norm", "final_norm", "w_router", "bb", "conv",
-               "decay", "ctx_down", "ctx_ln_w", "ctx_ln_b", "ctx_gate")
+               "decay", "ctx_down", "ctx_ln_w", "ctx_ln_b", "ctx_gate", "stream_seed",
+               "mhc_map_norm", "mhc_pre_bias", "mhc_post_bias", "mhc_res_bias", "mhc_alpha",
+               "mhc_gating", "mhc_scale", "mhc_ln_w", "mhc_ln_b")
 
 
 def is_fp32_param(name: str) -> bool:
@@ -147,6 +171,23 @@ def init_weights(cfg: HybridConfig, seed: int = 0, device: str | torch.device = 
             t = torch.zeros(shape, dtype=torch.float32, device=device)
         elif kind == "gate":
             t = torch.full(shape, cfg.route_gate_init, dtype=torch.float32, device=device)
+        elif kind == "seed":       # stream_seed ~ N(0, 1e-3) (model.py:389-390)
+            t = torch.empty(shape, dtype=torch.float32, device=device)
+            t.normal_(0.0, 1e-3, generator=gen)
+        elif kind == "mhc_pre":    # logit(1 / S) (mhc.py:75-77)
+            S_ = shape[0]
+            t = torch.full(shape, math.log((1.0 / S_) / (1.0 - 1.0 / S_)), dtype=torch.float32,
+                           device=device)
+        elif kind == "eye4":       # 4 I (mhc.py:79)
+            t = 4.0 * torch.eye(shape[0], dtype=torch.float32, device=device)
+        elif kind == "alpha":      # 0.01 each (mhc.py:80-82)
+            t = torch.full(shape, 0.01, dtype=torch.float32, device=device)
+        elif kind == "mhc_gate":   # logit(init gating factor) (mhc.py:83-84)
+            gi = min(max(cfg.mhc_gating_init, 1e-5), 1 - 1e-5)
+            t = torch.full(shape, math.log(gi / (1 - gi)), dtype=torch.float32, device=device)
+        elif kind == "collapse":   # [I/S ... I/S] (model.py:415-421)
+            D_, SD = shape
+            t = (torch.eye(D_, dtype=torch.float32, device=device) / (SD // D_)).repeat(1, SD // D_)
         else:
             t = torch.full(shape, cfg.decay_logit_init, dtype=torch.float32, device=device)
         weights[name] = t if is_fp32_param(name) else t.to(torch.bfloat16)

@@ -86,13 +86,30 @@ class HybridDecoder:
             self.w[p + "w_gate_up"] = gate_up.contiguous()
             self.w[p + "w_down"] = down.contiguous()
 
+        # multi-stream hyper-connections: per-layer map / read / write
+        # parameters in fp32, the maps' projection theta and the final
+        # collapse as packed bf16 GEMM weights
+        self.mhc = cfg.mhc_streams > 1
+        if self.mhc:
+            if cfg.context_router:
+                raise NotImplementedError("mHC with the context-aware router is not built")
+            self.w["stream_seed"] = up("stream_seed")
+            self.w["mhc_collapse"] = up("mhc_collapse")
+            for l in range(cfg.n_layers):
+                p = f"L{l}."
+                for n in ("mhc_map_norm", "mhc_pre_bias", "mhc_post_bias", "mhc_res_bias",
+                          "mhc_alpha", "mhc_gating", "mhc_scale", "mhc_ln_w", "mhc_ln_b"):
+                    self.w[p + n] = up(p + n)
+                self.w[p + "mhc_theta"] = _pad_rows(up(p + "mhc_theta"), 16).contiguous()
+
         # Decode GEMM weights are re-laid once into the packed operand order
         # (llmy_pack_weights_bf16), so every weight byte streams as contiguous
         # 1 KiB wavefront loads; the embedding keeps a row-major copy for the
         # token lookup and a packed copy for the tied LM head.
         for name in list(self.w):
             if name.split(".")[-1] in ("wqkv", "wo", "wproj", "wout", "w_gate_up", "w_down",
-                                       "ctx_local_out", "ctx_out"):
+                                       "ctx_local_out", "ctx_out", "mhc_theta",
+                                       "mhc_collapse"):
                 self.w[name] = ops.pack_weights(self.w[name])
         self.w["lm_head"] = ops.pack_weights(self.w["embed"])
 
@@ -175,7 +192,7 @@ class HybridDecoder:
         # all of them, and no residual round trip precedes the store.
         n_parts = max(Ha * hd, Hg * dv) // 256
         self.defer_resid = (self.fused_route and B <= 64 and (Ha * hd) % 256 == 0
-                            and (Hg * dv) % 256 == 0 and n_parts <= 8)
+                            and (Hg * dv) % 256 == 0 and n_parts <= 8 and not self.mhc)
         if self.defer_resid:
             self.buf["parts"] = torch.zeros(n_parts, B, D, dtype=f32, device=dev)
         # The GDN input projection the same way: its partials are summed by
@@ -184,6 +201,16 @@ class HybridDecoder:
         if self.proj_parts:
             self.buf["proj_parts"] = torch.zeros(D // 256, B, nproj, dtype=f32, device=dev)
         self._pending: tuple | None = None
+        if self.mhc:
+            Sm = cfg.mhc_streams
+            nt = self.w["L0.mhc_theta"].shape[0]
+            self.buf.update({
+                "X": torch.zeros(B, Sm, D, dtype=f32, device=dev),    # the streams
+                "xb": torch.zeros(B, Sm * D, dtype=bf, device=dev),   # GEMM operands
+                "raw": torch.zeros(B, nt, dtype=f32, device=dev),     # map logits
+                "maps": torch.zeros(B, Sm + Sm * Sm, dtype=f32, device=dev),
+                "U": torch.zeros(B, D, dtype=f32, device=dev),        # a sublayer's output
+                "route_ident": torch.arange(B * kx, dtype=torch.int32, device=dev)})
         # Optional record of every MoE application's expert ids (verification
         # aid: lets a checker replay the kernel's discrete routing decisions),
         # and of the residual stream after each application.
@@ -205,7 +232,7 @@ class HybridDecoder:
         self._app = 0
 
     # ------------------------------------------------------------------ blocks
-    def _attn(self, l: int, st: dict) -> None:
+    def _attn(self, l: int, st: dict, out=None, epilogue=None) -> None:
         cfg, w, b = self.cfg, self.w, self.buf
         p = f"L{l}."
         Hhd = cfg.attn_heads * cfg.attn_head_dim
@@ -223,10 +250,11 @@ class HybridDecoder:
                        epilogue=ops.EPI_PARTIAL_F32, layout=ops.LAYOUT_PACKED)
             self._pending = (parts, None)
         else:
-            ops.linear(b["ao"].view(B, Hhd), w[p + "wo"], out=b["x"],
-                       epilogue=ops.EPI_RESID_ADD, layout=ops.LAYOUT_PACKED)
+            ops.linear(b["ao"].view(B, Hhd), w[p + "wo"], out=b["x"] if out is None else out,
+                       epilogue=ops.EPI_RESID_ADD if epilogue is None else epilogue,
+                       layout=ops.LAYOUT_PACKED)
 
-    def _gdn(self, l: int, st: dict) -> None:
+    def _gdn(self, l: int, st: dict, out=None) -> None:
         w, b = self.w, self.buf
         p = f"L{l}."
         if self.proj_parts:
@@ -245,8 +273,8 @@ class HybridDecoder:
                        layout=ops.LAYOUT_PACKED)
             self._pending = (parts, b["cg"])
         else:
-            ops.linear(b["go"], w[p + "wout"], out=b["x"], epilogue=ops.EPI_RESID_GATED,
-                       aux=b["cg"], layout=ops.LAYOUT_PACKED)
+            ops.linear(b["go"], w[p + "wout"], out=b["x"] if out is None else out,
+                       epilogue=ops.EPI_RESID_GATED, aux=b["cg"], layout=ops.LAYOUT_PACKED)
 
     def _ctx_weights(self, p: str) -> dict:
         w = self.w
@@ -307,6 +335,9 @@ class HybridDecoder:
 
     # ------------------------------------------------------------------ step
     def _step_body(self) -> None:
+        if self.mhc:
+            self._step_body_mhc()
+            return
         cfg, w, b = self.cfg, self.w, self.buf
         ops.embed_norm(b["tokens"], w["embed"], w["L0.mix_norm"], b["x"], b["h"], cfg.eps)
         apps = [(loop, l) for loop in range(cfg.num_loops) for l in range(cfg.n_layers)]
@@ -319,6 +350,94 @@ class HybridDecoder:
             self._moe(l, nxt, self.state[(loop, l)])
         ops.linear(b["h"], w["lm_head"], out=b["logits"], epilogue=ops.EPI_STORE_F32,
                    layout=ops.LAYOUT_PACKED)
+        self._sample()
+        self.pos.add_(1)
+
+    # ------------------------------------------------------------------ mHC
+    def _mhc_params(self, l: int) -> dict:
+        p = f"L{l}."
+        return {n: self.w[p + "mhc_" + n] for n in ("pre_bias", "post_bias", "res_bias", "alpha",
+                                                     "ln_w", "ln_b")}
+
+    def _mhc_read(self, l: int, X, norm: str, raw, maps, h, xb) -> None:
+        """The maps of layer l's hyper-connection and the sublayer input h
+        (model.py:119-123; mhc.py:156-206): RMSNorm of the flattened streams
+        into bf16, the theta projection, then maps + read + LayerNorm + the
+        sublayer's RMSNorm in one kernel."""
+        cfg, w = self.cfg, self.w
+        p = f"L{l}."
+        M = X.shape[0]
+        ops.rmsnorm(X.view(M, -1), w[p + "mhc_map_norm"], ops.MHC_MAP_EPS, out=xb)
+        ops.linear(xb, w[p + "mhc_theta"], out=raw, epilogue=ops.EPI_STORE_F32,
+                   layout=ops.LAYOUT_PACKED)
+        ops.mhc_read(X, raw, self._mhc_params(l), w[p + norm], cfg.mhc_sinkhorn_iters,
+                     maps=maps, h=h, norm_eps=cfg.eps)
+
+    def _mhc_write(self, l: int, X, U, maps) -> None:
+        p = f"L{l}."
+        ops.mhc_write(X, U, maps, self.w[p + "mhc_scale"], self.w[p + "mhc_gating"])
+
+    def _mhc_head(self, X, xb, U) -> None:
+        """Collapse the streams (model.py:699-700), the final RMSNorm, the LM head."""
+        w, b, M = self.w, self.buf, X.shape[0]
+        ops.f32_to_bf16(X.view(M, -1), out=xb)
+        ops.linear(xb, w["mhc_collapse"], out=U, epilogue=ops.EPI_STORE_F32,
+                   layout=ops.LAYOUT_PACKED)
+        ops.rmsnorm(U, w["final_norm"], self.cfg.eps, out=b["h"])
+        ops.linear(b["h"], w["lm_head"], out=b["logits"], epilogue=ops.EPI_STORE_F32,
+                   layout=ops.LAYOUT_PACKED)
+
+    def _step_body_mhc(self) -> None:
+        """The decode step with multi-stream hyper-connections: each sublayer
+        reads the streams through its maps and writes its output back
+        (model.py:177-264); mixer and MoE kernels as in the single-stream step,
+        their outputs stored to U instead of added to a residual."""
+        from . import _lib
+        cfg, w, b = self.cfg, self.w, self.buf
+        X, U = b["X"], b["U"]
+        ops.mhc_embed(b["tokens"], w["embed"], w["stream_seed"], out=X)
+        s = torch.cuda.current_stream().cuda_stream
+        kx = cfg.top_k + cfg.shared_experts
+        for loop in range(cfg.num_loops):
+            for l in range(cfg.n_layers):
+                st = self.state[(loop, l)]
+                p = f"L{l}."
+                self._mhc_read(l, X, "mix_norm", b["raw"], b["maps"], b["h"], b["xb"])
+                if cfg.layer_kinds[l] == "attn":
+                    self._attn(l, st, out=U, epilogue=ops.EPI_STORE_F32)
+                else:
+                    U.zero_()
+                    self._gdn(l, st, out=U)
+                self._mhc_write(l, X, U, b["maps"])
+                self._mhc_read(l, X, "ffn_norm", b["raw"], b["maps"], b["h"], b["xb"])
+                _lib.call("llmy_router_topk_bf16", b["h"].data_ptr(),
+                          w[p + "router_norm"].data_ptr(), w[p + "w_router"].data_ptr(), None,
+                          b["idx"].data_ptr(), b["gates"].data_ptr(), self.B, cfg.d_model,
+                          cfg.n_experts, cfg.top_k, cfg.eps, s)
+                idx, gates = b["idx"], b["gates"]
+                if cfg.shared_experts > 0:
+                    idx, gates = ops.moe_append_shared(idx, gates, cfg.n_experts,
+                                                       cfg.shared_experts, idx_out=b["idx_all"],
+                                                       gates_out=b["gates_all"])
+                if self.route_log is not None:
+                    self.route_log[self._app].copy_(b["idx"])
+                    self._app = (self._app + 1) % self.route_log.shape[0]
+                if self.fused_route:
+                    ops.moe_experts_routed(b["h"], idx, gates, w[p + "w_gate_up"],
+                                           w[p + "w_down"], act=b["act"], y=b["y"],
+                                           layout=ops.LAYOUT_PACKED)
+                    route_pos = b["route_ident"]
+                else:
+                    _lib.call("llmy_moe_permute", idx.data_ptr(), self.B * kx,
+                              cfg.n_experts + cfg.shared_experts, b["counts"].data_ptr(),
+                              b["offsets"].data_ptr(), b["sorted_routes"].data_ptr(),
+                              b["route_pos"].data_ptr(), s)
+                    ops.moe_experts(b["h"], b, gates, w[p + "w_gate_up"], w[p + "w_down"],
+                                    act=b["act"], y=b["y"], layout=ops.LAYOUT_PACKED)
+                    route_pos = b["route_pos"]
+                ops.moe_combine(b["y"], route_pos, self.B, kx, out=U, mode=ops.MOE_OUT_F32)
+                self._mhc_write(l, X, U, b["maps"])
+        self._mhc_head(X, b["xb"], U)
         self._sample()
         self.pos.add_(1)
 
@@ -413,6 +532,8 @@ class HybridDecoder:
         B, T = tokens.shape
         R, D = B * T, cfg.d_model
         self.reset()
+        if self.mhc:
+            return self._prefill_mhc(tokens, B, T)
         x = torch.empty(R, D, dtype=torch.float32, device=self.dev)
         h = torch.empty(R, D, dtype=torch.bfloat16, device=self.dev)
         ops.embed_norm(tokens.contiguous().view(-1), w["embed"], w["L0.mix_norm"], x, h, cfg.eps)
@@ -433,7 +554,56 @@ class HybridDecoder:
         self.pos.fill_(T)
         return b["logits"]
 
-    def _attn_seq(self, l: int, st: dict, x, h, B: int, T: int) -> None:
+    def _prefill_mhc(self, tokens, B: int, T: int) -> torch.Tensor:
+        """Prefill with multi-stream hyper-connections: the sequence kernels of
+        ``prefill`` with each sublayer's output stored to U and written into the
+        [B*T, S, D] streams through the layer's maps (model.py:177-264)."""
+        from . import _lib
+        cfg, w, b = self.cfg, self.w, self.buf
+        R, D, Sm, dev = B * T, cfg.d_model, cfg.mhc_streams, self.dev
+        X = ops.mhc_embed(tokens.contiguous().view(-1), w["embed"], w["stream_seed"])
+        h = torch.empty(R, D, dtype=torch.bfloat16, device=dev)
+        U = torch.empty(R, D, dtype=torch.float32, device=dev)
+        xb = torch.empty(R, Sm * D, dtype=torch.bfloat16, device=dev)
+        raw = torch.empty(R, w["L0.mhc_theta"].shape[0], dtype=torch.float32, device=dev)
+        maps = torch.empty(R, Sm + Sm * Sm, dtype=torch.float32, device=dev)
+        s = torch.cuda.current_stream().cuda_stream
+        E, k = cfg.n_experts, cfg.top_k
+        for loop in range(cfg.num_loops):
+            for l in range(cfg.n_layers):
+                st = self.state[(loop, l)]
+                p = f"L{l}."
+                self._mhc_read(l, X, "mix_norm", raw, maps, h, xb)
+                if cfg.layer_kinds[l] == "attn":
+                    self._attn_seq(l, st, U, h, B, T, epilogue=ops.EPI_STORE_F32)
+                else:
+                    U.zero_()
+                    self._gdn_seq(l, st, U, h, B, T)
+                self._mhc_write(l, X, U, maps)
+                self._mhc_read(l, X, "ffn_norm", raw, maps, h, xb)
+                idx = torch.empty(R, k, dtype=torch.int32, device=dev)
+                gates = torch.empty(R, k, dtype=torch.float32, device=dev)
+                _lib.call("llmy_router_topk_bf16", h.data_ptr(), w[p + "router_norm"].data_ptr(),
+                          w[p + "w_router"].data_ptr(), None, idx.data_ptr(), gates.data_ptr(),
+                          R, D, E, k, cfg.eps, s)
+                if self.route_log_seq is not None:
+                    self.route_log_seq.append(idx.clone())
+                Ex, kx = E, k
+                if cfg.shared_experts > 0:
+                    idx, gates = ops.moe_append_shared(idx, gates, E, cfg.shared_experts)
+                    Ex, kx = E + cfg.shared_experts, k + cfg.shared_experts
+                perm = ops.moe_permute(idx.view(-1), Ex)
+                _, y = ops.moe_experts(h, perm, gates, w[p + "w_gate_up"], w[p + "w_down"],
+                                       layout=ops.LAYOUT_PACKED)
+                ops.moe_combine(y, perm["route_pos"], R, kx, out=U, mode=ops.MOE_OUT_F32)
+                self._mhc_write(l, X, U, maps)
+        b["X"].copy_(X.view(B, T, Sm, D)[:, -1])
+        self._mhc_head(b["X"], b["xb"], b["U"])
+        self._sample()
+        self.pos.fill_(T)
+        return b["logits"]
+
+    def _attn_seq(self, l: int, st: dict, x, h, B: int, T: int, epilogue=None) -> None:
         cfg, w = self.cfg, self.w
         p = f"L{l}."
         H, hd = cfg.attn_heads, cfg.attn_head_dim
@@ -446,7 +616,8 @@ class HybridDecoder:
         o = ops.banded_attn_prefill(q.view(B, T, H, hd), k.view(B, T, H, hd),
                                     v.view(B, T, H, hd), cfg.window, cfg.attn_scale)
         ops.kv_cache_fill(k.view(B, T, Hhd), v.view(B, T, Hhd), st["k"], st["v"])
-        ops.linear(o.view(R, Hhd), w[p + "wo"], out=x, epilogue=ops.EPI_RESID_ADD,
+        ops.linear(o.view(R, Hhd), w[p + "wo"], out=x,
+                   epilogue=ops.EPI_RESID_ADD if epilogue is None else epilogue,
                    layout=ops.LAYOUT_PACKED)
 
     def _gdn_seq(self, l: int, st: dict, x, h, B: int, T: int) -> None:

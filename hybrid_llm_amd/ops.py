@@ -552,6 +552,57 @@ def gdn_conv_gate(h, hist, w, out=None) -> torch.Tensor:
     return out
 
 
+# --------------------------------------------------------------------------- mHC
+MHC_MAP_EPS = 1.1920928955078125e-07   # nn.RMSNorm(eps=None) on fp32 (model/layers/mhc.py:72)
+
+
+def mhc_embed(tokens, table, seed, out=None) -> torch.Tensor:
+    """Streams [M, S, D] fp32: E[token] + seed[s] (model.py:442-444)."""
+    M = tokens.numel()
+    S, D = seed.shape
+    _check(tokens, torch.int32, "tokens")
+    _check(seed, torch.float32, "seed", (S, D))
+    if out is None:
+        out = torch.empty(M, S, D, dtype=torch.float32, device=tokens.device)
+    _lib.call("llmy_mhc_embed", _ptr(tokens), _ptr(table), _ptr(seed), _ptr(out), M, S, D,
+              table.shape[0], _stream())
+    return out
+
+
+def mhc_read(X, raw, p: dict, norm_w, iterations: int, maps=None, h=None, norm_eps: float = 1e-6):
+    """Maps and read of one sublayer: X [M, S, D] streams, raw [M, >= 2S+S^2] fp32
+    projection, p the layer's mHC parameters (pre_bias, post_bias, res_bias,
+    alpha, ln_w, ln_b).  Returns (maps [M, S+S^2], h [M, D] bf16)."""
+    M, S, D = X.shape
+    _check(X, torch.float32, "X")
+    if maps is None:
+        maps = torch.empty(M, S + S * S, dtype=torch.float32, device=X.device)
+    if h is None:
+        h = torch.empty(M, D, dtype=torch.bfloat16, device=X.device)
+    _lib.call("llmy_mhc_read", _ptr(X), _ptr(raw), raw.stride(0), _ptr(p["pre_bias"]),
+              _ptr(p["post_bias"]), _ptr(p["res_bias"]), _ptr(p["alpha"]), iterations,
+              _ptr(p["ln_w"]), _ptr(p["ln_b"]), 1e-5, _ptr(norm_w), norm_eps, _ptr(maps), _ptr(h),
+              M, S, D, _stream())
+    return maps, h
+
+
+def mhc_write(X, U, maps, scale, gating_logit) -> None:
+    """In place: X_i += sigmoid(g) scale_i (sum_j R_ij X_j + post_i U)."""
+    M, S, D = X.shape
+    _check(X, torch.float32, "X")
+    _check(U, torch.float32, "U")
+    _lib.call("llmy_mhc_write", _ptr(X), _ptr(U), U.stride(0), _ptr(maps), _ptr(scale),
+              _ptr(gating_logit), M, S, D, _stream())
+
+
+def f32_to_bf16(x, out=None) -> torch.Tensor:
+    _check(x, torch.float32, "x")
+    if out is None:
+        out = torch.empty(x.shape, dtype=torch.bfloat16, device=x.device)
+    _lib.call("llmy_f32_to_bf16", _ptr(x), _ptr(out), x.numel(), _stream())
+    return out
+
+
 def zero_rows(t: torch.Tensor, mask: torch.Tensor) -> None:
     """Zero t[b] wherever mask[b] != 0; t contiguous [rows, ...] on the device,
     mask device int32 [rows] (a kernel, so it may sit in a captured graph)."""

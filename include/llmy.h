@@ -325,6 +325,38 @@ int32_t llmy_gdn_conv_gate_prefill_reset(const llmy_bf16* h, llmy_bf16* hist, co
 int32_t llmy_zero_rows(void* base, int64_t row_bytes, int32_t rows, const int32_t* mask,
                        void* stream);
 
+/* --- Multi-stream hyper-connections (mHC) -------------------------------------
+ * model/layers/mhc.py:156-231 around the block's sublayers (model/model.py:
+ * 119-126,177-264); the reference's native twins are mhc_rmsnorm_flat,
+ * mhc_gemv_small, mhc_activate, sinkhorn, mhc_read and mhc_write
+ * (llmy_cuda/src/kernels/mhc.cu:26-443).  A token's residual is S streams
+ * [S, D] fp32 (S = 2 or 4).  The maps' projection raw = theta . RMSNorm(X)
+ * is the caller's: llmy_rmsnorm_f32_bf16 over the flattened [M, S*D] streams
+ * (eps = fp32 epsilon, mhc.py:72) then llmy_linear_bf16 with theta. */
+
+/* streams[m, s, :] = E[tokens[m], :] + seed[s, :]  (model.py:442-444) */
+int32_t llmy_mhc_embed(const int32_t* tokens, const llmy_bf16* table, const float* seed,
+                       float* streams, int32_t M, int32_t S, int32_t D, int32_t V,
+                       void* stream);
+/* Maps and read (mhc.py:156-206): from raw [M, raw_ld] (pre | post | residual
+ * logits), pre = sigmoid(alpha[0] raw + pre_bias), post = 2 sigmoid(alpha[1] raw
+ * + post_bias), R = Sinkhorn(alpha[2] raw + res_bias, iterations) -> maps
+ * [M, S + S*S] (post, then R row-major); h [M, D] = bf16(RMSNorm(norm_w,
+ * norm_eps)(LayerNorm(ln_w, ln_b, ln_eps)(sum_s pre_s X_s))), the sublayer
+ * input.  D % 4 == 0, D <= 4096. */
+int32_t llmy_mhc_read(const float* streams, const float* raw, int64_t raw_ld,
+                      const float* pre_bias, const float* post_bias, const float* res_bias,
+                      const float* alpha, int32_t iterations, const float* ln_w,
+                      const float* ln_b, float ln_eps, const float* norm_w, float norm_eps,
+                      float* maps, llmy_bf16* h, int32_t M, int32_t S, int32_t D, void* stream);
+/* Write (mhc.py:208-227), in place: X_i += sigmoid(gating_logit[0]) scale[i] *
+ * (sum_j R_ij X_j + post_i update[m]); update [M, update_ld] fp32. */
+int32_t llmy_mhc_write(float* streams, const float* update, int64_t update_ld,
+                       const float* maps, const float* scale, const float* gating_logit,
+                       int32_t M, int32_t S, int32_t D, void* stream);
+/* out[i] = bf16(x[i]), n % 4 == 0 (the collapse GEMM's operand, model.py:699). */
+int32_t llmy_f32_to_bf16(const float* x, llmy_bf16* out, int64_t n, void* stream);
+
 /* --- Glue (model/layers/norms.py:13-16, model/model.py:386) --------------- */
 
 /* out[m] = bf16(x[m] * rsqrt(mean(x[m]^2) + eps) * w); x [M,D] fp32. */

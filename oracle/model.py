@@ -1,8 +1,12 @@
 """Looped hybrid-block stack oracle (test infrastructure only).
 
-Composes the pinned ops into the block of model/model.py:162-264 with mHC
-disabled (model.py:119-126), looping the core ``num_loops`` times with one
-state per (loop, layer) (model.py:618-687, :645), tied LM head (model.py:705).
+Composes the pinned ops into the block of model/model.py:162-264, looping the
+core ``num_loops`` times with one state per (loop, layer) (model.py:618-687,
+:645), tied LM head (model.py:705).  With ``mhc_streams`` > 1 the residual is
+S streams read and written around each sublayer through the layer's
+hyper-connection maps (model.py:119-126,177-264), seeded from the embedding
+(:442-444) and collapsed before the final norm (:699-700); with 1 it is the
+single residual stream of mHC disabled (model.py:119-126).
 
 Mixers:
   * attention: q/k/v projections, banded attention over a ring KV cache
@@ -33,6 +37,7 @@ from hybrid_llm_amd.config import HybridConfig
 
 from .attention import banded_attention_decode
 from .gdn import gdn_step
+from .mhc import mhc_maps, mhc_read, mhc_write
 from .moe import moe_grouped, shared_experts
 from .router import (context_latents, context_route_logits, rmsnorm, router_logits,
                      router_topk)
@@ -156,25 +161,61 @@ class HybridOracle:
 
     # ---- step ------------------------------------------------------------
     def embed(self, tokens) -> torch.Tensor:
-        """The residual stream's start: embedding rows (model.py:386)."""
+        """The residual stream's start: embedding rows (model.py:386); with
+        mHC the S streams embed + stream_seed[s] (model.py:442-444), [B, S, D]."""
         tokens = torch.as_tensor(np.asarray(tokens), dtype=torch.long).view(-1)
-        return self.w["embed"][tokens].clone()
+        x = self.w["embed"][tokens].clone()
+        if self.cfg.mhc_streams > 1:
+            x = x[:, None, :] + self.w["stream_seed"][None]
+        return x
+
+    def _mhc_read(self, l: int, X: torch.Tensor):
+        """The maps of layer l's hyper-connection and the read of the streams
+        (model.py:119-123; mhc.py:156-206); the theta projection's input is
+        rounded as the engine's bf16 GEMM operand."""
+        cfg, w = self.cfg, self.w
+        p = f"L{l}."
+        maps = mhc_maps(X, w[p + "mhc_theta"], w[p + "mhc_map_norm"], w[p + "mhc_pre_bias"],
+                        w[p + "mhc_post_bias"], w[p + "mhc_res_bias"], w[p + "mhc_alpha"],
+                        cfg.mhc_sinkhorn_iters, act_round=self.rnd)
+        return mhc_read(X, maps[0], w[p + "mhc_ln_w"], w[p + "mhc_ln_b"]), maps
+
+    def _mhc_write(self, l: int, X, U, maps):
+        p = f"L{l}."
+        return mhc_write(X, U, maps[1], maps[2], self.w[p + "mhc_scale"], self.w[p + "mhc_gating"])
 
     def apply(self, l: int, x: torch.Tensor, s: dict, pos: torch.Tensor) -> torch.Tensor:
         """One application of layer l (mixer block then MoE block, each a
         pre-norm residual branch: model.py:119-126,162-264) to the residual x,
-        updating that (loop, layer)'s state s in place; returns the new x."""
+        updating that (loop, layer)'s state s in place; returns the new x.
+        With mHC, x is the [B, S, D] streams, each branch reads them through
+        the layer's maps and writes its output back (model.py:177-264)."""
         cfg, w, rnd = self.cfg, self.w, self.rnd
-        h = rnd(rmsnorm(x, w[f"L{l}.mix_norm"], cfg.eps))
-        if cfg.layer_kinds[l] == "attn":
-            x = x + self._attn(l, h, s, pos)
+        mhc = cfg.mhc_streams > 1
+        if mhc:
+            hidden, maps = self._mhc_read(l, x)
         else:
-            x = x + self._gdn(l, h, s)
-        h2 = rnd(rmsnorm(x, w[f"L{l}.ffn_norm"], cfg.eps))
-        return x + self._moe(l, h2, s)
+            hidden = x
+        h = rnd(rmsnorm(hidden, w[f"L{l}.mix_norm"], cfg.eps))
+        if cfg.layer_kinds[l] == "attn":
+            u = self._attn(l, h, s, pos)
+        else:
+            u = self._gdn(l, h, s)
+        x = self._mhc_write(l, x, u, maps) if mhc else x + u
+        if mhc:
+            hidden, maps = self._mhc_read(l, x)
+        else:
+            hidden = x
+        h2 = rnd(rmsnorm(hidden, w[f"L{l}.ffn_norm"], cfg.eps))
+        u = self._moe(l, h2, s)
+        return self._mhc_write(l, x, u, maps) if mhc else x + u
 
     def head(self, x: torch.Tensor) -> torch.Tensor:
-        """Final RMSNorm and the tied LM head (model.py:705): fp32 logits."""
+        """Final RMSNorm and the tied LM head (model.py:705): fp32 logits.  With
+        mHC the streams are first collapsed by mhc_collapse (model.py:699-700),
+        whose input is rounded as the engine's bf16 GEMM operand."""
+        if self.cfg.mhc_streams > 1:
+            x = self.rnd(x.reshape(x.shape[0], -1)) @ self.w["mhc_collapse"].t()
         hf = self.rnd(rmsnorm(x, self.w["final_norm"], self.cfg.eps))
         return hf @ self.w["embed"].t()
 
