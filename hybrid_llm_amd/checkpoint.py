@@ -63,17 +63,34 @@ _BLOCK = {"mix_norm": "mixer_norm.weight", "ffn_norm": "ffn_norm.weight",
           "ctx_gate": "moe.router.route_gate"}
 
 
+# mHC parameters (model/layers/mhc.py:63-84; the names llmy_cuda/src/model.cpp:34-63
+# reads); the three alpha scalars are one [3] tensor here (mhc_alpha)
+_MHC = {"mhc_map_norm": "mhc.mapping_norm.weight", "mhc_theta": "mhc.theta.weight",
+        "mhc_pre_bias": "mhc.pre_bias", "mhc_post_bias": "mhc.post_bias",
+        "mhc_res_bias": "mhc.residual_bias", "mhc_gating": "mhc.gating_logit",
+        "mhc_scale": "mhc.stream_scale", "mhc_ln_w": "mhc.stream_norm.weight",
+        "mhc_ln_b": "mhc.stream_norm.bias"}
+_MHC_ALPHA = ("mhc.alpha_pre", "mhc.alpha_post", "mhc.alpha_residual")
+
+
 def file_name(cfg: HybridConfig, key: str) -> str:
-    """The `.llmy` tensor name of a `config.weight_shapes` key."""
+    """The `.llmy` tensor name of a `config.weight_shapes` key (mhc_alpha maps
+    to the three names of _MHC_ALPHA, handled by the writer and reader)."""
     if key == "embed":
         return "embed_tokens.weight"
     if key == "final_norm":
         return "final_norm.weight"
+    if key == "stream_seed":
+        return "stream_seed"
+    if key == "mhc_collapse":
+        return "mhc_collapse.weight"
     layer, short = key.split(".", 1)
     l = int(layer[1:])
     p = f"recurrent_core.{l}."
     if short in _BLOCK:
         return p + _BLOCK[short]
+    if short in _MHC:
+        return p + _MHC[short]
     table = _ATTN if cfg.layer_kinds[l] == "attn" else _GDN
     return p + "mixer." + table[short]
 
@@ -82,7 +99,8 @@ def config_text(cfg: HybridConfig) -> str:
     keys = {
         "vocab_size": cfg.vocab, "d_model": cfg.d_model, "num_loops": cfg.num_loops,
         "stem_blocks": 0, "tail_blocks": 0, "recurrent_blocks": cfg.n_layers,
-        "recurrent_layout": ",".join(cfg.layer_kinds), "mhc.enabled": 0,
+        "recurrent_layout": ",".join(cfg.layer_kinds), "mhc.enabled": int(cfg.mhc_streams > 1),
+        "mhc.streams": cfg.mhc_streams, "mhc.sinkhorn_iterations": cfg.mhc_sinkhorn_iters,
         "attn.heads": cfg.attn_heads, "attn.head_dim": cfg.attn_head_dim,
         "attn.window": cfg.window,
         "gdn.qk_heads": cfg.gdn_heads, "gdn.value_heads": cfg.gdn_heads,
@@ -116,7 +134,22 @@ def config_from_text(text: str) -> HybridConfig:
         # absent keys take the reference defaults (llmy_cuda/include/config.h:60-66)
         context_router=_parse_bool(kv.get("router.context_aware", "1")),
         router_context=int(kv.get("router.local_context", 128)),
-        latent_dim=int(kv.get("mla.latent_dim", 256)))
+        latent_dim=int(kv.get("mla.latent_dim", 256)),
+        **_mhc_from(kv))
+
+
+def _mhc_from(kv: dict) -> dict:
+    """mhc.* keys with the reference's defaults (llmy_cuda/include/config.h:27-29):
+    streams read through the maps when mhc.enabled, else one stream."""
+    if _parse_bool(kv.get("mhc.enabled", "1")):
+        s = int(kv.get("mhc.streams", 4))
+        if s not in (2, 4):
+            raise ValueError("mhc.streams must be 2 or 4")
+        return {"mhc_streams": s, "mhc_sinkhorn_iters": int(kv.get("mhc.sinkhorn_iterations", 20))}
+    if int(kv.get("mhc.streams", 1)) != 1:
+        raise ValueError("streams without mHC maps (mhc.enabled = 0, mhc.streams > 1) are not "
+                         "part of this block stack")
+    return {"mhc_streams": 1}
 
 
 def _parse_bool(s: str) -> bool:
@@ -132,9 +165,6 @@ def save_llmy(path: str | Path, cfg: HybridConfig, weights: dict[str, torch.Tens
     """Write ``weights`` (keys of `config.weight_shapes`) as a `.llmy` v1 file.
     The depthwise conv is stored as nn.Conv1d's [D, 1, K]."""
     from .config import weight_shapes
-    if cfg.mhc_streams > 1:
-        raise ValueError("the .llmy writer and the native engine cover the single-stream "
-                         "block (mhc_streams = 1); mHC models run in HybridDecoder")
     entries = []
     for key, shape, _ in weight_shapes(cfg):
         t = weights[key].detach().to("cpu").contiguous()
@@ -142,6 +172,12 @@ def save_llmy(path: str | Path, cfg: HybridConfig, weights: dict[str, torch.Tens
             raise ValueError(f"{key}: shape {tuple(t.shape)} != {shape}")
         if key.endswith(".conv"):
             t = t.view(shape[0], 1, shape[1])
+        if key.endswith(".mhc_alpha"):  # three 0-d parameters in the reference
+            pre = file_name(cfg, key.replace("mhc_alpha", "mhc_map_norm")).rsplit("mhc.", 1)[0]
+            entries += [(pre + n, t[i].reshape(())) for i, n in enumerate(_MHC_ALPHA)]
+            continue
+        if key.endswith(".mhc_gating"):
+            t = t.reshape(())
         entries.append((file_name(cfg, key), t))
     entries.sort(key=lambda e: e[0])
     cfg_b = config_text(cfg).encode()
@@ -210,5 +246,9 @@ def load_weights(path: str | Path) -> tuple[HybridConfig, dict[str, torch.Tensor
     cfg = config_from_text(text)
     w = {}
     for key, shape, _ in weight_shapes(cfg):
+        if key.endswith(".mhc_alpha"):
+            pre = file_name(cfg, key.replace("mhc_alpha", "mhc_map_norm")).rsplit("mhc.", 1)[0]
+            w[key] = torch.stack([tensors[pre + n].reshape(()) for n in _MHC_ALPHA])
+            continue
         w[key] = tensors[file_name(cfg, key)].reshape(shape)
     return cfg, w

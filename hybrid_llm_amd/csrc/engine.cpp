@@ -181,7 +181,11 @@ struct Config {
   // router.local_context, mla.latent_dim (llmy_cuda/include/config.h:60-66)
   bool ctx = false;
   int ctx_window = 128, latent = 256;
+  // multi-stream hyper-connections: streams per token (mhc.streams when
+  // mhc.enabled; 1 = the single residual stream) and Sinkhorn iterations
+  int mhc = 1, mhc_iters = 20;
   float eps = 1e-6f;
+  int mhc_n16() const { return (2 * mhc + mhc * mhc + 15) / 16 * 16; }
   int routes() const { return top_k + shared; }      // routes per token, shared included
   int all_experts() const { return experts + shared; }
   int nproj16() const {
@@ -215,9 +219,17 @@ Config config_from(const std::string& text) {
   c.vocab = cfg_int(kv, "vocab_size", 0, true);
   c.d_model = cfg_int(kv, "d_model", 0, true);
   c.num_loops = cfg_int(kv, "num_loops", 1, true);
-  if (cfg_int(kv, "stem_blocks", 0, false) || cfg_int(kv, "tail_blocks", 0, false) ||
-      cfg_int(kv, "mhc.enabled", 0, false))
-    throw std::runtime_error("stem/tail blocks and mHC are not part of this engine");
+  if (cfg_int(kv, "stem_blocks", 0, false) || cfg_int(kv, "tail_blocks", 0, false))
+    throw std::runtime_error("stem/tail blocks are not part of this engine");
+  // mHC keys with the reference's defaults (llmy_cuda/include/config.h:27-29)
+  if (cfg_bool(kv, "mhc.enabled", true)) {
+    c.mhc = cfg_int(kv, "mhc.streams", 4, false);
+    c.mhc_iters = cfg_int(kv, "mhc.sinkhorn_iterations", 20, false);
+    if (c.mhc != 2 && c.mhc != 4) throw std::runtime_error("mhc.streams must be 2 or 4");
+  } else if (cfg_int(kv, "mhc.streams", 1, false) != 1) {
+    throw std::runtime_error("streams without mHC maps (mhc.enabled = 0, mhc.streams > 1) "
+                             "are not part of this engine");
+  }
   auto lay = kv.find("recurrent_layout");
   if (lay == kv.end()) throw std::runtime_error("config lacks recurrent_layout");
   size_t p = 0;
@@ -258,6 +270,8 @@ Config config_from(const std::string& text) {
   if (c.ctx && (c.latent % 256 != 0 || c.latent > 512 || c.d_model > 1024 || c.ctx_window < 1))
     throw std::runtime_error("context-aware router needs mla.latent_dim in {256, 512}, "
                              "d_model <= 1024, router.local_context >= 1");
+  if (c.mhc > 1 && (c.ctx || c.d_model > 4096 || c.mhc_iters < 0))
+    throw std::runtime_error("mHC needs d_model <= 4096 and the plain router");
   return c;
 }
 
@@ -332,6 +346,12 @@ struct Layer {
   // local_context_out [D, L] and context_out [D, D] packed bf16
   float *ctx_down = nullptr, *ctx_ln_w = nullptr, *ctx_ln_b = nullptr, *ctx_gate = nullptr;
   uint16_t *ctx_local_out = nullptr, *ctx_out = nullptr;
+  // mHC: the maps' projection theta (packed [n16, S D]) and fp32 parameters
+  // (alpha = pre, post, residual)
+  uint16_t* mhc_theta = nullptr;
+  float *mhc_map_norm = nullptr, *mhc_pre_bias = nullptr, *mhc_post_bias = nullptr,
+        *mhc_res_bias = nullptr, *mhc_alpha = nullptr, *mhc_gating = nullptr,
+        *mhc_scale = nullptr, *mhc_ln_w = nullptr, *mhc_ln_b = nullptr;
 };
 
 struct Model {
@@ -340,6 +360,8 @@ struct Model {
   uint16_t* embed = nullptr;    // row-major [V, D] (token lookup)
   uint16_t* lm_head = nullptr;  // packed copy (tied LM head)
   float* final_norm = nullptr;
+  float* stream_seed = nullptr;     // mHC: [S, D]
+  uint16_t* mhc_collapse = nullptr; // mHC: packed [D, S D]
   std::vector<Layer> layers;
   std::vector<void*> allocs;
 
@@ -398,6 +420,15 @@ std::unique_ptr<Model> load_model(const char* path) {
   const auto& fn = ck.get("final_norm.weight");
   expect_shape(fn, {D}, "final_norm.weight");
   m->final_norm = m->upload(as_f32(fn));
+  const int SM = c.mhc;
+  if (SM > 1) {  // model.py:389-390,415-421 (stream_seed, mhc_collapse)
+    const auto& sd = ck.get("stream_seed");
+    expect_shape(sd, {SM, D}, "stream_seed");
+    m->stream_seed = m->upload(as_f32(sd));
+    const auto& cl = ck.get("mhc_collapse.weight");
+    expect_shape(cl, {D, static_cast<int64_t>(SM) * D}, "mhc_collapse.weight");
+    m->mhc_collapse = m->upload_packed(as_bf16(cl), 1, D, SM * D);
+  }
   for (size_t l = 0; l < c.kinds.size(); ++l) {
     Layer L;
     L.kind = c.kinds[l];
@@ -412,6 +443,29 @@ std::unique_ptr<Model> load_model(const char* path) {
       expect_shape(t, shape, p + n);
       return as_bf16(t);
     };
+    if (SM > 1) {  // the block's hyper-connection (mhc.py:63-84; names of model.cpp:34-63)
+      auto scalar = [&](const std::string& n) {
+        const auto& t = ck.get(p + n);
+        if (!(t.shape.empty() || t.shape == std::vector<int64_t>{1}))
+          throw std::runtime_error("unexpected shape for " + p + n);
+        return as_f32(t)[0];
+      };
+      const int NT = 2 * SM + SM * SM;
+      L.mhc_theta = m->upload_packed(
+          concat_rows({mat_bf16("mhc.theta.weight", {NT, static_cast<int64_t>(SM) * D})},
+                      static_cast<size_t>(c.mhc_n16()) * SM * D),
+          1, c.mhc_n16(), SM * D);
+      L.mhc_map_norm = vec_f32("mhc.mapping_norm.weight", {static_cast<int64_t>(SM) * D});
+      L.mhc_pre_bias = vec_f32("mhc.pre_bias", {SM});
+      L.mhc_post_bias = vec_f32("mhc.post_bias", {SM});
+      L.mhc_res_bias = vec_f32("mhc.residual_bias", {SM, SM});
+      L.mhc_alpha = m->upload(std::vector<float>{scalar("mhc.alpha_pre"), scalar("mhc.alpha_post"),
+                                                 scalar("mhc.alpha_residual")});
+      L.mhc_gating = m->upload(std::vector<float>{scalar("mhc.gating_logit")});
+      L.mhc_scale = vec_f32("mhc.stream_scale", {SM, D});
+      L.mhc_ln_w = vec_f32("mhc.stream_norm.weight", {D});
+      L.mhc_ln_b = vec_f32("mhc.stream_norm.bias", {D});
+    }
     L.mix_norm = vec_f32("mixer_norm.weight", {D});
     L.ffn_norm = vec_f32("ffn_norm.weight", {D});
     L.router_norm = vec_f32("moe.router.norm.weight", {D});
@@ -530,6 +584,12 @@ struct Buffers {  // activations for `rows` token rows
   // window means [rows, L] and local_context_out [rows, D] bf16
   float *c_local = nullptr, *c_lat = nullptr, *c_c = nullptr, *c_logits = nullptr;
   uint16_t *c_ctx = nullptr, *c_d = nullptr;
+  // mHC: streams X [rows, S, D], their bf16 copy [rows, S D] (GEMM operand),
+  // map logits [rows, n16], maps [rows, S + S^2], a sublayer's output U
+  // [rows, D]; all-ones row mask (clearing U) and identity route positions
+  float *mX = nullptr, *mraw = nullptr, *mmaps = nullptr, *mU = nullptr;
+  uint16_t* mxb = nullptr;
+  int32_t *mones = nullptr, *mident = nullptr;
   void* ws = nullptr;
   int64_t ws_bytes = 0;
   DeviceArena arena;
@@ -592,6 +652,21 @@ void alloc_buffers(const Config& c, int rows, int B, int T, Buffers& b) {
     b.c_logits = b.arena.zeros<float>(static_cast<size_t>(rows) * c.experts);
     b.c_ctx = b.arena.zeros<uint16_t>(static_cast<size_t>(rows) * c.latent);
     b.c_d = b.arena.zeros<uint16_t>(static_cast<size_t>(rows) * D);
+  }
+  if (c.mhc > 1) {
+    const size_t S = c.mhc;
+    b.mX = b.arena.zeros<float>(static_cast<size_t>(rows) * S * D);
+    b.mxb = b.arena.zeros<uint16_t>(static_cast<size_t>(rows) * S * D);
+    b.mraw = b.arena.zeros<float>(static_cast<size_t>(rows) * c.mhc_n16());
+    b.mmaps = b.arena.zeros<float>(static_cast<size_t>(rows) * (S + S * S));
+    b.mU = b.arena.zeros<float>(static_cast<size_t>(rows) * D);
+    std::vector<int32_t> ones(rows, 1), ident(static_cast<size_t>(rows) * kx);
+    for (size_t i = 0; i < ident.size(); ++i) ident[i] = static_cast<int32_t>(i);
+    b.mones = b.arena.zeros<int32_t>(rows);
+    b.mident = b.arena.zeros<int32_t>(ident.size());
+    check_hip(hipMemcpy(b.mones, ones.data(), ones.size() * 4, hipMemcpyHostToDevice), "ones");
+    check_hip(hipMemcpy(b.mident, ident.data(), ident.size() * 4, hipMemcpyHostToDevice),
+              "ident");
   }
   b.counts = b.arena.zeros<int32_t>(EX);
   b.offsets = b.arena.zeros<int32_t>(EX + 1);
@@ -813,8 +888,134 @@ const float* next_norm_of(const Model& m, int loop, int l, int loops) {
   return loop + 1 < loops ? m.layers[0].mix_norm : m.final_norm;
 }
 
+// ------------------------------------------------------------------ mHC
+// Multi-stream hyper-connections around each sublayer (model/model.py:119-126,
+// 177-264; model/layers/mhc.py:156-231).  The kernels and their order are the
+// Python engine's (HybridDecoder._step_body_mhc / _prefill_mhc), so the two
+// engines agree bit for bit.
+constexpr float kMhcMapEps = 1.1920928955078125e-07f;  // nn.RMSNorm(eps=None), fp32
+
+// The sublayer input of layer L from the streams: maps into b.mmaps, h into b.h.
+void mhc_read(const Model& m, const Layer& L, Buffers& b, int rows, const float* norm,
+              hipStream_t st) {
+  const Config& c = m.cfg;
+  const int S = c.mhc, D = c.d_model;
+  check_call(llmy_rmsnorm_f32_bf16(b.mX, L.mhc_map_norm, b.mxb, rows, S * D, kMhcMapEps, st),
+             "llmy_rmsnorm_f32_bf16 (mHC)");
+  linear(b.mxb, L.mhc_theta, b.mraw, nullptr, rows, c.mhc_n16(), S * D, kStoreF32, st);
+  check_call(llmy_mhc_read(b.mX, b.mraw, c.mhc_n16(), L.mhc_pre_bias, L.mhc_post_bias,
+                           L.mhc_res_bias, L.mhc_alpha, c.mhc_iters, L.mhc_ln_w, L.mhc_ln_b, 1e-5f,
+                           norm, c.eps, b.mmaps, b.h, rows, S, D, st),
+             "llmy_mhc_read");
+}
+
+void mhc_write(const Model& m, const Layer& L, Buffers& b, int rows, hipStream_t st) {
+  check_call(llmy_mhc_write(b.mX, b.mU, m.cfg.d_model, b.mmaps, L.mhc_scale, L.mhc_gating, rows,
+                            m.cfg.mhc, m.cfg.d_model, st),
+             "llmy_mhc_write");
+}
+
+void mhc_clear_u(const Model& m, Buffers& b, int rows, hipStream_t st) {
+  check_call(llmy_zero_rows(b.mU, static_cast<int64_t>(m.cfg.d_model) * 4, rows, b.mones, st),
+             "llmy_zero_rows");
+}
+
+// The MoE of layer L on b.h into U: router + top-k, then route-indexed experts
+// (decode, where the sizes allow) or permutation + grouped experts.
+void mhc_moe(const Model& m, const Layer& L, Buffers& b, int rows, bool sequence, hipStream_t st) {
+  const Config& c = m.cfg;
+  const int D = c.d_model, E = c.experts, k = c.top_k, Hf = c.hidden;
+  const int kx = c.routes(), EX = c.all_experts();
+  check_call(llmy_router_topk_bf16(b.h, L.router_norm, L.w_router, nullptr, b.idx, b.gates, rows,
+                                   D, E, k, c.eps, st),
+             "llmy_router_topk_bf16");
+  const int32_t* ids = b.idx;
+  const float* gts = b.gates;
+  if (c.shared > 0) {
+    check_call(llmy_moe_append_shared(b.idx, b.gates, b.idx_all, b.gates_all, rows, k, E,
+                                      c.shared, st),
+               "llmy_moe_append_shared");
+    ids = b.idx_all;
+    gts = b.gates_all;
+  }
+  const int32_t* route_pos = b.mident;
+  if (!sequence && fused_route(c, rows)) {
+    check_call(llmy_moe_experts_routed_bf16(b.h, ids, gts, L.w_gate_up, L.w_down, b.act, b.y,
+                                            rows, D, Hf, EX, kx, kPacked, st),
+               "llmy_moe_experts_routed_bf16");
+  } else {
+    check_call(llmy_moe_permute(ids, rows * kx, EX, b.counts, b.offsets, b.sorted, b.route_pos,
+                                st),
+               "llmy_moe_permute");
+    check_call(llmy_moe_experts_bf16(b.h, b.offsets, b.sorted, gts, L.w_gate_up, L.w_down, b.act,
+                                     b.y, rows, D, Hf, EX, kx, kPacked, st),
+               "llmy_moe_experts_bf16");
+    route_pos = b.route_pos;
+  }
+  check_call(llmy_moe_combine(b.y, route_pos, b.mU, rows, D, kx, 1, st), "llmy_moe_combine");
+}
+
+// Collapse the streams, final RMSNorm, LM head, argmax (model.py:699-705).
+void mhc_head(const Model& m, State& s, Buffers& b, int rows, hipStream_t st) {
+  const Config& c = m.cfg;
+  const int S = c.mhc, D = c.d_model;
+  check_call(llmy_f32_to_bf16(b.mX, b.mxb, static_cast<int64_t>(rows) * S * D, st),
+             "llmy_f32_to_bf16");
+  linear(b.mxb, m.mhc_collapse, b.mU, nullptr, rows, D, S * D, kStoreF32, st);
+  check_call(llmy_rmsnorm_f32_bf16(b.mU, m.final_norm, b.h, rows, D, c.eps, st), "rmsnorm");
+  linear(b.h, m.lm_head, s.logits, nullptr, rows, c.vocab, D, kStoreF32, st);
+  check_call(llmy_sample_argmax_f32(s.logits, rows, c.vocab, s.next, st), "argmax");
+}
+
+void decode_step_mhc(Model& m, State& s, int loops) {
+  hipStream_t st_ = s.stream;
+  const Config& c = m.cfg;
+  Buffers& b = s.step;
+  const int B = s.B, D = c.d_model, n = static_cast<int>(m.layers.size());
+  const int Hhd = c.attn_heads * c.attn_head_dim, HV = c.gdn_heads * c.dv;
+  check_call(llmy_mhc_embed(b.tokens, m.embed, m.stream_seed, b.mX, B, c.mhc, D, c.vocab, st_),
+             "llmy_mhc_embed");
+  for (int loop = 0; loop < loops; ++loop) {
+    for (int l = 0; l < n; ++l) {
+      const Layer& L = m.layers[l];
+      LayerState& st = s.layers[static_cast<size_t>(loop) * n + l];
+      mhc_read(m, L, b, B, L.mix_norm, st_);
+      if (L.kind == kAttn) {
+        linear(b.h, L.wqkv, b.qkv, nullptr, B, 3 * Hhd, D, kStoreBf16, st_);
+        check_call(llmy_banded_attn_decode_bf16(b.qkv, b.qkv + Hhd, b.qkv + 2 * Hhd, 3 * Hhd,
+                                                3 * Hhd, st.k, st.v, s.pos, b.ao, B, c.attn_heads,
+                                                c.attn_head_dim, c.window,
+                                                1.0f / std::sqrt(static_cast<float>(c.attn_head_dim)),
+                                                st_),
+                   "llmy_banded_attn_decode_bf16");
+        linear(b.ao, L.wo, b.mU, nullptr, B, D, Hhd, kStoreF32, st_);
+      } else {
+        mhc_clear_u(m, b, B, st_);
+        const bool pp = b.proj_parts != nullptr;
+        float* proj = pp ? b.proj_parts : b.proj;
+        linear(b.h, L.wproj, proj, nullptr, B, c.nproj16(), D, pp ? kPartialF32 : kStoreF32, st_);
+        check_call(llmy_gdn_step_fused_f32(proj, c.nproj16(), pp ? D / 256 : 1, L.bb, L.decay,
+                                           st.S, b.go, b.h, st.hist, L.conv, b.cg, D, 4, B,
+                                           c.gdn_heads, c.dk, c.dv, st_),
+                   "llmy_gdn_step_fused_f32");
+        linear(b.go, L.wout, b.mU, b.cg, B, D, HV, kResidGated, st_);
+      }
+      mhc_write(m, L, b, B, st_);
+      mhc_read(m, L, b, B, L.ffn_norm, st_);
+      mhc_moe(m, L, b, B, false, st_);
+      mhc_write(m, L, b, B, st_);
+    }
+  }
+  mhc_head(m, s, b, B, st_);
+  s.last_loops = loops;
+}
+
 // One decode step for all B rows; tokens already in s.step.tokens, s.pos set.
 void decode_step(Model& m, State& s, int loops) {
+  if (m.cfg.mhc > 1) {
+    decode_step_mhc(m, s, loops);
+    return;
+  }
   hipStream_t st_ = s.stream;
   const Config& c = m.cfg;
   Buffers& b = s.step;
@@ -873,6 +1074,71 @@ void decode_step(Model& m, State& s, int loops) {
   s.last_loops = loops;
 }
 
+// Prefill with mHC: the sequence kernels of prefill() with each sublayer's
+// output in U, written into the [B T, S, D] streams (tokens already in b).
+void prefill_mhc(Model& m, State& s, Buffers& b, int T) {
+  hipStream_t st_ = s.stream;
+  const Config& c = m.cfg;
+  const int B = s.B, R = B * T, D = c.d_model, S = c.mhc, n = static_cast<int>(m.layers.size());
+  const int Hhd = c.attn_heads * c.attn_head_dim;
+  check_call(llmy_mhc_embed(b.tokens, m.embed, m.stream_seed, b.mX, R, S, D, c.vocab, st_),
+             "llmy_mhc_embed");
+  const int loops = m.loops;
+  for (int loop = 0; loop < loops; ++loop) {
+    for (int l = 0; l < n; ++l) {
+      const Layer& L = m.layers[l];
+      LayerState& st = s.layers[static_cast<size_t>(loop) * n + l];
+      mhc_read(m, L, b, R, L.mix_norm, st_);
+      if (L.kind == kAttn) {
+        const size_t slice = static_cast<size_t>(Hhd) * D;
+        linear(b.h, L.wqkv, b.q, nullptr, R, Hhd, D, kStoreBf16, st_);
+        linear(b.h, L.wqkv + slice, b.k, nullptr, R, Hhd, D, kStoreBf16, st_);
+        linear(b.h, L.wqkv + 2 * slice, b.v, nullptr, R, Hhd, D, kStoreBf16, st_);
+        check_call(llmy_banded_attn_prefill_bf16(b.q, b.k, b.v, b.ao, B, T, c.attn_heads,
+                                                 c.attn_head_dim, c.window,
+                                                 1.0f / std::sqrt(static_cast<float>(c.attn_head_dim)),
+                                                 st_),
+                   "llmy_banded_attn_prefill_bf16");
+        check_call(llmy_kv_cache_fill_bf16(b.k, b.v, Hhd, st.k, st.v, B, T, c.attn_heads,
+                                           c.attn_head_dim, c.window, st_),
+                   "llmy_kv_cache_fill_bf16");
+        linear(b.ao, L.wo, b.mU, nullptr, R, D, Hhd, kStoreF32, st_);
+      } else {
+        const int H = c.gdn_heads, HV = H * c.dv;
+        mhc_clear_u(m, b, R, st_);
+        linear(b.h, L.wproj, b.proj, nullptr, R, c.nproj16(), D, kStoreF32, st_);
+        check_call(llmy_gdn_prefill_prep_f32(b.proj, c.nproj16(), L.bb, L.decay, b.gq, b.gk, b.gv,
+                                             b.beta, b.g, R, H, c.dk, c.dv, st_),
+                   "llmy_gdn_prefill_prep_f32");
+        check_call(llmy_gdn_prefill_bf16(b.gq, b.gk, b.gv, b.beta, b.g, st.S, b.go, b.ws,
+                                         b.ws_bytes, B, T, H, c.dk, c.dv, st_),
+                   "llmy_gdn_prefill_bf16");
+        check_call(llmy_gdn_gate_bf16(b.go, b.proj, c.nproj16(), 2 * H * c.dk + HV, b.go, R, HV,
+                                      st_),
+                   "llmy_gdn_gate_bf16");
+        check_call(llmy_gdn_conv_gate_prefill(b.h, st.hist, L.conv, b.cg, B, T, D, 4, st_),
+                   "llmy_gdn_conv_gate_prefill");
+        linear(b.go, L.wout, b.mU, b.cg, R, D, HV, kResidGated, st_);
+      }
+      mhc_write(m, L, b, R, st_);
+      mhc_read(m, L, b, R, L.ffn_norm, st_);
+      mhc_moe(m, L, b, R, true, st_);
+      mhc_write(m, L, b, R, st_);
+    }
+  }
+  // each sequence's last streams -> the decode buffers, then the head
+  const size_t row = static_cast<size_t>(S) * D * 4;
+  check_hip(hipMemcpy2DAsync(s.step.mX, row, b.mX + static_cast<size_t>(T - 1) * S * D, T * row,
+                             row, B, hipMemcpyDeviceToDevice, st_),
+            "last streams");
+  mhc_head(m, s, s.step, B, st_);
+  s.hpos.assign(B, T);
+  check_hip(hipMemcpyAsync(s.pos, s.hpos.data(), sizeof(int32_t) * B, hipMemcpyHostToDevice, st_),
+            "pos");
+  check_hip(hipStreamSynchronize(st_), "prefill");
+  s.last_loops = loops;
+}
+
 // Prefill of B fresh sequences of T tokens each (tokens on the host, [B, T]).
 void prefill(Model& m, State& s, const int32_t* tokens, int T, bool tokens_on_device) {
   hipStream_t st_ = s.stream;
@@ -890,6 +1156,10 @@ void prefill(Model& m, State& s, const int32_t* tokens, int T, bool tokens_on_de
   check_hip(hipMemcpyAsync(b.tokens, tokens, sizeof(int32_t) * R,
                            tokens_on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice, st_),
             "tokens");
+  if (c.mhc > 1) {
+    prefill_mhc(m, s, b, T);
+    return;
+  }
   check_call(llmy_embed_norm_bf16(b.tokens, m.embed, m.layers[0].mix_norm, b.x, b.h, R, D, c.vocab,
                                   c.eps, st_),
              "llmy_embed_norm_bf16");
@@ -1027,7 +1297,9 @@ int32_t llmy_num_loops(const llmy_model* m) {
 int32_t llmy_max_loops(const llmy_model* m) {
   return m ? reinterpret_cast<const Model*>(m)->cfg.num_loops : 0;
 }
-int32_t llmy_mhc_streams(const llmy_model* m) { return m ? 1 : 0; }
+int32_t llmy_mhc_streams(const llmy_model* m) {
+  return m ? reinterpret_cast<const Model*>(m)->cfg.mhc : 0;
+}
 
 void llmy_set_num_loops(llmy_model* m, int32_t n) {
   if (!m) return;

@@ -517,7 +517,7 @@ int32_t llmy_d_model(const llmy_model* m);               /* llmy.h:36 */
 /* loops a forward runs by default (set_num_loops, clamped to the built ones) */
 int32_t llmy_num_loops(const llmy_model* m);             /* llmy.h:37 */
 int32_t llmy_max_loops(const llmy_model* m);             /* llmy.h:38 */
-/* 1: this block stack has no mHC stream mixing */
+/* residual streams per token: mhc.streams when mhc.enabled, else 1 */
 int32_t llmy_mhc_streams(const llmy_model* m);           /* llmy.h:39 */
 void    llmy_set_num_loops(llmy_model* m, int32_t n);    /* llmy.h:40 */
 void    llmy_set_fixed_loops(llmy_model* m, int32_t n);  /* llmy.h:41 */

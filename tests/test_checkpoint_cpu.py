@@ -156,6 +156,42 @@ def test_context_router_roundtrip(lib, tmp_path):
         config_from_text(config_text(TINY).replace("router.context_aware=0", "router.context_aware=2"))
 
 
+def test_mhc_roundtrip(lib, tmp_path):
+    """mHC parameters under the reference's names (llmy_cuda/src/model.cpp:34-63,
+    178-180): per block mhc.theta / mapping_norm / biases / stream_scale /
+    stream_norm, the alphas and the gating logit as 0-d tensors, stream_seed
+    and mhc_collapse.weight; config keys mhc.enabled / streams /
+    sinkhorn_iterations with the reference's defaults when absent
+    (llmy_cuda/include/config.h:27-29)."""
+    from dataclasses import replace
+    cfg = replace(TINY, mhc_streams=4, mhc_sinkhorn_iters=10)
+    w = init_weights(cfg, seed=6)
+    path = tmp_path / "mhc.llmy"
+    save_llmy(path, cfg, w)
+    back_cfg, back = load_weights(path)
+    assert back_cfg == cfg
+    for key, t in w.items():
+        assert torch.equal(back[key], t), key
+    text = config_text(cfg)
+    assert "mhc.enabled=1\n" in text and "mhc.streams=4\n" in text
+    assert file_name(cfg, "L1.mhc_theta") == "recurrent_core.1.mhc.theta.weight"
+    assert file_name(cfg, "mhc_collapse") == "mhc_collapse.weight"
+    st, desc = _describe(lib, path)
+    assert st == 0, lib.llmy_last_error()
+    lines = desc.split("--\n")[1].splitlines()
+    names = {l.split()[0]: l.split() for l in lines}
+    for n in ("alpha_pre", "alpha_post", "alpha_residual", "gating_logit"):
+        assert names[f"recurrent_core.0.mhc.{n}"][2] == "0"          # 0-d
+    assert "stream_seed" in names and "mhc_collapse.weight" in names
+    # defaults: no mhc keys -> 4 streams, 20 iterations; enabled=0 -> one stream
+    bare = "".join(l + "\n" for l in config_text(TINY).splitlines() if not l.startswith("mhc."))
+    c0 = config_from_text(bare)
+    assert c0.mhc_streams == 4 and c0.mhc_sinkhorn_iters == 20
+    assert config_from_text(config_text(TINY)).mhc_streams == 1
+    with pytest.raises(ValueError):
+        config_from_text(config_text(TINY).replace("mhc.streams=1", "mhc.streams=4"))
+
+
 @pytest.mark.parametrize("damage", ["magic", "version", "truncate_index", "payload", "name_len",
                                     "shape"])
 def test_native_parser_rejects_corrupt_files(lib, tiny_file, tmp_path, damage):

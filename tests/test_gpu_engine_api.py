@@ -269,6 +269,42 @@ def test_state_reset_rows_matches_python_engine(lib, tmp_path):
         lib.llmy_free(m)
 
 
+def test_mhc_matches_python_engine(lib, tmp_path):
+    """A 4-stream mHC model (model/layers/mhc.py in the block of model.py:
+    177-264): llmy_mhc_streams reports 4, and the native engine's prefill and
+    graph-replayed decode logits equal the Python engine's bit for bit."""
+    from dataclasses import replace
+    from hybrid_llm_amd.engine import HybridDecoder
+    cfg = replace(C1, layer_kinds=("attn", "gdn"), mhc_streams=4, mhc_gating_init=0.5)
+    w = init_weights(cfg, seed=7)
+    path = tmp_path / "mhc.llmy"
+    save_llmy(path, cfg, w)
+    B, T = 2, 24
+    prompt = torch.randint(0, cfg.vocab, (B, T), generator=torch.Generator().manual_seed(14),
+                           dtype=torch.int32)
+    print("[engine-api] mHC: prefill 24 + decode 3, B=2", flush=True)
+    m = lib.llmy_load(str(path).encode())
+    assert m, lib.llmy_last_error()
+    try:
+        lib.llmy_mhc_streams.argtypes = [C.c_void_p]
+        lib.llmy_mhc_streams.restype = C.c_int32
+        assert lib.llmy_mhc_streams(m) == 4
+        s = lib.llmy_state_new_batch(m, B)
+        assert s
+        out = torch.zeros(B, cfg.vocab, device="cuda")
+        assert lib.llmy_prefill_batch(m, s, prompt.cuda().data_ptr(), T, out.data_ptr()) == 0
+        py = HybridDecoder(cfg, w, B)
+        assert torch.equal(out, py.prefill(prompt.cuda()))
+        nxt = torch.zeros(B, dtype=torch.int32)
+        for _ in range(3):
+            assert lib.llmy_greedy_tokens(s, nxt.data_ptr()) == 0
+            assert lib.llmy_decode_batch(m, s, nxt.data_ptr(), None, 0, out.data_ptr()) == 0
+            assert torch.equal(out, py.step(nxt.cuda()))
+        lib.llmy_state_free(s)
+    finally:
+        lib.llmy_free(m)
+
+
 def test_context_router_matches_python_engine(lib, tmp_path):
     """router.context_aware=1 (local latent window of 8 tokens, latent 256):
     the native engine's prefill and decode logits equal the Python engine's
