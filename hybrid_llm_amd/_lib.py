@@ -70,6 +70,20 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
                            _I, _I, _I, _P]),
     "llmy_mhc_write": (_I, [_P, _P, _I64, _P, _P, _P, _I, _I, _I, _P]),
     "llmy_f32_to_bf16": (_I, [_P, _P, _I64, _P]),
+    "llmy_cmp_workspace_bytes": (C.c_int64, [_I, _I, _I, _I]),
+    "llmy_cmp_local_prefill_bf16": (_I, [_P, _I64, _P, _I64, _P, _I64, _P, _I64, _I, _I, _I, _I,
+                                         _I, _I, _F, _P, _I64, _P]),
+    "llmy_cmp_memory_prefill_bf16": (_I, [_P, _I64, _P, _I64, _P, _I64, _P, _I64, _I, _I, _I,
+                                          _I, _I, _I, _I, _I, _F, _P, _I64, _P]),
+    "llmy_cmp_local_decode_bf16": (_I, [_P, _I64, _P, _P, _I64, _P, _P, _P, _P, _I64, _I, _I, _I,
+                                        _I, _I, _F, _P, _I64, _P]),
+    "llmy_cmp_memory_decode_bf16": (_I, [_P, _I64, _P, _P, _P, _P, _P, _I64, _I, _I, _I, _I, _I,
+                                         _I, _F, _P, _I64, _P]),
+    "llmy_cmp_pool_prefill_bf16": (_I, [_P, _I64, _P, _P, _P, _I, _I, _I, _I, _P]),
+    "llmy_cmp_pool_step_bf16": (_I, [_P, _I64, _P, _P, _P, _P, _I, _I, _I, _P]),
+    "llmy_cmp_commit_bf16": (_I, [_P, _I64, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P]),
+    "llmy_cmp_memory_fill_bf16": (_I, [_P, _I64, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P]),
+    "llmy_cmp_ring_fill_bf16": (_I, [_P, _I64, _P, _I, _I, _I, _I, _P]),
     # engine handles (the reference binding's argtypes, llmy_cuda/python/sample.py:110-170)
     "llmy_load": (_P, [C.c_char_p]),
     "llmy_free": (None, [_P]),

@@ -1,0 +1,661 @@
+// Compressed-memory mixers (CSA, HCA): the attention branches and the
+// temporal compressor's state.
+//
+// Both mixers score H heads of width Dh (CSA: index_heads x index_head_dim,
+// model/layers/csa.py:21-24; HCA: one head of width d_model, hca.py:24-25)
+// against a candidate set and apply the heads' mean probabilities to one
+// value stream of width Dv shared by the heads (csa.py:74-75,131,203-206,257):
+//   * local branch: the last W tokens, the current one included
+//     (csa.py:55-75,185-206; hca.py:46-63,119-138), dense softmax;
+//   * memory branch: the compressor's summaries of complete ratio-token
+//     blocks (compressed_attention.py:109-123), visible from the block's last
+//     token on (csa.py:94,242; hca.py:79,171), dense softmax (hca.py:84-87) or
+//     softmax over each head's top_k (csa.py:99-105; hca.py:88-93; ties keep
+//     the lower index; invisible entries weigh 0, none visible gives 0).
+//
+// MI355X mapping:
+//   * selection kernels write, per (query, head), a list of probabilities over
+//     the candidate slots (dense: the slot is the index) or of (index,
+//     probability) pairs (top-k) into a caller workspace; one apply kernel per
+//     query then sums the heads (dense lists) in LDS and streams the value rows
+//     once per nonzero weight, 4 channels per thread, fp32 accumulation;
+//   * prefill scores are MFMA tiles S^T = K Q^T (v_mfma_f32_32x32x16_bf16, 32
+//     candidates x 32 queries, operands straight from global memory so any
+//     multiple-of-16 head width works), stored scaled and masked to LDS in
+//     row passes sized to the candidate count, then each wave reduces its
+//     rows;
+//   * decode scores use G = min(64, Dh/8) lanes per candidate (16-byte loads,
+//     xor-shuffle sums), one workgroup per (row, head);
+//   * memory entries carry a tag = position + 1 (0 = empty slot), so zeroed
+//     state is an empty memory and row resets are plain row clears.
+// D layout of a 32x32 MFMA result: lane l, register r holds row
+// (r & 3) + 8 (r >> 2) + 4 (l >> 5), column l & 31.
+#include "common.hpp"
+#include "abi_util.hpp"
+
+namespace llmy {
+
+typedef float f32x16c __attribute__((ext_vector_type(16)));
+
+constexpr float kLog2eC = 1.4426950408889634f;
+enum CmpMode { kBand = 0, kMemDense = 1, kMemTopK = 2 };
+constexpr int kCmpLdsBytes = 65536;   // score budget of one prefill selection workgroup
+
+// One wave turns a row of log2-domain scores into a dense list over n slots:
+// slot j reads score srow[j + off] and is a candidate when jlo <= j < jhi
+// (non-candidates and -inf scores weigh 0; a row with no finite score is 0).
+__device__ __forceinline__ void dense_row(const float* srow, int n, int off, int jlo, int jhi,
+                                          int lane, float* out) {
+  float m = -INFINITY;
+  for (int j = lane; j < n; j += kWave)
+    if (j >= jlo && j < jhi) m = fmaxf(m, srow[j + off]);
+  m = wave_max(m);
+  float s = 0.f;
+  if (m != -INFINITY)
+    for (int j = lane; j < n; j += kWave)
+      if (j >= jlo && j < jhi) s += exp2_fast(srow[j + off] - m);
+  s = wave_sum(s);
+  const float inv = s > 0.f ? 1.0f / s : 0.f;
+  for (int j = lane; j < n; j += kWave)
+    out[j] = (j >= jlo && j < jhi && inv > 0.f) ? exp2_fast(srow[j + off] - m) * inv : 0.f;
+}
+
+// One wave: the k largest of srow[0, n) (ties to the lower index; the row is
+// consumed), softmax over them; pairs (index, probability) to iout / wout.
+// Selections that are -inf (fewer than k candidates) weigh 0 with index 0.
+__device__ __forceinline__ void topk_row(float* srow, int n, int k, int lane, float* wout,
+                                         int32_t* iout) {
+  float mine = -INFINITY;
+  int32_t mine_idx = 0;
+  for (int it = 0; it < k; ++it) {
+    uint64_t best = 0;
+    for (int j = lane; j < n; j += kWave) best = umax64(best, value_index_key(srow[j], j));
+    best = wave_max_u64(best);
+    const int idx = static_cast<int>(key_index(best));
+    const bool ok = best != 0 && idx >= 0 && idx < n;
+    const float v = ok ? srow[idx] : -INFINITY;
+    if (lane == it) {
+      mine = v;
+      mine_idx = (ok && v != -INFINITY) ? idx : 0;
+    }
+    __builtin_amdgcn_wave_barrier();
+    if (ok && lane == 0) srow[idx] = -INFINITY;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+  const float m = wave_max(lane < k ? mine : -INFINITY);
+  const float e = (lane < k && mine != -INFINITY) ? exp2_fast(mine - m) : 0.f;
+  const float s = wave_sum(e);
+  if (lane < k) {
+    wout[lane] = s > 0.f ? e / s : 0.f;
+    iout[lane] = mine_idx;
+  }
+}
+
+// ---------------------------------------------------------------- prefill
+// Workgroup = (head h, 32-query block, row b), h fastest.  Candidates:
+//   band: keys [max(0, t0 - W + 1), min(T - 1, t0 + 31)] of row b (q/k rows
+//         b*T + t); the list of query t has W slots, slot j = key t - W + 1 + j;
+//   memory: entries [0, nv), nv = min(n, min(T, t0 + 32) / ratio) (rows b*n + i,
+//         entry i visible from position (i + 1) ratio - 1 on); dense lists have
+//         n slots, top-k lists top_k pairs.
+template <int MODE>
+__global__ __launch_bounds__(256) void cmp_select_prefill_kernel(
+    const uint16_t* __restrict__ q, int64_t q_ld, const uint16_t* __restrict__ k, int64_t k_ld,
+    int T, int n, int H, int Dh, int W, int ratio, int top_k, int Kmax, int rows_pass,
+    float scale_log2, float* __restrict__ wl, int32_t* __restrict__ il) {
+  extern __shared__ float sc[];
+  const int h = blockIdx.x % H;
+  const int rest = blockIdx.x / H;
+  const int nqb = (T + 31) / 32;
+  const int qb = rest % nqb;
+  const int b = rest / nqb;
+  const int t0 = qb * 32;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int col = lane & 31, half = lane >> 5;
+  int c_lo, nc;
+  if (MODE == kBand) {
+    c_lo = max(0, t0 - W + 1);
+    nc = min(T - 1, t0 + 31) - c_lo + 1;
+  } else {
+    c_lo = 0;
+    nc = min(n, min(T, t0 + 32) / ratio);
+  }
+  const int ntile = (nc + 31) / 32;
+  const int ncp = max(ntile, 1) * 32;
+  const bool q_ok = t0 + col < T;
+  const uint16_t* qrow =
+      q + static_cast<int64_t>(b * T + (q_ok ? t0 + col : 0)) * q_ld + h * Dh + 8 * half;
+  const int64_t krow0 = MODE == kBand ? static_cast<int64_t>(b) * T : static_cast<int64_t>(b) * n;
+  for (int p0 = 0; p0 < 32; p0 += rows_pass) {
+    if (ntile == 0) {   // no candidate yet (memory before the first block end)
+      for (int i = threadIdx.x; i < rows_pass * ncp; i += 256) sc[i] = -INFINITY;
+    }
+    for (int tile = wave; tile < ntile; tile += 4) {
+      const int c0 = c_lo + 32 * tile;
+      const bool c_ok = c0 + col < c_lo + nc;
+      const uint16_t* krow = k + (krow0 + (c_ok ? c0 + col : c_lo)) * k_ld + h * Dh + 8 * half;
+      f32x16c acc;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+      for (int s = 0; s < Dh / 16; ++s) {
+        const uint4 a = c_ok ? *reinterpret_cast<const uint4*>(krow + 16 * s) : uint4{0, 0, 0, 0};
+        const uint4 bq = q_ok ? *reinterpret_cast<const uint4*>(qrow + 16 * s) : uint4{0, 0, 0, 0};
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a), as_bf16x8(bq), acc, 0, 0, 0);
+      }
+      const int row = col - p0;
+      if (row >= 0 && row < rows_pass) {
+        const int t = t0 + col;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int cj = c0 + (r & 3) + 8 * (r >> 2) + 4 * half;
+          bool vis = t < T && cj < c_lo + nc;
+          if (MODE == kBand) vis = vis && cj <= t && t - cj < W;
+          else vis = vis && (cj + 1) * ratio - 1 <= t;
+          sc[row * ncp + (cj - c_lo)] = vis ? acc[r] * scale_log2 : -INFINITY;
+        }
+      }
+    }
+    __syncthreads();
+    for (int row = wave; row < rows_pass; row += 4) {
+      const int t = t0 + p0 + row;
+      if (t >= T) continue;
+      float* srow = sc + row * ncp;
+      const int64_t lb = (static_cast<int64_t>(b * T + t) * H + h) * Kmax;
+      if (MODE == kBand) {
+        // slot j <-> key t - W + 1 + j (a candidate when >= 0) <-> score
+        // index key - c_lo, inside the row for every candidate key
+        dense_row(srow, W, t - W + 1 - c_lo, max(0, W - 1 - t), W, lane, wl + lb);
+      } else if (MODE == kMemDense) {
+        dense_row(srow, Kmax, 0, 0, nc, lane, wl + lb);
+      } else {
+        topk_row(srow, nc, top_k, lane, wl + lb, il + lb);
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------- decode
+// Workgroup = (head h, row b).  band: candidate j in [0, W) <-> key
+// p - W + 1 + j (p = pos[b]; keys < 0 are not candidates), the current key
+// from k_new, older ones from the ring (slot key % W); the workgroup also
+// stores its head's slice of k_new (and head 0 the v_new row) into slot p % W,
+// which held key p - W, outside this step's window.  memory: candidates are
+// the C slots, visible when 1 <= tag <= p + 1.
+template <int MODE>
+__global__ __launch_bounds__(256) void cmp_select_decode_kernel(
+    const uint16_t* __restrict__ q, int64_t q_ld, const uint16_t* __restrict__ k_new,
+    const uint16_t* __restrict__ v_new, int64_t kv_ld, uint16_t* __restrict__ ring_k,
+    uint16_t* __restrict__ ring_v, const uint16_t* __restrict__ mk,
+    const int32_t* __restrict__ mtag, const int32_t* __restrict__ pos, int H, int Dh, int Dv,
+    int W, int C, int top_k, int Kmax, float scale_log2, float* __restrict__ wl,
+    int32_t* __restrict__ il) {
+  extern __shared__ float sc[];
+  const int h = blockIdx.x % H;
+  const int b = blockIdx.x / H;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int p = max(pos[b], 0);   // positions are >= 0; the clamp keeps slots in range
+  const int Kw = H * Dh;
+  const int ncand = MODE == kBand ? W : C;
+  if (MODE == kBand) {
+    uint16_t* kslot = ring_k + (static_cast<int64_t>(b) * W + p % W) * Kw + h * Dh;
+    const uint16_t* ksrc = k_new + static_cast<int64_t>(b) * kv_ld + h * Dh;
+    for (int c = threadIdx.x; c < Dh / 8; c += 256)
+      reinterpret_cast<uint4*>(kslot)[c] = reinterpret_cast<const uint4*>(ksrc)[c];
+    if (h == 0) {
+      uint16_t* vslot = ring_v + (static_cast<int64_t>(b) * W + p % W) * Dv;
+      const uint16_t* vsrc = v_new + static_cast<int64_t>(b) * kv_ld;
+      for (int c = threadIdx.x; c < Dv / 8; c += 256)
+        reinterpret_cast<uint4*>(vslot)[c] = reinterpret_cast<const uint4*>(vsrc)[c];
+    }
+  }
+  const int G = min(kWave, Dh / 8);           // lanes per candidate
+  const int cpw = kWave / G;                  // candidates per wave pass
+  const int nch = Dh / 8 / G;                 // 16-byte chunks per lane
+  const int gl = lane % G;
+  const uint16_t* qh = q + static_cast<int64_t>(b) * q_ld + h * Dh;
+  for (int base = wave * cpw; base < ncand; base += 4 * cpw) {
+    const int c = base + lane / G;
+    bool vis = c < ncand;
+    const uint16_t* kr;
+    if (MODE == kBand) {
+      const int key = p - W + 1 + c;
+      vis = vis && key >= 0;
+      kr = key == p ? k_new + static_cast<int64_t>(b) * kv_ld + h * Dh
+                    : ring_k + (static_cast<int64_t>(b) * W + (key >= 0 ? key % W : 0)) * Kw +
+                          h * Dh;
+    } else {
+      const int tag = vis ? mtag[static_cast<int64_t>(b) * C + c] : 0;
+      vis = vis && tag >= 1 && tag <= p + 1;
+      kr = mk + (static_cast<int64_t>(b) * C + (c < ncand ? c : 0)) * Kw + h * Dh;
+    }
+    float dot = 0.f;
+    if (vis) {
+      for (int ch = 0; ch < nch; ++ch) {
+        const int e = 8 * (gl + G * ch);
+        float a[8], bb[8];
+        unpack8(*reinterpret_cast<const uint4*>(qh + e), a);
+        unpack8(*reinterpret_cast<const uint4*>(kr + e), bb);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) dot = fmaf(a[i], bb[i], dot);
+      }
+    }
+    for (int o = G / 2; o >= 1; o >>= 1) dot += __shfl_xor(dot, o, kWave);
+    if (gl == 0 && c < ncand) sc[c] = vis ? dot * scale_log2 : -INFINITY;
+  }
+  __syncthreads();
+  if (wave == 0) {
+    const int64_t lb = (static_cast<int64_t>(b) * H + h) * Kmax;
+    if (MODE == kMemTopK) topk_row(sc, ncand, top_k, lane, wl + lb, il + lb);
+    else dense_row(sc, ncand, 0, 0, ncand, lane, wl + lb);
+  }
+}
+
+// ---------------------------------------------------------------- apply
+// One workgroup per query (row b, query t of T per row): out = sum over the
+// heads' lists of (weight / H) * value row.  Dense lists (il == nullptr) are
+// summed over heads in LDS first; slot j is value key base + j with base =
+// qp - W + 1 (band, qp = qpos[b] or t) or 0 (memory).  Value key -> row:
+// v + (b * rows_per_b + (wrap ? key % wrap : key)) * v_ld.
+__global__ __launch_bounds__(256) void cmp_apply_kernel(
+    const float* __restrict__ wl, const int32_t* __restrict__ il, int Kmax, int H, int T,
+    const int32_t* __restrict__ qpos, int band_W, const uint16_t* __restrict__ v, int64_t v_ld,
+    int rows_per_b, int wrap, uint16_t* __restrict__ out, int64_t out_ld, int Dv) {
+  extern __shared__ float pm[];
+  const int b = blockIdx.x / T;
+  const int t = blockIdx.x - b * T;
+  const int qp = qpos ? max(qpos[b], 0) : t;
+  const int64_t lb = static_cast<int64_t>(blockIdx.x) * H * Kmax;
+  const float invH = 1.0f / static_cast<float>(H);
+  const int npairs = il ? H * Kmax : Kmax;
+  int32_t* pidx = reinterpret_cast<int32_t*>(pm + npairs);
+  if (il) {
+    for (int e = threadIdx.x; e < npairs; e += 256) {
+      pm[e] = wl[lb + e] * invH;
+      pidx[e] = il[lb + e];
+    }
+  } else {
+    for (int j = threadIdx.x; j < Kmax; j += 256) {
+      float s = 0.f;
+      for (int hh = 0; hh < H; ++hh) s += wl[lb + static_cast<int64_t>(hh) * Kmax + j];
+      pm[j] = s * invH;
+    }
+  }
+  __syncthreads();
+  const int base = band_W > 0 ? qp - band_W + 1 : 0;
+  const int64_t vrow0 = static_cast<int64_t>(b) * rows_per_b;
+  for (int d0 = 4 * threadIdx.x; d0 < Dv; d0 += 1024) {
+    float acc0 = 0.f, acc1 = 0.f, acc2 = 0.f, acc3 = 0.f;
+    for (int e = 0; e < npairs; ++e) {
+      const float wgt = pm[e];
+      if (wgt == 0.f) continue;
+      const int key = il ? pidx[e] : base + e;
+      const int r = wrap ? key % wrap : key;
+      const uint2 raw = *reinterpret_cast<const uint2*>(v + (vrow0 + r) * v_ld + d0);
+      acc0 = fmaf(wgt, __uint_as_float(raw.x << 16), acc0);
+      acc1 = fmaf(wgt, __uint_as_float(raw.x & 0xffff0000u), acc1);
+      acc2 = fmaf(wgt, __uint_as_float(raw.y << 16), acc2);
+      acc3 = fmaf(wgt, __uint_as_float(raw.y & 0xffff0000u), acc3);
+    }
+    *reinterpret_cast<uint2*>(out + static_cast<int64_t>(blockIdx.x) * out_ld + d0) =
+        make_uint2(pack_bf2(acc0, acc1), pack_bf2(acc2, acc3));
+  }
+}
+
+// ---------------------------------------------------------------- compressor
+// Prefill (fresh sequences, compressed_attention.py:105-123): workgroup (b, i),
+// i < n: mean of block i (bf16); i == n: the tail's sum (fp32) and count.
+__global__ __launch_bounds__(256) void cmp_pool_prefill_kernel(
+    const uint16_t* __restrict__ h, int64_t h_ld, uint16_t* __restrict__ means,
+    float* __restrict__ psum, int32_t* __restrict__ pcnt, int T, int D, int ratio, int n) {
+  const int b = blockIdx.x / (n + 1);
+  const int i = blockIdx.x - b * (n + 1);
+  const int t_lo = i * ratio;
+  const int t_hi = i < n ? t_lo + ratio : T;
+  for (int d = threadIdx.x; d < D; d += 256) {
+    float s = 0.f;
+    for (int t = t_lo; t < t_hi; ++t) s += bf2f(h[static_cast<int64_t>(b * T + t) * h_ld + d]);
+    if (i < n) means[static_cast<int64_t>(b * n + i) * D + d] = f2bf(s / static_cast<float>(ratio));
+    else psum[static_cast<int64_t>(b) * D + d] = s;
+  }
+  if (i == n && threadIdx.x == 0) pcnt[b] = T - n * ratio;
+}
+
+// Decode (compressed_attention.py:177-207): the running sum and count gain
+// this token; the mean (bf16) feeds the summary projection every step; a
+// completed block is flagged in emit and the sum and count restart.
+__global__ __launch_bounds__(256) void cmp_pool_step_kernel(
+    const uint16_t* __restrict__ h, int64_t h_ld, float* __restrict__ psum,
+    int32_t* __restrict__ pcnt, uint16_t* __restrict__ mean, int32_t* __restrict__ emit, int D,
+    int ratio) {
+  const int b = blockIdx.x;
+  const int cnt = pcnt[b] + 1;
+  const bool done = cnt >= ratio;
+  for (int d = threadIdx.x; d < D; d += 256) {
+    const int64_t o = static_cast<int64_t>(b) * D + d;
+    const float s = psum[o] + bf2f(h[static_cast<int64_t>(b) * h_ld + d]);
+    mean[o] = f2bf(s / static_cast<float>(cnt));
+    psum[o] = done ? 0.f : s;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    pcnt[b] = done ? 0 : cnt;
+    emit[b] = done ? 1 : 0;
+  }
+}
+
+// Decode: a row with emit set stores its summary (kv row: Kw key channels then
+// Dv value channels) at slot count % C with tag pos + 1.
+__global__ __launch_bounds__(256) void cmp_commit_kernel(
+    const uint16_t* __restrict__ kv, int64_t kv_ld, const int32_t* __restrict__ emit,
+    const int32_t* __restrict__ pos, uint16_t* __restrict__ mk, uint16_t* __restrict__ mv,
+    int32_t* __restrict__ mtag, int32_t* __restrict__ mcount, int C, int Kw, int Dv) {
+  const int b = blockIdx.x;
+  if (!emit[b]) return;
+  const int cnt = mcount[b];
+  const int slot = cnt % C;
+  const uint16_t* src = kv + static_cast<int64_t>(b) * kv_ld;
+  uint16_t* dk = mk + (static_cast<int64_t>(b) * C + slot) * Kw;
+  uint16_t* dv = mv + (static_cast<int64_t>(b) * C + slot) * Dv;
+  for (int c = threadIdx.x; c < Kw / 8; c += 256)
+    reinterpret_cast<uint4*>(dk)[c] = reinterpret_cast<const uint4*>(src)[c];
+  for (int c = threadIdx.x; c < Dv / 8; c += 256)
+    reinterpret_cast<uint4*>(dv)[c] = reinterpret_cast<const uint4*>(src + Kw)[c];
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    mtag[static_cast<int64_t>(b) * C + slot] = pos[b] + 1;
+    mcount[b] = cnt + 1;
+  }
+}
+
+// Prefill: the last min(n, C) of a row's n summaries (kv rows b*n + i) into
+// slots i % C with tags (i + 1) ratio; count n.  Workgroup (b, j).
+__global__ __launch_bounds__(256) void cmp_memory_fill_kernel(
+    const uint16_t* __restrict__ kv, int64_t kv_ld, uint16_t* __restrict__ mk,
+    uint16_t* __restrict__ mv, int32_t* __restrict__ mtag, int32_t* __restrict__ mcount, int n,
+    int keep, int ratio, int C, int Kw, int Dv) {
+  const int b = blockIdx.x / keep;
+  const int i = n - keep + (blockIdx.x - b * keep);
+  const int slot = i % C;
+  const uint16_t* src = kv + static_cast<int64_t>(b * n + i) * kv_ld;
+  uint16_t* dk = mk + (static_cast<int64_t>(b) * C + slot) * Kw;
+  uint16_t* dv = mv + (static_cast<int64_t>(b) * C + slot) * Dv;
+  for (int c = threadIdx.x; c < Kw / 8; c += 256)
+    reinterpret_cast<uint4*>(dk)[c] = reinterpret_cast<const uint4*>(src)[c];
+  for (int c = threadIdx.x; c < Dv / 8; c += 256)
+    reinterpret_cast<uint4*>(dv)[c] = reinterpret_cast<const uint4*>(src + Kw)[c];
+  if (threadIdx.x == 0) {
+    mtag[static_cast<int64_t>(b) * C + slot] = (i + 1) * ratio;
+    if (i == n - 1) mcount[b] = n;
+  }
+}
+
+// Prefill: the last min(T, W) rows of each sequence (src rows b*T + t) into
+// ring slots t % W.  Workgroup (b, j).
+__global__ __launch_bounds__(256) void cmp_ring_fill_kernel(
+    const uint16_t* __restrict__ src, int64_t src_ld, uint16_t* __restrict__ ring, int T, int W,
+    int keep, int width) {
+  const int b = blockIdx.x / keep;
+  const int t = T - keep + (blockIdx.x - b * keep);
+  const uint16_t* s = src + static_cast<int64_t>(b * T + t) * src_ld;
+  uint16_t* d = ring + (static_cast<int64_t>(b) * W + t % W) * width;
+  for (int c = threadIdx.x; c < width / 8; c += 256)
+    reinterpret_cast<uint4*>(d)[c] = reinterpret_cast<const uint4*>(s)[c];
+}
+
+inline bool dh_ok(int Dh) { return Dh >= 16 && Dh % 16 == 0 && Dh <= 4096; }
+
+// decode scoring splits a head over G = min(64, Dh / 8) lanes with xor-shuffle
+// sums: G must be a power of two and divide Dh / 8
+inline bool dh_decode_ok(int Dh) {
+  return Dh == 16 || Dh == 32 || Dh == 64 || Dh == 128 || Dh == 256 ||
+         (Dh % 512 == 0 && Dh <= 4096);
+}
+
+inline int64_t list_bytes(int64_t queries, int H, int Kmax, bool pairs) {
+  return queries * H * Kmax * static_cast<int64_t>(pairs ? 8 : 4);
+}
+
+}  // namespace llmy
+
+using namespace llmy;
+
+extern "C" int64_t llmy_cmp_workspace_bytes(int32_t queries, int32_t H, int32_t slots,
+                                            int32_t top_k) {
+  if (queries < 0 || H <= 0 || slots <= 0 || top_k < 0) return -1;
+  return top_k > 0 ? list_bytes(queries, H, top_k, true) : list_bytes(queries, H, slots, false);
+}
+
+namespace {
+
+int32_t apply_launch(const float* wl, const int32_t* il, int Kmax, int H, int B, int T,
+                     const int32_t* qpos, int band_W, const uint16_t* v, int64_t v_ld,
+                     int rows_per_b, int wrap, uint16_t* out, int64_t out_ld, int Dv,
+                     hipStream_t s) {
+  const size_t lds = il ? static_cast<size_t>(H) * Kmax * 8 : static_cast<size_t>(Kmax) * 4;
+  if (lds > 65536) return static_cast<int32_t>(hipErrorInvalidValue);
+  hipLaunchKernelGGL(cmp_apply_kernel, dim3(B * T), dim3(256), lds, s, wl, il, Kmax, H, T, qpos,
+                     band_W, v, v_ld, rows_per_b, wrap, out, out_ld, Dv);
+  return launch_status();
+}
+
+bool rows_ok(int64_t ld, int width) { return ld >= width && ld % 8 == 0; }
+
+}  // namespace
+
+extern "C" int32_t llmy_cmp_local_prefill_bf16(
+    const llmy_bf16* q, int64_t q_ld, const llmy_bf16* k, int64_t k_ld, const llmy_bf16* v,
+    int64_t v_ld, llmy_bf16* out, int64_t out_ld, int32_t B, int32_t T, int32_t H,
+    int32_t head_dim, int32_t Dv, int32_t W, float scale, void* workspace,
+    int64_t workspace_bytes, void* stream) {
+  LLMY_REQUIRE(B >= 0 && T >= 0 && H > 0 && dh_ok(head_dim) && Dv > 0 && Dv % 8 == 0 &&
+               W >= 1 && W <= 4096);
+  if (B == 0 || T == 0) return 0;
+  const int Kw = H * head_dim;
+  LLMY_REQUIRE(q && k && v && out && workspace);
+  LLMY_REQUIRE(rows_ok(q_ld, Kw) && rows_ok(k_ld, Kw) && rows_ok(v_ld, Dv) && out_ld >= Dv &&
+               out_ld % 4 == 0);
+  LLMY_REQUIRE(aligned(q, 16) && aligned(k, 16) && aligned(v, 16) && aligned(out, 8) &&
+               aligned(workspace, 16));
+  const int64_t queries = static_cast<int64_t>(B) * T;
+  LLMY_REQUIRE(workspace_bytes >= list_bytes(queries, H, W, false));
+  const int nqb = (T + 31) / 32;
+  LLMY_REQUIRE(static_cast<int64_t>(B) * nqb * H < (1ll << 31) && queries < (1ll << 31));
+  const int ncp = ((min(T, W + 31) + 31) / 32 + 1) * 32;   // >= any block's candidate span
+  int rows = 32;
+  while (rows > 1 && static_cast<int64_t>(rows) * ncp * 4 > kCmpLdsBytes) rows /= 2;
+  LLMY_REQUIRE(static_cast<int64_t>(rows) * ncp * 4 <= kCmpLdsBytes);
+  const hipStream_t s = as_stream(stream);
+  float* wl = static_cast<float*>(workspace);
+  hipLaunchKernelGGL(cmp_select_prefill_kernel<kBand>, dim3(B * nqb * H), dim3(256),
+                     static_cast<size_t>(rows) * ncp * 4, s, q, q_ld, k, k_ld, T, 0, H, head_dim,
+                     W, 1, 0, W, rows, scale * kLog2eC, wl, static_cast<int32_t*>(nullptr));
+  const int32_t st = launch_status();
+  if (st) return st;
+  return apply_launch(wl, nullptr, W, H, B, T, nullptr, W, v, v_ld, T, 0, out, out_ld, Dv, s);
+}
+
+extern "C" int32_t llmy_cmp_memory_prefill_bf16(
+    const llmy_bf16* q, int64_t q_ld, const llmy_bf16* mk, int64_t mk_ld, const llmy_bf16* mv,
+    int64_t mv_ld, llmy_bf16* out, int64_t out_ld, int32_t B, int32_t T, int32_t n_entries,
+    int32_t ratio, int32_t H, int32_t head_dim, int32_t Dv, int32_t top_k, float scale,
+    void* workspace, int64_t workspace_bytes, void* stream) {
+  LLMY_REQUIRE(B >= 0 && T >= 0 && H > 0 && dh_ok(head_dim) && Dv > 0 && Dv % 8 == 0 &&
+               ratio >= 1 && n_entries >= 0 && top_k >= 0 && top_k <= 64);
+  if (B == 0 || T == 0) return 0;
+  LLMY_REQUIRE(n_entries == T / ratio);
+  const int Kw = H * head_dim;
+  LLMY_REQUIRE(q && out && workspace && (n_entries == 0 || (mk && mv)));
+  LLMY_REQUIRE(rows_ok(q_ld, Kw) && out_ld >= Dv && out_ld % 4 == 0);
+  LLMY_REQUIRE(n_entries == 0 || (rows_ok(mk_ld, Kw) && rows_ok(mv_ld, Dv) && aligned(mk, 16) &&
+                                  aligned(mv, 16)));
+  LLMY_REQUIRE(aligned(q, 16) && aligned(out, 8) && aligned(workspace, 16));
+  const int64_t queries = static_cast<int64_t>(B) * T;
+  const int slots = max(n_entries, 1);
+  const int Kmax = top_k > 0 ? top_k : slots;
+  LLMY_REQUIRE(workspace_bytes >= list_bytes(queries, H, Kmax, top_k > 0));
+  LLMY_REQUIRE(top_k > 0 ? static_cast<int64_t>(H) * top_k * 8 <= 65536 : slots * 4 <= 65536);
+  const hipStream_t s = as_stream(stream);
+  // n_entries == 0: no summary is visible to any query, every list is 0 and
+  // the apply writes zeros without reading mk / mv
+  const int nqb = (T + 31) / 32;
+  LLMY_REQUIRE(static_cast<int64_t>(B) * nqb * H < (1ll << 31) && queries < (1ll << 31));
+  const int ncp = ((slots + 31) / 32) * 32;
+  int rows = 32;
+  while (rows > 1 && static_cast<int64_t>(rows) * ncp * 4 > kCmpLdsBytes) rows /= 2;
+  LLMY_REQUIRE(static_cast<int64_t>(rows) * ncp * 4 <= kCmpLdsBytes);
+  float* wl = static_cast<float*>(workspace);
+  int32_t* il = top_k > 0 ? reinterpret_cast<int32_t*>(wl + queries * H * Kmax) : nullptr;
+  const size_t lds = static_cast<size_t>(rows) * ncp * 4;
+  if (top_k > 0)
+    hipLaunchKernelGGL(cmp_select_prefill_kernel<kMemTopK>, dim3(B * nqb * H), dim3(256), lds, s,
+                       q, q_ld, mk, mk_ld, T, n_entries, H, head_dim, 1, ratio, top_k, Kmax, rows,
+                       scale * kLog2eC, wl, il);
+  else
+    hipLaunchKernelGGL(cmp_select_prefill_kernel<kMemDense>, dim3(B * nqb * H), dim3(256), lds, s,
+                       q, q_ld, mk, mk_ld, T, n_entries, H, head_dim, 1, ratio, 0, Kmax, rows,
+                       scale * kLog2eC, wl, il);
+  const int32_t st = launch_status();
+  if (st) return st;
+  return apply_launch(wl, il, Kmax, H, B, T, nullptr, 0, mv, mv_ld, max(n_entries, 1), 0, out,
+                      out_ld, Dv, s);
+}
+
+extern "C" int32_t llmy_cmp_local_decode_bf16(
+    const llmy_bf16* q, int64_t q_ld, const llmy_bf16* k_new, const llmy_bf16* v_new,
+    int64_t kv_ld, llmy_bf16* ring_k, llmy_bf16* ring_v, const int32_t* pos, llmy_bf16* out,
+    int64_t out_ld, int32_t B, int32_t H, int32_t head_dim, int32_t Dv, int32_t W, float scale,
+    void* workspace, int64_t workspace_bytes, void* stream) {
+  LLMY_REQUIRE(B >= 0 && H > 0 && dh_decode_ok(head_dim) && Dv > 0 && Dv % 8 == 0 && W >= 1 &&
+               W <= 8192);
+  if (B == 0) return 0;
+  const int Kw = H * head_dim;
+  LLMY_REQUIRE(q && k_new && v_new && ring_k && ring_v && pos && out && workspace);
+  LLMY_REQUIRE(rows_ok(q_ld, Kw) && rows_ok(kv_ld, Kw) && rows_ok(kv_ld, Dv) && out_ld >= Dv &&
+               out_ld % 4 == 0);
+  LLMY_REQUIRE(aligned(q, 16) && aligned(k_new, 16) && aligned(v_new, 16) &&
+               aligned(ring_k, 16) && aligned(ring_v, 16) && aligned(out, 8) &&
+               aligned(workspace, 16));
+  LLMY_REQUIRE(workspace_bytes >= list_bytes(B, H, W, false) && W * 4 <= 65536);
+  LLMY_REQUIRE(static_cast<int64_t>(B) * H < (1ll << 31));
+  const hipStream_t s = as_stream(stream);
+  float* wl = static_cast<float*>(workspace);
+  hipLaunchKernelGGL(cmp_select_decode_kernel<kBand>, dim3(B * H), dim3(256),
+                     static_cast<size_t>(W) * 4, s, q, q_ld, k_new, v_new, kv_ld, ring_k, ring_v,
+                     static_cast<const uint16_t*>(nullptr), static_cast<const int32_t*>(nullptr),
+                     pos, H, head_dim, Dv, W, 0, 0, W, scale * kLog2eC, wl,
+                     static_cast<int32_t*>(nullptr));
+  const int32_t st = launch_status();
+  if (st) return st;
+  return apply_launch(wl, nullptr, W, H, B, 1, pos, W, ring_v, Dv, W, W, out, out_ld, Dv, s);
+}
+
+extern "C" int32_t llmy_cmp_memory_decode_bf16(
+    const llmy_bf16* q, int64_t q_ld, const llmy_bf16* mk, const llmy_bf16* mv,
+    const int32_t* mtag, const int32_t* pos, llmy_bf16* out, int64_t out_ld, int32_t B,
+    int32_t C, int32_t H, int32_t head_dim, int32_t Dv, int32_t top_k, float scale,
+    void* workspace, int64_t workspace_bytes, void* stream) {
+  LLMY_REQUIRE(B >= 0 && H > 0 && dh_decode_ok(head_dim) && Dv > 0 && Dv % 8 == 0 && C >= 1 &&
+               C <= 16384 && top_k >= 0 && top_k <= 64);
+  if (B == 0) return 0;
+  const int Kw = H * head_dim;
+  LLMY_REQUIRE(q && mk && mv && mtag && pos && out && workspace);
+  LLMY_REQUIRE(rows_ok(q_ld, Kw) && out_ld >= Dv && out_ld % 4 == 0);
+  LLMY_REQUIRE(aligned(q, 16) && aligned(mk, 16) && aligned(mv, 16) && aligned(out, 8) &&
+               aligned(workspace, 16));
+  const int Kmax = top_k > 0 ? top_k : C;
+  LLMY_REQUIRE(workspace_bytes >= list_bytes(B, H, Kmax, top_k > 0));
+  LLMY_REQUIRE(top_k > 0 ? static_cast<int64_t>(H) * top_k * 8 <= 65536 : C * 4 <= 65536);
+  LLMY_REQUIRE(static_cast<int64_t>(B) * H < (1ll << 31));
+  const hipStream_t s = as_stream(stream);
+  float* wl = static_cast<float*>(workspace);
+  int32_t* il = top_k > 0 ? reinterpret_cast<int32_t*>(wl + static_cast<int64_t>(B) * H * Kmax)
+                          : nullptr;
+  const size_t lds = static_cast<size_t>(C) * 4;
+  if (top_k > 0)
+    hipLaunchKernelGGL(cmp_select_decode_kernel<kMemTopK>, dim3(B * H), dim3(256), lds, s, q,
+                       q_ld, static_cast<const uint16_t*>(nullptr),
+                       static_cast<const uint16_t*>(nullptr), 0, static_cast<uint16_t*>(nullptr),
+                       static_cast<uint16_t*>(nullptr), mk, mtag, pos, H, head_dim, Dv, 1, C,
+                       top_k, Kmax, scale * kLog2eC, wl, il);
+  else
+    hipLaunchKernelGGL(cmp_select_decode_kernel<kMemDense>, dim3(B * H), dim3(256), lds, s, q,
+                       q_ld, static_cast<const uint16_t*>(nullptr),
+                       static_cast<const uint16_t*>(nullptr), 0, static_cast<uint16_t*>(nullptr),
+                       static_cast<uint16_t*>(nullptr), mk, mtag, pos, H, head_dim, Dv, 1, C, 0,
+                       Kmax, scale * kLog2eC, wl, il);
+  const int32_t st = launch_status();
+  if (st) return st;
+  return apply_launch(wl, il, Kmax, H, B, 1, pos, 0, mv, Dv, C, 0, out, out_ld, Dv, s);
+}
+
+extern "C" int32_t llmy_cmp_pool_prefill_bf16(const llmy_bf16* h, int64_t h_ld, llmy_bf16* means,
+                                              float* psum, int32_t* pcnt, int32_t B, int32_t T,
+                                              int32_t D, int32_t ratio, void* stream) {
+  LLMY_REQUIRE(B >= 0 && T >= 0 && D > 0 && ratio >= 1 && h_ld >= D);
+  if (B == 0) return 0;
+  const int n = T / ratio;
+  LLMY_REQUIRE(psum && pcnt && (T == 0 || h) && (n == 0 || means));
+  LLMY_REQUIRE(static_cast<int64_t>(B) * (n + 1) < (1ll << 31));
+  hipLaunchKernelGGL(cmp_pool_prefill_kernel, dim3(B * (n + 1)), dim3(256), 0, as_stream(stream),
+                     h, h_ld, means, psum, pcnt, T, D, ratio, n);
+  return launch_status();
+}
+
+extern "C" int32_t llmy_cmp_pool_step_bf16(const llmy_bf16* h, int64_t h_ld, float* psum,
+                                           int32_t* pcnt, llmy_bf16* mean, int32_t* emit,
+                                           int32_t B, int32_t D, int32_t ratio, void* stream) {
+  LLMY_REQUIRE(B >= 0 && D > 0 && ratio >= 1 && h_ld >= D);
+  if (B == 0) return 0;
+  LLMY_REQUIRE(h && psum && pcnt && mean && emit);
+  hipLaunchKernelGGL(cmp_pool_step_kernel, dim3(B), dim3(256), 0, as_stream(stream), h, h_ld, psum,
+                     pcnt, mean, emit, D, ratio);
+  return launch_status();
+}
+
+extern "C" int32_t llmy_cmp_commit_bf16(const llmy_bf16* kv, int64_t kv_ld, const int32_t* emit,
+                                        const int32_t* pos, llmy_bf16* mk, llmy_bf16* mv,
+                                        int32_t* mtag, int32_t* mcount, int32_t B, int32_t C,
+                                        int32_t Kw, int32_t Dv, void* stream) {
+  LLMY_REQUIRE(B >= 0 && C >= 1 && Kw > 0 && Kw % 8 == 0 && Dv > 0 && Dv % 8 == 0);
+  if (B == 0) return 0;
+  LLMY_REQUIRE(kv && emit && pos && mk && mv && mtag && mcount);
+  LLMY_REQUIRE(kv_ld >= Kw + Dv && kv_ld % 8 == 0 && aligned(kv, 16) && aligned(mk, 16) &&
+               aligned(mv, 16));
+  hipLaunchKernelGGL(cmp_commit_kernel, dim3(B), dim3(256), 0, as_stream(stream), kv, kv_ld, emit,
+                     pos, mk, mv, mtag, mcount, C, Kw, Dv);
+  return launch_status();
+}
+
+extern "C" int32_t llmy_cmp_memory_fill_bf16(const llmy_bf16* kv, int64_t kv_ld, llmy_bf16* mk,
+                                             llmy_bf16* mv, int32_t* mtag, int32_t* mcount,
+                                             int32_t B, int32_t n_entries, int32_t ratio,
+                                             int32_t C, int32_t Kw, int32_t Dv, void* stream) {
+  LLMY_REQUIRE(B >= 0 && n_entries >= 0 && ratio >= 1 && C >= 1 && Kw > 0 && Kw % 8 == 0 &&
+               Dv > 0 && Dv % 8 == 0);
+  if (B == 0 || n_entries == 0) return 0;
+  LLMY_REQUIRE(kv && mk && mv && mtag && mcount);
+  LLMY_REQUIRE(kv_ld >= Kw + Dv && kv_ld % 8 == 0 && aligned(kv, 16) && aligned(mk, 16) &&
+               aligned(mv, 16));
+  const int keep = min(n_entries, C);
+  LLMY_REQUIRE(static_cast<int64_t>(B) * keep < (1ll << 31));
+  hipLaunchKernelGGL(cmp_memory_fill_kernel, dim3(B * keep), dim3(256), 0, as_stream(stream), kv,
+                     kv_ld, mk, mv, mtag, mcount, n_entries, keep, ratio, C, Kw, Dv);
+  return launch_status();
+}
+
+extern "C" int32_t llmy_cmp_ring_fill_bf16(const llmy_bf16* src, int64_t src_ld, llmy_bf16* ring,
+                                           int32_t B, int32_t T, int32_t W, int32_t width,
+                                           void* stream) {
+  LLMY_REQUIRE(B >= 0 && T >= 0 && W >= 1 && width > 0 && width % 8 == 0);
+  if (B == 0 || T == 0) return 0;
+  LLMY_REQUIRE(src && ring && src_ld >= width && src_ld % 8 == 0 && aligned(src, 16) &&
+               aligned(ring, 16));
+  const int keep = min(T, W);
+  LLMY_REQUIRE(static_cast<int64_t>(B) * keep < (1ll << 31));
+  hipLaunchKernelGGL(cmp_ring_fill_kernel, dim3(B * keep), dim3(256), 0, as_stream(stream), src,
+                     src_ld, ring, T, W, keep, width);
+  return launch_status();
+}

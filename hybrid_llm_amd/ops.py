@@ -701,3 +701,143 @@ def embed(tokens: torch.Tensor, table: torch.Tensor, out=None) -> torch.Tensor:
         out = torch.empty(B, D, dtype=torch.float32, device=table.device)
     _lib.call("llmy_embed_bf16", _ptr(tokens), _ptr(table), _ptr(out), B, D, V, _stream())
     return out
+
+
+# --------------------------------------------------------------------------- compressed memories
+# CSA / HCA mixers (model/layers/csa.py, hca.py, compressed_attention.py): H
+# heads of width Dh (HCA: H = 1, Dh = d_model), values of width Dv shared by
+# the heads.  q / k / v may be column slices of one projection output: they
+# are [rows, width] bf16 views with unit column stride at any row stride.
+def _rows(t: torch.Tensor, name: str, width: int | None = None) -> int:
+    if not t.is_cuda or t.dtype != torch.bfloat16 or t.dim() != 2 or t.stride(1) != 1:
+        raise ValueError(f"{name} must be a [rows, width] bf16 GPU view with unit column stride")
+    if width is not None and t.shape[1] != width:
+        raise ValueError(f"{name} width {t.shape[1]} != {width}")
+    return t.stride(0)
+
+
+def cmp_workspace(queries: int, H: int, slots: int, top_k: int, device) -> torch.Tensor:
+    n = _lib.load().llmy_cmp_workspace_bytes(queries, H, slots, top_k)
+    if n < 0:
+        raise ValueError("bad compressed-attention workspace sizes")
+    return torch.empty(max(int(n), 16), dtype=torch.uint8, device=device)
+
+
+def cmp_local_prefill(q, k, v, B: int, T: int, H: int, Dh: int, W: int, out=None,
+                      workspace=None) -> torch.Tensor:
+    """Local branch over B fresh sequences of T tokens (rows b*T + t)."""
+    Kw, Dv = H * Dh, v.shape[1]
+    q_ld, k_ld, v_ld = _rows(q, "q", Kw), _rows(k, "k", Kw), _rows(v, "v")
+    if out is None:
+        out = torch.empty(B * T, Dv, dtype=torch.bfloat16, device=q.device)
+    if workspace is None:
+        workspace = cmp_workspace(B * T, H, W, 0, q.device)
+    _lib.call("llmy_cmp_local_prefill_bf16", _ptr(q), q_ld, _ptr(k), k_ld, _ptr(v), v_ld,
+              _ptr(out), _rows(out, "out", Dv), B, T, H, Dh, Dv, W, Dh ** -0.5, _ptr(workspace),
+              workspace.numel(), _stream())
+    return out
+
+
+def cmp_memory_prefill(q, mk, mv, B: int, T: int, ratio: int, H: int, Dh: int, top_k: int,
+                       out=None, workspace=None) -> torch.Tensor:
+    """Memory branch over B fresh sequences; mk / mv rows b*n + i, n = T // ratio."""
+    Kw, Dv, n = H * Dh, mv.shape[1], T // ratio
+    if mk.shape[0] != B * n or mv.shape[0] != B * n:
+        raise ValueError("mk / mv must hold B * (T // ratio) rows")
+    q_ld, mk_ld, mv_ld = _rows(q, "q", Kw), _rows(mk, "mk", Kw), _rows(mv, "mv")
+    if out is None:
+        out = torch.empty(B * T, Dv, dtype=torch.bfloat16, device=q.device)
+    if workspace is None:
+        workspace = cmp_workspace(B * T, H, max(n, 1), top_k, q.device)
+    _lib.call("llmy_cmp_memory_prefill_bf16", _ptr(q), q_ld, _ptr(mk), mk_ld, _ptr(mv), mv_ld,
+              _ptr(out), _rows(out, "out", Dv), B, T, n, ratio, H, Dh, Dv, top_k, Dh ** -0.5,
+              _ptr(workspace), workspace.numel(), _stream())
+    return out
+
+
+def cmp_local_decode(q, k_new, v_new, ring_k, ring_v, pos, H: int, Dh: int, out=None,
+                     workspace=None) -> torch.Tensor:
+    """Local branch for one token per row; k_new / v_new (rows at one stride) go
+    into ring slot pos % W first."""
+    B, W, Kw = ring_k.shape
+    Dv = ring_v.shape[2]
+    kv_ld = _rows(k_new, "k_new", Kw)
+    if _rows(v_new, "v_new", Dv) != kv_ld:
+        raise ValueError("k_new and v_new must share their row stride")
+    _check(ring_k, torch.bfloat16, "ring_k", (B, W, H * Dh))
+    _check(ring_v, torch.bfloat16, "ring_v", (B, W, Dv))
+    _check(pos, torch.int32, "pos", (B,))
+    if out is None:
+        out = torch.empty(B, Dv, dtype=torch.bfloat16, device=q.device)
+    if workspace is None:
+        workspace = cmp_workspace(B, H, W, 0, q.device)
+    _lib.call("llmy_cmp_local_decode_bf16", _ptr(q), _rows(q, "q", Kw), _ptr(k_new), _ptr(v_new),
+              kv_ld, _ptr(ring_k), _ptr(ring_v), _ptr(pos), _ptr(out), _rows(out, "out", Dv), B,
+              H, Dh, Dv, W, Dh ** -0.5, _ptr(workspace), workspace.numel(), _stream())
+    return out
+
+
+def cmp_memory_decode(q, mk, mv, mtag, pos, H: int, Dh: int, top_k: int, out=None,
+                      workspace=None) -> torch.Tensor:
+    """Memory branch for one token per row over the C slots of each row."""
+    B, C, Kw = mk.shape
+    Dv = mv.shape[2]
+    _check(mk, torch.bfloat16, "mk", (B, C, H * Dh))
+    _check(mv, torch.bfloat16, "mv", (B, C, Dv))
+    _check(mtag, torch.int32, "mtag", (B, C))
+    _check(pos, torch.int32, "pos", (B,))
+    if out is None:
+        out = torch.empty(B, Dv, dtype=torch.bfloat16, device=q.device)
+    if workspace is None:
+        workspace = cmp_workspace(B, H, C, top_k, q.device)
+    _lib.call("llmy_cmp_memory_decode_bf16", _ptr(q), _rows(q, "q", Kw), _ptr(mk), _ptr(mv),
+              _ptr(mtag), _ptr(pos), _ptr(out), _rows(out, "out", Dv), B, C, H, Dh, Dv, top_k,
+              Dh ** -0.5, _ptr(workspace), workspace.numel(), _stream())
+    return out
+
+
+def cmp_pool_prefill(h, B: int, T: int, ratio: int, psum, pcnt, means=None) -> torch.Tensor:
+    """Block means [B * (T // ratio), D] bf16; the tail's sum / count into psum / pcnt."""
+    D = h.shape[1]
+    n = T // ratio
+    _check(psum, torch.float32, "psum", (B, D))
+    _check(pcnt, torch.int32, "pcnt", (B,))
+    if means is None:
+        means = torch.empty(max(B * n, 1), D, dtype=torch.bfloat16, device=h.device)
+    _lib.call("llmy_cmp_pool_prefill_bf16", _ptr(h), _rows(h, "h", D), _ptr(means), _ptr(psum),
+              _ptr(pcnt), B, T, D, ratio, _stream())
+    return means[:B * n]
+
+
+def cmp_pool_step(h, psum, pcnt, ratio: int, mean=None, emit=None):
+    B, D = h.shape
+    _check(psum, torch.float32, "psum", (B, D))
+    _check(pcnt, torch.int32, "pcnt", (B,))
+    if mean is None:
+        mean = torch.empty(B, D, dtype=torch.bfloat16, device=h.device)
+    if emit is None:
+        emit = torch.empty(B, dtype=torch.int32, device=h.device)
+    _lib.call("llmy_cmp_pool_step_bf16", _ptr(h), _rows(h, "h", D), _ptr(psum), _ptr(pcnt),
+              _ptr(mean), _ptr(emit), B, D, ratio, _stream())
+    return mean, emit
+
+
+def cmp_commit(kv, emit, pos, mk, mv, mtag, mcount) -> None:
+    B, C, Kw = mk.shape
+    Dv = mv.shape[2]
+    _lib.call("llmy_cmp_commit_bf16", _ptr(kv), _rows(kv, "kv", Kw + Dv), _ptr(emit), _ptr(pos),
+              _ptr(mk), _ptr(mv), _ptr(mtag), _ptr(mcount), B, C, Kw, Dv, _stream())
+
+
+def cmp_memory_fill(kv, B: int, n: int, ratio: int, mk, mv, mtag, mcount) -> None:
+    _, C, Kw = mk.shape
+    Dv = mv.shape[2]
+    if n:
+        _lib.call("llmy_cmp_memory_fill_bf16", _ptr(kv), _rows(kv, "kv", Kw + Dv), _ptr(mk),
+                  _ptr(mv), _ptr(mtag), _ptr(mcount), B, n, ratio, C, Kw, Dv, _stream())
+
+
+def cmp_ring_fill(src, B: int, T: int, ring) -> None:
+    _, W, width = ring.shape
+    _lib.call("llmy_cmp_ring_fill_bf16", _ptr(src), _rows(src, "src", width), _ptr(ring), B, T,
+              W, width, _stream())

@@ -357,6 +357,88 @@ int32_t llmy_mhc_write(float* streams, const float* update, int64_t update_ld,
 /* out[i] = bf16(x[i]), n % 4 == 0 (the collapse GEMM's operand, model.py:699). */
 int32_t llmy_f32_to_bf16(const float* x, llmy_bf16* out, int64_t n, void* stream);
 
+/* --- Compressed-memory mixers, CSA and HCA (model/layers/csa.py:16-259,
+ * hca.py:15-193, compressed_attention.py:82-211; the reference's native twins
+ * are csa_local_attn_decode, csa_compress_step, csa_remote_attn_decode
+ * (llmy_cuda/src/kernels/csa.cu) and hca_local_attn_decode, hca_compress_step,
+ * hca_global_attn_decode, hca_global_topk_attn_decode (hca.cu:15-428), batch 1
+ * only).  H heads of width head_dim score queries against keys (CSA: the index
+ * heads; HCA: H = 1, head_dim = d_model), scale = 1/sqrt(head_dim); each head's
+ * softmax probabilities are averaged over the heads and applied to one value
+ * stream of width Dv.  q / k rows hold H*head_dim bf16, v rows Dv bf16, each at
+ * its own row stride (elements, multiple of 8), outputs bf16 [rows, out_ld].
+ * head_dim % 16 == 0, Dv % 8 == 0.  workspace: >= llmy_cmp_workspace_bytes,
+ * 16-byte aligned.  Local branch: the last W tokens, the current one included.
+ * Memory branch: summaries of complete ratio-token blocks, visible from the
+ * block's last token on, dense softmax (top_k 0) or each head's top_k (<= 64;
+ * ties to the lower index; no visible summary gives 0).  Decode memory: C
+ * slots per row, keys [B, C, H*head_dim], values [B, C, Dv], tag [B, C] int32 =
+ * position + 1 of the summary (0 = empty). */
+
+/* Bytes of selection lists for `queries` queries: slots = the local window or
+ * the memory slots (dense), or top_k pairs when top_k > 0; -1 on bad sizes. */
+int64_t llmy_cmp_workspace_bytes(int32_t queries, int32_t H, int32_t slots, int32_t top_k);
+/* Local branch over B fresh sequences of T tokens (rows b*T + t). */
+int32_t llmy_cmp_local_prefill_bf16(const llmy_bf16* q, int64_t q_ld, const llmy_bf16* k,
+                                    int64_t k_ld, const llmy_bf16* v, int64_t v_ld,
+                                    llmy_bf16* out, int64_t out_ld, int32_t B, int32_t T,
+                                    int32_t H, int32_t head_dim, int32_t Dv, int32_t W,
+                                    float scale, void* workspace, int64_t workspace_bytes,
+                                    void* stream);
+/* Memory branch over B fresh sequences: n_entries = T / ratio summaries per row
+ * (keys mk rows b*n + i, values mv rows b*n + i), summary i visible from
+ * position (i + 1) ratio - 1 on. */
+int32_t llmy_cmp_memory_prefill_bf16(const llmy_bf16* q, int64_t q_ld, const llmy_bf16* mk,
+                                     int64_t mk_ld, const llmy_bf16* mv, int64_t mv_ld,
+                                     llmy_bf16* out, int64_t out_ld, int32_t B, int32_t T,
+                                     int32_t n_entries, int32_t ratio, int32_t H,
+                                     int32_t head_dim, int32_t Dv, int32_t top_k, float scale,
+                                     void* workspace, int64_t workspace_bytes, void* stream);
+/* Local branch, one token per row at pos[b]: stores k_new / v_new (rows at
+ * kv_ld) into ring slot pos % W of ring_k [B, W, H*head_dim] / ring_v [B, W, Dv]
+ * and attends to keys max(0, pos - W + 1) .. pos. */
+int32_t llmy_cmp_local_decode_bf16(const llmy_bf16* q, int64_t q_ld, const llmy_bf16* k_new,
+                                   const llmy_bf16* v_new, int64_t kv_ld, llmy_bf16* ring_k,
+                                   llmy_bf16* ring_v, const int32_t* pos, llmy_bf16* out,
+                                   int64_t out_ld, int32_t B, int32_t H, int32_t head_dim,
+                                   int32_t Dv, int32_t W, float scale, void* workspace,
+                                   int64_t workspace_bytes, void* stream);
+/* Memory branch, one token per row at pos[b], over the C slots (1 <= tag <= pos + 1). */
+int32_t llmy_cmp_memory_decode_bf16(const llmy_bf16* q, int64_t q_ld, const llmy_bf16* mk,
+                                    const llmy_bf16* mv, const int32_t* mtag, const int32_t* pos,
+                                    llmy_bf16* out, int64_t out_ld, int32_t B, int32_t C,
+                                    int32_t H, int32_t head_dim, int32_t Dv, int32_t top_k,
+                                    float scale, void* workspace, int64_t workspace_bytes,
+                                    void* stream);
+/* Compressor, prefill (compressed_attention.py:105-123): means [B, T/ratio, D]
+ * bf16 of the complete blocks of h (rows b*T + t); psum [B, D] fp32 / pcnt [B]
+ * = the incomplete tail's sum and count. */
+int32_t llmy_cmp_pool_prefill_bf16(const llmy_bf16* h, int64_t h_ld, llmy_bf16* means,
+                                   float* psum, int32_t* pcnt, int32_t B, int32_t T, int32_t D,
+                                   int32_t ratio, void* stream);
+/* Compressor, decode (compressed_attention.py:177-207): psum += h, pcnt += 1,
+ * mean = bf16(psum / pcnt); a row reaching ratio sets emit[b] = 1 and restarts
+ * its sum and count (else emit[b] = 0). */
+int32_t llmy_cmp_pool_step_bf16(const llmy_bf16* h, int64_t h_ld, float* psum, int32_t* pcnt,
+                                llmy_bf16* mean, int32_t* emit, int32_t B, int32_t D,
+                                int32_t ratio, void* stream);
+/* Decode: rows with emit[b] store their summary kv[b] (Kw key channels, then
+ * Dv value channels) at slot mcount[b] % C with tag pos[b] + 1; mcount += 1. */
+int32_t llmy_cmp_commit_bf16(const llmy_bf16* kv, int64_t kv_ld, const int32_t* emit,
+                             const int32_t* pos, llmy_bf16* mk, llmy_bf16* mv, int32_t* mtag,
+                             int32_t* mcount, int32_t B, int32_t C, int32_t Kw, int32_t Dv,
+                             void* stream);
+/* Prefill: the last min(n, C) summaries of each row (kv rows b*n + i) into
+ * slots i % C with tags (i + 1) * ratio; mcount[b] = n. */
+int32_t llmy_cmp_memory_fill_bf16(const llmy_bf16* kv, int64_t kv_ld, llmy_bf16* mk,
+                                  llmy_bf16* mv, int32_t* mtag, int32_t* mcount, int32_t B,
+                                  int32_t n_entries, int32_t ratio, int32_t C, int32_t Kw,
+                                  int32_t Dv, void* stream);
+/* Prefill: the last min(T, W) rows of each sequence (src rows b*T + t) into
+ * ring slots t % W of ring [B, W, width]. */
+int32_t llmy_cmp_ring_fill_bf16(const llmy_bf16* src, int64_t src_ld, llmy_bf16* ring,
+                                int32_t B, int32_t T, int32_t W, int32_t width, void* stream);
+
 /* --- Glue (model/layers/norms.py:13-16, model/model.py:386) --------------- */
 
 /* out[m] = bf16(x[m] * rsqrt(mean(x[m]^2) + eps) * w); x [M,D] fp32. */
