@@ -56,6 +56,23 @@ class HybridConfig:
     mhc_streams: int = 1
     mhc_sinkhorn_iters: int = 10   # model/config.py:12
     mhc_gating_init: float = 0.01  # model/config.py:13
+    # compressed-memory mixers (layer kinds "csa" / "hca"; model/layers/csa.py,
+    # hca.py, defaults of model/config.py:56-70): index heads x head width of the
+    # CSA scores (HCA: one head of width d_model), local window, temporal
+    # compression ratio, top-k of the summaries (HCA: dense unless hca_dense is
+    # off), and the decode memory's slots per row (the reference native engine's
+    # fixed capacity, llmy_cuda/src/model.cpp:351-354; the oldest summary is
+    # overwritten once a row has emitted more)
+    csa_heads: int = 16
+    csa_head_dim: int = 128
+    csa_window: int = 128
+    csa_ratio: int = 4
+    csa_top_k: int = 32
+    hca_window: int = 128
+    hca_ratio: int = 32
+    hca_dense: bool = True
+    hca_top_k: int = 32
+    cmp_slots: int = 256
     eps: float = 1e-6
     init_std: float = 0.02
     decay_logit_init: float = 2.0  # model/layers/gated_deltanet.py:113
@@ -73,6 +90,17 @@ class HybridConfig:
 
     def gdn_layers(self) -> list[int]:
         return [i for i, k in enumerate(self.layer_kinds) if k == "gdn"]
+
+    def cmp_shape(self, kind: str) -> dict:
+        """Heads, head width, window, ratio and top-k (0 = dense) of a CSA / HCA
+        layer (model/model.py:95-106)."""
+        if kind == "csa":
+            return {"H": self.csa_heads, "Dh": self.csa_head_dim, "W": self.csa_window,
+                    "ratio": self.csa_ratio, "top_k": self.csa_top_k}
+        if kind == "hca":
+            return {"H": 1, "Dh": self.d_model, "W": self.hca_window, "ratio": self.hca_ratio,
+                    "top_k": 0 if self.hca_dense else self.hca_top_k}
+        raise ValueError(kind)
 
 
 def alternating(n: int) -> tuple[str, ...]:
@@ -111,6 +139,13 @@ def weight_shapes(cfg: HybridConfig) -> list[tuple[str, tuple[int, ...], str]]:
             w = cfg.attn_heads * cfg.attn_head_dim
             out += [(p + "wq", (w, D), "normal"), (p + "wk", (w, D), "normal"),
                     (p + "wv", (w, D), "normal"), (p + "wo", (D, w), "normal")]
+        elif kind in ("csa", "hca"):
+            cs = cfg.cmp_shape(kind)
+            Kw = cs["H"] * cs["Dh"]
+            out += [(p + "cmp_wq", (Kw, D), "normal"), (p + "cmp_wk", (Kw, D), "normal"),
+                    (p + "cmp_wv", (D, D), "normal"), (p + "cmp_wlo", (D, D), "normal"),
+                    (p + "cmp_wro", (D, D), "normal"), (p + "cmp_wout", (D, D), "normal"),
+                    (p + "cmp_wck", (Kw, D), "normal"), (p + "cmp_wcv", (D, D), "normal")]
         else:
             Hg, dk, dv = cfg.gdn_heads, cfg.gdn_dk, cfg.gdn_dv
             out += [(p + "wq", (Hg * dk, D), "normal"), (p + "wk", (Hg * dk, D), "normal"),

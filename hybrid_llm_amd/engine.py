@@ -25,6 +25,11 @@ from . import ops
 from .config import HybridConfig
 
 
+def _lib_load():
+    from . import _lib
+    return _lib.load()
+
+
 def _pad_rows(w: torch.Tensor, mult: int) -> torch.Tensor:
     n = w.shape[0]
     pad = (-n) % mult
@@ -59,6 +64,14 @@ class HybridDecoder:
             if kind == "attn":
                 self.w[p + "wqkv"] = torch.cat([up(p + "wq"), up(p + "wk"), up(p + "wv")], 0)
                 self.w[p + "wo"] = up(p + "wo")
+            elif kind in ("csa", "hca"):
+                # q | k | v in one projection, the compressor's key | value in
+                # another, [local_out | remote_out] over the branches' concat
+                self.w[p + "cmp_wqkv"] = torch.cat([up(p + "cmp_wq"), up(p + "cmp_wk"),
+                                                    up(p + "cmp_wv")], 0)
+                self.w[p + "cmp_wc"] = torch.cat([up(p + "cmp_wck"), up(p + "cmp_wcv")], 0)
+                self.w[p + "cmp_wlr"] = torch.cat([up(p + "cmp_wlo"), up(p + "cmp_wro")], 1)
+                self.w[p + "cmp_wout"] = up(p + "cmp_wout")
             else:
                 wproj = torch.cat([up(p + n) for n in ("wq", "wk", "wv", "wg", "wb")], 0)
                 self.w[p + "wproj"] = _pad_rows(wproj, 16).contiguous()
@@ -109,7 +122,8 @@ class HybridDecoder:
         for name in list(self.w):
             if name.split(".")[-1] in ("wqkv", "wo", "wproj", "wout", "w_gate_up", "w_down",
                                        "ctx_local_out", "ctx_out", "mhc_theta",
-                                       "mhc_collapse"):
+                                       "mhc_collapse", "cmp_wqkv", "cmp_wc", "cmp_wlr",
+                                       "cmp_wout"):
                 self.w[name] = ops.pack_weights(self.w[name])
         self.w["lm_head"] = ops.pack_weights(self.w["embed"])
 
@@ -123,6 +137,22 @@ class HybridDecoder:
                     self.state[(loop, l)] = {
                         "k": torch.zeros(shape, dtype=torch.bfloat16, device=dev),
                         "v": torch.zeros(shape, dtype=torch.bfloat16, device=dev)}
+                elif kind in ("csa", "hca"):
+                    # local window ring (keys, values), the memory's C slots
+                    # (keys, values, tag = position + 1, 0 empty), the count of
+                    # summaries a row emitted, the incomplete block's sum and count
+                    cs = cfg.cmp_shape(kind)
+                    Kw, W, C = cs["H"] * cs["Dh"], cs["W"], cfg.cmp_slots
+                    bf = torch.bfloat16
+                    self.state[(loop, l)] = {
+                        "lk": torch.zeros(B, W, Kw, dtype=bf, device=dev),
+                        "lv": torch.zeros(B, W, D, dtype=bf, device=dev),
+                        "mk": torch.zeros(B, C, Kw, dtype=bf, device=dev),
+                        "mv": torch.zeros(B, C, D, dtype=bf, device=dev),
+                        "mtag": torch.zeros(B, C, dtype=torch.int32, device=dev),
+                        "mcount": torch.zeros(B, dtype=torch.int32, device=dev),
+                        "psum": torch.zeros(B, D, dtype=torch.float32, device=dev),
+                        "pcnt": torch.zeros(B, dtype=torch.int32, device=dev)}
                 else:
                     self.state[(loop, l)] = {
                         "S": torch.zeros(B, cfg.gdn_heads, cfg.gdn_dk, cfg.gdn_dv,
@@ -166,6 +196,25 @@ class HybridDecoder:
             "sampled": torch.zeros(B, dtype=torch.int32, device=dev),
         }
         self.graph: torch.cuda.CUDAGraph | None = None
+        # CSA / HCA decode buffers: per kind the fused projection and the
+        # compressor's summary row; shared branch outputs and list workspace
+        cmp_kinds = sorted({k for k in cfg.layer_kinds if k in ("csa", "hca")})
+        if cmp_kinds:
+            ws = 16
+            for kind in cmp_kinds:
+                cs = cfg.cmp_shape(kind)
+                Kw = cs["H"] * cs["Dh"]
+                self.buf["cqkv_" + kind] = torch.zeros(B, 2 * Kw + D, dtype=bf, device=dev)
+                self.buf["ckv_" + kind] = torch.zeros(B, Kw + D, dtype=bf, device=dev)
+                lib = _lib_load()
+                ws = max(ws, int(lib.llmy_cmp_workspace_bytes(B, cs["H"], cs["W"], 0)),
+                         int(lib.llmy_cmp_workspace_bytes(B, cs["H"], cfg.cmp_slots,
+                                                          cs["top_k"])))
+            self.buf.update({"cloc": torch.zeros(B, 2 * D, dtype=bf, device=dev),
+                             "cy": torch.zeros(B, D, dtype=bf, device=dev),
+                             "cmean": torch.zeros(B, D, dtype=bf, device=dev),
+                             "cemit": torch.zeros(B, dtype=torch.int32, device=dev),
+                             "cws": torch.zeros(ws, dtype=torch.uint8, device=dev)})
         # Decode MoE: fused norm + router (W_r in LDS) and route-indexed experts
         # that derive their routes from the ids (no permutation pass) when the
         # sizes allow; else norm, router, permutation and sorted experts.
@@ -276,6 +325,35 @@ class HybridDecoder:
             ops.linear(b["go"], w[p + "wout"], out=b["x"] if out is None else out,
                        epilogue=ops.EPI_RESID_GATED, aux=b["cg"], layout=ops.LAYOUT_PACKED)
 
+    def _cmp(self, l: int, st: dict, out=None, epilogue=None) -> None:
+        """CSA / HCA decode (csa.py:157-259, hca.py:106-193): the q | k | v
+        projection, the local window over the ring (the new key and value stored
+        first), the compressor step with, for a row completing a block, its new
+        summary committed to the memory, the memory branch, then
+        out(local_out(local) + remote_out(memory)) into the residual."""
+        cfg, w, b = self.cfg, self.w, self.buf
+        p, kind = f"L{l}.", cfg.layer_kinds[l]
+        cs = cfg.cmp_shape(kind)
+        H, Dh, D = cs["H"], cs["Dh"], cfg.d_model
+        Kw = H * Dh
+        qkv = b["cqkv_" + kind]
+        ops.linear(b["h"], w[p + "cmp_wqkv"], out=qkv, layout=ops.LAYOUT_PACKED)
+        q, k, v = qkv[:, :Kw], qkv[:, Kw:2 * Kw], qkv[:, 2 * Kw:]
+        loc = b["cloc"]
+        ops.cmp_local_decode(q, k, v, st["lk"], st["lv"], self.pos, H, Dh, out=loc[:, :D],
+                             workspace=b["cws"])
+        ops.cmp_pool_step(b["h"], st["psum"], st["pcnt"], cs["ratio"], mean=b["cmean"],
+                          emit=b["cemit"])
+        ckv = b["ckv_" + kind]
+        ops.linear(b["cmean"], w[p + "cmp_wc"], out=ckv, layout=ops.LAYOUT_PACKED)
+        ops.cmp_commit(ckv, b["cemit"], self.pos, st["mk"], st["mv"], st["mtag"], st["mcount"])
+        ops.cmp_memory_decode(q, st["mk"], st["mv"], st["mtag"], self.pos, H, Dh, cs["top_k"],
+                              out=loc[:, D:], workspace=b["cws"])
+        ops.linear(loc, w[p + "cmp_wlr"], out=b["cy"], layout=ops.LAYOUT_PACKED)
+        ops.linear(b["cy"], w[p + "cmp_wout"], out=b["x"] if out is None else out,
+                   epilogue=ops.EPI_RESID_ADD if epilogue is None else epilogue,
+                   layout=ops.LAYOUT_PACKED)
+
     def _ctx_weights(self, p: str) -> dict:
         w = self.w
         return {n: w[p + n] for n in ("router_norm", "ctx_down", "ctx_ln_w", "ctx_ln_b",
@@ -344,6 +422,8 @@ class HybridDecoder:
         for i, (loop, l) in enumerate(apps):
             if cfg.layer_kinds[l] == "attn":
                 self._attn(l, self.state[(loop, l)])
+            elif cfg.layer_kinds[l] in ("csa", "hca"):
+                self._cmp(l, self.state[(loop, l)])
             else:
                 self._gdn(l, self.state[(loop, l)])
             nxt = w[f"L{apps[i + 1][1]}.mix_norm"] if i + 1 < len(apps) else w["final_norm"]
@@ -405,6 +485,8 @@ class HybridDecoder:
                 self._mhc_read(l, X, "mix_norm", b["raw"], b["maps"], b["h"], b["xb"])
                 if cfg.layer_kinds[l] == "attn":
                     self._attn(l, st, out=U, epilogue=ops.EPI_STORE_F32)
+                elif cfg.layer_kinds[l] in ("csa", "hca"):
+                    self._cmp(l, st, out=U, epilogue=ops.EPI_STORE_F32)
                 else:
                     U.zero_()
                     self._gdn(l, st, out=U)
@@ -542,6 +624,8 @@ class HybridDecoder:
             st = self.state[(loop, l)]
             if cfg.layer_kinds[l] == "attn":
                 self._attn_seq(l, st, x, h, B, T)
+            elif cfg.layer_kinds[l] in ("csa", "hca"):
+                self._cmp_seq(l, st, x, h, B, T)
             else:
                 self._gdn_seq(l, st, x, h, B, T)
             nxt = w[f"L{apps[i + 1][1]}.mix_norm"] if i + 1 < len(apps) else w["final_norm"]
@@ -576,6 +660,8 @@ class HybridDecoder:
                 self._mhc_read(l, X, "mix_norm", raw, maps, h, xb)
                 if cfg.layer_kinds[l] == "attn":
                     self._attn_seq(l, st, U, h, B, T, epilogue=ops.EPI_STORE_F32)
+                elif cfg.layer_kinds[l] in ("csa", "hca"):
+                    self._cmp_seq(l, st, U, h, B, T, epilogue=ops.EPI_STORE_F32)
                 else:
                     U.zero_()
                     self._gdn_seq(l, st, U, h, B, T)
@@ -617,6 +703,34 @@ class HybridDecoder:
                                     v.view(B, T, H, hd), cfg.window, cfg.attn_scale)
         ops.kv_cache_fill(k.view(B, T, Hhd), v.view(B, T, Hhd), st["k"], st["v"])
         ops.linear(o.view(R, Hhd), w[p + "wo"], out=x,
+                   epilogue=ops.EPI_RESID_ADD if epilogue is None else epilogue,
+                   layout=ops.LAYOUT_PACKED)
+
+    def _cmp_seq(self, l: int, st: dict, x, h, B: int, T: int, epilogue=None) -> None:
+        """CSA / HCA over B fresh sequences (csa.py:35-155, hca.py:32-104): the
+        projection over B*T rows, the local window, the block means and their
+        summaries, the memory branch, the output projections; then the state T
+        decode steps would leave (ring: the last W keys / values; memory: the
+        summaries with their tags; the incomplete block's sum and count)."""
+        cfg, w = self.cfg, self.w
+        p, kind = f"L{l}.", cfg.layer_kinds[l]
+        cs = cfg.cmp_shape(kind)
+        H, Dh, D, ratio = cs["H"], cs["Dh"], cfg.d_model, cs["ratio"]
+        Kw, R, n = H * Dh, B * T, T // cs["ratio"]
+        qkv = ops.linear(h, w[p + "cmp_wqkv"], layout=ops.LAYOUT_PACKED)
+        q, k, v = qkv[:, :Kw], qkv[:, Kw:2 * Kw], qkv[:, 2 * Kw:]
+        loc = torch.empty(R, 2 * D, dtype=torch.bfloat16, device=self.dev)
+        ops.cmp_local_prefill(q, k, v, B, T, H, Dh, cs["W"], out=loc[:, :D])
+        means = ops.cmp_pool_prefill(h, B, T, ratio, st["psum"], st["pcnt"])
+        kv = (ops.linear(means, w[p + "cmp_wc"], layout=ops.LAYOUT_PACKED) if n else
+              torch.empty(0, Kw + D, dtype=torch.bfloat16, device=self.dev))
+        ops.cmp_memory_prefill(q, kv[:, :Kw], kv[:, Kw:], B, T, ratio, H, Dh, cs["top_k"],
+                               out=loc[:, D:])
+        ops.cmp_memory_fill(kv, B, n, ratio, st["mk"], st["mv"], st["mtag"], st["mcount"])
+        ops.cmp_ring_fill(k, B, T, st["lk"])
+        ops.cmp_ring_fill(v, B, T, st["lv"])
+        y1 = ops.linear(loc, w[p + "cmp_wlr"], layout=ops.LAYOUT_PACKED)
+        ops.linear(y1, w[p + "cmp_wout"], out=x,
                    epilogue=ops.EPI_RESID_ADD if epilogue is None else epilogue,
                    layout=ops.LAYOUT_PACKED)
 
@@ -675,7 +789,10 @@ class HybridDecoder:
 
     # ------------------------------------------------------------------ state io
     def load_state(self, pos: torch.Tensor, state: dict) -> None:
-        """Copy a host state (the oracle's layout) into the device buffers."""
+        """Copy a host state (the oracle's layout) into the device buffers
+        (attention and GDN layers)."""
+        if any(k in ("csa", "hca") for k in self.cfg.layer_kinds):
+            raise NotImplementedError("load_state covers attention and GDN layers")
         self.pos.copy_(pos.to(torch.int32))
         for key, st in self.state.items():
             for name, t in st.items():

@@ -11,6 +11,9 @@ single residual stream of mHC disabled (model.py:119-126).
 Mixers:
   * attention: q/k/v projections, banded attention over a ring KV cache
     (decode window of model/layers/hca.py:119-128), output projection;
+  * CSA / HCA: the compressed-memory mixers of oracle/compressed.py (local
+    window plus block summaries, model/layers/csa.py, hca.py) through their
+    decode path;
   * GDN: gated_deltanet.py:125-149,254-275 — q/k/v/gate/beta projections,
     per-head L2 norm of q and k (clamp 1e-12), beta = sigmoid(.+bias),
     gate = sigmoid(.), decay = sigmoid(decay_logit) per head, the delta-rule
@@ -36,6 +39,7 @@ import torch.nn.functional as F
 from hybrid_llm_amd.config import HybridConfig
 
 from .attention import banded_attention_decode
+from .compressed import CompressedMixer
 from .gdn import gdn_step
 from .mhc import mhc_maps, mhc_read, mhc_write
 from .moe import moe_grouped, shared_experts
@@ -60,6 +64,12 @@ class HybridOracle:
         self.routes: list[np.ndarray] = []
         self.route_gaps: list[float] = []
         self.route_total = 0
+        self.cmp = {l: CompressedMixer(self.w, f"L{l}.", *self._cmp_args(k), act_round=self.rnd)
+                    for l, k in enumerate(cfg.layer_kinds) if k in ("csa", "hca")}
+
+    def _cmp_args(self, kind: str):
+        cs = self.cfg.cmp_shape(kind)
+        return cs["H"], cs["Dh"], cs["W"], cs["ratio"], cs["top_k"] or None
 
     # ---- state -----------------------------------------------------------
     def new_state(self, batch: int) -> dict:
@@ -70,6 +80,8 @@ class HybridOracle:
                 if kind == "attn":
                     shape = (batch, cfg.attn_heads, cfg.window, cfg.attn_head_dim)
                     st[(loop, l)] = {"k": torch.zeros(shape), "v": torch.zeros(shape)}
+                elif kind in ("csa", "hca"):
+                    st[(loop, l)] = {"cmp": self.cmp[l].new_state(batch, cfg.d_model)}
                 else:
                     st[(loop, l)] = {
                         "S": torch.zeros(batch, cfg.gdn_heads, cfg.gdn_dk, cfg.gdn_dv),
@@ -199,6 +211,8 @@ class HybridOracle:
         h = rnd(rmsnorm(hidden, w[f"L{l}.mix_norm"], cfg.eps))
         if cfg.layer_kinds[l] == "attn":
             u = self._attn(l, h, s, pos)
+        elif cfg.layer_kinds[l] in ("csa", "hca"):
+            u = self.cmp[l].step(h, s["cmp"], pos)
         else:
             u = self._gdn(l, h, s)
         x = self._mhc_write(l, x, u, maps) if mhc else x + u
@@ -234,6 +248,8 @@ class HybridOracle:
                 if name in s:
                     s[name] = s[name].clone()
                     s[name][rows] = 0
+            if "cmp" in s:
+                CompressedMixer.reset_rows(s["cmp"], rows)
             if self.cfg.context_router:
                 n = s.get("lat_n", torch.full((rows.numel(),), s["lat"].shape[1],
                                               dtype=torch.long))

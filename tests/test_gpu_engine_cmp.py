@@ -1,0 +1,132 @@
+"""GPU parity: models with CSA / HCA mixers in the Python engine against the
+model oracle (oracle/model.py with oracle/compressed.py, pinned to the
+reference modules), with the engine's routing replayed: decode steps past the
+local window and across several emitted summaries, a captured decode graph
+equal to eager bit for bit, a prefill followed by decoding, a row reset, and
+the mHC stack.
+
+Tolerances.  With a top-k that covers every summary (CM: the top-k kernels run,
+the selection is all of them) every step is within rel-L2 1e-2, as the other
+engine tests.  A selective top-k is a discrete decision like the MoE routing,
+but it is not replayed into the oracle: where two summaries' scores tie to
+within the bf16 rounding of q, the two sides can pick different ones and that
+step's logits move by up to about 1e-2 (measured: 1.0e-2 at one step of 40,
+all others <= 3.7e-3; with the top-k widened to all summaries the same run
+stays <= 3.8e-3).  Selective configs (CMK) therefore bound the median step by
+5e-3 and the worst by 2.5e-2; the mixer alone matches the oracle to 1e-6 per
+step (tests/test_gpu_compressed.py checks the kernels).
+"""
+from dataclasses import replace
+
+import numpy as np
+import pytest
+import torch
+
+from hybrid_llm_amd.config import C1, init_weights
+from oracle.model import HybridOracle
+
+pytestmark = pytest.mark.gpu
+
+REL_L2 = 1e-2
+
+# csa_top_k 16 covers every summary of these runs (<= 12 per row)
+CM = replace(C1, layer_kinds=("csa", "gdn", "hca", "attn"), vocab=2048, csa_heads=4,
+             csa_head_dim=64, csa_window=16, csa_ratio=4, csa_top_k=16, hca_window=12,
+             hca_ratio=8, cmp_slots=64)
+CMK = replace(CM, layer_kinds=("hca", "csa", "gdn"), csa_top_k=3, hca_dense=False, hca_top_k=2)
+SELECTIVE_MEDIAN, SELECTIVE_MAX = 5e-3, 2.5e-2
+
+
+def _bound(cfg, errs):
+    errs = np.asarray(errs)
+    if cfg is CMK:
+        assert float(np.median(errs)) <= SELECTIVE_MEDIAN and errs.max() <= SELECTIVE_MAX, errs
+    else:
+        assert errs.max() <= REL_L2, errs
+
+
+def rel_l2(a, b):
+    a, b = a.double().cpu(), b.double().cpu()
+    return float(torch.linalg.norm(a - b) / torch.linalg.norm(b))
+
+
+def _decode(cfg, B, steps, seed, reset_at=None, graph=False):
+    from hybrid_llm_amd.engine import HybridDecoder
+    w = init_weights(cfg, seed=seed)
+    toks = torch.randint(0, cfg.vocab, (steps, B), generator=torch.Generator().manual_seed(seed),
+                         dtype=torch.int32)
+    ref = HybridOracle(cfg, w, act_bf16=True)
+    st = ref.new_state(B)
+    eng = HybridDecoder(cfg, w, B)
+    eng.enable_route_log()
+    errs, outs = [], []
+    for i in range(steps):
+        reset = None
+        if reset_at is not None and i == reset_at[0]:
+            reset = torch.zeros(B, dtype=torch.int32)
+            reset[reset_at[1]] = 1
+        lg = eng.step(toks[i].cuda(), reset=None if reset is None else reset.cuda()).clone()
+        outs.append(lg)
+        ref.forced_routes = [r for r in eng.route_log.cpu().numpy()]
+        lr = ref.step(toks[i].numpy(), st, reset=None if reset is None else reset.numpy())
+        errs.append(rel_l2(lg, lr))
+    gaps = np.abs(np.array(ref.route_gaps))
+    assert np.all(gaps <= 5e-3), gaps.max()
+    return errs, outs, toks, w
+
+
+@pytest.mark.parametrize("cfg", [CM, CMK], ids=["dense", "topk"])
+def test_decode_matches_oracle_and_graph(cfg):
+    from hybrid_llm_amd.engine import HybridDecoder
+    B, steps = 3, 40
+    errs, eager, toks, w = _decode(cfg, B, steps, seed=3)
+    print(f"cmp decode: worst step rel-L2 {max(errs):.2e}, median {np.median(errs):.2e}",
+          flush=True)
+    _bound(cfg, errs)
+    g = HybridDecoder(cfg, w, B)
+    g.capture()
+    for i in range(steps):
+        out = g.step(toks[i].cuda()).clone()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager[i]), i
+
+
+def test_decode_row_reset():
+    errs, _, _, _ = _decode(CM, 3, 30, seed=7, reset_at=(21, 1))
+    print(f"cmp decode with a reset: worst step rel-L2 {max(errs):.2e}", flush=True)
+    _bound(CM, errs)
+
+
+@pytest.mark.parametrize("cfg,T", [(CM, 45), (CMK, 30), (CM, 5)], ids=["dense", "topk", "short"])
+def test_prefill_matches_oracle_then_decodes(cfg, T):
+    from hybrid_llm_amd.engine import HybridDecoder
+    w = init_weights(cfg, seed=5)
+    B = 2
+    prompt = torch.randint(0, cfg.vocab, (B, T), generator=torch.Generator().manual_seed(6),
+                           dtype=torch.int32)
+    eng = HybridDecoder(cfg, w, B)
+    eng.route_log_seq = []
+    lg = eng.prefill(prompt.cuda()).clone()
+    ref = HybridOracle(cfg, w, act_bf16=True)
+    st = ref.new_state(B)
+    logs = [r.view(B, T, -1).cpu().numpy() for r in eng.route_log_seq]
+    ref.forced_routes = [logs[a][:, t] for t in range(T) for a in range(len(logs))]
+    out = ref.prefill(prompt.numpy(), st)
+    errs = [rel_l2(lg, out[:, -1])]
+    print(f"cmp prefill T={T}: last-position rel-L2 {errs[0]:.2e}", flush=True)
+    eng.route_log_seq = None
+    eng.enable_route_log()
+    for i in range(6):
+        nxt = eng.buf["next"].clone()
+        lg2 = eng.step(nxt).clone()
+        ref.forced_routes = [r for r in eng.route_log.cpu().numpy()]
+        lr2 = ref.step(nxt.cpu().numpy(), st)
+        errs.append(rel_l2(lg2, lr2))
+    _bound(cfg, errs)
+
+
+def test_mhc_with_compressed_mixers():
+    cfg = replace(CM, mhc_streams=4, mhc_gating_init=0.5, num_loops=1)
+    errs, _, _, _ = _decode(cfg, 2, 20, seed=11)
+    print(f"mHC + cmp decode: worst step rel-L2 {max(errs):.2e}", flush=True)
+    _bound(cfg, errs)
