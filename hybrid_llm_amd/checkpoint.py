@@ -17,9 +17,12 @@ Tensor names and config keys follow the reference model's where the concept
 is the same (`embed_tokens.weight`, `recurrent_core.<i>.mixer_norm.weight`,
 GDN `q_proj/k_proj/v_proj/gate_proj/beta_proj/out_proj/conv/decay_logit`,
 MoE `router.norm/router.logits` and expert stacks `[E, H, D]`; `gdn.*` and
-`moe.*` keys).  The banded attention mixer of this block stack has no
-reference counterpart with the same weights, so its layout entry is `attn`
-and its keys are `attn.heads`, `attn.head_dim`, `attn.window`.
+`moe.*` keys; CSA / HCA `query/key/value/local_out/remote_out|global_out/out`
+and `compressor.key/value`, `csa.*` / `hca.*` keys).  The banded attention
+mixer of this block stack has no reference counterpart with the same weights,
+so its layout entry is `attn` and its keys are `attn.heads`, `attn.head_dim`,
+`attn.window`.  `memory.decode_slots` (the CSA / HCA decode memory's slots per
+row) is this engine's key; the reference reader ignores unknown keys.
 
 The native loader `llmy_load` (hybrid_llm_amd/csrc/engine.cpp) reads the same
 files; this module writes them from `config.init_weights`-style dicts and
@@ -48,6 +51,11 @@ _GDN = {"wq": "q_proj.weight", "wk": "k_proj.weight", "wv": "v_proj.weight",
         "wg": "gate_proj.weight", "wb": "beta_proj.weight", "bb": "beta_proj.bias",
         "wout": "out_proj.weight", "conv": "conv.weight", "decay": "decay_logit"}
 _ATTN = {"wq": "q.weight", "wk": "k.weight", "wv": "v.weight", "wo": "o.weight"}
+# CSA / HCA (model/layers/csa.py:21-29, hca.py:24-30; llmy_cuda/src/model.cpp:132-160):
+# remote_out is CSA's name, global_out HCA's
+_CMP = {"cmp_wq": "query.weight", "cmp_wk": "key.weight", "cmp_wv": "value.weight",
+        "cmp_wlo": "local_out.weight", "cmp_wout": "out.weight",
+        "cmp_wck": "compressor.key.weight", "cmp_wcv": "compressor.value.weight"}
 _BLOCK = {"mix_norm": "mixer_norm.weight", "ffn_norm": "ffn_norm.weight",
           "router_norm": "moe.router.norm.weight", "w_router": "moe.router.logits.weight",
           "w_gate": "moe.experts.gate_proj.weight", "w_up": "moe.experts.up_proj.weight",
@@ -91,7 +99,12 @@ def file_name(cfg: HybridConfig, key: str) -> str:
         return p + _BLOCK[short]
     if short in _MHC:
         return p + _MHC[short]
-    table = _ATTN if cfg.layer_kinds[l] == "attn" else _GDN
+    kind = cfg.layer_kinds[l]
+    if kind in ("csa", "hca"):
+        if short == "cmp_wro":
+            return p + "mixer." + ("remote_out.weight" if kind == "csa" else "global_out.weight")
+        return p + "mixer." + _CMP[short]
+    table = _ATTN if kind == "attn" else _GDN
     return p + "mixer." + table[short]
 
 
@@ -111,20 +124,26 @@ def config_text(cfg: HybridConfig) -> str:
         "router.context_aware": int(cfg.context_router),
         "router.local_context": cfg.router_context, "mla.latent_dim": cfg.latent_dim,
         "rms_norm_eps": repr(float(cfg.eps)),
+        "csa.temporal_compression": cfg.csa_ratio, "csa.local_window": cfg.csa_window,
+        "csa.index_heads": cfg.csa_heads, "csa.index_head_dim": cfg.csa_head_dim,
+        "csa.index_top_k": cfg.csa_top_k, "hca.temporal_compression": cfg.hca_ratio,
+        "hca.local_window": cfg.hca_window, "hca.dense_global_attention": int(cfg.hca_dense),
+        "hca.global_top_k": cfg.hca_top_k, "memory.decode_slots": cfg.cmp_slots,
     }
     return "".join(f"{k}={keys[k]}\n" for k in sorted(keys))
 
 
 def config_from_text(text: str) -> HybridConfig:
     kv = dict(line.split("=", 1) for line in text.splitlines() if "=" in line)
-    kinds = tuple(kv["recurrent_layout"].split(","))
+    # every core block carries a MoE: "gdn_moe" and "gdn" name the same block
+    kinds = tuple(k[:-4] if k.endswith("_moe") else k for k in kv["recurrent_layout"].split(","))
     if int(kv.get("stem_blocks", 0)) or int(kv.get("tail_blocks", 0)):
         raise ValueError("stem/tail blocks are not part of this block stack")
     if kv.get("gdn.qk_heads") != kv.get("gdn.value_heads"):
         raise ValueError("GDN q/k and value head counts must match")
     return HybridConfig(
-        d_model=int(kv["d_model"]), layer_kinds=kinds, attn_heads=int(kv["attn.heads"]),
-        attn_head_dim=int(kv["attn.head_dim"]), window=int(kv["attn.window"]),
+        d_model=int(kv["d_model"]), layer_kinds=kinds, attn_heads=int(kv.get("attn.heads", 0)),
+        attn_head_dim=int(kv.get("attn.head_dim", 0)), window=int(kv.get("attn.window", 0)),
         gdn_heads=int(kv["gdn.qk_heads"]), gdn_dk=int(kv["gdn.qk_head_dim"]),
         gdn_dv=int(kv["gdn.value_head_dim"]), n_experts=int(kv["moe.routed_experts"]),
         top_k=int(kv["moe.routed_top_k"]), expert_hidden=int(kv["moe.expert_hidden"]),
@@ -135,6 +154,17 @@ def config_from_text(text: str) -> HybridConfig:
         context_router=_parse_bool(kv.get("router.context_aware", "1")),
         router_context=int(kv.get("router.local_context", 128)),
         latent_dim=int(kv.get("mla.latent_dim", 256)),
+        # CSA / HCA keys with the reference defaults (llmy_cuda/include/config.h:41-51)
+        csa_ratio=int(kv.get("csa.temporal_compression", 4)),
+        csa_window=int(kv.get("csa.local_window", 128)),
+        csa_heads=int(kv.get("csa.index_heads", 16)),
+        csa_head_dim=int(kv.get("csa.index_head_dim", 128)),
+        csa_top_k=int(kv.get("csa.index_top_k", 32)),
+        hca_ratio=int(kv.get("hca.temporal_compression", 32)),
+        hca_window=int(kv.get("hca.local_window", 128)),
+        hca_dense=_parse_bool(kv.get("hca.dense_global_attention", "1")),
+        hca_top_k=int(kv.get("hca.global_top_k", 32)),
+        cmp_slots=int(kv.get("memory.decode_slots", 256)),
         **_mhc_from(kv))
 
 

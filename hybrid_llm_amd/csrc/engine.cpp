@@ -168,7 +168,14 @@ std::map<std::string, std::string> parse_config(const std::string& text) {
 }
 
 // ------------------------------------------------------------------ model
-enum Kind { kAttn = 0, kGdn = 1 };
+enum Kind { kAttn = 0, kGdn = 1, kCsa = 2, kHca = 3 };
+
+// Heads, head width, local window, compression ratio and top-k (0 = dense) of
+// a compressed-memory mixer (model/model.py:95-106).
+struct CmpShape {
+  int H = 0, Dh = 0, W = 0, ratio = 0, top_k = 0;
+  int kw() const { return H * Dh; }
+};
 
 struct Config {
   int vocab = 0, d_model = 0, num_loops = 0;
@@ -184,7 +191,26 @@ struct Config {
   // multi-stream hyper-connections: streams per token (mhc.streams when
   // mhc.enabled; 1 = the single residual stream) and Sinkhorn iterations
   int mhc = 1, mhc_iters = 20;
+  // compressed-memory mixers: csa.* / hca.* keys (llmy_cuda/include/config.h:41-51)
+  // and the decode memory's slots per row (memory.decode_slots; the reference
+  // native engine's fixed 256, llmy_cuda/src/model.cpp:351-354)
+  int csa_heads = 16, csa_head_dim = 128, csa_window = 128, csa_ratio = 4, csa_top_k = 32;
+  int hca_window = 128, hca_ratio = 32, hca_top_k = 32;
+  bool hca_dense = true;
+  int cmp_slots = 256;
   float eps = 1e-6f;
+  CmpShape cmp(int kind) const {
+    CmpShape c;
+    if (kind == kCsa) {
+      c.H = csa_heads, c.Dh = csa_head_dim, c.W = csa_window, c.ratio = csa_ratio;
+      c.top_k = csa_top_k;
+    } else {
+      c.H = 1, c.Dh = d_model, c.W = hca_window, c.ratio = hca_ratio;
+      c.top_k = hca_dense ? 0 : hca_top_k;
+    }
+    return c;
+  }
+  bool has(int kind) const { return std::count(kinds.begin(), kinds.end(), kind) > 0; }
   int mhc_n16() const { return (2 * mhc + mhc * mhc + 15) / 16 * 16; }
   int routes() const { return top_k + shared; }      // routes per token, shared included
   int all_experts() const { return experts + shared; }
@@ -237,9 +263,14 @@ Config config_from(const std::string& text) {
   while (p <= s.size()) {
     size_t e = s.find(',', p);
     if (e == std::string::npos) e = s.size();
-    const std::string k = s.substr(p, e - p);
+    std::string k = s.substr(p, e - p);
+    // every core block carries a MoE: "gdn_moe" and "gdn" name the same block
+    // (the mixer kind is the part before '_', model/model.py:395)
+    if (k.size() > 4 && k.compare(k.size() - 4, 4, "_moe") == 0) k.resize(k.size() - 4);
     if (k == "attn") c.kinds.push_back(kAttn);
     else if (k == "gdn") c.kinds.push_back(kGdn);
+    else if (k == "csa") c.kinds.push_back(kCsa);
+    else if (k == "hca") c.kinds.push_back(kHca);
     else throw std::runtime_error("unsupported block kind " + k);
     p = e + 1;
   }
@@ -261,6 +292,16 @@ Config config_from(const std::string& text) {
   c.ctx = cfg_bool(kv, "router.context_aware", true);
   c.ctx_window = cfg_int(kv, "router.local_context", 128, false);
   c.latent = cfg_int(kv, "mla.latent_dim", 256, false);
+  c.csa_ratio = cfg_int(kv, "csa.temporal_compression", 4, false);
+  c.csa_window = cfg_int(kv, "csa.local_window", 128, false);
+  c.csa_heads = cfg_int(kv, "csa.index_heads", 16, false);
+  c.csa_head_dim = cfg_int(kv, "csa.index_head_dim", 128, false);
+  c.csa_top_k = cfg_int(kv, "csa.index_top_k", 32, false);
+  c.hca_ratio = cfg_int(kv, "hca.temporal_compression", 32, false);
+  c.hca_window = cfg_int(kv, "hca.local_window", 128, false);
+  c.hca_dense = cfg_bool(kv, "hca.dense_global_attention", true);
+  c.hca_top_k = cfg_int(kv, "hca.global_top_k", 32, false);
+  c.cmp_slots = cfg_int(kv, "memory.decode_slots", 256, false);
   auto eps = kv.find("rms_norm_eps");
   if (eps != kv.end()) c.eps = std::stof(eps->second);
   if (c.kinds.empty() || c.num_loops < 1 || c.vocab < 1 || c.d_model % 256 != 0 ||
@@ -272,6 +313,19 @@ Config config_from(const std::string& text) {
                              "d_model <= 1024, router.local_context >= 1");
   if (c.mhc > 1 && (c.ctx || c.d_model > 4096 || c.mhc_iters < 0))
     throw std::runtime_error("mHC needs d_model <= 4096 and the plain router");
+  // compressed-memory mixers: head widths the decode scoring splits over
+  // lanes (16..256 or a multiple of 512), top-k <= 64, memory and window
+  // within the kernels' LDS lists
+  auto dh_ok = [](int d) {
+    return d == 16 || d == 32 || d == 64 || d == 128 || d == 256 || (d % 512 == 0 && d <= 4096);
+  };
+  for (int kind : {kCsa, kHca}) {
+    if (!c.has(kind)) continue;
+    const CmpShape cs = c.cmp(kind);
+    if (!dh_ok(cs.Dh) || cs.kw() % 16 != 0 || cs.W < 1 || cs.W > 8192 || cs.ratio < 1 ||
+        cs.top_k < 0 || cs.top_k > 64 || c.cmp_slots < 1 || c.cmp_slots > 16384 || c.d_model > 8192)
+      throw std::runtime_error("unsupported CSA / HCA shape");
+  }
   return c;
 }
 
@@ -352,6 +406,9 @@ struct Layer {
   float *mhc_map_norm = nullptr, *mhc_pre_bias = nullptr, *mhc_post_bias = nullptr,
         *mhc_res_bias = nullptr, *mhc_alpha = nullptr, *mhc_gating = nullptr,
         *mhc_scale = nullptr, *mhc_ln_w = nullptr, *mhc_ln_b = nullptr;
+  // CSA / HCA (packed bf16): query | key | value [2 Kw + D, D], the
+  // compressor's key | value [Kw + D, D], [local_out | remote_out] [D, 2 D], out [D, D]
+  uint16_t *cmp_wqkv = nullptr, *cmp_wc = nullptr, *cmp_wlr = nullptr, *cmp_wout = nullptr;
 };
 
 struct Model {
@@ -483,7 +540,30 @@ std::unique_ptr<Model> load_model(const char* path) {
                                          1, D, Lc);
       L.ctx_out = m->upload_packed(mat_bf16("moe.router.context_out.weight", {D, D}), 1, D, D);
     }
-    if (L.kind == kAttn) {
+    if (L.kind == kCsa || L.kind == kHca) {
+      // model/layers/csa.py:21-29, hca.py:24-30 (names of llmy_cuda/src/model.cpp:139-160)
+      const int Kw = c.cmp(L.kind).kw();
+      L.cmp_wqkv = m->upload_packed(concat_rows({mat_bf16("mixer.query.weight", {Kw, D}),
+                                                 mat_bf16("mixer.key.weight", {Kw, D}),
+                                                 mat_bf16("mixer.value.weight", {D, D})}, 0),
+                                    1, 2 * Kw + D, D);
+      L.cmp_wc = m->upload_packed(concat_rows({mat_bf16("mixer.compressor.key.weight", {Kw, D}),
+                                               mat_bf16("mixer.compressor.value.weight", {D, D})},
+                                              0),
+                                  1, Kw + D, D);
+      const auto lo = mat_bf16("mixer.local_out.weight", {D, D});
+      const auto ro = mat_bf16(L.kind == kCsa ? "mixer.remote_out.weight" : "mixer.global_out.weight",
+                               {D, D});
+      std::vector<uint16_t> lr(static_cast<size_t>(D) * 2 * D);
+      for (int i = 0; i < D; ++i) {  // row i: local_out[i, :] then remote_out[i, :]
+        std::memcpy(lr.data() + static_cast<size_t>(i) * 2 * D, lo.data() + static_cast<size_t>(i) * D,
+                    static_cast<size_t>(D) * 2);
+        std::memcpy(lr.data() + static_cast<size_t>(i) * 2 * D + D,
+                    ro.data() + static_cast<size_t>(i) * D, static_cast<size_t>(D) * 2);
+      }
+      L.cmp_wlr = m->upload_packed(lr, 1, D, 2 * D);
+      L.cmp_wout = m->upload_packed(mat_bf16("mixer.out.weight", {D, D}), 1, D, D);
+    } else if (L.kind == kAttn) {
       const int W = c.attn_heads * c.attn_head_dim;
       if (W % 16 != 0 || W % 256 != 0 || (c.attn_head_dim != 64 && c.attn_head_dim != 128))
         throw std::runtime_error("unsupported attention shape");
@@ -565,6 +645,13 @@ struct LayerState {
   uint16_t* hist = nullptr; // [B, 3, D]
   float* ring = nullptr;    // context router: [B, W, L], the last W latents (slot pos % W)
   size_t k_bytes = 0, s_bytes = 0, hist_bytes = 0, ring_bytes = 0;
+  // CSA / HCA: local ring keys [B, W, Kw] / values [B, W, D], memory slots keys
+  // [B, C, Kw] / values [B, C, D] / tags [B, C] (position + 1, 0 empty), summaries
+  // emitted per row [B], the incomplete block's sum [B, D] fp32 and count [B]
+  uint16_t *lk = nullptr, *lv = nullptr, *mk = nullptr, *mv = nullptr;
+  int32_t *mtag = nullptr, *mcount = nullptr, *pcnt = nullptr;
+  float* psum = nullptr;
+  std::vector<std::pair<void*, size_t>> cmp_bufs;  // every CSA / HCA buffer and its bytes
 };
 
 struct Buffers {  // activations for `rows` token rows
@@ -590,6 +677,13 @@ struct Buffers {  // activations for `rows` token rows
   float *mX = nullptr, *mraw = nullptr, *mmaps = nullptr, *mU = nullptr;
   uint16_t* mxb = nullptr;
   int32_t *mones = nullptr, *mident = nullptr;
+  // CSA / HCA: projection [rows, 2 Kw + D], branch outputs [rows, 2 D], their
+  // projection [rows, D], the compressor's mean [rows, D] and emit flags
+  // (decode), block means [B T/ratio, D] (prefill), summaries [., Kw + D], lists
+  uint16_t *cqkv = nullptr, *cloc = nullptr, *cy = nullptr, *cmean = nullptr, *ckv = nullptr;
+  int32_t* cemit = nullptr;
+  void* cws = nullptr;
+  int64_t cws_bytes = 0;
   void* ws = nullptr;
   int64_t ws_bytes = 0;
   DeviceArena arena;
@@ -681,6 +775,29 @@ void alloc_buffers(const Config& c, int rows, int B, int T, Buffers& b) {
   }
   if (T == 1 && rows <= 64 && D % 256 == 0 && D / 256 <= 8 && c.gdn_heads > 0)
     b.proj_parts = b.arena.zeros<float>(static_cast<size_t>(D / 256) * rows * c.nproj16());
+  if (c.has(kCsa) || c.has(kHca)) {
+    int kw = 0, rmin = 1 << 30;
+    int64_t ws = 16;
+    for (int kind : {kCsa, kHca}) {
+      if (!c.has(kind)) continue;
+      const CmpShape cs = c.cmp(kind);
+      kw = std::max(kw, cs.kw());
+      rmin = std::min(rmin, cs.ratio);
+      const int slots = T == 1 ? c.cmp_slots : std::max(T / cs.ratio, 1);
+      ws = std::max({ws, llmy_cmp_workspace_bytes(rows, cs.H, cs.W, 0),
+                     llmy_cmp_workspace_bytes(rows, cs.H, slots, cs.top_k)});
+    }
+    if (ws < 0) throw std::runtime_error("CSA / HCA workspace size");
+    const size_t nsum = T == 1 ? static_cast<size_t>(rows) : static_cast<size_t>(B) * (T / rmin);
+    b.cqkv = b.arena.zeros<uint16_t>(static_cast<size_t>(rows) * (2 * kw + D));
+    b.cloc = b.arena.zeros<uint16_t>(static_cast<size_t>(rows) * 2 * D);
+    b.cy = b.arena.zeros<uint16_t>(static_cast<size_t>(rows) * D);
+    b.cmean = b.arena.zeros<uint16_t>(std::max(nsum, static_cast<size_t>(1)) * D);
+    b.ckv = b.arena.zeros<uint16_t>(std::max(nsum, static_cast<size_t>(1)) * (kw + D));
+    b.cemit = b.arena.zeros<int32_t>(rows);
+    b.cws_bytes = ws;
+    b.cws = b.arena.zeros<unsigned char>(static_cast<size_t>(ws));
+  }
   if (T > 1 && c.gdn_heads > 0) {
     b.ws_bytes = llmy_gdn_prefill_workspace_bytes(B, T, c.gdn_heads, c.dk, c.dv);
     if (b.ws_bytes < 0) throw std::runtime_error("GDN prefill workspace size");
@@ -698,7 +815,22 @@ std::unique_ptr<State> new_state(Model* m, int B) {
   for (int loop = 0; loop < c.num_loops; ++loop) {
     for (int kind : c.kinds) {
       LayerState L;
-      if (kind == kAttn) {
+      if (kind == kCsa || kind == kHca) {
+        const CmpShape cs = c.cmp(kind);
+        const size_t Bz = B, W = cs.W, C = c.cmp_slots, Kw = cs.kw(), Dz = D;
+        auto add = [&](auto* p, size_t bytes) {
+          L.cmp_bufs.emplace_back(static_cast<void*>(p), bytes);
+          return p;
+        };
+        L.lk = add(s->arena.zeros<uint16_t>(Bz * W * Kw), Bz * W * Kw * 2);
+        L.lv = add(s->arena.zeros<uint16_t>(Bz * W * Dz), Bz * W * Dz * 2);
+        L.mk = add(s->arena.zeros<uint16_t>(Bz * C * Kw), Bz * C * Kw * 2);
+        L.mv = add(s->arena.zeros<uint16_t>(Bz * C * Dz), Bz * C * Dz * 2);
+        L.mtag = add(s->arena.zeros<int32_t>(Bz * C), Bz * C * 4);
+        L.mcount = add(s->arena.zeros<int32_t>(Bz), Bz * 4);
+        L.psum = add(s->arena.zeros<float>(Bz * Dz), Bz * Dz * 4);
+        L.pcnt = add(s->arena.zeros<int32_t>(Bz), Bz * 4);
+      } else if (kind == kAttn) {
         const size_t n = static_cast<size_t>(B) * c.attn_heads * c.window * c.attn_head_dim;
         L.k = s->arena.zeros<uint16_t>(n);
         L.v = s->arena.zeros<uint16_t>(n);
@@ -739,6 +871,7 @@ void reset_state(State& s) {
       check_hip(hipMemsetAsync(L.hist, 0, L.hist_bytes, s.stream), "reset");
     }
     if (L.ring) check_hip(hipMemsetAsync(L.ring, 0, L.ring_bytes, s.stream), "reset");
+    for (auto& pb : L.cmp_bufs) check_hip(hipMemsetAsync(pb.first, 0, pb.second, s.stream), "reset");
   }
   check_hip(hipMemsetAsync(s.pos, 0, sizeof(int32_t) * s.B, s.stream), "reset");
   check_hip(hipStreamSynchronize(s.stream), "reset");
@@ -763,6 +896,7 @@ void reset_rows(State& s, const int32_t* mask) {
     zero(L.S, L.s_bytes);
     zero(L.hist, L.hist_bytes);
     zero(L.ring, L.ring_bytes);
+    for (auto& pb : L.cmp_bufs) zero(pb.first, pb.second);
   }
   zero(s.pos, sizeof(int32_t) * s.B);
   std::vector<int32_t> host(s.B);
@@ -888,6 +1022,71 @@ const float* next_norm_of(const Model& m, int loop, int l, int loops) {
   return loop + 1 < loops ? m.layers[0].mix_norm : m.final_norm;
 }
 
+// ------------------------------------------------------------------ CSA / HCA
+// The compressed-memory mixers (model/layers/csa.py, hca.py).  Kernels and
+// their order are the Python engine's (HybridDecoder._cmp / _cmp_seq), so the
+// two engines agree bit for bit.  The mixer's output goes to `out` through
+// the epilogue `epi` (residual add into x, or a store into mHC's U).
+
+// Decode, one token per row at positions pos: q | k | v, the local window over
+// the ring (new key / value stored first), the compressor step and the commit
+// of completed blocks' summaries, the memory branch, out(local_out + remote_out).
+void cmp_decode(const Model& m, const Layer& L, LayerState& st, Buffers& b, int B,
+                const int32_t* pos, void* out, int epi, hipStream_t s) {
+  const Config& c = m.cfg;
+  const CmpShape cs = c.cmp(L.kind);
+  const int D = c.d_model, Kw = cs.kw(), N = 2 * Kw + D, C = c.cmp_slots;
+  const float scale = 1.0f / std::sqrt(static_cast<float>(cs.Dh));
+  linear(b.h, L.cmp_wqkv, b.cqkv, nullptr, B, N, D, kStoreBf16, s);
+  check_call(llmy_cmp_local_decode_bf16(b.cqkv, N, b.cqkv + Kw, b.cqkv + 2 * Kw, N, st.lk, st.lv,
+                                        pos, b.cloc, 2 * D, B, cs.H, cs.Dh, D, cs.W, scale, b.cws,
+                                        b.cws_bytes, s),
+             "llmy_cmp_local_decode_bf16");
+  check_call(llmy_cmp_pool_step_bf16(b.h, D, st.psum, st.pcnt, b.cmean, b.cemit, B, D, cs.ratio,
+                                     s),
+             "llmy_cmp_pool_step_bf16");
+  linear(b.cmean, L.cmp_wc, b.ckv, nullptr, B, Kw + D, D, kStoreBf16, s);
+  check_call(llmy_cmp_commit_bf16(b.ckv, Kw + D, b.cemit, pos, st.mk, st.mv, st.mtag, st.mcount,
+                                  B, C, Kw, D, s),
+             "llmy_cmp_commit_bf16");
+  check_call(llmy_cmp_memory_decode_bf16(b.cqkv, N, st.mk, st.mv, st.mtag, pos, b.cloc + D, 2 * D,
+                                         B, C, cs.H, cs.Dh, D, cs.top_k, scale, b.cws, b.cws_bytes,
+                                         s),
+             "llmy_cmp_memory_decode_bf16");
+  linear(b.cloc, L.cmp_wlr, b.cy, nullptr, B, D, 2 * D, kStoreBf16, s);
+  linear(b.cy, L.cmp_wout, out, nullptr, B, D, D, epi, s);
+}
+
+// Prefill of B fresh sequences of T tokens: the branches over all rows, the
+// block means and their summaries, then the state T decode steps leave.
+void cmp_prefill(const Model& m, const Layer& L, LayerState& st, Buffers& b, int B, int T,
+                 void* out, int epi, hipStream_t s) {
+  const Config& c = m.cfg;
+  const CmpShape cs = c.cmp(L.kind);
+  const int D = c.d_model, Kw = cs.kw(), N = 2 * Kw + D, C = c.cmp_slots, R = B * T;
+  const int n = T / cs.ratio;
+  const float scale = 1.0f / std::sqrt(static_cast<float>(cs.Dh));
+  linear(b.h, L.cmp_wqkv, b.cqkv, nullptr, R, N, D, kStoreBf16, s);
+  check_call(llmy_cmp_local_prefill_bf16(b.cqkv, N, b.cqkv + Kw, N, b.cqkv + 2 * Kw, N, b.cloc,
+                                         2 * D, B, T, cs.H, cs.Dh, D, cs.W, scale, b.cws,
+                                         b.cws_bytes, s),
+             "llmy_cmp_local_prefill_bf16");
+  check_call(llmy_cmp_pool_prefill_bf16(b.h, D, b.cmean, st.psum, st.pcnt, B, T, D, cs.ratio, s),
+             "llmy_cmp_pool_prefill_bf16");
+  if (n > 0) linear(b.cmean, L.cmp_wc, b.ckv, nullptr, B * n, Kw + D, D, kStoreBf16, s);
+  check_call(llmy_cmp_memory_prefill_bf16(b.cqkv, N, b.ckv, Kw + D, b.ckv + Kw, Kw + D,
+                                          b.cloc + D, 2 * D, B, T, n, cs.ratio, cs.H, cs.Dh, D,
+                                          cs.top_k, scale, b.cws, b.cws_bytes, s),
+             "llmy_cmp_memory_prefill_bf16");
+  check_call(llmy_cmp_memory_fill_bf16(b.ckv, Kw + D, st.mk, st.mv, st.mtag, st.mcount, B, n,
+                                       cs.ratio, C, Kw, D, s),
+             "llmy_cmp_memory_fill_bf16");
+  check_call(llmy_cmp_ring_fill_bf16(b.cqkv + Kw, N, st.lk, B, T, cs.W, Kw, s), "ring fill k");
+  check_call(llmy_cmp_ring_fill_bf16(b.cqkv + 2 * Kw, N, st.lv, B, T, cs.W, D, s), "ring fill v");
+  linear(b.cloc, L.cmp_wlr, b.cy, nullptr, R, D, 2 * D, kStoreBf16, s);
+  linear(b.cy, L.cmp_wout, out, nullptr, R, D, D, epi, s);
+}
+
 // ------------------------------------------------------------------ mHC
 // Multi-stream hyper-connections around each sublayer (model/model.py:119-126,
 // 177-264; model/layers/mhc.py:156-231).  The kernels and their order are the
@@ -989,6 +1188,8 @@ void decode_step_mhc(Model& m, State& s, int loops) {
                                                 st_),
                    "llmy_banded_attn_decode_bf16");
         linear(b.ao, L.wo, b.mU, nullptr, B, D, Hhd, kStoreF32, st_);
+      } else if (L.kind == kCsa || L.kind == kHca) {
+        cmp_decode(m, L, st, b, B, s.pos, b.mU, kStoreF32, st_);
       } else {
         mhc_clear_u(m, b, B, st_);
         const bool pp = b.proj_parts != nullptr;
@@ -1046,6 +1247,8 @@ void decode_step(Model& m, State& s, int loops) {
         } else {
           linear(b.ao, L.wo, b.x, nullptr, B, D, Hhd, kResidAdd, st_);
         }
+      } else if (L.kind == kCsa || L.kind == kHca) {
+        cmp_decode(m, L, st, b, B, s.pos, b.x, kResidAdd, st_);
       } else {
         const int HV = c.gdn_heads * c.dv;
         // the input projection as partial products, summed by the step kernel
@@ -1103,6 +1306,8 @@ void prefill_mhc(Model& m, State& s, Buffers& b, int T) {
                                            c.attn_head_dim, c.window, st_),
                    "llmy_kv_cache_fill_bf16");
         linear(b.ao, L.wo, b.mU, nullptr, R, D, Hhd, kStoreF32, st_);
+      } else if (L.kind == kCsa || L.kind == kHca) {
+        cmp_prefill(m, L, st, b, B, T, b.mU, kStoreF32, st_);
       } else {
         const int H = c.gdn_heads, HV = H * c.dv;
         mhc_clear_u(m, b, R, st_);
@@ -1186,6 +1391,8 @@ void prefill(Model& m, State& s, const int32_t* tokens, int T, bool tokens_on_de
                                            c.attn_head_dim, c.window, st_),
                    "llmy_kv_cache_fill_bf16");
         linear(b.ao, L.wo, b.x, nullptr, R, D, Hhd, kResidAdd, st_);
+      } else if (L.kind == kCsa || L.kind == kHca) {
+        cmp_prefill(m, L, st, b, B, T, b.x, kResidAdd, st_);
       } else {
         const int H = c.gdn_heads, HV = H * c.dv;
         linear(b.h, L.wproj, b.proj, nullptr, R, c.nproj16(), D, kStoreF32, st_);

@@ -282,3 +282,45 @@ def test_sampler_matches_oracle_rule(lib):
             assert tok == int(ref[0]), trial
             agree += 1
     assert agree >= 30
+
+
+def test_cmp_roundtrip(lib, tmp_path):
+    """CSA / HCA mixers under the reference's names (model/layers/csa.py:21-29,
+    hca.py:24-30; llmy_cuda/src/model.cpp:132-160): mixer.query / key / value /
+    local_out / out, remote_out (CSA) or global_out (HCA), compressor.key /
+    value; csa.* / hca.* keys with the reference defaults when absent
+    (llmy_cuda/include/config.h:41-51); the reference's "<kind>_moe" layout
+    entries."""
+    from dataclasses import replace
+    cfg = replace(TINY, layer_kinds=("csa", "gdn", "hca"), csa_heads=2, csa_head_dim=64,
+                  csa_window=8, csa_ratio=4, csa_top_k=5, hca_window=6, hca_ratio=8,
+                  hca_dense=False, hca_top_k=3, cmp_slots=32)
+    w = init_weights(cfg, seed=8)
+    path = tmp_path / "cmp.llmy"
+    save_llmy(path, cfg, w)
+    back_cfg, back = load_weights(path)
+    assert back_cfg == cfg
+    for key, t in w.items():
+        assert torch.equal(back[key], t), key
+    assert file_name(cfg, "L0.cmp_wro") == "recurrent_core.0.mixer.remote_out.weight"
+    assert file_name(cfg, "L2.cmp_wro") == "recurrent_core.2.mixer.global_out.weight"
+    assert file_name(cfg, "L2.cmp_wck") == "recurrent_core.2.mixer.compressor.key.weight"
+    assert file_name(cfg, "L0.cmp_wq") == "recurrent_core.0.mixer.query.weight"
+    st, desc = _describe(lib, path)
+    assert st == 0, lib.llmy_last_error()
+    names = {l.split()[0] for l in desc.split("--\n")[1].splitlines()}
+    for n in ("query", "key", "value", "local_out", "remote_out", "out", "compressor.key",
+              "compressor.value"):
+        assert f"recurrent_core.0.mixer.{n}.weight" in names
+    assert "recurrent_core.2.mixer.global_out.weight" in names
+    # the reference's layout spelling and defaults
+    text = config_text(cfg).replace("recurrent_layout=csa,gdn,hca",
+                                    "recurrent_layout=csa_moe,gdn_moe,hca_moe")
+    bare = "".join(l + "\n" for l in text.splitlines()
+                   if not l.startswith(("csa.", "hca.", "memory.")))
+    c0 = config_from_text(bare)
+    assert c0.layer_kinds == ("csa", "gdn", "hca")
+    assert (c0.csa_ratio, c0.csa_window, c0.csa_heads, c0.csa_head_dim, c0.csa_top_k) == \
+        (4, 128, 16, 128, 32)
+    assert (c0.hca_ratio, c0.hca_window, c0.hca_dense, c0.hca_top_k, c0.cmp_slots) == \
+        (32, 128, True, 32, 256)

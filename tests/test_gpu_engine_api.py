@@ -336,3 +336,46 @@ def test_context_router_matches_python_engine(lib, tmp_path):
         lib.llmy_state_free(s)
     finally:
         lib.llmy_free(m)
+
+
+@pytest.mark.parametrize("mhc", [1, 4])
+def test_cmp_matches_python_engine(lib, tmp_path, mhc):
+    """CSA and HCA mixers (model/layers/csa.py, hca.py; .llmy names of
+    llmy_cuda/src/model.cpp:132-160): the native engine's prefill, graph-replayed
+    decode (past the local window, across emitted summaries) and a row reset
+    equal the Python engine's bit for bit, single-stream and with 4 mHC streams."""
+    from dataclasses import replace
+    from hybrid_llm_amd.engine import HybridDecoder
+    cfg = replace(C1, layer_kinds=("csa", "gdn", "hca", "attn"), csa_heads=4, csa_head_dim=64,
+                  csa_window=16, csa_ratio=4, csa_top_k=3, hca_window=12, hca_ratio=8,
+                  hca_dense=mhc == 1, hca_top_k=2, cmp_slots=64, mhc_streams=mhc,
+                  mhc_gating_init=0.5)
+    w = init_weights(cfg, seed=17)
+    path = tmp_path / "cmp.llmy"
+    save_llmy(path, cfg, w)
+    B, T = 3, 21
+    prompt = torch.randint(0, cfg.vocab, (B, T), generator=torch.Generator().manual_seed(18),
+                           dtype=torch.int32)
+    print(f"[engine-api] CSA/HCA (mhc {mhc}): prefill 21 + decode 14 with a reset, B=3",
+          flush=True)
+    m = lib.llmy_load(str(path).encode())
+    assert m, lib.llmy_last_error()
+    try:
+        s = lib.llmy_state_new_batch(m, B)
+        assert s
+        out = torch.zeros(B, cfg.vocab, device="cuda")
+        assert lib.llmy_prefill_batch(m, s, prompt.cuda().data_ptr(), T, out.data_ptr()) == 0
+        py = HybridDecoder(cfg, w, B)
+        assert torch.equal(out, py.prefill(prompt.cuda()))
+        mask = torch.tensor([0, 1, 0], dtype=torch.int32)
+        nxt = torch.zeros(B, dtype=torch.int32)
+        for i in range(14):
+            assert lib.llmy_greedy_tokens(s, nxt.data_ptr()) == 0
+            if i == 5:
+                assert lib.llmy_state_reset_rows(s, mask.data_ptr()) == 0
+                py.reset_rows(mask.cuda())
+            assert lib.llmy_decode_batch(m, s, nxt.data_ptr(), None, 0, out.data_ptr()) == 0
+            assert torch.equal(out, py.step(nxt.cuda())), i
+        lib.llmy_state_free(s)
+    finally:
+        lib.llmy_free(m)
