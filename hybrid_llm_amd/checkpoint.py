@@ -68,7 +68,15 @@ _BLOCK = {"mix_norm": "mixer_norm.weight", "ffn_norm": "ffn_norm.weight",
           "ctx_ln_b": "moe.router.latent_memory.norm.bias",
           "ctx_local_out": "moe.router.local_context_out.weight",
           "ctx_out": "moe.router.context_out.weight",
-          "ctx_gate": "moe.router.route_gate"}
+          "ctx_gate": "moe.router.route_gate",
+          # the router's global branch (context_router.py:24; mla_memory.py:55-63)
+          # and the HCA block's summary latents (model.py:117; mla_memory.py:17-21)
+          "ctx_q": "moe.router.latent_attention.q.weight",
+          "ctx_k": "moe.router.latent_attention.k.weight",
+          "ctx_v": "moe.router.latent_attention.v.weight",
+          "ctx_o": "moe.router.latent_attention.o.weight",
+          "hca_lat_down": "hca_latent.down.weight", "hca_lat_ln_w": "hca_latent.norm.weight",
+          "hca_lat_ln_b": "hca_latent.norm.bias"}
 
 
 # mHC parameters (model/layers/mhc.py:63-84; the names llmy_cuda/src/model.cpp:34-63
@@ -123,6 +131,7 @@ def config_text(cfg: HybridConfig) -> str:
         "moe.expert_hidden": cfg.expert_hidden, "moe.shared_experts": cfg.shared_experts,
         "router.context_aware": int(cfg.context_router),
         "router.local_context": cfg.router_context, "mla.latent_dim": cfg.latent_dim,
+        "router.query_heads": cfg.router_heads, "router.query_head_dim": cfg.router_head_dim,
         "rms_norm_eps": repr(float(cfg.eps)),
         "csa.temporal_compression": cfg.csa_ratio, "csa.local_window": cfg.csa_window,
         "csa.index_heads": cfg.csa_heads, "csa.index_head_dim": cfg.csa_head_dim,
@@ -154,6 +163,8 @@ def config_from_text(text: str) -> HybridConfig:
         context_router=_parse_bool(kv.get("router.context_aware", "1")),
         router_context=int(kv.get("router.local_context", 128)),
         latent_dim=int(kv.get("mla.latent_dim", 256)),
+        router_heads=int(kv.get("router.query_heads", 4)),
+        router_head_dim=int(kv.get("router.query_head_dim", 64)),
         # CSA / HCA keys with the reference defaults (llmy_cuda/include/config.h:41-51)
         csa_ratio=int(kv.get("csa.temporal_compression", 4)),
         csa_window=int(kv.get("csa.local_window", 128)),

@@ -46,6 +46,11 @@ class HybridConfig:
     latent_dim: int = 256
     router_context: int = 128
     route_gate_init: float = -4.59512  # context_router.py:25
+    # the router's global branch (context_router.py:66-68,126-127): latent
+    # attention with router_heads heads of router_head_dim over the HCA block's
+    # summary latents (hca_latent: mla_memory.py:9-27), on HCA layers
+    router_heads: int = 4      # model/config.py:48
+    router_head_dim: int = 64  # model/config.py:49
     # multi-stream hyper-connections (model/layers/mhc.py:156-231; model.py:84-86,
     # 119-126,389-421,442-444,699-700): mhc_streams residual streams per token,
     # read before and written after every mixer and MoE sublayer through
@@ -171,6 +176,17 @@ def weight_shapes(cfg: HybridConfig) -> list[tuple[str, tuple[int, ...], str]]:
     if Sm > 1:
         out.append(("mhc_collapse", (D, Sm * D), "collapse"))
     out.append(("final_norm", (D,), "ones"))
+    if cfg.context_router:
+        # the router's latent attention (every router has one) and the HCA
+        # blocks' summary latents, drawn after every other weight
+        L, HQ = cfg.latent_dim, cfg.router_heads * cfg.router_head_dim
+        for l, kind in enumerate(cfg.layer_kinds):
+            p = f"L{l}."
+            out += [(p + "ctx_q", (HQ, D), "normal"), (p + "ctx_k", (HQ, L), "normal"),
+                    (p + "ctx_v", (HQ, L), "normal"), (p + "ctx_o", (D, HQ), "normal")]
+            if kind == "hca":
+                out += [(p + "hca_lat_down", (L, D), "normal"),
+                        (p + "hca_lat_ln_w", (L,), "ones"), (p + "hca_lat_ln_b", (L,), "zeros")]
     return out
 
 
@@ -178,7 +194,7 @@ def weight_shapes(cfg: HybridConfig) -> list[tuple[str, tuple[int, ...], str]]:
 FP32_PARAMS = ("mix_norm", "ffn_norm", "router_norm", "final_norm", "w_router", "bb", "conv",
                "decay", "ctx_down", "ctx_ln_w", "ctx_ln_b", "ctx_gate", "stream_seed",
                "mhc_map_norm", "mhc_pre_bias", "mhc_post_bias", "mhc_res_bias", "mhc_alpha",
-               "mhc_gating", "mhc_scale", "mhc_ln_w", "mhc_ln_b")
+               "mhc_gating", "mhc_scale", "mhc_ln_w", "mhc_ln_b", "hca_lat_ln_w", "hca_lat_ln_b")
 
 
 def is_fp32_param(name: str) -> bool:

@@ -230,3 +230,135 @@ extern "C" int32_t llmy_router_context_logits_f32(const float* local, const floa
   }
   return launch_status();
 }
+
+// ---------------------------------------------------------------- global branch
+// The context-aware router's global branch (context_router.py:66-68,126-127;
+// mla_memory.py:52-90; the native twin router_hca_latent_attention,
+// llmy_cuda/src/model.cpp:972-1062): multi-head attention of the router's
+// query over latents of the HCA block's compressed summaries, whose keys and
+// values the caller projects once per summary.
+
+namespace llmy {
+
+// out[r] = bf16(LayerNorm(x[r]) * w + b), biased variance (nn.LayerNorm).
+__global__ __launch_bounds__(256) void layernorm_kernel(const float* __restrict__ x,
+                                                        const float* __restrict__ w,
+                                                        const float* __restrict__ bias,
+                                                        uint16_t* __restrict__ out, int L,
+                                                        float eps) {
+  __shared__ float red[4];
+  const int r = blockIdx.x;
+  const float* xr = x + static_cast<int64_t>(r) * L;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  auto block_sum = [&](float v) {
+    v = wave_sum(v);
+    __syncthreads();
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    return (red[0] + red[1]) + (red[2] + red[3]);
+  };
+  float s = 0.f;
+  for (int i = threadIdx.x; i < L; i += 256) s += xr[i];
+  const float mean = block_sum(s) / static_cast<float>(L);
+  float q = 0.f;
+  for (int i = threadIdx.x; i < L; i += 256) {
+    const float d = xr[i] - mean;
+    q += d * d;
+  }
+  const float inv = 1.0f / sqrtf(block_sum(q) / static_cast<float>(L) + eps);
+  for (int i = threadIdx.x; i < L; i += 256)
+    out[static_cast<int64_t>(r) * L + i] = f2bf((xr[i] - mean) * inv * w[i] + bias[i]);
+}
+
+// Workgroup = (query row, head).  Query row r = b * T + t sits at position
+// pos[b] (pos NULL: t); slot j of row b is visible when 1 <= tag <= that + 1.
+__global__ __launch_bounds__(256) void latent_attn_kernel(
+    const uint16_t* __restrict__ q, int64_t q_ld, const uint16_t* __restrict__ keys,
+    const uint16_t* __restrict__ vals, const int32_t* __restrict__ tag,
+    const int32_t* __restrict__ pos, uint16_t* __restrict__ out, int64_t out_ld, int T, int C,
+    int heads, int hd, float scale_log2) {
+  extern __shared__ float sc[];
+  __shared__ float red[4];
+  const int h = blockIdx.x % heads;
+  const int r = blockIdx.x / heads;
+  const int b = r / T;
+  const int qp = pos ? pos[b] : r - b * T;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int W = heads * hd;
+  const uint16_t* qh = q + static_cast<int64_t>(r) * q_ld + h * hd;
+  for (int j = threadIdx.x; j < C; j += 256) {
+    const int tg = tag[static_cast<int64_t>(b) * C + j];
+    float s = -INFINITY;
+    if (tg >= 1 && tg <= qp + 1) {
+      const uint16_t* kr = keys + (static_cast<int64_t>(b) * C + j) * W + h * hd;
+      float dot = 0.f;
+      for (int e = 0; e < hd; e += 8) {
+        float a[8], c[8];
+        unpack8(*reinterpret_cast<const uint4*>(qh + e), a);
+        unpack8(*reinterpret_cast<const uint4*>(kr + e), c);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) dot = fmaf(a[i], c[i], dot);
+      }
+      s = dot * scale_log2;
+    }
+    sc[j] = s;
+  }
+  float m = -INFINITY;
+  for (int j = threadIdx.x; j < C; j += 256) m = fmaxf(m, sc[j]);
+  m = wave_max(m);
+  __syncthreads();
+  if (lane == 0) red[wave] = m;
+  __syncthreads();
+  m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  float sum = 0.f;
+  if (m != -INFINITY)
+    for (int j = threadIdx.x; j < C; j += 256) sum += exp2_fast(sc[j] - m);
+  sum = wave_sum(sum);
+  __syncthreads();
+  if (lane == 0) red[wave] = sum;
+  __syncthreads();
+  sum = (red[0] + red[1]) + (red[2] + red[3]);
+  const float inv = (m != -INFINITY && sum > 0.f) ? 1.0f / sum : 0.f;
+  for (int j = threadIdx.x; j < C; j += 256) sc[j] = inv > 0.f ? exp2_fast(sc[j] - m) * inv : 0.f;
+  __syncthreads();
+  for (int d = threadIdx.x; d < hd; d += 256) {
+    float acc = 0.f;
+    for (int j = 0; j < C; ++j) {
+      const float p = sc[j];
+      if (p == 0.f) continue;
+      acc = fmaf(p, bf2f(vals[(static_cast<int64_t>(b) * C + j) * W + h * hd + d]), acc);
+    }
+    out[static_cast<int64_t>(r) * out_ld + h * hd + d] = f2bf(acc);
+  }
+}
+
+}  // namespace llmy
+
+extern "C" int32_t llmy_layernorm_f32_bf16(const float* x, const float* w, const float* b,
+                                           llmy_bf16* out, int32_t rows, int32_t L, float eps,
+                                           void* stream) {
+  LLMY_REQUIRE(rows >= 0 && L > 0);
+  if (rows == 0) return 0;
+  LLMY_REQUIRE(x && w && b && out);
+  hipLaunchKernelGGL(layernorm_kernel, dim3(rows), dim3(256), 0, as_stream(stream), x, w, b,
+                     out, L, eps);
+  return launch_status();
+}
+
+extern "C" int32_t llmy_latent_attn_bf16(const llmy_bf16* q, int64_t q_ld, const llmy_bf16* keys,
+                                         const llmy_bf16* vals, const int32_t* tag,
+                                         const int32_t* pos, llmy_bf16* out, int64_t out_ld,
+                                         int32_t B, int32_t T, int32_t C, int32_t heads,
+                                         int32_t head_dim, float scale, void* stream) {
+  LLMY_REQUIRE(B >= 0 && T >= 1 && C >= 1 && C <= 16384 && heads > 0 && head_dim > 0 &&
+               head_dim % 8 == 0);
+  if (B == 0) return 0;
+  const int64_t W = static_cast<int64_t>(heads) * head_dim;
+  LLMY_REQUIRE(q && keys && vals && tag && out && q_ld >= W && q_ld % 8 == 0 && out_ld >= W);
+  LLMY_REQUIRE(aligned(q, 16) && aligned(keys, 16));
+  LLMY_REQUIRE(static_cast<int64_t>(B) * T * heads < (1ll << 31));
+  hipLaunchKernelGGL(latent_attn_kernel, dim3(B * T * heads), dim3(256),
+                     static_cast<size_t>(C) * 4, as_stream(stream), q, q_ld, keys, vals, tag, pos,
+                     out, out_ld, T, C, heads, head_dim, scale * 1.4426950408889634f);
+  return launch_status();
+}

@@ -188,6 +188,10 @@ struct Config {
   // router.local_context, mla.latent_dim (llmy_cuda/include/config.h:60-66)
   bool ctx = false;
   int ctx_window = 128, latent = 256;
+  // the router's global branch on HCA blocks: latent attention with
+  // router.query_heads x router.query_head_dim (llmy_cuda/include/config.h)
+  int router_heads = 4, router_head_dim = 64;
+  int hq() const { return router_heads * router_head_dim; }
   // multi-stream hyper-connections: streams per token (mhc.streams when
   // mhc.enabled; 1 = the single residual stream) and Sinkhorn iterations
   int mhc = 1, mhc_iters = 20;
@@ -292,6 +296,8 @@ Config config_from(const std::string& text) {
   c.ctx = cfg_bool(kv, "router.context_aware", true);
   c.ctx_window = cfg_int(kv, "router.local_context", 128, false);
   c.latent = cfg_int(kv, "mla.latent_dim", 256, false);
+  c.router_heads = cfg_int(kv, "router.query_heads", 4, false);
+  c.router_head_dim = cfg_int(kv, "router.query_head_dim", 64, false);
   c.csa_ratio = cfg_int(kv, "csa.temporal_compression", 4, false);
   c.csa_window = cfg_int(kv, "csa.local_window", 128, false);
   c.csa_heads = cfg_int(kv, "csa.index_heads", 16, false);
@@ -311,6 +317,10 @@ Config config_from(const std::string& text) {
   if (c.ctx && (c.latent % 256 != 0 || c.latent > 512 || c.d_model > 1024 || c.ctx_window < 1))
     throw std::runtime_error("context-aware router needs mla.latent_dim in {256, 512}, "
                              "d_model <= 1024, router.local_context >= 1");
+  if (c.ctx && std::count(c.kinds.begin(), c.kinds.end(), kHca) > 0 &&
+      (c.router_heads < 1 || c.router_head_dim % 8 != 0 || c.hq() % 256 != 0))
+    throw std::runtime_error("the router's latent attention needs router.query_heads * "
+                             "router.query_head_dim % 256 == 0 and head_dim % 8 == 0");
   if (c.mhc > 1 && (c.ctx || c.d_model > 4096 || c.mhc_iters < 0))
     throw std::runtime_error("mHC needs d_model <= 4096 and the plain router");
   // compressed-memory mixers: head widths the decode scoring splits over
@@ -409,6 +419,11 @@ struct Layer {
   // CSA / HCA (packed bf16): query | key | value [2 Kw + D, D], the
   // compressor's key | value [Kw + D, D], [local_out | remote_out] [D, 2 D], out [D, D]
   uint16_t *cmp_wqkv = nullptr, *cmp_wc = nullptr, *cmp_wlr = nullptr, *cmp_wout = nullptr;
+  // the context router's global branch (HCA blocks): hca_latent down [L, D]
+  // (packed) + LayerNorm (fp32), latent attention q [HQ, D], k | v [2 HQ, L],
+  // o [D, HQ] (packed)
+  uint16_t *hca_lat_down = nullptr, *ctx_q = nullptr, *ctx_kv = nullptr, *ctx_o = nullptr;
+  float *hca_lat_ln_w = nullptr, *hca_lat_ln_b = nullptr;
 };
 
 struct Model {
@@ -539,6 +554,20 @@ std::unique_ptr<Model> load_model(const char* path) {
       L.ctx_local_out = m->upload_packed(mat_bf16("moe.router.local_context_out.weight", {D, Lc}),
                                          1, D, Lc);
       L.ctx_out = m->upload_packed(mat_bf16("moe.router.context_out.weight", {D, D}), 1, D, D);
+      if (L.kind == kHca) {  // model.py:117, context_router.py:24 (model.cpp:98-104,234)
+        const int HQ = c.hq();
+        L.hca_lat_down = m->upload_packed(mat_bf16("hca_latent.down.weight", {Lc, D}), 1, Lc, D);
+        L.hca_lat_ln_w = vec_f32("hca_latent.norm.weight", {Lc});
+        L.hca_lat_ln_b = vec_f32("hca_latent.norm.bias", {Lc});
+        L.ctx_q = m->upload_packed(mat_bf16("moe.router.latent_attention.q.weight", {HQ, D}), 1,
+                                   HQ, D);
+        L.ctx_kv = m->upload_packed(
+            concat_rows({mat_bf16("moe.router.latent_attention.k.weight", {HQ, Lc}),
+                         mat_bf16("moe.router.latent_attention.v.weight", {HQ, Lc})}, 0),
+            1, 2 * HQ, Lc);
+        L.ctx_o = m->upload_packed(mat_bf16("moe.router.latent_attention.o.weight", {D, HQ}), 1,
+                                   D, HQ);
+      }
     }
     if (L.kind == kCsa || L.kind == kHca) {
       // model/layers/csa.py:21-29, hca.py:24-30 (names of llmy_cuda/src/model.cpp:139-160)
@@ -651,6 +680,10 @@ struct LayerState {
   uint16_t *lk = nullptr, *lv = nullptr, *mk = nullptr, *mv = nullptr;
   int32_t *mtag = nullptr, *mcount = nullptr, *pcnt = nullptr;
   float* psum = nullptr;
+  // HCA with the context router: the router's keys / values [B, C, HQ] of each
+  // summary's latent, their tags and count (kept as the memory's)
+  uint16_t *rk = nullptr, *rv = nullptr;
+  int32_t *rtag = nullptr, *rcount = nullptr;
   std::vector<std::pair<void*, size_t>> cmp_bufs;  // every CSA / HCA buffer and its bytes
 };
 
@@ -671,6 +704,12 @@ struct Buffers {  // activations for `rows` token rows
   // window means [rows, L] and local_context_out [rows, D] bf16
   float *c_local = nullptr, *c_lat = nullptr, *c_c = nullptr, *c_logits = nullptr;
   uint16_t *c_ctx = nullptr, *c_d = nullptr;
+  // the global branch (HCA): summary values [rows, D] / latents [rows, L] fp32 and
+  // bf16 / router k | v [rows, 2 HQ]; local in bf16, q and attention [rows, HQ],
+  // local_context_out + o in fp32 [rows, D]
+  uint16_t *g_val = nullptr, *g_lat = nullptr, *g_kvr = nullptr, *g_lq = nullptr,
+           *g_q = nullptr, *g_att = nullptr;
+  float *g_lat_raw = nullptr, *g_t = nullptr;
   // mHC: streams X [rows, S, D], their bf16 copy [rows, S D] (GEMM operand),
   // map logits [rows, n16], maps [rows, S + S^2], a sublayer's output U
   // [rows, D]; all-ones row mask (clearing U) and identity route positions
@@ -746,6 +785,17 @@ void alloc_buffers(const Config& c, int rows, int B, int T, Buffers& b) {
     b.c_logits = b.arena.zeros<float>(static_cast<size_t>(rows) * c.experts);
     b.c_ctx = b.arena.zeros<uint16_t>(static_cast<size_t>(rows) * c.latent);
     b.c_d = b.arena.zeros<uint16_t>(static_cast<size_t>(rows) * D);
+    if (c.has(kHca)) {
+      const size_t R = rows, HQ = c.hq(), Lc = c.latent;
+      b.g_val = b.arena.zeros<uint16_t>(R * D);
+      b.g_lat_raw = b.arena.zeros<float>(R * Lc);
+      b.g_lat = b.arena.zeros<uint16_t>(R * Lc);
+      b.g_kvr = b.arena.zeros<uint16_t>(R * 2 * HQ);
+      b.g_lq = b.arena.zeros<uint16_t>(R * D);
+      b.g_q = b.arena.zeros<uint16_t>(R * HQ);
+      b.g_att = b.arena.zeros<uint16_t>(R * HQ);
+      b.g_t = b.arena.zeros<float>(R * D);
+    }
   }
   if (c.mhc > 1) {
     const size_t S = c.mhc;
@@ -830,6 +880,13 @@ std::unique_ptr<State> new_state(Model* m, int B) {
         L.mcount = add(s->arena.zeros<int32_t>(Bz), Bz * 4);
         L.psum = add(s->arena.zeros<float>(Bz * Dz), Bz * Dz * 4);
         L.pcnt = add(s->arena.zeros<int32_t>(Bz), Bz * 4);
+        if (kind == kHca && c.ctx) {
+          const size_t HQ = c.hq();
+          L.rk = add(s->arena.zeros<uint16_t>(Bz * C * HQ), Bz * C * HQ * 2);
+          L.rv = add(s->arena.zeros<uint16_t>(Bz * C * HQ), Bz * C * HQ * 2);
+          L.rtag = add(s->arena.zeros<int32_t>(Bz * C), Bz * C * 4);
+          L.rcount = add(s->arena.zeros<int32_t>(Bz), Bz * 4);
+        }
       } else if (kind == kAttn) {
         const size_t n = static_cast<size_t>(B) * c.attn_heads * c.window * c.attn_head_dim;
         L.k = s->arena.zeros<uint16_t>(n);
@@ -941,7 +998,8 @@ bool fused_route(const Config& c, int rows) { return router_fusable(c) && rows *
 // `ring` is the layer's latent window state.
 void moe_block(const Model& m, const Layer& L, Buffers& b, int rows, const float* next_norm,
                bool sequence, hipStream_t st, float* ring, const int32_t* pos, int nseq,
-               const float* parts = nullptr, int nparts = 0, const float* gate = nullptr) {
+               const float* parts = nullptr, int nparts = 0, const float* gate = nullptr,
+               const LayerState* ls = nullptr) {
   const Config& c = m.cfg;
   const int D = c.d_model, E = c.experts, k = c.top_k, Hf = c.hidden;
   const int kx = c.routes(), EX = c.all_experts();
@@ -968,7 +1026,26 @@ void moe_block(const Model& m, const Layer& L, Buffers& b, int rows, const float
     check_call(llmy_router_context_window(b.c_lat, ring, pos, b.c_ctx, nseq, rows / nseq,
                                           c.ctx_window, Lc, st),
                "llmy_router_context_window");
-    linear(b.c_ctx, L.ctx_local_out, b.c_d, nullptr, rows, D, Lc, kStoreBf16, st);
+    if (ls && ls->rk) {
+      // the global branch: local_context_out(ctx) + o(latent attention of
+      // q(local) over the block's summaries), rounded once to bf16
+      const int HQ = c.hq();
+      linear(b.c_ctx, L.ctx_local_out, b.g_t, nullptr, rows, D, Lc, kStoreF32, st);
+      check_call(llmy_f32_to_bf16(b.c_local, b.g_lq, static_cast<int64_t>(rows) * D, st),
+                 "llmy_f32_to_bf16");
+      linear(b.g_lq, L.ctx_q, b.g_q, nullptr, rows, HQ, D, kStoreBf16, st);
+      check_call(llmy_latent_attn_bf16(b.g_q, HQ, ls->rk, ls->rv, ls->rtag, pos, b.g_att, HQ, nseq,
+                                       rows / nseq, c.cmp_slots, c.router_heads,
+                                       c.router_head_dim,
+                                       1.0f / std::sqrt(static_cast<float>(c.router_head_dim)),
+                                       st),
+                 "llmy_latent_attn_bf16");
+      linear(b.g_att, L.ctx_o, b.g_t, nullptr, rows, D, HQ, kResidAdd, st);
+      check_call(llmy_f32_to_bf16(b.g_t, b.c_d, static_cast<int64_t>(rows) * D, st),
+                 "llmy_f32_to_bf16");
+    } else {
+      linear(b.c_ctx, L.ctx_local_out, b.c_d, nullptr, rows, D, Lc, kStoreBf16, st);
+    }
     linear(b.c_d, L.ctx_out, b.c_c, nullptr, rows, D, D, kStoreF32, st);
     check_call(llmy_router_context_logits_f32(b.c_local, b.c_c, L.ctx_gate, L.w_router,
                                               b.c_logits, rows, D, E, st),
@@ -1028,6 +1105,21 @@ const float* next_norm_of(const Model& m, int loop, int l, int loops) {
 // two engines agree bit for bit.  The mixer's output goes to `out` through
 // the epilogue `epi` (residual add into x, or a store into mHC's U).
 
+// The router's [k | v] of `n` summary values (rows of kv at kv_ld, value part
+// at column Kw) into b.g_kvr: copied dense, LayerNorm(down . value) (hca_latent,
+// eps 1e-5), then the latent attention's k | v (model.py:318-334).
+void router_summary_kv(const Model& m, const Layer& L, Buffers& b, const uint16_t* vals,
+                       int64_t vals_ld, int n, hipStream_t s) {
+  const Config& c = m.cfg;
+  const int D = c.d_model, Lc = c.latent;
+  check_call(llmy_cmp_ring_fill_bf16(vals, vals_ld, b.g_val, n, 1, 1, D, s), "summary values");
+  linear(b.g_val, L.hca_lat_down, b.g_lat_raw, nullptr, n, Lc, D, kStoreF32, s);
+  check_call(llmy_layernorm_f32_bf16(b.g_lat_raw, L.hca_lat_ln_w, L.hca_lat_ln_b, b.g_lat, n, Lc,
+                                     1e-5f, s),
+             "llmy_layernorm_f32_bf16");
+  linear(b.g_lat, L.ctx_kv, b.g_kvr, nullptr, n, 2 * c.hq(), Lc, kStoreBf16, s);
+}
+
 // Decode, one token per row at positions pos: q | k | v, the local window over
 // the ring (new key / value stored first), the compressor step and the commit
 // of completed blocks' summaries, the memory branch, out(local_out + remote_out).
@@ -1049,6 +1141,12 @@ void cmp_decode(const Model& m, const Layer& L, LayerState& st, Buffers& b, int 
   check_call(llmy_cmp_commit_bf16(b.ckv, Kw + D, b.cemit, pos, st.mk, st.mv, st.mtag, st.mcount,
                                   B, C, Kw, D, s),
              "llmy_cmp_commit_bf16");
+  if (st.rk) {
+    router_summary_kv(m, L, b, b.ckv + Kw, Kw + D, B, s);
+    check_call(llmy_cmp_commit_bf16(b.g_kvr, 2 * c.hq(), b.cemit, pos, st.rk, st.rv, st.rtag,
+                                    st.rcount, B, C, c.hq(), c.hq(), s),
+               "llmy_cmp_commit_bf16 (router)");
+  }
   check_call(llmy_cmp_memory_decode_bf16(b.cqkv, N, st.mk, st.mv, st.mtag, pos, b.cloc + D, 2 * D,
                                          B, C, cs.H, cs.Dh, D, cs.top_k, scale, b.cws, b.cws_bytes,
                                          s),
@@ -1081,6 +1179,12 @@ void cmp_prefill(const Model& m, const Layer& L, LayerState& st, Buffers& b, int
   check_call(llmy_cmp_memory_fill_bf16(b.ckv, Kw + D, st.mk, st.mv, st.mtag, st.mcount, B, n,
                                        cs.ratio, C, Kw, D, s),
              "llmy_cmp_memory_fill_bf16");
+  if (st.rk && n > 0) {
+    router_summary_kv(m, L, b, b.ckv + Kw, Kw + D, B * n, s);
+    check_call(llmy_cmp_memory_fill_bf16(b.g_kvr, 2 * c.hq(), st.rk, st.rv, st.rtag, st.rcount, B,
+                                         n, cs.ratio, C, c.hq(), c.hq(), s),
+               "llmy_cmp_memory_fill_bf16 (router)");
+  }
   check_call(llmy_cmp_ring_fill_bf16(b.cqkv + Kw, N, st.lk, B, T, cs.W, Kw, s), "ring fill k");
   check_call(llmy_cmp_ring_fill_bf16(b.cqkv + 2 * Kw, N, st.lv, B, T, cs.W, D, s), "ring fill v");
   linear(b.cloc, L.cmp_wlr, b.cy, nullptr, R, D, 2 * D, kStoreBf16, s);
@@ -1269,7 +1373,7 @@ void decode_step(Model& m, State& s, int loops) {
         }
       }
       moe_block(m, L, b, B, next_norm_of(m, loop, l, loops), false, st_, st.ring, s.pos, B,
-                b.parts, nparts, gate);
+                b.parts, nparts, gate, &st);
     }
   }
   linear(b.h, m.lm_head, s.logits, nullptr, B, c.vocab, D, kStoreF32, st_);
@@ -1409,7 +1513,8 @@ void prefill(Model& m, State& s, const int32_t* tokens, int T, bool tokens_on_de
                    "llmy_gdn_conv_gate_prefill");
         linear(b.go, L.wout, b.x, b.cg, R, D, HV, kResidGated, st_);
       }
-      moe_block(m, L, b, R, next_norm_of(m, loop, l, loops), true, st_, st.ring, nullptr, B);
+      moe_block(m, L, b, R, next_norm_of(m, loop, l, loops), true, st_, st.ring, nullptr, B,
+                nullptr, 0, nullptr, &st);
     }
   }
   // last position of each sequence -> the decode buffer, then the LM head

@@ -88,6 +88,12 @@ class HybridDecoder:
                 for n in ("ctx_down", "ctx_ln_w", "ctx_ln_b", "ctx_gate", "ctx_local_out",
                           "ctx_out"):
                     self.w[p + n] = up(p + n)
+                if kind == "hca":
+                    # the global branch: the block's summary latents (hca_latent)
+                    # and the router's latent attention; k | v in one projection
+                    for n in ("hca_lat_down", "hca_lat_ln_w", "hca_lat_ln_b", "ctx_q", "ctx_o"):
+                        self.w[p + n] = up(p + n)
+                    self.w[p + "ctx_kv"] = torch.cat([up(p + "ctx_k"), up(p + "ctx_v")], 0)
             gate_up = torch.cat([up(p + "w_gate"), up(p + "w_up")], 1)
             down = up(p + "w_down")
             if cfg.shared_experts > 0:
@@ -123,7 +129,7 @@ class HybridDecoder:
             if name.split(".")[-1] in ("wqkv", "wo", "wproj", "wout", "w_gate_up", "w_down",
                                        "ctx_local_out", "ctx_out", "mhc_theta",
                                        "mhc_collapse", "cmp_wqkv", "cmp_wc", "cmp_wlr",
-                                       "cmp_wout"):
+                                       "cmp_wout", "hca_lat_down", "ctx_q", "ctx_kv", "ctx_o"):
                 self.w[name] = ops.pack_weights(self.w[name])
         self.w["lm_head"] = ops.pack_weights(self.w["embed"])
 
@@ -153,6 +159,15 @@ class HybridDecoder:
                         "mcount": torch.zeros(B, dtype=torch.int32, device=dev),
                         "psum": torch.zeros(B, D, dtype=torch.float32, device=dev),
                         "pcnt": torch.zeros(B, dtype=torch.int32, device=dev)}
+                    if kind == "hca" and cfg.context_router:
+                        # the router's keys / values of each summary's latent,
+                        # slots and tags as the memory's
+                        HQ = cfg.router_heads * cfg.router_head_dim
+                        self.state[(loop, l)].update({
+                            "rk": torch.zeros(B, C, HQ, dtype=bf, device=dev),
+                            "rv": torch.zeros(B, C, HQ, dtype=bf, device=dev),
+                            "rtag": torch.zeros(B, C, dtype=torch.int32, device=dev),
+                            "rcount": torch.zeros(B, dtype=torch.int32, device=dev)})
                 else:
                     self.state[(loop, l)] = {
                         "S": torch.zeros(B, cfg.gdn_heads, cfg.gdn_dk, cfg.gdn_dv,
@@ -235,6 +250,19 @@ class HybridDecoder:
                             "ctx_c": torch.zeros(B, D, dtype=f32, device=dev),
                             "logits": torch.zeros(B, E, dtype=f32, device=dev),
                             "idx": self.buf["idx"], "gates": self.buf["gates"]}
+            if "hca" in cfg.layer_kinds:
+                HQ = cfg.router_heads * cfg.router_head_dim
+                if HQ % 256 or cfg.router_head_dim % 8:
+                    raise ValueError("the router's latent attention needs heads * head_dim % 256 "
+                                     "== 0 and head_dim % 8 == 0")
+                self.ctx_buf.update({"ctx_t": torch.zeros(B, D, dtype=f32, device=dev),
+                                     "lq": torch.zeros(B, D, dtype=bf, device=dev),
+                                     "gq": torch.zeros(B, HQ, dtype=bf, device=dev),
+                                     "gattn": torch.zeros(B, HQ, dtype=bf, device=dev)})
+                self.buf.update({"cval": torch.zeros(B, 1, D, dtype=bf, device=dev),
+                                 "clat_raw": torch.zeros(B, Lc, dtype=f32, device=dev),
+                                 "clat": torch.zeros(B, Lc, dtype=bf, device=dev),
+                                 "ckvr": torch.zeros(B, 2 * HQ, dtype=bf, device=dev)})
         # Mixer output projections (attention o, GDN out) as per-K-block
         # partial products that the fused router folds into the residual: a
         # workgroup then reads a 256-wide slice of the activations instead of
@@ -347,12 +375,38 @@ class HybridDecoder:
         ckv = b["ckv_" + kind]
         ops.linear(b["cmean"], w[p + "cmp_wc"], out=ckv, layout=ops.LAYOUT_PACKED)
         ops.cmp_commit(ckv, b["cemit"], self.pos, st["mk"], st["mv"], st["mtag"], st["mcount"])
+        if "rk" in st:
+            # the router's keys / values of the new summary's latent, committed
+            # with the same flags (the summary values copied to a dense operand)
+            ops.cmp_ring_fill(ckv[:, Kw:], self.B, 1, b["cval"])
+            self._router_summary_kv(p, b["cval"].view(self.B, D), b["clat_raw"], b["clat"],
+                                    b["ckvr"])
+            ops.cmp_commit(b["ckvr"], b["cemit"], self.pos, st["rk"], st["rv"], st["rtag"],
+                           st["rcount"])
         ops.cmp_memory_decode(q, st["mk"], st["mv"], st["mtag"], self.pos, H, Dh, cs["top_k"],
                               out=loc[:, D:], workspace=b["cws"])
         ops.linear(loc, w[p + "cmp_wlr"], out=b["cy"], layout=ops.LAYOUT_PACKED)
         ops.linear(b["cy"], w[p + "cmp_wout"], out=b["x"] if out is None else out,
                    epilogue=ops.EPI_RESID_ADD if epilogue is None else epilogue,
                    layout=ops.LAYOUT_PACKED)
+
+    def _router_summary_kv(self, p: str, vals, lat_raw=None, lat=None, out=None):
+        """The router's [k | v] of summary values (model.py:318-334 with
+        mla_memory.py:23-24): LayerNorm(down . value) (eps 1e-5), then k | v."""
+        w = self.w
+        lat_raw = ops.linear(vals, w[p + "hca_lat_down"], out=lat_raw, epilogue=ops.EPI_STORE_F32,
+                             layout=ops.LAYOUT_PACKED)
+        lat = ops.layernorm(lat_raw, w[p + "hca_lat_ln_w"], w[p + "hca_lat_ln_b"], 1e-5, out=lat)
+        return ops.linear(lat, w[p + "ctx_kv"], out=out, layout=ops.LAYOUT_PACKED)
+
+    def _glob(self, l: int, st: dict) -> dict | None:
+        """The context router's global branch operands of an HCA layer."""
+        if "rk" not in st:
+            return None
+        p = f"L{l}."
+        return {"q": self.w[p + "ctx_q"], "o": self.w[p + "ctx_o"], "rk": st["rk"],
+                "rv": st["rv"], "rtag": st["rtag"], "heads": self.cfg.router_heads,
+                "head_dim": self.cfg.router_head_dim}
 
     def _ctx_weights(self, p: str) -> dict:
         w = self.w
@@ -383,7 +437,7 @@ class HybridDecoder:
             # the context-aware ids replace the plain router's (same buffers)
             ops.router_context(b["h"], self._ctx_weights(p), st["ctx_ring"], cfg.top_k,
                                pos=self.pos, eps=cfg.eps, layout=ops.LAYOUT_PACKED,
-                               bufs=self.ctx_buf)
+                               bufs=self.ctx_buf, glob=self._glob(l, st))
         S = cfg.shared_experts
         idx, gates = b["idx"], b["gates"]
         if S > 0:
@@ -727,6 +781,9 @@ class HybridDecoder:
         ops.cmp_memory_prefill(q, kv[:, :Kw], kv[:, Kw:], B, T, ratio, H, Dh, cs["top_k"],
                                out=loc[:, D:])
         ops.cmp_memory_fill(kv, B, n, ratio, st["mk"], st["mv"], st["mtag"], st["mcount"])
+        if "rk" in st and n:
+            kvr = self._router_summary_kv(p, kv[:, Kw:].contiguous())
+            ops.cmp_memory_fill(kvr, B, n, ratio, st["rk"], st["rv"], st["rtag"], st["rcount"])
         ops.cmp_ring_fill(k, B, T, st["lk"])
         ops.cmp_ring_fill(v, B, T, st["lv"])
         y1 = ops.linear(loc, w[p + "cmp_wlr"], layout=ops.LAYOUT_PACKED)
@@ -772,7 +829,8 @@ class HybridDecoder:
             # rows are B sequences of T tokens from position 0 (fresh state)
             idx, gates, _ = ops.router_context(h, self._ctx_weights(p), st["ctx_ring"], k,
                                                eps=cfg.eps, layout=ops.LAYOUT_PACKED,
-                                               bufs={"idx": idx, "gates": gates})
+                                               bufs={"idx": idx, "gates": gates},
+                                               glob=self._glob(l, st))
         elif not self.fused_router_ok:
             _lib.call("llmy_router_topk_bf16", h.data_ptr(), w[p + "router_norm"].data_ptr(),
                       w[p + "w_router"].data_ptr(), None, idx.data_ptr(), gates.data_ptr(), R, D,

@@ -499,19 +499,64 @@ def router_context_logits(local, c, route_gate, w_router, logits=None):
     return logits
 
 
+def layernorm(x, w, b, eps: float = 1e-5, out=None) -> torch.Tensor:
+    """bf16(LayerNorm(x) * w + b) of x [rows, L] fp32 (nn.LayerNorm, biased variance)."""
+    rows, L = x.shape
+    _check(x, torch.float32, "x")
+    if out is None:
+        out = torch.empty(rows, L, dtype=torch.bfloat16, device=x.device)
+    _check(out, torch.bfloat16, "out", (rows, L))
+    _lib.call("llmy_layernorm_f32_bf16", _ptr(x), _ptr(w), _ptr(b), _ptr(out), rows, L, eps,
+              _stream())
+    return out
+
+
+def latent_attn(q, keys, vals, tag, heads: int, head_dim: int, pos=None, out=None):
+    """Multi-head attention of q [B*T rows, heads*head_dim] over each row's C
+    slots (keys / vals [B, C, heads*head_dim] bf16, tag [B, C]): query b*T + t
+    at position pos[b] (None: t) sees slots with 1 <= tag <= position + 1."""
+    B, C, HQ = keys.shape
+    rows = q.shape[0]
+    if rows % max(B, 1) or HQ != heads * head_dim:
+        raise ValueError("latent_attn: rows must be B * T and keys heads * head_dim wide")
+    _check(keys, torch.bfloat16, "keys")
+    _check(vals, torch.bfloat16, "vals", (B, C, HQ))
+    _check(tag, torch.int32, "tag", (B, C))
+    if out is None:
+        out = torch.empty(rows, HQ, dtype=torch.bfloat16, device=q.device)
+    _lib.call("llmy_latent_attn_bf16", _ptr(q), _rows(q, "q", HQ), _ptr(keys), _ptr(vals),
+              _ptr(tag), _ptr(pos), _ptr(out), _rows(out, "out", HQ), B, rows // max(B, 1), C,
+              heads, head_dim, head_dim ** -0.5, _stream())
+    return out
+
+
 def router_context(h, w: dict, ring, k: int, pos=None, eps: float = 1e-6,
-                   layout: int = LAYOUT_ROWMAJOR, bufs: dict | None = None):
+                   layout: int = LAYOUT_ROWMAJOR, bufs: dict | None = None,
+                   glob: dict | None = None):
     """The whole context-aware routing of rows h [B*T, D] (bf16): returns
     (idx [rows, k] int32, gates [rows, k] fp32, logits [rows, E] fp32).
     ``w`` holds router_norm, ctx_down, ctx_ln_w, ctx_ln_b, ctx_local_out (bf16
     [D, L]), ctx_out (bf16 [D, D]), ctx_gate and w_router (fp32); ``layout``
-    is that of the two bf16 matrices."""
+    is that of the two bf16 matrices.  ``glob`` (HCA layers): the global
+    branch's q ([HQ, D]) and o ([D, HQ]) weights, the block's summary keys /
+    values / tags (rk, rv, rtag) and heads / head_dim; its output is added to
+    local_context_out(ctx) before context_out."""
     b = bufs if bufs is not None else {}
     local, lat = router_context_latent(h, w["router_norm"], w["ctx_down"], w["ctx_ln_w"],
                                        w["ctx_ln_b"], eps, local=b.get("local"), lat=b.get("lat"))
     ctx = router_context_window(lat, ring, pos, ctx=b.get("ctx"))
-    cl = linear(ctx, w["ctx_local_out"], out=b.get("ctx_d"), epilogue=EPI_STORE_BF16,
-                layout=layout)
+    if glob is None:
+        cl = linear(ctx, w["ctx_local_out"], out=b.get("ctx_d"), epilogue=EPI_STORE_BF16,
+                    layout=layout)
+    else:
+        t = linear(ctx, w["ctx_local_out"], out=b.get("ctx_t"), epilogue=EPI_STORE_F32,
+                   layout=layout)
+        lq = f32_to_bf16(local, out=b.get("lq"))
+        gq = linear(lq, glob["q"], out=b.get("gq"), layout=layout)
+        ga = latent_attn(gq, glob["rk"], glob["rv"], glob["rtag"], glob["heads"],
+                         glob["head_dim"], pos=pos, out=b.get("gattn"))
+        linear(ga, glob["o"], out=t, epilogue=EPI_RESID_ADD, layout=layout)
+        cl = f32_to_bf16(t, out=b.get("ctx_d"))
     c = linear(cl, w["ctx_out"], out=b.get("ctx_c"), epilogue=EPI_STORE_F32, layout=layout)
     logits = router_context_logits(local, c, w["ctx_gate"], w["w_router"],
                                    logits=b.get("logits"))

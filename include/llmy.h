@@ -502,6 +502,27 @@ int32_t llmy_router_context_logits_f32(const float* local, const float* c,
                                        const float* route_gate, const float* w_router,
                                        float* logits, int32_t rows, int32_t D, int32_t E,
                                        void* stream);
+/* The router's global branch over an HCA block's summaries
+ * (context_router.py:66-68,126-127; mla_memory.py:9-90; native
+ * router_hca_latent_attention, llmy_cuda/src/model.cpp:972-1062).  Per summary,
+ * once: latent = LayerNorm(down . value) (hca_latent, eps 1e-5) with
+ * llmy_linear_bf16 + llmy_layernorm_f32_bf16, then its keys and values
+ * [k; v] . latent (llmy_linear_bf16), stored in slots beside the summary's tag
+ * (llmy_cmp_commit_bf16 / llmy_cmp_memory_fill_bf16).  Per query: q =
+ * W_q . local (local = the router's RMSNorm of h, bf16), then
+ * llmy_latent_attn_bf16, then W_o . that added to local_context_out(ctx)
+ * before context_out. */
+/* out[r] = bf16((x[r] - mean) / sqrt(var + eps) * w + b), x [rows, L] fp32. */
+int32_t llmy_layernorm_f32_bf16(const float* x, const float* w, const float* b, llmy_bf16* out,
+                                int32_t rows, int32_t L, float eps, void* stream);
+/* Multi-head attention of q [B*T rows, heads*head_dim at q_ld] over each row's
+ * C slots (keys / values [B, C, heads*head_dim] bf16); query row b*T + t is at
+ * position pos[b] (pos NULL: t) and sees slots with 1 <= tag <= position + 1;
+ * out [B*T, out_ld] bf16, 0 where nothing is visible.  scale = 1/sqrt(head_dim). */
+int32_t llmy_latent_attn_bf16(const llmy_bf16* q, int64_t q_ld, const llmy_bf16* keys,
+                              const llmy_bf16* vals, const int32_t* tag, const int32_t* pos,
+                              llmy_bf16* out, int64_t out_ld, int32_t B, int32_t T, int32_t C,
+                              int32_t heads, int32_t head_dim, float scale, void* stream);
 
 /* Decode-time MoE front end (E*D <= 24576, D in {256,512,1024}, k <= 8):
  *   h2[t] = bf16(RMSNorm(x[t]) * ffn_w)   (the block's pre-MoE norm),

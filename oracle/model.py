@@ -21,7 +21,8 @@ Mixers:
     over the last ``conv_kernel`` normalised inputs.
 MoE: router (own RMSNorm + fp32 logits + top-k + softmax; with the context-aware
 router, the logits of context_router.py:94-137 from a per-(loop, layer)
-history of the last router_context latents), routed SwiGLU
+history of the last router_context latents and, on HCA layers, the global
+branch over the block's emitted summaries, hca_global_context), routed SwiGLU
 experts (model/layers/moe.py:172-199) plus the shared experts when the config has
 them (moe.py:185-199: their sum scaled by 1/sqrt(S), added to the routed output).
 
@@ -43,8 +44,8 @@ from .compressed import CompressedMixer
 from .gdn import gdn_step
 from .mhc import mhc_maps, mhc_read, mhc_write
 from .moe import moe_grouped, shared_experts
-from .router import (context_latents, context_route_logits, rmsnorm, router_logits,
-                     router_topk)
+from .router import (context_latents, context_route_logits, hca_global_context, rmsnorm,
+                     router_logits, router_topk)
 
 
 def _bf16(t: torch.Tensor) -> torch.Tensor:
@@ -142,8 +143,19 @@ class HybridOracle:
                                    for b in range(hist.shape[0])]).float()
             else:
                 ctx = hist.double().mean(1).float()
+            glob = None
+            if cfg.layer_kinds[l] == "hca":
+                # the global branch over this block's emitted summaries
+                cm = s["cmp"]
+                vals = [cm["mv"][b][cm["mpos"][b] >= 0] for b in range(h2.shape[0])]
+                glob = hca_global_context(local, vals, w[p + "hca_lat_down"],
+                                          w[p + "hca_lat_ln_w"], w[p + "hca_lat_ln_b"],
+                                          w[p + "ctx_q"], w[p + "ctx_k"], w[p + "ctx_v"],
+                                          w[p + "ctx_o"], cfg.router_heads, cfg.router_head_dim,
+                                          self.rnd)
             logits = context_route_logits(local, ctx, w[p + "ctx_local_out"], w[p + "ctx_out"],
-                                          w[p + "ctx_gate"], w[p + "w_router"], self.rnd)
+                                          w[p + "ctx_gate"], w[p + "w_router"], self.rnd,
+                                          global_ctx=glob)
         else:
             logits = router_logits(h2, w[p + "w_router"], w[p + "router_norm"], cfg.eps)
         idx, gates = router_topk(logits, cfg.top_k)

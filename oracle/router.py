@@ -3,6 +3,7 @@ from __future__ import annotations
 
 import numpy as np
 import torch
+import torch.nn.functional as F
 
 
 def rmsnorm(x: torch.Tensor, weight: torch.Tensor | None, eps: float = 1e-6) -> torch.Tensor:
@@ -71,12 +72,15 @@ def context_window_mean(lat: torch.Tensor, window: int) -> torch.Tensor:
 
 def context_route_logits(local: torch.Tensor, ctx: torch.Tensor, w_local_out: torch.Tensor,
                          w_ctx_out: torch.Tensor, route_gate: torch.Tensor,
-                         w_router: torch.Tensor, act_round=lambda t: t) -> torch.Tensor:
-    """route = local + sigmoid(g) * context_out(local_context_out(ctx)); logits =
-    route . W_r^T (context_router.py:65-72 without the HCA global branch).
-    ``act_round`` rounds the inputs of the two projections where the HIP path
-    stores them in bf16."""
-    cl = act_round(act_round(ctx) @ w_local_out.float().t())
+                         w_router: torch.Tensor, act_round=lambda t: t,
+                         global_ctx: torch.Tensor | None = None) -> torch.Tensor:
+    """route = local + sigmoid(g) * context_out(local_context_out(ctx) [+
+    global_ctx]); logits = route . W_r^T (context_router.py:65-72; global_ctx is
+    the HCA global branch of :66-68, ``hca_global_context``).  ``act_round``
+    rounds the inputs of the two projections where the HIP path stores them in
+    bf16."""
+    cl = act_round(act_round(ctx) @ w_local_out.float().t()
+                   + (0.0 if global_ctx is None else global_ctx))
     c = cl @ w_ctx_out.float().t()
     route = local + torch.sigmoid(route_gate.float()) * c
     return route @ w_router.float().t()
@@ -133,3 +137,32 @@ def moe_permute(expert_ids: np.ndarray, num_experts: int) -> dict[str, np.ndarra
     route_pos[sorted_routes] = np.arange(ids.size)
     return {"counts": counts, "offsets": offsets, "sorted_routes": sorted_routes,
             "route_pos": route_pos}
+
+
+def hca_global_context(local: torch.Tensor, values: list, w_down, ln_w, ln_b, w_q, w_k, w_v,
+                       w_o, heads: int, head_dim: int, act_round=lambda t: t) -> torch.Tensor:
+    """The router's global branch (context_router.py:66-68,126-127;
+    mla_memory.py:52-90) over an HCA block's summaries, as the native engine
+    computes it (router_hca_latent_attention, llmy_cuda/src/model.cpp:972-1062:
+    the block's own emitted summaries, masked to those visible): latents =
+    LayerNorm(down . value) (hca_latent, mla_memory.py:23-24, eps 1e-5), then
+    o(MHA(q(local), k(latents), v(latents))) with scale 1/sqrt(head_dim).
+    ``values[b]`` [n_b, D] holds row b's visible summary values (n_b may be 0:
+    that row's branch is 0).  Returns [B, D] fp32 (the o projection's input
+    rounded by ``act_round``)."""
+    B = local.shape[0]
+    HQ = heads * head_dim
+    q = act_round(act_round(local) @ w_q.float().t()).double().view(B, heads, head_dim)
+    att = torch.zeros(B, HQ, dtype=torch.float64)
+    for b in range(B):
+        v = values[b]
+        if v.shape[0] == 0:
+            continue
+        raw = act_round(v).double() @ w_down.double().t()
+        lat = act_round(F.layer_norm(raw, (raw.shape[-1],), ln_w.double(), ln_b.double(),
+                                     1e-5).float())
+        kk = act_round(lat @ w_k.float().t()).double().view(-1, heads, head_dim)
+        vv = act_round(lat @ w_v.float().t()).double().view(-1, heads, head_dim)
+        sc = torch.einsum("hd,nhd->hn", q[b], kk) / head_dim ** 0.5
+        att[b] = torch.einsum("hn,nhd->hd", sc.softmax(-1), vv).reshape(HQ)
+    return act_round(att.float()) @ w_o.float().t()

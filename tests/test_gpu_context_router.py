@@ -193,3 +193,46 @@ def test_engine_prefill_then_decode_with_context_router():
         ref.forced_routes = [r for r in eng.route_log.cpu().numpy()]
         lr = ref.step(nxt[t].numpy(), st)
         assert rel_l2(lg, lr) <= REL_L2
+
+
+def test_layernorm_kernel():
+    from hybrid_llm_amd import ops
+    g = torch.Generator().manual_seed(21)
+    x = torch.randn(37, 256, generator=g) * 3 + 1
+    w, b = 1 + 0.1 * torch.randn(256, generator=g), 0.1 * torch.randn(256, generator=g)
+    out = ops.layernorm(x.cuda(), w.cuda(), b.cuda(), 1e-5)
+    ref = torch.nn.functional.layer_norm(x.double(), (256,), w.double(), b.double(), 1e-5)
+    assert torch.allclose(out.float().cpu(), ref.float(), rtol=8e-3, atol=1e-5)
+
+
+@pytest.mark.parametrize("T,C", [(1, 64), (5, 40), (1, 300)])
+def test_latent_attention_kernel(T, C):
+    """llmy_latent_attn_bf16 against torch SDPA with the slot visibility mask
+    (1 <= tag <= position + 1), per row and head; rows with nothing visible give 0."""
+    import torch.nn.functional as F
+    from hybrid_llm_amd import ops
+    g = torch.Generator().manual_seed(T * C)
+    B, heads, hd = 3, 4, 64
+    HQ = heads * hd
+    q = torch.randn(B * T, HQ, generator=g).bfloat16()
+    keys = torch.randn(B, C, HQ, generator=g).bfloat16()
+    vals = torch.randn(B, C, HQ, generator=g).bfloat16()
+    tag = torch.randint(0, 120, (B, C), generator=g, dtype=torch.int32)
+    pos = torch.tensor([70, 3, 0], dtype=torch.int32)
+    tag[2] = 5                                     # row 2 at position 0: nothing visible
+    use_pos = T == 1
+    out = ops.latent_attn(q.cuda(), keys.cuda(), vals.cuda(), tag.cuda(), heads, hd,
+                          pos=pos.cuda() if use_pos else None)
+    for b in range(B):
+        for t in range(T):
+            qp = int(pos[b]) if use_pos else t
+            vis = (tag[b] >= 1) & (tag[b] <= qp + 1)
+            got = out[b * T + t].float().cpu()
+            if not vis.any():
+                assert torch.equal(got, torch.zeros(HQ))
+                continue
+            qh = q[b * T + t].float().view(heads, 1, hd)
+            kh = keys[b][vis].float().view(-1, heads, hd).transpose(0, 1)
+            vh = vals[b][vis].float().view(-1, heads, hd).transpose(0, 1)
+            ref = F.scaled_dot_product_attention(qh, kh, vh).reshape(HQ)
+            assert torch.allclose(got, ref, rtol=1e-2, atol=1e-2), (b, t)

@@ -379,3 +379,38 @@ def test_cmp_matches_python_engine(lib, tmp_path, mhc):
         lib.llmy_state_free(s)
     finally:
         lib.llmy_free(m)
+
+
+def test_context_router_global_branch_matches_python_engine(lib, tmp_path):
+    """HCA blocks with the context-aware router (the global branch over the
+    block's summaries, .llmy names moe.router.latent_attention.* and
+    hca_latent.*, llmy_cuda/src/model.cpp:98-104,234): the native engine's
+    prefill and graph-replayed decodes equal the Python engine's bit for bit."""
+    from dataclasses import replace
+    from hybrid_llm_amd.engine import HybridDecoder
+    cfg = replace(C1, layer_kinds=("hca", "gdn", "hca"), hca_window=12, hca_ratio=4,
+                  cmp_slots=64, context_router=True, router_context=8, route_gate_init=0.5)
+    w = init_weights(cfg, seed=19)
+    path = tmp_path / "hca_ctx.llmy"
+    save_llmy(path, cfg, w)
+    B, T = 2, 18
+    prompt = torch.randint(0, cfg.vocab, (B, T), generator=torch.Generator().manual_seed(20),
+                           dtype=torch.int32)
+    print("[engine-api] HCA + context router: prefill 18 + decode 9, B=2", flush=True)
+    m = lib.llmy_load(str(path).encode())
+    assert m, lib.llmy_last_error()
+    try:
+        s = lib.llmy_state_new_batch(m, B)
+        assert s
+        out = torch.zeros(B, cfg.vocab, device="cuda")
+        assert lib.llmy_prefill_batch(m, s, prompt.cuda().data_ptr(), T, out.data_ptr()) == 0
+        py = HybridDecoder(cfg, w, B)
+        assert torch.equal(out, py.prefill(prompt.cuda()))
+        nxt = torch.zeros(B, dtype=torch.int32)
+        for i in range(9):
+            assert lib.llmy_greedy_tokens(s, nxt.data_ptr()) == 0
+            assert lib.llmy_decode_batch(m, s, nxt.data_ptr(), None, 0, out.data_ptr()) == 0
+            assert torch.equal(out, py.step(nxt.cuda())), i
+        lib.llmy_state_free(s)
+    finally:
+        lib.llmy_free(m)

@@ -130,3 +130,35 @@ def test_mhc_with_compressed_mixers():
     errs, _, _, _ = _decode(cfg, 2, 20, seed=11)
     print(f"mHC + cmp decode: worst step rel-L2 {max(errs):.2e}", flush=True)
     _bound(cfg, errs)
+
+
+@pytest.mark.parametrize("mode", ["decode", "prefill"])
+def test_context_router_global_branch(mode):
+    """HCA layers with the context-aware router: the router's global branch over
+    the block's summaries (context_router.py:66-68,126-127) in the Python engine
+    against the model oracle (oracle.router.hca_global_context), decode steps and
+    a prefill, routing replayed."""
+    cfg = replace(C1, layer_kinds=("hca", "gdn", "hca"), vocab=2048, hca_window=12,
+                  hca_ratio=4, cmp_slots=64, context_router=True, router_context=8,
+                  route_gate_init=0.5, num_loops=1)
+    if mode == "decode":
+        errs, _, _, _ = _decode(cfg, 3, 24, seed=13)
+        print(f"global branch decode: worst step rel-L2 {max(errs):.2e}", flush=True)
+        assert max(errs) <= REL_L2, errs
+        return
+    from hybrid_llm_amd.engine import HybridDecoder
+    w = init_weights(cfg, seed=14)
+    B, T = 2, 26
+    prompt = torch.randint(0, cfg.vocab, (B, T), generator=torch.Generator().manual_seed(15),
+                           dtype=torch.int32)
+    eng = HybridDecoder(cfg, w, B)
+    eng.route_log_seq = []
+    lg = eng.prefill(prompt.cuda()).clone()
+    ref = HybridOracle(cfg, w, act_bf16=True)
+    st = ref.new_state(B)
+    logs = [r.view(B, T, -1).cpu().numpy() for r in eng.route_log_seq]
+    ref.forced_routes = [logs[a][:, t] for t in range(T) for a in range(len(logs))]
+    out = ref.prefill(prompt.numpy(), st)
+    e = rel_l2(lg, out[:, -1])
+    print(f"global branch prefill: last-position rel-L2 {e:.2e}", flush=True)
+    assert e <= REL_L2, e

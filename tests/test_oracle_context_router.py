@@ -117,3 +117,36 @@ def test_model_with_gate_off_equals_plain_router_model():
         assert torch.allclose(a.step(t, sa), b.step(t, sb), rtol=1e-5, atol=1e-6)
     assert sa[(0, 0)]["lat"].shape == (2, 3, cfg.latent_dim)
     assert np.array_equal(np.stack(a.routes), np.stack(b.routes))
+
+
+def test_hca_global_context_is_layernorm_then_sdpa():
+    """oracle.router.hca_global_context against nn.LayerNorm + torch's SDPA, the
+    routines the reference's MLALatentMemory.encode / LatentAttention call
+    (mla_memory.py:23-24,65-86), per row over that row's summaries; a row
+    without summaries gives 0."""
+    import torch.nn.functional as F
+    from oracle.router import hca_global_context
+    g = torch.Generator().manual_seed(4)
+    B, D, L, heads, hd = 3, 64, 32, 4, 8
+    HQ = heads * hd
+    local = torch.randn(B, D, generator=g)
+    values = [torch.randn(n, D, generator=g) for n in (5, 0, 9)]
+    w = {n: torch.randn(s, generator=g) * 0.2 for n, s in
+         (("down", (L, D)), ("q", (HQ, D)), ("k", (HQ, L)), ("v", (HQ, L)), ("o", (D, HQ)))}
+    ln_w, ln_b = 1 + 0.1 * torch.randn(L, generator=g), 0.1 * torch.randn(L, generator=g)
+    got = hca_global_context(local, values, w["down"], ln_w, ln_b, w["q"], w["k"], w["v"],
+                             w["o"], heads, hd)
+    ln = torch.nn.LayerNorm(L)
+    with torch.no_grad():
+        ln.weight.copy_(ln_w)
+        ln.bias.copy_(ln_b)
+        for b in range(B):
+            if values[b].shape[0] == 0:
+                assert torch.equal(got[b], torch.zeros(D))
+                continue
+            lat = ln(values[b] @ w["down"].t())
+            q = (local[b:b + 1] @ w["q"].t()).view(1, 1, heads, hd).transpose(1, 2)
+            k = (lat @ w["k"].t()).view(1, -1, heads, hd).transpose(1, 2)
+            v = (lat @ w["v"].t()).view(1, -1, heads, hd).transpose(1, 2)
+            o = F.scaled_dot_product_attention(q, k, v).transpose(1, 2).reshape(1, HQ)
+            assert torch.allclose(got[b], (o @ w["o"].t())[0], atol=1e-5, rtol=1e-4), b
