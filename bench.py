@@ -271,7 +271,8 @@ def n_sets(bytes_per_set: float, minimum: int = 3) -> int:
 
 KERNEL_ROWS = ("hbm_copy", "moe_decode_experts", "lm_head", "gdn_decode_step", "gdn_decode_step_c4",
                "sample_argmax", "sample_top_p", "moe_prefill_layer", "moe_prefill_experts",
-               "dense_prefill_gemm", "attn_prefill", "gdn_prefill")
+               "dense_prefill_gemm", "attn_prefill", "gdn_prefill", "csa_decode", "hca_decode",
+               "csa_prefill", "hca_prefill")
 
 
 def kernel_table(cfg, B, gen, iters, only=None):
@@ -482,12 +483,78 @@ def kernel_table(cfg, B, gen, iters, only=None):
         bytes4 = 4 * Bg * Tg * Hg4 * d4 * 2 + 2 * Bg * Tg * Hg4 * 4 + 2 * Bg * Hg4 * d4 * d4 * 4
         hbm("gdn_prefill", t, bytes4, f"C4: B={Bg}, T={Tg}, H={Hg4}, dk=dv={d4}, chunk 64")
 
+    # CSA / HCA mixers at the reference's defaults (model/config.py:56-70):
+    # d_model 1024, local window 128; CSA 16 index heads x 128, ratio 4, top-32;
+    # HCA one head of 1024, ratio 32, dense; 256 memory slots per row
+    def cmp_shape(kind):
+        return ((16, 128, 4, 32) if kind == "csa" else (1, D, 32, 0))
+
+    def cmp_decode(kind):
+        # local window + memory branch for B rows; rings and memories full
+        # (every slot visible); bytes = the window's and the memory's keys and
+        # values read once per row (the branches' algorithmic reads)
+        H, Dh, ratio, top_k = cmp_shape(kind)
+        Kw, W, C = H * Dh, 128, 256
+        per_set = B * (W + C) * (Kw + D) * 2
+        nsets = max(2, -(-300_000_000 // per_set))
+        sets = []
+        for _ in range(nsets):
+            sets.append({"lk": torch.randn(B, W, Kw, device="cuda", generator=gen).bfloat16(),
+                         "lv": torch.randn(B, W, D, device="cuda", generator=gen).bfloat16(),
+                         "mk": torch.randn(B, C, Kw, device="cuda", generator=gen).bfloat16(),
+                         "mv": torch.randn(B, C, D, device="cuda", generator=gen).bfloat16()})
+        tag = torch.arange(1, C + 1, device="cuda", dtype=torch.int32).repeat(B, 1)
+        pos = torch.full((B,), 5000, dtype=torch.int32, device="cuda")
+        qkv = torch.randn(B, 2 * Kw + D, device="cuda", generator=gen).bfloat16()
+        loc = torch.empty(B, 2 * D, dtype=torch.bfloat16, device="cuda")
+        ws = ops.cmp_workspace(B, H, C, top_k, "cuda", decode=True)
+        wsl = ops.cmp_workspace(B, H, W, 0, "cuda", decode=True)
+
+        def launch(i):
+            st = sets[i % nsets]
+            ops.cmp_local_decode(qkv[:, :Kw], qkv[:, Kw:2 * Kw], qkv[:, 2 * Kw:], st["lk"],
+                                 st["lv"], pos, H, Dh, out=loc[:, :D], workspace=wsl)
+            ops.cmp_memory_decode(qkv[:, :Kw], st["mk"], st["mv"], tag, pos, H, Dh, top_k,
+                                  out=loc[:, D:], workspace=ws)
+        t = event_time(launch, iters)
+        hbm(f"{kind}_decode", t, per_set,
+            f"{kind.upper()} decode branches: B={B}, heads={H} x {Dh}, d_model={D}, "
+            f"window={W}, {C} memory slots, top_k={top_k or 'dense'}")
+
+    def cmp_prefill(kind):
+        # local + memory branches over one fresh 4096-token sequence; FLOPs =
+        # scores and weighted sums over the candidates each query sees
+        H, Dh, ratio, top_k = cmp_shape(kind)
+        Kw, W, Bq, Tq = H * Dh, 128, 1, 4096
+        n = Tq // ratio
+        qkv = torch.randn(Bq * Tq, 2 * Kw + D, device="cuda", generator=gen).bfloat16()
+        kv = torch.randn(Bq * n, Kw + D, device="cuda", generator=gen).bfloat16()
+        loc = torch.empty(Bq * Tq, 2 * D, dtype=torch.bfloat16, device="cuda")
+        wsl = ops.cmp_workspace(Bq * Tq, H, W, 0, "cuda")
+        wsm = ops.cmp_workspace(Bq * Tq, H, n, top_k, "cuda")
+
+        def launch(i):
+            ops.cmp_local_prefill(qkv[:, :Kw], qkv[:, Kw:2 * Kw], qkv[:, 2 * Kw:], Bq, Tq, H, Dh,
+                                  W, out=loc[:, :D], workspace=wsl)
+            ops.cmp_memory_prefill(qkv[:, :Kw], kv[:, :Kw], kv[:, Kw:], Bq, Tq, ratio, H, Dh,
+                                   top_k, out=loc[:, D:], workspace=wsm)
+        t = event_time(launch, it_mfma)
+        band = sum(min(t_ + 1, W) for t_ in range(Tq))
+        vis = sum(min(n, (t_ + 1) // ratio) for t_ in range(Tq))
+        sel = sum(min(top_k, (t_ + 1) // ratio) for t_ in range(Tq)) * H if top_k else vis
+        flops = 2 * Bq * (band * (Kw + D) + vis * Kw + sel * D)
+        mfma(f"{kind}_prefill", t, flops,
+             f"{kind.upper()} prefill branches: B={Bq}, T={Tq}, heads={H} x {Dh}, "
+             f"d_model={D}, window={W}, ratio={ratio}, top_k={top_k or 'dense'}")
+
     fns = {"hbm_copy": hbm_copy, "moe_decode_experts": moe_decode_experts, "lm_head": lm_head,
            "gdn_decode_step": gdn_decode_step,
            "gdn_decode_step_c4": gdn_decode_step_c4, "sample_argmax": sample_argmax,
            "sample_top_p": sample_top_p, "moe_prefill_layer": moe_prefill_layer,
            "moe_prefill_experts": moe_prefill_experts, "dense_prefill_gemm": dense_prefill_gemm,
-           "attn_prefill": attn_prefill, "gdn_prefill": gdn_prefill}
+           "attn_prefill": attn_prefill, "gdn_prefill": gdn_prefill,
+           "csa_decode": lambda: cmp_decode("csa"), "hca_decode": lambda: cmp_decode("hca"),
+           "csa_prefill": lambda: cmp_prefill("csa"), "hca_prefill": lambda: cmp_prefill("hca")}
     for name in KERNEL_ROWS:
         if only is None or name in only:
             fns[name]()

@@ -73,7 +73,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "llmy_layernorm_f32_bf16": (_I, [_P, _P, _P, _P, _I, _I, _F, _P]),
     "llmy_latent_attn_bf16": (_I, [_P, _I64, _P, _P, _P, _P, _P, _I64, _I, _I, _I, _I, _I, _F,
                                    _P]),
-    "llmy_cmp_workspace_bytes": (C.c_int64, [_I, _I, _I, _I]),
+    "llmy_cmp_workspace_bytes": (C.c_int64, [_I, _I, _I, _I, _I]),
     "llmy_cmp_local_prefill_bf16": (_I, [_P, _I64, _P, _I64, _P, _I64, _P, _I64, _I, _I, _I, _I,
                                          _I, _I, _F, _P, _I64, _P]),
     "llmy_cmp_memory_prefill_bf16": (_I, [_P, _I64, _P, _I64, _P, _I64, _P, _I64, _I, _I, _I,

@@ -39,7 +39,7 @@ typedef float f32x16c __attribute__((ext_vector_type(16)));
 
 constexpr float kLog2eC = 1.4426950408889634f;
 enum CmpMode { kBand = 0, kMemDense = 1, kMemTopK = 2 };
-constexpr int kCmpLdsBytes = 65536;   // score budget of one prefill selection workgroup
+constexpr int kCmpLdsBytes = 131072;  // score budget of one prefill selection workgroup
 
 // One wave turns a row of log2-domain scores into a dense list over n slots:
 // slot j reads score srow[j + off] and is a candidate when jlo <= j < jhi
@@ -60,13 +60,79 @@ __device__ __forceinline__ void dense_row(const float* srow, int n, int off, int
     out[j] = (j >= jlo && j < jhi && inv > 0.f) ? exp2_fast(srow[j + off] - m) * inv : 0.f;
 }
 
-// One wave: the k largest of srow[0, n) (ties to the lower index; the row is
-// consumed), softmax over them; pairs (index, probability) to iout / wout.
-// Selections that are -inf (fewer than k candidates) weigh 0 with index 0.
+// One wave: the k largest of srow[0, n) (ties to the lower index), softmax
+// over them; pairs (index, probability) to iout / wout.  Selections that are
+// -inf (fewer than k candidates) weigh 0 with index -1.  sel_s / sel_i: the
+// wave's 64-entry LDS staging.
+//
+// n <= 2048: the scores' order keys (order_key: a larger value has a larger
+// key) stay in registers, NPL per lane; the k-th largest key is built bit by
+// bit from the top (keep a bit when at least k keys are >= the prefix with
+// it set: 32 counting rounds), then every key above it and the lowest-index
+// ones equal to it are selected and compacted with ballots.  Larger rows take
+// k rounds of a wave argmax over the LDS row (which it consumes).
+template <int NPL>
+__device__ __forceinline__ void topk_regs(const float* srow, int n, int k, int lane, float* wout,
+                                          int32_t* iout, float* sel_s, int* sel_i) {
+  uint32_t key[NPL];
+#pragma unroll
+  for (int i = 0; i < NPL; ++i) {
+    const int j = i * kWave + lane;
+    key[i] = j < n ? order_key(srow[j]) : 0u;   // 0: below every real key
+  }
+  // counts over the wave are popcounts of compare masks (no cross-lane data
+  // movement): the threshold search runs in the scalar unit
+  uint32_t thr = 0;
+  for (int bit = 31; bit >= 0; --bit) {
+    const uint32_t cand = thr | (1u << bit);
+    int c = 0;
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) c += __popcll(__ballot(key[i] >= cand));
+    if (c >= k) thr = cand;
+  }
+  int gt = 0;
+#pragma unroll
+  for (int i = 0; i < NPL; ++i) gt += __popcll(__ballot(key[i] > thr));
+  // thr == 0: fewer than k candidates, all of them are taken
+  const int need = thr > 0 ? k - gt : 0;
+  const uint64_t below = (1ull << lane) - 1ull;
+  int taken = 0, eq_seen = 0;
+#pragma unroll
+  for (int i = 0; i < NPL; ++i) {
+    const bool eq = thr > 0 && key[i] == thr;
+    const uint64_t meq = __ballot(eq);
+    const bool sel = key[i] > thr || (eq && eq_seen + __popcll(meq & below) < need);
+    eq_seen += __popcll(meq);
+    const uint64_t ms = __ballot(sel);
+    if (sel) {
+      const int at = taken + __popcll(ms & below);
+      sel_s[at] = srow[i * kWave + lane];
+      sel_i[at] = i * kWave + lane;
+    }
+    taken += __popcll(ms);
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  const float v = lane < taken ? sel_s[lane] : -INFINITY;
+  const float m = wave_max(lane < k ? v : -INFINITY);
+  const float e = (lane < k && v != -INFINITY) ? exp2_fast(v - m) : 0.f;
+  const float sum = wave_sum(e);
+  if (lane < k) {
+    wout[lane] = sum > 0.f ? e / sum : 0.f;
+    iout[lane] = v != -INFINITY ? sel_i[lane] : -1;
+  }
+}
+
 __device__ __forceinline__ void topk_row(float* srow, int n, int k, int lane, float* wout,
-                                         int32_t* iout) {
+                                         int32_t* iout, float* sel_s, int* sel_i) {
+  if (n <= 128) return topk_regs<2>(srow, n, k, lane, wout, iout, sel_s, sel_i);
+  if (n <= 256) return topk_regs<4>(srow, n, k, lane, wout, iout, sel_s, sel_i);
+  if (n <= 512) return topk_regs<8>(srow, n, k, lane, wout, iout, sel_s, sel_i);
+  if (n <= 1024) return topk_regs<16>(srow, n, k, lane, wout, iout, sel_s, sel_i);
+  if (n <= 2048) return topk_regs<32>(srow, n, k, lane, wout, iout, sel_s, sel_i);
   float mine = -INFINITY;
-  int32_t mine_idx = 0;
+  int32_t mine_idx = -1;
   for (int it = 0; it < k; ++it) {
     uint64_t best = 0;
     for (int j = lane; j < n; j += kWave) best = umax64(best, value_index_key(srow[j], j));
@@ -76,7 +142,7 @@ __device__ __forceinline__ void topk_row(float* srow, int n, int k, int lane, fl
     const float v = ok ? srow[idx] : -INFINITY;
     if (lane == it) {
       mine = v;
-      mine_idx = (ok && v != -INFINITY) ? idx : 0;
+      mine_idx = (ok && v != -INFINITY) ? idx : -1;
     }
     __builtin_amdgcn_wave_barrier();
     if (ok && lane == 0) srow[idx] = -INFINITY;
@@ -94,18 +160,26 @@ __device__ __forceinline__ void topk_row(float* srow, int n, int k, int lane, fl
 }
 
 // ---------------------------------------------------------------- prefill
-// Workgroup = (head h, 32-query block, row b), h fastest.  Candidates:
+// Workgroup = (head h, 32-query block, row b), h fastest; 8 waves.  Candidates:
 //   band: keys [max(0, t0 - W + 1), min(T - 1, t0 + 31)] of row b (q/k rows
 //         b*T + t); the list of query t has W slots, slot j = key t - W + 1 + j;
 //   memory: entries [0, nv), nv = min(n, min(T, t0 + 32) / ratio) (rows b*n + i,
 //         entry i visible from position (i + 1) ratio - 1 on); dense lists have
 //         n slots, top-k lists top_k pairs.
-template <int MODE>
-__global__ __launch_bounds__(256) void cmp_select_prefill_kernel(
+// NS = head_dim / 16 when it is at most 8: the 32 queries' fragments stay in
+// registers and each wave prefetches its next 32-candidate tile under the
+// current tile's MFMAs; NS = 0: any multiple-of-16 head width, operands loaded
+// per 16-wide slice.
+constexpr int kSelWaves = 8;
+
+template <int MODE, int NS>
+__global__ __launch_bounds__(512) void cmp_select_prefill_kernel(
     const uint16_t* __restrict__ q, int64_t q_ld, const uint16_t* __restrict__ k, int64_t k_ld,
     int T, int n, int H, int Dh, int W, int ratio, int top_k, int Kmax, int rows_pass,
     float scale_log2, float* __restrict__ wl, int32_t* __restrict__ il) {
   extern __shared__ float sc[];
+  __shared__ float sel_s[kSelWaves][kWave];
+  __shared__ int sel_i[kSelWaves][kWave];
   const int h = blockIdx.x % H;
   const int rest = blockIdx.x / H;
   const int nqb = (T + 31) / 32;
@@ -128,21 +202,61 @@ __global__ __launch_bounds__(256) void cmp_select_prefill_kernel(
   const uint16_t* qrow =
       q + static_cast<int64_t>(b * T + (q_ok ? t0 + col : 0)) * q_ld + h * Dh + 8 * half;
   const int64_t krow0 = MODE == kBand ? static_cast<int64_t>(b) * T : static_cast<int64_t>(b) * n;
+  constexpr int NQ = NS > 0 ? NS : 1;
+  uint4 qf[NQ];
+  if (NS > 0) {
+#pragma unroll
+    for (int s = 0; s < NQ; ++s)
+      qf[s] = q_ok ? *reinterpret_cast<const uint4*>(qrow + 16 * s) : uint4{0, 0, 0, 0};
+  }
+  auto krow_of = [&](int tile, bool& ok) {
+    const int c0 = c_lo + 32 * tile;
+    ok = c0 + col < c_lo + nc;
+    return k + (krow0 + (ok ? c0 + col : c_lo)) * k_ld + h * Dh + 8 * half;
+  };
   for (int p0 = 0; p0 < 32; p0 += rows_pass) {
     if (ntile == 0) {   // no candidate yet (memory before the first block end)
-      for (int i = threadIdx.x; i < rows_pass * ncp; i += 256) sc[i] = -INFINITY;
+      for (int i = threadIdx.x; i < rows_pass * ncp; i += 64 * kSelWaves) sc[i] = -INFINITY;
     }
-    for (int tile = wave; tile < ntile; tile += 4) {
+    uint4 an[NQ];
+    if (NS > 0 && wave < ntile) {
+      bool ok;
+      const uint16_t* kr = krow_of(wave, ok);
+#pragma unroll
+      for (int s = 0; s < NQ; ++s)
+        an[s] = ok ? *reinterpret_cast<const uint4*>(kr + 16 * s) : uint4{0, 0, 0, 0};
+    }
+    for (int tile = wave; tile < ntile; tile += kSelWaves) {
       const int c0 = c_lo + 32 * tile;
-      const bool c_ok = c0 + col < c_lo + nc;
-      const uint16_t* krow = k + (krow0 + (c_ok ? c0 + col : c_lo)) * k_ld + h * Dh + 8 * half;
       f32x16c acc;
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[r] = 0.f;
-      for (int s = 0; s < Dh / 16; ++s) {
-        const uint4 a = c_ok ? *reinterpret_cast<const uint4*>(krow + 16 * s) : uint4{0, 0, 0, 0};
-        const uint4 bq = q_ok ? *reinterpret_cast<const uint4*>(qrow + 16 * s) : uint4{0, 0, 0, 0};
-        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a), as_bf16x8(bq), acc, 0, 0, 0);
+      if (NS > 0) {
+        uint4 a[NQ];
+#pragma unroll
+        for (int s = 0; s < NQ; ++s) a[s] = an[s];
+        if (tile + kSelWaves < ntile) {   // the next tile's fragments, in flight meanwhile
+          bool ok;
+          const uint16_t* kr = krow_of(tile + kSelWaves, ok);
+#pragma unroll
+          for (int s = 0; s < NQ; ++s)
+            an[s] = ok ? *reinterpret_cast<const uint4*>(kr + 16 * s) : uint4{0, 0, 0, 0};
+        }
+#pragma unroll
+        for (int s = 0; s < NQ; ++s)
+          acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a[s]), as_bf16x8(qf[s]), acc,
+                                                        0, 0, 0);
+      } else {
+        bool ok;
+        const uint16_t* kr = krow_of(tile, ok);
+#pragma unroll 4
+        for (int s = 0; s < Dh / 16; ++s) {
+          const uint4 a = ok ? *reinterpret_cast<const uint4*>(kr + 16 * s) : uint4{0, 0, 0, 0};
+          const uint4 bq =
+              q_ok ? *reinterpret_cast<const uint4*>(qrow + 16 * s) : uint4{0, 0, 0, 0};
+          acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a), as_bf16x8(bq), acc, 0, 0,
+                                                        0);
+        }
       }
       const int row = col - p0;
       if (row >= 0 && row < rows_pass) {
@@ -158,7 +272,7 @@ __global__ __launch_bounds__(256) void cmp_select_prefill_kernel(
       }
     }
     __syncthreads();
-    for (int row = wave; row < rows_pass; row += 4) {
+    for (int row = wave; row < rows_pass; row += kSelWaves) {
       const int t = t0 + p0 + row;
       if (t >= T) continue;
       float* srow = sc + row * ncp;
@@ -170,36 +284,61 @@ __global__ __launch_bounds__(256) void cmp_select_prefill_kernel(
       } else if (MODE == kMemDense) {
         dense_row(srow, Kmax, 0, 0, nc, lane, wl + lb);
       } else {
-        topk_row(srow, nc, top_k, lane, wl + lb, il + lb);
+        topk_row(srow, nc, top_k, lane, wl + lb, il + lb, sel_s[wave], sel_i[wave]);
       }
     }
     __syncthreads();
   }
 }
 
-// ---------------------------------------------------------------- decode
-// Workgroup = (head h, row b).  band: candidate j in [0, W) <-> key
-// p - W + 1 + j (p = pos[b]; keys < 0 are not candidates), the current key
-// from k_new, older ones from the ring (slot key % W); the workgroup also
-// stores its head's slice of k_new (and head 0 the v_new row) into slot p % W,
-// which held key p - W, outside this step's window.  memory: candidates are
-// the C slots, visible when 1 <= tag <= p + 1.
+// Launch of the prefill selection: NS specialised for head widths 64 / 128.
 template <int MODE>
-__global__ __launch_bounds__(256) void cmp_select_decode_kernel(
+void select_prefill_launch(dim3 grid, size_t lds, hipStream_t s, const uint16_t* q, int64_t q_ld,
+                           const uint16_t* k, int64_t k_ld, int T, int n, int H, int Dh, int W,
+                           int ratio, int top_k, int Kmax, int rows, float scale_log2, float* wl,
+                           int32_t* il) {
+  const dim3 block(64 * kSelWaves);
+  if (Dh == 128)
+    hipLaunchKernelGGL((cmp_select_prefill_kernel<MODE, 8>), grid, block, lds, s, q, q_ld, k,
+                       k_ld, T, n, H, Dh, W, ratio, top_k, Kmax, rows, scale_log2, wl, il);
+  else if (Dh == 64)
+    hipLaunchKernelGGL((cmp_select_prefill_kernel<MODE, 4>), grid, block, lds, s, q, q_ld, k,
+                       k_ld, T, n, H, Dh, W, ratio, top_k, Kmax, rows, scale_log2, wl, il);
+  else
+    hipLaunchKernelGGL((cmp_select_prefill_kernel<MODE, 0>), grid, block, lds, s, q, q_ld, k,
+                       k_ld, T, n, H, Dh, W, ratio, top_k, Kmax, rows, scale_log2, wl, il);
+}
+
+// ---------------------------------------------------------------- decode
+// Scores: workgroup = (chunk of 16 * 64 / G candidates, head h, row b), chunk
+// fastest; each wave scores 4 passes of 64 / G candidates with G lanes per
+// candidate (16-byte loads, xor-shuffle sums) and writes them, log2-scaled,
+// -inf for non-candidates, to sc [B, H, ncand].  band: candidate j in [0, W) <-> key p - W + 1 + j
+// (p = pos[b]; keys < 0 are not candidates), the current key from k_new,
+// older ones from the ring (slot key % W); chunk 0 also stores its head's slice
+// of k_new (and head 0 the v_new row) into slot p % W, which held key p - W,
+// outside this step's window.  memory: candidates are the C slots, visible
+// when 1 <= tag <= p + 1.
+template <int MODE, int G>
+__global__ __launch_bounds__(256) void cmp_score_decode_kernel(
     const uint16_t* __restrict__ q, int64_t q_ld, const uint16_t* __restrict__ k_new,
     const uint16_t* __restrict__ v_new, int64_t kv_ld, uint16_t* __restrict__ ring_k,
     uint16_t* __restrict__ ring_v, const uint16_t* __restrict__ mk,
     const int32_t* __restrict__ mtag, const int32_t* __restrict__ pos, int H, int Dh, int Dv,
-    int W, int C, int top_k, int Kmax, float scale_log2, float* __restrict__ wl,
-    int32_t* __restrict__ il) {
-  extern __shared__ float sc[];
-  const int h = blockIdx.x % H;
-  const int b = blockIdx.x / H;
+    int W, int C, float scale_log2, float* __restrict__ sc) {
+  constexpr int kCpw = kWave / G;        // candidates per wave pass
+  constexpr int kPasses = 4;
+  constexpr int kChunk = 4 * kPasses * kCpw;   // candidates per workgroup
+  const int ncand = MODE == kBand ? W : C;
+  const int nchunk = (ncand + kChunk - 1) / kChunk;
+  const int chunk = blockIdx.x % nchunk;
+  const int bh = blockIdx.x / nchunk;
+  const int h = bh % H;
+  const int b = bh / H;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int p = max(pos[b], 0);   // positions are >= 0; the clamp keeps slots in range
   const int Kw = H * Dh;
-  const int ncand = MODE == kBand ? W : C;
-  if (MODE == kBand) {
+  if (MODE == kBand && chunk == 0) {
     uint16_t* kslot = ring_k + (static_cast<int64_t>(b) * W + p % W) * Kw + h * Dh;
     const uint16_t* ksrc = k_new + static_cast<int64_t>(b) * kv_ld + h * Dh;
     for (int c = threadIdx.x; c < Dh / 8; c += 256)
@@ -211,13 +350,13 @@ __global__ __launch_bounds__(256) void cmp_select_decode_kernel(
         reinterpret_cast<uint4*>(vslot)[c] = reinterpret_cast<const uint4*>(vsrc)[c];
     }
   }
-  const int G = min(kWave, Dh / 8);           // lanes per candidate
-  const int cpw = kWave / G;                  // candidates per wave pass
   const int nch = Dh / 8 / G;                 // 16-byte chunks per lane
   const int gl = lane % G;
   const uint16_t* qh = q + static_cast<int64_t>(b) * q_ld + h * Dh;
-  for (int base = wave * cpw; base < ncand; base += 4 * cpw) {
-    const int c = base + lane / G;
+  float* srow = sc + static_cast<int64_t>(bh) * ncand;
+#pragma unroll
+  for (int ps = 0; ps < kPasses; ++ps) {
+    const int c = chunk * kChunk + wave * (kPasses * kCpw) + ps * kCpw + lane / G;
     bool vis = c < ncand;
     const uint16_t* kr;
     if (MODE == kBand) {
@@ -242,65 +381,160 @@ __global__ __launch_bounds__(256) void cmp_select_decode_kernel(
         for (int i = 0; i < 8; ++i) dot = fmaf(a[i], bb[i], dot);
       }
     }
+#pragma unroll
     for (int o = G / 2; o >= 1; o >>= 1) dot += __shfl_xor(dot, o, kWave);
-    if (gl == 0 && c < ncand) sc[c] = vis ? dot * scale_log2 : -INFINITY;
-  }
-  __syncthreads();
-  if (wave == 0) {
-    const int64_t lb = (static_cast<int64_t>(b) * H + h) * Kmax;
-    if (MODE == kMemTopK) topk_row(sc, ncand, top_k, lane, wl + lb, il + lb);
-    else dense_row(sc, ncand, 0, 0, ncand, lane, wl + lb);
+    if (gl == 0 && c < ncand) srow[c] = vis ? dot * scale_log2 : -INFINITY;
   }
 }
 
+// Lists: one wave per (head h, row b) turns its score row into the dense list
+// (W or C slots) or the top_k (index, probability) pairs.
+template <int MODE>
+__global__ __launch_bounds__(64) void cmp_list_decode_kernel(const float* __restrict__ sc,
+                                                             int ncand, int top_k, int Kmax,
+                                                             float* __restrict__ wl,
+                                                             int32_t* __restrict__ il) {
+  extern __shared__ float srow[];
+  __shared__ float sel_s[kWave];
+  __shared__ int sel_i[kWave];
+  const int bh = blockIdx.x;
+  const int lane = threadIdx.x;
+  for (int j = lane; j < ncand; j += kWave) srow[j] = sc[static_cast<int64_t>(bh) * ncand + j];
+  __syncthreads();
+  const int64_t lb = static_cast<int64_t>(bh) * Kmax;
+  if (MODE == kMemTopK) topk_row(srow, ncand, top_k, lane, wl + lb, il + lb, sel_s, sel_i);
+  else dense_row(srow, ncand, 0, 0, ncand, lane, wl + lb);
+}
+
 // ---------------------------------------------------------------- apply
-// One workgroup per query (row b, query t of T per row): out = sum over the
-// heads' lists of (weight / H) * value row.  Dense lists (il == nullptr) are
-// summed over heads in LDS first; slot j is value key base + j with base =
-// qp - W + 1 (band, qp = qpos[b] or t) or 0 (memory).  Value key -> row:
-// v + (b * rows_per_b + (wrap ? key % wrap : key)) * v_ld.
+// Workgroup = (256-channel block, block of QB consecutive queries of one row),
+// channel block fastest; query b*T + t sits at position qpos[b] (qpos NULL:
+// t; decode runs QB = 1).  Block slots: memory slot j, or for the band key
+// t0 - W + 1 + js with t0 the block's first position, so query t's band slot j
+// is block slot j + (t - t0).  First the heads' lists become one weight per
+// (query, slot) in LDS: dense lists (il NULL; nslots == Kmax) are summed over
+// the heads slot by slot; (index, probability) pairs are added head by head
+// (one head's indices are distinct, so each sum runs in head order and the
+// result does not depend on scheduling).  Wave 0 compacts the slots any query
+// uses; the four waves split them, each lane 4 channels of every query, so a
+// value row is read once for the block; partial sums are added in wave order.
+// out = sum / H.  Value key -> row b * rows_per_b + (wrap ? key % wrap : key)
+// at v_ld.
+template <int QB>
 __global__ __launch_bounds__(256) void cmp_apply_kernel(
     const float* __restrict__ wl, const int32_t* __restrict__ il, int Kmax, int H, int T,
-    const int32_t* __restrict__ qpos, int band_W, const uint16_t* __restrict__ v, int64_t v_ld,
-    int rows_per_b, int wrap, uint16_t* __restrict__ out, int64_t out_ld, int Dv) {
+    const int32_t* __restrict__ qpos, int band_W, int nslots, const uint16_t* __restrict__ v,
+    int64_t v_ld, int rows_per_b, int wrap, uint16_t* __restrict__ out, int64_t out_ld,
+    int Dv) {
   extern __shared__ float pm[];
-  const int b = blockIdx.x / T;
-  const int t = blockIdx.x - b * T;
-  const int qp = qpos ? max(qpos[b], 0) : t;
-  const int64_t lb = static_cast<int64_t>(blockIdx.x) * H * Kmax;
-  const float invH = 1.0f / static_cast<float>(H);
-  const int npairs = il ? H * Kmax : Kmax;
-  int32_t* pidx = reinterpret_cast<int32_t*>(pm + npairs);
+  const int nsb = band_W > 0 ? nslots + QB - 1 : nslots;   // block slots
+  const int nsp = (nsb + 3) & ~3;
+  float* red = pm + QB * nsp;                          // [4][256] partial sums
+  int* nz = reinterpret_cast<int*>(red + 4 * 256);     // [nsb] compacted slots
+  __shared__ int nz_count;
+  const int ndb = (Dv + 255) / 256;
+  const int nqb = (T + QB - 1) / QB;
+  const int blk = blockIdx.x / ndb;
+  const int db = blockIdx.x - blk * ndb;
+  const int b = blk / nqb;
+  const int t0 = (blk - b * nqb) * QB;
+  const int nq = min(QB, T - t0);
+  const int p0 = qpos ? max(qpos[b], 0) : t0;
+  for (int i = threadIdx.x; i < QB * nsp; i += 256) pm[i] = 0.f;
+  __syncthreads();
+  const int64_t lb0 = (static_cast<int64_t>(b) * T + t0) * H * Kmax;
   if (il) {
-    for (int e = threadIdx.x; e < npairs; e += 256) {
-      pm[e] = wl[lb + e] * invH;
-      pidx[e] = il[lb + e];
+    for (int hh = 0; hh < H; ++hh) {
+      for (int e = threadIdx.x; e < nq * Kmax; e += 256) {
+        const int qq = e / Kmax, j = e - qq * Kmax;
+        const int64_t o = lb0 + (static_cast<int64_t>(qq) * H + hh) * Kmax + j;
+        const int idx = il[o];
+        if (idx >= 0 && idx < nslots) pm[qq * nsp + idx] += wl[o];
+      }
+      __syncthreads();
     }
   } else {
-    for (int j = threadIdx.x; j < Kmax; j += 256) {
-      float s = 0.f;
-      for (int hh = 0; hh < H; ++hh) s += wl[lb + static_cast<int64_t>(hh) * Kmax + j];
-      pm[j] = s * invH;
+    for (int e = threadIdx.x; e < nq * nslots; e += 256) {
+      const int qq = e / nslots, j = e - qq * nslots;
+      const int64_t o = lb0 + static_cast<int64_t>(qq) * H * Kmax + j;
+      float acc = 0.f;
+      for (int hh = 0; hh < H; ++hh) acc += wl[o + static_cast<int64_t>(hh) * Kmax];
+      pm[qq * nsp + j + (band_W > 0 ? qq : 0)] = acc;
     }
+    __syncthreads();
+  }
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (wave == 0) {
+    int cnt = 0;
+    for (int j0 = 0; j0 < nsb; j0 += kWave) {
+      const int j = j0 + lane;
+      bool live = false;
+      if (j < nsb)
+#pragma unroll
+        for (int qq = 0; qq < QB; ++qq) live = live || pm[qq * nsp + j] != 0.f;
+      const uint64_t m = __ballot(live);
+      if (live) nz[cnt + __popcll(m & ((1ull << lane) - 1ull))] = j;
+      cnt += __popcll(m);
+    }
+    if (lane == 0) nz_count = cnt;
   }
   __syncthreads();
-  const int base = band_W > 0 ? qp - band_W + 1 : 0;
-  const int64_t vrow0 = static_cast<int64_t>(b) * rows_per_b;
-  for (int d0 = 4 * threadIdx.x; d0 < Dv; d0 += 1024) {
-    float acc0 = 0.f, acc1 = 0.f, acc2 = 0.f, acc3 = 0.f;
-    for (int e = 0; e < npairs; ++e) {
-      const float wgt = pm[e];
-      if (wgt == 0.f) continue;
-      const int key = il ? pidx[e] : base + e;
-      const int r = wrap ? key % wrap : key;
-      const uint2 raw = *reinterpret_cast<const uint2*>(v + (vrow0 + r) * v_ld + d0);
-      acc0 = fmaf(wgt, __uint_as_float(raw.x << 16), acc0);
-      acc1 = fmaf(wgt, __uint_as_float(raw.x & 0xffff0000u), acc1);
-      acc2 = fmaf(wgt, __uint_as_float(raw.y << 16), acc2);
-      acc3 = fmaf(wgt, __uint_as_float(raw.y & 0xffff0000u), acc3);
+  const int n = nz_count;
+  const int c0 = db * 256 + 4 * lane;
+  const int cc = c0 < Dv ? c0 : 0;   // lanes past Dv read a valid column, store nothing
+  const int base = band_W > 0 ? p0 - band_W + 1 : 0;
+  const uint16_t* vb = v + static_cast<int64_t>(b) * rows_per_b * v_ld + cc;
+  auto row_of = [&](int j) {
+    const int key = base + j;
+    return static_cast<int64_t>(wrap ? key % wrap : key) * v_ld;
+  };
+  float acc[QB][4];
+#pragma unroll
+  for (int qq = 0; qq < QB; ++qq)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) acc[qq][c] = 0.f;
+  auto add = [&](int j, const uint2& r) {
+    const float x0 = __uint_as_float(r.x << 16), x1 = __uint_as_float(r.x & 0xffff0000u);
+    const float x2 = __uint_as_float(r.y << 16), x3 = __uint_as_float(r.y & 0xffff0000u);
+#pragma unroll
+    for (int qq = 0; qq < QB; ++qq) {
+      const float w = pm[qq * nsp + j];
+      acc[qq][0] = fmaf(w, x0, acc[qq][0]);
+      acc[qq][1] = fmaf(w, x1, acc[qq][1]);
+      acc[qq][2] = fmaf(w, x2, acc[qq][2]);
+      acc[qq][3] = fmaf(w, x3, acc[qq][3]);
     }
-    *reinterpret_cast<uint2*>(out + static_cast<int64_t>(blockIdx.x) * out_ld + d0) =
-        make_uint2(pack_bf2(acc0, acc1), pack_bf2(acc2, acc3));
+  };
+  int i = wave;
+  for (; i + 12 < n; i += 16) {
+    const int j0 = nz[i], j1 = nz[i + 4], j2 = nz[i + 8], j3 = nz[i + 12];
+    const uint2 r0 = *reinterpret_cast<const uint2*>(vb + row_of(j0));
+    const uint2 r1 = *reinterpret_cast<const uint2*>(vb + row_of(j1));
+    const uint2 r2 = *reinterpret_cast<const uint2*>(vb + row_of(j2));
+    const uint2 r3 = *reinterpret_cast<const uint2*>(vb + row_of(j3));
+    add(j0, r0);
+    add(j1, r1);
+    add(j2, r2);
+    add(j3, r3);
+  }
+  for (; i < n; i += 4) {
+    const int j = nz[i];
+    add(j, *reinterpret_cast<const uint2*>(vb + row_of(j)));
+  }
+  const float invH = 1.0f / static_cast<float>(H);
+  const int c = db * 256 + threadIdx.x;
+#pragma unroll
+  for (int qq = 0; qq < QB; ++qq) {
+    if (qq >= nq) break;   // workgroup-uniform
+    *reinterpret_cast<float4*>(red + wave * 256 + 4 * lane) =
+        make_float4(acc[qq][0], acc[qq][1], acc[qq][2], acc[qq][3]);
+    __syncthreads();
+    if (c < Dv) {
+      const float sum = ((red[threadIdx.x] + red[256 + threadIdx.x]) + red[512 + threadIdx.x]) +
+                        red[768 + threadIdx.x];
+      out[(static_cast<int64_t>(b) * T + t0 + qq) * out_ld + c] = f2bf(sum * invH);
+    }
+    __syncthreads();
   }
 }
 
@@ -408,14 +642,48 @@ __global__ __launch_bounds__(256) void cmp_ring_fill_kernel(
 inline bool dh_ok(int Dh) { return Dh >= 16 && Dh % 16 == 0 && Dh <= 4096; }
 
 // decode scoring splits a head over G = min(64, Dh / 8) lanes with xor-shuffle
-// sums: G must be a power of two and divide Dh / 8
+// sums, a wave scoring 16 candidates: G in {4, 8, 16, 32, 64}, dividing Dh / 8
 inline bool dh_decode_ok(int Dh) {
-  return Dh == 16 || Dh == 32 || Dh == 64 || Dh == 128 || Dh == 256 ||
-         (Dh % 512 == 0 && Dh <= 4096);
+  return Dh == 32 || Dh == 64 || Dh == 128 || Dh == 256 || (Dh % 512 == 0 && Dh <= 4096);
+}
+
+// Decode: scores (into sc), then the lists, for one branch.
+template <int MODE>
+int32_t decode_select(const uint16_t* q, int64_t q_ld, const uint16_t* k_new,
+                      const uint16_t* v_new, int64_t kv_ld, uint16_t* ring_k, uint16_t* ring_v,
+                      const uint16_t* mk, const int32_t* mtag, const int32_t* pos, int B, int H,
+                      int Dh, int Dv, int W, int C, int top_k, int Kmax, float scale_log2,
+                      float* sc, float* wl, int32_t* il, hipStream_t s) {
+  const int ncand = MODE == kBand ? W : C;
+  const int G = min(kWave, Dh / 8);
+  const int chunk = 16 * (kWave / G);
+  const dim3 grid(static_cast<unsigned>(B * H * ((ncand + chunk - 1) / chunk)));
+#define LLMY_SCORE(GG)                                                                      \
+  hipLaunchKernelGGL((cmp_score_decode_kernel<MODE, GG>), grid, dim3(256), 0, s, q, q_ld,   \
+                     k_new, v_new, kv_ld, ring_k, ring_v, mk, mtag, pos, H, Dh, Dv, W, C,  \
+                     scale_log2, sc)
+  switch (G) {
+    case 4: LLMY_SCORE(4); break;
+    case 8: LLMY_SCORE(8); break;
+    case 16: LLMY_SCORE(16); break;
+    case 32: LLMY_SCORE(32); break;
+    default: LLMY_SCORE(64); break;
+  }
+#undef LLMY_SCORE
+  const int32_t st = launch_status();
+  if (st) return st;
+  hipLaunchKernelGGL(cmp_list_decode_kernel<MODE>, dim3(B * H), dim3(64),
+                     static_cast<size_t>(ncand) * 4, s, sc, ncand, top_k, Kmax, wl, il);
+  return launch_status();
 }
 
 inline int64_t list_bytes(int64_t queries, int H, int Kmax, bool pairs) {
   return queries * H * Kmax * static_cast<int64_t>(pairs ? 8 : 4);
+}
+
+// decode keeps the raw scores of its slots beside the lists
+inline int64_t decode_bytes(int64_t rows, int H, int slots, int top_k) {
+  return list_bytes(rows, H, top_k > 0 ? top_k : slots, top_k > 0) + rows * H * slots * 4ll;
 }
 
 }  // namespace llmy
@@ -423,21 +691,35 @@ inline int64_t list_bytes(int64_t queries, int H, int Kmax, bool pairs) {
 using namespace llmy;
 
 extern "C" int64_t llmy_cmp_workspace_bytes(int32_t queries, int32_t H, int32_t slots,
-                                            int32_t top_k) {
+                                            int32_t top_k, int32_t decode) {
   if (queries < 0 || H <= 0 || slots <= 0 || top_k < 0) return -1;
+  if (decode) return decode_bytes(queries, H, slots, top_k);
   return top_k > 0 ? list_bytes(queries, H, top_k, true) : list_bytes(queries, H, slots, false);
 }
 
 namespace {
 
 int32_t apply_launch(const float* wl, const int32_t* il, int Kmax, int H, int B, int T,
-                     const int32_t* qpos, int band_W, const uint16_t* v, int64_t v_ld,
+                     const int32_t* qpos, int band_W, int nslots, const uint16_t* v, int64_t v_ld,
                      int rows_per_b, int wrap, uint16_t* out, int64_t out_ld, int Dv,
                      hipStream_t s) {
-  const size_t lds = il ? static_cast<size_t>(H) * Kmax * 8 : static_cast<size_t>(Kmax) * 4;
-  if (lds > 65536) return static_cast<int32_t>(hipErrorInvalidValue);
-  hipLaunchKernelGGL(cmp_apply_kernel, dim3(B * T), dim3(256), lds, s, wl, il, Kmax, H, T, qpos,
-                     band_W, v, v_ld, rows_per_b, wrap, out, out_ld, Dv);
+  // blocks of 8 queries for sequences (a value row serves the whole block),
+  // single queries for decode
+  const int QB = T >= 8 ? 8 : 1;
+  const int nsb = band_W > 0 ? nslots + QB - 1 : nslots;
+  const size_t lds = (static_cast<size_t>(QB) * ((nsb + 3) & ~3) + 4 * 256 +
+                      static_cast<size_t>(nsb)) * 4;
+  if (lds > 147456) return static_cast<int32_t>(hipErrorInvalidValue);
+  const int64_t nblk = static_cast<int64_t>(B) * ((T + QB - 1) / QB) * ((Dv + 255) / 256);
+  if (nblk >= (1ll << 31)) return static_cast<int32_t>(hipErrorInvalidValue);
+  if (QB == 8)
+    hipLaunchKernelGGL(cmp_apply_kernel<8>, dim3(static_cast<unsigned>(nblk)), dim3(256), lds, s,
+                       wl, il, Kmax, H, T, qpos, band_W, nslots, v, v_ld, rows_per_b, wrap, out,
+                       out_ld, Dv);
+  else
+    hipLaunchKernelGGL(cmp_apply_kernel<1>, dim3(static_cast<unsigned>(nblk)), dim3(256), lds, s,
+                       wl, il, Kmax, H, T, qpos, band_W, nslots, v, v_ld, rows_per_b, wrap, out,
+                       out_ld, Dv);
   return launch_status();
 }
 
@@ -469,12 +751,12 @@ extern "C" int32_t llmy_cmp_local_prefill_bf16(
   LLMY_REQUIRE(static_cast<int64_t>(rows) * ncp * 4 <= kCmpLdsBytes);
   const hipStream_t s = as_stream(stream);
   float* wl = static_cast<float*>(workspace);
-  hipLaunchKernelGGL(cmp_select_prefill_kernel<kBand>, dim3(B * nqb * H), dim3(256),
-                     static_cast<size_t>(rows) * ncp * 4, s, q, q_ld, k, k_ld, T, 0, H, head_dim,
-                     W, 1, 0, W, rows, scale * kLog2eC, wl, static_cast<int32_t*>(nullptr));
+  select_prefill_launch<kBand>(dim3(B * nqb * H), static_cast<size_t>(rows) * ncp * 4, s, q, q_ld,
+                               k, k_ld, T, 0, H, head_dim, W, 1, 0, W, rows, scale * kLog2eC, wl,
+                               nullptr);
   const int32_t st = launch_status();
   if (st) return st;
-  return apply_launch(wl, nullptr, W, H, B, T, nullptr, W, v, v_ld, T, 0, out, out_ld, Dv, s);
+  return apply_launch(wl, nullptr, W, H, B, T, nullptr, W, W, v, v_ld, T, 0, out, out_ld, Dv, s);
 }
 
 extern "C" int32_t llmy_cmp_memory_prefill_bf16(
@@ -496,7 +778,7 @@ extern "C" int32_t llmy_cmp_memory_prefill_bf16(
   const int slots = max(n_entries, 1);
   const int Kmax = top_k > 0 ? top_k : slots;
   LLMY_REQUIRE(workspace_bytes >= list_bytes(queries, H, Kmax, top_k > 0));
-  LLMY_REQUIRE(top_k > 0 ? static_cast<int64_t>(H) * top_k * 8 <= 65536 : slots * 4 <= 65536);
+  LLMY_REQUIRE(slots <= 4000);   // the apply's LDS: 9 words per slot + 4 KiB
   const hipStream_t s = as_stream(stream);
   // n_entries == 0: no summary is visible to any query, every list is 0 and
   // the apply writes zeros without reading mk / mv
@@ -510,16 +792,16 @@ extern "C" int32_t llmy_cmp_memory_prefill_bf16(
   int32_t* il = top_k > 0 ? reinterpret_cast<int32_t*>(wl + queries * H * Kmax) : nullptr;
   const size_t lds = static_cast<size_t>(rows) * ncp * 4;
   if (top_k > 0)
-    hipLaunchKernelGGL(cmp_select_prefill_kernel<kMemTopK>, dim3(B * nqb * H), dim3(256), lds, s,
-                       q, q_ld, mk, mk_ld, T, n_entries, H, head_dim, 1, ratio, top_k, Kmax, rows,
-                       scale * kLog2eC, wl, il);
+    select_prefill_launch<kMemTopK>(dim3(B * nqb * H), lds, s, q, q_ld, mk, mk_ld, T, n_entries,
+                                    H, head_dim, 1, ratio, top_k, Kmax, rows, scale * kLog2eC, wl,
+                                    il);
   else
-    hipLaunchKernelGGL(cmp_select_prefill_kernel<kMemDense>, dim3(B * nqb * H), dim3(256), lds, s,
-                       q, q_ld, mk, mk_ld, T, n_entries, H, head_dim, 1, ratio, 0, Kmax, rows,
-                       scale * kLog2eC, wl, il);
+    select_prefill_launch<kMemDense>(dim3(B * nqb * H), lds, s, q, q_ld, mk, mk_ld, T, n_entries,
+                                     H, head_dim, 1, ratio, 0, Kmax, rows, scale * kLog2eC, wl,
+                                     il);
   const int32_t st = launch_status();
   if (st) return st;
-  return apply_launch(wl, il, Kmax, H, B, T, nullptr, 0, mv, mv_ld, max(n_entries, 1), 0, out,
+  return apply_launch(wl, il, Kmax, H, B, T, nullptr, 0, slots, mv, mv_ld, slots, 0, out,
                       out_ld, Dv, s);
 }
 
@@ -529,7 +811,7 @@ extern "C" int32_t llmy_cmp_local_decode_bf16(
     int64_t out_ld, int32_t B, int32_t H, int32_t head_dim, int32_t Dv, int32_t W, float scale,
     void* workspace, int64_t workspace_bytes, void* stream) {
   LLMY_REQUIRE(B >= 0 && H > 0 && dh_decode_ok(head_dim) && Dv > 0 && Dv % 8 == 0 && W >= 1 &&
-               W <= 8192);
+               W <= 7168);
   if (B == 0) return 0;
   const int Kw = H * head_dim;
   LLMY_REQUIRE(q && k_new && v_new && ring_k && ring_v && pos && out && workspace);
@@ -538,18 +820,16 @@ extern "C" int32_t llmy_cmp_local_decode_bf16(
   LLMY_REQUIRE(aligned(q, 16) && aligned(k_new, 16) && aligned(v_new, 16) &&
                aligned(ring_k, 16) && aligned(ring_v, 16) && aligned(out, 8) &&
                aligned(workspace, 16));
-  LLMY_REQUIRE(workspace_bytes >= list_bytes(B, H, W, false) && W * 4 <= 65536);
-  LLMY_REQUIRE(static_cast<int64_t>(B) * H < (1ll << 31));
+  LLMY_REQUIRE(workspace_bytes >= decode_bytes(B, H, W, 0));
+  LLMY_REQUIRE(static_cast<int64_t>(B) * H * ((W + 15) / 16) < (1ll << 31));
   const hipStream_t s = as_stream(stream);
   float* wl = static_cast<float*>(workspace);
-  hipLaunchKernelGGL(cmp_select_decode_kernel<kBand>, dim3(B * H), dim3(256),
-                     static_cast<size_t>(W) * 4, s, q, q_ld, k_new, v_new, kv_ld, ring_k, ring_v,
-                     static_cast<const uint16_t*>(nullptr), static_cast<const int32_t*>(nullptr),
-                     pos, H, head_dim, Dv, W, 0, 0, W, scale * kLog2eC, wl,
-                     static_cast<int32_t*>(nullptr));
-  const int32_t st = launch_status();
+  float* sc = wl + static_cast<int64_t>(B) * H * W;
+  const int32_t st = decode_select<kBand>(q, q_ld, k_new, v_new, kv_ld, ring_k, ring_v, nullptr,
+                                          nullptr, pos, B, H, head_dim, Dv, W, 0, 0, W,
+                                          scale * kLog2eC, sc, wl, nullptr, s);
   if (st) return st;
-  return apply_launch(wl, nullptr, W, H, B, 1, pos, W, ring_v, Dv, W, W, out, out_ld, Dv, s);
+  return apply_launch(wl, nullptr, W, H, B, 1, pos, W, W, ring_v, Dv, W, W, out, out_ld, Dv, s);
 }
 
 extern "C" int32_t llmy_cmp_memory_decode_bf16(
@@ -558,7 +838,7 @@ extern "C" int32_t llmy_cmp_memory_decode_bf16(
     int32_t C, int32_t H, int32_t head_dim, int32_t Dv, int32_t top_k, float scale,
     void* workspace, int64_t workspace_bytes, void* stream) {
   LLMY_REQUIRE(B >= 0 && H > 0 && dh_decode_ok(head_dim) && Dv > 0 && Dv % 8 == 0 && C >= 1 &&
-               C <= 16384 && top_k >= 0 && top_k <= 64);
+               C <= 7168 && top_k >= 0 && top_k <= 64);
   if (B == 0) return 0;
   const int Kw = H * head_dim;
   LLMY_REQUIRE(q && mk && mv && mtag && pos && out && workspace);
@@ -566,29 +846,23 @@ extern "C" int32_t llmy_cmp_memory_decode_bf16(
   LLMY_REQUIRE(aligned(q, 16) && aligned(mk, 16) && aligned(mv, 16) && aligned(out, 8) &&
                aligned(workspace, 16));
   const int Kmax = top_k > 0 ? top_k : C;
-  LLMY_REQUIRE(workspace_bytes >= list_bytes(B, H, Kmax, top_k > 0));
-  LLMY_REQUIRE(top_k > 0 ? static_cast<int64_t>(H) * top_k * 8 <= 65536 : C * 4 <= 65536);
-  LLMY_REQUIRE(static_cast<int64_t>(B) * H < (1ll << 31));
+  LLMY_REQUIRE(workspace_bytes >= decode_bytes(B, H, C, top_k));
+  LLMY_REQUIRE(static_cast<int64_t>(B) * H * ((C + 15) / 16) < (1ll << 31));
   const hipStream_t s = as_stream(stream);
   float* wl = static_cast<float*>(workspace);
-  int32_t* il = top_k > 0 ? reinterpret_cast<int32_t*>(wl + static_cast<int64_t>(B) * H * Kmax)
-                          : nullptr;
-  const size_t lds = static_cast<size_t>(C) * 4;
-  if (top_k > 0)
-    hipLaunchKernelGGL(cmp_select_decode_kernel<kMemTopK>, dim3(B * H), dim3(256), lds, s, q,
-                       q_ld, static_cast<const uint16_t*>(nullptr),
-                       static_cast<const uint16_t*>(nullptr), 0, static_cast<uint16_t*>(nullptr),
-                       static_cast<uint16_t*>(nullptr), mk, mtag, pos, H, head_dim, Dv, 1, C,
-                       top_k, Kmax, scale * kLog2eC, wl, il);
-  else
-    hipLaunchKernelGGL(cmp_select_decode_kernel<kMemDense>, dim3(B * H), dim3(256), lds, s, q,
-                       q_ld, static_cast<const uint16_t*>(nullptr),
-                       static_cast<const uint16_t*>(nullptr), 0, static_cast<uint16_t*>(nullptr),
-                       static_cast<uint16_t*>(nullptr), mk, mtag, pos, H, head_dim, Dv, 1, C, 0,
-                       Kmax, scale * kLog2eC, wl, il);
-  const int32_t st = launch_status();
+  const int64_t nl = static_cast<int64_t>(B) * H * Kmax;
+  int32_t* il = top_k > 0 ? reinterpret_cast<int32_t*>(wl + nl) : nullptr;
+  float* sc = wl + nl * (top_k > 0 ? 2 : 1);
+  const int32_t st =
+      top_k > 0
+          ? decode_select<kMemTopK>(q, q_ld, nullptr, nullptr, 0, nullptr, nullptr, mk, mtag, pos,
+                                    B, H, head_dim, Dv, 1, C, top_k, Kmax, scale * kLog2eC, sc,
+                                    wl, il, s)
+          : decode_select<kMemDense>(q, q_ld, nullptr, nullptr, 0, nullptr, nullptr, mk, mtag,
+                                     pos, B, H, head_dim, Dv, 1, C, 0, Kmax, scale * kLog2eC, sc,
+                                     wl, il, s);
   if (st) return st;
-  return apply_launch(wl, il, Kmax, H, B, 1, pos, 0, mv, Dv, C, 0, out, out_ld, Dv, s);
+  return apply_launch(wl, il, Kmax, H, B, 1, pos, 0, C, mv, Dv, C, 0, out, out_ld, Dv, s);
 }
 
 extern "C" int32_t llmy_cmp_pool_prefill_bf16(const llmy_bf16* h, int64_t h_ld, llmy_bf16* means,

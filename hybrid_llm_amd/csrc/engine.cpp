@@ -327,13 +327,13 @@ Config config_from(const std::string& text) {
   // lanes (16..256 or a multiple of 512), top-k <= 64, memory and window
   // within the kernels' LDS lists
   auto dh_ok = [](int d) {
-    return d == 16 || d == 32 || d == 64 || d == 128 || d == 256 || (d % 512 == 0 && d <= 4096);
+    return d == 32 || d == 64 || d == 128 || d == 256 || (d % 512 == 0 && d <= 4096);
   };
   for (int kind : {kCsa, kHca}) {
     if (!c.has(kind)) continue;
     const CmpShape cs = c.cmp(kind);
-    if (!dh_ok(cs.Dh) || cs.kw() % 16 != 0 || cs.W < 1 || cs.W > 8192 || cs.ratio < 1 ||
-        cs.top_k < 0 || cs.top_k > 64 || c.cmp_slots < 1 || c.cmp_slots > 16384 || c.d_model > 8192)
+    if (!dh_ok(cs.Dh) || cs.kw() % 16 != 0 || cs.W < 1 || cs.W > 4096 || cs.ratio < 1 ||
+        cs.top_k < 0 || cs.top_k > 64 || c.cmp_slots < 1 || c.cmp_slots > 7168 || c.d_model > 8192)
       throw std::runtime_error("unsupported CSA / HCA shape");
   }
   return c;
@@ -834,8 +834,9 @@ void alloc_buffers(const Config& c, int rows, int B, int T, Buffers& b) {
       kw = std::max(kw, cs.kw());
       rmin = std::min(rmin, cs.ratio);
       const int slots = T == 1 ? c.cmp_slots : std::max(T / cs.ratio, 1);
-      ws = std::max({ws, llmy_cmp_workspace_bytes(rows, cs.H, cs.W, 0),
-                     llmy_cmp_workspace_bytes(rows, cs.H, slots, cs.top_k)});
+      const int dec = T == 1 ? 1 : 0;
+      ws = std::max({ws, llmy_cmp_workspace_bytes(rows, cs.H, cs.W, 0, dec),
+                     llmy_cmp_workspace_bytes(rows, cs.H, slots, cs.top_k, dec)});
     }
     if (ws < 0) throw std::runtime_error("CSA / HCA workspace size");
     const size_t nsum = T == 1 ? static_cast<size_t>(rows) : static_cast<size_t>(B) * (T / rmin);

@@ -222,9 +222,9 @@ class HybridDecoder:
                 self.buf["cqkv_" + kind] = torch.zeros(B, 2 * Kw + D, dtype=bf, device=dev)
                 self.buf["ckv_" + kind] = torch.zeros(B, Kw + D, dtype=bf, device=dev)
                 lib = _lib_load()
-                ws = max(ws, int(lib.llmy_cmp_workspace_bytes(B, cs["H"], cs["W"], 0)),
+                ws = max(ws, int(lib.llmy_cmp_workspace_bytes(B, cs["H"], cs["W"], 0, 1)),
                          int(lib.llmy_cmp_workspace_bytes(B, cs["H"], cfg.cmp_slots,
-                                                          cs["top_k"])))
+                                                          cs["top_k"], 1)))
             self.buf.update({"cloc": torch.zeros(B, 2 * D, dtype=bf, device=dev),
                              "cy": torch.zeros(B, D, dtype=bf, device=dev),
                              "cmean": torch.zeros(B, D, dtype=bf, device=dev),

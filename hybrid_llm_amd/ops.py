@@ -761,8 +761,9 @@ def _rows(t: torch.Tensor, name: str, width: int | None = None) -> int:
     return t.stride(0)
 
 
-def cmp_workspace(queries: int, H: int, slots: int, top_k: int, device) -> torch.Tensor:
-    n = _lib.load().llmy_cmp_workspace_bytes(queries, H, slots, top_k)
+def cmp_workspace(queries: int, H: int, slots: int, top_k: int, device,
+                  decode: bool = False) -> torch.Tensor:
+    n = _lib.load().llmy_cmp_workspace_bytes(queries, H, slots, top_k, int(decode))
     if n < 0:
         raise ValueError("bad compressed-attention workspace sizes")
     return torch.empty(max(int(n), 16), dtype=torch.uint8, device=device)
@@ -815,7 +816,7 @@ def cmp_local_decode(q, k_new, v_new, ring_k, ring_v, pos, H: int, Dh: int, out=
     if out is None:
         out = torch.empty(B, Dv, dtype=torch.bfloat16, device=q.device)
     if workspace is None:
-        workspace = cmp_workspace(B, H, W, 0, q.device)
+        workspace = cmp_workspace(B, H, W, 0, q.device, decode=True)
     _lib.call("llmy_cmp_local_decode_bf16", _ptr(q), _rows(q, "q", Kw), _ptr(k_new), _ptr(v_new),
               kv_ld, _ptr(ring_k), _ptr(ring_v), _ptr(pos), _ptr(out), _rows(out, "out", Dv), B,
               H, Dh, Dv, W, Dh ** -0.5, _ptr(workspace), workspace.numel(), _stream())
@@ -834,7 +835,7 @@ def cmp_memory_decode(q, mk, mv, mtag, pos, H: int, Dh: int, top_k: int, out=Non
     if out is None:
         out = torch.empty(B, Dv, dtype=torch.bfloat16, device=q.device)
     if workspace is None:
-        workspace = cmp_workspace(B, H, C, top_k, q.device)
+        workspace = cmp_workspace(B, H, C, top_k, q.device, decode=True)
     _lib.call("llmy_cmp_memory_decode_bf16", _ptr(q), _rows(q, "q", Kw), _ptr(mk), _ptr(mv),
               _ptr(mtag), _ptr(pos), _ptr(out), _rows(out, "out", Dv), B, C, H, Dh, Dv, top_k,
               Dh ** -0.5, _ptr(workspace), workspace.numel(), _stream())

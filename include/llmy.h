@@ -375,9 +375,12 @@ int32_t llmy_f32_to_bf16(const float* x, llmy_bf16* out, int64_t n, void* stream
  * slots per row, keys [B, C, H*head_dim], values [B, C, Dv], tag [B, C] int32 =
  * position + 1 of the summary (0 = empty). */
 
-/* Bytes of selection lists for `queries` queries: slots = the local window or
- * the memory slots (dense), or top_k pairs when top_k > 0; -1 on bad sizes. */
-int64_t llmy_cmp_workspace_bytes(int32_t queries, int32_t H, int32_t slots, int32_t top_k);
+/* Workspace bytes of one branch call for `queries` queries (prefill: B*T,
+ * decode: B): slots = the local window W or the memory's entries / slots;
+ * top_k 0 = dense lists, else top_k pairs; decode != 0 adds the raw scores the
+ * decode entries keep.  -1 on bad sizes. */
+int64_t llmy_cmp_workspace_bytes(int32_t queries, int32_t H, int32_t slots, int32_t top_k,
+                                 int32_t decode);
 /* Local branch over B fresh sequences of T tokens (rows b*T + t). */
 int32_t llmy_cmp_local_prefill_bf16(const llmy_bf16* q, int64_t q_ld, const llmy_bf16* k,
                                     int64_t k_ld, const llmy_bf16* v, int64_t v_ld,
