@@ -47,6 +47,10 @@ def sources() -> list[Path]:
 # one out and back; measured 12% faster, same results).
 FILE_FLAGS = {
     "attn_prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+    # gdn_chunk: the scan prefetches the next chunk's operands at the top of a
+    # chunk so the loads run behind its MFMAs; machine sinking would move them
+    # down next to their first use (the LDS stash at the chunk's end).
+    "gdn_chunk.hip": ["-mllvm", "-disable-machine-sink"],
 }
 
 

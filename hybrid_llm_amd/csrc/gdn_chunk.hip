@@ -403,9 +403,10 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(
 // Every fp32 operand enters the MFMA as a (hi, lo) bf16 pair made once: W and
 // A arrive split from kernel 1; the state slice lives in the registers of the
 // wave that owns each 16 x 16 tile and is split into a transposed LDS copy
-// after every update; U is split once into a transposed LDS tile, and
-// (Gamma_C/Gamma) o U is formed from that split where the state update reads
-// it.  Per chunk (tiles spread evenly over the waves):
+// after every update; U is split once into a transposed LDS tile, and so is
+// (Gamma_C/Gamma) o U from the fp32 U where LDS holds the extra tile (dk =
+// 128; with dk = 64 it is formed from the U split where the state update
+// reads it).  Per chunk (tiles spread evenly over the waves):
 //   U = U0 - W S
 //   O = Gamma Q S + A U                (bf16 out)
 //   S = Gamma_C S + K^T diag(Gamma_C / Gamma) U   (owner waves, registers)
@@ -438,7 +439,18 @@ __global__ __launch_bounds__(kScanThreads) void gdn_chunk_scan_kernel(
   __shared__ __align__(16) uint16_t KsT[DK * PT];                  // K^T [DK][64]
   __shared__ __align__(16) uint16_t SThi[DVS * PB], STlo[DVS * PB];  // S^T [DVS][DK]
   __shared__ __align__(16) uint16_t UThi[DVS * PT], UTlo[DVS * PT];  // U^T [DVS][64]
-  __shared__ float ecum[kC], dec[kC];  // per token: Gamma_t, Gamma_C / Gamma_t (kernel 1)
+  // (dec o U)^T [DVS][64], split once from the fp32 U where it fits: with
+  // dk = 64 two workgroups share a CU's LDS and the state update forms it from
+  // the U split instead
+  constexpr bool kDU = DK == 128;
+  __shared__ __align__(16) uint16_t DThi[kDU ? DVS * PT : 8], DTlo[kDU ? DVS * PT : 8];
+  // per token: Gamma_t, Gamma_C / Gamma_t (kernel 1), then one slot per thread
+  // past them: every thread stores its prefetched value, so no load of the
+  // loop is conditional and every wait on one counts a fixed number of
+  // memory operations after it
+  __shared__ float ecd[NT];
+  float* const ecum = ecd;
+  float* const dec = ecd + kC;
 
   const int per_xcd = (gridDim.x + 7) / 8;
   const int unit = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
@@ -488,13 +500,12 @@ __global__ __launch_bounds__(kScanThreads) void gdn_chunk_scan_kernel(
     const long long fkb = (static_cast<long long>(b) * T + ft0) * rk + static_cast<long long>(h) * DK; \
     _Pragma("unroll") for (int i = 0; i < KQ_N; ++i) {                                         \
       const int f = tid + NT * i;                                                              \
-      /* K: token fastest (conflict-free transposed stores); Q: row-major */                   \
+      /* K: token fastest (conflict-free transposed stores); Q: row-major.  Rows past */      \
+      /* the chunk re-read its last row (zeroed at the stash) */                               \
       const int tk = f % kC, ck = f / kC;                                                      \
       const int tq = f / (DK / 8), cq = f % (DK / 8);                                          \
-      pk[i] = tk < fTc ? *reinterpret_cast<const u32x4*>(k + fkb + tk * rk + 8 * ck)           \
-                       : u32x4{0u, 0u, 0u, 0u};                                                \
-      pq[i] = tq < fTc ? *reinterpret_cast<const u32x4*>(q + fkb + tq * rk + 8 * cq)           \
-                       : u32x4{0u, 0u, 0u, 0u};                                                \
+      pk[i] = *reinterpret_cast<const u32x4*>(k + fkb + min(tk, fTc - 1) * rk + 8 * ck);       \
+      pq[i] = *reinterpret_cast<const u32x4*>(q + fkb + min(tq, fTc - 1) * rk + 8 * cq);       \
     }                                                                                          \
     _Pragma("unroll") for (int i = 0; i < W_N; ++i)                                            \
       pw[i] = *reinterpret_cast<const u32x4*>(Wg + fcid * kC * DK * 2 + 8 * (tid + NT * i));   \
@@ -505,15 +516,18 @@ __global__ __launch_bounds__(kScanThreads) void gdn_chunk_scan_kernel(
       _Pragma("unroll") for (int i = 0; i < 4; ++i)                                            \
         pu_nxt[ot][i] = U0g[(fcid * kC + 16 * tm + 4 * g4 + i) * DV + DVS * sl + 16 * tn + r16]; \
     }                                                                                          \
-    pc = tid < 2 * kC ? edg[fcid * 2 * kC + tid] : 0.f;                                        \
+    pc = edg[fcid * 2 * kC + (tid & (2 * kC - 1))];                                            \
   } while (0)
-#define GDN_STASH()                                                                            \
+#define GDN_STASH(c_)                                                                          \
   do {                                                                                         \
+    const int sTc = min(kC, T - (c_) * kC);                                                    \
     _Pragma("unroll") for (int i = 0; i < KQ_N; ++i) {                                         \
       const int f = tid + NT * i;                                                              \
       const int tk = f % kC, ck = f / kC;                                                      \
       const int tq = f / (DK / 8), cq = f % (DK / 8);                                          \
-      *reinterpret_cast<u32x4*>(Qs + tq * PB + 8 * cq) = pq[i];                                \
+      if (tk >= sTc) pk[i] = u32x4{0u, 0u, 0u, 0u};                                            \
+      *reinterpret_cast<u32x4*>(Qs + tq * PB + 8 * cq) =                                       \
+          tq < sTc ? pq[i] : u32x4{0u, 0u, 0u, 0u};                                            \
       _Pragma("unroll") for (int jj = 0; jj < 8; ++jj)                                         \
         KsT[(8 * ck + jj) * PT + tk] = static_cast<uint16_t>(pk[i][jj >> 1] >> (16 * (jj & 1))); \
     }                                                                                          \
@@ -529,12 +543,11 @@ __global__ __launch_bounds__(kScanThreads) void gdn_chunk_scan_kernel(
       const int t = rem / kC, cc = rem % kC;                                                   \
       *reinterpret_cast<u32x4*>((pl ? Alo : Ahi) + t * PT + cc) = pa[i];                       \
     }                                                                                          \
-    if (tid < kC) ecum[tid] = pc;                                                              \
-    else if (tid < 2 * kC) dec[tid - kC] = pc;                                                 \
+    ecd[tid] = pc;                                                                             \
   } while (0)
 
   GDN_FETCH(0);
-  GDN_STASH();
+  GDN_STASH(0);
 #pragma unroll
   for (int ot = 0; ot < OT; ++ot)
 #pragma unroll
@@ -564,20 +577,34 @@ __global__ __launch_bounds__(kScanThreads) void gdn_chunk_scan_kernel(
         acc = mfma16(ah, blv, acc);
         acc = mfma16(al, bhv, acc);
       }
-      uint16_t uh[4], ul[4];
+      uint16_t uh[4], ul[4], dh[4], dl[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const float uval = pu[ot][i] - acc[i];
         uh[i] = f2bf(uval);
         ul[i] = f2bf(uval - bf2f(uh[i]));
+        if (kDU) {
+          const float dval = dec[16 * tm + 4 * g4 + i] * uval;
+          dh[i] = f2bf(dval);
+          dl[i] = f2bf(dval - bf2f(dh[i]));
+        }
       }
       const int off = (16 * tn + r16) * PT + 16 * tm + 4 * g4;
       *reinterpret_cast<uint2*>(UThi + off) = uint2{pack_bf2u(uh[0], uh[1]), pack_bf2u(uh[2], uh[3])};
       *reinterpret_cast<uint2*>(UTlo + off) = uint2{pack_bf2u(ul[0], ul[1]), pack_bf2u(ul[2], ul[3])};
+      if (kDU) {
+        *reinterpret_cast<uint2*>(DThi + off) = uint2{pack_bf2u(dh[0], dh[1]), pack_bf2u(dh[2], dh[3])};
+        *reinterpret_cast<uint2*>(DTlo + off) = uint2{pack_bf2u(dl[0], dl[1]), pack_bf2u(dl[2], dl[3])};
+      }
     }
     __syncthreads();  // U^T, (dec o U)^T complete
 
-    // ---- O = Gamma (Q S) + A U
+    // ---- O = Gamma (Q S) + A U, stored through a buffer resource over the
+    // chunk's rows of this slice: a token past the chunk lies beyond its range
+    // and the store is dropped, so every lane stores (no branch)
+    const __amdgpu_buffer_rsrc_t orsrc = __builtin_amdgcn_make_buffer_rsrc(
+        out + (static_cast<long long>(b) * T + t0) * rv + static_cast<long long>(h) * DV + DVS * sl,
+        static_cast<short>(0), static_cast<int>(((Tc - 1) * rv + DVS) * 2), 0x00020000);
 #pragma unroll
     for (int ot = 0; ot < OT; ++ot) {
       const int tt = OT * wave + ot, tm = tt / NTN, tn = tt % NTN;
@@ -603,11 +630,9 @@ __global__ __launch_bounds__(kScanThreads) void gdn_chunk_scan_kernel(
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int t = 16 * tm + 4 * g4 + i;
-        if (t < Tc) {
-          const float o = ecum[t] * qs[i] + au[i];
-          out[(static_cast<long long>(b) * T + t0 + t) * rv + static_cast<long long>(h) * DV +
-              DVS * sl + 16 * tn + r16] = f2bf(o);
-        }
+        const float o = ecum[t] * qs[i] + au[i];
+        __builtin_amdgcn_raw_buffer_store_b16(f2bf(o), orsrc,
+                                              static_cast<int>((t * rv + 16 * tn + r16) * 2), 0, 0);
       }
     }
     // ---- S = Gamma_C S + K^T (dec o U): the owner wave updates its tiles in registers
@@ -619,19 +644,23 @@ __global__ __launch_bounds__(kScanThreads) void gdn_chunk_scan_kernel(
       for (int s = 0; s < kC / 32; ++s) {
         const uint4 ka = *reinterpret_cast<const uint4*>(KsT + (16 * tm + r16) * PT + 32 * s + 8 * g4);
         const int bo = (16 * tn + r16) * PT + 32 * s + 8 * g4;
-        // B operand (dec o U)^T: dec[t] (U_hi + U_lo) for the 8 tokens of the
-        // fragment, split again into (hi, lo) bf16
-        const uint4 uhv = *reinterpret_cast<const uint4*>(UThi + bo);
-        const uint4 ulv = *reinterpret_cast<const uint4*>(UTlo + bo);
-        float hf[8], lf[8], dv[8];
-        unpack8(uhv, hf);
-        unpack8(ulv, lf);
+        if (kDU) {
+          acc = mfma16(ka, *reinterpret_cast<const uint4*>(DThi + bo), acc);
+          acc = mfma16(ka, *reinterpret_cast<const uint4*>(DTlo + bo), acc);
+        } else {
+          // dec[t] (U_hi + U_lo) for the fragment's 8 tokens, split again
+          const uint4 uhv = *reinterpret_cast<const uint4*>(UThi + bo);
+          const uint4 ulv = *reinterpret_cast<const uint4*>(UTlo + bo);
+          float hf[8], lf[8], dv[8];
+          unpack8(uhv, hf);
+          unpack8(ulv, lf);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) dv[j] = dec[32 * s + 8 * g4 + j] * (hf[j] + lf[j]);
-        uint4 dhv, dlv;
-        split8(dv, dhv, dlv);
-        acc = mfma16(ka, dhv, acc);
-        acc = mfma16(ka, dlv, acc);
+          for (int j = 0; j < 8; ++j) dv[j] = dec[32 * s + 8 * g4 + j] * (hf[j] + lf[j]);
+          uint4 dhv, dlv;
+          split8(dv, dhv, dlv);
+          acc = mfma16(ka, dhv, acc);
+          acc = mfma16(ka, dlv, acc);
+        }
       }
 #pragma unroll
       for (int i = 0; i < 4; ++i) sreg[u][i] = gc * sreg[u][i] + acc[i];
@@ -639,7 +668,7 @@ __global__ __launch_bounds__(kScanThreads) void gdn_chunk_scan_kernel(
     __syncthreads();  // every wave is done with this chunk's LDS operands and S^T
     GDN_SPLIT_STATE();
     if (c + 1 < NC) {
-      GDN_STASH();
+      GDN_STASH(c + 1);
 #pragma unroll
       for (int ot = 0; ot < OT; ++ot)
 #pragma unroll
@@ -657,6 +686,335 @@ __global__ __launch_bounds__(kScanThreads) void gdn_chunk_scan_kernel(
 #undef GDN_SPLIT_STATE
 #undef GDN_FETCH
 #undef GDN_STASH
+}
+
+
+// Kernel 2 for dk = dv = 128 (64-column state slices): the algebra of
+// gdn_chunk_scan_kernel with the eight waves in two groups of four, each wave
+// owning 32 x 32 blocks (2 x 2 tiles of 16 x 16), so every fragment read from
+// LDS feeds two MFMAs:
+//   phase 1  waves 0-3: U = U0 - W S (one block each), split into U^T and
+//            (dec o U)^T;  waves 4-7: Q S (one block each), kept in registers
+//   phase 2  waves 0-3: S = Gamma_C S + K^T (dec o U) on the 2 x 4 state tiles
+//            each owns (32 rows of the slice), then the transposed (hi, lo)
+//            copy for the next chunk;  waves 4-7: O = Gamma (Q S) + A U (A is
+//            causal: the first token block skips the second half of A)
+//   then the next chunk's operands go to LDS.
+// The next chunk's K, Q and W are fetched at the start of a chunk, its A, U0
+// and decay factors after phase 1, so the loads drain behind the MFMAs.  Every
+// wave issues the same memory operations in the same order in every
+// iteration (waves 4-7 load the U0 tiles of waves 0-3 too; waves 0-3 issue the
+// output stores of waves 4-7 with offsets past the
+// buffer, which the hardware drops; the last chunk fetches itself again), so
+// each wait for a load counts a fixed number of operations after it and the
+// loads of the next chunk stay in flight across it.
+template <int DK, int DV, int DVS>
+__global__ __launch_bounds__(kScanThreads) void gdn_chunk_scan_blocked_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
+    const uint16_t* __restrict__ Wg, const float* __restrict__ U0g, const uint16_t* __restrict__ Ag,
+    const float* __restrict__ edg, float* __restrict__ state, uint16_t* __restrict__ out, int T,
+    int H, int NC, int n_units) {
+  static_assert(DK == 128 && DVS == 64, "blocked scan: dk = 128, 64-column slices");
+  constexpr int NSL = DV / DVS;
+  constexpr int PB = DK + 8, PT = kC + 8, NT = kScanThreads;
+  constexpr int KQ_N = kC * DK / 8 / NT;     // uint4 of K (and of Q) per thread
+  constexpr int W_N = 2 * kC * DK / 8 / NT;  // uint4 of W (hi and lo planes) per thread
+  constexpr int A_N = 2 * kC * kC / 8 / NT;  // uint4 of A (hi and lo planes) per thread
+  static_assert(KQ_N == 2 && W_N == 4 && A_N == 2, "tile split");
+  __shared__ __align__(16) uint16_t Whi[kC * PB], Wlo[kC * PB], Qs[kC * PB];
+  __shared__ __align__(16) uint16_t Ahi[kC * PT], Alo[kC * PT];
+  __shared__ __align__(16) uint16_t KsT[DK * PT];                  // K^T [DK][64]
+  __shared__ __align__(16) uint16_t SThi[DVS * PB], STlo[DVS * PB];  // S^T [DVS][DK]
+  __shared__ __align__(16) uint16_t UThi[DVS * PT], UTlo[DVS * PT];  // U^T [DVS][64]
+  __shared__ __align__(16) uint16_t DThi[DVS * PT], DTlo[DVS * PT];  // (dec o U)^T
+  __shared__ float ecd[NT];  // Gamma_t, Gamma_C / Gamma_t, then one slot per thread
+  float* const ecum = ecd;
+  float* const dec = ecd + kC;
+
+  const int per_xcd = (gridDim.x + 7) / 8;
+  const int unit = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+  if (unit >= n_units) return;
+  const int bh = unit / NSL;
+  const int sl = unit - bh * NSL;
+  const int b = bh / H, h = bh - (bh / H) * H;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int grp = wave >> 2, wi = wave & 3;
+  const int bm = wi >> 1, bn = wi & 1;  // phase-1 block: token tiles 2bm, 2bm+1; column tiles 2bn, 2bn+1
+  const int r16 = lane & 15, g4 = lane >> 4;
+  const long long rk = static_cast<long long>(H) * DK, rv = static_cast<long long>(H) * DV;
+  float* Sg = state + (static_cast<long long>(bh) * DK) * DV + DVS * sl;
+
+  // ---- state tiles of waves 0-3: d tiles 2 wi + a, column tiles c (D layout)
+  f32x4 sreg[2][4];
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)  // (waves 4-7 read the same tiles and never use them)
+        sreg[a][c][i] = Sg[static_cast<long long>(16 * (2 * wi + a) + 4 * g4 + i) * DV + 16 * c + r16];
+  auto split_state = [&]() {
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        uint16_t hh[4], ll[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          hh[i] = f2bf(sreg[a][c][i]);
+          ll[i] = f2bf(sreg[a][c][i] - bf2f(hh[i]));
+        }
+        const int off = (16 * c + r16) * PB + 16 * (2 * wi + a) + 4 * g4;
+        *reinterpret_cast<uint2*>(SThi + off) = uint2{pack_bf2u(hh[0], hh[1]), pack_bf2u(hh[2], hh[3])};
+        *reinterpret_cast<uint2*>(STlo + off) = uint2{pack_bf2u(ll[0], ll[1]), pack_bf2u(ll[2], ll[3])};
+      }
+  };
+  if (grp == 0) split_state();
+
+  // ---- prefetch registers
+  u32x4 pk[KQ_N], pq[KQ_N], pw[W_N], pa[A_N];
+  float pu[2][2][4], pc;  // U0 of the next chunk is loaded into pu after phase 1 reads it
+  auto fetch1 = [&](int c_) {  // K, Q (rows past the chunk re-read its last row), W
+    const int ft0 = c_ * kC;
+    const int fTc = min(kC, T - ft0);
+    const long long fcid = static_cast<long long>(bh) * NC + c_;
+    const long long fkb = (static_cast<long long>(b) * T + ft0) * rk + static_cast<long long>(h) * DK;
+#pragma unroll
+    for (int i = 0; i < KQ_N; ++i) {
+      const int f = tid + NT * i;
+      const int tk = f % kC, ck = f / kC;
+      const int tq = f / (DK / 8), cq = f % (DK / 8);
+      pk[i] = *reinterpret_cast<const u32x4*>(k + fkb + min(tk, fTc - 1) * rk + 8 * ck);
+      pq[i] = *reinterpret_cast<const u32x4*>(q + fkb + min(tq, fTc - 1) * rk + 8 * cq);
+    }
+#pragma unroll
+    for (int i = 0; i < W_N; ++i)
+      pw[i] = *reinterpret_cast<const u32x4*>(Wg + fcid * kC * DK * 2 + 8 * (tid + NT * i));
+  };
+  auto fetch2 = [&](int c_) {  // A, decay factors, U0 (after phase 1, which reads pu)
+    const long long fcid = static_cast<long long>(bh) * NC + c_;
+#pragma unroll
+    for (int i = 0; i < A_N; ++i)
+      pa[i] = *reinterpret_cast<const u32x4*>(Ag + fcid * kC * kC * 2 + 8 * (tid + NT * i));
+    pc = edg[fcid * 2 * kC + (tid & (2 * kC - 1))];
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)  // (waves 4-7 load the tiles of waves 0-3 and never use them)
+          pu[a][c][i] = U0g[(fcid * kC + 16 * (2 * bm + a) + 4 * g4 + i) * DV + DVS * sl +
+                            16 * (2 * bn + c) + r16];
+  };
+  auto stash = [&](int c_) {
+    const int sTc = min(kC, T - c_ * kC);
+#pragma unroll
+    for (int i = 0; i < KQ_N; ++i) {
+      const int f = tid + NT * i;
+      const int tk = f % kC, ck = f / kC;
+      const int tq = f / (DK / 8), cq = f % (DK / 8);
+      const u32x4 kv = tk < sTc ? pk[i] : u32x4{0u, 0u, 0u, 0u};
+      *reinterpret_cast<u32x4*>(Qs + tq * PB + 8 * cq) = tq < sTc ? pq[i] : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj)
+        KsT[(8 * ck + jj) * PT + tk] = static_cast<uint16_t>(kv[jj >> 1] >> (16 * (jj & 1)));
+    }
+#pragma unroll
+    for (int i = 0; i < W_N; ++i) {
+      const int f = 8 * (tid + NT * i);
+      const int pl = f / (kC * DK), rem = f % (kC * DK);
+      *reinterpret_cast<u32x4*>((pl ? Wlo : Whi) + (rem / DK) * PB + rem % DK) = pw[i];
+    }
+#pragma unroll
+    for (int i = 0; i < A_N; ++i) {
+      const int f = 8 * (tid + NT * i);
+      const int pl = f / (kC * kC), rem = f % (kC * kC);
+      *reinterpret_cast<u32x4*>((pl ? Alo : Ahi) + (rem / kC) * PT + rem % kC) = pa[i];
+    }
+    ecd[tid] = pc;
+  };
+
+  fetch1(0);
+  fetch2(0);
+  stash(0);
+  __syncthreads();
+  for (int c = 0; c < NC; ++c) {
+    const int t0 = c * kC;
+    const int Tc = min(kC, T - t0);
+    const float gc = ecum[kC - 1];  // Gamma_C (0 when the chunk resets)
+    // the last chunk fetches itself again (never stored), so every iteration
+    // issues the same loads and each wait counts the same operations after it
+    const int cn = min(c + 1, NC - 1);
+    fetch1(cn);
+
+    // ---- phase 1
+    f32x4 acc[2][2];
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+      for (int cc = 0; cc < 2; ++cc) acc[a][cc] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (grp == 0) {
+      // U = U0 - W S on token tiles 2bm + a, column tiles 2bn + cc
+#pragma unroll
+      for (int s = 0; s < DK / 32; ++s) {
+        uint4 ah[2], al[2], bhv[2], blv[2];
+#pragma unroll
+        for (int a = 0; a < 2; ++a) {
+          const int ao = (16 * (2 * bm + a) + r16) * PB + 32 * s + 8 * g4;
+          ah[a] = *reinterpret_cast<const uint4*>(Whi + ao);
+          al[a] = *reinterpret_cast<const uint4*>(Wlo + ao);
+          const int bo = (16 * (2 * bn + a) + r16) * PB + 32 * s + 8 * g4;
+          bhv[a] = *reinterpret_cast<const uint4*>(SThi + bo);
+          blv[a] = *reinterpret_cast<const uint4*>(STlo + bo);
+        }
+#pragma unroll
+        for (int a = 0; a < 2; ++a)
+#pragma unroll
+          for (int cc = 0; cc < 2; ++cc) {
+            acc[a][cc] = mfma16(ah[a], bhv[cc], acc[a][cc]);
+            acc[a][cc] = mfma16(ah[a], blv[cc], acc[a][cc]);
+            acc[a][cc] = mfma16(al[a], bhv[cc], acc[a][cc]);
+          }
+      }
+#pragma unroll
+      for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int cc = 0; cc < 2; ++cc) {
+          const int tm = 2 * bm + a, tn = 2 * bn + cc;
+          uint16_t uh[4], ul[4], dh[4], dl[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float uval = pu[a][cc][i] - acc[a][cc][i];
+            uh[i] = f2bf(uval);
+            ul[i] = f2bf(uval - bf2f(uh[i]));
+            const float dval = dec[16 * tm + 4 * g4 + i] * uval;
+            dh[i] = f2bf(dval);
+            dl[i] = f2bf(dval - bf2f(dh[i]));
+          }
+          const int off = (16 * tn + r16) * PT + 16 * tm + 4 * g4;
+          *reinterpret_cast<uint2*>(UThi + off) = uint2{pack_bf2u(uh[0], uh[1]), pack_bf2u(uh[2], uh[3])};
+          *reinterpret_cast<uint2*>(UTlo + off) = uint2{pack_bf2u(ul[0], ul[1]), pack_bf2u(ul[2], ul[3])};
+          *reinterpret_cast<uint2*>(DThi + off) = uint2{pack_bf2u(dh[0], dh[1]), pack_bf2u(dh[2], dh[3])};
+          *reinterpret_cast<uint2*>(DTlo + off) = uint2{pack_bf2u(dl[0], dl[1]), pack_bf2u(dl[2], dl[3])};
+        }
+    } else {
+      // Q S on token tiles 2bm + a, column tiles 2bn + cc (kept in acc)
+#pragma unroll
+      for (int s = 0; s < DK / 32; ++s) {
+        uint4 qa[2], bhv[2], blv[2];
+#pragma unroll
+        for (int a = 0; a < 2; ++a) {
+          qa[a] = *reinterpret_cast<const uint4*>(Qs + (16 * (2 * bm + a) + r16) * PB + 32 * s + 8 * g4);
+          const int bo = (16 * (2 * bn + a) + r16) * PB + 32 * s + 8 * g4;
+          bhv[a] = *reinterpret_cast<const uint4*>(SThi + bo);
+          blv[a] = *reinterpret_cast<const uint4*>(STlo + bo);
+        }
+#pragma unroll
+        for (int a = 0; a < 2; ++a)
+#pragma unroll
+          for (int cc = 0; cc < 2; ++cc) {
+            acc[a][cc] = mfma16(qa[a], bhv[cc], acc[a][cc]);
+            acc[a][cc] = mfma16(qa[a], blv[cc], acc[a][cc]);
+          }
+      }
+    }
+    __syncthreads();  // U^T and (dec o U)^T complete; every read of S^T done
+    fetch2(cn);
+
+    // ---- phase 2; output rows past the chunk lie beyond the buffer range
+    const __amdgpu_buffer_rsrc_t orsrc = __builtin_amdgcn_make_buffer_rsrc(
+        out + (static_cast<long long>(b) * T + t0) * rv + static_cast<long long>(h) * DV + DVS * sl,
+        static_cast<short>(0), static_cast<int>(((Tc - 1) * rv + DVS) * 2), 0x00020000);
+    if (grp == 0) {
+      // S = Gamma_C S + K^T (dec o U) on d tiles 2 wi + a, column tiles c,
+      // accumulated onto the decayed state in place
+#pragma unroll
+      for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int cc = 0; cc < 4; ++cc)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) sreg[a][cc][i] *= gc;
+#pragma unroll
+      for (int s = 0; s < kC / 32; ++s) {
+        uint4 ka[2];
+#pragma unroll
+        for (int a = 0; a < 2; ++a)
+          ka[a] = *reinterpret_cast<const uint4*>(KsT + (16 * (2 * wi + a) + r16) * PT + 32 * s + 8 * g4);
+#pragma unroll
+        for (int cc = 0; cc < 4; ++cc) {
+          const int bo = (16 * cc + r16) * PT + 32 * s + 8 * g4;
+          const uint4 dhv = *reinterpret_cast<const uint4*>(DThi + bo);
+          const uint4 dlv = *reinterpret_cast<const uint4*>(DTlo + bo);
+#pragma unroll
+          for (int a = 0; a < 2; ++a) {
+            sreg[a][cc] = mfma16(ka[a], dhv, sreg[a][cc]);
+            sreg[a][cc] = mfma16(ka[a], dlv, sreg[a][cc]);
+          }
+        }
+      }
+      split_state();
+      // the output stores of waves 4-7, past the buffer range (dropped)
+#pragma unroll
+      for (int j = 0; j < 16; ++j)
+        __builtin_amdgcn_raw_buffer_store_b16(static_cast<uint16_t>(j), orsrc, 0x7fffff00 + 2 * j, 0,
+                                              0);
+    } else {
+      // O = Gamma (Q S) + A U on token tiles 2bm + a, column tiles 2bn + cc
+      f32x4 au[2][2];
+#pragma unroll
+      for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int cc = 0; cc < 2; ++cc) au[a][cc] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < kC / 32; ++s) {
+        if (s > bm) break;  // token tiles 0, 1 see no token of the second half
+        uint4 ah[2], al[2], uhv[2], ulv[2];
+#pragma unroll
+        for (int a = 0; a < 2; ++a) {
+          const int ao = (16 * (2 * bm + a) + r16) * PT + 32 * s + 8 * g4;
+          ah[a] = *reinterpret_cast<const uint4*>(Ahi + ao);
+          al[a] = *reinterpret_cast<const uint4*>(Alo + ao);
+          const int bo = (16 * (2 * bn + a) + r16) * PT + 32 * s + 8 * g4;
+          uhv[a] = *reinterpret_cast<const uint4*>(UThi + bo);
+          ulv[a] = *reinterpret_cast<const uint4*>(UTlo + bo);
+        }
+#pragma unroll
+        for (int a = 0; a < 2; ++a)
+#pragma unroll
+          for (int cc = 0; cc < 2; ++cc) {
+            au[a][cc] = mfma16(ah[a], uhv[cc], au[a][cc]);
+            au[a][cc] = mfma16(ah[a], ulv[cc], au[a][cc]);
+            au[a][cc] = mfma16(al[a], uhv[cc], au[a][cc]);
+          }
+      }
+#pragma unroll
+      for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int cc = 0; cc < 2; ++cc)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int t = 16 * (2 * bm + a) + 4 * g4 + i;
+            const float o = ecum[t] * acc[a][cc][i] + au[a][cc][i];
+            __builtin_amdgcn_raw_buffer_store_b16(
+                f2bf(o), orsrc, static_cast<int>((t * rv + 16 * (2 * bn + cc) + r16) * 2), 0, 0);
+          }
+    }
+    __syncthreads();  // every wave is done with this chunk's LDS operands; S^T updated
+    if (c + 1 < NC) {
+      stash(c + 1);
+      __syncthreads();
+    }
+  }
+  if (grp == 0) {
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          Sg[static_cast<long long>(16 * (2 * wi + a) + 4 * g4 + i) * DV + 16 * c + r16] = sreg[a][c][i];
+  }
 }
 
 }  // namespace llmy
@@ -702,7 +1060,7 @@ int32_t gdn_prefill_launch(const llmy_bf16* q, const llmy_bf16* k, const llmy_bf
     int32_t st = launch_status();
     if (st != 0) return st;
     const int units = B * H * (128 / 64);
-    hipLaunchKernelGGL((gdn_chunk_scan_kernel<128, 128, 64>), dim3((units + 7) / 8 * 8),
+    hipLaunchKernelGGL((gdn_chunk_scan_blocked_kernel<128, 128, 64>), dim3((units + 7) / 8 * 8),
                        dim3(kScanThreads), 0, s, q, k, W, U0, A, ed, state, out, T, H, NC, units);
   }
   return launch_status();

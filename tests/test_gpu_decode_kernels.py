@@ -411,6 +411,8 @@ def test_gdn_step_with_fused_conv_gate():
 @pytest.mark.parametrize("T,E,D,H", [(64, 24, 512, 512), (1, 8, 512, 512), (300, 24, 512, 512),
                                      # C5 decode shape: down K = 2048 is two pieces per wave
                                      (64, 24, 1024, 2048),
+                                     # down K = 1024 and 4096: one and four pieces per wave
+                                     (48, 12, 512, 1024), (32, 8, 256, 4096),
                                      # about 16 routes per expert: several 16-route chunks
                                      (64, 8, 512, 512), (20, 24, 256, 512)])
 def test_moe_routed_equals_sorted(T, E, D, H):
