@@ -81,8 +81,9 @@ __device__ __forceinline__ f32x4 mfma16(const uint4& a, const uint4& b, f32x4 c)
 
 // ---------------------------------------------------------------------------
 // Kernel 1: per-chunk preparation.  Scratch layout per chunk id
-// cid = (b*H + h) * NC + c:  W [64][DK], U0 [64][DV], A [64][64], decay
-// factors [2][64] (e_t then d_t, fp32).  reset [B, T] or null.
+// cid = (b*H + h) * NC + c:  W [64][DK], U0 [64][DV] (dk = 128: in the scan's
+// fragment order, [64-column slice][16 x 16 tile][lane][4 rows]), A [64][64],
+// decay factors [2][64] (e_t then d_t, fp32).  reset [B, T] or null.
 template <int DK, int DV>
 __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
@@ -119,16 +120,29 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(
   const long long kbase = (static_cast<long long>(b) * T + t0) * rk + static_cast<long long>(h) * DK;
   const long long vbase = (static_cast<long long>(b) * T + t0) * rv + static_cast<long long>(h) * DV;
 
-  // ---- stage K and Q rows, and K, V transposed; padded rows are zero
-  for (int f = threadIdx.x; f < kC * (DK / 8); f += 256) {
-    const int t = f / (DK / 8), cc = f - t * (DK / 8);
-    uint4 kv = uint4{0u, 0u, 0u, 0u}, qv = uint4{0u, 0u, 0u, 0u};
-    if (t < Tc) {
-      kv = *reinterpret_cast<const uint4*>(k + kbase + t * rk + 8 * cc);
-      qv = *reinterpret_cast<const uint4*>(q + kbase + t * rk + 8 * cc);
+  // ---- stage K and Q rows; padded rows are zero.  Every load is issued
+  // before the first store (rows past the chunk re-read its last row).
+  constexpr int SN = kC * (DK / 8) / 256;
+  static_assert(SN * 256 == kC * (DK / 8), "staging split");
+  {
+    uint4 skv[SN], sqv[SN];
+#pragma unroll
+    for (int i = 0; i < SN; ++i) {
+      const int f = threadIdx.x + 256 * i;
+      const int t = f / (DK / 8), cc = f - t * (DK / 8);
+      const int tr = min(t, Tc - 1);
+      skv[i] = *reinterpret_cast<const uint4*>(k + kbase + tr * rk + 8 * cc);
+      sqv[i] = *reinterpret_cast<const uint4*>(q + kbase + tr * rk + 8 * cc);
     }
-    *reinterpret_cast<uint4*>(Ks + t * PK + 8 * cc) = kv;
-    *reinterpret_cast<uint4*>(Qs + t * PK + 8 * cc) = qv;
+#pragma unroll
+    for (int i = 0; i < SN; ++i) {
+      const int f = threadIdx.x + 256 * i;
+      const int t = f / (DK / 8), cc = f - t * (DK / 8);
+      uint4 kv = skv[i], qv = sqv[i];
+      if (t >= Tc) kv = qv = uint4{0u, 0u, 0u, 0u};
+      *reinterpret_cast<uint4*>(Ks + t * PK + 8 * cc) = kv;
+      *reinterpret_cast<uint4*>(Qs + t * PK + 8 * cc) = qv;
+    }
   }
   if (wave == 0) {
     // inclusive prefix sum of log g over the chunk (padded tokens: g = 1, beta = 0)
@@ -160,12 +174,12 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(
     prv[lane] = sc - lg;
     bet[lane] = bt;
     seg[lane] = sg;
-    wsc[lane] = sg == 0 ? bt * expf(sc - lg) : 0.f;
+    wsc[lane] = sg == 0 ? bt * __expf(sc - lg) : 0.f;
   }
   __syncthreads();
 
   // ---- K K^T and Q K^T (exact): wave w owns output row block w, 4 column
-  // blocks.  K K^T goes to LDS (for L); A = (Gamma_t / Gamma_i) q_t . k_i
+  // blocks.  K K^T becomes L in LDS; A = (Gamma_t / Gamma_i) q_t . k_i
   // (i <= t) is formed in registers and written as (hi, lo) bf16 planes.
   const long long wo = static_cast<long long>(cid) * kC;
 #pragma unroll
@@ -179,10 +193,12 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(
       a1 = mfma16(ka, kb, a1);
       a2 = mfma16(kb, qa, a2);  // (K Q^T) block: lane holds 4 consecutive j of row t
     }
+    // L[t, j] = beta_t (Gamma_{t-1} / Gamma_j) k_t . k_j for j < t in the same
+    // segment (strictly lower), formed from the K K^T block in registers
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int t = 16 * wave + 4 * g4 + i, j = 16 * tj + r16;
-      Gm[t * PG + j] = a1[i];
+      Gm[t * PG + j] = j < t && seg[j] == seg[t] ? bet[t] * __expf(prv[t] - cum[j]) * a1[i] : 0.f;
     }
     {
       const int t = 16 * wave + r16, j0 = 16 * tj + 4 * g4;
@@ -190,7 +206,7 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int j = j0 + i;
-        const float am = j <= t && seg[j] == seg[t] ? expf(cum[t] - cum[j]) * a2[i] : 0.f;
+        const float am = j <= t && seg[j] == seg[t] ? __expf(cum[t] - cum[j]) * a2[i] : 0.f;
         hv[i] = f2bf(am);
         lv[i] = f2bf(am - bf2f(hv[i]));
       }
@@ -224,29 +240,30 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(
       vp[i][e] = *reinterpret_cast<const uint4*>(v + vbase + min(t2 + e, Tc - 1) * rv + 8 * cc);
   }
   __syncthreads();
-  // ---- L (strictly lower)
-  for (int e = threadIdx.x; e < kC * kC; e += 256) {
-    const int t = e >> 6, i = e & 63;
-    Gm[t * PG + i] = i < t && seg[i] == seg[t] ? bet[t] * expf(prv[t] - cum[i]) * Gm[t * PG + i]
-                                               : 0.f;
-  }
-  __syncthreads();
   // ---- (I + L)^{-1}, blocked by 16: N = I + L is unit lower triangular with
   // 16 x 16 blocks N_ij; T = N^{-1} has T_ii = N_ii^{-1} and, for i > j,
   // T_ij = -T_ii * sum_{m=j}^{i-1} N_im T_mj.  Wave w inverts diagonal block w
-  // by forward substitution (lanes 0..15 own its columns), then the three
-  // off-diagonal levels i - j = 1, 2, 3 are 16 x 16 products, one block per
-  // wave and level.
+  // by forward substitution (lanes 0..15 own its columns; the block's 120
+  // entries are read from LDS into registers first, so the substitution waits
+  // on no read), then the three off-diagonal levels i - j = 1, 2, 3 are 16 x 16
+  // products on fp32 MFMA (v_mfma_f32_16x16x4_f32: A lane l holds
+  // A[l % 16][l / 16], B lane l holds B[l / 16][l % 16], D lane l holds
+  // D[4 (l / 16) + r][l % 16]), one block per wave and level.
   {
     const int d0 = 16 * wave;
     if (lane < 16) {
       const int j = lane;
+      float nv[120];  // N[d0 + t][d0 + i], i < t, at t (t - 1) / 2 + i
+#pragma unroll
+      for (int t = 1; t < 16; ++t)
+#pragma unroll
+        for (int i = 0; i < t; ++i) nv[t * (t - 1) / 2 + i] = Gm[(d0 + t) * PG + d0 + i];
       float x[16];
 #pragma unroll
       for (int t = 0; t < 16; ++t) {
         float a = (t == j) ? 1.f : 0.f;
 #pragma unroll
-        for (int i = 0; i < t; ++i) a -= Gm[(d0 + t) * PG + d0 + i] * x[i];
+        for (int i = 0; i < t; ++i) a -= nv[t * (t - 1) / 2 + i] * x[i];
         x[t] = t < j ? 0.f : a;
         Ti[(d0 + t) * PG + d0 + j] = x[t];
       }
@@ -257,43 +274,34 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(
       if ((i >> 4) > (t >> 4)) Ti[t * PG + i] = 0.f;
     }
     __syncthreads();
+    const int c16 = lane & 15, k4 = lane >> 4;
 #pragma unroll
     for (int lvl = 1; lvl < 4; ++lvl) {
       const int bi = wave, bj = wave - lvl;  // block (bi, bj), bi - bj = lvl
-      float p[4];
       if (bj >= 0) {
-        // lane l: rows r = 4 (l / 16) + 0..3 of P = sum_m N_{bi,m} T_{m,bj}, column c = l % 16
-        const int c = lane & 15, r0 = 4 * (lane >> 4);
-#pragma unroll
-        for (int u = 0; u < 4; ++u) p[u] = 0.f;
+        // P = sum_m N_{bi,m} T_{m,bj}, kept in this wave's rows of Pm (only
+        // this wave reads them, and its LDS operations complete in order)
+        f32x4 p = f32x4{0.f, 0.f, 0.f, 0.f};
         for (int m = bj; m < bi; ++m) {
 #pragma unroll
-          for (int kk = 0; kk < 16; ++kk) {
-            const float tv = Ti[(16 * m + kk) * PG + 16 * bj + c];
-#pragma unroll
-            for (int u = 0; u < 4; ++u) p[u] += Gm[(16 * bi + r0 + u) * PG + 16 * m + kk] * tv;
+          for (int c4 = 0; c4 < 4; ++c4) {
+            const float av = Gm[(16 * bi + c16) * PG + 16 * m + 4 * c4 + k4];
+            const float bv = Ti[(16 * m + 4 * c4 + k4) * PG + 16 * bj + c16];
+            p = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, p, 0, 0, 0);
           }
         }
-      }
-      __syncthreads();
-      if (bj >= 0) {
-        const int c = lane & 15, r0 = 4 * (lane >> 4);
 #pragma unroll
-        for (int u = 0; u < 4; ++u) Pm[(16 * wave + r0 + u) * 17 + c] = p[u];
-      }
-      __syncthreads();
-      if (bj >= 0) {
+        for (int r = 0; r < 4; ++r) Pm[(16 * wave + 4 * k4 + r) * 17 + c16] = p[r];
         // T_{bi,bj} = -T_{bi,bi} P
-        const int c = lane & 15, r0 = 4 * (lane >> 4);
-        float o[4] = {0.f, 0.f, 0.f, 0.f};
+        f32x4 o = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int kk = 0; kk < 16; ++kk) {
-          const float pv = Pm[(16 * wave + kk) * 17 + c];
-#pragma unroll
-          for (int u = 0; u < 4; ++u) o[u] += Ti[(16 * bi + r0 + u) * PG + 16 * bi + kk] * pv;
+        for (int c4 = 0; c4 < 4; ++c4) {
+          const float av = Ti[(16 * bi + c16) * PG + 16 * bi + 4 * c4 + k4];
+          const float bv = Pm[(16 * wave + 4 * c4 + k4) * 17 + c16];
+          o = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, o, 0, 0, 0);
         }
 #pragma unroll
-        for (int u = 0; u < 4; ++u) Ti[(16 * bi + r0 + u) * PG + 16 * bj + c] = -o[u];
+        for (int r = 0; r < 4; ++r) Ti[(16 * bi + 4 * k4 + r) * PG + 16 * bj + c16] = -o[r];
       }
       __syncthreads();
     }
@@ -359,10 +367,17 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(
         for (int s = 0; s < kC / 32; ++s) {
           const uint4 bb = *reinterpret_cast<const uint4*>(
               (isW ? KsT : VsT) + (16 * tn + r16) * PT + 32 * s + 8 * g4);
-          // transposed product (B^T A^T): lane l ends with row 16 tm + l % 16
-          // and the 4 consecutive columns 16 tn + 4 (l / 16) .. +3
-          acc = mfma16(bb, ahi[s], acc);
-          acc = mfma16(bb, alo[s], acc);
+          if (isW || DK != 128) {
+            // transposed product (B^T A^T): lane l ends with row 16 tm + l % 16
+            // and the 4 consecutive columns 16 tn + 4 (l / 16) .. +3
+            acc = mfma16(bb, ahi[s], acc);
+            acc = mfma16(bb, alo[s], acc);
+          } else {
+            // U0 for the dk = 128 scan: lane l ends with rows 16 tm + 4 (l / 16)
+            // .. +3 of column 16 tn + l % 16 (the scan's fragment order)
+            acc = mfma16(ahi[s], bb, acc);
+            acc = mfma16(alo[s], bb, acc);
+          }
         }
         const int col0 = 16 * tn + 4 * g4;
         if (isW) {
@@ -378,8 +393,13 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(
               make_uint2(pack_bf2u(hv[0], hv[1]), pack_bf2u(hv[2], hv[3]));
           *reinterpret_cast<uint2*>(whi + kC * DK) =
               make_uint2(pack_bf2u(lv[0], lv[1]), pack_bf2u(lv[2], lv[3]));
-        } else {
+        } else if (DK != 128) {
           *reinterpret_cast<float4*>(U0g + wo * DV + row * DV + col0) =
+              make_float4(acc[0], acc[1], acc[2], acc[3]);
+        } else {
+          // [64-column slice][16 x 16 tile (row, column) of the slice][lane][4 rows]
+          const int sl = tn >> 2, tl = tn & 3;
+          *reinterpret_cast<float4*>(U0g + ((wo / kC * 2 + sl) * 16 + tm * 4 + tl) * 256 + lane * 4) =
               make_float4(acc[0], acc[1], acc[2], acc[3]);
         }
       }
@@ -390,8 +410,8 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(
     // masked to the segments that see S0 and reach the chunk's end
     const int t = threadIdx.x;
     const float ct = cum[t], cl = cum[kC - 1];
-    edg[2 * wo + t] = seg[t] == 0 ? expf(ct) : 0.f;
-    edg[2 * wo + kC + t] = seg[t] == seg[kC - 1] ? expf(cl - ct) : 0.f;
+    edg[2 * wo + t] = seg[t] == 0 ? __expf(ct) : 0.f;
+    edg[2 * wo + kC + t] = seg[t] == seg[kC - 1] ? __expf(cl - ct) : 0.f;
   }
 }
 
@@ -774,7 +794,8 @@ __global__ __launch_bounds__(kScanThreads) void gdn_chunk_scan_blocked_kernel(
 
   // ---- prefetch registers
   u32x4 pk[KQ_N], pq[KQ_N], pw[W_N], pa[A_N];
-  float pu[2][2][4], pc;  // U0 of the next chunk is loaded into pu after phase 1 reads it
+  f32x4 pu[2][2];  // U0 of the next chunk is loaded into pu after phase 1 reads it
+  float pc;
   auto fetch1 = [&](int c_) {  // K, Q (rows past the chunk re-read its last row), W
     const int ft0 = c_ * kC;
     const int fTc = min(kC, T - ft0);
@@ -798,14 +819,14 @@ __global__ __launch_bounds__(kScanThreads) void gdn_chunk_scan_blocked_kernel(
     for (int i = 0; i < A_N; ++i)
       pa[i] = *reinterpret_cast<const u32x4*>(Ag + fcid * kC * kC * 2 + 8 * (tid + NT * i));
     pc = edg[fcid * 2 * kC + (tid & (2 * kC - 1))];
+    // U0 in fragment order: [slice][16 x 16 tile][lane][4 rows] (waves 4-7
+    // load the tiles of waves 0-3 and never use them)
 #pragma unroll
     for (int a = 0; a < 2; ++a)
 #pragma unroll
       for (int c = 0; c < 2; ++c)
-#pragma unroll
-        for (int i = 0; i < 4; ++i)  // (waves 4-7 load the tiles of waves 0-3 and never use them)
-          pu[a][c][i] = U0g[(fcid * kC + 16 * (2 * bm + a) + 4 * g4 + i) * DV + DVS * sl +
-                            16 * (2 * bn + c) + r16];
+        pu[a][c] = *reinterpret_cast<const f32x4*>(
+            U0g + ((fcid * NSL + sl) * 16 + (2 * bm + a) * 4 + 2 * bn + c) * 256 + lane * 4);
   };
   auto stash = [&](int c_) {
     const int sTc = min(kC, T - c_ * kC);
