@@ -85,12 +85,12 @@ __device__ __forceinline__ f32x4 mfma16(const uint4& a, const uint4& b, f32x4 c)
 // fragment order, [64-column slice][16 x 16 tile][lane][4 rows]), A [64][64],
 // decay factors [2][64] (e_t then d_t, fp32).  reset [B, T] or null.
 template <int DK, int DV>
-__global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void gdn_chunk_prep_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, const float* __restrict__ beta,
     const float* __restrict__ g, const int32_t* __restrict__ reset, uint16_t* __restrict__ Wg,
     float* __restrict__ U0g, uint16_t* __restrict__ Ag, float* __restrict__ edg, int T, int H,
-    int NC) {
+    int NC, int n_chunks) {
   constexpr int PK = DK + 8, PG = kC + 1, PT = kC + 8;
   // LDS by lifetime, so that two workgroups fit on a CU: region R0 holds K
   // and Q rows (products), then the per-wave block products of the inverse,
@@ -108,47 +108,62 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(
   __shared__ float cum[kC], prv[kC], bet[kC], wsc[kC];  // wsc = beta * Gamma_prev
   __shared__ int seg[kC];  // segment of each token (resets seen up to it in the chunk)
 
-  const int cid = blockIdx.x;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r16 = lane & 15, g4 = lane >> 4;
+  const long long rk = static_cast<long long>(H) * DK, rv = static_cast<long long>(H) * DV;
+
+  // Persistent: workgroup w takes chunks w, w + gridDim.x, ...  The next
+  // chunk's K and Q rows and per-token g, beta and reset flags are loaded into
+  // registers during the current one's W and U0 products.  Every wave issues the same
+  // loads (rows past a chunk and the last chunk's "next" re-read valid rows;
+  // without resets the flags are read from g and ignored), so each wait counts
+  // a fixed number of memory operations after the load it waits for.
+  constexpr int SN = kC * (DK / 8) / 256;
+  static_assert(SN * 256 == kC * (DK / 8), "staging split");
+  uint4 skv[SN], sqv[SN];
+  float pg, pb;
+  int32_t prs;
+  auto prefetch = [&](int cid_) {
+    const int bh_ = cid_ / NC, c_ = cid_ - (cid_ / NC) * NC;
+    const int b_ = bh_ / H, h_ = bh_ - (bh_ / H) * H;
+    const int t0_ = c_ * kC, Tc_ = min(kC, T - t0_);
+    const long long kb_ = (static_cast<long long>(b_) * T + t0_) * rk + static_cast<long long>(h_) * DK;
+#pragma unroll
+    for (int i = 0; i < SN; ++i) {
+      const int f = threadIdx.x + 256 * i;
+      const int t = f / (DK / 8), cc = f - t * (DK / 8);
+      skv[i] = *reinterpret_cast<const uint4*>(k + kb_ + min(t, Tc_ - 1) * rk + 8 * cc);
+      sqv[i] = *reinterpret_cast<const uint4*>(q + kb_ + min(t, Tc_ - 1) * rk + 8 * cc);
+    }
+    const long long tok = static_cast<long long>(b_) * T + t0_ + min(lane, Tc_ - 1);
+    pg = g[tok * H + h_];
+    pb = beta[tok * H + h_];
+    prs = (reset != nullptr ? reset : reinterpret_cast<const int32_t*>(g))[tok];
+  };
+  if (static_cast<int>(blockIdx.x) < n_chunks) prefetch(blockIdx.x);
+  for (int cid = blockIdx.x; cid < n_chunks; cid += gridDim.x) {
   const int bh = cid / NC;
   const int c = cid - bh * NC;
   const int b = bh / H, h = bh - (bh / H) * H;
   const int t0 = c * kC;
   const int Tc = min(kC, T - t0);
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int r16 = lane & 15, g4 = lane >> 4;
-  const long long rk = static_cast<long long>(H) * DK, rv = static_cast<long long>(H) * DV;
   const long long kbase = (static_cast<long long>(b) * T + t0) * rk + static_cast<long long>(h) * DK;
   const long long vbase = (static_cast<long long>(b) * T + t0) * rv + static_cast<long long>(h) * DV;
 
-  // ---- stage K and Q rows; padded rows are zero.  Every load is issued
-  // before the first store (rows past the chunk re-read its last row).
-  constexpr int SN = kC * (DK / 8) / 256;
-  static_assert(SN * 256 == kC * (DK / 8), "staging split");
-  {
-    uint4 skv[SN], sqv[SN];
+  // ---- stage K and Q rows from the prefetch registers; padded rows are zero
 #pragma unroll
-    for (int i = 0; i < SN; ++i) {
-      const int f = threadIdx.x + 256 * i;
-      const int t = f / (DK / 8), cc = f - t * (DK / 8);
-      const int tr = min(t, Tc - 1);
-      skv[i] = *reinterpret_cast<const uint4*>(k + kbase + tr * rk + 8 * cc);
-      sqv[i] = *reinterpret_cast<const uint4*>(q + kbase + tr * rk + 8 * cc);
-    }
-#pragma unroll
-    for (int i = 0; i < SN; ++i) {
-      const int f = threadIdx.x + 256 * i;
-      const int t = f / (DK / 8), cc = f - t * (DK / 8);
-      uint4 kv = skv[i], qv = sqv[i];
-      if (t >= Tc) kv = qv = uint4{0u, 0u, 0u, 0u};
-      *reinterpret_cast<uint4*>(Ks + t * PK + 8 * cc) = kv;
-      *reinterpret_cast<uint4*>(Qs + t * PK + 8 * cc) = qv;
-    }
+  for (int i = 0; i < SN; ++i) {
+    const int f = threadIdx.x + 256 * i;
+    const int t = f / (DK / 8), cc = f - t * (DK / 8);
+    uint4 kv = skv[i], qv = sqv[i];
+    if (t >= Tc) kv = qv = uint4{0u, 0u, 0u, 0u};
+    *reinterpret_cast<uint4*>(Ks + t * PK + 8 * cc) = kv;
+    *reinterpret_cast<uint4*>(Qs + t * PK + 8 * cc) = qv;
   }
   if (wave == 0) {
     // inclusive prefix sum of log g over the chunk (padded tokens: g = 1, beta = 0)
-    const long long gi = (static_cast<long long>(b) * T + t0 + min(lane, Tc - 1)) * H + h;
-    float lg = lane < Tc ? logf(g[gi]) : 0.f;
-    const float bt = lane < Tc ? beta[gi] : 0.f;
+    float lg = lane < Tc ? logf(pg) : 0.f;
+    const float bt = lane < Tc ? pb : 0.f;
     float sc = lg;
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {
@@ -157,8 +172,7 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(
     }
     // segments: a reset at token r starts a new one; cumulative log-decays
     // restart there (minus the prefix before r)
-    const bool rs = reset != nullptr && lane < Tc &&
-                    reset[static_cast<long long>(b) * T + t0 + lane] != 0;
+    const bool rs = reset != nullptr && lane < Tc && prs != 0;
     const unsigned long long rm = __ballot(rs);
     const unsigned long long upto = lane == 63 ? ~0ull : ((2ull << lane) - 1);
     const int sg = __popcll(rm & upto);
@@ -216,29 +230,13 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(
           make_uint2(pack_bf2u(lv[0], lv[1]), pack_bf2u(lv[2], lv[3]));
     }
   }
-  // K and V rows for the transposed staging after the inverse, fetched now so
-  // their latency hides behind the inverse: item i = (token pair, 8-dim chunk)
-  // f = threadIdx.x + 256 i.  Rows past the chunk are clamped (valid
-  // addresses) here and zeroed at the store, so no load is waited on early.
+  // K and V rows for the transposed staging after the inverse: item i =
+  // (token pair, 8-dim chunk) f = threadIdx.x + 256 i, fetched after the
+  // diagonal blocks so their latency hides behind the block levels.  Rows past
+  // the chunk are clamped (valid addresses) here and zeroed at the store.
   constexpr int KPI = (kC / 2) * (DK / 8) / 256, VPI = (kC / 2) * (DV / 8) / 256;
   static_assert(KPI * 256 == (kC / 2) * (DK / 8) && VPI * 256 == (kC / 2) * (DV / 8), "pairs");
   uint4 kp[KPI][2], vp[VPI][2];
-#pragma unroll
-  for (int i = 0; i < KPI; ++i) {
-    const int f = threadIdx.x + 256 * i;
-    const int t2 = 2 * (f % (kC / 2)), cc = f / (kC / 2);
-#pragma unroll
-    for (int e = 0; e < 2; ++e)
-      kp[i][e] = *reinterpret_cast<const uint4*>(k + kbase + min(t2 + e, Tc - 1) * rk + 8 * cc);
-  }
-#pragma unroll
-  for (int i = 0; i < VPI; ++i) {
-    const int f = threadIdx.x + 256 * i;
-    const int t2 = 2 * (f % (kC / 2)), cc = f / (kC / 2);
-#pragma unroll
-    for (int e = 0; e < 2; ++e)
-      vp[i][e] = *reinterpret_cast<const uint4*>(v + vbase + min(t2 + e, Tc - 1) * rv + 8 * cc);
-  }
   __syncthreads();
   // ---- (I + L)^{-1}, blocked by 16: N = I + L is unit lower triangular with
   // 16 x 16 blocks N_ij; T = N^{-1} has T_ii = N_ii^{-1} and, for i > j,
@@ -272,6 +270,22 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(
     for (int e = threadIdx.x; e < kC * kC; e += 256) {
       const int t = e >> 6, i = e & 63;
       if ((i >> 4) > (t >> 4)) Ti[t * PG + i] = 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < KPI; ++i) {
+      const int f = threadIdx.x + 256 * i;
+      const int t2 = 2 * (f % (kC / 2)), cc = f / (kC / 2);
+#pragma unroll
+      for (int e = 0; e < 2; ++e)
+        kp[i][e] = *reinterpret_cast<const uint4*>(k + kbase + min(t2 + e, Tc - 1) * rk + 8 * cc);
+    }
+#pragma unroll
+    for (int i = 0; i < VPI; ++i) {
+      const int f = threadIdx.x + 256 * i;
+      const int t2 = 2 * (f % (kC / 2)), cc = f / (kC / 2);
+#pragma unroll
+      for (int e = 0; e < 2; ++e)
+        vp[i][e] = *reinterpret_cast<const uint4*>(v + vbase + min(t2 + e, Tc - 1) * rv + 8 * cc);
     }
     __syncthreads();
     const int c16 = lane & 15, k4 = lane >> 4;
@@ -339,6 +353,8 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(
       *reinterpret_cast<uint32_t*>(VsT + (8 * cc + jj) * PT + t2) = lo | (hi << 16);
     }
   }
+  // the next chunk's rows (this workgroup's last chunk fetches itself again)
+  prefetch(min(cid + static_cast<int>(gridDim.x), n_chunks - 1));
   __syncthreads();
   // ---- W = TW K  [64 x DK] (stored as (hi, lo) bf16 planes),  U0 = TU V  [64 x DV] (fp32)
   {
@@ -405,13 +421,16 @@ __global__ __launch_bounds__(256) void gdn_chunk_prep_kernel(
       }
     }
   }
-  if (threadIdx.x < kC) {
+  {
     // e_t = Gamma_t (the S0 term of O), d_t = Gamma_C / Gamma_t (the S' update),
-    // masked to the segments that see S0 and reach the chunk's end
-    const int t = threadIdx.x;
+    // masked to the segments that see S0 and reach the chunk's end; threads
+    // 128..255 store the same values as 0..127 (every wave stores)
+    const int e = threadIdx.x & (2 * kC - 1), t = e & (kC - 1);
     const float ct = cum[t], cl = cum[kC - 1];
-    edg[2 * wo + t] = seg[t] == 0 ? __expf(ct) : 0.f;
-    edg[2 * wo + kC + t] = seg[t] == seg[kC - 1] ? __expf(cl - ct) : 0.f;
+    edg[2 * wo + e] = e < kC ? (seg[t] == 0 ? __expf(ct) : 0.f)
+                             : (seg[t] == seg[kC - 1] ? __expf(cl - ct) : 0.f);
+  }
+  __syncthreads();  // LDS of this chunk is free for the next
   }
 }
 
@@ -801,12 +820,14 @@ __global__ __launch_bounds__(kScanThreads) void gdn_chunk_scan_blocked_kernel(
     const int fTc = min(kC, T - ft0);
     const long long fcid = static_cast<long long>(bh) * NC + c_;
     const long long fkb = (static_cast<long long>(b) * T + ft0) * rk + static_cast<long long>(h) * DK;
+    // K: thread = (token pair, 8-dim chunk), the pair's two rows in pk[0], pk[1]
+    // (stored transposed as dwords holding both tokens); Q row-major
+    const int tp2 = 2 * (tid % (kC / 2)), ckp = tid / (kC / 2);
 #pragma unroll
     for (int i = 0; i < KQ_N; ++i) {
       const int f = tid + NT * i;
-      const int tk = f % kC, ck = f / kC;
       const int tq = f / (DK / 8), cq = f % (DK / 8);
-      pk[i] = *reinterpret_cast<const u32x4*>(k + fkb + min(tk, fTc - 1) * rk + 8 * ck);
+      pk[i] = *reinterpret_cast<const u32x4*>(k + fkb + min(tp2 + i, fTc - 1) * rk + 8 * ckp);
       pq[i] = *reinterpret_cast<const u32x4*>(q + fkb + min(tq, fTc - 1) * rk + 8 * cq);
     }
 #pragma unroll
@@ -833,13 +854,20 @@ __global__ __launch_bounds__(kScanThreads) void gdn_chunk_scan_blocked_kernel(
 #pragma unroll
     for (int i = 0; i < KQ_N; ++i) {
       const int f = tid + NT * i;
-      const int tk = f % kC, ck = f / kC;
       const int tq = f / (DK / 8), cq = f % (DK / 8);
-      const u32x4 kv = tk < sTc ? pk[i] : u32x4{0u, 0u, 0u, 0u};
       *reinterpret_cast<u32x4*>(Qs + tq * PB + 8 * cq) = tq < sTc ? pq[i] : u32x4{0u, 0u, 0u, 0u};
+    }
+    {
+      const int tp2 = 2 * (tid % (kC / 2)), ckp = tid / (kC / 2);
+      u32x4 k0 = pk[0], k1 = pk[1];
+      if (tp2 >= sTc) k0 = u32x4{0u, 0u, 0u, 0u};
+      if (tp2 + 1 >= sTc) k1 = u32x4{0u, 0u, 0u, 0u};
 #pragma unroll
-      for (int jj = 0; jj < 8; ++jj)
-        KsT[(8 * ck + jj) * PT + tk] = static_cast<uint16_t>(kv[jj >> 1] >> (16 * (jj & 1)));
+      for (int jj = 0; jj < 8; ++jj) {
+        const uint32_t lo = (k0[jj >> 1] >> (16 * (jj & 1))) & 0xffffu;
+        const uint32_t hi = (k1[jj >> 1] >> (16 * (jj & 1))) & 0xffffu;
+        *reinterpret_cast<uint32_t*>(KsT + (8 * ckp + jj) * PT + tp2) = lo | (hi << 16);
+      }
     }
 #pragma unroll
     for (int i = 0; i < W_N; ++i) {
@@ -1054,6 +1082,19 @@ namespace {
 
 // The prep + scan launches over a caller-sized workspace (validated by the
 // entry points below).
+// Compute units of the current device (queried once per process).
+int device_cus() {
+  static int cus = 0;
+  if (cus == 0) {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    cus = n;
+  }
+  return cus;
+}
+
 int32_t gdn_prefill_launch(const llmy_bf16* q, const llmy_bf16* k, const llmy_bf16* v,
                            const float* beta, const float* g, const int32_t* reset, float* state,
                            llmy_bf16* out, void* workspace, int B, int T, int H, int dk,
@@ -1067,17 +1108,22 @@ int32_t gdn_prefill_launch(const llmy_bf16* q, const llmy_bf16* k, const llmy_bf
   float* U0 = reinterpret_cast<float*>(W + chunks * kC * dk * 2);
   uint16_t* A = reinterpret_cast<uint16_t*>(U0 + chunks * kC * dv);
   float* ed = reinterpret_cast<float*>(A + chunks * kC * kC * 2);
+  // persistent prep workgroups: two per CU (the kernel is built for two waves
+  // per SIMD), each taking every grid-th chunk
+  const int nch = static_cast<int>(chunks);
   if (dk == 64) {
-    hipLaunchKernelGGL((gdn_chunk_prep_kernel<64, 64>), dim3(static_cast<unsigned>(chunks)),
-                       dim3(256), 0, s, q, k, v, beta, g, reset, W, U0, A, ed, T, H, NC);
+    const int grid = static_cast<int>(std::min<long long>(chunks, 2ll * device_cus()));
+    hipLaunchKernelGGL((gdn_chunk_prep_kernel<64, 64>), dim3(static_cast<unsigned>(grid)),
+                       dim3(256), 0, s, q, k, v, beta, g, reset, W, U0, A, ed, T, H, NC, nch);
     int32_t st = launch_status();
     if (st != 0) return st;
     const int units = B * H * (64 / 32);
     hipLaunchKernelGGL((gdn_chunk_scan_kernel<64, 64, 32>), dim3((units + 7) / 8 * 8),
                        dim3(kScanThreads), 0, s, q, k, W, U0, A, ed, state, out, T, H, NC, units);
   } else {
-    hipLaunchKernelGGL((gdn_chunk_prep_kernel<128, 128>), dim3(static_cast<unsigned>(chunks)),
-                       dim3(256), 0, s, q, k, v, beta, g, reset, W, U0, A, ed, T, H, NC);
+    const int grid = static_cast<int>(std::min<long long>(chunks, 2ll * device_cus()));
+    hipLaunchKernelGGL((gdn_chunk_prep_kernel<128, 128>), dim3(static_cast<unsigned>(grid)),
+                       dim3(256), 0, s, q, k, v, beta, g, reset, W, U0, A, ed, T, H, NC, nch);
     int32_t st = launch_status();
     if (st != 0) return st;
     const int units = B * H * (128 / 64);
