@@ -81,7 +81,10 @@ __device__ __forceinline__ void topk_regs(const float* srow, int n, int k, int l
     key[i] = j < n ? order_key(srow[j]) : 0u;   // 0: below every real key
   }
   // counts over the wave are popcounts of compare masks (no cross-lane data
-  // movement): the threshold search runs in the scalar unit
+  // movement): the threshold search runs in the scalar unit.  It stops as
+  // soon as exactly k keys are at or above the candidate prefix: those are
+  // the top k, with no tie at the boundary, and thr - 1 then marks them as
+  // the keys above the threshold (the same set and order as a full search).
   uint32_t thr = 0;
   for (int bit = 31; bit >= 0; --bit) {
     const uint32_t cand = thr | (1u << bit);
@@ -89,6 +92,10 @@ __device__ __forceinline__ void topk_regs(const float* srow, int n, int k, int l
 #pragma unroll
     for (int i = 0; i < NPL; ++i) c += __popcll(__ballot(key[i] >= cand));
     if (c >= k) thr = cand;
+    if (c == k) {
+      thr = cand - 1u;
+      break;
+    }
   }
   int gt = 0;
 #pragma unroll
