@@ -92,6 +92,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
     float* __restrict__ U0g, uint16_t* __restrict__ Ag, float* __restrict__ edg, int T, int H,
     int NC, int n_chunks) {
   constexpr int PK = DK + 8, PG = kC + 1, PT = kC + 8;
+  constexpr bool kTOut = DK == 128;  // T and factors for gdn_chunk_scan_t_kernel
   // LDS by lifetime, so that two workgroups fit on a CU: region R0 holds K
   // and Q rows (products), then the per-wave block products of the inverse,
   // then K^T and V^T (the B operands of W and U0, staged after the inverse).
@@ -272,7 +273,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
       if ((i >> 4) > (t >> 4)) Ti[t * PG + i] = 0.f;
     }
 #pragma unroll
-    for (int i = 0; i < KPI; ++i) {
+    for (int i = 0; i < (kTOut ? 0 : KPI); ++i) {
       const int f = threadIdx.x + 256 * i;
       const int t2 = 2 * (f % (kC / 2)), cc = f / (kC / 2);
 #pragma unroll
@@ -280,7 +281,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
         kp[i][e] = *reinterpret_cast<const uint4*>(k + kbase + min(t2 + e, Tc - 1) * rk + 8 * cc);
     }
 #pragma unroll
-    for (int i = 0; i < VPI; ++i) {
+    for (int i = 0; i < (kTOut ? 0 : VPI); ++i) {
       const int f = threadIdx.x + 256 * i;
       const int t2 = 2 * (f % (kC / 2)), cc = f / (kC / 2);
 #pragma unroll
@@ -321,6 +322,37 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
     }
   }
 
+  if constexpr (kTOut) {
+    // ---- dk = 128: T = (I + L)^{-1} as (hi, lo) bf16 planes [2][64][64] in
+    // the chunk's W slot, and per token [Gamma_t | Gamma_C / Gamma_t | beta_t |
+    // beta_t Gamma_{t-1}] (masked as below) in its U0 slot: the scan forms
+    // U = T (beta V - beta Gamma_prev K S) itself
+    uint16_t* Tw = Wg + static_cast<long long>(cid) * kC * DK * 2;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int f = threadIdx.x + 256 * i;
+      const int t = f >> 3, c8 = f & 7;
+      float x[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) x[j] = Ti[t * PG + 8 * c8 + j];
+      uint4 hi, lo;
+      split8(x, hi, lo);
+      *reinterpret_cast<uint4*>(Tw + t * kC + 8 * c8) = hi;
+      *reinterpret_cast<uint4*>(Tw + kC * kC + t * kC + 8 * c8) = lo;
+    }
+    {
+      const int part = threadIdx.x >> 6, t = threadIdx.x & (kC - 1);
+      const float ct = cum[t], cl = cum[kC - 1];
+      const float fv = part == 0   ? (seg[t] == 0 ? __expf(ct) : 0.f)
+                       : part == 1 ? (seg[t] == seg[kC - 1] ? __expf(cl - ct) : 0.f)
+                       : part == 2 ? bet[t]
+                                   : wsc[t];
+      U0g[static_cast<long long>(cid) * kC * DV + threadIdx.x] = fv;
+    }
+    // the next chunk's rows (this workgroup's last chunk fetches itself again)
+    prefetch(min(cid + static_cast<int>(gridDim.x), n_chunks - 1));
+    __syncthreads();  // LDS of this chunk is free for the next
+  } else {
   // ---- K^T and V^T into R0 (the block products above are done), from the
   // rows fetched before the inverse: each of a pair's 8 dims is stored as one
   // dword holding both tokens (zero past the chunk), the lanes of a wave
@@ -431,6 +463,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
                              : (seg[t] == seg[kC - 1] ? __expf(cl - ct) : 0.f);
   }
   __syncthreads();  // LDS of this chunk is free for the next
+  }
   }
 }
 
@@ -728,47 +761,57 @@ __global__ __launch_bounds__(kScanThreads) void gdn_chunk_scan_kernel(
 }
 
 
-// Kernel 2 for dk = dv = 128 (64-column state slices): the algebra of
-// gdn_chunk_scan_kernel with the eight waves in two groups of four, each wave
-// owning 32 x 32 blocks (2 x 2 tiles of 16 x 16), so every fragment read from
-// LDS feeds two MFMAs:
-//   phase 1  waves 0-3: U = U0 - W S (one block each), split into U^T and
-//            (dec o U)^T;  waves 4-7: Q S (one block each), kept in registers
-//   phase 2  waves 0-3: S = Gamma_C S + K^T (dec o U) on the 2 x 4 state tiles
-//            each owns (32 rows of the slice), then the transposed (hi, lo)
-//            copy for the next chunk;  waves 4-7: O = Gamma (Q S) + A U (A is
-//            causal: the first token block skips the second half of A)
+// Kernel 2 for dk = dv = 128 (64-column state slices).  Kernel 1 hands over
+// T = (I + L)^{-1} (hi, lo planes), A, and per token Gamma_t, Gamma_C/Gamma_t,
+// beta_t and beta_t Gamma_{t-1}; this kernel forms U itself:
+//   U = T Y,  Y = beta o V - (beta Gamma_prev) o (K S)      (= U0 - W S)
+// Eight waves in two groups of four, each wave owning 32 x 32 blocks (2 x 2
+// tiles of 16 x 16), so every fragment read from LDS feeds two MFMAs:
+//   phase 1   waves 0-3: K S, then Y (one block each), split into the
+//             (dec o U)^T planes;  waves 4-7: Q S (one block each), kept in
+//             registers
+//   phase 1b  all waves: U = T Y (two 16 x 16 tiles each; T is unit lower
+//             triangular, so the first token half skips the second), then,
+//             after every read of Y, U^T and (dec o U)^T as (hi, lo) planes
+//   phase 2   waves 0-3: S = Gamma_C S + K^T (dec o U) on the 2 x 4 state
+//             tiles each owns (32 rows of the slice), K^T fragments gathered
+//             from the row-major K tile, then the transposed (hi, lo) copy of
+//             S for the next chunk;  waves 4-7: O = Gamma (Q S) + A U (A is
+//             causal: the first token block skips the second half of A)
 //   then the next chunk's operands go to LDS.
-// The next chunk's K, Q and W are fetched at the start of a chunk, its A, U0
-// and decay factors after phase 1, so the loads drain behind the MFMAs.  Every
-// wave issues the same memory operations in the same order in every
-// iteration (waves 4-7 load the U0 tiles of waves 0-3 too; waves 0-3 issue the
-// output stores of waves 4-7 with offsets past the
-// buffer, which the hardware drops; the last chunk fetches itself again), so
-// each wait for a load counts a fixed number of operations after it and the
+// The next chunk's K, Q, T and V rows are fetched at the start of a chunk, its
+// A and per-token factors after phase 1, so the loads drain behind the MFMAs.
+// Every wave issues the same memory operations in the same order in every
+// iteration (waves 0-3 issue the output stores of waves 4-7 with offsets past
+// the buffer, which the hardware drops; the last chunk fetches itself again),
+// so each wait for a load counts a fixed number of operations after it and the
 // loads of the next chunk stay in flight across it.
 template <int DK, int DV, int DVS>
-__global__ __launch_bounds__(kScanThreads) void gdn_chunk_scan_blocked_kernel(
+__global__ __launch_bounds__(kScanThreads) void gdn_chunk_scan_t_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
-    const uint16_t* __restrict__ Wg, const float* __restrict__ U0g, const uint16_t* __restrict__ Ag,
-    const float* __restrict__ edg, float* __restrict__ state, uint16_t* __restrict__ out, int T,
-    int H, int NC, int n_units) {
-  static_assert(DK == 128 && DVS == 64, "blocked scan: dk = 128, 64-column slices");
+    const uint16_t* __restrict__ v, const uint16_t* __restrict__ Tg,
+    const float* __restrict__ facg, const uint16_t* __restrict__ Ag, float* __restrict__ state,
+    uint16_t* __restrict__ out, int T, int H, int NC, int n_units) {
+  static_assert(DK == 128 && DVS == 64, "scan: dk = 128, 64-column slices");
   constexpr int NSL = DV / DVS;
-  constexpr int PB = DK + 8, PT = kC + 8, NT = kScanThreads;
+  constexpr int PB = DK + 8, PT = kC + 8, PV = DVS + 8, NT = kScanThreads;
   constexpr int KQ_N = kC * DK / 8 / NT;     // uint4 of K (and of Q) per thread
-  constexpr int W_N = 2 * kC * DK / 8 / NT;  // uint4 of W (hi and lo planes) per thread
+  constexpr int T_N = 2 * kC * kC / 8 / NT;  // uint4 of T (hi and lo planes) per thread
   constexpr int A_N = 2 * kC * kC / 8 / NT;  // uint4 of A (hi and lo planes) per thread
-  static_assert(KQ_N == 2 && W_N == 4 && A_N == 2, "tile split");
-  __shared__ __align__(16) uint16_t Whi[kC * PB], Wlo[kC * PB], Qs[kC * PB];
-  __shared__ __align__(16) uint16_t Ahi[kC * PT], Alo[kC * PT];
-  __shared__ __align__(16) uint16_t KsT[DK * PT];                  // K^T [DK][64]
+  static_assert(KQ_N == 2 && T_N == 2 && A_N == 2 && kC * DVS / 8 == NT, "tile split");
+  __shared__ __align__(16) uint16_t Qs[kC * PB], Ks[kC * PB];        // row-major [t][d]
+  __shared__ __align__(16) uint16_t Thi[kC * PT], Tlo[kC * PT];      // T [t][i]
+  __shared__ __align__(16) uint16_t Ahi[kC * PT], Alo[kC * PT];      // A [t][i]
+  __shared__ __align__(16) uint16_t Vs[kC * PV];                     // V slice [t][v]
   __shared__ __align__(16) uint16_t SThi[DVS * PB], STlo[DVS * PB];  // S^T [DVS][DK]
   __shared__ __align__(16) uint16_t UThi[DVS * PT], UTlo[DVS * PT];  // U^T [DVS][64]
-  __shared__ __align__(16) uint16_t DThi[DVS * PT], DTlo[DVS * PT];  // (dec o U)^T
-  __shared__ float ecd[NT];  // Gamma_t, Gamma_C / Gamma_t, then one slot per thread
-  float* const ecum = ecd;
-  float* const dec = ecd + kC;
+  // (dec o U)^T [DVS][64]; Y^T before phase 1b's barrier
+  __shared__ __align__(16) uint16_t DThi[DVS * PT], DTlo[DVS * PT];
+  __shared__ float ecd[4 * kC];  // Gamma_t | Gamma_C / Gamma_t | beta_t | beta_t Gamma_{t-1}
+  const float* const ecum = ecd;
+  const float* const dec = ecd + kC;
+  const float* const bet = ecd + 2 * kC;
+  const float* const wsc = ecd + 3 * kC;
 
   const int per_xcd = (gridDim.x + 7) / 8;
   const int unit = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
@@ -812,68 +855,50 @@ __global__ __launch_bounds__(kScanThreads) void gdn_chunk_scan_blocked_kernel(
   if (grp == 0) split_state();
 
   // ---- prefetch registers
-  u32x4 pk[KQ_N], pq[KQ_N], pw[W_N], pa[A_N];
-  f32x4 pu[2][2];  // U0 of the next chunk is loaded into pu after phase 1 reads it
+  u32x4 pk[KQ_N], pq[KQ_N], pt[T_N], pa[A_N], pv;
   float pc;
-  auto fetch1 = [&](int c_) {  // K, Q (rows past the chunk re-read its last row), W
+  auto fetch1 = [&](int c_) {  // K, Q, V rows (past the chunk: its last row again) and T
     const int ft0 = c_ * kC;
     const int fTc = min(kC, T - ft0);
     const long long fcid = static_cast<long long>(bh) * NC + c_;
     const long long fkb = (static_cast<long long>(b) * T + ft0) * rk + static_cast<long long>(h) * DK;
-    // K: thread = (token pair, 8-dim chunk), the pair's two rows in pk[0], pk[1]
-    // (stored transposed as dwords holding both tokens); Q row-major
-    const int tp2 = 2 * (tid % (kC / 2)), ckp = tid / (kC / 2);
 #pragma unroll
     for (int i = 0; i < KQ_N; ++i) {
       const int f = tid + NT * i;
-      const int tq = f / (DK / 8), cq = f % (DK / 8);
-      pk[i] = *reinterpret_cast<const u32x4*>(k + fkb + min(tp2 + i, fTc - 1) * rk + 8 * ckp);
-      pq[i] = *reinterpret_cast<const u32x4*>(q + fkb + min(tq, fTc - 1) * rk + 8 * cq);
+      const int t = f / (DK / 8), cq = f % (DK / 8);
+      pk[i] = *reinterpret_cast<const u32x4*>(k + fkb + min(t, fTc - 1) * rk + 8 * cq);
+      pq[i] = *reinterpret_cast<const u32x4*>(q + fkb + min(t, fTc - 1) * rk + 8 * cq);
     }
 #pragma unroll
-    for (int i = 0; i < W_N; ++i)
-      pw[i] = *reinterpret_cast<const u32x4*>(Wg + fcid * kC * DK * 2 + 8 * (tid + NT * i));
+    for (int i = 0; i < T_N; ++i)
+      pt[i] = *reinterpret_cast<const u32x4*>(Tg + fcid * kC * DK * 2 + 8 * (tid + NT * i));
+    const int tv = tid / (DVS / 8), cv = tid % (DVS / 8);
+    pv = *reinterpret_cast<const u32x4*>(
+        v + (static_cast<long long>(b) * T + ft0 + min(tv, fTc - 1)) * rv +
+        static_cast<long long>(h) * DV + DVS * sl + 8 * cv);
   };
-  auto fetch2 = [&](int c_) {  // A, decay factors, U0 (after phase 1, which reads pu)
+  auto fetch2 = [&](int c_) {  // A and the per-token factors
     const long long fcid = static_cast<long long>(bh) * NC + c_;
 #pragma unroll
     for (int i = 0; i < A_N; ++i)
       pa[i] = *reinterpret_cast<const u32x4*>(Ag + fcid * kC * kC * 2 + 8 * (tid + NT * i));
-    pc = edg[fcid * 2 * kC + (tid & (2 * kC - 1))];
-    // U0 in fragment order: [slice][16 x 16 tile][lane][4 rows] (waves 4-7
-    // load the tiles of waves 0-3 and never use them)
-#pragma unroll
-    for (int a = 0; a < 2; ++a)
-#pragma unroll
-      for (int c = 0; c < 2; ++c)
-        pu[a][c] = *reinterpret_cast<const f32x4*>(
-            U0g + ((fcid * NSL + sl) * 16 + (2 * bm + a) * 4 + 2 * bn + c) * 256 + lane * 4);
+    pc = facg[fcid * kC * DV + (tid & (4 * kC - 1))];
   };
   auto stash = [&](int c_) {
     const int sTc = min(kC, T - c_ * kC);
+    const u32x4 z = u32x4{0u, 0u, 0u, 0u};
 #pragma unroll
     for (int i = 0; i < KQ_N; ++i) {
       const int f = tid + NT * i;
-      const int tq = f / (DK / 8), cq = f % (DK / 8);
-      *reinterpret_cast<u32x4*>(Qs + tq * PB + 8 * cq) = tq < sTc ? pq[i] : u32x4{0u, 0u, 0u, 0u};
-    }
-    {
-      const int tp2 = 2 * (tid % (kC / 2)), ckp = tid / (kC / 2);
-      u32x4 k0 = pk[0], k1 = pk[1];
-      if (tp2 >= sTc) k0 = u32x4{0u, 0u, 0u, 0u};
-      if (tp2 + 1 >= sTc) k1 = u32x4{0u, 0u, 0u, 0u};
-#pragma unroll
-      for (int jj = 0; jj < 8; ++jj) {
-        const uint32_t lo = (k0[jj >> 1] >> (16 * (jj & 1))) & 0xffffu;
-        const uint32_t hi = (k1[jj >> 1] >> (16 * (jj & 1))) & 0xffffu;
-        *reinterpret_cast<uint32_t*>(KsT + (8 * ckp + jj) * PT + tp2) = lo | (hi << 16);
-      }
+      const int t = f / (DK / 8), cq = f % (DK / 8);
+      *reinterpret_cast<u32x4*>(Qs + t * PB + 8 * cq) = t < sTc ? pq[i] : z;
+      *reinterpret_cast<u32x4*>(Ks + t * PB + 8 * cq) = t < sTc ? pk[i] : z;
     }
 #pragma unroll
-    for (int i = 0; i < W_N; ++i) {
+    for (int i = 0; i < T_N; ++i) {
       const int f = 8 * (tid + NT * i);
-      const int pl = f / (kC * DK), rem = f % (kC * DK);
-      *reinterpret_cast<u32x4*>((pl ? Wlo : Whi) + (rem / DK) * PB + rem % DK) = pw[i];
+      const int pl = f / (kC * kC), rem = f % (kC * kC);
+      *reinterpret_cast<u32x4*>((pl ? Tlo : Thi) + (rem / kC) * PT + rem % kC) = pt[i];
     }
 #pragma unroll
     for (int i = 0; i < A_N; ++i) {
@@ -881,7 +906,11 @@ __global__ __launch_bounds__(kScanThreads) void gdn_chunk_scan_blocked_kernel(
       const int pl = f / (kC * kC), rem = f % (kC * kC);
       *reinterpret_cast<u32x4*>((pl ? Alo : Ahi) + (rem / kC) * PT + rem % kC) = pa[i];
     }
-    ecd[tid] = pc;
+    {
+      const int tv = tid / (DVS / 8), cv = tid % (DVS / 8);
+      *reinterpret_cast<u32x4*>(Vs + tv * PV + 8 * cv) = tv < sTc ? pv : z;
+    }
+    if (tid < 4 * kC) ecd[tid] = pc;
   };
 
   fetch1(0);
@@ -904,15 +933,13 @@ __global__ __launch_bounds__(kScanThreads) void gdn_chunk_scan_blocked_kernel(
 #pragma unroll
       for (int cc = 0; cc < 2; ++cc) acc[a][cc] = f32x4{0.f, 0.f, 0.f, 0.f};
     if (grp == 0) {
-      // U = U0 - W S on token tiles 2bm + a, column tiles 2bn + cc
+      // K S on token tiles 2bm + a, column tiles 2bn + cc (K exact in bf16)
 #pragma unroll
       for (int s = 0; s < DK / 32; ++s) {
-        uint4 ah[2], al[2], bhv[2], blv[2];
+        uint4 ka[2], bhv[2], blv[2];
 #pragma unroll
         for (int a = 0; a < 2; ++a) {
-          const int ao = (16 * (2 * bm + a) + r16) * PB + 32 * s + 8 * g4;
-          ah[a] = *reinterpret_cast<const uint4*>(Whi + ao);
-          al[a] = *reinterpret_cast<const uint4*>(Wlo + ao);
+          ka[a] = *reinterpret_cast<const uint4*>(Ks + (16 * (2 * bm + a) + r16) * PB + 32 * s + 8 * g4);
           const int bo = (16 * (2 * bn + a) + r16) * PB + 32 * s + 8 * g4;
           bhv[a] = *reinterpret_cast<const uint4*>(SThi + bo);
           blv[a] = *reinterpret_cast<const uint4*>(STlo + bo);
@@ -921,31 +948,27 @@ __global__ __launch_bounds__(kScanThreads) void gdn_chunk_scan_blocked_kernel(
         for (int a = 0; a < 2; ++a)
 #pragma unroll
           for (int cc = 0; cc < 2; ++cc) {
-            acc[a][cc] = mfma16(ah[a], bhv[cc], acc[a][cc]);
-            acc[a][cc] = mfma16(ah[a], blv[cc], acc[a][cc]);
-            acc[a][cc] = mfma16(al[a], bhv[cc], acc[a][cc]);
+            acc[a][cc] = mfma16(ka[a], bhv[cc], acc[a][cc]);
+            acc[a][cc] = mfma16(ka[a], blv[cc], acc[a][cc]);
           }
       }
+      // Y = beta o V - (beta Gamma_prev) o (K S), split into the Y^T planes
 #pragma unroll
       for (int a = 0; a < 2; ++a)
 #pragma unroll
         for (int cc = 0; cc < 2; ++cc) {
           const int tm = 2 * bm + a, tn = 2 * bn + cc;
-          uint16_t uh[4], ul[4], dh[4], dl[4];
+          uint16_t yh[4], yl[4];
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const float uval = pu[a][cc][i] - acc[a][cc][i];
-            uh[i] = f2bf(uval);
-            ul[i] = f2bf(uval - bf2f(uh[i]));
-            const float dval = dec[16 * tm + 4 * g4 + i] * uval;
-            dh[i] = f2bf(dval);
-            dl[i] = f2bf(dval - bf2f(dh[i]));
+            const int t = 16 * tm + 4 * g4 + i;
+            const float y = bet[t] * bf2f(Vs[t * PV + 16 * tn + r16]) - wsc[t] * acc[a][cc][i];
+            yh[i] = f2bf(y);
+            yl[i] = f2bf(y - bf2f(yh[i]));
           }
           const int off = (16 * tn + r16) * PT + 16 * tm + 4 * g4;
-          *reinterpret_cast<uint2*>(UThi + off) = uint2{pack_bf2u(uh[0], uh[1]), pack_bf2u(uh[2], uh[3])};
-          *reinterpret_cast<uint2*>(UTlo + off) = uint2{pack_bf2u(ul[0], ul[1]), pack_bf2u(ul[2], ul[3])};
-          *reinterpret_cast<uint2*>(DThi + off) = uint2{pack_bf2u(dh[0], dh[1]), pack_bf2u(dh[2], dh[3])};
-          *reinterpret_cast<uint2*>(DTlo + off) = uint2{pack_bf2u(dl[0], dl[1]), pack_bf2u(dl[2], dl[3])};
+          *reinterpret_cast<uint2*>(DThi + off) = uint2{pack_bf2u(yh[0], yh[1]), pack_bf2u(yh[2], yh[3])};
+          *reinterpret_cast<uint2*>(DTlo + off) = uint2{pack_bf2u(yl[0], yl[1]), pack_bf2u(yl[2], yl[3])};
         }
     } else {
       // Q S on token tiles 2bm + a, column tiles 2bn + cc (kept in acc)
@@ -968,8 +991,55 @@ __global__ __launch_bounds__(kScanThreads) void gdn_chunk_scan_blocked_kernel(
           }
       }
     }
-    __syncthreads();  // U^T and (dec o U)^T complete; every read of S^T done
+    __syncthreads();  // Y^T complete; every read of S^T done
     fetch2(cn);
+
+    // ---- phase 1b: U = T Y on token tiles 2 tp + a, column tile tn
+    const int tp = wave >> 2, tn1 = wave & 3;
+    f32x4 u[2];
+#pragma unroll
+    for (int a = 0; a < 2; ++a) u[a] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < kC / 32; ++s) {
+      if (s > tp) break;  // T is lower triangular: tokens 0..31 see no later token
+      uint4 th[2], tl[2];
+#pragma unroll
+      for (int a = 0; a < 2; ++a) {
+        const int ao = (16 * (2 * tp + a) + r16) * PT + 32 * s + 8 * g4;
+        th[a] = *reinterpret_cast<const uint4*>(Thi + ao);
+        tl[a] = *reinterpret_cast<const uint4*>(Tlo + ao);
+      }
+      const int bo = (16 * tn1 + r16) * PT + 32 * s + 8 * g4;
+      const uint4 yhv = *reinterpret_cast<const uint4*>(DThi + bo);
+      const uint4 ylv = *reinterpret_cast<const uint4*>(DTlo + bo);
+#pragma unroll
+      for (int a = 0; a < 2; ++a) {
+        u[a] = mfma16(th[a], yhv, u[a]);
+        u[a] = mfma16(th[a], ylv, u[a]);
+        u[a] = mfma16(tl[a], yhv, u[a]);
+      }
+    }
+    __syncthreads();  // every read of Y^T done
+#pragma unroll
+    for (int a = 0; a < 2; ++a) {
+      const int tm = 2 * tp + a;
+      uint16_t uh[4], ul[4], dh[4], dl[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float uval = u[a][i];
+        uh[i] = f2bf(uval);
+        ul[i] = f2bf(uval - bf2f(uh[i]));
+        const float dval = dec[16 * tm + 4 * g4 + i] * uval;
+        dh[i] = f2bf(dval);
+        dl[i] = f2bf(dval - bf2f(dh[i]));
+      }
+      const int off = (16 * tn1 + r16) * PT + 16 * tm + 4 * g4;
+      *reinterpret_cast<uint2*>(UThi + off) = uint2{pack_bf2u(uh[0], uh[1]), pack_bf2u(uh[2], uh[3])};
+      *reinterpret_cast<uint2*>(UTlo + off) = uint2{pack_bf2u(ul[0], ul[1]), pack_bf2u(ul[2], ul[3])};
+      *reinterpret_cast<uint2*>(DThi + off) = uint2{pack_bf2u(dh[0], dh[1]), pack_bf2u(dh[2], dh[3])};
+      *reinterpret_cast<uint2*>(DTlo + off) = uint2{pack_bf2u(dl[0], dl[1]), pack_bf2u(dl[2], dl[3])};
+    }
+    __syncthreads();  // U^T and (dec o U)^T complete
 
     // ---- phase 2; output rows past the chunk lie beyond the buffer range
     const __amdgpu_buffer_rsrc_t orsrc = __builtin_amdgcn_make_buffer_rsrc(
@@ -977,7 +1047,8 @@ __global__ __launch_bounds__(kScanThreads) void gdn_chunk_scan_blocked_kernel(
         static_cast<short>(0), static_cast<int>(((Tc - 1) * rv + DVS) * 2), 0x00020000);
     if (grp == 0) {
       // S = Gamma_C S + K^T (dec o U) on d tiles 2 wi + a, column tiles c,
-      // accumulated onto the decayed state in place
+      // accumulated onto the decayed state in place; the K^T fragment (8
+      // tokens of one dim per lane) is gathered from the row-major K tile
 #pragma unroll
       for (int a = 0; a < 2; ++a)
 #pragma unroll
@@ -988,8 +1059,14 @@ __global__ __launch_bounds__(kScanThreads) void gdn_chunk_scan_blocked_kernel(
       for (int s = 0; s < kC / 32; ++s) {
         uint4 ka[2];
 #pragma unroll
-        for (int a = 0; a < 2; ++a)
-          ka[a] = *reinterpret_cast<const uint4*>(KsT + (16 * (2 * wi + a) + r16) * PT + 32 * s + 8 * g4);
+        for (int a = 0; a < 2; ++a) {
+          const uint16_t* kc = Ks + (32 * s + 8 * g4) * PB + 16 * (2 * wi + a) + r16;
+          uint16_t e[8];
+#pragma unroll
+          for (int j = 0; j < 8; ++j) e[j] = kc[j * PB];
+          ka[a] = uint4{pack_bf2u(e[0], e[1]), pack_bf2u(e[2], e[3]), pack_bf2u(e[4], e[5]),
+                        pack_bf2u(e[6], e[7])};
+        }
 #pragma unroll
         for (int cc = 0; cc < 4; ++cc) {
           const int bo = (16 * cc + r16) * PT + 32 * s + 8 * g4;
@@ -1127,8 +1204,9 @@ int32_t gdn_prefill_launch(const llmy_bf16* q, const llmy_bf16* k, const llmy_bf
     int32_t st = launch_status();
     if (st != 0) return st;
     const int units = B * H * (128 / 64);
-    hipLaunchKernelGGL((gdn_chunk_scan_blocked_kernel<128, 128, 64>), dim3((units + 7) / 8 * 8),
-                       dim3(kScanThreads), 0, s, q, k, W, U0, A, ed, state, out, T, H, NC, units);
+    // dk = 128: W's slot holds T, U0's slot the per-token factors
+    hipLaunchKernelGGL((gdn_chunk_scan_t_kernel<128, 128, 64>), dim3((units + 7) / 8 * 8),
+                       dim3(kScanThreads), 0, s, q, k, v, W, U0, A, state, out, T, H, NC, units);
   }
   return launch_status();
 }
