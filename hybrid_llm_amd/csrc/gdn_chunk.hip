@@ -765,27 +765,25 @@ __global__ __launch_bounds__(kScanThreads) void gdn_chunk_scan_kernel(
 // T = (I + L)^{-1} (hi, lo planes), A, and per token Gamma_t, Gamma_C/Gamma_t,
 // beta_t and beta_t Gamma_{t-1}; this kernel forms U itself:
 //   U = T Y,  Y = beta o V - (beta Gamma_prev) o (K S)      (= U0 - W S)
-// Eight waves in two groups of four, each wave owning 32 x 32 blocks (2 x 2
-// tiles of 16 x 16), so every fragment read from LDS feeds two MFMAs:
-//   phase 1   waves 0-3: K S, then Y (one block each), split into the
-//             (dec o U)^T planes;  waves 4-7: Q S (one block each), kept in
-//             registers
-//   phase 1b  all waves: U = T Y (two 16 x 16 tiles each; T is unit lower
-//             triangular, so the first token half skips the second), then,
-//             after every read of Y, U^T and (dec o U)^T as (hi, lo) planes
-//   phase 2   waves 0-3: S = Gamma_C S + K^T (dec o U) on the 2 x 4 state
-//             tiles each owns (32 rows of the slice), K^T fragments gathered
-//             from the row-major K tile, then the transposed (hi, lo) copy of
-//             S for the next chunk;  waves 4-7: O = Gamma (Q S) + A U (A is
-//             causal: the first token block skips the second half of A)
+// Wave w owns the 16 x 16 tiles (token tile 2 tp + a, column tile tn), tp = w
+// / 4, tn = w % 4, a = 0, 1 (each fragment read from LDS feeds two MFMAs), and
+// the state rows 16 w .. 16 w + 15 of the slice (four tiles, in registers):
+//   phase 1   K S and Q S on its tiles, then Y, split into the Y^T planes
+//   phase 1b  U = T Y on its tiles (T is unit lower triangular, so the first
+//             token half skips the second), then, after every read of Y, U^T
+//             and (Gamma_C/Gamma o U)^T as (hi, lo) planes
+//   phase 2   O = Gamma (Q S) + A U on its tiles (A is causal likewise), and
+//             S = Gamma_C S + K^T (dec o U) on its state rows, the K^T
+//             fragment (8 tokens of one dim per lane) gathered from the
+//             row-major K tile, then the transposed (hi, lo) copy of S for the
+//             next chunk
 //   then the next chunk's operands go to LDS.
-// The next chunk's K, Q, T and V rows are fetched at the start of a chunk, its
-// A and per-token factors after phase 1, so the loads drain behind the MFMAs.
-// Every wave issues the same memory operations in the same order in every
-// iteration (waves 0-3 issue the output stores of waves 4-7 with offsets past
-// the buffer, which the hardware drops; the last chunk fetches itself again),
-// so each wait for a load counts a fixed number of operations after it and the
-// loads of the next chunk stay in flight across it.
+// Every wave does the same work.  The next chunk's K, Q, T and V rows are
+// fetched at the start of a chunk, its A and per-token factors after phase 1,
+// so the loads drain behind the MFMAs; every wave issues the same memory
+// operations in the same order in every iteration (the last chunk fetches
+// itself again), so each wait for a load counts a fixed number of operations
+// after it and the loads of the next chunk stay in flight across it.
 template <int DK, int DV, int DVS>
 __global__ __launch_bounds__(kScanThreads) void gdn_chunk_scan_t_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
@@ -799,6 +797,7 @@ __global__ __launch_bounds__(kScanThreads) void gdn_chunk_scan_t_kernel(
   constexpr int T_N = 2 * kC * kC / 8 / NT;  // uint4 of T (hi and lo planes) per thread
   constexpr int A_N = 2 * kC * kC / 8 / NT;  // uint4 of A (hi and lo planes) per thread
   static_assert(KQ_N == 2 && T_N == 2 && A_N == 2 && kC * DVS / 8 == NT, "tile split");
+  static_assert(NT / 64 == DK / 16, "one 16-row state stripe per wave");
   __shared__ __align__(16) uint16_t Qs[kC * PB], Ks[kC * PB];        // row-major [t][d]
   __shared__ __align__(16) uint16_t Thi[kC * PT], Tlo[kC * PT];      // T [t][i]
   __shared__ __align__(16) uint16_t Ahi[kC * PT], Alo[kC * PT];      // A [t][i]
@@ -821,38 +820,33 @@ __global__ __launch_bounds__(kScanThreads) void gdn_chunk_scan_t_kernel(
   const int b = bh / H, h = bh - (bh / H) * H;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int grp = wave >> 2, wi = wave & 3;
-  const int bm = wi >> 1, bn = wi & 1;  // phase-1 block: token tiles 2bm, 2bm+1; column tiles 2bn, 2bn+1
+  const int tp = wave >> 2, tn = wave & 3;  // tiles (2 tp + a, tn)
   const int r16 = lane & 15, g4 = lane >> 4;
   const long long rk = static_cast<long long>(H) * DK, rv = static_cast<long long>(H) * DV;
   float* Sg = state + (static_cast<long long>(bh) * DK) * DV + DVS * sl;
 
-  // ---- state tiles of waves 0-3: d tiles 2 wi + a, column tiles c (D layout)
-  f32x4 sreg[2][4];
+  // ---- this wave's state rows 16 wave + 4 g4 + i, column tiles c (D layout)
+  f32x4 sreg[4];
 #pragma unroll
-  for (int a = 0; a < 2; ++a)
+  for (int c = 0; c < 4; ++c)
 #pragma unroll
-    for (int c = 0; c < 4; ++c)
-#pragma unroll
-      for (int i = 0; i < 4; ++i)  // (waves 4-7 read the same tiles and never use them)
-        sreg[a][c][i] = Sg[static_cast<long long>(16 * (2 * wi + a) + 4 * g4 + i) * DV + 16 * c + r16];
+    for (int i = 0; i < 4; ++i)
+      sreg[c][i] = Sg[static_cast<long long>(16 * wave + 4 * g4 + i) * DV + 16 * c + r16];
   auto split_state = [&]() {
 #pragma unroll
-    for (int a = 0; a < 2; ++a)
+    for (int c = 0; c < 4; ++c) {
+      uint16_t hh[4], ll[4];
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        uint16_t hh[4], ll[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          hh[i] = f2bf(sreg[a][c][i]);
-          ll[i] = f2bf(sreg[a][c][i] - bf2f(hh[i]));
-        }
-        const int off = (16 * c + r16) * PB + 16 * (2 * wi + a) + 4 * g4;
-        *reinterpret_cast<uint2*>(SThi + off) = uint2{pack_bf2u(hh[0], hh[1]), pack_bf2u(hh[2], hh[3])};
-        *reinterpret_cast<uint2*>(STlo + off) = uint2{pack_bf2u(ll[0], ll[1]), pack_bf2u(ll[2], ll[3])};
+      for (int i = 0; i < 4; ++i) {
+        hh[i] = f2bf(sreg[c][i]);
+        ll[i] = f2bf(sreg[c][i] - bf2f(hh[i]));
       }
+      const int off = (16 * c + r16) * PB + 16 * wave + 4 * g4;
+      *reinterpret_cast<uint2*>(SThi + off) = uint2{pack_bf2u(hh[0], hh[1]), pack_bf2u(hh[2], hh[3])};
+      *reinterpret_cast<uint2*>(STlo + off) = uint2{pack_bf2u(ll[0], ll[1]), pack_bf2u(ll[2], ll[3])};
+    }
   };
-  if (grp == 0) split_state();
+  split_state();
 
   // ---- prefetch registers
   u32x4 pk[KQ_N], pq[KQ_N], pt[T_N], pa[A_N], pv;
@@ -926,76 +920,63 @@ __global__ __launch_bounds__(kScanThreads) void gdn_chunk_scan_t_kernel(
     const int cn = min(c + 1, NC - 1);
     fetch1(cn);
 
-    // ---- phase 1
-    f32x4 acc[2][2];
+    // ---- phase 1: K S and Q S on tiles (2 tp + a, tn); K and Q exact in bf16
+    // this lane's V, beta, beta Gamma_prev (for Y), Gamma_C / Gamma (for the
+    // U split) and Gamma (for O), read once per chunk
+    float vv[2][4], bt[2][4], ws[2][4], dv[2][4], ev[2][4];
 #pragma unroll
     for (int a = 0; a < 2; ++a)
 #pragma unroll
-      for (int cc = 0; cc < 2; ++cc) acc[a][cc] = f32x4{0.f, 0.f, 0.f, 0.f};
-    if (grp == 0) {
-      // K S on token tiles 2bm + a, column tiles 2bn + cc (K exact in bf16)
-#pragma unroll
-      for (int s = 0; s < DK / 32; ++s) {
-        uint4 ka[2], bhv[2], blv[2];
-#pragma unroll
-        for (int a = 0; a < 2; ++a) {
-          ka[a] = *reinterpret_cast<const uint4*>(Ks + (16 * (2 * bm + a) + r16) * PB + 32 * s + 8 * g4);
-          const int bo = (16 * (2 * bn + a) + r16) * PB + 32 * s + 8 * g4;
-          bhv[a] = *reinterpret_cast<const uint4*>(SThi + bo);
-          blv[a] = *reinterpret_cast<const uint4*>(STlo + bo);
-        }
-#pragma unroll
-        for (int a = 0; a < 2; ++a)
-#pragma unroll
-          for (int cc = 0; cc < 2; ++cc) {
-            acc[a][cc] = mfma16(ka[a], bhv[cc], acc[a][cc]);
-            acc[a][cc] = mfma16(ka[a], blv[cc], acc[a][cc]);
-          }
+      for (int i = 0; i < 4; ++i) {
+        const int t = 16 * (2 * tp + a) + 4 * g4 + i;
+        vv[a][i] = bf2f(Vs[t * PV + 16 * tn + r16]);
+        bt[a][i] = bet[t];
+        ws[a][i] = wsc[t];
+        dv[a][i] = dec[t];
+        ev[a][i] = ecum[t];
       }
-      // Y = beta o V - (beta Gamma_prev) o (K S), split into the Y^T planes
+    f32x4 ks[2], qs[2];
 #pragma unroll
-      for (int a = 0; a < 2; ++a)
+    for (int a = 0; a < 2; ++a) ks[a] = qs[a] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int cc = 0; cc < 2; ++cc) {
-          const int tm = 2 * bm + a, tn = 2 * bn + cc;
-          uint16_t yh[4], yl[4];
+    for (int s = 0; s < DK / 32; ++s) {
+      uint4 ka[2], qa[2];
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int t = 16 * tm + 4 * g4 + i;
-            const float y = bet[t] * bf2f(Vs[t * PV + 16 * tn + r16]) - wsc[t] * acc[a][cc][i];
-            yh[i] = f2bf(y);
-            yl[i] = f2bf(y - bf2f(yh[i]));
-          }
-          const int off = (16 * tn + r16) * PT + 16 * tm + 4 * g4;
-          *reinterpret_cast<uint2*>(DThi + off) = uint2{pack_bf2u(yh[0], yh[1]), pack_bf2u(yh[2], yh[3])};
-          *reinterpret_cast<uint2*>(DTlo + off) = uint2{pack_bf2u(yl[0], yl[1]), pack_bf2u(yl[2], yl[3])};
-        }
-    } else {
-      // Q S on token tiles 2bm + a, column tiles 2bn + cc (kept in acc)
-#pragma unroll
-      for (int s = 0; s < DK / 32; ++s) {
-        uint4 qa[2], bhv[2], blv[2];
-#pragma unroll
-        for (int a = 0; a < 2; ++a) {
-          qa[a] = *reinterpret_cast<const uint4*>(Qs + (16 * (2 * bm + a) + r16) * PB + 32 * s + 8 * g4);
-          const int bo = (16 * (2 * bn + a) + r16) * PB + 32 * s + 8 * g4;
-          bhv[a] = *reinterpret_cast<const uint4*>(SThi + bo);
-          blv[a] = *reinterpret_cast<const uint4*>(STlo + bo);
-        }
-#pragma unroll
-        for (int a = 0; a < 2; ++a)
-#pragma unroll
-          for (int cc = 0; cc < 2; ++cc) {
-            acc[a][cc] = mfma16(qa[a], bhv[cc], acc[a][cc]);
-            acc[a][cc] = mfma16(qa[a], blv[cc], acc[a][cc]);
-          }
+      for (int a = 0; a < 2; ++a) {
+        const int ao = (16 * (2 * tp + a) + r16) * PB + 32 * s + 8 * g4;
+        ka[a] = *reinterpret_cast<const uint4*>(Ks + ao);
+        qa[a] = *reinterpret_cast<const uint4*>(Qs + ao);
       }
+      const int bo = (16 * tn + r16) * PB + 32 * s + 8 * g4;
+      const uint4 bhv = *reinterpret_cast<const uint4*>(SThi + bo);
+      const uint4 blv = *reinterpret_cast<const uint4*>(STlo + bo);
+#pragma unroll
+      for (int a = 0; a < 2; ++a) {
+        ks[a] = mfma16(ka[a], bhv, ks[a]);
+        ks[a] = mfma16(ka[a], blv, ks[a]);
+        qs[a] = mfma16(qa[a], bhv, qs[a]);
+        qs[a] = mfma16(qa[a], blv, qs[a]);
+      }
+    }
+    // Y = beta o V - (beta Gamma_prev) o (K S), split into the Y^T planes
+#pragma unroll
+    for (int a = 0; a < 2; ++a) {
+      const int tm = 2 * tp + a;
+      uint16_t yh[4], yl[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float y = bt[a][i] * vv[a][i] - ws[a][i] * ks[a][i];
+        yh[i] = f2bf(y);
+        yl[i] = f2bf(y - bf2f(yh[i]));
+      }
+      const int off = (16 * tn + r16) * PT + 16 * tm + 4 * g4;
+      *reinterpret_cast<uint2*>(DThi + off) = uint2{pack_bf2u(yh[0], yh[1]), pack_bf2u(yh[2], yh[3])};
+      *reinterpret_cast<uint2*>(DTlo + off) = uint2{pack_bf2u(yl[0], yl[1]), pack_bf2u(yl[2], yl[3])};
     }
     __syncthreads();  // Y^T complete; every read of S^T done
     fetch2(cn);
 
-    // ---- phase 1b: U = T Y on token tiles 2 tp + a, column tile tn
-    const int tp = wave >> 2, tn1 = wave & 3;
+    // ---- phase 1b: U = T Y on tiles (2 tp + a, tn)
     f32x4 u[2];
 #pragma unroll
     for (int a = 0; a < 2; ++a) u[a] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -1009,7 +990,7 @@ __global__ __launch_bounds__(kScanThreads) void gdn_chunk_scan_t_kernel(
         th[a] = *reinterpret_cast<const uint4*>(Thi + ao);
         tl[a] = *reinterpret_cast<const uint4*>(Tlo + ao);
       }
-      const int bo = (16 * tn1 + r16) * PT + 32 * s + 8 * g4;
+      const int bo = (16 * tn + r16) * PT + 32 * s + 8 * g4;
       const uint4 yhv = *reinterpret_cast<const uint4*>(DThi + bo);
       const uint4 ylv = *reinterpret_cast<const uint4*>(DTlo + bo);
 #pragma unroll
@@ -1029,11 +1010,11 @@ __global__ __launch_bounds__(kScanThreads) void gdn_chunk_scan_t_kernel(
         const float uval = u[a][i];
         uh[i] = f2bf(uval);
         ul[i] = f2bf(uval - bf2f(uh[i]));
-        const float dval = dec[16 * tm + 4 * g4 + i] * uval;
+        const float dval = dv[a][i] * uval;
         dh[i] = f2bf(dval);
         dl[i] = f2bf(dval - bf2f(dh[i]));
       }
-      const int off = (16 * tn1 + r16) * PT + 16 * tm + 4 * g4;
+      const int off = (16 * tn + r16) * PT + 16 * tm + 4 * g4;
       *reinterpret_cast<uint2*>(UThi + off) = uint2{pack_bf2u(uh[0], uh[1]), pack_bf2u(uh[2], uh[3])};
       *reinterpret_cast<uint2*>(UTlo + off) = uint2{pack_bf2u(ul[0], ul[1]), pack_bf2u(ul[2], ul[3])};
       *reinterpret_cast<uint2*>(DThi + off) = uint2{pack_bf2u(dh[0], dh[1]), pack_bf2u(dh[2], dh[3])};
@@ -1041,106 +1022,78 @@ __global__ __launch_bounds__(kScanThreads) void gdn_chunk_scan_t_kernel(
     }
     __syncthreads();  // U^T and (dec o U)^T complete
 
-    // ---- phase 2; output rows past the chunk lie beyond the buffer range
-    const __amdgpu_buffer_rsrc_t orsrc = __builtin_amdgcn_make_buffer_rsrc(
-        out + (static_cast<long long>(b) * T + t0) * rv + static_cast<long long>(h) * DV + DVS * sl,
-        static_cast<short>(0), static_cast<int>(((Tc - 1) * rv + DVS) * 2), 0x00020000);
-    if (grp == 0) {
-      // S = Gamma_C S + K^T (dec o U) on d tiles 2 wi + a, column tiles c,
-      // accumulated onto the decayed state in place; the K^T fragment (8
-      // tokens of one dim per lane) is gathered from the row-major K tile
+    // ---- phase 2: O on tiles (2 tp + a, tn); output rows past the chunk lie
+    // beyond the buffer range (the hardware drops those stores)
+    {
+      const __amdgpu_buffer_rsrc_t orsrc = __builtin_amdgcn_make_buffer_rsrc(
+          out + (static_cast<long long>(b) * T + t0) * rv + static_cast<long long>(h) * DV + DVS * sl,
+          static_cast<short>(0), static_cast<int>(((Tc - 1) * rv + DVS) * 2), 0x00020000);
+      f32x4 au[2];
 #pragma unroll
-      for (int a = 0; a < 2; ++a)
-#pragma unroll
-        for (int cc = 0; cc < 4; ++cc)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) sreg[a][cc][i] *= gc;
+      for (int a = 0; a < 2; ++a) au[a] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int s = 0; s < kC / 32; ++s) {
-        uint4 ka[2];
+        if (s > tp) break;  // A is causal: tokens 0..31 see no later token
+        uint4 ah[2], al[2];
 #pragma unroll
         for (int a = 0; a < 2; ++a) {
-          const uint16_t* kc = Ks + (32 * s + 8 * g4) * PB + 16 * (2 * wi + a) + r16;
-          uint16_t e[8];
-#pragma unroll
-          for (int j = 0; j < 8; ++j) e[j] = kc[j * PB];
-          ka[a] = uint4{pack_bf2u(e[0], e[1]), pack_bf2u(e[2], e[3]), pack_bf2u(e[4], e[5]),
-                        pack_bf2u(e[6], e[7])};
-        }
-#pragma unroll
-        for (int cc = 0; cc < 4; ++cc) {
-          const int bo = (16 * cc + r16) * PT + 32 * s + 8 * g4;
-          const uint4 dhv = *reinterpret_cast<const uint4*>(DThi + bo);
-          const uint4 dlv = *reinterpret_cast<const uint4*>(DTlo + bo);
-#pragma unroll
-          for (int a = 0; a < 2; ++a) {
-            sreg[a][cc] = mfma16(ka[a], dhv, sreg[a][cc]);
-            sreg[a][cc] = mfma16(ka[a], dlv, sreg[a][cc]);
-          }
-        }
-      }
-      split_state();
-      // the output stores of waves 4-7, past the buffer range (dropped)
-#pragma unroll
-      for (int j = 0; j < 16; ++j)
-        __builtin_amdgcn_raw_buffer_store_b16(static_cast<uint16_t>(j), orsrc, 0x7fffff00 + 2 * j, 0,
-                                              0);
-    } else {
-      // O = Gamma (Q S) + A U on token tiles 2bm + a, column tiles 2bn + cc
-      f32x4 au[2][2];
-#pragma unroll
-      for (int a = 0; a < 2; ++a)
-#pragma unroll
-        for (int cc = 0; cc < 2; ++cc) au[a][cc] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int s = 0; s < kC / 32; ++s) {
-        if (s > bm) break;  // token tiles 0, 1 see no token of the second half
-        uint4 ah[2], al[2], uhv[2], ulv[2];
-#pragma unroll
-        for (int a = 0; a < 2; ++a) {
-          const int ao = (16 * (2 * bm + a) + r16) * PT + 32 * s + 8 * g4;
+          const int ao = (16 * (2 * tp + a) + r16) * PT + 32 * s + 8 * g4;
           ah[a] = *reinterpret_cast<const uint4*>(Ahi + ao);
           al[a] = *reinterpret_cast<const uint4*>(Alo + ao);
-          const int bo = (16 * (2 * bn + a) + r16) * PT + 32 * s + 8 * g4;
-          uhv[a] = *reinterpret_cast<const uint4*>(UThi + bo);
-          ulv[a] = *reinterpret_cast<const uint4*>(UTlo + bo);
         }
+        const int bo = (16 * tn + r16) * PT + 32 * s + 8 * g4;
+        const uint4 uhv = *reinterpret_cast<const uint4*>(UThi + bo);
+        const uint4 ulv = *reinterpret_cast<const uint4*>(UTlo + bo);
 #pragma unroll
-        for (int a = 0; a < 2; ++a)
-#pragma unroll
-          for (int cc = 0; cc < 2; ++cc) {
-            au[a][cc] = mfma16(ah[a], uhv[cc], au[a][cc]);
-            au[a][cc] = mfma16(ah[a], ulv[cc], au[a][cc]);
-            au[a][cc] = mfma16(al[a], uhv[cc], au[a][cc]);
-          }
+        for (int a = 0; a < 2; ++a) {
+          au[a] = mfma16(ah[a], uhv, au[a]);
+          au[a] = mfma16(ah[a], ulv, au[a]);
+          au[a] = mfma16(al[a], uhv, au[a]);
+        }
       }
 #pragma unroll
       for (int a = 0; a < 2; ++a)
 #pragma unroll
-        for (int cc = 0; cc < 2; ++cc)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int t = 16 * (2 * bm + a) + 4 * g4 + i;
-            const float o = ecum[t] * acc[a][cc][i] + au[a][cc][i];
-            __builtin_amdgcn_raw_buffer_store_b16(
-                f2bf(o), orsrc, static_cast<int>((t * rv + 16 * (2 * bn + cc) + r16) * 2), 0, 0);
-          }
+        for (int i = 0; i < 4; ++i) {
+          const int t = 16 * (2 * tp + a) + 4 * g4 + i;
+          const float o = ev[a][i] * qs[a][i] + au[a][i];
+          __builtin_amdgcn_raw_buffer_store_b16(
+              f2bf(o), orsrc, static_cast<int>((t * rv + 16 * tn + r16) * 2), 0, 0);
+        }
     }
+    // ---- phase 2: S = Gamma_C S + K^T (dec o U) on state rows 16 wave ..,
+    // accumulated onto the decayed state in place
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sreg[cc][i] *= gc;
+#pragma unroll
+    for (int s = 0; s < kC / 32; ++s) {
+      const uint16_t* kc = Ks + (32 * s + 8 * g4) * PB + 16 * wave + r16;
+      uint16_t e[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) e[j] = kc[j * PB];
+      const uint4 ka = uint4{pack_bf2u(e[0], e[1]), pack_bf2u(e[2], e[3]), pack_bf2u(e[4], e[5]),
+                             pack_bf2u(e[6], e[7])};
+#pragma unroll
+      for (int cc = 0; cc < 4; ++cc) {
+        const int bo = (16 * cc + r16) * PT + 32 * s + 8 * g4;
+        sreg[cc] = mfma16(ka, *reinterpret_cast<const uint4*>(DThi + bo), sreg[cc]);
+        sreg[cc] = mfma16(ka, *reinterpret_cast<const uint4*>(DTlo + bo), sreg[cc]);
+      }
+    }
+    split_state();
     __syncthreads();  // every wave is done with this chunk's LDS operands; S^T updated
     if (c + 1 < NC) {
       stash(c + 1);
       __syncthreads();
     }
   }
-  if (grp == 0) {
 #pragma unroll
-    for (int a = 0; a < 2; ++a)
+  for (int c = 0; c < 4; ++c)
 #pragma unroll
-      for (int c = 0; c < 4; ++c)
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          Sg[static_cast<long long>(16 * (2 * wi + a) + 4 * g4 + i) * DV + 16 * c + r16] = sreg[a][c][i];
-  }
+    for (int i = 0; i < 4; ++i)
+      Sg[static_cast<long long>(16 * wave + 4 * g4 + i) * DV + 16 * c + r16] = sreg[c][i];
 }
 
 }  // namespace llmy
