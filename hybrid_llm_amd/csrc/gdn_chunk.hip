@@ -115,7 +115,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
 
   // Persistent: workgroup w takes chunks w, w + gridDim.x, ...  The next
   // chunk's K and Q rows and per-token g, beta and reset flags are loaded into
-  // registers during the current one's W and U0 products.  Every wave issues the same
+  // registers while the current one is worked out (dk = 128: from the block
+  // levels of the inverse on; dk = 64: during the W and U0 products).  Every wave issues the same
   // loads (rows past a chunk and the last chunk's "next" re-read valid rows;
   // without resets the flags are read from g and ignored), so each wait counts
   // a fixed number of memory operations after the load it waits for.
@@ -142,6 +143,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
     prs = (reset != nullptr ? reset : reinterpret_cast<const int32_t*>(g))[tok];
   };
   if (static_cast<int>(blockIdx.x) < n_chunks) prefetch(blockIdx.x);
+  // the upper 16 x 16 blocks of T = (I + L)^{-1} are zero; no later write
+  // touches them (the inverse writes the diagonal and lower blocks)
+  for (int e = threadIdx.x; e < kC * kC; e += 256) {
+    const int t = e >> 6, i = e & 63;
+    if ((i >> 4) > (t >> 4)) Ti[t * PG + i] = 0.f;
+  }
   for (int cid = blockIdx.x; cid < n_chunks; cid += gridDim.x) {
   const int bh = cid / NC;
   const int c = cid - bh * NC;
@@ -197,8 +204,31 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
   // blocks.  K K^T becomes L in LDS; A = (Gamma_t / Gamma_i) q_t . k_i
   // (i <= t) is formed in registers and written as (hi, lo) bf16 planes.
   const long long wo = static_cast<long long>(cid) * kC;
+  // per-token factors of this lane's rows, read once: L rows 16 w + 4 g4 + i,
+  // the A row 16 w + r16
+  float lbet[4], lprv[4];
+  int lseg[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int t = 16 * wave + 4 * g4 + i;
+    lbet[i] = bet[t];
+    lprv[i] = prv[t];
+    lseg[i] = seg[t];
+  }
+  const float acum = cum[16 * wave + r16];
+  const int aseg = seg[16 * wave + r16];
 #pragma unroll
   for (int tj = 0; tj < 4; ++tj) {
+    // this column block's factors, requested before its MFMAs
+    const float lcum = cum[16 * tj + r16];
+    const int lsj = seg[16 * tj + r16];
+    float acj[4];
+    int asj[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      acj[i] = cum[16 * tj + 4 * g4 + i];
+      asj[i] = seg[16 * tj + 4 * g4 + i];
+    }
     f32x4 a1 = f32x4{0.f, 0.f, 0.f, 0.f}, a2 = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < DK / 32; ++s) {
@@ -213,7 +243,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int t = 16 * wave + 4 * g4 + i, j = 16 * tj + r16;
-      Gm[t * PG + j] = j < t && seg[j] == seg[t] ? bet[t] * __expf(prv[t] - cum[j]) * a1[i] : 0.f;
+      Gm[t * PG + j] = j < t && lsj == lseg[i] ? lbet[i] * __expf(lprv[i] - lcum) * a1[i] : 0.f;
     }
     {
       const int t = 16 * wave + r16, j0 = 16 * tj + 4 * g4;
@@ -221,7 +251,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int j = j0 + i;
-        const float am = j <= t && seg[j] == seg[t] ? __expf(cum[t] - cum[j]) * a2[i] : 0.f;
+        const float am = j <= t && asj[i] == aseg ? __expf(acum - acj[i]) * a2[i] : 0.f;
         hv[i] = f2bf(am);
         lv[i] = f2bf(am - bf2f(hv[i]));
       }
@@ -267,11 +297,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
         Ti[(d0 + t) * PG + d0 + j] = x[t];
       }
     }
-    // upper blocks of T are zero
-    for (int e = threadIdx.x; e < kC * kC; e += 256) {
-      const int t = e >> 6, i = e & 63;
-      if ((i >> 4) > (t >> 4)) Ti[t * PG + i] = 0.f;
-    }
+    // (the upper blocks of T are zero: set once, never written again)
 #pragma unroll
     for (int i = 0; i < (kTOut ? 0 : KPI); ++i) {
       const int f = threadIdx.x + 256 * i;
@@ -288,6 +314,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
       for (int e = 0; e < 2; ++e)
         vp[i][e] = *reinterpret_cast<const uint4*>(v + vbase + min(t2 + e, Tc - 1) * rv + 8 * cc);
     }
+    // dk = 128: the next chunk's rows now, behind the block levels and the T
+    // write (this workgroup's last chunk fetches itself again)
+    if constexpr (kTOut) prefetch(min(cid + static_cast<int>(gridDim.x), n_chunks - 1));
     __syncthreads();
     const int c16 = lane & 15, k4 = lane >> 4;
 #pragma unroll
@@ -349,8 +378,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
                                    : wsc[t];
       U0g[static_cast<long long>(cid) * kC * DV + threadIdx.x] = fv;
     }
-    // the next chunk's rows (this workgroup's last chunk fetches itself again)
-    prefetch(min(cid + static_cast<int>(gridDim.x), n_chunks - 1));
     __syncthreads();  // LDS of this chunk is free for the next
   } else {
   // ---- K^T and V^T into R0 (the block products above are done), from the
