@@ -217,6 +217,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
   }
   const float acum = cum[16 * wave + r16];
   const int aseg = seg[16 * wave + r16];
+  // this wave's row block of K and Q, read once for the four column blocks
+  uint4 kra[DK / 32], qra[DK / 32];
+#pragma unroll
+  for (int s = 0; s < DK / 32; ++s) {
+    kra[s] = *reinterpret_cast<const uint4*>(Ks + (16 * wave + r16) * PK + 32 * s + 8 * g4);
+    qra[s] = *reinterpret_cast<const uint4*>(Qs + (16 * wave + r16) * PK + 32 * s + 8 * g4);
+  }
 #pragma unroll
   for (int tj = 0; tj < 4; ++tj) {
     // this column block's factors, requested before its MFMAs
@@ -232,11 +239,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
     f32x4 a1 = f32x4{0.f, 0.f, 0.f, 0.f}, a2 = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < DK / 32; ++s) {
-      const uint4 ka = *reinterpret_cast<const uint4*>(Ks + (16 * wave + r16) * PK + 32 * s + 8 * g4);
-      const uint4 qa = *reinterpret_cast<const uint4*>(Qs + (16 * wave + r16) * PK + 32 * s + 8 * g4);
       const uint4 kb = *reinterpret_cast<const uint4*>(Ks + (16 * tj + r16) * PK + 32 * s + 8 * g4);
-      a1 = mfma16(ka, kb, a1);
-      a2 = mfma16(kb, qa, a2);  // (K Q^T) block: lane holds 4 consecutive j of row t
+      a1 = mfma16(kra[s], kb, a1);
+      a2 = mfma16(kb, qra[s], a2);  // (K Q^T) block: lane holds 4 consecutive j of row t
     }
     // L[t, j] = beta_t (Gamma_{t-1} / Gamma_j) k_t . k_j for j < t in the same
     // segment (strictly lower), formed from the K K^T block in registers
@@ -290,10 +295,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
       float x[16];
 #pragma unroll
       for (int t = 0; t < 16; ++t) {
-        float a = (t == j) ? 1.f : 0.f;
+        // the dot product in four interleaved partial sums (shorter chains)
+        float a[4] = {(t == j) ? 1.f : 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int i = 0; i < t; ++i) a -= nv[t * (t - 1) / 2 + i] * x[i];
-        x[t] = t < j ? 0.f : a;
+        for (int i = 0; i < t; ++i) a[i & 3] -= nv[t * (t - 1) / 2 + i] * x[i];
+        x[t] = t < j ? 0.f : (a[0] + a[1]) + (a[2] + a[3]);
         Ti[(d0 + t) * PG + d0 + j] = x[t];
       }
     }
@@ -326,7 +332,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
         // P = sum_m N_{bi,m} T_{m,bj}, kept in this wave's rows of Pm (only
         // this wave reads them, and its LDS operations complete in order)
         f32x4 p = f32x4{0.f, 0.f, 0.f, 0.f};
-        for (int m = bj; m < bi; ++m) {
+#pragma unroll
+        for (int mm = 0; mm < lvl; ++mm) {
+          const int m = bj + mm;
 #pragma unroll
           for (int c4 = 0; c4 < 4; ++c4) {
             const float av = Gm[(16 * bi + c16) * PG + 16 * m + 4 * c4 + k4];
