@@ -1167,8 +1167,10 @@ int32_t gdn_prefill_launch(const llmy_bf16* q, const llmy_bf16* k, const llmy_bf
   const int NC = (T + kC - 1) / kC;
   const long long chunks = static_cast<long long>(B) * H * NC;
   const int dv = dk;
-  // workspace: W as (hi, lo) bf16 planes, U0 fp32, A as (hi, lo) bf16 planes,
-  // decay factors [2][64] fp32
+  // workspace, per chunk: W as (hi, lo) bf16 planes, U0 fp32, A as (hi, lo)
+  // bf16 planes, decay factors [2][64] fp32.  dk = 128 uses the W slot for T
+  // = (I + L)^{-1} ((hi, lo) [2][64][64]) and the U0 slot for the per-token
+  // factors [4][64]; its decay-factor slot is unused.
   uint16_t* W = static_cast<uint16_t*>(workspace);
   float* U0 = reinterpret_cast<float*>(W + chunks * kC * dk * 2);
   uint16_t* A = reinterpret_cast<uint16_t*>(U0 + chunks * kC * dv);
