@@ -427,6 +427,8 @@ __global__ __launch_bounds__(64) void cmp_list_decode_kernel(const float* __rest
 // value row is read once for the block; partial sums are added in wave order.
 // out = sum / H.  Value key -> row b * rows_per_b + (wrap ? key % wrap : key)
 // at v_ld.
+constexpr int kApplyMaxH = 16;  // heads whose selections are read in one round trip
+
 template <int QB>
 __global__ __launch_bounds__(256) void cmp_apply_kernel(
     const float* __restrict__ wl, const int32_t* __restrict__ il, int Kmax, int H, int T,
@@ -450,7 +452,38 @@ __global__ __launch_bounds__(256) void cmp_apply_kernel(
   for (int i = threadIdx.x; i < QB * nsp; i += 256) pm[i] = 0.f;
   __syncthreads();
   const int64_t lb0 = (static_cast<int64_t>(b) * T + t0) * H * Kmax;
-  if (il) {
+  if (il && H <= kApplyMaxH && nq * Kmax <= 512) {
+    // every head's (slot, weight) entries requested at once (at most two per
+    // thread per head), then added head by head: a head's slots are
+    // distinct, so each pass is race-free and every slot sums its heads in
+    // head order
+    float wr[kApplyMaxH][2];
+    int ir[kApplyMaxH][2], pr[2];
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const int e = threadIdx.x + 256 * r;
+      pr[r] = e < nq * Kmax ? (e / Kmax) * nsp : -1;
+    }
+#pragma unroll
+    for (int hh = 0; hh < kApplyMaxH; ++hh)
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        const int e = threadIdx.x + 256 * r;
+        const bool ok = hh < H && pr[r] >= 0;
+        const int qq = e / Kmax, j = e - qq * Kmax;
+        const int64_t o = lb0 + (static_cast<int64_t>(qq) * H + hh) * Kmax + j;
+        wr[hh][r] = ok ? wl[o] : 0.f;
+        ir[hh][r] = ok ? il[o] : -1;
+      }
+#pragma unroll
+    for (int hh = 0; hh < kApplyMaxH; ++hh) {
+      if (hh >= H) break;  // uniform
+#pragma unroll
+      for (int r = 0; r < 2; ++r)
+        if (ir[hh][r] >= 0 && ir[hh][r] < nslots) pm[pr[r] + ir[hh][r]] += wr[hh][r];
+      __syncthreads();
+    }
+  } else if (il) {
     for (int hh = 0; hh < H; ++hh) {
       for (int e = threadIdx.x; e < nq * Kmax; e += 256) {
         const int qq = e / Kmax, j = e - qq * Kmax;
@@ -512,7 +545,20 @@ __global__ __launch_bounds__(256) void cmp_apply_kernel(
       acc[qq][3] = fmaf(w, x3, acc[qq][3]);
     }
   };
+  // RU rows in flight per wave (a single query has few workgroups per row, so
+  // the sweep is latency-bound); each wave still adds its rows in slot order
+  constexpr int RU = QB == 1 ? 16 : 4;
   int i = wave;
+  for (; i + 4 * (RU - 1) < n; i += 4 * RU) {
+    int jj[RU];
+    uint2 rr[RU];
+#pragma unroll
+    for (int u = 0; u < RU; ++u) jj[u] = nz[i + 4 * u];
+#pragma unroll
+    for (int u = 0; u < RU; ++u) rr[u] = *reinterpret_cast<const uint2*>(vb + row_of(jj[u]));
+#pragma unroll
+    for (int u = 0; u < RU; ++u) add(jj[u], rr[u]);
+  }
   for (; i + 12 < n; i += 16) {
     const int j0 = nz[i], j1 = nz[i + 4], j2 = nz[i + 8], j3 = nz[i + 12];
     const uint2 r0 = *reinterpret_cast<const uint2*>(vb + row_of(j0));
