@@ -361,36 +361,53 @@ __global__ __launch_bounds__(256) void cmp_score_decode_kernel(
   const int gl = lane % G;
   const uint16_t* qh = q + static_cast<int64_t>(b) * q_ld + h * Dh;
   float* srow = sc + static_cast<int64_t>(bh) * ncand;
+  // every pass's key row first (rows of invisible candidates are clamped in
+  // range and read anyway), so the passes' key loads are in flight together
+  int cs[kPasses];
+  bool vis[kPasses];
+  const uint16_t* kr[kPasses];
 #pragma unroll
   for (int ps = 0; ps < kPasses; ++ps) {
     const int c = chunk * kChunk + wave * (kPasses * kCpw) + ps * kCpw + lane / G;
-    bool vis = c < ncand;
-    const uint16_t* kr;
+    cs[ps] = c;
+    vis[ps] = c < ncand;
     if (MODE == kBand) {
       const int key = p - W + 1 + c;
-      vis = vis && key >= 0;
-      kr = key == p ? k_new + static_cast<int64_t>(b) * kv_ld + h * Dh
-                    : ring_k + (static_cast<int64_t>(b) * W + (key >= 0 ? key % W : 0)) * Kw +
-                          h * Dh;
+      vis[ps] = vis[ps] && key >= 0;
+      kr[ps] = key == p ? k_new + static_cast<int64_t>(b) * kv_ld + h * Dh
+                        : ring_k + (static_cast<int64_t>(b) * W + (key >= 0 ? key % W : 0)) * Kw +
+                              h * Dh;
     } else {
-      const int tag = vis ? mtag[static_cast<int64_t>(b) * C + c] : 0;
-      vis = vis && tag >= 1 && tag <= p + 1;
-      kr = mk + (static_cast<int64_t>(b) * C + (c < ncand ? c : 0)) * Kw + h * Dh;
+      const int cc = c < ncand ? c : 0;
+      const int tag = mtag[static_cast<int64_t>(b) * C + cc];
+      vis[ps] = vis[ps] && tag >= 1 && tag <= p + 1;
+      kr[ps] = mk + (static_cast<int64_t>(b) * C + cc) * Kw + h * Dh;
     }
-    float dot = 0.f;
-    if (vis) {
-      for (int ch = 0; ch < nch; ++ch) {
-        const int e = 8 * (gl + G * ch);
-        float a[8], bb[8];
-        unpack8(*reinterpret_cast<const uint4*>(qh + e), a);
-        unpack8(*reinterpret_cast<const uint4*>(kr + e), bb);
+  }
+  float dot[kPasses];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) dot = fmaf(a[i], bb[i], dot);
-      }
+  for (int ps = 0; ps < kPasses; ++ps) dot[ps] = 0.f;
+  for (int ch = 0; ch < nch; ++ch) {
+    const int e = 8 * (gl + G * ch);
+    uint4 kk[kPasses];
+#pragma unroll
+    for (int ps = 0; ps < kPasses; ++ps) kk[ps] = *reinterpret_cast<const uint4*>(kr[ps] + e);
+    float a[8];
+    unpack8(*reinterpret_cast<const uint4*>(qh + e), a);
+#pragma unroll
+    for (int ps = 0; ps < kPasses; ++ps) {
+      float bb[8];
+      unpack8(kk[ps], bb);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) dot[ps] = fmaf(a[i], bb[i], dot[ps]);
     }
+  }
 #pragma unroll
-    for (int o = G / 2; o >= 1; o >>= 1) dot += __shfl_xor(dot, o, kWave);
-    if (gl == 0 && c < ncand) srow[c] = vis ? dot * scale_log2 : -INFINITY;
+  for (int ps = 0; ps < kPasses; ++ps) {
+    float d = dot[ps];
+#pragma unroll
+    for (int o = G / 2; o >= 1; o >>= 1) d += __shfl_xor(d, o, kWave);
+    if (gl == 0 && cs[ps] < ncand) srow[cs[ps]] = vis[ps] ? d * scale_log2 : -INFINITY;
   }
 }
 
@@ -423,14 +440,19 @@ __global__ __launch_bounds__(64) void cmp_list_decode_kernel(const float* __rest
 // the heads slot by slot; (index, probability) pairs are added head by head
 // (one head's indices are distinct, so each sum runs in head order and the
 // result does not depend on scheduling).  Wave 0 compacts the slots any query
-// uses; the four waves split them, each lane 4 channels of every query, so a
+// uses; the NW waves split them, each lane 4 channels of every query, so a
 // value row is read once for the block; partial sums are added in wave order.
 // out = sum / H.  Value key -> row b * rows_per_b + (wrap ? key % wrap : key)
 // at v_ld.
 constexpr int kApplyMaxH = 16;  // heads whose selections are read in one round trip
+#ifndef LLMY_APPLY_DECODE_WAVES
+#define LLMY_APPLY_DECODE_WAVES 8
+#endif
+// single queries: few workgroups per row, so more waves share a row's slots
+constexpr int kApplyDecodeWaves = LLMY_APPLY_DECODE_WAVES;
 
-template <int QB>
-__global__ __launch_bounds__(256) void cmp_apply_kernel(
+template <int QB, int NW>
+__global__ __launch_bounds__(64 * NW) void cmp_apply_kernel(
     const float* __restrict__ wl, const int32_t* __restrict__ il, int Kmax, int H, int T,
     const int32_t* __restrict__ qpos, int band_W, int nslots, const uint16_t* __restrict__ v,
     int64_t v_ld, int rows_per_b, int wrap, uint16_t* __restrict__ out, int64_t out_ld,
@@ -438,8 +460,9 @@ __global__ __launch_bounds__(256) void cmp_apply_kernel(
   extern __shared__ float pm[];
   const int nsb = band_W > 0 ? nslots + QB - 1 : nslots;   // block slots
   const int nsp = (nsb + 3) & ~3;
-  float* red = pm + QB * nsp;                          // [4][256] partial sums
-  int* nz = reinterpret_cast<int*>(red + 4 * 256);     // [nsb] compacted slots
+  constexpr int NT = 64 * NW;
+  float* red = pm + QB * nsp;                          // [NW][256] partial sums
+  int* nz = reinterpret_cast<int*>(red + NW * 256);    // [nsb] compacted slots
   __shared__ int nz_count;
   const int ndb = (Dv + 255) / 256;
   const int nqb = (T + QB - 1) / QB;
@@ -449,26 +472,27 @@ __global__ __launch_bounds__(256) void cmp_apply_kernel(
   const int t0 = (blk - b * nqb) * QB;
   const int nq = min(QB, T - t0);
   const int p0 = qpos ? max(qpos[b], 0) : t0;
-  for (int i = threadIdx.x; i < QB * nsp; i += 256) pm[i] = 0.f;
+  for (int i = threadIdx.x; i < QB * nsp; i += NT) pm[i] = 0.f;
   __syncthreads();
   const int64_t lb0 = (static_cast<int64_t>(b) * T + t0) * H * Kmax;
   if (il && H <= kApplyMaxH && nq * Kmax <= 512) {
-    // every head's (slot, weight) entries requested at once (at most two per
+    // every head's (slot, weight) entries requested at once (at most RE per
     // thread per head), then added head by head: a head's slots are
     // distinct, so each pass is race-free and every slot sums its heads in
     // head order
-    float wr[kApplyMaxH][2];
-    int ir[kApplyMaxH][2], pr[2];
+    constexpr int RE = (512 + NT - 1) / NT;
+    float wr[kApplyMaxH][RE];
+    int ir[kApplyMaxH][RE], pr[RE];
 #pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      const int e = threadIdx.x + 256 * r;
+    for (int r = 0; r < RE; ++r) {
+      const int e = threadIdx.x + NT * r;
       pr[r] = e < nq * Kmax ? (e / Kmax) * nsp : -1;
     }
 #pragma unroll
     for (int hh = 0; hh < kApplyMaxH; ++hh)
 #pragma unroll
-      for (int r = 0; r < 2; ++r) {
-        const int e = threadIdx.x + 256 * r;
+      for (int r = 0; r < RE; ++r) {
+        const int e = threadIdx.x + NT * r;
         const bool ok = hh < H && pr[r] >= 0;
         const int qq = e / Kmax, j = e - qq * Kmax;
         const int64_t o = lb0 + (static_cast<int64_t>(qq) * H + hh) * Kmax + j;
@@ -479,13 +503,13 @@ __global__ __launch_bounds__(256) void cmp_apply_kernel(
     for (int hh = 0; hh < kApplyMaxH; ++hh) {
       if (hh >= H) break;  // uniform
 #pragma unroll
-      for (int r = 0; r < 2; ++r)
+      for (int r = 0; r < RE; ++r)
         if (ir[hh][r] >= 0 && ir[hh][r] < nslots) pm[pr[r] + ir[hh][r]] += wr[hh][r];
       __syncthreads();
     }
   } else if (il) {
     for (int hh = 0; hh < H; ++hh) {
-      for (int e = threadIdx.x; e < nq * Kmax; e += 256) {
+      for (int e = threadIdx.x; e < nq * Kmax; e += NT) {
         const int qq = e / Kmax, j = e - qq * Kmax;
         const int64_t o = lb0 + (static_cast<int64_t>(qq) * H + hh) * Kmax + j;
         const int idx = il[o];
@@ -494,7 +518,7 @@ __global__ __launch_bounds__(256) void cmp_apply_kernel(
       __syncthreads();
     }
   } else {
-    for (int e = threadIdx.x; e < nq * nslots; e += 256) {
+    for (int e = threadIdx.x; e < nq * nslots; e += NT) {
       const int qq = e / nslots, j = e - qq * nslots;
       const int64_t o = lb0 + static_cast<int64_t>(qq) * H * Kmax + j;
       float acc = 0.f;
@@ -549,18 +573,18 @@ __global__ __launch_bounds__(256) void cmp_apply_kernel(
   // the sweep is latency-bound); each wave still adds its rows in slot order
   constexpr int RU = QB == 1 ? 16 : 4;
   int i = wave;
-  for (; i + 4 * (RU - 1) < n; i += 4 * RU) {
+  for (; i + NW * (RU - 1) < n; i += NW * RU) {
     int jj[RU];
     uint2 rr[RU];
 #pragma unroll
-    for (int u = 0; u < RU; ++u) jj[u] = nz[i + 4 * u];
+    for (int u = 0; u < RU; ++u) jj[u] = nz[i + NW * u];
 #pragma unroll
     for (int u = 0; u < RU; ++u) rr[u] = *reinterpret_cast<const uint2*>(vb + row_of(jj[u]));
 #pragma unroll
     for (int u = 0; u < RU; ++u) add(jj[u], rr[u]);
   }
-  for (; i + 12 < n; i += 16) {
-    const int j0 = nz[i], j1 = nz[i + 4], j2 = nz[i + 8], j3 = nz[i + 12];
+  for (; i + 3 * NW < n; i += 4 * NW) {
+    const int j0 = nz[i], j1 = nz[i + NW], j2 = nz[i + 2 * NW], j3 = nz[i + 3 * NW];
     const uint2 r0 = *reinterpret_cast<const uint2*>(vb + row_of(j0));
     const uint2 r1 = *reinterpret_cast<const uint2*>(vb + row_of(j1));
     const uint2 r2 = *reinterpret_cast<const uint2*>(vb + row_of(j2));
@@ -570,7 +594,7 @@ __global__ __launch_bounds__(256) void cmp_apply_kernel(
     add(j2, r2);
     add(j3, r3);
   }
-  for (; i < n; i += 4) {
+  for (; i < n; i += NW) {
     const int j = nz[i];
     add(j, *reinterpret_cast<const uint2*>(vb + row_of(j)));
   }
@@ -582,9 +606,10 @@ __global__ __launch_bounds__(256) void cmp_apply_kernel(
     *reinterpret_cast<float4*>(red + wave * 256 + 4 * lane) =
         make_float4(acc[qq][0], acc[qq][1], acc[qq][2], acc[qq][3]);
     __syncthreads();
-    if (c < Dv) {
-      const float sum = ((red[threadIdx.x] + red[256 + threadIdx.x]) + red[512 + threadIdx.x]) +
-                        red[768 + threadIdx.x];
+    if (threadIdx.x < 256 && c < Dv) {
+      float sum = red[threadIdx.x];
+#pragma unroll
+      for (int w = 1; w < NW; ++w) sum += red[w * 256 + threadIdx.x];
       out[(static_cast<int64_t>(b) * T + t0 + qq) * out_ld + c] = f2bf(sum * invH);
     }
     __syncthreads();
@@ -760,17 +785,19 @@ int32_t apply_launch(const float* wl, const int32_t* il, int Kmax, int H, int B,
   // single queries for decode
   const int QB = T >= 8 ? 8 : 1;
   const int nsb = band_W > 0 ? nslots + QB - 1 : nslots;
-  const size_t lds = (static_cast<size_t>(QB) * ((nsb + 3) & ~3) + 4 * 256 +
+  const int NW = QB == 8 ? 4 : kApplyDecodeWaves;
+  const size_t lds = (static_cast<size_t>(QB) * ((nsb + 3) & ~3) + NW * 256 +
                       static_cast<size_t>(nsb)) * 4;
   if (lds > 147456) return static_cast<int32_t>(hipErrorInvalidValue);
   const int64_t nblk = static_cast<int64_t>(B) * ((T + QB - 1) / QB) * ((Dv + 255) / 256);
   if (nblk >= (1ll << 31)) return static_cast<int32_t>(hipErrorInvalidValue);
   if (QB == 8)
-    hipLaunchKernelGGL(cmp_apply_kernel<8>, dim3(static_cast<unsigned>(nblk)), dim3(256), lds, s,
+    hipLaunchKernelGGL((cmp_apply_kernel<8, 4>), dim3(static_cast<unsigned>(nblk)), dim3(256), lds, s,
                        wl, il, Kmax, H, T, qpos, band_W, nslots, v, v_ld, rows_per_b, wrap, out,
                        out_ld, Dv);
   else
-    hipLaunchKernelGGL(cmp_apply_kernel<1>, dim3(static_cast<unsigned>(nblk)), dim3(256), lds, s,
+    hipLaunchKernelGGL((cmp_apply_kernel<1, kApplyDecodeWaves>), dim3(static_cast<unsigned>(nblk)),
+                       dim3(64 * kApplyDecodeWaves), lds, s,
                        wl, il, Kmax, H, T, qpos, band_W, nslots, v, v_ld, rows_per_b, wrap, out,
                        out_ld, Dv);
   return launch_status();
