@@ -430,6 +430,107 @@ __global__ __launch_bounds__(64) void cmp_list_decode_kernel(const float* __rest
   else dense_row(srow, ncand, 0, 0, ncand, lane, wl + lb);
 }
 
+// Scores and list of one (head h, row b) in one workgroup, for rows of at
+// most kFusedMaxCand candidates when B * H is large enough to fill the GPU:
+// the same per-candidate dot products as cmp_score_decode_kernel (G lanes,
+// 16-byte chunks in order, xor-shuffle sums), so the scores are bitwise the
+// same, written to LDS instead of sc; then wave 0 forms the list as
+// cmp_list_decode_kernel does.  Candidate c of pass ps: ps * 4 * (64 / G) +
+// wave * (64 / G) + lane / G; the key rows of PB passes are loaded together.
+constexpr int kFusedMaxCand = 1024;
+
+template <int MODE, int G>
+__global__ __launch_bounds__(256) void cmp_score_list_decode_kernel(
+    const uint16_t* __restrict__ q, int64_t q_ld, const uint16_t* __restrict__ k_new,
+    const uint16_t* __restrict__ v_new, int64_t kv_ld, uint16_t* __restrict__ ring_k,
+    uint16_t* __restrict__ ring_v, const uint16_t* __restrict__ mk,
+    const int32_t* __restrict__ mtag, const int32_t* __restrict__ pos, int H, int Dh, int Dv,
+    int W, int C, float scale_log2, int top_k, int Kmax, float* __restrict__ wl,
+    int32_t* __restrict__ il) {
+  extern __shared__ float srow[];
+  __shared__ float sel_s[kWave];
+  __shared__ int sel_i[kWave];
+  constexpr int kCpw = kWave / G;   // candidates per wave pass
+  constexpr int PB = 8;             // passes whose key rows are in flight together
+  const int ncand = MODE == kBand ? W : C;
+  const int bh = blockIdx.x;
+  const int h = bh % H;
+  const int b = bh / H;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int p = max(pos[b], 0);
+  const int Kw = H * Dh;
+  if (MODE == kBand) {   // this head's slice of k_new (head 0: the v_new row) to slot p % W
+    uint16_t* kslot = ring_k + (static_cast<int64_t>(b) * W + p % W) * Kw + h * Dh;
+    const uint16_t* ksrc = k_new + static_cast<int64_t>(b) * kv_ld + h * Dh;
+    for (int c = threadIdx.x; c < Dh / 8; c += 256)
+      reinterpret_cast<uint4*>(kslot)[c] = reinterpret_cast<const uint4*>(ksrc)[c];
+    if (h == 0) {
+      uint16_t* vslot = ring_v + (static_cast<int64_t>(b) * W + p % W) * Dv;
+      const uint16_t* vsrc = v_new + static_cast<int64_t>(b) * kv_ld;
+      for (int c = threadIdx.x; c < Dv / 8; c += 256)
+        reinterpret_cast<uint4*>(vslot)[c] = reinterpret_cast<const uint4*>(vsrc)[c];
+    }
+  }
+  const int nch = Dh / 8 / G;
+  const int gl = lane % G;
+  const uint16_t* qh = q + static_cast<int64_t>(b) * q_ld + h * Dh;
+  const int per_pass = 4 * kCpw;
+  const int npass = (ncand + per_pass - 1) / per_pass;
+  for (int p0 = 0; p0 < npass; p0 += PB) {
+    int cs[PB];
+    bool vis[PB];
+    const uint16_t* kr[PB];
+#pragma unroll
+    for (int ps = 0; ps < PB; ++ps) {
+      const int c = (p0 + ps) * per_pass + wave * kCpw + lane / G;
+      cs[ps] = c;
+      vis[ps] = c < ncand;
+      if (MODE == kBand) {
+        const int key = p - W + 1 + c;
+        vis[ps] = vis[ps] && key >= 0;
+        kr[ps] = key == p ? k_new + static_cast<int64_t>(b) * kv_ld + h * Dh
+                          : ring_k + (static_cast<int64_t>(b) * W + (key >= 0 ? key % W : 0)) *
+                                         Kw + h * Dh;
+      } else {
+        const int cc = c < ncand ? c : 0;
+        const int tag = mtag[static_cast<int64_t>(b) * C + cc];
+        vis[ps] = vis[ps] && tag >= 1 && tag <= p + 1;
+        kr[ps] = mk + (static_cast<int64_t>(b) * C + cc) * Kw + h * Dh;
+      }
+    }
+    float dot[PB];
+#pragma unroll
+    for (int ps = 0; ps < PB; ++ps) dot[ps] = 0.f;
+    for (int ch = 0; ch < nch; ++ch) {
+      const int e = 8 * (gl + G * ch);
+      uint4 kk[PB];
+#pragma unroll
+      for (int ps = 0; ps < PB; ++ps) kk[ps] = *reinterpret_cast<const uint4*>(kr[ps] + e);
+      float a[8];
+      unpack8(*reinterpret_cast<const uint4*>(qh + e), a);
+#pragma unroll
+      for (int ps = 0; ps < PB; ++ps) {
+        float bb[8];
+        unpack8(kk[ps], bb);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) dot[ps] = fmaf(a[i], bb[i], dot[ps]);
+      }
+    }
+#pragma unroll
+    for (int ps = 0; ps < PB; ++ps) {
+      float d = dot[ps];
+#pragma unroll
+      for (int o = G / 2; o >= 1; o >>= 1) d += __shfl_xor(d, o, kWave);
+      if (gl == 0 && cs[ps] < ncand) srow[cs[ps]] = vis[ps] ? d * scale_log2 : -INFINITY;
+    }
+  }
+  __syncthreads();
+  if (wave != 0) return;
+  const int64_t lb = static_cast<int64_t>(bh) * Kmax;
+  if (MODE == kMemTopK) topk_row(srow, ncand, top_k, lane, wl + lb, il + lb, sel_s, sel_i);
+  else dense_row(srow, ncand, 0, 0, ncand, lane, wl + lb);
+}
+
 // ---------------------------------------------------------------- apply
 // Workgroup = (256-channel block, block of QB consecutive queries of one row),
 // channel block fastest; query b*T + t sits at position qpos[b] (qpos NULL:
@@ -725,7 +826,9 @@ inline bool dh_decode_ok(int Dh) {
   return Dh == 32 || Dh == 64 || Dh == 128 || Dh == 256 || (Dh % 512 == 0 && Dh <= 4096);
 }
 
-// Decode: scores (into sc), then the lists, for one branch.
+// Decode: scores (into sc), then the lists, for one branch; rows of at most
+// kFusedMaxCand candidates over B * H >= 512 workgroups take the one-kernel
+// form (the same scores and lists).
 template <int MODE>
 int32_t decode_select(const uint16_t* q, int64_t q_ld, const uint16_t* k_new,
                       const uint16_t* v_new, int64_t kv_ld, uint16_t* ring_k, uint16_t* ring_v,
@@ -734,6 +837,22 @@ int32_t decode_select(const uint16_t* q, int64_t q_ld, const uint16_t* k_new,
                       float* sc, float* wl, int32_t* il, hipStream_t s) {
   const int ncand = MODE == kBand ? W : C;
   const int G = min(kWave, Dh / 8);
+  if (ncand <= kFusedMaxCand && static_cast<int64_t>(B) * H >= 512) {
+    // one workgroup per (row, head): scores in LDS, list formed in place
+#define LLMY_SCORE_LIST(GG)                                                                  \
+  hipLaunchKernelGGL((cmp_score_list_decode_kernel<MODE, GG>), dim3(B * H), dim3(256),         \
+                     static_cast<size_t>(ncand) * 4, s, q, q_ld, k_new, v_new, kv_ld, ring_k,  \
+                     ring_v, mk, mtag, pos, H, Dh, Dv, W, C, scale_log2, top_k, Kmax, wl, il)
+    switch (G) {
+      case 4: LLMY_SCORE_LIST(4); break;
+      case 8: LLMY_SCORE_LIST(8); break;
+      case 16: LLMY_SCORE_LIST(16); break;
+      case 32: LLMY_SCORE_LIST(32); break;
+      default: LLMY_SCORE_LIST(64); break;
+    }
+#undef LLMY_SCORE_LIST
+    return launch_status();
+  }
   const int chunk = 16 * (kWave / G);
   const dim3 grid(static_cast<unsigned>(B * H * ((ncand + chunk - 1) / chunk)));
 #define LLMY_SCORE(GG)                                                                      \

@@ -101,12 +101,15 @@ def test_memory_prefill(B, T, ratio, H, Dh, Dv, top_k):
     _close(out, _mem_ref(q, kv[:, :Kw], kv[:, Kw:], B, T, ratio, H, Dh, top_k))
 
 
+# B * H >= 512 (the last case) takes the one-kernel scores + list form
 @pytest.mark.parametrize("B,H,Dh,Dv,W", [(8, 16, 128, 1024, 128), (4, 1, 1024, 1024, 128),
-                                         (3, 2, 64, 128, 7)])
+                                         (3, 2, 64, 128, 7), (32, 16, 128, 256, 128)])
 def test_local_decode(B, H, Dh, Dv, W):
+    print(f"local decode B={B} H={H} Dh={Dh} Dv={Dv} W={W}", flush=True)
     g = torch.Generator().manual_seed(B * W + Dh)
     Kw = H * Dh
-    pos = torch.tensor([0, 3, W - 1, W, 5 * W + 2, 2 * W - 1, 17, 1000][:B], dtype=torch.int32)
+    pos = torch.tensor(([0, 3, W - 1, W, 5 * W + 2, 2 * W - 1, 17, 1000] * ((B + 7) // 8))[:B],
+                       dtype=torch.int32)
     ring_k, ring_v = _bf(B, W, Kw, gen=g), _bf(B, W, Dv, gen=g)
     q = _bf(B, Kw, gen=g)
     kvn = _bf(B, Kw + Dv, gen=g)
@@ -132,9 +135,13 @@ def test_local_decode(B, H, Dh, Dv, W):
     _close(out, ref)
 
 
+# B * H >= 512 (the last two cases) takes the one-kernel scores + list form
 @pytest.mark.parametrize("B,C,H,Dh,Dv,top_k", [(8, 256, 16, 128, 1024, 32), (4, 64, 1, 1024, 1024, 0),
-                                               (3, 40, 2, 64, 128, 5), (2, 300, 1, 512, 512, 8)])
+                                               (3, 40, 2, 64, 128, 5), (2, 300, 1, 512, 512, 8),
+                                               (32, 256, 16, 128, 256, 32),
+                                               (64, 100, 8, 64, 128, 0)])
 def test_memory_decode(B, C, H, Dh, Dv, top_k):
+    print(f"memory decode B={B} C={C} H={H} Dh={Dh} Dv={Dv} k={top_k}", flush=True)
     g = torch.Generator().manual_seed(C + H + top_k)
     Kw = H * Dh
     mk, mv = _bf(B, C, Kw, gen=g), _bf(B, C, Dv, gen=g)
