@@ -79,18 +79,45 @@ def fill_state(eng, gen):
     torch.cuda.synchronize()
 
 
+_SLEEP_MS_PER_MCYCLE = None
+
+
+def _sleep_rate():
+    """Milliseconds of ``torch.cuda._sleep(1_000_000)`` on this GPU (event-timed once)."""
+    global _SLEEP_MS_PER_MCYCLE
+    if _SLEEP_MS_PER_MCYCLE is None:
+        import torch
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda._sleep(100_000)
+        a.record()
+        torch.cuda._sleep(1_000_000)
+        b.record()
+        b.synchronize()
+        _SLEEP_MS_PER_MCYCLE = max(a.elapsed_time(b), 1e-3)
+    return _SLEEP_MS_PER_MCYCLE
+
+
 def event_time(launch, iters, warm=10):
     """Duration (us) of ``launch(i)`` on a stream of its own: each of ``iters``
     launches (after ``warm`` untimed ones) is bracketed by its own pair of HIP
-    events recorded on that stream.  Returns (mean, median) over the launches."""
+    events recorded on that stream.  A sleep kernel queued ahead of the timed
+    launches keeps the GPU busy while the host enqueues them (sized from the
+    host time of the warmup launches), so the launches run back to back and
+    each pair measures device time, not the Python wrapper's launch gaps.
+    Returns (mean, median) over the launches."""
     import torch
     stream = torch.cuda.Stream()
     torch.cuda.synchronize()
     with torch.cuda.stream(stream):
+        t0 = time.perf_counter()
         for i in range(warm):
             launch(i)
+        host_ms = (time.perf_counter() - t0) * 1e3 / max(warm, 1)
+        stream.synchronize()
         ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
               for _ in range(iters)]
+        sleep_ms = min(2.0 + 2.0 * host_ms * iters, 2000.0)
+        torch.cuda._sleep(int(sleep_ms / _sleep_rate() * 1e6))
         for i, (a, b) in enumerate(ev):
             a.record(stream)
             launch(warm + i)
