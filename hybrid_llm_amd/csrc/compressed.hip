@@ -391,7 +391,7 @@ __global__ __launch_bounds__(256) void cmp_score_decode_kernel(
     const int e = 8 * (gl + G * ch);
     uint4 kk[kPasses];
 #pragma unroll
-    for (int ps = 0; ps < kPasses; ++ps) kk[ps] = *reinterpret_cast<const uint4*>(kr[ps] + e);
+    for (int ps = 0; ps < kPasses; ++ps) kk[ps] = ld_stream(kr[ps] + e);
     float a[8];
     unpack8(*reinterpret_cast<const uint4*>(qh + e), a);
 #pragma unroll
@@ -505,7 +505,7 @@ __global__ __launch_bounds__(256) void cmp_score_list_decode_kernel(
       const int e = 8 * (gl + G * ch);
       uint4 kk[PB];
 #pragma unroll
-      for (int ps = 0; ps < PB; ++ps) kk[ps] = *reinterpret_cast<const uint4*>(kr[ps] + e);
+      for (int ps = 0; ps < PB; ++ps) kk[ps] = ld_stream(kr[ps] + e);
       float a[8];
       unpack8(*reinterpret_cast<const uint4*>(qh + e), a);
 #pragma unroll
@@ -551,6 +551,22 @@ constexpr int kApplyMaxH = 16;  // heads whose selections are read in one round 
 #endif
 // single queries: few workgroups per row, so more waves share a row's slots
 constexpr int kApplyDecodeWaves = LLMY_APPLY_DECODE_WAVES;
+
+// 8-byte load of a value row piece.  Single-query (decode) applies read each
+// row once per step, so their loads carry the non-temporal hint (with
+// LLMY_NT); multi-query blocks re-read rows across query blocks and keep the
+// plain load.
+template <bool kStream>
+__device__ __forceinline__ uint2 ld_row8(const uint16_t* p) {
+#if defined(LLMY_NT) && LLMY_NT
+  if constexpr (kStream) {
+    typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+    const u32x2 v = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(p));
+    return uint2{v.x, v.y};
+  }
+#endif
+  return *reinterpret_cast<const uint2*>(p);
+}
 
 template <int QB, int NW>
 __global__ __launch_bounds__(64 * NW) void cmp_apply_kernel(
@@ -680,16 +696,16 @@ __global__ __launch_bounds__(64 * NW) void cmp_apply_kernel(
 #pragma unroll
     for (int u = 0; u < RU; ++u) jj[u] = nz[i + NW * u];
 #pragma unroll
-    for (int u = 0; u < RU; ++u) rr[u] = *reinterpret_cast<const uint2*>(vb + row_of(jj[u]));
+    for (int u = 0; u < RU; ++u) rr[u] = ld_row8<QB == 1>(vb + row_of(jj[u]));
 #pragma unroll
     for (int u = 0; u < RU; ++u) add(jj[u], rr[u]);
   }
   for (; i + 3 * NW < n; i += 4 * NW) {
     const int j0 = nz[i], j1 = nz[i + NW], j2 = nz[i + 2 * NW], j3 = nz[i + 3 * NW];
-    const uint2 r0 = *reinterpret_cast<const uint2*>(vb + row_of(j0));
-    const uint2 r1 = *reinterpret_cast<const uint2*>(vb + row_of(j1));
-    const uint2 r2 = *reinterpret_cast<const uint2*>(vb + row_of(j2));
-    const uint2 r3 = *reinterpret_cast<const uint2*>(vb + row_of(j3));
+    const uint2 r0 = ld_row8<QB == 1>(vb + row_of(j0));
+    const uint2 r1 = ld_row8<QB == 1>(vb + row_of(j1));
+    const uint2 r2 = ld_row8<QB == 1>(vb + row_of(j2));
+    const uint2 r3 = ld_row8<QB == 1>(vb + row_of(j3));
     add(j0, r0);
     add(j1, r1);
     add(j2, r2);
@@ -697,7 +713,7 @@ __global__ __launch_bounds__(64 * NW) void cmp_apply_kernel(
   }
   for (; i < n; i += NW) {
     const int j = nz[i];
-    add(j, *reinterpret_cast<const uint2*>(vb + row_of(j)));
+    add(j, ld_row8<QB == 1>(vb + row_of(j)));
   }
   const float invH = 1.0f / static_cast<float>(H);
   const int c = db * 256 + threadIdx.x;
