@@ -87,6 +87,11 @@ _MHC = {"mhc_map_norm": "mhc.mapping_norm.weight", "mhc_theta": "mhc.theta.weigh
         "mhc_scale": "mhc.stream_scale", "mhc_ln_w": "mhc.stream_norm.weight",
         "mhc_ln_b": "mhc.stream_norm.bias"}
 _MHC_ALPHA = ("mhc.alpha_pre", "mhc.alpha_post", "mhc.alpha_residual")
+# the dense SwiGLU FFN of a stem / tail block (model/layers/dense_ffn.py:9-11;
+# llmy_cuda/src/model.cpp:81-87 reads these names)
+_DENSE = {"ffn_gate": "ffn.gate_proj.weight", "ffn_up": "ffn.up_proj.weight",
+          "ffn_down": "ffn.down_proj.weight"}
+_SIDE = {"S": "stem", "T": "tail"}
 
 
 def file_name(cfg: HybridConfig, key: str) -> str:
@@ -102,6 +107,17 @@ def file_name(cfg: HybridConfig, key: str) -> str:
         return "mhc_collapse.weight"
     layer, short = key.split(".", 1)
     l = int(layer[1:])
+    if layer[0] in _SIDE:
+        # stem.<i> / tail.<i> blocks (model.py:391-394,411-414): GDN mixer,
+        # norms, hyper-connection and dense FFN
+        p = f"{_SIDE[layer[0]]}.{l}."
+        if short in _DENSE:
+            return p + _DENSE[short]
+        if short in _MHC:
+            return p + _MHC[short]
+        if short in ("mix_norm", "ffn_norm"):
+            return p + _BLOCK[short]
+        return p + "mixer." + _GDN[short]
     p = f"recurrent_core.{l}."
     if short in _BLOCK:
         return p + _BLOCK[short]
@@ -119,7 +135,10 @@ def file_name(cfg: HybridConfig, key: str) -> str:
 def config_text(cfg: HybridConfig) -> str:
     keys = {
         "vocab_size": cfg.vocab, "d_model": cfg.d_model, "num_loops": cfg.num_loops,
-        "stem_blocks": 0, "tail_blocks": 0, "recurrent_blocks": cfg.n_layers,
+        "stem_blocks": cfg.stem_blocks, "tail_blocks": cfg.tail_blocks,
+        "dense_ffn.hidden": cfg.dense_hidden,
+        "physical_blocks": cfg.stem_blocks + cfg.n_layers + cfg.tail_blocks,
+        "recurrent_blocks": cfg.n_layers,
         "recurrent_layout": ",".join(cfg.layer_kinds), "mhc.enabled": int(cfg.mhc_streams > 1),
         "mhc.streams": cfg.mhc_streams, "mhc.sinkhorn_iterations": cfg.mhc_sinkhorn_iters,
         "attn.heads": cfg.attn_heads, "attn.head_dim": cfg.attn_head_dim,
@@ -146,8 +165,7 @@ def config_from_text(text: str) -> HybridConfig:
     kv = dict(line.split("=", 1) for line in text.splitlines() if "=" in line)
     # every core block carries a MoE: "gdn_moe" and "gdn" name the same block
     kinds = tuple(k[:-4] if k.endswith("_moe") else k for k in kv["recurrent_layout"].split(","))
-    if int(kv.get("stem_blocks", 0)) or int(kv.get("tail_blocks", 0)):
-        raise ValueError("stem/tail blocks are not part of this block stack")
+    _refuse_unsupported(kv, kinds)
     if kv.get("gdn.qk_heads") != kv.get("gdn.value_heads"):
         raise ValueError("GDN q/k and value head counts must match")
     return HybridConfig(
@@ -176,7 +194,39 @@ def config_from_text(text: str) -> HybridConfig:
         hca_dense=_parse_bool(kv.get("hca.dense_global_attention", "1")),
         hca_top_k=int(kv.get("hca.global_top_k", 32)),
         cmp_slots=int(kv.get("memory.decode_slots", 256)),
+        stem_blocks=int(kv.get("stem_blocks", 0)), tail_blocks=int(kv.get("tail_blocks", 0)),
+        dense_hidden=int(kv.get("dense_ffn.hidden", 3584)),
         **_mhc_from(kv))
+
+
+def _refuse_unsupported(kv: dict, kinds: tuple) -> None:
+    """Config keys that change the reference model's math in ways this block
+    stack does not run are refused with a message rather than ignored."""
+    def on(key, dflt):
+        return _parse_bool(kv.get(key, dflt))
+    if on("loop_attnres.enabled", "0"):
+        raise ValueError("loop_attnres.enabled: the loop-attention residual (model/loop_memory.py) "
+                         "is not part of this block stack")
+    if on("adaptive_loops.enabled", "0"):
+        raise ValueError("adaptive_loops.enabled: learned halting (model.py:521-538) is not part "
+                         "of this block stack; run a fixed loop count")
+    if not on("mhc.shared_across_loops", "1"):
+        raise ValueError("mhc.shared_across_loops = 0: per-loop block copies (model.py:397-408) "
+                         "are not part of this block stack")
+    if not on("mhc.preserve_streams_across_loop_boundary", "1"):
+        raise ValueError("mhc.preserve_streams_across_loop_boundary = 0: the per-loop stream reset "
+                         "(model.py:634-635) is not part of this block stack")
+    if ("hca" in kinds and on("router.context_aware", "1")
+            and not on("router.use_hca_global_latents", "1")):
+        # both reference implementations build the router without this key
+        # (model/model.py:112-117, llmy_cuda/src/config.cpp) and always attend
+        # to the HCA summaries, so a file that turns it off asks for math that
+        # neither reference runs
+        raise ValueError("router.use_hca_global_latents = 0 with HCA blocks: the reference "
+                         "models ignore this key and always use the HCA global branch")
+    if int(kv.get("physical_blocks", -1)) not in (-1, int(kv.get("stem_blocks", 0)) + len(kinds)
+                                                  + int(kv.get("tail_blocks", 0))):
+        raise ValueError("physical_blocks must equal stem + recurrent + tail blocks")
 
 
 def _mhc_from(kv: dict) -> dict:
@@ -202,9 +252,11 @@ def _parse_bool(s: str) -> bool:
     raise ValueError(f"expected bool, got: {s}")
 
 
-def save_llmy(path: str | Path, cfg: HybridConfig, weights: dict[str, torch.Tensor]) -> None:
-    """Write ``weights`` (keys of `config.weight_shapes`) as a `.llmy` v1 file.
-    The depthwise conv is stored as nn.Conv1d's [D, 1, K]."""
+def llmy_entries(cfg: HybridConfig, weights: dict[str, torch.Tensor]) -> list:
+    """(file name, tensor) of every weight in a `.llmy` file, sorted by name:
+    the reference's state-dict names and shapes with expert lists stacked
+    (the depthwise conv as nn.Conv1d's [D, 1, K], the mHC alphas and gating
+    logit as 0-d tensors)."""
     from .config import weight_shapes
     entries = []
     for key, shape, _ in weight_shapes(cfg):
@@ -221,6 +273,12 @@ def save_llmy(path: str | Path, cfg: HybridConfig, weights: dict[str, torch.Tens
             t = t.reshape(())
         entries.append((file_name(cfg, key), t))
     entries.sort(key=lambda e: e[0])
+    return entries
+
+
+def save_llmy(path: str | Path, cfg: HybridConfig, weights: dict[str, torch.Tensor]) -> None:
+    """Write ``weights`` (keys of `config.weight_shapes`) as a `.llmy` v1 file."""
+    entries = llmy_entries(cfg, weights)
     cfg_b = config_text(cfg).encode()
     head = MAGIC + struct.pack("<II", VERSION, len(cfg_b)) + cfg_b + struct.pack("<I", len(entries))
     index_end = len(head) + INDEX_ENTRY.size * len(entries)

@@ -78,6 +78,14 @@ class HybridConfig:
     hca_dense: bool = True
     hca_top_k: int = 32
     cmp_slots: int = 256
+    # stem and tail blocks (model/model.py:391-394,411-414): GDN mixers of the
+    # core's GDN shape, each followed by a dense SwiGLU FFN of width dense_hidden
+    # (model/layers/dense_ffn.py:7-15) instead of a MoE; the stem runs once
+    # before the looped core and the tail once after it, each block with its
+    # own GDN state (state keys stem.<i> / tail.<i>, model.py:600-606,689-695)
+    stem_blocks: int = 0
+    tail_blocks: int = 0
+    dense_hidden: int = 0
     eps: float = 1e-6
     init_std: float = 0.02
     decay_logit_init: float = 2.0  # model/layers/gated_deltanet.py:113
@@ -95,6 +103,16 @@ class HybridConfig:
 
     def gdn_layers(self) -> list[int]:
         return [i for i, k in enumerate(self.layer_kinds) if k == "gdn"]
+
+    def side_blocks(self, where: str) -> list[str]:
+        """Weight prefixes of the stem ("S<i>.") or tail ("T<i>.") blocks."""
+        n = self.stem_blocks if where == "stem" else self.tail_blocks
+        return [f"{where[0].upper()}{i}." for i in range(n)]
+
+    @property
+    def has_gdn(self) -> bool:
+        """Whether any block (core, stem or tail) runs a GDN mixer."""
+        return bool(self.gdn_layers()) or self.stem_blocks > 0 or self.tail_blocks > 0
 
     def cmp_shape(self, kind: str) -> dict:
         """Heads, head width, window, ratio and top-k (0 = dense) of a CSA / HCA
@@ -123,6 +141,30 @@ C5 = HybridConfig(d_model=1024, layer_kinds=alternating(12), attn_heads=16, attn
                   expert_hidden=2048, vocab=32000, num_loops=2)
 
 
+def _mhc_shapes(cfg: HybridConfig, p: str) -> list[tuple[str, tuple[int, ...], str]]:
+    """A block's hyper-connection parameters (model/layers/mhc.py:63-84)."""
+    Sm, D = cfg.mhc_streams, cfg.d_model
+    if Sm <= 1:
+        return []
+    return [(p + "mhc_map_norm", (Sm * D,), "ones"),
+            (p + "mhc_theta", (2 * Sm + Sm * Sm, Sm * D), "normal"),
+            (p + "mhc_pre_bias", (Sm,), "mhc_pre"), (p + "mhc_post_bias", (Sm,), "zeros"),
+            (p + "mhc_res_bias", (Sm, Sm), "eye4"), (p + "mhc_alpha", (3,), "alpha"),
+            (p + "mhc_gating", (1,), "mhc_gate"), (p + "mhc_scale", (Sm, D), "ones"),
+            (p + "mhc_ln_w", (D,), "ones"), (p + "mhc_ln_b", (D,), "zeros")]
+
+
+def _gdn_shapes(cfg: HybridConfig, p: str) -> list[tuple[str, tuple[int, ...], str]]:
+    """A GDN mixer's parameters (model/layers/gated_deltanet.py:104-113)."""
+    D, Hg, dk, dv = cfg.d_model, cfg.gdn_heads, cfg.gdn_dk, cfg.gdn_dv
+    return [(p + "wq", (Hg * dk, D), "normal"), (p + "wk", (Hg * dk, D), "normal"),
+            (p + "wv", (Hg * dv, D), "normal"), (p + "wg", (Hg * dv, D), "normal"),
+            (p + "wb", (Hg, D), "normal"), (p + "bb", (Hg,), "zeros"),
+            (p + "wout", (D, Hg * dv), "normal"),
+            (p + "conv", (D, cfg.conv_kernel), "normal"),
+            (p + "decay", (Hg,), "decay")]
+
+
 def weight_shapes(cfg: HybridConfig) -> list[tuple[str, tuple[int, ...], str]]:
     """(name, shape, kind) in generation order; kind in {normal, ones, zeros, decay, gate}."""
     D, E, Hf = cfg.d_model, cfg.n_experts, cfg.expert_hidden
@@ -132,13 +174,7 @@ def weight_shapes(cfg: HybridConfig) -> list[tuple[str, tuple[int, ...], str]]:
         out.append(("stream_seed", (Sm, D), "seed"))
     for l, kind in enumerate(cfg.layer_kinds):
         p = f"L{l}."
-        if Sm > 1:
-            out += [(p + "mhc_map_norm", (Sm * D,), "ones"),
-                    (p + "mhc_theta", (2 * Sm + Sm * Sm, Sm * D), "normal"),
-                    (p + "mhc_pre_bias", (Sm,), "mhc_pre"), (p + "mhc_post_bias", (Sm,), "zeros"),
-                    (p + "mhc_res_bias", (Sm, Sm), "eye4"), (p + "mhc_alpha", (3,), "alpha"),
-                    (p + "mhc_gating", (1,), "mhc_gate"), (p + "mhc_scale", (Sm, D), "ones"),
-                    (p + "mhc_ln_w", (D,), "ones"), (p + "mhc_ln_b", (D,), "zeros")]
+        out += _mhc_shapes(cfg, p)
         out.append((p + "mix_norm", (D,), "ones"))
         if kind == "attn":
             w = cfg.attn_heads * cfg.attn_head_dim
@@ -152,13 +188,7 @@ def weight_shapes(cfg: HybridConfig) -> list[tuple[str, tuple[int, ...], str]]:
                     (p + "cmp_wro", (D, D), "normal"), (p + "cmp_wout", (D, D), "normal"),
                     (p + "cmp_wck", (Kw, D), "normal"), (p + "cmp_wcv", (D, D), "normal")]
         else:
-            Hg, dk, dv = cfg.gdn_heads, cfg.gdn_dk, cfg.gdn_dv
-            out += [(p + "wq", (Hg * dk, D), "normal"), (p + "wk", (Hg * dk, D), "normal"),
-                    (p + "wv", (Hg * dv, D), "normal"), (p + "wg", (Hg * dv, D), "normal"),
-                    (p + "wb", (Hg, D), "normal"), (p + "bb", (Hg,), "zeros"),
-                    (p + "wout", (D, Hg * dv), "normal"),
-                    (p + "conv", (D, cfg.conv_kernel), "normal"),
-                    (p + "decay", (Hg,), "decay")]
+            out += _gdn_shapes(cfg, p)
         out += [(p + "ffn_norm", (D,), "ones"), (p + "router_norm", (D,), "ones"),
                 (p + "w_router", (E, D), "normal"),
                 (p + "w_gate", (E, Hf, D), "normal"), (p + "w_up", (E, Hf, D), "normal"),
@@ -187,6 +217,14 @@ def weight_shapes(cfg: HybridConfig) -> list[tuple[str, tuple[int, ...], str]]:
             if kind == "hca":
                 out += [(p + "hca_lat_down", (L, D), "normal"),
                         (p + "hca_lat_ln_w", (L,), "ones"), (p + "hca_lat_ln_b", (L,), "zeros")]
+    # stem then tail blocks, drawn last (so the core's weights do not depend on them)
+    Hd = cfg.dense_hidden
+    for p in cfg.side_blocks("stem") + cfg.side_blocks("tail"):
+        out += _mhc_shapes(cfg, p)
+        out.append((p + "mix_norm", (D,), "ones"))
+        out += _gdn_shapes(cfg, p)
+        out += [(p + "ffn_norm", (D,), "ones"), (p + "ffn_gate", (Hd, D), "normal"),
+                (p + "ffn_up", (Hd, D), "normal"), (p + "ffn_down", (D, Hd), "normal")]
     return out
 
 

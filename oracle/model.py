@@ -2,7 +2,9 @@
 
 Composes the pinned ops into the block of model/model.py:162-264, looping the
 core ``num_loops`` times with one state per (loop, layer) (model.py:618-687,
-:645), tied LM head (model.py:705).  With ``mhc_streams`` > 1 the residual is
+:645), tied LM head (model.py:705).  Stem and tail blocks (GDN mixer, then a
+dense SwiGLU FFN: model.py:89-93,391-394,411-414, dense_ffn.py:14-15) run once
+before and after the loops (model.py:600-606,689-695; decode :842-845,906-909).  With ``mhc_streams`` > 1 the residual is
 S streams read and written around each sublayer through the layer's
 hyper-connection maps (model.py:119-126,177-264), seeded from the embedding
 (:442-444) and collapsed before the final norm (:699-700); with 1 it is the
@@ -90,6 +92,13 @@ class HybridOracle:
                     }
                 # the router's latent history (context_router.py:108-121)
                 st[(loop, l)]["lat"] = torch.zeros(batch, 0, cfg.latent_dim)
+        # stem / tail blocks: one GDN state and conv history each, outside the
+        # loops' namespaces (model.py:181-184 with state keys stem.<i> / tail.<i>)
+        for where in ("stem", "tail"):
+            for i in range(len(cfg.side_blocks(where))):
+                st[(where, i)] = {
+                    "S": torch.zeros(batch, cfg.gdn_heads, cfg.gdn_dk, cfg.gdn_dv),
+                    "hist": torch.zeros(batch, cfg.conv_kernel - 1, cfg.d_model)}
         return st
 
     # ---- blocks ----------------------------------------------------------
@@ -105,11 +114,11 @@ class HybridOracle:
                                                       cfg.attn_scale)
         return rnd(o).reshape(B, H * hd) @ w[p + "wo"].t()
 
-    def _gdn(self, l: int, h: torch.Tensor, st: dict) -> torch.Tensor:
+    def _gdn(self, p: str, h: torch.Tensor, st: dict) -> torch.Tensor:
+        """The GDN mixer of the block with weight prefix p."""
         cfg, w, rnd = self.cfg, self.w, self.rnd
         B = h.shape[0]
         H, dk, dv = cfg.gdn_heads, cfg.gdn_dk, cfg.gdn_dv
-        p = f"L{l}."
         q = (h @ w[p + "wq"].t()).view(B, H, dk)
         k = (h @ w[p + "wk"].t()).view(B, H, dk)
         v = (h @ w[p + "wv"].t()).view(B, H, dv)
@@ -193,48 +202,59 @@ class HybridOracle:
             x = x[:, None, :] + self.w["stream_seed"][None]
         return x
 
-    def _mhc_read(self, l: int, X: torch.Tensor):
-        """The maps of layer l's hyper-connection and the read of the streams
-        (model.py:119-123; mhc.py:156-206); the theta projection's input is
-        rounded as the engine's bf16 GEMM operand."""
+    def _dense(self, p: str, h2: torch.Tensor) -> torch.Tensor:
+        """The dense SwiGLU FFN of a stem / tail block (dense_ffn.py:14-15):
+        down(silu(gate h) * up h), the activation rounded as the engine's bf16
+        operand."""
+        w = self.w
+        a = self.rnd(F.silu(h2 @ w[p + "ffn_gate"].t()) * (h2 @ w[p + "ffn_up"].t()))
+        return a @ w[p + "ffn_down"].t()
+
+    def _mhc_read(self, p: str, X: torch.Tensor):
+        """The maps of the hyper-connection of the block with weight prefix p
+        and the read of the streams (model.py:119-123; mhc.py:156-206); the
+        theta projection's input is rounded as the engine's bf16 GEMM operand."""
         cfg, w = self.cfg, self.w
-        p = f"L{l}."
         maps = mhc_maps(X, w[p + "mhc_theta"], w[p + "mhc_map_norm"], w[p + "mhc_pre_bias"],
                         w[p + "mhc_post_bias"], w[p + "mhc_res_bias"], w[p + "mhc_alpha"],
                         cfg.mhc_sinkhorn_iters, act_round=self.rnd)
         return mhc_read(X, maps[0], w[p + "mhc_ln_w"], w[p + "mhc_ln_b"]), maps
 
-    def _mhc_write(self, l: int, X, U, maps):
-        p = f"L{l}."
+    def _mhc_write(self, p: str, X, U, maps):
         return mhc_write(X, U, maps[1], maps[2], self.w[p + "mhc_scale"], self.w[p + "mhc_gating"])
 
-    def apply(self, l: int, x: torch.Tensor, s: dict, pos: torch.Tensor) -> torch.Tensor:
-        """One application of layer l (mixer block then MoE block, each a
-        pre-norm residual branch: model.py:119-126,162-264) to the residual x,
-        updating that (loop, layer)'s state s in place; returns the new x.
-        With mHC, x is the [B, S, D] streams, each branch reads them through
-        the layer's maps and writes its output back (model.py:177-264)."""
+    def _block(self, p: str, mixer, ffn, x: torch.Tensor) -> torch.Tensor:
+        """A block with weight prefix p (mixer branch then FFN branch, each a
+        pre-norm residual branch: model.py:119-126,162-264) applied to the
+        residual x; ``mixer`` / ``ffn`` map the normalised input to the branch
+        output.  With mHC, x is the [B, S, D] streams, each branch reads them
+        through the block's maps and writes its output back (model.py:177-264)."""
         cfg, w, rnd = self.cfg, self.w, self.rnd
         mhc = cfg.mhc_streams > 1
-        if mhc:
-            hidden, maps = self._mhc_read(l, x)
+        hidden, maps = self._mhc_read(p, x) if mhc else (x, None)
+        u = mixer(rnd(rmsnorm(hidden, w[p + "mix_norm"], cfg.eps)))
+        x = self._mhc_write(p, x, u, maps) if mhc else x + u
+        hidden, maps = self._mhc_read(p, x) if mhc else (x, None)
+        u = ffn(rnd(rmsnorm(hidden, w[p + "ffn_norm"], cfg.eps)))
+        return self._mhc_write(p, x, u, maps) if mhc else x + u
+
+    def apply(self, l: int, x: torch.Tensor, s: dict, pos: torch.Tensor) -> torch.Tensor:
+        """One application of core layer l (its mixer, then its MoE) to the
+        residual x, updating that (loop, layer)'s state s in place; returns the
+        new x."""
+        kind = self.cfg.layer_kinds[l]
+        if kind == "attn":
+            mixer = lambda h: self._attn(l, h, s, pos)  # noqa: E731
+        elif kind in ("csa", "hca"):
+            mixer = lambda h: self.cmp[l].step(h, s["cmp"], pos)  # noqa: E731
         else:
-            hidden = x
-        h = rnd(rmsnorm(hidden, w[f"L{l}.mix_norm"], cfg.eps))
-        if cfg.layer_kinds[l] == "attn":
-            u = self._attn(l, h, s, pos)
-        elif cfg.layer_kinds[l] in ("csa", "hca"):
-            u = self.cmp[l].step(h, s["cmp"], pos)
-        else:
-            u = self._gdn(l, h, s)
-        x = self._mhc_write(l, x, u, maps) if mhc else x + u
-        if mhc:
-            hidden, maps = self._mhc_read(l, x)
-        else:
-            hidden = x
-        h2 = rnd(rmsnorm(hidden, w[f"L{l}.ffn_norm"], cfg.eps))
-        u = self._moe(l, h2, s)
-        return self._mhc_write(l, x, u, maps) if mhc else x + u
+            mixer = lambda h: self._gdn(f"L{l}.", h, s)  # noqa: E731
+        return self._block(f"L{l}.", mixer, lambda h2: self._moe(l, h2, s), x)
+
+    def apply_side(self, p: str, x: torch.Tensor, s: dict) -> torch.Tensor:
+        """One stem / tail block (weight prefix p): its GDN mixer, then its
+        dense SwiGLU FFN (model.py:89-93,391-394,411-414)."""
+        return self._block(p, lambda h: self._gdn(p, h, s), lambda h2: self._dense(p, h2), x)
 
     def head(self, x: torch.Tensor) -> torch.Tensor:
         """Final RMSNorm and the tied LM head (model.py:705): fp32 logits.  With
@@ -262,7 +282,7 @@ class HybridOracle:
                     s[name][rows] = 0
             if "cmp" in s:
                 CompressedMixer.reset_rows(s["cmp"], rows)
-            if self.cfg.context_router:
+            if self.cfg.context_router and "lat" in s:
                 n = s.get("lat_n", torch.full((rows.numel(),), s["lat"].shape[1],
                                               dtype=torch.long))
                 s["lat_n"] = torch.where(rows, torch.zeros_like(n), n)
@@ -277,10 +297,14 @@ class HybridOracle:
             self.reset_rows(st, reset)
         pos = st["pos"].clone()
         x = self.embed(tokens)
+        for i, p in enumerate(cfg.side_blocks("stem")):
+            x = self.apply_side(p, x, st[("stem", i)])
         loops = cfg.num_loops if not num_loops else num_loops
         for loop in range(loops):
             for l in range(cfg.n_layers):
                 x = self.apply(l, x, st[(loop, l)], pos)
+        for i, p in enumerate(cfg.side_blocks("tail")):
+            x = self.apply_side(p, x, st[("tail", i)])
         st["pos"] = pos + 1
         return self.head(x)
 
