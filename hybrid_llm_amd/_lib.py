@@ -70,6 +70,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
                            _I, _I, _I, _P]),
     "llmy_mhc_write": (_I, [_P, _P, _I64, _P, _P, _P, _I, _I, _I, _P]),
     "llmy_f32_to_bf16": (_I, [_P, _P, _I64, _P]),
+    "llmy_pad_cols_bf16": (_I, [_P, _P, _I, _I, _I, _P]),
     "llmy_layernorm_f32_bf16": (_I, [_P, _P, _P, _P, _I, _I, _F, _P]),
     "llmy_latent_attn_bf16": (_I, [_P, _I64, _P, _P, _P, _P, _P, _I64, _I, _I, _I, _I, _I, _F,
                                    _P]),

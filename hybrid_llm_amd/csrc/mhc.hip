@@ -222,6 +222,21 @@ __global__ __launch_bounds__(256) void f32_to_bf16_kernel(const float* __restric
   }
 }
 
+// out[r, k] = k < K ? x[r * K + k] : 0 for k < Kp: a GEMM operand whose input
+// width is zero-padded to the kernels' multiple of 256, one 32-bit word
+// (two bf16) per thread (K, Kp even).
+__global__ __launch_bounds__(256) void pad_cols_kernel(const uint32_t* __restrict__ x,
+                                                       uint32_t* __restrict__ out, long long rows,
+                                                       int K2, int Kp2) {
+  const long long n = rows * Kp2;
+  for (long long i = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x; i < n;
+       i += static_cast<long long>(gridDim.x) * 256) {
+    const long long r = i / Kp2;
+    const int c = static_cast<int>(i - r * Kp2);
+    out[i] = c < K2 ? x[r * K2 + c] : 0u;
+  }
+}
+
 }  // namespace llmy
 
 using namespace llmy;
@@ -289,5 +304,18 @@ extern "C" int32_t llmy_f32_to_bf16(const float* x, llmy_bf16* out, int64_t n, v
   const unsigned blocks = static_cast<unsigned>(std::min<long long>((n4 + 255) / 256, 8192));
   hipLaunchKernelGGL(f32_to_bf16_kernel, dim3(blocks), dim3(256), 0, as_stream(stream), x, out,
                      n4);
+  return launch_status();
+}
+
+extern "C" int32_t llmy_pad_cols_bf16(const llmy_bf16* x, llmy_bf16* out, int32_t rows,
+                                      int32_t K, int32_t Kp, void* stream) {
+  LLMY_REQUIRE(rows >= 0 && K > 0 && K <= Kp && K % 2 == 0 && Kp % 2 == 0);
+  if (rows == 0) return 0;
+  LLMY_REQUIRE(x && out && aligned(x, 4) && aligned(out, 4));
+  const long long n = static_cast<long long>(rows) * (Kp / 2);
+  const unsigned blocks = static_cast<unsigned>(std::min<long long>((n + 255) / 256, 8192));
+  hipLaunchKernelGGL(pad_cols_kernel, dim3(blocks), dim3(256), 0, as_stream(stream),
+                     reinterpret_cast<const uint32_t*>(x), reinterpret_cast<uint32_t*>(out),
+                     static_cast<long long>(rows), K / 2, Kp / 2);
   return launch_status();
 }

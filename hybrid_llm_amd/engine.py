@@ -38,6 +38,36 @@ def _pad_rows(w: torch.Tensor, mult: int) -> torch.Tensor:
     return torch.cat([w, torch.zeros(pad, *w.shape[1:], dtype=w.dtype, device=w.device)], 0)
 
 
+def round256(n: int) -> int:
+    return (n + 255) // 256 * 256
+
+
+def pad_hidden(gate_up: torch.Tensor, down: torch.Tensor):
+    """Zero-pad the hidden width H of an expert stack (gate_up [E, 2H, D],
+    down [E, D, H]) to the GEMM kernels' multiple of 256: zero gate and up rows
+    give activations silu(0) * 0 = 0 and the zero down columns add nothing, so
+    the result is the unpadded one (expert_hidden 320 / 640 of the reference's
+    configs, model/config.py:33)."""
+    E, H2, D = gate_up.shape
+    H = H2 // 2
+    Hp = round256(H)
+    if Hp == H:
+        return gate_up, down
+    gu = gate_up.new_zeros(E, 2 * Hp, D)
+    gu[:, :H] = gate_up[:, :H]
+    gu[:, Hp:Hp + H] = gate_up[:, H:]
+    dn = down.new_zeros(E, D, Hp)
+    dn[:, :, :H] = down
+    return gu, dn
+
+
+def pad_cols(w: torch.Tensor) -> torch.Tensor:
+    """Zero-pad the input width K of a [N, K] weight to a multiple of 256; its
+    GEMM then reads an activation zero-padded the same way (``ops.pad_cols``)."""
+    K = w.shape[-1]
+    return w if K % 256 == 0 else torch.nn.functional.pad(w, (0, round256(K) - K))
+
+
 class HybridDecoder:
     def __init__(self, cfg: HybridConfig, weights: dict[str, torch.Tensor], batch: int,
                  device: str | torch.device = "cuda",
@@ -58,6 +88,24 @@ class HybridDecoder:
             return t.to(device=dev, dtype=dtype or t.dtype).contiguous()
 
         self.w: dict[str, torch.Tensor] = {"embed": up("embed"), "final_norm": up("final_norm")}
+
+        def up_gdn(p):
+            wproj = torch.cat([up(p + n) for n in ("wq", "wk", "wv", "wg", "wb")], 0)
+            self.w[p + "wproj"] = _pad_rows(wproj, 16).contiguous()
+            for n in ("wout", "bb", "conv", "decay"):
+                self.w[p + n] = up(p + n)
+
+        # stem / tail blocks: GDN mixer and the dense SwiGLU FFN as a one-expert
+        # stack (gate | up [1, 2Hd, D], down [1, D, Hd]) run by the MoE kernels
+        # with every token routed to it at gate 1
+        self.side = {where: cfg.side_blocks(where) for where in ("stem", "tail")}
+        for p in self.side["stem"] + self.side["tail"]:
+            self.w[p + "mix_norm"] = up(p + "mix_norm")
+            self.w[p + "ffn_norm"] = up(p + "ffn_norm")
+            up_gdn(p)
+            gu, dn = pad_hidden(torch.cat([up(p + "ffn_gate"), up(p + "ffn_up")], 0)[None],
+                                up(p + "ffn_down")[None])
+            self.w[p + "ffn_gate_up"], self.w[p + "ffn_down"] = gu.contiguous(), dn.contiguous()
         for l, kind in enumerate(cfg.layer_kinds):
             p = f"L{l}."
             self.w[p + "mix_norm"] = up(p + "mix_norm")
@@ -73,27 +121,26 @@ class HybridDecoder:
                 self.w[p + "cmp_wlr"] = torch.cat([up(p + "cmp_wlo"), up(p + "cmp_wro")], 1)
                 self.w[p + "cmp_wout"] = up(p + "cmp_wout")
             else:
-                wproj = torch.cat([up(p + n) for n in ("wq", "wk", "wv", "wg", "wb")], 0)
-                self.w[p + "wproj"] = _pad_rows(wproj, 16).contiguous()
-                self.w[p + "wout"] = up(p + "wout")
-                self.w[p + "bb"] = up(p + "bb")
-                self.w[p + "conv"] = up(p + "conv")
-                self.w[p + "decay"] = up(p + "decay")
+                up_gdn(p)
             self.w[p + "ffn_norm"] = up(p + "ffn_norm")
             self.w[p + "router_norm"] = up(p + "router_norm")
             self.w[p + "w_router"] = up(p + "w_router")
             if cfg.context_router:
                 # latent encoder and gate fp32; the two wide projections bf16,
                 # packed below like the other GEMM weights
-                for n in ("ctx_down", "ctx_ln_w", "ctx_ln_b", "ctx_gate", "ctx_local_out",
-                          "ctx_out"):
+                # (the GEMMs over a latent_dim or heads x head_dim input not a
+                # multiple of 256 read their input zero-padded: pad_cols)
+                for n in ("ctx_down", "ctx_ln_w", "ctx_ln_b", "ctx_gate", "ctx_out"):
                     self.w[p + n] = up(p + n)
+                self.w[p + "ctx_local_out"] = pad_cols(up(p + "ctx_local_out"))
                 if kind == "hca":
                     # the global branch: the block's summary latents (hca_latent)
                     # and the router's latent attention; k | v in one projection
-                    for n in ("hca_lat_down", "hca_lat_ln_w", "hca_lat_ln_b", "ctx_q", "ctx_o"):
+                    for n in ("hca_lat_down", "hca_lat_ln_w", "hca_lat_ln_b", "ctx_q"):
                         self.w[p + n] = up(p + n)
-                    self.w[p + "ctx_kv"] = torch.cat([up(p + "ctx_k"), up(p + "ctx_v")], 0)
+                    self.w[p + "ctx_o"] = pad_cols(up(p + "ctx_o"))
+                    self.w[p + "ctx_kv"] = pad_cols(torch.cat([up(p + "ctx_k"),
+                                                               up(p + "ctx_v")], 0))
             gate_up = torch.cat([up(p + "w_gate"), up(p + "w_up")], 1)
             down = up(p + "w_down")
             if cfg.shared_experts > 0:
@@ -102,6 +149,7 @@ class HybridDecoder:
                 gate_up = torch.cat(
                     [gate_up, torch.cat([up(p + "w_shared_gate"), up(p + "w_shared_up")], 1)], 0)
                 down = torch.cat([down, up(p + "w_shared_down")], 0)
+            gate_up, down = pad_hidden(gate_up, down)
             self.w[p + "w_gate_up"] = gate_up.contiguous()
             self.w[p + "w_down"] = down.contiguous()
 
@@ -110,12 +158,9 @@ class HybridDecoder:
         # collapse as packed bf16 GEMM weights
         self.mhc = cfg.mhc_streams > 1
         if self.mhc:
-            if cfg.context_router:
-                raise NotImplementedError("mHC with the context-aware router is not built")
             self.w["stream_seed"] = up("stream_seed")
             self.w["mhc_collapse"] = up("mhc_collapse")
-            for l in range(cfg.n_layers):
-                p = f"L{l}."
+            for p in self.prefixes():
                 for n in ("mhc_map_norm", "mhc_pre_bias", "mhc_post_bias", "mhc_res_bias",
                           "mhc_alpha", "mhc_gating", "mhc_scale", "mhc_ln_w", "mhc_ln_b"):
                     self.w[p + n] = up(p + n)
@@ -127,6 +172,7 @@ class HybridDecoder:
         # token lookup and a packed copy for the tied LM head.
         for name in list(self.w):
             if name.split(".")[-1] in ("wqkv", "wo", "wproj", "wout", "w_gate_up", "w_down",
+                                       "ffn_gate_up", "ffn_down",
                                        "ctx_local_out", "ctx_out", "mhc_theta",
                                        "mhc_collapse", "cmp_wqkv", "cmp_wc", "cmp_wlr",
                                        "cmp_wout", "hca_lat_down", "ctx_q", "ctx_kv", "ctx_o"):
@@ -178,6 +224,13 @@ class HybridDecoder:
                     # the router's last router_context latents per sequence (slot pos % W)
                     self.state[(loop, l)]["ctx_ring"] = torch.zeros(
                         B, cfg.router_context, cfg.latent_dim, dtype=torch.float32, device=dev)
+        for where, prefixes in self.side.items():
+            for i in range(len(prefixes)):
+                self.state[(where, i)] = {
+                    "S": torch.zeros(B, cfg.gdn_heads, cfg.gdn_dk, cfg.gdn_dv,
+                                     dtype=torch.float32, device=dev),
+                    "hist": torch.zeros(B, cfg.conv_kernel - 1, D, dtype=torch.bfloat16,
+                                        device=dev)}
 
         # ---- activations / scratch (allocated once)
         f32, bf = torch.float32, torch.bfloat16
@@ -186,7 +239,10 @@ class HybridDecoder:
         k, E, Hf = cfg.top_k, cfg.n_experts, cfg.expert_hidden
         S = cfg.shared_experts
         kx, Ex = k + S, E + S  # routes per token and experts, shared ones included
-        nproj = self.w[f"L{cfg.gdn_layers()[0]}.wproj"].shape[0] if cfg.gdn_layers() else 16
+        gdn_p = [p for p in self.prefixes() if p + "wproj" in self.w]
+        side_p = self.side["stem"] + self.side["tail"]
+        nproj = self.w[gdn_p[0] + "wproj"].shape[0] if gdn_p else 16
+        Hf = self.w["L0.w_down"].shape[2]  # the (padded) expert hidden width
         self.buf = {
             "tokens": torch.zeros(B, dtype=torch.int32, device=dev),
             "reset": torch.zeros(B, dtype=torch.int32, device=dev),
@@ -204,6 +260,12 @@ class HybridDecoder:
             "sorted_routes": torch.zeros(B * kx, dtype=torch.int32, device=dev),
             "route_pos": torch.zeros(B * kx, dtype=torch.int32, device=dev),
             "act": torch.zeros(B * kx, Hf, dtype=bf, device=dev),
+            # the dense FFN of stem / tail blocks: its activation, and the one
+            # route per token (expert 0, gate 1)
+            "dact": torch.zeros(B, self.w[side_p[0] + "ffn_down"].shape[2] if side_p else 256,
+                                dtype=bf, device=dev),
+            "dids": torch.zeros(B, 1, dtype=torch.int32, device=dev),
+            "dgates": torch.ones(B, 1, dtype=f32, device=dev),
             "y": torch.zeros(B * kx, D, dtype=f32, device=dev),
             "logits": torch.zeros(B, cfg.vocab, dtype=f32, device=dev),
             "next": torch.zeros(B, dtype=torch.int32, device=dev),
@@ -240,28 +302,32 @@ class HybridDecoder:
             self.buf["idx_all"] = torch.zeros(B, kx, dtype=torch.int32, device=dev)
             self.buf["gates_all"] = torch.zeros(B, kx, dtype=f32, device=dev)
         if cfg.context_router:
-            if cfg.latent_dim % 256 or cfg.latent_dim > 512 or D > 1024:
-                raise ValueError("the context router needs latent_dim in {256, 512}, d_model <= 1024")
+            if cfg.latent_dim % 64 or cfg.latent_dim > 512 or D > 1024:
+                raise ValueError("the context router needs latent_dim % 64 == 0, latent_dim <= 512, "
+                                 "d_model <= 1024")
             Lc = cfg.latent_dim
             self.ctx_buf = {"local": torch.zeros(B, D, dtype=f32, device=dev),
                             "lat": torch.zeros(B, Lc, dtype=f32, device=dev),
                             "ctx": torch.zeros(B, Lc, dtype=bf, device=dev),
+                            "ctx_p": torch.zeros(B, round256(Lc), dtype=bf, device=dev),
                             "ctx_d": torch.zeros(B, D, dtype=bf, device=dev),
                             "ctx_c": torch.zeros(B, D, dtype=f32, device=dev),
                             "logits": torch.zeros(B, E, dtype=f32, device=dev),
                             "idx": self.buf["idx"], "gates": self.buf["gates"]}
             if "hca" in cfg.layer_kinds:
                 HQ = cfg.router_heads * cfg.router_head_dim
-                if HQ % 256 or cfg.router_head_dim % 8:
-                    raise ValueError("the router's latent attention needs heads * head_dim % 256 "
+                if HQ % 16 or cfg.router_head_dim % 8:
+                    raise ValueError("the router's latent attention needs heads * head_dim % 16 "
                                      "== 0 and head_dim % 8 == 0")
                 self.ctx_buf.update({"ctx_t": torch.zeros(B, D, dtype=f32, device=dev),
                                      "lq": torch.zeros(B, D, dtype=bf, device=dev),
                                      "gq": torch.zeros(B, HQ, dtype=bf, device=dev),
-                                     "gattn": torch.zeros(B, HQ, dtype=bf, device=dev)})
+                                     "gattn": torch.zeros(B, HQ, dtype=bf, device=dev),
+                                     "gattn_p": torch.zeros(B, round256(HQ), dtype=bf, device=dev)})
                 self.buf.update({"cval": torch.zeros(B, 1, D, dtype=bf, device=dev),
                                  "clat_raw": torch.zeros(B, Lc, dtype=f32, device=dev),
                                  "clat": torch.zeros(B, Lc, dtype=bf, device=dev),
+                                 "clat_p": torch.zeros(B, round256(Lc), dtype=bf, device=dev),
                                  "ckvr": torch.zeros(B, 2 * HQ, dtype=bf, device=dev)})
         # Mixer output projections (attention o, GDN out) as per-K-block
         # partial products that the fused router folds into the residual: a
@@ -274,7 +340,7 @@ class HybridDecoder:
             self.buf["parts"] = torch.zeros(n_parts, B, D, dtype=f32, device=dev)
         # The GDN input projection the same way: its partials are summed by
         # the GDN step kernel as it reads the row.
-        self.proj_parts = B <= 64 and D % 256 == 0 and D // 256 <= 8 and bool(cfg.gdn_layers())
+        self.proj_parts = B <= 64 and D % 256 == 0 and D // 256 <= 8 and cfg.has_gdn
         if self.proj_parts:
             self.buf["proj_parts"] = torch.zeros(D // 256, B, nproj, dtype=f32, device=dev)
         self._pending: tuple | None = None
@@ -308,6 +374,26 @@ class HybridDecoder:
                                   device=self.dev) if residuals else None)
         self._app = 0
 
+    def prefixes(self) -> list[str]:
+        """Weight prefixes of every block: stem, core layers, tail."""
+        return (self.side["stem"] + [f"L{l}." for l in range(self.cfg.n_layers)]
+                + self.side["tail"])
+
+    def _apps(self) -> list[tuple]:
+        """The blocks one token passes in order, (weight prefix, kind, core
+        layer or None, state): the stem, the core num_loops times (one state per
+        (loop, layer)), the tail (model.py:842-909).  Stem / tail blocks have
+        kind "side" (GDN mixer, dense FFN)."""
+        cfg = self.cfg
+        apps = [(p, "side", None, self.state[("stem", i)])
+                for i, p in enumerate(self.side["stem"])]
+        for loop in range(cfg.num_loops):
+            for l in range(cfg.n_layers):
+                apps.append((f"L{l}.", cfg.layer_kinds[l], l, self.state[(loop, l)]))
+        apps += [(p, "side", None, self.state[("tail", i)])
+                 for i, p in enumerate(self.side["tail"])]
+        return apps
+
     # ------------------------------------------------------------------ blocks
     def _attn(self, l: int, st: dict, out=None, epilogue=None) -> None:
         cfg, w, b = self.cfg, self.w, self.buf
@@ -331,9 +417,12 @@ class HybridDecoder:
                        epilogue=ops.EPI_RESID_ADD if epilogue is None else epilogue,
                        layout=ops.LAYOUT_PACKED)
 
-    def _gdn(self, l: int, st: dict, out=None) -> None:
+    def _gdn(self, p: str, st: dict, out=None, defer: bool = True) -> None:
+        """The GDN mixer of the block with weight prefix p on h; its output is
+        added to x (gated by the conv), stored to ``out``, or with ``defer`` (and
+        the engine's deferred residual) left as per-K-block partial products
+        that the next MoE router folds in."""
         w, b = self.w, self.buf
-        p = f"L{l}."
         if self.proj_parts:
             proj = b["proj_parts"]
             ops.linear(b["h"], w[p + "wproj"], out=proj, epilogue=ops.EPI_PARTIAL_F32,
@@ -344,7 +433,7 @@ class HybridDecoder:
                        layout=ops.LAYOUT_PACKED)
         ops.gdn_step_fused(proj, w[p + "bb"], w[p + "decay"], st["S"], out=b["go"],
                            conv=(b["h"], st["hist"], w[p + "conv"], b["cg"]))
-        if self.defer_resid:
+        if self.defer_resid and defer:
             parts = b["parts"][:b["go"].shape[1] // 256]
             ops.linear(b["go"], w[p + "wout"], out=parts, epilogue=ops.EPI_PARTIAL_F32,
                        layout=ops.LAYOUT_PACKED)
@@ -380,7 +469,7 @@ class HybridDecoder:
             # with the same flags (the summary values copied to a dense operand)
             ops.cmp_ring_fill(ckv[:, Kw:], self.B, 1, b["cval"])
             self._router_summary_kv(p, b["cval"].view(self.B, D), b["clat_raw"], b["clat"],
-                                    b["ckvr"])
+                                    b["ckvr"], b["clat_p"])
             ops.cmp_commit(b["ckvr"], b["cemit"], self.pos, st["rk"], st["rv"], st["rtag"],
                            st["rcount"])
         ops.cmp_memory_decode(q, st["mk"], st["mv"], st["mtag"], self.pos, H, Dh, cs["top_k"],
@@ -390,13 +479,14 @@ class HybridDecoder:
                    epilogue=ops.EPI_RESID_ADD if epilogue is None else epilogue,
                    layout=ops.LAYOUT_PACKED)
 
-    def _router_summary_kv(self, p: str, vals, lat_raw=None, lat=None, out=None):
+    def _router_summary_kv(self, p: str, vals, lat_raw=None, lat=None, out=None, lat_p=None):
         """The router's [k | v] of summary values (model.py:318-334 with
         mla_memory.py:23-24): LayerNorm(down . value) (eps 1e-5), then k | v."""
         w = self.w
         lat_raw = ops.linear(vals, w[p + "hca_lat_down"], out=lat_raw, epilogue=ops.EPI_STORE_F32,
                              layout=ops.LAYOUT_PACKED)
         lat = ops.layernorm(lat_raw, w[p + "hca_lat_ln_w"], w[p + "hca_lat_ln_b"], 1e-5, out=lat)
+        lat = ops.pad_cols(lat, w[p + "ctx_kv"].shape[1], out=lat_p)
         return ops.linear(lat, w[p + "ctx_kv"], out=out, layout=ops.LAYOUT_PACKED)
 
     def _glob(self, l: int, st: dict) -> dict | None:
@@ -412,6 +502,34 @@ class HybridDecoder:
         w = self.w
         return {n: w[p + n] for n in ("router_norm", "ctx_down", "ctx_ln_w", "ctx_ln_b",
                                        "ctx_local_out", "ctx_out", "ctx_gate", "w_router")}
+
+    def _dense(self, p: str, next_norm=None, out=None) -> None:
+        """The dense SwiGLU FFN of a stem / tail block (dense_ffn.py:14-15) on h:
+        the MoE kernels over the one-expert stack with every token routed to it
+        at gate 1, then added to x with the next block's pre-norm into h, or
+        stored to ``out``."""
+        cfg, w, b, B = self.cfg, self.w, self.buf, self.B
+        y = b["y"][:B]
+        ops.moe_experts_routed(b["h"], b["dids"], b["dgates"], w[p + "ffn_gate_up"],
+                               w[p + "ffn_down"], act=b["dact"], y=y, layout=ops.LAYOUT_PACKED)
+        if out is None:
+            ops.moe_combine_norm(y, None, b["x"], b["h"], next_norm, 1, cfg.eps)
+        else:
+            ops.moe_combine(y, b["route_ident"][:B], B, 1, out=out, mode=ops.MOE_OUT_F32)
+
+    def _dense_seq(self, p: str, x, h, next_norm=None, out=None) -> None:
+        """``_dense`` over the B*T rows of a prefill (the grouped expert GEMMs
+        with one expert)."""
+        cfg, w = self.cfg, self.w
+        R = h.shape[0]
+        perm = ops.moe_permute(torch.zeros(R, dtype=torch.int32, device=self.dev), 1)
+        gates = torch.ones(R, 1, dtype=torch.float32, device=self.dev)
+        _, y = ops.moe_experts(h, perm, gates, w[p + "ffn_gate_up"], w[p + "ffn_down"],
+                               layout=ops.LAYOUT_PACKED)
+        if out is None:
+            ops.moe_combine_norm(y, perm["route_pos"], x, h, next_norm, 1, cfg.eps)
+        else:
+            ops.moe_combine(y, perm["route_pos"], R, 1, out=out, mode=ops.MOE_OUT_F32)
 
     def _moe(self, l: int, next_norm: torch.Tensor | None, st: dict) -> None:
         """Pre-MoE norm + router + permutation, experts, then the combine fused
@@ -471,44 +589,47 @@ class HybridDecoder:
             self._step_body_mhc()
             return
         cfg, w, b = self.cfg, self.w, self.buf
-        ops.embed_norm(b["tokens"], w["embed"], w["L0.mix_norm"], b["x"], b["h"], cfg.eps)
-        apps = [(loop, l) for loop in range(cfg.num_loops) for l in range(cfg.n_layers)]
-        for i, (loop, l) in enumerate(apps):
-            if cfg.layer_kinds[l] == "attn":
-                self._attn(l, self.state[(loop, l)])
-            elif cfg.layer_kinds[l] in ("csa", "hca"):
-                self._cmp(l, self.state[(loop, l)])
+        apps = self._apps()
+        ops.embed_norm(b["tokens"], w["embed"], w[apps[0][0] + "mix_norm"], b["x"], b["h"],
+                       cfg.eps)
+        for i, (p, kind, l, st) in enumerate(apps):
+            nxt = w[apps[i + 1][0] + "mix_norm"] if i + 1 < len(apps) else w["final_norm"]
+            if kind == "side":
+                self._gdn(p, st, defer=False)
+                ops.rmsnorm(b["x"], w[p + "ffn_norm"], cfg.eps, out=b["h"])
+                self._dense(p, nxt)
+                continue
+            if kind == "attn":
+                self._attn(l, st)
+            elif kind in ("csa", "hca"):
+                self._cmp(l, st)
             else:
-                self._gdn(l, self.state[(loop, l)])
-            nxt = w[f"L{apps[i + 1][1]}.mix_norm"] if i + 1 < len(apps) else w["final_norm"]
-            self._moe(l, nxt, self.state[(loop, l)])
+                self._gdn(p, st)
+            self._moe(l, nxt, st)
         ops.linear(b["h"], w["lm_head"], out=b["logits"], epilogue=ops.EPI_STORE_F32,
                    layout=ops.LAYOUT_PACKED)
         self._sample()
         self.pos.add_(1)
 
     # ------------------------------------------------------------------ mHC
-    def _mhc_params(self, l: int) -> dict:
-        p = f"L{l}."
+    def _mhc_params(self, p: str) -> dict:
         return {n: self.w[p + "mhc_" + n] for n in ("pre_bias", "post_bias", "res_bias", "alpha",
                                                      "ln_w", "ln_b")}
 
-    def _mhc_read(self, l: int, X, norm: str, raw, maps, h, xb) -> None:
-        """The maps of layer l's hyper-connection and the sublayer input h
+    def _mhc_read(self, p: str, X, norm: str, raw, maps, h, xb) -> None:
+        """The maps of block p's hyper-connection and the sublayer input h
         (model.py:119-123; mhc.py:156-206): RMSNorm of the flattened streams
         into bf16, the theta projection, then maps + read + LayerNorm + the
         sublayer's RMSNorm in one kernel."""
         cfg, w = self.cfg, self.w
-        p = f"L{l}."
         M = X.shape[0]
         ops.rmsnorm(X.view(M, -1), w[p + "mhc_map_norm"], ops.MHC_MAP_EPS, out=xb)
         ops.linear(xb, w[p + "mhc_theta"], out=raw, epilogue=ops.EPI_STORE_F32,
                    layout=ops.LAYOUT_PACKED)
-        ops.mhc_read(X, raw, self._mhc_params(l), w[p + norm], cfg.mhc_sinkhorn_iters,
+        ops.mhc_read(X, raw, self._mhc_params(p), w[p + norm], cfg.mhc_sinkhorn_iters,
                      maps=maps, h=h, norm_eps=cfg.eps)
 
-    def _mhc_write(self, l: int, X, U, maps) -> None:
-        p = f"L{l}."
+    def _mhc_write(self, p: str, X, U, maps) -> None:
         ops.mhc_write(X, U, maps, self.w[p + "mhc_scale"], self.w[p + "mhc_gating"])
 
     def _mhc_head(self, X, xb, U) -> None:
@@ -524,55 +645,62 @@ class HybridDecoder:
     def _step_body_mhc(self) -> None:
         """The decode step with multi-stream hyper-connections: each sublayer
         reads the streams through its maps and writes its output back
-        (model.py:177-264); mixer and MoE kernels as in the single-stream step,
-        their outputs stored to U instead of added to a residual."""
+        (model.py:177-264); mixer, MoE and dense FFN kernels as in the
+        single-stream step, their outputs stored to U instead of added to a
+        residual."""
         from . import _lib
         cfg, w, b = self.cfg, self.w, self.buf
         X, U = b["X"], b["U"]
         ops.mhc_embed(b["tokens"], w["embed"], w["stream_seed"], out=X)
         s = torch.cuda.current_stream().cuda_stream
         kx = cfg.top_k + cfg.shared_experts
-        for loop in range(cfg.num_loops):
-            for l in range(cfg.n_layers):
-                st = self.state[(loop, l)]
-                p = f"L{l}."
-                self._mhc_read(l, X, "mix_norm", b["raw"], b["maps"], b["h"], b["xb"])
-                if cfg.layer_kinds[l] == "attn":
-                    self._attn(l, st, out=U, epilogue=ops.EPI_STORE_F32)
-                elif cfg.layer_kinds[l] in ("csa", "hca"):
-                    self._cmp(l, st, out=U, epilogue=ops.EPI_STORE_F32)
-                else:
-                    U.zero_()
-                    self._gdn(l, st, out=U)
-                self._mhc_write(l, X, U, b["maps"])
-                self._mhc_read(l, X, "ffn_norm", b["raw"], b["maps"], b["h"], b["xb"])
+        for p, kind, l, st in self._apps():
+            self._mhc_read(p, X, "mix_norm", b["raw"], b["maps"], b["h"], b["xb"])
+            if kind == "attn":
+                self._attn(l, st, out=U, epilogue=ops.EPI_STORE_F32)
+            elif kind in ("csa", "hca"):
+                self._cmp(l, st, out=U, epilogue=ops.EPI_STORE_F32)
+            else:
+                U.zero_()
+                self._gdn(p, st, out=U)
+            self._mhc_write(p, X, U, b["maps"])
+            self._mhc_read(p, X, "ffn_norm", b["raw"], b["maps"], b["h"], b["xb"])
+            if kind == "side":
+                self._dense(p, out=U)
+                self._mhc_write(p, X, U, b["maps"])
+                continue
+            if cfg.context_router:
+                ops.router_context(b["h"], self._ctx_weights(p), st["ctx_ring"], cfg.top_k,
+                                   pos=self.pos, eps=cfg.eps, layout=ops.LAYOUT_PACKED,
+                                   bufs=self.ctx_buf, glob=self._glob(l, st))
+            else:
                 _lib.call("llmy_router_topk_bf16", b["h"].data_ptr(),
                           w[p + "router_norm"].data_ptr(), w[p + "w_router"].data_ptr(), None,
                           b["idx"].data_ptr(), b["gates"].data_ptr(), self.B, cfg.d_model,
                           cfg.n_experts, cfg.top_k, cfg.eps, s)
-                idx, gates = b["idx"], b["gates"]
-                if cfg.shared_experts > 0:
-                    idx, gates = ops.moe_append_shared(idx, gates, cfg.n_experts,
-                                                       cfg.shared_experts, idx_out=b["idx_all"],
-                                                       gates_out=b["gates_all"])
-                if self.route_log is not None:
-                    self.route_log[self._app].copy_(b["idx"])
-                    self._app = (self._app + 1) % self.route_log.shape[0]
-                if self.fused_route:
-                    ops.moe_experts_routed(b["h"], idx, gates, w[p + "w_gate_up"],
-                                           w[p + "w_down"], act=b["act"], y=b["y"],
-                                           layout=ops.LAYOUT_PACKED)
-                    route_pos = b["route_ident"]
-                else:
-                    _lib.call("llmy_moe_permute", idx.data_ptr(), self.B * kx,
-                              cfg.n_experts + cfg.shared_experts, b["counts"].data_ptr(),
-                              b["offsets"].data_ptr(), b["sorted_routes"].data_ptr(),
-                              b["route_pos"].data_ptr(), s)
-                    ops.moe_experts(b["h"], b, gates, w[p + "w_gate_up"], w[p + "w_down"],
-                                    act=b["act"], y=b["y"], layout=ops.LAYOUT_PACKED)
-                    route_pos = b["route_pos"]
-                ops.moe_combine(b["y"], route_pos, self.B, kx, out=U, mode=ops.MOE_OUT_F32)
-                self._mhc_write(l, X, U, b["maps"])
+            idx, gates = b["idx"], b["gates"]
+            if cfg.shared_experts > 0:
+                idx, gates = ops.moe_append_shared(idx, gates, cfg.n_experts,
+                                                   cfg.shared_experts, idx_out=b["idx_all"],
+                                                   gates_out=b["gates_all"])
+            if self.route_log is not None:
+                self.route_log[self._app].copy_(b["idx"])
+                self._app = (self._app + 1) % self.route_log.shape[0]
+            if self.fused_route:
+                ops.moe_experts_routed(b["h"], idx, gates, w[p + "w_gate_up"],
+                                       w[p + "w_down"], act=b["act"], y=b["y"],
+                                       layout=ops.LAYOUT_PACKED)
+                route_pos = b["route_ident"]
+            else:
+                _lib.call("llmy_moe_permute", idx.data_ptr(), self.B * kx,
+                          cfg.n_experts + cfg.shared_experts, b["counts"].data_ptr(),
+                          b["offsets"].data_ptr(), b["sorted_routes"].data_ptr(),
+                          b["route_pos"].data_ptr(), s)
+                ops.moe_experts(b["h"], b, gates, w[p + "w_gate_up"], w[p + "w_down"],
+                                act=b["act"], y=b["y"], layout=ops.LAYOUT_PACKED)
+                route_pos = b["route_pos"]
+            ops.moe_combine(b["y"], route_pos, self.B, kx, out=U, mode=ops.MOE_OUT_F32)
+            self._mhc_write(p, X, U, b["maps"])
         self._mhc_head(X, b["xb"], U)
         self._sample()
         self.pos.add_(1)
@@ -672,17 +800,22 @@ class HybridDecoder:
             return self._prefill_mhc(tokens, B, T)
         x = torch.empty(R, D, dtype=torch.float32, device=self.dev)
         h = torch.empty(R, D, dtype=torch.bfloat16, device=self.dev)
-        ops.embed_norm(tokens.contiguous().view(-1), w["embed"], w["L0.mix_norm"], x, h, cfg.eps)
-        apps = [(loop, l) for loop in range(cfg.num_loops) for l in range(cfg.n_layers)]
-        for i, (loop, l) in enumerate(apps):
-            st = self.state[(loop, l)]
-            if cfg.layer_kinds[l] == "attn":
+        apps = self._apps()
+        ops.embed_norm(tokens.contiguous().view(-1), w["embed"], w[apps[0][0] + "mix_norm"], x, h,
+                       cfg.eps)
+        for i, (p, kind, l, st) in enumerate(apps):
+            nxt = w[apps[i + 1][0] + "mix_norm"] if i + 1 < len(apps) else w["final_norm"]
+            if kind == "side":
+                self._gdn_seq(p, st, x, h, B, T)
+                ops.rmsnorm(x, w[p + "ffn_norm"], cfg.eps, out=h)
+                self._dense_seq(p, x, h, nxt)
+                continue
+            if kind == "attn":
                 self._attn_seq(l, st, x, h, B, T)
-            elif cfg.layer_kinds[l] in ("csa", "hca"):
+            elif kind in ("csa", "hca"):
                 self._cmp_seq(l, st, x, h, B, T)
             else:
-                self._gdn_seq(l, st, x, h, B, T)
-            nxt = w[f"L{apps[i + 1][1]}.mix_norm"] if i + 1 < len(apps) else w["final_norm"]
+                self._gdn_seq(p, st, x, h, B, T)
             self._moe_seq(l, x, h, nxt, st, B)
         b = self.buf
         b["h"].copy_(h.view(B, T, D)[:, -1])
@@ -707,36 +840,44 @@ class HybridDecoder:
         maps = torch.empty(R, Sm + Sm * Sm, dtype=torch.float32, device=dev)
         s = torch.cuda.current_stream().cuda_stream
         E, k = cfg.n_experts, cfg.top_k
-        for loop in range(cfg.num_loops):
-            for l in range(cfg.n_layers):
-                st = self.state[(loop, l)]
-                p = f"L{l}."
-                self._mhc_read(l, X, "mix_norm", raw, maps, h, xb)
-                if cfg.layer_kinds[l] == "attn":
-                    self._attn_seq(l, st, U, h, B, T, epilogue=ops.EPI_STORE_F32)
-                elif cfg.layer_kinds[l] in ("csa", "hca"):
-                    self._cmp_seq(l, st, U, h, B, T, epilogue=ops.EPI_STORE_F32)
-                else:
-                    U.zero_()
-                    self._gdn_seq(l, st, U, h, B, T)
-                self._mhc_write(l, X, U, maps)
-                self._mhc_read(l, X, "ffn_norm", raw, maps, h, xb)
-                idx = torch.empty(R, k, dtype=torch.int32, device=dev)
-                gates = torch.empty(R, k, dtype=torch.float32, device=dev)
+        for p, kind, l, st in self._apps():
+            self._mhc_read(p, X, "mix_norm", raw, maps, h, xb)
+            if kind == "attn":
+                self._attn_seq(l, st, U, h, B, T, epilogue=ops.EPI_STORE_F32)
+            elif kind in ("csa", "hca"):
+                self._cmp_seq(l, st, U, h, B, T, epilogue=ops.EPI_STORE_F32)
+            else:
+                U.zero_()
+                self._gdn_seq(p, st, U, h, B, T)
+            self._mhc_write(p, X, U, maps)
+            self._mhc_read(p, X, "ffn_norm", raw, maps, h, xb)
+            if kind == "side":
+                self._dense_seq(p, None, h, out=U)
+                self._mhc_write(p, X, U, maps)
+                continue
+            idx = torch.empty(R, k, dtype=torch.int32, device=dev)
+            gates = torch.empty(R, k, dtype=torch.float32, device=dev)
+            if cfg.context_router:
+                # rows are B sequences of T tokens from position 0 (fresh state)
+                idx, gates, _ = ops.router_context(h, self._ctx_weights(p), st["ctx_ring"], k,
+                                                   eps=cfg.eps, layout=ops.LAYOUT_PACKED,
+                                                   bufs={"idx": idx, "gates": gates},
+                                                   glob=self._glob(l, st))
+            else:
                 _lib.call("llmy_router_topk_bf16", h.data_ptr(), w[p + "router_norm"].data_ptr(),
                           w[p + "w_router"].data_ptr(), None, idx.data_ptr(), gates.data_ptr(),
                           R, D, E, k, cfg.eps, s)
-                if self.route_log_seq is not None:
-                    self.route_log_seq.append(idx.clone())
-                Ex, kx = E, k
-                if cfg.shared_experts > 0:
-                    idx, gates = ops.moe_append_shared(idx, gates, E, cfg.shared_experts)
-                    Ex, kx = E + cfg.shared_experts, k + cfg.shared_experts
-                perm = ops.moe_permute(idx.view(-1), Ex)
-                _, y = ops.moe_experts(h, perm, gates, w[p + "w_gate_up"], w[p + "w_down"],
-                                       layout=ops.LAYOUT_PACKED)
-                ops.moe_combine(y, perm["route_pos"], R, kx, out=U, mode=ops.MOE_OUT_F32)
-                self._mhc_write(l, X, U, maps)
+            if self.route_log_seq is not None:
+                self.route_log_seq.append(idx.clone())
+            Ex, kx = E, k
+            if cfg.shared_experts > 0:
+                idx, gates = ops.moe_append_shared(idx, gates, E, cfg.shared_experts)
+                Ex, kx = E + cfg.shared_experts, k + cfg.shared_experts
+            perm = ops.moe_permute(idx.view(-1), Ex)
+            _, y = ops.moe_experts(h, perm, gates, w[p + "w_gate_up"], w[p + "w_down"],
+                                   layout=ops.LAYOUT_PACKED)
+            ops.moe_combine(y, perm["route_pos"], R, kx, out=U, mode=ops.MOE_OUT_F32)
+            self._mhc_write(p, X, U, maps)
         b["X"].copy_(X.view(B, T, Sm, D)[:, -1])
         self._mhc_head(b["X"], b["xb"], b["U"])
         self._sample()
@@ -791,9 +932,10 @@ class HybridDecoder:
                    epilogue=ops.EPI_RESID_ADD if epilogue is None else epilogue,
                    layout=ops.LAYOUT_PACKED)
 
-    def _gdn_seq(self, l: int, st: dict, x, h, B: int, T: int) -> None:
+    def _gdn_seq(self, p: str, st: dict, x, h, B: int, T: int) -> None:
+        """The GDN mixer of block p over B fresh sequences of T tokens, added to
+        x (gated by the conv)."""
         cfg, w = self.cfg, self.w
-        p = f"L{l}."
         H, dk, dv = cfg.gdn_heads, cfg.gdn_dk, cfg.gdn_dv
         R, HV = B * T, H * dv
         proj = ops.linear(h, w[p + "wproj"], epilogue=ops.EPI_STORE_F32,

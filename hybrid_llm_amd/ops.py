@@ -545,6 +545,9 @@ def router_context(h, w: dict, ring, k: int, pos=None, eps: float = 1e-6,
     local, lat = router_context_latent(h, w["router_norm"], w["ctx_down"], w["ctx_ln_w"],
                                        w["ctx_ln_b"], eps, local=b.get("local"), lat=b.get("lat"))
     ctx = router_context_window(lat, ring, pos, ctx=b.get("ctx"))
+    # a latent width (or query width) below a multiple of 256 reaches its GEMM
+    # zero-padded to the padded weight's input width
+    ctx = pad_cols(ctx, w["ctx_local_out"].shape[1], out=b.get("ctx_p"))
     if glob is None:
         cl = linear(ctx, w["ctx_local_out"], out=b.get("ctx_d"), epilogue=EPI_STORE_BF16,
                     layout=layout)
@@ -555,6 +558,7 @@ def router_context(h, w: dict, ring, k: int, pos=None, eps: float = 1e-6,
         gq = linear(lq, glob["q"], out=b.get("gq"), layout=layout)
         ga = latent_attn(gq, glob["rk"], glob["rv"], glob["rtag"], glob["heads"],
                          glob["head_dim"], pos=pos, out=b.get("gattn"))
+        ga = pad_cols(ga, glob["o"].shape[1], out=b.get("gattn_p"))
         linear(ga, glob["o"], out=t, epilogue=EPI_RESID_ADD, layout=layout)
         cl = f32_to_bf16(t, out=b.get("ctx_d"))
     c = linear(cl, w["ctx_out"], out=b.get("ctx_c"), epilogue=EPI_STORE_F32, layout=layout)
@@ -638,6 +642,20 @@ def mhc_write(X, U, maps, scale, gating_logit) -> None:
     _check(U, torch.float32, "U")
     _lib.call("llmy_mhc_write", _ptr(X), _ptr(U), U.stride(0), _ptr(maps), _ptr(scale),
               _ptr(gating_logit), M, S, D, _stream())
+
+
+def pad_cols(x, Kp: int, out=None) -> torch.Tensor:
+    """x [rows, K] bf16 -> [rows, Kp] with zero columns K .. Kp-1 (x itself when
+    K == Kp): the input of a GEMM whose weight was zero-padded to Kp inputs."""
+    rows, K = x.shape
+    if K == Kp:
+        return x
+    _check(x, torch.bfloat16, "x")
+    if out is None:
+        out = torch.empty(rows, Kp, dtype=torch.bfloat16, device=x.device)
+    _check(out, torch.bfloat16, "out", (rows, Kp))
+    _lib.call("llmy_pad_cols_bf16", _ptr(x), _ptr(out), rows, K, Kp, _stream())
+    return out
 
 
 def f32_to_bf16(x, out=None) -> torch.Tensor:

@@ -356,6 +356,13 @@ int32_t llmy_mhc_write(float* streams, const float* update, int64_t update_ld,
                        int32_t M, int32_t S, int32_t D, void* stream);
 /* out[i] = bf16(x[i]), n % 4 == 0 (the collapse GEMM's operand, model.py:699). */
 int32_t llmy_f32_to_bf16(const float* x, llmy_bf16* out, int64_t n, void* stream);
+/* out [rows, Kp] = x [rows, K] with columns K .. Kp-1 zero (K <= Kp, both
+ * even): the input of a GEMM whose weight was zero-padded from K inputs to
+ * the kernels' multiple of 256 (the reference's mla.latent_dim 128 and
+ * router query heads 4 x 32, runpod/config_a5000_moe24.yaml:47,50-51; the
+ * reference's own GEMMs take any width, llmy_cuda/src/model.cpp:1497-1515). */
+int32_t llmy_pad_cols_bf16(const llmy_bf16* x, llmy_bf16* out, int32_t rows, int32_t K,
+                           int32_t Kp, void* stream);
 
 /* --- Compressed-memory mixers, CSA and HCA (model/layers/csa.py:16-259,
  * hca.py:15-193, compressed_attention.py:82-211; the reference's native twins

@@ -71,8 +71,8 @@ def test_block_parity(kind):
             eng._attn(0, eng.state[(0, 0)])
             _fold_pending(eng)
         else:
-            ref = x + ora._gdn(1, h, st[(0, 1)])
-            eng._gdn(1, eng.state[(0, 1)])
+            ref = x + ora._gdn("L1.", h, st[(0, 1)])
+            eng._gdn("L1.", eng.state[(0, 1)])
             _fold_pending(eng)
             assert rel_l2(eng.state[(0, 1)]["S"], st[(0, 1)]["S"]) < 1e-4
             assert torch.equal(eng.state[(0, 1)]["hist"].float().cpu(), st[(0, 1)]["hist"])
