@@ -202,7 +202,17 @@ struct Config {
   int hca_window = 128, hca_ratio = 32, hca_top_k = 32;
   bool hca_dense = true;
   int cmp_slots = 256;
+  // stem / tail blocks (GDN + dense SwiGLU FFN of width dense_hidden,
+  // model/model.py:391-394,411-414): stem_blocks, tail_blocks, dense_ffn.hidden
+  int stem = 0, tail = 0, dense_hidden = 0;
   float eps = 1e-6f;
+  // widths as the GEMM kernels take them: zero-padded to a multiple of 256
+  static int pad256(int n) { return (n + 255) / 256 * 256; }
+  int hidden_p() const { return pad256(hidden); }
+  int dense_p() const { return pad256(dense_hidden); }
+  int latent_p() const { return pad256(latent); }
+  int hq_p() const { return pad256(hq()); }
+  bool has_gdn() const { return has(kGdn) || stem > 0 || tail > 0; }
   CmpShape cmp(int kind) const {
     CmpShape c;
     if (kind == kCsa) {
@@ -249,8 +259,23 @@ Config config_from(const std::string& text) {
   c.vocab = cfg_int(kv, "vocab_size", 0, true);
   c.d_model = cfg_int(kv, "d_model", 0, true);
   c.num_loops = cfg_int(kv, "num_loops", 1, true);
-  if (cfg_int(kv, "stem_blocks", 0, false) || cfg_int(kv, "tail_blocks", 0, false))
-    throw std::runtime_error("stem/tail blocks are not part of this engine");
+  c.stem = cfg_int(kv, "stem_blocks", 0, false);
+  c.tail = cfg_int(kv, "tail_blocks", 0, false);
+  c.dense_hidden = cfg_int(kv, "dense_ffn.hidden", 3584, false);
+  // keys that change the reference model's math in ways this engine does not
+  // run are refused rather than ignored
+  if (cfg_bool(kv, "loop_attnres.enabled", false))
+    throw std::runtime_error("loop_attnres.enabled: the loop-attention residual "
+                             "(model/loop_memory.py) is not part of this engine");
+  if (cfg_bool(kv, "adaptive_loops.enabled", false))
+    throw std::runtime_error("adaptive_loops.enabled: learned halting is not part of this "
+                             "engine; run a fixed loop count");
+  if (!cfg_bool(kv, "mhc.shared_across_loops", true))
+    throw std::runtime_error("mhc.shared_across_loops = 0: per-loop block copies "
+                             "(model.py:397-408) are not part of this engine");
+  if (!cfg_bool(kv, "mhc.preserve_streams_across_loop_boundary", true))
+    throw std::runtime_error("mhc.preserve_streams_across_loop_boundary = 0: the per-loop "
+                             "stream reset (model.py:634-635) is not part of this engine");
   // mHC keys with the reference's defaults (llmy_cuda/include/config.h:27-29)
   if (cfg_bool(kv, "mhc.enabled", true)) {
     c.mhc = cfg_int(kv, "mhc.streams", 4, false);
@@ -279,7 +304,10 @@ Config config_from(const std::string& text) {
     p = e + 1;
   }
   const bool any_attn = std::count(c.kinds.begin(), c.kinds.end(), kAttn) > 0;
-  const bool any_gdn = std::count(c.kinds.begin(), c.kinds.end(), kGdn) > 0;
+  const bool any_gdn = c.has_gdn();
+  if (cfg_int(kv, "physical_blocks", c.stem + static_cast<int>(c.kinds.size()) + c.tail, false) !=
+      c.stem + static_cast<int>(c.kinds.size()) + c.tail)
+    throw std::runtime_error("physical_blocks must equal stem + recurrent + tail blocks");
   c.attn_heads = cfg_int(kv, "attn.heads", 0, any_attn);
   c.attn_head_dim = cfg_int(kv, "attn.head_dim", 0, any_attn);
   c.window = cfg_int(kv, "attn.window", 0, any_attn);
@@ -311,18 +339,27 @@ Config config_from(const std::string& text) {
   auto eps = kv.find("rms_norm_eps");
   if (eps != kv.end()) c.eps = std::stof(eps->second);
   if (c.kinds.empty() || c.num_loops < 1 || c.vocab < 1 || c.d_model % 256 != 0 ||
-      c.hidden % 256 != 0 || c.top_k < 1 || c.top_k > c.experts || c.conv_kernel != 4 ||
-      c.shared < 0 || c.shared > 64)
+      c.hidden < 2 || c.hidden % 2 != 0 || c.top_k < 1 || c.top_k > c.experts ||
+      c.conv_kernel != 4 || c.shared < 0 || c.shared > 64 || c.stem < 0 || c.tail < 0 ||
+      ((c.stem > 0 || c.tail > 0) && (c.dense_hidden < 2 || c.dense_hidden % 2 != 0)))
     throw std::runtime_error("unsupported model shape");
-  if (c.ctx && (c.latent % 256 != 0 || c.latent > 512 || c.d_model > 1024 || c.ctx_window < 1))
-    throw std::runtime_error("context-aware router needs mla.latent_dim in {256, 512}, "
+  if (c.ctx && (c.latent % 64 != 0 || c.latent > 512 || c.d_model > 1024 || c.ctx_window < 1))
+    throw std::runtime_error("context-aware router needs mla.latent_dim % 64 == 0 and <= 512, "
                              "d_model <= 1024, router.local_context >= 1");
-  if (c.ctx && std::count(c.kinds.begin(), c.kinds.end(), kHca) > 0 &&
-      (c.router_heads < 1 || c.router_head_dim % 8 != 0 || c.hq() % 256 != 0))
-    throw std::runtime_error("the router's latent attention needs router.query_heads * "
-                             "router.query_head_dim % 256 == 0 and head_dim % 8 == 0");
-  if (c.mhc > 1 && (c.ctx || c.d_model > 4096 || c.mhc_iters < 0))
-    throw std::runtime_error("mHC needs d_model <= 4096 and the plain router");
+  if (c.ctx && std::count(c.kinds.begin(), c.kinds.end(), kHca) > 0) {
+    if (c.router_heads < 1 || c.router_head_dim % 8 != 0 || c.hq() % 16 != 0)
+      throw std::runtime_error("the router's latent attention needs router.query_heads * "
+                               "router.query_head_dim % 16 == 0 and head_dim % 8 == 0");
+    // both reference implementations build the router without this key
+    // (model/model.py:112-117; llmy_cuda/src/config.cpp) and always attend to
+    // the HCA summaries, so a file that turns it off asks for math neither runs
+    if (!cfg_bool(kv, "router.use_hca_global_latents", true))
+      throw std::runtime_error("router.use_hca_global_latents = 0 with HCA blocks: the "
+                               "reference models ignore this key and always use the HCA "
+                               "global branch");
+  }
+  if (c.mhc > 1 && (c.d_model > 4096 || c.mhc_iters < 0))
+    throw std::runtime_error("mHC needs d_model <= 4096");
   // compressed-memory mixers: head widths the decode scoring splits over
   // lanes (16..256 or a multiple of 512), top-k <= 64, memory and window
   // within the kernels' LDS lists
@@ -424,6 +461,11 @@ struct Layer {
   // o [D, HQ] (packed)
   uint16_t *hca_lat_down = nullptr, *ctx_q = nullptr, *ctx_kv = nullptr, *ctx_o = nullptr;
   float *hca_lat_ln_w = nullptr, *hca_lat_ln_b = nullptr;
+  // stem / tail blocks: the dense SwiGLU FFN as a one-expert stack (packed
+  // gate | up [1, 2 Hd, D], down [1, D, Hd]) that the MoE kernels run with every
+  // token routed to it at gate 1
+  bool side = false;
+  uint16_t *ffn_gate_up = nullptr, *ffn_down = nullptr;
 };
 
 struct Model {
@@ -434,7 +476,8 @@ struct Model {
   float* final_norm = nullptr;
   float* stream_seed = nullptr;     // mHC: [S, D]
   uint16_t* mhc_collapse = nullptr; // mHC: packed [D, S D]
-  std::vector<Layer> layers;
+  std::vector<Layer> layers;        // the recurrent core
+  std::vector<Layer> stem, tail;    // GDN + dense FFN blocks before / after the loops
   std::vector<void*> allocs;
 
   ~Model() {
@@ -476,6 +519,35 @@ std::vector<uint16_t> concat_rows(std::initializer_list<std::vector<uint16_t>> p
   return out;
 }
 
+// [N, K] -> [N, Kp] with zero columns K .. Kp-1: the weight of a GEMM whose
+// input width is zero-padded to the kernels' multiple of 256 (its input goes
+// through llmy_pad_cols_bf16).
+std::vector<uint16_t> pad_cols(const std::vector<uint16_t>& w, int N, int K, int Kp) {
+  if (K == Kp) return w;
+  std::vector<uint16_t> out(static_cast<size_t>(N) * Kp, 0);
+  for (int n = 0; n < N; ++n)
+    std::memcpy(out.data() + static_cast<size_t>(n) * Kp, w.data() + static_cast<size_t>(n) * K,
+                static_cast<size_t>(K) * 2);
+  return out;
+}
+
+// Expert stacks with their hidden width H zero-padded to Hp: gate | up
+// [EX, 2 Hp, D] (gate rows, zeros, up rows, zeros) and down [EX, D, Hp].
+// Padded gate / up rows give activations silu(0) * 0 = 0 and padded down
+// columns add nothing, so the result is the unpadded one.
+void pad_hidden(std::vector<uint16_t>& gu, std::vector<uint16_t>& dn, int EX, int H, int Hp,
+                int D) {
+  if (H == Hp) return;
+  std::vector<uint16_t> g2(static_cast<size_t>(EX) * 2 * Hp * D, 0);
+  const size_t blk = static_cast<size_t>(H) * D, blkp = static_cast<size_t>(Hp) * D;
+  for (int e = 0; e < EX; ++e) {
+    std::memcpy(g2.data() + 2 * e * blkp, gu.data() + 2 * e * blk, blk * 2);
+    std::memcpy(g2.data() + (2 * e + 1) * blkp, gu.data() + (2 * e + 1) * blk, blk * 2);
+  }
+  gu.swap(g2);
+  dn = pad_cols(dn, EX * D, H, Hp);
+}
+
 std::unique_ptr<Model> load_model(const char* path) {
   Checkpoint ck;
   parse_checkpoint(path, ck);
@@ -501,10 +573,12 @@ std::unique_ptr<Model> load_model(const char* path) {
     expect_shape(cl, {D, static_cast<int64_t>(SM) * D}, "mhc_collapse.weight");
     m->mhc_collapse = m->upload_packed(as_bf16(cl), 1, D, SM * D);
   }
-  for (size_t l = 0; l < c.kinds.size(); ++l) {
+  // One block under the name prefix p: a core block of `kind` (mixer + MoE), or
+  // a stem / tail block (side: GDN mixer + dense FFN).
+  auto load_block = [&](const std::string& p, int kind, bool side) {
     Layer L;
-    L.kind = c.kinds[l];
-    const std::string p = "recurrent_core." + std::to_string(l) + ".";
+    L.kind = kind;
+    L.side = side;
     auto vec_f32 = [&](const std::string& n, std::vector<int64_t> shape) {
       const auto& t = ck.get(p + n);
       expect_shape(t, shape, p + n);
@@ -540,9 +614,11 @@ std::unique_ptr<Model> load_model(const char* path) {
     }
     L.mix_norm = vec_f32("mixer_norm.weight", {D});
     L.ffn_norm = vec_f32("ffn_norm.weight", {D});
-    L.router_norm = vec_f32("moe.router.norm.weight", {D});
-    L.w_router = vec_f32("moe.router.logits.weight", {E, D});
-    if (c.ctx) {
+    if (!side) {
+      L.router_norm = vec_f32("moe.router.norm.weight", {D});
+      L.w_router = vec_f32("moe.router.logits.weight", {E, D});
+    }
+    if (c.ctx && !side) {
       const int Lc = c.latent;
       L.ctx_down = vec_f32("moe.router.latent_memory.down.weight", {Lc, D});
       L.ctx_ln_w = vec_f32("moe.router.latent_memory.norm.weight", {Lc});
@@ -551,8 +627,9 @@ std::unique_ptr<Model> load_model(const char* path) {
       if (!(gt.shape.empty() || gt.shape == std::vector<int64_t>{1}))
         throw std::runtime_error("unexpected shape for moe.router.route_gate");
       L.ctx_gate = m->upload(as_f32(gt));
-      L.ctx_local_out = m->upload_packed(mat_bf16("moe.router.local_context_out.weight", {D, Lc}),
-                                         1, D, Lc);
+      L.ctx_local_out = m->upload_packed(
+          pad_cols(mat_bf16("moe.router.local_context_out.weight", {D, Lc}), D, Lc, c.latent_p()),
+          1, D, c.latent_p());
       L.ctx_out = m->upload_packed(mat_bf16("moe.router.context_out.weight", {D, D}), 1, D, D);
       if (L.kind == kHca) {  // model.py:117, context_router.py:24 (model.cpp:98-104,234)
         const int HQ = c.hq();
@@ -562,11 +639,13 @@ std::unique_ptr<Model> load_model(const char* path) {
         L.ctx_q = m->upload_packed(mat_bf16("moe.router.latent_attention.q.weight", {HQ, D}), 1,
                                    HQ, D);
         L.ctx_kv = m->upload_packed(
-            concat_rows({mat_bf16("moe.router.latent_attention.k.weight", {HQ, Lc}),
-                         mat_bf16("moe.router.latent_attention.v.weight", {HQ, Lc})}, 0),
-            1, 2 * HQ, Lc);
-        L.ctx_o = m->upload_packed(mat_bf16("moe.router.latent_attention.o.weight", {D, HQ}), 1,
-                                   D, HQ);
+            pad_cols(concat_rows({mat_bf16("moe.router.latent_attention.k.weight", {HQ, Lc}),
+                                  mat_bf16("moe.router.latent_attention.v.weight", {HQ, Lc})}, 0),
+                     2 * HQ, Lc, c.latent_p()),
+            1, 2 * HQ, c.latent_p());
+        L.ctx_o = m->upload_packed(
+            pad_cols(mat_bf16("moe.router.latent_attention.o.weight", {D, HQ}), D, HQ, c.hq_p()),
+            1, D, c.hq_p());
       }
     }
     if (L.kind == kCsa || L.kind == kHca) {
@@ -620,6 +699,17 @@ std::unique_ptr<Model> load_model(const char* path) {
         throw std::runtime_error("unexpected conv shape");
       L.conv = m->upload(as_f32(cv));
     }
+    if (side) {
+      // the dense SwiGLU FFN (dense_ffn.py:9-11; names of llmy_cuda/src/model.cpp:81-87)
+      const int Hd = c.dense_hidden;
+      auto gu = concat_rows({mat_bf16("ffn.gate_proj.weight", {Hd, D}),
+                             mat_bf16("ffn.up_proj.weight", {Hd, D})}, 0);
+      auto dn = mat_bf16("ffn.down_proj.weight", {D, Hd});
+      pad_hidden(gu, dn, 1, Hd, c.dense_p(), D);
+      L.ffn_gate_up = m->upload_packed(gu, 1, 2 * c.dense_p(), D);
+      L.ffn_down = m->upload_packed(dn, 1, D, c.dense_p());
+      return L;
+    }
     // Routed experts, then the S shared experts (moe.shared.*, stacked
     // [S, H, D] / [S, D, H] by the converter) as experts E .. E+S-1.
     const int S = c.shared, EX = E + S;
@@ -641,10 +731,17 @@ std::unique_ptr<Model> load_model(const char* path) {
       std::memcpy(gu.data() + 2 * e * blk, ge, blk * 2);
       std::memcpy(gu.data() + (2 * e + 1) * blk, ue, blk * 2);
     }
-    L.w_gate_up = m->upload_packed(gu, EX, 2 * Hf, D);
-    L.w_down = m->upload_packed(dn, EX, D, Hf);
-    m->layers.push_back(L);
-  }
+    pad_hidden(gu, dn, EX, Hf, c.hidden_p(), D);
+    L.w_gate_up = m->upload_packed(gu, EX, 2 * c.hidden_p(), D);
+    L.w_down = m->upload_packed(dn, EX, D, c.hidden_p());
+    return L;
+  };
+  for (int i = 0; i < c.stem; ++i)
+    m->stem.push_back(load_block("stem." + std::to_string(i) + ".", kGdn, true));
+  for (size_t l = 0; l < c.kinds.size(); ++l)
+    m->layers.push_back(load_block("recurrent_core." + std::to_string(l) + ".", c.kinds[l], false));
+  for (int i = 0; i < c.tail; ++i)
+    m->tail.push_back(load_block("tail." + std::to_string(i) + ".", kGdn, true));
   return m;
 }
 
@@ -704,6 +801,14 @@ struct Buffers {  // activations for `rows` token rows
   // window means [rows, L] and local_context_out [rows, D] bf16
   float *c_local = nullptr, *c_lat = nullptr, *c_c = nullptr, *c_logits = nullptr;
   uint16_t *c_ctx = nullptr, *c_d = nullptr;
+  // zero-padded GEMM inputs (latent_dim / query width not a multiple of 256):
+  // window means [rows, Lp], summary latents [rows, Lp], latent attention [rows, HQp]
+  uint16_t *c_ctx_p = nullptr, *g_lat_p = nullptr, *g_att_p = nullptr;
+  // stem / tail dense FFN: activation [rows, Hdp], one route per row (expert 0,
+  // gate 1)
+  uint16_t* dact = nullptr;
+  int32_t* dids = nullptr;
+  float* dgates = nullptr;
   // the global branch (HCA): summary values [rows, D] / latents [rows, L] fp32 and
   // bf16 / router k | v [rows, 2 HQ]; local in bf16, q and attention [rows, HQ],
   // local_context_out + o in fp32 [rows, D]
@@ -736,6 +841,7 @@ struct State {
   std::map<int, hipGraphExec_t> graphs; // decode step per loop count, captured on first use
   std::vector<int32_t> hpos;            // host copy of pos
   std::vector<LayerState> layers;  // index loop * n_layers + layer
+  std::vector<LayerState> side;    // stem blocks, then tail blocks (GDN state each)
   DeviceArena arena;
   int32_t* pos = nullptr;    // [B] device: absolute position of the next token
   int32_t* reset_mask = nullptr;  // [B] device: rows of the last llmy_state_reset_rows
@@ -784,12 +890,15 @@ void alloc_buffers(const Config& c, int rows, int B, int T, Buffers& b) {
     b.c_c = b.arena.zeros<float>(static_cast<size_t>(rows) * D);
     b.c_logits = b.arena.zeros<float>(static_cast<size_t>(rows) * c.experts);
     b.c_ctx = b.arena.zeros<uint16_t>(static_cast<size_t>(rows) * c.latent);
+    b.c_ctx_p = b.arena.zeros<uint16_t>(static_cast<size_t>(rows) * c.latent_p());
     b.c_d = b.arena.zeros<uint16_t>(static_cast<size_t>(rows) * D);
     if (c.has(kHca)) {
       const size_t R = rows, HQ = c.hq(), Lc = c.latent;
       b.g_val = b.arena.zeros<uint16_t>(R * D);
       b.g_lat_raw = b.arena.zeros<float>(R * Lc);
       b.g_lat = b.arena.zeros<uint16_t>(R * Lc);
+      b.g_lat_p = b.arena.zeros<uint16_t>(R * c.latent_p());
+      b.g_att_p = b.arena.zeros<uint16_t>(R * c.hq_p());
       b.g_kvr = b.arena.zeros<uint16_t>(R * 2 * HQ);
       b.g_lq = b.arena.zeros<uint16_t>(R * D);
       b.g_q = b.arena.zeros<uint16_t>(R * HQ);
@@ -816,14 +925,21 @@ void alloc_buffers(const Config& c, int rows, int B, int T, Buffers& b) {
   b.offsets = b.arena.zeros<int32_t>(EX + 1);
   b.sorted = b.arena.zeros<int32_t>(static_cast<size_t>(rows) * kx);
   b.route_pos = b.arena.zeros<int32_t>(static_cast<size_t>(rows) * kx);
-  b.act = b.arena.zeros<uint16_t>(static_cast<size_t>(rows) * kx * c.hidden);
+  b.act = b.arena.zeros<uint16_t>(static_cast<size_t>(rows) * kx * c.hidden_p());
+  if (c.stem > 0 || c.tail > 0) {
+    b.dact = b.arena.zeros<uint16_t>(static_cast<size_t>(rows) * c.dense_p());
+    b.dids = b.arena.zeros<int32_t>(rows);
+    b.dgates = b.arena.zeros<float>(rows);
+    const std::vector<float> ones(rows, 1.0f);
+    check_hip(hipMemcpy(b.dgates, ones.data(), ones.size() * 4, hipMemcpyHostToDevice), "ones");
+  }
   b.y = b.arena.zeros<float>(static_cast<size_t>(rows) * kx * D);
   if (T == 1 && rows <= 64 && Hhd % 256 == 0 && HV % 256 == 0 &&
       std::max(Hhd, HV) / 256 <= 8) {
     b.max_parts = std::max(Hhd, HV) / 256;
     b.parts = b.arena.zeros<float>(static_cast<size_t>(b.max_parts) * rows * D);
   }
-  if (T == 1 && rows <= 64 && D % 256 == 0 && D / 256 <= 8 && c.gdn_heads > 0)
+  if (T == 1 && rows <= 64 && D % 256 == 0 && D / 256 <= 8 && c.has_gdn())
     b.proj_parts = b.arena.zeros<float>(static_cast<size_t>(D / 256) * rows * c.nproj16());
   if (c.has(kCsa) || c.has(kHca)) {
     int kw = 0, rmin = 1 << 30;
@@ -849,7 +965,7 @@ void alloc_buffers(const Config& c, int rows, int B, int T, Buffers& b) {
     b.cws_bytes = ws;
     b.cws = b.arena.zeros<unsigned char>(static_cast<size_t>(ws));
   }
-  if (T > 1 && c.gdn_heads > 0) {
+  if (T > 1 && c.has_gdn()) {
     b.ws_bytes = llmy_gdn_prefill_workspace_bytes(B, T, c.gdn_heads, c.dk, c.dv);
     if (b.ws_bytes < 0) throw std::runtime_error("GDN prefill workspace size");
     b.ws = b.arena.zeros<unsigned char>(static_cast<size_t>(b.ws_bytes));
@@ -908,6 +1024,15 @@ std::unique_ptr<State> new_state(Model* m, int B) {
       s->layers.push_back(L);
     }
   }
+  for (int i = 0; i < c.stem + c.tail; ++i) {  // stem / tail GDN states
+    LayerState L;
+    const size_t n = static_cast<size_t>(B) * c.gdn_heads * c.dk * c.dv;
+    L.S = s->arena.zeros<float>(n);
+    L.s_bytes = n * 4;
+    L.hist = s->arena.zeros<uint16_t>(static_cast<size_t>(B) * 3 * D);
+    L.hist_bytes = static_cast<size_t>(B) * 3 * D * 2;
+    s->side.push_back(L);
+  }
   check_hip(hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking), "hipStreamCreate");
   s->hpos.assign(B, 0);
   s->pos = s->arena.zeros<int32_t>(B);
@@ -919,7 +1044,11 @@ std::unique_ptr<State> new_state(Model* m, int B) {
 }
 
 void reset_state(State& s) {
-  for (auto& L : s.layers) {
+  std::vector<LayerState*> all;
+  for (auto& L : s.layers) all.push_back(&L);
+  for (auto& L : s.side) all.push_back(&L);
+  for (LayerState* Lp : all) {
+    LayerState& L = *Lp;
     if (L.k) {
       check_hip(hipMemsetAsync(L.k, 0, L.k_bytes, s.stream), "reset");
       check_hip(hipMemsetAsync(L.v, 0, L.k_bytes, s.stream), "reset");
@@ -948,7 +1077,11 @@ void reset_rows(State& s, const int32_t* mask) {
       check_call(llmy_zero_rows(p, static_cast<int64_t>(bytes / s.B), s.B, s.reset_mask, s.stream),
                  "llmy_zero_rows");
   };
-  for (auto& L : s.layers) {
+  std::vector<LayerState*> all;
+  for (auto& L : s.layers) all.push_back(&L);
+  for (auto& L : s.side) all.push_back(&L);
+  for (LayerState* Lp : all) {
+    LayerState& L = *Lp;
     zero(L.k, L.k_bytes);
     zero(L.v, L.k_bytes);
     zero(L.S, L.s_bytes);
@@ -987,22 +1120,73 @@ bool router_fusable(const Config& c) {
 
 bool fused_route(const Config& c, int rows) { return router_fusable(c) && rows * c.routes() <= 2048; }
 
-// MoE of layer l over `rows` rows (x updated, h = next pre-norm of x).
+// The context-aware routing of b.h (llmy_router_context_*): the ids and gates
+// into b.idx / b.gates.  Rows are nseq sequences of rows / nseq tokens at
+// positions pos[b] + t (pos NULL: a prompt from 0); `ring` is the block's
+// latent window state.  On an HCA block with the router's summary memory
+// (ls->rk) the global branch's latent attention is added to
+// local_context_out(ctx).  GEMM inputs narrower than their padded weights go
+// through llmy_pad_cols_bf16.  The kernels and their order are the Python
+// engine's (ops.router_context).
+void context_route(const Model& m, const Layer& L, Buffers& b, int rows, float* ring,
+                   const int32_t* pos, int nseq, const LayerState* ls, hipStream_t st) {
+  const Config& c = m.cfg;
+  const int D = c.d_model, E = c.experts, k = c.top_k, Lc = c.latent, Lp = c.latent_p();
+  check_call(llmy_router_context_latent_f32(b.h, L.router_norm, L.ctx_down, L.ctx_ln_w,
+                                            L.ctx_ln_b, b.c_local, b.c_lat, rows, D, Lc, c.eps,
+                                            1e-5f, st),
+             "llmy_router_context_latent_f32");
+  check_call(llmy_router_context_window(b.c_lat, ring, pos, b.c_ctx, nseq, rows / nseq,
+                                        c.ctx_window, Lc, st),
+             "llmy_router_context_window");
+  const uint16_t* ctx = b.c_ctx;
+  if (Lp != Lc) {
+    check_call(llmy_pad_cols_bf16(b.c_ctx, b.c_ctx_p, rows, Lc, Lp, st), "llmy_pad_cols_bf16");
+    ctx = b.c_ctx_p;
+  }
+  if (ls && ls->rk) {
+    // the global branch: local_context_out(ctx) + o(latent attention of
+    // q(local) over the block's summaries), rounded once to bf16
+    const int HQ = c.hq(), HQp = c.hq_p();
+    linear(ctx, L.ctx_local_out, b.g_t, nullptr, rows, D, Lp, kStoreF32, st);
+    check_call(llmy_f32_to_bf16(b.c_local, b.g_lq, static_cast<int64_t>(rows) * D, st),
+               "llmy_f32_to_bf16");
+    linear(b.g_lq, L.ctx_q, b.g_q, nullptr, rows, HQ, D, kStoreBf16, st);
+    check_call(llmy_latent_attn_bf16(b.g_q, HQ, ls->rk, ls->rv, ls->rtag, pos, b.g_att, HQ, nseq,
+                                     rows / nseq, c.cmp_slots, c.router_heads, c.router_head_dim,
+                                     1.0f / std::sqrt(static_cast<float>(c.router_head_dim)), st),
+               "llmy_latent_attn_bf16");
+    const uint16_t* att = b.g_att;
+    if (HQp != HQ) {
+      check_call(llmy_pad_cols_bf16(b.g_att, b.g_att_p, rows, HQ, HQp, st), "llmy_pad_cols_bf16");
+      att = b.g_att_p;
+    }
+    linear(att, L.ctx_o, b.g_t, nullptr, rows, D, HQp, kResidAdd, st);
+    check_call(llmy_f32_to_bf16(b.g_t, b.c_d, static_cast<int64_t>(rows) * D, st),
+               "llmy_f32_to_bf16");
+  } else {
+    linear(ctx, L.ctx_local_out, b.c_d, nullptr, rows, D, Lp, kStoreBf16, st);
+  }
+  linear(b.c_d, L.ctx_out, b.c_c, nullptr, rows, D, D, kStoreF32, st);
+  check_call(llmy_router_context_logits_f32(b.c_local, b.c_c, L.ctx_gate, L.w_router, b.c_logits,
+                                            rows, D, E, st),
+             "llmy_router_context_logits_f32");
+  check_call(llmy_router_topk_logits_f32(b.c_logits, b.idx, b.gates, rows, E, k, st),
+             "llmy_router_topk_logits_f32");
+}
+
+// MoE of core block L over `rows` rows (x updated, h = next pre-norm of x).
 // Decode uses the fused router and route-indexed experts where the sizes
 // allow; a prefill always takes router -> permutation -> grouped experts.
 // `parts` (decode, fused router only): nparts partial products of the mixer's
 // output projection that the router folds into x first (times `gate` if set).
-//
-// With the context-aware router the ids and gates of b.idx / b.gates come from
-// the context path (llmy_router_context_*): rows are nseq sequences of
-// rows / nseq tokens at positions pos[b] + t (pos NULL: a prompt from 0), and
-// `ring` is the layer's latent window state.
+// With the context-aware router the ids and gates come from context_route.
 void moe_block(const Model& m, const Layer& L, Buffers& b, int rows, const float* next_norm,
                bool sequence, hipStream_t st, float* ring, const int32_t* pos, int nseq,
                const float* parts = nullptr, int nparts = 0, const float* gate = nullptr,
                const LayerState* ls = nullptr) {
   const Config& c = m.cfg;
-  const int D = c.d_model, E = c.experts, k = c.top_k, Hf = c.hidden;
+  const int D = c.d_model, E = c.experts, k = c.top_k, Hf = c.hidden_p();
   const int kx = c.routes(), EX = c.all_experts();
   const bool fused = !sequence && fused_route(c, rows);
   if (nparts > 0 && !fused) throw std::logic_error("partial products need the fused router");
@@ -1017,43 +1201,6 @@ void moe_block(const Model& m, const Layer& L, Buffers& b, int rows, const float
     ids = b.idx_all;
     gts = b.gates_all;
   };
-  auto context_route = [&] {
-    if (!c.ctx) return;
-    const int Lc = c.latent;
-    check_call(llmy_router_context_latent_f32(b.h, L.router_norm, L.ctx_down, L.ctx_ln_w,
-                                              L.ctx_ln_b, b.c_local, b.c_lat, rows, D, Lc, c.eps,
-                                              1e-5f, st),
-               "llmy_router_context_latent_f32");
-    check_call(llmy_router_context_window(b.c_lat, ring, pos, b.c_ctx, nseq, rows / nseq,
-                                          c.ctx_window, Lc, st),
-               "llmy_router_context_window");
-    if (ls && ls->rk) {
-      // the global branch: local_context_out(ctx) + o(latent attention of
-      // q(local) over the block's summaries), rounded once to bf16
-      const int HQ = c.hq();
-      linear(b.c_ctx, L.ctx_local_out, b.g_t, nullptr, rows, D, Lc, kStoreF32, st);
-      check_call(llmy_f32_to_bf16(b.c_local, b.g_lq, static_cast<int64_t>(rows) * D, st),
-                 "llmy_f32_to_bf16");
-      linear(b.g_lq, L.ctx_q, b.g_q, nullptr, rows, HQ, D, kStoreBf16, st);
-      check_call(llmy_latent_attn_bf16(b.g_q, HQ, ls->rk, ls->rv, ls->rtag, pos, b.g_att, HQ, nseq,
-                                       rows / nseq, c.cmp_slots, c.router_heads,
-                                       c.router_head_dim,
-                                       1.0f / std::sqrt(static_cast<float>(c.router_head_dim)),
-                                       st),
-                 "llmy_latent_attn_bf16");
-      linear(b.g_att, L.ctx_o, b.g_t, nullptr, rows, D, HQ, kResidAdd, st);
-      check_call(llmy_f32_to_bf16(b.g_t, b.c_d, static_cast<int64_t>(rows) * D, st),
-                 "llmy_f32_to_bf16");
-    } else {
-      linear(b.c_ctx, L.ctx_local_out, b.c_d, nullptr, rows, D, Lc, kStoreBf16, st);
-    }
-    linear(b.c_d, L.ctx_out, b.c_c, nullptr, rows, D, D, kStoreF32, st);
-    check_call(llmy_router_context_logits_f32(b.c_local, b.c_c, L.ctx_gate, L.w_router,
-                                              b.c_logits, rows, D, E, st),
-               "llmy_router_context_logits_f32");
-    check_call(llmy_router_topk_logits_f32(b.c_logits, b.idx, b.gates, rows, E, k, st),
-               "llmy_router_topk_logits_f32");
-  };
   const int32_t* ids = nullptr;
   const float* gts = nullptr;
   if (fused) {
@@ -1061,7 +1208,7 @@ void moe_block(const Model& m, const Layer& L, Buffers& b, int rows, const float
                                      L.w_router, b.h, b.idx, b.gates, nullptr, nullptr, nullptr,
                                      nullptr, rows, D, E, k, c.eps, st),
                "llmy_moe_route_decode");
-    context_route();
+    if (c.ctx) context_route(m, L, b, rows, ring, pos, nseq, ls, st);
     with_shared(ids, gts);
     check_call(llmy_moe_experts_routed_bf16(b.h, ids, gts, L.w_gate_up, L.w_down, b.act, b.y,
                                             rows, D, Hf, EX, kx, kPacked, st),
@@ -1081,7 +1228,7 @@ void moe_block(const Model& m, const Layer& L, Buffers& b, int rows, const float
                                      rows, D, E, k, c.eps, st),
                "llmy_router_topk_bf16");
   }
-  context_route();
+  if (c.ctx) context_route(m, L, b, rows, ring, pos, nseq, ls, st);
   with_shared(ids, gts);
   check_call(llmy_moe_permute(ids, rows * kx, EX, b.counts, b.offsets, b.sorted, b.route_pos,
                               st),
@@ -1094,10 +1241,55 @@ void moe_block(const Model& m, const Layer& L, Buffers& b, int rows, const float
              "llmy_moe_combine_norm");
 }
 
-const float* next_norm_of(const Model& m, int loop, int l, int loops) {
-  const int n = static_cast<int>(m.layers.size());
-  if (l + 1 < n) return m.layers[l + 1].mix_norm;
-  return loop + 1 < loops ? m.layers[0].mix_norm : m.final_norm;
+// The dense SwiGLU FFN of a stem / tail block (dense_ffn.py:14-15) on b.h: the
+// MoE kernels over its one-expert stack with every row routed to it at gate 1
+// (decode: route-indexed; prefill: permutation + grouped GEMMs), then added to
+// x with h = the next pre-norm (u == nullptr), or stored to u (mHC).
+void dense_block(const Model& m, const Layer& L, Buffers& b, int rows, bool sequence,
+                 const float* next_norm, float* u, hipStream_t st) {
+  const Config& c = m.cfg;
+  const int D = c.d_model, Hd = c.dense_p();
+  const int32_t* route_pos = nullptr;
+  if (!sequence) {
+    check_call(llmy_moe_experts_routed_bf16(b.h, b.dids, b.dgates, L.ffn_gate_up, L.ffn_down,
+                                            b.dact, b.y, rows, D, Hd, 1, 1, kPacked, st),
+               "llmy_moe_experts_routed_bf16 (dense)");
+  } else {
+    check_call(llmy_moe_permute(b.dids, rows, 1, b.counts, b.offsets, b.sorted, b.route_pos, st),
+               "llmy_moe_permute (dense)");
+    check_call(llmy_moe_experts_bf16(b.h, b.offsets, b.sorted, b.dgates, L.ffn_gate_up,
+                                     L.ffn_down, b.dact, b.y, rows, D, Hd, 1, 1, kPacked, st),
+               "llmy_moe_experts_bf16 (dense)");
+    route_pos = b.route_pos;
+  }
+  if (u == nullptr)
+    check_call(llmy_moe_combine_norm(b.y, route_pos, next_norm, b.x, b.h, rows, D, 1, c.eps, st),
+               "llmy_moe_combine_norm (dense)");
+  else
+    check_call(llmy_moe_combine(b.y, route_pos ? route_pos : b.mident, u, rows, D, 1, 1, st),
+               "llmy_moe_combine (dense)");
+}
+
+// The blocks a token passes in order: the stem, the core `loops` times (one
+// state per (loop, layer)), the tail (model.py:842-909).
+struct App {
+  const Layer* L;
+  LayerState* st;
+};
+
+std::vector<App> apps_of(const Model& m, State& s, int loops) {
+  std::vector<App> a;
+  const size_t n = m.layers.size();
+  for (size_t i = 0; i < m.stem.size(); ++i) a.push_back({&m.stem[i], &s.side[i]});
+  for (int loop = 0; loop < loops; ++loop)
+    for (size_t l = 0; l < n; ++l) a.push_back({&m.layers[l], &s.layers[loop * n + l]});
+  for (size_t i = 0; i < m.tail.size(); ++i)
+    a.push_back({&m.tail[i], &s.side[m.stem.size() + i]});
+  return a;
+}
+
+const float* next_norm_of(const Model& m, const std::vector<App>& a, size_t i) {
+  return i + 1 < a.size() ? a[i + 1].L->mix_norm : m.final_norm;
 }
 
 // ------------------------------------------------------------------ CSA / HCA
@@ -1112,13 +1304,18 @@ const float* next_norm_of(const Model& m, int loop, int l, int loops) {
 void router_summary_kv(const Model& m, const Layer& L, Buffers& b, const uint16_t* vals,
                        int64_t vals_ld, int n, hipStream_t s) {
   const Config& c = m.cfg;
-  const int D = c.d_model, Lc = c.latent;
+  const int D = c.d_model, Lc = c.latent, Lp = c.latent_p();
   check_call(llmy_cmp_ring_fill_bf16(vals, vals_ld, b.g_val, n, 1, 1, D, s), "summary values");
   linear(b.g_val, L.hca_lat_down, b.g_lat_raw, nullptr, n, Lc, D, kStoreF32, s);
   check_call(llmy_layernorm_f32_bf16(b.g_lat_raw, L.hca_lat_ln_w, L.hca_lat_ln_b, b.g_lat, n, Lc,
                                      1e-5f, s),
              "llmy_layernorm_f32_bf16");
-  linear(b.g_lat, L.ctx_kv, b.g_kvr, nullptr, n, 2 * c.hq(), Lc, kStoreBf16, s);
+  const uint16_t* lat = b.g_lat;
+  if (Lp != Lc) {
+    check_call(llmy_pad_cols_bf16(b.g_lat, b.g_lat_p, n, Lc, Lp, s), "llmy_pad_cols_bf16");
+    lat = b.g_lat_p;
+  }
+  linear(lat, L.ctx_kv, b.g_kvr, nullptr, n, 2 * c.hq(), Lp, kStoreBf16, s);
 }
 
 // Decode, one token per row at positions pos: q | k | v, the local window over
@@ -1226,13 +1423,17 @@ void mhc_clear_u(const Model& m, Buffers& b, int rows, hipStream_t st) {
 
 // The MoE of layer L on b.h into U: router + top-k, then route-indexed experts
 // (decode, where the sizes allow) or permutation + grouped experts.
-void mhc_moe(const Model& m, const Layer& L, Buffers& b, int rows, bool sequence, hipStream_t st) {
+void mhc_moe(const Model& m, const Layer& L, Buffers& b, int rows, bool sequence, hipStream_t st,
+             float* ring, const int32_t* pos, int nseq, const LayerState* ls) {
   const Config& c = m.cfg;
-  const int D = c.d_model, E = c.experts, k = c.top_k, Hf = c.hidden;
+  const int D = c.d_model, E = c.experts, k = c.top_k, Hf = c.hidden_p();
   const int kx = c.routes(), EX = c.all_experts();
-  check_call(llmy_router_topk_bf16(b.h, L.router_norm, L.w_router, nullptr, b.idx, b.gates, rows,
-                                   D, E, k, c.eps, st),
-             "llmy_router_topk_bf16");
+  if (c.ctx)
+    context_route(m, L, b, rows, ring, pos, nseq, ls, st);
+  else
+    check_call(llmy_router_topk_bf16(b.h, L.router_norm, L.w_router, nullptr, b.idx, b.gates,
+                                     rows, D, E, k, c.eps, st),
+               "llmy_router_topk_bf16");
   const int32_t* ids = b.idx;
   const float* gts = b.gates;
   if (c.shared > 0) {
@@ -1271,46 +1472,107 @@ void mhc_head(const Model& m, State& s, Buffers& b, int rows, hipStream_t st) {
   check_call(llmy_sample_argmax_f32(s.logits, rows, c.vocab, s.next, st), "argmax");
 }
 
+// The attention mixer of one decode token per row into `out` (epilogue epi),
+// or, with `parts`, its output projection as per-K-block partial products.
+void attn_decode(const Model& m, const Layer& L, LayerState& st, Buffers& b, int B,
+                 const int32_t* pos, void* out, int epi, hipStream_t s) {
+  const Config& c = m.cfg;
+  const int D = c.d_model, Hhd = c.attn_heads * c.attn_head_dim;
+  linear(b.h, L.wqkv, b.qkv, nullptr, B, 3 * Hhd, D, kStoreBf16, s);
+  check_call(llmy_banded_attn_decode_bf16(b.qkv, b.qkv + Hhd, b.qkv + 2 * Hhd, 3 * Hhd, 3 * Hhd,
+                                          st.k, st.v, pos, b.ao, B, c.attn_heads, c.attn_head_dim,
+                                          c.window,
+                                          1.0f / std::sqrt(static_cast<float>(c.attn_head_dim)), s),
+             "llmy_banded_attn_decode_bf16");
+  linear(b.ao, L.wo, out, nullptr, B, D, Hhd, epi, s);
+}
+
+// The GDN mixer of one decode token per row: the input projection (as partial
+// products summed by the step kernel at small batches), the fused step, then
+// the output projection gated by the conv into `out` (epilogue epi: residual
+// add into x or U, or kPartialF32 into b.parts).
+void gdn_decode(const Model& m, const Layer& L, LayerState& st, Buffers& b, int B, void* out,
+                int epi, hipStream_t s) {
+  const Config& c = m.cfg;
+  const int D = c.d_model, HV = c.gdn_heads * c.dv;
+  const bool pp = b.proj_parts != nullptr;
+  float* proj = pp ? b.proj_parts : b.proj;
+  linear(b.h, L.wproj, proj, nullptr, B, c.nproj16(), D, pp ? kPartialF32 : kStoreF32, s);
+  check_call(llmy_gdn_step_fused_f32(proj, c.nproj16(), pp ? D / 256 : 1, L.bb, L.decay, st.S,
+                                     b.go, b.h, st.hist, L.conv, b.cg, D, 4, B, c.gdn_heads, c.dk,
+                                     c.dv, s),
+             "llmy_gdn_step_fused_f32");
+  linear(b.go, L.wout, out, epi == kPartialF32 ? nullptr : b.cg, B, D, HV, epi, s);
+}
+
+// The attention mixer over B fresh sequences of T tokens, into `out` (epi),
+// then the last min(T, W) keys / values into the ring caches.
+void attn_prefill(const Model& m, const Layer& L, LayerState& st, Buffers& b, int B, int T,
+                  void* out, int epi, hipStream_t s) {
+  const Config& c = m.cfg;
+  const int D = c.d_model, R = B * T, Hhd = c.attn_heads * c.attn_head_dim;
+  // q, k, v from row slices of the packed wqkv (each a packed [Hhd, D] matrix)
+  const size_t slice = static_cast<size_t>(Hhd) * D;
+  linear(b.h, L.wqkv, b.q, nullptr, R, Hhd, D, kStoreBf16, s);
+  linear(b.h, L.wqkv + slice, b.k, nullptr, R, Hhd, D, kStoreBf16, s);
+  linear(b.h, L.wqkv + 2 * slice, b.v, nullptr, R, Hhd, D, kStoreBf16, s);
+  check_call(llmy_banded_attn_prefill_bf16(b.q, b.k, b.v, b.ao, B, T, c.attn_heads,
+                                           c.attn_head_dim, c.window,
+                                           1.0f / std::sqrt(static_cast<float>(c.attn_head_dim)),
+                                           s),
+             "llmy_banded_attn_prefill_bf16");
+  check_call(llmy_kv_cache_fill_bf16(b.k, b.v, Hhd, st.k, st.v, B, T, c.attn_heads,
+                                     c.attn_head_dim, c.window, s),
+             "llmy_kv_cache_fill_bf16");
+  linear(b.ao, L.wo, out, nullptr, R, D, Hhd, epi, s);
+}
+
+// The GDN mixer over B fresh sequences of T tokens, gated by the conv and
+// added to `out` (x, or the cleared U).
+void gdn_prefill(const Model& m, const Layer& L, LayerState& st, Buffers& b, int B, int T,
+                 float* out, hipStream_t s) {
+  const Config& c = m.cfg;
+  const int D = c.d_model, R = B * T, H = c.gdn_heads, HV = H * c.dv;
+  linear(b.h, L.wproj, b.proj, nullptr, R, c.nproj16(), D, kStoreF32, s);
+  check_call(llmy_gdn_prefill_prep_f32(b.proj, c.nproj16(), L.bb, L.decay, b.gq, b.gk, b.gv,
+                                       b.beta, b.g, R, H, c.dk, c.dv, s),
+             "llmy_gdn_prefill_prep_f32");
+  check_call(llmy_gdn_prefill_bf16(b.gq, b.gk, b.gv, b.beta, b.g, st.S, b.go, b.ws, b.ws_bytes, B,
+                                   T, H, c.dk, c.dv, s),
+             "llmy_gdn_prefill_bf16");
+  check_call(llmy_gdn_gate_bf16(b.go, b.proj, c.nproj16(), 2 * H * c.dk + HV, b.go, R, HV, s),
+             "llmy_gdn_gate_bf16");
+  check_call(llmy_gdn_conv_gate_prefill(b.h, st.hist, L.conv, b.cg, B, T, D, 4, s),
+             "llmy_gdn_conv_gate_prefill");
+  linear(b.go, L.wout, out, b.cg, R, D, HV, kResidGated, s);
+}
+
 void decode_step_mhc(Model& m, State& s, int loops) {
   hipStream_t st_ = s.stream;
   const Config& c = m.cfg;
   Buffers& b = s.step;
-  const int B = s.B, D = c.d_model, n = static_cast<int>(m.layers.size());
-  const int Hhd = c.attn_heads * c.attn_head_dim, HV = c.gdn_heads * c.dv;
+  const int B = s.B, D = c.d_model;
   check_call(llmy_mhc_embed(b.tokens, m.embed, m.stream_seed, b.mX, B, c.mhc, D, c.vocab, st_),
              "llmy_mhc_embed");
-  for (int loop = 0; loop < loops; ++loop) {
-    for (int l = 0; l < n; ++l) {
-      const Layer& L = m.layers[l];
-      LayerState& st = s.layers[static_cast<size_t>(loop) * n + l];
-      mhc_read(m, L, b, B, L.mix_norm, st_);
-      if (L.kind == kAttn) {
-        linear(b.h, L.wqkv, b.qkv, nullptr, B, 3 * Hhd, D, kStoreBf16, st_);
-        check_call(llmy_banded_attn_decode_bf16(b.qkv, b.qkv + Hhd, b.qkv + 2 * Hhd, 3 * Hhd,
-                                                3 * Hhd, st.k, st.v, s.pos, b.ao, B, c.attn_heads,
-                                                c.attn_head_dim, c.window,
-                                                1.0f / std::sqrt(static_cast<float>(c.attn_head_dim)),
-                                                st_),
-                   "llmy_banded_attn_decode_bf16");
-        linear(b.ao, L.wo, b.mU, nullptr, B, D, Hhd, kStoreF32, st_);
-      } else if (L.kind == kCsa || L.kind == kHca) {
-        cmp_decode(m, L, st, b, B, s.pos, b.mU, kStoreF32, st_);
-      } else {
-        mhc_clear_u(m, b, B, st_);
-        const bool pp = b.proj_parts != nullptr;
-        float* proj = pp ? b.proj_parts : b.proj;
-        linear(b.h, L.wproj, proj, nullptr, B, c.nproj16(), D, pp ? kPartialF32 : kStoreF32, st_);
-        check_call(llmy_gdn_step_fused_f32(proj, c.nproj16(), pp ? D / 256 : 1, L.bb, L.decay,
-                                           st.S, b.go, b.h, st.hist, L.conv, b.cg, D, 4, B,
-                                           c.gdn_heads, c.dk, c.dv, st_),
-                   "llmy_gdn_step_fused_f32");
-        linear(b.go, L.wout, b.mU, b.cg, B, D, HV, kResidGated, st_);
-      }
-      mhc_write(m, L, b, B, st_);
-      mhc_read(m, L, b, B, L.ffn_norm, st_);
-      mhc_moe(m, L, b, B, false, st_);
-      mhc_write(m, L, b, B, st_);
+  for (const App& a : apps_of(m, s, loops)) {
+    const Layer& L = *a.L;
+    LayerState& st = *a.st;
+    mhc_read(m, L, b, B, L.mix_norm, st_);
+    if (L.kind == kAttn) {
+      attn_decode(m, L, st, b, B, s.pos, b.mU, kStoreF32, st_);
+    } else if (L.kind == kCsa || L.kind == kHca) {
+      cmp_decode(m, L, st, b, B, s.pos, b.mU, kStoreF32, st_);
+    } else {
+      mhc_clear_u(m, b, B, st_);
+      gdn_decode(m, L, st, b, B, b.mU, kResidGated, st_);
     }
+    mhc_write(m, L, b, B, st_);
+    mhc_read(m, L, b, B, L.ffn_norm, st_);
+    if (L.side)
+      dense_block(m, L, b, B, false, nullptr, b.mU, st_);
+    else
+      mhc_moe(m, L, b, B, false, st_, st.ring, s.pos, B, &st);
+    mhc_write(m, L, b, B, st_);
   }
   mhc_head(m, s, b, B, st_);
   s.last_loops = loops;
@@ -1325,57 +1587,39 @@ void decode_step(Model& m, State& s, int loops) {
   hipStream_t st_ = s.stream;
   const Config& c = m.cfg;
   Buffers& b = s.step;
-  const int B = s.B, D = c.d_model, n = static_cast<int>(m.layers.size());
-  check_call(llmy_embed_norm_bf16(b.tokens, m.embed, m.layers[0].mix_norm, b.x, b.h, B, D, c.vocab,
+  const int B = s.B, D = c.d_model;
+  const std::vector<App> apps = apps_of(m, s, loops);
+  check_call(llmy_embed_norm_bf16(b.tokens, m.embed, apps[0].L->mix_norm, b.x, b.h, B, D, c.vocab,
                                   c.eps, st_),
              "llmy_embed_norm_bf16");
-  const int Hhd = c.attn_heads * c.attn_head_dim;
-  // mixer output projections as partial products folded by the router
+  const int Hhd = c.attn_heads * c.attn_head_dim, HV = c.gdn_heads * c.dv;
+  // core mixers' output projections as partial products folded by the router
   const bool defer = b.parts != nullptr && fused_route(c, B);
-  for (int loop = 0; loop < loops; ++loop) {
-    for (int l = 0; l < n; ++l) {
-      const Layer& L = m.layers[l];
-      LayerState& st = s.layers[static_cast<size_t>(loop) * n + l];
-      int nparts = 0;
-      const float* gate = nullptr;
-      if (L.kind == kAttn) {
-        linear(b.h, L.wqkv, b.qkv, nullptr, B, 3 * Hhd, D, kStoreBf16, st_);
-        check_call(llmy_banded_attn_decode_bf16(b.qkv, b.qkv + Hhd, b.qkv + 2 * Hhd, 3 * Hhd,
-                                                3 * Hhd, st.k, st.v, s.pos, b.ao, B, c.attn_heads,
-                                                c.attn_head_dim, c.window,
-                                                1.0f / std::sqrt(static_cast<float>(c.attn_head_dim)),
-                                                st_),
-                   "llmy_banded_attn_decode_bf16");
-        if (defer) {
-          linear(b.ao, L.wo, b.parts, nullptr, B, D, Hhd, kPartialF32, st_);
-          nparts = Hhd / 256;
-        } else {
-          linear(b.ao, L.wo, b.x, nullptr, B, D, Hhd, kResidAdd, st_);
-        }
-      } else if (L.kind == kCsa || L.kind == kHca) {
-        cmp_decode(m, L, st, b, B, s.pos, b.x, kResidAdd, st_);
-      } else {
-        const int HV = c.gdn_heads * c.dv;
-        // the input projection as partial products, summed by the step kernel
-        const bool pp = b.proj_parts != nullptr;
-        float* proj = pp ? b.proj_parts : b.proj;
-        linear(b.h, L.wproj, proj, nullptr, B, c.nproj16(), D, pp ? kPartialF32 : kStoreF32, st_);
-        check_call(llmy_gdn_step_fused_f32(proj, c.nproj16(), pp ? D / 256 : 1, L.bb, L.decay, st.S,
-                                           b.go, b.h,
-                                           st.hist, L.conv, b.cg, D, 4, B, c.gdn_heads, c.dk,
-                                           c.dv, st_),
-                   "llmy_gdn_step_fused_f32");
-        if (defer) {
-          linear(b.go, L.wout, b.parts, nullptr, B, D, HV, kPartialF32, st_);
-          nparts = HV / 256;
-          gate = b.cg;
-        } else {
-          linear(b.go, L.wout, b.x, b.cg, B, D, HV, kResidGated, st_);
-        }
-      }
-      moe_block(m, L, b, B, next_norm_of(m, loop, l, loops), false, st_, st.ring, s.pos, B,
-                b.parts, nparts, gate, &st);
+  for (size_t i = 0; i < apps.size(); ++i) {
+    const Layer& L = *apps[i].L;
+    LayerState& st = *apps[i].st;
+    const float* next = next_norm_of(m, apps, i);
+    if (L.side) {  // GDN into x, the dense FFN's pre-norm, the FFN
+      gdn_decode(m, L, st, b, B, b.x, kResidGated, st_);
+      check_call(llmy_rmsnorm_f32_bf16(b.x, L.ffn_norm, b.h, B, D, c.eps, st_), "rmsnorm");
+      dense_block(m, L, b, B, false, next, nullptr, st_);
+      continue;
     }
+    int nparts = 0;
+    const float* gate = nullptr;
+    if (L.kind == kAttn) {
+      attn_decode(m, L, st, b, B, s.pos, defer ? static_cast<void*>(b.parts) : b.x,
+                  defer ? kPartialF32 : kResidAdd, st_);
+      nparts = defer ? Hhd / 256 : 0;
+    } else if (L.kind == kCsa || L.kind == kHca) {
+      cmp_decode(m, L, st, b, B, s.pos, b.x, kResidAdd, st_);
+    } else {
+      gdn_decode(m, L, st, b, B, defer ? static_cast<void*>(b.parts) : b.x,
+                 defer ? kPartialF32 : kResidGated, st_);
+      nparts = defer ? HV / 256 : 0;
+      gate = defer ? b.cg : nullptr;
+    }
+    moe_block(m, L, b, B, next, false, st_, st.ring, s.pos, B, b.parts, nparts, gate, &st);
   }
   linear(b.h, m.lm_head, s.logits, nullptr, B, c.vocab, D, kStoreF32, st_);
   check_call(llmy_sample_argmax_f32(s.logits, B, c.vocab, s.next, st_), "argmax");
@@ -1387,54 +1631,29 @@ void decode_step(Model& m, State& s, int loops) {
 void prefill_mhc(Model& m, State& s, Buffers& b, int T) {
   hipStream_t st_ = s.stream;
   const Config& c = m.cfg;
-  const int B = s.B, R = B * T, D = c.d_model, S = c.mhc, n = static_cast<int>(m.layers.size());
-  const int Hhd = c.attn_heads * c.attn_head_dim;
+  const int B = s.B, R = B * T, D = c.d_model, S = c.mhc;
   check_call(llmy_mhc_embed(b.tokens, m.embed, m.stream_seed, b.mX, R, S, D, c.vocab, st_),
              "llmy_mhc_embed");
   const int loops = m.loops;
-  for (int loop = 0; loop < loops; ++loop) {
-    for (int l = 0; l < n; ++l) {
-      const Layer& L = m.layers[l];
-      LayerState& st = s.layers[static_cast<size_t>(loop) * n + l];
-      mhc_read(m, L, b, R, L.mix_norm, st_);
-      if (L.kind == kAttn) {
-        const size_t slice = static_cast<size_t>(Hhd) * D;
-        linear(b.h, L.wqkv, b.q, nullptr, R, Hhd, D, kStoreBf16, st_);
-        linear(b.h, L.wqkv + slice, b.k, nullptr, R, Hhd, D, kStoreBf16, st_);
-        linear(b.h, L.wqkv + 2 * slice, b.v, nullptr, R, Hhd, D, kStoreBf16, st_);
-        check_call(llmy_banded_attn_prefill_bf16(b.q, b.k, b.v, b.ao, B, T, c.attn_heads,
-                                                 c.attn_head_dim, c.window,
-                                                 1.0f / std::sqrt(static_cast<float>(c.attn_head_dim)),
-                                                 st_),
-                   "llmy_banded_attn_prefill_bf16");
-        check_call(llmy_kv_cache_fill_bf16(b.k, b.v, Hhd, st.k, st.v, B, T, c.attn_heads,
-                                           c.attn_head_dim, c.window, st_),
-                   "llmy_kv_cache_fill_bf16");
-        linear(b.ao, L.wo, b.mU, nullptr, R, D, Hhd, kStoreF32, st_);
-      } else if (L.kind == kCsa || L.kind == kHca) {
-        cmp_prefill(m, L, st, b, B, T, b.mU, kStoreF32, st_);
-      } else {
-        const int H = c.gdn_heads, HV = H * c.dv;
-        mhc_clear_u(m, b, R, st_);
-        linear(b.h, L.wproj, b.proj, nullptr, R, c.nproj16(), D, kStoreF32, st_);
-        check_call(llmy_gdn_prefill_prep_f32(b.proj, c.nproj16(), L.bb, L.decay, b.gq, b.gk, b.gv,
-                                             b.beta, b.g, R, H, c.dk, c.dv, st_),
-                   "llmy_gdn_prefill_prep_f32");
-        check_call(llmy_gdn_prefill_bf16(b.gq, b.gk, b.gv, b.beta, b.g, st.S, b.go, b.ws,
-                                         b.ws_bytes, B, T, H, c.dk, c.dv, st_),
-                   "llmy_gdn_prefill_bf16");
-        check_call(llmy_gdn_gate_bf16(b.go, b.proj, c.nproj16(), 2 * H * c.dk + HV, b.go, R, HV,
-                                      st_),
-                   "llmy_gdn_gate_bf16");
-        check_call(llmy_gdn_conv_gate_prefill(b.h, st.hist, L.conv, b.cg, B, T, D, 4, st_),
-                   "llmy_gdn_conv_gate_prefill");
-        linear(b.go, L.wout, b.mU, b.cg, R, D, HV, kResidGated, st_);
-      }
-      mhc_write(m, L, b, R, st_);
-      mhc_read(m, L, b, R, L.ffn_norm, st_);
-      mhc_moe(m, L, b, R, true, st_);
-      mhc_write(m, L, b, R, st_);
+  for (const App& a : apps_of(m, s, loops)) {
+    const Layer& L = *a.L;
+    LayerState& st = *a.st;
+    mhc_read(m, L, b, R, L.mix_norm, st_);
+    if (L.kind == kAttn) {
+      attn_prefill(m, L, st, b, B, T, b.mU, kStoreF32, st_);
+    } else if (L.kind == kCsa || L.kind == kHca) {
+      cmp_prefill(m, L, st, b, B, T, b.mU, kStoreF32, st_);
+    } else {
+      mhc_clear_u(m, b, R, st_);
+      gdn_prefill(m, L, st, b, B, T, b.mU, st_);
     }
+    mhc_write(m, L, b, R, st_);
+    mhc_read(m, L, b, R, L.ffn_norm, st_);
+    if (L.side)
+      dense_block(m, L, b, R, true, nullptr, b.mU, st_);
+    else
+      mhc_moe(m, L, b, R, true, st_, st.ring, nullptr, B, &st);
+    mhc_write(m, L, b, R, st_);
   }
   // each sequence's last streams -> the decode buffers, then the head
   const size_t row = static_cast<size_t>(S) * D * 4;
@@ -1453,9 +1672,9 @@ void prefill_mhc(Model& m, State& s, Buffers& b, int T) {
 void prefill(Model& m, State& s, const int32_t* tokens, int T, bool tokens_on_device) {
   hipStream_t st_ = s.stream;
   const Config& c = m.cfg;
-  const int B = s.B, R = B * T, D = c.d_model, n = static_cast<int>(m.layers.size());
+  const int B = s.B, R = B * T, D = c.d_model;
   reset_state(s);
-  if (!s.seq || s.seq->rows < R || (c.gdn_heads > 0 && s.seq->ws_bytes <
+  if (!s.seq || s.seq->rows < R || (c.has_gdn() && s.seq->ws_bytes <
                                     llmy_gdn_prefill_workspace_bytes(B, T, c.gdn_heads, c.dk, c.dv))) {
     s.seq.reset();
     auto nb = std::make_unique<Buffers>();
@@ -1470,53 +1689,30 @@ void prefill(Model& m, State& s, const int32_t* tokens, int T, bool tokens_on_de
     prefill_mhc(m, s, b, T);
     return;
   }
-  check_call(llmy_embed_norm_bf16(b.tokens, m.embed, m.layers[0].mix_norm, b.x, b.h, R, D, c.vocab,
-                                  c.eps, st_),
-             "llmy_embed_norm_bf16");
   // the loop count set by llmy_set_num_loops (model_prefill runs cfg.num_loops,
   // which llmy_set_num_loops overwrites: llmy_cuda/src/model.cpp:1964, llmy.cpp:66-69)
   const int loops = m.loops;
-  const int Hhd = c.attn_heads * c.attn_head_dim;
-  for (int loop = 0; loop < loops; ++loop) {
-    for (int l = 0; l < n; ++l) {
-      const Layer& L = m.layers[l];
-      LayerState& st = s.layers[static_cast<size_t>(loop) * n + l];
-      if (L.kind == kAttn) {
-        // q, k, v from row slices of the packed wqkv (each a packed [Hhd, D] matrix)
-        const size_t slice = static_cast<size_t>(Hhd) * D;
-        linear(b.h, L.wqkv, b.q, nullptr, R, Hhd, D, kStoreBf16, st_);
-        linear(b.h, L.wqkv + slice, b.k, nullptr, R, Hhd, D, kStoreBf16, st_);
-        linear(b.h, L.wqkv + 2 * slice, b.v, nullptr, R, Hhd, D, kStoreBf16, st_);
-        check_call(llmy_banded_attn_prefill_bf16(b.q, b.k, b.v, b.ao, B, T, c.attn_heads,
-                                                 c.attn_head_dim, c.window,
-                                                 1.0f / std::sqrt(static_cast<float>(c.attn_head_dim)),
-                                                 st_),
-                   "llmy_banded_attn_prefill_bf16");
-        check_call(llmy_kv_cache_fill_bf16(b.k, b.v, Hhd, st.k, st.v, B, T, c.attn_heads,
-                                           c.attn_head_dim, c.window, st_),
-                   "llmy_kv_cache_fill_bf16");
-        linear(b.ao, L.wo, b.x, nullptr, R, D, Hhd, kResidAdd, st_);
-      } else if (L.kind == kCsa || L.kind == kHca) {
-        cmp_prefill(m, L, st, b, B, T, b.x, kResidAdd, st_);
-      } else {
-        const int H = c.gdn_heads, HV = H * c.dv;
-        linear(b.h, L.wproj, b.proj, nullptr, R, c.nproj16(), D, kStoreF32, st_);
-        check_call(llmy_gdn_prefill_prep_f32(b.proj, c.nproj16(), L.bb, L.decay, b.gq, b.gk, b.gv,
-                                             b.beta, b.g, R, H, c.dk, c.dv, st_),
-                   "llmy_gdn_prefill_prep_f32");
-        check_call(llmy_gdn_prefill_bf16(b.gq, b.gk, b.gv, b.beta, b.g, st.S, b.go, b.ws, b.ws_bytes,
-                                         B, T, H, c.dk, c.dv, st_),
-                   "llmy_gdn_prefill_bf16");
-        check_call(llmy_gdn_gate_bf16(b.go, b.proj, c.nproj16(), 2 * H * c.dk + HV, b.go, R, HV,
-                                      st_),
-                   "llmy_gdn_gate_bf16");
-        check_call(llmy_gdn_conv_gate_prefill(b.h, st.hist, L.conv, b.cg, B, T, D, 4, st_),
-                   "llmy_gdn_conv_gate_prefill");
-        linear(b.go, L.wout, b.x, b.cg, R, D, HV, kResidGated, st_);
-      }
-      moe_block(m, L, b, R, next_norm_of(m, loop, l, loops), true, st_, st.ring, nullptr, B,
-                nullptr, 0, nullptr, &st);
+  const std::vector<App> apps = apps_of(m, s, loops);
+  check_call(llmy_embed_norm_bf16(b.tokens, m.embed, apps[0].L->mix_norm, b.x, b.h, R, D, c.vocab,
+                                  c.eps, st_),
+             "llmy_embed_norm_bf16");
+  for (size_t i = 0; i < apps.size(); ++i) {
+    const Layer& L = *apps[i].L;
+    LayerState& st = *apps[i].st;
+    const float* next = next_norm_of(m, apps, i);
+    if (L.side) {
+      gdn_prefill(m, L, st, b, B, T, b.x, st_);
+      check_call(llmy_rmsnorm_f32_bf16(b.x, L.ffn_norm, b.h, R, D, c.eps, st_), "rmsnorm");
+      dense_block(m, L, b, R, true, next, nullptr, st_);
+      continue;
     }
+    if (L.kind == kAttn)
+      attn_prefill(m, L, st, b, B, T, b.x, kResidAdd, st_);
+    else if (L.kind == kCsa || L.kind == kHca)
+      cmp_prefill(m, L, st, b, B, T, b.x, kResidAdd, st_);
+    else
+      gdn_prefill(m, L, st, b, B, T, b.x, st_);
+    moe_block(m, L, b, R, next, true, st_, st.ring, nullptr, B, nullptr, 0, nullptr, &st);
   }
   // last position of each sequence -> the decode buffer, then the LM head
   check_hip(hipMemcpy2DAsync(s.step.h, static_cast<size_t>(D) * 2,

@@ -324,3 +324,73 @@ def test_cmp_roundtrip(lib, tmp_path):
         (4, 128, 16, 128, 32)
     assert (c0.hca_ratio, c0.hca_window, c0.hca_dense, c0.hca_top_k, c0.cmp_slots) == \
         (32, 128, True, 32, 256)
+
+
+def test_stem_tail_roundtrip(lib, tmp_path):
+    """Stem and tail blocks under the reference's names (stem.<i>. / tail.<i>.
+    mixer_norm, ffn_norm, mixer.<GDN>, ffn.gate_proj / up_proj / down_proj,
+    mhc.*: model/model.py:391-394,411-414; llmy_cuda/src/model.cpp:81-87,
+    205-250) and the keys stem_blocks / tail_blocks / dense_ffn.hidden /
+    physical_blocks; the native parser accepts the file."""
+    from dataclasses import replace
+    cfg = replace(TINY, stem_blocks=1, tail_blocks=2, dense_hidden=320, mhc_streams=4,
+                  expert_hidden=320)
+    w = init_weights(cfg, seed=9)
+    path = tmp_path / "side.llmy"
+    save_llmy(path, cfg, w)
+    back_cfg, back = load_weights(path)
+    assert back_cfg == cfg
+    for key, t in w.items():
+        assert torch.equal(back[key], t), key
+    assert file_name(cfg, "S0.ffn_gate") == "stem.0.ffn.gate_proj.weight"
+    assert file_name(cfg, "T1.ffn_down") == "tail.1.ffn.down_proj.weight"
+    assert file_name(cfg, "T0.wq") == "tail.0.mixer.q_proj.weight"
+    assert file_name(cfg, "S0.mix_norm") == "stem.0.mixer_norm.weight"
+    assert file_name(cfg, "S0.mhc_theta") == "stem.0.mhc.theta.weight"
+    text = config_text(cfg)
+    for kv in ("stem_blocks=1", "tail_blocks=2", "dense_ffn.hidden=320", "physical_blocks=5"):
+        assert kv + "\n" in text
+    st, desc = _describe(lib, path)
+    assert st == 0, lib.llmy_last_error()
+    names = {l.split()[0] for l in desc.split("--\n")[1].splitlines()}
+    assert {"stem.0.ffn.up_proj.weight", "tail.1.mixer.conv.weight",
+            "tail.1.mhc.alpha_pre"} <= names
+
+
+@pytest.mark.parametrize("key,value", [
+    ("loop_attnres.enabled", "true"), ("adaptive_loops.enabled", "1"),
+    ("mhc.shared_across_loops", "false"), ("mhc.preserve_streams_across_loop_boundary", "0"),
+    ("physical_blocks", "7")])
+def test_unsupported_keys_are_refused(lib, tmp_path, key, value):
+    """Config keys that change the reference model's math in ways this block
+    stack does not run are refused by both readers, with a message, rather
+    than ignored (model/config.py:14-15,80-102; model.py:397-408,634-635)."""
+    lines = [l for l in config_text(TINY).splitlines() if not l.startswith(key + "=")]
+    text = "".join(l + "\n" for l in lines + [f"{key}={value}"])
+    with pytest.raises(ValueError, match=key.split(".")[0]):
+        config_from_text(text)
+    # the same file written with that config text, for the native reader
+    from hybrid_llm_amd import checkpoint as ck
+    path = tmp_path / "k.llmy"
+    orig = ck.config_text
+    try:
+        ck.config_text = lambda cfg: text
+        save_llmy(path, TINY, init_weights(TINY, seed=3))
+    finally:
+        ck.config_text = orig
+    st, _ = _describe(lib, path)
+    assert st != 0
+    assert key.split(".")[0].encode() in lib.llmy_last_error() or b"physical" in lib.llmy_last_error()
+
+
+def test_hca_global_latents_off_is_refused():
+    """router.use_hca_global_latents = 0 with HCA blocks and the context router:
+    both reference implementations ignore the key, so a file asking for it is
+    refused; without HCA blocks (the reference training config) it is inert."""
+    from dataclasses import replace
+    cfg = replace(TINY, layer_kinds=("hca", "gdn"), context_router=True)
+    text = config_text(cfg) + "router.use_hca_global_latents=false\n"
+    with pytest.raises(ValueError, match="use_hca_global_latents"):
+        config_from_text(text)
+    plain = config_text(replace(TINY, context_router=True)) + "router.use_hca_global_latents=0\n"
+    assert config_from_text(plain).context_router
