@@ -78,7 +78,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "llmy_cmp_local_prefill_bf16": (_I, [_P, _I64, _P, _I64, _P, _I64, _P, _I64, _I, _I, _I, _I,
                                          _I, _I, _F, _P, _I64, _P]),
     "llmy_cmp_memory_prefill_bf16": (_I, [_P, _I64, _P, _I64, _P, _I64, _P, _I64, _I, _I, _I,
-                                          _I, _I, _I, _I, _I, _F, _P, _I64, _P]),
+                                          _I, _I, _I, _I, _I, _I, _F, _P, _I64, _P]),
     "llmy_cmp_local_decode_bf16": (_I, [_P, _I64, _P, _P, _I64, _P, _P, _P, _P, _I64, _I, _I, _I,
                                         _I, _I, _F, _P, _I64, _P]),
     "llmy_cmp_memory_decode_bf16": (_I, [_P, _I64, _P, _P, _P, _P, _P, _I64, _I, _I, _I, _I, _I,

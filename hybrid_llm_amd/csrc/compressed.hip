@@ -171,8 +171,10 @@ __device__ __forceinline__ void topk_row(float* srow, int n, int k, int lane, fl
 //   band: keys [max(0, t0 - W + 1), min(T - 1, t0 + 31)] of row b (q/k rows
 //         b*T + t); the list of query t has W slots, slot j = key t - W + 1 + j;
 //   memory: entries [0, nv), nv = min(n, min(T, t0 + 32) / ratio) (rows b*n + i,
-//         entry i visible from position (i + 1) ratio - 1 on); dense lists have
-//         n slots, top-k lists top_k pairs.
+//         entry i visible from position (i + 1) ratio - 1 on and, with W > 0 (the
+//         decode memory's slots), while it is among the last W entries emitted,
+//         i >= (t + 1) / ratio - W, as a token-by-token decode sees them);
+//         dense lists have n slots, top-k lists top_k pairs.
 // NS = head_dim / 16 when it is at most 8: the 32 queries' fragments stay in
 // registers and each wave prefetches its next 32-candidate tile under the
 // current tile's MFMAs; NS = 0: any multiple-of-16 head width, operands loaded
@@ -273,7 +275,7 @@ __global__ __launch_bounds__(512) void cmp_select_prefill_kernel(
           const int cj = c0 + (r & 3) + 8 * (r >> 2) + 4 * half;
           bool vis = t < T && cj < c_lo + nc;
           if (MODE == kBand) vis = vis && cj <= t && t - cj < W;
-          else vis = vis && (cj + 1) * ratio - 1 <= t;
+          else vis = vis && (cj + 1) * ratio - 1 <= t && (W <= 0 || cj >= (t + 1) / ratio - W);
           sc[row * ncp + (cj - c_lo)] = vis ? acc[r] * scale_log2 : -INFINITY;
         }
       }
@@ -977,10 +979,10 @@ extern "C" int32_t llmy_cmp_local_prefill_bf16(
 extern "C" int32_t llmy_cmp_memory_prefill_bf16(
     const llmy_bf16* q, int64_t q_ld, const llmy_bf16* mk, int64_t mk_ld, const llmy_bf16* mv,
     int64_t mv_ld, llmy_bf16* out, int64_t out_ld, int32_t B, int32_t T, int32_t n_entries,
-    int32_t ratio, int32_t H, int32_t head_dim, int32_t Dv, int32_t top_k, float scale,
-    void* workspace, int64_t workspace_bytes, void* stream) {
+    int32_t ratio, int32_t H, int32_t head_dim, int32_t Dv, int32_t top_k, int32_t slots_window,
+    float scale, void* workspace, int64_t workspace_bytes, void* stream) {
   LLMY_REQUIRE(B >= 0 && T >= 0 && H > 0 && dh_ok(head_dim) && Dv > 0 && Dv % 8 == 0 &&
-               ratio >= 1 && n_entries >= 0 && top_k >= 0 && top_k <= 64);
+               ratio >= 1 && n_entries >= 0 && top_k >= 0 && top_k <= 64 && slots_window >= 0);
   if (B == 0 || T == 0) return 0;
   LLMY_REQUIRE(n_entries == T / ratio);
   const int Kw = H * head_dim;
@@ -1008,12 +1010,12 @@ extern "C" int32_t llmy_cmp_memory_prefill_bf16(
   const size_t lds = static_cast<size_t>(rows) * ncp * 4;
   if (top_k > 0)
     select_prefill_launch<kMemTopK>(dim3(B * nqb * H), lds, s, q, q_ld, mk, mk_ld, T, n_entries,
-                                    H, head_dim, 1, ratio, top_k, Kmax, rows, scale * kLog2eC, wl,
-                                    il);
+                                    H, head_dim, slots_window, ratio, top_k, Kmax, rows,
+                                    scale * kLog2eC, wl, il);
   else
     select_prefill_launch<kMemDense>(dim3(B * nqb * H), lds, s, q, q_ld, mk, mk_ld, T, n_entries,
-                                     H, head_dim, 1, ratio, 0, Kmax, rows, scale * kLog2eC, wl,
-                                     il);
+                                     H, head_dim, slots_window, ratio, 0, Kmax, rows,
+                                     scale * kLog2eC, wl, il);
   const int32_t st = launch_status();
   if (st) return st;
   return apply_launch(wl, il, Kmax, H, B, T, nullptr, 0, slots, mv, mv_ld, slots, 0, out,

@@ -1372,7 +1372,7 @@ void cmp_prefill(const Model& m, const Layer& L, LayerState& st, Buffers& b, int
   if (n > 0) linear(b.cmean, L.cmp_wc, b.ckv, nullptr, B * n, Kw + D, D, kStoreBf16, s);
   check_call(llmy_cmp_memory_prefill_bf16(b.cqkv, N, b.ckv, Kw + D, b.ckv + Kw, Kw + D,
                                           b.cloc + D, 2 * D, B, T, n, cs.ratio, cs.H, cs.Dh, D,
-                                          cs.top_k, scale, b.cws, b.cws_bytes, s),
+                                          cs.top_k, C, scale, b.cws, b.cws_bytes, s),
              "llmy_cmp_memory_prefill_bf16");
   check_call(llmy_cmp_memory_fill_bf16(b.ckv, Kw + D, st.mk, st.mv, st.mtag, st.mcount, B, n,
                                        cs.ratio, C, Kw, D, s),
@@ -1673,6 +1673,18 @@ void prefill(Model& m, State& s, const int32_t* tokens, int T, bool tokens_on_de
   hipStream_t st_ = s.stream;
   const Config& c = m.cfg;
   const int B = s.B, R = B * T, D = c.d_model;
+  // prompts the compressed-memory prefill cannot take are refused before any
+  // kernel runs (the Python engine's check_prompt_length)
+  for (int kind : {kCsa, kHca}) {
+    if (!c.has(kind)) continue;
+    const int ratio = c.cmp(kind).ratio, n = T / ratio;
+    if (n > 4000)
+      throw std::runtime_error("prompt too long: a CSA / HCA block's prefill takes at most 4000 "
+                               "summaries per row");
+    if (kind == kHca && c.ctx && n > c.cmp_slots)
+      throw std::runtime_error("prompt emits more HCA summaries per row than the router's summary "
+                               "memory keeps (memory.decode_slots)");
+  }
   reset_state(s);
   if (!s.seq || s.seq->rows < R || (c.has_gdn() && s.seq->ws_bytes <
                                     llmy_gdn_prefill_workspace_bytes(B, T, c.gdn_heads, c.dk, c.dv))) {

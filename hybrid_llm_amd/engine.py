@@ -38,6 +38,29 @@ def _pad_rows(w: torch.Tensor, mult: int) -> torch.Tensor:
     return torch.cat([w, torch.zeros(pad, *w.shape[1:], dtype=w.dtype, device=w.device)], 0)
 
 
+CMP_PREFILL_MAX_SUMMARIES = 4000  # llmy_cmp_memory_prefill_bf16's limit per row
+
+
+def check_prompt_length(cfg: HybridConfig, T: int) -> None:
+    """Refuse, before any kernel runs, a prompt the compressed-memory prefill
+    cannot take: more than 4000 summaries per row on a CSA / HCA block, or, on an
+    HCA block with the context router, more summaries than the decode memory
+    keeps (its latent attention reads the router's summary ring, which then no
+    longer holds an early token's summaries; memory.decode_slots raises it)."""
+    for kind in sorted({k for k in cfg.layer_kinds if k in ("csa", "hca")}):
+        ratio = cfg.cmp_shape(kind)["ratio"]
+        n = T // ratio
+        if n > CMP_PREFILL_MAX_SUMMARIES:
+            raise ValueError(f"prompt of {T} tokens: a {kind.upper()} block's prefill takes at most "
+                             f"{CMP_PREFILL_MAX_SUMMARIES} summaries per row "
+                             f"(T < {(CMP_PREFILL_MAX_SUMMARIES + 1) * ratio})")
+        if kind == "hca" and cfg.context_router and n > cfg.cmp_slots:
+            raise ValueError(f"prompt of {T} tokens emits {n} HCA summaries per row, more than the "
+                             f"{cfg.cmp_slots} the router's summary memory keeps "
+                             f"(memory.decode_slots); prefill at most "
+                             f"{(cfg.cmp_slots + 1) * ratio - 1} tokens")
+
+
 def round256(n: int) -> int:
     return (n + 255) // 256 * 256
 
@@ -795,6 +818,7 @@ class HybridDecoder:
             raise ValueError(f"tokens must be [B={self.B}, T>=1], got {tuple(tokens.shape)}")
         B, T = tokens.shape
         R, D = B * T, cfg.d_model
+        check_prompt_length(cfg, T)
         self.reset()
         if self.mhc:
             return self._prefill_mhc(tokens, B, T)
@@ -920,7 +944,7 @@ class HybridDecoder:
         kv = (ops.linear(means, w[p + "cmp_wc"], layout=ops.LAYOUT_PACKED) if n else
               torch.empty(0, Kw + D, dtype=torch.bfloat16, device=self.dev))
         ops.cmp_memory_prefill(q, kv[:, :Kw], kv[:, Kw:], B, T, ratio, H, Dh, cs["top_k"],
-                               out=loc[:, D:])
+                               out=loc[:, D:], slots=cfg.cmp_slots)
         ops.cmp_memory_fill(kv, B, n, ratio, st["mk"], st["mv"], st["mtag"], st["mcount"])
         if "rk" in st and n:
             kvr = self._router_summary_kv(p, kv[:, Kw:].contiguous())

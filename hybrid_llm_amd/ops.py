@@ -803,8 +803,10 @@ def cmp_local_prefill(q, k, v, B: int, T: int, H: int, Dh: int, W: int, out=None
 
 
 def cmp_memory_prefill(q, mk, mv, B: int, T: int, ratio: int, H: int, Dh: int, top_k: int,
-                       out=None, workspace=None) -> torch.Tensor:
-    """Memory branch over B fresh sequences; mk / mv rows b*n + i, n = T // ratio."""
+                       out=None, workspace=None, slots: int = 0) -> torch.Tensor:
+    """Memory branch over B fresh sequences; mk / mv rows b*n + i, n = T // ratio.
+    ``slots`` > 0: a query sees only the last ``slots`` summaries emitted up to
+    it (the decode memory's ring); 0: all of them."""
     Kw, Dv, n = H * Dh, mv.shape[1], T // ratio
     if mk.shape[0] != B * n or mv.shape[0] != B * n:
         raise ValueError("mk / mv must hold B * (T // ratio) rows")
@@ -814,8 +816,8 @@ def cmp_memory_prefill(q, mk, mv, B: int, T: int, ratio: int, H: int, Dh: int, t
     if workspace is None:
         workspace = cmp_workspace(B * T, H, max(n, 1), top_k, q.device)
     _lib.call("llmy_cmp_memory_prefill_bf16", _ptr(q), q_ld, _ptr(mk), mk_ld, _ptr(mv), mv_ld,
-              _ptr(out), _rows(out, "out", Dv), B, T, n, ratio, H, Dh, Dv, top_k, Dh ** -0.5,
-              _ptr(workspace), workspace.numel(), _stream())
+              _ptr(out), _rows(out, "out", Dv), B, T, n, ratio, H, Dh, Dv, top_k, slots,
+              Dh ** -0.5, _ptr(workspace), workspace.numel(), _stream())
     return out
 
 

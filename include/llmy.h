@@ -397,13 +397,17 @@ int32_t llmy_cmp_local_prefill_bf16(const llmy_bf16* q, int64_t q_ld, const llmy
                                     void* stream);
 /* Memory branch over B fresh sequences: n_entries = T / ratio summaries per row
  * (keys mk rows b*n + i, values mv rows b*n + i), summary i visible from
- * position (i + 1) ratio - 1 on. */
+ * position (i + 1) ratio - 1 on; with slots_window > 0 (the decode memory's
+ * slots per row) only while it is among the last slots_window summaries
+ * emitted, as the token-by-token decode over that ring sees it (0: every
+ * summary emitted so far, as csa.py:99-105 / hca.py:88-93).  n_entries <= 4000. */
 int32_t llmy_cmp_memory_prefill_bf16(const llmy_bf16* q, int64_t q_ld, const llmy_bf16* mk,
                                      int64_t mk_ld, const llmy_bf16* mv, int64_t mv_ld,
                                      llmy_bf16* out, int64_t out_ld, int32_t B, int32_t T,
                                      int32_t n_entries, int32_t ratio, int32_t H,
-                                     int32_t head_dim, int32_t Dv, int32_t top_k, float scale,
-                                     void* workspace, int64_t workspace_bytes, void* stream);
+                                     int32_t head_dim, int32_t Dv, int32_t top_k,
+                                     int32_t slots_window, float scale, void* workspace,
+                                     int64_t workspace_bytes, void* stream);
 /* Local branch, one token per row at pos[b]: stores k_new / v_new (rows at
  * kv_ld) into ring slot pos % W of ring_k [B, W, H*head_dim] / ring_v [B, W, Dv]
  * and attends to keys max(0, pos - W + 1) .. pos. */

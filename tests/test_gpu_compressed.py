@@ -101,6 +101,42 @@ def test_memory_prefill(B, T, ratio, H, Dh, Dv, top_k):
     _close(out, _mem_ref(q, kv[:, :Kw], kv[:, Kw:], B, T, ratio, H, Dh, top_k))
 
 
+@pytest.mark.parametrize("T,ratio,C,top_k", [(100, 4, 4, 3), (100, 4, 4, 0), (300, 32, 3, 0)])
+def test_memory_prefill_ring_window(T, ratio, C, top_k):
+    """With slots = C below the prompt's T / ratio summaries, query t sees only
+    the last C summaries emitted up to it: the brute-force reference with that
+    window, and the decode kernel over a C-slot memory filled with the first
+    (t + 1) // ratio summaries, which is the token-by-token decode's state."""
+    B, H, Dh, Dv = 1, 2, 64, 128
+    print(f"memory prefill ring window T={T} r={ratio} C={C} k={top_k}", flush=True)
+    g = torch.Generator().manual_seed(T + C + top_k)
+    Kw, n = H * Dh, T // ratio
+    q = _bf(B * T, Kw, gen=g)
+    kv = _bf(B * n, Kw + Dv, gen=g)
+    d = kv.cuda()
+    out = ops().cmp_memory_prefill(q.cuda(), d[:, :Kw], d[:, Kw:], B, T, ratio, H, Dh, top_k,
+                                   slots=C)
+    torch.cuda.synchronize()
+    i = torch.arange(n)
+    t = torch.arange(T)[:, None]
+    vis = ((i * ratio + ratio - 1)[None] <= t) & (i[None] >= (t + 1) // ratio - C)
+    P = head_mean_probs(head_scores(q.float().view(B, T, Kw), kv[:, :Kw].float().view(B, n, Kw),
+                                    H, Dh), vis[None], top_k or None)
+    _close(out, (P.double() @ kv[:, Kw:].double().view(B, n, Dv)).view(B * T, Dv))
+    for tq in [0, ratio - 1, C * ratio - 1, C * ratio, T // 2, T - 1]:
+        cnt = (tq + 1) // ratio
+        mk = torch.zeros(B, C, Kw, dtype=torch.bfloat16, device="cuda")
+        mv = torch.zeros(B, C, Dv, dtype=torch.bfloat16, device="cuda")
+        mtag = torch.zeros(B, C, dtype=torch.int32, device="cuda")
+        mcount = torch.zeros(B, dtype=torch.int32, device="cuda")
+        ops().cmp_memory_fill(d[:cnt], B, cnt, ratio, mk, mv, mtag, mcount)
+        dec = ops().cmp_memory_decode(q[tq:tq + 1].cuda(), mk, mv, mtag,
+                                      torch.tensor([tq], dtype=torch.int32, device="cuda"), H, Dh,
+                                      top_k)
+        torch.cuda.synchronize()
+        assert float((dec.float() - out[tq:tq + 1].float()).abs().max()) <= 1e-2, tq
+
+
 # B * H >= 512 (the last case) takes the one-kernel scores + list form
 @pytest.mark.parametrize("B,H,Dh,Dv,W", [(8, 16, 128, 1024, 128), (4, 1, 1024, 1024, 128),
                                          (3, 2, 64, 128, 7), (32, 16, 128, 256, 128)])
