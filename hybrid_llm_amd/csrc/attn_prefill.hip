@@ -64,6 +64,7 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const uint16_t* __res
   const int col = lane & 31;
   const long long rs = static_cast<long long>(H) * HD;  // row stride (elements)
   const long long base = static_cast<long long>(b) * T * rs + static_cast<long long>(h) * HD;
+  const uint32_t rs32 = static_cast<uint32_t>(rs);      // T * H * HD < 2^31 (host check)
 
   const int q0 = qblk * kBM;
   const int qw = q0 + 32 * wave;       // first query of this wave
@@ -101,27 +102,36 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const uint16_t* __res
   // (2-byte stores put two lanes on one dword).
   constexpr int NPW = (kBN / 2) * CH / 256;      // key-pair entries per thread
   static_assert(2 * NPW == NCHK, "V pair staging covers the tile");
+  static_assert(NCHK * 256 == kBN * CH, "every thread fetches whole chunks");
+  // Each thread's chunks sit at fixed (key, column) offsets inside a tile, so
+  // a tile's loads are its base plus per-thread offsets plus constants.  K
+  // chunk u: row kr0 + u * (256 / CH), column kc0; V pair entry w: rows vr0 and
+  // vr0 + 1, column vc0 + 64 w.  Rows past the sequence (the last tile only)
+  // are zero: a key there follows every query and is masked.
+  const uint32_t kr0 = threadIdx.x / CH, kc0 = 8 * (threadIdx.x % CH);
+  const uint32_t vr0 = 2 * (threadIdx.x % (kBN / 2)), vc0 = 8 * (threadIdx.x / (kBN / 2));
+  const uint32_t koff0 = kr0 * rs32 + kc0, voff0 = vr0 * rs32 + vc0;
+  const uint16_t* kbase = k + base;
+  const uint16_t* vbase = v + base;
   auto fetch = [&](int tile) {
     const int kt = tile * kBN;
+    const uint16_t* kb = kbase + static_cast<long long>(kt) * rs;
+    const uint16_t* vb = vbase + static_cast<long long>(kt) * rs;
+    const uint32_t last = static_cast<uint32_t>(T - 1 - kt);
 #pragma unroll
     for (int u = 0; u < NCHK; ++u) {
-      const int f = threadIdx.x + 256 * u;
-      const int key = f / CH, c = f - (f / CH) * CH;
-      const int kk = kt + key;
-      const bool ok = f < kBN * CH && kk < T;
-      kreg[u] = ok ? *reinterpret_cast<const uint4*>(k + base + kk * rs + 8 * c)
-                   : uint4{0u, 0u, 0u, 0u};
+      const uint32_t kr = kr0 + u * (256 / CH);
+      kreg[u] = kr <= last ? *reinterpret_cast<const uint4*>(kb + koff0 + u * (256 / CH) * rs32)
+                           : uint4{0u, 0u, 0u, 0u};
     }
 #pragma unroll
-    for (int w = 0; w < NPW; ++w) {
-      const int f = threadIdx.x + 256 * w;
-      const int vk = kt + 2 * (f % (kBN / 2)), vc = f / (kBN / 2);
+    for (int w = 0; w < NPW; ++w)
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
-        vreg[2 * w + i] = vk + i < T
-                              ? *reinterpret_cast<const uint4*>(v + base + (vk + i) * rs + 8 * vc)
+      for (int i = 0; i < 2; ++i) {
+        vreg[2 * w + i] = vr0 + i <= last
+                              ? *reinterpret_cast<const uint4*>(vb + voff0 + i * rs32 + 64 * w)
                               : uint4{0u, 0u, 0u, 0u};
-    }
+      }
   };
   fetch(t_lo);
   for (int tile = t_lo; tile <= t_hi; ++tile) {
@@ -129,13 +139,8 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const uint16_t* __res
     // ---- stage K (row-major, padded) and V^T (transposed) for 64 keys
     __syncthreads();
 #pragma unroll
-    for (int u = 0; u < NCHK; ++u) {
-      const int f = threadIdx.x + 256 * u;
-      if (f < kBN * CH) {
-        const int key = f / CH, c = f - (f / CH) * CH;
-        *reinterpret_cast<uint4*>(Ks + key * (HD + kKPad) + 8 * c) = kreg[u];
-      }
-    }
+    for (int u = 0; u < NCHK; ++u)  // every thread's chunks lie in the tile (NCHK * 256 = kBN * CH)
+      *reinterpret_cast<uint4*>(Ks + (kr0 + u * (256 / CH)) * (HD + kKPad) + kc0) = kreg[u];
 #pragma unroll
     for (int w = 0; w < NPW; ++w) {
       const int f = threadIdx.x + 256 * w;
@@ -145,10 +150,11 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const uint16_t* __res
                               vreg[2 * w + 1].w};
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        // dim 8vc + e: key 2p in the low half, key 2p+1 in the high half
-        const uint32_t lo = (a4[e >> 1] >> (16 * (e & 1))) & 0xffffu;
-        const uint32_t hi = (b4[e >> 1] >> (16 * (e & 1))) & 0xffffu;
-        *reinterpret_cast<uint32_t*>(Vt + (8 * vc + e) * (kBN + kVPad) + p2) = lo | (hi << 16);
+        // dim 8vc + e: key 2p in the low half, key 2p+1 in the high half (one
+        // byte permute: bytes of a4 are selectors 0-3, of b4 4-7)
+        const uint32_t word = __builtin_amdgcn_perm(b4[e >> 1], a4[e >> 1],
+                                                    (e & 1) ? 0x07060302u : 0x05040100u);
+        *reinterpret_cast<uint32_t*>(Vt + (8 * vc + e) * (kBN + kVPad) + p2) = word;
       }
     }
     __syncthreads();
@@ -195,7 +201,11 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const uint16_t* __res
       // Weights are then at most 2^kRescaleSlack; the final 1/l uses the
       // same offset, so the result is unchanged up to rounding.
       constexpr float kRescaleSlack = 8.f;
-      mloc = fmaxf(mloc, __shfl_xor(mloc, 32, kWave));
+      {  // the other lane half's maximum (lanes l and l ^ 32 hold one query)
+        const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mloc),
+                                                         __float_as_uint(mloc), false, false);
+        mloc = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+      }
       const bool grow = !(mloc * scale_log2 <= m_run * scale_log2 + kRescaleSlack);
       if (__ballot(grow)) {
         const float m_new = fmaxf(m_run, mloc);
@@ -266,6 +276,7 @@ extern "C" int32_t llmy_banded_attn_prefill_bf16(const llmy_bf16* q, const llmy_
   if (B == 0 || T == 0) return 0;
   LLMY_REQUIRE(q && k && v && o);
   LLMY_REQUIRE(aligned(q, 16) && aligned(k, 16) && aligned(v, 16) && aligned(o, 8));
+  LLMY_REQUIRE(static_cast<long long>(T) * H * head_dim < (1ll << 31));  // 32-bit row offsets
   const long long nblk = static_cast<long long>((T + kBM - 1) / kBM) * B * H;
   LLMY_REQUIRE(nblk < (1ll << 31));
   const float scale_log2 = scale * 1.4426950408889634f;
