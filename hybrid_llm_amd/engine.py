@@ -384,6 +384,10 @@ class HybridDecoder:
         self.x_log: torch.Tensor | None = None
         # The same for prefill: one [B*T, k] id tensor per MoE application.
         self.route_log_seq: list | None = None
+        # Optional record of the CSA / HCA top-k memory selections (verification
+        # aid): (core layer, positions of the selected summaries, -1 none) per
+        # mixer call, [B, H, k] in decode and [B, T, H, k] in prefill.
+        self.sel_log: list | None = None
 
     def enable_route_log(self, residuals: bool = False) -> None:
         """Record every MoE application's expert ids in ``route_log`` [apps, B, k]
@@ -497,6 +501,14 @@ class HybridDecoder:
                            st["rcount"])
         ops.cmp_memory_decode(q, st["mk"], st["mv"], st["mtag"], self.pos, H, Dh, cs["top_k"],
                               out=loc[:, D:], workspace=b["cws"])
+        if self.sel_log is not None and cs["top_k"] > 0:
+            # the list's slot indices follow its weights in the workspace
+            B_, k_ = self.B, cs["top_k"]
+            nl = B_ * H * k_
+            il = b["cws"][:8 * nl].view(torch.int32)[nl:].view(B_, H * k_).long()
+            tag = torch.gather(st["mtag"], 1, il.clamp_min(0)).view(B_, H, k_)
+            self.sel_log.append((l, torch.where(il.view(B_, H, k_) >= 0, tag - 1,
+                                                torch.full_like(tag, -1)).cpu()))
         ops.linear(loc, w[p + "cmp_wlr"], out=b["cy"], layout=ops.LAYOUT_PACKED)
         ops.linear(b["cy"], w[p + "cmp_wout"], out=b["x"] if out is None else out,
                    epilogue=ops.EPI_RESID_ADD if epilogue is None else epilogue,
@@ -943,8 +955,16 @@ class HybridDecoder:
         means = ops.cmp_pool_prefill(h, B, T, ratio, st["psum"], st["pcnt"])
         kv = (ops.linear(means, w[p + "cmp_wc"], layout=ops.LAYOUT_PACKED) if n else
               torch.empty(0, Kw + D, dtype=torch.bfloat16, device=self.dev))
+        ws = (ops.cmp_workspace(R, H, max(n, 1), cs["top_k"], self.dev)
+              if self.sel_log is not None and cs["top_k"] > 0 else None)
         ops.cmp_memory_prefill(q, kv[:, :Kw], kv[:, Kw:], B, T, ratio, H, Dh, cs["top_k"],
-                               out=loc[:, D:], slots=cfg.cmp_slots)
+                               out=loc[:, D:], slots=cfg.cmp_slots, workspace=ws)
+        if ws is not None:
+            # entry i of a row is the summary at position (i + 1) ratio - 1
+            nl = R * H * cs["top_k"]
+            il = ws[:8 * nl].view(torch.int32)[nl:].view(B, T, H, cs["top_k"]).long()
+            self.sel_log.append((l, torch.where(il >= 0, (il + 1) * ratio - 1,
+                                                torch.full_like(il, -1)).cpu()))
         ops.cmp_memory_fill(kv, B, n, ratio, st["mk"], st["mv"], st["mtag"], st["mcount"])
         if "rk" in st and n:
             kvr = self._router_summary_kv(p, kv[:, Kw:].contiguous())

@@ -63,19 +63,28 @@ def head_scores(q: torch.Tensor, k: torch.Tensor, H: int, Dh: int) -> torch.Tens
     return ((qh @ kh) / math.sqrt(Dh)).float()
 
 
+def topk_keep(s: torch.Tensor, top_k: int) -> torch.Tensor:
+    """[B, H, T, S] mask of each row's top_k entries (stable: ties keep the
+    lower index), -inf entries included when fewer are finite."""
+    k = min(int(top_k), s.shape[-1])
+    order = torch.sort(s, dim=-1, descending=True, stable=True).indices
+    keep = torch.zeros_like(s, dtype=torch.bool)
+    keep.scatter_(-1, order[..., :k], True)
+    return keep
+
+
 def head_mean_probs(scores: torch.Tensor, visible: torch.Tensor,
-                    top_k: int | None = None) -> torch.Tensor:
+                    top_k: int | None = None, keep: torch.Tensor | None = None) -> torch.Tensor:
     """scores [B, H, T, S], visible [B, T, S] -> the heads' mean of each head's
     softmax over its visible entries (``top_k`` None) or over the top_k highest
     of all S entries (invisible ones weigh 0), [B, T, S] fp32.  A row with no
-    visible (selected) entry gives 0."""
+    visible (selected) entry gives 0.  ``keep`` [B, H, T, S] replaces the top-k
+    selection with a given one (a replayed discrete decision)."""
     s = scores.double().masked_fill(~visible[:, None], -math.inf)
-    if top_k is not None:
-        k = min(int(top_k), s.shape[-1])
-        order = torch.sort(s, dim=-1, descending=True, stable=True).indices
-        keep = torch.zeros_like(s, dtype=torch.bool)
-        keep.scatter_(-1, order[..., :k], True)
+    if keep is not None:
         s = s.masked_fill(~keep, -math.inf)
+    elif top_k is not None:
+        s = s.masked_fill(~topk_keep(s, top_k), -math.inf)
     m = s.amax(-1, keepdim=True)
     e = torch.exp(s - torch.where(torch.isfinite(m), m, torch.zeros_like(m)))
     den = e.sum(-1, keepdim=True)
@@ -118,6 +127,14 @@ class CompressedMixer:
         self.window, self.ratio = int(window), int(ratio)
         self.top_k = None if top_k is None else int(top_k)
         self.rnd = act_round or _ident
+        # Discrete-decision forcing (verification aid, like HybridOracle's
+        # forced_routes): a FIFO of [B, H, k] summary positions (-1: none), one
+        # per ``step`` call; the step then uses those summaries instead of its
+        # own top-k and records in sel_gaps, for each (row, head) whose choice
+        # differed, its own k-th best score minus the forced set's lowest.
+        self.forced_sel: list | None = None
+        self.sel_gaps: list[float] = []
+        self.sel_total = 0
 
     def _proj(self, h: torch.Tensor):
         w, rnd = self.w, self.rnd
@@ -201,9 +218,33 @@ class CompressedMixer:
         st["psum"] = torch.where(emitted[:, None], torch.zeros_like(st["psum"]), st["psum"])
         st["pcnt"] = torch.where(emitted, torch.zeros_like(st["pcnt"]), st["pcnt"])
         vis = ((st["mpos"] >= 0) & (st["mpos"] <= pos.long()[:, None]))[:, None]
-        Pm = head_mean_probs(head_scores(q[:, None], st["mk"], H, Dh), vis, self.top_k)
+        sc = head_scores(q[:, None], st["mk"], H, Dh)
+        keep = None
+        if self.top_k is not None and self.forced_sel:
+            keep = self._forced_keep(sc, vis, st["mpos"], self.forced_sel.pop(0))
+        Pm = head_mean_probs(sc, vis, self.top_k, keep=keep)
         remote = (Pm.double() @ st["mv"].double()).float()[:, 0]
         return self._out(local, remote)
+
+    def _forced_keep(self, sc, vis, mpos, forced) -> torch.Tensor:
+        """The keep mask [B, H, 1, S] of forced positions [B, H, k] (summaries
+        whose position is listed), recording the gaps of differing choices."""
+        forced = torch.as_tensor(forced).long()
+        keep = ((mpos[:, None, :, None] == forced[:, :, None, :]) & (forced[:, :, None, :] >= 0)
+                ).any(-1)[:, :, None] & vis[:, None]
+        s = sc.double().masked_fill(~vis[:, None], -math.inf)
+        own = topk_keep(s, self.top_k) & torch.isfinite(s)
+        for b in range(s.shape[0]):
+            for h in range(s.shape[1]):
+                self.sel_total += 1
+                only_own, only_forced = own[b, h] & ~keep[b, h], keep[b, h] & ~own[b, h]
+                if not (only_own.any() or only_forced.any()):
+                    continue
+                if only_own.any() and only_forced.any():
+                    self.sel_gaps.append(float(s[b, h][only_own].max() - s[b, h][only_forced].min()))
+                else:   # the forced set is not a swap of the own one's entries
+                    self.sel_gaps.append(math.inf)
+        return keep
 
     @staticmethod
     def reset_rows(st: dict, rows: torch.Tensor) -> None:

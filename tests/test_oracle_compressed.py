@@ -157,3 +157,45 @@ def test_reset_row_continues_as_fresh_sequence():
         y = m.step(x, st, pos + i)
         yf = m.step(x[1:2], fresh, torch.tensor([i]))
         assert torch.allclose(y[1:2], yf, atol=1e-6), i
+
+
+def test_forced_selection_replay():
+    """Forcing a mixer's top-k memory selection (the replay of the engine's
+    choice): forcing the selection a brute-force sort makes gives the unforced
+    output and records no gap; forcing another set changes the output and
+    records the score gap between the k-th best and the forced set's lowest."""
+    H, Dh, D, W, r, k = 2, 8, 16, 4, 2, 2
+    m = _mixer(H, Dh, D, W, r, k, seed=21)
+    gen = torch.Generator().manual_seed(22)
+    B, steps = 2, 9
+    xs = torch.randn(steps, B, D, generator=gen)
+    st_a, st_b = m.new_state(B, D), m.new_state(B, D)
+    for i in range(steps):
+        pos = torch.full((B,), i)
+        ya = m.step(xs[i], st_a, pos)
+        # the brute-force top-k positions of the memory after this step's emit
+        q = m._proj(xs[i])[0]
+        mpos_next = torch.cat([st_b["mpos"], torch.where(
+            st_b["pcnt"] + 1 >= r, pos, torch.full_like(pos, -1))[:, None]], 1)
+        mk_next = torch.cat([st_b["mk"], m._summaries(
+            (st_b["psum"] + xs[i]) / (st_b["pcnt"] + 1).float()[:, None])[0][:, None]], 1)
+        forced = np.full((B, H, k), -1)
+        for b in range(B):
+            for h in range(H):
+                vis = [(float(q[b, h * Dh:(h + 1) * Dh] @ mk_next[b, j, h * Dh:(h + 1) * Dh]), j)
+                       for j in range(mk_next.shape[1]) if 0 <= mpos_next[b, j] <= i]
+                best = sorted(vis, key=lambda t: (-t[0], t[1]))[:k]
+                for n, (_, j) in enumerate(best):
+                    forced[b, h, n] = int(mpos_next[b, j])
+        m.forced_sel = [forced]
+        yb = m.step(xs[i], st_b, pos)
+        assert torch.allclose(ya, yb, atol=1e-6), i
+    assert m.sel_gaps == [] and m.sel_total == steps * B * H
+    # force the lowest-scoring visible summary instead: a different output, one
+    # positive gap per (row, head) whose choice changed
+    q = m._proj(xs[0])[0]
+    m.forced_sel = [np.zeros((B, H, 1), dtype=np.int64) + r - 1]   # the first summary only
+    y_forced = m.step(xs[0], st_b, torch.full((B,), steps))
+    y_own = m.step(xs[0], st_a, torch.full((B,), steps))
+    assert not torch.allclose(y_forced, y_own)
+    assert len(m.sel_gaps) > 0 and all(g > 0 for g in m.sel_gaps)
