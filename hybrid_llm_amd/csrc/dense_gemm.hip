@@ -1,15 +1,8 @@
-// Tiled bf16 MFMA GEMMs on gfx950: the grouped expert GEMMs of MoE prefill
-// and the dense projections of a sequence prefill.
-//
-// Math of the grouped GEMMs (model/layers/moe.py:72-76, expert.py:14-15), per
-// expert e over its routes in permuted order p = offsets[e] .. offsets[e+1]-1:
-//   act[p, :] = silu(x[t_p] . W_gate[e]^T) * (x[t_p] . W_up[e]^T)   (bf16 out)
-//   y[p, :]   = gate[r_p] * (act[p] . W_down[e]^T)                  (fp32 out)
-// with r_p = sorted_routes[p] and t_p = r_p / k: the same contract, layouts
-// and rounding points as the weight-streaming path of llmy_moe_experts_bf16.
-// The dense mode (llmy_linear_bf16 with many rows) is one "expert" owning
-// all M rows, with an N tail (rows past N re-read row N-1, their columns are
-// not stored) and the linear epilogues.
+// Tiled bf16 MFMA GEMM on gfx950: the dense projections of a sequence
+// prefill (llmy_linear_bf16 with many rows), out[M, N] = x[M, K] . w[N, K]^T
+// with the linear epilogues, and an N tail (rows past N re-read row N-1,
+// their columns are not stored).  The MoE prefill GEMMs are the grouped
+// kernel of moe_grouped.hip.
 //
 // Tiling: a workgroup of 4 wavefronts computes a BM x BN tile of the A rows
 // times the B (weight) rows; wavefront (wm, wn) of the 2 x 2 grid owns a
@@ -20,10 +13,7 @@
 // two per CU, one wavefront of each per SIMD, so one workgroup's barrier and
 // load waits are covered by the other's MFMAs.  The MFMA takes the weight
 // fragment as its first operand, so each lane ends with four consecutive
-// output columns per register group and stores them as one vector.  The
-// gate_up tile's B rows are [gate | up] halves per wavefront column, so every
-// gate accumulator sits in the same lanes as its up partner and SwiGLU is
-// applied in registers.
+// output columns per register group and stores them as one vector.
 //
 // K advances BK (32 or 64) at a time through a ring of NS LDS stages filled
 // by global_load_lds_dwordx4 (global memory straight into LDS) from scalar
@@ -35,36 +25,28 @@
 // the fragment reads of k-step s+1 are in flight during the MFMAs of step s,
 // and the first reads of tile kt+1 during the last MFMAs of tile kt.
 //
-// Work order: work items (expert, n-tile, m-tile) are numbered expert-major,
-// m fastest, and each XCD (block id mod 8) takes a contiguous range of them,
-// so the m-tiles that share a weight tile, and the n-tiles that share an
-// expert's token rows, run back to back in the same XCD's L2.  Dense work is
-// grouped 4 m-tiles x all n-tiles, so the tiles an XCD runs together share
-// few A and B tiles.
+// Work order: work items (n-tile, m-tile) are grouped 4 m-tiles x all
+// n-tiles, m fastest inside a group, and each XCD (block id mod 8) takes a
+// contiguous range of them, so the tiles an XCD runs together share few A
+// and B tiles in its L2.
 #include "common.hpp"
 #include "abi_util.hpp"
 
 namespace llmy {
 
-enum Mode : int { kTileGateUp = 0, kTileDown = 1, kTileDense = 2 };
 // Dense epilogues (values of the linear entry's epilogue argument).
 enum DenseEpi : int { kDenseBf16 = 0, kDenseF32 = 1, kDenseResid = 2, kDenseGated = 3 };
 
 struct TileArgs {
-  const uint16_t* x;       // gate_up: token rows [x_rows, K]; down: act; dense: [M, K]
-  const uint16_t* w;       // weights, row-major [E, N_w, K] or packed
-  void* out;               // act bf16 / y f32 / dense out, row stride ldo
-  const float* gates;      // down: gate per route id
-  const float* aux;        // dense gated residual: out += acc * aux[m * ldo + n]
-  const int32_t* offsets;  // grouped: [E + 1]
-  const int32_t* sorted_routes;
-  long long w_expert_stride;  // elements per expert block of w
-  long long up_offset;        // gate_up: elements from gate row n to up row n (H * K)
-  int K, ldo, E, route_k, rows_total, x_rows;
-  int N;        // dense: output columns (last n-tile may be partial)
-  int n_tiles;  // output column tiles per expert
-  int m_tiles;  // dense: row tiles
-  int group_m;  // dense: m-tiles per work group (0: m fastest over all rows)
+  const uint16_t* x;  // [M, K]
+  const uint16_t* w;  // weights, row-major [N, K] or packed
+  void* out;          // [M, ldo] (bf16 or fp32 by epilogue)
+  const float* aux;   // gated residual: out += acc * aux[m * ldo + n]
+  int K, ldo, M;
+  int N;        // output columns (last n-tile may be partial)
+  int n_tiles;  // output column tiles
+  int m_tiles;  // row tiles
+  int group_m;  // m-tiles per work group (0: m fastest over all rows)
   int packed;
 };
 
@@ -136,7 +118,7 @@ __device__ __forceinline__ f32x16 mfma32(const u32x4& a, const u32x4& b, const f
 
 }  // namespace
 
-template <int MODE, int BM, int BN, int BK, int NS, int EPI, int OCC = 1>
+template <int BM, int BN, int BK, int NS, int EPI, int OCC = 1>
 __global__ __launch_bounds__(kThreads, OCC) void tile_gemm_kernel(TileArgs a) {
   constexpr int WM = BM / 2, WN = BN / 2;  // wavefront sub-tile
   constexpr int FA = WM / 32, FB = WN / 32;  // 32-row / 32-column MFMA blocks per wavefront
@@ -153,81 +135,37 @@ __global__ __launch_bounds__(kThreads, OCC) void tile_gemm_kernel(TileArgs a) {
   constexpr int NF = FA + FB;  // fragment reads per k-step
   static_assert(FA == 2 || FA == 4, "wavefront rows");
   static_assert(FB == 2 || FB == 4, "wavefront columns");
-  static_assert(MODE != kTileGateUp || FB % 2 == 0, "gate/up halves");
   static_assert(BK == 32 || BK == 64, "K tile");
   static_assert(NS >= 2 && DPT * (NS - 2) <= 63, "vmcnt range");
-  __shared__ int s_work[3];  // expert, m0, n-tile (or -1: no work)
+  __shared__ int s_work[3];  // work flag (-1: none), m0, n-tile
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave & 1, wn = wave >> 1;
 
-  // ---- which tile.  Dense: work item w = (n-tile, m-tile), m fastest.
-  // Grouped: wave 0 scans the experts' m-tile counts.
+  // ---- which tile: work item w = (n-tile, m-tile), m fastest.
   const int nblk = gridDim.x;
   const int per_xcd = (nblk + kNumXcd - 1) / kNumXcd;
   const int w_item = (blockIdx.x % kNumXcd) * per_xcd + blockIdx.x / kNumXcd;
-  if (MODE == kTileDense) {
-    if (tid == 0) {
-      const bool ok = w_item < a.m_tiles * a.n_tiles;
-      int mt = w_item % a.m_tiles, nt = w_item / a.m_tiles;
-      if (a.group_m > 0) {
-        // groups of group_m m-tiles x all n-tiles, m fastest inside a group,
-        // so the tiles an XCD runs together share few A and B tiles
-        const int per_group = a.group_m * a.n_tiles;
-        const int grp = w_item / per_group, in = w_item % per_group;
-        const int gm = min(a.group_m, a.m_tiles - grp * a.group_m);
-        mt = grp * a.group_m + in % gm;
-        nt = in / gm;
-      }
-      s_work[0] = ok ? 0 : -1;
-      s_work[1] = ok ? mt * BM : 0;
-      s_work[2] = ok ? nt : 0;
+  if (tid == 0) {
+    const bool ok = w_item < a.m_tiles * a.n_tiles;
+    int mt = w_item % a.m_tiles, nt = w_item / a.m_tiles;
+    if (a.group_m > 0) {
+      // groups of group_m m-tiles x all n-tiles, m fastest inside a group,
+      // so the tiles an XCD runs together share few A and B tiles
+      const int per_group = a.group_m * a.n_tiles;
+      const int grp = w_item / per_group, in = w_item % per_group;
+      const int gm = min(a.group_m, a.m_tiles - grp * a.group_m);
+      mt = grp * a.group_m + in % gm;
+      nt = in / gm;
     }
-  } else if (wave == 0) {
-    int found = -1, m0 = 0, nt = 0;
-    int base = 0;  // m-tiles of the experts before this chunk of 64
-    for (int e0 = 0; e0 < a.E; e0 += kWave) {
-      const int e = e0 + lane;
-      int tiles = 0;
-      if (e < a.E) {
-        const int lo = min(max(a.offsets[e], 0), a.rows_total);
-        const int hi = min(max(a.offsets[e + 1], lo), a.rows_total);
-        tiles = (hi - lo + BM - 1) / BM;
-      }
-      int inc = tiles;  // inclusive scan over the wave
-#pragma unroll
-      for (int off = 1; off < kWave; off <<= 1) {
-        const int o = __shfl_up(inc, off, kWave);
-        if (lane >= off) inc += o;
-      }
-      const int first = (base + inc - tiles) * a.n_tiles;  // first work item of expert e
-      const int last = (base + inc) * a.n_tiles;
-      const unsigned long long hit = __ballot(e < a.E && w_item >= first && w_item < last);
-      if (hit) {
-        const int src = __ffsll(static_cast<long long>(hit)) - 1;
-        const int f = __shfl(first, src, kWave);
-        const int t = __shfl(tiles, src, kWave);
-        found = e0 + src;
-        const int local = w_item - f;
-        nt = local / t;
-        m0 = (local - nt * t) * BM;
-        break;
-      }
-      base += __shfl(inc, kWave - 1, kWave);
-    }
-    if (lane == 0) {
-      s_work[0] = found;
-      s_work[1] = m0;
-      s_work[2] = nt;
-    }
+    s_work[0] = ok ? 0 : -1;
+    s_work[1] = ok ? mt * BM : 0;
+    s_work[2] = ok ? nt : 0;
   }
   __syncthreads();
-  const int e = s_work[0];
-  if (e < 0) return;
+  if (s_work[0] < 0) return;
   const int m0 = s_work[1], ntile = s_work[2];
-  const int row_lo = MODE == kTileDense ? 0 : min(max(a.offsets[e], 0), a.rows_total);
-  const int rows_e =
-      MODE == kTileDense ? a.rows_total : min(max(a.offsets[e + 1], row_lo), a.rows_total) - row_lo;
+  const int rows_e = a.M;
   const int K = a.K;
   const int nk = K / BK;
 
@@ -248,43 +186,22 @@ __global__ __launch_bounds__(kThreads, OCC) void tile_gemm_kernel(TileArgs a) {
 #pragma unroll
   for (int q = 0; q < A_INS; ++q) {
     const int r = RPI * (A_INS * wave + q) + dma_row;  // tile row
-    const int m = min(m0 + r, rows_e - 1);              // past the rows: repeat the last
-    const int p = row_lo + m;
-    long long src;
-    if (MODE == kTileGateUp) {
-      src = min(max(a.sorted_routes[p], 0), a.rows_total - 1) / a.route_k;
-      src = min(src, static_cast<long long>(a.x_rows - 1));
-    } else {
-      src = p;
-    }
-    a_off[q] = static_cast<uint32_t>((src * K + 8 * DMA_CH(r)) * 2);
+    const long long m = min(m0 + r, rows_e - 1);        // past the rows: repeat the last
+    a_off[q] = static_cast<uint32_t>((m * K + 8 * DMA_CH(r)) * 2);
   }
   const bool packed = a.packed != 0;
   uint32_t b_off[B_INS];
 #pragma unroll
   for (int q = 0; q < B_INS; ++q) {
     const int r = RPI * (B_INS * wave + q) + dma_row;  // tile row
-    long long off = 0;
-    int n;
-    if (MODE == kTileGateUp) {
-      // wavefront column c = r / WN holds [gate cols | up cols] of output
-      // columns (BN/2) ntile + (WN/2) c + 0 .. WN/2 - 1
-      const int c = r / WN, rr = r % WN;
-      n = (BN / 2) * ntile + (WN / 2) * c + rr % (WN / 2);
-      if (rr >= WN / 2) off = a.up_offset;
-    } else if (MODE == kTileDown) {
-      n = BN * ntile + r;
-    } else {
-      n = min(BN * ntile + r, a.N - 1);  // N tail: repeat the last row
-    }
+    const int n = min(BN * ntile + r, a.N - 1);  // N tail: repeat the last row
     const int ch = DMA_CH(r);
     b_off[q] = static_cast<uint32_t>(
-        (off + (packed ? packed_at(n, 8 * ch, K) : static_cast<long long>(n) * K + 8 * ch)) * 2);
+        (packed ? packed_at(n, 8 * ch, K) : static_cast<long long>(n) * K + 8 * ch) * 2);
   }
 #undef DMA_CH
   const char* a_base = reinterpret_cast<const char*>(a.x);
-  const char* b_base =
-      reinterpret_cast<const char*>(a.w + static_cast<long long>(e) * a.w_expert_stride);
+  const char* b_base = reinterpret_cast<const char*>(a.w);
   // The wavefront index as a scalar, so LDS destinations (M0) are scalar arithmetic.
   const int wv = __builtin_amdgcn_readfirstlane(wave);
 
@@ -437,36 +354,8 @@ __global__ __launch_bounds__(kThreads, OCC) void tile_gemm_kernel(TileArgs a) {
   for (int i = 0; i < FA; ++i) {
     const int m = m0 + WM * wm + 32 * i + (lane & 31);
     if (m >= rows_e) continue;
-    const long long p = row_lo + m;
-    if (MODE == kTileGateUp) {
-      uint16_t* act = static_cast<uint16_t*>(a.out) + p * a.ldo;
-#pragma unroll
-      for (int j = 0; j < FB / 2; ++j)
-#pragma unroll
-        for (int g4 = 0; g4 < 4; ++g4) {
-          const int c = (BN / 2) * ntile + (WN / 2) * wn + 32 * j + 8 * g4 + 4 * (lane >> 5);
-          float v[4];
-#pragma unroll
-          for (int t = 0; t < 4; ++t) {
-            const float g = acc[i][j][4 * g4 + t], u = acc[i][j + FB / 2][4 * g4 + t];
-            v[t] = siluf_(g) * u;
-          }
-          *reinterpret_cast<uint2*>(act + c) = make_uint2(pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3]));
-        }
-    } else if (MODE == kTileDown) {
-      const int route = min(max(a.sorted_routes[p], 0), a.rows_total - 1);
-      const float gs = a.gates[route];
-      float* y = static_cast<float*>(a.out) + p * a.ldo;
-#pragma unroll
-      for (int j = 0; j < FB; ++j)
-#pragma unroll
-        for (int g4 = 0; g4 < 4; ++g4) {
-          const int c = BN * ntile + WN * wn + 32 * j + 8 * g4 + 4 * (lane >> 5);
-          *reinterpret_cast<float4*>(y + c) =
-              make_float4(acc[i][j][4 * g4] * gs, acc[i][j][4 * g4 + 1] * gs,
-                          acc[i][j][4 * g4 + 2] * gs, acc[i][j][4 * g4 + 3] * gs);
-        }
-    } else {
+    const long long p = m;
+    {
       // Residual epilogues load a column block's residual (and gate) groups
       // before its first store: a store and a later load of another group
       // cannot be proved apart, so interleaving them would serialise one
@@ -512,59 +401,12 @@ __global__ __launch_bounds__(kThreads, OCC) void tile_gemm_kernel(TileArgs a) {
   }
 }
 
-template <int MODE, int BM, int BN, int BK, int NS, int EPI, int OCC = 1>
+template <int BM, int BN, int BK, int NS, int EPI, int OCC = 1>
 int32_t launch_tiles(const TileArgs& g, long long items, hipStream_t s) {
   const unsigned grid = static_cast<unsigned>((items + kNumXcd - 1) / kNumXcd * kNumXcd);
-  hipLaunchKernelGGL((tile_gemm_kernel<MODE, BM, BN, BK, NS, EPI, OCC>), dim3(grid), dim3(kThreads),
+  hipLaunchKernelGGL((tile_gemm_kernel<BM, BN, BK, NS, EPI, OCC>), dim3(grid), dim3(kThreads),
                      0, s, g);
   return launch_status();
-}
-
-// Launch both grouped GEMMs; returns the launch status.  Shapes were validated
-// by the caller: D % 256 == 0, H % 256 == 0, rows_total = T * k >= 1.
-int32_t moe_gemm_prefill(const uint16_t* x, const int32_t* offsets, const int32_t* sorted_routes,
-                         const float* gates, const uint16_t* w_gate_up, const uint16_t* w_down,
-                         uint16_t* act, float* y, int T, int D, int H, int E, int k, bool packed,
-                         hipStream_t s) {
-  constexpr int BM = 128;
-  const int rows_total = T * k;
-  // operand blocks addressed with 32-bit byte offsets
-  constexpr long long kMaxBytes = 1ll << 31;
-  if (2ll * T * D >= kMaxBytes || 2ll * rows_total * H >= kMaxBytes || 4ll * H * D >= kMaxBytes)
-    return static_cast<int32_t>(hipErrorInvalidValue);
-  const long long max_mtiles = (rows_total + BM - 1) / BM + E;  // >= sum_e ceil(n_e / BM)
-  TileArgs g{};
-  g.x = x;
-  g.w = w_gate_up;
-  g.out = act;
-  g.offsets = offsets;
-  g.sorted_routes = sorted_routes;
-  g.w_expert_stride = 2ll * H * D;
-  g.up_offset = static_cast<long long>(H) * D;
-  g.K = D;
-  g.ldo = H;
-  g.E = E;
-  g.route_k = k;
-  g.rows_total = rows_total;
-  g.x_rows = T;
-  g.n_tiles = H / 128;  // BN = 256 B rows -> 128 output columns
-  g.packed = packed;
-  // Two workgroups per CU (one wavefront of each per SIMD): one's barrier and
-  // load waits are covered by the other's MFMAs.  gate_up: 3 stages of K 32.
-  int32_t st = launch_tiles<kTileGateUp, BM, 256, 32, 3, 0, 2>(g, max_mtiles * g.n_tiles, s);
-  if (st != 0) return st;
-  TileArgs d = g;
-  d.x = act;
-  d.w = w_down;
-  d.out = y;
-  d.gates = gates;
-  d.w_expert_stride = static_cast<long long>(D) * H;
-  d.up_offset = 0;
-  d.K = H;
-  d.ldo = D;
-  d.x_rows = rows_total;
-  d.n_tiles = D / 128;
-  return launch_tiles<kTileDown, BM, 128, 64, 2, 0, 2>(d, max_mtiles * d.n_tiles, s);
 }
 
 int32_t dense_narrow_ws(const uint16_t* x, const uint16_t* w, void* out, const float* aux, int M,
@@ -585,10 +427,7 @@ int32_t dense_gemm_mfma(const uint16_t* x, const uint16_t* w, void* out, const f
   g.aux = aux;
   g.K = K;
   g.ldo = N;
-  g.E = 1;
-  g.route_k = 1;
-  g.rows_total = M;
-  g.x_rows = M;
+  g.M = M;
   g.N = N;
   g.packed = packed;
   // 256 x 256 tiles (one workgroup per CU) when there is one per CU, else
@@ -614,10 +453,10 @@ int32_t dense_gemm_mfma(const uint16_t* x, const uint16_t* w, void* out, const f
     int32_t st = 0;
 #define LLMY_DENSE_T(T_, OCC_, ARGS_, ITEMS_)                                                      \
   switch (epi) {                                                                                   \
-    case kDenseBf16: st = launch_tiles<kTileDense, T_, T_, 64, 2, kDenseBf16, OCC_>(ARGS_, ITEMS_, s); break; \
-    case kDenseF32: st = launch_tiles<kTileDense, T_, T_, 64, 2, kDenseF32, OCC_>(ARGS_, ITEMS_, s); break;   \
-    case kDenseResid: st = launch_tiles<kTileDense, T_, T_, 64, 2, kDenseResid, OCC_>(ARGS_, ITEMS_, s); break; \
-    default: st = launch_tiles<kTileDense, T_, T_, 64, 2, kDenseGated, OCC_>(ARGS_, ITEMS_, s); break;        \
+    case kDenseBf16: st = launch_tiles<T_, T_, 64, 2, kDenseBf16, OCC_>(ARGS_, ITEMS_, s); break; \
+    case kDenseF32: st = launch_tiles<T_, T_, 64, 2, kDenseF32, OCC_>(ARGS_, ITEMS_, s); break;   \
+    case kDenseResid: st = launch_tiles<T_, T_, 64, 2, kDenseResid, OCC_>(ARGS_, ITEMS_, s); break; \
+    default: st = launch_tiles<T_, T_, 64, 2, kDenseGated, OCC_>(ARGS_, ITEMS_, s); break;        \
   }
     LLMY_DENSE_T(256, 1, t, main_items)
     if (st != 0) return st;
@@ -638,10 +477,10 @@ int32_t dense_gemm_mfma(const uint16_t* x, const uint16_t* w, void* out, const f
   if (items >= (1ll << 31) - kNumXcd) return static_cast<int32_t>(hipErrorInvalidValue);
 #define LLMY_DENSE(T_, OCC_)                                                                 \
   switch (epi) {                                                                             \
-    case kDenseBf16: return launch_tiles<kTileDense, T_, T_, 64, 2, kDenseBf16, OCC_>(g, items, s); \
-    case kDenseF32: return launch_tiles<kTileDense, T_, T_, 64, 2, kDenseF32, OCC_>(g, items, s);   \
-    case kDenseResid: return launch_tiles<kTileDense, T_, T_, 64, 2, kDenseResid, OCC_>(g, items, s); \
-    default: return launch_tiles<kTileDense, T_, T_, 64, 2, kDenseGated, OCC_>(g, items, s);        \
+    case kDenseBf16: return launch_tiles<T_, T_, 64, 2, kDenseBf16, OCC_>(g, items, s); \
+    case kDenseF32: return launch_tiles<T_, T_, 64, 2, kDenseF32, OCC_>(g, items, s);   \
+    case kDenseResid: return launch_tiles<T_, T_, 64, 2, kDenseResid, OCC_>(g, items, s); \
+    default: return launch_tiles<T_, T_, 64, 2, kDenseGated, OCC_>(g, items, s);        \
   }
   if (wide) LLMY_DENSE(256, 1)
   LLMY_DENSE(128, 2)

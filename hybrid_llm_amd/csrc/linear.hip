@@ -612,16 +612,12 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restric
   }
 }
 
-// Tiled MFMA grouped GEMMs for MoE prefill (moe_gemm.hip).
-int32_t moe_gemm_prefill(const uint16_t* x, const int32_t* offsets, const int32_t* sorted_routes,
-                         const float* gates, const uint16_t* w_gate_up, const uint16_t* w_down,
-                         uint16_t* act, float* y, int T, int D, int H, int E, int k, bool packed,
-                         hipStream_t s);
+// Grouped MFMA GEMMs for MoE prefill (moe_grouped.hip).
 int32_t moe_grouped_prefill(const uint16_t* x, const int32_t* offsets, const int32_t* sorted_routes,
                             const float* gates, const uint16_t* w_gate_up, const uint16_t* w_down,
                             uint16_t* act, float* y, int T, int D, int H, int E, int k, bool packed,
                             hipStream_t s);
-// The same tiles as a dense GEMM with the epilogues above (moe_gemm.hip).
+// Tiled MFMA dense GEMM with the epilogues above (dense_gemm.hip).
 int32_t dense_gemm_mfma(const uint16_t* x, const uint16_t* w, void* out, const float* aux,
                         int M, int N, int K, int epi, bool packed, hipStream_t s);
 
@@ -732,13 +728,8 @@ extern "C" int32_t llmy_moe_experts_bf16(const llmy_bf16* x, const int32_t* offs
     return launch_ws<kMoeDown, kMoeDirect, 1, 1, 4>(b, E, packed, s);
   }
   // Prefill: grouped MFMA GEMMs (moe_grouped.hip).
-#ifdef LLMY_OLD_GROUPED
-  return moe_gemm_prefill(x, offsets, sorted_routes, gates, w_gate_up, w_down, act, y, T, D, H,
-                          E, k, packed, s);
-#else
   return moe_grouped_prefill(x, offsets, sorted_routes, gates, w_gate_up, w_down, act, y, T, D,
                              H, E, k, packed, s);
-#endif
 }
 
 extern "C" int32_t llmy_moe_combine(const float* y, const int32_t* route_pos, void* out,
