@@ -48,10 +48,15 @@
 // two register sets):
 //   reads of half 1; MFMAs of half 0 (read during the previous step); wait
 //   for half 1 and for step g+1's DMA; barrier (stage g is free, stage g+1
-//   complete); DMA of step g+1+P into stage g; reads of half 0 of step g+1;
-//   MFMAs of half 1, which cover those reads; wait for them (no fragment
-//   read is in flight across a loop edge or an epilogue); at an item's last
-//   step, its epilogue.
+//   complete); reads of half 0 of step g+1; the first MFMA of half 1, then
+//   the DMA of step g+1+P into stage g (its issue overlaps that MFMA), then
+//   the other MFMAs of half 1, which cover the reads; wait for them (no
+//   fragment read is in flight across a loop edge or an epilogue); at an
+//   item's last step, its epilogue.
+//
+// Set-up: the first 64 experts' route ranges are loaded once per workgroup
+// and held one per lane, so finding an item needs no memory access, and the
+// route loads of a batch's items are issued together.
 #include <algorithm>
 #include <type_traits>
 
@@ -132,13 +137,26 @@ __device__ __forceinline__ void expert_rows(const GroupedArgs& a, int e, int& lo
   n = min(max(a.offsets[e + 1], lo), a.rows_total) - lo;
 }
 
+// Row range of expert e0 + lane (e0 a multiple of 64); empty past E.  The
+// kernel loads the first 64 experts' ranges once (lo0, n0) and reuses them.
+__device__ __forceinline__ void lane_rows(const GroupedArgs& a, int e0, int lo0, int n0, int& lo,
+                                          int& n) {
+  if (e0 == 0) {
+    lo = lo0;
+    n = n0;
+    return;
+  }
+  const int e = e0 + (threadIdx.x & 63);
+  lo = n = 0;
+  if (e < a.E) expert_rows(a, e, lo, n);
+}
+
 // Number of work items (a wavefront-wide sum; every lane gets it).
-__device__ int count_items(const GroupedArgs& a) {
+__device__ int count_items(const GroupedArgs& a, int lo0, int n0) {
   int total = 0;
   for (int e0 = 0; e0 < a.E; e0 += kWave) {
-    const int e = e0 + (threadIdx.x & 63);
-    int lo = 0, n = 0;
-    if (e < a.E) expert_rows(a, e, lo, n);
+    int lo, n;
+    lane_rows(a, e0, lo0, n0, lo, n);
     int items = (n + kGChunk - 1) / kGChunk * a.n_slabs;
 #pragma unroll
     for (int off = 1; off < kWave; off <<= 1) items += __shfl_xor(items, off, kWave);
@@ -149,15 +167,16 @@ __device__ int count_items(const GroupedArgs& a) {
 
 // Work item `it` (< the item count): its expert, first row, row count and slab.
 // Wavefront-wide; every lane gets the same values.
-__device__ void find_item(const GroupedArgs& a, int it, int& e, int& row0, int& rows, int& slab) {
+__device__ void find_item(const GroupedArgs& a, int it, int lo0, int n0, int& e, int& row0,
+                          int& rows, int& slab) {
   const int lane = threadIdx.x & 63;
   e = -1;
   row0 = rows = slab = 0;
   int base = 0;
   for (int e0 = 0; e0 < a.E; e0 += kWave) {
     const int ee = e0 + lane;
-    int lo = 0, n = 0;
-    if (ee < a.E) expert_rows(a, ee, lo, n);
+    int lo, n;
+    lane_rows(a, e0, lo0, n0, lo, n);
     const int nc = (n + kGChunk - 1) / kGChunk;
     const int items = nc * a.n_slabs;
     int inc = items;
@@ -207,7 +226,11 @@ __global__ __launch_bounds__(kGThreads, 1) void grouped_gemm_kernel(GroupedArgs 
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
-  const int wm = wave & 1, wn = wave >> 1;
+  // The waves of a workgroup go to the SIMDs in turn (wave w to SIMD w % 4),
+  // so wm = w / 4 pairs a wm = 0 and a wm = 1 wave on every SIMD: each SIMD
+  // then runs the same number of active token blocks when a chunk's block
+  // count is odd.
+  const int wm = wave >> 2, wn = wave & 3;
   const int lr = lane & 31, lh = lane >> 5;
   const int K = a.K;
   const int nk = K >> 5;  // 32-wide K steps
@@ -215,7 +238,9 @@ __global__ __launch_bounds__(kGThreads, 1) void grouped_gemm_kernel(GroupedArgs 
 
   // this workgroup's items: XCD x = blockIdx % 8 owns items
   // [x * per_xcd, (x + 1) * per_xcd); its workgroups take them in turn
-  const int n_items = __builtin_amdgcn_readfirstlane(count_items(a));
+  int lo0 = 0, n0 = 0;  // expert `lane`'s routes (experts 0 .. 63)
+  if (lane < a.E) expert_rows(a, lane, lo0, n0);
+  const int n_items = __builtin_amdgcn_readfirstlane(count_items(a, lo0, n0));
   const int per_xcd = (n_items + kGXcd - 1) / kGXcd;
   const int grid_xcd = gridDim.x / kGXcd;  // workgroups per XCD (the host launches a multiple of 8)
   const int xcd = blockIdx.x % kGXcd, slot = blockIdx.x / kGXcd;
@@ -242,33 +267,34 @@ __global__ __launch_bounds__(kGThreads, 1) void grouped_gemm_kernel(GroupedArgs 
     for (int b = 0; b < kGBatch; ++b) {
       const int it = first + b * grid_xcd;
       int e = -1, row0 = 0, rows = 1, slab = 0;
-      if (it < x_end) find_item(a, it, e, row0, rows, slab);
+      if (it < x_end) find_item(a, it, lo0, n0, e, row0, rows, slab);
       if (e >= 0) nb = b + 1;
       else { e = 0; row0 = 0; rows = 1; slab = 0; }  // unused slot: any in-bounds item
       d_e[b] = __builtin_amdgcn_readfirstlane(e);
       d_row0[b] = __builtin_amdgcn_readfirstlane(row0);
       d_rows[b] = __builtin_amdgcn_readfirstlane(rows);
       d_slab[b] = __builtin_amdgcn_readfirstlane(slab);
+    }
+    // The items' route loads are issued together, without branches (rows
+    // clamped into the item), so their latencies overlap.
+#pragma unroll
+    for (int b = 0; b < kGBatch; ++b) {
       // token rows: instruction q fills stage rows 16 (2 w + q) .. +15; lane l
       // writes bytes 16 l of that 1 KiB (row l / 4, slot l % 4), holding the
       // row's chunk (l % 4) ^ (l / 16); groups past the chunk read row 0
 #pragma unroll
       for (int q = 0; q < 2; ++q) {
         const int g = 2 * wave + q;
-        long long src = 0;
-        int ch = 0;
-        if (16 * g < d_rows[b]) {
-          const int r = 16 * g + (lane >> 2);
-          const int p = d_row0[b] + min(r, d_rows[b] - 1);
-          if (MODE == 0) {
-            src = min(max(a.sorted_routes[p], 0), a.rows_total - 1) / a.route_k;
-            src = min(src, static_cast<long long>(a.x_rows - 1));
-          } else {
-            src = p;
-          }
-          ch = (lane & 3) ^ (lane >> 4);
+        const bool live = 16 * g < d_rows[b];
+        const int r = 16 * g + (lane >> 2);
+        const int p = d_row0[b] + min(r, d_rows[b] - 1);
+        long long src = p;
+        if (MODE == 0) {
+          src = min(max(a.sorted_routes[p], 0), a.rows_total - 1) / a.route_k;
+          src = min(src, static_cast<long long>(a.x_rows - 1));
         }
-        d_aoff[b][q] = static_cast<uint32_t>((src * K + 8 * ch) * 2);
+        const int ch = (lane & 3) ^ (lane >> 4);
+        d_aoff[b][q] = live ? static_cast<uint32_t>((src * K + 8 * ch) * 2) : 0u;
       }
       // weight fragments: stage fragment f = 2 w + q holds rows n0 .. n0 + 15
       // of the slab (f = 4 c + j for wavefront column c): gate_up j < 2 gate
@@ -277,26 +303,26 @@ __global__ __launch_bounds__(kGThreads, 1) void grouped_gemm_kernel(GroupedArgs 
 #pragma unroll
       for (int q = 0; q < 2; ++q) {
         const int f = 2 * wave + q, c = f >> 2, j = f & 3;
-        int n0;
-        if (MODE == 0) n0 = (j >= 2 ? a.up_rows : 0) + 128 * d_slab[b] + 32 * c + 16 * (j & 1);
-        else n0 = 256 * d_slab[b] + 64 * c + 16 * j;
+        int nr;
+        if (MODE == 0) nr = (j >= 2 ? a.up_rows : 0) + 128 * d_slab[b] + 32 * c + 16 * (j & 1);
+        else nr = 256 * d_slab[b] + 64 * c + 16 * j;
         if (PACKED)
           d_boff[b][q] =
-              static_cast<uint32_t>((static_cast<long long>(n0 >> 4) * nk) * 1024 + lane * 16);
+              static_cast<uint32_t>((static_cast<long long>(nr >> 4) * nk) * 1024 + lane * 16);
         else
           d_boff[b][q] = static_cast<uint32_t>(
-              ((static_cast<long long>(n0 + (lane & 15)) * K) + 8 * (lane >> 4)) * 2);
+              ((static_cast<long long>(nr + (lane & 15)) * K) + 8 * (lane >> 4)) * 2);
       }
-      // down: the gate of each of this lane's four output rows
+      // down: the gate of each of this lane's four output rows (0 past the chunk)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         d_gate[b][i] = 0.f;
         if (MODE == 1) {
           const int m = 32 * (2 * i + wm) + lr;
-          if (m < d_rows[b]) {
-            const int route = min(max(a.sorted_routes[d_row0[b] + m], 0), a.rows_total - 1);
-            d_gate[b][i] = a.gates[route];
-          }
+          const int route =
+              min(max(a.sorted_routes[d_row0[b] + min(m, d_rows[b] - 1)], 0), a.rows_total - 1);
+          const float gv = a.gates[route];
+          d_gate[b][i] = m < d_rows[b] ? gv : 0.f;
         }
       }
     }
@@ -386,12 +412,19 @@ __global__ __launch_bounds__(kGThreads, 1) void grouped_gemm_kernel(GroupedArgs 
         asm volatile("" ::: "memory");
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
-        G_ISSUE_NEXT(off);
+        // the next step's half-0 reads, then the DMA of step g+1+P into the
+        // freed stage, issued behind the first MFMA so its issue overlaps it
+        const uint32_t freed = off;
         off = off + STAGE == NS * STAGE ? 0 : off + STAGE;
         G_READ(h0, off, 0);
         G_FENCE();
+        if (NA > 0) acc[0][0] = mfma32(h1[4], h1[0], acc[0][0]);
+        G_FENCE();
+        G_ISSUE_NEXT(freed);
+        G_FENCE();
+        if (NA > 0) acc[0][1] = mfma32(h1[5], h1[0], acc[0][1]);
 #pragma unroll
-        for (int i = 0; i < NA; ++i) {
+        for (int i = 1; i < NA; ++i) {
           acc[i][0] = mfma32(h1[4], h1[i], acc[i][0]);
           acc[i][1] = mfma32(h1[5], h1[i], acc[i][1]);
         }
