@@ -66,46 +66,57 @@ __device__ __forceinline__ void dense_row(const float* srow, int n, int off, int
 // wave's 64-entry LDS staging.
 //
 // n <= 2048: the scores' order keys (order_key: a larger value has a larger
-// key) stay in registers, NPL per lane; the k-th largest key is built bit by
-// bit from the top (keep a bit when at least k keys are >= the prefix with
-// it set: 32 counting rounds), then every key above it and the lowest-index
-// ones equal to it are selected and compacted with ballots.  Larger rows take
-// k rounds of a wave argmax over the LDS row (which it consumes).
-template <int NPL>
-__device__ __forceinline__ void topk_regs(const float* srow, int n, int k, int lane, float* wout,
-                                          int32_t* iout, float* sel_s, int* sel_i) {
-  uint32_t key[NPL];
-#pragma unroll
-  for (int i = 0; i < NPL; ++i) {
-    const int j = i * kWave + lane;
-    key[i] = j < n ? order_key(srow[j]) : 0u;   // 0: below every real key
-  }
-  // counts over the wave are popcounts of compare masks (no cross-lane data
-  // movement): the threshold search runs in the scalar unit.  It stops as
-  // soon as exactly k keys are at or above the candidate prefix: those are
-  // the top k, with no tie at the boundary, and thr - 1 then marks them as
-  // the keys above the threshold (the same set and order as a full search).
+// key) stay in registers, NPL per lane.  With NPL >= 4 a prefilter first
+// finds L, the k-th largest of the 64 lanes' maximum keys (k lanes hold a key
+// >= L, so every key of the top k is >= L); the keys >= L (about 45 of 1024
+// for unordered scores) are compacted, in index order, one per lane, and the
+// selection below runs on them alone.  Past 64 survivors, and for NPL < 4, it
+// runs on all keys: the k-th largest key is built bit by bit from the top
+// (keep a bit when at least k keys are >= the prefix with it set: up to 32
+// counting rounds), then every key above it and the lowest-index ones equal
+// to it are selected and compacted with ballots.  Larger rows take k rounds
+// of a wave argmax over the LDS row (which it consumes).
+//
+// Threshold search over the keys a lane holds (NK per lane; counts are
+// popcounts of compare masks, so it runs in the scalar unit).  It stops as
+// soon as exactly k keys are at or above the candidate prefix: those are the
+// top k with no tie at the boundary, and the result then marks them as the
+// keys above the threshold (the same set and order as a full search).  0:
+// fewer than k keys are nonzero.
+template <int NK>
+__device__ __forceinline__ uint32_t topk_threshold(const uint32_t* key, int k) {
   uint32_t thr = 0;
   for (int bit = 31; bit >= 0; --bit) {
     const uint32_t cand = thr | (1u << bit);
     int c = 0;
 #pragma unroll
-    for (int i = 0; i < NPL; ++i) c += __popcll(__ballot(key[i] >= cand));
+    for (int i = 0; i < NK; ++i) c += __popcll(__ballot(key[i] >= cand));
     if (c >= k) thr = cand;
     if (c == k) {
       thr = cand - 1u;
       break;
     }
   }
+  return thr;
+}
+
+// Select the top k of the keys (NK per lane, index idx[i]; scores val[i]) by
+// threshold thr: every key above it and, of the keys equal to it, the lowest
+// indices (keys are visited in index order: i, then lane).  Selected pairs go
+// to sel_s / sel_i in index order; returns their count.
+template <int NK>
+__device__ __forceinline__ int topk_compact(const uint32_t* key, const float* val, const int* idx,
+                                            uint32_t thr, int k, int lane, float* sel_s,
+                                            int* sel_i) {
   int gt = 0;
 #pragma unroll
-  for (int i = 0; i < NPL; ++i) gt += __popcll(__ballot(key[i] > thr));
+  for (int i = 0; i < NK; ++i) gt += __popcll(__ballot(key[i] > thr));
   // thr == 0: fewer than k candidates, all of them are taken
   const int need = thr > 0 ? k - gt : 0;
   const uint64_t below = (1ull << lane) - 1ull;
   int taken = 0, eq_seen = 0;
 #pragma unroll
-  for (int i = 0; i < NPL; ++i) {
+  for (int i = 0; i < NK; ++i) {
     const bool eq = thr > 0 && key[i] == thr;
     const uint64_t meq = __ballot(eq);
     const bool sel = key[i] > thr || (eq && eq_seen + __popcll(meq & below) < need);
@@ -113,11 +124,18 @@ __device__ __forceinline__ void topk_regs(const float* srow, int n, int k, int l
     const uint64_t ms = __ballot(sel);
     if (sel) {
       const int at = taken + __popcll(ms & below);
-      sel_s[at] = srow[i * kWave + lane];
-      sel_i[at] = i * kWave + lane;
+      sel_s[at] = val[i];
+      sel_i[at] = idx[i];
     }
     taken += __popcll(ms);
   }
+  return taken;
+}
+
+// Softmax over the taken selections in sel_s (index order, sel_i their
+// indices) to wout / iout; entries past `taken` or at -inf weigh 0 with index -1.
+__device__ __forceinline__ void topk_emit(int taken, int k, int lane, const float* sel_s,
+                                          const int* sel_i, float* wout, int32_t* iout) {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -129,6 +147,62 @@ __device__ __forceinline__ void topk_regs(const float* srow, int n, int k, int l
     wout[lane] = sum > 0.f ? e / sum : 0.f;
     iout[lane] = v != -INFINITY ? sel_i[lane] : -1;
   }
+}
+
+template <int NPL>
+__device__ __forceinline__ void topk_regs(const float* srow, int n, int k, int lane, float* wout,
+                                          int32_t* iout, float* sel_s, int* sel_i) {
+  uint32_t key[NPL];
+#pragma unroll
+  for (int i = 0; i < NPL; ++i) {
+    const int j = i * kWave + lane;
+    key[i] = j < n ? order_key(srow[j]) : 0u;   // 0: below every real key
+  }
+  const uint64_t below = (1ull << lane) - 1ull;
+  int taken = -1;
+  if (NPL >= 4) {
+    uint32_t lm = key[0];
+#pragma unroll
+    for (int i = 1; i < NPL; ++i) lm = max(lm, key[i]);
+    // at least k lane maxima are >= lbound (0: fewer than k lanes hold a key)
+    const uint32_t lbound = topk_threshold<1>(&lm, k);
+    int nsv = 0;
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) nsv += __popcll(__ballot(key[i] >= lbound));
+    if (lbound > 0u && nsv <= kWave) {
+      // survivors, in index order, to sel_i; then one per lane
+      int at0 = 0;
+#pragma unroll
+      for (int i = 0; i < NPL; ++i) {
+        const bool sv = key[i] >= lbound;
+        const uint64_t m = __ballot(sv);
+        if (sv) sel_i[at0 + __popcll(m & below)] = i * kWave + lane;
+        at0 += __popcll(m);
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      const int idx = lane < nsv ? sel_i[lane] : 0;
+      const float val = lane < nsv ? srow[idx] : -INFINITY;
+      const uint32_t ky = lane < nsv ? order_key(val) : 0u;
+      const uint32_t thr = topk_threshold<1>(&ky, k);
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      taken = topk_compact<1>(&ky, &val, &idx, thr, k, lane, sel_s, sel_i);
+    }
+  }
+  if (taken < 0) {
+    float val[NPL];
+    int idx[NPL];
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) {
+      idx[i] = i * kWave + lane;
+      val[i] = idx[i] < n ? srow[idx[i]] : -INFINITY;
+    }
+    taken = topk_compact<NPL>(key, val, idx, topk_threshold<NPL>(key, k), k, lane, sel_s, sel_i);
+  }
+  topk_emit(taken, k, lane, sel_s, sel_i, wout, iout);
 }
 
 __device__ __forceinline__ void topk_row(float* srow, int n, int k, int lane, float* wout,

@@ -73,6 +73,8 @@ MEMORY = [  # B, T, ratio, H, Dh, Dv, top_k
     (1, 256, 8, 1, 1024, 1024, 4),
     (2, 40, 4, 2, 64, 64, 0),
     (2, 3, 4, 2, 64, 64, 2),          # no summary yet
+    (1, 2048, 4, 8, 64, 128, 32),     # 512 summaries: the lane-maximum prefilter
+    (1, 4096, 4, 4, 64, 64, 32),      # 1024 summaries, the bench's selection size
 ]
 
 
@@ -99,6 +101,29 @@ def test_memory_prefill(B, T, ratio, H, Dh, Dv, top_k):
     out = ops().cmp_memory_prefill(q.cuda(), d[:, :Kw], d[:, Kw:], B, T, ratio, H, Dh, top_k)
     torch.cuda.synchronize()
     _close(out, _mem_ref(q, kv[:, :Kw], kv[:, Kw:], B, T, ratio, H, Dh, top_k))
+
+
+@pytest.mark.parametrize("T,ratio,top_k,levels", [(2048, 4, 32, 3), (2048, 4, 16, 9), (1024, 2, 5, 2)])
+def test_memory_prefill_topk_ties(T, ratio, top_k, levels):
+    """Scores drawn from a few levels, so many summaries tie at the top-k
+    boundary (and the prefilter's survivors can pass 64, the all-key path):
+    the selection must keep the lowest indices among equal scores, which the
+    output shows, since every summary's value row differs."""
+    print(f"memory prefill ties T={T} r={ratio} k={top_k} levels={levels}", flush=True)
+    g = torch.Generator().manual_seed(T + top_k + levels)
+    B, H, Dh, Dv = 1, 2, 64, 64
+    Kw, n = H * Dh, T // ratio
+    # q . k takes (levels) distinct values per head: k rows are one of a few
+    # fixed directions, q rows one shared direction per head
+    base = torch.randn(levels, Kw, generator=g)
+    pick = torch.randint(0, levels, (B * n,), generator=g)
+    mk = (base[pick] * 0.5).bfloat16()
+    q = (torch.randn(1, Kw, generator=g).expand(B * T, Kw) * 0.5).bfloat16().contiguous()
+    mv = _bf(B * n, Dv, gen=g)
+    kv = torch.cat([mk, mv], 1).cuda()
+    out = ops().cmp_memory_prefill(q.cuda(), kv[:, :Kw], kv[:, Kw:], B, T, ratio, H, Dh, top_k)
+    torch.cuda.synchronize()
+    _close(out, _mem_ref(q, mk, mv, B, T, ratio, H, Dh, top_k))
 
 
 @pytest.mark.parametrize("T,ratio,C,top_k", [(100, 4, 4, 3), (100, 4, 4, 0), (300, 32, 3, 0)])
