@@ -296,7 +296,7 @@ def n_sets(bytes_per_set: float, minimum: int = 3) -> int:
     return max(minimum, int(MALL_BYTES // max(bytes_per_set, 1)) + 1)
 
 
-KERNEL_ROWS = ("hbm_copy", "moe_decode_experts", "lm_head", "gdn_decode_step", "gdn_decode_step_c4",
+KERNEL_ROWS = ("hbm_copy", "mfma_gemm", "moe_decode_experts", "lm_head", "gdn_decode_step", "gdn_decode_step_c4",
                "sample_argmax", "sample_top_p", "moe_prefill_layer", "moe_prefill_experts",
                "dense_prefill_gemm", "attn_prefill", "gdn_prefill", "csa_decode", "hca_decode",
                "csa_prefill", "hca_prefill")
@@ -348,6 +348,19 @@ def kernel_table(cfg, B, gen, iters, only=None):
         dst = torch.empty(n, device="cuda")
         t = event_time(lambda i: dst.copy_(srcs[i % 2]), max(10, iters // 5))
         hbm("hbm_copy", t, 2 * COPY_BYTES, "torch device copy of 512 MiB (read + write)")
+
+    def mfma_gemm():
+        # the practical ceiling of a bf16 MFMA stream on this box: a library
+        # GEMM (torch.matmul -> hipBLASLt) of random bf16 operands, 8192^3
+        # (random operands draw more power than constant ones; the clock, and
+        # with it the matrix rate, drops to match)
+        n = 8192
+        a = torch.randn(n, n, device="cuda", generator=gen).bfloat16()
+        bt = torch.randn(n, n, device="cuda", generator=gen).bfloat16()
+        c = torch.empty(n, n, device="cuda", dtype=torch.bfloat16)
+        t = event_time(lambda i: torch.matmul(a, bt, out=c), max(10, iters // 10))
+        mfma("mfma_gemm", t, 2 * n ** 3, "hipBLASLt bf16 GEMM (torch.matmul), random operands, "
+             "M=N=K=8192: the practical MFMA ceiling")
 
     def moe_decode_experts():
         # one C5 MoE application at decode: packed expert weights (302 MB per
@@ -574,7 +587,7 @@ def kernel_table(cfg, B, gen, iters, only=None):
              f"{kind.upper()} prefill branches: B={Bq}, T={Tq}, heads={H} x {Dh}, "
              f"d_model={D}, window={W}, ratio={ratio}, top_k={top_k or 'dense'}")
 
-    fns = {"hbm_copy": hbm_copy, "moe_decode_experts": moe_decode_experts, "lm_head": lm_head,
+    fns = {"hbm_copy": hbm_copy, "mfma_gemm": mfma_gemm, "moe_decode_experts": moe_decode_experts, "lm_head": lm_head,
            "gdn_decode_step": gdn_decode_step,
            "gdn_decode_step_c4": gdn_decode_step_c4, "sample_argmax": sample_argmax,
            "sample_top_p": sample_top_p, "moe_prefill_layer": moe_prefill_layer,
