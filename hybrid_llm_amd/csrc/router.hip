@@ -299,20 +299,27 @@ __device__ void permute_block(Get get, int n, int E, int32_t* __restrict__ count
 
   int32_t* running = cnt + wave * E;
   if (E <= kWave) {
-    // Lane e keeps expert e's next position for this wave; per chunk, one
-    // ballot per expert ranks the routes of that expert (ascending r) and one
-    // shuffle hands each route its expert's base.  Same placement as below.
+    // Lane e keeps expert e's next position for this wave.  Per chunk, one
+    // ballot per bit of the expert id (nb = ceil(log2 E) of them) gives every
+    // lane the mask of the lanes holding its expert (the AND over the bits of
+    // the matching ballot or its complement), which ranks the route among its
+    // expert's routes (ascending r); lane e forms its own expert's mask from
+    // the same ballots for the count.  One shuffle hands each route its
+    // expert's base.  Same placement as below.
+    int nb = 0;
+    while ((1 << nb) < E) ++nb;
     int next = lane < E ? running[lane] : 0;
     auto place = [&](int c, int e) {
       const int r = c * 64 + lane;
       if (r >= n || e < 0 || e >= E) e = -1;
-      uint64_t mine = 0ull;
-      int add = 0;
-      for (int ee = 0; ee < E; ++ee) {
-        const uint64_t m = __ballot(e == ee);
-        if (e == ee) mine = m;
-        if (lane == ee) add = __popcll(m);
+      const uint64_t valid = __ballot(e >= 0);
+      uint64_t mine = valid, lane_set = valid;
+      for (int k = 0; k < nb; ++k) {
+        const uint64_t bk = __ballot(e >= 0 && ((e >> k) & 1));
+        mine &= ((e >> k) & 1) ? bk : ~bk;
+        lane_set &= ((lane >> k) & 1) ? bk : ~bk;
       }
+      const int add = lane < E ? __popcll(lane_set) : 0;
       const int base = __shfl(next, e < 0 ? 0 : e, kWave);
       if (e >= 0) {
         const int pos = base + __popcll(mine & ((1ull << lane) - 1ull));
@@ -333,6 +340,12 @@ __device__ void permute_block(Get get, int n, int E, int32_t* __restrict__ count
     for (int c = c0 + kHeld; c < c1; ++c) place(c, c * 64 + lane < n ? get(c * 64 + lane) : -1);
     return;
   }
+  // More experts than lanes: the same per-bit masks, with the wave's next
+  // positions in LDS (running[e]); the first route of each expert in the
+  // chunk advances it.
+  int nb = 0;
+  while ((1 << nb) < E) ++nb;
+  const uint64_t below = (1ull << lane) - 1ull;
   for (int c = c0; c < c1; ++c) {
     const int r = c * 64 + lane;
     int e = -1;
@@ -346,22 +359,25 @@ __device__ void permute_block(Get get, int n, int E, int32_t* __restrict__ count
       }
       if (e < 0 || e >= E) e = -1;
     }
-    uint64_t pending = __ballot(e >= 0);
-    while (pending) {
-      const int leader = __builtin_ctzll(pending);
-      const int le = __shfl(e, leader, kWave);
-      const uint64_t same = __ballot(e == le);
-      if (e == le) {
-        const uint64_t below = same & ((1ull << lane) - 1ull);
-        const int pos = running[le] + __popcll(below);
-        sorted_routes[pos] = r;
-        route_pos[r] = pos;
-      }
-      __builtin_amdgcn_wave_barrier();
-      if (lane == leader) running[le] += __popcll(same);
-      __builtin_amdgcn_wave_barrier();
-      pending &= ~same;
+    uint64_t mine = __ballot(e >= 0);
+    for (int k = 0; k < nb; ++k) {
+      const uint64_t bk = __ballot(e >= 0 && ((e >> k) & 1));
+      mine &= ((e >> k) & 1) ? bk : ~bk;
     }
+    const int rank = __popcll(mine & below);
+    const int base = e >= 0 ? running[e] : 0;
+    if (e >= 0) {
+      const int pos = base + rank;
+      sorted_routes[pos] = r;
+      route_pos[r] = pos;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (e >= 0 && rank == 0) running[e] = base + __popcll(mine);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   }
 }
 

@@ -82,6 +82,23 @@ def test_permute_exact(n, E):
     assert np.array_equal(got["route_pos"].cpu().numpy(), ref["route_pos"])
 
 
+@pytest.mark.parametrize("n,E", [(8192, 24), (3000, 64), (500, 5), (20000, 256)])
+def test_permute_skips_out_of_range_ids(n, E):
+    """Ids outside [0, E) are not placed: the valid routes are counted and
+    sorted stably by expert exactly as if the others were absent."""
+    g = torch.Generator().manual_seed(7 * n + E)
+    ids = torch.randint(-2, E + 2, (n,), generator=g, dtype=torch.int32)
+    got = ops().moe_permute(ids.cuda(), E)
+    ok = ((ids >= 0) & (ids < E)).numpy()
+    valid = np.nonzero(ok)[0]
+    ref = moe_permute(ids.numpy()[valid], E)
+    nv = valid.size
+    assert np.array_equal(got["counts"].cpu().numpy(), ref["counts"])
+    assert np.array_equal(got["offsets"].cpu().numpy(), ref["offsets"])
+    assert np.array_equal(got["sorted_routes"].cpu().numpy()[:nv], valid[ref["sorted_routes"]])
+    assert np.array_equal(got["route_pos"].cpu().numpy()[valid], ref["route_pos"])
+
+
 def test_permute_skewed_all_one_expert():
     ids = torch.full((8192,), 5, dtype=torch.int32)
     got = ops().moe_permute(ids.cuda(), 24)
