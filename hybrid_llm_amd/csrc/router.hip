@@ -211,15 +211,6 @@ __global__ __launch_bounds__(256) void router_topk_from_logits_kernel(
 
 }
 
-// Stable counting sort of n = T*k expert ids in [0, E) with one 1024-thread
-// workgroup.  Wave w owns a contiguous run of 64-route chunks, so walking the
-// waves in order and the chunks in order visits routes in ascending r.
-//   pass 1: per-wave expert histograms (LDS integer atomics: order-free);
-//   scan:   expert offsets and per-wave bases;
-//   pass 2: each chunk ranks its lanes per expert with ballots and places
-//           route r at offsets[e] + (routes of e before r).
-// Routes with an id outside [0, E) are not placed (callers pass router
-// output, which is always in range).
 constexpr int kPermuteWaves = 16;
 
 // Stable counting sort of n expert ids (read through `get(r)`) by one
@@ -228,8 +219,11 @@ constexpr int kPermuteWaves = 16;
 // ascending r.
 //   pass 1: per-wave expert histograms (LDS integer atomics: order-free);
 //   scan:   expert offsets and per-wave bases;
-//   pass 2: each chunk ranks its lanes per expert with ballots and places
-//           route r at offsets[e] + (routes of e before r).
+//   pass 2: each chunk ranks its lanes per expert with one ballot per bit of
+//           the expert id (a lane's same-expert mask is the AND of the
+//           matching ballots or their complements: ceil(log2 E) ballots in
+//           place of one per expert) and places route r at offsets[e] +
+//           (routes of e before r).
 // `cnt` is LDS scratch of kPermuteWaves * E + E + 1 ints.  Ids outside
 // [0, E) are not placed.
 template <typename Get>
