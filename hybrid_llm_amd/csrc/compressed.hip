@@ -809,6 +809,171 @@ __global__ __launch_bounds__(64 * NW) void cmp_apply_kernel(
   }
 }
 
+// Sequence apply on MFMA (prefill): workgroup = (row b, 32-query block,
+// 256-channel block), 8 wavefronts.  The block's head-summed weights P [32
+// queries][block slots] are accumulated in LDS (fp32, heads in order, as
+// above), then O^T = V^T P^T runs as v_mfma_f32_32x32x16_bf16 over 32-slot
+// chunks: each chunk's value rows are staged transposed (V^T [channel][slot],
+// slot pairs packed per dword, the attention prefill's staging), wave w takes
+// the block's channels 32 w .. 32 w + 31, and each P fragment is split into
+// (hi, lo) bf16 in registers (so the weights keep fp32 accuracy; the values
+// are exact in bf16).  out = acc / H.  Dv % 32 == 0 and at most
+// kApplyMfmaSlots block slots (the fp32 P rows fill the LDS).
+constexpr int kApplyMfmaSlots = 1088;
+constexpr int kApplyVtPitch = 40;   // bf16 per staged V^T row (32 slots + 8 pad)
+
+__global__ __launch_bounds__(512) void cmp_apply_mfma_kernel(
+    const float* __restrict__ wl, const int32_t* __restrict__ il, int Kmax, int H, int T,
+    int band_W, int nslots, const uint16_t* __restrict__ v, int64_t v_ld, int rows_per_b,
+    uint16_t* __restrict__ out, int64_t out_ld, int Dv) {
+  extern __shared__ float pmf[];
+  const int nsb = band_W > 0 ? nslots + 31 : nslots;   // block slots
+  const int NP = (nsb + 31) & ~31;
+  const int RS = NP + 4;                                // fp32 per P row (16-byte pad)
+  uint16_t* vt = reinterpret_cast<uint16_t*>(pmf + 32 * RS);   // [256][kApplyVtPitch]
+  const int ndb = (Dv + 255) / 256;
+  const int nqb = (T + 31) / 32;
+  const int blk = blockIdx.x / ndb;
+  const int db = blockIdx.x - blk * ndb;
+  const int b = blk / nqb;
+  const int t0 = (blk - b * nqb) * 32;
+  const int nq = min(32, T - t0);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int c0 = db * 256;
+  const int base = band_W > 0 ? t0 - band_W + 1 : 0;    // key of block slot 0
+
+  // ---- P: the 32 queries' weights summed over the heads (head order)
+  for (int i = tid; i < 32 * RS; i += 512) pmf[i] = 0.f;
+  __syncthreads();
+  const int64_t lb0 = (static_cast<int64_t>(b) * T + t0) * H * Kmax;
+  if (il && H <= kApplyMaxH && nq * Kmax <= 1024) {
+    // every head's (slot, weight) entries requested at once (two per thread
+    // per head), then added head by head: a head's slots are distinct, so
+    // each pass is race-free and every slot sums its heads in head order
+    float wr[kApplyMaxH][2];
+    int ir[kApplyMaxH][2], pr[2];
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const int e = tid + 512 * r;
+      pr[r] = e < nq * Kmax ? (e / Kmax) * RS : -1;
+    }
+#pragma unroll
+    for (int hh = 0; hh < kApplyMaxH; ++hh)
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        const int e = tid + 512 * r;
+        const bool ok = hh < H && pr[r] >= 0;
+        const int qq = e / Kmax, j = e - qq * Kmax;
+        const int64_t o = lb0 + (static_cast<int64_t>(qq) * H + hh) * Kmax + j;
+        wr[hh][r] = ok ? wl[o] : 0.f;
+        ir[hh][r] = ok ? il[o] : -1;
+      }
+#pragma unroll
+    for (int hh = 0; hh < kApplyMaxH; ++hh) {
+      if (hh >= H) break;  // uniform
+#pragma unroll
+      for (int r = 0; r < 2; ++r)
+        if (ir[hh][r] >= 0 && ir[hh][r] < nslots) pmf[pr[r] + ir[hh][r]] += wr[hh][r];
+      __syncthreads();
+    }
+  } else if (il) {
+    for (int hh = 0; hh < H; ++hh) {
+      for (int e = tid; e < nq * Kmax; e += 512) {
+        const int qq = e / Kmax, j = e - qq * Kmax;
+        const int64_t o = lb0 + (static_cast<int64_t>(qq) * H + hh) * Kmax + j;
+        const int idx = il[o];
+        if (idx >= 0 && idx < nslots) pmf[qq * RS + idx] += wl[o];
+      }
+      __syncthreads();
+    }
+  } else {
+    for (int e = tid; e < nq * nslots; e += 512) {
+      const int qq = e / nslots, j = e - qq * nslots;
+      const int64_t o = lb0 + static_cast<int64_t>(qq) * H * Kmax + j;
+      float acc = 0.f;
+      for (int hh = 0; hh < H; ++hh) acc += wl[o + static_cast<int64_t>(hh) * Kmax];
+      pmf[qq * RS + j + (band_W > 0 ? qq : 0)] = acc;
+    }
+    __syncthreads();
+  }
+
+  // ---- V^T staging: thread (slot pair p, channel group g) fetches the two
+  // rows' 8 channels (rows clamped into the sequence; their weights are 0)
+  const int sp = tid & 15, cg = tid >> 4;   // slots 2 sp, 2 sp + 1; channels 8 cg ..
+  const int cch = c0 + 8 * cg;
+  const bool ch_ok = cch < Dv;
+  const uint16_t* vrow0 = v + static_cast<int64_t>(b) * rows_per_b * v_ld + (ch_ok ? cch : 0);
+  uint4 va, vb;
+  auto fetch = [&](int s0) {
+    const int k0 = min(max(base + s0 + 2 * sp, 0), rows_per_b - 1);
+    const int k1 = min(max(base + s0 + 2 * sp + 1, 0), rows_per_b - 1);
+    va = ch_ok ? *reinterpret_cast<const uint4*>(vrow0 + static_cast<int64_t>(k0) * v_ld)
+               : uint4{0u, 0u, 0u, 0u};
+    vb = ch_ok ? *reinterpret_cast<const uint4*>(vrow0 + static_cast<int64_t>(k1) * v_ld)
+               : uint4{0u, 0u, 0u, 0u};
+  };
+  auto stage = [&]() {
+    const uint32_t a4[4] = {va.x, va.y, va.z, va.w};
+    const uint32_t b4[4] = {vb.x, vb.y, vb.z, vb.w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      // channel 8 cg + e: slot 2 sp in the low half, 2 sp + 1 in the high half
+      const uint32_t word = __builtin_amdgcn_perm(b4[e >> 1], a4[e >> 1],
+                                                  (e & 1) ? 0x07060302u : 0x05040100u);
+      *reinterpret_cast<uint32_t*>(vt + (8 * cg + e) * kApplyVtPitch + 2 * sp) = word;
+    }
+  };
+
+  // ---- O^T = V^T P^T: wave w owns channels c0 + 32 w .. + 31 (all 32 queries)
+  const bool w_ok = c0 + 32 * wave < Dv;
+  const int col = lane & 31, hf = lane >> 5;
+  f32x16c acc;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+  fetch(0);
+  for (int s0 = 0; s0 < NP; s0 += 32) {
+    __syncthreads();   // the previous chunk's V^T reads are done
+    stage();
+    __syncthreads();
+    if (s0 + 32 < NP) fetch(s0 + 32);
+    if (w_ok) {
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const uint4 af = *reinterpret_cast<const uint4*>(
+            vt + (32 * wave + col) * kApplyVtPitch + 16 * ks + 8 * hf);
+        const float* pr = pmf + col * RS + s0 + 16 * ks + 8 * hf;
+        const float4 p0 = *reinterpret_cast<const float4*>(pr);
+        const float4 p1 = *reinterpret_cast<const float4*>(pr + 4);
+        const float pv[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+        uint16_t hi[8], lo[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          hi[i] = f2bf(pv[i]);
+          lo[i] = f2bf(pv[i] - bf2f(hi[i]));
+        }
+        auto pk = [](uint16_t x, uint16_t y) {
+          return static_cast<uint32_t>(x) | (static_cast<uint32_t>(y) << 16);
+        };
+        const uint4 bh = uint4{pk(hi[0], hi[1]), pk(hi[2], hi[3]), pk(hi[4], hi[5]),
+                               pk(hi[6], hi[7])};
+        const uint4 bl = uint4{pk(lo[0], lo[1]), pk(lo[2], lo[3]), pk(lo[4], lo[5]),
+                               pk(lo[6], lo[7])};
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(af), as_bf16x8(bh), acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(af), as_bf16x8(bl), acc, 0, 0, 0);
+      }
+    }
+  }
+  // ---- lane holds query col, channels 32 w + 8 g4 + 4 hf .. +3 in registers 4 g4 ..
+  if (!w_ok || col >= nq) return;
+  const float invH = 1.0f / static_cast<float>(H);
+  uint16_t* orow = out + (static_cast<int64_t>(b) * T + t0 + col) * out_ld + c0 + 32 * wave;
+#pragma unroll
+  for (int g4 = 0; g4 < 4; ++g4)
+    *reinterpret_cast<uint2*>(orow + 8 * g4 + 4 * hf) =
+        make_uint2(pack_bf2(acc[4 * g4] * invH, acc[4 * g4 + 1] * invH),
+                   pack_bf2(acc[4 * g4 + 2] * invH, acc[4 * g4 + 3] * invH));
+}
+
 // ---------------------------------------------------------------- compressor
 // Prefill (fresh sequences, compressed_attention.py:105-123): workgroup (b, i),
 // i < n: mean of block i (bf16); i == n: the tail's sum (fp32) and count.
@@ -992,6 +1157,19 @@ int32_t apply_launch(const float* wl, const int32_t* il, int Kmax, int H, int B,
                      const int32_t* qpos, int band_W, int nslots, const uint16_t* v, int64_t v_ld,
                      int rows_per_b, int wrap, uint16_t* out, int64_t out_ld, int Dv,
                      hipStream_t s) {
+  // sequences on MFMA where the block's weights fit the LDS
+  if (!qpos && T >= 8 && Dv % 32 == 0 && wrap == 0 &&
+      (band_W > 0 ? nslots + 31 : nslots) <= kApplyMfmaSlots) {
+    const int nsb = band_W > 0 ? nslots + 31 : nslots;
+    const int NP = (nsb + 31) & ~31;
+    const size_t lds = static_cast<size_t>(32) * (NP + 4) * 4 + 256 * kApplyVtPitch * 2;
+    const int64_t nblk = static_cast<int64_t>(B) * ((T + 31) / 32) * ((Dv + 255) / 256);
+    if (nblk >= (1ll << 31)) return static_cast<int32_t>(hipErrorInvalidValue);
+    hipLaunchKernelGGL(cmp_apply_mfma_kernel, dim3(static_cast<unsigned>(nblk)), dim3(512), lds,
+                       s, wl, il, Kmax, H, T, band_W, nslots, v, v_ld, rows_per_b, out, out_ld,
+                       Dv);
+    return launch_status();
+  }
   // blocks of 8 queries for sequences (a value row serves the whole block),
   // single queries for decode
   const int QB = T >= 8 ? 8 : 1;
