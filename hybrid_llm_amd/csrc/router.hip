@@ -403,6 +403,8 @@ __global__ __launch_bounds__(1024) void moe_permute_kernel(
 // (one fma per element), and the completed row is written back to x.  Every
 // wave reads x[t] before the workgroup barrier; wave 0 writes it after it.
 constexpr int kMaxParts = 8;
+// Rows from which a partial-free call (a prefill) takes the 32-token block kernel.
+constexpr int kRouteBlockRows = 256;
 // NPM: compile-time bound on nparts (0, 4 or 8) that sizes the slice registers.
 template <int NCH, int NPM>
 __global__ __launch_bounds__(256) void moe_route_norm_kernel(
@@ -537,6 +539,121 @@ __global__ __launch_bounds__(256) void moe_route_norm_kernel(
   topk_softmax_store(mine, E, k, lane, idx_out + t * k, gates_out + t * k);
 }
 
+// The same pre-MoE norms and router for a sequence (nparts == 0), 32 tokens
+// per workgroup, 8 wavefronts: wave w normalises tokens 4 w .. 4 w + 3 with
+// moe_route_norm_kernel's arithmetic (so h2 is the same bits) and keeps the
+// router input rows in LDS (fp32, rows padded to D + 4); the logits [32
+// tokens x E <= 32 experts] then run as fp32 MFMAs (v_mfma_f32_32x32x2_f32:
+// exact fp32 products, fp32 sums), wave w over the D/8-wide slice w of the
+// row, and the eight partial tiles are added in wave order.  W_r is read as
+// 16-byte pieces along d straight from global memory (L2-resident, 96 KiB at
+// C5), one piece feeding two MFMAs.  Then wave w takes the top-k of its four
+// tokens.
+template <int NCH>
+__global__ __launch_bounds__(512) void moe_route_norm_blk_kernel(
+    const float* __restrict__ x, const float* __restrict__ ffn_w,
+    const float* __restrict__ router_w, const float* __restrict__ w_router,
+    uint16_t* __restrict__ h2, int32_t* __restrict__ idx_out, float* __restrict__ gates_out,
+    int T, int E, int k, float eps) {
+  constexpr int D = NCH * 256;
+  constexpr int RS = D + 4;          // fp32 per LDS row
+  constexpr int KW = D / 8;          // d per wave in the logits
+  extern __shared__ float rs[];      // [32][RS] router input; then [8][32][32] partials
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int t0 = blockIdx.x * 32;
+  float4 fw[NCH], rw[NCH];
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    const int d = 4 * lane + 256 * c;
+    fw[c] = *reinterpret_cast<const float4*>(ffn_w + d);
+    rw[c] = *reinterpret_cast<const float4*>(router_w + d);
+  }
+  // ---- norms of tokens 4 wave .. 4 wave + 3 (rows past T: zero router input)
+  float4 v[4][NCH];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int t = min(t0 + 4 * wave + j, T - 1);
+#pragma unroll
+    for (int c = 0; c < NCH; ++c)
+      v[j][c] = *reinterpret_cast<const float4*>(x + static_cast<long long>(t) * D + 4 * lane +
+                                                 256 * c);
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int tl = 4 * wave + j;
+    const bool ok = t0 + tl < T;
+    float ss = 0.f;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c)
+      ss += v[j][c].x * v[j][c].x + v[j][c].y * v[j][c].y + v[j][c].z * v[j][c].z +
+            v[j][c].w * v[j][c].w;
+    const float r1 = rsqrtf(wave_sum(ss) / static_cast<float>(D) + eps);
+    float ss2 = 0.f;
+    uint16_t* hrow = h2 + static_cast<long long>(t0 + tl) * D;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      const int d = 4 * lane + 256 * c;
+      const uint32_t lo = pack_bf2(v[j][c].x * r1 * fw[c].x, v[j][c].y * r1 * fw[c].y);
+      const uint32_t hi = pack_bf2(v[j][c].z * r1 * fw[c].z, v[j][c].w * r1 * fw[c].w);
+      if (ok) *reinterpret_cast<uint2*>(hrow + d) = make_uint2(lo, hi);
+      v[j][c].x = __uint_as_float(lo << 16);
+      v[j][c].y = __uint_as_float(lo & 0xffff0000u);
+      v[j][c].z = __uint_as_float(hi << 16);
+      v[j][c].w = __uint_as_float(hi & 0xffff0000u);
+      ss2 += v[j][c].x * v[j][c].x + v[j][c].y * v[j][c].y + v[j][c].z * v[j][c].z +
+             v[j][c].w * v[j][c].w;
+    }
+    const float r2 = rsqrtf(wave_sum(ss2) / static_cast<float>(D) + eps);
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      const float4 r = ok ? make_float4((v[j][c].x * r2) * rw[c].x, (v[j][c].y * r2) * rw[c].y,
+                                        (v[j][c].z * r2) * rw[c].z, (v[j][c].w * r2) * rw[c].w)
+                          : make_float4(0.f, 0.f, 0.f, 0.f);
+      *reinterpret_cast<float4*>(rs + tl * RS + 4 * lane + 256 * c) = r;
+    }
+  }
+  __syncthreads();
+  // ---- logits: D[token][expert] over d in [KW wave, KW wave + KW); lane l
+  // feeds token / expert l % 32 at d offset l / 32 of each 2-wide step
+  const int col = lane & 31, hf = lane >> 5;
+  const bool e_ok = col < E;
+  const float* wrow = w_router + static_cast<long long>(e_ok ? col : 0) * D + KW * wave;
+  const float* arow = rs + col * RS + KW * wave;
+  typedef float f32x16r __attribute__((ext_vector_type(16)));
+  f32x16r acc;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+#pragma unroll 4
+  for (int u = 0; u < KW / 4; ++u) {
+    const float4 a4 = *reinterpret_cast<const float4*>(arow + 4 * u);
+    float4 b4 = *reinterpret_cast<const float4*>(wrow + 4 * u);
+    if (!e_ok) b4 = make_float4(0.f, 0.f, 0.f, 0.f);
+    // step 2u: d = 4u + hf; step 2u + 1: d = 4u + 2 + hf
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(hf ? a4.y : a4.x, hf ? b4.y : b4.x, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(hf ? a4.w : a4.z, hf ? b4.w : b4.z, acc, 0, 0, 0);
+  }
+  __syncthreads();   // every read of the router rows is done
+  float* part = rs + wave * 1024;   // [token][expert] partial of this wave
+#pragma unroll
+  for (int r = 0; r < 16; ++r) part[((r & 3) + 8 * (r >> 2) + 4 * hf) * 32 + col] = acc[r];
+  __syncthreads();
+  // ---- wave order sum, then the top-k of tokens 4 wave .. 4 wave + 3
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int tl = 4 * wave + j;
+    if (t0 + tl >= T) break;   // uniform
+    float mine[4] = {0.f, 0.f, 0.f, 0.f};
+    if (lane < 32) {
+      float a = rs[tl * 32 + lane];
+#pragma unroll
+      for (int w = 1; w < 8; ++w) a += rs[w * 1024 + tl * 32 + lane];
+      mine[0] = a;
+    }
+    topk_softmax_store(mine, E, k, lane, idx_out + static_cast<size_t>(t0 + tl) * k,
+                       gates_out + static_cast<size_t>(t0 + tl) * k);
+  }
+}
+
 }  // namespace llmy
 
 using namespace llmy;
@@ -620,10 +737,21 @@ extern "C" int32_t llmy_moe_route_decode(float* x, const float* parts, int32_t n
   } else {                             \
     LLMY_ROUTE_NP(NCH, 8);             \
   }
-    switch (D) {
-      case 256: LLMY_ROUTE(1); break;
-      case 512: LLMY_ROUTE(2); break;
-      default: LLMY_ROUTE(4); break;
+    if (nparts == 0 && T >= kRouteBlockRows && E <= 32) {
+      // a sequence: 32 tokens per workgroup, logits on fp32 MFMA
+      const dim3 grid((T + 31) / 32);
+      const size_t lds = static_cast<size_t>(32) * (D + 4) * sizeof(float);
+      switch (D) {
+        case 256: hipLaunchKernelGGL((moe_route_norm_blk_kernel<1>), grid, dim3(512), lds, s, x, ffn_w, router_w, w_router, h2, idx, gates, T, E, k, eps); break;
+        case 512: hipLaunchKernelGGL((moe_route_norm_blk_kernel<2>), grid, dim3(512), lds, s, x, ffn_w, router_w, w_router, h2, idx, gates, T, E, k, eps); break;
+        default: hipLaunchKernelGGL((moe_route_norm_blk_kernel<4>), grid, dim3(512), lds, s, x, ffn_w, router_w, w_router, h2, idx, gates, T, E, k, eps); break;
+      }
+    } else {
+      switch (D) {
+        case 256: LLMY_ROUTE(1); break;
+        case 512: LLMY_ROUTE(2); break;
+        default: LLMY_ROUTE(4); break;
+      }
     }
 #undef LLMY_ROUTE
 #undef LLMY_ROUTE_NP

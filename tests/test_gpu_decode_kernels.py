@@ -301,7 +301,10 @@ def test_rmsnorm_embed_conv():
 
 
 # ---------------------------------------------------------------- fused decode kernels
-@pytest.mark.parametrize("T,D,E,k", [(64, 1024, 24, 2), (1, 256, 8, 2), (200, 512, 40, 4)])
+@pytest.mark.parametrize("T,D,E,k", [(64, 1024, 24, 2), (1, 256, 8, 2), (200, 512, 40, 4),
+                                     # sequences: the 32-token block kernel (fp32 MFMA logits)
+                                     (4096, 1024, 24, 2), (300, 256, 8, 2), (512, 512, 32, 4),
+                                     (260, 512, 40, 2)])
 def test_moe_route_decode_equals_unfused(T, D, E, k):
     g = torch.Generator().manual_seed(T + D)
     x = (torch.randn(T, D, generator=g) * 2).cuda()
