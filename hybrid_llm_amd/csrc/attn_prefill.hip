@@ -18,6 +18,17 @@
 //   * K/V tiles of 64 keys are staged once per workgroup in LDS and shared by
 //     the 4 waves; the band is walked tile by tile and a wave skips 32-key
 //     sub-tiles that lie wholly outside its queries' windows;
+//   * tiles arrive by global_load_lds_dwordx4 (global memory straight into
+//     LDS, no register holds them) into two stages: the next tile's DMA runs
+//     while the current one is consumed, one barrier per tile.  K and V rows
+//     are kept row-major with their 16-byte chunks XOR-swizzled by row (K by
+//     row & 7, V by 2 (row & 3)), which keeps the 8-lane K fragment reads and
+//     the 16-lane transposing V reads free of bank conflicts; a DMA lane
+//     fetches the chunk that its fixed LDS slot holds under the swizzle;
+//   * the V^T fragments come from the row-major V by ds_read_b64_tr_b16: in
+//     each 16-lane group, lane 4a + e receives element e of the 8 bytes that
+//     lanes a, a + 4, a + 8 and a + 12 address, so lanes addressing 4
+//     consecutive keys at 4 dims each hand every lane one dim of 4 keys;
 //   * blockIdx.x enumerates (query block, b*H + h) with (b, h) fastest, so the
 //     consecutive query blocks of one head (which share 3/4 of their K/V
 //     window) are B*H apart in launch order and, with B*H a multiple of 8,
@@ -33,8 +44,44 @@ typedef float f32x16v __attribute__((ext_vector_type(16)));
 
 constexpr int kBM = 128;    // queries per workgroup
 constexpr int kBN = 64;     // keys per staged tile
-constexpr int kKPad = 8;    // bf16 pad per staged K row (16 bytes)
-constexpr int kVPad = 8;    // bf16 pad per staged V^T row
+
+typedef __attribute__((address_space(3))) void lds_void;
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ void dma16(const void* src, void* lds_dst) {
+  __builtin_amdgcn_global_load_lds(src, (lds_void*)lds_dst, 16, 0, 0);
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const lds_void*)p));
+}
+
+// LDS reads as inline asm: with a DMA into the other stage in flight, the
+// compiler would make every LDS read wait for it.  Their results are valid
+// after lds_settle.
+__device__ __forceinline__ u32x4 lds_b128(uint32_t addr) {
+  u32x4 v;
+  asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(addr) : "memory");
+  return v;
+}
+
+__device__ __forceinline__ u32x2 lds_tr16(uint32_t addr) {
+  u32x2 v;
+  asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(v) : "v"(addr) : "memory");
+  return v;
+}
+
+// Wait for every LDS read of this wave and tie the registers they filled to
+// the wait, so no use is scheduled above it.
+__device__ __forceinline__ void lds_settle4(u32x4* f) {
+  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(f[0]), "+v"(f[1]), "+v"(f[2]), "+v"(f[3])::"memory");
+}
+
+__device__ __forceinline__ void lds_settle_v(u32x2* f) {
+  asm volatile("s_waitcnt lgkmcnt(0)"
+               : "+v"(f[0]), "+v"(f[1]), "+v"(f[2]), "+v"(f[3]), "+v"(f[4]), "+v"(f[5]),
+                 "+v"(f[6]), "+v"(f[7])::"memory");
+}
 
 __device__ __forceinline__ uint4 pack8_bf16(const float* v) {
   return uint4{pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3]), pack_bf2(v[4], v[5]),
@@ -50,8 +97,10 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const uint16_t* __res
   static_assert(HD == 64 || HD == 128, "head dim");
   constexpr int ND = HD / 32;   // 32-dim output tiles
   constexpr int NS = HD / 16;   // 16-dim slices of the score MFMA
-  __shared__ __align__(16) uint16_t Ks[kBN * (HD + kKPad)];
-  __shared__ __align__(16) uint16_t Vt[HD * (kBN + kVPad)];
+  constexpr int TILE = kBN * HD;  // bf16 elements of one staged K or V tile
+  constexpr int RB = 2 * HD;      // bytes per staged row
+  // two stages, each the K tile then the V tile
+  __shared__ __align__(16) uint16_t smem[2 * 2 * TILE];
 
   const int BH = B * H;
   const int bh = blockIdx.x % BH;
@@ -89,76 +138,64 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const uint16_t* __res
   const int k_hi = min(T - 1, q0 + kBM - 1);
   const int t_lo = k_lo / kBN;
   const int t_hi = k_hi / kBN;
-  // Software pipeline: the next tile's K/V chunks are fetched into registers
-  // while the current tile is being consumed from LDS.
-  constexpr int CH = HD / 8;                     // 16-byte chunks per row
-  constexpr int NCHK = (kBN * CH + 255) / 256;   // chunks per thread per tile
-  uint4 kreg[NCHK], vreg[NCHK];
-  // K is fetched row-major (8 lanes per 128-byte row, 16-byte LDS stores).
-  // V is fetched as key pairs: entry f = (pair f % 32, chunk f / 32) holds
-  // keys 2p and 2p+1 of one 8-dim chunk in vreg[2w], vreg[2w+1], so each of
-  // the chunk's 8 dims is stored to V^T as one dword (the two keys' values),
-  // lanes of a wave writing consecutive dwords of a row: no bank conflicts
-  // (2-byte stores put two lanes on one dword).
-  constexpr int NPW = (kBN / 2) * CH / 256;      // key-pair entries per thread
-  static_assert(2 * NPW == NCHK, "V pair staging covers the tile");
-  static_assert(NCHK * 256 == kBN * CH, "every thread fetches whole chunks");
-  // Each thread's chunks sit at fixed (key, column) offsets inside a tile, so
-  // a tile's loads are its base plus per-thread offsets plus constants.  K
-  // chunk u: row kr0 + u * (256 / CH), column kc0; V pair entry w: rows vr0 and
-  // vr0 + 1, column vc0 + 64 w.  Rows past the sequence (the last tile only)
-  // are zero: a key there follows every query and is masked.
-  const uint32_t kr0 = threadIdx.x / CH, kc0 = 8 * (threadIdx.x % CH);
-  const uint32_t vr0 = 2 * (threadIdx.x % (kBN / 2)), vc0 = 8 * (threadIdx.x / (kBN / 2));
-  const uint32_t koff0 = kr0 * rs32 + kc0, voff0 = vr0 * rs32 + vc0;
+  // DMA: per tile and array, 1 KiB blocks j = wave + 4 i of RPB rows each;
+  // lane p of block j fills row RPB j + p / CH, 16-byte slot p % CH, which
+  // holds the row's chunk (slot ^ swizzle).  Rows past the sequence (the last
+  // tile only) re-read row T - 1: those keys follow every query and are masked.
+  constexpr int CH = HD / 8;             // 16-byte chunks per row
+  constexpr int RPB = 64 / CH;           // rows per 1 KiB block
+  constexpr int BPW = kBN / RPB / 4;     // blocks per wave per array
+  static_assert(BPW * 4 * RPB == kBN, "the waves' blocks cover the tile");
+  uint32_t kdo[BPW], vdo[BPW];
+  int drow[BPW];
+#pragma unroll
+  for (int i = 0; i < BPW; ++i) {
+    const int r = RPB * (wave + 4 * i) + lane / CH, sl = lane % CH;
+    drow[i] = r;
+    kdo[i] = 8 * (sl ^ (r & 7));
+    vdo[i] = 8 * (sl ^ (2 * (r & 3)));
+  }
   const uint16_t* kbase = k + base;
   const uint16_t* vbase = v + base;
-  auto fetch = [&](int tile) {
+  auto issue = [&](int tile, int st) {
     const int kt = tile * kBN;
-    const uint16_t* kb = kbase + static_cast<long long>(kt) * rs;
-    const uint16_t* vb = vbase + static_cast<long long>(kt) * rs;
-    const uint32_t last = static_cast<uint32_t>(T - 1 - kt);
+    uint16_t* sk = smem + st * 2 * TILE;
 #pragma unroll
-    for (int u = 0; u < NCHK; ++u) {
-      const uint32_t kr = kr0 + u * (256 / CH);
-      kreg[u] = kr <= last ? *reinterpret_cast<const uint4*>(kb + koff0 + u * (256 / CH) * rs32)
-                           : uint4{0u, 0u, 0u, 0u};
+    for (int i = 0; i < BPW; ++i) {
+      const uint32_t ro = static_cast<uint32_t>(min(kt + drow[i], T - 1)) * rs32;
+      dma16(kbase + ro + kdo[i], sk + (wave + 4 * i) * 512);
+      dma16(vbase + ro + vdo[i], sk + TILE + (wave + 4 * i) * 512);
     }
-#pragma unroll
-    for (int w = 0; w < NPW; ++w)
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        vreg[2 * w + i] = vr0 + i <= last
-                              ? *reinterpret_cast<const uint4*>(vb + voff0 + i * rs32 + 64 * w)
-                              : uint4{0u, 0u, 0u, 0u};
-      }
   };
-  fetch(t_lo);
+  // Fragment offsets (bytes from a stage's K or V tile).  K: key row col of the
+  // sub-tile, dims 16 t + 8 half (chunk 2 t + half).  V (transposing reads):
+  // lane 16 g + y addresses key 4 half + y / 4 (of the 16-key slice's lo or hi
+  // 8) at dims 32 d + 16 (g & 1) + 4 (y & 3) .. +3, and receives dim
+  // 32 d + col for keys 4 half .. +3 (lo) or 8 + 4 half .. +3 (hi), the
+  // B-operand key order of P.
+  const uint32_t sbase = lds_addr(smem);
+  uint32_t koff[NS], voff[ND];
+#pragma unroll
+  for (int t = 0; t < NS; ++t) koff[t] = col * RB + 16 * ((2 * t + half) ^ (col & 7));
+  {
+    const int y = lane & 15, g = lane >> 4, i = y >> 2;
+#pragma unroll
+    for (int d = 0; d < ND; ++d) {
+      const int dim0 = 32 * d + 16 * (g & 1) + 4 * (y & 3);
+      voff[d] = (4 * half + i) * RB + 16 * ((dim0 >> 3) ^ (2 * i)) + 2 * (dim0 & 7);
+    }
+  }
+  issue(t_lo, 0);
   for (int tile = t_lo; tile <= t_hi; ++tile) {
     const int kt = tile * kBN;
-    // ---- stage K (row-major, padded) and V^T (transposed) for 64 keys
+    const int st = (tile - t_lo) & 1;
+    // this wave's DMA of the tile has landed; after the barrier every wave's
+    // has, and every wave is done with the other stage, which the next tile's
+    // DMA then fills while this one is consumed
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-#pragma unroll
-    for (int u = 0; u < NCHK; ++u)  // every thread's chunks lie in the tile (NCHK * 256 = kBN * CH)
-      *reinterpret_cast<uint4*>(Ks + (kr0 + u * (256 / CH)) * (HD + kKPad) + kc0) = kreg[u];
-#pragma unroll
-    for (int w = 0; w < NPW; ++w) {
-      const int f = threadIdx.x + 256 * w;
-      const int p2 = 2 * (f % (kBN / 2)), vc = f / (kBN / 2);
-      const uint32_t a4[4] = {vreg[2 * w].x, vreg[2 * w].y, vreg[2 * w].z, vreg[2 * w].w};
-      const uint32_t b4[4] = {vreg[2 * w + 1].x, vreg[2 * w + 1].y, vreg[2 * w + 1].z,
-                              vreg[2 * w + 1].w};
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        // dim 8vc + e: key 2p in the low half, key 2p+1 in the high half (one
-        // byte permute: bytes of a4 are selectors 0-3, of b4 4-7)
-        const uint32_t word = __builtin_amdgcn_perm(b4[e >> 1], a4[e >> 1],
-                                                    (e & 1) ? 0x07060302u : 0x05040100u);
-        *reinterpret_cast<uint32_t*>(Vt + (8 * vc + e) * (kBN + kVPad) + p2) = word;
-      }
-    }
-    __syncthreads();
-    if (tile < t_hi) fetch(tile + 1);
+    if (tile < t_hi) issue(tile + 1, st ^ 1);
+    const uint32_t kst = sbase + st * 4 * TILE, vst = kst + 2 * TILE;
 
 #pragma unroll
     for (int sub = 0; sub < 2; ++sub) {
@@ -169,12 +206,26 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const uint16_t* __res
       f32x16v s;
 #pragma unroll
       for (int r = 0; r < 16; ++r) s[r] = 0.f;
+      u32x4 kf[NS];
 #pragma unroll
-      for (int t = 0; t < NS; ++t) {
-        const uint4 kf = *reinterpret_cast<const uint4*>(Ks + (32 * sub + col) * (HD + kKPad) +
-                                                          16 * t + 8 * half);
-        s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(kf), as_bf16x8(qf[t]), s, 0, 0, 0);
-      }
+      for (int t = 0; t < NS; ++t) kf[t] = lds_b128(kst + 32 * sub * RB + koff[t]);
+      static_assert(NS % 4 == 0, "K fragments settle four at a time");
+#pragma unroll
+      for (int t = 0; t < NS; t += 4) lds_settle4(kf + t);
+#pragma unroll
+      for (int t = 0; t < NS; ++t)
+        s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, kf[t]),
+                                                    as_bf16x8(qf[t]), s, 0, 0, 0);
+      // V^T fragments of both 16-key slices, requested ahead of the softmax
+      u32x2 vf[2][ND][2];
+#pragma unroll
+      for (int sl = 0; sl < 2; ++sl)
+#pragma unroll
+        for (int d = 0; d < ND; ++d) {
+          const uint32_t va = vst + (32 * sub + 16 * sl) * RB + voff[d];
+          vf[sl][d][0] = lds_tr16(va);
+          vf[sl][d][1] = lds_tr16(va + 8 * RB);
+        }
       // ---- mask + online softmax (log2 domain); register r holds key
       //      kk = ks + (r & 3) + 8 (r >> 2) + 4 half for query qi, kept when
       //      0 <= qi - kk < W: one unsigned compare of dq - c_r against W
@@ -228,18 +279,17 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(const uint16_t* __res
         psum += p[r];
       }
       l_run += psum;
-      // ---- O^T += V^T P^T over the two 16-key slices
+      // ---- O^T += V^T P^T over the two 16-key slices (keys of slice sl for
+      //      this lane: ks + 16 sl + kappa(half, j))
+      static_assert(ND % 2 == 0, "V fragments settle eight at a time");
+#pragma unroll
+      for (int q8 = 0; q8 < ND / 2; ++q8) lds_settle_v(&vf[0][0][0] + 8 * q8);
 #pragma unroll
       for (int sl = 0; sl < 2; ++sl) {
         const uint4 pb = pack8_bf16(p + 8 * sl);
-        // keys of slice sl for this lane: ks + 16 sl + kappa(half, j)
-        const int kb0 = 32 * sub + 16 * sl + 4 * half;  // j = 0..3 -> +0..3, j = 4..7 -> +8..11
 #pragma unroll
         for (int d = 0; d < ND; ++d) {
-          const uint16_t* vrow = Vt + (32 * d + col) * (kBN + kVPad);
-          const uint2 lo = *reinterpret_cast<const uint2*>(vrow + kb0);
-          const uint2 hi = *reinterpret_cast<const uint2*>(vrow + kb0 + 8);
-          const uint4 va = uint4{lo.x, lo.y, hi.x, hi.y};
+          const uint4 va = uint4{vf[sl][d][0].x, vf[sl][d][0].y, vf[sl][d][1].x, vf[sl][d][1].y};
           acc[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(va), as_bf16x8(pb), acc[d],
                                                            0, 0, 0);
         }
