@@ -809,6 +809,29 @@ __global__ __launch_bounds__(64 * NW) void cmp_apply_kernel(
   }
 }
 
+// Dense lists summed over the heads, for sequences: P[r][j] = sum over h, in
+// head order from 0, of wl[(r H + h) Kmax + j] -- the sum the apply forms
+// itself, bit for bit -- so the apply reads one list per query instead of H.
+// Thread = (row, slot), the H loads requested together.
+constexpr int kHeadSumMaxH = 16;
+
+__global__ __launch_bounds__(256) void cmp_head_sum_kernel(const float* __restrict__ wl, int H,
+                                                           int Kmax, int64_t n,
+                                                           float* __restrict__ P) {
+  const int64_t e = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (e >= n) return;
+  const int64_t r = e / Kmax, j = e - r * Kmax;
+  const float* src = wl + r * H * Kmax + j;
+  float w[kHeadSumMaxH];
+#pragma unroll
+  for (int h = 0; h < kHeadSumMaxH; ++h) w[h] = h < H ? src[static_cast<int64_t>(h) * Kmax] : 0.f;
+  float acc = 0.f;
+#pragma unroll
+  for (int h = 0; h < kHeadSumMaxH; ++h)
+    if (h < H) acc += w[h];
+  P[e] = acc;
+}
+
 // Sequence apply on MFMA (prefill): workgroup = (row b, 32-query block,
 // 256-channel block), 8 wavefronts.  The block's head-summed weights P [32
 // queries][block slots] are accumulated in LDS (fp32, heads in order, as
@@ -825,7 +848,7 @@ constexpr int kApplyVtPitch = 40;   // bf16 per staged V^T row (32 slots + 8 pad
 __global__ __launch_bounds__(512) void cmp_apply_mfma_kernel(
     const float* __restrict__ wl, const int32_t* __restrict__ il, int Kmax, int H, int T,
     int band_W, int nslots, const uint16_t* __restrict__ v, int64_t v_ld, int rows_per_b,
-    uint16_t* __restrict__ out, int64_t out_ld, int Dv) {
+    uint16_t* __restrict__ out, int64_t out_ld, int Dv, float invH) {
   extern __shared__ float pmf[];
   const int nsb = band_W > 0 ? nslots + 31 : nslots;   // block slots
   const int NP = (nsb + 31) & ~31;
@@ -965,7 +988,6 @@ __global__ __launch_bounds__(512) void cmp_apply_mfma_kernel(
   }
   // ---- lane holds query col, channels 32 w + 8 g4 + 4 hf .. +3 in registers 4 g4 ..
   if (!w_ok || col >= nq) return;
-  const float invH = 1.0f / static_cast<float>(H);
   uint16_t* orow = out + (static_cast<int64_t>(b) * T + t0 + col) * out_ld + c0 + 32 * wave;
 #pragma unroll
   for (int g4 = 0; g4 < 4; ++g4)
@@ -1135,6 +1157,11 @@ inline int64_t list_bytes(int64_t queries, int H, int Kmax, bool pairs) {
   return queries * H * Kmax * static_cast<int64_t>(pairs ? 8 : 4);
 }
 
+// sequences with dense lists keep the head-summed lists beside them
+inline int64_t dense_seq_bytes(int64_t queries, int H, int slots) {
+  return list_bytes(queries, H, slots, false) + (H > 1 ? list_bytes(queries, 1, slots, false) : 0);
+}
+
 // decode keeps the raw scores of its slots beside the lists
 inline int64_t decode_bytes(int64_t rows, int H, int slots, int top_k) {
   return list_bytes(rows, H, top_k > 0 ? top_k : slots, top_k > 0) + rows * H * slots * 4ll;
@@ -1148,7 +1175,7 @@ extern "C" int64_t llmy_cmp_workspace_bytes(int32_t queries, int32_t H, int32_t 
                                             int32_t top_k, int32_t decode) {
   if (queries < 0 || H <= 0 || slots <= 0 || top_k < 0) return -1;
   if (decode) return decode_bytes(queries, H, slots, top_k);
-  return top_k > 0 ? list_bytes(queries, H, top_k, true) : list_bytes(queries, H, slots, false);
+  return top_k > 0 ? list_bytes(queries, H, top_k, true) : dense_seq_bytes(queries, H, slots);
 }
 
 namespace {
@@ -1156,10 +1183,23 @@ namespace {
 int32_t apply_launch(const float* wl, const int32_t* il, int Kmax, int H, int B, int T,
                      const int32_t* qpos, int band_W, int nslots, const uint16_t* v, int64_t v_ld,
                      int rows_per_b, int wrap, uint16_t* out, int64_t out_ld, int Dv,
-                     hipStream_t s) {
+                     hipStream_t s, float* head_sum = nullptr) {
   // sequences on MFMA where the block's weights fit the LDS
   if (!qpos && T >= 8 && Dv % 32 == 0 && wrap == 0 &&
       (band_W > 0 ? nslots + 31 : nslots) <= kApplyMfmaSlots) {
+    const float invH = 1.0f / static_cast<float>(H);
+    if (head_sum && !il && H > 1 && H <= kHeadSumMaxH) {
+      // dense lists: sum the heads once, then apply one list per query
+      const int64_t n = static_cast<int64_t>(B) * T * Kmax;
+      const int64_t nb = (n + 255) / 256;
+      if (nb >= (1ll << 31)) return static_cast<int32_t>(hipErrorInvalidValue);
+      hipLaunchKernelGGL(cmp_head_sum_kernel, dim3(static_cast<unsigned>(nb)), dim3(256), 0, s,
+                         wl, H, Kmax, n, head_sum);
+      const int32_t st = launch_status();
+      if (st) return st;
+      wl = head_sum;
+      H = 1;
+    }
     const int nsb = band_W > 0 ? nslots + 31 : nslots;
     const int NP = (nsb + 31) & ~31;
     const size_t lds = static_cast<size_t>(32) * (NP + 4) * 4 + 256 * kApplyVtPitch * 2;
@@ -1167,7 +1207,7 @@ int32_t apply_launch(const float* wl, const int32_t* il, int Kmax, int H, int B,
     if (nblk >= (1ll << 31)) return static_cast<int32_t>(hipErrorInvalidValue);
     hipLaunchKernelGGL(cmp_apply_mfma_kernel, dim3(static_cast<unsigned>(nblk)), dim3(512), lds,
                        s, wl, il, Kmax, H, T, band_W, nslots, v, v_ld, rows_per_b, out, out_ld,
-                       Dv);
+                       Dv, invH);
     return launch_status();
   }
   // blocks of 8 queries for sequences (a value row serves the whole block),
@@ -1211,7 +1251,7 @@ extern "C" int32_t llmy_cmp_local_prefill_bf16(
   LLMY_REQUIRE(aligned(q, 16) && aligned(k, 16) && aligned(v, 16) && aligned(out, 8) &&
                aligned(workspace, 16));
   const int64_t queries = static_cast<int64_t>(B) * T;
-  LLMY_REQUIRE(workspace_bytes >= list_bytes(queries, H, W, false));
+  LLMY_REQUIRE(workspace_bytes >= dense_seq_bytes(queries, H, W));
   const int nqb = (T + 31) / 32;
   LLMY_REQUIRE(static_cast<int64_t>(B) * nqb * H < (1ll << 31) && queries < (1ll << 31));
   const int ncp = ((min(T, W + 31) + 31) / 32 + 1) * 32;   // >= any block's candidate span
@@ -1225,7 +1265,8 @@ extern "C" int32_t llmy_cmp_local_prefill_bf16(
                                nullptr);
   const int32_t st = launch_status();
   if (st) return st;
-  return apply_launch(wl, nullptr, W, H, B, T, nullptr, W, W, v, v_ld, T, 0, out, out_ld, Dv, s);
+  return apply_launch(wl, nullptr, W, H, B, T, nullptr, W, W, v, v_ld, T, 0, out, out_ld, Dv, s,
+                      wl + queries * H * W);
 }
 
 extern "C" int32_t llmy_cmp_memory_prefill_bf16(
@@ -1246,7 +1287,8 @@ extern "C" int32_t llmy_cmp_memory_prefill_bf16(
   const int64_t queries = static_cast<int64_t>(B) * T;
   const int slots = max(n_entries, 1);
   const int Kmax = top_k > 0 ? top_k : slots;
-  LLMY_REQUIRE(workspace_bytes >= list_bytes(queries, H, Kmax, top_k > 0));
+  LLMY_REQUIRE(workspace_bytes >= (top_k > 0 ? list_bytes(queries, H, Kmax, true)
+                                               : dense_seq_bytes(queries, H, Kmax)));
   LLMY_REQUIRE(slots <= 4000);   // the apply's LDS: 9 words per slot + 4 KiB
   const hipStream_t s = as_stream(stream);
   // n_entries == 0: no summary is visible to any query, every list is 0 and
@@ -1271,7 +1313,7 @@ extern "C" int32_t llmy_cmp_memory_prefill_bf16(
   const int32_t st = launch_status();
   if (st) return st;
   return apply_launch(wl, il, Kmax, H, B, T, nullptr, 0, slots, mv, mv_ld, slots, 0, out,
-                      out_ld, Dv, s);
+                      out_ld, Dv, s, top_k > 0 ? nullptr : wl + queries * H * Kmax);
 }
 
 extern "C" int32_t llmy_cmp_local_decode_bf16(
