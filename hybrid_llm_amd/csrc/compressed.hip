@@ -241,7 +241,10 @@ __device__ __forceinline__ void topk_row(float* srow, int n, int k, int lane, fl
 }
 
 // ---------------------------------------------------------------- prefill
-// Workgroup = (head h, 32-query block, row b), h fastest; 8 waves.  Candidates:
+// Workgroup = (head h, 32-query block, row b), h fastest; 16 waves (four per
+// SIMD: the scores' load latency and the selections' scalar chains of one
+// wave hide behind the others'; the block's score rows fill up to 128 KiB of
+// LDS, so a CU holds one workgroup).  Candidates:
 //   band: keys [max(0, t0 - W + 1), min(T - 1, t0 + 31)] of row b (q/k rows
 //         b*T + t); the list of query t has W slots, slot j = key t - W + 1 + j;
 //   memory: entries [0, nv), nv = min(n, min(T, t0 + 32) / ratio) (rows b*n + i,
@@ -250,13 +253,13 @@ __device__ __forceinline__ void topk_row(float* srow, int n, int k, int lane, fl
 //         i >= (t + 1) / ratio - W, as a token-by-token decode sees them);
 //         dense lists have n slots, top-k lists top_k pairs.
 // NS = head_dim / 16 when it is at most 8: the 32 queries' fragments stay in
-// registers and each wave prefetches its next 32-candidate tile under the
-// current tile's MFMAs; NS = 0: any multiple-of-16 head width, operands loaded
-// per 16-wide slice.
-constexpr int kSelWaves = 8;
+// registers through a pass's scores (128 VGPRs hold a wave at four per SIMD,
+// so a tile's fragments are not prefetched); NS = 0: any multiple-of-16 head
+// width, operands loaded per 16-wide slice.
+constexpr int kSelWaves = 16;
 
 template <int MODE, int NS>
-__global__ __launch_bounds__(512) void cmp_select_prefill_kernel(
+__global__ __launch_bounds__(1024) void cmp_select_prefill_kernel(
     const uint16_t* __restrict__ q, int64_t q_ld, const uint16_t* __restrict__ k, int64_t k_ld,
     int T, int n, int H, int Dh, int W, int ratio, int top_k, int Kmax, int rows_pass,
     float scale_log2, float* __restrict__ wl, int32_t* __restrict__ il) {
@@ -286,28 +289,21 @@ __global__ __launch_bounds__(512) void cmp_select_prefill_kernel(
       q + static_cast<int64_t>(b * T + (q_ok ? t0 + col : 0)) * q_ld + h * Dh + 8 * half;
   const int64_t krow0 = MODE == kBand ? static_cast<int64_t>(b) * T : static_cast<int64_t>(b) * n;
   constexpr int NQ = NS > 0 ? NS : 1;
-  uint4 qf[NQ];
-  if (NS > 0) {
-#pragma unroll
-    for (int s = 0; s < NQ; ++s)
-      qf[s] = q_ok ? *reinterpret_cast<const uint4*>(qrow + 16 * s) : uint4{0, 0, 0, 0};
-  }
   auto krow_of = [&](int tile, bool& ok) {
     const int c0 = c_lo + 32 * tile;
     ok = c0 + col < c_lo + nc;
     return k + (krow0 + (ok ? c0 + col : c_lo)) * k_ld + h * Dh + 8 * half;
   };
   for (int p0 = 0; p0 < 32; p0 += rows_pass) {
-    if (ntile == 0) {   // no candidate yet (memory before the first block end)
-      for (int i = threadIdx.x; i < rows_pass * ncp; i += 64 * kSelWaves) sc[i] = -INFINITY;
-    }
-    uint4 an[NQ];
-    if (NS > 0 && wave < ntile) {
-      bool ok;
-      const uint16_t* kr = krow_of(wave, ok);
+    // the queries' fragments, per pass (dead during the selection)
+    uint4 qf[NQ];
+    if (NS > 0) {
 #pragma unroll
       for (int s = 0; s < NQ; ++s)
-        an[s] = ok ? *reinterpret_cast<const uint4*>(kr + 16 * s) : uint4{0, 0, 0, 0};
+        qf[s] = q_ok ? *reinterpret_cast<const uint4*>(qrow + 16 * s) : uint4{0, 0, 0, 0};
+    }
+    if (ntile == 0) {   // no candidate yet (memory before the first block end)
+      for (int i = threadIdx.x; i < rows_pass * ncp; i += 64 * kSelWaves) sc[i] = -INFINITY;
     }
     for (int tile = wave; tile < ntile; tile += kSelWaves) {
       const int c0 = c_lo + 32 * tile;
@@ -316,14 +312,12 @@ __global__ __launch_bounds__(512) void cmp_select_prefill_kernel(
       for (int r = 0; r < 16; ++r) acc[r] = 0.f;
       if (NS > 0) {
         uint4 a[NQ];
-#pragma unroll
-        for (int s = 0; s < NQ; ++s) a[s] = an[s];
-        if (tile + kSelWaves < ntile) {   // the next tile's fragments, in flight meanwhile
+        {
           bool ok;
-          const uint16_t* kr = krow_of(tile + kSelWaves, ok);
+          const uint16_t* kr = krow_of(tile, ok);
 #pragma unroll
           for (int s = 0; s < NQ; ++s)
-            an[s] = ok ? *reinterpret_cast<const uint4*>(kr + 16 * s) : uint4{0, 0, 0, 0};
+            a[s] = ok ? *reinterpret_cast<const uint4*>(kr + 16 * s) : uint4{0, 0, 0, 0};
         }
 #pragma unroll
         for (int s = 0; s < NQ; ++s)
