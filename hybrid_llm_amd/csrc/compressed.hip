@@ -39,7 +39,7 @@ typedef float f32x16c __attribute__((ext_vector_type(16)));
 
 constexpr float kLog2eC = 1.4426950408889634f;
 enum CmpMode { kBand = 0, kMemDense = 1, kMemTopK = 2 };
-constexpr int kCmpLdsBytes = 131072;  // score budget of one prefill selection workgroup
+constexpr int kCmpLdsBytes = 135168;  // score budget of one prefill selection workgroup
 
 // One wave turns a row of log2-domain scores into a dense list over n slots:
 // slot j reads score srow[j + off] and is a candidate when jlo <= j < jhi
@@ -284,6 +284,9 @@ __global__ __launch_bounds__(1024) void cmp_select_prefill_kernel(
   }
   const int ntile = (nc + 31) / 32;
   const int ncp = max(ntile, 1) * 32;
+  // score rows one float longer than the candidates: the 32 queries of a tile
+  // store each candidate's score to 32 different banks
+  const int rsd = ncp + 1;
   const bool q_ok = t0 + col < T;
   const uint16_t* qrow =
       q + static_cast<int64_t>(b * T + (q_ok ? t0 + col : 0)) * q_ld + h * Dh + 8 * half;
@@ -303,7 +306,7 @@ __global__ __launch_bounds__(1024) void cmp_select_prefill_kernel(
         qf[s] = q_ok ? *reinterpret_cast<const uint4*>(qrow + 16 * s) : uint4{0, 0, 0, 0};
     }
     if (ntile == 0) {   // no candidate yet (memory before the first block end)
-      for (int i = threadIdx.x; i < rows_pass * ncp; i += 64 * kSelWaves) sc[i] = -INFINITY;
+      for (int i = threadIdx.x; i < rows_pass * rsd; i += 64 * kSelWaves) sc[i] = -INFINITY;
     }
     for (int tile = wave; tile < ntile; tile += kSelWaves) {
       const int c0 = c_lo + 32 * tile;
@@ -344,7 +347,7 @@ __global__ __launch_bounds__(1024) void cmp_select_prefill_kernel(
           bool vis = t < T && cj < c_lo + nc;
           if (MODE == kBand) vis = vis && cj <= t && t - cj < W;
           else vis = vis && (cj + 1) * ratio - 1 <= t && (W <= 0 || cj >= (t + 1) / ratio - W);
-          sc[row * ncp + (cj - c_lo)] = vis ? acc[r] * scale_log2 : -INFINITY;
+          sc[row * rsd + (cj - c_lo)] = vis ? acc[r] * scale_log2 : -INFINITY;
         }
       }
     }
@@ -352,7 +355,7 @@ __global__ __launch_bounds__(1024) void cmp_select_prefill_kernel(
     for (int row = wave; row < rows_pass; row += kSelWaves) {
       const int t = t0 + p0 + row;
       if (t >= T) continue;
-      float* srow = sc + row * ncp;
+      float* srow = sc + row * rsd;
       const int64_t lb = (static_cast<int64_t>(b * T + t) * H + h) * Kmax;
       if (MODE == kBand) {
         // slot j <-> key t - W + 1 + j (a candidate when >= 0) <-> score
@@ -1250,11 +1253,11 @@ extern "C" int32_t llmy_cmp_local_prefill_bf16(
   LLMY_REQUIRE(static_cast<int64_t>(B) * nqb * H < (1ll << 31) && queries < (1ll << 31));
   const int ncp = ((min(T, W + 31) + 31) / 32 + 1) * 32;   // >= any block's candidate span
   int rows = 32;
-  while (rows > 1 && static_cast<int64_t>(rows) * ncp * 4 > kCmpLdsBytes) rows /= 2;
-  LLMY_REQUIRE(static_cast<int64_t>(rows) * ncp * 4 <= kCmpLdsBytes);
+  while (rows > 1 && static_cast<int64_t>(rows) * (ncp + 1) * 4 > kCmpLdsBytes) rows /= 2;
+  LLMY_REQUIRE(static_cast<int64_t>(rows) * (ncp + 1) * 4 <= kCmpLdsBytes);
   const hipStream_t s = as_stream(stream);
   float* wl = static_cast<float*>(workspace);
-  select_prefill_launch<kBand>(dim3(B * nqb * H), static_cast<size_t>(rows) * ncp * 4, s, q, q_ld,
+  select_prefill_launch<kBand>(dim3(B * nqb * H), static_cast<size_t>(rows) * (ncp + 1) * 4, s, q, q_ld,
                                k, k_ld, T, 0, H, head_dim, W, 1, 0, W, rows, scale * kLog2eC, wl,
                                nullptr);
   const int32_t st = launch_status();
@@ -1291,11 +1294,11 @@ extern "C" int32_t llmy_cmp_memory_prefill_bf16(
   LLMY_REQUIRE(static_cast<int64_t>(B) * nqb * H < (1ll << 31) && queries < (1ll << 31));
   const int ncp = ((slots + 31) / 32) * 32;
   int rows = 32;
-  while (rows > 1 && static_cast<int64_t>(rows) * ncp * 4 > kCmpLdsBytes) rows /= 2;
-  LLMY_REQUIRE(static_cast<int64_t>(rows) * ncp * 4 <= kCmpLdsBytes);
+  while (rows > 1 && static_cast<int64_t>(rows) * (ncp + 1) * 4 > kCmpLdsBytes) rows /= 2;
+  LLMY_REQUIRE(static_cast<int64_t>(rows) * (ncp + 1) * 4 <= kCmpLdsBytes);
   float* wl = static_cast<float*>(workspace);
   int32_t* il = top_k > 0 ? reinterpret_cast<int32_t*>(wl + queries * H * Kmax) : nullptr;
-  const size_t lds = static_cast<size_t>(rows) * ncp * 4;
+  const size_t lds = static_cast<size_t>(rows) * (ncp + 1) * 4;
   if (top_k > 0)
     select_prefill_launch<kMemTopK>(dim3(B * nqb * H), lds, s, q, q_ld, mk, mk_ld, T, n_entries,
                                     H, head_dim, slots_window, ratio, top_k, Kmax, rows,
