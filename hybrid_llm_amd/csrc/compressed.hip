@@ -292,11 +292,33 @@ __global__ __launch_bounds__(1024) void cmp_select_prefill_kernel(
       q + static_cast<int64_t>(b * T + (q_ok ? t0 + col : 0)) * q_ld + h * Dh + 8 * half;
   const int64_t krow0 = MODE == kBand ? static_cast<int64_t>(b) * T : static_cast<int64_t>(b) * n;
   constexpr int NQ = NS > 0 ? NS : 1;
-  auto krow_of = [&](int tile, bool& ok) {
+  // candidate row of this lane in a tile (past the candidates: the first one,
+  // whose score the visibility test below replaces)
+  auto krow_of = [&](int tile) {
     const int c0 = c_lo + 32 * tile;
-    ok = c0 + col < c_lo + nc;
+    const bool ok = c0 + col < c_lo + nc;
     return k + (krow0 + (ok ? c0 + col : c_lo)) * k_ld + h * Dh + 8 * half;
   };
+  // The candidates query t = t0 + col sees form one interval [vlo, vlo + vspan]:
+  // band: max(t - W + 1, c_lo) .. min(t, last candidate); memory: entry i with
+  // (i + 1) ratio - 1 <= t, i.e. i < (t + 1) / ratio, and with W > 0 i >=
+  // (t + 1) / ratio - W.  An empty interval (or t >= T) puts vlo out of reach.
+  int vlo, vspan;
+  {
+    const int t = t0 + col;
+    int lo, hi;
+    if (MODE == kBand) {
+      lo = max(t - W + 1, c_lo);
+      hi = min(t, c_lo + nc - 1);
+    } else {
+      const int e = (t + 1) / ratio;
+      lo = W > 0 ? max(e - W, 0) : 0;
+      hi = min(e, nc) - 1;
+    }
+    const bool any = q_ok && lo <= hi;
+    vlo = any ? lo : (1 << 30);
+    vspan = any ? hi - lo : 0;
+  }
   for (int p0 = 0; p0 < 32; p0 += rows_pass) {
     // the queries' fragments, per pass (dead during the selection)
     uint4 qf[NQ];
@@ -315,23 +337,18 @@ __global__ __launch_bounds__(1024) void cmp_select_prefill_kernel(
       for (int r = 0; r < 16; ++r) acc[r] = 0.f;
       if (NS > 0) {
         uint4 a[NQ];
-        {
-          bool ok;
-          const uint16_t* kr = krow_of(tile, ok);
+        const uint16_t* kr = krow_of(tile);
 #pragma unroll
-          for (int s = 0; s < NQ; ++s)
-            a[s] = ok ? *reinterpret_cast<const uint4*>(kr + 16 * s) : uint4{0, 0, 0, 0};
-        }
+        for (int s = 0; s < NQ; ++s) a[s] = *reinterpret_cast<const uint4*>(kr + 16 * s);
 #pragma unroll
         for (int s = 0; s < NQ; ++s)
           acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a[s]), as_bf16x8(qf[s]), acc,
                                                         0, 0, 0);
       } else {
-        bool ok;
-        const uint16_t* kr = krow_of(tile, ok);
+        const uint16_t* kr = krow_of(tile);
 #pragma unroll 4
         for (int s = 0; s < Dh / 16; ++s) {
-          const uint4 a = ok ? *reinterpret_cast<const uint4*>(kr + 16 * s) : uint4{0, 0, 0, 0};
+          const uint4 a = *reinterpret_cast<const uint4*>(kr + 16 * s);
           const uint4 bq =
               q_ok ? *reinterpret_cast<const uint4*>(qrow + 16 * s) : uint4{0, 0, 0, 0};
           acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a), as_bf16x8(bq), acc, 0, 0,
@@ -340,14 +357,12 @@ __global__ __launch_bounds__(1024) void cmp_select_prefill_kernel(
       }
       const int row = col - p0;
       if (row >= 0 && row < rows_pass) {
-        const int t = t0 + col;
+        float* dst = sc + row * rsd - c_lo;   // indexed by candidate
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int cj = c0 + (r & 3) + 8 * (r >> 2) + 4 * half;
-          bool vis = t < T && cj < c_lo + nc;
-          if (MODE == kBand) vis = vis && cj <= t && t - cj < W;
-          else vis = vis && (cj + 1) * ratio - 1 <= t && (W <= 0 || cj >= (t + 1) / ratio - W);
-          sc[row * rsd + (cj - c_lo)] = vis ? acc[r] * scale_log2 : -INFINITY;
+          const bool vis = static_cast<unsigned>(cj - vlo) <= static_cast<unsigned>(vspan);
+          dst[cj] = vis ? acc[r] * scale_log2 : -INFINITY;
         }
       }
     }
