@@ -330,21 +330,53 @@ __global__ __launch_bounds__(1024) void cmp_select_prefill_kernel(
     if (ntile == 0) {   // no candidate yet (memory before the first block end)
       for (int i = threadIdx.x; i < rows_pass * rsd; i += 64 * kSelWaves) sc[i] = -INFINITY;
     }
-    for (int tile = wave; tile < ntile; tile += kSelWaves) {
-      const int c0 = c_lo + 32 * tile;
-      f32x16c acc;
+    auto store_scores = [&](int tile, const f32x16c& acc) {
+      const int row = col - p0;
+      if (row >= 0 && row < rows_pass) {
+        const int c0 = c_lo + 32 * tile;
+        float* dst = sc + row * rsd - c_lo;   // indexed by candidate
 #pragma unroll
-      for (int r = 0; r < 16; ++r) acc[r] = 0.f;
-      if (NS > 0) {
-        uint4 a[NQ];
+        for (int r = 0; r < 16; ++r) {
+          const int cj = c0 + (r & 3) + 8 * (r >> 2) + 4 * half;
+          const bool vis = static_cast<unsigned>(cj - vlo) <= static_cast<unsigned>(vspan);
+          dst[cj] = vis ? acc[r] * scale_log2 : -INFINITY;
+        }
+      }
+    };
+    if (NS > 0) {
+      // two tiles per round: both tiles' candidate rows are requested together
+      for (int tile = wave; tile < ntile; tile += 2 * kSelWaves) {
+        const int tile2 = tile + kSelWaves;
+        const bool two = tile2 < ntile;
+        uint4 a[NQ], a2[NQ];
         const uint16_t* kr = krow_of(tile);
+        const uint16_t* kr2 = krow_of(two ? tile2 : tile);
 #pragma unroll
-        for (int s = 0; s < NQ; ++s) a[s] = *reinterpret_cast<const uint4*>(kr + 16 * s);
+        for (int s = 0; s < NQ; ++s) {
+          a[s] = *reinterpret_cast<const uint4*>(kr + 16 * s);
+          a2[s] = *reinterpret_cast<const uint4*>(kr2 + 16 * s);
+        }
+        f32x16c acc, acc2;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[r] = acc2[r] = 0.f;
 #pragma unroll
         for (int s = 0; s < NQ; ++s)
           acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a[s]), as_bf16x8(qf[s]), acc,
                                                         0, 0, 0);
-      } else {
+        if (two) {
+#pragma unroll
+          for (int s = 0; s < NQ; ++s)
+            acc2 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a2[s]), as_bf16x8(qf[s]),
+                                                           acc2, 0, 0, 0);
+        }
+        store_scores(tile, acc);
+        if (two) store_scores(tile2, acc2);
+      }
+    } else {
+      for (int tile = wave; tile < ntile; tile += kSelWaves) {
+        f32x16c acc;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[r] = 0.f;
         const uint16_t* kr = krow_of(tile);
 #pragma unroll 4
         for (int s = 0; s < Dh / 16; ++s) {
@@ -354,16 +386,7 @@ __global__ __launch_bounds__(1024) void cmp_select_prefill_kernel(
           acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a), as_bf16x8(bq), acc, 0, 0,
                                                         0);
         }
-      }
-      const int row = col - p0;
-      if (row >= 0 && row < rows_pass) {
-        float* dst = sc + row * rsd - c_lo;   // indexed by candidate
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int cj = c0 + (r & 3) + 8 * (r >> 2) + 4 * half;
-          const bool vis = static_cast<unsigned>(cj - vlo) <= static_cast<unsigned>(vspan);
-          dst[cj] = vis ? acc[r] * scale_log2 : -INFINITY;
-        }
+        store_scores(tile, acc);
       }
     }
     __syncthreads();
