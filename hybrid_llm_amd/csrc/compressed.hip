@@ -241,10 +241,10 @@ __device__ __forceinline__ void topk_row(float* srow, int n, int k, int lane, fl
 }
 
 // ---------------------------------------------------------------- prefill
-// Workgroup = (head h, 32-query block, row b), h fastest; 16 waves (four per
-// SIMD: the scores' load latency and the selections' scalar chains of one
-// wave hide behind the others'; the block's score rows fill up to 128 KiB of
-// LDS, so a CU holds one workgroup).  Candidates:
+// Workgroup = (head h, 32-query block, row b), h fastest; NW waves (top-k: 16,
+// four per SIMD, so the scores' load latency and the selections' scalar
+// chains of one wave hide behind the others' -- the block's score rows fill
+// up to 132 KiB of LDS and a CU holds one workgroup).  Candidates:
 //   band: keys [max(0, t0 - W + 1), min(T - 1, t0 + 31)] of row b (q/k rows
 //         b*T + t); the list of query t has W slots, slot j = key t - W + 1 + j;
 //   memory: entries [0, nv), nv = min(n, min(T, t0 + 32) / ratio) (rows b*n + i,
@@ -256,16 +256,22 @@ __device__ __forceinline__ void topk_row(float* srow, int n, int k, int lane, fl
 // registers through a pass's scores (128 VGPRs hold a wave at four per SIMD,
 // so a tile's fragments are not prefetched); NS = 0: any multiple-of-16 head
 // width, operands loaded per 16-wide slice.
-constexpr int kSelWaves = 16;
-
+// NW waves per workgroup: 16 for top-k lists and for wide heads (NS = 0);
+// dense lists of 64- / 128-wide heads (a softmax per row, no selection) run
+// 4-wave workgroups, several per CU.
 template <int MODE, int NS>
-__global__ __launch_bounds__(1024) void cmp_select_prefill_kernel(
+constexpr int sel_waves() {
+  return MODE == kMemTopK || NS == 0 ? 16 : 4;
+}
+
+template <int MODE, int NS, int NW>
+__global__ __launch_bounds__(64 * NW) void cmp_select_prefill_kernel(
     const uint16_t* __restrict__ q, int64_t q_ld, const uint16_t* __restrict__ k, int64_t k_ld,
     int T, int n, int H, int Dh, int W, int ratio, int top_k, int Kmax, int rows_pass,
     float scale_log2, float* __restrict__ wl, int32_t* __restrict__ il) {
   extern __shared__ float sc[];
-  __shared__ float sel_s[kSelWaves][kWave];
-  __shared__ int sel_i[kSelWaves][kWave];
+  __shared__ float sel_s[MODE == kMemTopK ? NW : 1][kWave];
+  __shared__ int sel_i[MODE == kMemTopK ? NW : 1][kWave];
   const int h = blockIdx.x % H;
   const int rest = blockIdx.x / H;
   const int nqb = (T + 31) / 32;
@@ -328,7 +334,7 @@ __global__ __launch_bounds__(1024) void cmp_select_prefill_kernel(
         qf[s] = q_ok ? *reinterpret_cast<const uint4*>(qrow + 16 * s) : uint4{0, 0, 0, 0};
     }
     if (ntile == 0) {   // no candidate yet (memory before the first block end)
-      for (int i = threadIdx.x; i < rows_pass * rsd; i += 64 * kSelWaves) sc[i] = -INFINITY;
+      for (int i = threadIdx.x; i < rows_pass * rsd; i += 64 * NW) sc[i] = -INFINITY;
     }
     auto store_scores = [&](int tile, const f32x16c& acc) {
       const int row = col - p0;
@@ -345,8 +351,8 @@ __global__ __launch_bounds__(1024) void cmp_select_prefill_kernel(
     };
     if (NS > 0) {
       // two tiles per round: both tiles' candidate rows are requested together
-      for (int tile = wave; tile < ntile; tile += 2 * kSelWaves) {
-        const int tile2 = tile + kSelWaves;
+      for (int tile = wave; tile < ntile; tile += 2 * NW) {
+        const int tile2 = tile + NW;
         const bool two = tile2 < ntile;
         uint4 a[NQ], a2[NQ];
         const uint16_t* kr = krow_of(tile);
@@ -373,7 +379,7 @@ __global__ __launch_bounds__(1024) void cmp_select_prefill_kernel(
         if (two) store_scores(tile2, acc2);
       }
     } else {
-      for (int tile = wave; tile < ntile; tile += kSelWaves) {
+      for (int tile = wave; tile < ntile; tile += NW) {
         f32x16c acc;
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[r] = 0.f;
@@ -390,7 +396,7 @@ __global__ __launch_bounds__(1024) void cmp_select_prefill_kernel(
       }
     }
     __syncthreads();
-    for (int row = wave; row < rows_pass; row += kSelWaves) {
+    for (int row = wave; row < rows_pass; row += NW) {
       const int t = t0 + p0 + row;
       if (t >= T) continue;
       float* srow = sc + row * rsd;
@@ -415,16 +421,18 @@ void select_prefill_launch(dim3 grid, size_t lds, hipStream_t s, const uint16_t*
                            const uint16_t* k, int64_t k_ld, int T, int n, int H, int Dh, int W,
                            int ratio, int top_k, int Kmax, int rows, float scale_log2, float* wl,
                            int32_t* il) {
-  const dim3 block(64 * kSelWaves);
   if (Dh == 128)
-    hipLaunchKernelGGL((cmp_select_prefill_kernel<MODE, 8>), grid, block, lds, s, q, q_ld, k,
-                       k_ld, T, n, H, Dh, W, ratio, top_k, Kmax, rows, scale_log2, wl, il);
+    hipLaunchKernelGGL((cmp_select_prefill_kernel<MODE, 8, sel_waves<MODE, 8>()>), grid,
+                       dim3(64 * sel_waves<MODE, 8>()), lds, s, q, q_ld, k, k_ld, T, n, H, Dh, W,
+                       ratio, top_k, Kmax, rows, scale_log2, wl, il);
   else if (Dh == 64)
-    hipLaunchKernelGGL((cmp_select_prefill_kernel<MODE, 4>), grid, block, lds, s, q, q_ld, k,
-                       k_ld, T, n, H, Dh, W, ratio, top_k, Kmax, rows, scale_log2, wl, il);
+    hipLaunchKernelGGL((cmp_select_prefill_kernel<MODE, 4, sel_waves<MODE, 4>()>), grid,
+                       dim3(64 * sel_waves<MODE, 4>()), lds, s, q, q_ld, k, k_ld, T, n, H, Dh, W,
+                       ratio, top_k, Kmax, rows, scale_log2, wl, il);
   else
-    hipLaunchKernelGGL((cmp_select_prefill_kernel<MODE, 0>), grid, block, lds, s, q, q_ld, k,
-                       k_ld, T, n, H, Dh, W, ratio, top_k, Kmax, rows, scale_log2, wl, il);
+    hipLaunchKernelGGL((cmp_select_prefill_kernel<MODE, 0, sel_waves<MODE, 0>()>), grid,
+                       dim3(64 * sel_waves<MODE, 0>()), lds, s, q, q_ld, k, k_ld, T, n, H, Dh, W,
+                       ratio, top_k, Kmax, rows, scale_log2, wl, il);
 }
 
 // ---------------------------------------------------------------- decode
