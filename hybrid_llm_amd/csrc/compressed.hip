@@ -275,7 +275,9 @@ __global__ __launch_bounds__(64 * NW) void cmp_select_prefill_kernel(
   const int h = blockIdx.x % H;
   const int rest = blockIdx.x / H;
   const int nqb = (T + 31) / 32;
-  const int qb = rest % nqb;
+  // memory: later query blocks see more entries; they are dispatched first so
+  // the short blocks fill in behind them
+  const int qb = MODE == kBand ? rest % nqb : nqb - 1 - rest % nqb;
   const int b = rest / nqb;
   const int t0 = qb * 32;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -902,7 +904,10 @@ __global__ __launch_bounds__(512) void cmp_apply_mfma_kernel(
   const int blk = blockIdx.x / ndb;
   const int db = blockIdx.x - blk * ndb;
   const int b = blk / nqb;
-  const int t0 = (blk - b * nqb) * 32;
+  // memory: later query blocks weigh more slots; they are dispatched first so
+  // the short blocks fill in behind them
+  const int qb = band_W > 0 ? blk - b * nqb : nqb - 1 - (blk - b * nqb);
+  const int t0 = qb * 32;
   const int nq = min(32, T - t0);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int c0 = db * 256;
