@@ -384,8 +384,9 @@ int32_t llmy_pad_cols_bf16(const llmy_bf16* x, llmy_bf16* out, int32_t rows, int
 
 /* Workspace bytes of one branch call for `queries` queries (prefill: B*T,
  * decode: B): slots = the local window W or the memory's entries / slots;
- * top_k 0 = dense lists, else top_k pairs; decode != 0 adds the raw scores the
- * decode entries keep.  -1 on bad sizes. */
+ * top_k 0 = dense lists (prefill with H > 1: plus the head-summed lists), else
+ * top_k pairs; decode != 0 adds the raw scores the decode entries keep.  -1 on
+ * bad sizes. */
 int64_t llmy_cmp_workspace_bytes(int32_t queries, int32_t H, int32_t slots, int32_t top_k,
                                  int32_t decode);
 /* Local branch over B fresh sequences of T tokens (rows b*T + t). */
