@@ -37,6 +37,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "llmy_banded_attn_prefill_bf16": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _F, _P]),
     "llmy_banded_attn_decode_bf16": (_I, [_P, _P, _P, _I64, _I64, _P, _P, _P, _P, _I, _I, _I,
                                           _I, _F, _P]),
+    "llmy_banded_attn_decode_parts_bf16": (_I, [_P, _I, _I64, _I64, _I, _I, _P, _P, _P, _P, _I,
+                                                _I, _I, _I, _F, _P]),
     "llmy_gdn_prefill_workspace_bytes": (C.c_int64, [_I, _I, _I, _I, _I]),
     "llmy_gdn_prefill_bf16": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I, _I, _I, _I, _I, _P]),
     "llmy_gdn_prefill_bf16_noalloc": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),

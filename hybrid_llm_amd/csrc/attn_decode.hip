@@ -11,15 +11,38 @@
 // max in the log2 domain, rescaled sum and output).  The new token is taken
 // from registers rather than re-read from the cache, and the waves' partial
 // (max, sum, output) are merged through LDS.
+//
+// The new row's q, k and v come either as bf16 rows or, for decode batches
+// whose projection ran as per-256-wide-K-block partial products, as P fp32
+// slices summed here in slice order and rounded to bf16: the same values,
+// bit for bit, as a projection kernel that sums its K blocks in that order
+// before its bf16 store.
 #include "common.hpp"
 #include "abi_util.hpp"
 
 namespace llmy {
 
-template <int HD>
+// q/k/v partial slices: parts [P][B][row] fp32, q at column 0, k at koff, v at voff.
+struct QkvParts {
+  const float* p;
+  int n;
+  long long stride;  // floats between slices
+  long long row;     // floats between batch rows
+  int koff, voff;
+};
+
+// The summed slices of one value (column c of row b), in slice order.
+__device__ __forceinline__ float sum_parts1(const QkvParts& a, int b, int c) {
+  const float* src = a.p + static_cast<long long>(b) * a.row + c;
+  float acc = src[0];
+  for (int s = 1; s < a.n; ++s) acc += src[s * a.stride];
+  return acc;
+}
+
+template <int HD, bool PARTS>
 __global__ __launch_bounds__(256) void attn_decode_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k_new,
-    const uint16_t* __restrict__ v_new, long long q_bstride, long long kv_bstride,
+    const uint16_t* __restrict__ v_new, long long q_bstride, long long kv_bstride, QkvParts qp,
     uint16_t* __restrict__ k_cache, uint16_t* __restrict__ v_cache,
     const int32_t* __restrict__ pos, uint16_t* __restrict__ out, int H, int W,
     float scale_log2) {
@@ -43,9 +66,26 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
   const long long slab = static_cast<long long>(bh) * W * HD;
 
   float qf[8], knf[8], vnf[8];
-  unpack8(*reinterpret_cast<const uint4*>(q + b * q_bstride + h * HD + 8 * dc), qf);
-  const uint4 kraw = *reinterpret_cast<const uint4*>(k_new + b * kv_bstride + h * HD + 8 * dc);
-  const uint4 vraw = *reinterpret_cast<const uint4*>(v_new + b * kv_bstride + h * HD + 8 * dc);
+  uint4 qraw, kraw, vraw;
+  if (PARTS) {
+    // the workgroup's q, k and v rows (3 HD values) summed once, one value
+    // per thread, rounded to bf16 and shared through LDS
+    __shared__ __align__(16) uint16_t qkv_s[3 * HD];
+    for (int e = threadIdx.x; e < 3 * HD; e += 256) {
+      const int part = e / HD, dim = e - part * HD;
+      const int col = (part == 0 ? 0 : part == 1 ? qp.koff : qp.voff) + h * HD + dim;
+      qkv_s[e] = f2bf(sum_parts1(qp, b, col));
+    }
+    __syncthreads();
+    qraw = *reinterpret_cast<const uint4*>(qkv_s + 8 * dc);
+    kraw = *reinterpret_cast<const uint4*>(qkv_s + HD + 8 * dc);
+    vraw = *reinterpret_cast<const uint4*>(qkv_s + 2 * HD + 8 * dc);
+  } else {
+    qraw = *reinterpret_cast<const uint4*>(q + b * q_bstride + h * HD + 8 * dc);
+    kraw = *reinterpret_cast<const uint4*>(k_new + b * kv_bstride + h * HD + 8 * dc);
+    vraw = *reinterpret_cast<const uint4*>(v_new + b * kv_bstride + h * HD + 8 * dc);
+  }
+  unpack8(qraw, qf);
   unpack8(kraw, knf);
   unpack8(vraw, vnf);
   if (wave == 0 && kk == 0) {
@@ -193,12 +233,44 @@ extern "C" int32_t llmy_banded_attn_decode_bf16(
   if (B == 0) return 0;
   const float scale_log2 = scale * 1.4426950408889634f;
   const hipStream_t s = as_stream(stream);
+  const QkvParts none{};
   if (head_dim == 64) {
-    hipLaunchKernelGGL(attn_decode_kernel<64>, dim3(B * H), dim3(256), 0, s, q, k_new, v_new,
-                       q_bstride, kv_bstride, k_cache, v_cache, pos, out, H, W, scale_log2);
+    hipLaunchKernelGGL((attn_decode_kernel<64, false>), dim3(B * H), dim3(256), 0, s, q, k_new,
+                       v_new, q_bstride, kv_bstride, none, k_cache, v_cache, pos, out, H, W,
+                       scale_log2);
   } else {
-    hipLaunchKernelGGL(attn_decode_kernel<128>, dim3(B * H), dim3(256), 0, s, q, k_new, v_new,
-                       q_bstride, kv_bstride, k_cache, v_cache, pos, out, H, W, scale_log2);
+    hipLaunchKernelGGL((attn_decode_kernel<128, false>), dim3(B * H), dim3(256), 0, s, q, k_new,
+                       v_new, q_bstride, kv_bstride, none, k_cache, v_cache, pos, out, H, W,
+                       scale_log2);
+  }
+  return launch_status();
+}
+
+extern "C" int32_t llmy_banded_attn_decode_parts_bf16(
+    const float* parts, int32_t nparts, int64_t part_stride, int64_t row_stride, int32_t k_off,
+    int32_t v_off, llmy_bf16* k_cache, llmy_bf16* v_cache, const int32_t* pos, llmy_bf16* out,
+    int32_t B, int32_t H, int32_t head_dim, int32_t W, float scale, void* stream) {
+  LLMY_REQUIRE(B >= 0 && H > 0 && W > 0 && (head_dim == 64 || head_dim == 128) && nparts >= 1);
+  if (B == 0) return 0;
+  LLMY_REQUIRE(parts && k_cache && v_cache && pos && out);
+  const int64_t Hhd = static_cast<int64_t>(H) * head_dim;
+  LLMY_REQUIRE(k_off >= Hhd && v_off >= k_off + Hhd && row_stride >= v_off + Hhd);
+  LLMY_REQUIRE(k_off % 8 == 0 && v_off % 8 == 0 && row_stride % 4 == 0 &&
+               (nparts == 1 || (part_stride >= static_cast<int64_t>(B) * row_stride &&
+                                part_stride % 4 == 0)));
+  LLMY_REQUIRE(aligned(parts, 16) && aligned(k_cache, 16) && aligned(v_cache, 16) &&
+               aligned(out, 2));
+  const float scale_log2 = scale * 1.4426950408889634f;
+  const hipStream_t s = as_stream(stream);
+  const QkvParts qp{parts, nparts, part_stride, row_stride, k_off, v_off};
+  if (head_dim == 64) {
+    hipLaunchKernelGGL((attn_decode_kernel<64, true>), dim3(B * H), dim3(256), 0, s, nullptr,
+                       nullptr, nullptr, 0ll, 0ll, qp, k_cache, v_cache, pos, out, H, W,
+                       scale_log2);
+  } else {
+    hipLaunchKernelGGL((attn_decode_kernel<128, true>), dim3(B * H), dim3(256), 0, s, nullptr,
+                       nullptr, nullptr, 0ll, 0ll, qp, k_cache, v_cache, pos, out, H, W,
+                       scale_log2);
   }
   return launch_status();
 }

@@ -791,6 +791,7 @@ struct Buffers {  // activations for `rows` token rows
   float* parts = nullptr;  // decode: mixer output projection partials [n, rows, D]
   int max_parts = 0;
   float* proj_parts = nullptr;  // decode: GDN input projection partials [D/256, rows, nproj16]
+  float* qkv_parts = nullptr;   // decode: attention q/k/v projection partials [D/256, rows, 3 Hhd]
   uint16_t *h = nullptr, *qkv = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *ao = nullptr,
            *go = nullptr, *act = nullptr, *gq = nullptr, *gk = nullptr, *gv = nullptr;
   int32_t *tokens = nullptr, *idx = nullptr, *counts = nullptr, *offsets = nullptr,
@@ -941,6 +942,8 @@ void alloc_buffers(const Config& c, int rows, int B, int T, Buffers& b) {
   }
   if (T == 1 && rows <= 64 && D % 256 == 0 && D / 256 <= 8 && c.has_gdn())
     b.proj_parts = b.arena.zeros<float>(static_cast<size_t>(D / 256) * rows * c.nproj16());
+  if (T == 1 && rows <= 64 && D % 256 == 0 && D / 256 <= 8 && c.has(kAttn))
+    b.qkv_parts = b.arena.zeros<float>(static_cast<size_t>(D / 256) * rows * 3 * Hhd);
   if (c.has(kCsa) || c.has(kHca)) {
     int kw = 0, rmin = 1 << 30;
     int64_t ws = 16;
@@ -1478,12 +1481,23 @@ void attn_decode(const Model& m, const Layer& L, LayerState& st, Buffers& b, int
                  const int32_t* pos, void* out, int epi, hipStream_t s) {
   const Config& c = m.cfg;
   const int D = c.d_model, Hhd = c.attn_heads * c.attn_head_dim;
-  linear(b.h, L.wqkv, b.qkv, nullptr, B, 3 * Hhd, D, kStoreBf16, s);
-  check_call(llmy_banded_attn_decode_bf16(b.qkv, b.qkv + Hhd, b.qkv + 2 * Hhd, 3 * Hhd, 3 * Hhd,
-                                          st.k, st.v, pos, b.ao, B, c.attn_heads, c.attn_head_dim,
-                                          c.window,
-                                          1.0f / std::sqrt(static_cast<float>(c.attn_head_dim)), s),
-             "llmy_banded_attn_decode_bf16");
+  const float scale = 1.0f / std::sqrt(static_cast<float>(c.attn_head_dim));
+  if (b.qkv_parts != nullptr) {
+    // q/k/v as partial products, summed and rounded by the attention kernel
+    linear(b.h, L.wqkv, b.qkv_parts, nullptr, B, 3 * Hhd, D, kPartialF32, s);
+    check_call(llmy_banded_attn_decode_parts_bf16(b.qkv_parts, D / 256,
+                                                  static_cast<int64_t>(B) * 3 * Hhd, 3 * Hhd, Hhd,
+                                                  2 * Hhd, st.k, st.v, pos, b.ao, B,
+                                                  c.attn_heads, c.attn_head_dim, c.window, scale,
+                                                  s),
+               "llmy_banded_attn_decode_parts_bf16");
+  } else {
+    linear(b.h, L.wqkv, b.qkv, nullptr, B, 3 * Hhd, D, kStoreBf16, s);
+    check_call(llmy_banded_attn_decode_bf16(b.qkv, b.qkv + Hhd, b.qkv + 2 * Hhd, 3 * Hhd,
+                                            3 * Hhd, st.k, st.v, pos, b.ao, B, c.attn_heads,
+                                            c.attn_head_dim, c.window, scale, s),
+               "llmy_banded_attn_decode_bf16");
+  }
   linear(b.ao, L.wo, out, nullptr, B, D, Hhd, epi, s);
 }
 

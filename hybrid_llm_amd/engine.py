@@ -366,6 +366,13 @@ class HybridDecoder:
         self.proj_parts = B <= 64 and D % 256 == 0 and D // 256 <= 8 and cfg.has_gdn
         if self.proj_parts:
             self.buf["proj_parts"] = torch.zeros(D // 256, B, nproj, dtype=f32, device=dev)
+        # ... and the attention q/k/v projection: its partials are summed (and
+        # rounded to bf16, as the projection would have stored them) by the
+        # attention decode kernel
+        self.qkv_parts = (B <= 64 and D % 256 == 0 and D // 256 <= 8
+                          and "attn" in cfg.layer_kinds)
+        if self.qkv_parts:
+            self.buf["qkv_parts"] = torch.zeros(D // 256, B, 3 * Ha * hd, dtype=f32, device=dev)
         self._pending: tuple | None = None
         if self.mhc:
             Sm = cfg.mhc_streams
@@ -427,13 +434,19 @@ class HybridDecoder:
         p = f"L{l}."
         Hhd = cfg.attn_heads * cfg.attn_head_dim
         B, H, hd = self.B, cfg.attn_heads, cfg.attn_head_dim
-        ops.linear(b["h"], w[p + "wqkv"], out=b["qkv"], layout=ops.LAYOUT_PACKED)
-        qkv = b["qkv"]
-        q = qkv[:, :Hhd].view(B, H, hd)
-        kn = qkv[:, Hhd:2 * Hhd].view(B, H, hd)
-        vn = qkv[:, 2 * Hhd:].view(B, H, hd)
-        ops.banded_attn_decode(q, kn, vn, st["k"], st["v"], self.pos, cfg.attn_scale,
-                               out=b["ao"])
+        if self.qkv_parts:
+            ops.linear(b["h"], w[p + "wqkv"], out=b["qkv_parts"], epilogue=ops.EPI_PARTIAL_F32,
+                       layout=ops.LAYOUT_PACKED)
+            ops.banded_attn_decode_parts(b["qkv_parts"], Hhd, 2 * Hhd, st["k"], st["v"],
+                                         self.pos, cfg.attn_scale, out=b["ao"])
+        else:
+            ops.linear(b["h"], w[p + "wqkv"], out=b["qkv"], layout=ops.LAYOUT_PACKED)
+            qkv = b["qkv"]
+            q = qkv[:, :Hhd].view(B, H, hd)
+            kn = qkv[:, Hhd:2 * Hhd].view(B, H, hd)
+            vn = qkv[:, 2 * Hhd:].view(B, H, hd)
+            ops.banded_attn_decode(q, kn, vn, st["k"], st["v"], self.pos, cfg.attn_scale,
+                                   out=b["ao"])
         if self.defer_resid:
             parts = b["parts"][:Hhd // 256]
             ops.linear(b["ao"].view(B, Hhd), w[p + "wo"], out=parts,

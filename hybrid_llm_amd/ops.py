@@ -286,6 +286,29 @@ def banded_attn_decode(q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor
     return out
 
 
+def banded_attn_decode_parts(parts: torch.Tensor, k_off: int, v_off: int, k_cache: torch.Tensor,
+                             v_cache: torch.Tensor, pos: torch.Tensor, scale: float | None = None,
+                             out: torch.Tensor | None = None) -> torch.Tensor:
+    """banded_attn_decode with q / k_new / v_new given as the partial products
+    [P, B, row] fp32 of their projection (linear(..., epilogue=EPI_PARTIAL_F32)):
+    q at column 0, k at k_off, v at v_off; the slices are summed in order and
+    rounded to bf16 inside the kernel."""
+    B, H, W, hd = k_cache.shape
+    _check(parts, torch.float32, "parts")
+    if parts.dim() != 3 or parts.shape[1] != B or parts.stride(2) != 1:
+        raise ValueError("parts must be [P, B, row] fp32 with contiguous rows")
+    _check(k_cache, torch.bfloat16, "k_cache")
+    _check(v_cache, torch.bfloat16, "v_cache", (B, H, W, hd))
+    _check(pos, torch.int32, "pos", (B,))
+    if out is None:
+        out = torch.empty(B, H, hd, dtype=torch.bfloat16, device=parts.device)
+    scale = hd ** -0.5 if scale is None else scale
+    _lib.call("llmy_banded_attn_decode_parts_bf16", _ptr(parts), parts.shape[0], parts.stride(0),
+              parts.stride(1), k_off, v_off, _ptr(k_cache), _ptr(v_cache), _ptr(pos), _ptr(out),
+              B, H, hd, W, scale, _stream())
+    return out
+
+
 # --------------------------------------------------------------------------- GDN
 def _reset_arg(reset, shape, dev):
     """A reset mask as the device int32 array the kernels read (nonzero = reset)."""

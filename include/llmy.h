@@ -160,6 +160,20 @@ int32_t llmy_banded_attn_decode_bf16(const llmy_bf16* q, const llmy_bf16* k_new,
                                      llmy_bf16* out, int32_t B, int32_t H,
                                      int32_t head_dim, int32_t W, float scale,
                                      void* stream);
+/* The same step with q, k_new and v_new given as the partial products of a
+ * decode projection (llmy_linear_bf16 with epilogue 4): parts [nparts][B][row_stride]
+ * fp32, part_stride floats apart; q at column 0, k at k_off, v at v_off.  The
+ * slices are summed in order and rounded to bf16 -- the values the projection
+ * would have stored as bf16 -- so it computes what the call above computes on
+ * that projection.  No counterpart in the reference: it lets the decode step
+ * run its q/k/v projection on the partial-product kernel. */
+int32_t llmy_banded_attn_decode_parts_bf16(const float* parts, int32_t nparts,
+                                           int64_t part_stride, int64_t row_stride,
+                                           int32_t k_off, int32_t v_off, llmy_bf16* k_cache,
+                                           llmy_bf16* v_cache, const int32_t* pos,
+                                           llmy_bf16* out, int32_t B, int32_t H,
+                                           int32_t head_dim, int32_t W, float scale,
+                                           void* stream);
 
 /* --- Gated delta rule, prefill (chunked; model/layers/gated_deltanet.py:140-149) */
 

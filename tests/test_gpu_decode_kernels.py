@@ -215,6 +215,54 @@ def test_attn_decode_from_fused_projection_view():
     close_bf16(out, ref)
 
 
+@pytest.mark.parametrize("B,H,hd,W,P", [(64, 16, 64, 2048, 4), (5, 3, 128, 100, 2),
+                                        (1, 2, 64, 16, 1), (7, 4, 64, 64, 8)])
+def test_attn_decode_from_partial_products(B, H, hd, W, P):
+    # q/k/v as per-K-block partial products [P, B, 3 H hd]: the kernel sums the
+    # slices in order and rounds to bf16, so the step equals the bf16 entry
+    # point on that sum bit for bit (output and both caches)
+    g = torch.Generator().manual_seed(B * 31 + P)
+    Hhd = H * hd
+    parts = torch.randn(P, B, 3 * Hhd, generator=g) / P ** 0.5  # sums of unit variance
+    acc = parts[0].clone()
+    for s in range(1, P):
+        acc += parts[s]
+    qkv = acc.to(torch.bfloat16)
+    kc = _bf(torch.randn(B, H, W, hd, generator=g))
+    vc = _bf(torch.randn(B, H, W, hd, generator=g))
+    pos = torch.randint(0, 3 * W, (B,), generator=g, dtype=torch.int32)
+    q, kn, vn = (qkv[:, i * Hhd:(i + 1) * Hhd].reshape(B, H, hd).contiguous() for i in range(3))
+    kc1, vc1, kc2, vc2 = kc.cuda(), vc.cuda(), kc.cuda(), vc.cuda()
+    out1 = ops().banded_attn_decode(q.cuda(), kn.cuda(), vn.cuda(), kc1, vc1, pos.cuda())
+    out2 = ops().banded_attn_decode_parts(parts.cuda(), Hhd, 2 * Hhd, kc2, vc2, pos.cuda())
+    assert torch.equal(out1.view(torch.int16), out2.view(torch.int16))
+    assert torch.equal(kc1.view(torch.int16), kc2.view(torch.int16))
+    assert torch.equal(vc1.view(torch.int16), vc2.view(torch.int16))
+    ref, _, _ = banded_attention_decode(q, kn, vn, kc, vc, pos.long())
+    close_bf16(out2, ref)
+
+
+def test_attn_decode_parts_after_projection():
+    # the engine's path: linear(..., EPI_PARTIAL_F32) then the parts entry
+    # equals the bf16 projection then the bf16 entry, bit for bit
+    B, H, hd, W, D = 64, 16, 64, 256, 1024
+    g = torch.Generator().manual_seed(5)
+    x = _bf(torch.randn(B, D, generator=g)).cuda()
+    w = ops().pack_weights(_bf(torch.randn(3 * H * hd, D, generator=g) * 0.03).cuda())
+    kc = _bf(torch.randn(B, H, W, hd, generator=g)).cuda()
+    vc = _bf(torch.randn(B, H, W, hd, generator=g)).cuda()
+    pos = torch.randint(0, 2 * W, (B,), generator=g, dtype=torch.int32).cuda()
+    qkv = ops().linear(x, w, layout=ops().LAYOUT_PACKED)
+    q, kn, vn = (qkv[:, i * H * hd:(i + 1) * H * hd].view(B, H, hd) for i in range(3))
+    kc1, vc1 = kc.clone(), vc.clone()
+    out1 = ops().banded_attn_decode(q, kn, vn, kc1, vc1, pos)
+    parts = ops().linear(x, w, epilogue=ops().EPI_PARTIAL_F32, layout=ops().LAYOUT_PACKED)
+    out2 = ops().banded_attn_decode_parts(parts, H * hd, 2 * H * hd, kc, vc, pos)
+    assert torch.equal(out1.view(torch.int16), out2.view(torch.int16))
+    assert torch.equal(kc1.view(torch.int16), kc.view(torch.int16))
+    assert torch.equal(vc1.view(torch.int16), vc.view(torch.int16))
+
+
 # ---------------------------------------------------------------- GDN step
 @pytest.mark.parametrize("B,H,d,with_gate", [(64, 16, 128, False), (64, 16, 64, True),
                                              (3, 2, 64, False)])
