@@ -138,8 +138,11 @@ def attn_decode_sets(cfg, B, gen):
     for _ in range(3):
         kc = torch.empty(B, H, W, hd, dtype=torch.bfloat16, device="cuda").normal_(generator=gen)
         vc = torch.empty_like(kc).normal_(generator=gen)
-        qkv = torch.empty(B, 3 * H * hd, dtype=torch.bfloat16, device="cuda").normal_(generator=gen)
-        sets.append((kc, vc, qkv))
+        # q/k/v as the decode step hands them over: the projection's partial
+        # products, 4 fp32 slices (d_model / 256) of [B, 3 H hd]
+        parts = torch.empty(cfg.d_model // 256, B, 3 * H * hd, device="cuda").normal_(
+            generator=gen)
+        sets.append((kc, vc, parts))
     return sets
 
 
@@ -151,20 +154,22 @@ def attn_decode_launcher(cfg, B, sets):
     out = torch.empty(B, H, hd, dtype=torch.bfloat16, device="cuda")
 
     def launch(i):
-        kc, vc, qkv = sets[i % 3]
+        kc, vc, parts = sets[i % 3]
         Hhd = H * hd
-        p = qkv.data_ptr()
-        _lib.call("llmy_banded_attn_decode_bf16", p, p + 2 * Hhd, p + 4 * Hhd, 3 * Hhd, 3 * Hhd,
-                  kc.data_ptr(), vc.data_ptr(), pos.data_ptr(), out.data_ptr(), B, H, hd, W,
-                  cfg.attn_scale, torch.cuda.current_stream().cuda_stream)
+        _lib.call("llmy_banded_attn_decode_parts_bf16", parts.data_ptr(), parts.shape[0],
+                  parts.stride(0), parts.stride(1), Hhd, 2 * Hhd, kc.data_ptr(), vc.data_ptr(),
+                  pos.data_ptr(), out.data_ptr(), B, H, hd, W, cfg.attn_scale,
+                  torch.cuda.current_stream().cuda_stream)
     return launch
 
 
 def attn_decode_bytes(cfg, B):
-    """Algorithmic bytes of one decode launch: the K and V windows read, the new
-    K/V rows written, the q/k/v rows read and the output written (bf16)."""
+    """Algorithmic bytes of one decode launch as the step runs it: the K and V
+    windows read, the new K/V rows written (bf16), the q/k/v partial products
+    read (d_model / 256 fp32 slices) and the output written (bf16)."""
     H, hd, W = cfg.attn_heads, cfg.attn_head_dim, cfg.window
-    return 2 * B * H * W * hd * 2 + 2 * B * H * hd * 2 + 4 * B * H * hd * 2
+    P = cfg.d_model // 256
+    return 2 * B * H * W * hd * 2 + 2 * B * H * hd * 2 + P * 3 * B * H * hd * 4 + B * H * hd * 2
 
 
 def step_bytes(cfg, B: int) -> dict:
@@ -786,7 +791,7 @@ def main():
     torch.cuda.empty_cache()
     (us, us_med), bytes_ = time_attn_decode(cfg, B, args.kernel_iters, gen)
     achieved = bytes_ / (us * 1e-6) / 1e9
-    roofline = {"kernel": "attn_decode_kernel<64>", "bound": "hbm", "achieved": round(achieved, 1),
+    roofline = {"kernel": "attn_decode_kernel<64, true>", "bound": "hbm", "achieved": round(achieved, 1),
                 "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                 "traffic": None if traffic is None else round(traffic["bytes"]),
                 "avg_us": round(us, 2), "median_us": round(us_med, 2),
