@@ -10,8 +10,9 @@
 // v_mfma_f32_32x32x16_bf16, so LDS traffic is (BM/64 + BN/64) fragment reads
 // per (BM/64)(BN/64) MFMAs.  256 x 256 tiles run one workgroup per CU (the
 // accumulators fill the AGPR half of the register file); 128-row tiles run
-// two per CU, one wavefront of each per SIMD, so one workgroup's barrier and
-// load waits are covered by the other's MFMAs.  The MFMA takes the weight
+// two per CU when there are more tiles than CUs, one wavefront of each per
+// SIMD, so one workgroup's barrier and load waits are covered by the other's
+// MFMAs, and one per CU with a deeper ring otherwise.  The MFMA takes the weight
 // fragment as its first operand, so each lane ends with four consecutive
 // output columns per register group and stores them as one vector.
 //
@@ -430,10 +431,15 @@ int32_t dense_gemm_mfma(const uint16_t* x, const uint16_t* w, void* out, const f
   g.M = M;
   g.N = N;
   g.packed = packed;
-  // 256 x 256 tiles (one workgroup per CU) when there is one per CU, else
-  // 128 x 128 (two workgroups per CU); both 2 stages of K 64, in groups of 4
-  // m-tiles.
+  // 256 x 256 tiles (one workgroup per CU, 4 stages of K 32) when there is
+  // one per CU; else 128 x 128 tiles, two workgroups per CU with 4 stages of
+  // K 32 when there are more tiles than CUs, one per CU with 3 stages of K 64
+  // otherwise (the deeper ring covers the load latency that a lone
+  // workgroup's 4 wavefronts cannot); all in groups of 4 m-tiles.  Every
+  // choice accumulates each output over k in the same order, so the results
+  // do not depend on it.
   const bool wide = static_cast<long long>((M + 255) / 256) * ((N + 255) / 256) >= 256;
+  const bool crowded = static_cast<long long>((M + 127) / 128) * ((N + 127) / 128) > 256;
   const int bt = wide ? 256 : 128;
   // A narrow column tail (N = 256 n + 16 .. 64, e.g. a 4096-row projection
   // plus its 16 gate rows) would cost a whole 256-wide tile per m-tile, often
@@ -451,14 +457,14 @@ int32_t dense_gemm_mfma(const uint16_t* x, const uint16_t* w, void* out, const f
     const long long main_items = static_cast<long long>(t.m_tiles) * t.n_tiles;
     if (main_items >= (1ll << 31) - kNumXcd) return static_cast<int32_t>(hipErrorInvalidValue);
     int32_t st = 0;
-#define LLMY_DENSE_T(T_, OCC_, ARGS_, ITEMS_)                                                      \
-  switch (epi) {                                                                                   \
-    case kDenseBf16: st = launch_tiles<T_, T_, 64, 2, kDenseBf16, OCC_>(ARGS_, ITEMS_, s); break; \
-    case kDenseF32: st = launch_tiles<T_, T_, 64, 2, kDenseF32, OCC_>(ARGS_, ITEMS_, s); break;   \
-    case kDenseResid: st = launch_tiles<T_, T_, 64, 2, kDenseResid, OCC_>(ARGS_, ITEMS_, s); break; \
-    default: st = launch_tiles<T_, T_, 64, 2, kDenseGated, OCC_>(ARGS_, ITEMS_, s); break;        \
+#define LLMY_DENSE_T(T_, BK_, NS_, OCC_, ARGS_, ITEMS_)                                           \
+  switch (epi) {                                                                                \
+    case kDenseBf16: st = launch_tiles<T_, T_, BK_, NS_, kDenseBf16, OCC_>(ARGS_, ITEMS_, s); break; \
+    case kDenseF32: st = launch_tiles<T_, T_, BK_, NS_, kDenseF32, OCC_>(ARGS_, ITEMS_, s); break;   \
+    case kDenseResid: st = launch_tiles<T_, T_, BK_, NS_, kDenseResid, OCC_>(ARGS_, ITEMS_, s); break; \
+    default: st = launch_tiles<T_, T_, BK_, NS_, kDenseGated, OCC_>(ARGS_, ITEMS_, s); break;        \
   }
-    LLMY_DENSE_T(256, 1, t, main_items)
+    LLMY_DENSE_T(256, 32, 4, 1, t, main_items)
     if (st != 0) return st;
 #undef LLMY_DENSE_T
     // the tail: rows n_main .. N-1 of w (for the packed order too: 16-row
@@ -475,15 +481,16 @@ int32_t dense_gemm_mfma(const uint16_t* x, const uint16_t* w, void* out, const f
   g.group_m = 4;
   const long long items = static_cast<long long>(g.m_tiles) * g.n_tiles;
   if (items >= (1ll << 31) - kNumXcd) return static_cast<int32_t>(hipErrorInvalidValue);
-#define LLMY_DENSE(T_, OCC_)                                                                 \
-  switch (epi) {                                                                             \
-    case kDenseBf16: return launch_tiles<T_, T_, 64, 2, kDenseBf16, OCC_>(g, items, s); \
-    case kDenseF32: return launch_tiles<T_, T_, 64, 2, kDenseF32, OCC_>(g, items, s);   \
-    case kDenseResid: return launch_tiles<T_, T_, 64, 2, kDenseResid, OCC_>(g, items, s); \
-    default: return launch_tiles<T_, T_, 64, 2, kDenseGated, OCC_>(g, items, s);        \
+#define LLMY_DENSE(T_, BK_, NS_, OCC_)                                                          \
+  switch (epi) {                                                                               \
+    case kDenseBf16: return launch_tiles<T_, T_, BK_, NS_, kDenseBf16, OCC_>(g, items, s); \
+    case kDenseF32: return launch_tiles<T_, T_, BK_, NS_, kDenseF32, OCC_>(g, items, s);   \
+    case kDenseResid: return launch_tiles<T_, T_, BK_, NS_, kDenseResid, OCC_>(g, items, s); \
+    default: return launch_tiles<T_, T_, BK_, NS_, kDenseGated, OCC_>(g, items, s);        \
   }
-  if (wide) LLMY_DENSE(256, 1)
-  LLMY_DENSE(128, 2)
+  if (wide) LLMY_DENSE(256, 32, 4, 1)
+  if (crowded) LLMY_DENSE(128, 32, 4, 2)
+  LLMY_DENSE(128, 64, 3, 1)
 #undef LLMY_DENSE
 }
 
