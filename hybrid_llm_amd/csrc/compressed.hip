@@ -899,6 +899,9 @@ __global__ __launch_bounds__(512) void cmp_apply_mfma_kernel(
   const int NP = (nsb + 31) & ~31;
   const int RS = NP + 4;                                // fp32 per P row (16-byte pad)
   uint16_t* vt = reinterpret_cast<uint16_t*>(pmf + 32 * RS);   // [256][kApplyVtPitch]
+  // after V^T: s_used (kept in the dynamic area, whose 16-byte alignment a
+  // static LDS variable ahead of it would break)
+  int& s_used = *reinterpret_cast<int*>(vt + 256 * kApplyVtPitch);
   const int ndb = (Dv + 255) / 256;
   const int nqb = (T + 31) / 32;
   const int blk = blockIdx.x / ndb;
@@ -913,9 +916,14 @@ __global__ __launch_bounds__(512) void cmp_apply_mfma_kernel(
   const int c0 = db * 256;
   const int base = band_W > 0 ? t0 - band_W + 1 : 0;    // key of block slot 0
 
-  // ---- P: the 32 queries' weights summed over the heads (head order)
+  // ---- P: the 32 queries' weights summed over the heads (head order).
+  // Memory rows: s_used = 1 + the last slot any of them weighs (0: none);
+  // chunks past it hold only zero weights and are skipped (a causal row sees
+  // a prefix of the slots).
   for (int i = tid; i < 32 * RS; i += 512) pmf[i] = 0.f;
+  if (tid == 0) s_used = 0;
   __syncthreads();
+  int used = 0;
   const int64_t lb0 = (static_cast<int64_t>(b) * T + t0) * H * Kmax;
   if (il && H <= kApplyMaxH && nq * Kmax <= 1024) {
     // every head's (slot, weight) entries requested at once (two per thread
@@ -944,7 +952,10 @@ __global__ __launch_bounds__(512) void cmp_apply_mfma_kernel(
       if (hh >= H) break;  // uniform
 #pragma unroll
       for (int r = 0; r < 2; ++r)
-        if (ir[hh][r] >= 0 && ir[hh][r] < nslots) pmf[pr[r] + ir[hh][r]] += wr[hh][r];
+        if (ir[hh][r] >= 0 && ir[hh][r] < nslots) {
+          pmf[pr[r] + ir[hh][r]] += wr[hh][r];
+          if (wr[hh][r] != 0.f) used = max(used, ir[hh][r] + 1);
+        }
       __syncthreads();
     }
   } else if (il) {
@@ -953,7 +964,11 @@ __global__ __launch_bounds__(512) void cmp_apply_mfma_kernel(
         const int qq = e / Kmax, j = e - qq * Kmax;
         const int64_t o = lb0 + (static_cast<int64_t>(qq) * H + hh) * Kmax + j;
         const int idx = il[o];
-        if (idx >= 0 && idx < nslots) pmf[qq * RS + idx] += wl[o];
+        if (idx >= 0 && idx < nslots) {
+          const float w = wl[o];
+          pmf[qq * RS + idx] += w;
+          if (w != 0.f) used = max(used, idx + 1);
+        }
       }
       __syncthreads();
     }
@@ -963,10 +978,17 @@ __global__ __launch_bounds__(512) void cmp_apply_mfma_kernel(
       const int64_t o = lb0 + static_cast<int64_t>(qq) * H * Kmax + j;
       float acc = 0.f;
       for (int hh = 0; hh < H; ++hh) acc += wl[o + static_cast<int64_t>(hh) * Kmax];
-      pmf[qq * RS + j + (band_W > 0 ? qq : 0)] = acc;
+      const int col = j + (band_W > 0 ? qq : 0);
+      pmf[qq * RS + col] = acc;
+      if (acc != 0.f) used = max(used, col + 1);
     }
-    __syncthreads();
   }
+  if (band_W == 0) {  // uniform; a band's slots are nearly all weighed
+    used = static_cast<int>(wave_max(static_cast<float>(used)));  // exact: used <= NP
+    if (lane == 0 && used > 0) atomicMax(&s_used, used);
+  }
+  __syncthreads();
+  const int np_used = band_W == 0 ? min(NP, (s_used + 31) & ~31) : NP;
 
   // ---- V^T staging: thread (slot pair p, channel group g) fetches the two
   // rows' 8 channels (rows clamped into the sequence; their weights are 0)
@@ -1002,11 +1024,11 @@ __global__ __launch_bounds__(512) void cmp_apply_mfma_kernel(
 #pragma unroll
   for (int r = 0; r < 16; ++r) acc[r] = 0.f;
   fetch(0);
-  for (int s0 = 0; s0 < NP; s0 += 32) {
+  for (int s0 = 0; s0 < np_used; s0 += 32) {
     __syncthreads();   // the previous chunk's V^T reads are done
     stage();
     __syncthreads();
-    if (s0 + 32 < NP) fetch(s0 + 32);
+    if (s0 + 32 < np_used) fetch(s0 + 32);
     if (w_ok) {
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
@@ -1250,7 +1272,7 @@ int32_t apply_launch(const float* wl, const int32_t* il, int Kmax, int H, int B,
     }
     const int nsb = band_W > 0 ? nslots + 31 : nslots;
     const int NP = (nsb + 31) & ~31;
-    const size_t lds = static_cast<size_t>(32) * (NP + 4) * 4 + 256 * kApplyVtPitch * 2;
+    const size_t lds = static_cast<size_t>(32) * (NP + 4) * 4 + 256 * kApplyVtPitch * 2 + 16;
     const int64_t nblk = static_cast<int64_t>(B) * ((T + 31) / 32) * ((Dv + 255) / 256);
     if (nblk >= (1ll << 31)) return static_cast<int32_t>(hipErrorInvalidValue);
     hipLaunchKernelGGL(cmp_apply_mfma_kernel, dim3(static_cast<unsigned>(nblk)), dim3(512), lds,
