@@ -10,6 +10,8 @@
 // r = t*k + j, grouped by expert, counts = bincount, offsets = exclusive
 // cumsum) with the order inside an expert pinned to ascending r, i.e. the
 // order of a stable sort of the expert ids.
+#include <algorithm>
+
 #include "common.hpp"
 #include "abi_util.hpp"
 
@@ -539,17 +541,19 @@ __global__ __launch_bounds__(256) void moe_route_norm_kernel(
   topk_softmax_store(mine, E, k, lane, idx_out + t * k, gates_out + t * k);
 }
 
-// The same pre-MoE norms and router for a sequence (nparts == 0), 32 tokens
-// per workgroup, 8 wavefronts: wave w normalises tokens 4 w .. 4 w + 3 with
-// moe_route_norm_kernel's arithmetic (so h2 is the same bits) and keeps the
-// router input rows in LDS (fp32, rows padded to D + 4); the logits [32
-// tokens x E <= 32 experts] then run as fp32 MFMAs (v_mfma_f32_32x32x2_f32:
-// exact fp32 products, fp32 sums), wave w over the D/8-wide slice w of the
-// row, and the eight partial tiles are added in wave order.  W_r is read as
-// 16-byte pieces along d straight from global memory (L2-resident, 96 KiB at
-// C5), one piece feeding two MFMAs.  Then wave w takes the top-k of its four
-// tokens.
-template <int NCH>
+// The same pre-MoE norms and router for a sequence (nparts == 0), 8 TPW
+// tokens per workgroup, 8 wavefronts: wave w normalises tokens TPW w ..
+// TPW w + TPW - 1 with moe_route_norm_kernel's arithmetic (so h2 is the same
+// bits) and keeps the router input rows in LDS (fp32, rows padded to D + 4);
+// the logits [32 rows x E <= 32 experts] then run as fp32 MFMAs
+// (v_mfma_f32_32x32x2_f32: exact fp32 products, fp32 sums; with 16 tokens
+// rows 16..31 repeat rows 0..15 and are not used), wave w over the D/8-wide
+// slice w of the row, and the eight partial tiles are added in wave order.
+// W_r is read as 16-byte pieces along d straight from global memory
+// (L2-resident, 96 KiB at C5), one piece feeding two MFMAs.  Then wave w
+// takes the top-k of its tokens.  A token's results do not depend on TPW;
+// TPW = 2 gives a 4096-token prefill 256 workgroups, one per CU.
+template <int NCH, int TPW>
 __global__ __launch_bounds__(512) void moe_route_norm_blk_kernel(
     const float* __restrict__ x, const float* __restrict__ ffn_w,
     const float* __restrict__ router_w, const float* __restrict__ w_router,
@@ -558,9 +562,11 @@ __global__ __launch_bounds__(512) void moe_route_norm_blk_kernel(
   constexpr int D = NCH * 256;
   constexpr int RS = D + 4;          // fp32 per LDS row
   constexpr int KW = D / 8;          // d per wave in the logits
-  extern __shared__ float rs[];      // [32][RS] router input; then [8][32][32] partials
+  constexpr int TB = 8 * TPW;        // tokens per workgroup
+  static_assert(TPW == 2 || TPW == 4, "tokens per wave");
+  extern __shared__ float rs[];      // [TB][RS] router input; then [8][32][32] partials
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int t0 = blockIdx.x * 32;
+  const int t0 = blockIdx.x * TB;
   float4 fw[NCH], rw[NCH];
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
@@ -568,19 +574,19 @@ __global__ __launch_bounds__(512) void moe_route_norm_blk_kernel(
     fw[c] = *reinterpret_cast<const float4*>(ffn_w + d);
     rw[c] = *reinterpret_cast<const float4*>(router_w + d);
   }
-  // ---- norms of tokens 4 wave .. 4 wave + 3 (rows past T: zero router input)
-  float4 v[4][NCH];
+  // ---- norms of tokens TPW wave .. (rows past T: zero router input)
+  float4 v[TPW][NCH];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int t = min(t0 + 4 * wave + j, T - 1);
+  for (int j = 0; j < TPW; ++j) {
+    const int t = min(t0 + TPW * wave + j, T - 1);
 #pragma unroll
     for (int c = 0; c < NCH; ++c)
       v[j][c] = *reinterpret_cast<const float4*>(x + static_cast<long long>(t) * D + 4 * lane +
                                                  256 * c);
   }
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int tl = 4 * wave + j;
+  for (int j = 0; j < TPW; ++j) {
+    const int tl = TPW * wave + j;
     const bool ok = t0 + tl < T;
     float ss = 0.f;
 #pragma unroll
@@ -618,7 +624,7 @@ __global__ __launch_bounds__(512) void moe_route_norm_blk_kernel(
   const int col = lane & 31, hf = lane >> 5;
   const bool e_ok = col < E;
   const float* wrow = w_router + static_cast<long long>(e_ok ? col : 0) * D + KW * wave;
-  const float* arow = rs + col * RS + KW * wave;
+  const float* arow = rs + (col % TB) * RS + KW * wave;
   typedef float f32x16r __attribute__((ext_vector_type(16)));
   f32x16r acc;
 #pragma unroll
@@ -637,10 +643,10 @@ __global__ __launch_bounds__(512) void moe_route_norm_blk_kernel(
 #pragma unroll
   for (int r = 0; r < 16; ++r) part[((r & 3) + 8 * (r >> 2) + 4 * hf) * 32 + col] = acc[r];
   __syncthreads();
-  // ---- wave order sum, then the top-k of tokens 4 wave .. 4 wave + 3
+  // ---- wave order sum, then the top-k of tokens TPW wave ..
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int tl = 4 * wave + j;
+  for (int j = 0; j < TPW; ++j) {
+    const int tl = TPW * wave + j;
     if (t0 + tl >= T) break;   // uniform
     float mine[4] = {0.f, 0.f, 0.f, 0.f};
     if (lane < 32) {
@@ -738,13 +744,13 @@ extern "C" int32_t llmy_moe_route_decode(float* x, const float* parts, int32_t n
     LLMY_ROUTE_NP(NCH, 8);             \
   }
     if (nparts == 0 && T >= kRouteBlockRows && E <= 32) {
-      // a sequence: 32 tokens per workgroup, logits on fp32 MFMA
-      const dim3 grid((T + 31) / 32);
-      const size_t lds = static_cast<size_t>(32) * (D + 4) * sizeof(float);
+      // a sequence: 16 tokens per workgroup, logits on fp32 MFMA
+      const dim3 grid((T + 15) / 16);
+      const size_t lds = std::max<size_t>(static_cast<size_t>(16) * (D + 4), 8 * 1024) * sizeof(float);
       switch (D) {
-        case 256: hipLaunchKernelGGL((moe_route_norm_blk_kernel<1>), grid, dim3(512), lds, s, x, ffn_w, router_w, w_router, h2, idx, gates, T, E, k, eps); break;
-        case 512: hipLaunchKernelGGL((moe_route_norm_blk_kernel<2>), grid, dim3(512), lds, s, x, ffn_w, router_w, w_router, h2, idx, gates, T, E, k, eps); break;
-        default: hipLaunchKernelGGL((moe_route_norm_blk_kernel<4>), grid, dim3(512), lds, s, x, ffn_w, router_w, w_router, h2, idx, gates, T, E, k, eps); break;
+        case 256: hipLaunchKernelGGL((moe_route_norm_blk_kernel<1, 2>), grid, dim3(512), lds, s, x, ffn_w, router_w, w_router, h2, idx, gates, T, E, k, eps); break;
+        case 512: hipLaunchKernelGGL((moe_route_norm_blk_kernel<2, 2>), grid, dim3(512), lds, s, x, ffn_w, router_w, w_router, h2, idx, gates, T, E, k, eps); break;
+        default: hipLaunchKernelGGL((moe_route_norm_blk_kernel<4, 2>), grid, dim3(512), lds, s, x, ffn_w, router_w, w_router, h2, idx, gates, T, E, k, eps); break;
       }
     } else {
       switch (D) {
