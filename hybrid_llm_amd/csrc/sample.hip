@@ -359,10 +359,14 @@ __device__ bool fast_resolve(const float* x, uint32_t live, NucRow r, int base, 
     const int my = fs.cand_id[t];
     const u64 w = fs.cand_mass[t];
     u64 before = 0ull;
-#pragma unroll 8
+    // every member read unconditionally, the order test branch-free
+#pragma unroll 4
     for (int i = 0; i < n; ++i) {
       const uint32_t ki = fs.cand_key[i];
-      if (ki > k || (ki == k && fs.cand_id[i] < my)) before += fs.cand_mass[i];
+      const int ii = fs.cand_id[i];
+      const u64 mi = fs.cand_mass[i];
+      const bool ahead = (ki > k) | ((ki == k) & (ii < my));
+      before += ahead ? mi : 0ull;
     }
     if (before < rem && rem <= before + w) {  // exactly one member
       fs.id = my;
