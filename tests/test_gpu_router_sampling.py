@@ -70,7 +70,9 @@ def test_router_deterministic():
 @pytest.mark.parametrize("n,E", [(8192, 24), (128, 24), (0, 24), (1, 1), (65, 3), (20000, 256),
                                  (777, 1000),
                                  # more than 16 chunks per wave (held + reloaded chunks)
-                                 (20000, 24), (4097, 64), (3000, 7)])
+                                 (20000, 24), (4097, 64), (3000, 7),
+                                 # one expert, just past one wave's limit, long lists
+                                 (5000, 1), (2049, 24), (50000, 2), (65536, 64)])
 def test_permute_exact(n, E):
     g = torch.Generator().manual_seed(n + E)
     ids = torch.randint(0, E, (n,), generator=g, dtype=torch.int32)
