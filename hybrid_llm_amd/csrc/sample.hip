@@ -124,8 +124,8 @@ __device__ __forceinline__ float nuc_x(const float* x, int j) {
 // outside the row or outside the top-k.
 template <bool kCount>
 __device__ __forceinline__ u64 nuc_weight(float xj, uint32_t live, int j, NucRow r) {
-  if (!((live >> j) & 1u)) return 0ull;
-  return kCount ? 1ull : nuc_mass(xj, r);
+  const u64 w = kCount ? 1ull : nuc_mass(xj, r);
+  return ((live >> j) & 1u) ? w : 0ull;
 }
 
 // Exclusive prefix sum over the block in thread order; *total = block sum.
@@ -391,7 +391,7 @@ __device__ bool fast_top_p(const float* x, uint32_t live, NucRow r, int base, fl
   for (int j = 0; j < kNucPer; ++j) {
     const float xj = nuc_x(x, j);
     const u64 w = nuc_weight<false>(xj, live, j, r);
-    if (w != 0ull) atomicAdd(&fs.mass[fast_bin(xj, r)], w);
+    atomicAdd(&fs.mass[fast_bin(xj, r)], w);   // adds 0 for ids outside the row
   }
   __syncthreads();
   const u64 h0 = fs.mass[2 * t], h1 = fs.mass[2 * t + 1];
