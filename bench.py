@@ -11,8 +11,11 @@ GPU from seed 0 (synthetic; no checkpoint).
 
 Also reported on the same JSON line:
   roofline      the dominant kernel of the step (banded attention decode),
-                timed alone with HIP events on its launch stream over rotated
-                cache sets, against the HBM peak (8 TB/s); ``traffic`` is its
+                timed alone over rotated cache sets with one pair of HIP
+                events on its launch stream around the timed region's
+                launches (``avg_us`` = elapsed / launches; the mean and median
+                of per-launch event pairs are reported beside it), against
+                the HBM peak (8 TB/s); ``traffic`` is its
                 HBM bytes per launch from two rocprofv3 --pmc runs (FETCH_SIZE,
                 WRITE_SIZE) of this script's --pmc-child mode, each scaled by
                 the counter's reading for a plain copy of known size;
@@ -129,6 +132,32 @@ def event_time(launch, iters, warm=10):
     return sum(us) / len(us), median
 
 
+def region_time(launch, iters, warm=10):
+    """Average duration (us) of ``launch(i)`` over one timed region: ``iters``
+    launches back to back on a stream of their own between a single pair of HIP
+    events (after ``warm`` untimed launches and a sleep kernel that keeps the GPU
+    busy while the host enqueues them), divided by ``iters``.  Unlike
+    event_time, no event is recorded between the launches."""
+    import torch
+    stream = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        t0 = time.perf_counter()
+        for i in range(warm):
+            launch(i)
+        host_ms = (time.perf_counter() - t0) * 1e3 / max(warm, 1)
+        stream.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        sleep_ms = min(2.0 + 2.0 * host_ms * iters, 2000.0)
+        torch.cuda._sleep(int(sleep_ms / _sleep_rate() * 1e6))
+        a.record(stream)
+        for i in range(iters):
+            launch(warm + i)
+        b.record(stream)
+    b.synchronize()
+    return a.elapsed_time(b) * 1e3 / iters
+
+
 def attn_decode_sets(cfg, B, gen):
     """3 rotated cache sets (1.6 GB) so the 256 MB Infinity Cache cannot serve
     the window between launches."""
@@ -201,10 +230,12 @@ def step_bytes(cfg, B: int) -> dict:
 def time_attn_decode(cfg, B, iters, gen):
     import torch
     sets = attn_decode_sets(cfg, B, gen)
-    t = event_time(attn_decode_launcher(cfg, B, sets), iters)
+    launch = attn_decode_launcher(cfg, B, sets)
+    t = event_time(launch, iters)
+    region = region_time(launch, iters)
     del sets
     torch.cuda.empty_cache()
-    return t, attn_decode_bytes(cfg, B)
+    return t, region, attn_decode_bytes(cfg, B)
 
 
 # --------------------------------------------------------------------------- HBM traffic
@@ -789,12 +820,13 @@ def main():
 
     del eng
     torch.cuda.empty_cache()
-    (us, us_med), bytes_ = time_attn_decode(cfg, B, args.kernel_iters, gen)
+    (us_pl, us_med), us, bytes_ = time_attn_decode(cfg, B, args.kernel_iters, gen)
     achieved = bytes_ / (us * 1e-6) / 1e9
     roofline = {"kernel": "attn_decode_kernel<64, true>", "bound": "hbm", "achieved": round(achieved, 1),
                 "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                 "traffic": None if traffic is None else round(traffic["bytes"]),
-                "avg_us": round(us, 2), "median_us": round(us_med, 2),
+                "avg_us": round(us, 2), "timing": "one event pair over the timed region / launches",
+                "per_launch_event_avg_us": round(us_pl, 2), "per_launch_event_median_us": round(us_med, 2),
                 "bytes_per_launch": bytes_}
     if traffic is not None:
         roofline["traffic_detail"] = {k: (round(v, 4) if "factor" in k else round(v))
