@@ -241,7 +241,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
     for (int s = 0; s < DK / 32; ++s) {
       const uint4 kb = *reinterpret_cast<const uint4*>(Ks + (16 * tj + r16) * PK + 32 * s + 8 * g4);
       a1 = mfma16(kra[s], kb, a1);
-      a2 = mfma16(kb, qra[s], a2);  // (K Q^T) block: lane holds 4 consecutive j of row t
+      // (K Q^T) block: lane holds 4 consecutive j of row t (dk = 128: the
+      // scan forms A itself from the same operands)
+      if constexpr (!kTOut) a2 = mfma16(kb, qra[s], a2);
     }
     // L[t, j] = beta_t (Gamma_{t-1} / Gamma_j) k_t . k_j for j < t in the same
     // segment (strictly lower), formed from the K K^T block in registers
@@ -250,7 +252,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
       const int t = 16 * wave + 4 * g4 + i, j = 16 * tj + r16;
       Gm[t * PG + j] = j < t && lsj == lseg[i] ? lbet[i] * __expf(lprv[i] - lcum) * a1[i] : 0.f;
     }
-    {
+    if constexpr (!kTOut) {
       const int t = 16 * wave + r16, j0 = 16 * tj + 4 * g4;
       uint16_t hv[4], lv[4];
 #pragma unroll
@@ -377,14 +379,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
       *reinterpret_cast<uint4*>(Tw + t * kC + 8 * c8) = hi;
       *reinterpret_cast<uint4*>(Tw + kC * kC + t * kC + 8 * c8) = lo;
     }
-    {
-      const int part = threadIdx.x >> 6, t = threadIdx.x & (kC - 1);
+    for (int f = threadIdx.x; f < 6 * kC; f += 256) {
+      // parts 4, 5: the cumulative log-decay and the segment of each token,
+      // from which the scan forms A = (Gamma_t / Gamma_i) q_t . k_i
+      const int part = f >> 6, t = f & (kC - 1);
       const float ct = cum[t], cl = cum[kC - 1];
       const float fv = part == 0   ? (seg[t] == 0 ? __expf(ct) : 0.f)
                        : part == 1 ? (seg[t] == seg[kC - 1] ? __expf(cl - ct) : 0.f)
                        : part == 2 ? bet[t]
-                                   : wsc[t];
-      U0g[static_cast<long long>(cid) * kC * DV + threadIdx.x] = fv;
+                       : part == 3 ? wsc[t]
+                       : part == 4 ? ct
+                                   : static_cast<float>(seg[t]);
+      U0g[static_cast<long long>(cid) * kC * DV + f] = fv;
     }
     __syncthreads();  // LDS of this chunk is free for the next
   } else {
@@ -797,9 +803,14 @@ __global__ __launch_bounds__(kScanThreads) void gdn_chunk_scan_kernel(
 
 
 // Kernel 2 for dk = dv = 128 (64-column state slices).  Kernel 1 hands over
-// T = (I + L)^{-1} (hi, lo planes), A, and per token Gamma_t, Gamma_C/Gamma_t,
-// beta_t and beta_t Gamma_{t-1}; this kernel forms U itself:
+// T = (I + L)^{-1} (hi, lo planes) and per token Gamma_t, Gamma_C/Gamma_t,
+// beta_t, beta_t Gamma_{t-1}, the cumulative log-decay and the segment; this
+// kernel forms U and A itself:
 //   U = T Y,  Y = beta o V - (beta Gamma_prev) o (K S)      (= U0 - W S)
+//   A[t, i] = (Gamma_t / Gamma_i) q_t . k_i for i <= t in t's segment, with
+//             kernel 1's arithmetic (the same bits), by the first token
+//             half's waves in phase 1b, where they would wait for the
+//             second half's causal products
 // Wave w owns the 16 x 16 tiles (token tile 2 tp + a, column tile tn), tp = w
 // / 4, tn = w % 4, a = 0, 1 (each fragment read from LDS feeds two MFMAs), and
 // the state rows 16 w .. 16 w + 15 of the slice (four tiles, in registers):
@@ -814,7 +825,7 @@ __global__ __launch_bounds__(kScanThreads) void gdn_chunk_scan_kernel(
 //             next chunk
 //   then the next chunk's operands go to LDS.
 // Every wave does the same work.  The next chunk's K, Q, T and V rows are
-// fetched at the start of a chunk, its A and per-token factors after phase 1,
+// fetched at the start of a chunk, its per-token factors after phase 1,
 // so the loads drain behind the MFMAs; every wave issues the same memory
 // operations in the same order in every iteration (the last chunk fetches
 // itself again), so each wait for a load counts a fixed number of operations
@@ -823,15 +834,16 @@ template <int DK, int DV, int DVS>
 __global__ __launch_bounds__(kScanThreads) void gdn_chunk_scan_t_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, const uint16_t* __restrict__ Tg,
-    const float* __restrict__ facg, const uint16_t* __restrict__ Ag, float* __restrict__ state,
-    uint16_t* __restrict__ out, int T, int H, int NC, int n_units) {
+    const float* __restrict__ facg, float* __restrict__ state, uint16_t* __restrict__ out, int T,
+    int H, int NC, int n_units) {
   static_assert(DK == 128 && DVS == 64, "scan: dk = 128, 64-column slices");
   constexpr int NSL = DV / DVS;
   constexpr int PB = DK + 8, PT = kC + 8, PV = DVS + 8, NT = kScanThreads;
   constexpr int KQ_N = kC * DK / 8 / NT;     // uint4 of K (and of Q) per thread
   constexpr int T_N = 2 * kC * kC / 8 / NT;  // uint4 of T (hi and lo planes) per thread
-  constexpr int A_N = 2 * kC * kC / 8 / NT;  // uint4 of A (hi and lo planes) per thread
-  static_assert(KQ_N == 2 && T_N == 2 && A_N == 2 && kC * DVS / 8 == NT, "tile split");
+  static_assert(KQ_N == 2 && T_N == 2 && kC * DVS / 8 == NT, "tile split");
+  constexpr int NF = 6;  // per-token factors
+  static_assert(NF * kC <= NT, "one factor per thread");
   static_assert(NT / 64 == DK / 16, "one 16-row state stripe per wave");
   __shared__ __align__(16) uint16_t Qs[kC * PB], Ks[kC * PB];        // row-major [t][d]
   __shared__ __align__(16) uint16_t Thi[kC * PT], Tlo[kC * PT];      // T [t][i]
@@ -841,11 +853,15 @@ __global__ __launch_bounds__(kScanThreads) void gdn_chunk_scan_t_kernel(
   __shared__ __align__(16) uint16_t UThi[DVS * PT], UTlo[DVS * PT];  // U^T [DVS][64]
   // (dec o U)^T [DVS][64]; Y^T before phase 1b's barrier
   __shared__ __align__(16) uint16_t DThi[DVS * PT], DTlo[DVS * PT];
-  __shared__ float ecd[4 * kC];  // Gamma_t | Gamma_C / Gamma_t | beta_t | beta_t Gamma_{t-1}
+  // Gamma_t | Gamma_C / Gamma_t | beta_t | beta_t Gamma_{t-1} | cumulative
+  // log-decay | segment
+  __shared__ float ecd[NF * kC];
   const float* const ecum = ecd;
   const float* const dec = ecd + kC;
   const float* const bet = ecd + 2 * kC;
   const float* const wsc = ecd + 3 * kC;
+  const float* const lcum = ecd + 4 * kC;
+  const float* const lseg = ecd + 5 * kC;
 
   const int per_xcd = (gridDim.x + 7) / 8;
   const int unit = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
@@ -884,7 +900,7 @@ __global__ __launch_bounds__(kScanThreads) void gdn_chunk_scan_t_kernel(
   split_state();
 
   // ---- prefetch registers
-  u32x4 pk[KQ_N], pq[KQ_N], pt[T_N], pa[A_N], pv;
+  u32x4 pk[KQ_N], pq[KQ_N], pt[T_N], pv;
   float pc;
   auto fetch1 = [&](int c_) {  // K, Q, V rows (past the chunk: its last row again) and T
     const int ft0 = c_ * kC;
@@ -906,12 +922,9 @@ __global__ __launch_bounds__(kScanThreads) void gdn_chunk_scan_t_kernel(
         v + (static_cast<long long>(b) * T + ft0 + min(tv, fTc - 1)) * rv +
         static_cast<long long>(h) * DV + DVS * sl + 8 * cv);
   };
-  auto fetch2 = [&](int c_) {  // A and the per-token factors
+  auto fetch2 = [&](int c_) {  // the per-token factors
     const long long fcid = static_cast<long long>(bh) * NC + c_;
-#pragma unroll
-    for (int i = 0; i < A_N; ++i)
-      pa[i] = *reinterpret_cast<const u32x4*>(Ag + fcid * kC * kC * 2 + 8 * (tid + NT * i));
-    pc = facg[fcid * kC * DV + (tid & (4 * kC - 1))];
+    pc = facg[fcid * kC * DV + (tid < NF * kC ? tid : tid - NF * kC)];
   };
   auto stash = [&](int c_) {
     const int sTc = min(kC, T - c_ * kC);
@@ -929,19 +942,12 @@ __global__ __launch_bounds__(kScanThreads) void gdn_chunk_scan_t_kernel(
       const int pl = f / (kC * kC), rem = f % (kC * kC);
       *reinterpret_cast<u32x4*>((pl ? Tlo : Thi) + (rem / kC) * PT + rem % kC) = pt[i];
     }
-#pragma unroll
-    for (int i = 0; i < A_N; ++i) {
-      const int f = 8 * (tid + NT * i);
-      const int pl = f / (kC * kC), rem = f % (kC * kC);
-      *reinterpret_cast<u32x4*>((pl ? Alo : Ahi) + (rem / kC) * PT + rem % kC) = pa[i];
-    }
     {
       const int tv = tid / (DVS / 8), cv = tid % (DVS / 8);
       *reinterpret_cast<u32x4*>(Vs + tv * PV + 8 * cv) = tv < sTc ? pv : z;
     }
-    if (tid < 4 * kC) ecd[tid] = pc;
+    if (tid < NF * kC) ecd[tid] = pc;
   };
-
   fetch1(0);
   fetch2(0);
   stash(0);
@@ -1035,7 +1041,52 @@ __global__ __launch_bounds__(kScanThreads) void gdn_chunk_scan_t_kernel(
         u[a] = mfma16(tl[a], yhv, u[a]);
       }
     }
-    __syncthreads();  // every read of Y^T done
+    if (tp == 0) {  // uniform
+      // A in the first token half's slack (its T Y covers half the tokens):
+      // wave tn forms the tiles (tn / 2, tn % 2), (2 + tn / 2, tn % 2) and
+      // (2 + tn / 2, 2 + tn % 2) of A's K Q^T, every tile phase 2 reads
+      f32x4 a0 = f32x4{0.f, 0.f, 0.f, 0.f}, a1 = a0, a2 = a0;
+      const uint16_t* const k0 = Ks + (16 * (tn & 1) + r16) * PB + 8 * g4;
+      const uint16_t* const q0 = Qs + (16 * (tn >> 1) + r16) * PB + 8 * g4;
+#pragma unroll
+      for (int s = 0; s < DK / 32; ++s) {
+        const uint4 kv0 = *reinterpret_cast<const uint4*>(k0 + 32 * s);
+        const uint4 kv1 = *reinterpret_cast<const uint4*>(k0 + 32 * PB + 32 * s);
+        const uint4 qv0 = *reinterpret_cast<const uint4*>(q0 + 32 * s);
+        const uint4 qv1 = *reinterpret_cast<const uint4*>(q0 + 32 * PB + 32 * s);
+        a0 = mfma16(kv0, qv0, a0);
+        a1 = mfma16(kv0, qv1, a1);
+        a2 = mfma16(kv1, qv1, a2);
+      }
+      // A[t, j] = (Gamma_t / Gamma_j) q_t . k_j for j <= t in t's segment, as
+      // (hi, lo) planes; the lane holds row t = 16 ti + r16, columns j = 16 tj +
+      // 4 g4 + i (kernel 1's arithmetic, so the same bits)
+      auto store_a = [&](const f32x4& acc, int ti, int tj) {
+        const int t = 16 * ti + r16, j0 = 16 * tj + 4 * g4;
+        const float acum = lcum[t], aseg = lseg[t];
+        // the column factors read unconditionally, the mask applied by select
+        const float4 cj = *reinterpret_cast<const float4*>(lcum + j0);
+        const float4 sj = *reinterpret_cast<const float4*>(lseg + j0);
+        const float cjv[4] = {cj.x, cj.y, cj.z, cj.w}, sjv[4] = {sj.x, sj.y, sj.z, sj.w};
+        uint16_t hv[4], lv[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int j = j0 + i;
+          const float ex = __expf(acum - cjv[i]) * acc[i];
+          const float am = (j <= t) & (sjv[i] == aseg) ? ex : 0.f;
+          hv[i] = f2bf(am);
+          lv[i] = f2bf(am - bf2f(hv[i]));
+        }
+        *reinterpret_cast<uint2*>(Ahi + t * PT + j0) =
+            make_uint2(pack_bf2u(hv[0], hv[1]), pack_bf2u(hv[2], hv[3]));
+        *reinterpret_cast<uint2*>(Alo + t * PT + j0) =
+            make_uint2(pack_bf2u(lv[0], lv[1]), pack_bf2u(lv[2], lv[3]));
+      };
+      store_a(a0, tn >> 1, tn & 1);
+      store_a(a1, 2 + (tn >> 1), tn & 1);
+      store_a(a2, 2 + (tn >> 1), 2 + (tn & 1));
+    }
+    __syncthreads();  // every read of Y^T done; A complete
 #pragma unroll
     for (int a = 0; a < 2; ++a) {
       const int tm = 2 * tp + a;
@@ -1170,7 +1221,7 @@ int32_t gdn_prefill_launch(const llmy_bf16* q, const llmy_bf16* k, const llmy_bf
   // workspace, per chunk: W as (hi, lo) bf16 planes, U0 fp32, A as (hi, lo)
   // bf16 planes, decay factors [2][64] fp32.  dk = 128 uses the W slot for T
   // = (I + L)^{-1} ((hi, lo) [2][64][64]) and the U0 slot for the per-token
-  // factors [4][64]; its decay-factor slot is unused.
+  // factors [6][64]; its A and decay-factor slots are unused.
   uint16_t* W = static_cast<uint16_t*>(workspace);
   float* U0 = reinterpret_cast<float*>(W + chunks * kC * dk * 2);
   uint16_t* A = reinterpret_cast<uint16_t*>(U0 + chunks * kC * dv);
@@ -1196,7 +1247,7 @@ int32_t gdn_prefill_launch(const llmy_bf16* q, const llmy_bf16* k, const llmy_bf
     const int units = B * H * (128 / 64);
     // dk = 128: W's slot holds T, U0's slot the per-token factors
     hipLaunchKernelGGL((gdn_chunk_scan_t_kernel<128, 128, 64>), dim3((units + 7) / 8 * 8),
-                       dim3(kScanThreads), 0, s, q, k, v, W, U0, A, state, out, T, H, NC, units);
+                       dim3(kScanThreads), 0, s, q, k, v, W, U0, state, out, T, H, NC, units);
   }
   return launch_status();
 }
