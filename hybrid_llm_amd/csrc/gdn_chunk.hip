@@ -135,7 +135,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
       const int f = threadIdx.x + 256 * i;
       const int t = f / (DK / 8), cc = f - t * (DK / 8);
       skv[i] = *reinterpret_cast<const uint4*>(k + kb_ + min(t, Tc_ - 1) * rk + 8 * cc);
-      sqv[i] = *reinterpret_cast<const uint4*>(q + kb_ + min(t, Tc_ - 1) * rk + 8 * cc);
+      // Q only for A, which the dk = 128 scan forms itself
+      if constexpr (!kTOut)
+        sqv[i] = *reinterpret_cast<const uint4*>(q + kb_ + min(t, Tc_ - 1) * rk + 8 * cc);
     }
     const long long tok = static_cast<long long>(b_) * T + t0_ + min(lane, Tc_ - 1);
     pg = g[tok * H + h_];
@@ -163,10 +165,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
   for (int i = 0; i < SN; ++i) {
     const int f = threadIdx.x + 256 * i;
     const int t = f / (DK / 8), cc = f - t * (DK / 8);
-    uint4 kv = skv[i], qv = sqv[i];
-    if (t >= Tc) kv = qv = uint4{0u, 0u, 0u, 0u};
+    uint4 kv = skv[i];
+    if (t >= Tc) kv = uint4{0u, 0u, 0u, 0u};
     *reinterpret_cast<uint4*>(Ks + t * PK + 8 * cc) = kv;
-    *reinterpret_cast<uint4*>(Qs + t * PK + 8 * cc) = qv;
+    if constexpr (!kTOut) {
+      uint4 qv = sqv[i];
+      if (t >= Tc) qv = uint4{0u, 0u, 0u, 0u};
+      *reinterpret_cast<uint4*>(Qs + t * PK + 8 * cc) = qv;
+    }
   }
   if (wave == 0) {
     // inclusive prefix sum of log g over the chunk (padded tokens: g = 1, beta = 0)
@@ -222,7 +228,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
 #pragma unroll
   for (int s = 0; s < DK / 32; ++s) {
     kra[s] = *reinterpret_cast<const uint4*>(Ks + (16 * wave + r16) * PK + 32 * s + 8 * g4);
-    qra[s] = *reinterpret_cast<const uint4*>(Qs + (16 * wave + r16) * PK + 32 * s + 8 * g4);
+    if constexpr (!kTOut)
+      qra[s] = *reinterpret_cast<const uint4*>(Qs + (16 * wave + r16) * PK + 32 * s + 8 * g4);
   }
 #pragma unroll
   for (int tj = 0; tj < 4; ++tj) {
