@@ -129,7 +129,7 @@ __device__ __forceinline__ u64 nuc_weight(float xj, uint32_t live, int j, NucRow
 }
 
 // Exclusive prefix sum over the block in thread order; *total = block sum.
-__device__ u64 nuc_excl_scan(u64 v, u64* wave_tot, u64* total) {
+__device__ __forceinline__ u64 nuc_excl_scan(u64 v, u64* wave_tot, u64* total) {
   const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
   u64 inc = v;
 #pragma unroll
@@ -152,7 +152,7 @@ __device__ u64 nuc_excl_scan(u64 v, u64* wave_tot, u64* total) {
 // Scans hist from the top digit down; returns the digit at which the running
 // weight reaches rem (1 <= rem <= sum of hist) and the weight of the digits
 // above it.  Thread t covers the digits nb-1-t*per .. nb-per-t*per.
-__device__ void nuc_scan(const u64* hist, int nb, u64 rem, NucLds& sh, uint32_t* digit,
+__device__ __forceinline__ void nuc_scan(const u64* hist, int nb, u64 rem, NucLds& sh, uint32_t* digit,
                          u64* above) {
   const int per = nb / kNucThreads;
   const int t = threadIdx.x;
@@ -179,7 +179,7 @@ __device__ void nuc_scan(const u64* hist, int nb, u64 rem, NucLds& sh, uint32_t*
 
 // First-pass histogram of the live weights; returns the block's total weight.
 template <bool kCount>
-__device__ u64 nuc_top_hist(const float* x, uint32_t live, NucRow r, NucLds& sh) {
+__device__ __forceinline__ u64 nuc_top_hist(const float* x, uint32_t live, NucRow r, NucLds& sh) {
   for (int i = threadIdx.x; i < kTopBins; i += kNucThreads) sh.top[i] = 0ull;
   __syncthreads();
   u64 mine = 0;
@@ -200,7 +200,7 @@ __device__ u64 nuc_top_hist(const float* x, uint32_t live, NucRow r, NucLds& sh)
 // of the same weights.  *cum = running weight through that id, *key_out = its
 // key.
 template <bool kCount>
-__device__ int nuc_select(const float* x, uint32_t live, NucRow r, int base, u64 thr, NucLds& sh,
+__device__ __forceinline__ int nuc_select(const float* x, uint32_t live, NucRow r, int base, u64 thr, NucLds& sh,
                           u64* cum, uint32_t* key_out) {
   uint32_t digit;
   u64 above;
@@ -315,7 +315,7 @@ __device__ __forceinline__ int fast_bin(float x, NucRow r) {
 // Bucket holding running mass thr (1 <= thr <= total), from the scan state of
 // thread t (bins 2t, 2t+1: masses h0, h1, exclusive prefix P): sets fs.bin and
 // fs.above (the mass of the buckets before it).
-__device__ void fast_find(u64 thr, u64 P, u64 h0, u64 h1, FastLds& fs) {
+__device__ __forceinline__ void fast_find(u64 thr, u64 P, u64 h0, u64 h1, FastLds& fs) {
   if (P < thr && thr <= P + h0 + h1) {  // exactly one thread
     const int t = threadIdx.x;
     if (thr <= P + h0) {
@@ -333,7 +333,7 @@ __device__ void fast_find(u64 thr, u64 P, u64 h0, u64 h1, FastLds& fs) {
 // The member of bucket fs.bin at which the running mass inside the bucket
 // reaches rem; false (uniformly) when the bucket has more than kFastCap
 // members.  *id = that member, *run = the bucket-local running mass through it.
-__device__ bool fast_resolve(const float* x, uint32_t live, NucRow r, int base, u64 rem,
+__device__ __forceinline__ bool fast_resolve(const float* x, uint32_t live, NucRow r, int base, u64 rem,
                              FastLds& fs, int* id, u64* run) {
   const int bin = fs.bin;
 #pragma unroll
@@ -382,7 +382,7 @@ __device__ bool fast_resolve(const float* x, uint32_t live, NucRow r, int base, 
 
 // The whole draw without top-k; false (uniformly) when a bucket overflows or
 // the row has no mass, for the caller's radix path.
-__device__ bool fast_top_p(const float* x, uint32_t live, NucRow r, int base, float top_p,
+__device__ __forceinline__ bool fast_top_p(const float* x, uint32_t live, NucRow r, int base, float top_p,
                            float u, FastLds& fs, int* out_id) {
   const int t = threadIdx.x;
   for (int i = t; i < kFastBins; i += kNucThreads) fs.mass[i] = 0ull;
