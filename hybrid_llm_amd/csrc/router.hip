@@ -128,7 +128,7 @@ __global__ __launch_bounds__(256) void router_topk_bf16_kernel(
 // dot products, so a token waits on one memory round trip per four experts
 // instead of one per expert.  Every product, sum and reduction is taken in the
 // order of router_topk_bf16_kernel, so logits, ids and gates are identical.
-template <int NCH>
+template <int NCH, int TPW>
 __global__ __launch_bounds__(256) void router_topk_bf16_nch_kernel(
     const uint16_t* __restrict__ x, const float* __restrict__ norm_w,
     const float* __restrict__ w, float* __restrict__ logits_out,
@@ -138,28 +138,40 @@ __global__ __launch_bounds__(256) void router_topk_bf16_nch_kernel(
   constexpr int G = 4;  // experts per batch of W_r loads
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
-  const int t = blockIdx.x * 4 + wave;
-  if (t >= T) return;
-  const uint16_t* xr = x + static_cast<size_t>(t) * D;
-  float h[NCH][4];
-  float ss = 0.0f;
+  // TPW tokens per wavefront: each batch of W_r rows is loaded once and used
+  // for all of them (a token's products and sums in the same order as with
+  // one token per wavefront)
+  const int t0 = (blockIdx.x * 4 + wave) * TPW;
+  if (t0 >= T) return;
+  float h[TPW][NCH][4];
 #pragma unroll
-  for (int c = 0; c < NCH; ++c) {
-    const uint2 raw = *reinterpret_cast<const uint2*>(xr + 4 * lane + 256 * c);
-    h[c][0] = __uint_as_float(raw.x << 16);
-    h[c][1] = __uint_as_float(raw.x & 0xffff0000u);
-    h[c][2] = __uint_as_float(raw.y << 16);
-    h[c][3] = __uint_as_float(raw.y & 0xffff0000u);
-    ss += h[c][0] * h[c][0] + h[c][1] * h[c][1] + h[c][2] * h[c][2] + h[c][3] * h[c][3];
+  for (int j = 0; j < TPW; ++j) {
+    const int t = min(t0 + j, T - 1);  // rows past T: the last row again, not stored
+    const uint16_t* xr = x + static_cast<size_t>(t) * D;
+    float ss = 0.0f;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      const uint2 raw = *reinterpret_cast<const uint2*>(xr + 4 * lane + 256 * c);
+      h[j][c][0] = __uint_as_float(raw.x << 16);
+      h[j][c][1] = __uint_as_float(raw.x & 0xffff0000u);
+      h[j][c][2] = __uint_as_float(raw.y << 16);
+      h[j][c][3] = __uint_as_float(raw.y & 0xffff0000u);
+      ss += h[j][c][0] * h[j][c][0] + h[j][c][1] * h[j][c][1] + h[j][c][2] * h[j][c][2] +
+            h[j][c][3] * h[j][c][3];
+    }
+    if (norm_w != nullptr) {
+      const float r = rsqrtf(wave_sum(ss) / static_cast<float>(D) + eps);
+#pragma unroll
+      for (int c = 0; c < NCH; ++c)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) h[j][c][q] = (h[j][c][q] * r) * norm_w[4 * lane + 256 * c + q];
+    }
   }
-  if (norm_w != nullptr) {
-    const float r = rsqrtf(wave_sum(ss) / static_cast<float>(D) + eps);
+  float mine[TPW][4];
 #pragma unroll
-    for (int c = 0; c < NCH; ++c)
+  for (int j = 0; j < TPW; ++j)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) h[c][j] = (h[c][j] * r) * norm_w[4 * lane + 256 * c + j];
-  }
-  float mine[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int q = 0; q < 4; ++q) mine[j][q] = 0.f;
   for (int e0 = 0; e0 < E; e0 += G) {
     float4 wv[G][NCH];
 #pragma unroll
@@ -171,28 +183,35 @@ __global__ __launch_bounds__(256) void router_topk_bf16_nch_kernel(
                                                     256 * c);
     }
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-      float acc = 0.0f;
+    for (int j = 0; j < TPW; ++j)
 #pragma unroll
-      for (int c = 0; c < NCH; ++c) {
-        acc = fmaf(h[c][0], wv[g][c].x, acc);
-        acc = fmaf(h[c][1], wv[g][c].y, acc);
-        acc = fmaf(h[c][2], wv[g][c].z, acc);
-        acc = fmaf(h[c][3], wv[g][c].w, acc);
+      for (int g = 0; g < G; ++g) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+          acc = fmaf(h[j][c][0], wv[g][c].x, acc);
+          acc = fmaf(h[j][c][1], wv[g][c].y, acc);
+          acc = fmaf(h[j][c][2], wv[g][c].z, acc);
+          acc = fmaf(h[j][c][3], wv[g][c].w, acc);
+        }
+        acc = wave_sum(acc);
+        const int e = e0 + g;
+        if (e < E && (e & 63) == lane) mine[j][e >> 6] = acc;
       }
-      acc = wave_sum(acc);
-      const int e = e0 + g;
-      if (e < E && (e & 63) == lane) mine[e >> 6] = acc;
-    }
   }
-  if (logits_out != nullptr) {
-    for (int s = 0; s < 4; ++s) {
-      const int e = lane + 64 * s;
-      if (e < E) logits_out[static_cast<size_t>(t) * E + e] = mine[s];
+#pragma unroll
+  for (int j = 0; j < TPW; ++j) {
+    const int t = t0 + j;
+    if (t >= T) break;  // uniform
+    if (logits_out != nullptr) {
+      for (int s2 = 0; s2 < 4; ++s2) {
+        const int e = lane + 64 * s2;
+        if (e < E) logits_out[static_cast<size_t>(t) * E + e] = mine[j][s2];
+      }
     }
+    topk_softmax_store(mine[j], E, k, lane, idx_out + static_cast<size_t>(t) * k,
+                       gates_out + static_cast<size_t>(t) * k);
   }
-  topk_softmax_store(mine, E, k, lane, idx_out + static_cast<size_t>(t) * k,
-                     gates_out + static_cast<size_t>(t) * k);
 }
 
 // Top-k + softmax from precomputed fp32 logits [T, E]; one wavefront per token.
@@ -674,13 +693,26 @@ extern "C" int32_t llmy_router_topk_bf16(const uint16_t* x, const float* norm_w,
   LLMY_REQUIRE(x && w_router && idx && gates);
   LLMY_REQUIRE(aligned(x, 8) && aligned(w_router, 16) && (norm_w == nullptr || aligned(norm_w, 4)));
   const hipStream_t s = as_stream(stream);
-  const dim3 grid((T + 3) / 4);
+  // long sequences: two tokens per wavefront, so each W_r load serves both
+  // (four per wavefront were no faster: the per-token reductions remain)
+  constexpr int TPW_ = 2;
+  const bool many = T >= 1024;
+  const dim3 grid(many ? (T + 4 * TPW_ - 1) / (4 * TPW_) : (T + 3) / 4);
+#define LLMY_RT(NCH_)                                                                            \
+  if (many)                                                                                      \
+    hipLaunchKernelGGL((router_topk_bf16_nch_kernel<NCH_, TPW_>), grid, dim3(256), 0, s, x,      \
+                       norm_w, w_router, logits_out, idx, gates, T, E, k, eps);                  \
+  else                                                                                           \
+    hipLaunchKernelGGL((router_topk_bf16_nch_kernel<NCH_, 1>), grid, dim3(256), 0, s, x, norm_w, \
+                       w_router, logits_out, idx, gates, T, E, k, eps);                          \
+  return launch_status();
   switch (D) {
-    case 256: hipLaunchKernelGGL(router_topk_bf16_nch_kernel<1>, grid, dim3(256), 0, s, x, norm_w, w_router, logits_out, idx, gates, T, E, k, eps); return launch_status();
-    case 512: hipLaunchKernelGGL(router_topk_bf16_nch_kernel<2>, grid, dim3(256), 0, s, x, norm_w, w_router, logits_out, idx, gates, T, E, k, eps); return launch_status();
-    case 1024: hipLaunchKernelGGL(router_topk_bf16_nch_kernel<4>, grid, dim3(256), 0, s, x, norm_w, w_router, logits_out, idx, gates, T, E, k, eps); return launch_status();
+    case 256: LLMY_RT(1)
+    case 512: LLMY_RT(2)
+    case 1024: LLMY_RT(4)
     default: break;
   }
+#undef LLMY_RT
   const size_t lds = 4 * static_cast<size_t>(D) * sizeof(float);
   hipLaunchKernelGGL(router_topk_bf16_kernel, dim3((T + 3) / 4), dim3(256), lds,
                      as_stream(stream), x, norm_w, w_router, logits_out, idx, gates, T, D, E, k,
