@@ -50,6 +50,21 @@ def test_prefill_matches_sequential(B, T, H, d):
     assert rel_l2(out, o_ref) <= 1e-2
 
 
+@pytest.mark.parametrize("d,gval", [(128, 0.01), (128, 0.5), (64, 0.01)])
+def test_prefill_strong_decay(d, gval):
+    # log-decays summing to hundreds within a chunk (g = 0.01: Gamma_t underflows
+    # fp32 long before the chunk ends), so every decay ratio must come from
+    # log-decay differences, not from ratios of Gamma
+    q, k, v, beta, gd, S0 = _inputs(2, 150, 2, d, 11 + d)
+    gd = torch.full_like(gd, gval)
+    o_ref, S_ref = gdn_sequential(q.float(), k.float(), v.float(), beta, gd, S0)
+    out, S = _run(q, k, v, beta, gd, S0)
+    assert torch.isfinite(out).all() and torch.isfinite(S).all()
+    assert rel_l2(S, S_ref) <= 1e-4, rel_l2(S, S_ref)
+    assert float((out - o_ref).abs().max()) <= 2e-2
+    assert rel_l2(out, o_ref) <= 1e-2
+
+
 def test_prefill_zero_state_and_beta_zero_decay():
     # beta = 0: the state only decays, S_T = prod(g) S0, o_t = Gamma_t q_t^T S0
     q, k, v, beta, gd, S0 = _inputs(2, 150, 2, 64, 5)
